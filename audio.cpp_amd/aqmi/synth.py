@@ -1,0 +1,196 @@
+"""Seeded synthetic workloads for the quantizer path.
+
+The generator is counter-based and uses only IEEE basic operations
+(+, -, *, /, sqrt) on float64, so every machine produces the same float32
+inputs bit for bit (no libm log/cos whose last ulp differs across builds):
+
+  base(seed, stream) = splitmix64(splitmix64(seed) ^ (stream * 0xD1B54A32D192ED03))
+  a_i = splitmix64(base + 2 i),  b_i = splitmix64(base + 2 i + 1)      (mod 2**64)
+  u1  = ((a_i >> 11) + 1) * 2**-53  in (0, 1]
+  u2  =  (b_i >> 11)      * 2**-53  in [0, 1)
+  normal_i  = sqrt(-2 ln u1) * cos(2 pi u2)          (Box-Muller, first output)
+  uniform_i = lo + (hi - lo) * ((a_i >> 11) * 2**-53)
+
+`ln` and `cos` are evaluated with fixed series in float64 (see _det_log and
+_det_cos), accurate to a few 1e-16.  `N(0, s)` means standard deviation s.
+
+The BASELINE workloads (configs 0-4) are built by `make_config`.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+_M64 = np.uint64(0xFFFFFFFFFFFFFFFF)
+_GOLD = np.uint64(0x9E3779B97F4A7C15)
+_C1 = np.uint64(0xBF58476D1CE4E5B9)
+_C2 = np.uint64(0x94D049BB133111EB)
+_STREAM = np.uint64(0xD1B54A32D192ED03)
+_TWO_M53 = float(2.0 ** -53)
+_LN2 = 0.6931471805599453094172321
+_TWO_PI = 6.283185307179586476925287
+
+
+def _splitmix64(z: np.ndarray) -> np.ndarray:
+    with np.errstate(over="ignore"):
+        z = z + _GOLD
+        z = (z ^ (z >> np.uint64(30))) * _C1
+        z = (z ^ (z >> np.uint64(27))) * _C2
+        return z ^ (z >> np.uint64(31))
+
+
+def _base(seed: int, stream: int) -> np.uint64:
+    s = _splitmix64(np.array([seed], dtype=np.uint64))[0]
+    with np.errstate(over="ignore"):
+        k = np.uint64(stream) * _STREAM
+    return _splitmix64(np.array([s ^ k], dtype=np.uint64))[0]
+
+
+def _det_log(x: np.ndarray) -> np.ndarray:
+    """ln(x) for x in (0, 1] using frexp and the atanh series."""
+    m, e = np.frexp(x)                      # x = m * 2**e, m in [0.5, 1)
+    small = m < 0.7071067811865476
+    m = np.where(small, m * 2.0, m)         # m in [sqrt(1/2), sqrt(2))
+    e = np.where(small, e - 1, e).astype(np.float64)
+    s = (m - 1.0) / (m + 1.0)
+    s2 = s * s
+    acc = np.full_like(s, 1.0 / 23.0)
+    for k in range(21, 0, -2):
+        acc = acc * s2 + 1.0 / k
+    return e * _LN2 + 2.0 * s * acc
+
+
+def _det_cos_2pi(t: np.ndarray) -> np.ndarray:
+    """cos(2 pi t) for t in [0, 1) with range reduction to [0, pi/2]."""
+    r = t - np.floor(t + 0.5)               # [-0.5, 0.5)
+    a = np.abs(r)                           # [0, 0.5]
+    flip = a > 0.25
+    a = np.where(flip, 0.5 - a, a)          # [0, 0.25]
+    x = a * _TWO_PI
+    x2 = x * x
+    acc = np.zeros_like(x)
+    fact = [1.0]
+    for k in range(1, 26):
+        fact.append(fact[-1] * k)
+    for k in range(12, -1, -1):
+        acc = acc * x2 + ((-1.0) ** k) / fact[2 * k]
+    return np.where(flip, -acc, acc)
+
+
+def _uniform53(z: np.ndarray) -> np.ndarray:
+    return (z >> np.uint64(11)).astype(np.float64) * _TWO_M53
+
+
+def normal(seed: int, stream: int, shape, std: float = 1.0) -> np.ndarray:
+    n = int(np.prod(shape))
+    base = _base(seed, stream)
+    i = np.arange(n, dtype=np.uint64)
+    with np.errstate(over="ignore"):
+        a = _splitmix64(base + np.uint64(2) * i)
+        b = _splitmix64(base + np.uint64(2) * i + np.uint64(1))
+    u1 = ((a >> np.uint64(11)).astype(np.float64) + 1.0) * _TWO_M53
+    u2 = _uniform53(b)
+    z = np.sqrt(-2.0 * _det_log(u1)) * _det_cos_2pi(u2)
+    return (z * float(std)).astype(np.float32).reshape(shape)
+
+
+def uniform(seed: int, stream: int, shape, lo: float, hi: float) -> np.ndarray:
+    n = int(np.prod(shape))
+    base = _base(seed, stream)
+    i = np.arange(n, dtype=np.uint64)
+    with np.errstate(over="ignore"):
+        a = _splitmix64(base + np.uint64(2) * i)
+    return (lo + (hi - lo) * _uniform53(a)).astype(np.float32).reshape(shape)
+
+
+def uniform_f64(seed: int, stream: int, shape) -> np.ndarray:
+    n = int(np.prod(shape))
+    base = _base(seed, stream)
+    i = np.arange(n, dtype=np.uint64)
+    with np.errstate(over="ignore"):
+        a = _splitmix64(base + np.uint64(2) * i)
+    return _uniform53(a).reshape(shape)
+
+
+# --------------------------------------------------------------------------
+# Q8_0 block helpers (GGUF block_q8_0 = { fp16 d; int8 qs[32] }, 34 bytes)
+
+Q8_BLOCK = 32
+Q8_BYTES = 34
+Q8_DTYPE = np.dtype([("d", "<f2"), ("qs", "i1", (32,))])
+
+
+def q8_0_random_codebook(seed: int, stream: int, rows: int, dim: int) -> np.ndarray:
+    """Blocks with qs ~ U{-127..127} and d ~ U(1e-3, 1e-2) rounded to fp16."""
+    nb = dim // Q8_BLOCK
+    u = uniform_f64(seed, stream, (rows, nb, Q8_BLOCK))
+    qs = (np.floor(u * 255.0) - 127.0).astype(np.int8)
+    d = uniform(seed, stream + 1, (rows, nb), 1e-3, 1e-2).astype(np.float16)
+    out = np.zeros((rows, nb), dtype=Q8_DTYPE)
+    out["d"] = d
+    out["qs"] = qs
+    return out
+
+
+def q8_0_dequantize(blocks: np.ndarray) -> np.ndarray:
+    """Reference dequantisation y = q * d (ggml-quants.c:491-505)."""
+    d = blocks["d"].astype(np.float32)[..., None]
+    return (blocks["qs"].astype(np.float32) * d).reshape(blocks.shape[:-1] + (-1,))
+
+
+# --------------------------------------------------------------------------
+# BASELINE.json configs
+
+DAC_DIM = 8
+
+
+def dac_weights(seed: int, Q: int, D: int, N: int, bias: bool = False):
+    """Per-stage DAC weights: W_in [Q,8,D] ~N(0,1/sqrt(D)), codebook [Q,N,8]
+    ~N(0,1), W_out [Q,D,8] ~N(0,1/sqrt(8)); biases zero unless `bias`."""
+    w_in = np.stack([normal(seed, 100 * s + 2, (DAC_DIM, D), 1.0 / np.sqrt(D)) for s in range(Q)])
+    cb = np.stack([normal(seed, 100 * s + 3, (N, DAC_DIM), 1.0) for s in range(Q)])
+    w_out = np.stack([normal(seed, 100 * s + 4, (D, DAC_DIM), 1.0 / np.sqrt(DAC_DIM)) for s in range(Q)])
+    if bias:
+        b_in = np.stack([normal(seed, 100 * s + 5, (DAC_DIM,), 0.1) for s in range(Q)])
+        b_out = np.stack([normal(seed, 100 * s + 6, (D,), 0.1) for s in range(Q)])
+    else:
+        b_in = np.zeros((Q, DAC_DIM), np.float32)
+        b_out = np.zeros((Q, D), np.float32)
+    return dict(w_in=w_in, b_in=b_in, codebook=cb, w_out=w_out, b_out=b_out)
+
+
+def make_config(i: int, rows: int | None = None) -> dict:
+    """Inputs of BASELINE config i.  `rows` truncates the frame axis (the
+    generator is counter-based, so a truncated config is an exact prefix)."""
+    if i == 0:
+        B, T, D, Q, N = 1, 750, 1024, 1, 1024
+        M = B * T if rows is None else rows
+        x = normal(1, 1, (B * T, D))[:M]
+        return dict(kind="dac", seed=1, B=B, T=T, D=D, Q=Q, N=N, x=x, **dac_weights(1, Q, D, N))
+    if i == 1:
+        B, T, D, Q, N = 8, 750, 1024, 12, 1024
+        x = normal(2, 1, (B * T, D))
+        if rows is not None:
+            x = x[:rows]
+        return dict(kind="dac", seed=2, B=B, T=T, D=D, Q=Q, N=N, x=x, **dac_weights(2, Q, D, N))
+    if i == 2:
+        M, K, Q, N = 48000, 256, 8, 2048
+        M = M if rows is None else rows
+        x = normal(3, 1, (M, K))
+        cb = np.stack([normal(3, 100 * s + 2, (N, K), 1.0 / 16.0) for s in range(Q)])
+        return dict(kind="euclid", seed=3, M=M, K=K, Q=Q, N=N, x=x, codebook=cb)
+    if i == 3:
+        M, K, N = 200000, 768, 16384
+        M = M if rows is None else rows
+        z = normal(4, 1, (M, K))
+        s = uniform(4, 2, (K,), 0.5, 2.0)
+        x = (z * s[None, :]).astype(np.float32)
+        cb = normal(4, 3, (N, K), 1.0)[None]
+        return dict(kind="kmeans", seed=4, M=M, K=K, Q=1, N=N, x=x, codebook=cb)
+    if i == 4:
+        M, K, Q, N = 48000, 256, 8, 2048
+        M = M if rows is None else rows
+        x = normal(5, 1, (M, K))
+        cb = np.stack([q8_0_random_codebook(5, 100 * s + 2, N, K) for s in range(Q)])
+        return dict(kind="q8_0", seed=5, M=M, K=K, Q=Q, N=N, x=x, codebook_q8=cb, topk=4)
+    raise ValueError(f"unknown config {i}")

@@ -1,0 +1,225 @@
+"""Oracle for the quantizer path -- TEST INFRASTRUCTURE ONLY.
+
+`Oracle` wraps liboracle.so (the plain-C restatement in aq_oracle.c).
+`Ref` wraps oracle/_ref/libaqref-<isa>.so (the reference's own ggml CPU
+backend compiled from /root/reference by oracle/Makefile, plus
+ref_harness.cpp).  Only tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg may import this package, and only as the checker or the
+labelled CPU baseline -- the product path never does.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import os
+import pathlib
+import subprocess
+
+import numpy as np
+
+HERE = pathlib.Path(__file__).resolve().parent
+REF_DIR = HERE / "_ref"
+
+_f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+_i64 = C.c_int64
+
+
+def _opt(a, dtype):
+    if a is None:
+        return None
+    a = np.ascontiguousarray(a, dtype=dtype)
+    return a.ctypes.data_as(C.c_void_p)
+
+
+def build_oracle() -> pathlib.Path:
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    return HERE / "liboracle.so"
+
+
+def host_isa() -> str:
+    """Best _ref variant this CPU can run: native (only where it was built),
+    else v4 (AVX-512) or v3 (AVX2)."""
+    flags = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("flags"):
+                flags = line
+                break
+    except OSError:
+        pass
+    if " avx512f " in flags and " avx512bw " in flags and " avx512vl " in flags:
+        return "v4"
+    return "v3"
+
+
+class Oracle:
+    def __init__(self, path: str | os.PathLike | None = None):
+        path = pathlib.Path(path) if path else HERE / "liboracle.so"
+        if not path.exists():
+            build_oracle()
+        self.lib = C.CDLL(str(path))
+        L = self.lib
+        L.aqo_vec_dot_f32.restype = C.c_float
+        L.aqo_vec_dot_f32.argtypes = [C.c_int, _f32p, _f32p]
+        L.aqo_tinyblas_dot_f32.restype = C.c_float
+        L.aqo_tinyblas_dot_f32.argtypes = [C.c_int, _f32p, _f32p]
+        L.aqo_argmax_f32.restype = C.c_int
+        L.aqo_argmax_f32.argtypes = [C.c_int, _f32p]
+        L.aqo_sum_f32.restype = C.c_float
+        L.aqo_sum_f32.argtypes = [C.c_int, _f32p]
+        L.aqo_fp32_to_fp16.restype = C.c_uint16
+        L.aqo_fp32_to_fp16.argtypes = [C.c_float]
+        L.aqo_fp16_to_fp32.restype = C.c_float
+        L.aqo_fp16_to_fp32.argtypes = [C.c_uint16]
+        L.aqo_quantize_row_q8_0_x86.argtypes = [_f32p, C.c_void_p, C.c_int]
+        L.aqo_quantize_row_q8_0_ref.argtypes = [_f32p, C.c_void_p, C.c_int]
+        L.aqo_dequantize_row_q8_0.argtypes = [C.c_void_p, _f32p, C.c_int]
+        L.aqo_dot_q8_0.restype = C.c_float
+        L.aqo_dot_q8_0.argtypes = [C.c_int, C.c_void_p, C.c_void_p]
+        L.aqo_dac_rvq.restype = C.c_int
+        L.aqo_dac_rvq.argtypes = [_f32p, _i64, _i64, _i64, _i64, _i64, _f32p, C.c_void_p, _f32p, _f32p,
+                                  C.c_void_p, C.c_void_p, _i32p, _f32p, C.c_void_p]
+        L.aqo_euclid_rvq.restype = C.c_int
+        L.aqo_euclid_rvq.argtypes = [_f32p, _i64, _i64, _i64, _i64, _f32p, C.c_void_p, _i32p, _f32p, C.c_void_p]
+        L.aqo_higgs_rvq.restype = C.c_int
+        L.aqo_higgs_rvq.argtypes = [_f32p, _i64, _i64, _i64, _i64, C.c_void_p, C.c_int, C.c_int, C.c_void_p,
+                                    _i32p, _f32p, C.c_void_p, C.c_void_p, C.c_void_p]
+        L.aqo_gather_f32.restype = C.c_int
+        L.aqo_gather_f32.argtypes = [_f32p, _i64, _i64, _i32p, _i64, _f32p]
+        L.aqo_gather_q8_0.restype = C.c_int
+        L.aqo_gather_q8_0.argtypes = [C.c_void_p, _i64, _i64, _i32p, _i64, _f32p]
+
+    # -- whole path --------------------------------------------------------
+    def dac_rvq(self, cfg: dict, force_idx=None, recon: bool = True):
+        x = np.ascontiguousarray(cfg["x"], np.float32)
+        B, T, D, Q, N = cfg["B"], cfg["T"], cfg["D"], cfg["Q"], cfg["N"]
+        M = x.shape[0]
+        assert M % T == 0
+        B = M // T
+        idx = np.zeros((M, Q), np.int32)
+        res = np.zeros((M, D), np.float32)
+        rec = np.zeros((M, D), np.float32) if recon else None
+        fi = np.ascontiguousarray(force_idx, np.int32) if force_idx is not None else None
+        rc = self.lib.aqo_dac_rvq(x, B, T, D, Q, N, np.ascontiguousarray(cfg["w_in"], np.float32),
+                                  _opt(cfg.get("b_in"), np.float32), np.ascontiguousarray(cfg["codebook"], np.float32),
+                                  np.ascontiguousarray(cfg["w_out"], np.float32), _opt(cfg.get("b_out"), np.float32),
+                                  None if fi is None else fi.ctypes.data_as(C.c_void_p), idx, res,
+                                  None if rec is None else rec.ctypes.data_as(C.c_void_p))
+        assert rc == 0
+        return dict(idx=idx, residual=res, recon=rec)
+
+    def euclid_rvq(self, cfg: dict, force_idx=None):
+        x = np.ascontiguousarray(cfg["x"], np.float32)
+        M, K = x.shape
+        Q, N = cfg["Q"], cfg["N"]
+        idx = np.zeros((M, Q), np.int32)
+        res = np.zeros((M, K), np.float32)
+        lb = np.zeros((M, Q), np.float32)
+        fi = np.ascontiguousarray(force_idx, np.int32) if force_idx is not None else None
+        rc = self.lib.aqo_euclid_rvq(x, M, K, Q, N, np.ascontiguousarray(cfg["codebook"], np.float32),
+                                     None if fi is None else fi.ctypes.data_as(C.c_void_p), idx, res,
+                                     lb.ctypes.data_as(C.c_void_p))
+        assert rc == 0
+        return dict(idx=idx, residual=res, logit=lb)
+
+    def higgs_rvq(self, cfg: dict, force_idx=None, topk: int = 0):
+        x = np.ascontiguousarray(cfg["x"], np.float32)
+        M, K = x.shape
+        Q, N = cfg["Q"], cfg["N"]
+        if "codebook_q8" in cfg:
+            cb = np.ascontiguousarray(cfg["codebook_q8"])
+            cbt = 1
+        else:
+            cb = np.ascontiguousarray(cfg["codebook"], np.float32)
+            cbt = 0
+        idx = np.zeros((M, Q), np.int32)
+        res = np.zeros((M, K), np.float32)
+        dist = np.zeros((M, Q), np.float32)
+        tki = np.zeros((M, Q, max(topk, 1)), np.int32)
+        tkl = np.zeros((M, Q, max(topk, 1)), np.float32)
+        fi = np.ascontiguousarray(force_idx, np.int32) if force_idx is not None else None
+        rc = self.lib.aqo_higgs_rvq(x, M, K, Q, N, cb.ctypes.data_as(C.c_void_p), cbt, topk,
+                                    None if fi is None else fi.ctypes.data_as(C.c_void_p), idx, res,
+                                    dist.ctypes.data_as(C.c_void_p), tki.ctypes.data_as(C.c_void_p),
+                                    tkl.ctypes.data_as(C.c_void_p))
+        assert rc == 0
+        out = dict(idx=idx, residual=res, dist=dist)
+        if topk:
+            out["topk_idx"] = tki
+            out["topk_logit"] = tkl
+        return out
+
+
+class Ref:
+    """The reference's own ggml CPU backend (oracle/_ref)."""
+
+    def __init__(self, isa: str | None = None):
+        isa = isa or ("native" if (REF_DIR / "libaqref-native.so").exists() else host_isa())
+        path = REF_DIR / f"libaqref-{isa}.so"
+        if not path.exists():
+            raise FileNotFoundError(f"{path} not built (make -C oracle ref needs /root/reference)")
+        self.isa = isa
+        self.lib = C.CDLL(str(path))
+        L = self.lib
+        L.aqref_dac_rvq.restype = C.c_double
+        L.aqref_dac_rvq.argtypes = [_f32p, _i64, _i64, _i64, _i64, _i64, _f32p, C.c_void_p, _f32p, _f32p,
+                                    C.c_void_p, _i32p, _f32p, C.c_void_p, C.c_void_p, C.c_int, C.c_int]
+        L.aqref_euclid_rvq.restype = C.c_double
+        L.aqref_euclid_rvq.argtypes = [_f32p, _i64, _i64, _i64, _i64, _f32p, _i32p, _f32p, C.c_void_p, C.c_int]
+        L.aqref_higgs_rvq.restype = C.c_double
+        L.aqref_higgs_rvq.argtypes = [_f32p, _i64, _i64, _i64, _i64, C.c_void_p, C.c_int, C.c_int,
+                                      _i32p, _f32p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int]
+        L.aqref_quantize_row_q8_0.argtypes = [_f32p, C.c_void_p, _i64]
+        L.aqref_quantize_chunk_q8_0.argtypes = [_f32p, C.c_void_p, _i64, _i64]
+
+    def dac_rvq(self, cfg: dict, threads: int = 8, recon: bool = True, materialize: bool = True):
+        x = np.ascontiguousarray(cfg["x"], np.float32)
+        T, D, Q, N = cfg["T"], cfg["D"], cfg["Q"], cfg["N"]
+        M = x.shape[0]
+        B = M // T
+        idx = np.zeros((M, Q), np.int32)
+        res = np.zeros((M, D), np.float32)
+        rec = np.zeros((M, D), np.float32) if recon else None
+        ms = self.lib.aqref_dac_rvq(x, B, T, D, Q, N, np.ascontiguousarray(cfg["w_in"], np.float32),
+                                    _opt(cfg.get("b_in"), np.float32), np.ascontiguousarray(cfg["codebook"], np.float32),
+                                    np.ascontiguousarray(cfg["w_out"], np.float32), _opt(cfg.get("b_out"), np.float32),
+                                    idx, res, None if rec is None else rec.ctypes.data_as(C.c_void_p), None, threads,
+                                    1 if materialize else 0)
+        return dict(idx=idx, residual=res, recon=rec, ms=ms)
+
+    def euclid_rvq(self, cfg: dict, threads: int = 8):
+        x = np.ascontiguousarray(cfg["x"], np.float32)
+        M, K = x.shape
+        Q, N = cfg["Q"], cfg["N"]
+        idx = np.zeros((M, Q), np.int32)
+        res = np.zeros((M, K), np.float32)
+        lb = np.zeros((M, Q), np.float32)
+        ms = self.lib.aqref_euclid_rvq(x, M, K, Q, N, np.ascontiguousarray(cfg["codebook"], np.float32), idx, res,
+                                       lb.ctypes.data_as(C.c_void_p), threads)
+        return dict(idx=idx, residual=res, logit=lb, ms=ms)
+
+    def higgs_rvq(self, cfg: dict, topk: int = 0, threads: int = 8):
+        x = np.ascontiguousarray(cfg["x"], np.float32)
+        M, K = x.shape
+        Q, N = cfg["Q"], cfg["N"]
+        if "codebook_q8" in cfg:
+            cb = np.ascontiguousarray(cfg["codebook_q8"])
+            cbt = 1
+        else:
+            cb = np.ascontiguousarray(cfg["codebook"], np.float32)
+            cbt = 0
+        idx = np.zeros((M, Q), np.int32)
+        res = np.zeros((M, K), np.float32)
+        dist = np.zeros((M, Q), np.float32)
+        tki = np.zeros((M, Q, max(topk, 1)), np.int32)
+        tkl = np.zeros((M, Q, max(topk, 1)), np.float32)
+        ms = self.lib.aqref_higgs_rvq(x, M, K, Q, N, cb.ctypes.data_as(C.c_void_p), cbt, topk, idx, res,
+                                      dist.ctypes.data_as(C.c_void_p),
+                                      tki.ctypes.data_as(C.c_void_p) if topk else None,
+                                      tkl.ctypes.data_as(C.c_void_p) if topk else None, threads)
+        out = dict(idx=idx, residual=res, dist=dist, ms=ms)
+        if topk:
+            out["topk_idx"] = tki
+            out["topk_logit"] = tkl
+        return out

@@ -1,0 +1,434 @@
+/*
+ * aq_oracle.c -- plain-C restatement of the reference quantizer arithmetic.
+ *
+ * TEST INFRASTRUCTURE ONLY (see aq_oracle.h).  The product path never links
+ * or calls this file; it is the checker for the HIP path and the labelled
+ * "port" CPU baseline.
+ *
+ * Compiled with -ffp-contract=off: every fused multiply-add below is an
+ * explicit fmaf() standing for an FMA intrinsic of the reference build
+ * (_mm512_fmadd_ps / _mm256_fmadd_ps); every other product is rounded before
+ * it is added, as in the reference build (checked bit for bit against
+ * oracle/_ref).
+ *
+ * Reference paths are relative to /root/reference/external/ggml/src unless
+ * they start with src/ (the audio.cpp tree).
+ */
+#include "aq_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ---------------------------------------------------------------------------
+ * _mm512_reduce_add_ps as GCC 11 implements it (avx512fintrin.h
+ * __MM512_REDUCE_OP): halves 256 -> 128 -> 64 -> 32, i.e. pairwise sums at
+ * distances 8, 4, 2, 1.  Used by hsum(__m512) (ggml-cpu/llamafile/sgemm.cpp:
+ * 274-278) and GGML_F32x16_REDUCE (ggml-cpu/simd-mappings.h:451-476).
+ */
+static float reduce16(const float a[16]) {
+    float t3[8], t6[4], t8[2];
+    for (int i = 0; i < 8; ++i) t3[i] = a[i + 8] + a[i];
+    for (int i = 0; i < 4; ++i) t6[i] = t3[i + 4] + t3[i];
+    for (int i = 0; i < 2; ++i) t8[i] = t6[i] + t6[i + 2];
+    return t8[0] + t8[1];
+}
+
+/* hsum(__m256) (sgemm.cpp:267-271 -> 252-264) and hsum_float_8
+ * (ggml-cpu/arch/x86/quants.c:43-49): lanes i+4 added to i, then distance 2,
+ * then 1. */
+static float reduce8(const float a[8]) {
+    float v[4];
+    for (int i = 0; i < 4; ++i) v[i] = a[i + 4] + a[i];
+    const float y0 = v[0] + v[2];
+    const float y1 = v[1] + v[3];
+    return y0 + y1;
+}
+
+/* ggml_vec_dot_f32, GGML_SIMD AVX-512 branch (ggml-cpu/vec.cpp:11-135;
+ * GGML_F32_STEP 64, GGML_F32_EPR 16, GGML_F32_ARR 4 at simd-mappings.h:
+ * 439-478).  Four 16-lane accumulators take elements i+16j+l with FMA
+ * (GGML_F32x16_FMA = _mm512_fmadd_ps), are combined 0+=2, 1+=3, 0+=1, then
+ * reduced by reduce16.  The scalar leftovers `sumf += x[i]*y[i]` are a
+ * separate multiply and add: the reference build does not fuse them (checked
+ * bit for bit against oracle/_ref on the dim-8 score and out-projection). */
+float aqo_vec_dot_f32(int n, const float *x, const float *y) {
+    const int np = n & ~63;
+    float sum[4][16];
+    memset(sum, 0, sizeof(sum));
+    for (int i = 0; i < np; i += 64)
+        for (int j = 0; j < 4; ++j)
+            for (int l = 0; l < 16; ++l)
+                sum[j][l] = fmaf(x[i + 16 * j + l], y[i + 16 * j + l], sum[j][l]);
+    for (int l = 0; l < 16; ++l) {
+        sum[0][l] = sum[0][l] + sum[2][l];
+        sum[1][l] = sum[1][l] + sum[3][l];
+    }
+    for (int l = 0; l < 16; ++l) sum[0][l] = sum[0][l] + sum[1][l];
+    float sumf = reduce16(sum[0]);
+    for (int i = np; i < n; ++i) {
+        const float prod = x[i] * y[i];
+        sumf = sumf + prod;
+    }
+    return sumf;
+}
+
+/* One output element of tinyBLAS<16, __m512, __m512, float, float, float>
+ * (sgemm.cpp:523-580, dispatched at 3716-3725): a 16-lane FMA accumulator
+ * over k in steps of 16 (madd = _mm512_fmadd_ps, sgemm.cpp:145-149), then
+ * hsum = _mm512_reduce_add_ps. */
+float aqo_tinyblas_dot_f32(int k, const float *a, const float *b) {
+    float acc[16];
+    memset(acc, 0, sizeof(acc));
+    for (int l = 0; l < k; l += 16)
+        for (int j = 0; j < 16; ++j) acc[j] = fmaf(a[l + j], b[l + j], acc[j]);
+    return reduce16(acc);
+}
+
+/* When ggml_compute_forward_mul_mat hands an F32 x F32 product to tinyBLAS
+ * (ggml-cpu/ggml-cpu.c:1285-1306 -> sgemm.cpp:3705-3725 -> matmul 527-545,
+ * VECTOR_REGISTERS == 32): n >= 2, k % 16 == 0 and m % 4 == 0 (m = src0 rows,
+ * n = src1 rows).  Otherwise ggml_vec_dot_f32 computes each element. */
+int aqo_mul_mat_f32_uses_tinyblas(int64_t m, int64_t n, int64_t k) {
+    return n >= 2 && (k % 16) == 0 && (m % 4) == 0;
+}
+
+/* ggml_vec_argmax_f32 (ggml-cpu/vec.h:1576-1584): running MAX(max, x[i]) with
+ * MAX(a,b) = a > b ? a : b, index updated whenever max == x[i].  Keeps the
+ * last index of the maximum; NaN restarts the running max (see the loop). */
+int aqo_argmax_f32(int n, const float *x) {
+    float max = -INFINITY;
+    int idx = 0;
+    for (int i = 0; i < n; ++i) {
+        max = max > x[i] ? max : x[i];
+        if (max == x[i]) idx = i;
+    }
+    return idx;
+}
+
+/* ggml_vec_sum_f32 (ggml-cpu/vec.h:1513-1523): double accumulation, one
+ * final rounding to float; used by sum_rows (ops.cpp:1457-1489). */
+float aqo_sum_f32(int n, const float *x) {
+    double s = 0.0;
+    for (int i = 0; i < n; ++i) s += (double)x[i];
+    return (float)s;
+}
+
+/* IEEE binary16 round-to-nearest-even, as F16C _cvtss_sh(x, 0) which
+ * GGML_CPU_FP32_TO_FP16 maps to on x86 (simd-mappings.h). */
+uint16_t aqo_fp32_to_fp16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const uint32_t absx = x & 0x7FFFFFFFu;
+    if (absx > 0x7F800000u) return (uint16_t)(sign | 0x7E00u | ((absx >> 13) & 0x3FFu)); /* NaN */
+    if (absx >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u);                           /* overflow */
+    if (absx < 0x38800000u) {                                                              /* subnormal / zero */
+        if (absx < 0x33000000u) return (uint16_t)sign;
+        const uint32_t e = absx >> 23;
+        const uint32_t mant = (absx & 0x7FFFFFu) | 0x800000u;
+        const uint32_t shift = 126u - e;           /* 14 .. 24 */
+        uint32_t q = mant >> shift;
+        const uint32_t rem = mant & ((1u << shift) - 1u);
+        const uint32_t half = 1u << (shift - 1u);
+        if (rem > half || (rem == half && (q & 1u))) q += 1u;
+        return (uint16_t)(sign | q);
+    }
+    uint32_t h = ((absx - 0x38000000u) >> 13);
+    const uint32_t rem = absx & 0x1FFFu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h += 1u;
+    return (uint16_t)(sign | h);
+}
+
+float aqo_fp16_to_fp32(uint16_t h) {
+    const uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+    const uint32_t e = (h >> 10) & 0x1Fu;
+    const uint32_t m = h & 0x3FFu;
+    uint32_t bits;
+    if (e == 0) {
+        if (m == 0) {
+            bits = sign;
+        } else {
+            float v = ldexpf((float)m, -24);
+            memcpy(&bits, &v, 4);
+            bits |= sign;
+        }
+    } else if (e == 31) {
+        bits = sign | 0x7F800000u | (m << 13);
+    } else {
+        bits = sign | ((e + 112u) << 23) | (m << 13);
+    }
+    float out;
+    memcpy(&out, &bits, 4);
+    return out;
+}
+
+/* quantize_row_q8_0 for x86 AVX2 (ggml-cpu/arch/x86/quants.c:302-393): the
+ * from_float that mul_mat applies to the F32 operand of a Q8_0 product
+ * (ggml-cpu.c:1309-1340).  amax by max-tree, d = amax/127 stored as fp16,
+ * id = 127/amax, q = round-half-even(x*id), saturating packs to int8. */
+static int8_t sat_q(float v) {
+    if (isnan(v) || v >= 2147483648.0f || v < -2147483648.0f) return -128;
+    long q = (long)v;
+    if (q > 127) q = 127;
+    if (q < -128) q = -128;
+    return (int8_t)q;
+}
+
+void aqo_quantize_row_q8_0_x86(const float *x, aqo_block_q8_0 *y, int k) {
+    const int nb = k / 32;
+    for (int i = 0; i < nb; ++i) {
+        const float *xb = x + 32 * i;
+        float amax = 0.0f;
+        for (int j = 0; j < 32; ++j) {
+            const float a = fabsf(xb[j]);
+            amax = amax > a ? amax : a;
+        }
+        const float d = amax / 127.f;
+        y[i].d = aqo_fp32_to_fp16(d);
+        const float id = (amax != 0.0f) ? 127.f / amax : 0.0f;
+        for (int j = 0; j < 32; ++j) y[i].qs[j] = sat_q(nearbyintf(xb[j] * id));
+    }
+}
+
+/* quantize_row_q8_0_ref (ggml-quants.c:236-256): the weight-side rounding
+ * used by ggml_quantize_chunk (roundf, id = 1/d). */
+void aqo_quantize_row_q8_0_ref(const float *x, aqo_block_q8_0 *y, int k) {
+    const int nb = k / 32;
+    for (int i = 0; i < nb; ++i) {
+        float amax = 0.0f;
+        for (int j = 0; j < 32; ++j) {
+            const float v = fabsf(x[32 * i + j]);
+            amax = amax > v ? amax : v;
+        }
+        const float d = amax / ((1 << 7) - 1);
+        const float id = d ? 1.0f / d : 0.0f;
+        y[i].d = aqo_fp32_to_fp16(d);
+        for (int j = 0; j < 32; ++j) y[i].qs[j] = (int8_t)roundf(x[32 * i + j] * id);
+    }
+}
+
+/* dequantize_row_q8_0 (ggml-quants.c:491-505): y = q * d. */
+void aqo_dequantize_row_q8_0(const aqo_block_q8_0 *x, float *y, int k) {
+    const int nb = k / 32;
+    for (int i = 0; i < nb; ++i) {
+        const float d = aqo_fp16_to_fp32(x[i].d);
+        for (int j = 0; j < 32; ++j) y[32 * i + j] = (float)x[i].qs[j] * d;
+    }
+}
+
+/* One element of tinyBLAS_Q0_AVX<block_q8_0, block_q8_0, float>
+ * (sgemm.cpp:1353-1680, dispatched at 3928-3938) and of
+ * ggml_vec_dot_q8_0_q8_0 (ggml-cpu/arch/x86/quants.c:1170-1216), which share
+ * the arithmetic: per block, 8 lanes of exact 4-byte int8 dot products
+ * (updot / mul_sum_i8_pairs_float), scaled by fp32(d_a)*fp32(d_b) and
+ * accumulated with FMA; then reduce8. */
+float aqo_dot_q8_0(int nb, const aqo_block_q8_0 *a, const aqo_block_q8_0 *b) {
+    float acc[8];
+    memset(acc, 0, sizeof(acc));
+    for (int ib = 0; ib < nb; ++ib) {
+        const float dd = aqo_fp16_to_fp32(a[ib].d) * aqo_fp16_to_fp32(b[ib].d);
+        for (int l = 0; l < 8; ++l) {
+            int32_t s = 0;
+            for (int t = 0; t < 4; ++t) s += (int32_t)a[ib].qs[4 * l + t] * (int32_t)b[ib].qs[4 * l + t];
+            acc[l] = fmaf(dd, (float)s, acc[l]);
+        }
+    }
+    return reduce8(acc);
+}
+
+/* ------------------------------------------------------------------------- */
+
+static float dot_f32(int64_t m_rows, int64_t n_rows, int k, const float *src0_row, const float *src1_row) {
+    return aqo_mul_mat_f32_uses_tinyblas(m_rows, n_rows, k) ? aqo_tinyblas_dot_f32(k, src0_row, src1_row)
+                                                            : aqo_vec_dot_f32(k, src0_row, src1_row);
+}
+
+/* Fish Audio encode quantizer, one stage per codebook
+ * (src/models/fish_audio/codec.cpp:570-611, quantize_one 587-605):
+ *   projected = Conv1d(k=1)(residual) + b_in       conv_modules.cpp:284-341,152-166
+ *     (ggml_conv_1d = im2col + mul_mat(im2col, W), ggml.c:4554-4571; one
+ *     conv per clip, so m = T decides tinyBLAS vs vec_dot)
+ *   pn = projected / sqrt(sum(projected^2) + 1e-12)  codec.cpp:323-334
+ *   logits = mul_mat(normalized_codebook, pn)        k = 8 -> vec_dot_f32
+ *   code = argmax(logits)                            (last index of max)
+ *   z = Conv1d(k=1)(codebook[code]) + b_out          k = 8 -> vec_dot_f32
+ *   residual -= z ; recon += z (decode sum, codec.cpp:552-568)
+ * normalized_codebook = normalized_rows(codebook)    codec.cpp:171-189. */
+int aqo_dac_rvq(const float *x, int64_t B, int64_t T, int64_t D, int64_t Q, int64_t N,
+                const float *w_in, const float *b_in, const float *cb,
+                const float *w_out, const float *b_out, const int32_t *force_idx,
+                int32_t *idx, float *residual, float *recon) {
+    const int64_t M = B * T;
+    float *r = residual;
+    memcpy(r, x, (size_t)(M * D) * sizeof(float));
+    float *cbn = (float *)malloc((size_t)(N * 8) * sizeof(float));
+    float *scores = (float *)malloc((size_t)N * sizeof(float));
+    if (!cbn || !scores) { free(cbn); free(scores); return -1; }
+    const int inproj_tiny = aqo_mul_mat_f32_uses_tinyblas(T, 8, D);
+    for (int64_t s = 0; s < Q; ++s) {
+        const float *Wi = w_in + s * 8 * D;
+        const float *C = cb + s * N * 8;
+        const float *Wo = w_out + s * D * 8;
+        for (int64_t n = 0; n < N; ++n) {
+            double sum = 0.0;
+            for (int k = 0; k < 8; ++k) sum += (double)C[n * 8 + k] * (double)C[n * 8 + k];
+            const float inv = sum > 0.0 ? (float)(1.0 / sqrt(sum)) : 0.0f;
+            for (int k = 0; k < 8; ++k) cbn[n * 8 + k] = C[n * 8 + k] * inv;
+        }
+        for (int64_t m = 0; m < M; ++m) {
+            float *rm = r + m * D;
+            float p[8], pn[8], sq[8];
+            for (int j = 0; j < 8; ++j) {
+                p[j] = inproj_tiny ? aqo_tinyblas_dot_f32((int)D, rm, Wi + j * D) : aqo_vec_dot_f32((int)D, rm, Wi + j * D);
+                if (b_in) p[j] = p[j] + b_in[s * 8 + j];
+            }
+            for (int j = 0; j < 8; ++j) sq[j] = p[j] * p[j];
+            float ss = aqo_sum_f32(8, sq);
+            ss = fmaf(ss, 1.0f, 1.0e-12f);          /* ggml_scale_bias, vec.h:708-710 */
+            const float den = sqrtf(ss);
+            for (int j = 0; j < 8; ++j) pn[j] = p[j] / den;
+            for (int64_t n = 0; n < N; ++n) scores[n] = aqo_vec_dot_f32(8, cbn + n * 8, pn);
+            const int code = aqo_argmax_f32((int)N, scores);
+            idx[m * Q + s] = code;
+            const int use = force_idx ? force_idx[m * Q + s] : code;
+            const float *q = C + (int64_t)use * 8;
+            for (int64_t d = 0; d < D; ++d) {
+                float z = aqo_vec_dot_f32(8, q, Wo + d * 8);
+                if (b_out) z = z + b_out[s * D + d];
+                rm[d] = rm[d] - z;
+                if (recon) recon[m * D + d] = s == 0 ? z : recon[m * D + d] + z;
+            }
+        }
+    }
+    free(cbn);
+    free(scores);
+    return 0;
+}
+
+/* OmniVoice encode quantizer without projections
+ * (src/models/omnivoice/audio_tokenizer.cpp:1227-1237 score weights,
+ * 1897-1927 graph): logits = mul_mat(2c, r) + (float)(-sum_double(c^2)),
+ * argmax, get_rows(codebook), residual -= q. */
+int aqo_euclid_rvq(const float *x, int64_t M, int64_t K, int64_t Q, int64_t N,
+                   const float *cb, const int32_t *force_idx,
+                   int32_t *idx, float *residual, float *logit_best) {
+    float *r = residual;
+    memcpy(r, x, (size_t)(M * K) * sizeof(float));
+    float *w2 = (float *)malloc((size_t)(N * K) * sizeof(float));
+    float *bias = (float *)malloc((size_t)N * sizeof(float));
+    float *lg = (float *)malloc((size_t)N * sizeof(float));
+    if (!w2 || !bias || !lg) { free(w2); free(bias); free(lg); return -1; }
+    for (int64_t s = 0; s < Q; ++s) {
+        const float *C = cb + s * N * K;
+        for (int64_t n = 0; n < N; ++n) {
+            double norm = 0.0;
+            for (int64_t k = 0; k < K; ++k) {
+                const float v = C[n * K + k];
+                w2[n * K + k] = 2.0f * v;
+                norm += (double)v * (double)v;
+            }
+            bias[n] = (float)(-norm);
+        }
+        for (int64_t m = 0; m < M; ++m) {
+            float *rm = r + m * K;
+            for (int64_t n = 0; n < N; ++n) lg[n] = dot_f32(N, M, (int)K, w2 + n * K, rm) + bias[n];
+            const int code = aqo_argmax_f32((int)N, lg);
+            idx[m * Q + s] = code;
+            if (logit_best) logit_best[m * Q + s] = lg[code];
+            const int use = force_idx ? force_idx[m * Q + s] : code;
+            for (int64_t k = 0; k < K; ++k) rm[k] = rm[k] - C[(int64_t)use * K + k];
+        }
+    }
+    free(w2);
+    free(bias);
+    free(lg);
+    return 0;
+}
+
+typedef struct { float v; int32_t i; } aqo_pair;
+
+static int cmp_desc(const void *pa, const void *pb) {
+    const aqo_pair *a = (const aqo_pair *)pa, *b = (const aqo_pair *)pb;
+    if (a->v > b->v) return -1;
+    if (a->v < b->v) return 1;
+    return a->i < b->i ? -1 : (a->i > b->i);
+}
+
+/* Higgs encode quantizer without projections
+ * (src/models/higgs_audio_tts/codec.cpp:975-1013): dot = mul_mat(codebook, r)
+ * (MatMulModule, src/framework/modules/primitive_modules.cpp:186-212),
+ * x2 = sum_rows(r*r), e2 = sum_rows(c*c) on the F32 (dequantised) codebook,
+ * logits = ((scale(dot, 2) - x2) - e2), argmax, optional top_k
+ * (ops.cpp:8423-8456), get_rows(codebook) (dequantised for Q8_0), sub.
+ * For a Q8_0 codebook the F32 operand is quantised by x86
+ * quantize_row_q8_0 before the integer product (ggml-cpu.c:1309-1340). */
+int aqo_higgs_rvq(const float *x, int64_t M, int64_t K, int64_t Q, int64_t N,
+                  const void *cb, int cb_type, int topk, const int32_t *force_idx,
+                  int32_t *idx, float *residual, float *dist,
+                  int32_t *topk_idx, float *topk_logit) {
+    const int64_t nb = K / 32;
+    float *r = residual;
+    memcpy(r, x, (size_t)(M * K) * sizeof(float));
+    float *cbf = (float *)malloc((size_t)(N * K) * sizeof(float));
+    float *e2 = (float *)malloc((size_t)N * sizeof(float));
+    float *lg = (float *)malloc((size_t)N * sizeof(float));
+    float *tmp = (float *)malloc((size_t)(K > N ? K : N) * sizeof(float));
+    aqo_block_q8_0 *xq = (aqo_block_q8_0 *)malloc((size_t)(nb > 0 ? nb : 1) * sizeof(aqo_block_q8_0));
+    aqo_pair *pairs = (aqo_pair *)malloc((size_t)N * sizeof(aqo_pair));
+    if (!cbf || !e2 || !lg || !tmp || !xq || !pairs) {
+        free(cbf); free(e2); free(lg); free(tmp); free(xq); free(pairs);
+        return -1;
+    }
+    for (int64_t s = 0; s < Q; ++s) {
+        const float *Cf = cb_type == 0 ? (const float *)cb + s * N * K : NULL;
+        const aqo_block_q8_0 *Cq = cb_type == 1 ? (const aqo_block_q8_0 *)cb + s * N * nb : NULL;
+        for (int64_t n = 0; n < N; ++n) {
+            if (Cq) aqo_dequantize_row_q8_0(Cq + n * nb, cbf + n * K, (int)K);
+            else memcpy(cbf + n * K, Cf + n * K, (size_t)K * sizeof(float));
+            for (int64_t k = 0; k < K; ++k) tmp[k] = cbf[n * K + k] * cbf[n * K + k];
+            e2[n] = aqo_sum_f32((int)K, tmp);
+        }
+        for (int64_t m = 0; m < M; ++m) {
+            float *rm = r + m * K;
+            for (int64_t k = 0; k < K; ++k) tmp[k] = rm[k] * rm[k];
+            const float x2 = aqo_sum_f32((int)K, tmp);
+            if (Cq) aqo_quantize_row_q8_0_x86(rm, xq, (int)K);
+            for (int64_t n = 0; n < N; ++n) {
+                const float dot = Cq ? aqo_dot_q8_0((int)nb, Cq + n * nb, xq) : dot_f32(N, M, (int)K, Cf + n * K, rm);
+                lg[n] = ((dot * 2.0f) - x2) - e2[n];
+            }
+            const int code = aqo_argmax_f32((int)N, lg);
+            idx[m * Q + s] = code;
+            if (dist) dist[m * Q + s] = -lg[code];
+            if (topk > 0) {
+                for (int64_t n = 0; n < N; ++n) { pairs[n].v = lg[n]; pairs[n].i = (int32_t)n; }
+                qsort(pairs, (size_t)N, sizeof(aqo_pair), cmp_desc);
+                for (int k = 0; k < topk; ++k) {
+                    topk_idx[(m * Q + s) * topk + k] = pairs[k].i;
+                    topk_logit[(m * Q + s) * topk + k] = pairs[k].v;
+                }
+            }
+            const int use = force_idx ? force_idx[m * Q + s] : code;
+            for (int64_t k = 0; k < K; ++k) rm[k] = rm[k] - cbf[(int64_t)use * K + k];
+        }
+    }
+    free(cbf); free(e2); free(lg); free(tmp); free(xq); free(pairs);
+    return 0;
+}
+
+int aqo_gather_f32(const float *cb, int64_t N, int64_t K, const int32_t *idx, int64_t M, float *out) {
+    for (int64_t m = 0; m < M; ++m) {
+        if (idx[m] < 0 || idx[m] >= N) return -1;
+        memcpy(out + m * K, cb + (int64_t)idx[m] * K, (size_t)K * sizeof(float));
+    }
+    return 0;
+}
+
+int aqo_gather_q8_0(const aqo_block_q8_0 *cb, int64_t N, int64_t K, const int32_t *idx, int64_t M, float *out) {
+    for (int64_t m = 0; m < M; ++m) {
+        if (idx[m] < 0 || idx[m] >= N) return -1;
+        aqo_dequantize_row_q8_0(cb + (int64_t)idx[m] * (K / 32), out + m * K, (int)K);
+    }
+    return 0;
+}

@@ -1,0 +1,77 @@
+/*
+ * aq_oracle.h -- CPU restatement of the reference quantizer path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load this library, and only as the checker
+ * (or as the labelled CPU baseline), never as the thing measured or shipped.
+ *
+ * Every function restates, in plain C, the arithmetic that the reference's
+ * ggml CPU backend (vendored at external/ggml, v0.12.0) performs for the op
+ * it names, on an AVX-512 x86 host built with the reference's defaults
+ * (-O3 -march=native, GCC, -ffp-contract=fast by GNU dialect).  Operation
+ * order, fused multiply-adds, double accumulations and tie rules follow the
+ * cited lines so results are bit-identical, which the CPU tests check against
+ * oracle/_ref (ggml itself) and the golden fixtures.
+ */
+#ifndef AQ_ORACLE_H
+#define AQ_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct {
+    uint16_t d;      /* fp16 scale */
+    int8_t qs[32];
+} aqo_block_q8_0;    /* ggml-common.h:241-246 (34 bytes, packed) */
+
+/* ---- primitives ---------------------------------------------------------- */
+float aqo_vec_dot_f32(int n, const float *x, const float *y);
+float aqo_tinyblas_dot_f32(int k, const float *a, const float *b);
+int   aqo_mul_mat_f32_uses_tinyblas(int64_t m, int64_t n, int64_t k);
+int   aqo_argmax_f32(int n, const float *x);
+float aqo_sum_f32(int n, const float *x);
+uint16_t aqo_fp32_to_fp16(float f);
+float aqo_fp16_to_fp32(uint16_t h);
+void  aqo_quantize_row_q8_0_x86(const float *x, aqo_block_q8_0 *y, int k);
+void  aqo_quantize_row_q8_0_ref(const float *x, aqo_block_q8_0 *y, int k);
+void  aqo_dequantize_row_q8_0(const aqo_block_q8_0 *x, float *y, int k);
+float aqo_dot_q8_0(int nb, const aqo_block_q8_0 *a, const aqo_block_q8_0 *b);
+
+/* ---- whole-path restatements -------------------------------------------- */
+/* DAC cosine RVQ (Fish recipe).  x [B*T, D] frame-major; weights per stage:
+ * w_in [Q,8,D], b_in [Q,8] (nullable), cb [Q,N,8], w_out [Q,D,8],
+ * b_out [Q,D] (nullable).  force_idx [M,Q] (nullable) teacher-forces the code
+ * used for the residual update; idx always receives the computed argmax. */
+int aqo_dac_rvq(const float *x, int64_t B, int64_t T, int64_t D, int64_t Q, int64_t N,
+                const float *w_in, const float *b_in, const float *cb,
+                const float *w_out, const float *b_out, const int32_t *force_idx,
+                int32_t *idx, float *residual, float *recon);
+
+/* OmniVoice-style Euclidean RVQ: logit = dot(2c, r) + (-|c|^2). x [M,K],
+ * cb [Q,N,K].  logit_best [M,Q] nullable. */
+int aqo_euclid_rvq(const float *x, int64_t M, int64_t K, int64_t Q, int64_t N,
+                   const float *cb, const int32_t *force_idx,
+                   int32_t *idx, float *residual, float *logit_best);
+
+/* Higgs-style Euclidean RVQ: logit = ((2*dot) - |x|^2) - |c|^2, F32 codebook
+ * (cb_type 0, [Q,N,K] floats) or Q8_0 (cb_type 1, [Q,N,K/32] blocks).
+ * dist [M,Q] = -logit[idx]; topk_idx/topk_logit [M,Q,topk] sorted by
+ * descending logit, ties by ascending index (ggml's own order is unspecified
+ * and compared as a set). */
+int aqo_higgs_rvq(const float *x, int64_t M, int64_t K, int64_t Q, int64_t N,
+                  const void *cb, int cb_type, int topk, const int32_t *force_idx,
+                  int32_t *idx, float *residual, float *dist,
+                  int32_t *topk_idx, float *topk_logit);
+
+/* Codebook gather (get_rows, ops.cpp:4923-4962 / 4797-4840). Returns -1 on an
+ * out-of-range index (the reference asserts). */
+int aqo_gather_f32(const float *cb, int64_t N, int64_t K, const int32_t *idx, int64_t M, float *out);
+int aqo_gather_q8_0(const aqo_block_q8_0 *cb, int64_t N, int64_t K, const int32_t *idx, int64_t M, float *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,334 @@
+// Reference harness (test infrastructure, never shipped): runs the
+// reference's quantizer op graphs on the reference's own ggml CPU backend,
+// compiled from /root/reference/external/ggml by oracle/Makefile into
+// oracle/_ref/libaqref-*.so.  It is the ground truth that the plain-C
+// restatement (oracle/aq_oracle.c) and the golden fixtures are pinned to.
+//
+// Each entry point builds the same ggml op sequence as one reference recipe:
+//   aqref_dac_rvq     Fish Audio encode quantizer
+//                     src/models/fish_audio/codec.cpp:570-611 (quantize_one
+//                     587-605), normalized_rows 171-189, l2_normalize_last
+//                     323-334, build_quantizer_out 542-550, decode sum 552-568;
+//                     Conv1dModule per-batch conv_1d (conv_modules.cpp:284-341)
+//                     plus add_bias_if_needed (conv_modules.cpp:152-166).
+//   aqref_euclid_rvq  OmniVoice encode quantizer without projections:
+//                     score = Linear(2c, -|c|^2) -> argmax -> lookup -> sub
+//                     src/models/omnivoice/audio_tokenizer.cpp:1227-1253
+//                     (score weights), 1897-1927 (graph).
+//   aqref_higgs_rvq   Higgs-style logits = 2*dot - |x|^2 - |c|^2 with an F32
+//                     or Q8_0 codebook, argmax, optional top_k, lookup, sub
+//                     src/models/higgs_audio_tts/codec.cpp:958-1016.
+//
+// Data layouts at this C boundary (all row-major, frame-major):
+//   x          [M, D]                 M = B*T frames
+//   codebooks  [Q, N, K]  (F32)  or   [Q, N, K/32] block_q8_0 (34 B each)
+//   idx_out    [M, Q] int32
+// All timings cover ggml_graph_compute only (graph build/alloc excluded).
+
+#include "ggml.h"
+#include "ggml-cpu.h"
+
+#include <chrono>
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <vector>
+
+namespace {
+
+struct Ctx {
+    ggml_context * ctx = nullptr;
+    explicit Ctx(size_t bytes) {
+        ggml_init_params p{bytes, nullptr, false};
+        ctx = ggml_init(p);
+    }
+    ~Ctx() { if (ctx) ggml_free(ctx); }
+};
+
+double run_graph(ggml_context * ctx, ggml_tensor * out, int n_threads, ggml_cgraph ** gf_out = nullptr,
+                 ggml_tensor * out2 = nullptr, ggml_tensor * out3 = nullptr, ggml_tensor * out4 = nullptr) {
+    ggml_cgraph * gf = ggml_new_graph_custom(ctx, 8192, false);
+    ggml_build_forward_expand(gf, out);
+    if (out2) ggml_build_forward_expand(gf, out2);
+    if (out3) ggml_build_forward_expand(gf, out3);
+    if (out4) ggml_build_forward_expand(gf, out4);
+    auto t0 = std::chrono::steady_clock::now();
+    ggml_graph_compute_with_ctx(ctx, gf, n_threads);
+    auto t1 = std::chrono::steady_clock::now();
+    if (gf_out) *gf_out = gf;
+    return std::chrono::duration<double, std::milli>(t1 - t0).count();
+}
+
+// Fish normalized_rows (codec.cpp:171-189): double sum of squares, float inverse.
+std::vector<float> fish_normalized_rows(const float * v, int64_t rows, int64_t cols) {
+    std::vector<float> out(static_cast<size_t>(rows * cols), 0.0f);
+    for (int64_t r = 0; r < rows; ++r) {
+        double sum = 0.0;
+        for (int64_t c = 0; c < cols; ++c) {
+            const double d = static_cast<double>(v[r * cols + c]);
+            sum += d * d;
+        }
+        const float inv = sum > 0.0 ? static_cast<float>(1.0 / std::sqrt(sum)) : 0.0f;
+        for (int64_t c = 0; c < cols; ++c) out[r * cols + c] = v[r * cols + c] * inv;
+    }
+    return out;
+}
+
+// Conv1dModule with kernel 1 (conv_modules.cpp:284-341): one ggml_conv_1d per
+// batch element, concatenated along the batch axis, then the repeated bias add.
+// input ne = [T, IC, B], weight ne = [1, IC, OC], bias ne = [OC] or null.
+ggml_tensor * conv1d_k1(ggml_context * ctx, ggml_tensor * input, ggml_tensor * weight, ggml_tensor * bias) {
+    const int64_t T = input->ne[0], IC = input->ne[1], B = input->ne[2];
+    const int64_t OC = weight->ne[2];
+    ggml_tensor * in = ggml_is_contiguous(input) ? input : ggml_cont(ctx, input);
+    ggml_tensor * out = nullptr;
+    if (B == 1) {
+        out = ggml_conv_1d(ctx, weight, in, 1, 0, 1);
+    } else {
+        for (int64_t b = 0; b < B; ++b) {
+            ggml_tensor * mat = ggml_view_2d(ctx, in, T, IC, in->nb[1], static_cast<size_t>(b) * in->nb[2]);
+            ggml_tensor * o = ggml_conv_1d(ctx, weight, mat, 1, 0, 1);
+            o = ggml_reshape_3d(ctx, o, T, OC, 1);
+            out = out ? ggml_concat(ctx, out, o, 2) : o;
+        }
+    }
+    if (bias) {
+        ggml_tensor * bv = ggml_reshape_3d(ctx, bias, 1, OC, 1);
+        ggml_tensor * rep = ggml_repeat(ctx, bv, out);
+        out = ggml_add(ctx, out, rep);
+    }
+    return out;
+}
+
+// l2_normalize_last (fish codec.cpp:323-334) on ne = [C, T, B].  MulModule
+// makes its operands contiguous (primitive_modules.cpp:243-254); ggml_div gets
+// `x` as passed in.
+ggml_tensor * l2_normalize_last(ggml_context * ctx, ggml_tensor * x) {
+    ggml_tensor * xc = ggml_is_contiguous(x) ? x : ggml_cont(ctx, x);
+    ggml_tensor * sq = ggml_mul(ctx, xc, xc);
+    ggml_tensor * sum = ggml_sum_rows(ctx, sq);
+    ggml_tensor * shifted = ggml_scale_bias(ctx, sum, 1.0f, 1.0e-12f);
+    ggml_tensor * denom = ggml_sqrt(ctx, shifted);
+    ggml_tensor * rep = ggml_repeat(ctx, denom, x);
+    return ggml_div(ctx, x, rep);
+}
+
+void to_channel_major(const float * x, int64_t B, int64_t T, int64_t D, float * dst) {
+    for (int64_t b = 0; b < B; ++b)
+        for (int64_t t = 0; t < T; ++t)
+            for (int64_t d = 0; d < D; ++d)
+                dst[(b * D + d) * T + t] = x[(b * T + t) * D + d];
+}
+
+void from_channel_major(const float * src, int64_t B, int64_t T, int64_t D, float * x) {
+    for (int64_t b = 0; b < B; ++b)
+        for (int64_t t = 0; t < T; ++t)
+            for (int64_t d = 0; d < D; ++d)
+                x[(b * T + t) * D + d] = src[(b * D + d) * T + t];
+}
+
+}  // namespace
+
+extern "C" {
+
+int aqref_version(void) { return 1; }
+
+// DAC/Fish cosine RVQ.  Weights per stage s:
+//   w_in  [Q, 8, D]   b_in  [Q, 8]   (may be null -> no bias add)
+//   cb    [Q, N, 8]
+//   w_out [Q, D, 8]   b_out [Q, D]  (may be null)
+// Outputs: idx [M, Q]; residual [M, D] (final); recon [M, D] = sum_s z_s
+// (decode recipe codec.cpp:552-568); stage_res optional [Q, M, D] = residual
+// after each stage.  Returns compute milliseconds.
+double aqref_dac_rvq(const float * x, int64_t B, int64_t T, int64_t D, int64_t Q, int64_t N,
+                     const float * w_in, const float * b_in, const float * cb,
+                     const float * w_out, const float * b_out,
+                     int32_t * idx, float * residual, float * recon, float * stage_res,
+                     int n_threads, int materialize) {
+    ggml_cpu_init();
+    const int64_t M = B * T;
+    double ms = 0.0;
+    std::vector<float> res_cm(static_cast<size_t>(M * D));
+    std::vector<float> rec_cm(static_cast<size_t>(M * D), 0.0f);
+    to_channel_major(x, B, T, D, res_cm.data());
+    std::vector<float> tmp(static_cast<size_t>(M * D));
+    for (int64_t s = 0; s < Q; ++s) {
+        const size_t bytes = static_cast<size_t>(M) * static_cast<size_t>(D + N + 64) * 4 * 12 + (64u << 20);
+        Ctx c(bytes);
+        ggml_context * ctx = c.ctx;
+        ggml_tensor * R = ggml_new_tensor_3d(ctx, GGML_TYPE_F32, T, D, B);
+        std::memcpy(R->data, res_cm.data(), res_cm.size() * 4);
+        ggml_tensor * Win = ggml_new_tensor_3d(ctx, GGML_TYPE_F32, 1, D, 8);
+        std::memcpy(Win->data, w_in + s * 8 * D, static_cast<size_t>(8 * D) * 4);
+        ggml_tensor * Bin = nullptr;
+        if (b_in) {
+            Bin = ggml_new_tensor_1d(ctx, GGML_TYPE_F32, 8);
+            std::memcpy(Bin->data, b_in + s * 8, 8 * 4);
+        }
+        ggml_tensor * CB = ggml_new_tensor_2d(ctx, GGML_TYPE_F32, 8, N);
+        std::memcpy(CB->data, cb + s * N * 8, static_cast<size_t>(N * 8) * 4);
+        ggml_tensor * CBn = ggml_new_tensor_2d(ctx, GGML_TYPE_F32, 8, N);
+        {
+            auto nr = fish_normalized_rows(cb + s * N * 8, N, 8);
+            std::memcpy(CBn->data, nr.data(), nr.size() * 4);
+        }
+        ggml_tensor * Wout = ggml_new_tensor_3d(ctx, GGML_TYPE_F32, 1, 8, D);
+        std::memcpy(Wout->data, w_out + s * D * 8, static_cast<size_t>(D * 8) * 4);
+        ggml_tensor * Bout = nullptr;
+        if (b_out) {
+            Bout = ggml_new_tensor_1d(ctx, GGML_TYPE_F32, D);
+            std::memcpy(Bout->data, b_out + s * D, static_cast<size_t>(D) * 4);
+        }
+        // quantize_one (codec.cpp:587-605)
+        ggml_tensor * projected = conv1d_k1(ctx, R, Win, Bin);                  // [T, 8, B]
+        ggml_tensor * proj_btd = ggml_permute(ctx, projected, 1, 0, 2, 3);     // [8, T, B] view
+        // materialize != 0: the contiguous copy that codec.cpp:324-327 makes on
+        // Metal.  materialize == 0: the view as the CPU branch passes it; ggml's
+        // CPU binary ops read src0 rows as contiguous (binary-ops.cpp:120-136),
+        // so ggml_div then reads the wrong elements (kept only to document it).
+        if (materialize) proj_btd = ggml_cont(ctx, proj_btd);
+        ggml_tensor * pn = l2_normalize_last(ctx, proj_btd);                   // [8, T, B]
+        ggml_tensor * pn2 = ggml_reshape_2d(ctx, ggml_cont(ctx, pn), 8, M);
+        ggml_tensor * logits = ggml_mul_mat(ctx, CBn, pn2);                    // [N, M]
+        ggml_mul_mat_set_prec(logits, GGML_PREC_F32);
+        ggml_tensor * ids = ggml_argmax(ctx, logits);                          // [M]
+        ggml_tensor * emb = ggml_get_rows(ctx, CB, ids);                       // [8, M]
+        ggml_tensor * emb_btd = ggml_reshape_3d(ctx, emb, 8, T, B);
+        ggml_tensor * emb_bdt = ggml_permute(ctx, emb_btd, 1, 0, 2, 3);        // [T, 8, B] view
+        ggml_tensor * z = conv1d_k1(ctx, emb_bdt, Wout, Bout);                 // [T, D, B]
+        ggml_tensor * Rn = ggml_sub(ctx, R, z);
+        ggml_tensor * Rec = ggml_new_tensor_3d(ctx, GGML_TYPE_F32, T, D, B);
+        std::memcpy(Rec->data, rec_cm.data(), rec_cm.size() * 4);
+        ggml_tensor * RecN = s == 0 ? z : ggml_add(ctx, Rec, z);
+        ms += run_graph(ctx, Rn, n_threads, nullptr, ids, RecN);
+        std::memcpy(res_cm.data(), Rn->data, res_cm.size() * 4);
+        std::memcpy(rec_cm.data(), RecN->data, rec_cm.size() * 4);
+        const int32_t * ip = static_cast<const int32_t *>(ids->data);
+        for (int64_t m = 0; m < M; ++m) idx[m * Q + s] = ip[m];
+        if (stage_res) from_channel_major(res_cm.data(), B, T, D, stage_res + s * M * D);
+    }
+    if (residual) from_channel_major(res_cm.data(), B, T, D, residual);
+    if (recon) from_channel_major(rec_cm.data(), B, T, D, recon);
+    return ms;
+}
+
+// OmniVoice-style Euclidean RVQ (no projections): logits = (2c)·x + (-|c|^2).
+// x [M, K]; cb [Q, N, K]; idx [M, Q]; residual [M, K]; logit_best [M, Q] (optional).
+double aqref_euclid_rvq(const float * x, int64_t M, int64_t K, int64_t Q, int64_t N, const float * cb,
+                        int32_t * idx, float * residual, float * logit_best, int n_threads) {
+    ggml_cpu_init();
+    double ms = 0.0;
+    std::vector<float> res(x, x + M * K);
+    for (int64_t s = 0; s < Q; ++s) {
+        const size_t bytes = static_cast<size_t>(M) * static_cast<size_t>(N + 4 * K) * 4 + static_cast<size_t>(N * K) * 12 + (64u << 20);
+        Ctx c(bytes);
+        ggml_context * ctx = c.ctx;
+        const float * cbs = cb + s * N * K;
+        ggml_tensor * R = ggml_new_tensor_2d(ctx, GGML_TYPE_F32, K, M);
+        std::memcpy(R->data, res.data(), res.size() * 4);
+        ggml_tensor * W = ggml_new_tensor_2d(ctx, GGML_TYPE_F32, K, N);
+        ggml_tensor * Bs = ggml_new_tensor_1d(ctx, GGML_TYPE_F32, N);
+        ggml_tensor * CB = ggml_new_tensor_2d(ctx, GGML_TYPE_F32, K, N);
+        std::memcpy(CB->data, cbs, static_cast<size_t>(N * K) * 4);
+        float * wp = static_cast<float *>(W->data);
+        float * bp = static_cast<float *>(Bs->data);
+        for (int64_t r = 0; r < N; ++r) {   // audio_tokenizer.cpp:1227-1237
+            double norm = 0.0;
+            for (int64_t k = 0; k < K; ++k) {
+                const float v = cbs[r * K + k];
+                wp[r * K + k] = 2.0f * v;
+                norm += static_cast<double>(v) * static_cast<double>(v);
+            }
+            bp[r] = static_cast<float>(-norm);
+        }
+        ggml_tensor * lg = ggml_mul_mat(ctx, W, R);                           // [N, M]
+        ggml_mul_mat_set_prec(lg, GGML_PREC_F32);
+        lg = ggml_add(ctx, lg, Bs);
+        ggml_tensor * ids = ggml_argmax(ctx, lg);
+        ggml_tensor * q = ggml_get_rows(ctx, CB, ids);
+        ggml_tensor * Rn = ggml_sub(ctx, R, q);
+        ms += run_graph(ctx, Rn, n_threads, nullptr, ids, lg);
+        std::memcpy(res.data(), Rn->data, res.size() * 4);
+        const int32_t * ip = static_cast<const int32_t *>(ids->data);
+        const float * lp = static_cast<const float *>(lg->data);
+        for (int64_t m = 0; m < M; ++m) {
+            idx[m * Q + s] = ip[m];
+            if (logit_best) logit_best[m * Q + s] = lp[m * N + ip[m]];
+        }
+    }
+    if (residual) std::memcpy(residual, res.data(), res.size() * 4);
+    return ms;
+}
+
+// Higgs-style Euclidean RVQ: logits = scale(dot,2) - |x|^2 - |c|^2 (codec.cpp:975-999).
+// cb_type 0 = F32 codebook [Q, N, K]; 1 = Q8_0 blocks [Q, N, K/32] (34 B each).
+// Outputs: idx [M, Q]; residual [M, K]; dist [M, Q] = -logit[idx] (optional);
+// topk_idx / topk_logit [M, Q, topk] in ggml_top_k order (optional, topk > 0).
+double aqref_higgs_rvq(const float * x, int64_t M, int64_t K, int64_t Q, int64_t N,
+                       const void * cb, int cb_type, int topk,
+                       int32_t * idx, float * residual, float * dist,
+                       int32_t * topk_idx, float * topk_logit, int n_threads) {
+    ggml_cpu_init();
+    double ms = 0.0;
+    std::vector<float> res(x, x + M * K);
+    const ggml_type t = cb_type == 1 ? GGML_TYPE_Q8_0 : GGML_TYPE_F32;
+    const size_t cb_bytes = ggml_row_size(t, K) * static_cast<size_t>(N);
+    for (int64_t s = 0; s < Q; ++s) {
+        const size_t bytes = static_cast<size_t>(M) * static_cast<size_t>(N * 4 + 6 * K) * 4 + static_cast<size_t>(N * K) * 16 + (64u << 20);
+        Ctx c(bytes);
+        ggml_context * ctx = c.ctx;
+        ggml_tensor * R = ggml_new_tensor_2d(ctx, GGML_TYPE_F32, K, M);
+        std::memcpy(R->data, res.data(), res.size() * 4);
+        ggml_tensor * CB = ggml_new_tensor_2d(ctx, t, K, N);
+        std::memcpy(CB->data, static_cast<const char *>(cb) + s * cb_bytes, cb_bytes);
+        // MatMulModule(flat, codebook_t) -> ggml_mul_mat(codebook, flat) (primitive_modules.cpp:186-212)
+        ggml_tensor * dot = ggml_mul_mat(ctx, CB, R);                           // [N, M]
+        ggml_tensor * x2 = ggml_sum_rows(ctx, ggml_mul(ctx, R, R));              // [1, M]
+        x2 = ggml_repeat(ctx, x2, dot);
+        ggml_tensor * cbf = t == GGML_TYPE_F32 ? CB : ggml_cast(ctx, CB, GGML_TYPE_F32);
+        ggml_tensor * e2 = ggml_sum_rows(ctx, ggml_mul(ctx, cbf, cbf));          // [1, N]
+        e2 = ggml_reshape_2d(ctx, e2, N, 1);
+        e2 = ggml_repeat(ctx, e2, dot);
+        ggml_tensor * lg = ggml_scale(ctx, dot, 2.0f);
+        lg = ggml_sub(ctx, lg, x2);
+        lg = ggml_sub(ctx, lg, e2);
+        ggml_tensor * ids = ggml_argmax(ctx, lg);
+        ggml_tensor * tk = topk > 0 ? ggml_top_k(ctx, lg, topk) : nullptr;
+        ggml_tensor * q = ggml_get_rows(ctx, CB, ids);                          // dequantized rows
+        ggml_tensor * Rn = ggml_sub(ctx, R, q);
+        ms += run_graph(ctx, Rn, n_threads, nullptr, ids, lg, tk);
+        std::memcpy(res.data(), Rn->data, res.size() * 4);
+        const int32_t * ip = static_cast<const int32_t *>(ids->data);
+        const float * lp = static_cast<const float *>(lg->data);
+        for (int64_t m = 0; m < M; ++m) {
+            idx[m * Q + s] = ip[m];
+            if (dist) dist[m * Q + s] = -lp[m * N + ip[m]];
+            if (tk) {
+                const int32_t * tp = static_cast<const int32_t *>(tk->data) + m * topk;
+                for (int k = 0; k < topk; ++k) {
+                    topk_idx[(m * Q + s) * topk + k] = tp[k];
+                    topk_logit[(m * Q + s) * topk + k] = lp[m * N + tp[k]];
+                }
+            }
+        }
+    }
+    if (residual) std::memcpy(residual, res.data(), res.size() * 4);
+    return ms;
+}
+
+// x86 query quantisation as ggml applies it inside mul_mat (quantize_row_q8_0,
+// ggml-cpu/arch/x86/quants.c:302), exposed for known-answer checks.
+void aqref_quantize_row_q8_0(const float * x, void * y, int64_t k) {
+    ggml_cpu_init();
+    const auto * tr = ggml_get_type_traits_cpu(GGML_TYPE_Q8_0);
+    tr->from_float(x, y, k);
+}
+
+// Reference-rounding quantisation (ggml_quantize_chunk -> quantize_row_q8_0_ref,
+// ggml-quants.c:236-256), used by the reference's weight store for Q8_0 weights.
+void aqref_quantize_chunk_q8_0(const float * x, void * y, int64_t rows, int64_t k) {
+    ggml_cpu_init();
+    ggml_quantize_chunk(GGML_TYPE_Q8_0, x, y, 0, rows, k, nullptr);
+}
+
+}  // extern "C"
