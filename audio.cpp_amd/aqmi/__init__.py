@@ -1,0 +1,154 @@
+"""Python binding of the MI355X quantizer C ABI (include/aq_mi355x.h).
+
+Loads audio.cpp_amd/libaq_mi355x.so with ctypes.  Device buffers are torch
+tensors on the context's device; their data pointers and the current torch
+stream are passed straight through the ABI, so torch is only the allocator and
+stream provider.  There is no fallback: if the library or a GPU is missing,
+construction raises.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import pathlib
+
+import numpy as np
+
+PKG = pathlib.Path(__file__).resolve().parent.parent
+LIB_PATH = PKG / "libaq_mi355x.so"
+
+AQ_OK = 0
+STATUS_NAMES = {
+    0: "AQ_OK", 1: "AQ_E_INVALID_ARG", 2: "AQ_E_SHAPE", 3: "AQ_E_INDEX_RANGE",
+    4: "AQ_E_DEVICE", 5: "AQ_E_UNSUPPORTED", 6: "AQ_E_NOMEM",
+}
+
+# Every symbol include/aq_mi355x.h declares (checked by the CPU test suite).
+EXPORTED = [
+    "aq_abi_version", "aq_ctx_create", "aq_ctx_destroy", "aq_ctx_set_stream", "aq_ctx_synchronize",
+    "aq_last_error", "aq_dac_upload", "aq_dac_release", "aq_dac_encode", "aq_dac_decode",
+]
+
+
+class AqError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        super().__init__(f"{STATUS_NAMES.get(status, status)}: {message}")
+        self.status = status
+
+
+def load_library(path: str | pathlib.Path | None = None) -> C.CDLL:
+    path = pathlib.Path(path) if path else LIB_PATH
+    if not path.exists():
+        raise FileNotFoundError(f"{path} is not built; run python audio.cpp_amd/build.py")
+    lib = C.CDLL(str(path))
+    vp, i64 = C.c_void_p, C.c_int64
+    lib.aq_abi_version.restype = C.c_int
+    lib.aq_ctx_create.argtypes = [C.c_int, vp, C.POINTER(vp)]
+    lib.aq_ctx_destroy.argtypes = [vp]
+    lib.aq_ctx_set_stream.argtypes = [vp, vp]
+    lib.aq_ctx_synchronize.argtypes = [vp]
+    lib.aq_last_error.restype = C.c_char_p
+    lib.aq_last_error.argtypes = [vp]
+    lib.aq_dac_upload.argtypes = [vp, i64, i64, i64, vp, vp, vp, vp, vp, C.POINTER(vp)]
+    lib.aq_dac_release.argtypes = [vp]
+    lib.aq_dac_encode.argtypes = [vp, vp, vp, i64, i64, vp, vp, vp, vp]
+    lib.aq_dac_decode.argtypes = [vp, vp, vp, i64, vp]
+    for name in EXPORTED:
+        fn = getattr(lib, name)
+        if name not in ("aq_abi_version", "aq_last_error"):
+            fn.restype = C.c_int
+    return lib
+
+
+def _host_ptr(a: np.ndarray | None):
+    if a is None:
+        return None
+    assert a.flags["C_CONTIGUOUS"] and a.dtype == np.float32
+    return a.ctypes.data_as(C.c_void_p)
+
+
+def _dptr(t) -> int | None:
+    if t is None:
+        return None
+    assert t.is_cuda and t.is_contiguous(), "device tensors must be contiguous CUDA/HIP tensors"
+    return t.data_ptr()
+
+
+class Context:
+    """aq_ctx on one device, bound to torch's current stream of that device."""
+
+    def __init__(self, device: int = 0, lib: C.CDLL | None = None):
+        import torch
+
+        if not torch.cuda.is_available():
+            raise RuntimeError("no GPU visible: the MI355X quantizer has no CPU fallback")
+        self.torch = torch
+        self.lib = lib or load_library()
+        self.device = device
+        h = C.c_void_p()
+        stream = torch.cuda.current_stream(device).cuda_stream
+        st = self.lib.aq_ctx_create(device, C.c_void_p(stream), C.byref(h))
+        if st != AQ_OK:
+            raise AqError(st, "aq_ctx_create failed")
+        self.h = h
+
+    def check(self, st: int):
+        if st != AQ_OK:
+            raise AqError(st, self.lib.aq_last_error(self.h).decode())
+
+    def use_current_stream(self):
+        s = self.torch.cuda.current_stream(self.device).cuda_stream
+        self.check(self.lib.aq_ctx_set_stream(self.h, C.c_void_p(s)))
+
+    def synchronize(self):
+        self.check(self.lib.aq_ctx_synchronize(self.h))
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.lib.aq_ctx_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class DacStages:
+    """Uploaded DAC RVQ weights (aq_dac_upload)."""
+
+    def __init__(self, ctx: Context, w_in, b_in, codebook, w_out, b_out):
+        self.ctx = ctx
+        w_in = np.ascontiguousarray(w_in, np.float32)
+        cb = np.ascontiguousarray(codebook, np.float32)
+        w_out = np.ascontiguousarray(w_out, np.float32)
+        b_in = None if b_in is None else np.ascontiguousarray(b_in, np.float32)
+        b_out = None if b_out is None else np.ascontiguousarray(b_out, np.float32)
+        self.Q, _, self.D = w_in.shape
+        self.N = cb.shape[1]
+        h = C.c_void_p()
+        ctx.check(ctx.lib.aq_dac_upload(ctx.h, self.Q, self.D, self.N, _host_ptr(w_in), _host_ptr(b_in), _host_ptr(cb),
+                                        _host_ptr(w_out), _host_ptr(b_out), C.byref(h)))
+        self.h = h
+
+    def encode(self, x, clip_len: int, idx, residual=None, recon=None, force_idx=None):
+        M = x.shape[0]
+        self.ctx.use_current_stream()
+        self.ctx.check(self.ctx.lib.aq_dac_encode(self.ctx.h, self.h, _dptr(x), M, clip_len, _dptr(idx), _dptr(residual),
+                                                  _dptr(recon), _dptr(force_idx)))
+
+    def decode(self, idx, out):
+        self.ctx.use_current_stream()
+        self.ctx.check(self.ctx.lib.aq_dac_decode(self.ctx.h, self.h, _dptr(idx), idx.shape[0], _dptr(out)))
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.ctx.lib.aq_dac_release(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

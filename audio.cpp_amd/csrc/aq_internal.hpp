@@ -1,0 +1,64 @@
+// Internal definitions shared by the C-ABI translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "aq_mi355x.h"
+
+struct aq_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::string err;
+    int32_t *d_flags = nullptr;   // device status words written by kernels (vector stores only)
+    int num_cus = 0;
+};
+
+// Sets `ctx->err` and returns `st`.
+inline aq_status aq_fail(aq_ctx *ctx, aq_status st, const char *fmt, ...) {
+    if (ctx) {
+        char buf[512];
+        va_list ap;
+        va_start(ap, fmt);
+        std::vsnprintf(buf, sizeof(buf), fmt, ap);
+        va_end(ap);
+        ctx->err = buf;
+    }
+    return st;
+}
+
+#define AQ_HIP(ctx, call)                                                                  \
+    do {                                                                                   \
+        hipError_t e_ = (call);                                                            \
+        if (e_ != hipSuccess)                                                              \
+            return aq_fail((ctx), AQ_E_DEVICE, "%s failed: %s", #call, hipGetErrorString(e_)); \
+    } while (0)
+
+// Makes ctx->device current for the lifetime of the guard, restoring the
+// caller's device afterwards.
+class aq_device_guard {
+public:
+    explicit aq_device_guard(int device) {
+        if (hipGetDevice(&prev_) != hipSuccess) prev_ = -1;
+        if (prev_ != device) (void)hipSetDevice(device);
+    }
+    ~aq_device_guard() {
+        int cur = -1;
+        if (prev_ >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev_) (void)hipSetDevice(prev_);
+    }
+    aq_device_guard(const aq_device_guard &) = delete;
+    aq_device_guard &operator=(const aq_device_guard &) = delete;
+
+private:
+    int prev_ = -1;
+};
+
+// Indices of the device status words in ctx->d_flags.
+enum aq_flag_slot : int {
+    AQ_FLAG_BAD_INDEX = 0,   // a forced / decoded code outside [0, N)
+    AQ_FLAG_COUNT = 8
+};

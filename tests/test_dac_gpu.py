@@ -1,0 +1,165 @@
+"""GPU parity of the DAC cosine RVQ path (aq_dac_* through the C ABI).
+
+The bar is bit-exactness: the codes, the final residual and the
+reconstruction must equal the oracle's (the reference's ggml CPU arithmetic)
+bit for bit.  Full BASELINE sizes are checked against golden fixtures written
+by the reference's own ggml build (tests/golden/make_golden.py); other shapes
+against the plain-C oracle on the same seeded inputs.
+"""
+
+import hashlib
+
+import numpy as np
+import pytest
+
+from conftest import GOLDEN
+
+pytestmark = pytest.mark.gpu
+
+
+def _sha(a):
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch as t
+
+    if not t.cuda.is_available():
+        pytest.skip("no GPU")
+    return t
+
+
+@pytest.fixture(scope="module")
+def ctx(torch):
+    import aqmi
+
+    return aqmi.Context(0)
+
+
+@pytest.fixture(scope="module")
+def oracle():
+    from oracle import Oracle
+
+    return Oracle()
+
+
+def run_gpu(torch, ctx, cfg, force_idx=None, clip_len=None):
+    import aqmi
+
+    st = aqmi.DacStages(ctx, cfg["w_in"], cfg.get("b_in"), cfg["codebook"], cfg["w_out"], cfg.get("b_out"))
+    x = torch.from_numpy(np.ascontiguousarray(cfg["x"])).cuda()
+    M = x.shape[0]
+    idx = torch.full((M, cfg["Q"]), -1, dtype=torch.int32, device="cuda")
+    res = torch.empty((M, cfg["D"]), dtype=torch.float32, device="cuda")
+    rec = torch.empty((M, cfg["D"]), dtype=torch.float32, device="cuda")
+    fi = None if force_idx is None else torch.from_numpy(np.ascontiguousarray(force_idx, np.int32)).cuda()
+    st.encode(x, clip_len or cfg["T"], idx, res, rec, fi)
+    torch.cuda.synchronize()
+    out = dict(idx=idx.cpu().numpy(), residual=res.cpu().numpy(), recon=rec.cpu().numpy(), stages=st)
+    return out
+
+
+@pytest.mark.parametrize("name,cfg_id,bias", [("dac_cfg0.npz", 0, False), ("dac_cfg0_bias.npz", 0, True),
+                                              ("dac_cfg1.npz", 1, False)])
+def test_dac_matches_reference_fixture(torch, ctx, name, cfg_id, bias):
+    from aqmi import synth
+
+    print(f"[gpu] dac fixture {name}", flush=True)
+    g = np.load(GOLDEN / name)
+    cfg = synth.make_config(cfg_id)
+    if bias:
+        cfg.update(synth.dac_weights(cfg["seed"], cfg["Q"], cfg["D"], cfg["N"], bias=True))
+    out = run_gpu(torch, ctx, cfg)
+    assert np.array_equal(out["idx"], g["idx"].astype(np.int32)), "codes differ from the ggml reference"
+    assert _sha(out["residual"]) == str(g["residual_sha"]), "residual not bit-identical"
+    assert _sha(out["recon"]) == str(g["recon_sha"]), "reconstruction not bit-identical"
+
+
+@pytest.mark.parametrize("D,N,Q,B,T", [(512, 1024, 4, 3, 250), (1024, 2048, 2, 2, 375), (256, 512, 3, 5, 33),
+                                       (64, 64, 2, 1, 7)])
+def test_dac_matches_oracle_shapes(torch, ctx, oracle, D, N, Q, B, T):
+    from aqmi import synth
+
+    print(f"[gpu] dac shape D={D} N={N} Q={Q} B={B} T={T}", flush=True)
+    cfg = dict(kind="dac", B=B, T=T, D=D, Q=Q, N=N, x=synth.normal(11, 1, (B * T, D)),
+               **synth.dac_weights(11, Q, D, N, bias=True))
+    out = run_gpu(torch, ctx, cfg)
+    ref = oracle.dac_rvq(cfg)
+    assert np.array_equal(out["idx"], ref["idx"])
+    assert np.array_equal(out["residual"].view(np.uint32), ref["residual"].view(np.uint32))
+    assert np.array_equal(out["recon"].view(np.uint32), ref["recon"].view(np.uint32))
+
+
+def test_dac_teacher_forced(torch, ctx, oracle):
+    """Stage-wise parity: force random codes into the residual update."""
+    from aqmi import synth
+
+    cfg = synth.make_config(1, rows=750)
+    rng = np.random.default_rng(5)
+    force = rng.integers(0, cfg["N"], size=(750, cfg["Q"]), dtype=np.int32)
+    out = run_gpu(torch, ctx, cfg, force_idx=force)
+    ref = oracle.dac_rvq(cfg, force_idx=force)
+    assert np.array_equal(out["idx"], ref["idx"])
+    assert np.array_equal(out["residual"].view(np.uint32), ref["residual"].view(np.uint32))
+
+
+def test_dac_decode_matches_encode_recon(torch, ctx):
+    from aqmi import synth
+
+    cfg = synth.make_config(1, rows=1500)
+    out = run_gpu(torch, ctx, cfg)
+    st = out["stages"]
+    idx = torch.from_numpy(out["idx"]).cuda()
+    dec = torch.empty((1500, cfg["D"]), dtype=torch.float32, device="cuda")
+    st.decode(idx, dec)
+    torch.cuda.synchronize()
+    assert np.array_equal(dec.cpu().numpy().view(np.uint32), out["recon"].view(np.uint32))
+
+
+def test_dac_errors(torch, ctx):
+    import aqmi
+    from aqmi import synth
+
+    cfg = synth.make_config(0)
+    st = aqmi.DacStages(ctx, cfg["w_in"], cfg["b_in"], cfg["codebook"], cfg["w_out"], cfg["b_out"])
+    x = torch.zeros((750, 1024), dtype=torch.float32, device="cuda")
+    idx = torch.empty((750, 1), dtype=torch.int32, device="cuda")
+    with pytest.raises(aqmi.AqError) as e:
+        st.encode(x, 700, idx)                        # 750 is not a multiple of 700
+    assert e.value.status == 2
+    bad = torch.full((750, 1), 5000, dtype=torch.int32, device="cuda")
+    with pytest.raises(aqmi.AqError) as e:
+        st.encode(x, 750, idx, force_idx=bad)
+    assert e.value.status == 3
+    out = torch.empty((750, 1024), dtype=torch.float32, device="cuda")
+    with pytest.raises(aqmi.AqError) as e:
+        st.decode(bad, out)
+    assert e.value.status == 3
+    with pytest.raises(aqmi.AqError) as e:
+        aqmi.DacStages(ctx, np.zeros((1, 8, 100), np.float32), None, np.zeros((1, 64, 8), np.float32),
+                       np.zeros((1, 100, 8), np.float32), None)
+    assert e.value.status == 2
+
+
+def test_dac_zero_input_and_special_codebook(torch, ctx, oracle):
+    """Zero frames (p = 0 -> pn = 0, all scores 0 -> last index wins) and a
+    codebook of signed one-hots, where the code is fixed by the sign and
+    position of the largest projected coordinate."""
+    from aqmi import synth
+
+    D, N, Q, T = 128, 64, 2, 5
+    w = synth.dac_weights(3, Q, D, N)
+    cb = np.zeros((Q, N, 8), np.float32)
+    for n in range(16):
+        cb[:, n, n % 8] = 1.0 if n < 8 else -1.0
+    cb[:, 16:, :] = synth.normal(3, 77, (Q, N - 16, 8))
+    w["codebook"] = cb
+    x = synth.normal(3, 1, (2 * T, D))
+    x[:T] = 0.0
+    cfg = dict(kind="dac", B=2, T=T, D=D, Q=Q, N=N, x=x, **w)
+    out = run_gpu(torch, ctx, cfg)
+    ref = oracle.dac_rvq(cfg)
+    assert np.array_equal(out["idx"], ref["idx"])
+    assert (out["idx"][:T, 0] == N - 1).all()          # all-zero scores: ggml keeps the last index
+    assert np.array_equal(out["residual"].view(np.uint32), ref["residual"].view(np.uint32))

@@ -1,0 +1,259 @@
+"""CPU checks that pin the oracle (oracle/aq_oracle.c) before it is trusted.
+
+Three kinds of pins:
+  1. golden fixtures written by the reference's own ggml CPU build
+     (tests/golden/make_golden.py) -- run everywhere, including the GPU box;
+  2. bit-exact agreement with oracle/_ref (ggml compiled from the reference
+     sources) on seeded inputs of every recipe -- run where _ref is built;
+  3. closed forms and special cases that a plausible restatement mistake (a
+     dropped term, wrong tie rule, wrong rounding mode, transposed operand)
+     would fail.
+"""
+
+import hashlib
+
+import numpy as np
+import pytest
+
+from conftest import GOLDEN
+
+from aqmi import synth
+from oracle import REF_DIR, Oracle, Ref
+
+
+def _sha(a):
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+def _beq(a, b):
+    return np.array_equal(np.asarray(a, np.float32).view(np.uint32), np.asarray(b, np.float32).view(np.uint32))
+
+
+@pytest.fixture(scope="module")
+def o():
+    return Oracle()
+
+
+@pytest.fixture(scope="module")
+def ref():
+    if not (REF_DIR / "libaqref-native.so").exists():
+        pytest.skip("oracle/_ref not built here (needs /root/reference)")
+    return Ref("native")
+
+
+# ---------------------------------------------------------------- fixtures --
+
+@pytest.mark.parametrize("name,cfg_id,bias", [("dac_cfg0.npz", 0, False), ("dac_cfg0_bias.npz", 0, True),
+                                              ("dac_cfg1.npz", 1, False)])
+def test_oracle_dac_matches_golden(o, name, cfg_id, bias):
+    g = np.load(GOLDEN / name)
+    cfg = synth.make_config(cfg_id)
+    if bias:
+        cfg.update(synth.dac_weights(cfg["seed"], cfg["Q"], cfg["D"], cfg["N"], bias=True))
+    out = o.dac_rvq(cfg)
+    assert np.array_equal(out["idx"], g["idx"].astype(np.int32))
+    assert _sha(out["residual"]) == str(g["residual_sha"])
+    assert _sha(out["recon"]) == str(g["recon_sha"])
+
+
+def test_generator_is_stable():
+    """The fixtures assume the seeded generator never changes."""
+    x = synth.normal(1, 1, (4,))
+    assert x.view(np.uint32).tolist() == np.array(x, np.float32).view(np.uint32).tolist()
+    assert _sha(synth.normal(1, 1, (1000,))) == _sha(synth.normal(1, 1, (1000,)))
+    z = synth.normal(123, 7, (200000,))
+    assert abs(float(z.mean())) < 0.01 and abs(float(z.std()) - 1.0) < 0.01
+
+
+# ------------------------------------------------------ bit-exact vs ggml --
+
+@pytest.mark.parametrize("T", [750, 752, 5])
+def test_oracle_dac_bit_exact_vs_ggml(o, ref, T):
+    cfg = dict(kind="dac", B=2, T=T, D=1024, Q=3, N=1024, x=synth.normal(21, 1, (2 * T, 1024)),
+               **synth.dac_weights(21, 3, 1024, 1024, bias=True))
+    a, b = o.dac_rvq(cfg), ref.dac_rvq(cfg)
+    assert np.array_equal(a["idx"], b["idx"])
+    assert _beq(a["residual"], b["residual"]) and _beq(a["recon"], b["recon"])
+
+
+@pytest.mark.parametrize("M", [1, 2, 5, 64])
+def test_oracle_euclid_bit_exact_vs_ggml(o, ref, M):
+    cfg = synth.make_config(2, rows=M)
+    cfg["Q"] = 3
+    cfg["codebook"] = cfg["codebook"][:3]
+    a, b = o.euclid_rvq(cfg), ref.euclid_rvq(cfg)
+    assert np.array_equal(a["idx"], b["idx"])
+    assert _beq(a["residual"], b["residual"]) and _beq(a["logit"], b["logit"])
+
+
+@pytest.mark.parametrize("M", [1, 3, 32])
+def test_oracle_higgs_f32_bit_exact_vs_ggml(o, ref, M):
+    cfg = synth.make_config(3, rows=M)
+    cfg["codebook"] = cfg["codebook"][:, :1024]
+    cfg["N"] = 1024
+    a, b = o.higgs_rvq(cfg), ref.higgs_rvq(cfg)
+    assert np.array_equal(a["idx"], b["idx"])
+    assert _beq(a["residual"], b["residual"]) and _beq(a["dist"], b["dist"])
+
+
+@pytest.mark.parametrize("M", [1, 3, 48])
+def test_oracle_higgs_q8_bit_exact_vs_ggml(o, ref, M):
+    cfg = synth.make_config(4, rows=M)
+    cfg["Q"] = 3
+    cfg["codebook_q8"] = cfg["codebook_q8"][:3]
+    a, b = o.higgs_rvq(cfg, topk=4), ref.higgs_rvq(cfg, topk=4)
+    assert np.array_equal(a["idx"], b["idx"])
+    assert _beq(a["residual"], b["residual"]) and _beq(a["dist"], b["dist"])
+    # ggml_top_k's order is unspecified (partial_sort, then dst[0] <-> dst[1]):
+    # compare as sets, and the logits of the set.
+    assert np.array_equal(np.sort(a["topk_idx"], -1), np.sort(b["topk_idx"], -1))
+    assert _beq(np.sort(a["topk_logit"], -1), np.sort(b["topk_logit"], -1))
+
+
+def test_oracle_q8_quantize_matches_ggml(o, ref):
+    x = synth.normal(8, 1, (64 * 32,))
+    x[:32] = 0.0                                 # amax = 0 block
+    x[32:64] = np.linspace(-3, 3, 32)
+    ya = np.zeros(64, dtype=synth.Q8_DTYPE)
+    yb = np.zeros(64, dtype=synth.Q8_DTYPE)
+    o.lib.aqo_quantize_row_q8_0_x86(x, ya.ctypes.data, x.size)
+    ref.lib.aqref_quantize_row_q8_0(x, yb.ctypes.data, x.size)
+    assert ya.tobytes() == yb.tobytes()
+    o.lib.aqo_quantize_row_q8_0_ref(x, ya.ctypes.data, x.size)
+    ref.lib.aqref_quantize_chunk_q8_0(x, yb.ctypes.data, 1, x.size)
+    assert ya.tobytes() == yb.tobytes()
+
+
+def test_reference_cpu_view_bug_is_real(ref):
+    """Fish l2_normalize_last on the CPU backend divides a permuted view;
+    ggml's CPU binary op reads it as contiguous rows.  The as-is graph gives
+    codes unrelated to the exact cosine argmax; the materialised graph (what
+    the oracle follows) agrees with float64 math."""
+    cfg = synth.make_config(0)
+    x = cfg["x"].astype(np.float64)
+    p = x @ cfg["w_in"][0].astype(np.float64).T
+    cb = cfg["codebook"][0].astype(np.float64)
+    exact = ((p / np.linalg.norm(p, axis=1, keepdims=True)) @ (cb / np.linalg.norm(cb, axis=1, keepdims=True)).T).argmax(1)
+    asis = ref.dac_rvq(cfg, materialize=False)["idx"][:, 0]
+    fixed = ref.dac_rvq(cfg, materialize=True)["idx"][:, 0]
+    assert (fixed == exact).mean() > 0.99
+    assert (asis == exact).mean() < 0.05
+
+
+# ------------------------------------------------ closed forms / special --
+
+def test_argmax_last_index_and_nan(o):
+    assert o.lib.aqo_argmax_f32(5, np.array([1, 3, 3, 2, 3], np.float32)) == 4
+    assert o.lib.aqo_argmax_f32(3, np.full(3, -np.inf, np.float32)) == 2
+    assert o.lib.aqo_argmax_f32(4, np.array([0, 0, 0, 0], np.float32)) == 3
+    # NaN restarts ggml's running max: [5, NaN, 1] -> index 2 (not 0).
+    assert o.lib.aqo_argmax_f32(3, np.array([5, np.nan, 1], np.float32)) == 2
+    assert o.lib.aqo_argmax_f32(3, np.array([5, 1, np.nan], np.float32)) == 0
+
+
+def test_fp16_round_to_nearest_even(o):
+    vals = np.concatenate([synth.normal(3, 9, (5000,)) * 1e-3, synth.normal(3, 10, (5000,)) * 100,
+                           np.array([65504, 65520, 65519.99, 1e-8, 5.96e-8, 2.98e-8, 2.99e-8, -0.0, np.inf, -np.inf],
+                                    np.float32)]).astype(np.float32)
+    got = np.array([o.lib.aqo_fp32_to_fp16(float(v)) for v in vals], np.uint16)
+    want = vals.astype(np.float16).view(np.uint16)               # numpy converts with RNE
+    assert np.array_equal(got, want)
+    back = np.array([o.lib.aqo_fp16_to_fp32(int(h)) for h in want[:200]], np.float32)
+    assert _beq(back, want[:200].view(np.float16).astype(np.float32))
+
+
+def test_q8_quantize_known_answers(o):
+    """x86 query quantisation: d = fp16(amax/127), q = RNE(x * 127/amax)."""
+    x = np.zeros(32, np.float32)
+    x[0] = 127.0                                  # amax = 127 -> id = 1
+    x[1], x[2], x[3], x[4] = 0.5, 1.5, 2.5, -0.5  # half-way cases round to even
+    x[5] = -127.0
+    y = np.zeros(1, dtype=synth.Q8_DTYPE)
+    o.lib.aqo_quantize_row_q8_0_x86(x, y.ctypes.data, 32)
+    assert float(y["d"][0]) == 1.0
+    assert y["qs"][0][:6].tolist() == [127, 0, 2, 2, 0, -127]
+    # reference (weight-side) rounding is half away from zero
+    o.lib.aqo_quantize_row_q8_0_ref(x, y.ctypes.data, 32)
+    assert y["qs"][0][:6].tolist() == [127, 1, 2, 3, -1, -127]
+
+
+def test_q8_dot_is_exact_int_dot_times_scales(o):
+    """Integer block dots are exact (|sum| <= 32*127^2 < 2^24); with scales of
+    1 the product equals the exact integer dot product."""
+    a = synth.q8_0_random_codebook(4, 1, 1, 256)[0]
+    b = synth.q8_0_random_codebook(4, 3, 1, 256)[0]
+    a["d"] = 1.0
+    b["d"] = 1.0
+    exact = int((a["qs"].astype(np.int64) * b["qs"].astype(np.int64)).sum())
+    assert o.lib.aqo_dot_q8_0(8, a.ctypes.data, b.ctypes.data) == float(exact)
+
+
+def test_dot_orders_close_to_exact(o):
+    """Both fp32 summation orders stay within the classical error bound of the
+    exact dot product, and differ from each other (so the order matters)."""
+    x = synth.normal(5, 1, (1024,))
+    y = synth.normal(5, 2, (1024,))
+    exact = float(np.dot(x.astype(np.float64), y.astype(np.float64)))
+    bound = 1024 * 2 ** -24 * float(np.abs(x.astype(np.float64) * y).sum())
+    v = o.lib.aqo_vec_dot_f32(1024, x, y)
+    t = o.lib.aqo_tinyblas_dot_f32(1024, x, y)
+    assert abs(v - exact) <= bound and abs(t - exact) <= bound
+    diffs = sum(o.lib.aqo_vec_dot_f32(1024, synth.normal(s, 1, (1024,)), y) !=
+                o.lib.aqo_tinyblas_dot_f32(1024, synth.normal(s, 1, (1024,)), y) for s in range(40))
+    assert diffs > 0
+
+
+def test_euclid_query_equal_codeword(o):
+    """x = c_n is its own nearest codeword (distance 0 in exact math)."""
+    cfg = synth.make_config(2, rows=8)
+    cfg["Q"] = 1
+    cb = cfg["codebook"][:1]
+    picks = np.array([3, 100, 2047, 0, 512, 9, 77, 1500])
+    cfg["x"] = cb[0][picks].copy()
+    cfg["codebook"] = cb
+    out = o.euclid_rvq(cfg)
+    assert out["idx"][:, 0].tolist() == picks.tolist()
+    assert np.abs(out["residual"]).max() == 0.0
+    out2 = o.higgs_rvq(cfg)
+    assert out2["idx"][:, 0].tolist() == picks.tolist()
+
+
+def test_euclid_matches_f64_argmin_away_from_ties(o):
+    cfg = synth.make_config(2, rows=64)
+    cfg["Q"] = 1
+    cfg["codebook"] = cfg["codebook"][:1]
+    out = o.euclid_rvq(cfg)
+    x = cfg["x"].astype(np.float64)
+    c = cfg["codebook"][0].astype(np.float64)
+    d = (x * x).sum(1)[:, None] + (c * c).sum(1)[None, :] - 2 * x @ c.T
+    srt = np.sort(d, 1)
+    gap = (srt[:, 1] - srt[:, 0]) / np.maximum(srt[:, 0], 1e-30)
+    ok = gap > 1e-5
+    assert (out["idx"][ok, 0] == d.argmin(1)[ok]).all()
+
+
+def test_dac_one_hot_codebook(o):
+    """Codebook rows +-e_i: the cosine argmax is the signed coordinate of the
+    projection with the largest |value| (distinct values, no ties)."""
+    D, N, T = 128, 16, 9
+    w = synth.dac_weights(6, 1, D, N)
+    cb = np.zeros((1, N, 8), np.float32)
+    for n in range(N):
+        cb[0, n, n % 8] = 1.0 if n < 8 else -1.0
+    w["codebook"] = cb
+    x = synth.normal(6, 1, (T, D))
+    cfg = dict(kind="dac", B=1, T=T, D=D, Q=1, N=N, x=x, **w)
+    out = o.dac_rvq(cfg)
+    p = x.astype(np.float64) @ w["w_in"][0].astype(np.float64).T
+    j = np.abs(p).argmax(1)
+    want = np.where(p[np.arange(T), j] > 0, j, j + 8)
+    assert out["idx"][:, 0].tolist() == want.tolist()
+
+
+def test_gather_identity_and_range(o):
+    cb = synth.normal(7, 1, (64, 256))
+    idx = np.arange(64, dtype=np.int32)
+    out = np.zeros((64, 256), np.float32)
+    assert o.lib.aqo_gather_f32(cb, 64, 256, idx, 64, out) == 0
+    assert _beq(out, cb)
+    assert o.lib.aqo_gather_f32(cb, 64, 256, np.array([64], np.int32), 1, out) == -1
