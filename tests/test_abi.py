@@ -10,7 +10,7 @@ from conftest import ROOT
 
 def declared_symbols():
     text = (ROOT / "include" / "aq_mi355x.h").read_text()
-    return sorted(set(re.findall(r"^\s*(?:const\s+char\s*\*|aq_status|int)\s+(aq_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:const\s+char\s*\*\s*|aq_status\s+|int\s+)(aq_\w+)\s*\(", text, re.M)))
 
 
 def test_header_declares_entry_points():
@@ -26,7 +26,6 @@ def test_library_exports_every_declared_symbol():
     lib = aqmi.load_library()
     for name in declared_symbols():
         assert hasattr(lib, name), f"{name} declared in aq_mi355x.h but not exported"
-    assert sorted(aqmi.EXPORTED) == sorted(set(aqmi.EXPORTED) & set(declared_symbols())) or True
     assert lib.aq_abi_version() == 1
 
 
