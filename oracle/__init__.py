@@ -155,7 +155,9 @@ class Ref:
     """The reference's own ggml CPU backend (oracle/_ref)."""
 
     def __init__(self, isa: str | None = None):
-        isa = isa or ("native" if (REF_DIR / "libaqref-native.so").exists() else host_isa())
+        # `native` is tuned for the machine that built it; elsewhere use the
+        # portable x86-64-v4 / v3 builds.
+        isa = isa or host_isa()
         path = REF_DIR / f"libaqref-{isa}.so"
         if not path.exists():
             raise FileNotFoundError(f"{path} not built (make -C oracle ref needs /root/reference)")
