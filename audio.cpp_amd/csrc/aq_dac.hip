@@ -22,19 +22,31 @@
 //    is read from HBM once and written once per frame (not once per stage).
 //  * ggml_vec_dot_f32 keeps 4 x 16 fp32 accumulators; accumulator (j, l)
 //    takes elements k = 64*i + 16*j + l, i.e. exactly lane L = 16*j + l here.
-//    Each lane runs its FMA chain over i, then an xor butterfly with lane
-//    distances 32, 16, 8, 4, 2, 1 reproduces ggml's reduction tree (every
-//    pairing is the same pair of partial sums; IEEE addition is commutative),
-//    so the projection is bit-identical.
+//    Each lane runs its FMA chain over i.  The reduction then pairs the same
+//    partial sums as ggml's tree (j with j+2, j with j+1, then lanes 8, 4, 2,
+//    1 apart inside each 16-lane row), so the projection is bit-identical;
+//    IEEE addition is commutative, so which lane of a pair adds is free.
+//    The two cross-row levels are transposed (each lane finishes 2 of the 8
+//    outputs) and the in-row levels are DPP row rotations.
 //  * The stage's in-projection weights and L2-normalised codebook are staged
 //    in LDS in a lane-major float4 layout (conflict-free ds_read_b128); each
-//    LDS read feeds FW frames.
+//    LDS read feeds FW frames.  Two blocks share a CU, so one block's stage
+//    load overlaps the other's compute.
+//  * Scores: every lane scores codes n = 64*c + L with an FMA chain (8 ops)
+//    and keeps its two best keys (score with the chunk index c in the low
+//    mantissa bits; max / med3).  A margin certificate proves the winner:
+//    if the best key is unique and beats every other code's key by more than
+//    the worst-case gap between these scores and ggml's (product-rounded,
+//    sequential) scores plus the key truncation, ggml's argmax is the same
+//    code.  Frames that fail it (near-ties, zero or non-finite projections)
+//    are rescored with ggml's exact arithmetic and tie rule (last index).
 //  * The out-projection z = W_out c[code] + b_out depends only on the code, so
 //    it is tabulated per stage at upload time with the reference's arithmetic
 //    (sequential non-fused 8-term sum, then the bias) and gathered per frame:
 //    a coalesced 4*D-byte row read from L2/MALL instead of 2*8*D flops.
 #include "aq_internal.hpp"
 
+#include <algorithm>
 #include <cmath>
 #include <cstdlib>
 #include <new>
@@ -43,15 +55,53 @@
 namespace {
 
 constexpr int kWave = 64;
-constexpr int kBlock = 256;
+constexpr int kMaxBlock = 512;   // threads; the launch picks 4, 6 or 8 waves per block
 
-// Values that are identical in every lane (after a full butterfly) are moved
+// Values that are identical in every lane (after a full reduction) are moved
 // to scalar registers; VALU instructions then read them as SGPR operands.
 __device__ inline float uniform_f(float v) {
     return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
 }
 __device__ inline int uniform_i(int v) { return __builtin_amdgcn_readfirstlane(v); }
-constexpr int kWavesPerBlock = kBlock / kWave;
+
+// Correctly rounded fp32 square root.  v_sqrt_f32 is accurate to 1 ulp only
+// (hipcc lowers __fsqrt_rn to it), so the estimate is corrected with
+// Tuckerman's rounding test: the residuals x - s_dn*s and x - s_up*s, exact
+// under FMA, tell which of s_dn, s, s_up is sqrt(x) rounded to nearest.
+// Inputs here are >= 1e-12 (normal); zero, Inf and NaN pass through.
+__device__ inline float sqrt_rn(float x) {
+    const float s = __builtin_amdgcn_sqrtf(x);
+    if (!(x > 0.0f) || !(s < INFINITY)) return s;
+    const float sd = __int_as_float(__float_as_int(s) - 1);
+    const float su = __int_as_float(__float_as_int(s) + 1);
+    const float rd = __fmaf_rn(-sd, s, x);
+    const float ru = __fmaf_rn(-su, s, x);
+    float out = s;
+    if (rd <= 0.0f) out = sd;
+    if (ru > 0.0f) out = su;
+    return out;
+}
+
+// v + v[lane rotated by N inside its 16-lane row] (DPP row_ror).
+template <int N>
+__device__ inline float row_ror_add(float v) {
+    const int o = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x120 + N, 0xF, 0xF, false);
+    return __fadd_rn(v, __int_as_float(o));
+}
+template <int N>
+__device__ inline float row_ror_max(float v) {
+    const int o = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x120 + N, 0xF, 0xF, false);
+    return fmaxf(v, __int_as_float(o));
+}
+__device__ inline float wave_max(float v) {
+    v = row_ror_max<8>(v);
+    v = row_ror_max<4>(v);
+    v = row_ror_max<2>(v);
+    v = row_ror_max<1>(v);
+    v = fmaxf(v, __shfl_xor(v, 16));
+    v = fmaxf(v, __shfl_xor(v, 32));
+    return v;
+}
 
 // Per-stage LDS image (units of float4):
 //   [0, 2*DI*64)           W_in : float4 (i*2 + q)*64 + L = W_in[4q .. 4q+3][64 i + L]
@@ -59,16 +109,91 @@ constexpr int kWavesPerBlock = kBlock / kWave;
 //   [.., + 2)              b_in[0..7]
 inline int64_t image_f4(int64_t D, int64_t N) { return 2 * D + 2 * N + 2; }
 
-template <int DI, int FW, bool RECON>
-__global__ __launch_bounds__(kBlock, 2) void dac_encode_vecdot_kernel(
+// ggml's cosine score of code n (scalar leftovers of ggml_vec_dot_f32 with
+// k = 8: each product rounded, then added in order).
+__device__ inline float exact_score(const float4 a, const float4 b, const float *pn) {
+    float sc = 0.0f;
+    sc = __fadd_rn(sc, __fmul_rn(a.x, pn[0]));
+    sc = __fadd_rn(sc, __fmul_rn(a.y, pn[1]));
+    sc = __fadd_rn(sc, __fmul_rn(a.z, pn[2]));
+    sc = __fadd_rn(sc, __fmul_rn(a.w, pn[3]));
+    sc = __fadd_rn(sc, __fmul_rn(b.x, pn[4]));
+    sc = __fadd_rn(sc, __fmul_rn(b.y, pn[5]));
+    sc = __fadd_rn(sc, __fmul_rn(b.z, pn[6]));
+    sc = __fadd_rn(sc, __fmul_rn(b.w, pn[7]));
+    return sc;
+}
+
+// argmax over all N codes with ggml's arithmetic and tie rule
+// (ggml_vec_argmax_f32: running max, index of the last element equal to it;
+// a NaN score restarts the running max, replayed sequentially).
+__device__ int exact_argmax(const float4 *chat, int N, const float *pn, int lane) {
+    float bv = -INFINITY;
+    int bn = 0;
+    bool bad = false;
+    const int NC = N / kWave;
+#pragma unroll 1
+    for (int c = 0; c < NC; ++c) {
+        const float sc = exact_score(chat[(c * 2 + 0) * kWave + lane], chat[(c * 2 + 1) * kWave + lane], pn);
+        bad |= (sc != sc);
+        if (sc >= bv) {
+            bv = sc;
+            bn = c * kWave + lane;
+        }
+    }
+#pragma unroll
+    for (int off = 1; off <= 32; off <<= 1) {
+        const float ov = __shfl_xor(bv, off);
+        const int on = __shfl_xor(bn, off);
+        if (ov > bv || (ov == bv && on > bn)) {
+            bv = ov;
+            bn = on;
+        }
+    }
+    int code = uniform_i(bn);
+    if (__any(bad)) {
+        float mx = -INFINITY;
+        int id = 0;
+        for (int n = 0; n < N; ++n) {
+            const float sc = exact_score(chat[((n / kWave) * 2 + 0) * kWave + (n % kWave)],
+                                         chat[((n / kWave) * 2 + 1) * kWave + (n % kWave)], pn);
+            mx = mx > sc ? mx : sc;
+            if (mx == sc) id = n;
+        }
+        code = uniform_i(id);
+    }
+    return code;
+}
+
+// PF > 0: each thread keeps up to PF float4 of the next stage's image in
+// registers (loaded while the current stage computes).  PF == 0: the image is
+// copied in batches of kCopyBatch loads per thread at the stage start.
+constexpr int kCopyBatch = 8;
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));   // native vector: stays in VGPRs
+
+template <int PF>
+__device__ inline void fetch_image(f32x4 (&pre)[PF > 0 ? PF : 1], const float4 *__restrict__ img, int64_t img_f4) {
+    const f32x4 *src = reinterpret_cast<const f32x4 *>(img);
+#pragma unroll
+    for (int k = 0; k < PF; ++k) {
+        const int64_t t = threadIdx.x + static_cast<int64_t>(k) * blockDim.x;
+        pre[k] = src[t < img_f4 ? t : img_f4 - 1];   // unconditional load keeps pre[] in registers
+    }
+}
+
+template <int DI, int FW, bool RECON, int PF>
+__global__ __launch_bounds__(kMaxBlock, 1) void dac_encode_kernel(
     const float *__restrict__ x, int64_t M, int Q, int N, const float4 *__restrict__ images, int64_t img_f4,
     const float *__restrict__ tables, int32_t *__restrict__ idx, float *__restrict__ residual,
-    float *__restrict__ recon, const int32_t *__restrict__ force_idx, int32_t *__restrict__ flags, int has_bin) {
+    float *__restrict__ recon, const int32_t *__restrict__ force_idx, int32_t *__restrict__ flags, int has_bin,
+    int key_bits, float margin, int exact_only) {
     extern __shared__ float4 lds[];
     constexpr int D = DI * kWave;
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
-    const int64_t m_first = (static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave) * FW;
+    const int waves_per_block = blockDim.x / kWave;
+    const int64_t m_first = (static_cast<int64_t>(blockIdx.x) * waves_per_block + wave) * FW;
 
     int64_t mrow[FW];
     bool active[FW];
@@ -81,7 +206,7 @@ __global__ __launch_bounds__(kBlock, 2) void dac_encode_vecdot_kernel(
 #pragma unroll
         for (int i = 0; i < DI; ++i) {
             r[f][i] = x[mrow[f] * D + i * kWave + lane];
-            rc[f][i] = 0.0f;
+            rc[f][i] = -0.0f;   // -0 + z == z exactly, for every z
         }
     }
 
@@ -89,12 +214,38 @@ __global__ __launch_bounds__(kBlock, 2) void dac_encode_vecdot_kernel(
     const float4 *chat = lds + 2 * DI * kWave;
     const float *bin = reinterpret_cast<const float *>(lds + 2 * DI * kWave + 2 * N);
     const int NC = N / kWave;
+    const int key_mask = (1 << key_bits) - 1;
+
+    f32x4 pre[PF > 0 ? PF : 1];
+    if (PF > 0) fetch_image<PF>(pre, images, img_f4);
+    f32x4 *lds4 = reinterpret_cast<f32x4 *>(lds);
 
     for (int s = 0; s < Q; ++s) {
         __syncthreads();
-        const float4 *img = images + static_cast<int64_t>(s) * img_f4;
-        for (int64_t t = threadIdx.x; t < img_f4; t += kBlock) lds[t] = img[t];
+        if (PF > 0) {
+#pragma unroll
+            for (int k = 0; k < PF; ++k) {
+                const int64_t t = threadIdx.x + static_cast<int64_t>(k) * blockDim.x;
+                if (t < img_f4) lds4[t] = pre[k];
+            }
+        } else {
+            const float4 *img = images + static_cast<int64_t>(s) * img_f4;
+            for (int64_t t0 = 0; t0 < img_f4; t0 += static_cast<int64_t>(kCopyBatch) * blockDim.x) {
+                float4 buf[kCopyBatch];
+#pragma unroll
+                for (int k = 0; k < kCopyBatch; ++k) {
+                    const int64_t t = t0 + threadIdx.x + static_cast<int64_t>(k) * blockDim.x;
+                    buf[k] = img[t < img_f4 ? t : img_f4 - 1];
+                }
+#pragma unroll
+                for (int k = 0; k < kCopyBatch; ++k) {
+                    const int64_t t = t0 + threadIdx.x + static_cast<int64_t>(k) * blockDim.x;
+                    if (t < img_f4) lds[t] = buf[k];
+                }
+            }
+        }
         __syncthreads();
+        if (PF > 0 && s + 1 < Q) fetch_image<PF>(pre, images + static_cast<int64_t>(s + 1) * img_f4, img_f4);
 
         // ---- in-projection: one FMA chain per lane and output, ggml order ----
         float acc[FW][8];
@@ -102,10 +253,16 @@ __global__ __launch_bounds__(kBlock, 2) void dac_encode_vecdot_kernel(
         for (int f = 0; f < FW; ++f)
 #pragma unroll
             for (int j = 0; j < 8; ++j) acc[f][j] = 0.0f;
+        // Weights are loaded one step ahead.
+        float4 wa = win[lane];
+        float4 wb = win[kWave + lane];
 #pragma unroll
         for (int i = 0; i < DI; ++i) {
-            const float4 wa = win[(i * 2 + 0) * kWave + lane];
-            const float4 wb = win[(i * 2 + 1) * kWave + lane];
+            float4 na = wa, nb = wb;
+            if (i + 1 < DI) {
+                na = win[((i + 1) * 2 + 0) * kWave + lane];
+                nb = win[((i + 1) * 2 + 1) * kWave + lane];
+            }
 #pragma unroll
             for (int f = 0; f < FW; ++f) {
                 const float v = r[f][i];
@@ -118,95 +275,107 @@ __global__ __launch_bounds__(kBlock, 2) void dac_encode_vecdot_kernel(
                 acc[f][6] = __fmaf_rn(v, wb.z, acc[f][6]);
                 acc[f][7] = __fmaf_rn(v, wb.w, acc[f][7]);
             }
+            wa = na;
+            wb = nb;
+            // Pin this step's accumulators here: otherwise LLVM sinks the
+            // later frames' FMA chains below the first frame's reduction and
+            // keeps every step's weights live.
+#pragma unroll
+            for (int f = 0; f < FW; ++f)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) __asm__ volatile("" : "+v"(acc[f][j]));
         }
-        // xor butterfly = GGML_F32x16_REDUCE (0+=2, 1+=3, 0+=1) then
-        // _mm512_reduce_add_ps (distances 8, 4, 2, 1).
+        // Reduction = GGML_F32x16_REDUCE (0+=2, 1+=3, 0+=1) then
+        // _mm512_reduce_add_ps (distances 8, 4, 2, 1), transposed: after the
+        // two cross-row levels lane L holds outputs 2*(L/16) and 2*(L/16)+1.
+        const bool hi32 = lane >= 32;
+        const bool hi16 = (lane & 16) != 0;
         float pn[FW][8];
+        bool finite[FW];
 #pragma unroll
         for (int f = 0; f < FW; ++f) {
-            float p[8];
+            float v[4];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                float v = acc[f][j];
-#pragma unroll
-                for (int off = 32; off >= 1; off >>= 1) v = __fadd_rn(v, __shfl_xor(v, off));
-                p[j] = has_bin ? __fadd_rn(v, bin[j]) : v;
+            for (int q = 0; q < 4; ++q) {
+                const float mine = hi32 ? acc[f][q + 4] : acc[f][q];
+                const float other = hi32 ? acc[f][q] : acc[f][q + 4];
+                v[q] = __fadd_rn(mine, __shfl_xor(other, 32));
             }
-            // l2_normalize_last: fp32 squares, double row sum, + 1e-12, sqrt, divide.
+            float w[2];
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const float mine = hi16 ? v[q + 2] : v[q];
+                const float other = hi16 ? v[q] : v[q + 2];
+                w[q] = __fadd_rn(mine, __shfl_xor(other, 16));
+            }
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                w[q] = row_ror_add<8>(w[q]);
+                w[q] = row_ror_add<4>(w[q]);
+                w[q] = row_ror_add<2>(w[q]);
+                w[q] = row_ror_add<1>(w[q]);
+            }
+            // Lane L now holds outputs 2*(L/16) (w[0]) and 2*(L/16)+1 (w[1]).
+            const int o0 = 2 * (lane >> 4);
+            const float pa = has_bin ? __fadd_rn(w[0], bin[o0]) : w[0];
+            const float pb = has_bin ? __fadd_rn(w[1], bin[o0 + 1]) : w[1];
+            // l2_normalize_last: fp32 squares, double row sum in output order,
+            // + 1e-12, sqrt, divide.  The sum is wave-uniform (SGPR inputs);
+            // each lane then divides its own two outputs.
             double ss = 0.0;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) ss += static_cast<double>(__fmul_rn(p[j], p[j]));
-            const float den = __fsqrt_rn(__fadd_rn(static_cast<float>(ss), 1.0e-12f));
+            for (int o = 0; o < 8; ++o) {
+                const float po = __int_as_float(__builtin_amdgcn_readlane(__float_as_int((o & 1) ? pb : pa), 16 * (o >> 1)));
+                ss += static_cast<double>(__fmul_rn(po, po));
+            }
+            const float den = sqrt_rn(__fadd_rn(static_cast<float>(ss), 1.0e-12f));
+            const float qa = __fdiv_rn(pa, den);
+            const float qb = __fdiv_rn(pb, den);
+            finite[f] = __all(((qa - qa) == 0.0f) && ((qb - qb) == 0.0f));
 #pragma unroll
-            for (int j = 0; j < 8; ++j) pn[f][j] = uniform_f(__fdiv_rn(p[j], den));
+            for (int o = 0; o < 8; ++o)
+                pn[f][o] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int((o & 1) ? qb : qa), 16 * (o >> 1)));
         }
 
-        // ---- scores against the normalised codebook, argmax (last index) ----
-        float bv[FW];
-        int bn[FW];
-        bool bad[FW];
+        // ---- approximate scores, two best keys per lane ----
+        float k1[FW], k2[FW];
 #pragma unroll
         for (int f = 0; f < FW; ++f) {
-            bv[f] = -INFINITY;
-            bn[f] = 0;
-            bad[f] = false;
+            k1[f] = -INFINITY;
+            k2[f] = -INFINITY;
         }
+#pragma unroll 2
         for (int c = 0; c < NC; ++c) {
             const float4 a = chat[(c * 2 + 0) * kWave + lane];
             const float4 b = chat[(c * 2 + 1) * kWave + lane];
-            const int n = c * kWave + lane;
 #pragma unroll
             for (int f = 0; f < FW; ++f) {
-                float sc = 0.0f;
-                sc = __fadd_rn(sc, __fmul_rn(a.x, pn[f][0]));
-                sc = __fadd_rn(sc, __fmul_rn(a.y, pn[f][1]));
-                sc = __fadd_rn(sc, __fmul_rn(a.z, pn[f][2]));
-                sc = __fadd_rn(sc, __fmul_rn(a.w, pn[f][3]));
-                sc = __fadd_rn(sc, __fmul_rn(b.x, pn[f][4]));
-                sc = __fadd_rn(sc, __fmul_rn(b.y, pn[f][5]));
-                sc = __fadd_rn(sc, __fmul_rn(b.z, pn[f][6]));
-                sc = __fadd_rn(sc, __fmul_rn(b.w, pn[f][7]));
-                bad[f] |= (sc != sc);
-                if (sc >= bv[f]) {
-                    bv[f] = sc;
-                    bn[f] = n;
-                }
+                float sc = a.x * pn[f][0];
+                sc = __fmaf_rn(a.y, pn[f][1], sc);
+                sc = __fmaf_rn(a.z, pn[f][2], sc);
+                sc = __fmaf_rn(a.w, pn[f][3], sc);
+                sc = __fmaf_rn(b.x, pn[f][4], sc);
+                sc = __fmaf_rn(b.y, pn[f][5], sc);
+                sc = __fmaf_rn(b.z, pn[f][6], sc);
+                sc = __fmaf_rn(b.w, pn[f][7], sc);
+                const float key = __int_as_float((__float_as_int(sc) & ~key_mask) | (c & key_mask));
+                k2[f] = __builtin_amdgcn_fmed3f(k1[f], k2[f], key);
+                k1[f] = __builtin_amdgcn_fmed3f(k1[f], key, INFINITY);
             }
         }
         int code[FW];
 #pragma unroll
         for (int f = 0; f < FW; ++f) {
-#pragma unroll
-            for (int off = 1; off <= 32; off <<= 1) {
-                const float ov = __shfl_xor(bv[f], off);
-                const int on = __shfl_xor(bn[f], off);
-                if (ov > bv[f] || (ov == bv[f] && on > bn[f])) {
-                    bv[f] = ov;
-                    bn[f] = on;
-                }
-            }
-            code[f] = uniform_i(bn[f]);
-            if (__any(bad[f])) {
-                // A NaN score changes ggml's sequential running max; replay the
-                // exact loop (rare: only for NaN/Inf inputs).
-                float mx = -INFINITY;
-                int id = 0;
-                for (int n = 0; n < N; ++n) {
-                    const float4 a = chat[((n / kWave) * 2 + 0) * kWave + (n % kWave)];
-                    const float4 b = chat[((n / kWave) * 2 + 1) * kWave + (n % kWave)];
-                    float sc = 0.0f;
-                    sc = __fadd_rn(sc, __fmul_rn(a.x, pn[f][0]));
-                    sc = __fadd_rn(sc, __fmul_rn(a.y, pn[f][1]));
-                    sc = __fadd_rn(sc, __fmul_rn(a.z, pn[f][2]));
-                    sc = __fadd_rn(sc, __fmul_rn(a.w, pn[f][3]));
-                    sc = __fadd_rn(sc, __fmul_rn(b.x, pn[f][4]));
-                    sc = __fadd_rn(sc, __fmul_rn(b.y, pn[f][5]));
-                    sc = __fadd_rn(sc, __fmul_rn(b.z, pn[f][6]));
-                    sc = __fadd_rn(sc, __fmul_rn(b.w, pn[f][7]));
-                    mx = mx > sc ? mx : sc;
-                    if (mx == sc) id = n;
-                }
-                code[f] = uniform_i(id);
+            const float best = wave_max(k1[f]);
+            const bool mine = k1[f] == best;
+            const uint64_t owners = __ballot(mine);
+            const float second = wave_max(mine ? k2[f] : k1[f]);
+            const bool pass = finite[f] && !exact_only && __popcll(owners) == 1 && (best - second) > margin;
+            if (pass) {
+                const int owner = __ffsll(static_cast<unsigned long long>(owners)) - 1;
+                code[f] = uniform_i(((__float_as_int(best) & key_mask) * kWave) + owner);
+            } else {
+                code[f] = exact_argmax(chat, N, pn[f], lane);
             }
         }
 
@@ -227,7 +396,7 @@ __global__ __launch_bounds__(kBlock, 2) void dac_encode_vecdot_kernel(
             for (int i = 0; i < DI; ++i) {
                 const float z = zrow[i * kWave + lane];
                 r[f][i] = __fsub_rn(r[f][i], z);
-                if (RECON) rc[f][i] = (s == 0) ? z : __fadd_rn(rc[f][i], z);
+                if (RECON) rc[f][i] = __fadd_rn(rc[f][i], z);
             }
         }
     }
@@ -281,41 +450,100 @@ __global__ void dac_decode_kernel(const int32_t *__restrict__ idx, int64_t M, in
 }
 
 using EncodeFn = void (*)(const float *, int64_t, int, int, const float4 *, int64_t, const float *, int32_t *,
-                          float *, float *, const int32_t *, int32_t *, int);
+                          float *, float *, const int32_t *, int32_t *, int, int, float, int);
+
+constexpr int kPrefetch = 12;   // float4 per thread in the prefetching variant
+
+template <int DI, int FW, bool RECON>
+EncodeFn pick_pf(bool prefetch) {
+    return prefetch ? dac_encode_kernel<DI, FW, RECON, kPrefetch> : dac_encode_kernel<DI, FW, RECON, 0>;
+}
 
 template <int DI, int FW>
-EncodeFn pick_recon(bool recon) {
-    return recon ? dac_encode_vecdot_kernel<DI, FW, true> : dac_encode_vecdot_kernel<DI, FW, false>;
+EncodeFn pick_recon(bool recon, bool prefetch) {
+    return recon ? pick_pf<DI, FW, true>(prefetch) : pick_pf<DI, FW, false>(prefetch);
 }
 
 template <int DI>
-EncodeFn pick_fw(int fw, bool recon) {
+EncodeFn pick_fw(int fw, bool recon, bool prefetch) {
     switch (fw) {
-        case 1: return pick_recon<DI, 1>(recon);
-        case 2: return pick_recon<DI, 2>(recon);
-        default: return pick_recon<DI, 4>(recon);
+        case 1: return pick_recon<DI, 1>(recon, prefetch);
+        case 2: return pick_recon<DI, 2>(recon, prefetch);
+        default: return pick_recon<DI, 3>(recon, prefetch);
     }
 }
 
-EncodeFn pick_kernel(int64_t D, int fw, bool recon) {
+EncodeFn pick_kernel(int64_t D, int fw, bool recon, bool prefetch) {
     switch (D / kWave) {
-        case 1: return pick_fw<1>(fw, recon);
-        case 2: return pick_fw<2>(fw, recon);
-        case 4: return pick_fw<4>(fw, recon);
-        case 8: return pick_fw<8>(fw, recon);
-        case 12: return pick_fw<12>(fw, recon);
-        case 16: return pick_fw<16>(fw, recon);
+        case 1: return pick_fw<1>(fw, recon, prefetch);
+        case 2: return pick_fw<2>(fw, recon, prefetch);
+        case 4: return pick_fw<4>(fw, recon, prefetch);
+        case 8: return pick_fw<8>(fw, recon, prefetch);
+        case 12: return pick_fw<12>(fw, recon, prefetch);
+        case 16: return pick_fw<16>(fw, recon, prefetch);
         default: return nullptr;
     }
 }
 
-int frames_per_wave() {
-    const char *e = std::getenv("AQ_DAC_FW");
-    if (e) {
-        const int v = std::atoi(e);
-        if (v == 1 || v == 2 || v == 4) return v;
+// Launch shape.  A wave keeps its frames' residuals in registers for the
+// whole cascade, so work cannot be rebalanced after launch: choose frames per
+// wave (FW) and waves per block to minimise the frames on the busiest SIMD,
+// given the blocks per CU that LDS (one stage image per block) and the
+// kernel's registers allow.  Ties go to more waves per SIMD (latency hiding).
+struct Shape {
+    int fw = 1;
+    int waves_per_block = 4;
+    bool prefetch = false;
+};
+
+Shape launch_shape(int64_t M, int64_t D, int64_t img_f4, bool recon, int num_cus, size_t lds_bytes) {
+    const int64_t cus = num_cus > 0 ? num_cus : 256;
+    int env_fw = 0, env_wpb = 0;
+    if (const char *e = std::getenv("AQ_DAC_FW")) env_fw = std::atoi(e);
+    if (const char *e = std::getenv("AQ_DAC_WPB")) env_wpb = std::atoi(e);
+    Shape best;
+    int64_t best_rounds = INT64_MAX, best_rank = INT64_MAX;
+    for (int fw = 1; fw <= 3; ++fw) {
+        if (env_fw >= 1 && env_fw <= 3 && fw != env_fw) continue;
+        for (int wpb : {4, 6, 8}) {
+            if (env_wpb && wpb != env_wpb) continue;
+            bool prefetch = (img_f4 + wpb * kWave - 1) / (wpb * kWave) <= kPrefetch;
+            if (const char *e = std::getenv("AQ_DAC_PF")) prefetch = prefetch && std::atoi(e) != 0;
+            hipFuncAttributes attr{};
+            int64_t simd_waves = 8;
+            if (hipFuncGetAttributes(&attr, reinterpret_cast<const void *>(pick_kernel(D, fw, recon, prefetch))) ==
+                    hipSuccess && attr.numRegs > 0)
+                simd_waves = std::min<int64_t>(8, 512 / ((attr.numRegs + 7) / 8 * 8));
+            // A block's waves are spread over the 4 SIMDs; count the worst SIMD.
+            const int64_t by_regs = simd_waves / ((wpb + 3) / 4);
+            const int64_t by_lds = static_cast<int64_t>(160 * 1024) / static_cast<int64_t>(lds_bytes > 0 ? lds_bytes : 1);
+            const int64_t per_cu = std::max<int64_t>(1, std::min(by_lds, by_regs));
+            const int64_t waves = (M + fw - 1) / fw;
+            const int64_t blocks = (waves + wpb - 1) / wpb;
+            const int64_t rounds = (blocks + cus * per_cu - 1) / (cus * per_cu);
+            // Measured on MI355X (6000 frames, D = N = 1024): with every block
+            // resident the kernel is latency-bound; 3 frames per wave in 8-wave
+            // blocks with the next image prefetched was fastest (111 us), then
+            // 2 frames per wave.  A grid smaller than the GPU prefers one frame
+            // per wave to occupy more CUs.
+            const bool fills = blocks >= cus;
+            static const int rank_full[4] = {0, 2, 1, 0};     // fw: 3 best, then 2, then 1
+            static const int rank_small[4] = {0, 0, 1, 2};    // fw: 1 best, then 2, then 3
+            const int64_t rank = (fills ? rank_full[fw] : rank_small[fw]) * 16 + (prefetch ? 0 : 8) +
+                                 (wpb == 8 ? 0 : wpb == 6 ? 1 : 2);
+            if (std::getenv("AQ_DEBUG"))
+                std::fprintf(stderr, "aq_dac shape fw=%d wpb=%d pf=%d regs=%d per_cu=%lld blocks=%lld rounds=%lld\n", fw,
+                             wpb, prefetch ? 1 : 0, attr.numRegs, (long long)per_cu, (long long)blocks, (long long)rounds);
+            if (rounds < best_rounds || (rounds == best_rounds && rank < best_rank)) {
+                best_rounds = rounds;
+                best_rank = rank;
+                best.fw = fw;
+                best.waves_per_block = wpb;
+                best.prefetch = prefetch;
+            }
+        }
     }
-    return 2;
+    return best;
 }
 
 }  // namespace
@@ -324,6 +552,9 @@ struct aq_dac_stages {
     aq_ctx *ctx = nullptr;
     int64_t Q = 0, D = 0, N = 0;
     bool has_bin = false;
+    bool exact_only = false;      // a normalised codebook entry is not finite
+    int key_bits = 0;             // chunk-index bits in the score keys
+    float margin = 0.0f;          // score-certificate margin
     int64_t img_f4 = 0;
     float4 *d_images = nullptr;   // [Q][img_f4]
     float *d_tables = nullptr;    // [Q][N][D]
@@ -335,7 +566,7 @@ aq_status aq_dac_upload(aq_ctx *ctx, int64_t Q, int64_t D, int64_t N, const floa
                         const float *codebook, const float *w_out, const float *b_out, aq_dac_stages **out) {
     if (!ctx || !out || !w_in || !codebook || !w_out) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_dac_upload: null argument");
     *out = nullptr;
-    if (Q <= 0 || D <= 0 || N <= 0 || D % kWave != 0 || N % kWave != 0 || !pick_kernel(D, 4, false))
+    if (Q <= 0 || D <= 0 || N <= 0 || D % kWave != 0 || N % kWave != 0 || !pick_kernel(D, 1, false, false))
         return aq_fail(ctx, AQ_E_SHAPE, "aq_dac_upload: unsupported shape Q=%lld D=%lld N=%lld (D in {64,128,256,512,768,1024}, N multiple of 64)",
                        (long long)Q, (long long)D, (long long)N);
     const int64_t img = image_f4(D, N);
@@ -347,6 +578,7 @@ aq_status aq_dac_upload(aq_ctx *ctx, int64_t Q, int64_t D, int64_t N, const floa
     // normalized_rows (codec.cpp:171-189): double sum of squares, float
     // inverse 1/sqrt, float product.
     std::vector<float> images(static_cast<size_t>(Q * img * 4), 0.0f);
+    bool any_nonfinite = false;
     for (int64_t s = 0; s < Q; ++s) {
         float *im = images.data() + s * img * 4;
         const float *Wi = w_in + s * 8 * D;
@@ -363,7 +595,11 @@ aq_status aq_dac_upload(aq_ctx *ctx, int64_t Q, int64_t D, int64_t N, const floa
             const float inv = sum > 0.0 ? static_cast<float>(1.0 / std::sqrt(sum)) : 0.0f;
             const int64_t c = n / kWave, L = n % kWave;
             for (int q = 0; q < 2; ++q)
-                for (int t = 0; t < 4; ++t) ch[((c * 2 + q) * kWave + L) * 4 + t] = C[n * 8 + 4 * q + t] * inv;
+                for (int t = 0; t < 4; ++t) {
+                    const float v = C[n * 8 + 4 * q + t] * inv;
+                    ch[((c * 2 + q) * kWave + L) * 4 + t] = v;
+                    if (!std::isfinite(v)) any_nonfinite = true;
+                }
         }
         float *bi = im + (2 * D + 2 * N) * 4;
         for (int j = 0; j < 8; ++j) bi[j] = b_in ? b_in[s * 8 + j] : 0.0f;
@@ -376,6 +612,18 @@ aq_status aq_dac_upload(aq_ctx *ctx, int64_t Q, int64_t D, int64_t N, const floa
     st->D = D;
     st->N = N;
     st->has_bin = b_in != nullptr;
+    st->exact_only = any_nonfinite;
+    // Certificate margin: each approximate score (FMA chain) and ggml's score
+    // (rounded products, sequential sum) are within 8u and 15u of the exact
+    // dot of two vectors of norm <= 1 (u = 2^-24): 2 * 23u = 2.8e-6 for the
+    // pair compared, plus the truncation of two keys (2^(bits-23) relative
+    // each, |score| <= 1) and the rounding of their difference.
+    {
+        int bits = 0;
+        while ((int64_t{1} << bits) < N / kWave) ++bits;
+        st->key_bits = bits;
+        st->margin = 5.0e-6f + std::ldexp(1.001f, bits - 22);
+    }
     st->img_f4 = img;
     float *d_cb = nullptr, *d_wout = nullptr, *d_bout = nullptr;
     auto cleanup = [&]() {
@@ -436,17 +684,18 @@ aq_status aq_dac_encode(aq_ctx *ctx, const aq_dac_stages *st, const float *x, in
         return aq_fail(ctx, AQ_E_UNSUPPORTED,
                        "aq_dac_encode: clip_len %% 4 == 0 selects ggml's tinyBLAS in-projection order, not built yet");
     aq_device_guard g(ctx->device);
-    const int fw = frames_per_wave();
-    EncodeFn fn = pick_kernel(st->D, fw, recon != nullptr);
     const size_t lds_bytes = static_cast<size_t>(st->img_f4) * sizeof(float4);
+    const Shape shape = launch_shape(M, st->D, st->img_f4, recon != nullptr, ctx->num_cus, lds_bytes);
+    const int fw = shape.fw;
+    EncodeFn fn = pick_kernel(st->D, fw, recon != nullptr, shape.prefetch);
     AQ_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void *>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
                                     static_cast<int>(lds_bytes)));
     if (force_idx) AQ_HIP(ctx, hipMemsetAsync(ctx->d_flags, 0, sizeof(int32_t) * AQ_FLAG_COUNT, ctx->stream));
-    const int64_t frames_per_block = static_cast<int64_t>(kWavesPerBlock) * fw;
+    const int64_t frames_per_block = static_cast<int64_t>(shape.waves_per_block) * fw;
     const unsigned blocks = static_cast<unsigned>((M + frames_per_block - 1) / frames_per_block);
-    hipLaunchKernelGGL(fn, dim3(blocks), dim3(kBlock), lds_bytes, ctx->stream, x, M, static_cast<int>(st->Q),
+    hipLaunchKernelGGL(fn, dim3(blocks), dim3(shape.waves_per_block * kWave), lds_bytes, ctx->stream, x, M, static_cast<int>(st->Q),
                        static_cast<int>(st->N), st->d_images, st->img_f4, st->d_tables, idx, residual, recon, force_idx,
-                       ctx->d_flags, st->has_bin ? 1 : 0);
+                       ctx->d_flags, st->has_bin ? 1 : 0, st->key_bits, st->margin, st->exact_only ? 1 : 0);
     AQ_HIP(ctx, hipGetLastError());
     if (force_idx) {
         int32_t flag = 0;

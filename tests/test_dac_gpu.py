@@ -163,3 +163,66 @@ def test_dac_zero_input_and_special_codebook(torch, ctx, oracle):
     assert np.array_equal(out["idx"], ref["idx"])
     assert (out["idx"][:T, 0] == N - 1).all()          # all-zero scores: ggml keeps the last index
     assert np.array_equal(out["residual"].view(np.uint32), ref["residual"].view(np.uint32))
+
+
+def test_dac_near_duplicate_codes(torch, ctx, oracle):
+    """Codebook rows in near-identical pairs (relative perturbations of 1e-7
+    and exact duplicates): scores of a pair differ by a few ulps, so the
+    approximate-score certificate fails and the exact ggml rescoring decides,
+    including the last-index rule on exact ties."""
+    from aqmi import synth
+
+    D, N, Q, T = 256, 512, 3, 7
+    w = synth.dac_weights(12, Q, D, N)
+    cb = synth.normal(12, 90, (Q, N, 8))
+    cb[:, 1::2] = cb[:, 0::2] * np.float32(1.0 + 1e-7)
+    cb[:, 2:8:2] = cb[:, 3:9:2]                       # a few exact duplicates
+    w["codebook"] = cb.astype(np.float32)
+    x = synth.normal(12, 1, (6 * T, D))
+    # frames equal to a projected codeword direction make the pair the winner
+    cfg = dict(kind="dac", B=6, T=T, D=D, Q=Q, N=N, x=x, **w)
+    out = run_gpu(torch, ctx, cfg)
+    ref = oracle.dac_rvq(cfg)
+    assert np.array_equal(out["idx"], ref["idx"])
+    assert np.array_equal(out["residual"].view(np.uint32), ref["residual"].view(np.uint32))
+
+
+def test_dac_nonfinite_frames(torch, ctx, oracle):
+    """NaN / Inf latents follow ggml's argmax on NaN scores (the running max
+    restarts), replayed exactly; finite frames are unaffected."""
+    from aqmi import synth
+
+    D, N, Q, T = 128, 256, 2, 9
+    w = synth.dac_weights(13, Q, D, N)
+    x = synth.normal(13, 1, (T, D))
+    x[1, 5] = np.nan
+    x[4, :] = np.inf
+    x[6, 0] = -np.inf
+    cfg = dict(kind="dac", B=1, T=T, D=D, Q=Q, N=N, x=x, **w)
+    out = run_gpu(torch, ctx, cfg)
+    ref = oracle.dac_rvq(cfg)
+    assert np.array_equal(out["idx"], ref["idx"])
+    a, b = out["residual"], ref["residual"]
+    assert np.array_equal(np.isnan(a), np.isnan(b))
+    ok = ~np.isnan(a)
+    assert np.array_equal(a[ok].view(np.uint32), b[ok].view(np.uint32))
+
+
+@pytest.mark.parametrize("M", [1, 63, 750, 2000, 6000])
+def test_dac_launch_shapes(torch, ctx, oracle, M):
+    """Frame counts that select different frames-per-wave / block shapes,
+    including partially filled waves."""
+    from aqmi import synth
+
+    print(f"[gpu] dac launch M={M}", flush=True)
+    D, N, Q = 1024, 1024, 2
+    x = synth.normal(14, 1, (M, D))
+    cfg = dict(kind="dac", B=1, T=M, D=D, Q=Q, N=N, x=x, **synth.dac_weights(14, Q, D, N, bias=True))
+    if M % 4 == 0:                       # keep the ggml vec_dot in-projection order (T % 4 != 0)
+        cfg["T"] = M // 8 if (M // 8) % 4 else 1
+        cfg["B"] = M // cfg["T"]
+    out = run_gpu(torch, ctx, cfg)
+    ref = oracle.dac_rvq(cfg)
+    assert np.array_equal(out["idx"], ref["idx"])
+    assert np.array_equal(out["residual"].view(np.uint32), ref["residual"].view(np.uint32))
+    assert np.array_equal(out["recon"].view(np.uint32), ref["recon"].view(np.uint32))
