@@ -27,7 +27,13 @@ STATUS_NAMES = {
 EXPORTED = [
     "aq_abi_version", "aq_ctx_create", "aq_ctx_destroy", "aq_ctx_set_stream", "aq_ctx_synchronize",
     "aq_last_error", "aq_dac_upload", "aq_dac_release", "aq_dac_encode", "aq_dac_decode",
+    "aq_euclid_upload", "aq_euclid_release", "aq_euclid_encode", "aq_euclid_failures", "aq_codebook_gather",
+    "aq_euclid_decode", "aq_ctx_set_timing", "aq_ctx_read_timing",
 ]
+
+# aq_euclid_recipe / aq_codebook_type
+OMNIVOICE, HIGGS, DIRECT = 0, 1, 2
+CB_F32, CB_Q8_0 = 0, 1
 
 
 class AqError(RuntimeError):
@@ -53,6 +59,14 @@ def load_library(path: str | pathlib.Path | None = None) -> C.CDLL:
     lib.aq_dac_release.argtypes = [vp]
     lib.aq_dac_encode.argtypes = [vp, vp, vp, i64, i64, vp, vp, vp, vp]
     lib.aq_dac_decode.argtypes = [vp, vp, vp, i64, vp]
+    lib.aq_ctx_set_timing.argtypes = [vp, C.c_int]
+    lib.aq_ctx_read_timing.argtypes = [vp, vp, C.c_int, C.POINTER(C.c_int)]
+    lib.aq_euclid_upload.argtypes = [vp, i64, i64, i64, C.c_int, vp, C.c_int, C.POINTER(vp)]
+    lib.aq_euclid_release.argtypes = [vp]
+    lib.aq_euclid_encode.argtypes = [vp, vp, vp, i64, vp, vp, vp, C.c_int, vp, vp, vp]
+    lib.aq_euclid_failures.argtypes = [vp, vp, vp]
+    lib.aq_codebook_gather.argtypes = [vp, vp, i64, vp, i64, vp]
+    lib.aq_euclid_decode.argtypes = [vp, vp, vp, i64, vp]
     for name in EXPORTED:
         fn = getattr(lib, name)
         if name not in ("aq_abi_version", "aq_last_error"):
@@ -103,6 +117,16 @@ class Context:
     def synchronize(self):
         self.check(self.lib.aq_ctx_synchronize(self.h))
 
+    def set_timing(self, enable: bool):
+        self.check(self.lib.aq_ctx_set_timing(self.h, 1 if enable else 0))
+
+    def read_timing(self, capacity: int = 1 << 16) -> np.ndarray:
+        """Durations (ms) of the library's main kernels since timing started."""
+        buf = np.zeros(capacity, np.float32)
+        n = C.c_int()
+        self.check(self.lib.aq_ctx_read_timing(self.h, buf.ctypes.data_as(C.c_void_p), capacity, C.byref(n)))
+        return buf[: min(n.value, capacity)].copy()
+
     def close(self):
         if getattr(self, "h", None):
             self.lib.aq_ctx_destroy(self.h)
@@ -145,6 +169,62 @@ class DacStages:
     def close(self):
         if getattr(self, "h", None):
             self.ctx.lib.aq_dac_release(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Codebooks:
+    """Uploaded Euclidean codebooks (aq_euclid_upload).
+
+    codebook: float32 [Q, N, K] (CB_F32) or a structured block_q8_0 array
+    [Q, N, K/32] (CB_Q8_0, dtype aqmi.synth.Q8_DTYPE).  recipe: OMNIVOICE,
+    HIGGS or DIRECT."""
+
+    def __init__(self, ctx: Context, codebook, recipe: int, cb_type: int = CB_F32):
+        self.ctx = ctx
+        if cb_type == CB_F32:
+            cb = np.ascontiguousarray(codebook, np.float32)
+            self.Q, self.N, self.K = cb.shape
+        else:
+            cb = np.ascontiguousarray(codebook)
+            assert cb.dtype.itemsize == 34, "Q8_0 blocks are 34 bytes"
+            self.Q, self.N, nb = cb.shape
+            self.K = nb * 32
+        self.recipe = recipe
+        h = C.c_void_p()
+        ctx.check(ctx.lib.aq_euclid_upload(ctx.h, self.Q, self.N, self.K, cb_type, cb.ctypes.data_as(C.c_void_p),
+                                           recipe, C.byref(h)))
+        self.h = h
+
+    def encode(self, x, idx, residual=None, dist=None, topk: int = 0, topk_idx=None, topk_dist=None,
+               force_idx=None):
+        self.ctx.use_current_stream()
+        self.ctx.check(self.ctx.lib.aq_euclid_encode(self.ctx.h, self.h, _dptr(x), x.shape[0], _dptr(idx),
+                                                     _dptr(residual), _dptr(dist), topk, _dptr(topk_idx),
+                                                     _dptr(topk_dist), _dptr(force_idx)))
+
+    def failures(self) -> np.ndarray:
+        out = np.zeros(64, np.int32)
+        self.ctx.check(self.ctx.lib.aq_euclid_failures(self.ctx.h, self.h, out.ctypes.data_as(C.c_void_p)))
+        return out[: min(self.Q, 64)]
+
+    def gather(self, stage: int, idx, out):
+        self.ctx.use_current_stream()
+        self.ctx.check(self.ctx.lib.aq_codebook_gather(self.ctx.h, self.h, stage, _dptr(idx), idx.shape[0],
+                                                       _dptr(out)))
+
+    def decode(self, idx, out):
+        self.ctx.use_current_stream()
+        self.ctx.check(self.ctx.lib.aq_euclid_decode(self.ctx.h, self.h, _dptr(idx), idx.shape[0], _dptr(out)))
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.ctx.lib.aq_euclid_release(self.h)
             self.h = None
 
     def __del__(self):

@@ -693,9 +693,11 @@ aq_status aq_dac_encode(aq_ctx *ctx, const aq_dac_stages *st, const float *x, in
     if (force_idx) AQ_HIP(ctx, hipMemsetAsync(ctx->d_flags, 0, sizeof(int32_t) * AQ_FLAG_COUNT, ctx->stream));
     const int64_t frames_per_block = static_cast<int64_t>(shape.waves_per_block) * fw;
     const unsigned blocks = static_cast<unsigned>((M + frames_per_block - 1) / frames_per_block);
+    const int tslot = aq_timing_start(ctx);
     hipLaunchKernelGGL(fn, dim3(blocks), dim3(shape.waves_per_block * kWave), lds_bytes, ctx->stream, x, M, static_cast<int>(st->Q),
                        static_cast<int>(st->N), st->d_images, st->img_f4, st->d_tables, idx, residual, recon, force_idx,
                        ctx->d_flags, st->has_bin ? 1 : 0, st->key_bits, st->margin, st->exact_only ? 1 : 0);
+    aq_timing_stop(ctx, tslot);
     AQ_HIP(ctx, hipGetLastError());
     if (force_idx) {
         int32_t flag = 0;

@@ -1,0 +1,1470 @@
+// Euclidean VQ / RVQ encode on gfx950: nearest codeword by bf16 MFMA
+// distance contraction, a per-lane top-L epilogue, a rigorous error
+// certificate, and exact re-ranking in the reference recipe's own fp32
+// arithmetic.  Also the codebook gather and the multi-stage decode sum.
+//
+// Reference recipes (paths relative to the audio.cpp tree):
+//   OMNIVOICE  score weight 2c, bias -(double)|c|^2 cast to float
+//              (src/models/omnivoice/audio_tokenizer.cpp:1227-1237); logits =
+//              mul_mat(2c, r) + bias; ggml_argmax; get_rows; r -= c[code]
+//              (audio_tokenizer.cpp:1897-1927)
+//   HIGGS      logits = ((2 * mul_mat(c, r)) - sum_rows(r*r)) - sum_rows(c*c)
+//              (src/models/higgs_audio_tts/codec.cpp:975-1013), F32 or Q8_0
+//              codebook (a Q8_0 mul_mat quantises r to Q8_0 first)
+//   DIRECT     distance = sum_k (x_k - c_k)^2, rounded products added in
+//              order, first index of the minimum: VectorQuantizer::compute
+//              (src/framework/runtime/host_ops.cpp:236-273) and Qwen3
+//              nearest_code (src/models/qwen3_tts/tokenizer_speech_encoder.cpp:287-303)
+// on the ggml CPU arithmetic (external/ggml/src/ggml-cpu): tinyBLAS F32
+// (llamafile/sgemm.cpp:523-580: 16 FMA lanes, then _mm512_reduce_add_ps),
+// ggml_vec_dot_f32 (vec.cpp:11-135) when tinyBLAS declines, tinyBLAS_Q0 /
+// ggml_vec_dot_q8_0_q8_0 (sgemm.cpp:1353-, arch/x86/quants.c:1170-), x86
+// quantize_row_q8_0 (arch/x86/quants.c:302-), ggml_vec_sum_f32 (vec.h, double
+// accumulation), ggml_vec_argmax_f32 (vec.h:1576-1584, last index of the max).
+//
+// Design
+//  * Scores: v(n) = x~ . c~_n - |c_n|^2/2 with x~, c~ rounded to bf16, from
+//    v_mfma_f32_16x16x32_bf16 with codes as A and frames as B.  Each wave
+//    keeps FG groups of 16 frames of x~ in registers for the whole sweep over
+//    the codebook, which streams through double-buffered, XOR-swizzled LDS
+//    (conflict-free 16-byte reads).  Output lane l owns frame l%16 and codes
+//    4*(l/16)+i of each 16-code block.
+//  * Epilogue per score: key = v with the lane-local code index in the low
+//    mantissa bits; the lane keeps its TOPL best keys (one max + med3 per
+//    level).  The full score matrix never leaves the CU.
+//  * Certificate: for every code, |v(n) - S'(n)| <= E, where S' is the
+//    recipe's value (ggml's fp32 arithmetic) in the same units.  E is built
+//    from the actual rounding residuals (|x~| |c~_n - c_n| + |x~ - x| |c_n|,
+//    Cauchy-Schwarz), the fp32 accumulation bounds and the key truncation.
+//    Kept candidates that could still be in the top T are re-ranked exactly;
+//    the result is certified when the T-th exact value beats every unkept
+//    code's bound.  Otherwise the frame goes to an exact full scan (fallback
+//    kernel), so results never depend on bf16 rounding.
+//  * Residual cascade: per stage one score kernel (re-rank, update r -= c)
+//    and one fallback kernel that exits at once when no frame failed.
+#include "aq_internal.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <new>
+#include <vector>
+
+namespace {
+
+constexpr int kWave = 64;
+constexpr int kWaves = 4;
+constexpr int kThreads = kWave * kWaves;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+enum Recipe : int { OMNI = 0, HIGGS = 1, DIRECT = 2 };
+
+struct StageArgs {
+    const float *xin;        // [M, K] residual entering the stage
+    float *xout;             // [M, K] residual leaving the stage (may alias xin)
+    int64_t M;
+    int N;
+    const uint16_t *cbh;     // [N, K] bf16 codebook (scores)
+    const float *hh;         // [N] |c|^2 / 2
+    const float *cbf;        // [N, K] fp32 codebook (dequantised for Q8_0)
+    const float *bias;       // [N] OmniVoice score bias
+    const float *e2;         // [N] Higgs sum_rows(c*c)
+    const int8_t *q8;        // [N, K] Q8_0 quants
+    const float *q8d;        // [N, K/32] Q8_0 scales (fp32 of fp16)
+    float cmax, dcmax, chmax;   // max |c_n|, max |c~_n - c_n|, max |c~_n|
+    int order;               // exact dot order: 0 tinyBLAS, 1 ggml_vec_dot_f32
+    int Q, s;
+    int32_t *idx;            // [M, Q]
+    float *dist;             // [M, Q] or null
+    int topk;                // 0..4
+    int32_t *topk_idx;       // [M, Q, topk]
+    float *topk_dist;        // [M, Q, topk]
+    const int32_t *force_idx;   // [M, Q] or null
+    int32_t *fail_count;     // this stage's counter
+    int32_t *fail_list;      // [M]
+    int32_t *flags;
+    int exact_only;
+    int64_t debug_frame;     // >= 0: dump this frame's selection state to debug
+    float *debug;            // [4 lanes][64] (AQ_DEBUG_FRAME; diagnostics only)
+};
+
+// --------------------------------------------------------------- exact math
+
+// _mm512_reduce_add_ps order (pairs 8, 4, 2, 1).
+__device__ inline float reduce16(const float (&a)[16]) {
+    float t3[8], t6[4];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) t3[i] = __fadd_rn(a[i + 8], a[i]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) t6[i] = __fadd_rn(t3[i + 4], t3[i]);
+    const float t80 = __fadd_rn(t6[0], t6[2]);
+    const float t81 = __fadd_rn(t6[1], t6[3]);
+    return __fadd_rn(t80, t81);
+}
+
+// hsum of 8 lanes (hsum(__m256) / hsum_float_8): i+4, then 2, then 1.
+__device__ inline float reduce8(const float (&a)[8]) {
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = __fadd_rn(a[i + 4], a[i]);
+    return __fadd_rn(__fadd_rn(v[0], v[2]), __fadd_rn(v[1], v[3]));
+}
+
+// One tinyBLAS<16> element: sa*a . b with 16 FMA accumulators over k = 16l + j.
+// sa is 1 or 2 (exact scaling, OmniVoice's 2c).
+__device__ float dot_tinyblas(const float *__restrict__ a, const float *__restrict__ b, int K, float sa) {
+    float acc[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
+    for (int l = 0; l < K; l += 16) {
+        const f32x4 *pa = reinterpret_cast<const f32x4 *>(a + l);
+        const f32x4 *pb = reinterpret_cast<const f32x4 *>(b + l);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const f32x4 va = pa[q], vb = pb[q];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) acc[4 * q + t] = __fmaf_rn(va[t] * sa, vb[t], acc[4 * q + t]);
+        }
+    }
+    return reduce16(acc);
+}
+
+// ggml_vec_dot_f32, AVX-512 branch: 4 x 16 accumulators over 64-element
+// steps, combined 0+=2, 1+=3, 0+=1, reduced, then scalar leftovers (rounded
+// products added in order).
+__device__ float dot_vecdot(const float *__restrict__ a, const float *__restrict__ b, int K, float sa) {
+    float s[4][16];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int l = 0; l < 16; ++l) s[j][l] = 0.0f;
+    const int np = K & ~63;
+    for (int i = 0; i < np; i += 64) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int l = 0; l < 16; ++l) s[j][l] = __fmaf_rn(a[i + 16 * j + l] * sa, b[i + 16 * j + l], s[j][l]);
+    }
+    float r[16];
+#pragma unroll
+    for (int l = 0; l < 16; ++l) r[l] = __fadd_rn(__fadd_rn(s[0][l], s[2][l]), __fadd_rn(s[1][l], s[3][l]));
+    float sum = reduce16(r);
+    for (int i = np; i < K; ++i) sum = __fadd_rn(sum, __fmul_rn(a[i] * sa, b[i]));
+    return sum;
+}
+
+// ggml_vec_sum_f32 of the fp32 squares (sum_rows(mul(x, x))): double
+// accumulation in order, one rounding to float.
+__device__ float sum_squares(const float *__restrict__ x, int K) {
+    double s = 0.0;
+    for (int k = 0; k < K; ++k) s += static_cast<double>(__fmul_rn(x[k], x[k]));
+    return static_cast<float>(s);
+}
+
+// Direct squared distance: rounded (x - c)^2 added in order.
+__device__ float dist_direct(const float *__restrict__ x, const float *__restrict__ c, int K) {
+    float d = 0.0f;
+    for (int k = 0; k < K; ++k) {
+        const float diff = __fsub_rn(x[k], c[k]);
+        d = __fadd_rn(d, __fmul_rn(diff, diff));
+    }
+    return d;
+}
+
+// x86 quantize_row_q8_0 on one 32-element block: d = amax/127 stored as fp16,
+// id = 127/amax, q = round-half-even(x*id) with int8 saturation.
+__device__ inline void quantize_block_q8(const float *__restrict__ x, int8_t *__restrict__ q, float *__restrict__ d) {
+    float amax = 0.0f;
+    for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(x[j]));
+    const _Float16 h = static_cast<_Float16>(__fdiv_rn(amax, 127.0f));
+    *d = static_cast<float>(h);
+    const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+    for (int j = 0; j < 32; ++j) {
+        const float v = __builtin_rintf(__fmul_rn(x[j], id));
+        int qi;
+        if (!(v >= -2147483648.0f && v < 2147483648.0f)) qi = -128;
+        else qi = static_cast<int>(v) < -128 ? -128 : (static_cast<int>(v) > 127 ? 127 : static_cast<int>(v));
+        q[j] = static_cast<int8_t>(qi);
+    }
+}
+
+// tinyBLAS_Q0 / ggml_vec_dot_q8_0_q8_0: per block, 8 exact 4-element int
+// dots scaled by d_c*d_x and accumulated with FMA, then an 8-lane hsum.
+__device__ float dot_q8(const int8_t *__restrict__ qc, const float *__restrict__ dc, const int8_t *__restrict__ qx,
+                        const float *__restrict__ dx, int nb) {
+    float acc[8];
+#pragma unroll
+    for (int l = 0; l < 8; ++l) acc[l] = 0.0f;
+    for (int ib = 0; ib < nb; ++ib) {
+        const float dd = __fmul_rn(dc[ib], dx[ib]);
+        const int *pc = reinterpret_cast<const int *>(qc + 32 * ib);
+        const int *px = reinterpret_cast<const int *>(qx + 32 * ib);
+#pragma unroll
+        for (int l = 0; l < 8; ++l) {
+            const int s = __builtin_amdgcn_sdot4(pc[l], px[l], 0, false);
+            acc[l] = __fmaf_rn(dd, static_cast<float>(s), acc[l]);
+        }
+    }
+    return reduce8(acc);
+}
+
+// Recipe value of code n ("larger is better" for OMNI/HIGGS: the logit;
+// DIRECT returns the distance, smaller is better).  x2 is sum_rows(x*x)
+// (HIGGS); xq/xd the quantised query (HIGGS with a Q8_0 codebook).
+template <int RECIPE, bool Q8>
+__device__ float exact_value(const StageArgs &a, int K, const float *__restrict__ x, int n, float x2,
+                             const int8_t *xq, const float *xd) {
+    const float *c = a.cbf + static_cast<int64_t>(n) * K;
+    if (RECIPE == DIRECT) return dist_direct(x, c, K);
+    float dot;
+    if (Q8) {
+        dot = dot_q8(a.q8 + static_cast<int64_t>(n) * K, a.q8d + static_cast<int64_t>(n) * (K / 32), xq, xd, K / 32);
+    } else {
+        const float sa = RECIPE == OMNI ? 2.0f : 1.0f;
+        dot = a.order == 0 ? dot_tinyblas(c, x, K, sa) : dot_vecdot(c, x, K, sa);
+    }
+    if (RECIPE == OMNI) return __fadd_rn(dot, a.bias[n]);
+    return __fsub_rn(__fsub_rn(__fmul_rn(dot, 2.0f), x2), a.e2[n]);
+}
+
+// True if (va, na) ranks before (vb, nb): ggml recipes take the larger logit
+// and, on equality, the larger index (argmax keeps the last maximum);
+// DIRECT takes the smaller distance and, on equality, the smaller index.
+template <int RECIPE>
+__device__ inline bool ranks_before(float va, int na, float vb, int nb) {
+    if (RECIPE == DIRECT) return va < vb || (va == vb && na < nb);
+    return va > vb || (va == vb && na > nb);
+}
+// Top-k order for ggml recipes (a set in ggml): value desc, index asc.
+template <int RECIPE>
+__device__ inline bool topk_before(float va, int na, float vb, int nb) {
+    if (RECIPE == DIRECT) return va < vb || (va == vb && na < nb);
+    return va > vb || (va == vb && na < nb);
+}
+
+// --------------------------------------------------------------- score kernel
+
+__device__ inline float key_of(float v, unsigned local, unsigned mask) {
+    return __uint_as_float((__float_as_uint(v) & ~mask) | (local & mask));
+}
+
+template <int KS>
+struct Tile {
+    static constexpr int K = KS * 32;
+    static constexpr int ROWB = K * 2;                         // bytes per bf16 code row
+    static constexpr int CH16 = K / 8;                         // 16-byte chunks per row
+    static constexpr int SWZ = CH16 >= 16 ? 15 : CH16 - 1;     // XOR swizzle mask
+    static constexpr int CC = (32768 / ROWB) >= 16 ? ((32768 / ROWB) / 16) * 16 : 16;   // codes per LDS chunk
+    static constexpr int CHUNKB = CC * ROWB;                   // codebook bytes per chunk
+    static constexpr int BUFB = CHUNKB + CC * 4;               // + |c|^2/2 of the chunk
+    static constexpr int STAGE16 = CHUNKB / 16 / kThreads;     // 16-byte loads per thread per chunk
+    static constexpr int LDS = 2 * BUFB;
+};
+
+template <int RECIPE, bool Q8, int KS, int FG, int TOPL>
+__global__ __launch_bounds__(kThreads, 1) void euclid_stage_kernel(StageArgs a) {
+    using T = Tile<KS>;
+    constexpr int K = T::K;
+    static_assert(T::CHUNKB % (16 * kThreads) == 0, "chunk must split evenly over the block");
+    extern __shared__ __align__(16) unsigned char lds[];
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int col = lane & 15;      // frame within a 16-frame group
+    const int kq = lane >> 4;       // which 8-element quarter of each 32-wide K slice
+    const int64_t m_base = (static_cast<int64_t>(blockIdx.x) * kWaves + wave) * (FG * 16);
+    const int N = a.N;
+
+    // ---- phase 0: frames -> bf16 fragments in registers, rounding norms ----
+    // x~ fragments stay packed (2 bf16 per register) for the whole sweep.
+    u32x4 xb[FG][KS];
+    float nx2[FG], nd2[FG], nq2[FG], nxx2[FG];
+#pragma unroll
+    for (int g = 0; g < FG; ++g) {
+        const int64_t m = m_base + g * 16 + col;
+        const int64_t mc = m < a.M ? m : a.M - 1;
+        const float *xr = a.xin + mc * K;
+        float sx = 0.0f, sd = 0.0f, sq = 0.0f, sxx = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const f32x4 lo = *reinterpret_cast<const f32x4 *>(xr + ks * 32 + kq * 8);
+            const f32x4 hi = *reinterpret_cast<const f32x4 *>(xr + ks * 32 + kq * 8 + 4);
+            const float v[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            u32x4 packed;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+                const bf16x2 pr = {static_cast<__bf16>(v[2 * t]), static_cast<__bf16>(v[2 * t + 1])};
+                const unsigned w = __builtin_bit_cast(unsigned, pr);
+                packed[t] = w;
+                const float r0 = __uint_as_float(w << 16), r1 = __uint_as_float(w & 0xFFFF0000u);
+                sx = __fmaf_rn(r0, r0, sx);
+                sx = __fmaf_rn(r1, r1, sx);
+                const float d0 = v[2 * t] - r0, d1 = v[2 * t + 1] - r1;
+                sd = __fmaf_rn(d0, d0, sd);
+                sd = __fmaf_rn(d1, d1, sd);
+                sxx = __fmaf_rn(v[2 * t], v[2 * t], sxx);
+                sxx = __fmaf_rn(v[2 * t + 1], v[2 * t + 1], sxx);
+            }
+            xb[g][ks] = packed;
+            if (Q8) {
+                // the query block is this K slice: amax over the 4 quarters
+                float am = 0.0f;
+#pragma unroll
+                for (int t = 0; t < 8; ++t) am = fmaxf(am, fabsf(v[t]));
+                am = fmaxf(am, __shfl_xor(am, 16));
+                am = fmaxf(am, __shfl_xor(am, 32));
+                const float dq = static_cast<float>(static_cast<_Float16>(__fdiv_rn(am, 127.0f)));
+                const float id = am != 0.0f ? __fdiv_rn(127.0f, am) : 0.0f;
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    const float q = __builtin_rintf(__fmul_rn(v[t], id));
+                    const float e = v[t] - q * dq;
+                    sq = __fmaf_rn(e, e, sq);
+                }
+            }
+        }
+        sx += __shfl_xor(sx, 16);
+        sx += __shfl_xor(sx, 32);
+        sd += __shfl_xor(sd, 16);
+        sd += __shfl_xor(sd, 32);
+        sxx += __shfl_xor(sxx, 16);
+        sxx += __shfl_xor(sxx, 32);
+        nx2[g] = sx;
+        nd2[g] = sd;
+        nxx2[g] = sxx;
+        if (Q8) {
+            sq += __shfl_xor(sq, 16);
+            sq += __shfl_xor(sq, 32);
+        }
+        nq2[g] = sq;
+    }
+
+    // ---- phase 1: sweep the codebook ----
+    float top[FG][TOPL];
+#pragma unroll
+    for (int g = 0; g < FG; ++g)
+#pragma unroll
+        for (int j = 0; j < TOPL; ++j) top[g][j] = -INFINITY;
+
+    const int nchunks = N / T::CC;
+    int lbits = 0;   // bits of the lane-local code index (N/4 codes per lane)
+    while ((1 << lbits) < N / 4) ++lbits;
+    const unsigned kmask = (1u << lbits) - 1u;
+
+    // Software pipeline over 16-code blocks bb = 0 .. N/16-1 (chunk c = bb/BPC):
+    //  * A fragments live in a ring of R registers, loaded L = R-1 K-slices
+    //    ahead (across the block boundary inside a chunk);
+    //  * the epilogue of block bb-1 runs while block bb's MFMAs execute;
+    //  * the next chunk is staged into the other LDS buffer a few 16-byte
+    //    pieces per block (global load in one block, LDS store in the next),
+    //    with one barrier per chunk.
+    constexpr int BPC = T::CC / 16;
+    constexpr int R = KS % 4 == 0 ? 4 : 2;
+    constexpr int L = R - 1;
+    constexpr int PPB = (T::STAGE16 + BPC - 1) / BPC;   // staged pieces per block
+    const int nblk = N / 16;
+
+    auto lds_a = [&](int buf, int blk, int ks) -> bf16x8 {
+        const int r = blk * 16 + col;
+        const int j = ks * 4 + kq;
+        return *reinterpret_cast<const bf16x8 *>(lds + buf * T::BUFB + r * T::ROWB + ((j ^ (r & T::SWZ)) * 16));
+    };
+    auto lds_h = [&](int buf, int blk) -> f32x4 {
+        return *reinterpret_cast<const f32x4 *>(lds + buf * T::BUFB + T::CHUNKB + (blk * 16 + kq * 4) * 4);
+    };
+    auto piece_dst = [&](int buf, int p) -> u32x4 * {
+        const int r = p / T::CH16, j = p % T::CH16;
+        return reinterpret_cast<u32x4 *>(lds + buf * T::BUFB + r * T::ROWB + ((j ^ (r & T::SWZ)) * 16));
+    };
+    const u32x4 *cb16 = reinterpret_cast<const u32x4 *>(a.cbh);
+
+    // prologue: chunk 0 in full
+    {
+#pragma unroll
+        for (int k = 0; k < T::STAGE16; ++k) {
+            const int p = threadIdx.x + k * kThreads;
+            *piece_dst(0, p) = cb16[p];
+        }
+        if (threadIdx.x < T::CC) reinterpret_cast<float *>(lds + T::CHUNKB)[threadIdx.x] = a.hh[threadIdx.x];
+    }
+    __syncthreads();
+
+    bf16x8 ring[R];
+#pragma unroll
+    for (int l = 0; l < L; ++l) ring[l] = lds_a(0, 0, l);
+    f32x4 hcur = lds_h(0, 0);
+    f32x4 accp[FG];
+    f32x4 hprev = hcur;
+    unsigned lprev = 0;
+    bool pend = false;
+    u32x4 stg[PPB];
+    float hstg = 0.0f;
+
+    auto epilogue = [&](const f32x4 (&acc)[FG], const f32x4 &hv, unsigned local0) {
+#pragma unroll
+        for (int g = 0; g < FG; ++g)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float key = key_of(acc[g][i] - hv[i], local0 + i, kmask);
+#pragma unroll
+                for (int j = TOPL - 1; j > 0; --j) top[g][j] = __builtin_amdgcn_fmed3f(top[g][j - 1], top[g][j], key);
+                top[g][0] = __builtin_amdgcn_fmed3f(top[g][0], key, INFINITY);
+            }
+    };
+
+    for (int bb = 0; bb < nblk; ++bb) {
+        const int c = bb / BPC, b = bb - c * BPC, buf = c & 1;
+        const bool last_in_chunk = b == BPC - 1;
+        const bool next_chunk = (c + 1) * BPC < nblk;
+        if (next_chunk) {
+            // store the pieces fetched in the previous block, fetch this block's
+            if (b > 0) {
+#pragma unroll
+                for (int i = 0; i < PPB; ++i) {
+                    const int k = (b - 1) + i * BPC;
+                    if (k < T::STAGE16) *piece_dst(buf ^ 1, threadIdx.x + k * kThreads) = stg[i];
+                }
+                if (b - 1 == 0 && threadIdx.x < T::CC)
+                    reinterpret_cast<float *>(lds + (buf ^ 1) * T::BUFB + T::CHUNKB)[threadIdx.x] = hstg;
+            }
+            const u32x4 *src = cb16 + static_cast<int64_t>(c + 1) * (T::CHUNKB / 16);
+#pragma unroll
+            for (int i = 0; i < PPB; ++i) {
+                const int k = b + i * BPC;
+                if (k < T::STAGE16) stg[i] = src[threadIdx.x + k * kThreads];
+            }
+            if (b == 0 && threadIdx.x < T::CC) hstg = a.hh[static_cast<int64_t>(c + 1) * T::CC + threadIdx.x];
+        }
+
+        f32x4 acc[FG];
+#pragma unroll
+        for (int g = 0; g < FG; ++g) acc[g] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const int pk = ks + L;
+            if (pk < KS) ring[pk % R] = lds_a(buf, b, pk);
+            else if (!last_in_chunk) ring[pk % R] = lds_a(buf, b + 1, pk - KS);
+#pragma unroll
+            for (int g = 0; g < FG; ++g)
+                acc[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ring[ks % R], __builtin_bit_cast(bf16x8, xb[g][ks]),
+                                                                 acc[g], 0, 0, 0);
+        }
+        const f32x4 hnext = last_in_chunk ? hcur : lds_h(buf, b + 1);
+        if (pend) epilogue(accp, hprev, lprev);
+#pragma unroll
+        for (int g = 0; g < FG; ++g) accp[g] = acc[g];
+        hprev = hcur;
+        lprev = static_cast<unsigned>(bb * 4);
+        pend = true;
+        hcur = hnext;
+        if (last_in_chunk) {
+            if (next_chunk) {
+#pragma unroll
+                for (int i = 0; i < PPB; ++i) {
+                    const int k = (BPC - 1) + i * BPC;
+                    if (k < T::STAGE16) *piece_dst(buf ^ 1, threadIdx.x + k * kThreads) = stg[i];
+                }
+                if (BPC == 1 && threadIdx.x < T::CC)
+                    reinterpret_cast<float *>(lds + (buf ^ 1) * T::BUFB + T::CHUNKB)[threadIdx.x] = hstg;
+            }
+            __syncthreads();
+            if (next_chunk) {
+#pragma unroll
+                for (int l = 0; l < L; ++l) ring[l] = lds_a(buf ^ 1, 0, l);
+                hcur = lds_h(buf ^ 1, 0);
+            }
+        }
+    }
+    if (pend) epilogue(accp, hprev, lprev);
+
+    // ---- phase 2: per-frame certificate and exact re-ranking ----
+    const float u = 5.9604645e-8f;   // 2^-24
+    const int Tk = a.topk > 0 ? a.topk : 1;
+    const bool want_value = a.dist != nullptr || a.topk > 0;
+    int win_code[FG];
+    bool win_ok[FG];
+#pragma unroll
+    for (int g = 0; g < FG; ++g) {
+        const int64_t m = m_base + g * 16 + col;
+        const bool live = m < a.M;
+        const int64_t mc = live ? m : a.M - 1;
+        const float *xr = a.xin + mc * K;
+
+        // Bound E (in units of v = x.c - |c|^2/2) on |v(n) - S'(n)| for every n.
+        const float nx = sqrtf(nx2[g]) * 1.0001f, nd = sqrtf(nd2[g]) * 1.0001f;
+        const float nxe = nx + nd;                           // >= |x|
+        const float e_bf16 = nx * a.dcmax + nd * a.cmax;
+        const float e_acc = (K + 4) * u * nx * a.chmax;
+        const float e_rec = (K + 16) * u * (nxe * a.cmax + nxe * nxe + a.cmax * a.cmax);
+        const float e_q8 = Q8 ? sqrtf(nq2[g]) * 1.0001f * a.cmax : 0.0f;
+        const float vmax = nx * a.chmax + 0.5f * a.cmax * a.cmax + e_rec;
+        const float trunc = ldexpf(vmax, lbits - 23);
+        float E = 1.02f * (e_bf16 + e_acc + e_rec + e_q8 + 4.0f * u * vmax) + trunc + 1e-30f;
+
+        // Keys of the frame's 4 lanes, gathered in every one of them.
+        float all[4 * TOPL];
+#pragma unroll
+        for (int j = 0; j < TOPL; ++j) {
+            const float k0 = top[g][j];
+            const float k1 = __shfl_xor(k0, 16);
+            const float k2 = __shfl_xor(k0, 32);
+            const float k3 = __shfl_xor(k1, 32);
+            all[4 * j + 0] = k0;
+            all[4 * j + 1] = k1;
+            all[4 * j + 2] = k2;
+            all[4 * j + 3] = k3;
+        }
+        // tau bounds every key a lane dropped; vT is the T-th largest kept key.
+        float tau = -INFINITY;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) tau = fmaxf(tau, all[4 * (TOPL - 1) + q]);
+        float best[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+#pragma unroll
+        for (int t = 0; t < 4 * TOPL; ++t) {
+            float v = all[t];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float hi = fmaxf(best[r], v);
+                v = fminf(best[r], v);
+                best[r] = hi;
+            }
+        }
+        const float vT = best[Tk - 1];
+        bool ok = !a.exact_only && (E < INFINITY) && (vT - vT == 0.0f);
+
+        // Candidates this lane must evaluate exactly.
+        float cand_val[TOPL];
+        int cand_n[TOPL];
+        int ncand = 0;
+        const float thr = vT - 2.0f * E;
+        int nabove = 0;
+#pragma unroll
+        for (int t = 0; t < 4 * TOPL; ++t) nabove += all[t] >= thr ? 1 : 0;
+        const bool need_exact = want_value || nabove > 1;
+        float x2 = 0.0f;
+        int8_t xq[Q8 ? K : 1];
+        float xd[Q8 ? K / 32 : 1];
+        if (ok && need_exact) {
+            if (RECIPE != OMNI) x2 = sum_squares(xr, K);
+            if (Q8)
+                for (int ib = 0; ib < K / 32; ++ib) quantize_block_q8(xr + 32 * ib, xq + 32 * ib, xd + ib);
+        }
+#pragma unroll
+        for (int j = 0; j < TOPL; ++j) {
+            cand_n[j] = -1;
+            cand_val[j] = 0.0f;
+            const float key = top[g][j];
+            if (ok && need_exact && key >= thr && key > -INFINITY) {
+                const unsigned local = __float_as_uint(key) & kmask;
+                const int n = static_cast<int>((local >> 2) * 16 + kq * 4 + (local & 3));
+                cand_n[j] = n;
+                cand_val[j] = exact_value<RECIPE, Q8>(a, K, xr, n, x2, xq, xd);
+                ++ncand;
+            }
+        }
+        // Exact top-T over the frame's evaluated candidates (all 4 lanes agree).
+        float sel_v[4];
+        int sel_n[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            sel_v[r] = 0.0f;
+            sel_n[r] = -1;
+        }
+        if (ok && need_exact) {
+            // Branch-free insertion of every evaluated candidate of the
+            // frame's 4 lanes into the ranked list sel[0..Tk).
+#pragma unroll
+            for (int j = 0; j < TOPL; ++j) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    int cn = __shfl(cand_n[j], col + 16 * q);
+                    float cv = __shfl(cand_val[j], col + 16 * q);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const bool before = Tk == 1 ? ranks_before<RECIPE>(cv, cn, sel_v[r], sel_n[r])
+                                                    : topk_before<RECIPE>(cv, cn, sel_v[r], sel_n[r]);
+                        const bool take = cn >= 0 && r < Tk && (sel_n[r] < 0 || before);
+                        const float tv = sel_v[r];
+                        const int tn = sel_n[r];
+                        sel_v[r] = take ? cv : tv;
+                        sel_n[r] = take ? cn : tn;
+                        cv = take ? tv : cv;
+                        cn = take ? tn : cn;
+                    }
+                }
+            }
+            // S' of the T-th exact value in v units, against the bound of unkept codes.
+            if (sel_n[Tk - 1] < 0) {
+                ok = false;
+            } else {
+                const float sv = sel_v[Tk - 1];
+                float sprime;
+                if (RECIPE == OMNI) sprime = 0.5f * sv;
+                else if (RECIPE == HIGGS) sprime = 0.5f * sv + 0.5f * x2;
+                else sprime = -0.5f * sv + 0.5f * nxx2[g];
+                // DIRECT's offset |x|^2/2 comes from fp32 partial sums
+                // (relative error <= (K + 8) u); widen E by it.
+                const float off_err = RECIPE == DIRECT ? 0.5f * (K + 8) * u * nxx2[g] * 1.01f : 0.0f;
+                ok = (sv - sv == 0.0f) && (sprime - off_err > tau + E);
+                // Every evaluated candidate must be finite for the order to be exact.
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (r < Tk && sel_n[r] >= 0 && !(sel_v[r] - sel_v[r] == 0.0f)) ok = false;
+                // With Tk ties at the maximum, a further tie outside the list
+                // could hold the larger index argmax keeps: scan exactly.
+                if (RECIPE != DIRECT && Tk > 1 && sv == sel_v[0]) ok = false;
+            }
+            // argmax among exact ties keeps ggml's last index
+            int w = sel_n[0];
+            if (RECIPE != DIRECT)
+#pragma unroll
+                for (int r = 1; r < 4; ++r)
+                    if (r < Tk && sel_n[r] >= 0 && sel_v[r] == sel_v[0] && sel_n[r] > w) w = sel_n[r];
+            win_code[g] = w;
+        } else {
+            // One candidate clears the threshold: it wins if it also clears
+            // every dropped code by 2E (no exact value is needed).
+            ok = ok && (best[0] - E > tau + E);
+            const float kb = best[0];
+            // owner lane of the best key
+            const bool mine = top[g][0] == kb;
+            const unsigned local = __float_as_uint(kb) & kmask;
+            int n = mine ? static_cast<int>((local >> 2) * 16 + kq * 4 + (local & 3)) : 0x7fffffff;
+            n = min(n, __shfl_xor(n, 16));
+            n = min(n, __shfl_xor(n, 32));
+            win_code[g] = n;
+            ok = ok && n < N;
+        }
+        win_ok[g] = ok;
+        if (a.debug && m == a.debug_frame) {
+            float *d = a.debug + kq * 64;
+            d[0] = E; d[1] = tau; d[2] = vT; d[3] = thr; d[4] = ok ? 1.0f : 0.0f; d[5] = need_exact ? 1.0f : 0.0f;
+            d[6] = static_cast<float>(ncand); d[7] = static_cast<float>(lbits);
+            for (int j = 0; j < TOPL; ++j) {
+                d[8 + j] = top[g][j];
+                d[16 + j] = static_cast<float>(__float_as_uint(top[g][j]) & kmask);
+                d[24 + j] = static_cast<float>(cand_n[j]);
+                d[32 + j] = cand_val[j];
+            }
+            for (int r = 0; r < 4; ++r) {
+                d[40 + r] = static_cast<float>(sel_n[r]);
+                d[44 + r] = sel_v[r];
+            }
+            d[48] = nx; d[49] = nd; d[50] = x2;
+        }
+
+        if (kq == 0 && live) {
+            if (!ok) {
+                const int slot = atomicAdd(a.fail_count, 1);
+                a.fail_list[slot] = static_cast<int32_t>(m);
+            } else {
+                a.idx[m * a.Q + a.s] = win_code[g];
+                if (a.dist) {
+                    const float v = sel_v[0];   // the argmax's value (ties share it)
+                    a.dist[m * a.Q + a.s] = RECIPE == DIRECT ? v : -v;
+                }
+                for (int r = 0; r < a.topk; ++r) {
+                    a.topk_idx[(m * a.Q + a.s) * a.topk + r] = sel_n[r];
+                    a.topk_dist[(m * a.Q + a.s) * a.topk + r] = RECIPE == DIRECT ? sel_v[r] : -sel_v[r];
+                }
+            }
+        }
+    }
+
+    // ---- phase 3: residual update r -= c[code] for certified frames ----
+    // One frame at a time with all 64 lanes: coalesced rows.
+#pragma unroll
+    for (int g = 0; g < FG; ++g) {
+        for (int f = 0; f < 16; ++f) {
+            const int64_t m = m_base + g * 16 + f;
+            if (m >= a.M) break;
+            const int ok = __builtin_amdgcn_readlane(win_ok[g] ? 1 : 0, f);
+            if (!ok) continue;
+            int use = __builtin_amdgcn_readlane(win_code[g], f);
+            if (a.force_idx) {
+                use = a.force_idx[m * a.Q + a.s];
+                if (use < 0 || use >= N) {
+                    if (lane == 0) a.flags[AQ_FLAG_BAD_INDEX] = 1;
+                    use = 0;
+                }
+            }
+            const float *xr = a.xin + m * K;
+            const float *cr = a.cbf + static_cast<int64_t>(use) * K;
+            float *xo = a.xout + m * K;
+            for (int k = lane * 4; k < K; k += kWave * 4) {
+                const f32x4 xv = *reinterpret_cast<const f32x4 *>(xr + k);
+                const f32x4 cv = *reinterpret_cast<const f32x4 *>(cr + k);
+                f32x4 o;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) o[t] = __fsub_rn(xv[t], cv[t]);
+                *reinterpret_cast<f32x4 *>(xo + k) = o;
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------ fallback kernels
+
+// Frames the certificate could not settle get an exact scan of every code,
+// in two launches that each spread over the whole GPU:
+//  * fb_values: a block takes FQ failed frames x 256 codes (one code per
+//    thread), evaluates the recipe value of every (frame, code) pair with one
+//    pass over the code's row, and reduces it to the block's best T codes per
+//    frame (the reference's ranking);
+//  * fb_select: one wave per failed frame merges the per-block candidates,
+//    writes the codes / distances / top-k and updates the residual.  A frame
+//    whose values contain NaN replays ggml_vec_argmax_f32 in code order.
+constexpr int kFQ = 4;        // failed frames per fb_values block
+constexpr int kFbChunk = 256; // codes per fb_values block
+
+struct FbArgs {
+    float *cand_v;     // [M][nch][T]
+    int32_t *cand_n;   // [M][nch][T]
+    int32_t *nan_flag; // [M]
+    int nch;
+};
+
+// Recipe values of code n for FQ query frames held in LDS, one pass over the
+// code's row (tinyBLAS order; the vec_dot order only occurs for M == 1 and is
+// evaluated frame by frame).
+template <int RECIPE, bool Q8>
+__device__ void exact_values_fq(const StageArgs &a, int K, int n, const float *xs, const float *x2, const int8_t *xq,
+                                const float *xd, int nf, float (&out)[kFQ]) {
+    const float *c = a.cbf + static_cast<int64_t>(n) * K;
+    if (RECIPE == DIRECT) {
+        float d[kFQ];
+#pragma unroll
+        for (int f = 0; f < kFQ; ++f) d[f] = 0.0f;
+        for (int k = 0; k < K; ++k) {
+            const float ck = c[k];
+#pragma unroll
+            for (int f = 0; f < kFQ; ++f) {
+                const float diff = __fsub_rn(xs[f * K + k], ck);
+                d[f] = __fadd_rn(d[f], __fmul_rn(diff, diff));
+            }
+        }
+#pragma unroll
+        for (int f = 0; f < kFQ; ++f) out[f] = d[f];
+        return;
+    }
+    float dot[kFQ];
+    if (Q8) {
+        const int8_t *qc = a.q8 + static_cast<int64_t>(n) * K;
+        const float *dc = a.q8d + static_cast<int64_t>(n) * (K / 32);
+        float acc[kFQ][8];
+#pragma unroll
+        for (int f = 0; f < kFQ; ++f)
+#pragma unroll
+            for (int l = 0; l < 8; ++l) acc[f][l] = 0.0f;
+        for (int ib = 0; ib < K / 32; ++ib) {
+            const int *pc = reinterpret_cast<const int *>(qc + 32 * ib);
+            int cw[8];
+#pragma unroll
+            for (int l = 0; l < 8; ++l) cw[l] = pc[l];
+#pragma unroll
+            for (int f = 0; f < kFQ; ++f) {
+                const float dd = __fmul_rn(dc[ib], xd[f * (K / 32) + ib]);
+                const int *px = reinterpret_cast<const int *>(xq + f * K + 32 * ib);
+#pragma unroll
+                for (int l = 0; l < 8; ++l)
+                    acc[f][l] = __fmaf_rn(dd, static_cast<float>(__builtin_amdgcn_sdot4(cw[l], px[l], 0, false)), acc[f][l]);
+            }
+        }
+#pragma unroll
+        for (int f = 0; f < kFQ; ++f) dot[f] = reduce8(acc[f]);
+    } else if (a.order == 0) {
+        const float sa = RECIPE == OMNI ? 2.0f : 1.0f;
+        float acc[kFQ][16];
+#pragma unroll
+        for (int f = 0; f < kFQ; ++f)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) acc[f][j] = 0.0f;
+        for (int l = 0; l < K; l += 16) {
+            float cv[16];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const f32x4 v = *reinterpret_cast<const f32x4 *>(c + l + 4 * q);
+#pragma unroll
+                for (int t = 0; t < 4; ++t) cv[4 * q + t] = v[t] * sa;
+            }
+#pragma unroll
+            for (int f = 0; f < kFQ; ++f)
+#pragma unroll
+                for (int j = 0; j < 16; ++j) acc[f][j] = __fmaf_rn(cv[j], xs[f * K + l + j], acc[f][j]);
+        }
+#pragma unroll
+        for (int f = 0; f < kFQ; ++f) dot[f] = reduce16(acc[f]);
+    } else {
+        const float sa = RECIPE == OMNI ? 2.0f : 1.0f;
+#pragma unroll
+        for (int f = 0; f < kFQ; ++f) dot[f] = f < nf ? dot_vecdot(c, xs + f * K, K, sa) : 0.0f;
+    }
+#pragma unroll
+    for (int f = 0; f < kFQ; ++f)
+        out[f] = RECIPE == OMNI ? __fadd_rn(dot[f], a.bias[n])
+                                : __fsub_rn(__fsub_rn(__fmul_rn(dot[f], 2.0f), x2[f]), a.e2[n]);
+}
+
+template <int RECIPE>
+__device__ inline bool fb_before(float va, int na, float vb, int nb, bool topk) {
+    return topk ? topk_before<RECIPE>(va, na, vb, nb) : ranks_before<RECIPE>(va, na, vb, nb);
+}
+
+template <int RECIPE, bool Q8>
+__global__ __launch_bounds__(kFbChunk) void euclid_fb_values_kernel(StageArgs a, int K, FbArgs fb) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    float *xs = reinterpret_cast<float *>(lds);                         // [kFQ][K]
+    int8_t *xq = reinterpret_cast<int8_t *>(xs + kFQ * K);              // [kFQ][K]
+    float *xd = reinterpret_cast<float *>(xq + kFQ * K);                // [kFQ][K/32]
+    __shared__ float x2s[kFQ];
+    __shared__ float red_v[kFbChunk];
+    __shared__ int red_n[kFbChunk];
+    __shared__ int chosen[4];
+    const int count = *a.fail_count;
+    const int T = a.topk;  // top-k slots (ranked value desc, index asc) ...
+    const int Tc = T + 1;  // ... plus the argmax slot (the reference's tie rule)
+    const int ngroups = (count + kFQ - 1) / kFQ;
+    const int64_t nwork = static_cast<int64_t>(ngroups) * fb.nch;
+    for (int64_t w = blockIdx.x; w < nwork; w += gridDim.x) {
+        const int grp = static_cast<int>(w / fb.nch), ch = static_cast<int>(w % fb.nch);
+        const int nf = min(kFQ, count - grp * kFQ);
+        __syncthreads();
+        for (int i = threadIdx.x; i < kFQ * K; i += kFbChunk) {
+            const int f = i / K, k = i % K;
+            xs[i] = f < nf ? a.xin[static_cast<int64_t>(a.fail_list[grp * kFQ + f]) * K + k] : 0.0f;
+        }
+        __syncthreads();
+        if (threadIdx.x < kFQ) {
+            const int f = threadIdx.x;
+            x2s[f] = RECIPE == OMNI || f >= nf ? 0.0f : sum_squares(xs + f * K, K);
+            if (Q8)
+                for (int ib = 0; ib < K / 32; ++ib) quantize_block_q8(xs + f * K + 32 * ib, xq + f * K + 32 * ib, xd + f * (K / 32) + ib);
+        }
+        __syncthreads();
+        const int n = ch * kFbChunk + threadIdx.x;
+        float vals[kFQ];
+        if (n < a.N) {
+            exact_values_fq<RECIPE, Q8>(a, K, n, xs, x2s, xq, xd, nf, vals);
+        } else {
+#pragma unroll
+            for (int f = 0; f < kFQ; ++f) vals[f] = 0.0f;
+        }
+        for (int f = 0; f < nf; ++f) {
+            const int slot = grp * kFQ + f;
+            float v = vals[f];
+            if (n < a.N && v != v) fb.nan_flag[slot] = 1;
+            if (v != v) v = RECIPE == DIRECT ? INFINITY : -INFINITY;
+            for (int r = 0; r < Tc; ++r) {
+                const bool tk = r < T;
+                bool skip = n >= a.N;
+                if (tk)
+                    for (int q = 0; q < r; ++q) skip |= (chosen[q] == n);
+                red_v[threadIdx.x] = v;
+                red_n[threadIdx.x] = skip ? -1 : n;
+                __syncthreads();
+                for (int step = kFbChunk / 2; step > 0; step >>= 1) {
+                    if (threadIdx.x < step) {
+                        const int on = red_n[threadIdx.x + step], cn = red_n[threadIdx.x];
+                        const float ov = red_v[threadIdx.x + step], cv = red_v[threadIdx.x];
+                        if (on >= 0 && (cn < 0 || fb_before<RECIPE>(ov, on, cv, cn, tk))) {
+                            red_v[threadIdx.x] = ov;
+                            red_n[threadIdx.x] = on;
+                        }
+                    }
+                    __syncthreads();
+                }
+                if (threadIdx.x == 0) {
+                    if (tk) chosen[r] = red_n[0];
+                    const int64_t o = (static_cast<int64_t>(slot) * fb.nch + ch) * Tc + r;
+                    fb.cand_v[o] = red_v[0];
+                    fb.cand_n[o] = red_n[0];
+                }
+                __syncthreads();
+            }
+        }
+    }
+}
+
+template <int RECIPE, bool Q8>
+__global__ __launch_bounds__(kWave) void euclid_fb_select_kernel(StageArgs a, int K, FbArgs fb) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    float *xs = reinterpret_cast<float *>(lds);                         // [K]
+    int8_t *xq = reinterpret_cast<int8_t *>(xs + K);                    // [K]
+    float *xd = reinterpret_cast<float *>(xq + K);                      // [K/32]
+    __shared__ float vals64[kWave];
+    const int lane = threadIdx.x;
+    const int count = *a.fail_count;
+    const int T = a.topk;
+    const int Tc = T + 1;
+    for (int slot = blockIdx.x; slot < count; slot += gridDim.x) {
+        const int64_t m = a.fail_list[slot];
+        float sel_v[4];
+        int sel_n[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            sel_v[r] = 0.0f;
+            sel_n[r] = -1;
+        }
+        // ranked merge of the per-block candidates (lane-strided, then a wave
+        // merge): r < T merges the top-k slots, r == T the argmax slots
+        const int total = fb.nch * Tc;
+        int code = 0;
+        float code_v = 0.0f;
+        for (int r = 0; r < Tc; ++r) {
+            const bool tk = r < T;
+            float bv = 0.0f;
+            int bn = -1;
+            for (int i = lane; i < total; i += kWave) {
+                if (tk != (i % Tc < T)) continue;
+                const int64_t o = static_cast<int64_t>(slot) * total + i;
+                const int n = fb.cand_n[o];
+                if (n < 0) continue;
+                bool skip = false;
+                if (tk)
+                    for (int q = 0; q < r; ++q) skip |= (sel_n[q] == n);
+                const float v = fb.cand_v[o];
+                if (!skip && (bn < 0 || fb_before<RECIPE>(v, n, bv, bn, tk))) {
+                    bv = v;
+                    bn = n;
+                }
+            }
+            for (int off = 1; off < kWave; off <<= 1) {
+                const float ov = __shfl_xor(bv, off);
+                const int on = __shfl_xor(bn, off);
+                if (on >= 0 && (bn < 0 || fb_before<RECIPE>(ov, on, bv, bn, tk))) {
+                    bv = ov;
+                    bn = on;
+                }
+            }
+            if (tk) {
+                sel_v[r] = bv;
+                sel_n[r] = bn;
+            } else {
+                code = bn < 0 ? 0 : bn;
+                code_v = bv;
+            }
+        }
+        if (RECIPE != DIRECT && fb.nan_flag[slot]) {
+            // ggml_vec_argmax_f32 in code order: MAX(max, v), index of the
+            // last element equal to the running max (NaN restarts it).
+            for (int k = lane; k < K; k += kWave) xs[k] = a.xin[m * K + k];
+            __syncthreads();
+            float x2 = 0.0f;
+            if (RECIPE == HIGGS) x2 = sum_squares(xs, K);
+            if (Q8 && lane == 0)
+                for (int ib = 0; ib < K / 32; ++ib) quantize_block_q8(xs + 32 * ib, xq + 32 * ib, xd + ib);
+            __syncthreads();
+            float mx = -INFINITY;
+            int id = 0;
+            for (int base = 0; base < a.N; base += kWave) {
+                const int n = base + lane;
+                vals64[lane] = n < a.N ? exact_value<RECIPE, Q8>(a, K, xs, n, x2, xq, xd) : 0.0f;
+                __syncthreads();
+                if (lane == 0)
+                    for (int i = 0; i < kWave && base + i < a.N; ++i) {
+                        const float v = vals64[i];
+                        mx = mx > v ? mx : v;
+                        if (mx == v) id = base + i;
+                    }
+                __syncthreads();
+            }
+            code = __shfl(id, 0);
+            code_v = __shfl(mx, 0);
+            __syncthreads();
+        }
+        if (lane == 0) {
+            a.idx[m * a.Q + a.s] = code;
+            if (a.dist) a.dist[m * a.Q + a.s] = RECIPE == DIRECT ? code_v : -code_v;
+            for (int r = 0; r < a.topk; ++r) {
+                a.topk_idx[(m * a.Q + a.s) * a.topk + r] = sel_n[r];
+                a.topk_dist[(m * a.Q + a.s) * a.topk + r] = RECIPE == DIRECT ? sel_v[r] : -sel_v[r];
+            }
+        }
+        int use = code;
+        if (a.force_idx) {
+            use = a.force_idx[m * a.Q + a.s];
+            if (use < 0 || use >= a.N) {
+                if (lane == 0) a.flags[AQ_FLAG_BAD_INDEX] = 1;
+                use = 0;
+            }
+        }
+        for (int k = lane; k < K; k += kWave)
+            a.xout[m * K + k] = __fsub_rn(a.xin[m * K + k], a.cbf[static_cast<int64_t>(use) * K + k]);
+        if (lane == 0) fb.nan_flag[slot] = 0;
+    }
+}
+
+// --------------------------------------------------------------- gather, sum
+
+// out[m] = cbf[stage][idx[m]] (get_rows; Q8_0 rows dequantised).
+__global__ void gather_kernel(const float *__restrict__ cbf, int64_t N, int64_t K, const int32_t *__restrict__ idx,
+                              int64_t M, float *__restrict__ out, int32_t *__restrict__ flags) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= M * K) return;
+    const int64_t m = t / K, k = t % K;
+    int32_t c = idx[m];
+    if (c < 0 || c >= N) {
+        flags[AQ_FLAG_BAD_INDEX] = 1;
+        c = 0;
+    }
+    out[t] = cbf[static_cast<int64_t>(c) * K + k];
+}
+
+// out[m] = sum over stages of cbf[s][idx[m, s]] in stage order (-0 start).
+__global__ void decode_sum_kernel(const float *__restrict__ cbf, int Q, int64_t N, int64_t K,
+                                  const int32_t *__restrict__ idx, int64_t M, float *__restrict__ out,
+                                  int32_t *__restrict__ flags) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= M * K) return;
+    const int64_t m = t / K, k = t % K;
+    float acc = -0.0f;
+    for (int s = 0; s < Q; ++s) {
+        int32_t c = idx[m * Q + s];
+        if (c < 0 || c >= N) {
+            flags[AQ_FLAG_BAD_INDEX] = 1;
+            c = 0;
+        }
+        acc = __fadd_rn(acc, cbf[(static_cast<int64_t>(s) * N + c) * K + k]);
+    }
+    out[t] = acc;
+}
+
+// --------------------------------------------------------------- dispatch
+
+using StageFn = void (*)(StageArgs);
+using FallbackFn = void (*)(StageArgs, int, FbArgs);
+
+// 16-frame groups per wave: the bf16 frames of a wave stay in registers
+// (4 * KS registers per group), so wider codebooks take fewer groups.
+constexpr int groups_for(int ks) { return ks <= 2 ? 4 : (ks <= 8 ? 3 : 2); }
+
+template <int RECIPE, bool Q8, int KS>
+StageFn pick_stage(int topl) {
+    constexpr int FG = groups_for(KS);
+    return topl >= 4 ? euclid_stage_kernel<RECIPE, Q8, KS, FG, 4> : euclid_stage_kernel<RECIPE, Q8, KS, FG, 3>;
+}
+
+template <int RECIPE, bool Q8>
+StageFn pick_stage_ks(int ks, int topl) {
+    switch (ks) {
+        case 2: return pick_stage<RECIPE, Q8, 2>(topl);
+        case 8: return pick_stage<RECIPE, Q8, 8>(topl);
+        case 16: return pick_stage<RECIPE, Q8, 16>(topl);
+        case 24: return pick_stage<RECIPE, Q8, 24>(topl);
+        default: return nullptr;
+    }
+}
+
+StageFn pick_stage_fn(int recipe, bool q8, int ks, int topl) {
+    if (q8) return recipe == HIGGS ? pick_stage_ks<HIGGS, true>(ks, topl) : nullptr;
+    switch (recipe) {
+        case OMNI: return pick_stage_ks<OMNI, false>(ks, topl);
+        case HIGGS: return pick_stage_ks<HIGGS, false>(ks, topl);
+        case DIRECT: return pick_stage_ks<DIRECT, false>(ks, topl);
+        default: return nullptr;
+    }
+}
+
+FallbackFn pick_fb_values(int recipe, bool q8) {
+    if (q8) return recipe == HIGGS ? euclid_fb_values_kernel<HIGGS, true> : nullptr;
+    switch (recipe) {
+        case OMNI: return euclid_fb_values_kernel<OMNI, false>;
+        case HIGGS: return euclid_fb_values_kernel<HIGGS, false>;
+        case DIRECT: return euclid_fb_values_kernel<DIRECT, false>;
+        default: return nullptr;
+    }
+}
+
+FallbackFn pick_fb_select(int recipe, bool q8) {
+    if (q8) return recipe == HIGGS ? euclid_fb_select_kernel<HIGGS, true> : nullptr;
+    switch (recipe) {
+        case OMNI: return euclid_fb_select_kernel<OMNI, false>;
+        case HIGGS: return euclid_fb_select_kernel<HIGGS, false>;
+        case DIRECT: return euclid_fb_select_kernel<DIRECT, false>;
+        default: return nullptr;
+    }
+}
+
+int tile_lds(int ks) {
+    switch (ks) {
+        case 2: return Tile<2>::LDS;
+        case 8: return Tile<8>::LDS;
+        case 16: return Tile<16>::LDS;
+        case 24: return Tile<24>::LDS;
+        default: return 0;
+    }
+}
+int tile_cc(int ks) {
+    switch (ks) {
+        case 2: return Tile<2>::CC;
+        case 8: return Tile<8>::CC;
+        case 16: return Tile<16>::CC;
+        case 24: return Tile<24>::CC;
+        default: return 0;
+    }
+}
+
+uint16_t to_bf16(float f) {   // round to nearest even (finite inputs)
+    uint32_t u;
+    std::memcpy(&u, &f, 4);
+    if ((u & 0x7F800000u) == 0x7F800000u) return static_cast<uint16_t>((u >> 16) | ((u & 0xFFFFu) ? 0x40u : 0u));
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return static_cast<uint16_t>(u >> 16);
+}
+float from_bf16(uint16_t h) {
+    const uint32_t u = static_cast<uint32_t>(h) << 16;
+    float f;
+    std::memcpy(&f, &u, 4);
+    return f;
+}
+float from_fp16(uint16_t h) {
+    const uint32_t sign = (static_cast<uint32_t>(h) & 0x8000u) << 16;
+    const uint32_t e = (h >> 10) & 0x1Fu, mant = h & 0x3FFu;
+    uint32_t bits;
+    if (e == 0) {
+        if (mant == 0) {
+            bits = sign;
+        } else {
+            float v = std::ldexp(static_cast<float>(mant), -24);
+            std::memcpy(&bits, &v, 4);
+            bits |= sign;
+        }
+    } else if (e == 31) {
+        bits = sign | 0x7F800000u | (mant << 13);
+    } else {
+        bits = sign | ((e + 112u) << 23) | (mant << 13);
+    }
+    float out;
+    std::memcpy(&out, &bits, 4);
+    return out;
+}
+float round_up(double v) {
+    float f = static_cast<float>(v);
+    if (static_cast<double>(f) < v) f = std::nextafter(f, INFINITY);
+    return f;
+}
+
+}  // namespace
+
+struct aq_codebooks {
+    aq_ctx *ctx = nullptr;
+    int64_t Q = 0, N = 0, K = 0;
+    int recipe = 0;
+    bool q8 = false;
+    bool exact_only = false;
+    uint16_t *d_cbh = nullptr;   // [Q][N][K] bf16
+    float *d_hh = nullptr;       // [Q][N]
+    float *d_cbf = nullptr;      // [Q][N][K]
+    float *d_bias = nullptr;     // [Q][N] (OMNI)
+    float *d_e2 = nullptr;       // [Q][N] (HIGGS)
+    int8_t *d_q8 = nullptr;      // [Q][N][K]
+    float *d_q8d = nullptr;      // [Q][N][K/32]
+    std::vector<float> cmax, dcmax, chmax;
+};
+
+extern "C" {
+
+aq_status aq_euclid_upload(aq_ctx *ctx, int64_t Q, int64_t N, int64_t K, int cb_type, const void *data, int recipe,
+                           aq_codebooks **out) {
+    if (!ctx || !out || !data) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_euclid_upload: null argument");
+    *out = nullptr;
+    if (recipe < AQ_EUCLID_OMNIVOICE || recipe > AQ_EUCLID_DIRECT)
+        return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_euclid_upload: unknown recipe %d", recipe);
+    if (cb_type != AQ_CB_F32 && cb_type != AQ_CB_Q8_0)
+        return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_euclid_upload: unknown codebook type %d", cb_type);
+    const bool q8 = cb_type == AQ_CB_Q8_0;
+    if (q8 && recipe != AQ_EUCLID_HIGGS)
+        return aq_fail(ctx, AQ_E_UNSUPPORTED, "aq_euclid_upload: Q8_0 codebooks follow the Higgs recipe only");
+    const int ks = static_cast<int>(K / 32);
+    if (Q <= 0 || N <= 0 || K <= 0 || K % 32 != 0 || !pick_stage_fn(recipe, q8, ks, 3))
+        return aq_fail(ctx, AQ_E_SHAPE, "aq_euclid_upload: unsupported shape Q=%lld N=%lld K=%lld (K in {64,256,512,768})",
+                       (long long)Q, (long long)N, (long long)K);
+    if (N % tile_cc(ks) != 0 || N > (1 << 20))
+        return aq_fail(ctx, AQ_E_SHAPE, "aq_euclid_upload: N=%lld must be a multiple of %d", (long long)N, tile_cc(ks));
+    aq_device_guard g(ctx->device);
+
+    const size_t QNK = static_cast<size_t>(Q * N * K), QN = static_cast<size_t>(Q * N);
+    std::vector<float> cbf(QNK);
+    std::vector<int8_t> qs;
+    std::vector<float> qd;
+    if (q8) {
+        // block_q8_0 {fp16 d; int8 qs[32]} (ggml-common.h:241-246); dequantised
+        // as q * d (ggml-quants.c:491-505).
+        qs.resize(QNK);
+        qd.resize(QNK / 32);
+        const unsigned char *p = static_cast<const unsigned char *>(data);
+        for (size_t b = 0; b < QNK / 32; ++b) {
+            uint16_t h;
+            std::memcpy(&h, p + b * 34, 2);
+            const float d = from_fp16(h);
+            qd[b] = d;
+            for (int j = 0; j < 32; ++j) {
+                const int8_t q = static_cast<int8_t>(p[b * 34 + 2 + j]);
+                qs[b * 32 + j] = q;
+                cbf[b * 32 + j] = static_cast<float>(q) * d;
+            }
+        }
+    } else {
+        std::memcpy(cbf.data(), data, QNK * sizeof(float));
+    }
+    std::vector<uint16_t> cbh(QNK);
+    std::vector<float> hh(QN), bias(QN), e2(QN);
+    aq_codebooks *cb = new (std::nothrow) aq_codebooks();
+    if (!cb) return aq_fail(ctx, AQ_E_NOMEM, "aq_euclid_upload: host allocation failed");
+    cb->ctx = ctx;
+    cb->Q = Q;
+    cb->N = N;
+    cb->K = K;
+    cb->recipe = recipe;
+    cb->q8 = q8;
+    cb->cmax.assign(Q, 0.0f);
+    cb->dcmax.assign(Q, 0.0f);
+    cb->chmax.assign(Q, 0.0f);
+    bool nonfinite = false;
+    for (int64_t s = 0; s < Q; ++s) {
+        double cm = 0.0, dm = 0.0, hm = 0.0;
+        for (int64_t n = 0; n < N; ++n) {
+            const size_t row = static_cast<size_t>((s * N + n) * K);
+            double sq = 0.0, dq = 0.0, hq = 0.0, e2d = 0.0;
+            for (int64_t k = 0; k < K; ++k) {
+                const float c = cbf[row + k];
+                if (!std::isfinite(c)) nonfinite = true;
+                const uint16_t h = to_bf16(c);
+                cbh[row + k] = h;
+                const double cd = c, hd = from_bf16(h);
+                sq += cd * cd;                                    // OmniVoice: double products
+                e2d += static_cast<double>(c * c);               // sum_rows(c*c): fp32 squares
+                dq += (hd - cd) * (hd - cd);
+                hq += hd * hd;
+            }
+            hh[s * N + n] = static_cast<float>(0.5 * sq);
+            bias[s * N + n] = static_cast<float>(-sq);
+            e2[s * N + n] = static_cast<float>(e2d);
+            cm = std::max(cm, std::sqrt(sq));
+            dm = std::max(dm, std::sqrt(dq));
+            hm = std::max(hm, std::sqrt(hq));
+        }
+        cb->cmax[s] = round_up(cm * (1.0 + 1e-6));
+        cb->dcmax[s] = round_up(dm * (1.0 + 1e-6));
+        cb->chmax[s] = round_up(hm * (1.0 + 1e-6));
+    }
+    cb->exact_only = nonfinite;
+    bool ok = hipMalloc(&cb->d_cbh, QNK * 2) == hipSuccess && hipMalloc(&cb->d_hh, QN * 4) == hipSuccess &&
+              hipMalloc(&cb->d_cbf, QNK * 4) == hipSuccess && hipMalloc(&cb->d_bias, QN * 4) == hipSuccess &&
+              hipMalloc(&cb->d_e2, QN * 4) == hipSuccess;
+    if (ok && q8) ok = hipMalloc(&cb->d_q8, QNK) == hipSuccess && hipMalloc(&cb->d_q8d, QNK / 32 * 4) == hipSuccess;
+    if (!ok) {
+        aq_euclid_release(cb);
+        return aq_fail(ctx, AQ_E_NOMEM, "aq_euclid_upload: device allocation failed");
+    }
+    ok = hipMemcpy(cb->d_cbh, cbh.data(), QNK * 2, hipMemcpyHostToDevice) == hipSuccess &&
+         hipMemcpy(cb->d_hh, hh.data(), QN * 4, hipMemcpyHostToDevice) == hipSuccess &&
+         hipMemcpy(cb->d_cbf, cbf.data(), QNK * 4, hipMemcpyHostToDevice) == hipSuccess &&
+         hipMemcpy(cb->d_bias, bias.data(), QN * 4, hipMemcpyHostToDevice) == hipSuccess &&
+         hipMemcpy(cb->d_e2, e2.data(), QN * 4, hipMemcpyHostToDevice) == hipSuccess;
+    if (ok && q8)
+        ok = hipMemcpy(cb->d_q8, qs.data(), QNK, hipMemcpyHostToDevice) == hipSuccess &&
+             hipMemcpy(cb->d_q8d, qd.data(), QNK / 32 * 4, hipMemcpyHostToDevice) == hipSuccess;
+    if (!ok) {
+        aq_euclid_release(cb);
+        return aq_fail(ctx, AQ_E_DEVICE, "aq_euclid_upload: host to device copy failed");
+    }
+    *out = cb;
+    return AQ_OK;
+}
+
+aq_status aq_euclid_release(aq_codebooks *cb) {
+    if (!cb) return AQ_E_INVALID_ARG;
+    {
+        aq_device_guard g(cb->ctx->device);
+        for (void *p : {static_cast<void *>(cb->d_cbh), static_cast<void *>(cb->d_hh), static_cast<void *>(cb->d_cbf),
+                        static_cast<void *>(cb->d_bias), static_cast<void *>(cb->d_e2), static_cast<void *>(cb->d_q8),
+                        static_cast<void *>(cb->d_q8d)})
+            if (p) (void)hipFree(p);
+    }
+    delete cb;
+    return AQ_OK;
+}
+
+aq_status aq_euclid_encode(aq_ctx *ctx, const aq_codebooks *cb, const float *x, int64_t M, int32_t *idx,
+                           float *residual, float *dist, int topk, int32_t *topk_idx, float *topk_dist,
+                           const int32_t *force_idx) {
+    if (!ctx || !cb || !idx || (!x && M > 0)) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_euclid_encode: null argument");
+    if (cb->ctx->device != ctx->device)
+        return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_euclid_encode: codebooks belong to another device");
+    if (M < 0 || M > (int64_t{1} << 31) - 1) return aq_fail(ctx, AQ_E_SHAPE, "aq_euclid_encode: M=%lld out of range", (long long)M);
+    if (topk < 0 || topk > 4 || topk > cb->N)
+        return aq_fail(ctx, AQ_E_SHAPE, "aq_euclid_encode: topk=%d (supported 0..4, at most N)", topk);
+    if (topk > 0 && (!topk_idx || !topk_dist))
+        return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_euclid_encode: topk outputs missing");
+    if (M == 0) return AQ_OK;
+    aq_device_guard g(ctx->device);
+    const int K = static_cast<int>(cb->K);
+    const int ks = K / 32;
+    StageFn sfn = pick_stage_fn(cb->recipe, cb->q8, ks, topk >= 4 ? 4 : 3);
+    FallbackFn fvals = pick_fb_values(cb->recipe, cb->q8);
+    FallbackFn fsel = pick_fb_select(cb->recipe, cb->q8);
+    const int lds = tile_lds(ks);
+    AQ_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void *>(sfn), hipFuncAttributeMaxDynamicSharedMemorySize, lds));
+    const size_t fbv_lds = static_cast<size_t>(kFQ) * K * 5 + static_cast<size_t>(kFQ) * (K / 32) * 4 + 64;
+    const size_t fbs_lds = static_cast<size_t>(K) * 5 + (K / 32) * 4 + 64;
+
+    // Work buffers: the residual (the caller's buffer when given) and the
+    // per-stage failure lists.
+    float *work = residual;
+    if (!work) {
+        aq_status st = aq_ctx_scratch(ctx, 0, static_cast<size_t>(M) * K * sizeof(float), reinterpret_cast<void **>(&work));
+        if (st != AQ_OK) return st;
+    }
+    int32_t *fails = nullptr;
+    {
+        aq_status st = aq_ctx_scratch(ctx, 1, (static_cast<size_t>(M) + cb->Q + 64) * sizeof(int32_t),
+                                      reinterpret_cast<void **>(&fails));
+        if (st != AQ_OK) return st;
+    }
+    int32_t *counts = fails;
+    int32_t *list = fails + 64;
+    // Exact-scan work space: per failed frame, the best T codes of every
+    // 256-code block, and a NaN flag.
+    const int Tfb = topk + 1;
+    FbArgs fb{};
+    fb.nch = static_cast<int>((cb->N + kFbChunk - 1) / kFbChunk);
+    {
+        const size_t cand = static_cast<size_t>(M) * fb.nch * Tfb;
+        void *w = nullptr;
+        aq_status st = aq_ctx_scratch(ctx, 2, cand * 8 + static_cast<size_t>(M) * 4, &w);
+        if (st != AQ_OK) return st;
+        fb.cand_v = static_cast<float *>(w);
+        fb.cand_n = reinterpret_cast<int32_t *>(fb.cand_v + cand);
+        fb.nan_flag = fb.cand_n + cand;
+        AQ_HIP(ctx, hipMemsetAsync(fb.nan_flag, 0, static_cast<size_t>(M) * 4, ctx->stream));
+    }
+    AQ_HIP(ctx, hipMemsetAsync(counts, 0, sizeof(int32_t) * 64, ctx->stream));
+    AQ_HIP(ctx, hipMemsetAsync(ctx->d_flags, 0, sizeof(int32_t) * AQ_FLAG_COUNT, ctx->stream));
+
+    const int FG = groups_for(ks);
+    const int64_t frames_per_block = static_cast<int64_t>(kWaves) * FG * 16;
+    const unsigned blocks = static_cast<unsigned>((M + frames_per_block - 1) / frames_per_block);
+    for (int64_t s = 0; s < cb->Q; ++s) {
+        StageArgs a{};
+        a.xin = s == 0 ? x : work;
+        a.xout = work;
+        a.M = M;
+        a.N = static_cast<int>(cb->N);
+        a.cbh = cb->d_cbh + s * cb->N * K;
+        a.hh = cb->d_hh + s * cb->N;
+        a.cbf = cb->d_cbf + s * cb->N * K;
+        a.bias = cb->d_bias + s * cb->N;
+        a.e2 = cb->d_e2 + s * cb->N;
+        a.q8 = cb->q8 ? cb->d_q8 + s * cb->N * K : nullptr;
+        a.q8d = cb->q8 ? cb->d_q8d + s * cb->N * (K / 32) : nullptr;
+        a.cmax = cb->cmax[s];
+        a.dcmax = cb->dcmax[s];
+        a.chmax = cb->chmax[s];
+        // ggml hands an F32 x F32 mul_mat to tinyBLAS when the query batch has
+        // >= 2 rows, k % 16 == 0 and the codebook has a multiple of 4 rows
+        // (ggml-cpu.c:1285-1306, sgemm.cpp:3705-3725); else ggml_vec_dot_f32.
+        a.order = (M >= 2 && K % 16 == 0 && cb->N % 4 == 0) ? 0 : 1;
+        a.Q = static_cast<int>(cb->Q);
+        a.s = static_cast<int>(s);
+        a.idx = idx;
+        a.dist = dist;
+        a.topk = topk;
+        a.topk_idx = topk_idx;
+        a.topk_dist = topk_dist;
+        a.force_idx = force_idx;
+        a.fail_count = counts + (s % 64);
+        a.fail_list = list;
+        a.flags = ctx->d_flags;
+        a.exact_only = cb->exact_only ? 1 : 0;
+        a.debug_frame = -1;
+        if (const char *e = std::getenv("AQ_DEBUG_FRAME")) {
+            void *dbg = nullptr;
+            if (aq_ctx_scratch(ctx, 3, 256 * sizeof(float) * 64, &dbg) == AQ_OK) {
+                a.debug_frame = std::atoll(e);
+                a.debug = static_cast<float *>(dbg) + s * 256;
+            }
+        }
+        if (s >= 64 && s % 64 == 0) AQ_HIP(ctx, hipMemsetAsync(counts, 0, sizeof(int32_t) * 64, ctx->stream));
+        const int tslot = aq_timing_start(ctx);
+        hipLaunchKernelGGL(sfn, dim3(blocks), dim3(kThreads), lds, ctx->stream, a);
+        aq_timing_stop(ctx, tslot);
+        AQ_HIP(ctx, hipGetLastError());
+        const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
+        hipLaunchKernelGGL(fvals, dim3(static_cast<unsigned>(2 * cus)), dim3(kFbChunk), fbv_lds, ctx->stream, a, K, fb);
+        AQ_HIP(ctx, hipGetLastError());
+        hipLaunchKernelGGL(fsel, dim3(static_cast<unsigned>(4 * cus)), dim3(kWave), fbs_lds, ctx->stream, a, K, fb);
+        AQ_HIP(ctx, hipGetLastError());
+    }
+    if (force_idx) {
+        int32_t flag = 0;
+        AQ_HIP(ctx, hipMemcpyAsync(&flag, ctx->d_flags + AQ_FLAG_BAD_INDEX, sizeof(int32_t), hipMemcpyDeviceToHost, ctx->stream));
+        AQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        if (flag) return aq_fail(ctx, AQ_E_INDEX_RANGE, "aq_euclid_encode: force_idx holds a code outside [0, %lld)", (long long)cb->N);
+    }
+    return AQ_OK;
+}
+
+// Diagnostics: the AQ_DEBUG_FRAME dump of the last encode (stage-major,
+// 256 floats per stage); returns the number of floats copied.
+extern "C" int aq_euclid_debug_dump(aq_ctx *ctx, float *host, int capacity) {
+    void *dbg = nullptr;
+    if (!ctx || aq_ctx_scratch(ctx, 3, 0, &dbg) != AQ_OK || !dbg) return 0;
+    aq_device_guard g(ctx->device);
+    const size_t n = std::min<size_t>(static_cast<size_t>(capacity), 256 * 64);
+    if (hipMemcpy(host, dbg, n * sizeof(float), hipMemcpyDeviceToHost) != hipSuccess) return 0;
+    return static_cast<int>(n);
+}
+
+aq_status aq_euclid_failures(aq_ctx *ctx, const aq_codebooks *cb, int32_t *host_counts) {
+    if (!ctx || !cb || !host_counts) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_euclid_failures: null argument");
+    int32_t *fails = nullptr;
+    aq_status st = aq_ctx_scratch(ctx, 1, 0, reinterpret_cast<void **>(&fails));
+    if (st != AQ_OK || !fails) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_euclid_failures: no encode has run");
+    aq_device_guard g(ctx->device);
+    const int64_t n = std::min<int64_t>(cb->Q, 64);
+    AQ_HIP(ctx, hipMemcpyAsync(host_counts, fails, sizeof(int32_t) * n, hipMemcpyDeviceToHost, ctx->stream));
+    AQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return AQ_OK;
+}
+
+aq_status aq_codebook_gather(aq_ctx *ctx, const aq_codebooks *cb, int64_t stage, const int32_t *idx, int64_t M, float *out) {
+    if (!ctx || !cb || (M > 0 && (!idx || !out))) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_codebook_gather: null argument");
+    if (stage < 0 || stage >= cb->Q || M < 0) return aq_fail(ctx, AQ_E_SHAPE, "aq_codebook_gather: stage or M out of range");
+    if (M == 0) return AQ_OK;
+    aq_device_guard g(ctx->device);
+    AQ_HIP(ctx, hipMemsetAsync(ctx->d_flags, 0, sizeof(int32_t) * AQ_FLAG_COUNT, ctx->stream));
+    const int64_t total = M * cb->K;
+    hipLaunchKernelGGL(gather_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, ctx->stream,
+                       cb->d_cbf + stage * cb->N * cb->K, cb->N, cb->K, idx, M, out, ctx->d_flags);
+    AQ_HIP(ctx, hipGetLastError());
+    int32_t flag = 0;
+    AQ_HIP(ctx, hipMemcpyAsync(&flag, ctx->d_flags + AQ_FLAG_BAD_INDEX, sizeof(int32_t), hipMemcpyDeviceToHost, ctx->stream));
+    AQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (flag) return aq_fail(ctx, AQ_E_INDEX_RANGE, "aq_codebook_gather: code outside [0, %lld)", (long long)cb->N);
+    return AQ_OK;
+}
+
+aq_status aq_euclid_decode(aq_ctx *ctx, const aq_codebooks *cb, const int32_t *idx, int64_t M, float *out) {
+    if (!ctx || !cb || (M > 0 && (!idx || !out))) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_euclid_decode: null argument");
+    if (M < 0) return aq_fail(ctx, AQ_E_SHAPE, "aq_euclid_decode: negative M");
+    if (M == 0) return AQ_OK;
+    aq_device_guard g(ctx->device);
+    AQ_HIP(ctx, hipMemsetAsync(ctx->d_flags, 0, sizeof(int32_t) * AQ_FLAG_COUNT, ctx->stream));
+    const int64_t total = M * cb->K;
+    hipLaunchKernelGGL(decode_sum_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, ctx->stream,
+                       cb->d_cbf, static_cast<int>(cb->Q), cb->N, cb->K, idx, M, out, ctx->d_flags);
+    AQ_HIP(ctx, hipGetLastError());
+    int32_t flag = 0;
+    AQ_HIP(ctx, hipMemcpyAsync(&flag, ctx->d_flags + AQ_FLAG_BAD_INDEX, sizeof(int32_t), hipMemcpyDeviceToHost, ctx->stream));
+    AQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (flag) return aq_fail(ctx, AQ_E_INDEX_RANGE, "aq_euclid_decode: code outside [0, %lld)", (long long)cb->N);
+    return AQ_OK;
+}
+
+}  // extern "C"

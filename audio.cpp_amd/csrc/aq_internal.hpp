@@ -7,6 +7,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <string>
+#include <vector>
 
 #include "aq_mi355x.h"
 
@@ -16,7 +17,25 @@ struct aq_ctx {
     std::string err;
     int32_t *d_flags = nullptr;   // device status words written by kernels (vector stores only)
     int num_cus = 0;
+    // Work buffers owned by the context, grown on demand (slot 0: residual
+    // cascade, slot 1: per-stage failure counters and lists).
+    static constexpr int kScratchSlots = 4;
+    void *scratch[kScratchSlots] = {};
+    size_t scratch_bytes[kScratchSlots] = {};
+    // Kernel timing (aq_ctx_set_timing): event pairs around each main kernel.
+    bool timing = false;
+    std::vector<hipEvent_t> ev_start, ev_stop;
+    size_t ev_used = 0;
 };
+
+// Records the start of a timed kernel on ctx's stream; returns the slot, or
+// -1 when timing is off.  aq_timing_stop closes it.
+int aq_timing_start(aq_ctx *ctx);
+void aq_timing_stop(aq_ctx *ctx, int slot);
+
+// Device buffer `slot` of at least `bytes` (grows it, waiting for the stream
+// first; bytes == 0 returns the current buffer, possibly null).
+aq_status aq_ctx_scratch(aq_ctx *ctx, int slot, size_t bytes, void **out);
 
 // Sets `ctx->err` and returns `st`.
 inline aq_status aq_fail(aq_ctx *ctx, aq_status st, const char *fmt, ...) {

@@ -1,9 +1,62 @@
 // Context management for the C ABI declared in include/aq_mi355x.h.
 #include "aq_internal.hpp"
 
+aq_status aq_ctx_scratch(aq_ctx *ctx, int slot, size_t bytes, void **out) {
+    if (!ctx || !out || slot < 0 || slot >= aq_ctx::kScratchSlots) return AQ_E_INVALID_ARG;
+    if (bytes > ctx->scratch_bytes[slot]) {
+        aq_device_guard g(ctx->device);
+        AQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        if (ctx->scratch[slot]) (void)hipFree(ctx->scratch[slot]);
+        ctx->scratch[slot] = nullptr;
+        ctx->scratch_bytes[slot] = 0;
+        if (hipMalloc(&ctx->scratch[slot], bytes) != hipSuccess)
+            return aq_fail(ctx, AQ_E_NOMEM, "work buffer of %zu bytes could not be allocated", bytes);
+        ctx->scratch_bytes[slot] = bytes;
+    }
+    *out = ctx->scratch[slot];
+    return AQ_OK;
+}
+
+int aq_timing_start(aq_ctx *ctx) {
+    if (!ctx || !ctx->timing) return -1;
+    if (ctx->ev_used == ctx->ev_start.size()) {
+        hipEvent_t a = nullptr, b = nullptr;
+        if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess) return -1;
+        ctx->ev_start.push_back(a);
+        ctx->ev_stop.push_back(b);
+    }
+    const size_t slot = ctx->ev_used++;
+    if (hipEventRecord(ctx->ev_start[slot], ctx->stream) != hipSuccess) return -1;
+    return static_cast<int>(slot);
+}
+
+void aq_timing_stop(aq_ctx *ctx, int slot) {
+    if (!ctx || slot < 0) return;
+    (void)hipEventRecord(ctx->ev_stop[static_cast<size_t>(slot)], ctx->stream);
+}
+
 extern "C" {
 
 int aq_abi_version(void) { return AQ_ABI_VERSION; }
+
+aq_status aq_ctx_set_timing(aq_ctx *ctx, int enable) {
+    if (!ctx) return AQ_E_INVALID_ARG;
+    ctx->timing = enable != 0;
+    ctx->ev_used = 0;
+    return AQ_OK;
+}
+
+aq_status aq_ctx_read_timing(aq_ctx *ctx, float *ms, int capacity, int *count) {
+    if (!ctx || !count || (capacity > 0 && !ms)) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_ctx_read_timing: null argument");
+    aq_device_guard g(ctx->device);
+    AQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    const int n = static_cast<int>(ctx->ev_used);
+    for (int i = 0; i < n && i < capacity; ++i)
+        AQ_HIP(ctx, hipEventElapsedTime(&ms[i], ctx->ev_start[static_cast<size_t>(i)], ctx->ev_stop[static_cast<size_t>(i)]));
+    *count = n;
+    ctx->ev_used = 0;
+    return AQ_OK;
+}
 
 aq_status aq_ctx_create(int device, void *hip_stream, aq_ctx **out) {
     if (!out) return AQ_E_INVALID_ARG;
@@ -33,7 +86,12 @@ aq_status aq_ctx_destroy(aq_ctx *ctx) {
     if (!ctx) return AQ_E_INVALID_ARG;
     {
         aq_device_guard g(ctx->device);
+        (void)hipStreamSynchronize(ctx->stream);
         if (ctx->d_flags) (void)hipFree(ctx->d_flags);
+        for (int i = 0; i < aq_ctx::kScratchSlots; ++i)
+            if (ctx->scratch[i]) (void)hipFree(ctx->scratch[i]);
+        for (hipEvent_t e : ctx->ev_start) (void)hipEventDestroy(e);
+        for (hipEvent_t e : ctx->ev_stop) (void)hipEventDestroy(e);
     }
     delete ctx;
     return AQ_OK;

@@ -74,6 +74,15 @@ aq_status aq_ctx_synchronize(aq_ctx *ctx);
 const char *aq_last_error(const aq_ctx *ctx);
 int aq_abi_version(void);
 
+/* Kernel timing, a measurement aid with no counterpart in the reference: when
+ * enabled, the library brackets each launch of its main kernels (the DAC
+ * encode kernel, each Euclidean stage's score kernel) with HIP events on the
+ * context's stream.  aq_ctx_read_timing synchronises the stream, writes up to
+ * `capacity` durations in milliseconds (launch order) and the number
+ * recorded to *count, and starts a new record. */
+aq_status aq_ctx_set_timing(aq_ctx *ctx, int enable);
+aq_status aq_ctx_read_timing(aq_ctx *ctx, float *ms, int capacity, int *count);
+
 /* ---- DAC-style cosine RVQ (Fish Audio recipe) --------------------------------
  *
  * Per stage s (codec.cpp:587-605):
@@ -121,6 +130,76 @@ aq_status aq_dac_encode(aq_ctx *ctx, const aq_dac_stages *stages, const float *x
  * synchronises the stream to report it). */
 aq_status aq_dac_decode(aq_ctx *ctx, const aq_dac_stages *stages, const int32_t *idx, int64_t M,
                         float *out);
+
+/* ---- Euclidean VQ / RVQ (Mimi-style codecs, k-means tokenisers) ------------
+ *
+ * Nearest codeword by squared Euclidean distance, with the residual cascade
+ * r <- r - c[code] across Q stages.  `recipe` selects the reference
+ * arithmetic the results are identical to:
+ *   AQ_EUCLID_OMNIVOICE  logit = mul_mat(2c, r) + (float)(-(double)|c|^2),
+ *                        argmax, last index among equal maxima
+ *                        (omnivoice/audio_tokenizer.cpp:1227-1237,1897-1927)
+ *   AQ_EUCLID_HIGGS      logit = ((2*mul_mat(c, r)) - sum_rows(r*r)) -
+ *                        sum_rows(c*c), argmax (higgs_audio_tts/codec.cpp:975-1013);
+ *                        F32 or Q8_0 codebooks (a Q8_0 mul_mat quantises r to
+ *                        Q8_0 with x86 rounding first)
+ *   AQ_EUCLID_DIRECT     distance = sum (x-c)^2 (rounded products added in
+ *                        order), first index of the minimum
+ *                        (VectorQuantizer::compute, host_ops.cpp:236-273;
+ *                        Qwen3 nearest_code, tokenizer_speech_encoder.cpp:287-303)
+ * Scores are contracted in bf16 on the matrix cores; every code that could
+ * win is re-ranked in the recipe's fp32 arithmetic under a rigorous error
+ * bound, and frames the bound cannot settle are rescanned exactly, so the
+ * outputs equal the reference's. */
+typedef enum aq_euclid_recipe {
+    AQ_EUCLID_OMNIVOICE = 0,
+    AQ_EUCLID_HIGGS = 1,
+    AQ_EUCLID_DIRECT = 2
+} aq_euclid_recipe;
+
+typedef enum aq_codebook_type {
+    AQ_CB_F32 = 0,    /* float [Q][N][K]                                       */
+    AQ_CB_Q8_0 = 1    /* GGUF block_q8_0 {fp16 d; int8 qs[32]} [Q][N][K/32],
+                         34 bytes per block (ggml-common.h:241-246)             */
+} aq_codebook_type;
+
+/* Upload Q codebooks of N codes of dimension K from host memory (upload
+ * once; replaces BackendWeightStore loads, backend_weight_store.h:272-392,
+ * and the per-call codebook set-up of the host loops).
+ * Supported: K in {64, 256, 512, 768}; N a multiple of 256, 64, 32, 16
+ * respectively; Q8_0 with AQ_EUCLID_HIGGS only. */
+aq_status aq_euclid_upload(aq_ctx *ctx, int64_t Q, int64_t N, int64_t K, int cb_type, const void *data,
+                           int recipe, aq_codebooks **out);
+aq_status aq_euclid_release(aq_codebooks *cb);
+
+/* Encode M frames through all stages.
+ *   x          device [M, K] (frame-major; not modified)
+ *   idx        device [M, Q] int32 codes
+ *   residual   device [M, K] or NULL: residual after the last stage
+ *   dist       device [M, Q] or NULL: the winner's distance in the recipe's
+ *              arithmetic (DIRECT: the distance; OMNIVOICE / HIGGS: -logit)
+ *   topk       0..4: also the topk best codes per stage, best first (ties
+ *              by index; ggml_top_k's order is unspecified, compare as sets)
+ *   topk_idx   device [M, Q, topk];  topk_dist device [M, Q, topk]
+ *   force_idx  device [M, Q] or NULL: teacher forcing of the residual update */
+aq_status aq_euclid_encode(aq_ctx *ctx, const aq_codebooks *cb, const float *x, int64_t M, int32_t *idx,
+                           float *residual, float *dist, int topk, int32_t *topk_idx, float *topk_dist,
+                           const int32_t *force_idx);
+
+/* Frames per stage (first min(Q, 64) stages) of the last encode on ctx that
+ * the error certificate could not settle and the exact scan decided (host
+ * int32 array; synchronises the stream).  A measurement aid. */
+aq_status aq_euclid_failures(aq_ctx *ctx, const aq_codebooks *cb, int32_t *host_counts);
+
+/* Codebook gather of one stage: out[m] = codebook[stage][idx[m]] (ggml_get_rows,
+ * lookup_modules.cpp:88-112,182-187; Q8_0 rows dequantised as q*d).
+ * idx device [M], out device [M, K].  Out-of-range codes -> AQ_E_INDEX_RANGE. */
+aq_status aq_codebook_gather(aq_ctx *ctx, const aq_codebooks *cb, int64_t stage, const int32_t *idx, int64_t M,
+                             float *out);
+
+/* Decode: out[m] = sum over stages of codebook[s][idx[m, s]], in stage order.
+ * idx device [M, Q], out device [M, K]. */
+aq_status aq_euclid_decode(aq_ctx *ctx, const aq_codebooks *cb, const int32_t *idx, int64_t M, float *out);
 
 #ifdef __cplusplus
 }

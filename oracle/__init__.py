@@ -85,6 +85,8 @@ class Oracle:
         L.aqo_higgs_rvq.restype = C.c_int
         L.aqo_higgs_rvq.argtypes = [_f32p, _i64, _i64, _i64, _i64, C.c_void_p, C.c_int, C.c_int, C.c_void_p,
                                     _i32p, _f32p, C.c_void_p, C.c_void_p, C.c_void_p]
+        L.aqo_direct_rvq.restype = C.c_int
+        L.aqo_direct_rvq.argtypes = [_f32p, _i64, _i64, _i64, _i64, _f32p, C.c_void_p, _i32p, _f32p, C.c_void_p]
         L.aqo_gather_f32.restype = C.c_int
         L.aqo_gather_f32.argtypes = [_f32p, _i64, _i64, _i32p, _i64, _f32p]
         L.aqo_gather_q8_0.restype = C.c_int
@@ -122,6 +124,20 @@ class Oracle:
                                      lb.ctypes.data_as(C.c_void_p))
         assert rc == 0
         return dict(idx=idx, residual=res, logit=lb)
+
+    def direct_rvq(self, cfg: dict, force_idx=None):
+        x = np.ascontiguousarray(cfg["x"], np.float32)
+        M, K = x.shape
+        Q, N = cfg["Q"], cfg["N"]
+        idx = np.zeros((M, Q), np.int32)
+        res = np.zeros((M, K), np.float32)
+        dist = np.zeros((M, Q), np.float32)
+        fi = np.ascontiguousarray(force_idx, np.int32) if force_idx is not None else None
+        rc = self.lib.aqo_direct_rvq(x, M, K, Q, N, np.ascontiguousarray(cfg["codebook"], np.float32),
+                                     None if fi is None else fi.ctypes.data_as(C.c_void_p), idx, res,
+                                     dist.ctypes.data_as(C.c_void_p))
+        assert rc == 0
+        return dict(idx=idx, residual=res, dist=dist)
 
     def higgs_rvq(self, cfg: dict, force_idx=None, topk: int = 0):
         x = np.ascontiguousarray(cfg["x"], np.float32)
@@ -173,6 +189,8 @@ class Ref:
         L.aqref_higgs_rvq.argtypes = [_f32p, _i64, _i64, _i64, _i64, C.c_void_p, C.c_int, C.c_int,
                                       _i32p, _f32p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int]
         L.aqref_quantize_row_q8_0.argtypes = [_f32p, C.c_void_p, _i64]
+        L.aqref_vector_quantizer.restype = C.c_int
+        L.aqref_vector_quantizer.argtypes = [_f32p, _i64, _i64, _i64, _i64, _f32p, _i64, _i64, _f32p]
         L.aqref_quantize_chunk_q8_0.argtypes = [_f32p, C.c_void_p, _i64, _i64]
 
     def dac_rvq(self, cfg: dict, threads: int = 8, recon: bool = True, materialize: bool = True):
@@ -224,4 +242,15 @@ class Ref:
         if topk:
             out["topk_idx"] = tki
             out["topk_logit"] = tkl
+        return out
+
+    def vector_quantizer(self, x, codebook, batch: int = 1):
+        """engine::runtime::VectorQuantizer::compute: nearest codewords."""
+        x = np.ascontiguousarray(x, np.float32)
+        cb = np.ascontiguousarray(codebook, np.float32)
+        M, K = x.shape
+        out = np.zeros_like(x)
+        rc = self.lib.aqref_vector_quantizer(x, x.size, batch, M // batch, K, cb, cb.size, cb.shape[0], out)
+        if rc != 0:
+            raise RuntimeError("VectorQuantizer input size mismatch")
         return out

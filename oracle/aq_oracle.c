@@ -417,6 +417,41 @@ int aqo_higgs_rvq(const float *x, int64_t M, int64_t K, int64_t Q, int64_t N,
     return 0;
 }
 
+/* Direct-distance RVQ: VectorQuantizer::compute
+ * (src/framework/runtime/host_ops.cpp:236-273) per stage, and the Qwen3
+ * cascade quantize_projected (src/models/qwen3_tts/tokenizer_speech_encoder.cpp:
+ * 287-349): distance = sum_k (x_k - c_k)^2 with each square rounded and added
+ * in order (the reference is built as ISO C++17, so GCC does not contract),
+ * first index of the minimum (strict <, NaN never wins, start at index 0),
+ * residual -= c[code]. */
+int aqo_direct_rvq(const float *x, int64_t M, int64_t K, int64_t Q, int64_t N, const float *cb,
+                   const int32_t *force_idx, int32_t *idx, float *residual, float *dist) {
+    float *r = residual;
+    memcpy(r, x, (size_t)(M * K) * sizeof(float));
+    for (int64_t s = 0; s < Q; ++s) {
+        const float *C = cb + s * N * K;
+        for (int64_t m = 0; m < M; ++m) {
+            float *rm = r + m * K;
+            int32_t best = 0;
+            float best_d = INFINITY;
+            for (int64_t n = 0; n < N; ++n) {
+                float d = 0.0f;
+                for (int64_t k = 0; k < K; ++k) {
+                    const float diff = rm[k] - C[n * K + k];
+                    const float sq = diff * diff;
+                    d = d + sq;
+                }
+                if (d < best_d) { best_d = d; best = (int32_t)n; }
+            }
+            idx[m * Q + s] = best;
+            if (dist) dist[m * Q + s] = best_d;
+            const int64_t use = force_idx ? force_idx[m * Q + s] : best;
+            for (int64_t k = 0; k < K; ++k) rm[k] = rm[k] - C[use * K + k];
+        }
+    }
+    return 0;
+}
+
 int aqo_gather_f32(const float *cb, int64_t N, int64_t K, const int32_t *idx, int64_t M, float *out) {
     for (int64_t m = 0; m < M; ++m) {
         if (idx[m] < 0 || idx[m] >= N) return -1;

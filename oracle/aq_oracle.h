@@ -66,6 +66,12 @@ int aqo_higgs_rvq(const float *x, int64_t M, int64_t K, int64_t Q, int64_t N,
                   int32_t *idx, float *residual, float *dist,
                   int32_t *topk_idx, float *topk_logit);
 
+/* Direct-distance RVQ (VectorQuantizer::compute / Qwen3 nearest_code):
+ * rounded squares added in order, first index of the minimum.  dist [M,Q]
+ * (nullable) receives the winner's distance. */
+int aqo_direct_rvq(const float *x, int64_t M, int64_t K, int64_t Q, int64_t N, const float *cb,
+                   const int32_t *force_idx, int32_t *idx, float *residual, float *dist);
+
 /* Codebook gather (get_rows, ops.cpp:4923-4962 / 4797-4840). Returns -1 on an
  * out-of-range index (the reference asserts). */
 int aqo_gather_f32(const float *cb, int64_t N, int64_t K, const int32_t *idx, int64_t M, float *out);

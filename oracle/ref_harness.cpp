@@ -27,6 +27,7 @@
 
 #include "ggml.h"
 #include "ggml-cpu.h"
+#include "engine/framework/runtime/host_ops.h"
 
 #include <chrono>
 #include <cmath>
@@ -314,6 +315,24 @@ double aqref_higgs_rvq(const float * x, int64_t M, int64_t K, int64_t Q, int64_t
     }
     if (residual) std::memcpy(residual, res.data(), res.size() * 4);
     return ms;
+}
+
+// The reference's framework host quantizer, engine::runtime::VectorQuantizer
+// (src/framework/runtime/host_ops.cpp:236-273, compiled from the reference
+// sources): x_len floats of input and cb_len floats of codebook as given, so
+// the reference's own size check sees the true lengths.  Writes the nearest
+// codewords (x_len floats) and returns 0, or -1 when the reference throws.
+int aqref_vector_quantizer(const float * x, int64_t x_len, int64_t batch, int64_t steps, int64_t dim,
+                           const float * cb, int64_t cb_len, int64_t N, float * out) {
+    try {
+        std::vector<float> in(x, x + x_len);
+        std::vector<float> code(cb, cb + cb_len);
+        const auto res = engine::runtime::VectorQuantizer().compute(in, code, batch, steps, dim, N);
+        std::memcpy(out, res.values.data(), res.values.size() * sizeof(float));
+        return 0;
+    } catch (...) {
+        return -1;
+    }
 }
 
 // x86 query quantisation as ggml applies it inside mul_mat (quantize_row_q8_0,

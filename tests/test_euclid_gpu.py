@@ -1,0 +1,257 @@
+"""GPU parity of the Euclidean VQ / RVQ path (aq_euclid_* through the C ABI).
+
+Every recipe is compared with the oracle on the same seeded inputs: codes
+equal, the final residual and the reported distances bit-identical, top-k
+sets and values identical.  The bf16 matrix-core scores only choose
+candidates; the certificate plus the exact re-rank make the outputs the
+reference arithmetic's, which these tests check at shapes the oracle
+finishes in seconds (full BASELINE sizes are checked against golden
+fixtures in test_golden_gpu.py).
+"""
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch as t
+
+    if not t.cuda.is_available():
+        pytest.skip("no GPU")
+    return t
+
+
+@pytest.fixture(scope="module")
+def ctx(torch):
+    import aqmi
+
+    return aqmi.Context(0)
+
+
+@pytest.fixture(scope="module")
+def oracle():
+    from oracle import Oracle
+
+    return Oracle()
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def run(torch, ctx, cb_host, recipe, x, cb_type=0, topk=0, force=None, want_dist=True):
+    import aqmi
+
+    cbs = aqmi.Codebooks(ctx, cb_host, recipe, cb_type)
+    M = x.shape[0]
+    xd = torch.from_numpy(np.ascontiguousarray(x, np.float32)).cuda()
+    idx = torch.full((M, cbs.Q), -1, dtype=torch.int32, device="cuda")
+    res = torch.empty((M, cbs.K), dtype=torch.float32, device="cuda")
+    dist = torch.empty((M, cbs.Q), dtype=torch.float32, device="cuda") if want_dist else None
+    tki = torch.empty((M, cbs.Q, max(topk, 1)), dtype=torch.int32, device="cuda")
+    tkd = torch.empty((M, cbs.Q, max(topk, 1)), dtype=torch.float32, device="cuda")
+    fi = None if force is None else torch.from_numpy(np.ascontiguousarray(force, np.int32)).cuda()
+    cbs.encode(xd, idx, res, dist, topk, tki if topk else None, tkd if topk else None, fi)
+    torch.cuda.synchronize()
+    out = dict(idx=idx.cpu().numpy(), residual=res.cpu().numpy(), cbs=cbs, fails=cbs.failures())
+    if want_dist:
+        out["dist"] = dist.cpu().numpy()
+    if topk:
+        out["topk_idx"] = tki.cpu().numpy()
+        out["topk_dist"] = tkd.cpu().numpy()
+    return out
+
+
+def mimi(rows, Q=3):
+    from aqmi import synth
+
+    cfg = synth.make_config(2, rows=rows)
+    cfg["Q"] = Q
+    cfg["codebook"] = np.ascontiguousarray(cfg["codebook"][:Q])
+    return cfg
+
+
+@pytest.mark.parametrize("M", [1, 17, 191, 193, 1000])
+def test_omnivoice_matches_oracle(torch, ctx, oracle, M):
+    import aqmi
+
+    print(f"[gpu] omnivoice M={M}", flush=True)
+    cfg = mimi(M)
+    out = run(torch, ctx, cfg["codebook"], aqmi.OMNIVOICE, cfg["x"])
+    ref = oracle.euclid_rvq(cfg)
+    assert np.array_equal(out["idx"], ref["idx"])
+    assert np.array_equal(bits(out["residual"]), bits(ref["residual"]))
+    assert np.array_equal(bits(out["dist"]), bits(-ref["logit"]))
+
+
+@pytest.mark.parametrize("K,N,M,Q", [(768, 1024, 300, 1), (64, 1024, 500, 2), (256, 2048, 400, 2)])
+def test_higgs_f32_matches_oracle(torch, ctx, oracle, K, N, M, Q):
+    import aqmi
+    from aqmi import synth
+
+    print(f"[gpu] higgs f32 K={K} N={N} M={M}", flush=True)
+    cfg = synth.make_config(3, rows=M)
+    cb = synth.normal(21, 3, (Q, N, K), 1.0)
+    x = cfg["x"][:, :K].copy()
+    c = dict(x=x, M=M, K=K, Q=Q, N=N, codebook=cb)
+    out = run(torch, ctx, cb, aqmi.HIGGS, x)
+    ref = oracle.higgs_rvq(c)
+    assert np.array_equal(out["idx"], ref["idx"])
+    assert np.array_equal(bits(out["residual"]), bits(ref["residual"]))
+    assert np.array_equal(bits(out["dist"]), bits(ref["dist"]))
+
+
+def test_higgs_q8_topk_matches_oracle(torch, ctx, oracle):
+    import aqmi
+    from aqmi import synth
+
+    print("[gpu] higgs q8 topk", flush=True)
+    cfg = synth.make_config(4, rows=300)
+    cfg["Q"] = 2
+    cfg["codebook_q8"] = np.ascontiguousarray(cfg["codebook_q8"][:2])
+    out = run(torch, ctx, cfg["codebook_q8"], aqmi.HIGGS, cfg["x"], cb_type=aqmi.CB_Q8_0, topk=4)
+    ref = oracle.higgs_rvq(cfg, topk=4)
+    assert np.array_equal(out["idx"], ref["idx"])
+    assert np.array_equal(bits(out["residual"]), bits(ref["residual"]))
+    assert np.array_equal(bits(out["dist"]), bits(ref["dist"]))
+    assert np.array_equal(np.sort(out["topk_idx"], -1), np.sort(ref["topk_idx"], -1))
+    assert np.array_equal(bits(np.sort(out["topk_dist"], -1)), bits(np.sort(-ref["topk_logit"], -1)))
+
+
+def test_direct_matches_oracle(torch, ctx, oracle):
+    import aqmi
+
+    print("[gpu] direct", flush=True)
+    cfg = mimi(300, Q=2)
+    out = run(torch, ctx, cfg["codebook"], aqmi.DIRECT, cfg["x"])
+    ref = oracle.direct_rvq(cfg)
+    assert np.array_equal(out["idx"], ref["idx"])
+    assert np.array_equal(bits(out["residual"]), bits(ref["residual"]))
+    assert np.array_equal(bits(out["dist"]), bits(ref["dist"]))
+
+
+@pytest.mark.parametrize("recipe", [0, 1, 2])
+def test_exact_ties_and_zero_distance(torch, ctx, oracle, recipe):
+    """Duplicated codewords (exact ties) and queries equal to codewords
+    (distance 0): the certificate cannot settle these, the exact scan must
+    apply the reference's tie rule (ggml argmax: last index; DIRECT: first)."""
+    from aqmi import synth
+
+    print(f"[gpu] ties recipe={recipe}", flush=True)
+    Q, N, K, M = 2, 2048, 256, 200
+    cb = synth.normal(31, 2, (Q, N, K), 1.0 / 16)
+    cb[:, 1::2] = cb[:, 0::2]
+    x = synth.normal(31, 1, (M, K))
+    x[:50] = cb[0, 10:60]
+    cfg = dict(x=x, M=M, K=K, Q=Q, N=N, codebook=cb)
+    out = run(torch, ctx, cb, recipe, x)
+    ref = {0: oracle.euclid_rvq, 1: oracle.higgs_rvq, 2: oracle.direct_rvq}[recipe](cfg)
+    assert np.array_equal(out["idx"], ref["idx"])
+    assert np.array_equal(bits(out["residual"]), bits(ref["residual"]))
+    assert out["fails"].sum() > 0
+
+
+def test_teacher_forced(torch, ctx, oracle):
+    import aqmi
+
+    cfg = mimi(400)
+    rng = np.random.default_rng(3)
+    force = rng.integers(0, cfg["N"], size=(400, cfg["Q"]), dtype=np.int32)
+    out = run(torch, ctx, cfg["codebook"], aqmi.OMNIVOICE, cfg["x"], force=force)
+    ref = oracle.euclid_rvq(cfg, force_idx=force)
+    assert np.array_equal(out["idx"], ref["idx"])
+    assert np.array_equal(bits(out["residual"]), bits(ref["residual"]))
+
+
+def test_nonfinite_queries(torch, ctx, oracle):
+    import aqmi
+
+    cfg = mimi(64, Q=2)
+    x = cfg["x"].copy()
+    x[3, 7] = np.nan
+    x[9, :] = np.inf
+    cfg["x"] = x
+    out = run(torch, ctx, cfg["codebook"], aqmi.OMNIVOICE, x)
+    ref = oracle.euclid_rvq(cfg)
+    assert np.array_equal(out["idx"], ref["idx"])
+    a, b = out["residual"], ref["residual"]
+    assert np.array_equal(np.isnan(a), np.isnan(b))
+    assert np.array_equal(bits(a[~np.isnan(a)]), bits(b[~np.isnan(b)]))
+
+
+def test_gather_and_decode(torch, ctx):
+    import aqmi
+    from aqmi import synth
+
+    cfg = mimi(10)
+    cbs = aqmi.Codebooks(ctx, cfg["codebook"], aqmi.OMNIVOICE)
+    N, K = cbs.N, cbs.K
+    idx = torch.arange(N, dtype=torch.int32, device="cuda")
+    out = torch.empty((N, K), dtype=torch.float32, device="cuda")
+    cbs.gather(1, idx, out)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(out.cpu().numpy()), bits(cfg["codebook"][1]))
+    codes = np.stack([np.arange(50) * 7 % N, np.arange(50) * 13 % N, np.arange(50) * 3 % N], 1).astype(np.int32)
+    dec = torch.empty((50, K), dtype=torch.float32, device="cuda")
+    cbs.decode(torch.from_numpy(codes).cuda(), dec)
+    torch.cuda.synchronize()
+    want = np.full((50, K), -0.0, np.float32)
+    for s in range(3):
+        want = (want + cfg["codebook"][s][codes[:, s]]).astype(np.float32)
+    assert np.array_equal(bits(dec.cpu().numpy()), bits(want))
+    bad = torch.tensor([0, N], dtype=torch.int32, device="cuda")
+    with pytest.raises(aqmi.AqError) as e:
+        cbs.gather(0, bad, out[:2])
+    assert e.value.status == 3
+    with pytest.raises(aqmi.AqError) as e:
+        aqmi.Codebooks(ctx, synth.normal(1, 1, (1, 100, 256)), aqmi.OMNIVOICE)
+    assert e.value.status == 2
+    q8 = synth.q8_0_random_codebook(1, 1, 64, 256)[None]
+    with pytest.raises(aqmi.AqError) as e:
+        aqmi.Codebooks(ctx, q8, aqmi.OMNIVOICE, aqmi.CB_Q8_0)
+    assert e.value.status == 5
+
+
+def test_certificate_settles_almost_every_frame(torch, ctx):
+    """On the Mimi workload the exact scan is the rare path."""
+    import aqmi
+
+    cfg = mimi(4000, Q=2)
+    out = run(torch, ctx, cfg["codebook"], aqmi.OMNIVOICE, cfg["x"], want_dist=False)
+    print(f"[gpu] fallback frames per stage: {out['fails'].tolist()}", flush=True)
+    assert (out["fails"] <= 40).all()
+
+
+@pytest.mark.parametrize("cb_type", [0, 1])
+def test_topk_with_more_ties_than_k(torch, ctx, oracle, cb_type):
+    """Six copies of one codeword and queries on it: top-4 lists the four
+    smallest tied indices (ggml top_k order) while the code is the last tied
+    index (ggml argmax), which lies outside the top-4 list."""
+    import aqmi
+    from aqmi import synth
+
+    print(f"[gpu] topk ties cb_type={cb_type}", flush=True)
+    Q, N, K, M = 1, 1024, 256, 64
+    if cb_type == 1:
+        cb = synth.q8_0_random_codebook(41, 1, N, K)[None]
+        dq = synth.q8_0_dequantize(cb[0])
+        for j in (100, 300, 500, 700, 900):
+            cb[0, j] = cb[0, 7]
+        x = np.repeat(dq[7][None], M, 0) + synth.normal(41, 2, (M, K), 1e-4)
+    else:
+        cb = synth.normal(41, 1, (Q, N, K), 1.0)
+        for j in (100, 300, 500, 700, 900):
+            cb[0, j] = cb[0, 7]
+        x = np.repeat(cb[0, 7][None], M, 0) + synth.normal(41, 2, (M, K), 1e-4)
+    x = x.astype(np.float32)
+    cfg = dict(x=x, M=M, K=K, Q=Q, N=N, codebook=cb) if cb_type == 0 else dict(x=x, M=M, K=K, Q=Q, N=N, codebook_q8=cb)
+    out = run(torch, ctx, cb, aqmi.HIGGS, x, cb_type=cb_type, topk=4)
+    ref = oracle.higgs_rvq(cfg, topk=4)
+    assert (ref["idx"] == 900).all()
+    assert np.array_equal(out["idx"], ref["idx"])
+    assert np.array_equal(bits(out["residual"]), bits(ref["residual"]))
+    assert np.array_equal(out["topk_idx"], ref["topk_idx"])
+    assert np.array_equal(bits(out["topk_dist"]), bits(-ref["topk_logit"]))

@@ -257,3 +257,32 @@ def test_gather_identity_and_range(o):
     assert o.lib.aqo_gather_f32(cb, 64, 256, idx, 64, out) == 0
     assert _beq(out, cb)
     assert o.lib.aqo_gather_f32(cb, 64, 256, np.array([64], np.int32), 1, out) == -1
+
+
+# ------------------------------------------------ direct-distance recipe --
+
+def test_oracle_direct_matches_reference_vector_quantizer(o, ref):
+    """engine::runtime::VectorQuantizer::compute, compiled from the reference
+    sources, returns the nearest codewords; the restatement's codes gather
+    the same rows bit for bit."""
+    cfg = synth.make_config(2, rows=40)
+    cb = cfg["codebook"][0]
+    want = ref.vector_quantizer(cfg["x"], cb, batch=4)
+    c = dict(x=cfg["x"], M=40, K=256, Q=1, N=cb.shape[0], codebook=cb[None])
+    got = o.direct_rvq(c)
+    assert _beq(cb[got["idx"][:, 0]], want)
+
+
+def test_oracle_direct_first_index_on_ties(o, ref):
+    cb = synth.normal(9, 2, (64, 32), 0.5)
+    cb[1::2] = cb[0::2]
+    x = cb[[4, 5, 10]].copy() + np.float32(0.0)
+    c = dict(x=x, M=3, K=32, Q=1, N=64, codebook=cb[None])
+    got = o.direct_rvq(c)
+    assert got["idx"][:, 0].tolist() == [4, 4, 10]          # first of the equal minima
+    assert _beq(ref.vector_quantizer(x, cb), cb[got["idx"][:, 0]])
+
+
+def test_reference_vector_quantizer_size_check(ref):
+    with pytest.raises(RuntimeError):
+        ref.vector_quantizer(np.zeros((4, 8), np.float32), np.zeros((3, 7), np.float32))
