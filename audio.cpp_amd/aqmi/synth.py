@@ -19,6 +19,8 @@ The BASELINE workloads (configs 0-4) are built by `make_config`.
 
 from __future__ import annotations
 
+import os
+
 import numpy as np
 
 _M64 = np.uint64(0xFFFFFFFFFFFFFFFF)
@@ -81,17 +83,39 @@ def _uniform53(z: np.ndarray) -> np.ndarray:
     return (z >> np.uint64(11)).astype(np.float64) * _TWO_M53
 
 
-def normal(seed: int, stream: int, shape, std: float = 1.0) -> np.ndarray:
-    n = int(np.prod(shape))
-    base = _base(seed, stream)
-    i = np.arange(n, dtype=np.uint64)
+_CHUNK = 1 << 20   # elements per pass: keeps the float64 temporaries in cache
+
+
+def _normal_chunk(base: np.uint64, i0: int, n: int) -> np.ndarray:
+    i = np.arange(i0, i0 + n, dtype=np.uint64)
     with np.errstate(over="ignore"):
         a = _splitmix64(base + np.uint64(2) * i)
         b = _splitmix64(base + np.uint64(2) * i + np.uint64(1))
     u1 = ((a >> np.uint64(11)).astype(np.float64) + 1.0) * _TWO_M53
     u2 = _uniform53(b)
-    z = np.sqrt(-2.0 * _det_log(u1)) * _det_cos_2pi(u2)
-    return (z * float(std)).astype(np.float32).reshape(shape)
+    return np.sqrt(-2.0 * _det_log(u1)) * _det_cos_2pi(u2)
+
+
+def normal(seed: int, stream: int, shape, std: float = 1.0) -> np.ndarray:
+    n = int(np.prod(shape))
+    base = _base(seed, stream)
+    out = np.empty(n, np.float32)
+
+    def fill(i0):
+        m = min(_CHUNK, n - i0)
+        out[i0:i0 + m] = (_normal_chunk(base, i0, m) * float(std)).astype(np.float32)
+
+    starts = range(0, n, _CHUNK)
+    if len(starts) > 2:
+        # numpy releases the GIL inside these element-wise loops
+        from concurrent.futures import ThreadPoolExecutor
+
+        with ThreadPoolExecutor(max_workers=min(8, os.cpu_count() or 1)) as pool:
+            list(pool.map(fill, starts))
+    else:
+        for i0 in starts:
+            fill(i0)
+    return out.reshape(shape)
 
 
 def uniform(seed: int, stream: int, shape, lo: float, hi: float) -> np.ndarray:

@@ -282,18 +282,33 @@ __global__ __launch_bounds__(kThreads, 1) void euclid_stage_kernel(StageArgs a) 
     // ---- phase 0: frames -> bf16 fragments in registers, rounding norms ----
     // x~ fragments stay packed (2 bf16 per register) for the whole sweep.
     u32x4 xb[FG][KS];
-    float nx2[FG], nd2[FG], nq2[FG], nxx2[FG];
+    float nx2[FG], nd2[FG], nxx2[FG];
 #pragma unroll
     for (int g = 0; g < FG; ++g) {
         const int64_t m = m_base + g * 16 + col;
         const int64_t mc = m < a.M ? m : a.M - 1;
         const float *xr = a.xin + mc * K;
-        float sx = 0.0f, sd = 0.0f, sq = 0.0f, sxx = 0.0f;
+        float sx = 0.0f, sd = 0.0f, sxx = 0.0f;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
             const f32x4 lo = *reinterpret_cast<const f32x4 *>(xr + ks * 32 + kq * 8);
             const f32x4 hi = *reinterpret_cast<const f32x4 *>(xr + ks * 32 + kq * 8 + 4);
-            const float v[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            float v[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            if (Q8) {
+                // A Q8_0 mul_mat scores the query's Q8_0 image x_q = q * d
+                // (x86 quantize_row_q8_0: one block = this 32-wide K slice),
+                // so the matrix cores contract bf16(x_q) and the bound only
+                // has to cover bf16 rounding.  x_q is exact in fp32.
+                float am = 0.0f;
+#pragma unroll
+                for (int t = 0; t < 8; ++t) am = fmaxf(am, fabsf(v[t]));
+                am = fmaxf(am, __shfl_xor(am, 16));
+                am = fmaxf(am, __shfl_xor(am, 32));
+                const float dq = static_cast<float>(static_cast<_Float16>(__fdiv_rn(am, 127.0f)));
+                const float id = am != 0.0f ? __fdiv_rn(127.0f, am) : 0.0f;
+#pragma unroll
+                for (int t = 0; t < 8; ++t) v[t] = __fmul_rn(__builtin_rintf(__fmul_rn(v[t], id)), dq);
+            }
             u32x4 packed;
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
@@ -311,22 +326,6 @@ __global__ __launch_bounds__(kThreads, 1) void euclid_stage_kernel(StageArgs a) 
                 sxx = __fmaf_rn(v[2 * t + 1], v[2 * t + 1], sxx);
             }
             xb[g][ks] = packed;
-            if (Q8) {
-                // the query block is this K slice: amax over the 4 quarters
-                float am = 0.0f;
-#pragma unroll
-                for (int t = 0; t < 8; ++t) am = fmaxf(am, fabsf(v[t]));
-                am = fmaxf(am, __shfl_xor(am, 16));
-                am = fmaxf(am, __shfl_xor(am, 32));
-                const float dq = static_cast<float>(static_cast<_Float16>(__fdiv_rn(am, 127.0f)));
-                const float id = am != 0.0f ? __fdiv_rn(127.0f, am) : 0.0f;
-#pragma unroll
-                for (int t = 0; t < 8; ++t) {
-                    const float q = __builtin_rintf(__fmul_rn(v[t], id));
-                    const float e = v[t] - q * dq;
-                    sq = __fmaf_rn(e, e, sq);
-                }
-            }
         }
         sx += __shfl_xor(sx, 16);
         sx += __shfl_xor(sx, 32);
@@ -337,11 +336,6 @@ __global__ __launch_bounds__(kThreads, 1) void euclid_stage_kernel(StageArgs a) 
         nx2[g] = sx;
         nd2[g] = sd;
         nxx2[g] = sxx;
-        if (Q8) {
-            sq += __shfl_xor(sq, 16);
-            sq += __shfl_xor(sq, 32);
-        }
-        nq2[g] = sq;
     }
 
     // ---- phase 1: sweep the codebook ----
@@ -485,6 +479,7 @@ __global__ __launch_bounds__(kThreads, 1) void euclid_stage_kernel(StageArgs a) 
     // ---- phase 2: per-frame certificate and exact re-ranking ----
     const float u = 5.9604645e-8f;   // 2^-24
     const int Tk = a.topk > 0 ? a.topk : 1;
+    const int Tsel = a.topk > 0 ? a.topk + 1 : 1;
     const bool want_value = a.dist != nullptr || a.topk > 0;
     int win_code[FG];
     bool win_ok[FG];
@@ -501,10 +496,9 @@ __global__ __launch_bounds__(kThreads, 1) void euclid_stage_kernel(StageArgs a) 
         const float e_bf16 = nx * a.dcmax + nd * a.cmax;
         const float e_acc = (K + 4) * u * nx * a.chmax;
         const float e_rec = (K + 16) * u * (nxe * a.cmax + nxe * nxe + a.cmax * a.cmax);
-        const float e_q8 = Q8 ? sqrtf(nq2[g]) * 1.0001f * a.cmax : 0.0f;
         const float vmax = nx * a.chmax + 0.5f * a.cmax * a.cmax + e_rec;
         const float trunc = ldexpf(vmax, lbits - 23);
-        float E = 1.02f * (e_bf16 + e_acc + e_rec + e_q8 + 4.0f * u * vmax) + trunc + 1e-30f;
+        float E = 1.02f * (e_bf16 + e_acc + e_rec + 4.0f * u * vmax) + trunc + 1e-30f;
 
         // Keys of the frame's 4 lanes, gathered in every one of them.
         float all[4 * TOPL];
@@ -568,10 +562,12 @@ __global__ __launch_bounds__(kThreads, 1) void euclid_stage_kernel(StageArgs a) 
             }
         }
         // Exact top-T over the frame's evaluated candidates (all 4 lanes agree).
-        float sel_v[4];
-        int sel_n[4];
+        // With top-k the list holds one entry more than reported, so that a
+        // tie at the k-th place (which ggml_top_k's heap resolves) is seen.
+        float sel_v[5];
+        int sel_n[5];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
+        for (int r = 0; r < 5; ++r) {
             sel_v[r] = 0.0f;
             sel_n[r] = -1;
         }
@@ -585,10 +581,10 @@ __global__ __launch_bounds__(kThreads, 1) void euclid_stage_kernel(StageArgs a) 
                     int cn = __shfl(cand_n[j], col + 16 * q);
                     float cv = __shfl(cand_val[j], col + 16 * q);
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const bool before = Tk == 1 ? ranks_before<RECIPE>(cv, cn, sel_v[r], sel_n[r])
-                                                    : topk_before<RECIPE>(cv, cn, sel_v[r], sel_n[r]);
-                        const bool take = cn >= 0 && r < Tk && (sel_n[r] < 0 || before);
+                    for (int r = 0; r < 5; ++r) {
+                        const bool before = a.topk == 0 ? ranks_before<RECIPE>(cv, cn, sel_v[r], sel_n[r])
+                                                        : topk_before<RECIPE>(cv, cn, sel_v[r], sel_n[r]);
+                        const bool take = cn >= 0 && r < Tsel && (sel_n[r] < 0 || before);
                         const float tv = sel_v[r];
                         const int tn = sel_n[r];
                         sel_v[r] = take ? cv : tv;
@@ -618,6 +614,9 @@ __global__ __launch_bounds__(kThreads, 1) void euclid_stage_kernel(StageArgs a) 
                 // With Tk ties at the maximum, a further tie outside the list
                 // could hold the larger index argmax keeps: scan exactly.
                 if (RECIPE != DIRECT && Tk > 1 && sv == sel_v[0]) ok = false;
+                // A tie at the k-th place: ggml_top_k keeps whichever of the
+                // tied codes its heap keeps; the exact scan replays it.
+                if (RECIPE != DIRECT && a.topk > 0 && sel_n[Tk] >= 0 && sel_v[Tk] == sv) ok = false;
             }
             // argmax among exact ties keeps ggml's last index
             int w = sel_n[0];
@@ -810,6 +809,38 @@ __device__ void exact_values_fq(const StageArgs &a, int K, int n, const float *x
                                 : __fsub_rn(__fsub_rn(__fmul_rn(dot[f], 2.0f), x2[f]), a.e2[n]);
 }
 
+// One step of libstdc++'s binary heap (GCC 11.4 std::__adjust_heap followed
+// by std::__push_heap) with comp(a, b) = value(a) > value(b): the root holds
+// the worst kept element.  std::partial_sort builds the heap over the first k
+// codes and lets each later code that is strictly better than the root
+// replace it, which decides which of several equal values ggml_top_k keeps.
+__device__ void heap_adjust(int *hn, float *hv, int hole, int len, int vn, float vv) {
+    const int top = hole;
+    int child = hole;
+    while (child < (len - 1) / 2) {
+        child = 2 * (child + 1);
+        if (hv[child] > hv[child - 1]) child--;
+        hn[hole] = hn[child];
+        hv[hole] = hv[child];
+        hole = child;
+    }
+    if ((len & 1) == 0 && child == (len - 2) / 2) {
+        child = 2 * (child + 1);
+        hn[hole] = hn[child - 1];
+        hv[hole] = hv[child - 1];
+        hole = child - 1;
+    }
+    int parent = (hole - 1) / 2;
+    while (hole > top && hv[parent] > vv) {
+        hn[hole] = hn[parent];
+        hv[hole] = hv[parent];
+        hole = parent;
+        parent = (hole - 1) / 2;
+    }
+    hn[hole] = vn;
+    hv[hole] = vv;
+}
+
 template <int RECIPE>
 __device__ inline bool fb_before(float va, int na, float vb, int nb, bool topk) {
     return topk ? topk_before<RECIPE>(va, na, vb, nb) : ranks_before<RECIPE>(va, na, vb, nb);
@@ -824,10 +855,12 @@ __global__ __launch_bounds__(kFbChunk) void euclid_fb_values_kernel(StageArgs a,
     __shared__ float x2s[kFQ];
     __shared__ float red_v[kFbChunk];
     __shared__ int red_n[kFbChunk];
-    __shared__ int chosen[4];
+    __shared__ int chosen[5];
     const int count = *a.fail_count;
-    const int T = a.topk;  // top-k slots (ranked value desc, index asc) ...
-    const int Tc = T + 1;  // ... plus the argmax slot (the reference's tie rule)
+    // top-k slots (value desc, index asc; one more than k to see a tie at the
+    // k-th place), then the argmax slot (the reference's tie rule)
+    const int T = a.topk > 0 ? a.topk + 1 : 0;
+    const int Tc = T + 1;
     const int ngroups = (count + kFQ - 1) / kFQ;
     const int64_t nwork = static_cast<int64_t>(ngroups) * fb.nch;
     for (int64_t w = blockIdx.x; w < nwork; w += gridDim.x) {
@@ -899,14 +932,16 @@ __global__ __launch_bounds__(kWave) void euclid_fb_select_kernel(StageArgs a, in
     __shared__ float vals64[kWave];
     const int lane = threadIdx.x;
     const int count = *a.fail_count;
-    const int T = a.topk;
+    __shared__ int heap_n[4];
+    __shared__ float heap_v[4];
+    const int T = a.topk > 0 ? a.topk + 1 : 0;
     const int Tc = T + 1;
     for (int slot = blockIdx.x; slot < count; slot += gridDim.x) {
         const int64_t m = a.fail_list[slot];
-        float sel_v[4];
-        int sel_n[4];
+        float sel_v[5];
+        int sel_n[5];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
+        for (int r = 0; r < 5; ++r) {
             sel_v[r] = 0.0f;
             sel_n[r] = -1;
         }
@@ -942,17 +977,28 @@ __global__ __launch_bounds__(kWave) void euclid_fb_select_kernel(StageArgs a, in
                 }
             }
             if (tk) {
-                sel_v[r] = bv;
-                sel_n[r] = bn;
+#pragma unroll
+                for (int q = 0; q < 5; ++q)
+                    if (q == r) {
+                        sel_v[q] = bv;
+                        sel_n[q] = bn;
+                    }
             } else {
                 code = bn < 0 ? 0 : bn;
                 code_v = bv;
             }
         }
-        if (RECIPE != DIRECT && fb.nan_flag[slot]) {
-            // ggml_vec_argmax_f32 in code order: MAX(max, v), index of the
-            // last element equal to the running max (NaN restarts it).
-            for (int k = lane; k < K; k += kWave) xs[k] = a.xin[m * K + k];
+        const int ktop = a.topk;
+        bool kth_tie = false;
+#pragma unroll
+        for (int q = 1; q < 5; ++q)
+            if (q == ktop) kth_tie = sel_n[q] >= 0 && sel_v[q] == sel_v[q - 1];
+        const bool nan_seen = fb.nan_flag[slot] != 0;
+        if (RECIPE != DIRECT && (nan_seen || (ktop > 0 && kth_tie))) {
+            // Replay in code order: ggml_vec_argmax_f32 (MAX(max, v), index of
+            // the last element equal to the running max; NaN restarts it) and
+            // ggml_top_k's heap selection (libstdc++ std::partial_sort).
+            for (int kk = lane; kk < K; kk += kWave) xs[kk] = a.xin[m * K + kk];
             __syncthreads();
             float x2 = 0.0f;
             if (RECIPE == HIGGS) x2 = sum_squares(xs, K);
@@ -967,14 +1013,47 @@ __global__ __launch_bounds__(kWave) void euclid_fb_select_kernel(StageArgs a, in
                 __syncthreads();
                 if (lane == 0)
                     for (int i = 0; i < kWave && base + i < a.N; ++i) {
+                        const int n_i = base + i;
                         const float v = vals64[i];
                         mx = mx > v ? mx : v;
-                        if (mx == v) id = base + i;
+                        if (mx == v) id = n_i;
+                        if (ktop > 0) {
+                            if (n_i < ktop) {
+                                heap_n[n_i] = n_i;
+                                heap_v[n_i] = v;
+                                if (n_i == ktop - 1 && ktop >= 2)
+                                    for (int par = (ktop - 2) / 2;; --par) {
+                                        heap_adjust(heap_n, heap_v, par, ktop, heap_n[par], heap_v[par]);
+                                        if (par == 0) break;
+                                    }
+                            } else if (v > heap_v[0]) {
+                                heap_adjust(heap_n, heap_v, 0, ktop, n_i, v);
+                            }
+                        }
                     }
                 __syncthreads();
             }
-            code = __shfl(id, 0);
-            code_v = __shfl(mx, 0);
+            if (nan_seen) {
+                code = __shfl(id, 0);
+                code_v = __shfl(mx, 0);
+            }
+            if (ktop > 0 && lane == 0) {
+                // report the kept set best first, ties by index
+                for (int r = 0; r < ktop; ++r) {
+                    int b = -1;
+                    for (int q = 0; q < ktop; ++q) {
+                        bool used = false;
+                        for (int t = 0; t < r; ++t) used |= sel_n[t] == heap_n[q];
+                        if (!used && (b < 0 || topk_before<RECIPE>(heap_v[q], heap_n[q], heap_v[b], heap_n[b]))) b = q;
+                    }
+#pragma unroll
+                    for (int q = 0; q < 5; ++q)
+                        if (q == r) {
+                            sel_n[q] = heap_n[b];
+                            sel_v[q] = heap_v[b];
+                        }
+                }
+            }
             __syncthreads();
         }
         if (lane == 0) {
@@ -1331,7 +1410,7 @@ aq_status aq_euclid_encode(aq_ctx *ctx, const aq_codebooks *cb, const float *x, 
     int32_t *list = fails + 64;
     // Exact-scan work space: per failed frame, the best T codes of every
     // 256-code block, and a NaN flag.
-    const int Tfb = topk + 1;
+    const int Tfb = (topk > 0 ? topk + 1 : 0) + 1;
     FbArgs fb{};
     fb.nch = static_cast<int>((cb->N + kFbChunk - 1) / kFbChunk);
     {

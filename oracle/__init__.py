@@ -83,6 +83,8 @@ class Oracle:
         L.aqo_euclid_rvq.restype = C.c_int
         L.aqo_euclid_rvq.argtypes = [_f32p, _i64, _i64, _i64, _i64, _f32p, C.c_void_p, _i32p, _f32p, C.c_void_p]
         L.aqo_higgs_rvq.restype = C.c_int
+        L.aqo_top_k_f32.restype = None
+        L.aqo_top_k_f32.argtypes = [_f32p, _i64, C.c_int, _i32p]
         L.aqo_higgs_rvq.argtypes = [_f32p, _i64, _i64, _i64, _i64, C.c_void_p, C.c_int, C.c_int, C.c_void_p,
                                     _i32p, _f32p, C.c_void_p, C.c_void_p, C.c_void_p]
         L.aqo_direct_rvq.restype = C.c_int
@@ -139,6 +141,14 @@ class Oracle:
         assert rc == 0
         return dict(idx=idx, residual=res, dist=dist)
 
+    def top_k(self, v, k: int):
+        """aqo_top_k_f32 over the rows of v."""
+        v = np.ascontiguousarray(v, np.float32)
+        out = np.zeros((v.shape[0], k), np.int32)
+        for r in range(v.shape[0]):
+            self.lib.aqo_top_k_f32(v[r], v.shape[1], k, out[r])
+        return out
+
     def higgs_rvq(self, cfg: dict, force_idx=None, topk: int = 0):
         x = np.ascontiguousarray(cfg["x"], np.float32)
         M, K = x.shape
@@ -192,6 +202,16 @@ class Ref:
         L.aqref_vector_quantizer.restype = C.c_int
         L.aqref_vector_quantizer.argtypes = [_f32p, _i64, _i64, _i64, _i64, _f32p, _i64, _i64, _f32p]
         L.aqref_quantize_chunk_q8_0.argtypes = [_f32p, C.c_void_p, _i64, _i64]
+        L.aqref_top_k.restype = None
+        L.aqref_top_k.argtypes = [_f32p, _i64, _i64, C.c_int, _i32p, C.c_int]
+
+    def top_k(self, v, k: int, threads: int = 8):
+        """ggml_top_k over the rows of v, in ggml's order."""
+        v = np.ascontiguousarray(v, np.float32)
+        rows, n = v.shape
+        out = np.zeros((rows, k), np.int32)
+        self.lib.aqref_top_k(v, rows, n, k, out, threads)
+        return out
 
     def dac_rvq(self, cfg: dict, threads: int = 8, recon: bool = True, materialize: bool = True):
         x = np.ascontiguousarray(cfg["x"], np.float32)

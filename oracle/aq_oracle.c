@@ -346,13 +346,54 @@ int aqo_euclid_rvq(const float *x, int64_t M, int64_t K, int64_t Q, int64_t N,
     return 0;
 }
 
-typedef struct { float v; int32_t i; } aqo_pair;
+/* ggml_top_k on the CPU (ops.cpp:8423-8456) is std::partial_sort over the
+ * index sequence 0..N-1 with comp(a, b) = v[a] > v[b], then dst[0] and
+ * dst[1] swapped.  Which of several equal values survive at the k-th place
+ * is decided by the heap inside std::partial_sort, so the heap is restated
+ * here as libstdc++ (GCC 11.4, the toolchain the reference build uses)
+ * implements it: std::__heap_select = make_heap over the first k, then every
+ * later element strictly better than the root replaces it (pop_heap), then
+ * std::__sort_heap.  Textbook binary heap with the hole-sifting adjust_heap
+ * followed by push_heap. */
+static void heap_adjust(int32_t *h, const float *v, int64_t hole, int64_t len, int32_t val) {
+    const int64_t top = hole;
+    int64_t child = hole;
+    while (child < (len - 1) / 2) {
+        child = 2 * (child + 1);
+        if (v[h[child]] > v[h[child - 1]]) child--;
+        h[hole] = h[child];
+        hole = child;
+    }
+    if ((len & 1) == 0 && child == (len - 2) / 2) {
+        child = 2 * (child + 1);
+        h[hole] = h[child - 1];
+        hole = child - 1;
+    }
+    int64_t parent = (hole - 1) / 2;
+    while (hole > top && v[h[parent]] > v[val]) {
+        h[hole] = h[parent];
+        hole = parent;
+        parent = (hole - 1) / 2;
+    }
+    h[hole] = val;
+}
 
-static int cmp_desc(const void *pa, const void *pb) {
-    const aqo_pair *a = (const aqo_pair *)pa, *b = (const aqo_pair *)pb;
-    if (a->v > b->v) return -1;
-    if (a->v < b->v) return 1;
-    return a->i < b->i ? -1 : (a->i > b->i);
+void aqo_top_k_f32(const float *v, int64_t n, int k, int32_t *dst) {
+    int32_t *h = dst;
+    for (int i = 0; i < k; ++i) h[i] = i;
+    if (k >= 2)
+        for (int64_t parent = (k - 2) / 2;; --parent) {
+            heap_adjust(h, v, parent, k, h[parent]);
+            if (parent == 0) break;
+        }
+    for (int64_t i = k; i < n; ++i)
+        if (v[i] > v[h[0]]) heap_adjust(h, v, 0, k, (int32_t)i);
+    for (int64_t last = k - 1; last > 0; --last) {   /* sort_heap */
+        const int32_t val = h[last];
+        h[last] = h[0];
+        heap_adjust(h, v, 0, last, val);
+    }
+    if (k > 1) { const int32_t t = dst[0]; dst[0] = dst[1]; dst[1] = t; }
 }
 
 /* Higgs encode quantizer without projections
@@ -375,9 +416,8 @@ int aqo_higgs_rvq(const float *x, int64_t M, int64_t K, int64_t Q, int64_t N,
     float *lg = (float *)malloc((size_t)N * sizeof(float));
     float *tmp = (float *)malloc((size_t)(K > N ? K : N) * sizeof(float));
     aqo_block_q8_0 *xq = (aqo_block_q8_0 *)malloc((size_t)(nb > 0 ? nb : 1) * sizeof(aqo_block_q8_0));
-    aqo_pair *pairs = (aqo_pair *)malloc((size_t)N * sizeof(aqo_pair));
-    if (!cbf || !e2 || !lg || !tmp || !xq || !pairs) {
-        free(cbf); free(e2); free(lg); free(tmp); free(xq); free(pairs);
+    if (!cbf || !e2 || !lg || !tmp || !xq) {
+        free(cbf); free(e2); free(lg); free(tmp); free(xq);
         return -1;
     }
     for (int64_t s = 0; s < Q; ++s) {
@@ -402,18 +442,15 @@ int aqo_higgs_rvq(const float *x, int64_t M, int64_t K, int64_t Q, int64_t N,
             idx[m * Q + s] = code;
             if (dist) dist[m * Q + s] = -lg[code];
             if (topk > 0) {
-                for (int64_t n = 0; n < N; ++n) { pairs[n].v = lg[n]; pairs[n].i = (int32_t)n; }
-                qsort(pairs, (size_t)N, sizeof(aqo_pair), cmp_desc);
-                for (int k = 0; k < topk; ++k) {
-                    topk_idx[(m * Q + s) * topk + k] = pairs[k].i;
-                    topk_logit[(m * Q + s) * topk + k] = pairs[k].v;
-                }
+                int32_t *ti = topk_idx + (m * Q + s) * topk;
+                aqo_top_k_f32(lg, N, topk, ti);
+                for (int k = 0; k < topk; ++k) topk_logit[(m * Q + s) * topk + k] = lg[ti[k]];
             }
             const int use = force_idx ? force_idx[m * Q + s] : code;
             for (int64_t k = 0; k < K; ++k) rm[k] = rm[k] - cbf[(int64_t)use * K + k];
         }
     }
-    free(cbf); free(e2); free(lg); free(tmp); free(xq); free(pairs);
+    free(cbf); free(e2); free(lg); free(tmp); free(xq);
     return 0;
 }
 

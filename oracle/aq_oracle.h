@@ -58,13 +58,16 @@ int aqo_euclid_rvq(const float *x, int64_t M, int64_t K, int64_t Q, int64_t N,
 
 /* Higgs-style Euclidean RVQ: logit = ((2*dot) - |x|^2) - |c|^2, F32 codebook
  * (cb_type 0, [Q,N,K] floats) or Q8_0 (cb_type 1, [Q,N,K/32] blocks).
- * dist [M,Q] = -logit[idx]; topk_idx/topk_logit [M,Q,topk] sorted by
- * descending logit, ties by ascending index (ggml's own order is unspecified
- * and compared as a set). */
+ * dist [M,Q] = -logit[idx]; topk_idx/topk_logit [M,Q,topk] as ggml_top_k
+ * leaves them (aqo_top_k_f32: the same set and the same order). */
 int aqo_higgs_rvq(const float *x, int64_t M, int64_t K, int64_t Q, int64_t N,
                   const void *cb, int cb_type, int topk, const int32_t *force_idx,
                   int32_t *idx, float *residual, float *dist,
                   int32_t *topk_idx, float *topk_logit);
+
+/* ggml_top_k of one row: the k indices std::partial_sort (libstdc++) keeps
+ * with comp(a, b) = v[a] > v[b], in its order, dst[0] and dst[1] swapped. */
+void aqo_top_k_f32(const float *v, int64_t n, int k, int32_t *dst);
 
 /* Direct-distance RVQ (VectorQuantizer::compute / Qwen3 nearest_code):
  * rounded squares added in order, first index of the minimum.  dist [M,Q]

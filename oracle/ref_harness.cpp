@@ -221,7 +221,7 @@ double aqref_euclid_rvq(const float * x, int64_t M, int64_t K, int64_t Q, int64_
     double ms = 0.0;
     std::vector<float> res(x, x + M * K);
     for (int64_t s = 0; s < Q; ++s) {
-        const size_t bytes = static_cast<size_t>(M) * static_cast<size_t>(N + 4 * K) * 4 + static_cast<size_t>(N * K) * 12 + (64u << 20);
+        const size_t bytes = static_cast<size_t>(M) * static_cast<size_t>(2 * N + 4 * K) * 4 + static_cast<size_t>(N * K) * 12 + (64u << 20);
         Ctx c(bytes);
         ggml_context * ctx = c.ctx;
         const float * cbs = cb + s * N * K;
@@ -275,7 +275,7 @@ double aqref_higgs_rvq(const float * x, int64_t M, int64_t K, int64_t Q, int64_t
     const ggml_type t = cb_type == 1 ? GGML_TYPE_Q8_0 : GGML_TYPE_F32;
     const size_t cb_bytes = ggml_row_size(t, K) * static_cast<size_t>(N);
     for (int64_t s = 0; s < Q; ++s) {
-        const size_t bytes = static_cast<size_t>(M) * static_cast<size_t>(N * 4 + 6 * K) * 4 + static_cast<size_t>(N * K) * 16 + (64u << 20);
+        const size_t bytes = static_cast<size_t>(M) * static_cast<size_t>(N * 6 + 6 * K) * 4 + static_cast<size_t>(N * K) * 16 + (64u << 20);
         Ctx c(bytes);
         ggml_context * ctx = c.ctx;
         ggml_tensor * R = ggml_new_tensor_2d(ctx, GGML_TYPE_F32, K, M);
@@ -315,6 +315,18 @@ double aqref_higgs_rvq(const float * x, int64_t M, int64_t K, int64_t Q, int64_t
     }
     if (residual) std::memcpy(residual, res.data(), res.size() * 4);
     return ms;
+}
+
+// ggml_top_k alone (ops.cpp:8423-8456) on rows of n values: v [rows, n],
+// dst [rows, k] in ggml's order.
+void aqref_top_k(const float * v, int64_t rows, int64_t n, int k, int32_t * dst, int n_threads) {
+    ggml_cpu_init();
+    Ctx c(static_cast<size_t>(rows) * static_cast<size_t>(n + k) * 8 + (16u << 20));
+    ggml_tensor * V = ggml_new_tensor_2d(c.ctx, GGML_TYPE_F32, n, rows);
+    std::memcpy(V->data, v, static_cast<size_t>(rows * n) * 4);
+    ggml_tensor * tk = ggml_top_k(c.ctx, V, k);
+    run_graph(c.ctx, tk, n_threads);
+    std::memcpy(dst, tk->data, static_cast<size_t>(rows * k) * 4);
 }
 
 // The reference's framework host quantizer, engine::runtime::VectorQuantizer

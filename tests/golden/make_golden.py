@@ -7,7 +7,7 @@ Inputs come from audio.cpp_amd/aqmi/synth.py (deterministic, seeded), so a
 fixture stores only outputs: codes, and SHA-256 digests of the fp32 residual
 and reconstruction bytes (bit-exact checks), plus small value samples.
 
-    python tests/golden/make_golden.py
+    python tests/golden/make_golden.py [dac] [mimi] [kmeans] [q8]
 """
 
 from __future__ import annotations
@@ -48,11 +48,65 @@ def dac(ref: Ref, cfg_id: int, name: str, bias: bool = False, **over):
          recon_head=out["recon"][:4, :16].copy(), bias=np.array(bias), ggml_isa=np.array(ref.isa))
 
 
+def sorted_topk(idx: np.ndarray, val: np.ndarray):
+    """ggml_top_k leaves the k best in no particular order: sort each list by
+    (value desc, index asc) so fixtures compare as sets."""
+    order = np.lexsort((idx, -val.astype(np.float64)), axis=-1)
+    return np.take_along_axis(idx, order, -1), np.take_along_axis(val, order, -1)
+
+
+def mimi(ref: Ref, name: str):
+    """BASELINE configs[2] with the OmniVoice score recipe (logit = 2c.r - |c|^2)."""
+    cfg = synth.make_config(2)
+    out = ref.euclid_rvq(cfg)
+    save(name, idx=out["idx"].astype(np.uint16), residual_sha=np.array(sha(out["residual"])),
+         logit_sha=np.array(sha(out["logit"])), residual_head=out["residual"][:64].copy(),
+         logit_head=out["logit"][:64].copy(), recipe=np.array("omnivoice"), ggml_isa=np.array(ref.isa))
+
+
+def kmeans(ref: Ref, name: str, chunk: int = 20000):
+    """BASELINE configs[3] with the Higgs recipe (dist = |r|^2 + |c|^2 - 2c.r).
+    Rows are independent, so the 200k x 16384 score matrix is evaluated in row
+    chunks (multiples of 16 rows keep ggml on the same tinyBLAS path)."""
+    cfg = synth.make_config(3)
+    M = cfg["M"]
+    idx = np.zeros((M, 1), np.int32)
+    dist = np.zeros((M, 1), np.float32)
+    for r0 in range(0, M, chunk):
+        part = dict(cfg, x=cfg["x"][r0:r0 + chunk], M=min(chunk, M - r0))
+        out = ref.higgs_rvq(part)
+        idx[r0:r0 + chunk] = out["idx"]
+        dist[r0:r0 + chunk] = out["dist"]
+        print(f"  k-means rows {r0}..{r0 + part['M']}", flush=True)
+    save(name, idx=idx[:, 0].astype(np.uint16), dist_sha=np.array(sha(dist)), dist_head=dist[:256, 0].copy(),
+         recipe=np.array("higgs"), ggml_isa=np.array(ref.isa))
+
+
+def q8(ref: Ref, name: str):
+    """Q8_0 codebooks, Higgs recipe, top-4 per stage."""
+    cfg = synth.make_config(4)
+    out = ref.higgs_rvq(cfg, topk=4)
+    ti, tl = sorted_topk(out["topk_idx"], out["topk_logit"])
+    save(name, idx=out["idx"].astype(np.uint16), residual_sha=np.array(sha(out["residual"])),
+         dist_sha=np.array(sha(out["dist"])), topk_idx_sha=np.array(sha(ti.astype(np.int32))),
+         topk_logit_sha=np.array(sha(tl)), residual_head=out["residual"][:64].copy(),
+         topk_idx_head=ti[:64].copy(), topk_logit_head=tl[:64].copy(), recipe=np.array("higgs-q8_0"),
+         ggml_isa=np.array(ref.isa))
+
+
 def main():
+    which = set(sys.argv[1:]) or {"dac", "mimi", "kmeans", "q8"}
     ref = Ref("native")
-    dac(ref, 0, "dac_cfg0.npz")
-    dac(ref, 1, "dac_cfg1.npz")
-    dac(ref, 0, "dac_cfg0_bias.npz", bias=True)
+    if "dac" in which:
+        dac(ref, 0, "dac_cfg0.npz")
+        dac(ref, 1, "dac_cfg1.npz")
+        dac(ref, 0, "dac_cfg0_bias.npz", bias=True)
+    if "mimi" in which:
+        mimi(ref, "mimi_cfg2.npz")
+    if "kmeans" in which:
+        kmeans(ref, "kmeans_cfg3.npz")
+    if "q8" in which:
+        q8(ref, "q8_cfg4.npz")
 
 
 if __name__ == "__main__":

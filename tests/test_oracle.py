@@ -56,6 +56,47 @@ def test_oracle_dac_matches_golden(o, name, cfg_id, bias):
     assert _sha(out["recon"]) == str(g["recon_sha"])
 
 
+def _sorted_topk(idx, val):
+    order = np.lexsort((idx, -val.astype(np.float64)), axis=-1)
+    return np.take_along_axis(idx, order, -1), np.take_along_axis(val, order, -1)
+
+
+def test_oracle_mimi_matches_golden_prefix(o):
+    """configs[2] (OmniVoice recipe): frames are independent through the
+    cascade, so the oracle on the first rows must reproduce the fixture's
+    first rows (codes, best logits and final residual, bit for bit)."""
+    g = np.load(GOLDEN / "mimi_cfg2.npz")
+    rows = 64
+    cfg = synth.make_config(2, rows=rows)
+    out = o.euclid_rvq(cfg)
+    assert np.array_equal(out["idx"], g["idx"][:rows].astype(np.int32))
+    assert _beq(out["logit"], g["logit_head"])
+    assert _beq(out["residual"], g["residual_head"])
+
+
+def test_oracle_kmeans_matches_golden_prefix(o):
+    """configs[3] (Higgs recipe, one stage of 16384 centroids, K = 768)."""
+    g = np.load(GOLDEN / "kmeans_cfg3.npz")
+    rows = 48
+    cfg = synth.make_config(3, rows=rows)
+    out = o.higgs_rvq(cfg)
+    assert np.array_equal(out["idx"][:, 0], g["idx"][:rows].astype(np.int32))
+    assert _beq(out["dist"][:, 0], g["dist_head"][:rows])
+
+
+def test_oracle_q8_topk_matches_golden_prefix(o):
+    """configs[4] (Q8_0 codebooks, Higgs recipe, top-4 sets with logits)."""
+    g = np.load(GOLDEN / "q8_cfg4.npz")
+    rows = 64
+    cfg = synth.make_config(4, rows=rows)
+    out = o.higgs_rvq(cfg, topk=4)
+    assert np.array_equal(out["idx"], g["idx"][:rows].astype(np.int32))
+    assert _beq(out["residual"], g["residual_head"])
+    ti, tl = _sorted_topk(out["topk_idx"], out["topk_logit"])
+    assert np.array_equal(ti, g["topk_idx_head"])
+    assert _beq(tl, g["topk_logit_head"])
+
+
 def test_generator_is_stable():
     """The fixtures assume the seeded generator never changes."""
     x = synth.normal(1, 1, (4,))
@@ -104,10 +145,32 @@ def test_oracle_higgs_q8_bit_exact_vs_ggml(o, ref, M):
     a, b = o.higgs_rvq(cfg, topk=4), ref.higgs_rvq(cfg, topk=4)
     assert np.array_equal(a["idx"], b["idx"])
     assert _beq(a["residual"], b["residual"]) and _beq(a["dist"], b["dist"])
-    # ggml_top_k's order is unspecified (partial_sort, then dst[0] <-> dst[1]):
-    # compare as sets, and the logits of the set.
-    assert np.array_equal(np.sort(a["topk_idx"], -1), np.sort(b["topk_idx"], -1))
-    assert _beq(np.sort(a["topk_logit"], -1), np.sort(b["topk_logit"], -1))
+    # the oracle restates ggml_top_k's own order (heap, then dst[0] <-> dst[1])
+    assert np.array_equal(a["topk_idx"], b["topk_idx"])
+    assert _beq(a["topk_logit"], b["topk_logit"])
+
+
+@pytest.mark.parametrize("n,k", [(1, 1), (2, 2), (5, 4), (6, 3), (17, 4), (64, 2), (2048, 4), (2048, 1)])
+def test_top_k_heap_selection_matches_ggml(o, ref, n, k):
+    """Rows drawn from a handful of values (many exact ties, also at the k-th
+    place) and rows with NaN / inf: which tied codes ggml_top_k keeps is
+    decided by std::partial_sort's heap; the restatement must keep the same
+    ones, in the same order.  A plain stable sort would fail these."""
+    rng = np.random.default_rng(n * 10 + k)
+    rows = [rng.integers(0, 4, size=n).astype(np.float32) for _ in range(200)]
+    rows += [rng.normal(size=n).astype(np.float32) for _ in range(20)]
+    for _ in range(20):
+        r = rng.integers(0, 3, size=n).astype(np.float32)
+        r[rng.integers(0, n, size=max(1, n // 5))] = np.nan
+        r[rng.integers(0, n)] = np.inf
+        rows.append(r)
+    v = np.stack(rows)
+    a, b = o.top_k(v, k), ref.top_k(v, k)
+    assert np.array_equal(a, b)
+    if n in (5, 6, 17):
+        # on these rows the set is not "the smallest indices among ties"
+        stable = np.argsort(-v[:200].astype(np.float64), axis=1, kind="stable")[:, :k]
+        assert not np.array_equal(np.sort(stable, 1), np.sort(b[:200], 1))
 
 
 def test_oracle_q8_quantize_matches_ggml(o, ref):
