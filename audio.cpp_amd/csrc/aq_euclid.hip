@@ -69,7 +69,7 @@ struct StageArgs {
     int64_t M;
     int N;
     const uint16_t *cbh;     // [N, K] bf16 codebook (scores)
-    const float *hh;         // [N] |c|^2 / 2
+    const float *nhh;        // [N] -|c|^2 / 2 (the score accumulators start from it)
     const float *cbf;        // [N, K] fp32 codebook (dequantised for Q8_0)
     const float *bias;       // [N] OmniVoice score bias
     const float *e2;         // [N] Higgs sum_rows(c*c)
@@ -88,8 +88,6 @@ struct StageArgs {
     int32_t *fail_list;      // [M]
     int32_t *flags;
     int exact_only;
-    int64_t debug_frame;     // >= 0: dump this frame's selection state to debug
-    float *debug;            // [4 lanes][64] (AQ_DEBUG_FRAME; diagnostics only)
 };
 
 // --------------------------------------------------------------- exact math
@@ -212,6 +210,115 @@ __device__ float dot_q8(const int8_t *__restrict__ qc, const float *__restrict__
     return reduce8(acc);
 }
 
+// Compile-time-K forms for the stage kernel: the loops unroll, so the loads
+// of later steps are issued ahead of the FMA chains that consume them.
+template <int K>
+__device__ float dot_tinyblas_k(const float *__restrict__ a, const float *__restrict__ b, float sa) {
+    float acc[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
+#pragma unroll 4
+    for (int l = 0; l < K; l += 16) {
+        const f32x4 *pa = reinterpret_cast<const f32x4 *>(a + l);
+        const f32x4 *pb = reinterpret_cast<const f32x4 *>(b + l);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const f32x4 va = pa[q], vb = pb[q];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) acc[4 * q + t] = __fmaf_rn(va[t] * sa, vb[t], acc[4 * q + t]);
+        }
+    }
+    return reduce16(acc);
+}
+
+template <int K>
+__device__ float sum_squares_k(const float *__restrict__ x) {
+    double s = 0.0;
+#pragma unroll 8
+    for (int k = 0; k < K; k += 4) {
+        const f32x4 v = *reinterpret_cast<const f32x4 *>(x + k);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) s += static_cast<double>(__fmul_rn(v[t], v[t]));
+    }
+    return static_cast<float>(s);
+}
+
+template <int K>
+__device__ float dist_direct_k(const float *__restrict__ x, const float *__restrict__ c) {
+    float d = 0.0f;
+#pragma unroll 4
+    for (int k = 0; k < K; k += 4) {
+        const f32x4 xv = *reinterpret_cast<const f32x4 *>(x + k);
+        const f32x4 cv = *reinterpret_cast<const f32x4 *>(c + k);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const float diff = __fsub_rn(xv[t], cv[t]);
+            d = __fadd_rn(d, __fmul_rn(diff, diff));
+        }
+    }
+    return d;
+}
+
+// dot_q8 with the query block quantised on the fly (quantize_block_q8's
+// arithmetic, block by block), so no per-lane copy of the quantised row.
+template <int K>
+__device__ float dot_q8_fused(const int8_t *__restrict__ qc, const float *__restrict__ dc, const float *__restrict__ x) {
+    float acc[8];
+#pragma unroll
+    for (int l = 0; l < 8; ++l) acc[l] = 0.0f;
+#pragma unroll 2
+    for (int ib = 0; ib < K / 32; ++ib) {
+        float v[32];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const f32x4 t = *reinterpret_cast<const f32x4 *>(x + 32 * ib + 4 * q);
+            v[4 * q] = t[0]; v[4 * q + 1] = t[1]; v[4 * q + 2] = t[2]; v[4 * q + 3] = t[3];
+        }
+        float amax = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(v[j]));
+        const float dx = static_cast<float>(static_cast<_Float16>(__fdiv_rn(amax, 127.0f)));
+        const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+        int qw[8];
+#pragma unroll
+        for (int l = 0; l < 8; ++l) {
+            unsigned w = 0;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const float r = __builtin_rintf(__fmul_rn(v[4 * l + t], id));
+                int qi;
+                if (!(r >= -2147483648.0f && r < 2147483648.0f)) qi = -128;
+                else qi = static_cast<int>(r) < -128 ? -128 : (static_cast<int>(r) > 127 ? 127 : static_cast<int>(r));
+                w |= (static_cast<unsigned>(qi) & 0xFFu) << (8 * t);
+            }
+            qw[l] = static_cast<int>(w);
+        }
+        const float dd = __fmul_rn(dc[ib], dx);
+        const int *pc = reinterpret_cast<const int *>(qc + 32 * ib);
+#pragma unroll
+        for (int l = 0; l < 8; ++l) {
+            const int s = __builtin_amdgcn_sdot4(pc[l], qw[l], 0, false);
+            acc[l] = __fmaf_rn(dd, static_cast<float>(s), acc[l]);
+        }
+    }
+    return reduce8(acc);
+}
+
+template <int RECIPE, bool Q8, int K>
+__device__ float exact_value_k(const StageArgs &a, const float *__restrict__ x, int n, float x2) {
+    const float *c = a.cbf + static_cast<int64_t>(n) * K;
+    if (RECIPE == DIRECT) return dist_direct_k<K>(x, c);
+    float dot;
+    if (Q8) {
+        dot = dot_q8_fused<K>(a.q8 + static_cast<int64_t>(n) * K, a.q8d + static_cast<int64_t>(n) * (K / 32), x);
+    } else {
+        const float sa = RECIPE == OMNI ? 2.0f : 1.0f;
+        dot = a.order == 0 ? dot_tinyblas_k<K>(c, x, sa) : dot_vecdot(c, x, K, sa);
+    }
+    if (RECIPE == OMNI) return __fadd_rn(dot, a.bias[n]);
+    return __fsub_rn(__fsub_rn(__fmul_rn(dot, 2.0f), x2), a.e2[n]);
+}
+
 // Recipe value of code n ("larger is better" for OMNI/HIGGS: the logit;
 // DIRECT returns the distance, smaller is better).  x2 is sum_rows(x*x)
 // (HIGGS); xq/xd the quantised query (HIGGS with a Q8_0 codebook).
@@ -248,8 +355,11 @@ __device__ inline bool topk_before(float va, int na, float vb, int nb) {
 
 // --------------------------------------------------------------- score kernel
 
-__device__ inline float key_of(float v, unsigned local, unsigned mask) {
-    return __uint_as_float((__float_as_uint(v) & ~mask) | (local & mask));
+// Score key: the score's bits with the low ones replaced by the lane-local
+// code index.  `keep` is the complement of the index mask, held in a VGPR so
+// that the bit select is one v_and_or_b32 with the (wave-uniform) index.
+__device__ inline float key_of(float v, unsigned local, unsigned keep) {
+    return __uint_as_float((__float_as_uint(v) & keep) | local);
 }
 
 template <int KS>
@@ -349,6 +459,8 @@ __global__ __launch_bounds__(kThreads, 1) void euclid_stage_kernel(StageArgs a) 
     int lbits = 0;   // bits of the lane-local code index (N/4 codes per lane)
     while ((1 << lbits) < N / 4) ++lbits;
     const unsigned kmask = (1u << lbits) - 1u;
+    unsigned vkeep;   // ~kmask in a VGPR (one scalar operand per VOP3 on gfx950)
+    asm volatile("v_mov_b32 %0, %1" : "=v"(vkeep) : "s"(~kmask));
 
     // Software pipeline over 16-code blocks bb = 0 .. N/16-1 (chunk c = bb/BPC):
     //  * A fragments live in a ring of R registers, loaded L = R-1 K-slices
@@ -384,7 +496,7 @@ __global__ __launch_bounds__(kThreads, 1) void euclid_stage_kernel(StageArgs a) 
             const int p = threadIdx.x + k * kThreads;
             *piece_dst(0, p) = cb16[p];
         }
-        if (threadIdx.x < T::CC) reinterpret_cast<float *>(lds + T::CHUNKB)[threadIdx.x] = a.hh[threadIdx.x];
+        if (threadIdx.x < T::CC) reinterpret_cast<float *>(lds + T::CHUNKB)[threadIdx.x] = a.nhh[threadIdx.x];
     }
     __syncthreads();
 
@@ -393,21 +505,24 @@ __global__ __launch_bounds__(kThreads, 1) void euclid_stage_kernel(StageArgs a) 
     for (int l = 0; l < L; ++l) ring[l] = lds_a(0, 0, l);
     f32x4 hcur = lds_h(0, 0);
     f32x4 accp[FG];
-    f32x4 hprev = hcur;
     unsigned lprev = 0;
     bool pend = false;
     u32x4 stg[PPB];
     float hstg = 0.0f;
 
-    auto epilogue = [&](const f32x4 (&acc)[FG], const f32x4 &hv, unsigned local0) {
+    // Per score: key (1 op), TOPL-1 med3 and one max-by-med3.  The upper
+    // clamp is FLT_MAX rather than +inf so the compiler keeps a plain med3
+    // (an fmax would need NaN canonicalisation of both operands); frames with
+    // a key of +inf or NaN fail the certificate in any case.
+    auto epilogue = [&](const f32x4 (&acc)[FG], unsigned local0) {
 #pragma unroll
         for (int g = 0; g < FG; ++g)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float key = key_of(acc[g][i] - hv[i], local0 + i, kmask);
+                const float key = key_of(acc[g][i], local0 + i, vkeep);
 #pragma unroll
                 for (int j = TOPL - 1; j > 0; --j) top[g][j] = __builtin_amdgcn_fmed3f(top[g][j - 1], top[g][j], key);
-                top[g][0] = __builtin_amdgcn_fmed3f(top[g][0], key, INFINITY);
+                top[g][0] = __builtin_amdgcn_fmed3f(top[g][0], key, 3.40282347e38f);
             }
     };
 
@@ -432,12 +547,13 @@ __global__ __launch_bounds__(kThreads, 1) void euclid_stage_kernel(StageArgs a) 
                 const int k = b + i * BPC;
                 if (k < T::STAGE16) stg[i] = src[threadIdx.x + k * kThreads];
             }
-            if (b == 0 && threadIdx.x < T::CC) hstg = a.hh[static_cast<int64_t>(c + 1) * T::CC + threadIdx.x];
+            if (b == 0 && threadIdx.x < T::CC) hstg = a.nhh[static_cast<int64_t>(c + 1) * T::CC + threadIdx.x];
         }
 
+        // the accumulators start from -|c|^2/2 of the block's codes
         f32x4 acc[FG];
 #pragma unroll
-        for (int g = 0; g < FG; ++g) acc[g] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int g = 0; g < FG; ++g) acc[g] = hcur;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
             const int pk = ks + L;
@@ -449,10 +565,9 @@ __global__ __launch_bounds__(kThreads, 1) void euclid_stage_kernel(StageArgs a) 
                                                                  acc[g], 0, 0, 0);
         }
         const f32x4 hnext = last_in_chunk ? hcur : lds_h(buf, b + 1);
-        if (pend) epilogue(accp, hprev, lprev);
+        if (pend) epilogue(accp, lprev);
 #pragma unroll
         for (int g = 0; g < FG; ++g) accp[g] = acc[g];
-        hprev = hcur;
         lprev = static_cast<unsigned>(bb * 4);
         pend = true;
         hcur = hnext;
@@ -474,31 +589,45 @@ __global__ __launch_bounds__(kThreads, 1) void euclid_stage_kernel(StageArgs a) 
             }
         }
     }
-    if (pend) epilogue(accp, hprev, lprev);
+    if (pend) epilogue(accp, lprev);
 
     // ---- phase 2: per-frame certificate and exact re-ranking ----
+    // 2a bounds and candidates per frame; 2b the frames' |x|^2 (Higgs);
+    // 2c every candidate (frame, code) pair of the wave evaluated exactly, one
+    // pair per lane, through a queue in LDS (the codebook tiles are dead);
+    // 2d per-frame selection, certificate and outputs.
     const float u = 5.9604645e-8f;   // 2^-24
     const int Tk = a.topk > 0 ? a.topk : 1;
     const int Tsel = a.topk > 0 ? a.topk + 1 : 1;
     const bool want_value = a.dist != nullptr || a.topk > 0;
-    int win_code[FG];
-    bool win_ok[FG];
+    constexpr int QCAP = FG * 16 * 4 * TOPL;
+    static_assert(kWaves * QCAP * 12 + kWaves * FG * 16 * 4 <= T::LDS, "exact-evaluation queue must fit in LDS");
+    __syncthreads();
+    int32_t *q_n = reinterpret_cast<int32_t *>(lds) + wave * QCAP;
+    int32_t *q_f = reinterpret_cast<int32_t *>(lds) + kWaves * QCAP + wave * QCAP;
+    float *q_v = reinterpret_cast<float *>(lds) + 2 * kWaves * QCAP + wave * QCAP;
+    float *q_x2 = reinterpret_cast<float *>(lds) + 3 * kWaves * QCAP + wave * FG * 16;
+
+    float Eg[FG], taug[FG], best0g[FG];
+    bool okg[FG], needg[FG];
+    int cand_n[FG][TOPL], qpos[FG][TOPL];
+    int qcount = 0;
 #pragma unroll
     for (int g = 0; g < FG; ++g) {
         const int64_t m = m_base + g * 16 + col;
         const bool live = m < a.M;
-        const int64_t mc = live ? m : a.M - 1;
-        const float *xr = a.xin + mc * K;
 
         // Bound E (in units of v = x.c - |c|^2/2) on |v(n) - S'(n)| for every n.
         const float nx = sqrtf(nx2[g]) * 1.0001f, nd = sqrtf(nd2[g]) * 1.0001f;
         const float nxe = nx + nd;                           // >= |x|
         const float e_bf16 = nx * a.dcmax + nd * a.cmax;
-        const float e_acc = (K + 4) * u * nx * a.chmax;
+        // fp32 accumulation from -|c|^2/2: partial sums stay below
+        // |x~||c~| + |c|^2/2
+        const float e_acc = (K + 4) * u * (nx * a.chmax + 0.5f * a.cmax * a.cmax);
         const float e_rec = (K + 16) * u * (nxe * a.cmax + nxe * nxe + a.cmax * a.cmax);
         const float vmax = nx * a.chmax + 0.5f * a.cmax * a.cmax + e_rec;
         const float trunc = ldexpf(vmax, lbits - 23);
-        float E = 1.02f * (e_bf16 + e_acc + e_rec + 4.0f * u * vmax) + trunc + 1e-30f;
+        const float E = 1.02f * (e_bf16 + e_acc + e_rec + 4.0f * u * vmax) + trunc + 1e-30f;
 
         // Keys of the frame's 4 lanes, gathered in every one of them.
         float all[4 * TOPL];
@@ -529,38 +658,77 @@ __global__ __launch_bounds__(kThreads, 1) void euclid_stage_kernel(StageArgs a) 
             }
         }
         const float vT = best[Tk - 1];
-        bool ok = !a.exact_only && (E < INFINITY) && (vT - vT == 0.0f);
-
-        // Candidates this lane must evaluate exactly.
-        float cand_val[TOPL];
-        int cand_n[TOPL];
-        int ncand = 0;
+        const bool ok = live && !a.exact_only && (E < INFINITY) && (vT - vT == 0.0f);
         const float thr = vT - 2.0f * E;
         int nabove = 0;
 #pragma unroll
         for (int t = 0; t < 4 * TOPL; ++t) nabove += all[t] >= thr ? 1 : 0;
-        const bool need_exact = want_value || nabove > 1;
-        float x2 = 0.0f;
-        int8_t xq[Q8 ? K : 1];
-        float xd[Q8 ? K / 32 : 1];
-        if (ok && need_exact) {
-            if (RECIPE != OMNI) x2 = sum_squares(xr, K);
-            if (Q8)
-                for (int ib = 0; ib < K / 32; ++ib) quantize_block_q8(xr + 32 * ib, xq + 32 * ib, xd + ib);
-        }
+        const bool need = ok && (want_value || nabove > 1);
+        Eg[g] = E;
+        taug[g] = tau;
+        best0g[g] = best[0];
+        okg[g] = ok;
+        needg[g] = need;
+        // enqueue this lane's candidates
 #pragma unroll
         for (int j = 0; j < TOPL; ++j) {
-            cand_n[j] = -1;
-            cand_val[j] = 0.0f;
             const float key = top[g][j];
-            if (ok && need_exact && key >= thr && key > -INFINITY) {
-                const unsigned local = __float_as_uint(key) & kmask;
-                const int n = static_cast<int>((local >> 2) * 16 + kq * 4 + (local & 3));
-                cand_n[j] = n;
-                cand_val[j] = exact_value<RECIPE, Q8>(a, K, xr, n, x2, xq, xd);
-                ++ncand;
+            const bool c = need && key >= thr && key > -INFINITY;
+            const unsigned local = __float_as_uint(key) & kmask;
+            const int n = static_cast<int>((local >> 2) * 16 + kq * 4 + (local & 3));
+            const unsigned long long bal = __ballot(c);
+            const int pos = qcount + static_cast<int>(__builtin_amdgcn_mbcnt_hi(
+                                         static_cast<unsigned>(bal >> 32),
+                                         __builtin_amdgcn_mbcnt_lo(static_cast<unsigned>(bal), 0u)));
+            if (c) {
+                q_n[pos] = n;
+                q_f[pos] = g * 16 + col;
             }
+            cand_n[g][j] = c ? n : -1;
+            qpos[g][j] = pos;
+            qcount += __popcll(bal);
         }
+    }
+    // 2b: sum_rows(x*x) of each frame that has candidates (one lane per frame)
+    if (RECIPE == HIGGS) {
+        int needmask = 0;   // bit g: frame (g, lane % 16) has candidates
+#pragma unroll
+        for (int g = 0; g < FG; ++g) needmask |= (__shfl(needg[g] ? 1 : 0, lane % 16) & 1) << g;
+        if (lane < FG * 16) {
+            const bool need = ((needmask >> (lane / 16)) & 1) != 0;
+            q_x2[lane] = need ? sum_squares_k<K>(a.xin + (m_base + lane) * K) : 0.0f;
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // 2c: exact values of the queued pairs
+    for (int e0 = 0; e0 < qcount; e0 += kWave) {
+        const int e = e0 + lane;
+        if (e < qcount) {
+            const int fs = q_f[e];
+            const int n = q_n[e];
+            const float x2 = RECIPE == HIGGS ? q_x2[fs] : 0.0f;
+            q_v[e] = exact_value_k<RECIPE, Q8, K>(a, a.xin + (m_base + fs) * K, n, x2);
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // 2d: selection, certificate, outputs
+    int win_code[FG];
+    bool win_ok[FG];
+#pragma unroll
+    for (int g = 0; g < FG; ++g) {
+        const int64_t m = m_base + g * 16 + col;
+        const bool live = m < a.M;
+        bool ok = okg[g];
+        const float E = Eg[g], tau = taug[g];
+        const float x2 = RECIPE == HIGGS ? q_x2[g * 16 + col] : 0.0f;
+        float cand_val[TOPL];
+#pragma unroll
+        for (int j = 0; j < TOPL; ++j) cand_val[j] = cand_n[g][j] >= 0 ? q_v[qpos[g][j]] : 0.0f;
         // Exact top-T over the frame's evaluated candidates (all 4 lanes agree).
         // With top-k the list holds one entry more than reported, so that a
         // tie at the k-th place (which ggml_top_k's heap resolves) is seen.
@@ -571,14 +739,14 @@ __global__ __launch_bounds__(kThreads, 1) void euclid_stage_kernel(StageArgs a) 
             sel_v[r] = 0.0f;
             sel_n[r] = -1;
         }
-        if (ok && need_exact) {
+        if (needg[g]) {
             // Branch-free insertion of every evaluated candidate of the
-            // frame's 4 lanes into the ranked list sel[0..Tk).
+            // frame's 4 lanes into the ranked list sel[0..Tsel).
 #pragma unroll
             for (int j = 0; j < TOPL; ++j) {
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
-                    int cn = __shfl(cand_n[j], col + 16 * q);
+                    int cn = __shfl(cand_n[g][j], col + 16 * q);
                     float cv = __shfl(cand_val[j], col + 16 * q);
 #pragma unroll
                     for (int r = 0; r < 5; ++r) {
@@ -606,7 +774,7 @@ __global__ __launch_bounds__(kThreads, 1) void euclid_stage_kernel(StageArgs a) 
                 // DIRECT's offset |x|^2/2 comes from fp32 partial sums
                 // (relative error <= (K + 8) u); widen E by it.
                 const float off_err = RECIPE == DIRECT ? 0.5f * (K + 8) * u * nxx2[g] * 1.01f : 0.0f;
-                ok = (sv - sv == 0.0f) && (sprime - off_err > tau + E);
+                ok = ok && (sv - sv == 0.0f) && (sprime - off_err > tau + E);
                 // Every evaluated candidate must be finite for the order to be exact.
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
@@ -628,8 +796,8 @@ __global__ __launch_bounds__(kThreads, 1) void euclid_stage_kernel(StageArgs a) 
         } else {
             // One candidate clears the threshold: it wins if it also clears
             // every dropped code by 2E (no exact value is needed).
-            ok = ok && (best[0] - E > tau + E);
-            const float kb = best[0];
+            ok = ok && (best0g[g] - E > tau + E);
+            const float kb = best0g[g];
             // owner lane of the best key
             const bool mine = top[g][0] == kb;
             const unsigned local = __float_as_uint(kb) & kmask;
@@ -640,22 +808,6 @@ __global__ __launch_bounds__(kThreads, 1) void euclid_stage_kernel(StageArgs a) 
             ok = ok && n < N;
         }
         win_ok[g] = ok;
-        if (a.debug && m == a.debug_frame) {
-            float *d = a.debug + kq * 64;
-            d[0] = E; d[1] = tau; d[2] = vT; d[3] = thr; d[4] = ok ? 1.0f : 0.0f; d[5] = need_exact ? 1.0f : 0.0f;
-            d[6] = static_cast<float>(ncand); d[7] = static_cast<float>(lbits);
-            for (int j = 0; j < TOPL; ++j) {
-                d[8 + j] = top[g][j];
-                d[16 + j] = static_cast<float>(__float_as_uint(top[g][j]) & kmask);
-                d[24 + j] = static_cast<float>(cand_n[j]);
-                d[32 + j] = cand_val[j];
-            }
-            for (int r = 0; r < 4; ++r) {
-                d[40 + r] = static_cast<float>(sel_n[r]);
-                d[44 + r] = sel_v[r];
-            }
-            d[48] = nx; d[49] = nd; d[50] = x2;
-        }
 
         if (kq == 0 && live) {
             if (!ok) {
@@ -676,32 +828,59 @@ __global__ __launch_bounds__(kThreads, 1) void euclid_stage_kernel(StageArgs a) 
     }
 
     // ---- phase 3: residual update r -= c[code] for certified frames ----
-    // One frame at a time with all 64 lanes: coalesced rows.
+    // Rows across the lanes (coalesced), and the loads of kP3 frames issued
+    // before the first wait so one memory round trip covers all of them.
+    constexpr int kP3 = 8;
+    constexpr int KV = (K + 4 * kWave - 1) / (4 * kWave);   // float4 per lane per row
 #pragma unroll
     for (int g = 0; g < FG; ++g) {
-        for (int f = 0; f < 16; ++f) {
-            const int64_t m = m_base + g * 16 + f;
-            if (m >= a.M) break;
-            const int ok = __builtin_amdgcn_readlane(win_ok[g] ? 1 : 0, f);
-            if (!ok) continue;
-            int use = __builtin_amdgcn_readlane(win_code[g], f);
+#pragma unroll
+        for (int f0 = 0; f0 < 16; f0 += kP3) {
+            bool okf[kP3];
+            int64_t mrow[kP3];
+            int use[kP3];
+#pragma unroll
+            for (int t = 0; t < kP3; ++t) {
+                const int f = f0 + t;
+                const int64_t m = m_base + g * 16 + f;
+                okf[t] = m < a.M && __builtin_amdgcn_readlane(win_ok[g] ? 1 : 0, f) != 0;
+                mrow[t] = okf[t] ? m : 0;
+                // rows of frames that are skipped are clamped to row 0, so the
+                // loads below need no branches (only the stores are predicated)
+                use[t] = okf[t] ? __builtin_amdgcn_readlane(win_code[g], f) : 0;
+            }
             if (a.force_idx) {
-                use = a.force_idx[m * a.Q + a.s];
-                if (use < 0 || use >= N) {
-                    if (lane == 0) a.flags[AQ_FLAG_BAD_INDEX] = 1;
-                    use = 0;
+#pragma unroll
+                for (int t = 0; t < kP3; ++t) {
+                    if (!okf[t]) continue;
+                    int u2 = a.force_idx[mrow[t] * a.Q + a.s];
+                    if (u2 < 0 || u2 >= N) {
+                        if (lane == 0) a.flags[AQ_FLAG_BAD_INDEX] = 1;
+                        u2 = 0;
+                    }
+                    use[t] = u2;
                 }
             }
-            const float *xr = a.xin + m * K;
-            const float *cr = a.cbf + static_cast<int64_t>(use) * K;
-            float *xo = a.xout + m * K;
-            for (int k = lane * 4; k < K; k += kWave * 4) {
-                const f32x4 xv = *reinterpret_cast<const f32x4 *>(xr + k);
-                const f32x4 cv = *reinterpret_cast<const f32x4 *>(cr + k);
-                f32x4 o;
 #pragma unroll
-                for (int t = 0; t < 4; ++t) o[t] = __fsub_rn(xv[t], cv[t]);
-                *reinterpret_cast<f32x4 *>(xo + k) = o;
+            for (int kv = 0; kv < KV; ++kv) {
+                const int k = (kv * kWave + lane) * 4;
+                const bool inb = k < K;
+                const int kc = inb ? k : 0;
+                f32x4 xv[kP3], cv[kP3];
+#pragma unroll
+                for (int t = 0; t < kP3; ++t) {
+                    xv[t] = *reinterpret_cast<const f32x4 *>(a.xin + mrow[t] * K + kc);
+                    cv[t] = *reinterpret_cast<const f32x4 *>(a.cbf + static_cast<int64_t>(use[t]) * K + kc);
+                }
+#pragma unroll
+                for (int t = 0; t < kP3; ++t) {
+                    if (okf[t] && inb) {
+                        f32x4 o;
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) o[q] = __fsub_rn(xv[t][q], cv[t][q]);
+                        *reinterpret_cast<f32x4 *>(a.xout + mrow[t] * K + k) = o;
+                    }
+                }
             }
         }
     }
@@ -1237,7 +1416,7 @@ struct aq_codebooks {
     bool q8 = false;
     bool exact_only = false;
     uint16_t *d_cbh = nullptr;   // [Q][N][K] bf16
-    float *d_hh = nullptr;       // [Q][N]
+    float *d_hh = nullptr;       // [Q][N] -|c|^2 / 2 (fp32 of the double sum)
     float *d_cbf = nullptr;      // [Q][N][K]
     float *d_bias = nullptr;     // [Q][N] (OMNI)
     float *d_e2 = nullptr;       // [Q][N] (HIGGS)
@@ -1321,7 +1500,7 @@ aq_status aq_euclid_upload(aq_ctx *ctx, int64_t Q, int64_t N, int64_t K, int cb_
                 dq += (hd - cd) * (hd - cd);
                 hq += hd * hd;
             }
-            hh[s * N + n] = static_cast<float>(0.5 * sq);
+            hh[s * N + n] = static_cast<float>(-0.5 * sq);
             bias[s * N + n] = static_cast<float>(-sq);
             e2[s * N + n] = static_cast<float>(e2d);
             cm = std::max(cm, std::sqrt(sq));
@@ -1436,7 +1615,7 @@ aq_status aq_euclid_encode(aq_ctx *ctx, const aq_codebooks *cb, const float *x, 
         a.M = M;
         a.N = static_cast<int>(cb->N);
         a.cbh = cb->d_cbh + s * cb->N * K;
-        a.hh = cb->d_hh + s * cb->N;
+        a.nhh = cb->d_hh + s * cb->N;
         a.cbf = cb->d_cbf + s * cb->N * K;
         a.bias = cb->d_bias + s * cb->N;
         a.e2 = cb->d_e2 + s * cb->N;
@@ -1461,14 +1640,6 @@ aq_status aq_euclid_encode(aq_ctx *ctx, const aq_codebooks *cb, const float *x, 
         a.fail_list = list;
         a.flags = ctx->d_flags;
         a.exact_only = cb->exact_only ? 1 : 0;
-        a.debug_frame = -1;
-        if (const char *e = std::getenv("AQ_DEBUG_FRAME")) {
-            void *dbg = nullptr;
-            if (aq_ctx_scratch(ctx, 3, 256 * sizeof(float) * 64, &dbg) == AQ_OK) {
-                a.debug_frame = std::atoll(e);
-                a.debug = static_cast<float *>(dbg) + s * 256;
-            }
-        }
         if (s >= 64 && s % 64 == 0) AQ_HIP(ctx, hipMemsetAsync(counts, 0, sizeof(int32_t) * 64, ctx->stream));
         const int tslot = aq_timing_start(ctx);
         hipLaunchKernelGGL(sfn, dim3(blocks), dim3(kThreads), lds, ctx->stream, a);
@@ -1487,17 +1658,6 @@ aq_status aq_euclid_encode(aq_ctx *ctx, const aq_codebooks *cb, const float *x, 
         if (flag) return aq_fail(ctx, AQ_E_INDEX_RANGE, "aq_euclid_encode: force_idx holds a code outside [0, %lld)", (long long)cb->N);
     }
     return AQ_OK;
-}
-
-// Diagnostics: the AQ_DEBUG_FRAME dump of the last encode (stage-major,
-// 256 floats per stage); returns the number of floats copied.
-extern "C" int aq_euclid_debug_dump(aq_ctx *ctx, float *host, int capacity) {
-    void *dbg = nullptr;
-    if (!ctx || aq_ctx_scratch(ctx, 3, 0, &dbg) != AQ_OK || !dbg) return 0;
-    aq_device_guard g(ctx->device);
-    const size_t n = std::min<size_t>(static_cast<size_t>(capacity), 256 * 64);
-    if (hipMemcpy(host, dbg, n * sizeof(float), hipMemcpyDeviceToHost) != hipSuccess) return 0;
-    return static_cast<int>(n);
 }
 
 aq_status aq_euclid_failures(aq_ctx *ctx, const aq_codebooks *cb, int32_t *host_counts) {
