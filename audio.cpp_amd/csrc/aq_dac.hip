@@ -486,10 +486,17 @@ EncodeFn pick_kernel(int64_t D, int fw, bool recon, bool prefetch) {
 }
 
 // Launch shape.  A wave keeps its frames' residuals in registers for the
-// whole cascade, so work cannot be rebalanced after launch: choose frames per
-// wave (FW) and waves per block to minimise the frames on the busiest SIMD,
-// given the blocks per CU that LDS (one stage image per block) and the
-// kernel's registers allow.  Ties go to more waves per SIMD (latency hiding).
+// whole cascade, so work cannot be rebalanced after launch.  The shape is
+// ranked by
+//   1. frames on the busiest SIMD: ceil(blocks / CUs) blocks per CU, each
+//      spreading waves_per_block * FW frames over the 4 SIMDs;
+//   2. stage-image prefetch (the next stage's image is loaded into registers
+//      while the current stage computes, so no wave waits on the copy);
+//   3. 8-wave blocks (one image copy per CU and stage feeds 8 waves);
+//   4. more frames per wave (each LDS read of the image feeds FW frames).
+// Measured on MI355X (6000 frames, D = N = 1024, 12 stages): FW = 3 in 8-wave
+// blocks with prefetch 113 us; the same without prefetch 134 us; FW = 1 in
+// 8-wave blocks with prefetch 148 us; FW = 3 in 4-wave blocks 148 us.
 struct Shape {
     int fw = 1;
     int waves_per_block = 4;
@@ -502,7 +509,7 @@ Shape launch_shape(int64_t M, int64_t D, int64_t img_f4, bool recon, int num_cus
     if (const char *e = std::getenv("AQ_DAC_FW")) env_fw = std::atoi(e);
     if (const char *e = std::getenv("AQ_DAC_WPB")) env_wpb = std::atoi(e);
     Shape best;
-    int64_t best_rounds = INT64_MAX, best_rank = INT64_MAX;
+    int64_t best_rank = INT64_MAX;
     for (int fw = 1; fw <= 3; ++fw) {
         if (env_fw >= 1 && env_fw <= 3 && fw != env_fw) continue;
         for (int wpb : {4, 6, 8}) {
@@ -514,28 +521,18 @@ Shape launch_shape(int64_t M, int64_t D, int64_t img_f4, bool recon, int num_cus
             if (hipFuncGetAttributes(&attr, reinterpret_cast<const void *>(pick_kernel(D, fw, recon, prefetch))) ==
                     hipSuccess && attr.numRegs > 0)
                 simd_waves = std::min<int64_t>(8, 512 / ((attr.numRegs + 7) / 8 * 8));
-            // A block's waves are spread over the 4 SIMDs; count the worst SIMD.
-            const int64_t by_regs = simd_waves / ((wpb + 3) / 4);
-            const int64_t by_lds = static_cast<int64_t>(160 * 1024) / static_cast<int64_t>(lds_bytes > 0 ? lds_bytes : 1);
-            const int64_t per_cu = std::max<int64_t>(1, std::min(by_lds, by_regs));
+            // The block must fit on a CU at all (waves per SIMD by registers,
+            // one stage image in LDS).
+            if (simd_waves < (wpb + 3) / 4 || lds_bytes > static_cast<size_t>(160 * 1024)) continue;
             const int64_t waves = (M + fw - 1) / fw;
             const int64_t blocks = (waves + wpb - 1) / wpb;
-            const int64_t rounds = (blocks + cus * per_cu - 1) / (cus * per_cu);
-            // Measured on MI355X (6000 frames, D = N = 1024): with every block
-            // resident the kernel is latency-bound; 3 frames per wave in 8-wave
-            // blocks with the next image prefetched was fastest (111 us), then
-            // 2 frames per wave.  A grid smaller than the GPU prefers one frame
-            // per wave to occupy more CUs.
-            const bool fills = blocks >= cus;
-            static const int rank_full[4] = {0, 2, 1, 0};     // fw: 3 best, then 2, then 1
-            static const int rank_small[4] = {0, 0, 1, 2};    // fw: 1 best, then 2, then 3
-            const int64_t rank = (fills ? rank_full[fw] : rank_small[fw]) * 16 + (prefetch ? 0 : 8) +
-                                 (wpb == 8 ? 0 : wpb == 6 ? 1 : 2);
+            const int64_t per_simd = ((blocks + cus - 1) / cus) * ((wpb * fw + 3) / 4);
+            const int64_t rank = per_simd * 64 + (prefetch ? 0 : 16) + (wpb == 8 ? 0 : 8) + (3 - fw);
             if (std::getenv("AQ_DEBUG"))
-                std::fprintf(stderr, "aq_dac shape fw=%d wpb=%d pf=%d regs=%d per_cu=%lld blocks=%lld rounds=%lld\n", fw,
-                             wpb, prefetch ? 1 : 0, attr.numRegs, (long long)per_cu, (long long)blocks, (long long)rounds);
-            if (rounds < best_rounds || (rounds == best_rounds && rank < best_rank)) {
-                best_rounds = rounds;
+                std::fprintf(stderr, "aq_dac shape fw=%d wpb=%d pf=%d regs=%d blocks=%lld per_simd=%lld rank=%lld\n", fw,
+                             wpb, prefetch ? 1 : 0, attr.numRegs, (long long)blocks, (long long)per_simd,
+                             (long long)rank);
+            if (rank < best_rank) {
                 best_rank = rank;
                 best.fw = fw;
                 best.waves_per_block = wpb;

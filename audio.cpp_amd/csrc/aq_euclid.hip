@@ -1,48 +1,8 @@
-// Euclidean VQ / RVQ encode on gfx950: nearest codeword by bf16 MFMA
-// distance contraction, a per-lane top-L epilogue, a rigorous error
-// certificate, and exact re-ranking in the reference recipe's own fp32
-// arithmetic.  Also the codebook gather and the multi-stage decode sum.
-//
-// Reference recipes (paths relative to the audio.cpp tree):
-//   OMNIVOICE  score weight 2c, bias -(double)|c|^2 cast to float
-//              (src/models/omnivoice/audio_tokenizer.cpp:1227-1237); logits =
-//              mul_mat(2c, r) + bias; ggml_argmax; get_rows; r -= c[code]
-//              (audio_tokenizer.cpp:1897-1927)
-//   HIGGS      logits = ((2 * mul_mat(c, r)) - sum_rows(r*r)) - sum_rows(c*c)
-//              (src/models/higgs_audio_tts/codec.cpp:975-1013), F32 or Q8_0
-//              codebook (a Q8_0 mul_mat quantises r to Q8_0 first)
-//   DIRECT     distance = sum_k (x_k - c_k)^2, rounded products added in
-//              order, first index of the minimum: VectorQuantizer::compute
-//              (src/framework/runtime/host_ops.cpp:236-273) and Qwen3
-//              nearest_code (src/models/qwen3_tts/tokenizer_speech_encoder.cpp:287-303)
-// on the ggml CPU arithmetic (external/ggml/src/ggml-cpu): tinyBLAS F32
-// (llamafile/sgemm.cpp:523-580: 16 FMA lanes, then _mm512_reduce_add_ps),
-// ggml_vec_dot_f32 (vec.cpp:11-135) when tinyBLAS declines, tinyBLAS_Q0 /
-// ggml_vec_dot_q8_0_q8_0 (sgemm.cpp:1353-, arch/x86/quants.c:1170-), x86
-// quantize_row_q8_0 (arch/x86/quants.c:302-), ggml_vec_sum_f32 (vec.h, double
-// accumulation), ggml_vec_argmax_f32 (vec.h:1576-1584, last index of the max).
-//
-// Design
-//  * Scores: v(n) = x~ . c~_n - |c_n|^2/2 with x~, c~ rounded to bf16, from
-//    v_mfma_f32_16x16x32_bf16 with codes as A and frames as B.  Each wave
-//    keeps FG groups of 16 frames of x~ in registers for the whole sweep over
-//    the codebook, which streams through double-buffered, XOR-swizzled LDS
-//    (conflict-free 16-byte reads).  Output lane l owns frame l%16 and codes
-//    4*(l/16)+i of each 16-code block.
-//  * Epilogue per score: key = v with the lane-local code index in the low
-//    mantissa bits; the lane keeps its TOPL best keys (one max + med3 per
-//    level).  The full score matrix never leaves the CU.
-//  * Certificate: for every code, |v(n) - S'(n)| <= E, where S' is the
-//    recipe's value (ggml's fp32 arithmetic) in the same units.  E is built
-//    from the actual rounding residuals (|x~| |c~_n - c_n| + |x~ - x| |c_n|,
-//    Cauchy-Schwarz), the fp32 accumulation bounds and the key truncation.
-//    Kept candidates that could still be in the top T are re-ranked exactly;
-//    the result is certified when the T-th exact value beats every unkept
-//    code's bound.  Otherwise the frame goes to an exact full scan (fallback
-//    kernel), so results never depend on bf16 rounding.
-//  * Residual cascade: per stage one score kernel (re-rank, update r -= c)
-//    and one fallback kernel that exits at once when no frame failed.
-#include "aq_internal.hpp"
+// Euclidean VQ / RVQ: host side of the C ABI (upload, encode, decode,
+// gather) and the kernels that do not depend on the codebook width.  The
+// kernels, the certificate and the reference recipes are described in
+// aq_euclid_kernels.hpp.
+#include "aq_euclid_kernels.hpp"
 
 #include <algorithm>
 #include <cmath>
@@ -53,1209 +13,7 @@
 
 namespace {
 
-constexpr int kWave = 64;
-constexpr int kWaves = 4;
-constexpr int kThreads = kWave * kWaves;
-
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-
-enum Recipe : int { OMNI = 0, HIGGS = 1, DIRECT = 2 };
-
-struct StageArgs {
-    const float *xin;        // [M, K] residual entering the stage
-    float *xout;             // [M, K] residual leaving the stage (may alias xin)
-    int64_t M;
-    int N;
-    const uint16_t *cbh;     // [N, K] bf16 codebook (scores)
-    const float *nhh;        // [N] -|c|^2 / 2 (the score accumulators start from it)
-    const float *cbf;        // [N, K] fp32 codebook (dequantised for Q8_0)
-    const float *bias;       // [N] OmniVoice score bias
-    const float *e2;         // [N] Higgs sum_rows(c*c)
-    const int8_t *q8;        // [N, K] Q8_0 quants
-    const float *q8d;        // [N, K/32] Q8_0 scales (fp32 of fp16)
-    float cmax, dcmax, chmax;   // max |c_n|, max |c~_n - c_n|, max |c~_n|
-    int order;               // exact dot order: 0 tinyBLAS, 1 ggml_vec_dot_f32
-    int Q, s;
-    int32_t *idx;            // [M, Q]
-    float *dist;             // [M, Q] or null
-    int topk;                // 0..4
-    int32_t *topk_idx;       // [M, Q, topk]
-    float *topk_dist;        // [M, Q, topk]
-    const int32_t *force_idx;   // [M, Q] or null
-    int32_t *fail_count;     // this stage's counter
-    int32_t *fail_list;      // [M]
-    int32_t *flags;
-    int exact_only;
-};
-
-// --------------------------------------------------------------- exact math
-
-// _mm512_reduce_add_ps order (pairs 8, 4, 2, 1).
-__device__ inline float reduce16(const float (&a)[16]) {
-    float t3[8], t6[4];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) t3[i] = __fadd_rn(a[i + 8], a[i]);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) t6[i] = __fadd_rn(t3[i + 4], t3[i]);
-    const float t80 = __fadd_rn(t6[0], t6[2]);
-    const float t81 = __fadd_rn(t6[1], t6[3]);
-    return __fadd_rn(t80, t81);
-}
-
-// hsum of 8 lanes (hsum(__m256) / hsum_float_8): i+4, then 2, then 1.
-__device__ inline float reduce8(const float (&a)[8]) {
-    float v[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = __fadd_rn(a[i + 4], a[i]);
-    return __fadd_rn(__fadd_rn(v[0], v[2]), __fadd_rn(v[1], v[3]));
-}
-
-// One tinyBLAS<16> element: sa*a . b with 16 FMA accumulators over k = 16l + j.
-// sa is 1 or 2 (exact scaling, OmniVoice's 2c).
-__device__ float dot_tinyblas(const float *__restrict__ a, const float *__restrict__ b, int K, float sa) {
-    float acc[16];
-#pragma unroll
-    for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
-    for (int l = 0; l < K; l += 16) {
-        const f32x4 *pa = reinterpret_cast<const f32x4 *>(a + l);
-        const f32x4 *pb = reinterpret_cast<const f32x4 *>(b + l);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const f32x4 va = pa[q], vb = pb[q];
-#pragma unroll
-            for (int t = 0; t < 4; ++t) acc[4 * q + t] = __fmaf_rn(va[t] * sa, vb[t], acc[4 * q + t]);
-        }
-    }
-    return reduce16(acc);
-}
-
-// ggml_vec_dot_f32, AVX-512 branch: 4 x 16 accumulators over 64-element
-// steps, combined 0+=2, 1+=3, 0+=1, reduced, then scalar leftovers (rounded
-// products added in order).
-__device__ float dot_vecdot(const float *__restrict__ a, const float *__restrict__ b, int K, float sa) {
-    float s[4][16];
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int l = 0; l < 16; ++l) s[j][l] = 0.0f;
-    const int np = K & ~63;
-    for (int i = 0; i < np; i += 64) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int l = 0; l < 16; ++l) s[j][l] = __fmaf_rn(a[i + 16 * j + l] * sa, b[i + 16 * j + l], s[j][l]);
-    }
-    float r[16];
-#pragma unroll
-    for (int l = 0; l < 16; ++l) r[l] = __fadd_rn(__fadd_rn(s[0][l], s[2][l]), __fadd_rn(s[1][l], s[3][l]));
-    float sum = reduce16(r);
-    for (int i = np; i < K; ++i) sum = __fadd_rn(sum, __fmul_rn(a[i] * sa, b[i]));
-    return sum;
-}
-
-// ggml_vec_sum_f32 of the fp32 squares (sum_rows(mul(x, x))): double
-// accumulation in order, one rounding to float.
-__device__ float sum_squares(const float *__restrict__ x, int K) {
-    double s = 0.0;
-    for (int k = 0; k < K; ++k) s += static_cast<double>(__fmul_rn(x[k], x[k]));
-    return static_cast<float>(s);
-}
-
-// Direct squared distance: rounded (x - c)^2 added in order.
-__device__ float dist_direct(const float *__restrict__ x, const float *__restrict__ c, int K) {
-    float d = 0.0f;
-    for (int k = 0; k < K; ++k) {
-        const float diff = __fsub_rn(x[k], c[k]);
-        d = __fadd_rn(d, __fmul_rn(diff, diff));
-    }
-    return d;
-}
-
-// x86 quantize_row_q8_0 on one 32-element block: d = amax/127 stored as fp16,
-// id = 127/amax, q = round-half-even(x*id) with int8 saturation.
-__device__ inline void quantize_block_q8(const float *__restrict__ x, int8_t *__restrict__ q, float *__restrict__ d) {
-    float amax = 0.0f;
-    for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(x[j]));
-    const _Float16 h = static_cast<_Float16>(__fdiv_rn(amax, 127.0f));
-    *d = static_cast<float>(h);
-    const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
-    for (int j = 0; j < 32; ++j) {
-        const float v = __builtin_rintf(__fmul_rn(x[j], id));
-        int qi;
-        if (!(v >= -2147483648.0f && v < 2147483648.0f)) qi = -128;
-        else qi = static_cast<int>(v) < -128 ? -128 : (static_cast<int>(v) > 127 ? 127 : static_cast<int>(v));
-        q[j] = static_cast<int8_t>(qi);
-    }
-}
-
-// tinyBLAS_Q0 / ggml_vec_dot_q8_0_q8_0: per block, 8 exact 4-element int
-// dots scaled by d_c*d_x and accumulated with FMA, then an 8-lane hsum.
-__device__ float dot_q8(const int8_t *__restrict__ qc, const float *__restrict__ dc, const int8_t *__restrict__ qx,
-                        const float *__restrict__ dx, int nb) {
-    float acc[8];
-#pragma unroll
-    for (int l = 0; l < 8; ++l) acc[l] = 0.0f;
-    for (int ib = 0; ib < nb; ++ib) {
-        const float dd = __fmul_rn(dc[ib], dx[ib]);
-        const int *pc = reinterpret_cast<const int *>(qc + 32 * ib);
-        const int *px = reinterpret_cast<const int *>(qx + 32 * ib);
-#pragma unroll
-        for (int l = 0; l < 8; ++l) {
-            const int s = __builtin_amdgcn_sdot4(pc[l], px[l], 0, false);
-            acc[l] = __fmaf_rn(dd, static_cast<float>(s), acc[l]);
-        }
-    }
-    return reduce8(acc);
-}
-
-// Compile-time-K forms for the stage kernel: the loops unroll, so the loads
-// of later steps are issued ahead of the FMA chains that consume them.
-template <int K>
-__device__ float dot_tinyblas_k(const float *__restrict__ a, const float *__restrict__ b, float sa) {
-    float acc[16];
-#pragma unroll
-    for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
-#pragma unroll 4
-    for (int l = 0; l < K; l += 16) {
-        const f32x4 *pa = reinterpret_cast<const f32x4 *>(a + l);
-        const f32x4 *pb = reinterpret_cast<const f32x4 *>(b + l);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const f32x4 va = pa[q], vb = pb[q];
-#pragma unroll
-            for (int t = 0; t < 4; ++t) acc[4 * q + t] = __fmaf_rn(va[t] * sa, vb[t], acc[4 * q + t]);
-        }
-    }
-    return reduce16(acc);
-}
-
-template <int K>
-__device__ float sum_squares_k(const float *__restrict__ x) {
-    double s = 0.0;
-#pragma unroll 8
-    for (int k = 0; k < K; k += 4) {
-        const f32x4 v = *reinterpret_cast<const f32x4 *>(x + k);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) s += static_cast<double>(__fmul_rn(v[t], v[t]));
-    }
-    return static_cast<float>(s);
-}
-
-template <int K>
-__device__ float dist_direct_k(const float *__restrict__ x, const float *__restrict__ c) {
-    float d = 0.0f;
-#pragma unroll 4
-    for (int k = 0; k < K; k += 4) {
-        const f32x4 xv = *reinterpret_cast<const f32x4 *>(x + k);
-        const f32x4 cv = *reinterpret_cast<const f32x4 *>(c + k);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const float diff = __fsub_rn(xv[t], cv[t]);
-            d = __fadd_rn(d, __fmul_rn(diff, diff));
-        }
-    }
-    return d;
-}
-
-// dot_q8 with the query block quantised on the fly (quantize_block_q8's
-// arithmetic, block by block), so no per-lane copy of the quantised row.
-template <int K>
-__device__ float dot_q8_fused(const int8_t *__restrict__ qc, const float *__restrict__ dc, const float *__restrict__ x) {
-    float acc[8];
-#pragma unroll
-    for (int l = 0; l < 8; ++l) acc[l] = 0.0f;
-#pragma unroll 2
-    for (int ib = 0; ib < K / 32; ++ib) {
-        float v[32];
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            const f32x4 t = *reinterpret_cast<const f32x4 *>(x + 32 * ib + 4 * q);
-            v[4 * q] = t[0]; v[4 * q + 1] = t[1]; v[4 * q + 2] = t[2]; v[4 * q + 3] = t[3];
-        }
-        float amax = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(v[j]));
-        const float dx = static_cast<float>(static_cast<_Float16>(__fdiv_rn(amax, 127.0f)));
-        const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
-        int qw[8];
-#pragma unroll
-        for (int l = 0; l < 8; ++l) {
-            unsigned w = 0;
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const float r = __builtin_rintf(__fmul_rn(v[4 * l + t], id));
-                int qi;
-                if (!(r >= -2147483648.0f && r < 2147483648.0f)) qi = -128;
-                else qi = static_cast<int>(r) < -128 ? -128 : (static_cast<int>(r) > 127 ? 127 : static_cast<int>(r));
-                w |= (static_cast<unsigned>(qi) & 0xFFu) << (8 * t);
-            }
-            qw[l] = static_cast<int>(w);
-        }
-        const float dd = __fmul_rn(dc[ib], dx);
-        const int *pc = reinterpret_cast<const int *>(qc + 32 * ib);
-#pragma unroll
-        for (int l = 0; l < 8; ++l) {
-            const int s = __builtin_amdgcn_sdot4(pc[l], qw[l], 0, false);
-            acc[l] = __fmaf_rn(dd, static_cast<float>(s), acc[l]);
-        }
-    }
-    return reduce8(acc);
-}
-
-template <int RECIPE, bool Q8, int K>
-__device__ float exact_value_k(const StageArgs &a, const float *__restrict__ x, int n, float x2) {
-    const float *c = a.cbf + static_cast<int64_t>(n) * K;
-    if (RECIPE == DIRECT) return dist_direct_k<K>(x, c);
-    float dot;
-    if (Q8) {
-        dot = dot_q8_fused<K>(a.q8 + static_cast<int64_t>(n) * K, a.q8d + static_cast<int64_t>(n) * (K / 32), x);
-    } else {
-        const float sa = RECIPE == OMNI ? 2.0f : 1.0f;
-        dot = a.order == 0 ? dot_tinyblas_k<K>(c, x, sa) : dot_vecdot(c, x, K, sa);
-    }
-    if (RECIPE == OMNI) return __fadd_rn(dot, a.bias[n]);
-    return __fsub_rn(__fsub_rn(__fmul_rn(dot, 2.0f), x2), a.e2[n]);
-}
-
-// Recipe value of code n ("larger is better" for OMNI/HIGGS: the logit;
-// DIRECT returns the distance, smaller is better).  x2 is sum_rows(x*x)
-// (HIGGS); xq/xd the quantised query (HIGGS with a Q8_0 codebook).
-template <int RECIPE, bool Q8>
-__device__ float exact_value(const StageArgs &a, int K, const float *__restrict__ x, int n, float x2,
-                             const int8_t *xq, const float *xd) {
-    const float *c = a.cbf + static_cast<int64_t>(n) * K;
-    if (RECIPE == DIRECT) return dist_direct(x, c, K);
-    float dot;
-    if (Q8) {
-        dot = dot_q8(a.q8 + static_cast<int64_t>(n) * K, a.q8d + static_cast<int64_t>(n) * (K / 32), xq, xd, K / 32);
-    } else {
-        const float sa = RECIPE == OMNI ? 2.0f : 1.0f;
-        dot = a.order == 0 ? dot_tinyblas(c, x, K, sa) : dot_vecdot(c, x, K, sa);
-    }
-    if (RECIPE == OMNI) return __fadd_rn(dot, a.bias[n]);
-    return __fsub_rn(__fsub_rn(__fmul_rn(dot, 2.0f), x2), a.e2[n]);
-}
-
-// True if (va, na) ranks before (vb, nb): ggml recipes take the larger logit
-// and, on equality, the larger index (argmax keeps the last maximum);
-// DIRECT takes the smaller distance and, on equality, the smaller index.
-template <int RECIPE>
-__device__ inline bool ranks_before(float va, int na, float vb, int nb) {
-    if (RECIPE == DIRECT) return va < vb || (va == vb && na < nb);
-    return va > vb || (va == vb && na > nb);
-}
-// Top-k order for ggml recipes (a set in ggml): value desc, index asc.
-template <int RECIPE>
-__device__ inline bool topk_before(float va, int na, float vb, int nb) {
-    if (RECIPE == DIRECT) return va < vb || (va == vb && na < nb);
-    return va > vb || (va == vb && na < nb);
-}
-
-// --------------------------------------------------------------- score kernel
-
-// Score key: the score's bits with the low ones replaced by the lane-local
-// code index.  `keep` is the complement of the index mask, held in a VGPR so
-// that the bit select is one v_and_or_b32 with the (wave-uniform) index.
-__device__ inline float key_of(float v, unsigned local, unsigned keep) {
-    return __uint_as_float((__float_as_uint(v) & keep) | local);
-}
-
-template <int KS>
-struct Tile {
-    static constexpr int K = KS * 32;
-    static constexpr int ROWB = K * 2;                         // bytes per bf16 code row
-    static constexpr int CH16 = K / 8;                         // 16-byte chunks per row
-    static constexpr int SWZ = CH16 >= 16 ? 15 : CH16 - 1;     // XOR swizzle mask
-    static constexpr int CC = (32768 / ROWB) >= 16 ? ((32768 / ROWB) / 16) * 16 : 16;   // codes per LDS chunk
-    static constexpr int CHUNKB = CC * ROWB;                   // codebook bytes per chunk
-    static constexpr int BUFB = CHUNKB + CC * 4;               // + |c|^2/2 of the chunk
-    static constexpr int STAGE16 = CHUNKB / 16 / kThreads;     // 16-byte loads per thread per chunk
-    static constexpr int LDS = 2 * BUFB;
-};
-
-template <int RECIPE, bool Q8, int KS, int FG, int TOPL>
-__global__ __launch_bounds__(kThreads, 1) void euclid_stage_kernel(StageArgs a) {
-    using T = Tile<KS>;
-    constexpr int K = T::K;
-    static_assert(T::CHUNKB % (16 * kThreads) == 0, "chunk must split evenly over the block");
-    extern __shared__ __align__(16) unsigned char lds[];
-
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x / kWave;
-    const int col = lane & 15;      // frame within a 16-frame group
-    const int kq = lane >> 4;       // which 8-element quarter of each 32-wide K slice
-    const int64_t m_base = (static_cast<int64_t>(blockIdx.x) * kWaves + wave) * (FG * 16);
-    const int N = a.N;
-
-    // ---- phase 0: frames -> bf16 fragments in registers, rounding norms ----
-    // x~ fragments stay packed (2 bf16 per register) for the whole sweep.
-    u32x4 xb[FG][KS];
-    float nx2[FG], nd2[FG], nxx2[FG];
-#pragma unroll
-    for (int g = 0; g < FG; ++g) {
-        const int64_t m = m_base + g * 16 + col;
-        const int64_t mc = m < a.M ? m : a.M - 1;
-        const float *xr = a.xin + mc * K;
-        float sx = 0.0f, sd = 0.0f, sxx = 0.0f;
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-            const f32x4 lo = *reinterpret_cast<const f32x4 *>(xr + ks * 32 + kq * 8);
-            const f32x4 hi = *reinterpret_cast<const f32x4 *>(xr + ks * 32 + kq * 8 + 4);
-            float v[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-            if (Q8) {
-                // A Q8_0 mul_mat scores the query's Q8_0 image x_q = q * d
-                // (x86 quantize_row_q8_0: one block = this 32-wide K slice),
-                // so the matrix cores contract bf16(x_q) and the bound only
-                // has to cover bf16 rounding.  x_q is exact in fp32.
-                float am = 0.0f;
-#pragma unroll
-                for (int t = 0; t < 8; ++t) am = fmaxf(am, fabsf(v[t]));
-                am = fmaxf(am, __shfl_xor(am, 16));
-                am = fmaxf(am, __shfl_xor(am, 32));
-                const float dq = static_cast<float>(static_cast<_Float16>(__fdiv_rn(am, 127.0f)));
-                const float id = am != 0.0f ? __fdiv_rn(127.0f, am) : 0.0f;
-#pragma unroll
-                for (int t = 0; t < 8; ++t) v[t] = __fmul_rn(__builtin_rintf(__fmul_rn(v[t], id)), dq);
-            }
-            u32x4 packed;
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-                const bf16x2 pr = {static_cast<__bf16>(v[2 * t]), static_cast<__bf16>(v[2 * t + 1])};
-                const unsigned w = __builtin_bit_cast(unsigned, pr);
-                packed[t] = w;
-                const float r0 = __uint_as_float(w << 16), r1 = __uint_as_float(w & 0xFFFF0000u);
-                sx = __fmaf_rn(r0, r0, sx);
-                sx = __fmaf_rn(r1, r1, sx);
-                const float d0 = v[2 * t] - r0, d1 = v[2 * t + 1] - r1;
-                sd = __fmaf_rn(d0, d0, sd);
-                sd = __fmaf_rn(d1, d1, sd);
-                sxx = __fmaf_rn(v[2 * t], v[2 * t], sxx);
-                sxx = __fmaf_rn(v[2 * t + 1], v[2 * t + 1], sxx);
-            }
-            xb[g][ks] = packed;
-        }
-        sx += __shfl_xor(sx, 16);
-        sx += __shfl_xor(sx, 32);
-        sd += __shfl_xor(sd, 16);
-        sd += __shfl_xor(sd, 32);
-        sxx += __shfl_xor(sxx, 16);
-        sxx += __shfl_xor(sxx, 32);
-        nx2[g] = sx;
-        nd2[g] = sd;
-        nxx2[g] = sxx;
-    }
-
-    // ---- phase 1: sweep the codebook ----
-    float top[FG][TOPL];
-#pragma unroll
-    for (int g = 0; g < FG; ++g)
-#pragma unroll
-        for (int j = 0; j < TOPL; ++j) top[g][j] = -INFINITY;
-
-    const int nchunks = N / T::CC;
-    int lbits = 0;   // bits of the lane-local code index (N/4 codes per lane)
-    while ((1 << lbits) < N / 4) ++lbits;
-    const unsigned kmask = (1u << lbits) - 1u;
-    unsigned vkeep;   // ~kmask in a VGPR (one scalar operand per VOP3 on gfx950)
-    asm volatile("v_mov_b32 %0, %1" : "=v"(vkeep) : "s"(~kmask));
-
-    // Software pipeline over 16-code blocks bb = 0 .. N/16-1 (chunk c = bb/BPC):
-    //  * A fragments live in a ring of R registers, loaded L = R-1 K-slices
-    //    ahead (across the block boundary inside a chunk);
-    //  * the epilogue of block bb-1 runs while block bb's MFMAs execute;
-    //  * the next chunk is staged into the other LDS buffer a few 16-byte
-    //    pieces per block (global load in one block, LDS store in the next),
-    //    with one barrier per chunk.
-    constexpr int BPC = T::CC / 16;
-    constexpr int R = KS % 4 == 0 ? 4 : 2;
-    constexpr int L = R - 1;
-    constexpr int PPB = (T::STAGE16 + BPC - 1) / BPC;   // staged pieces per block
-    const int nblk = N / 16;
-
-    auto lds_a = [&](int buf, int blk, int ks) -> bf16x8 {
-        const int r = blk * 16 + col;
-        const int j = ks * 4 + kq;
-        return *reinterpret_cast<const bf16x8 *>(lds + buf * T::BUFB + r * T::ROWB + ((j ^ (r & T::SWZ)) * 16));
-    };
-    auto lds_h = [&](int buf, int blk) -> f32x4 {
-        return *reinterpret_cast<const f32x4 *>(lds + buf * T::BUFB + T::CHUNKB + (blk * 16 + kq * 4) * 4);
-    };
-    auto piece_dst = [&](int buf, int p) -> u32x4 * {
-        const int r = p / T::CH16, j = p % T::CH16;
-        return reinterpret_cast<u32x4 *>(lds + buf * T::BUFB + r * T::ROWB + ((j ^ (r & T::SWZ)) * 16));
-    };
-    const u32x4 *cb16 = reinterpret_cast<const u32x4 *>(a.cbh);
-
-    // prologue: chunk 0 in full
-    {
-#pragma unroll
-        for (int k = 0; k < T::STAGE16; ++k) {
-            const int p = threadIdx.x + k * kThreads;
-            *piece_dst(0, p) = cb16[p];
-        }
-        if (threadIdx.x < T::CC) reinterpret_cast<float *>(lds + T::CHUNKB)[threadIdx.x] = a.nhh[threadIdx.x];
-    }
-    __syncthreads();
-
-    bf16x8 ring[R];
-#pragma unroll
-    for (int l = 0; l < L; ++l) ring[l] = lds_a(0, 0, l);
-    f32x4 hcur = lds_h(0, 0);
-    f32x4 accp[FG];
-    unsigned lprev = 0;
-    bool pend = false;
-    u32x4 stg[PPB];
-    float hstg = 0.0f;
-
-    // Per score: key (1 op), TOPL-1 med3 and one max-by-med3.  The upper
-    // clamp is FLT_MAX rather than +inf so the compiler keeps a plain med3
-    // (an fmax would need NaN canonicalisation of both operands); frames with
-    // a key of +inf or NaN fail the certificate in any case.
-    auto epilogue = [&](const f32x4 (&acc)[FG], unsigned local0) {
-#pragma unroll
-        for (int g = 0; g < FG; ++g)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float key = key_of(acc[g][i], local0 + i, vkeep);
-#pragma unroll
-                for (int j = TOPL - 1; j > 0; --j) top[g][j] = __builtin_amdgcn_fmed3f(top[g][j - 1], top[g][j], key);
-                top[g][0] = __builtin_amdgcn_fmed3f(top[g][0], key, 3.40282347e38f);
-            }
-    };
-
-    for (int bb = 0; bb < nblk; ++bb) {
-        const int c = bb / BPC, b = bb - c * BPC, buf = c & 1;
-        const bool last_in_chunk = b == BPC - 1;
-        const bool next_chunk = (c + 1) * BPC < nblk;
-        if (next_chunk) {
-            // store the pieces fetched in the previous block, fetch this block's
-            if (b > 0) {
-#pragma unroll
-                for (int i = 0; i < PPB; ++i) {
-                    const int k = (b - 1) + i * BPC;
-                    if (k < T::STAGE16) *piece_dst(buf ^ 1, threadIdx.x + k * kThreads) = stg[i];
-                }
-                if (b - 1 == 0 && threadIdx.x < T::CC)
-                    reinterpret_cast<float *>(lds + (buf ^ 1) * T::BUFB + T::CHUNKB)[threadIdx.x] = hstg;
-            }
-            const u32x4 *src = cb16 + static_cast<int64_t>(c + 1) * (T::CHUNKB / 16);
-#pragma unroll
-            for (int i = 0; i < PPB; ++i) {
-                const int k = b + i * BPC;
-                if (k < T::STAGE16) stg[i] = src[threadIdx.x + k * kThreads];
-            }
-            if (b == 0 && threadIdx.x < T::CC) hstg = a.nhh[static_cast<int64_t>(c + 1) * T::CC + threadIdx.x];
-        }
-
-        // the accumulators start from -|c|^2/2 of the block's codes
-        f32x4 acc[FG];
-#pragma unroll
-        for (int g = 0; g < FG; ++g) acc[g] = hcur;
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-            const int pk = ks + L;
-            if (pk < KS) ring[pk % R] = lds_a(buf, b, pk);
-            else if (!last_in_chunk) ring[pk % R] = lds_a(buf, b + 1, pk - KS);
-#pragma unroll
-            for (int g = 0; g < FG; ++g)
-                acc[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ring[ks % R], __builtin_bit_cast(bf16x8, xb[g][ks]),
-                                                                 acc[g], 0, 0, 0);
-        }
-        const f32x4 hnext = last_in_chunk ? hcur : lds_h(buf, b + 1);
-        if (pend) epilogue(accp, lprev);
-#pragma unroll
-        for (int g = 0; g < FG; ++g) accp[g] = acc[g];
-        lprev = static_cast<unsigned>(bb * 4);
-        pend = true;
-        hcur = hnext;
-        if (last_in_chunk) {
-            if (next_chunk) {
-#pragma unroll
-                for (int i = 0; i < PPB; ++i) {
-                    const int k = (BPC - 1) + i * BPC;
-                    if (k < T::STAGE16) *piece_dst(buf ^ 1, threadIdx.x + k * kThreads) = stg[i];
-                }
-                if (BPC == 1 && threadIdx.x < T::CC)
-                    reinterpret_cast<float *>(lds + (buf ^ 1) * T::BUFB + T::CHUNKB)[threadIdx.x] = hstg;
-            }
-            __syncthreads();
-            if (next_chunk) {
-#pragma unroll
-                for (int l = 0; l < L; ++l) ring[l] = lds_a(buf ^ 1, 0, l);
-                hcur = lds_h(buf ^ 1, 0);
-            }
-        }
-    }
-    if (pend) epilogue(accp, lprev);
-
-    // ---- phase 2: per-frame certificate and exact re-ranking ----
-    // 2a bounds and candidates per frame; 2b the frames' |x|^2 (Higgs);
-    // 2c every candidate (frame, code) pair of the wave evaluated exactly, one
-    // pair per lane, through a queue in LDS (the codebook tiles are dead);
-    // 2d per-frame selection, certificate and outputs.
-    const float u = 5.9604645e-8f;   // 2^-24
-    const int Tk = a.topk > 0 ? a.topk : 1;
-    const int Tsel = a.topk > 0 ? a.topk + 1 : 1;
-    const bool want_value = a.dist != nullptr || a.topk > 0;
-    constexpr int QCAP = FG * 16 * 4 * TOPL;
-    static_assert(kWaves * QCAP * 12 + kWaves * FG * 16 * 4 <= T::LDS, "exact-evaluation queue must fit in LDS");
-    __syncthreads();
-    int32_t *q_n = reinterpret_cast<int32_t *>(lds) + wave * QCAP;
-    int32_t *q_f = reinterpret_cast<int32_t *>(lds) + kWaves * QCAP + wave * QCAP;
-    float *q_v = reinterpret_cast<float *>(lds) + 2 * kWaves * QCAP + wave * QCAP;
-    float *q_x2 = reinterpret_cast<float *>(lds) + 3 * kWaves * QCAP + wave * FG * 16;
-
-    float Eg[FG], taug[FG], best0g[FG];
-    bool okg[FG], needg[FG];
-    int cand_n[FG][TOPL], qpos[FG][TOPL];
-    int qcount = 0;
-#pragma unroll
-    for (int g = 0; g < FG; ++g) {
-        const int64_t m = m_base + g * 16 + col;
-        const bool live = m < a.M;
-
-        // Bound E (in units of v = x.c - |c|^2/2) on |v(n) - S'(n)| for every n.
-        const float nx = sqrtf(nx2[g]) * 1.0001f, nd = sqrtf(nd2[g]) * 1.0001f;
-        const float nxe = nx + nd;                           // >= |x|
-        const float e_bf16 = nx * a.dcmax + nd * a.cmax;
-        // fp32 accumulation from -|c|^2/2: partial sums stay below
-        // |x~||c~| + |c|^2/2
-        const float e_acc = (K + 4) * u * (nx * a.chmax + 0.5f * a.cmax * a.cmax);
-        const float e_rec = (K + 16) * u * (nxe * a.cmax + nxe * nxe + a.cmax * a.cmax);
-        const float vmax = nx * a.chmax + 0.5f * a.cmax * a.cmax + e_rec;
-        const float trunc = ldexpf(vmax, lbits - 23);
-        const float E = 1.02f * (e_bf16 + e_acc + e_rec + 4.0f * u * vmax) + trunc + 1e-30f;
-
-        // Keys of the frame's 4 lanes, gathered in every one of them.
-        float all[4 * TOPL];
-#pragma unroll
-        for (int j = 0; j < TOPL; ++j) {
-            const float k0 = top[g][j];
-            const float k1 = __shfl_xor(k0, 16);
-            const float k2 = __shfl_xor(k0, 32);
-            const float k3 = __shfl_xor(k1, 32);
-            all[4 * j + 0] = k0;
-            all[4 * j + 1] = k1;
-            all[4 * j + 2] = k2;
-            all[4 * j + 3] = k3;
-        }
-        // tau bounds every key a lane dropped; vT is the T-th largest kept key.
-        float tau = -INFINITY;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) tau = fmaxf(tau, all[4 * (TOPL - 1) + q]);
-        float best[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-#pragma unroll
-        for (int t = 0; t < 4 * TOPL; ++t) {
-            float v = all[t];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float hi = fmaxf(best[r], v);
-                v = fminf(best[r], v);
-                best[r] = hi;
-            }
-        }
-        const float vT = best[Tk - 1];
-        const bool ok = live && !a.exact_only && (E < INFINITY) && (vT - vT == 0.0f);
-        const float thr = vT - 2.0f * E;
-        int nabove = 0;
-#pragma unroll
-        for (int t = 0; t < 4 * TOPL; ++t) nabove += all[t] >= thr ? 1 : 0;
-        const bool need = ok && (want_value || nabove > 1);
-        Eg[g] = E;
-        taug[g] = tau;
-        best0g[g] = best[0];
-        okg[g] = ok;
-        needg[g] = need;
-        // enqueue this lane's candidates
-#pragma unroll
-        for (int j = 0; j < TOPL; ++j) {
-            const float key = top[g][j];
-            const bool c = need && key >= thr && key > -INFINITY;
-            const unsigned local = __float_as_uint(key) & kmask;
-            const int n = static_cast<int>((local >> 2) * 16 + kq * 4 + (local & 3));
-            const unsigned long long bal = __ballot(c);
-            const int pos = qcount + static_cast<int>(__builtin_amdgcn_mbcnt_hi(
-                                         static_cast<unsigned>(bal >> 32),
-                                         __builtin_amdgcn_mbcnt_lo(static_cast<unsigned>(bal), 0u)));
-            if (c) {
-                q_n[pos] = n;
-                q_f[pos] = g * 16 + col;
-            }
-            cand_n[g][j] = c ? n : -1;
-            qpos[g][j] = pos;
-            qcount += __popcll(bal);
-        }
-    }
-    // 2b: sum_rows(x*x) of each frame that has candidates (one lane per frame)
-    if (RECIPE == HIGGS) {
-        int needmask = 0;   // bit g: frame (g, lane % 16) has candidates
-#pragma unroll
-        for (int g = 0; g < FG; ++g) needmask |= (__shfl(needg[g] ? 1 : 0, lane % 16) & 1) << g;
-        if (lane < FG * 16) {
-            const bool need = ((needmask >> (lane / 16)) & 1) != 0;
-            q_x2[lane] = need ? sum_squares_k<K>(a.xin + (m_base + lane) * K) : 0.0f;
-        }
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // 2c: exact values of the queued pairs
-    for (int e0 = 0; e0 < qcount; e0 += kWave) {
-        const int e = e0 + lane;
-        if (e < qcount) {
-            const int fs = q_f[e];
-            const int n = q_n[e];
-            const float x2 = RECIPE == HIGGS ? q_x2[fs] : 0.0f;
-            q_v[e] = exact_value_k<RECIPE, Q8, K>(a, a.xin + (m_base + fs) * K, n, x2);
-        }
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-    // 2d: selection, certificate, outputs
-    int win_code[FG];
-    bool win_ok[FG];
-#pragma unroll
-    for (int g = 0; g < FG; ++g) {
-        const int64_t m = m_base + g * 16 + col;
-        const bool live = m < a.M;
-        bool ok = okg[g];
-        const float E = Eg[g], tau = taug[g];
-        const float x2 = RECIPE == HIGGS ? q_x2[g * 16 + col] : 0.0f;
-        float cand_val[TOPL];
-#pragma unroll
-        for (int j = 0; j < TOPL; ++j) cand_val[j] = cand_n[g][j] >= 0 ? q_v[qpos[g][j]] : 0.0f;
-        // Exact top-T over the frame's evaluated candidates (all 4 lanes agree).
-        // With top-k the list holds one entry more than reported, so that a
-        // tie at the k-th place (which ggml_top_k's heap resolves) is seen.
-        float sel_v[5];
-        int sel_n[5];
-#pragma unroll
-        for (int r = 0; r < 5; ++r) {
-            sel_v[r] = 0.0f;
-            sel_n[r] = -1;
-        }
-        if (needg[g]) {
-            // Branch-free insertion of every evaluated candidate of the
-            // frame's 4 lanes into the ranked list sel[0..Tsel).
-#pragma unroll
-            for (int j = 0; j < TOPL; ++j) {
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    int cn = __shfl(cand_n[g][j], col + 16 * q);
-                    float cv = __shfl(cand_val[j], col + 16 * q);
-#pragma unroll
-                    for (int r = 0; r < 5; ++r) {
-                        const bool before = a.topk == 0 ? ranks_before<RECIPE>(cv, cn, sel_v[r], sel_n[r])
-                                                        : topk_before<RECIPE>(cv, cn, sel_v[r], sel_n[r]);
-                        const bool take = cn >= 0 && r < Tsel && (sel_n[r] < 0 || before);
-                        const float tv = sel_v[r];
-                        const int tn = sel_n[r];
-                        sel_v[r] = take ? cv : tv;
-                        sel_n[r] = take ? cn : tn;
-                        cv = take ? tv : cv;
-                        cn = take ? tn : cn;
-                    }
-                }
-            }
-            // S' of the T-th exact value in v units, against the bound of unkept codes.
-            if (sel_n[Tk - 1] < 0) {
-                ok = false;
-            } else {
-                const float sv = sel_v[Tk - 1];
-                float sprime;
-                if (RECIPE == OMNI) sprime = 0.5f * sv;
-                else if (RECIPE == HIGGS) sprime = 0.5f * sv + 0.5f * x2;
-                else sprime = -0.5f * sv + 0.5f * nxx2[g];
-                // DIRECT's offset |x|^2/2 comes from fp32 partial sums
-                // (relative error <= (K + 8) u); widen E by it.
-                const float off_err = RECIPE == DIRECT ? 0.5f * (K + 8) * u * nxx2[g] * 1.01f : 0.0f;
-                ok = ok && (sv - sv == 0.0f) && (sprime - off_err > tau + E);
-                // Every evaluated candidate must be finite for the order to be exact.
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    if (r < Tk && sel_n[r] >= 0 && !(sel_v[r] - sel_v[r] == 0.0f)) ok = false;
-                // With Tk ties at the maximum, a further tie outside the list
-                // could hold the larger index argmax keeps: scan exactly.
-                if (RECIPE != DIRECT && Tk > 1 && sv == sel_v[0]) ok = false;
-                // A tie at the k-th place: ggml_top_k keeps whichever of the
-                // tied codes its heap keeps; the exact scan replays it.
-                if (RECIPE != DIRECT && a.topk > 0 && sel_n[Tk] >= 0 && sel_v[Tk] == sv) ok = false;
-            }
-            // argmax among exact ties keeps ggml's last index
-            int w = sel_n[0];
-            if (RECIPE != DIRECT)
-#pragma unroll
-                for (int r = 1; r < 4; ++r)
-                    if (r < Tk && sel_n[r] >= 0 && sel_v[r] == sel_v[0] && sel_n[r] > w) w = sel_n[r];
-            win_code[g] = w;
-        } else {
-            // One candidate clears the threshold: it wins if it also clears
-            // every dropped code by 2E (no exact value is needed).
-            ok = ok && (best0g[g] - E > tau + E);
-            const float kb = best0g[g];
-            // owner lane of the best key
-            const bool mine = top[g][0] == kb;
-            const unsigned local = __float_as_uint(kb) & kmask;
-            int n = mine ? static_cast<int>((local >> 2) * 16 + kq * 4 + (local & 3)) : 0x7fffffff;
-            n = min(n, __shfl_xor(n, 16));
-            n = min(n, __shfl_xor(n, 32));
-            win_code[g] = n;
-            ok = ok && n < N;
-        }
-        win_ok[g] = ok;
-
-        if (kq == 0 && live) {
-            if (!ok) {
-                const int slot = atomicAdd(a.fail_count, 1);
-                a.fail_list[slot] = static_cast<int32_t>(m);
-            } else {
-                a.idx[m * a.Q + a.s] = win_code[g];
-                if (a.dist) {
-                    const float v = sel_v[0];   // the argmax's value (ties share it)
-                    a.dist[m * a.Q + a.s] = RECIPE == DIRECT ? v : -v;
-                }
-                for (int r = 0; r < a.topk; ++r) {
-                    a.topk_idx[(m * a.Q + a.s) * a.topk + r] = sel_n[r];
-                    a.topk_dist[(m * a.Q + a.s) * a.topk + r] = RECIPE == DIRECT ? sel_v[r] : -sel_v[r];
-                }
-            }
-        }
-    }
-
-    // ---- phase 3: residual update r -= c[code] for certified frames ----
-    // Rows across the lanes (coalesced), and the loads of kP3 frames issued
-    // before the first wait so one memory round trip covers all of them.
-    constexpr int kP3 = 8;
-    constexpr int KV = (K + 4 * kWave - 1) / (4 * kWave);   // float4 per lane per row
-#pragma unroll
-    for (int g = 0; g < FG; ++g) {
-#pragma unroll
-        for (int f0 = 0; f0 < 16; f0 += kP3) {
-            bool okf[kP3];
-            int64_t mrow[kP3];
-            int use[kP3];
-#pragma unroll
-            for (int t = 0; t < kP3; ++t) {
-                const int f = f0 + t;
-                const int64_t m = m_base + g * 16 + f;
-                okf[t] = m < a.M && __builtin_amdgcn_readlane(win_ok[g] ? 1 : 0, f) != 0;
-                mrow[t] = okf[t] ? m : 0;
-                // rows of frames that are skipped are clamped to row 0, so the
-                // loads below need no branches (only the stores are predicated)
-                use[t] = okf[t] ? __builtin_amdgcn_readlane(win_code[g], f) : 0;
-            }
-            if (a.force_idx) {
-#pragma unroll
-                for (int t = 0; t < kP3; ++t) {
-                    if (!okf[t]) continue;
-                    int u2 = a.force_idx[mrow[t] * a.Q + a.s];
-                    if (u2 < 0 || u2 >= N) {
-                        if (lane == 0) a.flags[AQ_FLAG_BAD_INDEX] = 1;
-                        u2 = 0;
-                    }
-                    use[t] = u2;
-                }
-            }
-#pragma unroll
-            for (int kv = 0; kv < KV; ++kv) {
-                const int k = (kv * kWave + lane) * 4;
-                const bool inb = k < K;
-                const int kc = inb ? k : 0;
-                f32x4 xv[kP3], cv[kP3];
-#pragma unroll
-                for (int t = 0; t < kP3; ++t) {
-                    xv[t] = *reinterpret_cast<const f32x4 *>(a.xin + mrow[t] * K + kc);
-                    cv[t] = *reinterpret_cast<const f32x4 *>(a.cbf + static_cast<int64_t>(use[t]) * K + kc);
-                }
-#pragma unroll
-                for (int t = 0; t < kP3; ++t) {
-                    if (okf[t] && inb) {
-                        f32x4 o;
-#pragma unroll
-                        for (int q = 0; q < 4; ++q) o[q] = __fsub_rn(xv[t][q], cv[t][q]);
-                        *reinterpret_cast<f32x4 *>(a.xout + mrow[t] * K + k) = o;
-                    }
-                }
-            }
-        }
-    }
-}
-
-// ------------------------------------------------------------ fallback kernels
-
-// Frames the certificate could not settle get an exact scan of every code,
-// in two launches that each spread over the whole GPU:
-//  * fb_values: a block takes FQ failed frames x 256 codes (one code per
-//    thread), evaluates the recipe value of every (frame, code) pair with one
-//    pass over the code's row, and reduces it to the block's best T codes per
-//    frame (the reference's ranking);
-//  * fb_select: one wave per failed frame merges the per-block candidates,
-//    writes the codes / distances / top-k and updates the residual.  A frame
-//    whose values contain NaN replays ggml_vec_argmax_f32 in code order.
-constexpr int kFQ = 4;        // failed frames per fb_values block
-constexpr int kFbChunk = 256; // codes per fb_values block
-
-struct FbArgs {
-    float *cand_v;     // [M][nch][T]
-    int32_t *cand_n;   // [M][nch][T]
-    int32_t *nan_flag; // [M]
-    int nch;
-};
-
-// Recipe values of code n for FQ query frames held in LDS, one pass over the
-// code's row (tinyBLAS order; the vec_dot order only occurs for M == 1 and is
-// evaluated frame by frame).
-template <int RECIPE, bool Q8>
-__device__ void exact_values_fq(const StageArgs &a, int K, int n, const float *xs, const float *x2, const int8_t *xq,
-                                const float *xd, int nf, float (&out)[kFQ]) {
-    const float *c = a.cbf + static_cast<int64_t>(n) * K;
-    if (RECIPE == DIRECT) {
-        float d[kFQ];
-#pragma unroll
-        for (int f = 0; f < kFQ; ++f) d[f] = 0.0f;
-        for (int k = 0; k < K; ++k) {
-            const float ck = c[k];
-#pragma unroll
-            for (int f = 0; f < kFQ; ++f) {
-                const float diff = __fsub_rn(xs[f * K + k], ck);
-                d[f] = __fadd_rn(d[f], __fmul_rn(diff, diff));
-            }
-        }
-#pragma unroll
-        for (int f = 0; f < kFQ; ++f) out[f] = d[f];
-        return;
-    }
-    float dot[kFQ];
-    if (Q8) {
-        const int8_t *qc = a.q8 + static_cast<int64_t>(n) * K;
-        const float *dc = a.q8d + static_cast<int64_t>(n) * (K / 32);
-        float acc[kFQ][8];
-#pragma unroll
-        for (int f = 0; f < kFQ; ++f)
-#pragma unroll
-            for (int l = 0; l < 8; ++l) acc[f][l] = 0.0f;
-        for (int ib = 0; ib < K / 32; ++ib) {
-            const int *pc = reinterpret_cast<const int *>(qc + 32 * ib);
-            int cw[8];
-#pragma unroll
-            for (int l = 0; l < 8; ++l) cw[l] = pc[l];
-#pragma unroll
-            for (int f = 0; f < kFQ; ++f) {
-                const float dd = __fmul_rn(dc[ib], xd[f * (K / 32) + ib]);
-                const int *px = reinterpret_cast<const int *>(xq + f * K + 32 * ib);
-#pragma unroll
-                for (int l = 0; l < 8; ++l)
-                    acc[f][l] = __fmaf_rn(dd, static_cast<float>(__builtin_amdgcn_sdot4(cw[l], px[l], 0, false)), acc[f][l]);
-            }
-        }
-#pragma unroll
-        for (int f = 0; f < kFQ; ++f) dot[f] = reduce8(acc[f]);
-    } else if (a.order == 0) {
-        const float sa = RECIPE == OMNI ? 2.0f : 1.0f;
-        float acc[kFQ][16];
-#pragma unroll
-        for (int f = 0; f < kFQ; ++f)
-#pragma unroll
-            for (int j = 0; j < 16; ++j) acc[f][j] = 0.0f;
-        for (int l = 0; l < K; l += 16) {
-            float cv[16];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const f32x4 v = *reinterpret_cast<const f32x4 *>(c + l + 4 * q);
-#pragma unroll
-                for (int t = 0; t < 4; ++t) cv[4 * q + t] = v[t] * sa;
-            }
-#pragma unroll
-            for (int f = 0; f < kFQ; ++f)
-#pragma unroll
-                for (int j = 0; j < 16; ++j) acc[f][j] = __fmaf_rn(cv[j], xs[f * K + l + j], acc[f][j]);
-        }
-#pragma unroll
-        for (int f = 0; f < kFQ; ++f) dot[f] = reduce16(acc[f]);
-    } else {
-        const float sa = RECIPE == OMNI ? 2.0f : 1.0f;
-#pragma unroll
-        for (int f = 0; f < kFQ; ++f) dot[f] = f < nf ? dot_vecdot(c, xs + f * K, K, sa) : 0.0f;
-    }
-#pragma unroll
-    for (int f = 0; f < kFQ; ++f)
-        out[f] = RECIPE == OMNI ? __fadd_rn(dot[f], a.bias[n])
-                                : __fsub_rn(__fsub_rn(__fmul_rn(dot[f], 2.0f), x2[f]), a.e2[n]);
-}
-
-// One step of libstdc++'s binary heap (GCC 11.4 std::__adjust_heap followed
-// by std::__push_heap) with comp(a, b) = value(a) > value(b): the root holds
-// the worst kept element.  std::partial_sort builds the heap over the first k
-// codes and lets each later code that is strictly better than the root
-// replace it, which decides which of several equal values ggml_top_k keeps.
-__device__ void heap_adjust(int *hn, float *hv, int hole, int len, int vn, float vv) {
-    const int top = hole;
-    int child = hole;
-    while (child < (len - 1) / 2) {
-        child = 2 * (child + 1);
-        if (hv[child] > hv[child - 1]) child--;
-        hn[hole] = hn[child];
-        hv[hole] = hv[child];
-        hole = child;
-    }
-    if ((len & 1) == 0 && child == (len - 2) / 2) {
-        child = 2 * (child + 1);
-        hn[hole] = hn[child - 1];
-        hv[hole] = hv[child - 1];
-        hole = child - 1;
-    }
-    int parent = (hole - 1) / 2;
-    while (hole > top && hv[parent] > vv) {
-        hn[hole] = hn[parent];
-        hv[hole] = hv[parent];
-        hole = parent;
-        parent = (hole - 1) / 2;
-    }
-    hn[hole] = vn;
-    hv[hole] = vv;
-}
-
-template <int RECIPE>
-__device__ inline bool fb_before(float va, int na, float vb, int nb, bool topk) {
-    return topk ? topk_before<RECIPE>(va, na, vb, nb) : ranks_before<RECIPE>(va, na, vb, nb);
-}
-
-template <int RECIPE, bool Q8>
-__global__ __launch_bounds__(kFbChunk) void euclid_fb_values_kernel(StageArgs a, int K, FbArgs fb) {
-    extern __shared__ __align__(16) unsigned char lds[];
-    float *xs = reinterpret_cast<float *>(lds);                         // [kFQ][K]
-    int8_t *xq = reinterpret_cast<int8_t *>(xs + kFQ * K);              // [kFQ][K]
-    float *xd = reinterpret_cast<float *>(xq + kFQ * K);                // [kFQ][K/32]
-    __shared__ float x2s[kFQ];
-    __shared__ float red_v[kFbChunk];
-    __shared__ int red_n[kFbChunk];
-    __shared__ int chosen[5];
-    const int count = *a.fail_count;
-    // top-k slots (value desc, index asc; one more than k to see a tie at the
-    // k-th place), then the argmax slot (the reference's tie rule)
-    const int T = a.topk > 0 ? a.topk + 1 : 0;
-    const int Tc = T + 1;
-    const int ngroups = (count + kFQ - 1) / kFQ;
-    const int64_t nwork = static_cast<int64_t>(ngroups) * fb.nch;
-    for (int64_t w = blockIdx.x; w < nwork; w += gridDim.x) {
-        const int grp = static_cast<int>(w / fb.nch), ch = static_cast<int>(w % fb.nch);
-        const int nf = min(kFQ, count - grp * kFQ);
-        __syncthreads();
-        for (int i = threadIdx.x; i < kFQ * K; i += kFbChunk) {
-            const int f = i / K, k = i % K;
-            xs[i] = f < nf ? a.xin[static_cast<int64_t>(a.fail_list[grp * kFQ + f]) * K + k] : 0.0f;
-        }
-        __syncthreads();
-        if (threadIdx.x < kFQ) {
-            const int f = threadIdx.x;
-            x2s[f] = RECIPE == OMNI || f >= nf ? 0.0f : sum_squares(xs + f * K, K);
-            if (Q8)
-                for (int ib = 0; ib < K / 32; ++ib) quantize_block_q8(xs + f * K + 32 * ib, xq + f * K + 32 * ib, xd + f * (K / 32) + ib);
-        }
-        __syncthreads();
-        const int n = ch * kFbChunk + threadIdx.x;
-        float vals[kFQ];
-        if (n < a.N) {
-            exact_values_fq<RECIPE, Q8>(a, K, n, xs, x2s, xq, xd, nf, vals);
-        } else {
-#pragma unroll
-            for (int f = 0; f < kFQ; ++f) vals[f] = 0.0f;
-        }
-        for (int f = 0; f < nf; ++f) {
-            const int slot = grp * kFQ + f;
-            float v = vals[f];
-            if (n < a.N && v != v) fb.nan_flag[slot] = 1;
-            if (v != v) v = RECIPE == DIRECT ? INFINITY : -INFINITY;
-            for (int r = 0; r < Tc; ++r) {
-                const bool tk = r < T;
-                bool skip = n >= a.N;
-                if (tk)
-                    for (int q = 0; q < r; ++q) skip |= (chosen[q] == n);
-                red_v[threadIdx.x] = v;
-                red_n[threadIdx.x] = skip ? -1 : n;
-                __syncthreads();
-                for (int step = kFbChunk / 2; step > 0; step >>= 1) {
-                    if (threadIdx.x < step) {
-                        const int on = red_n[threadIdx.x + step], cn = red_n[threadIdx.x];
-                        const float ov = red_v[threadIdx.x + step], cv = red_v[threadIdx.x];
-                        if (on >= 0 && (cn < 0 || fb_before<RECIPE>(ov, on, cv, cn, tk))) {
-                            red_v[threadIdx.x] = ov;
-                            red_n[threadIdx.x] = on;
-                        }
-                    }
-                    __syncthreads();
-                }
-                if (threadIdx.x == 0) {
-                    if (tk) chosen[r] = red_n[0];
-                    const int64_t o = (static_cast<int64_t>(slot) * fb.nch + ch) * Tc + r;
-                    fb.cand_v[o] = red_v[0];
-                    fb.cand_n[o] = red_n[0];
-                }
-                __syncthreads();
-            }
-        }
-    }
-}
-
-template <int RECIPE, bool Q8>
-__global__ __launch_bounds__(kWave) void euclid_fb_select_kernel(StageArgs a, int K, FbArgs fb) {
-    extern __shared__ __align__(16) unsigned char lds[];
-    float *xs = reinterpret_cast<float *>(lds);                         // [K]
-    int8_t *xq = reinterpret_cast<int8_t *>(xs + K);                    // [K]
-    float *xd = reinterpret_cast<float *>(xq + K);                      // [K/32]
-    __shared__ float vals64[kWave];
-    const int lane = threadIdx.x;
-    const int count = *a.fail_count;
-    __shared__ int heap_n[4];
-    __shared__ float heap_v[4];
-    const int T = a.topk > 0 ? a.topk + 1 : 0;
-    const int Tc = T + 1;
-    for (int slot = blockIdx.x; slot < count; slot += gridDim.x) {
-        const int64_t m = a.fail_list[slot];
-        float sel_v[5];
-        int sel_n[5];
-#pragma unroll
-        for (int r = 0; r < 5; ++r) {
-            sel_v[r] = 0.0f;
-            sel_n[r] = -1;
-        }
-        // ranked merge of the per-block candidates (lane-strided, then a wave
-        // merge): r < T merges the top-k slots, r == T the argmax slots
-        const int total = fb.nch * Tc;
-        int code = 0;
-        float code_v = 0.0f;
-        for (int r = 0; r < Tc; ++r) {
-            const bool tk = r < T;
-            float bv = 0.0f;
-            int bn = -1;
-            for (int i = lane; i < total; i += kWave) {
-                if (tk != (i % Tc < T)) continue;
-                const int64_t o = static_cast<int64_t>(slot) * total + i;
-                const int n = fb.cand_n[o];
-                if (n < 0) continue;
-                bool skip = false;
-                if (tk)
-                    for (int q = 0; q < r; ++q) skip |= (sel_n[q] == n);
-                const float v = fb.cand_v[o];
-                if (!skip && (bn < 0 || fb_before<RECIPE>(v, n, bv, bn, tk))) {
-                    bv = v;
-                    bn = n;
-                }
-            }
-            for (int off = 1; off < kWave; off <<= 1) {
-                const float ov = __shfl_xor(bv, off);
-                const int on = __shfl_xor(bn, off);
-                if (on >= 0 && (bn < 0 || fb_before<RECIPE>(ov, on, bv, bn, tk))) {
-                    bv = ov;
-                    bn = on;
-                }
-            }
-            if (tk) {
-#pragma unroll
-                for (int q = 0; q < 5; ++q)
-                    if (q == r) {
-                        sel_v[q] = bv;
-                        sel_n[q] = bn;
-                    }
-            } else {
-                code = bn < 0 ? 0 : bn;
-                code_v = bv;
-            }
-        }
-        const int ktop = a.topk;
-        bool kth_tie = false;
-#pragma unroll
-        for (int q = 1; q < 5; ++q)
-            if (q == ktop) kth_tie = sel_n[q] >= 0 && sel_v[q] == sel_v[q - 1];
-        const bool nan_seen = fb.nan_flag[slot] != 0;
-        if (RECIPE != DIRECT && (nan_seen || (ktop > 0 && kth_tie))) {
-            // Replay in code order: ggml_vec_argmax_f32 (MAX(max, v), index of
-            // the last element equal to the running max; NaN restarts it) and
-            // ggml_top_k's heap selection (libstdc++ std::partial_sort).
-            for (int kk = lane; kk < K; kk += kWave) xs[kk] = a.xin[m * K + kk];
-            __syncthreads();
-            float x2 = 0.0f;
-            if (RECIPE == HIGGS) x2 = sum_squares(xs, K);
-            if (Q8 && lane == 0)
-                for (int ib = 0; ib < K / 32; ++ib) quantize_block_q8(xs + 32 * ib, xq + 32 * ib, xd + ib);
-            __syncthreads();
-            float mx = -INFINITY;
-            int id = 0;
-            for (int base = 0; base < a.N; base += kWave) {
-                const int n = base + lane;
-                vals64[lane] = n < a.N ? exact_value<RECIPE, Q8>(a, K, xs, n, x2, xq, xd) : 0.0f;
-                __syncthreads();
-                if (lane == 0)
-                    for (int i = 0; i < kWave && base + i < a.N; ++i) {
-                        const int n_i = base + i;
-                        const float v = vals64[i];
-                        mx = mx > v ? mx : v;
-                        if (mx == v) id = n_i;
-                        if (ktop > 0) {
-                            if (n_i < ktop) {
-                                heap_n[n_i] = n_i;
-                                heap_v[n_i] = v;
-                                if (n_i == ktop - 1 && ktop >= 2)
-                                    for (int par = (ktop - 2) / 2;; --par) {
-                                        heap_adjust(heap_n, heap_v, par, ktop, heap_n[par], heap_v[par]);
-                                        if (par == 0) break;
-                                    }
-                            } else if (v > heap_v[0]) {
-                                heap_adjust(heap_n, heap_v, 0, ktop, n_i, v);
-                            }
-                        }
-                    }
-                __syncthreads();
-            }
-            if (nan_seen) {
-                code = __shfl(id, 0);
-                code_v = __shfl(mx, 0);
-            }
-            if (ktop > 0 && lane == 0) {
-                // report the kept set best first, ties by index
-                for (int r = 0; r < ktop; ++r) {
-                    int b = -1;
-                    for (int q = 0; q < ktop; ++q) {
-                        bool used = false;
-                        for (int t = 0; t < r; ++t) used |= sel_n[t] == heap_n[q];
-                        if (!used && (b < 0 || topk_before<RECIPE>(heap_v[q], heap_n[q], heap_v[b], heap_n[b]))) b = q;
-                    }
-#pragma unroll
-                    for (int q = 0; q < 5; ++q)
-                        if (q == r) {
-                            sel_n[q] = heap_n[b];
-                            sel_v[q] = heap_v[b];
-                        }
-                }
-            }
-            __syncthreads();
-        }
-        if (lane == 0) {
-            a.idx[m * a.Q + a.s] = code;
-            if (a.dist) a.dist[m * a.Q + a.s] = RECIPE == DIRECT ? code_v : -code_v;
-            for (int r = 0; r < a.topk; ++r) {
-                a.topk_idx[(m * a.Q + a.s) * a.topk + r] = sel_n[r];
-                a.topk_dist[(m * a.Q + a.s) * a.topk + r] = RECIPE == DIRECT ? sel_v[r] : -sel_v[r];
-            }
-        }
-        int use = code;
-        if (a.force_idx) {
-            use = a.force_idx[m * a.Q + a.s];
-            if (use < 0 || use >= a.N) {
-                if (lane == 0) a.flags[AQ_FLAG_BAD_INDEX] = 1;
-                use = 0;
-            }
-        }
-        for (int k = lane; k < K; k += kWave)
-            a.xout[m * K + k] = __fsub_rn(a.xin[m * K + k], a.cbf[static_cast<int64_t>(use) * K + k]);
-        if (lane == 0) fb.nan_flag[slot] = 0;
-    }
-}
+using namespace aq_euclid;
 
 // --------------------------------------------------------------- gather, sum
 
@@ -1294,39 +52,18 @@ __global__ void decode_sum_kernel(const float *__restrict__ cbf, int Q, int64_t 
 
 // --------------------------------------------------------------- dispatch
 
-using StageFn = void (*)(StageArgs);
-using FallbackFn = void (*)(StageArgs, int, FbArgs);
-
-// 16-frame groups per wave: the bf16 frames of a wave stay in registers
-// (4 * KS registers per group), so wider codebooks take fewer groups.
-constexpr int groups_for(int ks) { return ks <= 2 ? 4 : (ks <= 8 ? 3 : 2); }
-
-template <int RECIPE, bool Q8, int KS>
-StageFn pick_stage(int topl) {
-    constexpr int FG = groups_for(KS);
-    return topl >= 4 ? euclid_stage_kernel<RECIPE, Q8, KS, FG, 4> : euclid_stage_kernel<RECIPE, Q8, KS, FG, 3>;
-}
-
-template <int RECIPE, bool Q8>
-StageFn pick_stage_ks(int ks, int topl) {
+const KsKernels *kernels_for(int ks) {
     switch (ks) {
-        case 2: return pick_stage<RECIPE, Q8, 2>(topl);
-        case 8: return pick_stage<RECIPE, Q8, 8>(topl);
-        case 16: return pick_stage<RECIPE, Q8, 16>(topl);
-        case 24: return pick_stage<RECIPE, Q8, 24>(topl);
+        case 2: return kernels_ks2();
+        case 8: return kernels_ks8();
+        case 16: return kernels_ks16();
+        case 24: return kernels_ks24();
         default: return nullptr;
     }
 }
 
-StageFn pick_stage_fn(int recipe, bool q8, int ks, int topl) {
-    if (q8) return recipe == HIGGS ? pick_stage_ks<HIGGS, true>(ks, topl) : nullptr;
-    switch (recipe) {
-        case OMNI: return pick_stage_ks<OMNI, false>(ks, topl);
-        case HIGGS: return pick_stage_ks<HIGGS, false>(ks, topl);
-        case DIRECT: return pick_stage_ks<DIRECT, false>(ks, topl);
-        default: return nullptr;
-    }
-}
+// Recipe variant index of KsKernels.
+int variant_of(int recipe, bool q8) { return q8 ? 3 : recipe; }
 
 FallbackFn pick_fb_values(int recipe, bool q8) {
     if (q8) return recipe == HIGGS ? euclid_fb_values_kernel<HIGGS, true> : nullptr;
@@ -1345,25 +82,6 @@ FallbackFn pick_fb_select(int recipe, bool q8) {
         case HIGGS: return euclid_fb_select_kernel<HIGGS, false>;
         case DIRECT: return euclid_fb_select_kernel<DIRECT, false>;
         default: return nullptr;
-    }
-}
-
-int tile_lds(int ks) {
-    switch (ks) {
-        case 2: return Tile<2>::LDS;
-        case 8: return Tile<8>::LDS;
-        case 16: return Tile<16>::LDS;
-        case 24: return Tile<24>::LDS;
-        default: return 0;
-    }
-}
-int tile_cc(int ks) {
-    switch (ks) {
-        case 2: return Tile<2>::CC;
-        case 8: return Tile<8>::CC;
-        case 16: return Tile<16>::CC;
-        case 24: return Tile<24>::CC;
-        default: return 0;
     }
 }
 
@@ -1416,6 +134,7 @@ struct aq_codebooks {
     bool q8 = false;
     bool exact_only = false;
     uint16_t *d_cbh = nullptr;   // [Q][N][K] bf16
+    uint16_t *d_cbl = nullptr;   // [Q][N][K] bf16(c - bf16(c)) (refine pass)
     float *d_hh = nullptr;       // [Q][N] -|c|^2 / 2 (fp32 of the double sum)
     float *d_cbf = nullptr;      // [Q][N][K]
     float *d_bias = nullptr;     // [Q][N] (OMNI)
@@ -1423,6 +142,7 @@ struct aq_codebooks {
     int8_t *d_q8 = nullptr;      // [Q][N][K]
     float *d_q8d = nullptr;      // [Q][N][K/32]
     std::vector<float> cmax, dcmax, chmax;
+    std::vector<float> clmax, crmax;   // max |c_l|, max |c - c_h - c_l| (refine bound)
 };
 
 extern "C" {
@@ -1439,11 +159,12 @@ aq_status aq_euclid_upload(aq_ctx *ctx, int64_t Q, int64_t N, int64_t K, int cb_
     if (q8 && recipe != AQ_EUCLID_HIGGS)
         return aq_fail(ctx, AQ_E_UNSUPPORTED, "aq_euclid_upload: Q8_0 codebooks follow the Higgs recipe only");
     const int ks = static_cast<int>(K / 32);
-    if (Q <= 0 || N <= 0 || K <= 0 || K % 32 != 0 || !pick_stage_fn(recipe, q8, ks, 3))
+    const KsKernels *kk = K % 32 == 0 ? kernels_for(ks) : nullptr;
+    if (Q <= 0 || N <= 0 || K <= 0 || !kk)
         return aq_fail(ctx, AQ_E_SHAPE, "aq_euclid_upload: unsupported shape Q=%lld N=%lld K=%lld (K in {64,256,512,768})",
                        (long long)Q, (long long)N, (long long)K);
-    if (N % tile_cc(ks) != 0 || N > (1 << 20))
-        return aq_fail(ctx, AQ_E_SHAPE, "aq_euclid_upload: N=%lld must be a multiple of %d", (long long)N, tile_cc(ks));
+    if (N % kk->cc != 0 || N > (1 << 20))
+        return aq_fail(ctx, AQ_E_SHAPE, "aq_euclid_upload: N=%lld must be a multiple of %d", (long long)N, kk->cc);
     aq_device_guard g(ctx->device);
 
     const size_t QNK = static_cast<size_t>(Q * N * K), QN = static_cast<size_t>(Q * N);
@@ -1470,7 +191,7 @@ aq_status aq_euclid_upload(aq_ctx *ctx, int64_t Q, int64_t N, int64_t K, int cb_
     } else {
         std::memcpy(cbf.data(), data, QNK * sizeof(float));
     }
-    std::vector<uint16_t> cbh(QNK);
+    std::vector<uint16_t> cbh(QNK), cbl(QNK);
     std::vector<float> hh(QN), bias(QN), e2(QN);
     aq_codebooks *cb = new (std::nothrow) aq_codebooks();
     if (!cb) return aq_fail(ctx, AQ_E_NOMEM, "aq_euclid_upload: host allocation failed");
@@ -1483,23 +204,34 @@ aq_status aq_euclid_upload(aq_ctx *ctx, int64_t Q, int64_t N, int64_t K, int cb_
     cb->cmax.assign(Q, 0.0f);
     cb->dcmax.assign(Q, 0.0f);
     cb->chmax.assign(Q, 0.0f);
+    cb->clmax.assign(Q, 0.0f);
+    cb->crmax.assign(Q, 0.0f);
     bool nonfinite = false;
     for (int64_t s = 0; s < Q; ++s) {
-        double cm = 0.0, dm = 0.0, hm = 0.0;
+        double cm = 0.0, dm = 0.0, hm = 0.0, lm = 0.0, rm = 0.0;
         for (int64_t n = 0; n < N; ++n) {
             const size_t row = static_cast<size_t>((s * N + n) * K);
-            double sq = 0.0, dq = 0.0, hq = 0.0, e2d = 0.0;
+            double sq = 0.0, dq = 0.0, hq = 0.0, e2d = 0.0, lq = 0.0, rq = 0.0;
             for (int64_t k = 0; k < K; ++k) {
                 const float c = cbf[row + k];
                 if (!std::isfinite(c)) nonfinite = true;
                 const uint16_t h = to_bf16(c);
                 cbh[row + k] = h;
+                // c - c_h and c - c_h - c_l are exact in fp32 (finite c)
+                const float dl = c - from_bf16(h);
+                const uint16_t l = std::isfinite(dl) ? to_bf16(dl) : 0;
+                cbl[row + k] = l;
+                const double ld = from_bf16(l), rd = static_cast<double>(dl) - ld;
                 const double cd = c, hd = from_bf16(h);
                 sq += cd * cd;                                    // OmniVoice: double products
                 e2d += static_cast<double>(c * c);               // sum_rows(c*c): fp32 squares
                 dq += (hd - cd) * (hd - cd);
                 hq += hd * hd;
+                lq += ld * ld;
+                rq += rd * rd;
             }
+            lm = std::max(lm, std::sqrt(lq));
+            rm = std::max(rm, std::sqrt(rq));
             hh[s * N + n] = static_cast<float>(-0.5 * sq);
             bias[s * N + n] = static_cast<float>(-sq);
             e2[s * N + n] = static_cast<float>(e2d);
@@ -1510,9 +242,12 @@ aq_status aq_euclid_upload(aq_ctx *ctx, int64_t Q, int64_t N, int64_t K, int cb_
         cb->cmax[s] = round_up(cm * (1.0 + 1e-6));
         cb->dcmax[s] = round_up(dm * (1.0 + 1e-6));
         cb->chmax[s] = round_up(hm * (1.0 + 1e-6));
+        cb->clmax[s] = round_up(lm * (1.0 + 1e-6));
+        cb->crmax[s] = round_up(rm * (1.0 + 1e-6));
     }
     cb->exact_only = nonfinite;
-    bool ok = hipMalloc(&cb->d_cbh, QNK * 2) == hipSuccess && hipMalloc(&cb->d_hh, QN * 4) == hipSuccess &&
+    bool ok = hipMalloc(&cb->d_cbh, QNK * 2) == hipSuccess && hipMalloc(&cb->d_cbl, QNK * 2) == hipSuccess &&
+              hipMalloc(&cb->d_hh, QN * 4) == hipSuccess &&
               hipMalloc(&cb->d_cbf, QNK * 4) == hipSuccess && hipMalloc(&cb->d_bias, QN * 4) == hipSuccess &&
               hipMalloc(&cb->d_e2, QN * 4) == hipSuccess;
     if (ok && q8) ok = hipMalloc(&cb->d_q8, QNK) == hipSuccess && hipMalloc(&cb->d_q8d, QNK / 32 * 4) == hipSuccess;
@@ -1521,6 +256,7 @@ aq_status aq_euclid_upload(aq_ctx *ctx, int64_t Q, int64_t N, int64_t K, int cb_
         return aq_fail(ctx, AQ_E_NOMEM, "aq_euclid_upload: device allocation failed");
     }
     ok = hipMemcpy(cb->d_cbh, cbh.data(), QNK * 2, hipMemcpyHostToDevice) == hipSuccess &&
+         hipMemcpy(cb->d_cbl, cbl.data(), QNK * 2, hipMemcpyHostToDevice) == hipSuccess &&
          hipMemcpy(cb->d_hh, hh.data(), QN * 4, hipMemcpyHostToDevice) == hipSuccess &&
          hipMemcpy(cb->d_cbf, cbf.data(), QNK * 4, hipMemcpyHostToDevice) == hipSuccess &&
          hipMemcpy(cb->d_bias, bias.data(), QN * 4, hipMemcpyHostToDevice) == hipSuccess &&
@@ -1540,7 +276,8 @@ aq_status aq_euclid_release(aq_codebooks *cb) {
     if (!cb) return AQ_E_INVALID_ARG;
     {
         aq_device_guard g(cb->ctx->device);
-        for (void *p : {static_cast<void *>(cb->d_cbh), static_cast<void *>(cb->d_hh), static_cast<void *>(cb->d_cbf),
+        for (void *p : {static_cast<void *>(cb->d_cbh), static_cast<void *>(cb->d_cbl), static_cast<void *>(cb->d_hh),
+                        static_cast<void *>(cb->d_cbf),
                         static_cast<void *>(cb->d_bias), static_cast<void *>(cb->d_e2), static_cast<void *>(cb->d_q8),
                         static_cast<void *>(cb->d_q8d)})
             if (p) (void)hipFree(p);
@@ -1564,29 +301,74 @@ aq_status aq_euclid_encode(aq_ctx *ctx, const aq_codebooks *cb, const float *x, 
     aq_device_guard g(ctx->device);
     const int K = static_cast<int>(cb->K);
     const int ks = K / 32;
-    StageFn sfn = pick_stage_fn(cb->recipe, cb->q8, ks, topk >= 4 ? 4 : 3);
+    const int topl = topk >= 4 ? 4 : 3;
+    const KsKernels *kk = kernels_for(ks);
+    const int var = variant_of(cb->recipe, cb->q8);
+    StageFn sweep = kk->sweep[cb->q8 ? 1 : 0][topl - 3];
+    StageFn select = kk->select[var][topl - 3];
     FallbackFn fvals = pick_fb_values(cb->recipe, cb->q8);
     FallbackFn fsel = pick_fb_select(cb->recipe, cb->q8);
-    const int lds = tile_lds(ks);
-    AQ_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void *>(sfn), hipFuncAttributeMaxDynamicSharedMemorySize, lds));
+    const int lds = kk->lds;
+    AQ_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void *>(sweep), hipFuncAttributeMaxDynamicSharedMemorySize, lds));
+    const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
+
+    // Sweep launch: tiles of kWaves * FG * 16 frames; the codebook is split
+    // over blockIdx.y so that there are about two sweep waves per SIMD (each
+    // split a whole number of LDS chunks, at most 4 splits).
+    const int FG = groups_for(ks);
+    const int64_t frames_per_block = static_cast<int64_t>(kWaves) * FG * 16;
+    const int64_t tiles = (M + frames_per_block - 1) / frames_per_block;
+    const int nch = static_cast<int>(cb->N / kk->cc);
+    int nsplit = 1;
+    for (int sp = 1; sp <= 4; ++sp)
+        if (nch % sp == 0 && tiles * sp <= 2 * cus) nsplit = sp;
+    const int64_t ngroups = (M + 15) / 16;
     const size_t fbv_lds = static_cast<size_t>(kFQ) * K * 5 + static_cast<size_t>(kFQ) * (K / 32) * 4 + 64;
     const size_t fbs_lds = static_cast<size_t>(K) * 5 + (K / 32) * 4 + 64;
 
-    // Work buffers: the residual (the caller's buffer when given) and the
-    // per-stage failure lists.
+    // Work buffers: the residual (the caller's buffer when given), the
+    // sweep's keys and frame norms, and the per-stage failure lists.
     float *work = residual;
     if (!work) {
         aq_status st = aq_ctx_scratch(ctx, 0, static_cast<size_t>(M) * K * sizeof(float), reinterpret_cast<void **>(&work));
         if (st != AQ_OK) return st;
     }
+    float *keys = nullptr;
+    {
+        const size_t key_bytes = static_cast<size_t>(nsplit) * ngroups * topl * kWave * sizeof(float);
+        void *w = nullptr;
+        aq_status st = aq_ctx_scratch(ctx, 4, key_bytes + 3 * static_cast<size_t>(M) * sizeof(float), &w);
+        if (st != AQ_OK) return st;
+        keys = static_cast<float *>(w);
+    }
+    // Counters (per stage, modulo 64): [0, 64) frames the bf16 certificate
+    // left open, [64, 128) frames sent on to the exact scan; then the two
+    // frame lists.
     int32_t *fails = nullptr;
     {
-        aq_status st = aq_ctx_scratch(ctx, 1, (static_cast<size_t>(M) + cb->Q + 64) * sizeof(int32_t),
+        aq_status st = aq_ctx_scratch(ctx, 1, (2 * static_cast<size_t>(M) + 128) * sizeof(int32_t),
                                       reinterpret_cast<void **>(&fails));
         if (st != AQ_OK) return st;
     }
     int32_t *counts = fails;
-    int32_t *list = fails + 64;
+    int32_t *counts2 = fails + 64;
+    int32_t *list = fails + 128;
+    int32_t *list2 = list + M;
+    // Refine-pass keys: up to 64 MiB, frames beyond the capacity go straight
+    // to the exact scan.
+    RefArgs rf{};
+    rf.nslices = static_cast<int>((cb->N + kRS - 1) / kRS);
+    {
+        const int64_t per_frame = static_cast<int64_t>(rf.nslices) * 4 * kTopR * 4;
+        rf.cap = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(M, (int64_t{64} << 20) / per_frame)));
+        void *w = nullptr;
+        aq_status st = aq_ctx_scratch(ctx, 3, static_cast<size_t>(rf.cap) * per_frame, &w);
+        if (st != AQ_OK) return st;
+        rf.keys = static_cast<float *>(w);
+    }
+    rf.list2 = list2;
+    RefineFn rvals = kk->refine_values[var];
+    RefineFn rsel = kk->refine_select[var];
     // Exact-scan work space: per failed frame, the best T codes of every
     // 256-code block, and a NaN flag.
     const int Tfb = (topk > 0 ? topk + 1 : 0) + 1;
@@ -1602,12 +384,9 @@ aq_status aq_euclid_encode(aq_ctx *ctx, const aq_codebooks *cb, const float *x, 
         fb.nan_flag = fb.cand_n + cand;
         AQ_HIP(ctx, hipMemsetAsync(fb.nan_flag, 0, static_cast<size_t>(M) * 4, ctx->stream));
     }
-    AQ_HIP(ctx, hipMemsetAsync(counts, 0, sizeof(int32_t) * 64, ctx->stream));
+    AQ_HIP(ctx, hipMemsetAsync(counts, 0, sizeof(int32_t) * 128, ctx->stream));
     AQ_HIP(ctx, hipMemsetAsync(ctx->d_flags, 0, sizeof(int32_t) * AQ_FLAG_COUNT, ctx->stream));
 
-    const int FG = groups_for(ks);
-    const int64_t frames_per_block = static_cast<int64_t>(kWaves) * FG * 16;
-    const unsigned blocks = static_cast<unsigned>((M + frames_per_block - 1) / frames_per_block);
     for (int64_t s = 0; s < cb->Q; ++s) {
         StageArgs a{};
         a.xin = s == 0 ? x : work;
@@ -1640,15 +419,34 @@ aq_status aq_euclid_encode(aq_ctx *ctx, const aq_codebooks *cb, const float *x, 
         a.fail_list = list;
         a.flags = ctx->d_flags;
         a.exact_only = cb->exact_only ? 1 : 0;
-        if (s >= 64 && s % 64 == 0) AQ_HIP(ctx, hipMemsetAsync(counts, 0, sizeof(int32_t) * 64, ctx->stream));
+        a.keys = keys;
+        a.norms = keys + static_cast<size_t>(nsplit) * ngroups * topl * kWave;
+        a.nsplit = nsplit;
+        if (s >= 64 && s % 64 == 0) AQ_HIP(ctx, hipMemsetAsync(counts, 0, sizeof(int32_t) * 128, ctx->stream));
         const int tslot = aq_timing_start(ctx);
-        hipLaunchKernelGGL(sfn, dim3(blocks), dim3(kThreads), lds, ctx->stream, a);
+        hipLaunchKernelGGL(sweep, dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(nsplit)), dim3(kThreads), lds,
+                           ctx->stream, a);
         aq_timing_stop(ctx, tslot);
         AQ_HIP(ctx, hipGetLastError());
-        const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
-        hipLaunchKernelGGL(fvals, dim3(static_cast<unsigned>(2 * cus)), dim3(kFbChunk), fbv_lds, ctx->stream, a, K, fb);
+        hipLaunchKernelGGL(select, dim3(static_cast<unsigned>((ngroups + kWaves - 1) / kWaves)), dim3(kThreads), 0,
+                           ctx->stream, a);
         AQ_HIP(ctx, hipGetLastError());
-        hipLaunchKernelGGL(fsel, dim3(static_cast<unsigned>(4 * cus)), dim3(kWave), fbs_lds, ctx->stream, a, K, fb);
+        // refine pass over the frames the stage kernel left open
+        rf.cbl = cb->d_cbl + s * cb->N * K;
+        rf.clmax = cb->clmax[s];
+        rf.crmax = cb->crmax[s];
+        rf.count2 = counts2 + (s % 64);
+        hipLaunchKernelGGL(rvals, dim3(static_cast<unsigned>(2 * cus)), dim3(kWave * kRWaves), 0, ctx->stream, a, rf);
+        AQ_HIP(ctx, hipGetLastError());
+        hipLaunchKernelGGL(rsel, dim3(static_cast<unsigned>(4 * cus)), dim3(kWave), 0, ctx->stream, a, rf);
+        AQ_HIP(ctx, hipGetLastError());
+        // exact scan of what the refine pass left open
+        StageArgs a2 = a;
+        a2.fail_count = rf.count2;
+        a2.fail_list = list2;
+        hipLaunchKernelGGL(fvals, dim3(static_cast<unsigned>(2 * cus)), dim3(kFbChunk), fbv_lds, ctx->stream, a2, K, fb);
+        AQ_HIP(ctx, hipGetLastError());
+        hipLaunchKernelGGL(fsel, dim3(static_cast<unsigned>(4 * cus)), dim3(kWave), fbs_lds, ctx->stream, a2, K, fb);
         AQ_HIP(ctx, hipGetLastError());
     }
     if (force_idx) {

@@ -1,0 +1,4 @@
+// Euclidean VQ / RVQ kernels for codebooks of width K = 512.
+#include "aq_euclid_kernels.hpp"
+
+AQ_EUCLID_KS_TABLE(16)
