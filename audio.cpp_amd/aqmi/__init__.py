@@ -27,7 +27,8 @@ STATUS_NAMES = {
 EXPORTED = [
     "aq_abi_version", "aq_ctx_create", "aq_ctx_destroy", "aq_ctx_set_stream", "aq_ctx_synchronize",
     "aq_last_error", "aq_dac_upload", "aq_dac_release", "aq_dac_encode", "aq_dac_decode",
-    "aq_euclid_upload", "aq_euclid_release", "aq_euclid_encode", "aq_euclid_failures", "aq_codebook_gather",
+    "aq_euclid_upload", "aq_euclid_release", "aq_euclid_encode", "aq_euclid_failures", "aq_euclid_exact_scans",
+    "aq_codebook_gather",
     "aq_euclid_decode", "aq_ctx_set_timing", "aq_ctx_read_timing",
 ]
 
@@ -65,6 +66,7 @@ def load_library(path: str | pathlib.Path | None = None) -> C.CDLL:
     lib.aq_euclid_release.argtypes = [vp]
     lib.aq_euclid_encode.argtypes = [vp, vp, vp, i64, vp, vp, vp, C.c_int, vp, vp, vp]
     lib.aq_euclid_failures.argtypes = [vp, vp, vp]
+    lib.aq_euclid_exact_scans.argtypes = [vp, vp, vp]
     lib.aq_codebook_gather.argtypes = [vp, vp, i64, vp, i64, vp]
     lib.aq_euclid_decode.argtypes = [vp, vp, vp, i64, vp]
     for name in EXPORTED:
@@ -209,8 +211,15 @@ class Codebooks:
                                                      _dptr(topk_dist), _dptr(force_idx)))
 
     def failures(self) -> np.ndarray:
+        """Frames per stage the bf16 certificate left to the refine pass."""
         out = np.zeros(64, np.int32)
         self.ctx.check(self.ctx.lib.aq_euclid_failures(self.ctx.h, self.h, out.ctypes.data_as(C.c_void_p)))
+        return out[: min(self.Q, 64)]
+
+    def exact_scans(self) -> np.ndarray:
+        """Frames per stage the refine pass left to the exact scan."""
+        out = np.zeros(64, np.int32)
+        self.ctx.check(self.ctx.lib.aq_euclid_exact_scans(self.ctx.h, self.h, out.ctypes.data_as(C.c_void_p)))
         return out[: min(self.Q, 64)]
 
     def gather(self, stage: int, idx, out):

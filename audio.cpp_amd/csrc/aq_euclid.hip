@@ -438,7 +438,7 @@ aq_status aq_euclid_encode(aq_ctx *ctx, const aq_codebooks *cb, const float *x, 
         rf.count2 = counts2 + (s % 64);
         hipLaunchKernelGGL(rvals, dim3(static_cast<unsigned>(2 * cus)), dim3(kWave * kRWaves), 0, ctx->stream, a, rf);
         AQ_HIP(ctx, hipGetLastError());
-        hipLaunchKernelGGL(rsel, dim3(static_cast<unsigned>(4 * cus)), dim3(kWave), 0, ctx->stream, a, rf);
+        hipLaunchKernelGGL(rsel, dim3(static_cast<unsigned>(16 * cus)), dim3(kWave), 0, ctx->stream, a, rf);
         AQ_HIP(ctx, hipGetLastError());
         // exact scan of what the refine pass left open
         StageArgs a2 = a;
@@ -446,7 +446,7 @@ aq_status aq_euclid_encode(aq_ctx *ctx, const aq_codebooks *cb, const float *x, 
         a2.fail_list = list2;
         hipLaunchKernelGGL(fvals, dim3(static_cast<unsigned>(2 * cus)), dim3(kFbChunk), fbv_lds, ctx->stream, a2, K, fb);
         AQ_HIP(ctx, hipGetLastError());
-        hipLaunchKernelGGL(fsel, dim3(static_cast<unsigned>(4 * cus)), dim3(kWave), fbs_lds, ctx->stream, a2, K, fb);
+        hipLaunchKernelGGL(fsel, dim3(static_cast<unsigned>(cus)), dim3(kFbSel), fbs_lds, ctx->stream, a2, K, fb);
         AQ_HIP(ctx, hipGetLastError());
     }
     if (force_idx) {
@@ -466,6 +466,18 @@ aq_status aq_euclid_failures(aq_ctx *ctx, const aq_codebooks *cb, int32_t *host_
     aq_device_guard g(ctx->device);
     const int64_t n = std::min<int64_t>(cb->Q, 64);
     AQ_HIP(ctx, hipMemcpyAsync(host_counts, fails, sizeof(int32_t) * n, hipMemcpyDeviceToHost, ctx->stream));
+    AQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return AQ_OK;
+}
+
+aq_status aq_euclid_exact_scans(aq_ctx *ctx, const aq_codebooks *cb, int32_t *host_counts) {
+    if (!ctx || !cb || !host_counts) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_euclid_exact_scans: null argument");
+    int32_t *fails = nullptr;
+    aq_status st = aq_ctx_scratch(ctx, 1, 0, reinterpret_cast<void **>(&fails));
+    if (st != AQ_OK || !fails) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_euclid_exact_scans: no encode has run");
+    aq_device_guard g(ctx->device);
+    const int64_t n = std::min<int64_t>(cb->Q, 64);
+    AQ_HIP(ctx, hipMemcpyAsync(host_counts, fails + 64, sizeof(int32_t) * n, hipMemcpyDeviceToHost, ctx->stream));
     AQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
     return AQ_OK;
 }

@@ -397,6 +397,15 @@ __device__ float exact_value_k(const StageArgs &a, const float *__restrict__ x, 
     return __fsub_rn(__fsub_rn(__fmul_rn(dot, 2.0f), x2), a.e2[n]);
 }
 
+// exact_value_k with the query's Q8_0 blocks already quantised (xq, xd).
+template <int RECIPE, bool Q8, int K>
+__device__ float exact_value_kq(const StageArgs &a, const float *__restrict__ x, int n, float x2,
+                                const int8_t *__restrict__ xq, const float *__restrict__ xd) {
+    if (!Q8) return exact_value_k<RECIPE, Q8, K>(a, x, n, x2);
+    const float dot = dot_q8(a.q8 + static_cast<int64_t>(n) * K, a.q8d + static_cast<int64_t>(n) * (K / 32), xq, xd, K / 32);
+    return __fsub_rn(__fsub_rn(__fmul_rn(dot, 2.0f), x2), a.e2[n]);
+}
+
 // Recipe value of code n ("larger is better" for OMNI/HIGGS: the logit;
 // DIRECT returns the distance, smaller is better).  x2 is sum_rows(x*x)
 // (HIGGS); xq/xd the quantised query (HIGGS with a Q8_0 codebook).
@@ -988,7 +997,7 @@ __global__ __launch_bounds__(kThreads) void euclid_select_kernel(StageArgs a) {
     // ---- phase 3: residual update r -= c[code] for certified frames ----
     // Rows across the lanes (coalesced), and the loads of kP3 frames issued
     // before the first wait so one memory round trip covers all of them.
-    constexpr int kP3 = 8;
+    constexpr int kP3 = 16;
     constexpr int KV = (K + 4 * kWave - 1) / (4 * kWave);   // float4 per lane per row
 #pragma unroll
     for (int g = 0; g < FG; ++g) {
@@ -1175,21 +1184,38 @@ __device__ inline bool fb_before(float va, int na, float vb, int nb, bool topk) 
     return topk ? topk_before<RECIPE>(va, na, vb, nb) : ranks_before<RECIPE>(va, na, vb, nb);
 }
 
+// Wave-wide selection of the best (value, index) pair under fb_before;
+// entries with index < 0 are empty.  Every lane returns the winner.
+template <int RECIPE>
+__device__ inline void wave_best(float &v, int &n, bool topk) {
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+        const float ov = __shfl_xor(v, off);
+        const int on = __shfl_xor(n, off);
+        if (on >= 0 && (n < 0 || fb_before<RECIPE>(ov, on, v, n, topk))) {
+            v = ov;
+            n = on;
+        }
+    }
+}
+
 template <int RECIPE, bool Q8>
 __global__ __launch_bounds__(kFbChunk) void euclid_fb_values_kernel(StageArgs a, int K, FbArgs fb) {
     extern __shared__ __align__(16) unsigned char lds[];
     float *xs = reinterpret_cast<float *>(lds);                         // [kFQ][K]
     int8_t *xq = reinterpret_cast<int8_t *>(xs + kFQ * K);              // [kFQ][K]
     float *xd = reinterpret_cast<float *>(xq + kFQ * K);                // [kFQ][K/32]
+    constexpr int kW = kFbChunk / kWave;
     __shared__ float x2s[kFQ];
-    __shared__ float red_v[kFbChunk];
-    __shared__ int red_n[kFbChunk];
-    __shared__ int chosen[5];
+    __shared__ float wv[kW][kFQ][6];
+    __shared__ int wn[kW][kFQ][6];
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const int count = *a.fail_count;
     // top-k slots (value desc, index asc; one more than k to see a tie at the
     // k-th place), then the argmax slot (the reference's tie rule)
     const int T = a.topk > 0 ? a.topk + 1 : 0;
     const int Tc = T + 1;
+    const int nb = K / 32;
     const int ngroups = (count + kFQ - 1) / kFQ;
     const int64_t nwork = static_cast<int64_t>(ngroups) * fb.nch;
     for (int64_t w = blockIdx.x; w < nwork; w += gridDim.x) {
@@ -1204,146 +1230,199 @@ __global__ __launch_bounds__(kFbChunk) void euclid_fb_values_kernel(StageArgs a,
         if (threadIdx.x < kFQ) {
             const int f = threadIdx.x;
             x2s[f] = RECIPE == OMNI || f >= nf ? 0.0f : sum_squares(xs + f * K, K);
-            if (Q8)
-                for (int ib = 0; ib < K / 32; ++ib) quantize_block_q8(xs + f * K + 32 * ib, xq + f * K + 32 * ib, xd + f * (K / 32) + ib);
+        }
+        if (Q8 && threadIdx.x < kFQ * nb) {   // one 32-element block per thread
+            const int f = threadIdx.x / nb, ib = threadIdx.x % nb;
+            quantize_block_q8(xs + f * K + 32 * ib, xq + f * K + 32 * ib, xd + f * nb + ib);
         }
         __syncthreads();
         const int n = ch * kFbChunk + threadIdx.x;
+        const bool valid = n < a.N;
         float vals[kFQ];
-        if (n < a.N) {
+        if (valid) {
             exact_values_fq<RECIPE, Q8>(a, K, n, xs, x2s, xq, xd, nf, vals);
         } else {
 #pragma unroll
             for (int f = 0; f < kFQ; ++f) vals[f] = 0.0f;
         }
-        for (int f = 0; f < nf; ++f) {
-            const int slot = grp * kFQ + f;
+        // Per wave: the best T codes in top-k order (T rounds with the
+        // winners excluded) and the best in argmax order, per frame.
+#pragma unroll
+        for (int f = 0; f < kFQ; ++f) {
+            if (f >= nf) break;
             float v = vals[f];
-            if (n < a.N && v != v) fb.nan_flag[slot] = 1;
+            if (valid && v != v) fb.nan_flag[grp * kFQ + f] = 1;
             if (v != v) v = RECIPE == DIRECT ? INFINITY : -INFINITY;
+            bool taken = false;
             for (int r = 0; r < Tc; ++r) {
                 const bool tk = r < T;
-                bool skip = n >= a.N;
-                if (tk)
-                    for (int q = 0; q < r; ++q) skip |= (chosen[q] == n);
-                red_v[threadIdx.x] = v;
-                red_n[threadIdx.x] = skip ? -1 : n;
-                __syncthreads();
-                for (int step = kFbChunk / 2; step > 0; step >>= 1) {
-                    if (threadIdx.x < step) {
-                        const int on = red_n[threadIdx.x + step], cn = red_n[threadIdx.x];
-                        const float ov = red_v[threadIdx.x + step], cv = red_v[threadIdx.x];
-                        if (on >= 0 && (cn < 0 || fb_before<RECIPE>(ov, on, cv, cn, tk))) {
-                            red_v[threadIdx.x] = ov;
-                            red_n[threadIdx.x] = on;
-                        }
-                    }
-                    __syncthreads();
+                float bv = v;
+                int bn = valid && !(tk && taken) ? n : -1;
+                wave_best<RECIPE>(bv, bn, tk);
+                if (tk && bn == n) taken = true;
+                if (lane == 0) {
+                    wv[wave][f][r] = bv;
+                    wn[wave][f][r] = bn;
                 }
-                if (threadIdx.x == 0) {
-                    if (tk) chosen[r] = red_n[0];
-                    const int64_t o = (static_cast<int64_t>(slot) * fb.nch + ch) * Tc + r;
-                    fb.cand_v[o] = red_v[0];
-                    fb.cand_n[o] = red_n[0];
-                }
-                __syncthreads();
             }
+        }
+        __syncthreads();
+        // Merge the waves' lists: thread (f, r) writes slot r of frame f.
+        if (threadIdx.x < nf * Tc) {
+            const int f = threadIdx.x / Tc, r = threadIdx.x % Tc;
+            const int slot = grp * kFQ + f;
+            float bv = 0.0f;
+            int bn = -1;
+            if (r < T) {
+                // r-th best of the union in top-k order: count the entries
+                // that rank before each candidate.
+                for (int q = 0; q < kW * T; ++q) {
+                    const float cv = wv[q / T][f][q % T];
+                    const int cn = wn[q / T][f][q % T];
+                    if (cn < 0) continue;
+                    int before = 0;
+                    for (int o = 0; o < kW * T; ++o) {
+                        const int on = wn[o / T][f][o % T];
+                        if (on >= 0 && fb_before<RECIPE>(wv[o / T][f][o % T], on, cv, cn, true)) ++before;
+                    }
+                    if (before == r) {
+                        bv = cv;
+                        bn = cn;
+                    }
+                }
+            } else {
+                for (int q = 0; q < kW; ++q) {
+                    const float cv = wv[q][f][T];
+                    const int cn = wn[q][f][T];
+                    if (cn >= 0 && (bn < 0 || fb_before<RECIPE>(cv, cn, bv, bn, false))) {
+                        bv = cv;
+                        bn = cn;
+                    }
+                }
+            }
+            const int64_t o = (static_cast<int64_t>(slot) * fb.nch + ch) * Tc + r;
+            fb.cand_v[o] = bv;
+            fb.cand_n[o] = bn;
         }
     }
 }
 
+// fb_select block: wave 0 merges the candidates; a replay in code order
+// (NaN scores or a tie at the k-th place) uses the whole block to compute the
+// exact values kFbReplay codes at a time, then one thread runs ggml's argmax
+// and the top-k heap over them.
+constexpr int kFbSel = 256;
+constexpr int kFbReplay = 2048;
+
 template <int RECIPE, bool Q8>
-__global__ __launch_bounds__(kWave) void euclid_fb_select_kernel(StageArgs a, int K, FbArgs fb) {
+__global__ __launch_bounds__(kFbSel) void euclid_fb_select_kernel(StageArgs a, int K, FbArgs fb) {
     extern __shared__ __align__(16) unsigned char lds[];
     float *xs = reinterpret_cast<float *>(lds);                         // [K]
     int8_t *xq = reinterpret_cast<int8_t *>(xs + K);                    // [K]
     float *xd = reinterpret_cast<float *>(xq + K);                      // [K/32]
-    __shared__ float vals64[kWave];
-    const int lane = threadIdx.x;
-    const int count = *a.fail_count;
+    __shared__ float rv[kFbReplay];
     __shared__ int heap_n[4];
     __shared__ float heap_v[4];
+    __shared__ int o_code, o_sel_n[5], o_replay, o_nan;
+    __shared__ float o_code_v, o_sel_v[5], o_x2;
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int count = *a.fail_count;
     const int T = a.topk > 0 ? a.topk + 1 : 0;
     const int Tc = T + 1;
+    const int ktop = a.topk;
     for (int slot = blockIdx.x; slot < count; slot += gridDim.x) {
         const int64_t m = a.fail_list[slot];
-        float sel_v[5];
-        int sel_n[5];
+        __syncthreads();
+        if (tid < kWave) {
+            float sel_v[5];
+            int sel_n[5];
 #pragma unroll
-        for (int r = 0; r < 5; ++r) {
-            sel_v[r] = 0.0f;
-            sel_n[r] = -1;
-        }
-        // ranked merge of the per-block candidates (lane-strided, then a wave
-        // merge): r < T merges the top-k slots, r == T the argmax slots
-        const int total = fb.nch * Tc;
-        int code = 0;
-        float code_v = 0.0f;
-        for (int r = 0; r < Tc; ++r) {
-            const bool tk = r < T;
-            float bv = 0.0f;
-            int bn = -1;
-            for (int i = lane; i < total; i += kWave) {
-                if (tk != (i % Tc < T)) continue;
-                const int64_t o = static_cast<int64_t>(slot) * total + i;
-                const int n = fb.cand_n[o];
-                if (n < 0) continue;
-                bool skip = false;
-                if (tk)
-                    for (int q = 0; q < r; ++q) skip |= (sel_n[q] == n);
-                const float v = fb.cand_v[o];
-                if (!skip && (bn < 0 || fb_before<RECIPE>(v, n, bv, bn, tk))) {
-                    bv = v;
-                    bn = n;
-                }
+            for (int r = 0; r < 5; ++r) {
+                sel_v[r] = 0.0f;
+                sel_n[r] = -1;
             }
-            for (int off = 1; off < kWave; off <<= 1) {
-                const float ov = __shfl_xor(bv, off);
-                const int on = __shfl_xor(bn, off);
-                if (on >= 0 && (bn < 0 || fb_before<RECIPE>(ov, on, bv, bn, tk))) {
-                    bv = ov;
-                    bn = on;
-                }
-            }
-            if (tk) {
-#pragma unroll
-                for (int q = 0; q < 5; ++q)
-                    if (q == r) {
-                        sel_v[q] = bv;
-                        sel_n[q] = bn;
+            // ranked merge of the per-block candidates (lane-strided, then a wave
+            // merge): r < T merges the top-k slots, r == T the argmax slots
+            const int total = fb.nch * Tc;
+            int code = 0;
+            float code_v = 0.0f;
+            for (int r = 0; r < Tc; ++r) {
+                const bool tk = r < T;
+                float bv = 0.0f;
+                int bn = -1;
+                for (int i = lane; i < total; i += kWave) {
+                    if (tk != (i % Tc < T)) continue;
+                    const int64_t o = static_cast<int64_t>(slot) * total + i;
+                    const int n = fb.cand_n[o];
+                    if (n < 0) continue;
+                    bool skip = false;
+                    if (tk)
+                        for (int q = 0; q < r; ++q) skip |= (sel_n[q] == n);
+                    const float v = fb.cand_v[o];
+                    if (!skip && (bn < 0 || fb_before<RECIPE>(v, n, bv, bn, tk))) {
+                        bv = v;
+                        bn = n;
                     }
-            } else {
-                code = bn < 0 ? 0 : bn;
-                code_v = bv;
+                }
+                for (int off = 1; off < kWave; off <<= 1) {
+                    const float ov = __shfl_xor(bv, off);
+                    const int on = __shfl_xor(bn, off);
+                    if (on >= 0 && (bn < 0 || fb_before<RECIPE>(ov, on, bv, bn, tk))) {
+                        bv = ov;
+                        bn = on;
+                    }
+                }
+                if (tk) {
+#pragma unroll
+                    for (int q = 0; q < 5; ++q)
+                        if (q == r) {
+                            sel_v[q] = bv;
+                            sel_n[q] = bn;
+                        }
+                } else {
+                    code = bn < 0 ? 0 : bn;
+                    code_v = bv;
+                }
+            }
+            bool kth_tie = false;
+#pragma unroll
+            for (int q = 1; q < 5; ++q)
+                if (q == ktop) kth_tie = sel_n[q] >= 0 && sel_v[q] == sel_v[q - 1];
+            const bool nan_seen = fb.nan_flag[slot] != 0;
+            if (lane == 0) {
+                o_code = code;
+                o_code_v = code_v;
+#pragma unroll
+                for (int q = 0; q < 5; ++q) {
+                    o_sel_n[q] = sel_n[q];
+                    o_sel_v[q] = sel_v[q];
+                }
+                o_nan = nan_seen ? 1 : 0;
+                o_replay = (RECIPE != DIRECT && (nan_seen || (ktop > 0 && kth_tie))) ? 1 : 0;
             }
         }
-        const int ktop = a.topk;
-        bool kth_tie = false;
-#pragma unroll
-        for (int q = 1; q < 5; ++q)
-            if (q == ktop) kth_tie = sel_n[q] >= 0 && sel_v[q] == sel_v[q - 1];
-        const bool nan_seen = fb.nan_flag[slot] != 0;
-        if (RECIPE != DIRECT && (nan_seen || (ktop > 0 && kth_tie))) {
+        __syncthreads();
+        if (o_replay) {
             // Replay in code order: ggml_vec_argmax_f32 (MAX(max, v), index of
             // the last element equal to the running max; NaN restarts it) and
             // ggml_top_k's heap selection (libstdc++ std::partial_sort).
-            for (int kk = lane; kk < K; kk += kWave) xs[kk] = a.xin[m * K + kk];
+            for (int k = tid; k < K; k += kFbSel) xs[k] = a.xin[m * K + k];
             __syncthreads();
-            float x2 = 0.0f;
-            if (RECIPE == HIGGS) x2 = sum_squares(xs, K);
-            if (Q8 && lane == 0)
-                for (int ib = 0; ib < K / 32; ++ib) quantize_block_q8(xs + 32 * ib, xq + 32 * ib, xd + ib);
+            if (tid == 0) o_x2 = RECIPE == HIGGS ? sum_squares(xs, K) : 0.0f;
+            if (Q8 && tid < K / 32) quantize_block_q8(xs + 32 * tid, xq + 32 * tid, xd + tid);
             __syncthreads();
-            float mx = -INFINITY;
+            const float x2 = o_x2;
+            float mx = -INFINITY, root = 0.0f;
             int id = 0;
-            for (int base = 0; base < a.N; base += kWave) {
-                const int n = base + lane;
-                vals64[lane] = n < a.N ? exact_value<RECIPE, Q8>(a, K, xs, n, x2, xq, xd) : 0.0f;
+            for (int base = 0; base < a.N; base += kFbReplay) {
+                const int len = min(kFbReplay, a.N - base);
+                for (int i = tid; i < len; i += kFbSel) rv[i] = exact_value<RECIPE, Q8>(a, K, xs, base + i, x2, xq, xd);
                 __syncthreads();
-                if (lane == 0)
-                    for (int i = 0; i < kWave && base + i < a.N; ++i) {
+                if (tid == 0) {
+                    for (int i = 0; i < len; ++i) {
                         const int n_i = base + i;
-                        const float v = vals64[i];
+                        const float v = rv[i];
                         mx = mx > v ? mx : v;
                         if (mx == v) id = n_i;
                         if (ktop > 0) {
@@ -1355,55 +1434,59 @@ __global__ __launch_bounds__(kWave) void euclid_fb_select_kernel(StageArgs a, in
                                         heap_adjust(heap_n, heap_v, par, ktop, heap_n[par], heap_v[par]);
                                         if (par == 0) break;
                                     }
-                            } else if (v > heap_v[0]) {
+                                if (n_i == ktop - 1) root = heap_v[0];
+                            } else if (v > root) {
                                 heap_adjust(heap_n, heap_v, 0, ktop, n_i, v);
+                                root = heap_v[0];
                             }
                         }
                     }
+                }
                 __syncthreads();
             }
-            if (nan_seen) {
-                code = __shfl(id, 0);
-                code_v = __shfl(mx, 0);
-            }
-            if (ktop > 0 && lane == 0) {
-                // report the kept set best first, ties by index
-                for (int r = 0; r < ktop; ++r) {
-                    int b = -1;
-                    for (int q = 0; q < ktop; ++q) {
-                        bool used = false;
-                        for (int t = 0; t < r; ++t) used |= sel_n[t] == heap_n[q];
-                        if (!used && (b < 0 || topk_before<RECIPE>(heap_v[q], heap_n[q], heap_v[b], heap_n[b]))) b = q;
-                    }
-#pragma unroll
-                    for (int q = 0; q < 5; ++q)
-                        if (q == r) {
-                            sel_n[q] = heap_n[b];
-                            sel_v[q] = heap_v[b];
+            if (tid == 0) {
+                if (o_nan) {
+                    o_code = id;
+                    o_code_v = mx;
+                }
+                if (ktop > 0) {
+                    // report the kept set best first, ties by index
+                    int used[4] = {-1, -1, -1, -1};
+                    for (int r = 0; r < ktop; ++r) {
+                        int b = -1;
+                        for (int q = 0; q < ktop; ++q) {
+                            bool u = false;
+                            for (int t = 0; t < r; ++t) u |= used[t] == q;
+                            if (!u && (b < 0 || topk_before<RECIPE>(heap_v[q], heap_n[q], heap_v[b], heap_n[b]))) b = q;
                         }
+                        used[r] = b;
+                        o_sel_n[r] = heap_n[b];
+                        o_sel_v[r] = heap_v[b];
+                    }
                 }
             }
             __syncthreads();
         }
-        if (lane == 0) {
+        const int code = o_code;
+        if (tid == 0) {
             a.idx[m * a.Q + a.s] = code;
-            if (a.dist) a.dist[m * a.Q + a.s] = RECIPE == DIRECT ? code_v : -code_v;
+            if (a.dist) a.dist[m * a.Q + a.s] = RECIPE == DIRECT ? o_code_v : -o_code_v;
             for (int r = 0; r < a.topk; ++r) {
-                a.topk_idx[(m * a.Q + a.s) * a.topk + r] = sel_n[r];
-                a.topk_dist[(m * a.Q + a.s) * a.topk + r] = RECIPE == DIRECT ? sel_v[r] : -sel_v[r];
+                a.topk_idx[(m * a.Q + a.s) * a.topk + r] = o_sel_n[r];
+                a.topk_dist[(m * a.Q + a.s) * a.topk + r] = RECIPE == DIRECT ? o_sel_v[r] : -o_sel_v[r];
             }
         }
         int use = code;
         if (a.force_idx) {
             use = a.force_idx[m * a.Q + a.s];
             if (use < 0 || use >= a.N) {
-                if (lane == 0) a.flags[AQ_FLAG_BAD_INDEX] = 1;
+                if (tid == 0) a.flags[AQ_FLAG_BAD_INDEX] = 1;
                 use = 0;
             }
         }
-        for (int k = lane; k < K; k += kWave)
+        for (int k = tid; k < K; k += kFbSel)
             a.xout[m * K + k] = __fsub_rn(a.xin[m * K + k], a.cbf[static_cast<int64_t>(use) * K + k]);
-        if (lane == 0) fb.nan_flag[slot] = 0;
+        if (tid == 0) fb.nan_flag[slot] = 0;
     }
 }
 
@@ -1428,19 +1511,55 @@ __global__ __launch_bounds__(kWave) void euclid_fb_select_kernel(StageArgs a, in
 //    certificate and writes codes, distances, top-k and the residual.
 
 
+// LDS image of one 16-code block for the refine pass: bf16 high and low
+// rows (XOR-swizzled 16-byte pieces, as in the sweep) and -|c|^2/2.
+template <int KS>
+struct RefTile {
+    static constexpr int K = KS * 32;
+    static constexpr int ROWB = K * 2;
+    static constexpr int CH16 = K / 8;
+    static constexpr int SWZ = CH16 >= 16 ? 15 : CH16 - 1;
+    static constexpr int ROWS16 = 16 * CH16;                    // 16-byte pieces per 16-row array
+    static constexpr int PIECES = 2 * ROWS16;                   // high + low
+    static constexpr int STG = (PIECES + kThreads - 1) / kThreads;
+    static constexpr int BUFB = 2 * 16 * ROWB + 16 * 4;
+};
+
 template <int RECIPE, bool Q8, int KS>
-__global__ __launch_bounds__(kWave * kRWaves) void euclid_refine_values_kernel(StageArgs a, RefArgs rf) {
+__global__ __launch_bounds__(kWave * kRWaves, KS <= 8 ? 2 : 1) void euclid_refine_values_kernel(StageArgs a, RefArgs rf) {
+    using T = RefTile<KS>;
     constexpr int K = KS * 32;
+    static_assert(kWave * kRWaves == kThreads, "refine blocks have the sweep's shape");
+    __shared__ __align__(16) unsigned char lds[2 * T::BUFB];
     const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
     const int col = lane & 15, kq = lane >> 4;
     const int count = min(*a.fail_count, rf.cap);
-    const int64_t nwork = static_cast<int64_t>((count + 15) / 16) * rf.nslices;
+    const int ntiles = (count + 16 * kRWaves - 1) / (16 * kRWaves);
+    const int64_t nwork = static_cast<int64_t>(ntiles) * rf.nslices;
     unsigned vkeep;
     asm volatile("v_mov_b32 %0, %1" : "=v"(vkeep) : "s"(~63u));
-    for (int64_t w = static_cast<int64_t>(blockIdx.x) * kRWaves + threadIdx.x / kWave; w < nwork;
-         w += static_cast<int64_t>(gridDim.x) * kRWaves) {
-        const int grp = static_cast<int>(w / rf.nslices), sl = static_cast<int>(w % rf.nslices);
-        const int fs = grp * 16 + col;
+
+    auto piece_off = [&](int buf, int p) -> int {   // byte offset of staged piece p
+        const int arr = p / T::ROWS16, q = p % T::ROWS16;
+        const int r = q / T::CH16, j = q % T::CH16;
+        return buf * T::BUFB + arr * (16 * T::ROWB) + r * T::ROWB + ((j ^ (r & T::SWZ)) * 16);
+    };
+    auto lds_a = [&](int buf, int arr, int ks) -> bf16x8 {
+        const int j = ks * 4 + kq;
+        return *reinterpret_cast<const bf16x8 *>(lds + buf * T::BUFB + arr * (16 * T::ROWB) + col * T::ROWB +
+                                                 ((j ^ (col & T::SWZ)) * 16));
+    };
+    // global source of piece p of block n16 (16 codes from n16)
+    auto piece_src = [&](int n16, int p) -> const u32x4 * {
+        const int arr = p / T::ROWS16, q = p % T::ROWS16;
+        const uint16_t *base = arr == 0 ? a.cbh : rf.cbl;
+        return reinterpret_cast<const u32x4 *>(base + static_cast<int64_t>(n16) * K) + q;
+    };
+
+    for (int64_t w = blockIdx.x; w < nwork; w += gridDim.x) {
+        const int tile = static_cast<int>(w / rf.nslices), sl = static_cast<int>(w % rf.nslices);
+        const int fs = (tile * kRWaves + wave) * 16 + col;
         const int64_t m = a.fail_list[fs < count ? fs : count - 1];
         const float *xr = a.xin + m * K;
         u32x4 xh[KS], xl[KS];
@@ -1467,14 +1586,36 @@ __global__ __launch_bounds__(kWave * kRWaves) void euclid_refine_values_kernel(S
         for (int j = 0; j < kTopR; ++j) top[j] = -INFINITY;
         const int n0 = sl * kRS;
         const int nb = min(kRS, a.N - n0) / 16;
+
+        // stage block 0 of the slice
+        __syncthreads();   // the previous work item's last reads of buffer 0/1
+#pragma unroll
+        for (int i = 0; i < T::STG; ++i) {
+            const int p = threadIdx.x + i * kThreads;
+            if (p < T::PIECES) *reinterpret_cast<u32x4 *>(lds + piece_off(0, p)) = *piece_src(n0, p);
+        }
+        if (threadIdx.x < 16) reinterpret_cast<float *>(lds + 2 * 16 * T::ROWB)[threadIdx.x] = a.nhh[n0 + threadIdx.x];
+        __syncthreads();
         for (int b = 0; b < nb; ++b) {
-            const int64_t row = static_cast<int64_t>(n0 + b * 16 + col) * K + kq * 8;
-            f32x4 acc = *reinterpret_cast<const f32x4 *>(a.nhh + n0 + b * 16 + kq * 4);
+            const int buf = b & 1;
+            const bool more = b + 1 < nb;
+            // the next block's pieces are fetched while this one computes
+            u32x4 stg[T::STG];
+            float hst = 0.0f;
+            if (more) {
+#pragma unroll
+                for (int i = 0; i < T::STG; ++i) {
+                    const int p = threadIdx.x + i * kThreads;
+                    if (p < T::PIECES) stg[i] = *piece_src(n0 + (b + 1) * 16, p);
+                }
+                if (threadIdx.x < 16) hst = a.nhh[n0 + (b + 1) * 16 + threadIdx.x];
+            }
+            f32x4 acc = *reinterpret_cast<const f32x4 *>(lds + buf * T::BUFB + 2 * 16 * T::ROWB + kq * 16);
             f32x4 acx = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
-                const bf16x8 ah = *reinterpret_cast<const bf16x8 *>(a.cbh + row + ks * 32);
-                const bf16x8 al = *reinterpret_cast<const bf16x8 *>(rf.cbl + row + ks * 32);
+                const bf16x8 ah = lds_a(buf, 0, ks);
+                const bf16x8 al = lds_a(buf, 1, ks);
                 const bf16x8 bh = __builtin_bit_cast(bf16x8, xh[ks]);
                 acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc, 0, 0, 0);
                 acx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acx, 0, 0, 0);
@@ -1487,6 +1628,15 @@ __global__ __launch_bounds__(kWave * kRWaves) void euclid_refine_values_kernel(S
                 for (int j = kTopR - 1; j > 0; --j) top[j] = __builtin_amdgcn_fmed3f(top[j - 1], top[j], key);
                 top[0] = __builtin_amdgcn_fmed3f(top[0], key, 3.40282347e38f);
             }
+            if (more) {
+#pragma unroll
+                for (int i = 0; i < T::STG; ++i) {
+                    const int p = threadIdx.x + i * kThreads;
+                    if (p < T::PIECES) *reinterpret_cast<u32x4 *>(lds + piece_off(buf ^ 1, p)) = stg[i];
+                }
+                if (threadIdx.x < 16) reinterpret_cast<float *>(lds + (buf ^ 1) * T::BUFB + 2 * 16 * T::ROWB)[threadIdx.x] = hst;
+            }
+            __syncthreads();
         }
         if (fs < count) {
             f32x4 *dst = reinterpret_cast<f32x4 *>(rf.keys + ((static_cast<int64_t>(fs) * rf.nslices + sl) * 4 + kq) * kTopR);
@@ -1507,6 +1657,10 @@ __global__ __launch_bounds__(kWave) void euclid_refine_select_kernel(StageArgs a
     constexpr int KPL = K / kWave;   // frame elements per lane
     __shared__ int cand_n[kRCand];
     __shared__ float cand_v[kRCand];
+    __shared__ float xs[K];                // the frame (exact evaluation reads it here)
+    __shared__ int8_t xq[Q8 ? K : 4];      // its Q8_0 blocks
+    __shared__ float xd[Q8 ? K / 32 : 1];
+    __shared__ float x2s;
     const int lane = threadIdx.x;
     const float u = 5.9604645e-8f;   // 2^-24
     const int Tk = a.topk > 0 ? a.topk : 1;
@@ -1524,6 +1678,7 @@ __global__ __launch_bounds__(kWave) void euclid_refine_select_kernel(StageArgs a
 #pragma unroll
         for (int j = 0; j < KPL; ++j) {
             float v = xr[lane + kWave * j];
+            xs[lane + kWave * j] = v;
             if (Q8) {
                 float am = fabsf(v);
 #pragma unroll
@@ -1614,9 +1769,13 @@ __global__ __launch_bounds__(kWave) void euclid_refine_select_kernel(StageArgs a
         }
         __syncthreads();
         if (ok) {
-            const float x2 = RECIPE == HIGGS ? sum_squares_k<K>(xr) : 0.0f;
-            for (int c = lane; c < ncand; c += kWave) cand_v[c] = exact_value_k<RECIPE, Q8, K>(a, xr, cand_n[c], x2);
+            if (Q8 && lane < K / 32) quantize_block_q8(xs + 32 * lane, xq + 32 * lane, xd + lane);
+            if (RECIPE == HIGGS && lane == 0) x2s = sum_squares_k<K>(xs);
         }
+        __syncthreads();
+        const float x2c = RECIPE == HIGGS ? x2s : 0.0f;
+        if (ok)
+            for (int c = lane; c < ncand; c += kWave) cand_v[c] = exact_value_kq<RECIPE, Q8, K>(a, xs, cand_n[c], x2c, xq, xd);
         __syncthreads();
 
         // Ranked selection of the evaluated candidates (every lane computes
@@ -1657,8 +1816,6 @@ __global__ __launch_bounds__(kWave) void euclid_refine_select_kernel(StageArgs a
             if (!have) {
                 ok = false;
             } else {
-                float x2c = 0.0f;
-                if (RECIPE == HIGGS) x2c = sum_squares_k<K>(xr);
                 float sprime;
                 if (RECIPE == OMNI) sprime = 0.5f * sv;
                 else if (RECIPE == HIGGS) sprime = 0.5f * sv + 0.5f * x2c;
@@ -1713,7 +1870,7 @@ __global__ __launch_bounds__(kWave) void euclid_refine_select_kernel(StageArgs a
 #pragma unroll
         for (int j = 0; j < KPL; ++j) {
             const int k = lane + kWave * j;
-            a.xout[m * K + k] = __fsub_rn(xr[k], a.cbf[static_cast<int64_t>(use) * K + k]);
+            a.xout[m * K + k] = __fsub_rn(xs[k], a.cbf[static_cast<int64_t>(use) * K + k]);
         }
     }
 }

@@ -187,9 +187,16 @@ aq_status aq_euclid_encode(aq_ctx *ctx, const aq_codebooks *cb, const float *x, 
                            const int32_t *force_idx);
 
 /* Frames per stage (first min(Q, 64) stages) of the last encode on ctx that
- * the error certificate could not settle and the exact scan decided (host
- * int32 array; synchronises the stream).  A measurement aid. */
+ * the bf16 error certificate could not settle; the split-bf16 refine pass
+ * took them (host int32 array; synchronises the stream).  A measurement aid
+ * with no reference counterpart. */
 aq_status aq_euclid_failures(aq_ctx *ctx, const aq_codebooks *cb, int32_t *host_counts);
+
+/* Frames per stage (first min(Q, 64) stages) of the last encode on ctx that
+ * the refine pass could not settle either and the exact scan decided (host
+ * int32 array; synchronises the stream).  A measurement aid with no
+ * reference counterpart. */
+aq_status aq_euclid_exact_scans(aq_ctx *ctx, const aq_codebooks *cb, int32_t *host_counts);
 
 /* Codebook gather of one stage: out[m] = codebook[stage][idx[m]] (ggml_get_rows,
  * lookup_modules.cpp:88-112,182-187; Q8_0 rows dequantised as q*d).
