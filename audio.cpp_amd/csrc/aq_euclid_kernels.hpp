@@ -442,6 +442,14 @@ __device__ inline bool topk_before(float va, int na, float vb, int nb) {
 
 // --------------------------------------------------------------- score kernel
 
+// v + v[lane rotated by N inside its 16-lane row] (DPP row_ror).  IEEE
+// addition is commutative, so each lane's sum is the pair the reference adds.
+template <int N>
+__device__ inline float row_ror_add(float v) {
+    const int o = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x120 + N, 0xF, 0xF, false);
+    return __fadd_rn(v, __int_as_float(o));
+}
+
 // The query's Q8_0 image x_q = q * d of one 32-wide block (x86
 // quantize_row_q8_0: d = fp16(amax/127), q = round-half-even(x * 127/amax)),
 // held by 4 lanes 16 apart with 8 elements each.  x_q is exact in fp32
@@ -770,10 +778,14 @@ __global__ __launch_bounds__(kThreads) void euclid_select_kernel(StageArgs a) {
     constexpr int QCAP = FG * 16 * 4 * TOPL;
     __shared__ int32_t q_n_s[kWaves][QCAP], q_f_s[kWaves][QCAP];
     __shared__ float q_v_s[kWaves][QCAP], q_x2_s[kWaves][FG * 16];
+    __shared__ __align__(16) int8_t q_xq_s[kWaves][Q8 ? 16 * K : 4];     // Q8_0 blocks of the frames
+    __shared__ float q_xd_s[kWaves][Q8 ? 16 * (K / 32) : 1];
     int32_t *q_n = q_n_s[wave];
     int32_t *q_f = q_f_s[wave];
     float *q_v = q_v_s[wave];
     float *q_x2 = q_x2_s[wave];
+    int8_t *q_xq = q_xq_s[wave];
+    float *q_xd = q_xd_s[wave];
 
     float Eg[FG], taug[FG], best0g[FG];
     bool okg[FG], needg[FG];
@@ -866,17 +878,89 @@ __global__ __launch_bounds__(kThreads) void euclid_select_kernel(StageArgs a) {
             q_x2[lane] = need ? sum_squares_k<K>(a.xin + (m_base + lane) * K) : 0.0f;
         }
     }
+    // Q8_0: each frame's query blocks are quantised once (x86
+    // quantize_row_q8_0), the 4 lanes of a frame taking every 4th block.
+    if (Q8 && qcount > 0) {
+        const int64_t mq = m_base + col < a.M ? m_base + col : a.M - 1;
+#pragma unroll
+        for (int ib = kq; ib < K / 32; ib += 4)
+            quantize_block_q8(a.xin + mq * K + 32 * ib, q_xq + col * K + 32 * ib, q_xd + col * (K / 32) + ib);
+    }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // 2c: exact values of the queued pairs
-    for (int e0 = 0; e0 < qcount; e0 += kWave) {
-        const int e = e0 + lane;
-        if (e < qcount) {
+    // 2c: exact values of the queued pairs, in the reference's arithmetic.
+    if (!Q8 && RECIPE != DIRECT && a.order == 0) {
+        // tinyBLAS: 16 accumulators over k = 16 l + j, one per lane of a
+        // 16-lane row (coalesced row reads), then _mm512_reduce_add_ps's
+        // pairing tree as DPP row rotations 8, 4, 2, 1; 4 pairs per pass.
+        // Two pairs per row and pass, so that their row reads are in flight
+        // together.
+        constexpr int P = 2;
+        const int j = lane & 15, grp = lane >> 4;
+        const float sa = RECIPE == OMNI ? 2.0f : 1.0f;
+        for (int e0 = grp; e0 < qcount; e0 += 4 * P) {
+            int fs[P], n[P];
+            float acc[P];
+#pragma unroll
+            for (int p = 0; p < P; ++p) {
+                const int e = e0 + 4 * p;
+                fs[p] = e < qcount ? q_f[e] : 0;
+                n[p] = e < qcount ? q_n[e] : 0;
+                acc[p] = 0.0f;
+            }
+#pragma unroll
+            for (int l = 0; l < K / 16; ++l)
+#pragma unroll
+                for (int p = 0; p < P; ++p)
+                    acc[p] = __fmaf_rn(a.cbf[static_cast<int64_t>(n[p]) * K + 16 * l + j] * sa,
+                                       a.xin[(m_base + fs[p]) * K + 16 * l + j], acc[p]);
+#pragma unroll
+            for (int p = 0; p < P; ++p) {
+                float v = row_ror_add<8>(acc[p]);
+                v = row_ror_add<4>(v);
+                v = row_ror_add<2>(v);
+                v = row_ror_add<1>(v);
+                const int e = e0 + 4 * p;
+                if (j == 0 && e < qcount) {
+                    if (RECIPE == OMNI) q_v[e] = __fadd_rn(v, a.bias[n[p]]);
+                    else q_v[e] = __fsub_rn(__fsub_rn(__fmul_rn(v, 2.0f), q_x2[fs[p]]), a.e2[n[p]]);
+                }
+            }
+        }
+    } else if (Q8) {
+        // ggml_vec_dot_q8_0_q8_0: 8 accumulators over the 4-element groups
+        // of every block, one per lane of an 8-lane group, then hsum_float_8
+        // (i + 4, then pairs) as lane exchanges 4, 2, 1; 8 pairs per pass.
+        const int j = lane & 7, grp = lane >> 3;
+        for (int e = grp; e < qcount; e += 8) {
             const int fs = q_f[e];
             const int n = q_n[e];
-            const float x2 = RECIPE == HIGGS ? q_x2[fs] : 0.0f;
-            q_v[e] = exact_value_k<RECIPE, Q8, K>(a, a.xin + (m_base + fs) * K, n, x2);
+            const int *cq = reinterpret_cast<const int *>(a.q8 + static_cast<int64_t>(n) * K) + j;
+            const float *cd = a.q8d + static_cast<int64_t>(n) * (K / 32);
+            const int *xq = reinterpret_cast<const int *>(q_xq + fs * K) + j;
+            const float *xd = q_xd + fs * (K / 32);
+            float acc = 0.0f;
+#pragma unroll
+            for (int ib = 0; ib < K / 32; ++ib) {
+                const float dd = __fmul_rn(cd[ib], xd[ib]);
+                acc = __fmaf_rn(dd, static_cast<float>(__builtin_amdgcn_sdot4(cq[8 * ib], xq[8 * ib], 0, false)), acc);
+            }
+            // lane 0 of the group: ((a0 + a4) + (a2 + a6)) + ((a1 + a5) + (a3 + a7))
+            acc = __fadd_rn(acc, __shfl_xor(acc, 4));
+            acc = __fadd_rn(acc, __shfl_xor(acc, 2));
+            acc = __fadd_rn(acc, __shfl_xor(acc, 1));
+            if (j == 0) q_v[e] = __fsub_rn(__fsub_rn(__fmul_rn(acc, 2.0f), q_x2[fs]), a.e2[n]);
+        }
+    } else {
+        for (int e0 = 0; e0 < qcount; e0 += kWave) {
+            const int e = e0 + lane;
+            if (e < qcount) {
+                const int fs = q_f[e];
+                const int n = q_n[e];
+                const float x2 = RECIPE == HIGGS ? q_x2[fs] : 0.0f;
+                q_v[e] = exact_value_k<RECIPE, Q8, K>(a, a.xin + (m_base + fs) * K, n, x2);
+            }
         }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
