@@ -65,26 +65,6 @@ const KsKernels *kernels_for(int ks) {
 // Recipe variant index of KsKernels.
 int variant_of(int recipe, bool q8) { return q8 ? 3 : recipe; }
 
-FallbackFn pick_fb_values(int recipe, bool q8) {
-    if (q8) return recipe == HIGGS ? euclid_fb_values_kernel<HIGGS, true> : nullptr;
-    switch (recipe) {
-        case OMNI: return euclid_fb_values_kernel<OMNI, false>;
-        case HIGGS: return euclid_fb_values_kernel<HIGGS, false>;
-        case DIRECT: return euclid_fb_values_kernel<DIRECT, false>;
-        default: return nullptr;
-    }
-}
-
-FallbackFn pick_fb_select(int recipe, bool q8) {
-    if (q8) return recipe == HIGGS ? euclid_fb_select_kernel<HIGGS, true> : nullptr;
-    switch (recipe) {
-        case OMNI: return euclid_fb_select_kernel<OMNI, false>;
-        case HIGGS: return euclid_fb_select_kernel<HIGGS, false>;
-        case DIRECT: return euclid_fb_select_kernel<DIRECT, false>;
-        default: return nullptr;
-    }
-}
-
 uint16_t to_bf16(float f) {   // round to nearest even (finite inputs)
     uint32_t u;
     std::memcpy(&u, &f, 4);
@@ -306,8 +286,8 @@ aq_status aq_euclid_encode(aq_ctx *ctx, const aq_codebooks *cb, const float *x, 
     const int var = variant_of(cb->recipe, cb->q8);
     StageFn sweep = kk->sweep[cb->q8 ? 1 : 0][topl - 3];
     StageFn select = kk->select[var][topl - 3];
-    FallbackFn fvals = pick_fb_values(cb->recipe, cb->q8);
-    FallbackFn fsel = pick_fb_select(cb->recipe, cb->q8);
+    FallbackFn fvals = kk->fb_values[var];
+    FallbackFn fsel = kk->fb_select[var];
     const int lds = kk->lds;
     AQ_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void *>(sweep), hipFuncAttributeMaxDynamicSharedMemorySize, lds));
     const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;

@@ -151,6 +151,8 @@ struct KsKernels {
     StageFn select[4][2];     // [variant][topl]
     RefineFn refine_values[4];
     RefineFn refine_select[4];
+    FallbackFn fb_values[4];
+    FallbackFn fb_select[4];
     int lds;                  // sweep dynamic LDS bytes
     int cc;                   // codes per LDS chunk
 };
@@ -1153,8 +1155,8 @@ __global__ __launch_bounds__(kThreads) void euclid_select_kernel(StageArgs a) {
 // Recipe values of code n for FQ query frames held in LDS, one pass over the
 // code's row (tinyBLAS order; the vec_dot order only occurs for M == 1 and is
 // evaluated frame by frame).
-template <int RECIPE, bool Q8>
-__device__ void exact_values_fq(const StageArgs &a, int K, int n, const float *xs, const float *x2, const int8_t *xq,
+template <int RECIPE, bool Q8, int K>
+__device__ void exact_values_fq(const StageArgs &a, int n, const float *xs, const float *x2, const int8_t *xq,
                                 const float *xd, int nf, float (&out)[kFQ]) {
     const float *c = a.cbf + static_cast<int64_t>(n) * K;
     if (RECIPE == DIRECT) {
@@ -1283,8 +1285,9 @@ __device__ inline void wave_best(float &v, int &n, bool topk) {
     }
 }
 
-template <int RECIPE, bool Q8>
-__global__ __launch_bounds__(kFbChunk) void euclid_fb_values_kernel(StageArgs a, int K, FbArgs fb) {
+template <int RECIPE, bool Q8, int KS>
+__global__ __launch_bounds__(kFbChunk) void euclid_fb_values_kernel(StageArgs a, int /*K*/, FbArgs fb) {
+    constexpr int K = KS * 32;
     extern __shared__ __align__(16) unsigned char lds[];
     float *xs = reinterpret_cast<float *>(lds);                         // [kFQ][K]
     int8_t *xq = reinterpret_cast<int8_t *>(xs + kFQ * K);              // [kFQ][K]
@@ -1324,7 +1327,7 @@ __global__ __launch_bounds__(kFbChunk) void euclid_fb_values_kernel(StageArgs a,
         const bool valid = n < a.N;
         float vals[kFQ];
         if (valid) {
-            exact_values_fq<RECIPE, Q8>(a, K, n, xs, x2s, xq, xd, nf, vals);
+            exact_values_fq<RECIPE, Q8, K>(a, n, xs, x2s, xq, xd, nf, vals);
         } else {
 #pragma unroll
             for (int f = 0; f < kFQ; ++f) vals[f] = 0.0f;
@@ -1398,8 +1401,9 @@ __global__ __launch_bounds__(kFbChunk) void euclid_fb_values_kernel(StageArgs a,
 constexpr int kFbSel = 256;
 constexpr int kFbReplay = 2048;
 
-template <int RECIPE, bool Q8>
-__global__ __launch_bounds__(kFbSel) void euclid_fb_select_kernel(StageArgs a, int K, FbArgs fb) {
+template <int RECIPE, bool Q8, int KS>
+__global__ __launch_bounds__(kFbSel) void euclid_fb_select_kernel(StageArgs a, int /*K*/, FbArgs fb) {
+    constexpr int K = KS * 32;
     extern __shared__ __align__(16) unsigned char lds[];
     float *xs = reinterpret_cast<float *>(lds);                         // [K]
     int8_t *xq = reinterpret_cast<int8_t *>(xs + K);                    // [K]
@@ -1501,27 +1505,66 @@ __global__ __launch_bounds__(kFbSel) void euclid_fb_select_kernel(StageArgs a, i
             int id = 0;
             for (int base = 0; base < a.N; base += kFbReplay) {
                 const int len = min(kFbReplay, a.N - base);
-                for (int i = tid; i < len; i += kFbSel) rv[i] = exact_value<RECIPE, Q8>(a, K, xs, base + i, x2, xq, xd);
+                for (int i = tid; i < len; i += kFbSel) rv[i] = exact_value_kq<RECIPE, Q8, K>(a, xs, base + i, x2, xq, xd);
                 __syncthreads();
-                if (tid == 0) {
-                    for (int i = 0; i < len; ++i) {
-                        const int n_i = base + i;
-                        const float v = rv[i];
-                        mx = mx > v ? mx : v;
-                        if (mx == v) id = n_i;
+                if (tid < kWave) {
+                    // Wave 0 walks the codes 64 at a time.  The argmax of a
+                    // chunk without NaN is the last code equal to its largest
+                    // value (MAX keeps a later equal element); a chunk with a
+                    // NaN, or after one, is walked code by code.  The heap
+                    // takes a code only if it beats the root, so a chunk where
+                    // no code does is skipped at once.
+                    for (int c0 = 0; c0 < len; c0 += kWave) {
+                        const int i = c0 + lane;
+                        const bool in = i < len;
+                        const float v = in ? rv[i] : 0.0f;
+                        const bool nan_chunk = __any(in && v != v) || mx != mx;
+                        if (nan_chunk) {
+                            const int cl = min(kWave, len - c0);
+                            for (int t = 0; t < cl; ++t) {
+                                const float vt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), t));
+                                mx = mx > vt ? mx : vt;
+                                if (mx == vt) id = base + c0 + t;
+                            }
+                        } else {
+                            float cm = in ? v : -INFINITY;
+#pragma unroll
+                            for (int off = 1; off < kWave; off <<= 1) cm = fmaxf(cm, __shfl_xor(cm, off));
+                            const unsigned long long eq = __ballot(in && v == cm);
+                            if (eq != 0 && !(mx > cm)) {
+                                const int last = 63 - __clzll(static_cast<long long>(eq));
+                                mx = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), last));
+                                id = base + c0 + last;
+                            }
+                        }
                         if (ktop > 0) {
-                            if (n_i < ktop) {
-                                heap_n[n_i] = n_i;
-                                heap_v[n_i] = v;
-                                if (n_i == ktop - 1 && ktop >= 2)
-                                    for (int par = (ktop - 2) / 2;; --par) {
-                                        heap_adjust(heap_n, heap_v, par, ktop, heap_n[par], heap_v[par]);
-                                        if (par == 0) break;
-                                    }
-                                if (n_i == ktop - 1) root = heap_v[0];
-                            } else if (v > root) {
-                                heap_adjust(heap_n, heap_v, 0, ktop, n_i, v);
+                            // the first ktop codes build the heap
+                            for (int t = 0; t < kWave && base + c0 + t < ktop; ++t) {
+                                const int n_t = base + c0 + t;
+                                const float vt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), t));
+                                if (lane == 0) {
+                                    heap_n[n_t] = n_t;
+                                    heap_v[n_t] = vt;
+                                    if (n_t == ktop - 1 && ktop >= 2)
+                                        for (int par = (ktop - 2) / 2;; --par) {
+                                            heap_adjust(heap_n, heap_v, par, ktop, heap_n[par], heap_v[par]);
+                                            if (par == 0) break;
+                                        }
+                                }
+                                __builtin_amdgcn_wave_barrier();
+                                if (n_t == ktop - 1) root = heap_v[0];
+                            }
+                            int from = 0;   // lanes before `from` are done
+                            while (true) {
+                                const unsigned long long take =
+                                    __ballot(in && lane >= from && base + i >= ktop && v > root);
+                                if (take == 0) break;
+                                const int f = __ffsll(static_cast<long long>(take)) - 1;
+                                const float vf = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), f));
+                                if (lane == 0) heap_adjust(heap_n, heap_v, 0, ktop, base + c0 + f, vf);
+                                __builtin_amdgcn_wave_barrier();
                                 root = heap_v[0];
+                                from = f + 1;
                             }
                         }
                     }
@@ -1977,6 +2020,10 @@ __global__ __launch_bounds__(kWave) void euclid_refine_select_kernel(StageArgs a
              euclid_refine_values_kernel<DIRECT, false, KS>, euclid_refine_values_kernel<HIGGS, true, KS>},     \
             {euclid_refine_select_kernel<OMNI, false, KS>, euclid_refine_select_kernel<HIGGS, false, KS>,       \
              euclid_refine_select_kernel<DIRECT, false, KS>, euclid_refine_select_kernel<HIGGS, true, KS>},     \
+            {euclid_fb_values_kernel<OMNI, false, KS>, euclid_fb_values_kernel<HIGGS, false, KS>,               \
+             euclid_fb_values_kernel<DIRECT, false, KS>, euclid_fb_values_kernel<HIGGS, true, KS>},             \
+            {euclid_fb_select_kernel<OMNI, false, KS>, euclid_fb_select_kernel<HIGGS, false, KS>,               \
+             euclid_fb_select_kernel<DIRECT, false, KS>, euclid_fb_select_kernel<HIGGS, true, KS>},             \
             Tile<KS>::LDS,                                                                                      \
             Tile<KS>::CC};                                                                                      \
         return &t;                                                                                              \
