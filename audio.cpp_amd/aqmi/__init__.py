@@ -28,7 +28,7 @@ EXPORTED = [
     "aq_abi_version", "aq_ctx_create", "aq_ctx_destroy", "aq_ctx_set_stream", "aq_ctx_synchronize",
     "aq_last_error", "aq_dac_upload", "aq_dac_release", "aq_dac_encode", "aq_dac_decode",
     "aq_euclid_upload", "aq_euclid_release", "aq_euclid_encode", "aq_euclid_failures", "aq_euclid_exact_scans",
-    "aq_codebook_gather",
+    "aq_codebook_gather", "aq_ema_codebook", "aq_euclid_upload_ema",
     "aq_euclid_decode", "aq_ctx_set_timing", "aq_ctx_read_timing",
 ]
 
@@ -68,6 +68,8 @@ def load_library(path: str | pathlib.Path | None = None) -> C.CDLL:
     lib.aq_euclid_failures.argtypes = [vp, vp, vp]
     lib.aq_euclid_exact_scans.argtypes = [vp, vp, vp]
     lib.aq_codebook_gather.argtypes = [vp, vp, i64, vp, i64, vp]
+    lib.aq_ema_codebook.argtypes = [vp, vp, vp, i64, i64, i64, C.c_float, vp]
+    lib.aq_euclid_upload_ema.argtypes = [vp, i64, i64, i64, vp, vp, C.c_float, C.c_int, C.POINTER(vp)]
     lib.aq_euclid_decode.argtypes = [vp, vp, vp, i64, vp]
     for name in EXPORTED:
         fn = getattr(lib, name)
@@ -203,6 +205,24 @@ class Codebooks:
                                            recipe, C.byref(h)))
         self.h = h
 
+    @classmethod
+    def from_ema(cls, ctx: Context, embedding_sum, cluster_usage, recipe: int, eps: float = 1.0e-5):
+        """aq_euclid_upload_ema: codebooks materialised from EMA statistics
+        (embedding_sum [Q, N, K], cluster_usage [Q, N], host float32)."""
+        es = np.ascontiguousarray(embedding_sum, np.float32)
+        cu = np.ascontiguousarray(cluster_usage, np.float32)
+        self = cls.__new__(cls)
+        self.ctx = ctx
+        self.Q, self.N, self.K = es.shape
+        assert cu.shape == (self.Q, self.N)
+        self.recipe = recipe
+        h = C.c_void_p()
+        ctx.check(ctx.lib.aq_euclid_upload_ema(ctx.h, self.Q, self.N, self.K, es.ctypes.data_as(C.c_void_p),
+                                               cu.ctypes.data_as(C.c_void_p), eps, recipe, C.byref(h)))
+        self.h = h
+        return self
+
+
     def encode(self, x, idx, residual=None, dist=None, topk: int = 0, topk_idx=None, topk_dist=None,
                force_idx=None):
         self.ctx.use_current_stream()
@@ -241,3 +261,10 @@ class Codebooks:
             self.close()
         except Exception:
             pass
+
+
+def ema_codebook(ctx: Context, embedding_sum, cluster_usage, eps: float, out):
+    """aq_ema_codebook on device tensors: out = embedding_sum / max(usage, eps)."""
+    Q, N, K = embedding_sum.shape
+    ctx.use_current_stream()
+    ctx.check(ctx.lib.aq_ema_codebook(ctx.h, _dptr(embedding_sum), _dptr(cluster_usage), Q, N, K, eps, _dptr(out)))

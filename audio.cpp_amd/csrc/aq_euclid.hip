@@ -50,6 +50,17 @@ __global__ void decode_sum_kernel(const float *__restrict__ cbf, int Q, int64_t 
     out[t] = acc;
 }
 
+// codebook[q,n,k] = embedding_sum[q,n,k] / std::max(usage[q,n], eps): the
+// max is (u < eps) ? eps : u, so a NaN usage stays NaN; IEEE division.
+__global__ void ema_codebook_kernel(const float *__restrict__ esum, const float *__restrict__ usage, int64_t QN,
+                                    int64_t K, float eps, float *__restrict__ out) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= QN * K) return;
+    const float u = usage[t / K];
+    const float denom = u < eps ? eps : u;
+    out[t] = __fdiv_rn(esum[t], denom);
+}
+
 // --------------------------------------------------------------- dispatch
 
 const KsKernels *kernels_for(int ks) {
@@ -250,6 +261,45 @@ aq_status aq_euclid_upload(aq_ctx *ctx, int64_t Q, int64_t N, int64_t K, int cb_
     }
     *out = cb;
     return AQ_OK;
+}
+
+aq_status aq_ema_codebook(aq_ctx *ctx, const float *embedding_sum, const float *cluster_usage, int64_t Q, int64_t N,
+                          int64_t K, float eps, float *codebook) {
+    if (!ctx || !embedding_sum || !cluster_usage || !codebook)
+        return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_ema_codebook: null argument");
+    if (Q <= 0 || N <= 0 || K <= 0) return aq_fail(ctx, AQ_E_SHAPE, "aq_ema_codebook: empty shape");
+    aq_device_guard g(ctx->device);
+    const int64_t total = Q * N * K;
+    hipLaunchKernelGGL(ema_codebook_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, ctx->stream,
+                       embedding_sum, cluster_usage, Q * N, K, eps, codebook);
+    AQ_HIP(ctx, hipGetLastError());
+    return AQ_OK;
+}
+
+aq_status aq_euclid_upload_ema(aq_ctx *ctx, int64_t Q, int64_t N, int64_t K, const float *embedding_sum,
+                               const float *cluster_usage, float eps, int recipe, aq_codebooks **out) {
+    if (!ctx || !out || !embedding_sum || !cluster_usage)
+        return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_euclid_upload_ema: null argument");
+    if (Q <= 0 || N <= 0 || K <= 0) return aq_fail(ctx, AQ_E_SHAPE, "aq_euclid_upload_ema: empty shape");
+    aq_device_guard g(ctx->device);
+    const size_t QNK = static_cast<size_t>(Q * N * K), QN = static_cast<size_t>(Q * N);
+    float *d = nullptr;
+    if (hipMalloc(&d, (2 * QNK + QN) * sizeof(float)) != hipSuccess)
+        return aq_fail(ctx, AQ_E_NOMEM, "aq_euclid_upload_ema: device allocation failed");
+    std::vector<float> cb(QNK);
+    aq_status st = AQ_OK;
+    if (hipMemcpy(d, embedding_sum, QNK * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(d + QNK, cluster_usage, QN * 4, hipMemcpyHostToDevice) != hipSuccess) {
+        st = aq_fail(ctx, AQ_E_DEVICE, "aq_euclid_upload_ema: host to device copy failed");
+    } else {
+        st = aq_ema_codebook(ctx, d, d + QNK, Q, N, K, eps, d + QNK + QN);
+        if (st == AQ_OK && (hipStreamSynchronize(ctx->stream) != hipSuccess ||
+                            hipMemcpy(cb.data(), d + QNK + QN, QNK * 4, hipMemcpyDeviceToHost) != hipSuccess))
+            st = aq_fail(ctx, AQ_E_DEVICE, "aq_euclid_upload_ema: device to host copy failed");
+    }
+    (void)hipFree(d);
+    if (st != AQ_OK) return st;
+    return aq_euclid_upload(ctx, Q, N, K, AQ_CB_F32, cb.data(), recipe, out);
 }
 
 aq_status aq_euclid_release(aq_codebooks *cb) {

@@ -198,6 +198,22 @@ aq_status aq_euclid_failures(aq_ctx *ctx, const aq_codebooks *cb, int32_t *host_
  * reference counterpart. */
 aq_status aq_euclid_exact_scans(aq_ctx *ctx, const aq_codebooks *cb, int32_t *host_counts);
 
+/* EMA codebook materialisation, once at load (Mimi-style codecs store
+ * embedding_sum and cluster_usage): codebook[q,n,k] = embedding_sum[q,n,k] /
+ * std::max(cluster_usage[q,n], eps).  Replaces codebook_embedding
+ * (qwen3_tts/tokenizer_speech_encoder.cpp:271-285, called per encode there;
+ * also tokenizer_speech_decoder.cpp:205-212), whose eps is 1e-5.
+ * Device pointers: embedding_sum [Q,N,K], cluster_usage [Q,N], codebook
+ * [Q,N,K] (may not alias the inputs). */
+aq_status aq_ema_codebook(aq_ctx *ctx, const float *embedding_sum, const float *cluster_usage, int64_t Q, int64_t N,
+                          int64_t K, float eps, float *codebook);
+
+/* aq_euclid_upload of an EMA codebook: host embedding_sum [Q,N,K] and
+ * cluster_usage [Q,N] are materialised on the device with aq_ema_codebook's
+ * arithmetic, then prepared as an F32 codebook for `recipe`. */
+aq_status aq_euclid_upload_ema(aq_ctx *ctx, int64_t Q, int64_t N, int64_t K, const float *embedding_sum,
+                               const float *cluster_usage, float eps, int recipe, aq_codebooks **out);
+
 /* Codebook gather of one stage: out[m] = codebook[stage][idx[m]] (ggml_get_rows,
  * lookup_modules.cpp:88-112,182-187; Q8_0 rows dequantised as q*d).
  * idx device [M], out device [M, K].  Out-of-range codes -> AQ_E_INDEX_RANGE. */

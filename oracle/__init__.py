@@ -93,6 +93,8 @@ class Oracle:
         L.aqo_gather_f32.argtypes = [_f32p, _i64, _i64, _i32p, _i64, _f32p]
         L.aqo_gather_q8_0.restype = C.c_int
         L.aqo_gather_q8_0.argtypes = [C.c_void_p, _i64, _i64, _i32p, _i64, _f32p]
+        L.aqo_ema_codebook.restype = C.c_int
+        L.aqo_ema_codebook.argtypes = [_f32p, _f32p, _i64, _i64, _i64, C.c_float, _f32p]
 
     # -- whole path --------------------------------------------------------
     def dac_rvq(self, cfg: dict, force_idx=None, recon: bool = True):
@@ -140,6 +142,16 @@ class Oracle:
                                      dist.ctypes.data_as(C.c_void_p))
         assert rc == 0
         return dict(idx=idx, residual=res, dist=dist)
+
+    def ema_codebook(self, embedding_sum, cluster_usage, eps: float = 1.0e-5):
+        """codebook_embedding: sum / std::max(usage, eps), per stage [Q, N, K]."""
+        es = np.ascontiguousarray(embedding_sum, np.float32)
+        cu = np.ascontiguousarray(cluster_usage, np.float32)
+        Q, N, K = es.shape
+        assert cu.shape == (Q, N)
+        out = np.zeros_like(es)
+        assert self.lib.aqo_ema_codebook(es, cu, Q, N, K, eps, out) == 0
+        return out
 
     def top_k(self, v, k: int):
         """aqo_top_k_f32 over the rows of v."""

@@ -504,3 +504,17 @@ int aqo_gather_q8_0(const aqo_block_q8_0 *cb, int64_t N, int64_t K, const int32_
     }
     return 0;
 }
+
+/* codebook_embedding (src/models/qwen3_tts/tokenizer_speech_encoder.cpp:271-285;
+ * the decoder's copy at tokenizer_speech_decoder.cpp:205-212): per code,
+ * denom = std::max(usage, eps), i.e. (usage < eps) ? eps : usage (a NaN usage
+ * stays NaN), then one fp32 division per element. */
+int aqo_ema_codebook(const float *embedding_sum, const float *cluster_usage, int64_t Q, int64_t N, int64_t K,
+                     float eps, float *cb) {
+    for (int64_t qn = 0; qn < Q * N; ++qn) {
+        const float u = cluster_usage[qn];
+        const float denom = (u < eps) ? eps : u;
+        for (int64_t k = 0; k < K; ++k) cb[qn * K + k] = embedding_sum[qn * K + k] / denom;
+    }
+    return 0;
+}

@@ -78,6 +78,11 @@ int aqo_direct_rvq(const float *x, int64_t M, int64_t K, int64_t Q, int64_t N, c
 /* Codebook gather (get_rows, ops.cpp:4923-4962 / 4797-4840). Returns -1 on an
  * out-of-range index (the reference asserts). */
 int aqo_gather_f32(const float *cb, int64_t N, int64_t K, const int32_t *idx, int64_t M, float *out);
+
+/* EMA codebook materialisation (Mimi / Qwen3 speech tokenizer):
+ * cb[q,n,k] = embedding_sum[q,n,k] / std::max(cluster_usage[q,n], eps). */
+int aqo_ema_codebook(const float *embedding_sum, const float *cluster_usage, int64_t Q, int64_t N, int64_t K,
+                     float eps, float *cb);
 int aqo_gather_q8_0(const aqo_block_q8_0 *cb, int64_t N, int64_t K, const int32_t *idx, int64_t M, float *out);
 
 #ifdef __cplusplus

@@ -320,3 +320,41 @@ def test_topk_tie_at_kth_place_follows_ggml_heap(torch, ctx, oracle, cb_type):
     assert np.array_equal(bits(out["residual"]), bits(ref["residual"]))
     check_topk(out, ref)
     assert out["fails"][0] == M
+
+
+def test_ema_codebook_and_upload(torch, ctx, oracle):
+    """aq_ema_codebook bit for bit against the oracle (usage below eps, zero,
+    NaN), and aq_euclid_upload_ema encoding exactly like an upload of the
+    oracle's materialised codebook (Qwen3's nearest_code: DIRECT recipe)."""
+    import aqmi
+
+    print("[gpu] ema codebook", flush=True)
+    rng = np.random.default_rng(11)
+    Q, N, K, M = 3, 2048, 256, 257
+    es = (rng.standard_normal((Q, N, K)) * 4.0).astype(np.float32)
+    cu = rng.uniform(1.0, 30.0, (Q, N)).astype(np.float32)
+    cu[0, :4] = [0.0, 1e-7, -1.0, 1e-5]
+    want = oracle.ema_codebook(es, cu, 1e-5)
+    d_es = torch.from_numpy(es).cuda()
+    d_cu = torch.from_numpy(cu).cuda()
+    d_out = torch.empty_like(d_es)
+    aqmi.ema_codebook(ctx, d_es, d_cu, 1e-5, d_out)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(d_out.cpu().numpy()), bits(want))
+    cu_nan = cu.copy()
+    cu_nan[1, 7] = np.nan
+    aqmi.ema_codebook(ctx, d_es, torch.from_numpy(cu_nan).cuda(), 1e-5, d_out)
+    torch.cuda.synchronize()
+    got = d_out.cpu().numpy()
+    assert np.isnan(got[1, 7]).all() and np.array_equal(bits(np.delete(got[1], 7, 0)), bits(np.delete(want[1], 7, 0)))
+
+    x = (rng.standard_normal((M, K)) * 4.0).astype(np.float32)
+    cbs = aqmi.Codebooks.from_ema(ctx, es, cu, aqmi.DIRECT)
+    xd = torch.from_numpy(x).cuda()
+    idx = torch.full((M, Q), -1, dtype=torch.int32, device="cuda")
+    res = torch.empty((M, K), dtype=torch.float32, device="cuda")
+    cbs.encode(xd, idx, res)
+    torch.cuda.synchronize()
+    ref = oracle.direct_rvq(dict(x=x, M=M, K=K, Q=Q, N=N, codebook=want))
+    assert np.array_equal(idx.cpu().numpy(), ref["idx"])
+    assert np.array_equal(bits(res.cpu().numpy()), bits(ref["residual"]))

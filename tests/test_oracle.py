@@ -349,3 +349,35 @@ def test_oracle_direct_first_index_on_ties(o, ref):
 def test_reference_vector_quantizer_size_check(ref):
     with pytest.raises(RuntimeError):
         ref.vector_quantizer(np.zeros((4, 8), np.float32), np.zeros((3, 7), np.float32))
+
+
+def test_ema_codebook_closed_form(o):
+    """codebook_embedding (qwen3_tts/tokenizer_speech_encoder.cpp:271-285):
+    sum / std::max(usage, 1e-5).  Pinned by the format's special cases:
+    usage 1 is the identity, usage below eps (0, negative, subnormal) divides
+    by eps, a NaN usage stays NaN (std::max keeps its first argument when the
+    comparison is false), and otherwise out * usage recovers sum to within
+    one rounding of each operation."""
+    rng = np.random.default_rng(5)
+    Q, N, K = 2, 16, 8
+    es = rng.standard_normal((Q, N, K)).astype(np.float32)
+    cu = rng.uniform(0.5, 100.0, (Q, N)).astype(np.float32)
+    cu[0, 0] = 1.0
+    cu[0, 1] = 0.0
+    cu[0, 2] = -3.0
+    cu[0, 3] = 1e-40
+    cu[0, 4] = np.nan
+    cu[0, 5] = 1e-5
+    cu[0, 6] = np.inf
+    out = o.ema_codebook(es, cu, 1e-5)
+    assert np.array_equal(out[0, 0], es[0, 0])
+    eps = np.float32(1e-5)
+    for n in (1, 2, 3, 5):
+        assert np.array_equal(out[0, n], es[0, n] / eps)
+    assert np.isnan(out[0, 4]).all()
+    assert np.array_equal(out[0, 6], es[0, 6] / np.float32(np.inf))
+    rest = np.ones((Q, N), bool)
+    rest[0, :7] = False
+    back = (out * cu[:, :, None]).astype(np.float64)
+    err = np.abs(back - es) / np.maximum(np.abs(es), 1e-30)
+    assert (err[rest] <= 2.5 * 2.0 ** -24).all()
