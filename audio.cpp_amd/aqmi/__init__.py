@@ -26,7 +26,7 @@ STATUS_NAMES = {
 # Every symbol include/aq_mi355x.h declares (checked by the CPU test suite).
 EXPORTED = [
     "aq_abi_version", "aq_ctx_create", "aq_ctx_destroy", "aq_ctx_set_stream", "aq_ctx_synchronize",
-    "aq_last_error", "aq_dac_upload", "aq_dac_release", "aq_dac_encode", "aq_dac_decode",
+    "aq_last_error", "aq_dac_upload", "aq_dac_upload_ex", "aq_dac_release", "aq_dac_encode", "aq_dac_decode",
     "aq_euclid_upload", "aq_euclid_release", "aq_euclid_encode", "aq_euclid_failures", "aq_euclid_exact_scans",
     "aq_codebook_gather", "aq_ema_codebook", "aq_euclid_upload_ema",
     "aq_euclid_decode", "aq_ctx_set_timing", "aq_ctx_read_timing",
@@ -34,6 +34,8 @@ EXPORTED = [
 
 # aq_euclid_recipe / aq_codebook_type
 OMNIVOICE, HIGGS, DIRECT = 0, 1, 2
+# aq_dac_recipe
+DAC_FISH, DAC_INDEXTTS2, DAC_VEVO2 = 0, 1, 2
 CB_F32, CB_Q8_0 = 0, 1
 
 
@@ -57,6 +59,7 @@ def load_library(path: str | pathlib.Path | None = None) -> C.CDLL:
     lib.aq_last_error.restype = C.c_char_p
     lib.aq_last_error.argtypes = [vp]
     lib.aq_dac_upload.argtypes = [vp, i64, i64, i64, vp, vp, vp, vp, vp, C.POINTER(vp)]
+    lib.aq_dac_upload_ex.argtypes = [vp, i64, i64, i64, vp, vp, vp, vp, vp, C.c_int, C.POINTER(vp)]
     lib.aq_dac_release.argtypes = [vp]
     lib.aq_dac_encode.argtypes = [vp, vp, vp, i64, i64, vp, vp, vp, vp]
     lib.aq_dac_decode.argtypes = [vp, vp, vp, i64, vp]
@@ -144,20 +147,23 @@ class Context:
 
 
 class DacStages:
-    """Uploaded DAC RVQ weights (aq_dac_upload)."""
+    """Uploaded DAC RVQ weights (aq_dac_upload_ex).  recipe: DAC_FISH,
+    DAC_INDEXTTS2 or DAC_VEVO2 (query / codebook normalisation); w_out None
+    uploads a codes-only single stage."""
 
-    def __init__(self, ctx: Context, w_in, b_in, codebook, w_out, b_out):
+    def __init__(self, ctx: Context, w_in, b_in, codebook, w_out, b_out, recipe: int = 0):
         self.ctx = ctx
         w_in = np.ascontiguousarray(w_in, np.float32)
         cb = np.ascontiguousarray(codebook, np.float32)
-        w_out = np.ascontiguousarray(w_out, np.float32)
+        w_out = None if w_out is None else np.ascontiguousarray(w_out, np.float32)
         b_in = None if b_in is None else np.ascontiguousarray(b_in, np.float32)
         b_out = None if b_out is None else np.ascontiguousarray(b_out, np.float32)
         self.Q, _, self.D = w_in.shape
         self.N = cb.shape[1]
+        self.recipe = recipe
         h = C.c_void_p()
-        ctx.check(ctx.lib.aq_dac_upload(ctx.h, self.Q, self.D, self.N, _host_ptr(w_in), _host_ptr(b_in), _host_ptr(cb),
-                                        _host_ptr(w_out), _host_ptr(b_out), C.byref(h)))
+        ctx.check(ctx.lib.aq_dac_upload_ex(ctx.h, self.Q, self.D, self.N, _host_ptr(w_in), _host_ptr(b_in),
+                                           _host_ptr(cb), _host_ptr(w_out), _host_ptr(b_out), recipe, C.byref(h)))
         self.h = h
 
     def encode(self, x, clip_len: int, idx, residual=None, recon=None, force_idx=None):

@@ -103,11 +103,15 @@ __device__ inline float wave_max(float v) {
     return v;
 }
 
-// Per-stage LDS image (units of float4):
+// Per-stage image (units of float4), staged in LDS:
 //   [0, 2*DI*64)           W_in : float4 (i*2 + q)*64 + L = W_in[4q .. 4q+3][64 i + L]
-//   [.., + 2*(N/64)*64)    c_hat: float4 (c*2 + q)*64 + L = c_hat[64 c + L][4q .. 4q+3]
 //   [.., + 2)              b_in[0..7]
-inline int64_t image_f4(int64_t D, int64_t N) { return 2 * D + 2 * N + 2; }
+//   [.., + 2*(N/64)*64)    c_hat: float4 (c*2 + q)*64 + L = c_hat[64 c + L][4q .. 4q+3]
+// When W_in and c_hat do not fit in LDS together (large codebooks), only the
+// prefix W_in + b_in is staged and c_hat is read from global memory (L2), in
+// the same lane-major layout (coalesced 1 KB per wave load).
+inline int64_t image_f4(int64_t D, int64_t N) { return 2 * D + 2 + 2 * N; }
+inline int64_t image_prefix_f4(int64_t D) { return 2 * D + 2; }
 
 // ggml's cosine score of code n (scalar leftovers of ggml_vec_dot_f32 with
 // k = 8: each product rounded, then added in order).
@@ -174,6 +178,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));   // native vector: sta
 
 template <int PF>
 __device__ inline void fetch_image(f32x4 (&pre)[PF > 0 ? PF : 1], const float4 *__restrict__ img, int64_t img_f4) {
+    // img_f4: the float4 staged in LDS (a prefix of the stage image)
     const f32x4 *src = reinterpret_cast<const f32x4 *>(img);
 #pragma unroll
     for (int k = 0; k < PF; ++k) {
@@ -182,12 +187,14 @@ __device__ inline void fetch_image(f32x4 (&pre)[PF > 0 ? PF : 1], const float4 *
     }
 }
 
-template <int DI, int FW, bool RECON, int PF>
+template <int DI, int FW, bool RECON, int PF, bool CBG>
 __global__ __launch_bounds__(kMaxBlock, 1) void dac_encode_kernel(
-    const float *__restrict__ x, int64_t M, int Q, int N, const float4 *__restrict__ images, int64_t img_f4,
-    const float *__restrict__ tables, int32_t *__restrict__ idx, float *__restrict__ residual,
+    const float *__restrict__ x, int64_t M, int Q, int N, const float4 *__restrict__ images, int64_t stride_f4,
+    int64_t img_f4, const float *__restrict__ tables, int32_t *__restrict__ idx, float *__restrict__ residual,
     float *__restrict__ recon, const int32_t *__restrict__ force_idx, int32_t *__restrict__ flags, int has_bin,
-    int key_bits, float margin, int exact_only) {
+    int key_bits, float margin, int exact_only, float qeps) {
+    // stride_f4: float4 per stage image; img_f4: the prefix staged in LDS
+    // (the whole image, or W_in + b_in when CBG reads c_hat from memory).
     extern __shared__ float4 lds[];
     constexpr int D = DI * kWave;
     const int lane = threadIdx.x & (kWave - 1);
@@ -211,8 +218,7 @@ __global__ __launch_bounds__(kMaxBlock, 1) void dac_encode_kernel(
     }
 
     const float4 *win = lds;
-    const float4 *chat = lds + 2 * DI * kWave;
-    const float *bin = reinterpret_cast<const float *>(lds + 2 * DI * kWave + 2 * N);
+    const float *bin = reinterpret_cast<const float *>(lds + 2 * DI * kWave);
     const int NC = N / kWave;
     const int key_mask = (1 << key_bits) - 1;
 
@@ -229,7 +235,7 @@ __global__ __launch_bounds__(kMaxBlock, 1) void dac_encode_kernel(
                 if (t < img_f4) lds4[t] = pre[k];
             }
         } else {
-            const float4 *img = images + static_cast<int64_t>(s) * img_f4;
+            const float4 *img = images + static_cast<int64_t>(s) * stride_f4;
             for (int64_t t0 = 0; t0 < img_f4; t0 += static_cast<int64_t>(kCopyBatch) * blockDim.x) {
                 float4 buf[kCopyBatch];
 #pragma unroll
@@ -245,7 +251,9 @@ __global__ __launch_bounds__(kMaxBlock, 1) void dac_encode_kernel(
             }
         }
         __syncthreads();
-        if (PF > 0 && s + 1 < Q) fetch_image<PF>(pre, images + static_cast<int64_t>(s + 1) * img_f4, img_f4);
+        if (PF > 0 && s + 1 < Q) fetch_image<PF>(pre, images + static_cast<int64_t>(s + 1) * stride_f4, img_f4);
+        const float4 *chat = CBG ? images + static_cast<int64_t>(s) * stride_f4 + 2 * DI * kWave + 2
+                                 : lds + 2 * DI * kWave + 2;
 
         // ---- in-projection: one FMA chain per lane and output, ggml order ----
         float acc[FW][8];
@@ -328,7 +336,9 @@ __global__ __launch_bounds__(kMaxBlock, 1) void dac_encode_kernel(
                 const float po = __int_as_float(__builtin_amdgcn_readlane(__float_as_int((o & 1) ? pb : pa), 16 * (o >> 1)));
                 ss += static_cast<double>(__fmul_rn(po, po));
             }
-            const float den = sqrt_rn(__fadd_rn(static_cast<float>(ss), 1.0e-12f));
+            // ggml_scale_bias(sum, 1, eps): 1e-12 (Fish), 1e-20 (Vevo2), none
+            // (IndexTTS2: qeps = 0, and sum + 0 == sum for a sum >= +0)
+            const float den = sqrt_rn(__fadd_rn(static_cast<float>(ss), qeps));
             const float qa = __fdiv_rn(pa, den);
             const float qb = __fdiv_rn(pb, den);
             finite[f] = __all(((qa - qa) == 0.0f) && ((qb - qb) == 0.0f));
@@ -391,6 +401,7 @@ __global__ __launch_bounds__(kMaxBlock, 1) void dac_encode_kernel(
                     use = 0;
                 }
             }
+            if (!tables) continue;   // codes only: no out-projection was uploaded
             const float *zrow = tables + (static_cast<int64_t>(s) * N + use) * D;
 #pragma unroll
             for (int i = 0; i < DI; ++i) {
@@ -449,38 +460,41 @@ __global__ void dac_decode_kernel(const int32_t *__restrict__ idx, int64_t M, in
     out[t] = acc;
 }
 
-using EncodeFn = void (*)(const float *, int64_t, int, int, const float4 *, int64_t, const float *, int32_t *,
-                          float *, float *, const int32_t *, int32_t *, int, int, float, int);
+using EncodeFn = void (*)(const float *, int64_t, int, int, const float4 *, int64_t, int64_t, const float *, int32_t *,
+                          float *, float *, const int32_t *, int32_t *, int, int, float, int, float);
 
 constexpr int kPrefetch = 12;   // float4 per thread in the prefetching variant
 
+// Variants: image copied at each stage start, prefetched a stage ahead, or
+// (large codebooks) the W_in + b_in prefix prefetched with c_hat in memory.
 template <int DI, int FW, bool RECON>
-EncodeFn pick_pf(bool prefetch) {
-    return prefetch ? dac_encode_kernel<DI, FW, RECON, kPrefetch> : dac_encode_kernel<DI, FW, RECON, 0>;
+EncodeFn pick_pf(bool prefetch, bool cbg) {
+    if (cbg) return dac_encode_kernel<DI, FW, RECON, kPrefetch, true>;
+    return prefetch ? dac_encode_kernel<DI, FW, RECON, kPrefetch, false> : dac_encode_kernel<DI, FW, RECON, 0, false>;
 }
 
 template <int DI, int FW>
-EncodeFn pick_recon(bool recon, bool prefetch) {
-    return recon ? pick_pf<DI, FW, true>(prefetch) : pick_pf<DI, FW, false>(prefetch);
+EncodeFn pick_recon(bool recon, bool prefetch, bool cbg) {
+    return recon ? pick_pf<DI, FW, true>(prefetch, cbg) : pick_pf<DI, FW, false>(prefetch, cbg);
 }
 
 template <int DI>
-EncodeFn pick_fw(int fw, bool recon, bool prefetch) {
+EncodeFn pick_fw(int fw, bool recon, bool prefetch, bool cbg) {
     switch (fw) {
-        case 1: return pick_recon<DI, 1>(recon, prefetch);
-        case 2: return pick_recon<DI, 2>(recon, prefetch);
-        default: return pick_recon<DI, 3>(recon, prefetch);
+        case 1: return pick_recon<DI, 1>(recon, prefetch, cbg);
+        case 2: return pick_recon<DI, 2>(recon, prefetch, cbg);
+        default: return pick_recon<DI, 3>(recon, prefetch, cbg);
     }
 }
 
-EncodeFn pick_kernel(int64_t D, int fw, bool recon, bool prefetch) {
+EncodeFn pick_kernel(int64_t D, int fw, bool recon, bool prefetch, bool cbg) {
     switch (D / kWave) {
-        case 1: return pick_fw<1>(fw, recon, prefetch);
-        case 2: return pick_fw<2>(fw, recon, prefetch);
-        case 4: return pick_fw<4>(fw, recon, prefetch);
-        case 8: return pick_fw<8>(fw, recon, prefetch);
-        case 12: return pick_fw<12>(fw, recon, prefetch);
-        case 16: return pick_fw<16>(fw, recon, prefetch);
+        case 1: return pick_fw<1>(fw, recon, prefetch, cbg);
+        case 2: return pick_fw<2>(fw, recon, prefetch, cbg);
+        case 4: return pick_fw<4>(fw, recon, prefetch, cbg);
+        case 8: return pick_fw<8>(fw, recon, prefetch, cbg);
+        case 12: return pick_fw<12>(fw, recon, prefetch, cbg);
+        case 16: return pick_fw<16>(fw, recon, prefetch, cbg);
         default: return nullptr;
     }
 }
@@ -503,7 +517,7 @@ struct Shape {
     bool prefetch = false;
 };
 
-Shape launch_shape(int64_t M, int64_t D, int64_t img_f4, bool recon, int num_cus, size_t lds_bytes) {
+Shape launch_shape(int64_t M, int64_t D, int64_t img_f4, bool recon, int num_cus, size_t lds_bytes, bool cbg) {
     const int64_t cus = num_cus > 0 ? num_cus : 256;
     int env_fw = 0, env_wpb = 0;
     if (const char *e = std::getenv("AQ_DAC_FW")) env_fw = std::atoi(e);
@@ -516,9 +530,10 @@ Shape launch_shape(int64_t M, int64_t D, int64_t img_f4, bool recon, int num_cus
             if (env_wpb && wpb != env_wpb) continue;
             bool prefetch = (img_f4 + wpb * kWave - 1) / (wpb * kWave) <= kPrefetch;
             if (const char *e = std::getenv("AQ_DAC_PF")) prefetch = prefetch && std::atoi(e) != 0;
+            if (cbg && !prefetch) continue;   // the in-memory codebook variant always prefetches
             hipFuncAttributes attr{};
             int64_t simd_waves = 8;
-            if (hipFuncGetAttributes(&attr, reinterpret_cast<const void *>(pick_kernel(D, fw, recon, prefetch))) ==
+            if (hipFuncGetAttributes(&attr, reinterpret_cast<const void *>(pick_kernel(D, fw, recon, prefetch, cbg))) ==
                     hipSuccess && attr.numRegs > 0)
                 simd_waves = std::min<int64_t>(8, 512 / ((attr.numRegs + 7) / 8 * 8));
             // The block must fit on a CU at all (waves per SIMD by registers,
@@ -548,6 +563,10 @@ Shape launch_shape(int64_t M, int64_t D, int64_t img_f4, bool recon, int num_cus
 struct aq_dac_stages {
     aq_ctx *ctx = nullptr;
     int64_t Q = 0, D = 0, N = 0;
+    int recipe = AQ_DAC_FISH;
+    float qeps = 1.0e-12f;        // ggml_scale_bias bias before the query norm's sqrt
+    bool cbg = false;             // c_hat read from memory (does not fit in LDS with W_in)
+    int64_t lds_f4 = 0;           // float4 of each stage image staged in LDS
     bool has_bin = false;
     bool exact_only = false;      // a normalised codebook entry is not finite
     int key_bits = 0;             // chunk-index bits in the score keys
@@ -561,19 +580,33 @@ extern "C" {
 
 aq_status aq_dac_upload(aq_ctx *ctx, int64_t Q, int64_t D, int64_t N, const float *w_in, const float *b_in,
                         const float *codebook, const float *w_out, const float *b_out, aq_dac_stages **out) {
-    if (!ctx || !out || !w_in || !codebook || !w_out) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_dac_upload: null argument");
+    return aq_dac_upload_ex(ctx, Q, D, N, w_in, b_in, codebook, w_out, b_out, AQ_DAC_FISH, out);
+}
+
+aq_status aq_dac_upload_ex(aq_ctx *ctx, int64_t Q, int64_t D, int64_t N, const float *w_in, const float *b_in,
+                           const float *codebook, const float *w_out, const float *b_out, int recipe,
+                           aq_dac_stages **out) {
+    if (!ctx || !out || !w_in || !codebook) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_dac_upload: null argument");
     *out = nullptr;
-    if (Q <= 0 || D <= 0 || N <= 0 || D % kWave != 0 || N % kWave != 0 || !pick_kernel(D, 1, false, false))
+    if (recipe < AQ_DAC_FISH || recipe > AQ_DAC_VEVO2)
+        return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_dac_upload: unknown recipe %d", recipe);
+    if (!w_out && Q != 1)
+        return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_dac_upload: a residual cascade (Q=%lld) needs the out-projection",
+                       (long long)Q);
+    if (Q <= 0 || D <= 0 || N <= 0 || D % kWave != 0 || N % kWave != 0 || !pick_kernel(D, 1, false, false, false))
         return aq_fail(ctx, AQ_E_SHAPE, "aq_dac_upload: unsupported shape Q=%lld D=%lld N=%lld (D in {64,128,256,512,768,1024}, N multiple of 64)",
                        (long long)Q, (long long)D, (long long)N);
     const int64_t img = image_f4(D, N);
-    if (img * 16 > 160 * 1024)
-        return aq_fail(ctx, AQ_E_SHAPE, "aq_dac_upload: D=%lld N=%lld exceeds the LDS budget", (long long)D, (long long)N);
+    const bool cbg = img * 16 > 160 * 1024;
+    if (N > (int64_t{1} << 20))
+        return aq_fail(ctx, AQ_E_SHAPE, "aq_dac_upload: N=%lld exceeds 2^20", (long long)N);
     aq_device_guard g(ctx->device);
 
-    // Host-side layout of the per-stage LDS images.  c_hat follows
-    // normalized_rows (codec.cpp:171-189): double sum of squares, float
-    // inverse 1/sqrt, float product.
+    // Host-side layout of the per-stage images.  c_hat follows the recipe's
+    // codebook normalisation (all: double sum of squares, float products):
+    //   Fish      inv = sum > 0 ? (float)(1 / sqrt(sum)) : 0   (fish_audio/codec.cpp:171-189)
+    //   IndexTTS2 inv = 1.0F / (float)sqrt(sum)               (index_tts2/semantic_codec.cpp:43-58)
+    //   Vevo2     inv = (float)(1 / sqrt(sum)), zero rows rejected (vevo2/components.cpp:566-590)
     std::vector<float> images(static_cast<size_t>(Q * img * 4), 0.0f);
     bool any_nonfinite = false;
     for (int64_t s = 0; s < Q; ++s) {
@@ -584,12 +617,25 @@ aq_status aq_dac_upload(aq_ctx *ctx, int64_t Q, int64_t D, int64_t N, const floa
                 for (int L = 0; L < kWave; ++L)
                     for (int t = 0; t < 4; ++t)
                         im[((i * 2 + q) * kWave + L) * 4 + t] = Wi[(4 * q + t) * D + i * kWave + L];
-        float *ch = im + 2 * D * 4;
+        float *bi = im + 2 * D * 4;
+        for (int j = 0; j < 8; ++j) bi[j] = b_in ? b_in[s * 8 + j] : 0.0f;
+        float *ch = im + (2 * D + 2) * 4;
         const float *C = codebook + s * N * 8;
         for (int64_t n = 0; n < N; ++n) {
             double sum = 0.0;
             for (int k = 0; k < 8; ++k) sum += static_cast<double>(C[n * 8 + k]) * static_cast<double>(C[n * 8 + k]);
-            const float inv = sum > 0.0 ? static_cast<float>(1.0 / std::sqrt(sum)) : 0.0f;
+            float inv;
+            if (recipe == AQ_DAC_INDEXTTS2) {
+                inv = 1.0f / static_cast<float>(std::sqrt(sum));
+            } else if (recipe == AQ_DAC_VEVO2) {
+                const double norm = std::sqrt(sum);
+                if (norm == 0.0)
+                    return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_dac_upload: codebook row %lld of stage %lld has zero norm",
+                                   (long long)n, (long long)s);
+                inv = static_cast<float>(1.0 / norm);
+            } else {
+                inv = sum > 0.0 ? static_cast<float>(1.0 / std::sqrt(sum)) : 0.0f;
+            }
             const int64_t c = n / kWave, L = n % kWave;
             for (int q = 0; q < 2; ++q)
                 for (int t = 0; t < 4; ++t) {
@@ -598,8 +644,6 @@ aq_status aq_dac_upload(aq_ctx *ctx, int64_t Q, int64_t D, int64_t N, const floa
                     if (!std::isfinite(v)) any_nonfinite = true;
                 }
         }
-        float *bi = im + (2 * D + 2 * N) * 4;
-        for (int j = 0; j < 8; ++j) bi[j] = b_in ? b_in[s * 8 + j] : 0.0f;
     }
 
     aq_dac_stages *st = new (std::nothrow) aq_dac_stages();
@@ -610,6 +654,10 @@ aq_status aq_dac_upload(aq_ctx *ctx, int64_t Q, int64_t D, int64_t N, const floa
     st->N = N;
     st->has_bin = b_in != nullptr;
     st->exact_only = any_nonfinite;
+    st->recipe = recipe;
+    st->qeps = recipe == AQ_DAC_INDEXTTS2 ? 0.0f : (recipe == AQ_DAC_VEVO2 ? 1.0e-20f : 1.0e-12f);
+    st->cbg = cbg;
+    st->lds_f4 = cbg ? image_prefix_f4(D) : img;
     // Certificate margin: each approximate score (FMA chain) and ggml's score
     // (rounded products, sequential sum) are within 8u and 15u of the exact
     // dot of two vectors of norm <= 1 (u = 2^-24): 2 * 23u = 2.8e-6 for the
@@ -629,19 +677,21 @@ aq_status aq_dac_upload(aq_ctx *ctx, int64_t Q, int64_t D, int64_t N, const floa
         if (d_bout) (void)hipFree(d_bout);
     };
     if (hipMalloc(&st->d_images, images.size() * sizeof(float)) != hipSuccess ||
-        hipMalloc(&st->d_tables, sizeof(float) * static_cast<size_t>(Q * N * D)) != hipSuccess ||
-        hipMalloc(&d_cb, sizeof(float) * static_cast<size_t>(Q * N * 8)) != hipSuccess ||
-        hipMalloc(&d_wout, sizeof(float) * static_cast<size_t>(Q * D * 8)) != hipSuccess ||
-        (b_out && hipMalloc(&d_bout, sizeof(float) * static_cast<size_t>(Q * D)) != hipSuccess)) {
+        (w_out && (hipMalloc(&st->d_tables, sizeof(float) * static_cast<size_t>(Q * N * D)) != hipSuccess ||
+                   hipMalloc(&d_cb, sizeof(float) * static_cast<size_t>(Q * N * 8)) != hipSuccess ||
+                   hipMalloc(&d_wout, sizeof(float) * static_cast<size_t>(Q * D * 8)) != hipSuccess ||
+                   (b_out && hipMalloc(&d_bout, sizeof(float) * static_cast<size_t>(Q * D)) != hipSuccess)))) {
         cleanup();
         aq_dac_release(st);
         return aq_fail(ctx, AQ_E_NOMEM, "aq_dac_upload: device allocation failed");
     }
-    bool ok = hipMemcpyAsync(st->d_images, images.data(), images.size() * sizeof(float), hipMemcpyHostToDevice, ctx->stream) == hipSuccess &&
-              hipMemcpyAsync(d_cb, codebook, sizeof(float) * static_cast<size_t>(Q * N * 8), hipMemcpyHostToDevice, ctx->stream) == hipSuccess &&
-              hipMemcpyAsync(d_wout, w_out, sizeof(float) * static_cast<size_t>(Q * D * 8), hipMemcpyHostToDevice, ctx->stream) == hipSuccess &&
-              (!b_out || hipMemcpyAsync(d_bout, b_out, sizeof(float) * static_cast<size_t>(Q * D), hipMemcpyHostToDevice, ctx->stream) == hipSuccess);
-    for (int64_t s = 0; ok && s < Q; ++s) {
+    bool ok = hipMemcpyAsync(st->d_images, images.data(), images.size() * sizeof(float), hipMemcpyHostToDevice, ctx->stream) == hipSuccess;
+    if (w_out)
+        ok = ok &&
+             hipMemcpyAsync(d_cb, codebook, sizeof(float) * static_cast<size_t>(Q * N * 8), hipMemcpyHostToDevice, ctx->stream) == hipSuccess &&
+             hipMemcpyAsync(d_wout, w_out, sizeof(float) * static_cast<size_t>(Q * D * 8), hipMemcpyHostToDevice, ctx->stream) == hipSuccess &&
+             (!b_out || hipMemcpyAsync(d_bout, b_out, sizeof(float) * static_cast<size_t>(Q * D), hipMemcpyHostToDevice, ctx->stream) == hipSuccess);
+    for (int64_t s = 0; ok && w_out && s < Q; ++s) {
         const int64_t total = N * D;
         const unsigned blocks = static_cast<unsigned>((total + 255) / 256);
         hipLaunchKernelGGL(dac_table_kernel, dim3(blocks), dim3(256), 0, ctx->stream, d_cb + s * N * 8, d_wout + s * D * 8,
@@ -680,11 +730,13 @@ aq_status aq_dac_encode(aq_ctx *ctx, const aq_dac_stages *st, const float *x, in
     if (clip_len % 4 == 0)
         return aq_fail(ctx, AQ_E_UNSUPPORTED,
                        "aq_dac_encode: clip_len %% 4 == 0 selects ggml's tinyBLAS in-projection order, not built yet");
+    if (!st->d_tables && (residual || recon))
+        return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_dac_encode: no out-projection was uploaded (codes only)");
     aq_device_guard g(ctx->device);
-    const size_t lds_bytes = static_cast<size_t>(st->img_f4) * sizeof(float4);
-    const Shape shape = launch_shape(M, st->D, st->img_f4, recon != nullptr, ctx->num_cus, lds_bytes);
+    const size_t lds_bytes = static_cast<size_t>(st->lds_f4) * sizeof(float4);
+    const Shape shape = launch_shape(M, st->D, st->lds_f4, recon != nullptr, ctx->num_cus, lds_bytes, st->cbg);
     const int fw = shape.fw;
-    EncodeFn fn = pick_kernel(st->D, fw, recon != nullptr, shape.prefetch);
+    EncodeFn fn = pick_kernel(st->D, fw, recon != nullptr, shape.prefetch, st->cbg);
     AQ_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void *>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
                                     static_cast<int>(lds_bytes)));
     if (force_idx) AQ_HIP(ctx, hipMemsetAsync(ctx->d_flags, 0, sizeof(int32_t) * AQ_FLAG_COUNT, ctx->stream));
@@ -692,8 +744,9 @@ aq_status aq_dac_encode(aq_ctx *ctx, const aq_dac_stages *st, const float *x, in
     const unsigned blocks = static_cast<unsigned>((M + frames_per_block - 1) / frames_per_block);
     const int tslot = aq_timing_start(ctx);
     hipLaunchKernelGGL(fn, dim3(blocks), dim3(shape.waves_per_block * kWave), lds_bytes, ctx->stream, x, M, static_cast<int>(st->Q),
-                       static_cast<int>(st->N), st->d_images, st->img_f4, st->d_tables, idx, residual, recon, force_idx,
-                       ctx->d_flags, st->has_bin ? 1 : 0, st->key_bits, st->margin, st->exact_only ? 1 : 0);
+                       static_cast<int>(st->N), st->d_images, st->img_f4, st->lds_f4, st->d_tables, idx, residual, recon,
+                       force_idx, ctx->d_flags, st->has_bin ? 1 : 0, st->key_bits, st->margin, st->exact_only ? 1 : 0,
+                       st->qeps);
     aq_timing_stop(ctx, tslot);
     AQ_HIP(ctx, hipGetLastError());
     if (force_idx) {
@@ -709,6 +762,7 @@ aq_status aq_dac_decode(aq_ctx *ctx, const aq_dac_stages *st, const int32_t *idx
     if (!ctx || !st || (M > 0 && (!idx || !out))) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_dac_decode: null argument");
     if (M < 0) return aq_fail(ctx, AQ_E_SHAPE, "aq_dac_decode: negative M");
     if (M == 0) return AQ_OK;
+    if (!st->d_tables) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_dac_decode: no out-projection was uploaded");
     aq_device_guard g(ctx->device);
     AQ_HIP(ctx, hipMemsetAsync(ctx->d_flags, 0, sizeof(int32_t) * AQ_FLAG_COUNT, ctx->stream));
     const int64_t total = M * st->D;

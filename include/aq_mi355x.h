@@ -100,11 +100,36 @@ aq_status aq_ctx_read_timing(aq_ctx *ctx, float *ms, int capacity, int *count);
  *   codebook [Q, N, 8]
  *   w_out [Q, D, 8]   b_out [Q, D]   (NULL = no bias)
  * Supported: codebook dim 8, D in {64, 128, ..., 1024} (multiple of 64),
- * N a multiple of 64 up to 8192.
+ * N a multiple of 64 up to 2^20.
  * Replaces load_quantizer_unit (codec.cpp:693-720) / BackendWeightStore. */
 aq_status aq_dac_upload(aq_ctx *ctx, int64_t Q, int64_t D, int64_t N,
                         const float *w_in, const float *b_in, const float *codebook,
                         const float *w_out, const float *b_out, aq_dac_stages **out);
+
+/* The same cosine quantizer with another model family's normalisation
+ * (SURVEY-listed variants of the query and codebook L2 normalisation):
+ *   AQ_DAC_FISH       pn = p / sqrt(sum(p*p) + 1e-12); rows c * (float)(1/|c|),
+ *                     zero rows -> 0 (fish_audio/codec.cpp:171-189,323-334)
+ *   AQ_DAC_INDEXTTS2  pn = p / sqrt(sum(p*p)) (normalize_code_latents,
+ *                     index_tts2/semantic_codec.cpp:110-115); rows
+ *                     c * (1.0F / (float)|c|) (normalized_codebook, :43-58)
+ *   AQ_DAC_VEVO2      pn = p / sqrt(sum(p*p) + 1e-20) (build_l2_normalized_rows,
+ *                     vevo2/components.cpp:848-863); rows c * (float)(1/|c|),
+ *                     a zero row is an error (l2_normalized_rows, :566-590)
+ * All take the ggml arithmetic of the Fish path otherwise (1x1 conv, k = 8
+ * mul_mat scores, argmax keeping the last maximum).  w_out (and b_out) may be
+ * NULL for a single stage (Q = 1): codes only, as the IndexTTS2 and Vevo2
+ * tokenisers use them; encode then takes no residual / recon and decode is
+ * unavailable.  Codebooks too large for LDS next to W_in (e.g. IndexTTS2's
+ * 8192 x 8 with D = 1024) are read from device memory. */
+typedef enum aq_dac_recipe {
+    AQ_DAC_FISH = 0,
+    AQ_DAC_INDEXTTS2 = 1,
+    AQ_DAC_VEVO2 = 2
+} aq_dac_recipe;
+aq_status aq_dac_upload_ex(aq_ctx *ctx, int64_t Q, int64_t D, int64_t N,
+                           const float *w_in, const float *b_in, const float *codebook,
+                           const float *w_out, const float *b_out, int recipe, aq_dac_stages **out);
 aq_status aq_dac_release(aq_dac_stages *stages);
 
 /* Encode M frames through all Q stages (codec.cpp:570-611).

@@ -80,6 +80,9 @@ class Oracle:
         L.aqo_dac_rvq.restype = C.c_int
         L.aqo_dac_rvq.argtypes = [_f32p, _i64, _i64, _i64, _i64, _i64, _f32p, C.c_void_p, _f32p, _f32p,
                                   C.c_void_p, C.c_void_p, _i32p, _f32p, C.c_void_p]
+        L.aqo_dac_rvq_ex.restype = C.c_int
+        L.aqo_dac_rvq_ex.argtypes = [_f32p, _i64, _i64, _i64, _i64, _i64, _f32p, C.c_void_p, _f32p, C.c_void_p,
+                                     C.c_void_p, C.c_void_p, _i32p, _f32p, C.c_void_p, C.c_int]
         L.aqo_euclid_rvq.restype = C.c_int
         L.aqo_euclid_rvq.argtypes = [_f32p, _i64, _i64, _i64, _i64, _f32p, C.c_void_p, _i32p, _f32p, C.c_void_p]
         L.aqo_higgs_rvq.restype = C.c_int
@@ -97,7 +100,8 @@ class Oracle:
         L.aqo_ema_codebook.argtypes = [_f32p, _f32p, _i64, _i64, _i64, C.c_float, _f32p]
 
     # -- whole path --------------------------------------------------------
-    def dac_rvq(self, cfg: dict, force_idx=None, recon: bool = True):
+    def dac_rvq(self, cfg: dict, force_idx=None, recon: bool = True, recipe: int = 0):
+        """recipe 0 Fish, 1 IndexTTS2, 2 Vevo2; cfg["w_out"] None: codes only."""
         x = np.ascontiguousarray(cfg["x"], np.float32)
         B, T, D, Q, N = cfg["B"], cfg["T"], cfg["D"], cfg["Q"], cfg["N"]
         M = x.shape[0]
@@ -107,11 +111,13 @@ class Oracle:
         res = np.zeros((M, D), np.float32)
         rec = np.zeros((M, D), np.float32) if recon else None
         fi = np.ascontiguousarray(force_idx, np.int32) if force_idx is not None else None
-        rc = self.lib.aqo_dac_rvq(x, B, T, D, Q, N, np.ascontiguousarray(cfg["w_in"], np.float32),
-                                  _opt(cfg.get("b_in"), np.float32), np.ascontiguousarray(cfg["codebook"], np.float32),
-                                  np.ascontiguousarray(cfg["w_out"], np.float32), _opt(cfg.get("b_out"), np.float32),
-                                  None if fi is None else fi.ctypes.data_as(C.c_void_p), idx, res,
-                                  None if rec is None else rec.ctypes.data_as(C.c_void_p))
+        rc = self.lib.aqo_dac_rvq_ex(x, B, T, D, Q, N, np.ascontiguousarray(cfg["w_in"], np.float32),
+                                     _opt(cfg.get("b_in"), np.float32), np.ascontiguousarray(cfg["codebook"], np.float32),
+                                     _opt(cfg.get("w_out"), np.float32), _opt(cfg.get("b_out"), np.float32),
+                                     None if fi is None else fi.ctypes.data_as(C.c_void_p), idx, res,
+                                     None if rec is None else rec.ctypes.data_as(C.c_void_p), recipe)
+        if rc == -2:
+            raise ValueError("the recipe rejects a zero codebook row")
         assert rc == 0
         return dict(idx=idx, residual=res, recon=rec)
 
@@ -205,6 +211,9 @@ class Ref:
         L.aqref_dac_rvq.restype = C.c_double
         L.aqref_dac_rvq.argtypes = [_f32p, _i64, _i64, _i64, _i64, _i64, _f32p, C.c_void_p, _f32p, _f32p,
                                     C.c_void_p, _i32p, _f32p, C.c_void_p, C.c_void_p, C.c_int, C.c_int]
+        L.aqref_dac_rvq_ex.restype = C.c_double
+        L.aqref_dac_rvq_ex.argtypes = [_f32p, _i64, _i64, _i64, _i64, _i64, _f32p, C.c_void_p, _f32p, _f32p,
+                                       C.c_void_p, _i32p, _f32p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int]
         L.aqref_euclid_rvq.restype = C.c_double
         L.aqref_euclid_rvq.argtypes = [_f32p, _i64, _i64, _i64, _i64, _f32p, _i32p, _f32p, C.c_void_p, C.c_int]
         L.aqref_higgs_rvq.restype = C.c_double
@@ -225,7 +234,7 @@ class Ref:
         self.lib.aqref_top_k(v, rows, n, k, out, threads)
         return out
 
-    def dac_rvq(self, cfg: dict, threads: int = 8, recon: bool = True, materialize: bool = True):
+    def dac_rvq(self, cfg: dict, threads: int = 8, recon: bool = True, materialize: bool = True, recipe: int = 0):
         x = np.ascontiguousarray(cfg["x"], np.float32)
         T, D, Q, N = cfg["T"], cfg["D"], cfg["Q"], cfg["N"]
         M = x.shape[0]
@@ -233,11 +242,13 @@ class Ref:
         idx = np.zeros((M, Q), np.int32)
         res = np.zeros((M, D), np.float32)
         rec = np.zeros((M, D), np.float32) if recon else None
-        ms = self.lib.aqref_dac_rvq(x, B, T, D, Q, N, np.ascontiguousarray(cfg["w_in"], np.float32),
-                                    _opt(cfg.get("b_in"), np.float32), np.ascontiguousarray(cfg["codebook"], np.float32),
-                                    np.ascontiguousarray(cfg["w_out"], np.float32), _opt(cfg.get("b_out"), np.float32),
-                                    idx, res, None if rec is None else rec.ctypes.data_as(C.c_void_p), None, threads,
-                                    1 if materialize else 0)
+        ms = self.lib.aqref_dac_rvq_ex(x, B, T, D, Q, N, np.ascontiguousarray(cfg["w_in"], np.float32),
+                                       _opt(cfg.get("b_in"), np.float32), np.ascontiguousarray(cfg["codebook"], np.float32),
+                                       np.ascontiguousarray(cfg["w_out"], np.float32), _opt(cfg.get("b_out"), np.float32),
+                                       idx, res, None if rec is None else rec.ctypes.data_as(C.c_void_p), None, threads,
+                                       1 if materialize else 0, recipe)
+        if ms < 0:
+            raise ValueError("the recipe rejects a zero codebook row")
         return dict(idx=idx, residual=res, recon=rec, ms=ms)
 
     def euclid_rvq(self, cfg: dict, threads: int = 8):

@@ -255,10 +255,16 @@ static float dot_f32(int64_t m_rows, int64_t n_rows, int k, const float *src0_ro
  *   z = Conv1d(k=1)(codebook[code]) + b_out          k = 8 -> vec_dot_f32
  *   residual -= z ; recon += z (decode sum, codec.cpp:552-568)
  * normalized_codebook = normalized_rows(codebook)    codec.cpp:171-189. */
-int aqo_dac_rvq(const float *x, int64_t B, int64_t T, int64_t D, int64_t Q, int64_t N,
-                const float *w_in, const float *b_in, const float *cb,
-                const float *w_out, const float *b_out, const int32_t *force_idx,
-                int32_t *idx, float *residual, float *recon) {
+/* recipe: 0 Fish (normalized_rows codec.cpp:171-189, l2_normalize_last
+ * 323-334: +1e-12 by ggml_scale_bias), 1 IndexTTS2 (normalized_codebook
+ * semantic_codec.cpp:43-58: 1.0F / (float)sqrt; normalize_code_latents
+ * 110-115: no bias), 2 Vevo2 (l2_normalized_rows components.cpp:566-590:
+ * zero rows rejected; build_l2_normalized_rows 848-863: +1e-20).  Returns -2
+ * when the recipe rejects the codebook. */
+int aqo_dac_rvq_ex(const float *x, int64_t B, int64_t T, int64_t D, int64_t Q, int64_t N,
+                   const float *w_in, const float *b_in, const float *cb,
+                   const float *w_out, const float *b_out, const int32_t *force_idx,
+                   int32_t *idx, float *residual, float *recon, int recipe) {
     const int64_t M = B * T;
     float *r = residual;
     memcpy(r, x, (size_t)(M * D) * sizeof(float));
@@ -269,11 +275,20 @@ int aqo_dac_rvq(const float *x, int64_t B, int64_t T, int64_t D, int64_t Q, int6
     for (int64_t s = 0; s < Q; ++s) {
         const float *Wi = w_in + s * 8 * D;
         const float *C = cb + s * N * 8;
-        const float *Wo = w_out + s * D * 8;
+        const float *Wo = w_out ? w_out + s * D * 8 : NULL;
         for (int64_t n = 0; n < N; ++n) {
             double sum = 0.0;
             for (int k = 0; k < 8; ++k) sum += (double)C[n * 8 + k] * (double)C[n * 8 + k];
-            const float inv = sum > 0.0 ? (float)(1.0 / sqrt(sum)) : 0.0f;
+            float inv;
+            if (recipe == 1) {
+                inv = 1.0f / (float)sqrt(sum);
+            } else if (recipe == 2) {
+                const double norm = sqrt(sum);
+                if (norm == 0.0) { free(cbn); free(scores); return -2; }
+                inv = (float)(1.0 / norm);
+            } else {
+                inv = sum > 0.0 ? (float)(1.0 / sqrt(sum)) : 0.0f;
+            }
             for (int k = 0; k < 8; ++k) cbn[n * 8 + k] = C[n * 8 + k] * inv;
         }
         for (int64_t m = 0; m < M; ++m) {
@@ -285,7 +300,7 @@ int aqo_dac_rvq(const float *x, int64_t B, int64_t T, int64_t D, int64_t Q, int6
             }
             for (int j = 0; j < 8; ++j) sq[j] = p[j] * p[j];
             float ss = aqo_sum_f32(8, sq);
-            ss = fmaf(ss, 1.0f, 1.0e-12f);          /* ggml_scale_bias, vec.h:708-710 */
+            if (recipe != 1) ss = fmaf(ss, 1.0f, recipe == 2 ? 1.0e-20f : 1.0e-12f);   /* ggml_scale_bias, vec.h:708-710 */
             const float den = sqrtf(ss);
             for (int j = 0; j < 8; ++j) pn[j] = p[j] / den;
             for (int64_t n = 0; n < N; ++n) scores[n] = aqo_vec_dot_f32(8, cbn + n * 8, pn);
@@ -293,6 +308,7 @@ int aqo_dac_rvq(const float *x, int64_t B, int64_t T, int64_t D, int64_t Q, int6
             idx[m * Q + s] = code;
             const int use = force_idx ? force_idx[m * Q + s] : code;
             const float *q = C + (int64_t)use * 8;
+            if (!w_out) continue;   /* codes only (no out-projection given) */
             for (int64_t d = 0; d < D; ++d) {
                 float z = aqo_vec_dot_f32(8, q, Wo + d * 8);
                 if (b_out) z = z + b_out[s * D + d];
@@ -517,4 +533,11 @@ int aqo_ema_codebook(const float *embedding_sum, const float *cluster_usage, int
         for (int64_t k = 0; k < K; ++k) cb[qn * K + k] = embedding_sum[qn * K + k] / denom;
     }
     return 0;
+}
+
+int aqo_dac_rvq(const float *x, int64_t B, int64_t T, int64_t D, int64_t Q, int64_t N,
+                const float *w_in, const float *b_in, const float *cb,
+                const float *w_out, const float *b_out, const int32_t *force_idx,
+                int32_t *idx, float *residual, float *recon) {
+    return aqo_dac_rvq_ex(x, B, T, D, Q, N, w_in, b_in, cb, w_out, b_out, force_idx, idx, residual, recon, 0);
 }

@@ -49,6 +49,12 @@ int aqo_dac_rvq(const float *x, int64_t B, int64_t T, int64_t D, int64_t Q, int6
                 const float *w_in, const float *b_in, const float *cb,
                 const float *w_out, const float *b_out, const int32_t *force_idx,
                 int32_t *idx, float *residual, float *recon);
+/* Same with the normalisation recipe: 0 Fish, 1 IndexTTS2, 2 Vevo2; w_out may
+ * be NULL (codes only; the residual stays the input). */
+int aqo_dac_rvq_ex(const float *x, int64_t B, int64_t T, int64_t D, int64_t Q, int64_t N,
+                   const float *w_in, const float *b_in, const float *cb,
+                   const float *w_out, const float *b_out, const int32_t *force_idx,
+                   int32_t *idx, float *residual, float *recon, int recipe);
 
 /* OmniVoice-style Euclidean RVQ: logit = dot(2c, r) + (-|c|^2). x [M,K],
  * cb [Q,N,K].  logit_best [M,Q] nullable. */

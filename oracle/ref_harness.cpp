@@ -75,6 +75,35 @@ std::vector<float> fish_normalized_rows(const float * v, int64_t rows, int64_t c
     return out;
 }
 
+// IndexTTS2 normalized_codebook (index_tts2/semantic_codec.cpp:43-58): double
+// sum, inv_norm = 1.0F / (float)sqrt(norm), float product (no zero guard).
+std::vector<float> indextts2_normalized_rows(const float * v, int64_t rows, int64_t cols) {
+    std::vector<float> out(static_cast<size_t>(rows * cols), 0.0f);
+    for (int64_t r = 0; r < rows; ++r) {
+        double norm = 0.0;
+        for (int64_t c = 0; c < cols; ++c) norm += static_cast<double>(v[r * cols + c]) * static_cast<double>(v[r * cols + c]);
+        const float inv_norm = 1.0F / static_cast<float>(std::sqrt(norm));
+        for (int64_t c = 0; c < cols; ++c) out[r * cols + c] = v[r * cols + c] * inv_norm;
+    }
+    return out;
+}
+
+// Vevo2 l2_normalized_rows (vevo2/components.cpp:566-590): double sum, norm =
+// sqrt, inv = (float)(1.0 / norm), float product; a zero row is an error there
+// (returns false here).
+bool vevo2_normalized_rows(const float * v, int64_t rows, int64_t cols, std::vector<float> & out) {
+    out.assign(static_cast<size_t>(rows * cols), 0.0f);
+    for (int64_t r = 0; r < rows; ++r) {
+        double sum = 0.0;
+        for (int64_t c = 0; c < cols; ++c) sum += static_cast<double>(v[r * cols + c]) * static_cast<double>(v[r * cols + c]);
+        const double norm = std::sqrt(sum);
+        if (norm == 0.0) return false;
+        const float inv = static_cast<float>(1.0 / norm);
+        for (int64_t c = 0; c < cols; ++c) out[r * cols + c] = v[r * cols + c] * inv;
+    }
+    return true;
+}
+
 // Conv1dModule with kernel 1 (conv_modules.cpp:284-341): one ggml_conv_1d per
 // batch element, concatenated along the batch axis, then the repeated bias add.
 // input ne = [T, IC, B], weight ne = [1, IC, OC], bias ne = [OC] or null.
@@ -104,11 +133,14 @@ ggml_tensor * conv1d_k1(ggml_context * ctx, ggml_tensor * input, ggml_tensor * w
 // l2_normalize_last (fish codec.cpp:323-334) on ne = [C, T, B].  MulModule
 // makes its operands contiguous (primitive_modules.cpp:243-254); ggml_div gets
 // `x` as passed in.
-ggml_tensor * l2_normalize_last(ggml_context * ctx, ggml_tensor * x) {
+// recipe 1 (IndexTTS2 normalize_code_latents, index_tts2/semantic_codec.cpp:110-115)
+// takes ggml_sqr, no bias; recipe 2 (Vevo2 build_l2_normalized_rows,
+// vevo2/components.cpp:848-863) adds 1e-20 with ggml_scale_bias.
+ggml_tensor * l2_normalize_last(ggml_context * ctx, ggml_tensor * x, int recipe = 0) {
     ggml_tensor * xc = ggml_is_contiguous(x) ? x : ggml_cont(ctx, x);
-    ggml_tensor * sq = ggml_mul(ctx, xc, xc);
+    ggml_tensor * sq = recipe == 1 ? ggml_sqr(ctx, xc) : ggml_mul(ctx, xc, xc);
     ggml_tensor * sum = ggml_sum_rows(ctx, sq);
-    ggml_tensor * shifted = ggml_scale_bias(ctx, sum, 1.0f, 1.0e-12f);
+    ggml_tensor * shifted = recipe == 1 ? sum : ggml_scale_bias(ctx, sum, 1.0f, recipe == 2 ? 1.0e-20f : 1.0e-12f);
     ggml_tensor * denom = ggml_sqrt(ctx, shifted);
     ggml_tensor * rep = ggml_repeat(ctx, denom, x);
     return ggml_div(ctx, x, rep);
@@ -141,11 +173,13 @@ int aqref_version(void) { return 1; }
 // Outputs: idx [M, Q]; residual [M, D] (final); recon [M, D] = sum_s z_s
 // (decode recipe codec.cpp:552-568); stage_res optional [Q, M, D] = residual
 // after each stage.  Returns compute milliseconds.
-double aqref_dac_rvq(const float * x, int64_t B, int64_t T, int64_t D, int64_t Q, int64_t N,
-                     const float * w_in, const float * b_in, const float * cb,
-                     const float * w_out, const float * b_out,
-                     int32_t * idx, float * residual, float * recon, float * stage_res,
-                     int n_threads, int materialize) {
+// recipe: 0 Fish, 1 IndexTTS2, 2 Vevo2 (query and codebook normalisation).
+// Returns compute milliseconds, or -1 when the recipe rejects the codebook.
+double aqref_dac_rvq_ex(const float * x, int64_t B, int64_t T, int64_t D, int64_t Q, int64_t N,
+                        const float * w_in, const float * b_in, const float * cb,
+                        const float * w_out, const float * b_out,
+                        int32_t * idx, float * residual, float * recon, float * stage_res,
+                        int n_threads, int materialize, int recipe) {
     ggml_cpu_init();
     const int64_t M = B * T;
     double ms = 0.0;
@@ -170,7 +204,10 @@ double aqref_dac_rvq(const float * x, int64_t B, int64_t T, int64_t D, int64_t Q
         std::memcpy(CB->data, cb + s * N * 8, static_cast<size_t>(N * 8) * 4);
         ggml_tensor * CBn = ggml_new_tensor_2d(ctx, GGML_TYPE_F32, 8, N);
         {
-            auto nr = fish_normalized_rows(cb + s * N * 8, N, 8);
+            std::vector<float> nr;
+            if (recipe == 1) nr = indextts2_normalized_rows(cb + s * N * 8, N, 8);
+            else if (recipe == 2) { if (!vevo2_normalized_rows(cb + s * N * 8, N, 8, nr)) return -1.0; }
+            else nr = fish_normalized_rows(cb + s * N * 8, N, 8);
             std::memcpy(CBn->data, nr.data(), nr.size() * 4);
         }
         ggml_tensor * Wout = ggml_new_tensor_3d(ctx, GGML_TYPE_F32, 1, 8, D);
@@ -188,7 +225,7 @@ double aqref_dac_rvq(const float * x, int64_t B, int64_t T, int64_t D, int64_t Q
         // CPU binary ops read src0 rows as contiguous (binary-ops.cpp:120-136),
         // so ggml_div then reads the wrong elements (kept only to document it).
         if (materialize) proj_btd = ggml_cont(ctx, proj_btd);
-        ggml_tensor * pn = l2_normalize_last(ctx, proj_btd);                   // [8, T, B]
+        ggml_tensor * pn = l2_normalize_last(ctx, proj_btd, recipe);           // [8, T, B]
         ggml_tensor * pn2 = ggml_reshape_2d(ctx, ggml_cont(ctx, pn), 8, M);
         ggml_tensor * logits = ggml_mul_mat(ctx, CBn, pn2);                    // [N, M]
         ggml_mul_mat_set_prec(logits, GGML_PREC_F32);
@@ -211,6 +248,15 @@ double aqref_dac_rvq(const float * x, int64_t B, int64_t T, int64_t D, int64_t Q
     if (residual) from_channel_major(res_cm.data(), B, T, D, residual);
     if (recon) from_channel_major(rec_cm.data(), B, T, D, recon);
     return ms;
+}
+
+double aqref_dac_rvq(const float * x, int64_t B, int64_t T, int64_t D, int64_t Q, int64_t N,
+                     const float * w_in, const float * b_in, const float * cb,
+                     const float * w_out, const float * b_out,
+                     int32_t * idx, float * residual, float * recon, float * stage_res,
+                     int n_threads, int materialize) {
+    return aqref_dac_rvq_ex(x, B, T, D, Q, N, w_in, b_in, cb, w_out, b_out, idx, residual, recon, stage_res,
+                            n_threads, materialize, 0);
 }
 
 // OmniVoice-style Euclidean RVQ (no projections): logits = (2c)·x + (-|c|^2).

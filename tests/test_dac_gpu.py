@@ -226,3 +226,85 @@ def test_dac_launch_shapes(torch, ctx, oracle, M):
     assert np.array_equal(out["idx"], ref["idx"])
     assert np.array_equal(out["residual"].view(np.uint32), ref["residual"].view(np.uint32))
     assert np.array_equal(out["recon"].view(np.uint32), ref["recon"].view(np.uint32))
+
+
+def _bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+@pytest.mark.parametrize("recipe", [1, 2])
+def test_dac_recipes_match_oracle(torch, ctx, oracle, recipe):
+    """IndexTTS2 (no eps; 1.0F / (float)|c| rows) and Vevo2 (1e-20; zero rows
+    rejected) normalisation through the full residual cascade, bit for bit."""
+    import aqmi
+    from aqmi import synth
+
+    print(f"[gpu] dac recipe {recipe}", flush=True)
+    T, B, D, N, Q = 75, 2, 1024, 1024, 3
+    cfg = dict(kind="dac", B=B, T=T, D=D, Q=Q, N=N, x=synth.normal(41, 1, (B * T, D)),
+               **synth.dac_weights(41, Q, D, N, bias=True))
+    st = aqmi.DacStages(ctx, cfg["w_in"], cfg["b_in"], cfg["codebook"], cfg["w_out"], cfg["b_out"], recipe)
+    x = torch.from_numpy(cfg["x"]).cuda()
+    idx = torch.full((B * T, Q), -1, dtype=torch.int32, device="cuda")
+    res = torch.empty((B * T, D), dtype=torch.float32, device="cuda")
+    rec = torch.empty((B * T, D), dtype=torch.float32, device="cuda")
+    st.encode(x, T, idx, res, rec)
+    torch.cuda.synchronize()
+    ref = oracle.dac_rvq(cfg, recipe=recipe)
+    assert np.array_equal(idx.cpu().numpy(), ref["idx"])
+    assert np.array_equal(_bits(res.cpu().numpy()), _bits(ref["residual"]))
+    assert np.array_equal(_bits(rec.cpu().numpy()), _bits(ref["recon"]))
+
+
+@pytest.mark.parametrize("recipe", [0, 1, 2])
+def test_dac_large_codebook_codes_only(torch, ctx, oracle, recipe):
+    """IndexTTS2's semantic codec shape: one stage, D = 1024, N = 8192 (too
+    large for LDS next to W_in: read from device memory), codes only (no
+    out-projection), with a zero frame (IndexTTS2 divides by 0: NaN scores,
+    ggml_argmax's NaN rule)."""
+    import aqmi
+    from aqmi import synth
+
+    print(f"[gpu] dac large codebook recipe {recipe}", flush=True)
+    T, B, D, N = 75, 2, 1024, 8192
+    w = synth.dac_weights(42, 1, D, N, bias=True)
+    x = synth.normal(42, 1, (B * T, D))
+    x[3] = 0.0
+    w["b_in"][:] = 0.0
+    cfg = dict(kind="dac", B=B, T=T, D=D, Q=1, N=N, x=x, w_in=w["w_in"], b_in=w["b_in"], codebook=w["codebook"],
+               w_out=None, b_out=None)
+    st = aqmi.DacStages(ctx, w["w_in"], w["b_in"], w["codebook"], None, None, recipe)
+    xd = torch.from_numpy(x).cuda()
+    idx = torch.full((B * T, 1), -1, dtype=torch.int32, device="cuda")
+    st.encode(xd, T, idx)
+    torch.cuda.synchronize()
+    ref = oracle.dac_rvq(cfg, recon=False, recipe=recipe)
+    assert np.array_equal(idx.cpu().numpy(), ref["idx"])
+    with pytest.raises(aqmi.AqError):
+        st.encode(xd, T, idx, torch.empty((B * T, D), dtype=torch.float32, device="cuda"))
+
+
+def test_dac_large_codebook_cascade(torch, ctx, oracle):
+    """N = 4096 with two stages and the out-projection: codebook in device
+    memory, residual and reconstruction bit for bit."""
+    from aqmi import synth
+
+    print("[gpu] dac large codebook cascade", flush=True)
+    T, B, D, N, Q = 75, 2, 1024, 4096, 2
+    cfg = dict(kind="dac", B=B, T=T, D=D, Q=Q, N=N, x=synth.normal(43, 1, (B * T, D)),
+               **synth.dac_weights(43, Q, D, N, bias=True))
+    out = run_gpu(torch, ctx, cfg)
+    ref = oracle.dac_rvq(cfg)
+    assert np.array_equal(out["idx"], ref["idx"])
+    assert np.array_equal(_bits(out["residual"]), _bits(ref["residual"]))
+    assert np.array_equal(_bits(out["recon"]), _bits(ref["recon"]))
+
+
+def test_dac_vevo2_rejects_zero_codebook_row(torch, ctx):
+    import aqmi
+    from aqmi import synth
+
+    w = synth.dac_weights(44, 1, 64, 128, bias=False)
+    w["codebook"][0, 7] = 0.0
+    with pytest.raises(aqmi.AqError):
+        aqmi.DacStages(ctx, w["w_in"], None, w["codebook"], None, None, aqmi.DAC_VEVO2)

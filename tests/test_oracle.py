@@ -117,6 +117,45 @@ def test_oracle_dac_bit_exact_vs_ggml(o, ref, T):
     assert _beq(a["residual"], b["residual"]) and _beq(a["recon"], b["recon"])
 
 
+@pytest.mark.parametrize("recipe", [1, 2])
+@pytest.mark.parametrize("T", [75, 5])
+def test_oracle_dac_recipes_bit_exact_vs_ggml(o, ref, recipe, T):
+    """IndexTTS2 (ggml_sqr, no bias; 1.0F / (float)sqrt codebook rows) and
+    Vevo2 (+1e-20; (float)(1 / norm) rows) normalisation, N = 8192 as in
+    IndexTTS2's semantic codec, against the ggml op sequences."""
+    cfg = dict(kind="dac", B=2, T=T, D=1024, Q=2, N=8192, x=synth.normal(22, 1, (2 * T, 1024)),
+               **synth.dac_weights(22, 2, 1024, 8192, bias=True))
+    a, b = o.dac_rvq(cfg, recipe=recipe), ref.dac_rvq(cfg, recipe=recipe)
+    assert np.array_equal(a["idx"], b["idx"])
+    assert _beq(a["residual"], b["residual"]) and _beq(a["recon"], b["recon"])
+
+
+def test_oracle_dac_recipe_edge_cases(o, ref):
+    """A zero projection: Fish and Vevo2 divide by sqrt(eps) (codes defined),
+    IndexTTS2 divides by 0 (NaN scores; ggml_argmax's NaN rule picks the
+    code).  A zero codebook row: Fish maps it to 0, IndexTTS2 to NaN, Vevo2
+    rejects the codebook."""
+    T = 6
+    w = synth.dac_weights(23, 1, 64, 128, bias=False)
+    x = synth.normal(23, 1, (T, 64))
+    x[2] = 0.0
+    cfg = dict(kind="dac", B=1, T=T, D=64, Q=1, N=128, x=x, **w)
+    for recipe in (0, 1, 2):
+        a, b = o.dac_rvq(cfg, recipe=recipe), ref.dac_rvq(cfg, recipe=recipe)
+        assert np.array_equal(a["idx"], b["idx"])
+    w2 = dict(w)
+    w2["codebook"] = w["codebook"].copy()
+    w2["codebook"][0, 5] = 0.0
+    cfg2 = dict(cfg, **w2)
+    for recipe in (0, 1):
+        a, b = o.dac_rvq(cfg2, recipe=recipe), ref.dac_rvq(cfg2, recipe=recipe)
+        assert np.array_equal(a["idx"], b["idx"])
+    with pytest.raises(ValueError):
+        o.dac_rvq(cfg2, recipe=2)
+    with pytest.raises(ValueError):
+        ref.dac_rvq(cfg2, recipe=2)
+
+
 @pytest.mark.parametrize("M", [1, 2, 5, 64])
 def test_oracle_euclid_bit_exact_vs_ggml(o, ref, M):
     cfg = synth.make_config(2, rows=M)
