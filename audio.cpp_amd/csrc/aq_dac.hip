@@ -187,7 +187,16 @@ __device__ inline void fetch_image(f32x4 (&pre)[PF > 0 ? PF : 1], const float4 *
     }
 }
 
-template <int DI, int FW, bool RECON, int PF, bool CBG>
+// The tinyBLAS image's W_in: float4 ((j * 16 + t) * DI + sw(u4, t)) holds
+// W_in[j][16 * (4 u4 + c) + t], c = 0..3 -- accumulator t of output j walks
+// u = 0, 1, 2, ... in order.  The XOR swizzle keeps the 16 lanes of a row on
+// distinct banks when DI is a power of two.
+template <int DI>
+__device__ __host__ inline int tb_sw(int u4, int t) {
+    return (DI & (DI - 1)) == 0 ? (u4 ^ (t & (DI - 1))) : u4;
+}
+
+template <int DI, int FW, bool RECON, int PF, bool CBG, int ORDER>
 __global__ __launch_bounds__(kMaxBlock, 1) void dac_encode_kernel(
     const float *__restrict__ x, int64_t M, int Q, int N, const float4 *__restrict__ images, int64_t stride_f4,
     int64_t img_f4, const float *__restrict__ tables, int32_t *__restrict__ idx, float *__restrict__ residual,
@@ -255,6 +264,55 @@ __global__ __launch_bounds__(kMaxBlock, 1) void dac_encode_kernel(
         const float4 *chat = CBG ? images + static_cast<int64_t>(s) * stride_f4 + 2 * DI * kWave + 2
                                  : lds + 2 * DI * kWave + 2;
 
+        float wred[FW][2];   // lane 16 g holds outputs 2 g and 2 g + 1 of each frame
+        if (ORDER == 1) {
+            // ---- in-projection, tinyBLAS order (sgemm.cpp:527-545: 16 FMA
+            // accumulators over k = 16 u + t, then _mm512_reduce_add_ps) ----
+            // Lane L = 16 g + t runs accumulator t of outputs 2g and 2g+1 over
+            // the frame's elements k = 16 u + t, read from a transposed copy
+            // of the residual in LDS (the cascade keeps k = L + 64 i per lane).
+            float *rt = reinterpret_cast<float *>(lds + img_f4) + wave * D;
+            const int t = lane & 15, g = lane >> 4;
+            const float4 *w0 = win + (2 * g * 16 + t) * DI;
+            const float4 *w1 = win + ((2 * g + 1) * 16 + t) * DI;
+#pragma unroll
+            for (int f = 0; f < FW; ++f) {
+#pragma unroll
+                for (int i = 0; i < DI; ++i) rt[t * (D / 16) + tb_sw<DI>(i, t) * 4 + g] = r[f][i];
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+                for (int u4 = 0; u4 < DI; ++u4) {
+                    const int sw = tb_sw<DI>(u4, t);
+                    const float4 rv = *reinterpret_cast<const float4 *>(rt + t * (D / 16) + sw * 4);
+                    const float4 x0 = w0[sw], x1 = w1[sw];
+                    a0 = __fmaf_rn(x0.x, rv.x, a0);
+                    a0 = __fmaf_rn(x0.y, rv.y, a0);
+                    a0 = __fmaf_rn(x0.z, rv.z, a0);
+                    a0 = __fmaf_rn(x0.w, rv.w, a0);
+                    a1 = __fmaf_rn(x1.x, rv.x, a1);
+                    a1 = __fmaf_rn(x1.y, rv.y, a1);
+                    a1 = __fmaf_rn(x1.z, rv.z, a1);
+                    a1 = __fmaf_rn(x1.w, rv.w, a1);
+                }
+                a0 = row_ror_add<8>(a0);
+                a0 = row_ror_add<4>(a0);
+                a0 = row_ror_add<2>(a0);
+                a0 = row_ror_add<1>(a0);
+                a1 = row_ror_add<8>(a1);
+                a1 = row_ror_add<4>(a1);
+                a1 = row_ror_add<2>(a1);
+                a1 = row_ror_add<1>(a1);
+                wred[f][0] = a0;
+                wred[f][1] = a1;
+                // the next frame overwrites rt
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            }
+        } else {
         // ---- in-projection: one FMA chain per lane and output, ggml order ----
         float acc[FW][8];
 #pragma unroll
@@ -298,8 +356,6 @@ __global__ __launch_bounds__(kMaxBlock, 1) void dac_encode_kernel(
         // two cross-row levels lane L holds outputs 2*(L/16) and 2*(L/16)+1.
         const bool hi32 = lane >= 32;
         const bool hi16 = (lane & 16) != 0;
-        float pn[FW][8];
-        bool finite[FW];
 #pragma unroll
         for (int f = 0; f < FW; ++f) {
             float v[4];
@@ -323,10 +379,18 @@ __global__ __launch_bounds__(kMaxBlock, 1) void dac_encode_kernel(
                 w[q] = row_ror_add<2>(w[q]);
                 w[q] = row_ror_add<1>(w[q]);
             }
-            // Lane L now holds outputs 2*(L/16) (w[0]) and 2*(L/16)+1 (w[1]).
+            wred[f][0] = w[0];
+            wred[f][1] = w[1];
+        }
+        }
+        float pn[FW][8];
+        bool finite[FW];
+#pragma unroll
+        for (int f = 0; f < FW; ++f) {
+            // Lane 16 g holds outputs 2 g (wred[f][0]) and 2 g + 1 (wred[f][1]).
             const int o0 = 2 * (lane >> 4);
-            const float pa = has_bin ? __fadd_rn(w[0], bin[o0]) : w[0];
-            const float pb = has_bin ? __fadd_rn(w[1], bin[o0 + 1]) : w[1];
+            const float pa = has_bin ? __fadd_rn(wred[f][0], bin[o0]) : wred[f][0];
+            const float pb = has_bin ? __fadd_rn(wred[f][1], bin[o0 + 1]) : wred[f][1];
             // l2_normalize_last: fp32 squares, double row sum in output order,
             // + 1e-12, sqrt, divide.  The sum is wave-uniform (SGPR inputs);
             // each lane then divides its own two outputs.
@@ -467,36 +531,43 @@ constexpr int kPrefetch = 12;   // float4 per thread in the prefetching variant
 
 // Variants: image copied at each stage start, prefetched a stage ahead, or
 // (large codebooks) the W_in + b_in prefix prefetched with c_hat in memory.
-template <int DI, int FW, bool RECON>
+// ORDER: the in-projection's summation order, 0 ggml_vec_dot_f32, 1 tinyBLAS.
+template <int DI, int FW, bool RECON, int ORDER>
 EncodeFn pick_pf(bool prefetch, bool cbg) {
-    if (cbg) return dac_encode_kernel<DI, FW, RECON, kPrefetch, true>;
-    return prefetch ? dac_encode_kernel<DI, FW, RECON, kPrefetch, false> : dac_encode_kernel<DI, FW, RECON, 0, false>;
+    if (cbg) return dac_encode_kernel<DI, FW, RECON, kPrefetch, true, ORDER>;
+    return prefetch ? dac_encode_kernel<DI, FW, RECON, kPrefetch, false, ORDER>
+                    : dac_encode_kernel<DI, FW, RECON, 0, false, ORDER>;
 }
 
-template <int DI, int FW>
+template <int DI, int FW, int ORDER>
 EncodeFn pick_recon(bool recon, bool prefetch, bool cbg) {
-    return recon ? pick_pf<DI, FW, true>(prefetch, cbg) : pick_pf<DI, FW, false>(prefetch, cbg);
+    return recon ? pick_pf<DI, FW, true, ORDER>(prefetch, cbg) : pick_pf<DI, FW, false, ORDER>(prefetch, cbg);
 }
 
-template <int DI>
+template <int DI, int ORDER>
 EncodeFn pick_fw(int fw, bool recon, bool prefetch, bool cbg) {
     switch (fw) {
-        case 1: return pick_recon<DI, 1>(recon, prefetch, cbg);
-        case 2: return pick_recon<DI, 2>(recon, prefetch, cbg);
-        default: return pick_recon<DI, 3>(recon, prefetch, cbg);
+        case 1: return pick_recon<DI, 1, ORDER>(recon, prefetch, cbg);
+        case 2: return pick_recon<DI, 2, ORDER>(recon, prefetch, cbg);
+        default: return pick_recon<DI, 3, ORDER>(recon, prefetch, cbg);
     }
 }
 
-EncodeFn pick_kernel(int64_t D, int fw, bool recon, bool prefetch, bool cbg) {
+template <int ORDER>
+EncodeFn pick_kernel_o(int64_t D, int fw, bool recon, bool prefetch, bool cbg) {
     switch (D / kWave) {
-        case 1: return pick_fw<1>(fw, recon, prefetch, cbg);
-        case 2: return pick_fw<2>(fw, recon, prefetch, cbg);
-        case 4: return pick_fw<4>(fw, recon, prefetch, cbg);
-        case 8: return pick_fw<8>(fw, recon, prefetch, cbg);
-        case 12: return pick_fw<12>(fw, recon, prefetch, cbg);
-        case 16: return pick_fw<16>(fw, recon, prefetch, cbg);
+        case 1: return pick_fw<1, ORDER>(fw, recon, prefetch, cbg);
+        case 2: return pick_fw<2, ORDER>(fw, recon, prefetch, cbg);
+        case 4: return pick_fw<4, ORDER>(fw, recon, prefetch, cbg);
+        case 8: return pick_fw<8, ORDER>(fw, recon, prefetch, cbg);
+        case 12: return pick_fw<12, ORDER>(fw, recon, prefetch, cbg);
+        case 16: return pick_fw<16, ORDER>(fw, recon, prefetch, cbg);
         default: return nullptr;
     }
+}
+
+EncodeFn pick_kernel(int64_t D, int fw, bool recon, bool prefetch, bool cbg, int order = 0) {
+    return order == 1 ? pick_kernel_o<1>(D, fw, recon, prefetch, cbg) : pick_kernel_o<0>(D, fw, recon, prefetch, cbg);
 }
 
 // Launch shape.  A wave keeps its frames' residuals in registers for the
@@ -517,7 +588,8 @@ struct Shape {
     bool prefetch = false;
 };
 
-Shape launch_shape(int64_t M, int64_t D, int64_t img_f4, bool recon, int num_cus, size_t lds_bytes, bool cbg) {
+Shape launch_shape(int64_t M, int64_t D, int64_t img_f4, bool recon, int num_cus, size_t lds_bytes, bool cbg,
+                   int order) {
     const int64_t cus = num_cus > 0 ? num_cus : 256;
     int env_fw = 0, env_wpb = 0;
     if (const char *e = std::getenv("AQ_DAC_FW")) env_fw = std::atoi(e);
@@ -533,12 +605,14 @@ Shape launch_shape(int64_t M, int64_t D, int64_t img_f4, bool recon, int num_cus
             if (cbg && !prefetch) continue;   // the in-memory codebook variant always prefetches
             hipFuncAttributes attr{};
             int64_t simd_waves = 8;
-            if (hipFuncGetAttributes(&attr, reinterpret_cast<const void *>(pick_kernel(D, fw, recon, prefetch, cbg))) ==
+            if (hipFuncGetAttributes(&attr, reinterpret_cast<const void *>(pick_kernel(D, fw, recon, prefetch, cbg, order))) ==
                     hipSuccess && attr.numRegs > 0)
                 simd_waves = std::min<int64_t>(8, 512 / ((attr.numRegs + 7) / 8 * 8));
             // The block must fit on a CU at all (waves per SIMD by registers,
             // one stage image in LDS).
-            if (simd_waves < (wpb + 3) / 4 || lds_bytes > static_cast<size_t>(160 * 1024)) continue;
+            // order 1 adds a transposed copy of one frame per wave to LDS
+            const size_t lds_total = lds_bytes + (order == 1 ? static_cast<size_t>(wpb) * D * 4 : 0);
+            if (simd_waves < (wpb + 3) / 4 || lds_total > static_cast<size_t>(160 * 1024)) continue;
             const int64_t waves = (M + fw - 1) / fw;
             const int64_t blocks = (waves + wpb - 1) / wpb;
             const int64_t per_simd = ((blocks + cus - 1) / cus) * ((wpb * fw + 3) / 4);
@@ -573,6 +647,7 @@ struct aq_dac_stages {
     float margin = 0.0f;          // score-certificate margin
     int64_t img_f4 = 0;
     float4 *d_images = nullptr;   // [Q][img_f4]
+    float4 *d_images_tb = nullptr;   // the same with W_in in the tinyBLAS layout
     float *d_tables = nullptr;    // [Q][N][D]
 };
 
@@ -646,6 +721,21 @@ aq_status aq_dac_upload_ex(aq_ctx *ctx, int64_t Q, int64_t D, int64_t N, const f
         }
     }
 
+    // The same images with W_in in the tinyBLAS order's layout (see tb_sw).
+    std::vector<float> images_tb(images);
+    for (int64_t s = 0; s < Q; ++s) {
+        float *im = images_tb.data() + s * img * 4;
+        const float *Wi = w_in + s * 8 * D;
+        const int DI = static_cast<int>(D / kWave);
+        for (int j = 0; j < 8; ++j)
+            for (int t = 0; t < 16; ++t)
+                for (int u4 = 0; u4 < DI; ++u4) {
+                    const int sw = (DI & (DI - 1)) == 0 ? (u4 ^ (t & (DI - 1))) : u4;
+                    for (int c = 0; c < 4; ++c)
+                        im[((j * 16 + t) * DI + sw) * 4 + c] = Wi[j * D + 16 * (4 * u4 + c) + t];
+                }
+    }
+
     aq_dac_stages *st = new (std::nothrow) aq_dac_stages();
     if (!st) return aq_fail(ctx, AQ_E_NOMEM, "aq_dac_upload: host allocation failed");
     st->ctx = ctx;
@@ -677,6 +767,7 @@ aq_status aq_dac_upload_ex(aq_ctx *ctx, int64_t Q, int64_t D, int64_t N, const f
         if (d_bout) (void)hipFree(d_bout);
     };
     if (hipMalloc(&st->d_images, images.size() * sizeof(float)) != hipSuccess ||
+        hipMalloc(&st->d_images_tb, images_tb.size() * sizeof(float)) != hipSuccess ||
         (w_out && (hipMalloc(&st->d_tables, sizeof(float) * static_cast<size_t>(Q * N * D)) != hipSuccess ||
                    hipMalloc(&d_cb, sizeof(float) * static_cast<size_t>(Q * N * 8)) != hipSuccess ||
                    hipMalloc(&d_wout, sizeof(float) * static_cast<size_t>(Q * D * 8)) != hipSuccess ||
@@ -685,7 +776,9 @@ aq_status aq_dac_upload_ex(aq_ctx *ctx, int64_t Q, int64_t D, int64_t N, const f
         aq_dac_release(st);
         return aq_fail(ctx, AQ_E_NOMEM, "aq_dac_upload: device allocation failed");
     }
-    bool ok = hipMemcpyAsync(st->d_images, images.data(), images.size() * sizeof(float), hipMemcpyHostToDevice, ctx->stream) == hipSuccess;
+    bool ok = hipMemcpyAsync(st->d_images, images.data(), images.size() * sizeof(float), hipMemcpyHostToDevice, ctx->stream) == hipSuccess &&
+              hipMemcpyAsync(st->d_images_tb, images_tb.data(), images_tb.size() * sizeof(float), hipMemcpyHostToDevice,
+                             ctx->stream) == hipSuccess;
     if (w_out)
         ok = ok &&
              hipMemcpyAsync(d_cb, codebook, sizeof(float) * static_cast<size_t>(Q * N * 8), hipMemcpyHostToDevice, ctx->stream) == hipSuccess &&
@@ -713,6 +806,7 @@ aq_status aq_dac_release(aq_dac_stages *st) {
     {
         aq_device_guard g(st->ctx->device);
         if (st->d_images) (void)hipFree(st->d_images);
+        if (st->d_images_tb) (void)hipFree(st->d_images_tb);
         if (st->d_tables) (void)hipFree(st->d_tables);
     }
     delete st;
@@ -727,16 +821,19 @@ aq_status aq_dac_encode(aq_ctx *ctx, const aq_dac_stages *st, const float *x, in
         return aq_fail(ctx, AQ_E_SHAPE, "aq_dac_encode: M=%lld must be a non-negative multiple of clip_len=%lld",
                        (long long)M, (long long)clip_len);
     if (M == 0) return AQ_OK;
-    if (clip_len % 4 == 0)
-        return aq_fail(ctx, AQ_E_UNSUPPORTED,
-                       "aq_dac_encode: clip_len %% 4 == 0 selects ggml's tinyBLAS in-projection order, not built yet");
+    // ggml hands the in-projection (m = T rows, n = 8, k = D) to tinyBLAS when
+    // T % 4 == 0 (ggml-cpu.c:1285-1306, sgemm.cpp:3705-3725), otherwise each
+    // element is a ggml_vec_dot_f32.
+    const int order = clip_len % 4 == 0 ? 1 : 0;
     if (!st->d_tables && (residual || recon))
         return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_dac_encode: no out-projection was uploaded (codes only)");
     aq_device_guard g(ctx->device);
-    const size_t lds_bytes = static_cast<size_t>(st->lds_f4) * sizeof(float4);
-    const Shape shape = launch_shape(M, st->D, st->lds_f4, recon != nullptr, ctx->num_cus, lds_bytes, st->cbg);
+    const size_t img_bytes = static_cast<size_t>(st->lds_f4) * sizeof(float4);
+    const Shape shape = launch_shape(M, st->D, st->lds_f4, recon != nullptr, ctx->num_cus, img_bytes, st->cbg, order);
     const int fw = shape.fw;
-    EncodeFn fn = pick_kernel(st->D, fw, recon != nullptr, shape.prefetch, st->cbg);
+    EncodeFn fn = pick_kernel(st->D, fw, recon != nullptr, shape.prefetch, st->cbg, order);
+    const size_t lds_bytes =
+        img_bytes + (order == 1 ? static_cast<size_t>(shape.waves_per_block) * static_cast<size_t>(st->D) * 4 : 0);
     AQ_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void *>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
                                     static_cast<int>(lds_bytes)));
     if (force_idx) AQ_HIP(ctx, hipMemsetAsync(ctx->d_flags, 0, sizeof(int32_t) * AQ_FLAG_COUNT, ctx->stream));
@@ -744,7 +841,8 @@ aq_status aq_dac_encode(aq_ctx *ctx, const aq_dac_stages *st, const float *x, in
     const unsigned blocks = static_cast<unsigned>((M + frames_per_block - 1) / frames_per_block);
     const int tslot = aq_timing_start(ctx);
     hipLaunchKernelGGL(fn, dim3(blocks), dim3(shape.waves_per_block * kWave), lds_bytes, ctx->stream, x, M, static_cast<int>(st->Q),
-                       static_cast<int>(st->N), st->d_images, st->img_f4, st->lds_f4, st->d_tables, idx, residual, recon,
+                       static_cast<int>(st->N), order == 1 ? st->d_images_tb : st->d_images, st->img_f4, st->lds_f4,
+                       st->d_tables, idx, residual, recon,
                        force_idx, ctx->d_flags, st->has_bin ? 1 : 0, st->key_bits, st->margin, st->exact_only ? 1 : 0,
                        st->qeps);
     aq_timing_stop(ctx, tslot);

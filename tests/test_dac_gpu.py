@@ -218,7 +218,7 @@ def test_dac_launch_shapes(torch, ctx, oracle, M):
     D, N, Q = 1024, 1024, 2
     x = synth.normal(14, 1, (M, D))
     cfg = dict(kind="dac", B=1, T=M, D=D, Q=Q, N=N, x=x, **synth.dac_weights(14, Q, D, N, bias=True))
-    if M % 4 == 0:                       # keep the ggml vec_dot in-projection order (T % 4 != 0)
+    if M % 4 == 0:                       # one clip of M frames would select the tinyBLAS order
         cfg["T"] = M // 8 if (M // 8) % 4 else 1
         cfg["B"] = M // cfg["T"]
     out = run_gpu(torch, ctx, cfg)
@@ -308,3 +308,23 @@ def test_dac_vevo2_rejects_zero_codebook_row(torch, ctx):
     w["codebook"][0, 7] = 0.0
     with pytest.raises(aqmi.AqError):
         aqmi.DacStages(ctx, w["w_in"], None, w["codebook"], None, None, aqmi.DAC_VEVO2)
+
+
+@pytest.mark.parametrize("T,B,D", [(752, 2, 1024), (4, 3, 1024), (100, 2, 768), (8, 5, 64), (12, 4, 512)])
+def test_dac_tinyblas_inprojection(torch, ctx, oracle, T, B, D):
+    """Clip lengths that are a multiple of 4 make ggml compute the
+    in-projection with tinyBLAS (16 FMA accumulators over k = 16 u + t, then
+    _mm512_reduce_add_ps), the other summation order; codes, residual and
+    reconstruction bit for bit, including widths whose swizzle is off
+    (D = 768)."""
+    from aqmi import synth
+
+    print(f"[gpu] dac tinyblas T={T} B={B} D={D}", flush=True)
+    N, Q = 1024, 3
+    cfg = dict(kind="dac", B=B, T=T, D=D, Q=Q, N=N, x=synth.normal(45, 1, (B * T, D)),
+               **synth.dac_weights(45, Q, D, N, bias=True))
+    out = run_gpu(torch, ctx, cfg)
+    ref = oracle.dac_rvq(cfg)
+    assert np.array_equal(out["idx"], ref["idx"])
+    assert np.array_equal(_bits(out["residual"]), _bits(ref["residual"]))
+    assert np.array_equal(_bits(out["recon"]), _bits(ref["recon"]))
