@@ -218,3 +218,35 @@ def make_config(i: int, rows: int | None = None) -> dict:
         cb = np.stack([q8_0_random_codebook(5, 100 * s + 2, N, K) for s in range(Q)])
         return dict(kind="q8_0", seed=5, M=M, K=K, Q=Q, N=N, x=x, codebook_q8=cb, topk=4)
     raise ValueError(f"unknown config {i}")
+
+
+# --------------------------------------------------------------------------
+# Host-loop DAC quantizers (test shapes; not BASELINE configs)
+
+def outetts_config(M: int, seed: int = 11, D: int = 1024, Q: int = 2, N: int = 1024, bias: bool = True) -> dict:
+    """OuteTTS DAC quantizer inputs (dac.cpp:376-456 shapes: D = N = 1024,
+    Q = 2): x [M, D] ~N(0,1) and DAC-style weights with biases."""
+    x = normal(seed, 1, (M, D))
+    return dict(kind="outetts", seed=seed, M=M, D=D, Q=Q, N=N, x=x, **dac_weights(seed, Q, D, N, bias=bias))
+
+
+def moss_config(M: int, seed: int = 12, C: int = 768, R: int = 512, Q: int = 12, N: int = 1024) -> dict:
+    """MOSS RLFQ quantizer inputs (audio_tokenizer_quantizer.cpp, config
+    code_dim 768, rvq_dim 512, 12 x 1024 x 8): hidden [M, C] ~N(0,1); every
+    weight-normalised conv as (g ~U(0.5, 2), v ~N(0,1)); biases ~N(0, 0.1);
+    codebooks ~N(0,1)."""
+    def wn(stream, out_ch, in_ch, lead=()):
+        g = uniform(seed, stream, lead + (out_ch,), 0.5, 2.0)
+        v = normal(seed, stream + 1, lead + (out_ch, in_ch), 1.0)
+        return g, v
+    ip_g, ip_v = wn(10, R, C)
+    op_g, op_v = wn(20, C, R)
+    in_g, in_v = wn(30, 8, R, (Q,))
+    out_g, out_v = wn(40, R, 8, (Q,))
+    return dict(kind="moss", seed=seed, M=M, C=C, R=R, Q=Q, N=N,
+                hidden=normal(seed, 1, (M, C)),
+                ip_g=ip_g, ip_v=ip_v, ip_b=normal(seed, 12, (R,), 0.1),
+                op_g=op_g, op_v=op_v, op_b=normal(seed, 22, (C,), 0.1),
+                in_g=in_g, in_v=in_v, in_b=normal(seed, 32, (Q, 8), 0.1),
+                out_g=out_g, out_v=out_v, out_b=normal(seed, 42, (Q, R), 0.1),
+                codebook=normal(seed, 50, (Q, N, 8), 1.0))

@@ -98,6 +98,16 @@ class Oracle:
         L.aqo_gather_q8_0.argtypes = [C.c_void_p, _i64, _i64, _i32p, _i64, _f32p]
         L.aqo_ema_codebook.restype = C.c_int
         L.aqo_ema_codebook.argtypes = [_f32p, _f32p, _i64, _i64, _i64, C.c_float, _f32p]
+        L.aqo_outetts_rvq.argtypes = [_f32p, _i64, _i64, _i64, _i64, _f32p, C.c_void_p, _f32p, _f32p,
+                                      C.c_void_p, C.c_void_p, _i32p, _f32p]
+        L.aqo_moss_weight_norm.restype = None
+        L.aqo_moss_weight_norm.argtypes = [_f32p, _f32p, _i64, _i64, _f32p]
+        L.aqo_moss_normalize_rows.restype = None
+        L.aqo_moss_normalize_rows.argtypes = [_f32p, _i64, _i64, _f32p]
+        L.aqo_moss_rvq.argtypes = [_f32p, _i64, _i64, _i64, _i64, _i64, _f32p, _f32p, _f32p, _f32p, _f32p,
+                                   _f32p, _f32p, C.c_void_p, _i32p, C.c_void_p]
+        L.aqo_moss_decode.argtypes = [_i32p, _i64, _i64, _i64, _i64, _i64, _f32p, _f32p, _f32p, _f32p, _f32p,
+                                      _f32p]
 
     # -- whole path --------------------------------------------------------
     def dac_rvq(self, cfg: dict, force_idx=None, recon: bool = True, recipe: int = 0):
@@ -149,6 +159,74 @@ class Oracle:
         assert rc == 0
         return dict(idx=idx, residual=res, dist=dist)
 
+    def outetts_rvq(self, cfg: dict, force_idx=None):
+        """OuteTTS quantize_reference generalised to Q stages; codes and the
+        residual after the last stage."""
+        x = np.ascontiguousarray(cfg["x"], np.float32)
+        M, D = x.shape
+        Q, N = cfg["Q"], cfg["N"]
+        idx = np.zeros((M, Q), np.int32)
+        res = np.zeros((M, D), np.float32)
+        fi = np.ascontiguousarray(force_idx, np.int32) if force_idx is not None else None
+        rc = self.lib.aqo_outetts_rvq(x, M, D, Q, N, np.ascontiguousarray(cfg["w_in"], np.float32),
+                                      _opt(cfg.get("b_in"), np.float32), np.ascontiguousarray(cfg["codebook"], np.float32),
+                                      np.ascontiguousarray(cfg["w_out"], np.float32), _opt(cfg.get("b_out"), np.float32),
+                                      None if fi is None else fi.ctypes.data_as(C.c_void_p), idx, res)
+        assert rc == 0
+        return dict(idx=idx, residual=res)
+
+    def moss_weight_norm(self, g, v):
+        """reconstruct_weight_norm over the last two axes of v ([..., out, in])."""
+        v = np.ascontiguousarray(v, np.float32)
+        g = np.ascontiguousarray(g, np.float32)
+        out_ch, in_ch = v.shape[-2:]
+        lead = int(np.prod(v.shape[:-2], dtype=np.int64))
+        w = np.zeros_like(v)
+        vf, gf, wf = v.reshape(lead, out_ch, in_ch), g.reshape(lead, out_ch), w.reshape(lead, out_ch, in_ch)
+        for i in range(lead):
+            gi, vi, wi = np.ascontiguousarray(gf[i]), np.ascontiguousarray(vf[i]), np.zeros((out_ch, in_ch), np.float32)
+            self.lib.aqo_moss_weight_norm(gi, vi, out_ch, in_ch, wi)
+            wf[i] = wi
+        return w
+
+    def moss_fold(self, cfg: dict) -> dict:
+        """The folded conv weights the MOSS constructor builds from (g, v)."""
+        return dict(w_ip=self.moss_weight_norm(cfg["ip_g"], cfg["ip_v"]),
+                    w_in=self.moss_weight_norm(cfg["in_g"], cfg["in_v"]),
+                    w_out=self.moss_weight_norm(cfg["out_g"], cfg["out_v"]),
+                    w_op=self.moss_weight_norm(cfg["op_g"], cfg["op_v"]))
+
+    def moss_rvq(self, cfg: dict, force_idx=None, folded: dict | None = None):
+        """MOSS encode: codes [M, Q] and the fp64 residual [M, R]."""
+        f = folded or self.moss_fold(cfg)
+        h = np.ascontiguousarray(cfg["hidden"], np.float32)
+        M, Cd = h.shape
+        R, Q, N = cfg["R"], cfg["Q"], cfg["N"]
+        idx = np.zeros((M, Q), np.int32)
+        res = np.zeros((M, R), np.float64)
+        fi = np.ascontiguousarray(force_idx, np.int32) if force_idx is not None else None
+        a = lambda k: np.ascontiguousarray(cfg[k], np.float32)
+        rc = self.lib.aqo_moss_rvq(h, M, Cd, R, Q, N, f["w_ip"], a("ip_b"), f["w_in"], a("in_b"), a("codebook"),
+                                   f["w_out"], a("out_b"), None if fi is None else fi.ctypes.data_as(C.c_void_p),
+                                   idx, res.ctypes.data_as(C.c_void_p))
+        assert rc == 0
+        return dict(idx=idx, residual=res)
+
+    def moss_decode(self, cfg: dict, idx, folded: dict | None = None):
+        """MOSS dequantisation, frame-major latent [M, C]."""
+        f = folded or self.moss_fold(cfg)
+        idx = np.ascontiguousarray(idx, np.int32)
+        M = idx.shape[0]
+        Cd, R, Q, N = cfg["C"], cfg["R"], cfg["Q"], cfg["N"]
+        out = np.zeros((M, Cd), np.float32)
+        a = lambda k: np.ascontiguousarray(cfg[k], np.float32)
+        rc = self.lib.aqo_moss_decode(idx, M, Cd, R, Q, N, a("codebook"), f["w_out"], a("out_b"), f["w_op"],
+                                      a("op_b"), out)
+        if rc == -1:
+            raise IndexError("MOSS codec code index out of range")
+        assert rc == 0
+        return out
+
     def ema_codebook(self, embedding_sum, cluster_usage, eps: float = 1.0e-5):
         """codebook_embedding: sum / std::max(usage, eps), per stage [Q, N, K]."""
         es = np.ascontiguousarray(embedding_sum, np.float32)
@@ -195,6 +273,13 @@ class Oracle:
         return out
 
 
+class _MossWeights(C.Structure):
+    """MossWeights in ref_moss.cpp."""
+    _fields_ = [("C", C.c_int64), ("R", C.c_int64), ("Q", C.c_int64), ("N", C.c_int64)] + [
+        (n, C.POINTER(C.c_float)) for n in ("ip_g", "ip_v", "ip_b", "in_g", "in_v", "in_b", "cb", "out_g", "out_v",
+                                              "out_b", "op_g", "op_v", "op_b")]
+
+
 class Ref:
     """The reference's own ggml CPU backend (oracle/_ref)."""
 
@@ -225,6 +310,53 @@ class Ref:
         L.aqref_quantize_chunk_q8_0.argtypes = [_f32p, C.c_void_p, _i64, _i64]
         L.aqref_top_k.restype = None
         L.aqref_top_k.argtypes = [_f32p, _i64, _i64, C.c_int, _i32p, C.c_int]
+        L.aqref_outetts_rvq.restype = C.c_int
+        L.aqref_outetts_rvq.argtypes = [_f32p, _i64, _f32p, _f32p, _f32p, _f32p, _f32p, _i32p]
+        L.aqref_moss_encode.restype = C.c_int
+        L.aqref_moss_encode.argtypes = [C.POINTER(_MossWeights), _f32p, _i64, _i32p]
+        L.aqref_moss_decode.restype = C.c_int
+        L.aqref_moss_decode.argtypes = [C.POINTER(_MossWeights), _i32p, _i64, _f32p]
+
+    def outetts_rvq(self, cfg: dict):
+        """The reference's quantize_reference (2 stages, D = N = 1024): codes [M, 2]."""
+        x = np.ascontiguousarray(cfg["x"], np.float32)
+        M = x.shape[0]
+        assert cfg["Q"] == 2 and cfg["D"] == 1024 and cfg["N"] == 1024
+        a = lambda k: np.ascontiguousarray(cfg[k], np.float32)
+        idx = np.zeros((M, 2), np.int32)
+        rc = self.lib.aqref_outetts_rvq(x, M, a("w_in"), a("b_in"), a("codebook"), a("w_out"), a("b_out"), idx)
+        if rc != 0:
+            raise RuntimeError("OuteTTS DAC encoder produced invalid acoustic latents")
+        return idx
+
+    def _moss_weights(self, cfg: dict):
+        keep = {k: np.ascontiguousarray(cfg[k], np.float32) for k in
+                ("ip_g", "ip_v", "ip_b", "in_g", "in_v", "in_b", "codebook", "out_g", "out_v", "out_b",
+                 "op_g", "op_v", "op_b")}
+        p = lambda k: keep[k].ctypes.data_as(C.POINTER(C.c_float))
+        w = _MossWeights(cfg["C"], cfg["R"], cfg["Q"], cfg["N"], p("ip_g"), p("ip_v"), p("ip_b"), p("in_g"),
+                         p("in_v"), p("in_b"), p("codebook"), p("out_g"), p("out_v"), p("out_b"), p("op_g"),
+                         p("op_v"), p("op_b"))
+        return w, keep
+
+    def moss_encode(self, cfg: dict):
+        """MossAudioTokenizerQuantizer::encode: codes [M, Q]."""
+        w, keep = self._moss_weights(cfg)
+        h = np.ascontiguousarray(cfg["hidden"], np.float32)
+        idx = np.zeros((h.shape[0], cfg["Q"]), np.int32)
+        if self.lib.aqref_moss_encode(C.byref(w), h, h.shape[0], idx) != 0:
+            raise RuntimeError("MOSS codec quantizer rejected its input")
+        return idx
+
+    def moss_decode(self, cfg: dict, idx):
+        """MossAudioTokenizerQuantizer::decode, returned frame-major [M, C]."""
+        w, keep = self._moss_weights(cfg)
+        idx = np.ascontiguousarray(idx, np.int32)
+        M = idx.shape[0]
+        out = np.zeros((cfg["C"], M), np.float32)
+        if self.lib.aqref_moss_decode(C.byref(w), idx, M, out) != 0:
+            raise IndexError("MOSS codec code index out of range")
+        return np.ascontiguousarray(out.T)
 
     def top_k(self, v, k: int, threads: int = 8):
         """ggml_top_k over the rows of v, in ggml's order."""

@@ -541,3 +541,179 @@ int aqo_dac_rvq(const float *x, int64_t B, int64_t T, int64_t D, int64_t Q, int6
                 int32_t *idx, float *residual, float *recon) {
     return aqo_dac_rvq_ex(x, B, T, D, Q, N, w_in, b_in, cb, w_out, b_out, force_idx, idx, residual, recon, 0);
 }
+
+/* ------------------------------------------------------------------------
+ * Host-loop DAC quantizers.  The reference builds its engine code without
+ * -march (reference CMakeLists.txt: only ggml gets the native ISA flags), so
+ * x86-64 has no FMA there and every product below is rounded before it is
+ * added; this file is compiled with -ffp-contract=off to match.
+ * ------------------------------------------------------------------------ */
+
+/* quantize_reference, src/community_models/outetts/dac.cpp:376-456. */
+int aqo_outetts_rvq(const float *x, int64_t M, int64_t D, int64_t Q, int64_t N,
+                    const float *w_in, const float *b_in, const float *cb,
+                    const float *w_out, const float *b_out, const int32_t *force_idx,
+                    int32_t *idx, float *residual) {
+    float *r = residual;
+    memcpy(r, x, (size_t)(M * D) * sizeof(float));
+    for (int64_t s = 0; s < Q; ++s) {
+        const float *W = w_in + s * 8 * D;
+        const float *C = cb + s * N * 8;
+        const float *Wo = w_out + s * D * 8;
+        for (int64_t m = 0; m < M; ++m) {
+            float *rm = r + m * D;
+            float p[8];
+            float nsq = 0.0f;                              /* :399-411 */
+            for (int d = 0; d < 8; ++d) {
+                float v = b_in ? b_in[s * 8 + d] : 0.0f;
+                for (int64_t h = 0; h < D; ++h) v = v + W[d * D + h] * rm[h];
+                p[d] = v;
+                nsq = nsq + v * v;
+            }
+            const float pn = sqrtf(nsq) + 1.0e-12f;        /* :412 */
+            int32_t best = 0;
+            float best_d = INFINITY;
+            for (int64_t n = 0; n < N; ++n) {              /* :415-434 */
+                float e2 = 0.0f;
+                for (int d = 0; d < 8; ++d) e2 = e2 + C[n * 8 + d] * C[n * 8 + d];
+                const float en = sqrtf(e2) + 1.0e-12f;
+                float dist = 0.0f;
+                for (int d = 0; d < 8; ++d) {
+                    const float diff = p[d] / pn - C[n * 8 + d] / en;
+                    dist = dist + diff * diff;
+                }
+                if (dist < best_d) { best_d = dist; best = (int32_t)n; }
+            }
+            idx[m * Q + s] = best;
+            const int64_t use = force_idx ? force_idx[m * Q + s] : best;
+            for (int64_t o = 0; o < D; ++o) {              /* :438-453 */
+                float v = b_out ? b_out[s * D + o] : 0.0f;
+                for (int d = 0; d < 8; ++d) v = v + Wo[o * 8 + d] * C[use * 8 + d];
+                rm[o] = rm[o] - v;
+            }
+        }
+    }
+    return 0;
+}
+
+/* reconstruct_weight_norm, src/models/moss/shared/audio_tokenizer_quantizer.cpp:17-39. */
+void aqo_moss_weight_norm(const float *g, const float *v, int64_t out_ch, int64_t in_ch, float *w) {
+    for (int64_t o = 0; o < out_ch; ++o) {
+        double norm = 0.0;
+        for (int64_t k = 0; k < in_ch; ++k) {
+            const double value = v[o * in_ch + k];
+            norm = norm + value * value;
+        }
+        const float scale = (float)(g[o] / sqrt(norm));
+        for (int64_t k = 0; k < in_ch; ++k) w[o * in_ch + k] = v[o * in_ch + k] * scale;
+    }
+}
+
+/* std::max(a, b) for doubles: (a < b) ? b : a (a NaN stays). */
+static double aqo_std_max_d(double a, double b) { return (a < b) ? b : a; }
+
+/* MossAudioTokenizerQuantizer constructor, :116-130. */
+void aqo_moss_normalize_rows(const float *cb, int64_t rows, int64_t dim, float *out) {
+    for (int64_t n = 0; n < rows; ++n) {
+        double norm = 0.0;
+        for (int64_t k = 0; k < dim; ++k) norm = norm + (double)cb[n * dim + k] * (double)cb[n * dim + k];
+        const double scale = 1.0 / aqo_std_max_d(sqrt(norm), 1.0e-12);
+        for (int64_t k = 0; k < dim; ++k) out[n * dim + k] = (float)(cb[n * dim + k] * scale);
+    }
+}
+
+/* MossAudioTokenizerQuantizer::encode, :174-271. */
+int aqo_moss_rvq(const float *hidden, int64_t M, int64_t C, int64_t R, int64_t Q, int64_t N,
+                 const float *w_ip, const float *b_ip, const float *w_in, const float *b_in,
+                 const float *cb, const float *w_out, const float *b_out, const int32_t *force_idx,
+                 int32_t *idx, double *residual) {
+    float *tn = (float *)malloc((size_t)(Q * N * 8) * sizeof(float));
+    double *r = (double *)malloc((size_t)R * sizeof(double));
+    if (!tn || !r) { free(tn); free(r); return -1; }
+    aqo_moss_normalize_rows(cb, Q * N, 8, tn);
+    for (int64_t m = 0; m < M; ++m) {
+        const float *h = hidden + m * C;
+        for (int64_t o = 0; o < R; ++o) {                  /* input_proj, :193-201 */
+            double sum = b_ip[o];
+            for (int64_t k = 0; k < C; ++k) sum = sum + (double)w_ip[o * C + k] * (double)h[k];
+            r[o] = sum;
+        }
+        for (int64_t s = 0; s < Q; ++s) {
+            double enc[8];
+            double enc_norm = 0.0;                         /* in_proj + norm, :207-221 */
+            for (int c = 0; c < 8; ++c) {
+                double sum = b_in[s * 8 + c];
+                const float *row = w_in + (s * 8 + c) * R;
+                for (int64_t k = 0; k < R; ++k) sum = sum + (double)row[k] * r[k];
+                enc[c] = sum;
+                enc_norm = enc_norm + sum * sum;
+            }
+            const double enc_scale = 1.0 / aqo_std_max_d(sqrt(enc_norm), 1.0e-12);
+            for (int c = 0; c < 8; ++c) enc[c] = enc[c] * enc_scale;
+            int32_t best = 0;                              /* :225-237 */
+            double best_dot = -INFINITY;
+            const float *T = tn + s * N * 8;
+            for (int64_t n = 0; n < N; ++n) {
+                double dot = 0.0;
+                for (int c = 0; c < 8; ++c) dot = dot + (double)T[n * 8 + c] * enc[c];
+                if (dot > best_dot) { best_dot = dot; best = (int32_t)n; }
+            }
+            idx[m * Q + s] = best;
+            const int64_t use = force_idx ? force_idx[m * Q + s] : best;
+            const float *emb = cb + (s * N + use) * 8;     /* :240-248 */
+            for (int64_t o = 0; o < R; ++o) {
+                double sum = b_out[s * R + o];
+                const float *row = w_out + (s * R + o) * 8;
+                for (int k = 0; k < 8; ++k) sum = sum + (double)row[k] * (double)emb[k];
+                r[o] = r[o] - sum;
+            }
+        }
+        if (residual) memcpy(residual + m * R, r, (size_t)R * sizeof(double));
+    }
+    free(tn); free(r);
+    return 0;
+}
+
+/* MossAudioTokenizerQuantizer::decode, :139-172, with the constructor's
+ * combined out-projection and latent tables, :77-115. */
+int aqo_moss_decode(const int32_t *idx, int64_t M, int64_t C, int64_t R, int64_t Q, int64_t N,
+                    const float *cb, const float *w_out, const float *b_out,
+                    const float *w_op, const float *b_op, float *latent) {
+    for (int64_t i = 0; i < M * Q; ++i)
+        if (idx[i] < 0 || idx[i] >= N) return -1;
+    float *cbias = (float *)malloc((size_t)C * sizeof(float));
+    float *cw = (float *)malloc((size_t)(C * 8) * sizeof(float));
+    float *table = (float *)malloc((size_t)(Q * N * C) * sizeof(float));
+    if (!cbias || !cw || !table) { free(cbias); free(cw); free(table); return -2; }
+    for (int64_t s = 0; s < Q; ++s) {
+        const float *Wo = w_out + s * R * 8;
+        const float *bo = b_out + s * R;
+        for (int64_t o = 0; o < C; ++o) {
+            const float *orow = w_op + o * R;
+            float bsum = 0.0f;
+            for (int64_t k = 0; k < R; ++k) bsum = bsum + orow[k] * bo[k];
+            cbias[o] = bsum;
+            for (int k = 0; k < 8; ++k) {
+                float sum = 0.0f;
+                for (int64_t j = 0; j < R; ++j) sum = sum + orow[j] * Wo[j * 8 + k];
+                cw[o * 8 + k] = sum;
+            }
+        }
+        for (int64_t n = 0; n < N; ++n) {
+            const float *e = cb + (s * N + n) * 8;
+            for (int64_t o = 0; o < C; ++o) {
+                float sum = cbias[o];
+                for (int k = 0; k < 8; ++k) sum = sum + cw[o * 8 + k] * e[k];
+                table[(s * N + n) * C + o] = sum;
+            }
+        }
+    }
+    for (int64_t m = 0; m < M; ++m)
+        for (int64_t o = 0; o < C; ++o) {
+            float v = b_op[o];
+            for (int64_t s = 0; s < Q; ++s) v = v + table[(s * N + idx[m * Q + s]) * C + o];
+            latent[m * C + o] = v;
+        }
+    free(cbias); free(cw); free(table);
+    return 0;
+}

@@ -89,6 +89,46 @@ int aqo_gather_f32(const float *cb, int64_t N, int64_t K, const int32_t *idx, in
  * cb[q,n,k] = embedding_sum[q,n,k] / std::max(cluster_usage[q,n], eps). */
 int aqo_ema_codebook(const float *embedding_sum, const float *cluster_usage, int64_t Q, int64_t N, int64_t K,
                      float eps, float *cb);
+/* OuteTTS DAC host quantizer (quantize_reference,
+ * src/community_models/outetts/dac.cpp:376-456), generalised to Q stages,
+ * D latent channels, N codes of dim 8: fp32, every product rounded before it
+ * is added (the reference's engine code is built without FMA), bias first,
+ * first index of the minimum of |p/|p|' - c/|c|'|^2 with |v|' = sqrt(.)+1e-12.
+ * b_in / b_out may be NULL (zeros).  x [M,D], w_in [Q,8,D], cb [Q,N,8],
+ * w_out [Q,D,8]; idx [M,Q]; residual [M,D] (required). */
+int aqo_outetts_rvq(const float *x, int64_t M, int64_t D, int64_t Q, int64_t N,
+                    const float *w_in, const float *b_in, const float *cb,
+                    const float *w_out, const float *b_out, const int32_t *force_idx,
+                    int32_t *idx, float *residual);
+
+/* MOSS weight-norm reconstruction (reconstruct_weight_norm,
+ * src/models/moss/shared/audio_tokenizer_quantizer.cpp:17-39):
+ * w[o,k] = v[o,k] * (float)(g[o] / sqrt(sum_k (double)v[o,k]^2)). */
+void aqo_moss_weight_norm(const float *g, const float *v, int64_t out_ch, int64_t in_ch, float *w);
+
+/* MOSS codebook row normalisation (constructor, :116-130):
+ * row * (1 / max(sqrt(sum (double)c^2), 1e-12)) in double, stored as float. */
+void aqo_moss_normalize_rows(const float *cb, int64_t rows, int64_t dim, float *out);
+
+/* MOSS RLFQ encode (MossAudioTokenizerQuantizer::encode, :174-271): fp64
+ * input projection [C -> R], then per stage an fp64 in-projection [R -> 8],
+ * L2 normalisation with max(|e|, 1e-12), the first index of the maximum dot
+ * with the normalised codebook, and the fp64 residual update by the
+ * out-projection of the raw codebook row.  hidden [M,C], w_ip [R,C], b_ip [R],
+ * w_in [Q,8,R], b_in [Q,8], cb [Q,N,8] (raw), w_out [Q,R,8], b_out [Q,R];
+ * idx [M,Q]; residual [M,R] doubles (nullable). */
+int aqo_moss_rvq(const float *hidden, int64_t M, int64_t C, int64_t R, int64_t Q, int64_t N,
+                 const float *w_ip, const float *b_ip, const float *w_in, const float *b_in,
+                 const float *cb, const float *w_out, const float *b_out, const int32_t *force_idx,
+                 int32_t *idx, double *residual);
+
+/* MOSS dequantisation (MossAudioTokenizerQuantizer::decode, :139-172 with the
+ * constructor's latent tables, :77-115): latent[m,c] = b_op[c] + sum over
+ * stages of table_q[idx[m,q], c] in fp32, frame-major [M,C].  w_op [C,R].
+ * Returns -1 on an out-of-range code. */
+int aqo_moss_decode(const int32_t *idx, int64_t M, int64_t C, int64_t R, int64_t Q, int64_t N,
+                    const float *cb, const float *w_out, const float *b_out,
+                    const float *w_op, const float *b_op, float *latent);
 int aqo_gather_q8_0(const aqo_block_q8_0 *cb, int64_t N, int64_t K, const int32_t *idx, int64_t M, float *out);
 
 #ifdef __cplusplus

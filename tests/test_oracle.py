@@ -420,3 +420,92 @@ def test_ema_codebook_closed_form(o):
     back = (out * cu[:, :, None]).astype(np.float64)
     err = np.abs(back - es) / np.maximum(np.abs(es), 1e-30)
     assert (err[rest] <= 2.5 * 2.0 ** -24).all()
+
+
+# ------------------------------------------------- host-loop DAC quantizers --
+
+def _near_duplicate_pairs(cb, seed):
+    """Odd codes = the even code before them with one component moved by one
+    ulp: the winner between the two depends on every rounding of the
+    distance, so an arithmetic slip (a fused multiply-add, another order)
+    changes codes."""
+    cb = np.array(cb, np.float32, copy=True)
+    rng = np.random.default_rng(seed)
+    for s in range(cb.shape[0]):
+        half = cb.shape[1] // 2
+        cb[s, 1::2] = cb[s, 0::2]
+        k = rng.integers(0, cb.shape[2], half)
+        rows = cb[s, 1::2]
+        rows[np.arange(half), k] = np.nextafter(rows[np.arange(half), k], np.float32(np.inf))
+        cb[s, 1::2] = rows
+    return cb
+
+
+@pytest.mark.parametrize("M,near_dup", [(1, False), (300, False), (2000, True)])
+def test_oracle_outetts_bit_exact_vs_reference(o, ref, M, near_dup):
+    cfg = synth.outetts_config(M)
+    if near_dup:
+        cfg["codebook"] = _near_duplicate_pairs(cfg["codebook"], 7)
+    assert np.array_equal(o.outetts_rvq(cfg)["idx"], ref.outetts_rvq(cfg))
+
+
+def test_outetts_pin_detects_fused_multiply_add(ref, tmp_path):
+    """The near-duplicate comparison is not vacuous: the same restatement
+    built with contraction (FMA) disagrees with the reference."""
+    import shutil
+    import subprocess
+    from oracle import HERE
+    if not shutil.which("gcc") or " fma " not in open("/proc/cpuinfo").read():
+        pytest.skip("needs gcc and an FMA-capable host")
+    so = tmp_path / "liboracle_fma.so"
+    subprocess.run(["gcc", "-O2", "-fPIC", "-ffp-contract=fast", "-mfma", "-std=c11", "-shared", "-o", str(so),
+                    str(HERE / "aq_oracle.c"), "-lm"], check=True)
+    cfg = synth.outetts_config(2000)
+    cfg["codebook"] = _near_duplicate_pairs(cfg["codebook"], 7)
+    wrong = Oracle(so).outetts_rvq(cfg)["idx"]
+    assert (wrong != ref.outetts_rvq(cfg)).sum() > 10
+
+
+@pytest.mark.parametrize("M", [1, 37])
+def test_oracle_moss_bit_exact_vs_reference(o, ref, M):
+    cfg = synth.moss_config(M, Q=4, N=256)
+    out = o.moss_rvq(cfg)
+    assert np.array_equal(out["idx"], ref.moss_encode(cfg))
+    assert _beq(o.moss_decode(cfg, out["idx"]), ref.moss_decode(cfg, out["idx"]))
+
+
+def test_oracle_moss_full_shape_vs_reference(o, ref):
+    """The MOSS-Audio-Tokenizer-v2 shape: 768 -> 512, 12 x 1024 x 8."""
+    cfg = synth.moss_config(24)
+    out = o.moss_rvq(cfg)
+    assert np.array_equal(out["idx"], ref.moss_encode(cfg))
+    assert _beq(o.moss_decode(cfg, out["idx"]), ref.moss_decode(cfg, out["idx"]))
+
+
+def test_oracle_moss_zero_projection_takes_first_code(o, ref):
+    """A stage whose in-projection is zero (g = 0, zero bias): the encoding is
+    0 / max(0, 1e-12) = 0, every dot is 0 and the first code wins."""
+    cfg = synth.moss_config(9, Q=3, N=128)
+    cfg["in_g"][1] = 0.0
+    cfg["in_b"][1] = 0.0
+    out = o.moss_rvq(cfg)
+    assert (out["idx"][:, 1] == 0).all()
+    assert np.array_equal(out["idx"], ref.moss_encode(cfg))
+
+
+def test_oracle_moss_weight_norm_closed_form(o):
+    """w = g v / |v| row-wise: rows of w have norm g (to fp32 rounding)."""
+    g = synth.uniform(3, 1, (16,), 0.5, 2.0)
+    v = synth.normal(3, 2, (16, 40))
+    w = o.moss_weight_norm(g, v)
+    np.testing.assert_allclose(np.linalg.norm(w.astype(np.float64), axis=1), g, rtol=1e-6)
+    assert (np.sign(w) == np.sign(v)).all()
+
+
+def test_oracle_moss_decode_range(o, ref):
+    cfg = synth.moss_config(2, Q=2, N=64)
+    bad = np.array([[0, 64], [1, 2]], np.int32)
+    with pytest.raises(IndexError):
+        o.moss_decode(cfg, bad)
+    with pytest.raises(IndexError):
+        ref.moss_decode(cfg, bad)
