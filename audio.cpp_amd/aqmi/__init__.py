@@ -30,12 +30,13 @@ EXPORTED = [
     "aq_euclid_upload", "aq_euclid_release", "aq_euclid_encode", "aq_euclid_failures", "aq_euclid_exact_scans",
     "aq_codebook_gather", "aq_ema_codebook", "aq_euclid_upload_ema",
     "aq_euclid_decode", "aq_ctx_set_timing", "aq_ctx_read_timing",
+    "aq_moss_upload", "aq_moss_release", "aq_moss_encode", "aq_moss_decode",
 ]
 
 # aq_euclid_recipe / aq_codebook_type
 OMNIVOICE, HIGGS, DIRECT = 0, 1, 2
 # aq_dac_recipe
-DAC_FISH, DAC_INDEXTTS2, DAC_VEVO2 = 0, 1, 2
+DAC_FISH, DAC_INDEXTTS2, DAC_VEVO2, DAC_OUTETTS = 0, 1, 2, 3
 CB_F32, CB_Q8_0 = 0, 1
 
 
@@ -74,6 +75,10 @@ def load_library(path: str | pathlib.Path | None = None) -> C.CDLL:
     lib.aq_ema_codebook.argtypes = [vp, vp, vp, i64, i64, i64, C.c_float, vp]
     lib.aq_euclid_upload_ema.argtypes = [vp, i64, i64, i64, vp, vp, C.c_float, C.c_int, C.POINTER(vp)]
     lib.aq_euclid_decode.argtypes = [vp, vp, vp, i64, vp]
+    lib.aq_moss_upload.argtypes = [vp, i64, i64, i64, i64] + [vp] * 9 + [C.POINTER(vp)]
+    lib.aq_moss_release.argtypes = [vp]
+    lib.aq_moss_encode.argtypes = [vp, vp, vp, i64, vp, vp, vp]
+    lib.aq_moss_decode.argtypes = [vp, vp, vp, i64, vp]
     for name in EXPORTED:
         fn = getattr(lib, name)
         if name not in ("aq_abi_version", "aq_last_error"):
@@ -148,8 +153,9 @@ class Context:
 
 class DacStages:
     """Uploaded DAC RVQ weights (aq_dac_upload_ex).  recipe: DAC_FISH,
-    DAC_INDEXTTS2 or DAC_VEVO2 (query / codebook normalisation); w_out None
-    uploads a codes-only single stage."""
+    DAC_INDEXTTS2 or DAC_VEVO2 (query / codebook normalisation of the ggml
+    graphs), or DAC_OUTETTS (the OuteTTS fp32 host loop); w_out None uploads
+    a codes-only single stage."""
 
     def __init__(self, ctx: Context, w_in, b_in, codebook, w_out, b_out, recipe: int = 0):
         self.ctx = ctx
@@ -179,6 +185,48 @@ class DacStages:
     def close(self):
         if getattr(self, "h", None):
             self.ctx.lib.aq_dac_release(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class MossQuantizer:
+    """MOSS RLFQ quantizer (aq_moss_upload): folded conv weights as the
+    reference's constructor builds them; output_w / output_b None = encode
+    only.  Shapes: input_w [R, C], input_b [R], in_w [Q, 8, R], in_b [Q, 8],
+    codebook [Q, N, 8], out_w [Q, R, 8], out_b [Q, R], output_w [C, R],
+    output_b [C]."""
+
+    def __init__(self, ctx: Context, input_w, input_b, in_w, in_b, codebook, out_w, out_b, output_w=None,
+                 output_b=None):
+        self.ctx = ctx
+        f = lambda a: None if a is None else np.ascontiguousarray(a, np.float32)
+        arrs = [f(a) for a in (input_w, input_b, in_w, in_b, codebook, out_w, out_b, output_w, output_b)]
+        self.R, self.C = arrs[0].shape
+        self.Q, self.N = arrs[4].shape[:2]
+        h = C.c_void_p()
+        ctx.check(ctx.lib.aq_moss_upload(ctx.h, self.Q, self.N, self.C, self.R, *[_host_ptr(a) for a in arrs],
+                                         C.byref(h)))
+        self.h = h
+
+    def encode(self, hidden, idx, residual=None, force_idx=None):
+        """hidden [M, C] f32, idx [M, Q] i32, residual [M, R] f64 (device)."""
+        self.ctx.use_current_stream()
+        self.ctx.check(self.ctx.lib.aq_moss_encode(self.ctx.h, self.h, _dptr(hidden), hidden.shape[0], _dptr(idx),
+                                                   _dptr(residual), _dptr(force_idx)))
+
+    def decode(self, idx, out):
+        """idx [M, Q] i32 -> out [M, C] f32 (device)."""
+        self.ctx.use_current_stream()
+        self.ctx.check(self.ctx.lib.aq_moss_decode(self.ctx.h, self.h, _dptr(idx), idx.shape[0], _dptr(out)))
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.ctx.lib.aq_moss_release(self.h)
             self.h = None
 
     def __del__(self):

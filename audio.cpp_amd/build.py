@@ -7,7 +7,8 @@ hipcc compiles every HIP / C++ source in csrc/ for gfx950 only.  Flags:
                          bit-identical to the ggml CPU backend.
   -fno-gpu-flush-denormals-to-zero   IEEE fp32 subnormals, as on the CPU.
   -target-feature -packed-fp32-ops   no v_pk_{add,mul,fma}_f32 generation.
-Usage: python audio.cpp_amd/build.py [--jobs N]
+Usage: python audio.cpp_amd/build.py [--jobs N] [--changed]
+(--changed recompiles only sources newer than their objects.)
 """
 
 from __future__ import annotations
@@ -48,11 +49,25 @@ def compile_one(src: pathlib.Path) -> pathlib.Path:
     return obj
 
 
-def build(jobs: int | None = None) -> pathlib.Path:
+def _stale(src: pathlib.Path) -> bool:
+    """Object missing or older than its source or any shared header."""
+    obj = BUILD / (src.name + ".o")
+    if not obj.exists():
+        return True
+    deps = [src, *CSRC.glob("*.hpp"), *(ROOT / "include").glob("*.h")]
+    return max(d.stat().st_mtime for d in deps) > obj.stat().st_mtime
+
+
+def build(jobs: int | None = None, changed_only: bool = False) -> pathlib.Path:
+    """Compile every source (or, with changed_only, the stale ones) and link."""
     BUILD.mkdir(exist_ok=True)
     srcs = sources()
-    with cf.ThreadPoolExecutor(max_workers=jobs or min(8, len(srcs))) as ex:
-        objs = list(ex.map(compile_one, srcs))
+    if changed_only:
+        srcs = [s for s in srcs if _stale(s)]
+    if srcs:
+        with cf.ThreadPoolExecutor(max_workers=jobs or min(8, len(srcs))) as ex:
+            list(ex.map(compile_one, srcs))
+    objs = [BUILD / (s.name + ".o") for s in sources()]
     tmp = OUT.with_suffix(".so.tmp")
     cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     subprocess.run(cmd, check=True)
@@ -64,4 +79,4 @@ if __name__ == "__main__":
     jobs = None
     if "--jobs" in sys.argv:
         jobs = int(sys.argv[sys.argv.index("--jobs") + 1])
-    print(build(jobs))
+    print(build(jobs, changed_only="--changed" in sys.argv))

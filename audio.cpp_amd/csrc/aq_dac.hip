@@ -44,6 +44,7 @@
 //    it is tabulated per stage at upload time with the reference's arithmetic
 //    (sequential non-fused 8-term sum, then the bias) and gathered per frame:
 //    a coalesced 4*D-byte row read from L2/MALL instead of 2*8*D flops.
+#include "aq_device_math.hpp"
 #include "aq_internal.hpp"
 
 #include <algorithm>
@@ -64,23 +65,7 @@ __device__ inline float uniform_f(float v) {
 }
 __device__ inline int uniform_i(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
-// Correctly rounded fp32 square root.  v_sqrt_f32 is accurate to 1 ulp only
-// (hipcc lowers __fsqrt_rn to it), so the estimate is corrected with
-// Tuckerman's rounding test: the residuals x - s_dn*s and x - s_up*s, exact
-// under FMA, tell which of s_dn, s, s_up is sqrt(x) rounded to nearest.
-// Inputs here are >= 1e-12 (normal); zero, Inf and NaN pass through.
-__device__ inline float sqrt_rn(float x) {
-    const float s = __builtin_amdgcn_sqrtf(x);
-    if (!(x > 0.0f) || !(s < INFINITY)) return s;
-    const float sd = __int_as_float(__float_as_int(s) - 1);
-    const float su = __int_as_float(__float_as_int(s) + 1);
-    const float rd = __fmaf_rn(-sd, s, x);
-    const float ru = __fmaf_rn(-su, s, x);
-    float out = s;
-    if (rd <= 0.0f) out = sd;
-    if (ru > 0.0f) out = su;
-    return out;
-}
+using aq_math::sqrt_rn;   // correctly rounded fp32 square root
 
 // v + v[lane rotated by N inside its 16-lane row] (DPP row_ror).
 template <int N>
@@ -649,7 +634,78 @@ struct aq_dac_stages {
     float4 *d_images = nullptr;   // [Q][img_f4]
     float4 *d_images_tb = nullptr;   // the same with W_in in the tinyBLAS layout
     float *d_tables = nullptr;    // [Q][N][D]
+    // OuteTTS host-loop recipe: raw weights, one allocation
+    float *d_ot = nullptr;
+    aq_outetts_args ot{};         // the weight pointers into d_ot
 };
+
+namespace {
+
+// The OuteTTS recipe keeps the raw weights: its host loop recomputes
+// everything per frame in sequential fp32 (aq_hostloop.hip).  The decode
+// tables are the Fish ones (its decoder graph is the same 1x1 conv).
+aq_status upload_outetts(aq_ctx *ctx, int64_t Q, int64_t D, int64_t N, const float *w_in, const float *b_in,
+                         const float *codebook, const float *w_out, const float *b_out, aq_dac_stages **out) {
+    if (!w_out) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_dac_upload: the OuteTTS recipe needs the out-projection");
+    if (Q <= 0 || D <= 0 || D % kWave != 0 || D > 2048 || N <= 0 || N % 8 != 0 || N > (int64_t{1} << 20))
+        return aq_fail(ctx, AQ_E_SHAPE,
+                       "aq_dac_upload: unsupported OuteTTS shape Q=%lld D=%lld N=%lld (D a multiple of 64 up to 2048, "
+                       "N a multiple of 8)",
+                       (long long)Q, (long long)D, (long long)N);
+    aq_device_guard g(ctx->device);
+    const int64_t sizes[] = {Q * 8 * D, Q * 8, Q * N * 8, Q * N * 8, Q * D * 8, Q * D};
+    int64_t total = 0;
+    for (int64_t v : sizes) total += (v + 63) / 64 * 64;
+    auto *st = new aq_dac_stages();
+    st->ctx = ctx;
+    st->Q = Q;
+    st->D = D;
+    st->N = N;
+    st->recipe = AQ_DAC_OUTETTS;
+    st->has_bin = b_in != nullptr;
+    bool ok = hipMalloc(&st->d_ot, static_cast<size_t>(total) * sizeof(float)) == hipSuccess &&
+              hipMalloc(&st->d_tables, static_cast<size_t>(Q * N * D) * sizeof(float)) == hipSuccess;
+    std::vector<float> zeros;
+    if (ok) {
+        float *slot[6];
+        int64_t off = 0;
+        for (int i = 0; i < 6; ++i) {
+            slot[i] = st->d_ot + off;
+            off += (sizes[i] + 63) / 64 * 64;
+        }
+        zeros.assign(static_cast<size_t>(std::max(Q * 8, Q * D)), 0.0f);
+        const float *src[6] = {w_in, b_in ? b_in : zeros.data(), codebook, nullptr, w_out, b_out ? b_out : zeros.data()};
+        for (int i = 0; i < 6 && ok; ++i)
+            if (src[i])
+                ok = hipMemcpyAsync(slot[i], src[i], static_cast<size_t>(sizes[i]) * sizeof(float), hipMemcpyHostToDevice,
+                                    ctx->stream) == hipSuccess;
+        ok = ok && aq_outetts_prepare(ctx, slot[2], Q * N, slot[3]) == AQ_OK;
+        for (int64_t s = 0; s < Q && ok; ++s) {
+            const unsigned blocks = static_cast<unsigned>((N * D + 255) / 256);
+            hipLaunchKernelGGL(dac_table_kernel, dim3(blocks), dim3(256), 0, ctx->stream, slot[2] + s * N * 8,
+                               slot[4] + s * D * 8, b_out ? slot[5] + s * D : nullptr, N, D, st->d_tables + s * N * D);
+            ok = hipGetLastError() == hipSuccess;
+        }
+        st->ot.w_in = slot[0];
+        st->ot.b_in = slot[1];
+        st->ot.cb = slot[2];
+        st->ot.chat = slot[3];
+        st->ot.w_out = slot[4];
+        st->ot.b_out = slot[5];
+        st->ot.D = static_cast<int>(D);
+        st->ot.N = static_cast<int>(N);
+        st->ot.Q = static_cast<int>(Q);
+    }
+    ok = hipStreamSynchronize(ctx->stream) == hipSuccess && ok;
+    if (!ok) {
+        aq_dac_release(st);
+        return aq_fail(ctx, AQ_E_DEVICE, "aq_dac_upload: device copy or OuteTTS preparation failed");
+    }
+    *out = st;
+    return AQ_OK;
+}
+
+}  // namespace
 
 extern "C" {
 
@@ -663,6 +719,7 @@ aq_status aq_dac_upload_ex(aq_ctx *ctx, int64_t Q, int64_t D, int64_t N, const f
                            aq_dac_stages **out) {
     if (!ctx || !out || !w_in || !codebook) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_dac_upload: null argument");
     *out = nullptr;
+    if (recipe == AQ_DAC_OUTETTS) return upload_outetts(ctx, Q, D, N, w_in, b_in, codebook, w_out, b_out, out);
     if (recipe < AQ_DAC_FISH || recipe > AQ_DAC_VEVO2)
         return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_dac_upload: unknown recipe %d", recipe);
     if (!w_out && Q != 1)
@@ -808,6 +865,7 @@ aq_status aq_dac_release(aq_dac_stages *st) {
         if (st->d_images) (void)hipFree(st->d_images);
         if (st->d_images_tb) (void)hipFree(st->d_images_tb);
         if (st->d_tables) (void)hipFree(st->d_tables);
+        if (st->d_ot) (void)hipFree(st->d_ot);
     }
     delete st;
     return AQ_OK;
@@ -821,6 +879,31 @@ aq_status aq_dac_encode(aq_ctx *ctx, const aq_dac_stages *st, const float *x, in
         return aq_fail(ctx, AQ_E_SHAPE, "aq_dac_encode: M=%lld must be a non-negative multiple of clip_len=%lld",
                        (long long)M, (long long)clip_len);
     if (M == 0) return AQ_OK;
+    if (st->recipe == AQ_DAC_OUTETTS) {
+        if (recon)
+            return aq_fail(ctx, AQ_E_INVALID_ARG,
+                           "aq_dac_encode: the OuteTTS recipe gives no recon (aq_dac_decode of the codes does)");
+        aq_device_guard g(ctx->device);
+        if (force_idx) AQ_HIP(ctx, hipMemsetAsync(ctx->d_flags, 0, sizeof(int32_t) * AQ_FLAG_COUNT, ctx->stream));
+        aq_outetts_args a = st->ot;
+        a.x = x;
+        a.M = M;
+        a.force_idx = force_idx;
+        a.idx = idx;
+        a.residual = residual;
+        a.flags = ctx->d_flags;
+        aq_status rs = aq_outetts_launch(ctx, a);
+        if (rs != AQ_OK) return rs;
+        if (force_idx) {
+            int32_t flag = 0;
+            AQ_HIP(ctx, hipMemcpyAsync(&flag, ctx->d_flags + AQ_FLAG_BAD_INDEX, sizeof(int32_t), hipMemcpyDeviceToHost,
+                                       ctx->stream));
+            AQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
+            if (flag)
+                return aq_fail(ctx, AQ_E_INDEX_RANGE, "aq_dac_encode: force_idx holds a code outside [0, %lld)", (long long)st->N);
+        }
+        return AQ_OK;
+    }
     // ggml hands the in-projection (m = T rows, n = 8, k = D) to tinyBLAS when
     // T % 4 == 0 (ggml-cpu.c:1285-1306, sgemm.cpp:3705-3725), otherwise each
     // element is a ggml_vec_dot_f32.

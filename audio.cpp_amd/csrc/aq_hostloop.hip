@@ -1,0 +1,622 @@
+// Host-loop members of the DAC quantizer family on the MI355X.
+//
+//   OuteTTS  quantize_reference (community_models/outetts/dac.cpp:376-456):
+//            fp32, every product rounded before it is added, bias first,
+//            first index of the minimum squared distance between the
+//            normalised projection and the normalised code.
+//   MOSS     MossAudioTokenizerQuantizer (models/moss/shared/
+//            audio_tokenizer_quantizer.cpp): fp64 input projection, per
+//            stage an fp64 in-projection, max(|e|, 1e-12) normalisation,
+//            first index of the maximum dot, fp64 residual update; fp32
+//            latent tables for decode.
+//
+// The reference builds this code without FMA (x86-64 baseline), so the exact
+// arithmetic below is written as separate multiplies and adds (the library
+// is compiled with -ffp-contract=off).  Where a product of two floats is
+// formed in double it is exact, and a fused multiply-add gives the same
+// result as the reference's multiply then add; those places use __fma_rn.
+//
+// Layout of one encode: a wave owns 8 frames and keeps their residuals in
+// LDS (row stride padded by 16 bytes so the 8 frames fall in different
+// banks).  Lane (f, j) = (lane / 8, lane % 8) runs the in-projection chain of
+// code dimension j of frame f -- the reference's sequential sum over the
+// latent channels -- and then scores codes j, j + 8, ... of the frame; the
+// 8 lanes of a frame merge their winners with the reference's tie rule.  The
+// residual update then sweeps each frame's channels across the wave.
+#include "aq_device_math.hpp"
+#include "aq_internal.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <vector>
+
+namespace {
+
+constexpr int kWave = 64;
+constexpr int kHF = 8;   // frames per wave
+constexpr int kHW = 2;   // waves per block
+
+// ------------------------------------------------------------------ OuteTTS
+
+__global__ void outetts_chat_kernel(const float *__restrict__ cb, int64_t rows, float *__restrict__ chat) {
+    const int64_t n = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (n >= rows) return;
+    const float *c = cb + n * 8;
+    float e2 = 0.0f;   // dac.cpp:417-421
+    for (int d = 0; d < 8; ++d) e2 = e2 + c[d] * c[d];
+    const float en = aq_math::sqrt_rn(e2) + 1.0e-12f;
+    for (int d = 0; d < 8; ++d) chat[n * 8 + d] = c[d] / en;   // dac.cpp:426-427
+}
+
+__global__ __launch_bounds__(kWave *kHW) void outetts_encode_kernel(aq_outetts_args a) {
+    extern __shared__ float lds_ot[];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int D = a.D;
+    const int stride = D + 4;
+    float *r = lds_ot + wave * kHF * stride;
+    const int64_t m0 = (static_cast<int64_t>(blockIdx.x) * kHW + wave) * kHF;
+    for (int f = 0; f < kHF; ++f) {
+        const int64_t m = m0 + f;
+        for (int e = lane * 4; e < D; e += kWave * 4) {
+            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (m < a.M) v = *reinterpret_cast<const float4 *>(a.x + m * D + e);
+            *reinterpret_cast<float4 *>(r + f * stride + e) = v;
+        }
+    }
+    __syncthreads();
+    const int f = lane >> 3;
+    const int j = lane & 7;
+    const int64_t mf = m0 + f;
+    const bool live = mf < a.M;
+    for (int s = 0; s < a.Q; ++s) {
+        // in-projection chain of (frame f, dim j), dac.cpp:402-410
+        const float *W = a.w_in + (static_cast<int64_t>(s) * 8 + j) * D;
+        const float *rf = r + f * stride;
+        float v = a.b_in[s * 8 + j];
+        for (int h = 0; h < D; h += 4) {
+            const float4 w4 = *reinterpret_cast<const float4 *>(W + h);
+            const float4 r4 = *reinterpret_cast<const float4 *>(rf + h);
+            v = v + w4.x * r4.x;
+            v = v + w4.y * r4.y;
+            v = v + w4.z * r4.z;
+            v = v + w4.w * r4.w;
+        }
+        // |p| and p / (|p| + 1e-12), dac.cpp:409-412,425-426
+        float p[8];
+        float nsq = 0.0f;
+#pragma unroll
+        for (int d = 0; d < 8; ++d) {
+            p[d] = __shfl(v, (f << 3) + d);
+            nsq = nsq + p[d] * p[d];
+        }
+        const float pn = aq_math::sqrt_rn(nsq) + 1.0e-12f;
+#pragma unroll
+        for (int d = 0; d < 8; ++d) p[d] = p[d] / pn;
+        // distances to codes j, j + 8, ... (dac.cpp:415-434), strict < keeps
+        // the first index of the minimum; NaN distances never win
+        float bd = INFINITY;
+        int bn = -1;
+        const float *Ch = a.chat + static_cast<int64_t>(s) * a.N * 8;
+        for (int n = j; n < a.N; n += 8) {
+            const float4 c0 = *reinterpret_cast<const float4 *>(Ch + static_cast<int64_t>(n) * 8);
+            const float4 c1 = *reinterpret_cast<const float4 *>(Ch + static_cast<int64_t>(n) * 8 + 4);
+            const float cc[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+            float dist = 0.0f;
+#pragma unroll
+            for (int d = 0; d < 8; ++d) {
+                const float diff = p[d] - cc[d];
+                dist = dist + diff * diff;
+            }
+            if (dist < bd) {
+                bd = dist;
+                bn = n;
+            }
+        }
+#pragma unroll
+        for (int o = 1; o < 8; o <<= 1) {
+            const float od = __shfl_xor(bd, o);
+            const int on = __shfl_xor(bn, o);
+            if (on >= 0 && (bn < 0 || od < bd || (od == bd && on < bn))) {
+                bd = od;
+                bn = on;
+            }
+        }
+        const int code = bn < 0 ? 0 : bn;
+        int use = code;
+        if (live) {
+            if (j == 0) a.idx[mf * a.Q + s] = code;
+            if (a.force_idx) {
+                use = a.force_idx[mf * a.Q + s];
+                if (use < 0 || use >= a.N) {
+                    if (j == 0) a.flags[AQ_FLAG_BAD_INDEX] = 1;
+                    use = 0;
+                }
+            }
+        }
+        __syncthreads();
+        // residual -= b_out + W_out c[use], dac.cpp:438-453
+        for (int g = 0; g < kHF; ++g) {
+            const int ug = __shfl(use, g << 3);
+            const float *c = a.cb + (static_cast<int64_t>(s) * a.N + ug) * 8;
+            const float4 c0 = *reinterpret_cast<const float4 *>(c);
+            const float4 c1 = *reinterpret_cast<const float4 *>(c + 4);
+            float *rg = r + g * stride;
+            for (int o = lane; o < D; o += kWave) {
+                const float *wo = a.w_out + (static_cast<int64_t>(s) * D + o) * 8;
+                const float4 w0 = *reinterpret_cast<const float4 *>(wo);
+                const float4 w1 = *reinterpret_cast<const float4 *>(wo + 4);
+                float val = a.b_out[static_cast<int64_t>(s) * D + o];
+                val = val + w0.x * c0.x;
+                val = val + w0.y * c0.y;
+                val = val + w0.z * c0.z;
+                val = val + w0.w * c0.w;
+                val = val + w1.x * c1.x;
+                val = val + w1.y * c1.y;
+                val = val + w1.z * c1.z;
+                val = val + w1.w * c1.w;
+                rg[o] = rg[o] - val;
+            }
+        }
+        __syncthreads();
+    }
+    if (a.residual) {
+        for (int g = 0; g < kHF; ++g) {
+            const int64_t m = m0 + g;
+            if (m >= a.M) break;
+            for (int e = lane * 4; e < D; e += kWave * 4)
+                *reinterpret_cast<float4 *>(a.residual + m * D + e) = *reinterpret_cast<const float4 *>(r + g * stride + e);
+        }
+    }
+}
+
+// --------------------------------------------------------------------- MOSS
+
+constexpr int kIpF = 64;   // input projection tile: frames
+constexpr int kIpO = 64;   //                         outputs
+constexpr int kIpK = 32;   //                         channels per LDS chunk
+
+// residual[m, o] = b[o] + sum_k w[o, k] h[m, k] in fp64, k in order
+// (audio_tokenizer_quantizer.cpp:193-201).  256 threads, 4 x 4 outputs each.
+__global__ __launch_bounds__(256) void moss_input_kernel(const float *__restrict__ h, int64_t M, int C, int R,
+                                                         const float *__restrict__ w, const float *__restrict__ b,
+                                                         double *__restrict__ res) {
+    __shared__ float hs[kIpK][kIpF + 4];
+    __shared__ float ws[kIpK][kIpO + 4];
+    const int tid = threadIdx.x;
+    const int tx = tid & 15;
+    const int ty = tid >> 4;
+    const int64_t m0 = static_cast<int64_t>(blockIdx.x) * kIpF;
+    const int o0 = blockIdx.y * kIpO;
+    double acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc[i][q] = static_cast<double>(b[o0 + tx * 4 + q]);
+    for (int k0 = 0; k0 < C; k0 += kIpK) {
+        const int kn = min(kIpK, C - k0);
+        for (int e = tid; e < kIpF * kIpK; e += 256) {
+            const int rr = e / kIpK;
+            const int cc = e % kIpK;
+            const int64_t m = m0 + rr;
+            hs[cc][rr] = (m < M && cc < kn) ? h[m * C + k0 + cc] : 0.0f;
+            ws[cc][rr] = cc < kn ? w[static_cast<int64_t>(o0 + rr) * C + k0 + cc] : 0.0f;
+        }
+        __syncthreads();
+        for (int kk = 0; kk < kn; ++kk) {
+            const float4 xa = *reinterpret_cast<const float4 *>(&hs[kk][ty * 4]);
+            const float4 wb = *reinterpret_cast<const float4 *>(&ws[kk][tx * 4]);
+            const double xv[4] = {xa.x, xa.y, xa.z, xa.w};
+            const double wv[4] = {wb.x, wb.y, wb.z, wb.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) acc[i][q] = __fma_rn(wv[q], xv[i], acc[i][q]);   // exact product
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int64_t m = m0 + ty * 4 + i;
+        if (m >= M) break;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) res[m * R + o0 + tx * 4 + q] = acc[i][q];
+    }
+}
+
+__global__ __launch_bounds__(kWave *kHW) void moss_cascade_kernel(aq_moss_args a) {
+    extern __shared__ double lds_ms[];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int R = a.R;
+    const int stride = R + 2;
+    double *r = lds_ms + wave * kHF * stride;
+    const int64_t m0 = (static_cast<int64_t>(blockIdx.x) * kHW + wave) * kHF;
+    for (int f = 0; f < kHF; ++f) {
+        const int64_t m = m0 + f;
+        for (int e = lane * 2; e < R; e += kWave * 2) {
+            double2 v = make_double2(0.0, 0.0);
+            if (m < a.M) v = *reinterpret_cast<const double2 *>(a.res + m * R + e);
+            *reinterpret_cast<double2 *>(r + f * stride + e) = v;
+        }
+    }
+    __syncthreads();
+    const int f = lane >> 3;
+    const int j = lane & 7;
+    const int64_t mf = m0 + f;
+    const bool live = mf < a.M;
+    for (int s = 0; s < a.Q; ++s) {
+        // in_proj of (frame f, dim j): float weight times fp64 residual,
+        // rounded, then added (:207-216)
+        const float *W = a.w_in + (static_cast<int64_t>(s) * 8 + j) * R;
+        const double *rf = r + f * stride;
+        double v = a.b_in[s * 8 + j];
+        for (int k = 0; k < R; k += 4) {
+            const float4 w4 = *reinterpret_cast<const float4 *>(W + k);
+            const double2 r01 = *reinterpret_cast<const double2 *>(rf + k);
+            const double2 r23 = *reinterpret_cast<const double2 *>(rf + k + 2);
+            v = v + static_cast<double>(w4.x) * r01.x;
+            v = v + static_cast<double>(w4.y) * r01.y;
+            v = v + static_cast<double>(w4.z) * r23.x;
+            v = v + static_cast<double>(w4.w) * r23.y;
+        }
+        // encoding * (1 / std::max(sqrt(|e|^2), 1e-12)) (:210-221)
+        double e[8];
+        double nrm = 0.0;
+#pragma unroll
+        for (int d = 0; d < 8; ++d) {
+            e[d] = __shfl(v, (f << 3) + d);
+            nrm = nrm + e[d] * e[d];
+        }
+        const double sq = aq_math::sqrt_rn(nrm);
+        const double scale = 1.0 / ((sq < 1.0e-12) ? 1.0e-12 : sq);
+#pragma unroll
+        for (int d = 0; d < 8; ++d) e[d] = e[d] * scale;
+        // first index of the maximum dot with the normalised codebook (:225-237)
+        double bd = -INFINITY;
+        int bn = -1;
+        const float *T = a.tn + static_cast<int64_t>(s) * a.N * 8;
+        for (int n = j; n < a.N; n += 8) {
+            const float4 t0 = *reinterpret_cast<const float4 *>(T + static_cast<int64_t>(n) * 8);
+            const float4 t1 = *reinterpret_cast<const float4 *>(T + static_cast<int64_t>(n) * 8 + 4);
+            double dot = 0.0;
+            dot = dot + static_cast<double>(t0.x) * e[0];
+            dot = dot + static_cast<double>(t0.y) * e[1];
+            dot = dot + static_cast<double>(t0.z) * e[2];
+            dot = dot + static_cast<double>(t0.w) * e[3];
+            dot = dot + static_cast<double>(t1.x) * e[4];
+            dot = dot + static_cast<double>(t1.y) * e[5];
+            dot = dot + static_cast<double>(t1.z) * e[6];
+            dot = dot + static_cast<double>(t1.w) * e[7];
+            if (dot > bd) {
+                bd = dot;
+                bn = n;
+            }
+        }
+#pragma unroll
+        for (int o = 1; o < 8; o <<= 1) {
+            const double od = __shfl_xor(bd, o);
+            const int on = __shfl_xor(bn, o);
+            if (on >= 0 && (bn < 0 || od > bd || (od == bd && on < bn))) {
+                bd = od;
+                bn = on;
+            }
+        }
+        const int code = bn < 0 ? 0 : bn;
+        int use = code;
+        if (live) {
+            if (j == 0) a.idx[mf * a.Q + s] = code;
+            if (a.force_idx) {
+                use = a.force_idx[mf * a.Q + s];
+                if (use < 0 || use >= a.N) {
+                    if (j == 0) a.flags[AQ_FLAG_BAD_INDEX] = 1;
+                    use = 0;
+                }
+            }
+        }
+        __syncthreads();
+        // residual -= b_out + W_out c[use] in fp64 (:240-248)
+        for (int g = 0; g < kHF; ++g) {
+            const int ug = __shfl(use, g << 3);
+            const float *c = a.cb + (static_cast<int64_t>(s) * a.N + ug) * 8;
+            const float4 c0 = *reinterpret_cast<const float4 *>(c);
+            const float4 c1 = *reinterpret_cast<const float4 *>(c + 4);
+            const double cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+            double *rg = r + g * stride;
+            for (int o = lane; o < R; o += kWave) {
+                const float *wo = a.w_out + (static_cast<int64_t>(s) * R + o) * 8;
+                const float4 w0 = *reinterpret_cast<const float4 *>(wo);
+                const float4 w1 = *reinterpret_cast<const float4 *>(wo + 4);
+                const double wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+                double z = a.b_out[static_cast<int64_t>(s) * R + o];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) z = __fma_rn(wv[k], cv[k], z);   // exact product
+                rg[o] = rg[o] - z;
+            }
+        }
+        __syncthreads();
+    }
+    if (a.write_res) {
+        for (int g = 0; g < kHF; ++g) {
+            const int64_t m = m0 + g;
+            if (m >= a.M) break;
+            for (int e = lane * 2; e < R; e += kWave * 2)
+                *reinterpret_cast<double2 *>(a.res + m * R + e) = *reinterpret_cast<const double2 *>(r + g * stride + e);
+        }
+    }
+}
+
+// Constructor tables (:77-115): per stage, comb[o][0..7] = sum_j w_op[o][j]
+// w_out[j][k] and comb[o][8] = sum_j w_op[o][j] b_out[j] (fp32, from 0, in
+// order), then table[n][o] = comb[o][8] + sum_k comb[o][k] c[n][k].
+__global__ void moss_combine_kernel(const float *__restrict__ w_op, const float *__restrict__ w_out,
+                                    const float *__restrict__ b_out, int Q, int C, int R, float *__restrict__ comb) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= static_cast<int64_t>(Q) * C * 9) return;
+    const int s = static_cast<int>(t / (static_cast<int64_t>(C) * 9));
+    const int rem = static_cast<int>(t % (static_cast<int64_t>(C) * 9));
+    const int o = rem / 9;
+    const int k = rem % 9;
+    const float *orow = w_op + static_cast<int64_t>(o) * R;
+    float sum = 0.0f;
+    if (k < 8) {
+        for (int q = 0; q < R; ++q) sum = sum + orow[q] * w_out[(static_cast<int64_t>(s) * R + q) * 8 + k];
+    } else {
+        for (int q = 0; q < R; ++q) sum = sum + orow[q] * b_out[static_cast<int64_t>(s) * R + q];
+    }
+    comb[t] = sum;
+}
+
+__global__ void moss_table_kernel(const float *__restrict__ comb, const float *__restrict__ cb, int Q, int64_t N,
+                                  int C, float *__restrict__ tables) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= static_cast<int64_t>(Q) * N * C) return;
+    const int64_t sn = t / C;
+    const int o = static_cast<int>(t % C);
+    const int s = static_cast<int>(sn / N);
+    const float *cw = comb + (static_cast<int64_t>(s) * C + o) * 9;
+    const float *e = cb + sn * 8;
+    float sum = cw[8];
+    for (int k = 0; k < 8; ++k) sum = sum + cw[k] * e[k];
+    tables[t] = sum;
+}
+
+// latent[m][o] = b_op[o] + sum over stages of table[s][idx[m][s]][o] (:160-171)
+__global__ void moss_decode_kernel(const int32_t *__restrict__ idx, int64_t M, int Q, int64_t N, int C,
+                                   const float *__restrict__ tables, const float *__restrict__ b_op,
+                                   float *__restrict__ out, int32_t *__restrict__ flags) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= M * C) return;
+    const int64_t m = t / C;
+    const int o = static_cast<int>(t % C);
+    float v = b_op[o];
+    for (int s = 0; s < Q; ++s) {
+        int32_t code = idx[m * Q + s];
+        if (code < 0 || code >= N) {
+            flags[AQ_FLAG_BAD_INDEX] = 1;
+            code = 0;
+        }
+        v = v + tables[(static_cast<int64_t>(s) * N + code) * C + o];
+    }
+    out[t] = v;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------- OuteTTS host
+
+size_t aq_outetts_lds_bytes(int64_t D) { return static_cast<size_t>(kHW) * kHF * (D + 4) * sizeof(float); }
+
+aq_status aq_outetts_prepare(aq_ctx *ctx, const float *d_cb, int64_t rows, float *d_chat) {
+    hipLaunchKernelGGL(outetts_chat_kernel, dim3(static_cast<unsigned>((rows + 255) / 256)), dim3(256), 0, ctx->stream,
+                       d_cb, rows, d_chat);
+    AQ_HIP(ctx, hipGetLastError());
+    return AQ_OK;
+}
+
+aq_status aq_outetts_launch(aq_ctx *ctx, const aq_outetts_args &a) {
+    const size_t lds = aq_outetts_lds_bytes(a.D);
+    AQ_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void *>(outetts_encode_kernel),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+    const int64_t per_block = static_cast<int64_t>(kHW) * kHF;
+    const unsigned blocks = static_cast<unsigned>((a.M + per_block - 1) / per_block);
+    const int tslot = aq_timing_start(ctx);
+    hipLaunchKernelGGL(outetts_encode_kernel, dim3(blocks), dim3(kWave * kHW), lds, ctx->stream, a);
+    aq_timing_stop(ctx, tslot);
+    AQ_HIP(ctx, hipGetLastError());
+    return AQ_OK;
+}
+
+// ------------------------------------------------------------------- MOSS host
+
+struct aq_moss_quantizer {
+    aq_ctx *ctx = nullptr;
+    int64_t Q = 0, N = 0, C = 0, R = 0;
+    float *d_mem = nullptr;      // one allocation holding the arrays below
+    float *d_wip = nullptr;      // [R][C]
+    float *d_bip = nullptr;      // [R]
+    float *d_win = nullptr;      // [Q][8][R]
+    float *d_bin = nullptr;      // [Q][8]
+    float *d_cb = nullptr;       // [Q][N][8] raw
+    float *d_tn = nullptr;       // [Q][N][8] normalised
+    float *d_wout = nullptr;     // [Q][R][8]
+    float *d_bout = nullptr;     // [Q][R]
+    float *d_bop = nullptr;      // [C]
+    float *d_tables = nullptr;   // [Q][N][C] decode latent tables (null: encode only)
+};
+
+namespace {
+constexpr int64_t kMossMaxR = 1024;
+}
+
+extern "C" {
+
+aq_status aq_moss_upload(aq_ctx *ctx, int64_t Q, int64_t N, int64_t code_dim, int64_t rvq_dim, const float *input_w,
+                         const float *input_b, const float *in_w, const float *in_b, const float *codebook,
+                         const float *out_w, const float *out_b, const float *output_w, const float *output_b,
+                         aq_moss_quantizer **out) {
+    if (!ctx || !out || !input_w || !input_b || !in_w || !in_b || !codebook || !out_w || !out_b)
+        return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_moss_upload: null argument");
+    *out = nullptr;
+    if ((output_w == nullptr) != (output_b == nullptr))
+        return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_moss_upload: output_w and output_b come together (both or neither)");
+    if (Q <= 0)
+        return aq_fail(ctx, AQ_E_SHAPE, "aq_moss_upload: MOSS codec dequantizer requires a positive quantizer count");
+    if (N <= 0 || N % 8 != 0 || N > (int64_t{1} << 20) || code_dim <= 0 || code_dim > (int64_t{1} << 16) ||
+        rvq_dim <= 0 || rvq_dim % kIpO != 0 || rvq_dim > kMossMaxR)
+        return aq_fail(ctx, AQ_E_SHAPE,
+                       "aq_moss_upload: unsupported shape N=%lld code_dim=%lld rvq_dim=%lld (N a multiple of 8, "
+                       "rvq_dim a multiple of 64 up to 1024)",
+                       (long long)N, (long long)code_dim, (long long)rvq_dim);
+    aq_device_guard g(ctx->device);
+    const int64_t C = code_dim, R = rvq_dim;
+    // codebook rows normalised once, in double (:116-130)
+    std::vector<float> tn(static_cast<size_t>(Q * N * 8));
+    for (int64_t n = 0; n < Q * N; ++n) {
+        double norm = 0.0;
+        for (int k = 0; k < 8; ++k) norm = norm + static_cast<double>(codebook[n * 8 + k]) * codebook[n * 8 + k];
+        const double scale = 1.0 / std::max(std::sqrt(norm), 1.0e-12);
+        for (int k = 0; k < 8; ++k) tn[n * 8 + k] = static_cast<float>(codebook[n * 8 + k] * scale);
+    }
+    const int64_t sizes[] = {R * C, R, Q * 8 * R, Q * 8, Q * N * 8, Q * N * 8, Q * R * 8, Q * R, C};
+    int64_t total = 0;
+    for (int64_t s : sizes) total += (s + 63) / 64 * 64;
+    auto *q = new aq_moss_quantizer();
+    q->ctx = ctx;
+    q->Q = Q;
+    q->N = N;
+    q->C = C;
+    q->R = R;
+    if (hipMalloc(&q->d_mem, static_cast<size_t>(total) * sizeof(float)) != hipSuccess) {
+        delete q;
+        return aq_fail(ctx, AQ_E_DEVICE, "aq_moss_upload: device allocation of %lld bytes failed",
+                       (long long)(total * 4));
+    }
+    float **slots[] = {&q->d_wip, &q->d_bip, &q->d_win, &q->d_bin, &q->d_cb, &q->d_tn, &q->d_wout, &q->d_bout, &q->d_bop};
+    const float *srcs[] = {input_w, input_b, in_w, in_b, codebook, tn.data(), out_w, out_b, output_b};
+    int64_t off = 0;
+    bool ok = true;
+    for (int i = 0; i < 9; ++i) {
+        *slots[i] = q->d_mem + off;
+        if (srcs[i])
+            ok = ok && hipMemcpyAsync(*slots[i], srcs[i], static_cast<size_t>(sizes[i]) * sizeof(float),
+                                      hipMemcpyHostToDevice, ctx->stream) == hipSuccess;
+        off += (sizes[i] + 63) / 64 * 64;
+    }
+    float *d_wop = nullptr;
+    float *d_comb = nullptr;
+    if (ok && output_w) {
+        ok = hipMalloc(&q->d_tables, static_cast<size_t>(Q * N * C) * sizeof(float)) == hipSuccess &&
+             hipMalloc(&d_wop, static_cast<size_t>(C * R) * sizeof(float)) == hipSuccess &&
+             hipMalloc(&d_comb, static_cast<size_t>(Q * C * 9) * sizeof(float)) == hipSuccess;
+        ok = ok && hipMemcpyAsync(d_wop, output_w, static_cast<size_t>(C * R) * sizeof(float), hipMemcpyHostToDevice,
+                                  ctx->stream) == hipSuccess;
+        if (ok) {
+            const int64_t nc = Q * C * 9;
+            hipLaunchKernelGGL(moss_combine_kernel, dim3(static_cast<unsigned>((nc + 255) / 256)), dim3(256), 0,
+                               ctx->stream, d_wop, q->d_wout, q->d_bout, static_cast<int>(Q), static_cast<int>(C),
+                               static_cast<int>(R), d_comb);
+            const int64_t nt = Q * N * C;
+            hipLaunchKernelGGL(moss_table_kernel, dim3(static_cast<unsigned>((nt + 255) / 256)), dim3(256), 0,
+                               ctx->stream, d_comb, q->d_cb, static_cast<int>(Q), N, static_cast<int>(C), q->d_tables);
+            ok = hipGetLastError() == hipSuccess;
+        }
+    }
+    ok = hipStreamSynchronize(ctx->stream) == hipSuccess && ok;
+    if (d_wop) (void)hipFree(d_wop);
+    if (d_comb) (void)hipFree(d_comb);
+    if (!ok) {
+        aq_moss_release(q);
+        return aq_fail(ctx, AQ_E_DEVICE, "aq_moss_upload: device copy or table preparation failed");
+    }
+    *out = q;
+    return AQ_OK;
+}
+
+aq_status aq_moss_release(aq_moss_quantizer *q) {
+    if (!q) return AQ_E_INVALID_ARG;
+    {
+        aq_device_guard g(q->ctx->device);
+        if (q->d_mem) (void)hipFree(q->d_mem);
+        if (q->d_tables) (void)hipFree(q->d_tables);
+    }
+    delete q;
+    return AQ_OK;
+}
+
+aq_status aq_moss_encode(aq_ctx *ctx, const aq_moss_quantizer *q, const float *hidden, int64_t M, int32_t *idx,
+                         double *residual, const int32_t *force_idx) {
+    if (!ctx || !q || !idx) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_moss_encode: null argument");
+    if (q->ctx->device != ctx->device)
+        return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_moss_encode: quantizer belongs to another device");
+    if (M <= 0 || M > (int64_t{1} << 31) - 1)
+        return aq_fail(ctx, AQ_E_SHAPE, "aq_moss_encode: MOSS codec quantizer requires a non-empty encoder latent");
+    if (!hidden) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_moss_encode: null argument");
+    aq_device_guard g(ctx->device);
+    double *res = residual;
+    if (!res) {
+        aq_status st = aq_ctx_scratch(ctx, 0, static_cast<size_t>(M * q->R) * sizeof(double), reinterpret_cast<void **>(&res));
+        if (st != AQ_OK) return st;
+    }
+    if (force_idx) AQ_HIP(ctx, hipMemsetAsync(ctx->d_flags, 0, sizeof(int32_t) * AQ_FLAG_COUNT, ctx->stream));
+    hipLaunchKernelGGL(moss_input_kernel, dim3(static_cast<unsigned>((M + kIpF - 1) / kIpF), static_cast<unsigned>(q->R / kIpO)),
+                       dim3(256), 0, ctx->stream, hidden, M, static_cast<int>(q->C), static_cast<int>(q->R), q->d_wip,
+                       q->d_bip, res);
+    AQ_HIP(ctx, hipGetLastError());
+    aq_moss_args a{};
+    a.res = res;
+    a.M = M;
+    a.R = static_cast<int>(q->R);
+    a.N = static_cast<int>(q->N);
+    a.Q = static_cast<int>(q->Q);
+    a.w_in = q->d_win;
+    a.b_in = q->d_bin;
+    a.tn = q->d_tn;
+    a.cb = q->d_cb;
+    a.w_out = q->d_wout;
+    a.b_out = q->d_bout;
+    a.force_idx = force_idx;
+    a.idx = idx;
+    a.flags = ctx->d_flags;
+    a.write_res = residual ? 1 : 0;
+    const size_t lds = static_cast<size_t>(kHW) * kHF * (q->R + 2) * sizeof(double);
+    AQ_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void *>(moss_cascade_kernel),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+    const int64_t per_block = static_cast<int64_t>(kHW) * kHF;
+    const int tslot = aq_timing_start(ctx);
+    hipLaunchKernelGGL(moss_cascade_kernel, dim3(static_cast<unsigned>((M + per_block - 1) / per_block)), dim3(kWave * kHW),
+                       lds, ctx->stream, a);
+    aq_timing_stop(ctx, tslot);
+    AQ_HIP(ctx, hipGetLastError());
+    if (force_idx) {
+        int32_t flag = 0;
+        AQ_HIP(ctx, hipMemcpyAsync(&flag, ctx->d_flags + AQ_FLAG_BAD_INDEX, sizeof(int32_t), hipMemcpyDeviceToHost, ctx->stream));
+        AQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        if (flag)
+            return aq_fail(ctx, AQ_E_INDEX_RANGE, "aq_moss_encode: force_idx holds a code outside [0, %lld)", (long long)q->N);
+    }
+    return AQ_OK;
+}
+
+aq_status aq_moss_decode(aq_ctx *ctx, const aq_moss_quantizer *q, const int32_t *idx, int64_t M, float *latent) {
+    if (!ctx || !q) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_moss_decode: null argument");
+    if (q->ctx->device != ctx->device)
+        return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_moss_decode: quantizer belongs to another device");
+    if (M <= 0) return aq_fail(ctx, AQ_E_SHAPE, "aq_moss_decode: MOSS codec dequantizer requires a non-empty code sequence");
+    if (!idx || !latent) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_moss_decode: null argument");
+    if (!q->d_tables)
+        return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_moss_decode: no output projection was uploaded (encode only)");
+    aq_device_guard g(ctx->device);
+    AQ_HIP(ctx, hipMemsetAsync(ctx->d_flags, 0, sizeof(int32_t) * AQ_FLAG_COUNT, ctx->stream));
+    const int64_t total = M * q->C;
+    hipLaunchKernelGGL(moss_decode_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, ctx->stream, idx, M,
+                       static_cast<int>(q->Q), q->N, static_cast<int>(q->C), q->d_tables, q->d_bop, latent, ctx->d_flags);
+    AQ_HIP(ctx, hipGetLastError());
+    int32_t flag = 0;
+    AQ_HIP(ctx, hipMemcpyAsync(&flag, ctx->d_flags + AQ_FLAG_BAD_INDEX, sizeof(int32_t), hipMemcpyDeviceToHost, ctx->stream));
+    AQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (flag) return aq_fail(ctx, AQ_E_INDEX_RANGE, "aq_moss_decode: MOSS codec code index out of range");
+    return AQ_OK;
+}
+
+}  // extern "C"

@@ -82,3 +82,40 @@ enum aq_flag_slot : int {
     AQ_FLAG_BAD_INDEX = 0,   // a forced / decoded code outside [0, N)
     AQ_FLAG_COUNT = 8
 };
+
+// Host-loop DAC quantizers (aq_hostloop.hip).  Device pointers throughout.
+struct aq_outetts_args {
+    const float *x;        // [M, D]
+    int64_t M;
+    int D, N, Q;
+    const float *w_in;     // [Q, 8, D]
+    const float *b_in;     // [Q, 8]
+    const float *chat;     // [Q, N, 8] normalised codes
+    const float *cb;       // [Q, N, 8] raw codes
+    const float *w_out;    // [Q, D, 8]
+    const float *b_out;    // [Q, D]
+    const int32_t *force_idx;
+    int32_t *idx;          // [M, Q]
+    float *residual;       // [M, D] or null
+    int32_t *flags;
+};
+size_t aq_outetts_lds_bytes(int64_t D);
+// chat[n] = c[n] / (sqrt(|c[n]|^2) + 1e-12) for `rows` codes of dim 8.
+aq_status aq_outetts_prepare(aq_ctx *ctx, const float *d_cb, int64_t rows, float *d_chat);
+aq_status aq_outetts_launch(aq_ctx *ctx, const aq_outetts_args &a);
+
+struct aq_moss_args {
+    double *res;           // [M, R] in / out
+    int64_t M;
+    int R, N, Q;
+    const float *w_in;     // [Q, 8, R]
+    const float *b_in;     // [Q, 8]
+    const float *tn;       // [Q, N, 8] normalised codes
+    const float *cb;       // [Q, N, 8] raw codes
+    const float *w_out;    // [Q, R, 8]
+    const float *b_out;    // [Q, R]
+    const int32_t *force_idx;
+    int32_t *idx;          // [M, Q]
+    int32_t *flags;
+    int write_res;
+};

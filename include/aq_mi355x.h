@@ -107,7 +107,8 @@ aq_status aq_dac_upload(aq_ctx *ctx, int64_t Q, int64_t D, int64_t N,
                         const float *w_out, const float *b_out, aq_dac_stages **out);
 
 /* The same cosine quantizer with another model family's normalisation
- * (SURVEY-listed variants of the query and codebook L2 normalisation):
+ * (the variants of the query and codebook L2 normalisation in the model
+ * code):
  *   AQ_DAC_FISH       pn = p / sqrt(sum(p*p) + 1e-12); rows c * (float)(1/|c|),
  *                     zero rows -> 0 (fish_audio/codec.cpp:171-189,323-334)
  *   AQ_DAC_INDEXTTS2  pn = p / sqrt(sum(p*p)) (normalize_code_latents,
@@ -116,16 +117,27 @@ aq_status aq_dac_upload(aq_ctx *ctx, int64_t Q, int64_t D, int64_t N,
  *   AQ_DAC_VEVO2      pn = p / sqrt(sum(p*p) + 1e-20) (build_l2_normalized_rows,
  *                     vevo2/components.cpp:848-863); rows c * (float)(1/|c|),
  *                     a zero row is an error (l2_normalized_rows, :566-590)
- * All take the ggml arithmetic of the Fish path otherwise (1x1 conv, k = 8
- * mul_mat scores, argmax keeping the last maximum).  w_out (and b_out) may be
- * NULL for a single stage (Q = 1): codes only, as the IndexTTS2 and Vevo2
- * tokenisers use them; encode then takes no residual / recon and decode is
- * unavailable.  Codebooks too large for LDS next to W_in (e.g. IndexTTS2's
- * 8192 x 8 with D = 1024) are read from device memory. */
+ * These three take the ggml arithmetic of the Fish path otherwise (1x1 conv,
+ * k = 8 mul_mat scores, argmax keeping the last maximum).  w_out (and b_out)
+ * may be NULL for a single stage (Q = 1): codes only, as the IndexTTS2 and
+ * Vevo2 tokenisers use them; encode then takes no residual / recon and decode
+ * is unavailable.  Codebooks too large for LDS next to W_in (e.g. IndexTTS2's
+ * 8192 x 8 with D = 1024) are read from device memory.
+ *   AQ_DAC_OUTETTS    the OuteTTS host loop (quantize_reference,
+ *                     community_models/outetts/dac.cpp:376-456): fp32, each
+ *                     product rounded before it is added, bias first;
+ *                     p / (sqrt(sum p*p) + 1e-12) against c / (sqrt(sum c*c)
+ *                     + 1e-12), first index of the minimum squared distance;
+ *                     residual -= b_out + W_out c.  w_out is required; D a
+ *                     multiple of 64 up to 2048, N a multiple of 8; clip_len
+ *                     does not change the arithmetic; encode takes no recon
+ *                     (aq_dac_decode gives it, with the ggml 1x1-conv
+ *                     arithmetic of the OuteTTS decoder graph, dac.cpp:596-611). */
 typedef enum aq_dac_recipe {
     AQ_DAC_FISH = 0,
     AQ_DAC_INDEXTTS2 = 1,
-    AQ_DAC_VEVO2 = 2
+    AQ_DAC_VEVO2 = 2,
+    AQ_DAC_OUTETTS = 3
 } aq_dac_recipe;
 aq_status aq_dac_upload_ex(aq_ctx *ctx, int64_t Q, int64_t D, int64_t N,
                            const float *w_in, const float *b_in, const float *codebook,
@@ -238,6 +250,47 @@ aq_status aq_ema_codebook(aq_ctx *ctx, const float *embedding_sum, const float *
  * arithmetic, then prepared as an F32 codebook for `recipe`. */
 aq_status aq_euclid_upload_ema(aq_ctx *ctx, int64_t Q, int64_t N, int64_t K, const float *embedding_sum,
                                const float *cluster_usage, float eps, int recipe, aq_codebooks **out);
+
+/* ---- MOSS RLFQ quantizer (fp64 host loop) ---------------------------------
+ *
+ * MossAudioTokenizerQuantizer (models/moss/shared/audio_tokenizer_quantizer.cpp):
+ *   encode (:174-271)  residual = b_ip + W_ip h in fp64 (W_ip [R, C]); per
+ *                      stage e = b_in + W_in residual in fp64 (each float
+ *                      weight times the double residual rounded, then added),
+ *                      e *= 1 / std::max(|e|, 1e-12), code = first index of
+ *                      the maximum fp64 dot with the normalised codebook,
+ *                      residual -= b_out + W_out c[code] in fp64.
+ *   decode (:139-172)  latent = b_op + sum over stages of the constructor's
+ *                      fp32 latent tables (:77-115).
+ * Weight-normalised convs are passed folded (w = g v / |v|, as
+ * reconstruct_weight_norm builds them, :17-39).  Host weights:
+ *   input_w [R, C], input_b [R]               (quantizer.input_proj)
+ *   in_w [Q, 8, R], in_b [Q, 8]               (quantizers.s.in_proj)
+ *   codebook [Q, N, 8]                        (quantizers.s.codebook, raw)
+ *   out_w [Q, R, 8], out_b [Q, R]             (quantizers.s.out_proj)
+ *   output_w [C, R], output_b [C] or both NULL (quantizer.output_proj; decode)
+ * with C = code_dim, R = rvq_dim.  Supported: N a multiple of 8, R a multiple
+ * of 64 up to 1024.  Replaces the MossAudioTokenizerQuantizer constructor. */
+typedef struct aq_moss_quantizer aq_moss_quantizer;
+aq_status aq_moss_upload(aq_ctx *ctx, int64_t Q, int64_t N, int64_t code_dim, int64_t rvq_dim,
+                         const float *input_w, const float *input_b, const float *in_w, const float *in_b,
+                         const float *codebook, const float *out_w, const float *out_b,
+                         const float *output_w, const float *output_b, aq_moss_quantizer **out);
+aq_status aq_moss_release(aq_moss_quantizer *q);
+
+/* Encode (MossAudioTokenizerQuantizer::encode): hidden device [M, C]
+ * frame-major; idx device [M, Q] (the reference returns [Q][M]); residual
+ * device [M, R] doubles or NULL (the fp64 residual after the last stage);
+ * force_idx device [M, Q] or NULL (teacher forcing, as aq_dac_encode).
+ * M = 0 is AQ_E_SHAPE with the reference's message. */
+aq_status aq_moss_encode(aq_ctx *ctx, const aq_moss_quantizer *q, const float *hidden, int64_t M, int32_t *idx,
+                         double *residual, const int32_t *force_idx);
+
+/* Decode (MossAudioTokenizerQuantizer::decode): idx device [M, Q], latent
+ * device [M, C] frame-major (the reference returns [C, M]).  Out-of-range
+ * codes -> AQ_E_INDEX_RANGE with the reference's message (checked on device;
+ * the call synchronises the stream). */
+aq_status aq_moss_decode(aq_ctx *ctx, const aq_moss_quantizer *q, const int32_t *idx, int64_t M, float *latent);
 
 /* Codebook gather of one stage: out[m] = codebook[stage][idx[m]] (ggml_get_rows,
  * lookup_modules.cpp:88-112,182-187; Q8_0 rows dequantised as q*d).
