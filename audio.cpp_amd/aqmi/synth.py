@@ -250,3 +250,34 @@ def moss_config(M: int, seed: int = 12, C: int = 768, R: int = 512, Q: int = 12,
                 in_g=in_g, in_v=in_v, in_b=normal(seed, 32, (Q, 8), 0.1),
                 out_g=out_g, out_v=out_v, out_b=normal(seed, 42, (Q, R), 0.1),
                 codebook=normal(seed, 50, (Q, N, 8), 1.0))
+
+
+def near_duplicate_pairs(cb: np.ndarray, seed: int) -> np.ndarray:
+    """Codebooks [Q, N, dim] whose odd codes repeat the even code before them
+    with one component moved up by one ulp: the winner of each pair depends
+    on the last rounding of its score, so a test on them sees arithmetic
+    slips (a fused multiply-add, another summation order) as code changes."""
+    cb = np.array(cb, np.float32, copy=True)
+    rng = np.random.default_rng(seed)
+    for s in range(cb.shape[0]):
+        half = cb.shape[1] // 2
+        cb[s, 1::2] = cb[s, 0::2]
+        k = rng.integers(0, cb.shape[2], half)
+        rows = cb[s, 1::2]
+        rows[np.arange(half), k] = np.nextafter(rows[np.arange(half), k], np.float32(np.inf))
+        cb[s, 1::2] = rows
+    return cb
+
+
+def moss_fold(cfg: dict) -> dict:
+    """The folded conv weights of a moss_config, w = v * (float)(g / |v|) per
+    output row with |v|^2 summed in order in double, as the MOSS loader's
+    weight-norm reconstruction builds them from (g, v)."""
+    def fold(g, v):
+        v = np.asarray(v, np.float32)
+        v64 = v.astype(np.float64)
+        norm = np.cumsum(v64 * v64, axis=-1)[..., -1]
+        scale = (np.asarray(g, np.float32).astype(np.float64) / np.sqrt(norm)).astype(np.float32)
+        return (v * scale[..., None]).astype(np.float32)
+    return dict(w_ip=fold(cfg["ip_g"], cfg["ip_v"]), w_in=fold(cfg["in_g"], cfg["in_v"]),
+                w_out=fold(cfg["out_g"], cfg["out_v"]), w_op=fold(cfg["op_g"], cfg["op_v"]))

@@ -559,9 +559,11 @@ aq_status aq_moss_encode(aq_ctx *ctx, const aq_moss_quantizer *q, const float *h
         if (st != AQ_OK) return st;
     }
     if (force_idx) AQ_HIP(ctx, hipMemsetAsync(ctx->d_flags, 0, sizeof(int32_t) * AQ_FLAG_COUNT, ctx->stream));
+    const int islot = aq_timing_start(ctx);
     hipLaunchKernelGGL(moss_input_kernel, dim3(static_cast<unsigned>((M + kIpF - 1) / kIpF), static_cast<unsigned>(q->R / kIpO)),
                        dim3(256), 0, ctx->stream, hidden, M, static_cast<int>(q->C), static_cast<int>(q->R), q->d_wip,
                        q->d_bip, res);
+    aq_timing_stop(ctx, islot);
     AQ_HIP(ctx, hipGetLastError());
     aq_moss_args a{};
     a.res = res;

@@ -310,24 +310,28 @@ class Ref:
         L.aqref_quantize_chunk_q8_0.argtypes = [_f32p, C.c_void_p, _i64, _i64]
         L.aqref_top_k.restype = None
         L.aqref_top_k.argtypes = [_f32p, _i64, _i64, C.c_int, _i32p, C.c_int]
-        L.aqref_outetts_rvq.restype = C.c_int
-        L.aqref_outetts_rvq.argtypes = [_f32p, _i64, _f32p, _f32p, _f32p, _f32p, _f32p, _i32p]
+        L.aqref_outetts_rvq.restype = C.c_double
+        L.aqref_outetts_rvq.argtypes = [_f32p, _i64, _f32p, _f32p, _f32p, _f32p, _f32p, _i32p, C.c_int]
+        L.aqref_moss_encode_timed.restype = C.c_double
+        L.aqref_moss_encode_timed.argtypes = [C.POINTER(_MossWeights), _f32p, _i64, _i32p, C.c_int]
         L.aqref_moss_encode.restype = C.c_int
         L.aqref_moss_encode.argtypes = [C.POINTER(_MossWeights), _f32p, _i64, _i32p]
         L.aqref_moss_decode.restype = C.c_int
         L.aqref_moss_decode.argtypes = [C.POINTER(_MossWeights), _i32p, _i64, _f32p]
 
-    def outetts_rvq(self, cfg: dict):
-        """The reference's quantize_reference (2 stages, D = N = 1024): codes [M, 2]."""
+    def outetts_rvq(self, cfg: dict, threads: int = 0, timed: bool = False):
+        """The reference's quantize_reference (2 stages, D = N = 1024): codes
+        [M, 2] (and its milliseconds when timed)."""
         x = np.ascontiguousarray(cfg["x"], np.float32)
         M = x.shape[0]
         assert cfg["Q"] == 2 and cfg["D"] == 1024 and cfg["N"] == 1024
         a = lambda k: np.ascontiguousarray(cfg[k], np.float32)
         idx = np.zeros((M, 2), np.int32)
-        rc = self.lib.aqref_outetts_rvq(x, M, a("w_in"), a("b_in"), a("codebook"), a("w_out"), a("b_out"), idx)
-        if rc != 0:
+        ms = self.lib.aqref_outetts_rvq(x, M, a("w_in"), a("b_in"), a("codebook"), a("w_out"), a("b_out"), idx,
+                                        threads)
+        if ms < 0:
             raise RuntimeError("OuteTTS DAC encoder produced invalid acoustic latents")
-        return idx
+        return (idx, ms) if timed else idx
 
     def _moss_weights(self, cfg: dict):
         keep = {k: np.ascontiguousarray(cfg[k], np.float32) for k in
@@ -347,6 +351,16 @@ class Ref:
         if self.lib.aqref_moss_encode(C.byref(w), h, h.shape[0], idx) != 0:
             raise RuntimeError("MOSS codec quantizer rejected its input")
         return idx
+
+    def moss_encode_timed(self, cfg: dict, threads: int = 0):
+        """encode() alone on the clock: (codes [M, Q], milliseconds)."""
+        w, keep = self._moss_weights(cfg)
+        h = np.ascontiguousarray(cfg["hidden"], np.float32)
+        idx = np.zeros((h.shape[0], cfg["Q"]), np.int32)
+        ms = self.lib.aqref_moss_encode_timed(C.byref(w), h, h.shape[0], idx, threads)
+        if ms < 0:
+            raise RuntimeError("MOSS codec quantizer rejected its input")
+        return idx, ms
 
     def moss_decode(self, cfg: dict, idx):
         """MossAudioTokenizerQuantizer::decode, returned frame-major [M, C]."""

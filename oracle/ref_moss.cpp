@@ -9,8 +9,10 @@
 #include "engine/framework/assets/tensor_source.h"
 #include "engine/models/moss/shared/audio_tokenizer_quantizer.h"
 
+#include <chrono>
 #include <cstdint>
 #include <map>
+#include <omp.h>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -102,6 +104,27 @@ extern "C" __attribute__((visibility("default"))) int aqref_moss_encode(const Mo
         return -1;
     }
     return 0;
+}
+
+// The same encode with the constructor outside the clock: returns the
+// milliseconds encode() took (threads > 0 sets the OpenMP team), or -1.
+extern "C" __attribute__((visibility("default"))) double aqref_moss_encode_timed(const MossWeights *w,
+                                                                                  const float *hidden, int64_t frames,
+                                                                                  int32_t *idx, int threads) {
+    if (threads > 0) omp_set_num_threads(threads);
+    try {
+        MapSource src;
+        const auto q = make(*w, src);
+        std::vector<float> h(hidden, hidden + frames * w->C);
+        const auto t0 = std::chrono::steady_clock::now();
+        const auto codes = q.encode(h, frames);
+        const double ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+        for (int64_t s = 0; s < w->Q; ++s)
+            for (int64_t m = 0; m < frames; ++m) idx[m * w->Q + s] = codes[static_cast<size_t>(s)][static_cast<size_t>(m)];
+        return ms;
+    } catch (...) {
+        return -1.0;
+    }
 }
 
 // idx [frames, Q] -> latent [C, frames] (channel-major, as the reference returns it).

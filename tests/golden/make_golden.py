@@ -7,7 +7,7 @@ Inputs come from audio.cpp_amd/aqmi/synth.py (deterministic, seeded), so a
 fixture stores only outputs: codes, and SHA-256 digests of the fp32 residual
 and reconstruction bytes (bit-exact checks), plus small value samples.
 
-    python tests/golden/make_golden.py [dac] [mimi] [kmeans] [q8]
+    python tests/golden/make_golden.py [dac] [mimi] [kmeans] [q8] [outetts] [moss]
 """
 
 from __future__ import annotations
@@ -94,8 +94,33 @@ def q8(ref: Ref, name: str):
          ggml_isa=np.array(ref.isa))
 
 
+def outetts(ref: Ref, name: str):
+    """OuteTTS host loop (quantize_reference), 3001 frames, near-duplicate
+    codebooks (synth.near_duplicate_pairs seed 7): codes only -- the
+    reference function returns nothing else."""
+    cfg = synth.outetts_config(3001)
+    cfg["codebook"] = synth.near_duplicate_pairs(cfg["codebook"], 7)
+    save(name, idx=ref.outetts_rvq(cfg).astype(np.int16))
+
+
+def moss(ref: Ref, name: str):
+    """MOSS-Audio-Tokenizer-v2 quantizer (768 -> 512, 12 x 1024 x 8), 256
+    frames: the reference's codes, and its decode of them (frame-major)."""
+    cfg = synth.moss_config(256)
+    idx = ref.moss_encode(cfg)
+    lat = ref.moss_decode(cfg, idx)
+    save(name, idx=idx.astype(np.int16), latent_sha=sha(lat), latent_head=lat[:2, :16])
+
+
+def host_loop_bench(ref: Ref):
+    """Codes of bench.py's outetts_rvq and moss_rvq workloads (6 000 frames
+    each), from the reference's own functions."""
+    save("outetts_bench.npz", idx=ref.outetts_rvq(synth.outetts_config(6000)).astype(np.int16))
+    save("moss_bench.npz", idx=ref.moss_encode(synth.moss_config(6000)).astype(np.int16))
+
+
 def main():
-    which = set(sys.argv[1:]) or {"dac", "mimi", "kmeans", "q8"}
+    which = set(sys.argv[1:]) or {"dac", "mimi", "kmeans", "q8", "outetts", "moss"}
     ref = Ref("native")
     if "dac" in which:
         dac(ref, 0, "dac_cfg0.npz")
@@ -107,6 +132,11 @@ def main():
         kmeans(ref, "kmeans_cfg3.npz")
     if "q8" in which:
         q8(ref, "q8_cfg4.npz")
+    if "outetts" in which:
+        outetts(ref, "outetts_neardup.npz")
+    if "moss" in which:
+        moss(ref, "moss_v2.npz")
+        host_loop_bench(ref)
 
 
 if __name__ == "__main__":

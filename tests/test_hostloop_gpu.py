@@ -40,19 +40,6 @@ def oracle():
     return Oracle()
 
 
-def _near_duplicate_pairs(cb, seed):
-    cb = np.array(cb, np.float32, copy=True)
-    rng = np.random.default_rng(seed)
-    for s in range(cb.shape[0]):
-        half = cb.shape[1] // 2
-        cb[s, 1::2] = cb[s, 0::2]
-        k = rng.integers(0, cb.shape[2], half)
-        rows = cb[s, 1::2]
-        rows[np.arange(half), k] = np.nextafter(rows[np.arange(half), k], np.float32(np.inf))
-        cb[s, 1::2] = rows
-    return cb
-
-
 def _beq(a, b):
     a, b = np.asarray(a), np.asarray(b)
     return a.shape == b.shape and np.array_equal(a.view(np.uint8), b.view(np.uint8))
@@ -77,9 +64,11 @@ def run_outetts(torch, ctx, cfg, force_idx=None):
 
 @pytest.mark.parametrize("M,Q,near_dup", [(1, 2, False), (37, 2, False), (3001, 2, True), (200, 5, True)])
 def test_outetts_matches_oracle(torch, ctx, oracle, M, Q, near_dup):
-    cfg = __import__("aqmi.synth", fromlist=["x"]).outetts_config(M, Q=Q)
+    from aqmi import synth
+
+    cfg = synth.outetts_config(M, Q=Q)
     if near_dup:
-        cfg["codebook"] = _near_duplicate_pairs(cfg["codebook"], 7)
+        cfg["codebook"] = synth.near_duplicate_pairs(cfg["codebook"], 7)
     print(f"outetts M={M} Q={Q} near_dup={near_dup}", flush=True)
     got = run_outetts(torch, ctx, cfg)
     want = oracle.outetts_rvq(cfg)
@@ -238,3 +227,25 @@ def test_moss_errors(torch, ctx, oracle):
     with pytest.raises(aqmi.AqError, match="unsupported shape"):
         aqmi.MossQuantizer(ctx, f["w_ip"][:48], cfg["ip_b"][:48], f["w_in"][:, :, :48], cfg["in_b"], cfg["codebook"],
                            f["w_out"][:, :48], cfg["out_b"][:, :48])
+
+
+def test_outetts_golden(torch, ctx):
+    """Codes the reference's quantize_reference wrote (tests/golden)."""
+    from aqmi import synth
+
+    g = np.load(GOLDEN / "outetts_neardup.npz")
+    cfg = synth.outetts_config(3001)
+    cfg["codebook"] = synth.near_duplicate_pairs(cfg["codebook"], 7)
+    assert np.array_equal(run_outetts(torch, ctx, cfg)["idx"], g["idx"].astype(np.int32))
+
+
+def test_moss_golden(torch, ctx, oracle):
+    """Codes and decoded latent the reference's MossAudioTokenizerQuantizer
+    wrote (tests/golden)."""
+    import hashlib
+    from aqmi import synth
+
+    g = np.load(GOLDEN / "moss_v2.npz")
+    got = run_moss(torch, ctx, oracle, synth.moss_config(256))
+    assert np.array_equal(got["idx"], g["idx"].astype(np.int32))
+    assert hashlib.sha256(np.ascontiguousarray(got["latent"]).tobytes()).hexdigest() == str(g["latent_sha"])

@@ -424,28 +424,11 @@ def test_ema_codebook_closed_form(o):
 
 # ------------------------------------------------- host-loop DAC quantizers --
 
-def _near_duplicate_pairs(cb, seed):
-    """Odd codes = the even code before them with one component moved by one
-    ulp: the winner between the two depends on every rounding of the
-    distance, so an arithmetic slip (a fused multiply-add, another order)
-    changes codes."""
-    cb = np.array(cb, np.float32, copy=True)
-    rng = np.random.default_rng(seed)
-    for s in range(cb.shape[0]):
-        half = cb.shape[1] // 2
-        cb[s, 1::2] = cb[s, 0::2]
-        k = rng.integers(0, cb.shape[2], half)
-        rows = cb[s, 1::2]
-        rows[np.arange(half), k] = np.nextafter(rows[np.arange(half), k], np.float32(np.inf))
-        cb[s, 1::2] = rows
-    return cb
-
-
 @pytest.mark.parametrize("M,near_dup", [(1, False), (300, False), (2000, True)])
 def test_oracle_outetts_bit_exact_vs_reference(o, ref, M, near_dup):
     cfg = synth.outetts_config(M)
     if near_dup:
-        cfg["codebook"] = _near_duplicate_pairs(cfg["codebook"], 7)
+        cfg["codebook"] = synth.near_duplicate_pairs(cfg["codebook"], 7)
     assert np.array_equal(o.outetts_rvq(cfg)["idx"], ref.outetts_rvq(cfg))
 
 
@@ -461,7 +444,7 @@ def test_outetts_pin_detects_fused_multiply_add(ref, tmp_path):
     subprocess.run(["gcc", "-O2", "-fPIC", "-ffp-contract=fast", "-mfma", "-std=c11", "-shared", "-o", str(so),
                     str(HERE / "aq_oracle.c"), "-lm"], check=True)
     cfg = synth.outetts_config(2000)
-    cfg["codebook"] = _near_duplicate_pairs(cfg["codebook"], 7)
+    cfg["codebook"] = synth.near_duplicate_pairs(cfg["codebook"], 7)
     wrong = Oracle(so).outetts_rvq(cfg)["idx"]
     assert (wrong != ref.outetts_rvq(cfg)).sum() > 10
 
@@ -509,3 +492,27 @@ def test_oracle_moss_decode_range(o, ref):
         o.moss_decode(cfg, bad)
     with pytest.raises(IndexError):
         ref.moss_decode(cfg, bad)
+
+
+def test_oracle_outetts_matches_golden(o):
+    g = np.load(GOLDEN / "outetts_neardup.npz")
+    cfg = synth.outetts_config(3001)
+    cfg["codebook"] = synth.near_duplicate_pairs(cfg["codebook"], 7)
+    assert np.array_equal(o.outetts_rvq(cfg)["idx"], g["idx"].astype(np.int32))
+
+
+def test_oracle_moss_matches_golden(o):
+    g = np.load(GOLDEN / "moss_v2.npz")
+    cfg = synth.moss_config(256)
+    out = o.moss_rvq(cfg)
+    assert np.array_equal(out["idx"], g["idx"].astype(np.int32))
+    assert _sha(o.moss_decode(cfg, out["idx"])) == str(g["latent_sha"])
+
+
+def test_synth_moss_fold_is_the_reference_fold(o):
+    """bench.py folds the MOSS weights with numpy (aqmi.synth.moss_fold); the
+    bits must be the reference's reconstruct_weight_norm (via the oracle)."""
+    cfg = synth.moss_config(1, Q=3, N=64)
+    a, b = synth.moss_fold(cfg), o.moss_fold(cfg)
+    for k in a:
+        assert _beq(a[k], b[k]), k
