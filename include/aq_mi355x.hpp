@@ -162,15 +162,17 @@ private:
     aq_codebooks *cb_ = nullptr;
 };
 
-// Fish Audio DAC cosine RVQ (codec.cpp:552-611).
+// DAC cosine RVQ: Fish Audio (codec.cpp:552-611) and, by recipe, IndexTTS2,
+// Vevo2 and the OuteTTS host loop (dac.cpp:376-456).
 class DacRvq {
 public:
     // Host weights: w_in [Q,8,D], b_in [Q,8] or null, codebook [Q,N,8],
-    // w_out [Q,D,8], b_out [Q,D] or null (weight norm already folded).
+    // w_out [Q,D,8] (null: codes-only single stage), b_out [Q,D] or null
+    // (weight norm already folded).
     DacRvq(Context &ctx, int64_t Q, int64_t D, int64_t N, const float *w_in, const float *b_in, const float *codebook,
-           const float *w_out, const float *b_out)
+           const float *w_out, const float *b_out, aq_dac_recipe recipe = AQ_DAC_FISH)
         : ctx_(&ctx), Q_(Q), D_(D), N_(N) {
-        ctx.check(aq_dac_upload(ctx.get(), Q, D, N, w_in, b_in, codebook, w_out, b_out, &st_));
+        ctx.check(aq_dac_upload_ex(ctx.get(), Q, D, N, w_in, b_in, codebook, w_out, b_out, recipe, &st_));
     }
     DacRvq(const DacRvq &) = delete;
     DacRvq &operator=(const DacRvq &) = delete;
@@ -209,6 +211,61 @@ private:
     Context *ctx_;
     int64_t Q_, D_, N_;
     aq_dac_stages *st_ = nullptr;
+};
+
+// MOSS RLFQ quantizer (MossAudioTokenizerQuantizer,
+// models/moss/shared/audio_tokenizer_quantizer.cpp): fp64 encode, fp32 decode.
+class MossQuantizer {
+public:
+    // Host weights, weight norm folded: input_w [R,C], input_b [R], in_w
+    // [Q,8,R], in_b [Q,8], codebook [Q,N,8], out_w [Q,R,8], out_b [Q,R],
+    // output_w [C,R] and output_b [C] (both null: encode only).
+    MossQuantizer(Context &ctx, int64_t Q, int64_t N, int64_t code_dim, int64_t rvq_dim, const float *input_w,
+                  const float *input_b, const float *in_w, const float *in_b, const float *codebook,
+                  const float *out_w, const float *out_b, const float *output_w, const float *output_b)
+        : ctx_(&ctx), Q_(Q), C_(code_dim) {
+        ctx.check(aq_moss_upload(ctx.get(), Q, N, code_dim, rvq_dim, input_w, input_b, in_w, in_b, codebook, out_w,
+                                 out_b, output_w, output_b, &q_));
+    }
+    MossQuantizer(const MossQuantizer &) = delete;
+    MossQuantizer &operator=(const MossQuantizer &) = delete;
+    ~MossQuantizer() {
+        if (q_) aq_moss_release(q_);
+    }
+
+    // Device pointers: hidden [M, C] -> codes [M, Q]; residual [M, R] doubles or null.
+    void encode(const float *hidden, int64_t M, int32_t *codes, double *residual = nullptr,
+                const int32_t *force_idx = nullptr) const {
+        ctx_->check(aq_moss_encode(ctx_->get(), q_, hidden, M, codes, residual, force_idx));
+    }
+
+    // The reference's signature: hidden [frames, C] host, codes [Q][frames].
+    std::vector<std::vector<int32_t>> encode(const std::vector<float> &hidden, int64_t frames) const {
+        if (frames <= 0) throw std::runtime_error("MOSS codec quantizer requires a non-empty encoder latent");
+        if (static_cast<int64_t>(hidden.size()) != frames * C_)
+            throw std::runtime_error("MOSS codec quantizer got a mis-shaped encoder latent");
+        detail::DeviceBuffer<float> h(hidden.size());
+        detail::DeviceBuffer<int32_t> c(static_cast<size_t>(frames * Q_));
+        h.upload(hidden.data(), ctx_->stream());
+        encode(h.get(), frames, c.get());
+        std::vector<int32_t> flat(static_cast<size_t>(frames * Q_));
+        c.download(flat.data(), ctx_->stream());
+        ctx_->synchronize();
+        std::vector<std::vector<int32_t>> codes(static_cast<size_t>(Q_), std::vector<int32_t>(static_cast<size_t>(frames)));
+        for (int64_t m = 0; m < frames; ++m)
+            for (int64_t s = 0; s < Q_; ++s) codes[static_cast<size_t>(s)][static_cast<size_t>(m)] = flat[static_cast<size_t>(m * Q_ + s)];
+        return codes;
+    }
+
+    // Device pointers: codes [M, Q] -> latent [M, C] (frame-major).
+    void decode(const int32_t *codes, int64_t M, float *latent) const {
+        ctx_->check(aq_moss_decode(ctx_->get(), q_, codes, M, latent));
+    }
+
+private:
+    Context *ctx_;
+    int64_t Q_, C_;
+    aq_moss_quantizer *q_ = nullptr;
 };
 
 namespace engine::runtime {

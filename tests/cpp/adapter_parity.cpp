@@ -108,6 +108,56 @@ int main() {
                     idx.data(), res.data(), rec.data());
         expect(codes.values == idx, "DacRvq (Fish) codes == oracle");
     }
+    {   // DacRvq, OuteTTS host-loop recipe, its shapes (2 stages, D = N = 1024)
+        const int64_t M = 500, D = 1024, Q = 2, N = 1024;
+        const auto x = rng.normal(M * D, 1.0);
+        const auto w_in = rng.normal(Q * 8 * D, 1.0 / 32);
+        const auto cb = rng.normal(Q * N * 8, 1.0);
+        const auto w_out = rng.normal(Q * D * 8, 0.35);
+        const auto b_in = rng.normal(Q * 8, 0.1);
+        const auto b_out = rng.normal(Q * D, 0.1);
+        aq::DacRvq dac(*ctx, Q, D, N, w_in.data(), b_in.data(), cb.data(), w_out.data(), b_out.data(),
+                       AQ_DAC_OUTETTS);
+        const auto codes = dac.encode(x, M, M);
+        std::vector<int32_t> idx(M * Q);
+        std::vector<float> res(M * D);
+        aqo_outetts_rvq(x.data(), M, D, Q, N, w_in.data(), b_in.data(), cb.data(), w_out.data(), b_out.data(), nullptr,
+                        idx.data(), res.data());
+        expect(codes.values == idx, "DacRvq (OuteTTS) codes == oracle");
+    }
+    {   // MossQuantizer with the reference's encode signature ([Q][frames] codes)
+        const int64_t M = 64, C = 768, R = 512, Q = 12, N = 1024;
+        const auto h = rng.normal(M * C, 1.0);
+        auto fold = [&](int64_t lead, int64_t out_ch, int64_t in_ch) {
+            const auto v = rng.normal(lead * out_ch * in_ch, 1.0);
+            std::vector<float> g(static_cast<size_t>(lead * out_ch), 1.25f), w(v.size());
+            for (int64_t i = 0; i < lead; ++i)
+                aqo_moss_weight_norm(g.data() + i * out_ch, v.data() + i * out_ch * in_ch, out_ch, in_ch,
+                                     w.data() + i * out_ch * in_ch);
+            return w;
+        };
+        const auto w_ip = fold(1, R, C), w_in = fold(Q, 8, R), w_out = fold(Q, R, 8), w_op = fold(1, C, R);
+        const auto b_ip = rng.normal(R, 0.1), b_in = rng.normal(Q * 8, 0.1), b_out = rng.normal(Q * R, 0.1);
+        const auto b_op = rng.normal(C, 0.1);
+        const auto cb = rng.normal(Q * N * 8, 1.0);
+        aq::MossQuantizer moss(*ctx, Q, N, C, R, w_ip.data(), b_ip.data(), w_in.data(), b_in.data(), cb.data(),
+                               w_out.data(), b_out.data(), w_op.data(), b_op.data());
+        const auto codes = moss.encode(h, M);
+        std::vector<int32_t> idx(M * Q);
+        aqo_moss_rvq(h.data(), M, C, R, Q, N, w_ip.data(), b_ip.data(), w_in.data(), b_in.data(), cb.data(),
+                     w_out.data(), b_out.data(), nullptr, idx.data(), nullptr);
+        bool same = codes.size() == static_cast<size_t>(Q);
+        for (int64_t s = 0; same && s < Q; ++s)
+            for (int64_t m = 0; m < M; ++m) same = same && codes[s][m] == idx[m * Q + s];
+        expect(same, "MossQuantizer codes [Q][frames] == oracle");
+        try {
+            (void)moss.encode(std::vector<float>(10), 2);
+            expect(false, "MossQuantizer shape check throws");
+        } catch (const std::runtime_error &e) {
+            expect(std::string(e.what()) == "MOSS codec quantizer got a mis-shaped encoder latent",
+                   "MossQuantizer shape message");
+        }
+    }
     {   // errors surface as std::runtime_error with the library's message
         try {
             const auto cb = rng.normal(100 * 256, 1.0);
