@@ -336,8 +336,7 @@ aq_status aq_euclid_encode(aq_ctx *ctx, const aq_codebooks *cb, const float *x, 
     const int var = variant_of(cb->recipe, cb->q8);
     StageFn sweep = kk->sweep[cb->q8 ? 1 : 0][topl - 3];
     StageFn select = kk->select[var][topl - 3];
-    FallbackFn fvals = kk->fb_values[var];
-    FallbackFn fsel = kk->fb_select[var];
+    StageFn scan = kk->exact_scan[var];
     const int lds = kk->lds;
     AQ_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void *>(sweep), hipFuncAttributeMaxDynamicSharedMemorySize, lds));
     const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
@@ -353,8 +352,7 @@ aq_status aq_euclid_encode(aq_ctx *ctx, const aq_codebooks *cb, const float *x, 
     for (int sp = 1; sp <= 4; ++sp)
         if (nch % sp == 0 && tiles * sp <= 2 * cus) nsplit = sp;
     const int64_t ngroups = (M + 15) / 16;
-    const size_t fbv_lds = static_cast<size_t>(kFQ) * K * 5 + static_cast<size_t>(kFQ) * (K / 32) * 4 + 64;
-    const size_t fbs_lds = static_cast<size_t>(K) * 5 + (K / 32) * 4 + 64;
+    const size_t scan_lds = static_cast<size_t>(K) * 5 + (K / 32) * 4 + 64;
 
     // Work buffers: the residual (the caller's buffer when given), the
     // sweep's keys and frame norms, and the per-stage failure lists.
@@ -399,21 +397,6 @@ aq_status aq_euclid_encode(aq_ctx *ctx, const aq_codebooks *cb, const float *x, 
     rf.list2 = list2;
     RefineFn rvals = kk->refine_values[var];
     RefineFn rsel = kk->refine_select[var];
-    // Exact-scan work space: per failed frame, the best T codes of every
-    // 256-code block, and a NaN flag.
-    const int Tfb = (topk > 0 ? topk + 1 : 0) + 1;
-    FbArgs fb{};
-    fb.nch = static_cast<int>((cb->N + kFbChunk - 1) / kFbChunk);
-    {
-        const size_t cand = static_cast<size_t>(M) * fb.nch * Tfb;
-        void *w = nullptr;
-        aq_status st = aq_ctx_scratch(ctx, 2, cand * 8 + static_cast<size_t>(M) * 4, &w);
-        if (st != AQ_OK) return st;
-        fb.cand_v = static_cast<float *>(w);
-        fb.cand_n = reinterpret_cast<int32_t *>(fb.cand_v + cand);
-        fb.nan_flag = fb.cand_n + cand;
-        AQ_HIP(ctx, hipMemsetAsync(fb.nan_flag, 0, static_cast<size_t>(M) * 4, ctx->stream));
-    }
     AQ_HIP(ctx, hipMemsetAsync(counts, 0, sizeof(int32_t) * 128, ctx->stream));
     AQ_HIP(ctx, hipMemsetAsync(ctx->d_flags, 0, sizeof(int32_t) * AQ_FLAG_COUNT, ctx->stream));
 
@@ -454,7 +437,7 @@ aq_status aq_euclid_encode(aq_ctx *ctx, const aq_codebooks *cb, const float *x, 
         a.nsplit = nsplit;
         if (s >= 64 && s % 64 == 0) AQ_HIP(ctx, hipMemsetAsync(counts, 0, sizeof(int32_t) * 128, ctx->stream));
         const int tslot = aq_timing_start(ctx);
-        hipLaunchKernelGGL(sweep, dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(nsplit)), dim3(kThreads), lds,
+        hipLaunchKernelGGL(sweep, dim3(static_cast<unsigned>((tiles + 7) / 8 * 8 * nsplit)), dim3(kThreads), lds,
                            ctx->stream, a);
         aq_timing_stop(ctx, tslot);
         AQ_HIP(ctx, hipGetLastError());
@@ -474,9 +457,7 @@ aq_status aq_euclid_encode(aq_ctx *ctx, const aq_codebooks *cb, const float *x, 
         StageArgs a2 = a;
         a2.fail_count = rf.count2;
         a2.fail_list = list2;
-        hipLaunchKernelGGL(fvals, dim3(static_cast<unsigned>(2 * cus)), dim3(kFbChunk), fbv_lds, ctx->stream, a2, K, fb);
-        AQ_HIP(ctx, hipGetLastError());
-        hipLaunchKernelGGL(fsel, dim3(static_cast<unsigned>(cus)), dim3(kFbSel), fbs_lds, ctx->stream, a2, K, fb);
+        hipLaunchKernelGGL(scan, dim3(static_cast<unsigned>(cus)), dim3(kScanThreads), scan_lds, ctx->stream, a2);
         AQ_HIP(ctx, hipGetLastError());
     }
     if (force_idx) {

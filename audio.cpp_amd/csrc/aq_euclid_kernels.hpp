@@ -41,10 +41,13 @@
 //    Cauchy-Schwarz), the fp32 accumulation bounds and the key truncation.
 //    Kept candidates that could still be in the top T are re-ranked exactly;
 //    the result is certified when the T-th exact value beats every unkept
-//    code's bound.  Otherwise the frame goes to an exact full scan (fallback
-//    kernel), so results never depend on bf16 rounding.
-//  * Residual cascade: per stage one score kernel (re-rank, update r -= c)
-//    and one fallback kernel that exits at once when no frame failed.
+//    code's bound.  Otherwise the frame is scored again with split bf16
+//    operands (a bound about 2^-8 of the first) and, if that certificate
+//    fails too, by an exact full scan, so results never depend on bf16
+//    rounding.
+//  * Residual cascade: per stage the sweep, the select (re-rank, update
+//    r -= c), the refine pair and the exact scan; the last three exit at
+//    once when no frame is left for them.
 #pragma once
 
 #include "aq_internal.hpp"
@@ -63,9 +66,6 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 enum Recipe : int { OMNI = 0, HIGGS = 1, DIRECT = 2 };
-
-constexpr int kFQ = 4;        // failed frames per fb_values block
-constexpr int kFbChunk = 256; // codes per fb_values block
 
 constexpr int kRS = 256;       // codes per refine slice (64 per lane: 6 index bits)
 constexpr int kTopR = 4;       // keys per lane and slice
@@ -115,13 +115,6 @@ struct StageArgs {
     int nsplit;              // code splits of the sweep
 };
 
-struct FbArgs {
-    float *cand_v;     // [M][nch][T]
-    int32_t *cand_n;   // [M][nch][T]
-    int32_t *nan_flag; // [M]
-    int nch;
-};
-
 struct RefArgs {
     const uint16_t *cbl;       // [N, K] bf16(c - bf16(c))
     float *keys;               // [cap][nslices][4][kTopR]
@@ -133,7 +126,6 @@ struct RefArgs {
 };
 
 using StageFn = void (*)(StageArgs);
-using FallbackFn = void (*)(StageArgs, int, FbArgs);
 using RefineFn = void (*)(StageArgs, RefArgs);
 
 // 16-frame groups per sweep wave: the bf16 frames of a wave stay in
@@ -151,8 +143,7 @@ struct KsKernels {
     StageFn select[4][2];     // [variant][topl]
     RefineFn refine_values[4];
     RefineFn refine_select[4];
-    FallbackFn fb_values[4];
-    FallbackFn fb_select[4];
+    StageFn exact_scan[4];
     int lds;                  // sweep dynamic LDS bytes
     int cc;                   // codes per LDS chunk
 };
@@ -476,7 +467,7 @@ __device__ inline float key_of(float v, unsigned local, unsigned keep) {
 }
 
 
-// Sweep of one stage: every frame against the codes of split blockIdx.y.
+// Sweep of one stage: every frame of a tile against the codes of one split.
 // Up to K = 256 two blocks share a CU (256 VGPRs per lane at most), so the
 // matrix pipe of a SIMD is fed by two waves; wider frames need the whole
 // register file of one wave.  The frames' certificate and re-ranking run in
@@ -492,10 +483,18 @@ __global__ __launch_bounds__(kThreads, sweep_blocks_per_cu(KS)) void euclid_swee
     const int wave = threadIdx.x / kWave;
     const int col = lane & 15;      // frame within a 16-frame group
     const int kq = lane >> 4;       // which 8-element quarter of each 32-wide K slice
-    const int64_t m_base = (static_cast<int64_t>(blockIdx.x) * kWaves + wave) * (FG * 16);
+    // Block order: the nsplit blocks of a frame tile have ids 8 apart, so
+    // the round-robin dispatch over the 8 XCDs puts them on one XCD and the
+    // second read of the tile's frames is served by that XCD's L2.  Ids
+    // past the last tile (the grid is a whole number of 8-tile groups) exit.
+    const int per = 8 * a.nsplit;
+    const int split = static_cast<int>(blockIdx.x % per) / 8;
+    const int64_t tile = static_cast<int64_t>(blockIdx.x / per) * 8 + (blockIdx.x % per) % 8;
+    if (tile * (kWaves * FG * 16) >= a.M) return;
+    const int64_t m_base = (tile * kWaves + wave) * (FG * 16);
     const int N = a.N;
     const int cps = (N / T::CC) / a.nsplit;   // chunks per split
-    const int c0 = static_cast<int>(blockIdx.y) * cps, c1 = c0 + cps;
+    const int c0 = split * cps, c1 = c0 + cps;
 
     // ---- phase 0: frames -> bf16 fragments in registers, rounding norms ----
     // x~ fragments stay packed (2 bf16 per register) for the whole sweep.
@@ -708,10 +707,10 @@ __global__ __launch_bounds__(kThreads, sweep_blocks_per_cu(KS)) void euclid_swee
         if (gi < ngroups) {
 #pragma unroll
             for (int j = 0; j < TOPL; ++j)
-                a.keys[((static_cast<int64_t>(blockIdx.y) * ngroups + gi) * TOPL + j) * kWave + lane] = top[g][j];
+                a.keys[((static_cast<int64_t>(split) * ngroups + gi) * TOPL + j) * kWave + lane] = top[g][j];
         }
         const int64_t m = m_base + g * 16 + col;
-        if (blockIdx.y == 0 && kq == 0 && m < a.M) {
+        if (split == 0 && kq == 0 && m < a.M) {
             a.norms[m] = nx2[g];
             a.norms[a.M + m] = nd2[g];
             a.norms[2 * a.M + m] = nxx2[g];
@@ -1139,99 +1138,21 @@ __global__ __launch_bounds__(kThreads) void euclid_select_kernel(StageArgs a) {
     }
 }
 
-// ------------------------------------------------------------ fallback kernels
+// ------------------------------------------------------------- exact scan
 
-// Frames the certificate could not settle get an exact scan of every code,
-// in two launches that each spread over the whole GPU:
-//  * fb_values: a block takes FQ failed frames x 256 codes (one code per
-//    thread), evaluates the recipe value of every (frame, code) pair with one
-//    pass over the code's row, and reduces it to the block's best T codes per
-//    frame (the reference's ranking);
-//  * fb_select: one wave per failed frame merges the per-block candidates,
-//    writes the codes / distances / top-k and updates the residual.  A frame
-//    whose values contain NaN replays ggml_vec_argmax_f32 in code order.
-
-
-// Recipe values of code n for FQ query frames held in LDS, one pass over the
-// code's row (tinyBLAS order; the vec_dot order only occurs for M == 1 and is
-// evaluated frame by frame).
-template <int RECIPE, bool Q8, int K>
-__device__ void exact_values_fq(const StageArgs &a, int n, const float *xs, const float *x2, const int8_t *xq,
-                                const float *xd, int nf, float (&out)[kFQ]) {
-    const float *c = a.cbf + static_cast<int64_t>(n) * K;
-    if (RECIPE == DIRECT) {
-        float d[kFQ];
-#pragma unroll
-        for (int f = 0; f < kFQ; ++f) d[f] = 0.0f;
-        for (int k = 0; k < K; ++k) {
-            const float ck = c[k];
-#pragma unroll
-            for (int f = 0; f < kFQ; ++f) {
-                const float diff = __fsub_rn(xs[f * K + k], ck);
-                d[f] = __fadd_rn(d[f], __fmul_rn(diff, diff));
-            }
-        }
-#pragma unroll
-        for (int f = 0; f < kFQ; ++f) out[f] = d[f];
-        return;
-    }
-    float dot[kFQ];
-    if (Q8) {
-        const int8_t *qc = a.q8 + static_cast<int64_t>(n) * K;
-        const float *dc = a.q8d + static_cast<int64_t>(n) * (K / 32);
-        float acc[kFQ][8];
-#pragma unroll
-        for (int f = 0; f < kFQ; ++f)
-#pragma unroll
-            for (int l = 0; l < 8; ++l) acc[f][l] = 0.0f;
-        for (int ib = 0; ib < K / 32; ++ib) {
-            const int *pc = reinterpret_cast<const int *>(qc + 32 * ib);
-            int cw[8];
-#pragma unroll
-            for (int l = 0; l < 8; ++l) cw[l] = pc[l];
-#pragma unroll
-            for (int f = 0; f < kFQ; ++f) {
-                const float dd = __fmul_rn(dc[ib], xd[f * (K / 32) + ib]);
-                const int *px = reinterpret_cast<const int *>(xq + f * K + 32 * ib);
-#pragma unroll
-                for (int l = 0; l < 8; ++l)
-                    acc[f][l] = __fmaf_rn(dd, static_cast<float>(__builtin_amdgcn_sdot4(cw[l], px[l], 0, false)), acc[f][l]);
-            }
-        }
-#pragma unroll
-        for (int f = 0; f < kFQ; ++f) dot[f] = reduce8(acc[f]);
-    } else if (a.order == 0) {
-        const float sa = RECIPE == OMNI ? 2.0f : 1.0f;
-        float acc[kFQ][16];
-#pragma unroll
-        for (int f = 0; f < kFQ; ++f)
-#pragma unroll
-            for (int j = 0; j < 16; ++j) acc[f][j] = 0.0f;
-        for (int l = 0; l < K; l += 16) {
-            float cv[16];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const f32x4 v = *reinterpret_cast<const f32x4 *>(c + l + 4 * q);
-#pragma unroll
-                for (int t = 0; t < 4; ++t) cv[4 * q + t] = v[t] * sa;
-            }
-#pragma unroll
-            for (int f = 0; f < kFQ; ++f)
-#pragma unroll
-                for (int j = 0; j < 16; ++j) acc[f][j] = __fmaf_rn(cv[j], xs[f * K + l + j], acc[f][j]);
-        }
-#pragma unroll
-        for (int f = 0; f < kFQ; ++f) dot[f] = reduce16(acc[f]);
-    } else {
-        const float sa = RECIPE == OMNI ? 2.0f : 1.0f;
-#pragma unroll
-        for (int f = 0; f < kFQ; ++f) dot[f] = f < nf ? dot_vecdot(c, xs + f * K, K, sa) : 0.0f;
-    }
-#pragma unroll
-    for (int f = 0; f < kFQ; ++f)
-        out[f] = RECIPE == OMNI ? __fadd_rn(dot[f], a.bias[n])
-                                : __fsub_rn(__fsub_rn(__fmul_rn(dot[f], 2.0f), x2[f]), a.e2[n]);
-}
+// Frames that neither certificate settles get an exact scan: one block per
+// frame evaluates the recipe value of every code (kScanChunk codes at a time
+// into LDS, one code per thread), and wave 0 walks each chunk in code order
+// with the reference's selection rules, so the result is the reference's by
+// construction, ties and NaN included:
+//  * ggml recipes: ggml_vec_argmax_f32 (running MAX(max, v), index of the
+//    last element equal to the running max, a NaN restarts it) and
+//    ggml_top_k's std::partial_sort heap;
+//  * DIRECT: the first index of the minimum distance (strict <, NaN never
+//    wins) and the k smallest distances (ties by index).
+// The walk takes 64 codes per step: a chunk without NaN is reduced with a
+// wave max / min and a ballot, and the heap only visits codes that beat its
+// root.
 
 // One step of libstdc++'s binary heap (GCC 11.4 std::__adjust_heap followed
 // by std::__push_heap) with comp(a, b) = value(a) > value(b): the root holds
@@ -1265,335 +1186,162 @@ __device__ void heap_adjust(int *hn, float *hv, int hole, int len, int vn, float
     hv[hole] = vv;
 }
 
-template <int RECIPE>
-__device__ inline bool fb_before(float va, int na, float vb, int nb, bool topk) {
-    return topk ? topk_before<RECIPE>(va, na, vb, nb) : ranks_before<RECIPE>(va, na, vb, nb);
-}
-
-// Wave-wide selection of the best (value, index) pair under fb_before;
-// entries with index < 0 are empty.  Every lane returns the winner.
-template <int RECIPE>
-__device__ inline void wave_best(float &v, int &n, bool topk) {
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-        const float ov = __shfl_xor(v, off);
-        const int on = __shfl_xor(n, off);
-        if (on >= 0 && (n < 0 || fb_before<RECIPE>(ov, on, v, n, topk))) {
-            v = ov;
-            n = on;
-        }
-    }
-}
+constexpr int kScanThreads = 256;
+constexpr int kScanChunk = 2048;
 
 template <int RECIPE, bool Q8, int KS>
-__global__ __launch_bounds__(kFbChunk) void euclid_fb_values_kernel(StageArgs a, int /*K*/, FbArgs fb) {
-    constexpr int K = KS * 32;
-    extern __shared__ __align__(16) unsigned char lds[];
-    float *xs = reinterpret_cast<float *>(lds);                         // [kFQ][K]
-    int8_t *xq = reinterpret_cast<int8_t *>(xs + kFQ * K);              // [kFQ][K]
-    float *xd = reinterpret_cast<float *>(xq + kFQ * K);                // [kFQ][K/32]
-    constexpr int kW = kFbChunk / kWave;
-    __shared__ float x2s[kFQ];
-    __shared__ float wv[kW][kFQ][6];
-    __shared__ int wn[kW][kFQ][6];
-    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-    const int count = *a.fail_count;
-    // top-k slots (value desc, index asc; one more than k to see a tie at the
-    // k-th place), then the argmax slot (the reference's tie rule)
-    const int T = a.topk > 0 ? a.topk + 1 : 0;
-    const int Tc = T + 1;
-    const int nb = K / 32;
-    const int ngroups = (count + kFQ - 1) / kFQ;
-    const int64_t nwork = static_cast<int64_t>(ngroups) * fb.nch;
-    for (int64_t w = blockIdx.x; w < nwork; w += gridDim.x) {
-        const int grp = static_cast<int>(w / fb.nch), ch = static_cast<int>(w % fb.nch);
-        const int nf = min(kFQ, count - grp * kFQ);
-        __syncthreads();
-        for (int i = threadIdx.x; i < kFQ * K; i += kFbChunk) {
-            const int f = i / K, k = i % K;
-            xs[i] = f < nf ? a.xin[static_cast<int64_t>(a.fail_list[grp * kFQ + f]) * K + k] : 0.0f;
-        }
-        __syncthreads();
-        if (threadIdx.x < kFQ) {
-            const int f = threadIdx.x;
-            x2s[f] = RECIPE == OMNI || f >= nf ? 0.0f : sum_squares(xs + f * K, K);
-        }
-        if (Q8 && threadIdx.x < kFQ * nb) {   // one 32-element block per thread
-            const int f = threadIdx.x / nb, ib = threadIdx.x % nb;
-            quantize_block_q8(xs + f * K + 32 * ib, xq + f * K + 32 * ib, xd + f * nb + ib);
-        }
-        __syncthreads();
-        const int n = ch * kFbChunk + threadIdx.x;
-        const bool valid = n < a.N;
-        float vals[kFQ];
-        if (valid) {
-            exact_values_fq<RECIPE, Q8, K>(a, n, xs, x2s, xq, xd, nf, vals);
-        } else {
-#pragma unroll
-            for (int f = 0; f < kFQ; ++f) vals[f] = 0.0f;
-        }
-        // Per wave: the best T codes in top-k order (T rounds with the
-        // winners excluded) and the best in argmax order, per frame.
-#pragma unroll
-        for (int f = 0; f < kFQ; ++f) {
-            if (f >= nf) break;
-            float v = vals[f];
-            if (valid && v != v) fb.nan_flag[grp * kFQ + f] = 1;
-            if (v != v) v = RECIPE == DIRECT ? INFINITY : -INFINITY;
-            bool taken = false;
-            for (int r = 0; r < Tc; ++r) {
-                const bool tk = r < T;
-                float bv = v;
-                int bn = valid && !(tk && taken) ? n : -1;
-                wave_best<RECIPE>(bv, bn, tk);
-                if (tk && bn == n) taken = true;
-                if (lane == 0) {
-                    wv[wave][f][r] = bv;
-                    wn[wave][f][r] = bn;
-                }
-            }
-        }
-        __syncthreads();
-        // Merge the waves' lists: thread (f, r) writes slot r of frame f.
-        if (threadIdx.x < nf * Tc) {
-            const int f = threadIdx.x / Tc, r = threadIdx.x % Tc;
-            const int slot = grp * kFQ + f;
-            float bv = 0.0f;
-            int bn = -1;
-            if (r < T) {
-                // r-th best of the union in top-k order: count the entries
-                // that rank before each candidate.
-                for (int q = 0; q < kW * T; ++q) {
-                    const float cv = wv[q / T][f][q % T];
-                    const int cn = wn[q / T][f][q % T];
-                    if (cn < 0) continue;
-                    int before = 0;
-                    for (int o = 0; o < kW * T; ++o) {
-                        const int on = wn[o / T][f][o % T];
-                        if (on >= 0 && fb_before<RECIPE>(wv[o / T][f][o % T], on, cv, cn, true)) ++before;
-                    }
-                    if (before == r) {
-                        bv = cv;
-                        bn = cn;
-                    }
-                }
-            } else {
-                for (int q = 0; q < kW; ++q) {
-                    const float cv = wv[q][f][T];
-                    const int cn = wn[q][f][T];
-                    if (cn >= 0 && (bn < 0 || fb_before<RECIPE>(cv, cn, bv, bn, false))) {
-                        bv = cv;
-                        bn = cn;
-                    }
-                }
-            }
-            const int64_t o = (static_cast<int64_t>(slot) * fb.nch + ch) * Tc + r;
-            fb.cand_v[o] = bv;
-            fb.cand_n[o] = bn;
-        }
-    }
-}
-
-// fb_select block: wave 0 merges the candidates; a replay in code order
-// (NaN scores or a tie at the k-th place) uses the whole block to compute the
-// exact values kFbReplay codes at a time, then one thread runs ggml's argmax
-// and the top-k heap over them.
-constexpr int kFbSel = 256;
-constexpr int kFbReplay = 2048;
-
-template <int RECIPE, bool Q8, int KS>
-__global__ __launch_bounds__(kFbSel) void euclid_fb_select_kernel(StageArgs a, int /*K*/, FbArgs fb) {
+__global__ __launch_bounds__(kScanThreads) void euclid_exact_scan_kernel(StageArgs a) {
     constexpr int K = KS * 32;
     extern __shared__ __align__(16) unsigned char lds[];
     float *xs = reinterpret_cast<float *>(lds);                         // [K]
     int8_t *xq = reinterpret_cast<int8_t *>(xs + K);                    // [K]
     float *xd = reinterpret_cast<float *>(xq + K);                      // [K/32]
-    __shared__ float rv[kFbReplay];
+    __shared__ float rv[kScanChunk];
     __shared__ int heap_n[4];
     __shared__ float heap_v[4];
-    __shared__ int o_code, o_sel_n[5], o_replay, o_nan;
-    __shared__ float o_code_v, o_sel_v[5], o_x2;
+    __shared__ int o_code, o_sel_n[4];
+    __shared__ float o_code_v, o_sel_v[4], o_x2;
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const int count = *a.fail_count;
-    const int T = a.topk > 0 ? a.topk + 1 : 0;
-    const int Tc = T + 1;
     const int ktop = a.topk;
     for (int slot = blockIdx.x; slot < count; slot += gridDim.x) {
         const int64_t m = a.fail_list[slot];
         __syncthreads();
-        if (tid < kWave) {
-            float sel_v[5];
-            int sel_n[5];
-#pragma unroll
-            for (int r = 0; r < 5; ++r) {
-                sel_v[r] = 0.0f;
-                sel_n[r] = -1;
-            }
-            // ranked merge of the per-block candidates (lane-strided, then a wave
-            // merge): r < T merges the top-k slots, r == T the argmax slots
-            const int total = fb.nch * Tc;
-            int code = 0;
-            float code_v = 0.0f;
-            for (int r = 0; r < Tc; ++r) {
-                const bool tk = r < T;
-                float bv = 0.0f;
-                int bn = -1;
-                for (int i = lane; i < total; i += kWave) {
-                    if (tk != (i % Tc < T)) continue;
-                    const int64_t o = static_cast<int64_t>(slot) * total + i;
-                    const int n = fb.cand_n[o];
-                    if (n < 0) continue;
-                    bool skip = false;
-                    if (tk)
-                        for (int q = 0; q < r; ++q) skip |= (sel_n[q] == n);
-                    const float v = fb.cand_v[o];
-                    if (!skip && (bn < 0 || fb_before<RECIPE>(v, n, bv, bn, tk))) {
-                        bv = v;
-                        bn = n;
-                    }
-                }
-                for (int off = 1; off < kWave; off <<= 1) {
-                    const float ov = __shfl_xor(bv, off);
-                    const int on = __shfl_xor(bn, off);
-                    if (on >= 0 && (bn < 0 || fb_before<RECIPE>(ov, on, bv, bn, tk))) {
-                        bv = ov;
-                        bn = on;
-                    }
-                }
-                if (tk) {
-#pragma unroll
-                    for (int q = 0; q < 5; ++q)
-                        if (q == r) {
-                            sel_v[q] = bv;
-                            sel_n[q] = bn;
-                        }
-                } else {
-                    code = bn < 0 ? 0 : bn;
-                    code_v = bv;
-                }
-            }
-            bool kth_tie = false;
-#pragma unroll
-            for (int q = 1; q < 5; ++q)
-                if (q == ktop) kth_tie = sel_n[q] >= 0 && sel_v[q] == sel_v[q - 1];
-            const bool nan_seen = fb.nan_flag[slot] != 0;
-            if (lane == 0) {
-                o_code = code;
-                o_code_v = code_v;
-#pragma unroll
-                for (int q = 0; q < 5; ++q) {
-                    o_sel_n[q] = sel_n[q];
-                    o_sel_v[q] = sel_v[q];
-                }
-                o_nan = nan_seen ? 1 : 0;
-                o_replay = (RECIPE != DIRECT && (nan_seen || (ktop > 0 && kth_tie))) ? 1 : 0;
-            }
-        }
+        for (int k = tid; k < K; k += kScanThreads) xs[k] = a.xin[m * K + k];
         __syncthreads();
-        if (o_replay) {
-            // Replay in code order: ggml_vec_argmax_f32 (MAX(max, v), index of
-            // the last element equal to the running max; NaN restarts it) and
-            // ggml_top_k's heap selection (libstdc++ std::partial_sort).
-            for (int k = tid; k < K; k += kFbSel) xs[k] = a.xin[m * K + k];
+        if (tid == 0) o_x2 = RECIPE == HIGGS ? sum_squares(xs, K) : 0.0f;
+        if (Q8 && tid < K / 32) quantize_block_q8(xs + 32 * tid, xq + 32 * tid, xd + tid);
+        __syncthreads();
+        const float x2 = o_x2;
+        // wave 0's running selection state (uniform across its lanes)
+        float mx = RECIPE == DIRECT ? INFINITY : -INFINITY;
+        int id = 0;
+        float root = 0.0f;   // heap root (ggml recipes) / k-th kept distance (DIRECT)
+        int kept = 0;        // DIRECT: entries in the kept list
+        for (int base = 0; base < a.N; base += kScanChunk) {
+            const int len = min(kScanChunk, a.N - base);
+            for (int i = tid; i < len; i += kScanThreads) rv[i] = exact_value_kq<RECIPE, Q8, K>(a, xs, base + i, x2, xq, xd);
             __syncthreads();
-            if (tid == 0) o_x2 = RECIPE == HIGGS ? sum_squares(xs, K) : 0.0f;
-            if (Q8 && tid < K / 32) quantize_block_q8(xs + 32 * tid, xq + 32 * tid, xd + tid);
-            __syncthreads();
-            const float x2 = o_x2;
-            float mx = -INFINITY, root = 0.0f;
-            int id = 0;
-            for (int base = 0; base < a.N; base += kFbReplay) {
-                const int len = min(kFbReplay, a.N - base);
-                for (int i = tid; i < len; i += kFbSel) rv[i] = exact_value_kq<RECIPE, Q8, K>(a, xs, base + i, x2, xq, xd);
-                __syncthreads();
-                if (tid < kWave) {
-                    // Wave 0 walks the codes 64 at a time.  The argmax of a
-                    // chunk without NaN is the last code equal to its largest
-                    // value (MAX keeps a later equal element); a chunk with a
-                    // NaN, or after one, is walked code by code.  The heap
-                    // takes a code only if it beats the root, so a chunk where
-                    // no code does is skipped at once.
-                    for (int c0 = 0; c0 < len; c0 += kWave) {
-                        const int i = c0 + lane;
-                        const bool in = i < len;
-                        const float v = in ? rv[i] : 0.0f;
-                        const bool nan_chunk = __any(in && v != v) || mx != mx;
-                        if (nan_chunk) {
-                            const int cl = min(kWave, len - c0);
-                            for (int t = 0; t < cl; ++t) {
-                                const float vt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), t));
-                                mx = mx > vt ? mx : vt;
-                                if (mx == vt) id = base + c0 + t;
-                            }
-                        } else {
-                            float cm = in ? v : -INFINITY;
+            if (tid < kWave) {
+                for (int c0 = 0; c0 < len; c0 += kWave) {
+                    const int i = c0 + lane;
+                    const bool in = i < len;
+                    const float v = in ? rv[i] : 0.0f;
+                    if (RECIPE == DIRECT) {
+                        // first index of the minimum: strict <, NaN never wins
+                        float cm = in ? v : INFINITY;
 #pragma unroll
-                            for (int off = 1; off < kWave; off <<= 1) cm = fmaxf(cm, __shfl_xor(cm, off));
+                        for (int off = 1; off < kWave; off <<= 1) cm = fminf(cm, __shfl_xor(cm, off));
+                        if (cm < mx) {
                             const unsigned long long eq = __ballot(in && v == cm);
-                            if (eq != 0 && !(mx > cm)) {
-                                const int last = 63 - __clzll(static_cast<long long>(eq));
-                                mx = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), last));
-                                id = base + c0 + last;
-                            }
+                            const int first = __ffsll(static_cast<long long>(eq)) - 1;
+                            mx = cm;
+                            id = base + c0 + first;
                         }
                         if (ktop > 0) {
-                            // the first ktop codes build the heap
-                            for (int t = 0; t < kWave && base + c0 + t < ktop; ++t) {
-                                const int n_t = base + c0 + t;
-                                const float vt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), t));
-                                if (lane == 0) {
-                                    heap_n[n_t] = n_t;
-                                    heap_v[n_t] = vt;
-                                    if (n_t == ktop - 1 && ktop >= 2)
-                                        for (int par = (ktop - 2) / 2;; --par) {
-                                            heap_adjust(heap_n, heap_v, par, ktop, heap_n[par], heap_v[par]);
-                                            if (par == 0) break;
-                                        }
-                                }
-                                __builtin_amdgcn_wave_barrier();
-                                if (n_t == ktop - 1) root = heap_v[0];
-                            }
-                            int from = 0;   // lanes before `from` are done
+                            // the k smallest (value, index): insert, in code
+                            // order, every code that ranks before the k-th
+                            int from = 0;
                             while (true) {
-                                const unsigned long long take =
-                                    __ballot(in && lane >= from && base + i >= ktop && v > root);
+                                const bool cand = in && lane >= from && v == v &&
+                                                  (kept < ktop || v < root);
+                                const unsigned long long take = __ballot(cand);
                                 if (take == 0) break;
                                 const int f = __ffsll(static_cast<long long>(take)) - 1;
                                 const float vf = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), f));
-                                if (lane == 0) heap_adjust(heap_n, heap_v, 0, ktop, base + c0 + f, vf);
+                                if (lane == 0) {
+                                    int p = kept < ktop ? kept : ktop - 1;
+                                    while (p > 0 && vf < heap_v[p - 1]) {
+                                        heap_v[p] = heap_v[p - 1];
+                                        heap_n[p] = heap_n[p - 1];
+                                        --p;
+                                    }
+                                    heap_v[p] = vf;
+                                    heap_n[p] = base + c0 + f;
+                                }
                                 __builtin_amdgcn_wave_barrier();
-                                root = heap_v[0];
+                                kept = min(kept + 1, ktop);
+                                root = heap_v[ktop - 1];
                                 from = f + 1;
                             }
                         }
+                        continue;
                     }
-                }
-                __syncthreads();
-            }
-            if (tid == 0) {
-                if (o_nan) {
-                    o_code = id;
-                    o_code_v = mx;
-                }
-                if (ktop > 0) {
-                    // report the kept set best first, ties by index
-                    int used[4] = {-1, -1, -1, -1};
-                    for (int r = 0; r < ktop; ++r) {
-                        int b = -1;
-                        for (int q = 0; q < ktop; ++q) {
-                            bool u = false;
-                            for (int t = 0; t < r; ++t) u |= used[t] == q;
-                            if (!u && (b < 0 || topk_before<RECIPE>(heap_v[q], heap_n[q], heap_v[b], heap_n[b]))) b = q;
+                    // ggml_vec_argmax_f32
+                    const bool nan_chunk = __any(in && v != v) || mx != mx;
+                    if (nan_chunk) {
+                        const int cl = min(kWave, len - c0);
+                        for (int t = 0; t < cl; ++t) {
+                            const float vt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), t));
+                            mx = mx > vt ? mx : vt;
+                            if (mx == vt) id = base + c0 + t;
                         }
-                        used[r] = b;
-                        o_sel_n[r] = heap_n[b];
-                        o_sel_v[r] = heap_v[b];
+                    } else {
+                        float cm = in ? v : -INFINITY;
+#pragma unroll
+                        for (int off = 1; off < kWave; off <<= 1) cm = fmaxf(cm, __shfl_xor(cm, off));
+                        const unsigned long long eq = __ballot(in && v == cm);
+                        if (eq != 0 && !(mx > cm)) {
+                            const int last = 63 - __clzll(static_cast<long long>(eq));
+                            mx = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), last));
+                            id = base + c0 + last;
+                        }
+                    }
+                    if (ktop > 0) {
+                        // ggml_top_k: the first ktop codes build the heap,
+                        // a later code replaces the root if strictly better
+                        for (int t = 0; t < kWave && base + c0 + t < ktop; ++t) {
+                            const int n_t = base + c0 + t;
+                            const float vt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), t));
+                            if (lane == 0) {
+                                heap_n[n_t] = n_t;
+                                heap_v[n_t] = vt;
+                                if (n_t == ktop - 1 && ktop >= 2)
+                                    for (int par = (ktop - 2) / 2;; --par) {
+                                        heap_adjust(heap_n, heap_v, par, ktop, heap_n[par], heap_v[par]);
+                                        if (par == 0) break;
+                                    }
+                            }
+                            __builtin_amdgcn_wave_barrier();
+                            if (n_t == ktop - 1) root = heap_v[0];
+                        }
+                        int from = 0;   // lanes before `from` are done
+                        while (true) {
+                            const unsigned long long take =
+                                __ballot(in && lane >= from && base + i >= ktop && v > root);
+                            if (take == 0) break;
+                            const int f = __ffsll(static_cast<long long>(take)) - 1;
+                            const float vf = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), f));
+                            if (lane == 0) heap_adjust(heap_n, heap_v, 0, ktop, base + c0 + f, vf);
+                            __builtin_amdgcn_wave_barrier();
+                            root = heap_v[0];
+                            from = f + 1;
+                        }
                     }
                 }
             }
             __syncthreads();
         }
+        if (tid == 0) {
+            o_code = id;
+            o_code_v = mx;
+            // the kept set, best first, ties by index
+            int used[4] = {-1, -1, -1, -1};
+            const int nk = RECIPE == DIRECT ? kept : ktop;
+            for (int r = 0; r < ktop; ++r) {
+                int b = -1;
+                for (int q = 0; q < nk; ++q) {
+                    bool u = false;
+                    for (int t = 0; t < r; ++t) u |= used[t] == q;
+                    if (!u && (b < 0 || topk_before<RECIPE>(heap_v[q], heap_n[q], heap_v[b], heap_n[b]))) b = q;
+                }
+                used[r] = b;
+                o_sel_n[r] = b < 0 ? 0 : heap_n[b];
+                o_sel_v[r] = b < 0 ? INFINITY : heap_v[b];
+            }
+        }
+        __syncthreads();
         const int code = o_code;
         if (tid == 0) {
             a.idx[m * a.Q + a.s] = code;
@@ -1611,9 +1359,8 @@ __global__ __launch_bounds__(kFbSel) void euclid_fb_select_kernel(StageArgs a, i
                 use = 0;
             }
         }
-        for (int k = tid; k < K; k += kFbSel)
+        for (int k = tid; k < K; k += kScanThreads)
             a.xout[m * K + k] = __fsub_rn(a.xin[m * K + k], a.cbf[static_cast<int64_t>(use) * K + k]);
-        if (tid == 0) fb.nan_flag[slot] = 0;
     }
 }
 
@@ -2020,10 +1767,8 @@ __global__ __launch_bounds__(kWave) void euclid_refine_select_kernel(StageArgs a
              euclid_refine_values_kernel<DIRECT, false, KS>, euclid_refine_values_kernel<HIGGS, true, KS>},     \
             {euclid_refine_select_kernel<OMNI, false, KS>, euclid_refine_select_kernel<HIGGS, false, KS>,       \
              euclid_refine_select_kernel<DIRECT, false, KS>, euclid_refine_select_kernel<HIGGS, true, KS>},     \
-            {euclid_fb_values_kernel<OMNI, false, KS>, euclid_fb_values_kernel<HIGGS, false, KS>,               \
-             euclid_fb_values_kernel<DIRECT, false, KS>, euclid_fb_values_kernel<HIGGS, true, KS>},             \
-            {euclid_fb_select_kernel<OMNI, false, KS>, euclid_fb_select_kernel<HIGGS, false, KS>,               \
-             euclid_fb_select_kernel<DIRECT, false, KS>, euclid_fb_select_kernel<HIGGS, true, KS>},             \
+            {euclid_exact_scan_kernel<OMNI, false, KS>, euclid_exact_scan_kernel<HIGGS, false, KS>,             \
+             euclid_exact_scan_kernel<DIRECT, false, KS>, euclid_exact_scan_kernel<HIGGS, true, KS>},           \
             Tile<KS>::LDS,                                                                                      \
             Tile<KS>::CC};                                                                                      \
         return &t;                                                                                              \

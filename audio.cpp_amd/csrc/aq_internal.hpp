@@ -18,8 +18,8 @@ struct aq_ctx {
     int32_t *d_flags = nullptr;   // device status words written by kernels (vector stores only)
     int num_cus = 0;
     // Work buffers owned by the context, grown on demand (slot 0: residual
-    // cascade, 1: per-stage failure counters and lists, 2: exact-scan
-    // candidates, 3: refine-pass keys, 4: sweep keys and frame norms).
+    // cascade, 1: per-stage failure counters and lists, 3: refine-pass keys,
+    // 4: sweep keys and frame norms; 2 and 5 unused).
     static constexpr int kScratchSlots = 6;
     void *scratch[kScratchSlots] = {};
     size_t scratch_bytes[kScratchSlots] = {};
