@@ -331,7 +331,10 @@ aq_status aq_euclid_encode(aq_ctx *ctx, const aq_codebooks *cb, const float *x, 
     aq_device_guard g(ctx->device);
     const int K = static_cast<int>(cb->K);
     const int ks = K / 32;
-    const int topl = topk >= 4 ? 4 : 3;
+    // Keys per lane: 4 for top-4, and for large codebooks (N * K >= 2^22),
+    // where a frame the first certificate leaves open costs a split-bf16
+    // pass over N * K; 3 otherwise (one med3 less per score in the sweep).
+    const int topl = (topk >= 4 || cb->N * cb->K >= (int64_t{1} << 22)) ? 4 : 3;
     const KsKernels *kk = kernels_for(ks);
     const int var = variant_of(cb->recipe, cb->q8);
     StageFn sweep = kk->sweep[cb->q8 ? 1 : 0][topl - 3];
