@@ -270,11 +270,16 @@ __device__ float dot_q8(const int8_t *__restrict__ qc, const float *__restrict__
     for (int l = 0; l < 8; ++l) acc[l] = 0.0f;
     for (int ib = 0; ib < nb; ++ib) {
         const float dd = __fmul_rn(dc[ib], dx[ib]);
-        const int *pc = reinterpret_cast<const int *>(qc + 32 * ib);
+        // the code's 32 quants as two 16-byte loads (rows are 32-byte aligned)
+        const u32x4 *pc = reinterpret_cast<const u32x4 *>(qc + 32 * ib);
+        const u32x4 c0 = pc[0], c1 = pc[1];
+        const int cw[8] = {static_cast<int>(c0[0]), static_cast<int>(c0[1]), static_cast<int>(c0[2]),
+                           static_cast<int>(c0[3]), static_cast<int>(c1[0]), static_cast<int>(c1[1]),
+                           static_cast<int>(c1[2]), static_cast<int>(c1[3])};
         const int *px = reinterpret_cast<const int *>(qx + 32 * ib);
 #pragma unroll
         for (int l = 0; l < 8; ++l) {
-            const int s = __builtin_amdgcn_sdot4(pc[l], px[l], 0, false);
+            const int s = __builtin_amdgcn_sdot4(cw[l], px[l], 0, false);
             acc[l] = __fmaf_rn(dd, static_cast<float>(s), acc[l]);
         }
     }
@@ -365,10 +370,14 @@ __device__ float dot_q8_fused(const int8_t *__restrict__ qc, const float *__rest
             qw[l] = static_cast<int>(w);
         }
         const float dd = __fmul_rn(dc[ib], dx);
-        const int *pc = reinterpret_cast<const int *>(qc + 32 * ib);
+        const u32x4 *pc = reinterpret_cast<const u32x4 *>(qc + 32 * ib);
+        const u32x4 c0 = pc[0], c1 = pc[1];
+        const int cw[8] = {static_cast<int>(c0[0]), static_cast<int>(c0[1]), static_cast<int>(c0[2]),
+                           static_cast<int>(c0[3]), static_cast<int>(c1[0]), static_cast<int>(c1[1]),
+                           static_cast<int>(c1[2]), static_cast<int>(c1[3])};
 #pragma unroll
         for (int l = 0; l < 8; ++l) {
-            const int s = __builtin_amdgcn_sdot4(pc[l], qw[l], 0, false);
+            const int s = __builtin_amdgcn_sdot4(cw[l], qw[l], 0, false);
             acc[l] = __fmaf_rn(dd, static_cast<float>(s), acc[l]);
         }
     }
@@ -1221,6 +1230,8 @@ __global__ __launch_bounds__(kScanThreads) void euclid_exact_scan_kernel(StageAr
         int kept = 0;        // DIRECT: entries in the kept list
         for (int base = 0; base < a.N; base += kScanChunk) {
             const int len = min(kScanChunk, a.N - base);
+            // unrolled so that the row loads of several codes are in flight at once
+#pragma unroll 4
             for (int i = tid; i < len; i += kScanThreads) rv[i] = exact_value_kq<RECIPE, Q8, K>(a, xs, base + i, x2, xq, xd);
             __syncthreads();
             if (tid < kWave) {
@@ -1230,9 +1241,14 @@ __global__ __launch_bounds__(kScanThreads) void euclid_exact_scan_kernel(StageAr
                     const float v = in ? rv[i] : 0.0f;
                     if (RECIPE == DIRECT) {
                         // first index of the minimum: strict <, NaN never wins
-                        float cm = in ? v : INFINITY;
+                        // (a chunk with no code below the running minimum is
+                        // skipped after one ballot)
+                        float cm = INFINITY;
+                        if (__any(in && v < mx)) {
+                            cm = in ? v : INFINITY;
 #pragma unroll
-                        for (int off = 1; off < kWave; off <<= 1) cm = fminf(cm, __shfl_xor(cm, off));
+                            for (int off = 1; off < kWave; off <<= 1) cm = fminf(cm, __shfl_xor(cm, off));
+                        }
                         if (cm < mx) {
                             const unsigned long long eq = __ballot(in && v == cm);
                             const int first = __ffsll(static_cast<long long>(eq)) - 1;
@@ -1277,7 +1293,9 @@ __global__ __launch_bounds__(kScanThreads) void euclid_exact_scan_kernel(StageAr
                             mx = mx > vt ? mx : vt;
                             if (mx == vt) id = base + c0 + t;
                         }
-                    } else {
+                    } else if (__any(in && v >= mx)) {
+                        // only a chunk with a code >= the running max can
+                        // move the argmax (MAX keeps a later equal element)
                         float cm = in ? v : -INFINITY;
 #pragma unroll
                         for (int off = 1; off < kWave; off <<= 1) cm = fmaxf(cm, __shfl_xor(cm, off));
