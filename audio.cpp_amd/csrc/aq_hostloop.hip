@@ -74,6 +74,8 @@ __global__ __launch_bounds__(kWave *kHW) void outetts_encode_kernel(aq_outetts_a
         const float *W = a.w_in + (static_cast<int64_t>(s) * 8 + j) * D;
         const float *rf = r + f * stride;
         float v = a.b_in[s * 8 + j];
+        // unrolled: the weight loads of 8 steps are in flight ahead of the chain
+#pragma unroll 8
         for (int h = 0; h < D; h += 4) {
             const float4 w4 = *reinterpret_cast<const float4 *>(W + h);
             const float4 r4 = *reinterpret_cast<const float4 *>(rf + h);
@@ -98,6 +100,7 @@ __global__ __launch_bounds__(kWave *kHW) void outetts_encode_kernel(aq_outetts_a
         float bd = INFINITY;
         int bn = -1;
         const float *Ch = a.chat + static_cast<int64_t>(s) * a.N * 8;
+#pragma unroll 4
         for (int n = j; n < a.N; n += 8) {
             const float4 c0 = *reinterpret_cast<const float4 *>(Ch + static_cast<int64_t>(n) * 8);
             const float4 c1 = *reinterpret_cast<const float4 *>(Ch + static_cast<int64_t>(n) * 8 + 4);
@@ -142,6 +145,7 @@ __global__ __launch_bounds__(kWave *kHW) void outetts_encode_kernel(aq_outetts_a
             const float4 c0 = *reinterpret_cast<const float4 *>(c);
             const float4 c1 = *reinterpret_cast<const float4 *>(c + 4);
             float *rg = r + g * stride;
+#pragma unroll 4
             for (int o = lane; o < D; o += kWave) {
                 const float *wo = a.w_out + (static_cast<int64_t>(s) * D + o) * 8;
                 const float4 w0 = *reinterpret_cast<const float4 *>(wo);
@@ -251,6 +255,8 @@ __global__ __launch_bounds__(kWave *kHW) void moss_cascade_kernel(aq_moss_args a
         const float *W = a.w_in + (static_cast<int64_t>(s) * 8 + j) * R;
         const double *rf = r + f * stride;
         double v = a.b_in[s * 8 + j];
+        // unrolled: the weight loads of 8 steps are in flight ahead of the chain
+#pragma unroll 8
         for (int k = 0; k < R; k += 4) {
             const float4 w4 = *reinterpret_cast<const float4 *>(W + k);
             const double2 r01 = *reinterpret_cast<const double2 *>(rf + k);
@@ -276,6 +282,7 @@ __global__ __launch_bounds__(kWave *kHW) void moss_cascade_kernel(aq_moss_args a
         double bd = -INFINITY;
         int bn = -1;
         const float *T = a.tn + static_cast<int64_t>(s) * a.N * 8;
+#pragma unroll 4
         for (int n = j; n < a.N; n += 8) {
             const float4 t0 = *reinterpret_cast<const float4 *>(T + static_cast<int64_t>(n) * 8);
             const float4 t1 = *reinterpret_cast<const float4 *>(T + static_cast<int64_t>(n) * 8 + 4);
@@ -323,6 +330,7 @@ __global__ __launch_bounds__(kWave *kHW) void moss_cascade_kernel(aq_moss_args a
             const float4 c1 = *reinterpret_cast<const float4 *>(c + 4);
             const double cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
             double *rg = r + g * stride;
+#pragma unroll 4
             for (int o = lane; o < R; o += kWave) {
                 const float *wo = a.w_out + (static_cast<int64_t>(s) * R + o) * 8;
                 const float4 w0 = *reinterpret_cast<const float4 *>(wo);
