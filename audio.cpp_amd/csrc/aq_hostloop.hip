@@ -282,23 +282,30 @@ __global__ __launch_bounds__(kWave *kHW) void moss_cascade_kernel(aq_moss_args a
         double bd = -INFINITY;
         int bn = -1;
         const float *T = a.tn + static_cast<int64_t>(s) * a.N * 8;
-#pragma unroll 4
-        for (int n = j; n < a.N; n += 8) {
-            const float4 t0 = *reinterpret_cast<const float4 *>(T + static_cast<int64_t>(n) * 8);
-            const float4 t1 = *reinterpret_cast<const float4 *>(T + static_cast<int64_t>(n) * 8 + 4);
-            double dot = 0.0;
-            dot = dot + static_cast<double>(t0.x) * e[0];
-            dot = dot + static_cast<double>(t0.y) * e[1];
-            dot = dot + static_cast<double>(t0.z) * e[2];
-            dot = dot + static_cast<double>(t0.w) * e[3];
-            dot = dot + static_cast<double>(t1.x) * e[4];
-            dot = dot + static_cast<double>(t1.y) * e[5];
-            dot = dot + static_cast<double>(t1.z) * e[6];
-            dot = dot + static_cast<double>(t1.w) * e[7];
-            if (dot > bd) {
-                bd = dot;
-                bn = n;
+        // four codes per step, their dot chains interleaved (the compares stay
+        // in code order)
+        for (int n0 = j; n0 < a.N; n0 += 32) {
+            double dot[4];
+            float tv[4][8];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int n = n0 + 8 * q < a.N ? n0 + 8 * q : j;
+                const float4 t0 = *reinterpret_cast<const float4 *>(T + static_cast<int64_t>(n) * 8);
+                const float4 t1 = *reinterpret_cast<const float4 *>(T + static_cast<int64_t>(n) * 8 + 4);
+                tv[q][0] = t0.x; tv[q][1] = t0.y; tv[q][2] = t0.z; tv[q][3] = t0.w;
+                tv[q][4] = t1.x; tv[q][5] = t1.y; tv[q][6] = t1.z; tv[q][7] = t1.w;
+                dot[q] = 0.0;
             }
+#pragma unroll
+            for (int c = 0; c < 8; ++c)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) dot[q] = dot[q] + static_cast<double>(tv[q][c]) * e[c];
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                if (n0 + 8 * q < a.N && dot[q] > bd) {
+                    bd = dot[q];
+                    bn = n0 + 8 * q;
+                }
         }
 #pragma unroll
         for (int o = 1; o < 8; o <<= 1) {
