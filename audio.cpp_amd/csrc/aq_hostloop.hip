@@ -100,21 +100,33 @@ __global__ __launch_bounds__(kWave *kHW) void outetts_encode_kernel(aq_outetts_a
         float bd = INFINITY;
         int bn = -1;
         const float *Ch = a.chat + static_cast<int64_t>(s) * a.N * 8;
-#pragma unroll 4
-        for (int n = j; n < a.N; n += 8) {
-            const float4 c0 = *reinterpret_cast<const float4 *>(Ch + static_cast<int64_t>(n) * 8);
-            const float4 c1 = *reinterpret_cast<const float4 *>(Ch + static_cast<int64_t>(n) * 8 + 4);
-            const float cc[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-            float dist = 0.0f;
+        // four codes per step, their distance chains interleaved (the
+        // compares stay in code order)
+        for (int n0 = j; n0 < a.N; n0 += 32) {
+            float dist[4];
+            float cv[4][8];
 #pragma unroll
-            for (int d = 0; d < 8; ++d) {
-                const float diff = p[d] - cc[d];
-                dist = dist + diff * diff;
+            for (int q = 0; q < 4; ++q) {
+                const int n = n0 + 8 * q < a.N ? n0 + 8 * q : j;
+                const float4 c0 = *reinterpret_cast<const float4 *>(Ch + static_cast<int64_t>(n) * 8);
+                const float4 c1 = *reinterpret_cast<const float4 *>(Ch + static_cast<int64_t>(n) * 8 + 4);
+                cv[q][0] = c0.x; cv[q][1] = c0.y; cv[q][2] = c0.z; cv[q][3] = c0.w;
+                cv[q][4] = c1.x; cv[q][5] = c1.y; cv[q][6] = c1.z; cv[q][7] = c1.w;
+                dist[q] = 0.0f;
             }
-            if (dist < bd) {
-                bd = dist;
-                bn = n;
-            }
+#pragma unroll
+            for (int d = 0; d < 8; ++d)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float diff = p[d] - cv[q][d];
+                    dist[q] = dist[q] + diff * diff;
+                }
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                if (n0 + 8 * q < a.N && dist[q] < bd) {
+                    bd = dist[q];
+                    bn = n0 + 8 * q;
+                }
         }
 #pragma unroll
         for (int o = 1; o < 8; o <<= 1) {
