@@ -406,7 +406,8 @@ aq_status aq_euclid_encode(aq_ctx *ctx, const aq_codebooks *cb, const float *x, 
     for (int64_t s = 0; s < cb->Q; ++s) {
         StageArgs a{};
         a.xin = s == 0 ? x : work;
-        a.xout = work;
+        // the last stage's residual is only written when the caller asks for it
+        a.xout = (s + 1 < cb->Q || residual) ? work : nullptr;
         a.M = M;
         a.N = static_cast<int>(cb->N);
         a.cbh = cb->d_cbh + s * cb->N * K;

@@ -87,7 +87,7 @@ struct Tile {
 
 struct StageArgs {
     const float *xin;        // [M, K] residual entering the stage
-    float *xout;             // [M, K] residual leaving the stage (may alias xin)
+    float *xout;             // [M, K] residual leaving the stage (may alias xin; null: not needed)
     int64_t M;
     int N;
     const uint16_t *cbh;     // [N, K] bf16 codebook (scores)
@@ -1122,6 +1122,7 @@ __global__ __launch_bounds__(kThreads) void euclid_select_kernel(StageArgs a) {
                     use[t] = u2;
                 }
             }
+            if (!a.xout) continue;   // last stage, no residual asked for
 #pragma unroll
             for (int kv = 0; kv < KV; ++kv) {
                 const int k = (kv * kWave + lane) * 4;
@@ -1377,8 +1378,9 @@ __global__ __launch_bounds__(kScanThreads) void euclid_exact_scan_kernel(StageAr
                 use = 0;
             }
         }
-        for (int k = tid; k < K; k += kScanThreads)
-            a.xout[m * K + k] = __fsub_rn(a.xin[m * K + k], a.cbf[static_cast<int64_t>(use) * K + k]);
+        if (a.xout)
+            for (int k = tid; k < K; k += kScanThreads)
+                a.xout[m * K + k] = __fsub_rn(a.xin[m * K + k], a.cbf[static_cast<int64_t>(use) * K + k]);
     }
 }
 
@@ -1759,10 +1761,12 @@ __global__ __launch_bounds__(kWave) void euclid_refine_select_kernel(StageArgs a
                 use = 0;
             }
         }
+        if (a.xout) {
 #pragma unroll
-        for (int j = 0; j < KPL; ++j) {
-            const int k = lane + kWave * j;
-            a.xout[m * K + k] = __fsub_rn(xs[k], a.cbf[static_cast<int64_t>(use) * K + k]);
+            for (int j = 0; j < KPL; ++j) {
+                const int k = lane + kWave * j;
+                a.xout[m * K + k] = __fsub_rn(xs[k], a.cbf[static_cast<int64_t>(use) * K + k]);
+            }
         }
     }
 }
