@@ -73,19 +73,64 @@ __device__ inline float row_ror_add(float v) {
     const int o = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x120 + N, 0xF, 0xF, false);
     return __fadd_rn(v, __int_as_float(o));
 }
+// v from lane + N of its 16-lane row (DPP row_shl; lanes past the row end read 0).
 template <int N>
-__device__ inline float row_ror_max(float v) {
-    const int o = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x120 + N, 0xF, 0xF, false);
-    return fmaxf(v, __int_as_float(o));
+__device__ inline float row_shl(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x100 + N, 0xF, 0xF, false));
 }
-__device__ inline float wave_max(float v) {
-    v = row_ror_max<8>(v);
-    v = row_ror_max<4>(v);
-    v = row_ror_max<2>(v);
-    v = row_ror_max<1>(v);
-    v = fmaxf(v, __shfl_xor(v, 16));
-    v = fmaxf(v, __shfl_xor(v, 32));
+
+// +inf in a scalar register the compiler cannot see through.  With a literal
+// +inf, fmed3(x, y, +inf) is folded to maxnum, which in IEEE mode costs a
+// canonicalising v_max per operand; v_med3_f32 needs none.  The max of the
+// score keys never sees a NaN (a query or codebook row that is not finite
+// takes the exact path).
+__device__ inline float opaque_inf() {
+    float v;
+    asm volatile("s_mov_b32 %0, 0x7f800000" : "=s"(v));
     return v;
+}
+
+// A wave-uniform value copied to a vector register by an instruction the
+// compiler cannot rematerialise, so the copy is made once, outside the loop
+// that reads it, and bit selects against it stay single v_bfi_b32.
+__device__ inline int in_vgpr(int v) {
+    int r;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "s"(v));
+    return r;
+}
+
+// gfx950 permlane swaps: {a, b} -> {lo, hi} where lo holds, in each pair of
+// rows (16 lanes for permlane16, 32 for permlane32), the even row of a then
+// the even row of b, and hi the odd row of a then the odd row of b.  Lane L of
+// an even row therefore sees a(L) and a(L + row) and lane L of an odd row
+// b(L - row) and b(L): the cross-row half of a butterfly in one VALU op.
+__device__ inline void swap16(float a, float b, float &lo, float &hi) {
+    const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    lo = __uint_as_float(s[0]);
+    hi = __uint_as_float(s[1]);
+}
+__device__ inline void swap32(float a, float b, float &lo, float &hi) {
+    const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    lo = __uint_as_float(s[0]);
+    hi = __uint_as_float(s[1]);
+}
+
+template <int N>
+__device__ inline float row_ror_max(float v, float pinf) {
+    const int o = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x120 + N, 0xF, 0xF, false);
+    return __builtin_amdgcn_fmed3f(v, __int_as_float(o), pinf);
+}
+// Maximum over the wave, in every lane (NaN-free inputs).
+__device__ inline float wave_max(float v, float pinf) {
+    v = row_ror_max<8>(v, pinf);
+    v = row_ror_max<4>(v, pinf);
+    v = row_ror_max<2>(v, pinf);
+    v = row_ror_max<1>(v, pinf);
+    float lo, hi;
+    swap16(v, v, lo, hi);
+    v = __builtin_amdgcn_fmed3f(lo, hi, pinf);
+    swap32(v, v, lo, hi);
+    return __builtin_amdgcn_fmed3f(lo, hi, pinf);
 }
 
 // Per-stage image (units of float4), staged in LDS:
@@ -339,23 +384,25 @@ __global__ __launch_bounds__(kMaxBlock, 1) void dac_encode_kernel(
         // Reduction = GGML_F32x16_REDUCE (0+=2, 1+=3, 0+=1) then
         // _mm512_reduce_add_ps (distances 8, 4, 2, 1), transposed: after the
         // two cross-row levels lane L holds outputs 2*(L/16) and 2*(L/16)+1.
-        const bool hi32 = lane >= 32;
-        const bool hi16 = (lane & 16) != 0;
+        // Each level is one permlane swap: lanes 0-31 add acc[q] of lanes L
+        // and L + 32, lanes 32-63 acc[q + 4] of lanes L - 32 and L; then
+        // rows 0 and 2 add v[q] of lanes L and L + 16, rows 1 and 3 v[q + 2]
+        // of lanes L - 16 and L.
 #pragma unroll
         for (int f = 0; f < FW; ++f) {
             float v[4];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const float mine = hi32 ? acc[f][q + 4] : acc[f][q];
-                const float other = hi32 ? acc[f][q] : acc[f][q + 4];
-                v[q] = __fadd_rn(mine, __shfl_xor(other, 32));
+                float lo, hi;
+                swap32(acc[f][q], acc[f][q + 4], lo, hi);
+                v[q] = __fadd_rn(lo, hi);
             }
             float w[2];
 #pragma unroll
             for (int q = 0; q < 2; ++q) {
-                const float mine = hi16 ? v[q + 2] : v[q];
-                const float other = hi16 ? v[q] : v[q + 2];
-                w[q] = __fadd_rn(mine, __shfl_xor(other, 16));
+                float lo, hi;
+                swap16(v[q], v[q + 2], lo, hi);
+                w[q] = __fadd_rn(lo, hi);
             }
 #pragma unroll
             for (int q = 0; q < 2; ++q) {
@@ -368,35 +415,50 @@ __global__ __launch_bounds__(kMaxBlock, 1) void dac_encode_kernel(
             wred[f][1] = w[1];
         }
         }
+        // ---- query normalisation, every frame of the wave at once ----
+        // Output o of frame f moves to lane 8 f + o: in row g, lane 16 g + j
+        // (j < 2 FW) offers wred[j / 2][j % 2], i.e. output 2 g + j % 2 of
+        // frame j / 2.  Lanes 8 FW .. 63 carry don't-care values.
+        const int jrow = lane & 15;
+        float offer = wred[0][0];
+#pragma unroll
+        for (int f = 0; f < FW; ++f) {
+            if (jrow == 2 * f) offer = wred[f][0];
+            if (jrow == 2 * f + 1) offer = wred[f][1];
+        }
+        const int ol = lane & 7;
+        float p = __shfl(offer, 16 * (ol >> 1) + 2 * (lane >> 3) + (ol & 1));
+        if (has_bin) p = __fadd_rn(p, bin[ol]);
+        // l2_normalize_last: fp32 squares, double row sum in output order,
+        // + eps, sqrt, divide.  Lane 8 f sums ((sq_0 + sq_1) + sq_2) + ... of
+        // frame f, reading sq_k from lane 8 f + k (the leading 0.0 + sq_0 of
+        // the reference is sq_0 exactly: a square is +0 or more, or NaN).
+        const float sq = __fmul_rn(p, p);
+        double ss = static_cast<double>(sq);
+        ss += static_cast<double>(row_shl<1>(sq));
+        ss += static_cast<double>(row_shl<2>(sq));
+        ss += static_cast<double>(row_shl<3>(sq));
+        ss += static_cast<double>(row_shl<4>(sq));
+        ss += static_cast<double>(row_shl<5>(sq));
+        ss += static_cast<double>(row_shl<6>(sq));
+        ss += static_cast<double>(row_shl<7>(sq));
+        // ggml_scale_bias(sum, 1, eps): 1e-12 (Fish), 1e-20 (Vevo2), none
+        // (IndexTTS2: qeps = 0, and sum + 0 == sum for a sum >= +0)
+        const float den8 = sqrt_rn(__fadd_rn(static_cast<float>(ss), qeps));
+        const float qv = __fdiv_rn(p, __shfl(den8, lane & ~7));
+        const uint64_t good = __ballot((qv - qv) == 0.0f);
         float pn[FW][8];
         bool finite[FW];
 #pragma unroll
         for (int f = 0; f < FW; ++f) {
-            // Lane 16 g holds outputs 2 g (wred[f][0]) and 2 g + 1 (wred[f][1]).
-            const int o0 = 2 * (lane >> 4);
-            const float pa = has_bin ? __fadd_rn(wred[f][0], bin[o0]) : wred[f][0];
-            const float pb = has_bin ? __fadd_rn(wred[f][1], bin[o0 + 1]) : wred[f][1];
-            // l2_normalize_last: fp32 squares, double row sum in output order,
-            // + 1e-12, sqrt, divide.  The sum is wave-uniform (SGPR inputs);
-            // each lane then divides its own two outputs.
-            double ss = 0.0;
+            finite[f] = ((good >> (8 * f)) & 0xffull) == 0xffull;
 #pragma unroll
-            for (int o = 0; o < 8; ++o) {
-                const float po = __int_as_float(__builtin_amdgcn_readlane(__float_as_int((o & 1) ? pb : pa), 16 * (o >> 1)));
-                ss += static_cast<double>(__fmul_rn(po, po));
-            }
-            // ggml_scale_bias(sum, 1, eps): 1e-12 (Fish), 1e-20 (Vevo2), none
-            // (IndexTTS2: qeps = 0, and sum + 0 == sum for a sum >= +0)
-            const float den = sqrt_rn(__fadd_rn(static_cast<float>(ss), qeps));
-            const float qa = __fdiv_rn(pa, den);
-            const float qb = __fdiv_rn(pb, den);
-            finite[f] = __all(((qa - qa) == 0.0f) && ((qb - qb) == 0.0f));
-#pragma unroll
-            for (int o = 0; o < 8; ++o)
-                pn[f][o] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int((o & 1) ? qb : qa), 16 * (o >> 1)));
+            for (int o = 0; o < 8; ++o) pn[f][o] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(qv), 8 * f + o));
         }
 
         // ---- approximate scores, two best keys per lane ----
+        const float pinf = opaque_inf();
+        const int vmask = in_vgpr(key_mask);
         float k1[FW], k2[FW];
 #pragma unroll
         for (int f = 0; f < FW; ++f) {
@@ -417,18 +479,18 @@ __global__ __launch_bounds__(kMaxBlock, 1) void dac_encode_kernel(
                 sc = __fmaf_rn(b.y, pn[f][5], sc);
                 sc = __fmaf_rn(b.z, pn[f][6], sc);
                 sc = __fmaf_rn(b.w, pn[f][7], sc);
-                const float key = __int_as_float((__float_as_int(sc) & ~key_mask) | (c & key_mask));
+                const float key = __int_as_float((__float_as_int(sc) & ~vmask) | (c & vmask));
                 k2[f] = __builtin_amdgcn_fmed3f(k1[f], k2[f], key);
-                k1[f] = __builtin_amdgcn_fmed3f(k1[f], key, INFINITY);
+                k1[f] = __builtin_amdgcn_fmed3f(k1[f], key, pinf);
             }
         }
         int code[FW];
 #pragma unroll
         for (int f = 0; f < FW; ++f) {
-            const float best = wave_max(k1[f]);
+            const float best = wave_max(k1[f], pinf);
             const bool mine = k1[f] == best;
             const uint64_t owners = __ballot(mine);
-            const float second = wave_max(mine ? k2[f] : k1[f]);
+            const float second = wave_max(mine ? k2[f] : k1[f], pinf);
             const bool pass = finite[f] && !exact_only && __popcll(owners) == 1 && (best - second) > margin;
             if (pass) {
                 const int owner = __ffsll(static_cast<unsigned long long>(owners)) - 1;
@@ -439,25 +501,37 @@ __global__ __launch_bounds__(kMaxBlock, 1) void dac_encode_kernel(
         }
 
         // ---- out-projection by table gather, residual update ----
+        int use[FW];
 #pragma unroll
         for (int f = 0; f < FW; ++f) {
             if (lane == 0 && active[f]) idx[mrow[f] * Q + s] = code[f];
-            int use = code[f];
+            use[f] = code[f];
             if (force_idx) {
-                use = force_idx[mrow[f] * Q + s];
-                if (use < 0 || use >= N) {
+                use[f] = force_idx[mrow[f] * Q + s];
+                if (use[f] < 0 || use[f] >= N) {
                     if (lane == 0) flags[AQ_FLAG_BAD_INDEX] = 1;
-                    use = 0;
+                    use[f] = 0;
                 }
             }
-            if (!tables) continue;   // codes only: no out-projection was uploaded
-            const float *zrow = tables + (static_cast<int64_t>(s) * N + use) * D;
+        }
+        if (tables) {   // (codes only: no out-projection was uploaded)
+            // Every row load of the wave's frames is issued before the first
+            // use, so the gathers overlap instead of waiting one by one.
+            float z[FW][DI];
 #pragma unroll
-            for (int i = 0; i < DI; ++i) {
-                const float z = zrow[i * kWave + lane];
-                r[f][i] = __fsub_rn(r[f][i], z);
-                if (RECON) rc[f][i] = __fadd_rn(rc[f][i], z);
+            for (int f = 0; f < FW; ++f) {
+                const float *zrow = tables + (static_cast<int64_t>(s) * N + use[f]) * D;
+#pragma unroll
+                for (int i = 0; i < DI; ++i) z[f][i] = zrow[i * kWave + lane];
             }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int f = 0; f < FW; ++f)
+#pragma unroll
+                for (int i = 0; i < DI; ++i) {
+                    r[f][i] = __fsub_rn(r[f][i], z[f][i]);
+                    if (RECON) rc[f][i] = __fadd_rn(rc[f][i], z[f][i]);
+                }
         }
     }
 
