@@ -711,6 +711,15 @@ struct aq_dac_stages {
     // OuteTTS host-loop recipe: raw weights, one allocation
     float *d_ot = nullptr;
     aq_outetts_args ot{};         // the weight pointers into d_ot
+    // Launch-shape cache: the shape depends on M, recon and the summation
+    // order only, and finding it queries the attributes of up to nine kernel
+    // variants.  Calls that overlap on one stages object from several host
+    // threads race on it (as they would on the context's stream).
+    mutable int64_t shape_m = -1;
+    mutable int shape_key = -1;
+    mutable Shape shape{};
+    mutable const void *lds_fn = nullptr;   // the kernel whose dynamic-LDS limit was last raised
+    mutable size_t lds_limit = 0;
 };
 
 namespace {
@@ -986,13 +995,23 @@ aq_status aq_dac_encode(aq_ctx *ctx, const aq_dac_stages *st, const float *x, in
         return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_dac_encode: no out-projection was uploaded (codes only)");
     aq_device_guard g(ctx->device);
     const size_t img_bytes = static_cast<size_t>(st->lds_f4) * sizeof(float4);
-    const Shape shape = launch_shape(M, st->D, st->lds_f4, recon != nullptr, ctx->num_cus, img_bytes, st->cbg, order);
+    const int shape_key = (recon != nullptr ? 1 : 0) | (order << 1);
+    if (st->shape_m != M || st->shape_key != shape_key) {
+        st->shape = launch_shape(M, st->D, st->lds_f4, recon != nullptr, ctx->num_cus, img_bytes, st->cbg, order);
+        st->shape_m = M;
+        st->shape_key = shape_key;
+    }
+    const Shape shape = st->shape;
     const int fw = shape.fw;
     EncodeFn fn = pick_kernel(st->D, fw, recon != nullptr, shape.prefetch, st->cbg, order);
     const size_t lds_bytes =
         img_bytes + (order == 1 ? static_cast<size_t>(shape.waves_per_block) * static_cast<size_t>(st->D) * 4 : 0);
-    AQ_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void *>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    static_cast<int>(lds_bytes)));
+    if (st->lds_fn != reinterpret_cast<const void *>(fn) || st->lds_limit != lds_bytes) {
+        AQ_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void *>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        static_cast<int>(lds_bytes)));
+        st->lds_fn = reinterpret_cast<const void *>(fn);
+        st->lds_limit = lds_bytes;
+    }
     if (force_idx) AQ_HIP(ctx, hipMemsetAsync(ctx->d_flags, 0, sizeof(int32_t) * AQ_FLAG_COUNT, ctx->stream));
     const int64_t frames_per_block = static_cast<int64_t>(shape.waves_per_block) * fw;
     const unsigned blocks = static_cast<unsigned>((M + frames_per_block - 1) / frames_per_block);
