@@ -385,17 +385,22 @@ aq_status aq_euclid_encode(aq_ctx *ctx, const aq_codebooks *cb, const float *x, 
     int32_t *counts2 = fails + 64;
     int32_t *list = fails + 128;
     int32_t *list2 = list + M;
-    // Refine-pass keys: up to 64 MiB, frames beyond the capacity go straight
-    // to the exact scan.
     RefArgs rf{};
-    rf.nslices = static_cast<int>((cb->N + kRS - 1) / kRS);
+    // Refine-pass keys: the larger of the two slicings' needs (short slices
+    // for up to kRSmallFrames open frames, long slices for all M), at most
+    // 64 MiB; frames beyond the capacity go straight to the exact scan.
     {
-        const int64_t per_frame = static_cast<int64_t>(rf.nslices) * 4 * kTopR * 4;
-        rf.cap = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(M, (int64_t{64} << 20) / per_frame)));
+        const int64_t per_small =   // floats per frame
+            cb->N <= kRSmallCodes ? ((cb->N + kRSSmall - 1) / kRSSmall) * 4 * kTopR : ((cb->N + kRS - 1) / kRS) * 4 * kTopR;
+        const int64_t per_big = ((cb->N + kRS - 1) / kRS) * 4 * kTopR;
+        int64_t floats = std::max(std::min<int64_t>(M, kRSmallFrames) * per_small, M * per_big);
+        floats = std::min<int64_t>(floats, (int64_t{64} << 20) / 4);
+        floats = std::max(floats, per_small);
         void *w = nullptr;
-        aq_status st = aq_ctx_scratch(ctx, 3, static_cast<size_t>(rf.cap) * per_frame, &w);
+        aq_status st = aq_ctx_scratch(ctx, 3, static_cast<size_t>(floats) * 4, &w);
         if (st != AQ_OK) return st;
         rf.keys = static_cast<float *>(w);
+        rf.key_floats = floats;
     }
     rf.list2 = list2;
     RefineFn rvals = kk->refine_values[var];

@@ -67,7 +67,7 @@ typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 enum Recipe : int { OMNI = 0, HIGGS = 1, DIRECT = 2 };
 
-constexpr int kRS = 256;       // codes per refine slice (64 per lane: 6 index bits)
+constexpr int kRS = 256;       // most codes per refine slice (64 per lane: 6 index bits)
 constexpr int kTopR = 4;       // keys per lane and slice
 constexpr int kRCand = 256;    // exact candidates per frame in refine_select
 constexpr int kRWaves = 4;     // refine_values waves per block
@@ -117,13 +117,34 @@ struct StageArgs {
 
 struct RefArgs {
     const uint16_t *cbl;       // [N, K] bf16(c - bf16(c))
-    float *keys;               // [cap][nslices][4][kTopR]
-    int nslices;
-    int cap;                   // open frames the key buffer holds
+    float *keys;               // [cap][nslices][4][kTopR] (RefShape)
+    int64_t key_floats;        // capacity of the key buffer
     int32_t *count2;           // exact-scan counter of this stage
     int32_t *list2;            // exact-scan frame list
     float clmax, crmax;        // max |c_l|, max |c_r| over the stage's codes
 };
+
+// Slicing of the refine pass, chosen on the device from the number of open
+// frames (both refine kernels derive the same shape): a few hundred open
+// frames of a codebook of up to kRSmallCodes codes fill the GPU only with
+// short slices (kRSSmall codes, two 16-code blocks per work item); many open
+// frames, or larger codebooks, take long slices (kRS codes), which keep the
+// per-item set-up and the keys per frame low.  Frames past the key buffer's
+// capacity go to the exact scan.
+constexpr int kRSSmall = 32;
+constexpr int kRSmallFrames = 512;
+constexpr int kRSmallCodes = 4096;
+struct RefShape {
+    int rs, nslices, cap;
+};
+__device__ inline RefShape ref_shape(const RefArgs &rf, int N, int count) {
+    RefShape r;
+    r.rs = count <= kRSmallFrames && N <= kRSmallCodes ? kRSSmall : kRS;
+    r.nslices = (N + r.rs - 1) / r.rs;
+    const int64_t cap = rf.key_floats / (static_cast<int64_t>(r.nslices) * 4 * kTopR);
+    r.cap = static_cast<int>(cap < count ? cap : count);
+    return r;
+}
 
 using StageFn = void (*)(StageArgs);
 using RefineFn = void (*)(StageArgs, RefArgs);
@@ -1397,7 +1418,7 @@ __global__ __launch_bounds__(kScanThreads) void euclid_exact_scan_kernel(StageAr
 // |x||c|, against 2^-8 for plain bf16.  The same certificate as in the stage
 // kernel then settles nearly every open frame with a bound about 100 times
 // smaller; the rest go to the exact scan.
-//  * refine_values: a wave takes 16 open frames x one slice of kRS codes and
+//  * refine_values: a wave takes 16 open frames x one slice of rs codes and
 //    keeps, per lane, its kTopR best keys (score with the slice-local code
 //    index in the low 6 mantissa bits) in a key buffer.
 //  * refine_select: a wave per frame merges the key lists of all slices,
@@ -1428,9 +1449,10 @@ __global__ __launch_bounds__(kWave * kRWaves, KS <= 8 ? 2 : 1) void euclid_refin
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
     const int col = lane & 15, kq = lane >> 4;
-    const int count = min(*a.fail_count, rf.cap);
+    const RefShape rsh = ref_shape(rf, a.N, *a.fail_count);
+    const int count = rsh.cap;
     const int ntiles = (count + 16 * kRWaves - 1) / (16 * kRWaves);
-    const int64_t nwork = static_cast<int64_t>(ntiles) * rf.nslices;
+    const int64_t nwork = static_cast<int64_t>(ntiles) * rsh.nslices;
     unsigned vkeep;
     asm volatile("v_mov_b32 %0, %1" : "=v"(vkeep) : "s"(~63u));
 
@@ -1452,7 +1474,7 @@ __global__ __launch_bounds__(kWave * kRWaves, KS <= 8 ? 2 : 1) void euclid_refin
     };
 
     for (int64_t w = blockIdx.x; w < nwork; w += gridDim.x) {
-        const int tile = static_cast<int>(w / rf.nslices), sl = static_cast<int>(w % rf.nslices);
+        const int tile = static_cast<int>(w / rsh.nslices), sl = static_cast<int>(w % rsh.nslices);
         const int fs = (tile * kRWaves + wave) * 16 + col;
         const int64_t m = a.fail_list[fs < count ? fs : count - 1];
         const float *xr = a.xin + m * K;
@@ -1478,8 +1500,8 @@ __global__ __launch_bounds__(kWave * kRWaves, KS <= 8 ? 2 : 1) void euclid_refin
         float top[kTopR];
 #pragma unroll
         for (int j = 0; j < kTopR; ++j) top[j] = -INFINITY;
-        const int n0 = sl * kRS;
-        const int nb = min(kRS, a.N - n0) / 16;
+        const int n0 = sl * rsh.rs;
+        const int nb = min(rsh.rs, a.N - n0) / 16;
 
         // stage block 0 of the slice
         __syncthreads();   // the previous work item's last reads of buffer 0/1
@@ -1533,7 +1555,7 @@ __global__ __launch_bounds__(kWave * kRWaves, KS <= 8 ? 2 : 1) void euclid_refin
             __syncthreads();
         }
         if (fs < count) {
-            f32x4 *dst = reinterpret_cast<f32x4 *>(rf.keys + ((static_cast<int64_t>(fs) * rf.nslices + sl) * 4 + kq) * kTopR);
+            f32x4 *dst = reinterpret_cast<f32x4 *>(rf.keys + ((static_cast<int64_t>(fs) * rsh.nslices + sl) * 4 + kq) * kTopR);
             *dst = f32x4{top[0], top[1], top[2], top[3]};
         }
     }
@@ -1543,6 +1565,73 @@ __device__ inline float wave_sum(float v) {
 #pragma unroll
     for (int off = 1; off < kWave; off <<= 1) v += __shfl_xor(v, off);
     return v;
+}
+
+// Exact values of one frame's candidates cn[0 .. ncand), in exact_value_kq's
+// arithmetic, with several candidates per pass and coalesced row reads:
+//  * tinyBLAS order: 16 lanes per candidate, lane j accumulating the
+//    elements k = 16 l + j, then _mm512_reduce_add_ps's pairing tree as DPP
+//    row rotations 8, 4, 2, 1; two candidates per 16-lane row and pass, so
+//    that their row reads are in flight together;
+//  * Q8_0 (ggml_vec_dot_q8_0_q8_0): 8 lanes per candidate, lane j taking the
+//    j-th 4-element group of every block, then hsum_float_8 as lane
+//    exchanges 4, 2, 1;
+//  * otherwise one candidate per lane.
+// x, xq, xd may live in LDS; every lane of the wave calls this.
+template <int RECIPE, bool Q8, int K>
+__device__ void exact_values_frame(const StageArgs &a, const float *__restrict__ x, float x2, const int8_t *xq,
+                                   const float *xd, const int *cn, float *cv, int ncand, int lane) {
+    if (!Q8 && RECIPE != DIRECT && a.order == 0) {
+        constexpr int P = 2;
+        const int j = lane & 15, grp = lane >> 4;
+        const float sa = RECIPE == OMNI ? 2.0f : 1.0f;
+        for (int c0 = grp; c0 < ncand; c0 += 4 * P) {
+            int n[P];
+            float acc[P];
+#pragma unroll
+            for (int p = 0; p < P; ++p) {
+                const int c = c0 + 4 * p;
+                n[p] = cn[c < ncand ? c : c0];
+                acc[p] = 0.0f;
+            }
+#pragma unroll
+            for (int l = 0; l < K / 16; ++l)
+#pragma unroll
+                for (int p = 0; p < P; ++p)
+                    acc[p] = __fmaf_rn(a.cbf[static_cast<int64_t>(n[p]) * K + 16 * l + j] * sa, x[16 * l + j], acc[p]);
+#pragma unroll
+            for (int p = 0; p < P; ++p) {
+                float v = row_ror_add<8>(acc[p]);
+                v = row_ror_add<4>(v);
+                v = row_ror_add<2>(v);
+                v = row_ror_add<1>(v);
+                const int c = c0 + 4 * p;
+                if (j == 0 && c < ncand)
+                    cv[c] = RECIPE == OMNI ? __fadd_rn(v, a.bias[n[p]])
+                                           : __fsub_rn(__fsub_rn(__fmul_rn(v, 2.0f), x2), a.e2[n[p]]);
+            }
+        }
+    } else if (Q8) {
+        const int j = lane & 7, grp = lane >> 3;
+        const int *xqi = reinterpret_cast<const int *>(xq) + j;
+        for (int c = grp; c < ncand; c += 8) {
+            const int n = cn[c];
+            const int *cq = reinterpret_cast<const int *>(a.q8 + static_cast<int64_t>(n) * K) + j;
+            const float *cd = a.q8d + static_cast<int64_t>(n) * (K / 32);
+            float acc = 0.0f;
+#pragma unroll
+            for (int ib = 0; ib < K / 32; ++ib) {
+                const float dd = __fmul_rn(cd[ib], xd[ib]);
+                acc = __fmaf_rn(dd, static_cast<float>(__builtin_amdgcn_sdot4(cq[8 * ib], xqi[8 * ib], 0, false)), acc);
+            }
+            acc = __fadd_rn(acc, __shfl_xor(acc, 4));
+            acc = __fadd_rn(acc, __shfl_xor(acc, 2));
+            acc = __fadd_rn(acc, __shfl_xor(acc, 1));
+            if (j == 0) cv[c] = __fsub_rn(__fsub_rn(__fmul_rn(acc, 2.0f), x2), a.e2[n]);
+        }
+    } else {
+        for (int c = lane; c < ncand; c += kWave) cv[c] = exact_value_kq<RECIPE, Q8, K>(a, x, cn[c], x2, xq, xd);
+    }
 }
 
 template <int RECIPE, bool Q8, int KS>
@@ -1560,11 +1649,12 @@ __global__ __launch_bounds__(kWave) void euclid_refine_select_kernel(StageArgs a
     const int Tk = a.topk > 0 ? a.topk : 1;
     const int Tsel = a.topk > 0 ? a.topk + 1 : 1;
     const int count = *a.fail_count;
-    const int nk = rf.nslices * 4 * kTopR;
+    const RefShape rsh = ref_shape(rf, a.N, count);
+    const int nk = rsh.nslices * 4 * kTopR;
     for (int slot = blockIdx.x; slot < count; slot += gridDim.x) {
         const int64_t m = a.fail_list[slot];
         const float *xr = a.xin + m * K;
-        bool ok = slot < rf.cap && !a.exact_only;
+        bool ok = slot < rsh.cap && !a.exact_only;
 
         // Norms of the split of x (of its Q8_0 image for a Q8_0 codebook).
         // Element k = lane + 64 j; a 32-wide Q8_0 block is 32 adjacent lanes.
@@ -1655,7 +1745,7 @@ __global__ __launch_bounds__(kWave) void euclid_refine_select_kernel(StageArgs a
                 if (c && pos < kRCand) {
                     const int slc = e / (4 * kTopR), q = (e / kTopR) % 4;
                     const unsigned local = __float_as_uint(kv) & 63u;
-                    cand_n[pos] = slc * kRS + static_cast<int>(local >> 2) * 16 + q * 4 + static_cast<int>(local & 3);
+                    cand_n[pos] = slc * rsh.rs + static_cast<int>(local >> 2) * 16 + q * 4 + static_cast<int>(local & 3);
                 }
                 ncand += __popcll(bal);
             }
@@ -1668,8 +1758,7 @@ __global__ __launch_bounds__(kWave) void euclid_refine_select_kernel(StageArgs a
         }
         __syncthreads();
         const float x2c = RECIPE == HIGGS ? x2s : 0.0f;
-        if (ok)
-            for (int c = lane; c < ncand; c += kWave) cand_v[c] = exact_value_kq<RECIPE, Q8, K>(a, xs, cand_n[c], x2c, xq, xd);
+        if (ok) exact_values_frame<RECIPE, Q8, K>(a, xs, x2c, xq, xd, cand_n, cand_v, ncand, lane);
         __syncthreads();
 
         // Ranked selection of the evaluated candidates (every lane computes
