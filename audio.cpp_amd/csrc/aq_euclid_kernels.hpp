@@ -70,6 +70,7 @@ enum Recipe : int { OMNI = 0, HIGGS = 1, DIRECT = 2 };
 constexpr int kRS = 256;       // most codes per refine slice (64 per lane: 6 index bits)
 constexpr int kTopR = 4;       // keys per lane and slice
 constexpr int kRCand = 256;    // exact candidates per frame in refine_select
+constexpr int kRKeyLds = 1024; // keys per frame refine_select stages in LDS
 constexpr int kRWaves = 4;     // refine_values waves per block
 
 template <int KS>
@@ -1640,6 +1641,7 @@ __global__ __launch_bounds__(kWave) void euclid_refine_select_kernel(StageArgs a
     constexpr int KPL = K / kWave;   // frame elements per lane
     __shared__ int cand_n[kRCand];
     __shared__ float cand_v[kRCand];
+    __shared__ float keys_s[kRKeyLds];     // the frame's keys of every slice
     __shared__ float xs[K];                // the frame (exact evaluation reads it here)
     __shared__ int8_t xq[Q8 ? K : 4];      // its Q8_0 blocks
     __shared__ float xd[Q8 ? K / 32 : 1];
@@ -1697,6 +1699,25 @@ __global__ __launch_bounds__(kWave) void euclid_refine_select_kernel(StageArgs a
         // Keys of every slice: tau bounds every code a lane dropped; vT is
         // the T-th largest key (ties by position).
         const float *kp = rf.keys + static_cast<int64_t>(slot) * nk;
+        // The frame's keys are read three times below: from LDS when they fit.
+        if (nk <= kRKeyLds) {
+            __syncthreads();   // the previous frame's reads of keys_s
+            for (int e0 = 0; e0 < nk; e0 += 16 * kWave) {   // 16 loads in flight per lane
+                float t[16];
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    const int e = e0 + j * kWave + lane;
+                    t[j] = e < nk ? kp[e] : 0.0f;
+                }
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    const int e = e0 + j * kWave + lane;
+                    if (e < nk) keys_s[e] = t[j];
+                }
+            }
+            __syncthreads();
+            kp = keys_s;
+        }
         float tau = -INFINITY;
         float vT = -INFINITY;
         int ncand = 0;
