@@ -1242,7 +1242,7 @@ __global__ __launch_bounds__(kScanThreads) void euclid_exact_scan_kernel(StageAr
         __syncthreads();
         for (int k = tid; k < K; k += kScanThreads) xs[k] = a.xin[m * K + k];
         __syncthreads();
-        if (tid == 0) o_x2 = RECIPE == HIGGS ? sum_squares(xs, K) : 0.0f;
+        if (tid == 0) o_x2 = RECIPE == HIGGS ? sum_squares_k<K>(xs) : 0.0f;   // unrolled: LDS reads in flight
         if (Q8 && tid < K / 32) quantize_block_q8(xs + 32 * tid, xq + 32 * tid, xd + tid);
         __syncthreads();
         const float x2 = o_x2;
