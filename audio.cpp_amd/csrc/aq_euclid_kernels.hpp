@@ -248,14 +248,6 @@ __device__ float dot_vecdot(const float *__restrict__ a, const float *__restrict
     return sum;
 }
 
-// ggml_vec_sum_f32 of the fp32 squares (sum_rows(mul(x, x))): double
-// accumulation in order, one rounding to float.
-__device__ float sum_squares(const float *__restrict__ x, int K) {
-    double s = 0.0;
-    for (int k = 0; k < K; ++k) s += static_cast<double>(__fmul_rn(x[k], x[k]));
-    return static_cast<float>(s);
-}
-
 // Direct squared distance: rounded (x - c)^2 added in order.
 __device__ float dist_direct(const float *__restrict__ x, const float *__restrict__ c, int K) {
     float d = 0.0f;
@@ -329,6 +321,8 @@ __device__ float dot_tinyblas_k(const float *__restrict__ a, const float *__rest
     return reduce16(acc);
 }
 
+// ggml_vec_sum_f32 of the fp32 squares (sum_rows(mul(x, x))): double
+// accumulation in order, one rounding to float.
 template <int K>
 __device__ float sum_squares_k(const float *__restrict__ x) {
     double s = 0.0;
