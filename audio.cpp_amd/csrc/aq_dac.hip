@@ -231,7 +231,7 @@ __global__ __launch_bounds__(kMaxBlock, 1) void dac_encode_kernel(
     const float *__restrict__ x, int64_t M, int Q, int N, const float4 *__restrict__ images, int64_t stride_f4,
     int64_t img_f4, const float *__restrict__ tables, int32_t *__restrict__ idx, float *__restrict__ residual,
     float *__restrict__ recon, const int32_t *__restrict__ force_idx, int32_t *__restrict__ flags, int has_bin,
-    int key_bits, float margin, int exact_only, float qeps) {
+    int key_bits, float margin, int exact_only, float qeps, int64_t dbuf_f4) {
     // stride_f4: float4 per stage image; img_f4: the prefix staged in LDS
     // (the whole image, or W_in + b_in when CBG reads c_hat from memory).
     extern __shared__ float4 lds[];
@@ -256,18 +256,21 @@ __global__ __launch_bounds__(kMaxBlock, 1) void dac_encode_kernel(
         }
     }
 
-    const float4 *win = lds;
-    const float *bin = reinterpret_cast<const float *>(lds + 2 * DI * kWave);
     const int NC = N / kWave;
     const int key_mask = (1 << key_bits) - 1;
 
     f32x4 pre[PF > 0 ? PF : 1];
     if (PF > 0) fetch_image<PF>(pre, images, img_f4);
-    f32x4 *lds4 = reinterpret_cast<f32x4 *>(lds);
 
     for (int s = 0; s < Q; ++s) {
-        __syncthreads();
+        // dbuf_f4 > 0: two LDS images, stage s in the one at (s & 1) * dbuf_f4.
+        // The image written here was last read two stages ago, and every wave
+        // has finished that stage once it passed the previous stage's barrier,
+        // so one barrier per stage suffices.
+        float4 *img_lds = lds + ((s & 1) ? dbuf_f4 : 0);
+        if (dbuf_f4 == 0) __syncthreads();
         if (PF > 0) {
+            f32x4 *lds4 = reinterpret_cast<f32x4 *>(img_lds);
 #pragma unroll
             for (int k = 0; k < PF; ++k) {
                 const int64_t t = threadIdx.x + static_cast<int64_t>(k) * blockDim.x;
@@ -285,14 +288,16 @@ __global__ __launch_bounds__(kMaxBlock, 1) void dac_encode_kernel(
 #pragma unroll
                 for (int k = 0; k < kCopyBatch; ++k) {
                     const int64_t t = t0 + threadIdx.x + static_cast<int64_t>(k) * blockDim.x;
-                    if (t < img_f4) lds[t] = buf[k];
+                    if (t < img_f4) img_lds[t] = buf[k];
                 }
             }
         }
         __syncthreads();
         if (PF > 0 && s + 1 < Q) fetch_image<PF>(pre, images + static_cast<int64_t>(s + 1) * stride_f4, img_f4);
+        const float4 *win = img_lds;
+        const float *bin = reinterpret_cast<const float *>(img_lds + 2 * DI * kWave);
         const float4 *chat = CBG ? images + static_cast<int64_t>(s) * stride_f4 + 2 * DI * kWave + 2
-                                 : lds + 2 * DI * kWave + 2;
+                                 : img_lds + 2 * DI * kWave + 2;
 
         float wred[FW][2];   // lane 16 g holds outputs 2 g and 2 g + 1 of each frame
         if (ORDER == 1) {
@@ -301,7 +306,7 @@ __global__ __launch_bounds__(kMaxBlock, 1) void dac_encode_kernel(
             // Lane L = 16 g + t runs accumulator t of outputs 2g and 2g+1 over
             // the frame's elements k = 16 u + t, read from a transposed copy
             // of the residual in LDS (the cascade keeps k = L + 64 i per lane).
-            float *rt = reinterpret_cast<float *>(lds + img_f4) + wave * D;
+            float *rt = reinterpret_cast<float *>(lds + img_f4 + dbuf_f4) + wave * D;
             const int t = lane & 15, g = lane >> 4;
             const float4 *w0 = win + (2 * g * 16 + t) * DI;
             const float4 *w1 = win + ((2 * g + 1) * 16 + t) * DI;
@@ -584,7 +589,7 @@ __global__ void dac_decode_kernel(const int32_t *__restrict__ idx, int64_t M, in
 }
 
 using EncodeFn = void (*)(const float *, int64_t, int, int, const float4 *, int64_t, int64_t, const float *, int32_t *,
-                          float *, float *, const int32_t *, int32_t *, int, int, float, int, float);
+                          float *, float *, const int32_t *, int32_t *, int, int, float, int, float, int64_t);
 
 constexpr int kPrefetch = 12;   // float4 per thread in the prefetching variant
 
@@ -1004,8 +1009,10 @@ aq_status aq_dac_encode(aq_ctx *ctx, const aq_dac_stages *st, const float *x, in
     const Shape shape = st->shape;
     const int fw = shape.fw;
     EncodeFn fn = pick_kernel(st->D, fw, recon != nullptr, shape.prefetch, st->cbg, order);
-    const size_t lds_bytes =
-        img_bytes + (order == 1 ? static_cast<size_t>(shape.waves_per_block) * static_cast<size_t>(st->D) * 4 : 0);
+    const size_t rt_bytes = order == 1 ? static_cast<size_t>(shape.waves_per_block) * static_cast<size_t>(st->D) * 4 : 0;
+    // A second stage image in LDS when it fits: one barrier per stage.
+    const int64_t dbuf_f4 = 2 * img_bytes + rt_bytes <= static_cast<size_t>(160 * 1024) ? st->lds_f4 : 0;
+    const size_t lds_bytes = img_bytes * (dbuf_f4 > 0 ? 2 : 1) + rt_bytes;
     if (st->lds_fn != reinterpret_cast<const void *>(fn) || st->lds_limit != lds_bytes) {
         AQ_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void *>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
                                         static_cast<int>(lds_bytes)));
@@ -1020,7 +1027,7 @@ aq_status aq_dac_encode(aq_ctx *ctx, const aq_dac_stages *st, const float *x, in
                        static_cast<int>(st->N), order == 1 ? st->d_images_tb : st->d_images, st->img_f4, st->lds_f4,
                        st->d_tables, idx, residual, recon,
                        force_idx, ctx->d_flags, st->has_bin ? 1 : 0, st->key_bits, st->margin, st->exact_only ? 1 : 0,
-                       st->qeps);
+                       st->qeps, dbuf_f4);
     aq_timing_stop(ctx, tslot);
     AQ_HIP(ctx, hipGetLastError());
     if (force_idx) {
