@@ -1692,9 +1692,13 @@ __global__ __launch_bounds__(kWave) void euclid_refine_select_kernel(StageArgs a
 
         // Keys of every slice: tau bounds every code a lane dropped; vT is
         // the T-th largest key (ties by position).
+        // Keys exist only for slots below the capacity (refine_values wrote
+        // them); a frame past it, or with E = inf, reads none and goes to the
+        // exact scan.  `ok` is uniform over the block (one wave; E comes from
+        // butterfly sums), so the barriers below are reached by every lane.
         const float *kp = rf.keys + static_cast<int64_t>(slot) * nk;
         // The frame's keys are read three times below: from LDS when they fit.
-        if (nk <= kRKeyLds) {
+        if (ok && nk <= kRKeyLds) {
             __syncthreads();   // the previous frame's reads of keys_s
             for (int e0 = 0; e0 < nk; e0 += 16 * kWave) {   // 16 loads in flight per lane
                 float t[16];
