@@ -220,6 +220,56 @@ def make_config(i: int, rows: int | None = None) -> dict:
     raise ValueError(f"unknown config {i}")
 
 
+def q8_0_quantize_ref(rows: np.ndarray) -> np.ndarray:
+    """block_q8_0 image of float rows [..., K] with the weight-side rounding
+    (quantize_row_q8_0_ref, ggml-quants.c:236-256: d = amax / 127 in fp32,
+    id = 1 / d, q = roundf(x * id), d stored as fp16)."""
+    x = np.ascontiguousarray(rows, np.float32)
+    b = x.reshape(x.shape[:-1] + (x.shape[-1] // Q8_BLOCK, Q8_BLOCK))
+    amax = np.abs(b).max(-1)
+    d = (amax / np.float32(127.0)).astype(np.float32)
+    with np.errstate(divide="ignore"):
+        idv = np.where(d != 0, np.float32(1.0) / np.where(d != 0, d, np.float32(1.0)), np.float32(0.0)).astype(np.float32)
+    v = (b * idv[..., None]).astype(np.float32).astype(np.float64)
+    q = np.sign(v) * np.floor(np.abs(v) + 0.5)          # roundf: half away from zero
+    out = np.zeros(b.shape[:-1], dtype=Q8_DTYPE)
+    out["d"] = d.astype(np.float16)
+    out["qs"] = q.astype(np.int8)
+    return out
+
+
+# --------------------------------------------------------------------------
+# Projected Euclidean RVQ (OmniVoice / Higgs acoustic quantizers; test shapes)
+
+def projected_config(M: int, recipe: int = 1, seed: int = 13, H: int = 1024, K: int = 64, N: int = 1024, Q: int = 8,
+                     cb_q8: bool = False, proj_q8: bool = False) -> dict:
+    """Inputs of the OmniVoice (recipe 0) / Higgs (recipe 1) quantizer with
+    projections, at the reference's shapes (hidden 1024, codebook dim 64,
+    1024 codes, 8 stages; higgs_audio_tts/codec.cpp:34-37): x [M, H] ~N(0,1),
+    project_in W [Q, K, H] ~N(0, 1/sqrt(H)) with bias ~N(0, 0.1), codebooks
+    [Q, N, K] ~N(0, 1), project_out W [Q, H, K] ~N(0, 1/sqrt(K)) with bias
+    ~N(0, 0.1).  cb_q8 / proj_q8 store the codebook / the projection weights
+    as GGUF Q8_0 (weight-side rounding), as a Q8_0 codec weight type does."""
+    x = normal(seed, 1, (M, H))
+    w_in = np.stack([normal(seed, 100 * s + 2, (K, H), 1.0 / np.sqrt(H)) for s in range(Q)])
+    b_in = np.stack([normal(seed, 100 * s + 3, (K,), 0.1) for s in range(Q)])
+    cb = np.stack([normal(seed, 100 * s + 4, (N, K), 1.0) for s in range(Q)])
+    w_out = np.stack([normal(seed, 100 * s + 5, (H, K), 1.0 / np.sqrt(K)) for s in range(Q)])
+    b_out = np.stack([normal(seed, 100 * s + 6, (H,), 0.1) for s in range(Q)])
+    cfg = dict(kind="projected", seed=seed, recipe=recipe, M=M, H=H, K=K, Q=Q, N=N, x=x, b_in=b_in, b_out=b_out)
+    if cb_q8:
+        cfg["codebook_q8"] = q8_0_quantize_ref(cb)
+    else:
+        cfg["codebook"] = cb
+    if proj_q8:
+        cfg["w_in_q8"] = q8_0_quantize_ref(w_in)
+        cfg["w_out_q8"] = q8_0_quantize_ref(w_out)
+    else:
+        cfg["w_in"] = w_in
+        cfg["w_out"] = w_out
+    return cfg
+
+
 # --------------------------------------------------------------------------
 # Host-loop DAC quantizers (test shapes; not BASELINE configs)
 

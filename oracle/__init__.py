@@ -106,6 +106,11 @@ class Oracle:
         L.aqo_moss_normalize_rows.argtypes = [_f32p, _i64, _i64, _f32p]
         L.aqo_moss_rvq.argtypes = [_f32p, _i64, _i64, _i64, _i64, _i64, _f32p, _f32p, _f32p, _f32p, _f32p,
                                    _f32p, _f32p, C.c_void_p, _i32p, C.c_void_p]
+        L.aqo_projected_rvq.argtypes = [_f32p, _i64, _i64, _i64, _i64, _i64, C.c_int, C.c_void_p, C.c_int,
+                                        C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int,
+                                        C.c_void_p, _i32p, _f32p, C.c_void_p, C.c_void_p, C.c_void_p]
+        L.aqo_projected_decode.argtypes = [_i32p, _i64, _i64, _i64, _i64, _i64, C.c_void_p, C.c_int, C.c_void_p,
+                                           C.c_void_p, C.c_int, _f32p]
         L.aqo_moss_decode.argtypes = [_i32p, _i64, _i64, _i64, _i64, _i64, _f32p, _f32p, _f32p, _f32p, _f32p,
                                       _f32p]
 
@@ -273,6 +278,57 @@ class Oracle:
         return out
 
 
+    def projected_rvq(self, cfg: dict, force_idx=None, topk: int = 0):
+        """OmniVoice / Higgs RVQ with per-stage projections (aqo_projected_rvq)."""
+        x = np.ascontiguousarray(cfg["x"], np.float32)
+        M, H = x.shape
+        Q, N, K = cfg["Q"], cfg["N"], cfg["K"]
+        cb, cbt = _cb_arg(cfg)
+        wi, wo, pt = _proj_args(cfg)
+        idx = np.zeros((M, Q), np.int32)
+        res = np.zeros((M, H), np.float32)
+        dist = np.zeros((M, Q), np.float32)
+        tki = np.zeros((M, Q, max(topk, 1)), np.int32)
+        tkl = np.zeros((M, Q, max(topk, 1)), np.float32)
+        fi = np.ascontiguousarray(force_idx, np.int32) if force_idx is not None else None
+        rc = self.lib.aqo_projected_rvq(
+            x, M, H, K, Q, N, cfg["recipe"], cb.ctypes.data_as(C.c_void_p), cbt, wi.ctypes.data_as(C.c_void_p),
+            _opt(cfg.get("b_in"), np.float32), wo.ctypes.data_as(C.c_void_p), _opt(cfg.get("b_out"), np.float32), pt,
+            topk, None if fi is None else fi.ctypes.data_as(C.c_void_p), idx, res, dist.ctypes.data_as(C.c_void_p),
+            tki.ctypes.data_as(C.c_void_p), tkl.ctypes.data_as(C.c_void_p))
+        assert rc == 0
+        out = dict(idx=idx, residual=res, dist=dist)
+        if topk:
+            out["topk_idx"] = tki
+            out["topk_logit"] = tkl
+        return out
+
+    def projected_decode(self, cfg: dict, idx):
+        """Sum over stages of project_out(c[idx]) (aqo_projected_decode)."""
+        idx = np.ascontiguousarray(idx, np.int32)
+        M = idx.shape[0]
+        Q, N, K, H = cfg["Q"], cfg["N"], cfg["K"], cfg["H"]
+        cb, cbt = _cb_arg(cfg)
+        _, wo, pt = _proj_args(cfg)
+        out = np.zeros((M, H), np.float32)
+        rc = self.lib.aqo_projected_decode(idx, M, H, K, Q, N, cb.ctypes.data_as(C.c_void_p), cbt,
+                                           wo.ctypes.data_as(C.c_void_p), _opt(cfg.get("b_out"), np.float32), pt, out)
+        if rc != 0:
+            raise IndexError("code outside [0, N)")
+        return out
+
+
+def _cb_arg(cfg: dict):
+    if "codebook_q8" in cfg:
+        return np.ascontiguousarray(cfg["codebook_q8"]), 1
+    return np.ascontiguousarray(cfg["codebook"], np.float32), 0
+
+
+def _proj_args(cfg: dict):
+    if "w_in_q8" in cfg:
+        return np.ascontiguousarray(cfg["w_in_q8"]), np.ascontiguousarray(cfg["w_out_q8"]), 1
+    return np.ascontiguousarray(cfg["w_in"], np.float32), np.ascontiguousarray(cfg["w_out"], np.float32), 0
+
 class _MossWeights(C.Structure):
     """MossWeights in ref_moss.cpp."""
     _fields_ = [("C", C.c_int64), ("R", C.c_int64), ("Q", C.c_int64), ("N", C.c_int64)] + [
@@ -304,6 +360,13 @@ class Ref:
         L.aqref_higgs_rvq.restype = C.c_double
         L.aqref_higgs_rvq.argtypes = [_f32p, _i64, _i64, _i64, _i64, C.c_void_p, C.c_int, C.c_int,
                                       _i32p, _f32p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int]
+        L.aqref_projected_rvq.restype = C.c_double
+        L.aqref_projected_rvq.argtypes = [_f32p, _i64, _i64, _i64, _i64, _i64, C.c_int, C.c_void_p, C.c_int,
+                                          C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int,
+                                          _i32p, _f32p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int]
+        L.aqref_projected_decode.restype = C.c_double
+        L.aqref_projected_decode.argtypes = [_i32p, _i64, _i64, _i64, _i64, _i64, C.c_void_p, C.c_int, C.c_void_p,
+                                             C.c_void_p, C.c_int, _f32p, C.c_int]
         L.aqref_quantize_row_q8_0.argtypes = [_f32p, C.c_void_p, _i64]
         L.aqref_vector_quantizer.restype = C.c_int
         L.aqref_vector_quantizer.argtypes = [_f32p, _i64, _i64, _i64, _i64, _f32p, _i64, _i64, _f32p]
@@ -431,6 +494,40 @@ class Ref:
         if topk:
             out["topk_idx"] = tki
             out["topk_logit"] = tkl
+        return out
+
+    def projected_rvq(self, cfg: dict, topk: int = 0, threads: int = 8):
+        """The OmniVoice / Higgs graphs with projections (aqref_projected_rvq)."""
+        x = np.ascontiguousarray(cfg["x"], np.float32)
+        M, H = x.shape
+        Q, N, K = cfg["Q"], cfg["N"], cfg["K"]
+        cb, cbt = _cb_arg(cfg)
+        wi, wo, pt = _proj_args(cfg)
+        idx = np.zeros((M, Q), np.int32)
+        res = np.zeros((M, H), np.float32)
+        dist = np.zeros((M, Q), np.float32)
+        tki = np.zeros((M, Q, max(topk, 1)), np.int32)
+        tkl = np.zeros((M, Q, max(topk, 1)), np.float32)
+        ms = self.lib.aqref_projected_rvq(
+            x, M, H, K, Q, N, cfg["recipe"], cb.ctypes.data_as(C.c_void_p), cbt, wi.ctypes.data_as(C.c_void_p),
+            _opt(cfg.get("b_in"), np.float32), wo.ctypes.data_as(C.c_void_p), _opt(cfg.get("b_out"), np.float32), pt,
+            topk, idx, res, dist.ctypes.data_as(C.c_void_p), tki.ctypes.data_as(C.c_void_p) if topk else None,
+            tkl.ctypes.data_as(C.c_void_p) if topk else None, threads)
+        out = dict(idx=idx, residual=res, dist=dist, ms=ms)
+        if topk:
+            out["topk_idx"] = tki
+            out["topk_logit"] = tkl
+        return out
+
+    def projected_decode(self, cfg: dict, idx, threads: int = 8):
+        idx = np.ascontiguousarray(idx, np.int32)
+        M = idx.shape[0]
+        cb, cbt = _cb_arg(cfg)
+        _, wo, pt = _proj_args(cfg)
+        out = np.zeros((M, cfg["H"]), np.float32)
+        self.lib.aqref_projected_decode(idx, M, cfg["H"], cfg["K"], cfg["Q"], cfg["N"], cb.ctypes.data_as(C.c_void_p),
+                                        cbt, wo.ctypes.data_as(C.c_void_p), _opt(cfg.get("b_out"), np.float32), pt, out,
+                                        threads)
         return out
 
     def vector_quantizer(self, x, codebook, batch: int = 1):

@@ -505,6 +505,140 @@ int aqo_direct_rvq(const float *x, int64_t M, int64_t K, int64_t Q, int64_t N, c
     return 0;
 }
 
+/* One row of LinearModule (src/framework/modules/linear_module.cpp:73-108):
+ * out[o] = mul_mat(W, x)[o] (+ bias[o] by ggml_add), for a weight of n_out
+ * rows of k values (F32, or Q8_0 blocks whose product quantises x with x86
+ * quantize_row_q8_0 first, ggml-cpu.c:1309-1340) applied to a batch of
+ * n_rows input rows (the batch size decides tinyBLAS vs vec_dot for F32).
+ * xq: scratch of k/32 blocks. */
+static void linear_row(const void *w, int w_type, const float *bias, int64_t n_out, int64_t k, int64_t n_rows,
+                       const float *x, aqo_block_q8_0 *xq, float *out) {
+    if (w_type == 1) aqo_quantize_row_q8_0_x86(x, xq, (int)k);
+    for (int64_t o = 0; o < n_out; ++o) {
+        float v = w_type == 1 ? aqo_dot_q8_0((int)(k / 32), (const aqo_block_q8_0 *)w + o * (k / 32), xq)
+                              : dot_f32(n_out, n_rows, (int)k, (const float *)w + o * k, x);
+        if (bias) v = v + bias[o];
+        out[o] = v;
+    }
+}
+
+/* OmniVoice and Higgs acoustic RVQ with the projections of the reference
+ * (omnivoice/audio_tokenizer.cpp:1886-1927; higgs_audio_tts/codec.cpp:958-1016):
+ * per stage, on the residual r of hidden size H (frame-major after the
+ * graphs' transposes, which only move data):
+ *   p      = project_in(r)                 LinearModule H -> K (+ bias)
+ *   logits = OmniVoice: mul_mat(2c, p) + (float)(-sum_double c^2)
+ *            Higgs:     ((2*mul_mat(c, p)) - sum_rows(p*p)) - sum_rows(c*c)
+ *   code   = argmax (last index), optional top_k (Higgs)
+ *   z      = project_out(get_rows(c, code)) LinearModule K -> H (+ bias)
+ *   r     -= z
+ * recipe 0 OmniVoice (F32 codebook), 1 Higgs (F32 or Q8_0 codebook);
+ * w_in [Q,K,H] and w_out [Q,H,K] are F32 (type 0) or Q8_0 blocks (type 1).
+ * x [M,H]; idx [M,Q]; residual [M,H]; dist [M,Q] = -logit[code] (nullable);
+ * topk_idx / topk_logit [M,Q,topk] (Higgs only). */
+int aqo_projected_rvq(const float *x, int64_t M, int64_t H, int64_t K, int64_t Q, int64_t N, int recipe,
+                      const void *cb, int cb_type, const void *w_in, const float *b_in, const void *w_out,
+                      const float *b_out, int proj_type, int topk, const int32_t *force_idx, int32_t *idx,
+                      float *residual, float *dist, int32_t *topk_idx, float *topk_logit) {
+    const int64_t nbk = K / 32;
+    float *r = residual;
+    memcpy(r, x, (size_t)(M * H) * sizeof(float));
+    float *cbf = (float *)malloc((size_t)(N * K) * sizeof(float));
+    float *w2 = (float *)malloc((size_t)(N * K) * sizeof(float));
+    float *cterm = (float *)malloc((size_t)N * sizeof(float));
+    float *lg = (float *)malloc((size_t)N * sizeof(float));
+    float *p = (float *)malloc((size_t)K * sizeof(float));
+    float *z = (float *)malloc((size_t)H * sizeof(float));
+    float *tmp = (float *)malloc((size_t)K * sizeof(float));
+    aqo_block_q8_0 *xq = (aqo_block_q8_0 *)malloc((size_t)(H / 32 + nbk + 1) * sizeof(aqo_block_q8_0));
+    if (!cbf || !w2 || !cterm || !lg || !p || !z || !tmp || !xq) {
+        free(cbf); free(w2); free(cterm); free(lg); free(p); free(z); free(tmp); free(xq);
+        return -1;
+    }
+    const size_t win_stage = proj_type == 1 ? (size_t)(K * (H / 32)) * sizeof(aqo_block_q8_0) : (size_t)(K * H) * 4;
+    const size_t wout_stage = proj_type == 1 ? (size_t)(H * nbk) * sizeof(aqo_block_q8_0) : (size_t)(H * K) * 4;
+    for (int64_t s = 0; s < Q; ++s) {
+        const aqo_block_q8_0 *Cq = cb_type == 1 ? (const aqo_block_q8_0 *)cb + s * N * nbk : NULL;
+        const void *Wi = (const char *)w_in + s * win_stage;
+        const void *Wo = (const char *)w_out + s * wout_stage;
+        const float *bi = b_in ? b_in + s * K : NULL;
+        const float *bo = b_out ? b_out + s * H : NULL;
+        for (int64_t n = 0; n < N; ++n) {
+            if (Cq) aqo_dequantize_row_q8_0(Cq + n * nbk, cbf + n * K, (int)K);
+            else memcpy(cbf + n * K, (const float *)cb + (s * N + n) * K, (size_t)K * sizeof(float));
+            if (recipe == 0) {   /* audio_tokenizer.cpp:1227-1237 */
+                double norm = 0.0;
+                for (int64_t k = 0; k < K; ++k) {
+                    const float v = cbf[n * K + k];
+                    w2[n * K + k] = 2.0f * v;
+                    norm += (double)v * (double)v;
+                }
+                cterm[n] = (float)(-norm);
+            } else {             /* sum_rows(c*c) */
+                for (int64_t k = 0; k < K; ++k) tmp[k] = cbf[n * K + k] * cbf[n * K + k];
+                cterm[n] = aqo_sum_f32((int)K, tmp);
+            }
+        }
+        for (int64_t m = 0; m < M; ++m) {
+            float *rm = r + m * H;
+            linear_row(Wi, proj_type, bi, K, H, M, rm, xq, p);
+            if (recipe == 0) {
+                for (int64_t n = 0; n < N; ++n) lg[n] = dot_f32(N, M, (int)K, w2 + n * K, p) + cterm[n];
+            } else {
+                for (int64_t k = 0; k < K; ++k) tmp[k] = p[k] * p[k];
+                const float x2 = aqo_sum_f32((int)K, tmp);
+                if (Cq) aqo_quantize_row_q8_0_x86(p, xq, (int)K);
+                for (int64_t n = 0; n < N; ++n) {
+                    const float dot = Cq ? aqo_dot_q8_0((int)nbk, Cq + n * nbk, xq) : dot_f32(N, M, (int)K, cbf + n * K, p);
+                    lg[n] = ((dot * 2.0f) - x2) - cterm[n];
+                }
+            }
+            const int code = aqo_argmax_f32((int)N, lg);
+            idx[m * Q + s] = code;
+            if (dist) dist[m * Q + s] = -lg[code];
+            if (topk > 0) {
+                int32_t *ti = topk_idx + (m * Q + s) * topk;
+                aqo_top_k_f32(lg, N, topk, ti);
+                for (int k = 0; k < topk; ++k) topk_logit[(m * Q + s) * topk + k] = lg[ti[k]];
+            }
+            const int64_t use = force_idx ? force_idx[m * Q + s] : code;
+            linear_row(Wo, proj_type, bo, H, K, M, cbf + use * K, xq, z);
+            for (int64_t h = 0; h < H; ++h) rm[h] = rm[h] - z[h];
+        }
+    }
+    free(cbf); free(w2); free(cterm); free(lg); free(p); free(z); free(tmp); free(xq);
+    return 0;
+}
+
+/* Decode of the projected cascades (omnivoice/audio_tokenizer.cpp:1745-1771,
+ * higgs_audio_tts/codec.cpp:1040-1065): out[m] = z_0 + z_1 + ... in stage
+ * order, z_s = project_out(get_rows(c_s, idx[m,s])).  Returns -1 on an
+ * out-of-range code. */
+int aqo_projected_decode(const int32_t *idx, int64_t M, int64_t H, int64_t K, int64_t Q, int64_t N,
+                         const void *cb, int cb_type, const void *w_out, const float *b_out, int proj_type,
+                         float *out) {
+    const int64_t nbk = K / 32;
+    float *c = (float *)malloc((size_t)K * sizeof(float));
+    float *z = (float *)malloc((size_t)H * sizeof(float));
+    aqo_block_q8_0 *xq = (aqo_block_q8_0 *)malloc((size_t)(nbk + 1) * sizeof(aqo_block_q8_0));
+    if (!c || !z || !xq) { free(c); free(z); free(xq); return -1; }
+    const size_t wout_stage = proj_type == 1 ? (size_t)(H * nbk) * sizeof(aqo_block_q8_0) : (size_t)(H * K) * 4;
+    int rc = 0;
+    for (int64_t m = 0; m < M && rc == 0; ++m) {
+        float *om = out + m * H;
+        for (int64_t s = 0; s < Q; ++s) {
+            const int32_t code = idx[m * Q + s];
+            if (code < 0 || code >= N) { rc = -1; break; }
+            if (cb_type == 1) aqo_dequantize_row_q8_0((const aqo_block_q8_0 *)cb + (s * N + code) * nbk, c, (int)K);
+            else memcpy(c, (const float *)cb + (s * N + code) * K, (size_t)K * sizeof(float));
+            linear_row((const char *)w_out + s * wout_stage, proj_type, b_out ? b_out + s * H : NULL, H, K, M, c, xq, z);
+            for (int64_t h = 0; h < H; ++h) om[h] = s == 0 ? z[h] : om[h] + z[h];
+        }
+    }
+    free(c); free(z); free(xq);
+    return rc;
+}
+
 int aqo_gather_f32(const float *cb, int64_t N, int64_t K, const int32_t *idx, int64_t M, float *out) {
     for (int64_t m = 0; m < M; ++m) {
         if (idx[m] < 0 || idx[m] >= N) return -1;

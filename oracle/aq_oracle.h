@@ -71,6 +71,21 @@ int aqo_higgs_rvq(const float *x, int64_t M, int64_t K, int64_t Q, int64_t N,
                   int32_t *idx, float *residual, float *dist,
                   int32_t *topk_idx, float *topk_logit);
 
+/* OmniVoice / Higgs RVQ with per-stage project_in (H -> K) and project_out
+ * (K -> H) around the score, the residual kept in hidden space
+ * (omnivoice/audio_tokenizer.cpp:1886-1927, higgs_audio_tts/codec.cpp:958-1016).
+ * recipe 0 OmniVoice, 1 Higgs; cb [Q,N,K] F32 (cb_type 0) or [Q,N,K/32] Q8_0
+ * blocks (cb_type 1); w_in [Q,K,H] and w_out [Q,H,K] F32 (proj_type 0) or
+ * Q8_0 blocks (proj_type 1); b_in [Q,K], b_out [Q,H] nullable.  x [M,H];
+ * idx [M,Q]; residual [M,H]; dist [M,Q] nullable; topk outputs [M,Q,topk]. */
+int aqo_projected_rvq(const float *x, int64_t M, int64_t H, int64_t K, int64_t Q, int64_t N, int recipe,
+                      const void *cb, int cb_type, const void *w_in, const float *b_in, const void *w_out,
+                      const float *b_out, int proj_type, int topk, const int32_t *force_idx, int32_t *idx,
+                      float *residual, float *dist, int32_t *topk_idx, float *topk_logit);
+/* Their decode: out[m] = sum over stages, in order, of project_out(c_s[idx]). */
+int aqo_projected_decode(const int32_t *idx, int64_t M, int64_t H, int64_t K, int64_t Q, int64_t N,
+                         const void *cb, int cb_type, const void *w_out, const float *b_out, int proj_type,
+                         float *out);
 /* ggml_top_k of one row: the k indices std::partial_sort (libstdc++) keeps
  * with comp(a, b) = v[a] > v[b], in its order, dst[0] and dst[1] swapped. */
 void aqo_top_k_f32(const float *v, int64_t n, int k, int32_t *dst);

@@ -363,6 +363,145 @@ double aqref_higgs_rvq(const float * x, int64_t M, int64_t K, int64_t Q, int64_t
     return ms;
 }
 
+// OmniVoice / Higgs RVQ with the per-stage projections
+// (omnivoice/audio_tokenizer.cpp:1886-1927; higgs_audio_tts/codec.cpp:958-1016).
+// The residual is kept frame-major [H, M] (ne order): the graphs' bct <-> btc
+// transposes only move data, and LinearModule makes its input contiguous
+// (ensure_backend_addressable_layout, src/framework/core/module.cpp:199-210)
+// before mul_mat + bias add (linear_module.cpp:73-108).
+// recipe 0 OmniVoice (score = Linear(2c, -|c|^2)), 1 Higgs (2*dot - x2 - e2).
+// cb_type / proj_type: 0 F32, 1 Q8_0 blocks.  w_in [Q, K, H], w_out [Q, H, K]
+// (row-major: ne = [H, K] and [K, H]); b_in [Q, K], b_out [Q, H] nullable.
+// Outputs idx [M, Q]; residual [M, H]; dist [M, Q] = -logit[idx] (nullable);
+// topk_idx / topk_logit [M, Q, topk] (Higgs, topk > 0).
+double aqref_projected_rvq(const float * x, int64_t M, int64_t H, int64_t K, int64_t Q, int64_t N, int recipe,
+                           const void * cb, int cb_type, const void * w_in, const float * b_in,
+                           const void * w_out, const float * b_out, int proj_type, int topk,
+                           int32_t * idx, float * residual, float * dist,
+                           int32_t * topk_idx, float * topk_logit, int n_threads) {
+    ggml_cpu_init();
+    double ms = 0.0;
+    std::vector<float> res(x, x + M * H);
+    const ggml_type tc = cb_type == 1 ? GGML_TYPE_Q8_0 : GGML_TYPE_F32;
+    const ggml_type tp = proj_type == 1 ? GGML_TYPE_Q8_0 : GGML_TYPE_F32;
+    const size_t cb_bytes = ggml_row_size(tc, K) * static_cast<size_t>(N);
+    const size_t wi_bytes = ggml_row_size(tp, H) * static_cast<size_t>(K);
+    const size_t wo_bytes = ggml_row_size(tp, K) * static_cast<size_t>(H);
+    for (int64_t s = 0; s < Q; ++s) {
+        const size_t bytes = static_cast<size_t>(M) * static_cast<size_t>(N * 8 + 6 * H + 8 * K) * 4 +
+                             static_cast<size_t>(N * K) * 16 + static_cast<size_t>(H * K) * 12 + (64u << 20);
+        Ctx c(bytes);
+        ggml_context * ctx = c.ctx;
+        ggml_tensor * R = ggml_new_tensor_2d(ctx, GGML_TYPE_F32, H, M);
+        std::memcpy(R->data, res.data(), res.size() * 4);
+        ggml_tensor * CB = ggml_new_tensor_2d(ctx, tc, K, N);
+        std::memcpy(CB->data, static_cast<const char *>(cb) + s * cb_bytes, cb_bytes);
+        ggml_tensor * Wi = ggml_new_tensor_2d(ctx, tp, H, K);
+        std::memcpy(Wi->data, static_cast<const char *>(w_in) + s * wi_bytes, wi_bytes);
+        ggml_tensor * Wo = ggml_new_tensor_2d(ctx, tp, K, H);
+        std::memcpy(Wo->data, static_cast<const char *>(w_out) + s * wo_bytes, wo_bytes);
+        ggml_tensor * p = ggml_mul_mat(ctx, Wi, R);                              // [K, M]
+        ggml_mul_mat_set_prec(p, GGML_PREC_F32);
+        if (b_in) {
+            ggml_tensor * Bi = ggml_new_tensor_1d(ctx, GGML_TYPE_F32, K);
+            std::memcpy(Bi->data, b_in + s * K, static_cast<size_t>(K) * 4);
+            p = ggml_add(ctx, p, Bi);
+        }
+        ggml_tensor * lg = nullptr;
+        if (recipe == 0) {   // audio_tokenizer.cpp:1227-1237 score weights
+            ggml_tensor * W = ggml_new_tensor_2d(ctx, GGML_TYPE_F32, K, N);
+            ggml_tensor * Bs = ggml_new_tensor_1d(ctx, GGML_TYPE_F32, N);
+            const float * cbs = static_cast<const float *>(cb) + s * N * K;
+            float * wp = static_cast<float *>(W->data);
+            float * bp = static_cast<float *>(Bs->data);
+            for (int64_t r = 0; r < N; ++r) {
+                double norm = 0.0;
+                for (int64_t k = 0; k < K; ++k) {
+                    const float v = cbs[r * K + k];
+                    wp[r * K + k] = 2.0f * v;
+                    norm += static_cast<double>(v) * static_cast<double>(v);
+                }
+                bp[r] = static_cast<float>(-norm);
+            }
+            lg = ggml_mul_mat(ctx, W, p);
+            ggml_mul_mat_set_prec(lg, GGML_PREC_F32);
+            lg = ggml_add(ctx, lg, Bs);
+        } else {             // codec.cpp:975-999
+            ggml_tensor * dot = ggml_mul_mat(ctx, CB, p);                        // [N, M]
+            ggml_tensor * x2 = ggml_repeat(ctx, ggml_sum_rows(ctx, ggml_mul(ctx, p, p)), dot);
+            ggml_tensor * cbf = tc == GGML_TYPE_F32 ? CB : ggml_cast(ctx, CB, GGML_TYPE_F32);
+            ggml_tensor * e2 = ggml_reshape_2d(ctx, ggml_sum_rows(ctx, ggml_mul(ctx, cbf, cbf)), N, 1);
+            e2 = ggml_repeat(ctx, e2, dot);
+            lg = ggml_sub(ctx, ggml_sub(ctx, ggml_scale(ctx, dot, 2.0f), x2), e2);
+        }
+        ggml_tensor * ids = ggml_argmax(ctx, lg);
+        ggml_tensor * tk = topk > 0 ? ggml_top_k(ctx, lg, topk) : nullptr;
+        ggml_tensor * emb = ggml_get_rows(ctx, CB, ids);                         // [K, M] F32
+        ggml_tensor * z = ggml_mul_mat(ctx, Wo, emb);                            // [H, M]
+        ggml_mul_mat_set_prec(z, GGML_PREC_F32);
+        if (b_out) {
+            ggml_tensor * Bo = ggml_new_tensor_1d(ctx, GGML_TYPE_F32, H);
+            std::memcpy(Bo->data, b_out + s * H, static_cast<size_t>(H) * 4);
+            z = ggml_add(ctx, z, Bo);
+        }
+        ggml_tensor * Rn = ggml_sub(ctx, R, z);
+        ms += run_graph(ctx, Rn, n_threads, nullptr, ids, lg, tk);
+        std::memcpy(res.data(), Rn->data, res.size() * 4);
+        const int32_t * ip = static_cast<const int32_t *>(ids->data);
+        const float * lp = static_cast<const float *>(lg->data);
+        for (int64_t m = 0; m < M; ++m) {
+            idx[m * Q + s] = ip[m];
+            if (dist) dist[m * Q + s] = -lp[m * N + ip[m]];
+            if (tk) {
+                const int32_t * tkp = static_cast<const int32_t *>(tk->data) + m * topk;
+                for (int k = 0; k < topk; ++k) {
+                    topk_idx[(m * Q + s) * topk + k] = tkp[k];
+                    topk_logit[(m * Q + s) * topk + k] = lp[m * N + tkp[k]];
+                }
+            }
+        }
+    }
+    if (residual) std::memcpy(residual, res.data(), res.size() * 4);
+    return ms;
+}
+
+// Their decode (omnivoice/audio_tokenizer.cpp:1745-1771; higgs codec.cpp:
+// 1040-1065): latent = z_0, then latent = latent + z_s, z_s =
+// Linear(project_out)(get_rows(c_s, idx[:, s])).  idx [M, Q]; out [M, H].
+double aqref_projected_decode(const int32_t * idx, int64_t M, int64_t H, int64_t K, int64_t Q, int64_t N,
+                              const void * cb, int cb_type, const void * w_out, const float * b_out, int proj_type,
+                              float * out, int n_threads) {
+    ggml_cpu_init();
+    const ggml_type tc = cb_type == 1 ? GGML_TYPE_Q8_0 : GGML_TYPE_F32;
+    const ggml_type tp = proj_type == 1 ? GGML_TYPE_Q8_0 : GGML_TYPE_F32;
+    const size_t cb_bytes = ggml_row_size(tc, K) * static_cast<size_t>(N);
+    const size_t wo_bytes = ggml_row_size(tp, K) * static_cast<size_t>(H);
+    const size_t bytes = static_cast<size_t>(Q) * (cb_bytes + wo_bytes + static_cast<size_t>(M) * (3 * H + 2 * K + 4) * 4) +
+                         (64u << 20);
+    Ctx c(bytes);
+    ggml_context * ctx = c.ctx;
+    ggml_tensor * latent = nullptr;
+    for (int64_t s = 0; s < Q; ++s) {
+        ggml_tensor * ids = ggml_new_tensor_1d(ctx, GGML_TYPE_I32, M);
+        int32_t * ip = static_cast<int32_t *>(ids->data);
+        for (int64_t m = 0; m < M; ++m) ip[m] = idx[m * Q + s];
+        ggml_tensor * CB = ggml_new_tensor_2d(ctx, tc, K, N);
+        std::memcpy(CB->data, static_cast<const char *>(cb) + s * cb_bytes, cb_bytes);
+        ggml_tensor * Wo = ggml_new_tensor_2d(ctx, tp, K, H);
+        std::memcpy(Wo->data, static_cast<const char *>(w_out) + s * wo_bytes, wo_bytes);
+        ggml_tensor * z = ggml_mul_mat(ctx, Wo, ggml_get_rows(ctx, CB, ids));
+        if (b_out) {
+            ggml_tensor * Bo = ggml_new_tensor_1d(ctx, GGML_TYPE_F32, H);
+            std::memcpy(Bo->data, b_out + s * H, static_cast<size_t>(H) * 4);
+            z = ggml_add(ctx, z, Bo);
+        }
+        latent = latent ? ggml_add(ctx, latent, z) : z;
+    }
+    const double ms = run_graph(ctx, latent, n_threads);
+    std::memcpy(out, latent->data, static_cast<size_t>(M * H) * 4);
+    return ms;
+}
+
 // ggml_top_k alone (ops.cpp:8423-8456) on rows of n values: v [rows, n],
 // dst [rows, k] in ggml's order.
 void aqref_top_k(const float * v, int64_t rows, int64_t n, int k, int32_t * dst, int n_threads) {

@@ -516,3 +516,67 @@ def test_synth_moss_fold_is_the_reference_fold(o):
     a, b = synth.moss_fold(cfg), o.moss_fold(cfg)
     for k in a:
         assert _beq(a[k], b[k]), k
+
+
+# ------------------------------------------- projected cascades (OmniVoice / Higgs) --
+
+@pytest.mark.parametrize("recipe,cb_q8,proj_q8,M,topk", [
+    (0, False, False, 37, 0), (0, False, True, 21, 0), (1, False, False, 30, 0), (1, True, True, 25, 4),
+    (1, False, True, 9, 0), (1, True, False, 12, 2), (0, False, False, 1, 0), (1, True, True, 1, 0),
+    (1, False, False, 1, 3)])
+def test_oracle_projected_bit_exact_vs_ggml(o, ref, recipe, cb_q8, proj_q8, M, topk):
+    """project_in -> score -> argmax (top_k) -> lookup -> project_out -> sub
+    per stage, against the reference's op graph on ggml (M = 1 takes
+    ggml_vec_dot_f32 for the F32 products, M >= 2 tinyBLAS)."""
+    cfg = synth.projected_config(M, recipe=recipe, cb_q8=cb_q8, proj_q8=proj_q8, Q=3)
+    a = o.projected_rvq(cfg, topk=topk)
+    b = ref.projected_rvq(cfg, topk=topk)
+    assert np.array_equal(a["idx"], b["idx"])
+    assert _beq(a["residual"], b["residual"])
+    assert _beq(a["dist"], b["dist"])
+    if topk:
+        assert np.array_equal(a["topk_idx"], b["topk_idx"])
+        assert _beq(a["topk_logit"], b["topk_logit"])
+
+
+@pytest.mark.parametrize("cb_q8,proj_q8,M", [(False, False, 40), (True, True, 33), (False, True, 1)])
+def test_oracle_projected_decode_vs_ggml(o, ref, cb_q8, proj_q8, M):
+    cfg = synth.projected_config(M, recipe=1, cb_q8=cb_q8, proj_q8=proj_q8, Q=4)
+    idx = o.projected_rvq(cfg)["idx"]
+    assert _beq(o.projected_decode(cfg, idx), ref.projected_decode(cfg, idx))
+    bad = idx.copy()
+    bad[0, 2] = cfg["N"]
+    with pytest.raises(IndexError):
+        o.projected_decode(cfg, bad)
+
+
+@pytest.mark.parametrize("recipe", [0, 1])
+def test_projected_with_selector_weights_is_the_plain_cascade(o, recipe):
+    """project_in = [I_K 0] and project_out = its transpose, no biases: the
+    projection picks the first K hidden channels exactly, so the projected
+    cascade must give the plain cascade's codes on those channels, their
+    residual, and leave the other channels untouched.  A transposed weight,
+    a sub in codebook space or a dropped stage fails this."""
+    H, K, N, Q, M = 256, 64, 256, 3, 50
+    cfg = synth.projected_config(M, recipe=recipe, H=H, K=K, N=N, Q=Q)
+    sel = np.zeros((Q, K, H), np.float32)
+    sel[:, np.arange(K), np.arange(K)] = 1.0
+    cfg.update(w_in=sel, w_out=np.ascontiguousarray(sel.transpose(0, 2, 1)), b_in=None, b_out=None)
+    out = o.projected_rvq(cfg)
+    plain = dict(x=np.ascontiguousarray(cfg["x"][:, :K]), M=M, K=K, Q=Q, N=N, codebook=cfg["codebook"])
+    want = o.euclid_rvq(plain) if recipe == 0 else o.higgs_rvq(plain)
+    assert np.array_equal(out["idx"], want["idx"])
+    assert np.array_equal(out["residual"][:, :K], want["residual"])
+    assert _beq(out["residual"][:, K:], cfg["x"][:, K:])
+
+
+def test_synth_q8_weight_rounding_matches_ggml(ref):
+    """synth.q8_0_quantize_ref is the reference weight store's rounding
+    (ggml_quantize_chunk -> quantize_row_q8_0_ref)."""
+    w = synth.normal(5, 9, (16, 256), 0.3)
+    w[0, :32] = np.arange(32) - 15.5          # half-way values after scaling
+    w[1, :32] = 0.0                           # amax = 0 block
+    got = synth.q8_0_quantize_ref(w)
+    want = np.zeros((16, 8), dtype=synth.Q8_DTYPE)
+    ref.lib.aqref_quantize_chunk_q8_0(np.ascontiguousarray(w, np.float32), want.ctypes.data_as(__import__("ctypes").c_void_p), 16, 256)
+    assert np.array_equal(got.view(np.uint8), want.view(np.uint8))
