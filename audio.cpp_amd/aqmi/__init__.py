@@ -31,6 +31,7 @@ EXPORTED = [
     "aq_codebook_gather", "aq_ema_codebook", "aq_euclid_upload_ema",
     "aq_euclid_decode", "aq_ctx_set_timing", "aq_ctx_read_timing",
     "aq_moss_upload", "aq_moss_release", "aq_moss_encode", "aq_moss_decode",
+    "aq_euclid_encode_strided", "aq_euclid_upload_projected",
 ]
 
 # aq_euclid_recipe / aq_codebook_type
@@ -75,6 +76,9 @@ def load_library(path: str | pathlib.Path | None = None) -> C.CDLL:
     lib.aq_ema_codebook.argtypes = [vp, vp, vp, i64, i64, i64, C.c_float, vp]
     lib.aq_euclid_upload_ema.argtypes = [vp, i64, i64, i64, vp, vp, C.c_float, C.c_int, C.POINTER(vp)]
     lib.aq_euclid_decode.argtypes = [vp, vp, vp, i64, vp]
+    lib.aq_euclid_encode_strided.argtypes = [vp, vp, vp, i64, i64, i64, i64, i64, vp, vp, vp, C.c_int, vp, vp, vp]
+    lib.aq_euclid_upload_projected.argtypes = [vp, i64, i64, i64, i64, C.c_int, vp, C.c_int, vp, vp, vp, vp,
+                                               C.c_int, C.POINTER(vp)]
     lib.aq_moss_upload.argtypes = [vp, i64, i64, i64, i64] + [vp] * 9 + [C.POINTER(vp)]
     lib.aq_moss_release.argtypes = [vp]
     lib.aq_moss_encode.argtypes = [vp, vp, vp, i64, vp, vp, vp]
@@ -254,10 +258,47 @@ class Codebooks:
             self.Q, self.N, nb = cb.shape
             self.K = nb * 32
         self.recipe = recipe
+        self.H = self.K
         h = C.c_void_p()
         ctx.check(ctx.lib.aq_euclid_upload(ctx.h, self.Q, self.N, self.K, cb_type, cb.ctypes.data_as(C.c_void_p),
                                            recipe, C.byref(h)))
         self.h = h
+
+    @classmethod
+    def projected(cls, ctx: Context, codebook, w_in, b_in, w_out, b_out, recipe: int, cb_type: int = CB_F32,
+                  proj_type: int = CB_F32):
+        """aq_euclid_upload_projected: OmniVoice / Higgs stages with
+        project_in w_in [Q, K, H] (+ b_in [Q, K]) and project_out w_out
+        [Q, H, K] (+ b_out [Q, H]); F32 arrays or block_q8_0 arrays of the
+        same rows (proj_type CB_Q8_0).  Encode takes x and residual [M, H]."""
+        self = cls.__new__(cls)
+        self.ctx = ctx
+        if cb_type == CB_F32:
+            cb = np.ascontiguousarray(codebook, np.float32)
+            self.Q, self.N, self.K = cb.shape
+        else:
+            cb = np.ascontiguousarray(codebook)
+            self.Q, self.N, nb = cb.shape
+            self.K = nb * 32
+        if proj_type == CB_F32:
+            wi = np.ascontiguousarray(w_in, np.float32)
+            wo = np.ascontiguousarray(w_out, np.float32)
+            self.H = wi.shape[2]
+        else:
+            wi = np.ascontiguousarray(w_in)
+            wo = np.ascontiguousarray(w_out)
+            self.H = wi.shape[2] * 32
+        bi = None if b_in is None else np.ascontiguousarray(b_in, np.float32)
+        bo = None if b_out is None else np.ascontiguousarray(b_out, np.float32)
+        self.recipe = recipe
+        h = C.c_void_p()
+        ctx.check(ctx.lib.aq_euclid_upload_projected(ctx.h, self.Q, self.N, self.K, self.H, cb_type,
+                                                     cb.ctypes.data_as(C.c_void_p), proj_type,
+                                                     wi.ctypes.data_as(C.c_void_p), _host_ptr(bi),
+                                                     wo.ctypes.data_as(C.c_void_p), _host_ptr(bo), recipe,
+                                                     C.byref(h)))
+        self.h = h
+        return self
 
     @classmethod
     def from_ema(cls, ctx: Context, embedding_sum, cluster_usage, recipe: int, eps: float = 1.0e-5):
@@ -270,6 +311,7 @@ class Codebooks:
         self.Q, self.N, self.K = es.shape
         assert cu.shape == (self.Q, self.N)
         self.recipe = recipe
+        self.H = self.K
         h = C.c_void_p()
         ctx.check(ctx.lib.aq_euclid_upload_ema(ctx.h, self.Q, self.N, self.K, es.ctypes.data_as(C.c_void_p),
                                                cu.ctypes.data_as(C.c_void_p), eps, recipe, C.byref(h)))
@@ -283,6 +325,17 @@ class Codebooks:
         self.ctx.check(self.ctx.lib.aq_euclid_encode(self.ctx.h, self.h, _dptr(x), x.shape[0], _dptr(idx),
                                                      _dptr(residual), _dptr(dist), topk, _dptr(topk_idx),
                                                      _dptr(topk_dist), _dptr(force_idx)))
+
+    def encode_strided(self, x, M: int, clip_len: int, clip_stride: int, frame_stride: int, chan_stride: int, idx,
+                       residual=None, dist=None, topk: int = 0, topk_idx=None, topk_dist=None, force_idx=None):
+        """aq_euclid_encode_strided: x is any device tensor holding frame m,
+        channel c at (m // clip_len) * clip_stride + (m % clip_len) *
+        frame_stride + c * chan_stride (in floats)."""
+        assert x.is_cuda and x.dtype == self.ctx.torch.float32
+        self.ctx.use_current_stream()
+        self.ctx.check(self.ctx.lib.aq_euclid_encode_strided(
+            self.ctx.h, self.h, x.data_ptr(), M, clip_len, clip_stride, frame_stride, chan_stride, _dptr(idx),
+            _dptr(residual), _dptr(dist), topk, _dptr(topk_idx), _dptr(topk_dist), _dptr(force_idx)))
 
     def failures(self) -> np.ndarray:
         """Frames per stage the bf16 certificate left to the refine pass."""

@@ -270,6 +270,19 @@ def projected_config(M: int, recipe: int = 1, seed: int = 13, H: int = 1024, K: 
     return cfg
 
 
+def qwen3_config(frames: int, seed: int = 14, S: int = 16, N: int = 2048, K: int = 256) -> dict:
+    """Qwen3-TTS speech-tokenizer quantizer inputs (tokenizer_speech_encoder.cpp
+    shapes: 1 semantic + 15 acoustic EMA codebooks of 2048 x 256): the
+    encoder's projected semantic and acoustic latents channel-major [K, frames]
+    ~N(0,1) as the graph leaves them, cluster_usage [S, N] ~U(1, 30) and
+    embedding_sum = usage * N(0, 1/4) per row, so the codebooks
+    (embedding_sum / usage) are close to N(0, 1/4)."""
+    usage = uniform(seed, 1, (S, N), 1.0, 30.0)
+    es = (normal(seed, 2, (S, N, K), 0.25) * usage[..., None]).astype(np.float32)
+    return dict(kind="qwen3", seed=seed, frames=frames, S=S, N=N, K=K, embedding_sum=es, cluster_usage=usage,
+                semantic=normal(seed, 3, (K, frames)), acoustic=normal(seed, 4, (K, frames)))
+
+
 # --------------------------------------------------------------------------
 # Host-loop DAC quantizers (test shapes; not BASELINE configs)
 

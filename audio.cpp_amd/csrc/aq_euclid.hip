@@ -3,6 +3,7 @@
 // kernels, the certificate and the reference recipes are described in
 // aq_euclid_kernels.hpp.
 #include "aq_euclid_kernels.hpp"
+#include "aq_projected.hpp"
 
 #include <algorithm>
 #include <cmath>
@@ -134,6 +135,7 @@ struct aq_codebooks {
     float *d_q8d = nullptr;      // [Q][N][K/32]
     std::vector<float> cmax, dcmax, chmax;
     std::vector<float> clmax, crmax;   // max |c_l|, max |c - c_h - c_l| (refine bound)
+    aq_proj_weights *proj = nullptr;   // project_in / project_out (projected cascades)
 };
 
 extern "C" {
@@ -302,10 +304,40 @@ aq_status aq_euclid_upload_ema(aq_ctx *ctx, int64_t Q, int64_t N, int64_t K, con
     return aq_euclid_upload(ctx, Q, N, K, AQ_CB_F32, cb.data(), recipe, out);
 }
 
+aq_status aq_euclid_upload_projected(aq_ctx *ctx, int64_t Q, int64_t N, int64_t K, int64_t H, int cb_type,
+                                     const void *codebook, int proj_type, const void *w_in, const float *b_in,
+                                     const void *w_out, const float *b_out, int recipe, aq_codebooks **out) {
+    if (!ctx || !out || !codebook || !w_in || !w_out)
+        return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_euclid_upload_projected: null argument");
+    *out = nullptr;
+    if (recipe != AQ_EUCLID_OMNIVOICE && recipe != AQ_EUCLID_HIGGS)
+        return aq_fail(ctx, AQ_E_UNSUPPORTED, "aq_euclid_upload_projected: projections follow the OmniVoice and Higgs recipes");
+    if (proj_type != AQ_CB_F32 && proj_type != AQ_CB_Q8_0)
+        return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_euclid_upload_projected: unknown weight type %d", proj_type);
+    // The projection block keeps 16 residual rows of H + 1 floats in LDS
+    // (plus their Q8_0 image for Q8_0 weights).
+    const int64_t lds = 16 * (H + 1) * 4 + (proj_type == AQ_CB_Q8_0 ? 16 * H + 16 * (H / 32) * 4 : 0);
+    if (H <= 0 || H % 64 != 0 || lds > 160 * 1024)
+        return aq_fail(ctx, AQ_E_SHAPE, "aq_euclid_upload_projected: hidden size H=%lld (a multiple of 64 up to %d)",
+                       (long long)H, proj_type == AQ_CB_Q8_0 ? 1984 : 2496);
+    aq_codebooks *cb = nullptr;
+    aq_status st = aq_euclid_upload(ctx, Q, N, K, cb_type, codebook, recipe, &cb);
+    if (st != AQ_OK) return st;
+    aq_device_guard g(ctx->device);
+    st = aq_proj_create(ctx, Q, N, K, H, cb->d_cbf, proj_type, w_in, b_in, w_out, b_out, &cb->proj);
+    if (st != AQ_OK) {
+        aq_euclid_release(cb);
+        return st;
+    }
+    *out = cb;
+    return AQ_OK;
+}
+
 aq_status aq_euclid_release(aq_codebooks *cb) {
     if (!cb) return AQ_E_INVALID_ARG;
     {
         aq_device_guard g(cb->ctx->device);
+        aq_proj_release(cb->proj);
         for (void *p : {static_cast<void *>(cb->d_cbh), static_cast<void *>(cb->d_cbl), static_cast<void *>(cb->d_hh),
                         static_cast<void *>(cb->d_cbf),
                         static_cast<void *>(cb->d_bias), static_cast<void *>(cb->d_e2), static_cast<void *>(cb->d_q8),
@@ -316,13 +348,23 @@ aq_status aq_euclid_release(aq_codebooks *cb) {
     return AQ_OK;
 }
 
-aq_status aq_euclid_encode(aq_ctx *ctx, const aq_codebooks *cb, const float *x, int64_t M, int32_t *idx,
-                           float *residual, float *dist, int topk, int32_t *topk_idx, float *topk_dist,
-                           const int32_t *force_idx) {
-    if (!ctx || !cb || !idx || (!x && M > 0)) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_euclid_encode: null argument");
+}  // extern "C"
+
+namespace {
+
+// Encode M frames (strided input `in`) through every stage of cb.  Plain
+// codebooks: the residual cascade in codebook space, r -= c[code].
+// Projected codebooks: per stage p = project_in(r), the stage pipeline on p,
+// and r -= project_out(c[code]) in hidden space, fused into the next stage's
+// projection.
+aq_status euclid_encode_impl(aq_ctx *ctx, const aq_codebooks *cb, const aq_frames_desc &in, int64_t M, int32_t *idx,
+                             float *residual, float *dist, int topk, int32_t *topk_idx, float *topk_dist,
+                             const int32_t *force_idx) {
+    if (!ctx || !cb || !idx || (!in.x && M > 0)) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_euclid_encode: null argument");
     if (cb->ctx->device != ctx->device)
         return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_euclid_encode: codebooks belong to another device");
     if (M < 0 || M > (int64_t{1} << 31) - 1) return aq_fail(ctx, AQ_E_SHAPE, "aq_euclid_encode: M=%lld out of range", (long long)M);
+    if (in.clip_len <= 0) return aq_fail(ctx, AQ_E_SHAPE, "aq_euclid_encode: clip_len must be positive");
     if (topk < 0 || topk > 4 || topk > cb->N)
         return aq_fail(ctx, AQ_E_SHAPE, "aq_euclid_encode: topk=%d (supported 0..4, at most N)", topk);
     if (topk > 0 && (!topk_idx || !topk_dist))
@@ -331,6 +373,8 @@ aq_status aq_euclid_encode(aq_ctx *ctx, const aq_codebooks *cb, const float *x, 
     aq_device_guard g(ctx->device);
     const int K = static_cast<int>(cb->K);
     const int ks = K / 32;
+    const aq_proj_weights *pw = cb->proj;
+    const int64_t H = pw ? pw->H : K;   // width of the input and of the residual
     // Keys per lane: 4 for top-4, and for large codebooks (N * K >= 2^22),
     // where a frame the first certificate leaves open costs a split-bf16
     // pass over N * K; 3 otherwise (one med3 less per score in the sweep).
@@ -357,11 +401,17 @@ aq_status aq_euclid_encode(aq_ctx *ctx, const aq_codebooks *cb, const float *x, 
     const int64_t ngroups = (M + 15) / 16;
     const size_t scan_lds = static_cast<size_t>(K) * 5 + (K / 32) * 4 + 64;
 
-    // Work buffers: the residual (the caller's buffer when given), the
-    // sweep's keys and frame norms, and the per-stage failure lists.
+    // Work buffers: the residual (the caller's buffer when given; [M, H]),
+    // the projected queries of a projected cascade ([M, K]), the sweep's keys
+    // and frame norms, and the per-stage failure lists.
     float *work = residual;
     if (!work) {
-        aq_status st = aq_ctx_scratch(ctx, 0, static_cast<size_t>(M) * K * sizeof(float), reinterpret_cast<void **>(&work));
+        aq_status st = aq_ctx_scratch(ctx, 0, static_cast<size_t>(M) * H * sizeof(float), reinterpret_cast<void **>(&work));
+        if (st != AQ_OK) return st;
+    }
+    float *pbuf = nullptr;
+    if (pw) {
+        aq_status st = aq_ctx_scratch(ctx, 2, static_cast<size_t>(M) * K * sizeof(float), reinterpret_cast<void **>(&pbuf));
         if (st != AQ_OK) return st;
     }
     float *keys = nullptr;
@@ -395,6 +445,12 @@ aq_status aq_euclid_encode(aq_ctx *ctx, const aq_codebooks *cb, const float *x, 
         const int64_t per_big = ((cb->N + kRS - 1) / kRS) * 4 * kTopR;
         int64_t floats = std::max(std::min<int64_t>(M, kRSmallFrames) * per_small, M * per_big);
         floats = std::min<int64_t>(floats, (int64_t{64} << 20) / 4);
+        // Test hook: AQ_EUCLID_REFINE_KEY_FLOATS caps the buffer, so that the
+        // path from the capacity limit to the exact scan runs at small sizes.
+        if (const char *cap = std::getenv("AQ_EUCLID_REFINE_KEY_FLOATS")) {
+            const long long v = std::atoll(cap);
+            if (v > 0) floats = std::min<int64_t>(floats, v);
+        }
         floats = std::max(floats, per_small);
         void *w = nullptr;
         aq_status st = aq_ctx_scratch(ctx, 3, static_cast<size_t>(floats) * 4, &w);
@@ -408,11 +464,12 @@ aq_status aq_euclid_encode(aq_ctx *ctx, const aq_codebooks *cb, const float *x, 
     AQ_HIP(ctx, hipMemsetAsync(counts, 0, sizeof(int32_t) * 128, ctx->stream));
     AQ_HIP(ctx, hipMemsetAsync(ctx->d_flags, 0, sizeof(int32_t) * AQ_FLAG_COUNT, ctx->stream));
 
-    for (int64_t s = 0; s < cb->Q; ++s) {
+    // Stage s of the pipeline: queries xin [M, K], residual out xout (null:
+    // not needed), teacher forcing `force` of the codebook-space update.
+    auto run_stage = [&](int64_t s, const float *xin, float *xout, const int32_t *force) -> aq_status {
         StageArgs a{};
-        a.xin = s == 0 ? x : work;
-        // the last stage's residual is only written when the caller asks for it
-        a.xout = (s + 1 < cb->Q || residual) ? work : nullptr;
+        a.xin = xin;
+        a.xout = xout;
         a.M = M;
         a.N = static_cast<int>(cb->N);
         a.cbh = cb->d_cbh + s * cb->N * K;
@@ -436,7 +493,7 @@ aq_status aq_euclid_encode(aq_ctx *ctx, const aq_codebooks *cb, const float *x, 
         a.topk = topk;
         a.topk_idx = topk_idx;
         a.topk_dist = topk_dist;
-        a.force_idx = force_idx;
+        a.force_idx = force;
         a.fail_count = counts + (s % 64);
         a.fail_list = list;
         a.flags = ctx->d_flags;
@@ -454,20 +511,57 @@ aq_status aq_euclid_encode(aq_ctx *ctx, const aq_codebooks *cb, const float *x, 
                            ctx->stream, a);
         AQ_HIP(ctx, hipGetLastError());
         // refine pass over the frames the stage kernel left open
-        rf.cbl = cb->d_cbl + s * cb->N * K;
-        rf.clmax = cb->clmax[s];
-        rf.crmax = cb->crmax[s];
-        rf.count2 = counts2 + (s % 64);
-        hipLaunchKernelGGL(rvals, dim3(static_cast<unsigned>(2 * cus)), dim3(kWave * kRWaves), 0, ctx->stream, a, rf);
+        RefArgs r = rf;
+        r.cbl = cb->d_cbl + s * cb->N * K;
+        r.clmax = cb->clmax[s];
+        r.crmax = cb->crmax[s];
+        r.count2 = counts2 + (s % 64);
+        hipLaunchKernelGGL(rvals, dim3(static_cast<unsigned>(2 * cus)), dim3(kWave * kRWaves), 0, ctx->stream, a, r);
         AQ_HIP(ctx, hipGetLastError());
-        hipLaunchKernelGGL(rsel, dim3(static_cast<unsigned>(16 * cus)), dim3(kWave), 0, ctx->stream, a, rf);
+        hipLaunchKernelGGL(rsel, dim3(static_cast<unsigned>(16 * cus)), dim3(kWave), 0, ctx->stream, a, r);
         AQ_HIP(ctx, hipGetLastError());
         // exact scan of what the refine pass left open
         StageArgs a2 = a;
-        a2.fail_count = rf.count2;
+        a2.fail_count = r.count2;
         a2.fail_list = list2;
         hipLaunchKernelGGL(scan, dim3(static_cast<unsigned>(cus)), dim3(kScanThreads), scan_lds, ctx->stream, a2);
         AQ_HIP(ctx, hipGetLastError());
+        return AQ_OK;
+    };
+
+    const bool row_major = in.frame_stride == H && in.chan_stride == 1 && (in.clip_len >= M || in.clip_stride == in.clip_len * H);
+    if (!pw) {
+        // A strided input is gathered into the residual buffer first.
+        const float *x0 = in.x;
+        if (!row_major) {
+            aq_status st = aq_gather_frames(ctx, in, M, H, work);
+            if (st != AQ_OK) return st;
+            x0 = work;
+        }
+        for (int64_t s = 0; s < cb->Q; ++s) {
+            // the last stage's residual is only written when the caller asks for it
+            aq_status st = run_stage(s, s == 0 ? x0 : work, (s + 1 < cb->Q || residual) ? work : nullptr, force_idx);
+            if (st != AQ_OK) return st;
+        }
+    } else {
+        // Stage s reads the input (s <= 1) or the residual buffer, subtracts
+        // the table row of stage s - 1's code (teacher-forced when asked) and
+        // projects.
+        const int32_t *codes = force_idx ? force_idx : idx;
+        const int ld = static_cast<int>(cb->Q);
+        const aq_frames_desc wdesc = aq_frames_row_major(work, M, H);
+        for (int64_t s = 0; s < cb->Q; ++s) {
+            aq_status st = aq_proj_step(ctx, pw, static_cast<int>(s), static_cast<int>(s) - 1, s <= 1 ? in : wdesc,
+                                        s >= 1 ? work : nullptr, codes, ld, pbuf, M);
+            if (st != AQ_OK) return st;
+            st = run_stage(s, pbuf, nullptr, nullptr);
+            if (st != AQ_OK) return st;
+        }
+        if (residual) {
+            aq_status st = aq_proj_step(ctx, pw, -1, static_cast<int>(cb->Q) - 1, cb->Q == 1 ? in : wdesc, residual,
+                                        codes, ld, nullptr, M);
+            if (st != AQ_OK) return st;
+        }
     }
     if (force_idx) {
         int32_t flag = 0;
@@ -476,6 +570,27 @@ aq_status aq_euclid_encode(aq_ctx *ctx, const aq_codebooks *cb, const float *x, 
         if (flag) return aq_fail(ctx, AQ_E_INDEX_RANGE, "aq_euclid_encode: force_idx holds a code outside [0, %lld)", (long long)cb->N);
     }
     return AQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+aq_status aq_euclid_encode(aq_ctx *ctx, const aq_codebooks *cb, const float *x, int64_t M, int32_t *idx,
+                           float *residual, float *dist, int topk, int32_t *topk_idx, float *topk_dist,
+                           const int32_t *force_idx) {
+    if (!cb) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_euclid_encode: null argument");
+    const int64_t H = cb->proj ? cb->proj->H : cb->K;
+    return euclid_encode_impl(ctx, cb, aq_frames_row_major(x, M, H), M, idx, residual, dist, topk, topk_idx, topk_dist,
+                              force_idx);
+}
+
+aq_status aq_euclid_encode_strided(aq_ctx *ctx, const aq_codebooks *cb, const float *x, int64_t M, int64_t clip_len,
+                                   int64_t clip_stride, int64_t frame_stride, int64_t chan_stride, int32_t *idx,
+                                   float *residual, float *dist, int topk, int32_t *topk_idx, float *topk_dist,
+                                   const int32_t *force_idx) {
+    return euclid_encode_impl(ctx, cb, aq_frames_desc{x, clip_len, clip_stride, frame_stride, chan_stride}, M, idx,
+                              residual, dist, topk, topk_idx, topk_dist, force_idx);
 }
 
 aq_status aq_euclid_failures(aq_ctx *ctx, const aq_codebooks *cb, int32_t *host_counts) {
@@ -526,8 +641,13 @@ aq_status aq_euclid_decode(aq_ctx *ctx, const aq_codebooks *cb, const int32_t *i
     aq_device_guard g(ctx->device);
     AQ_HIP(ctx, hipMemsetAsync(ctx->d_flags, 0, sizeof(int32_t) * AQ_FLAG_COUNT, ctx->stream));
     const int64_t total = M * cb->K;
-    hipLaunchKernelGGL(decode_sum_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, ctx->stream,
-                       cb->d_cbf, static_cast<int>(cb->Q), cb->N, cb->K, idx, M, out, ctx->d_flags);
+    if (cb->proj) {
+        aq_status st = aq_proj_decode(ctx, cb->proj, idx, M, out);
+        if (st != AQ_OK) return st;
+    } else {
+        hipLaunchKernelGGL(decode_sum_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, ctx->stream,
+                           cb->d_cbf, static_cast<int>(cb->Q), cb->N, cb->K, idx, M, out, ctx->d_flags);
+    }
     AQ_HIP(ctx, hipGetLastError());
     int32_t flag = 0;
     AQ_HIP(ctx, hipMemcpyAsync(&flag, ctx->d_flags + AQ_FLAG_BAD_INDEX, sizeof(int32_t), hipMemcpyDeviceToHost, ctx->stream));

@@ -6,7 +6,16 @@
  * search, the residual cascade across codebooks, and the codebook-gather
  * decode.  Results are bit-identical to the reference's ggml CPU backend on
  * the same inputs (same fp32 operation order, fused multiply-adds, double
- * accumulations and tie rules).
+ * accumulations and tie rules), with one documented exception: the Fish
+ * recipe (AQ_DAC_FISH) gives the exact cosine argmax, which is what the
+ * reference computes on its Metal branch (fish_audio/codec.cpp:324-327, a
+ * contiguous copy of the transposed projection before ggml_div).  On the CPU
+ * backend the reference hands ggml_div the transposed view itself
+ * (codec.cpp:323-334 with the transpose at :589), and ggml's CPU binary ops
+ * read src0 rows as contiguous (external/ggml/src/ggml-cpu/binary-ops.cpp:
+ * 120-136), so the reference's CPU Fish codes are not the cosine argmax and
+ * differ from this library's (tests/test_oracle.py
+ * test_reference_cpu_view_bug_is_real shows it on ggml itself).
  *
  * Conventions
  *  - Plain C types only.  Every entry point returns aq_status; a message for
@@ -26,8 +35,8 @@
  *      src/framework/runtime/host_ops.cpp:236-273
  *  - the inline encode quantizers of the codec models:
  *      Fish DAC cosine   src/models/fish_audio/codec.cpp:570-611
- *      OmniVoice         src/models/omnivoice/audio_tokenizer.cpp:1886-1927
- *      Higgs             src/models/higgs_audio_tts/codec.cpp:958-1016
+ *      OmniVoice         src/models/omnivoice/audio_tokenizer.cpp:1886-1927 (with projections)
+ *      Higgs             src/models/higgs_audio_tts/codec.cpp:958-1016 (with projections)
  *      Qwen3 / VieNeu    src/models/qwen3_tts/tokenizer_speech_encoder.cpp:287-349
  *      MOSS RLFQ         src/models/moss/shared/audio_tokenizer_quantizer.cpp:174-271
  *  - engine::modules::CodebookLookupModule / EmbeddingModule (ggml_get_rows)
@@ -171,7 +180,12 @@ aq_status aq_dac_decode(aq_ctx *ctx, const aq_dac_stages *stages, const int32_t 
 /* ---- Euclidean VQ / RVQ (Mimi-style codecs, k-means tokenisers) ------------
  *
  * Nearest codeword by squared Euclidean distance, with the residual cascade
- * r <- r - c[code] across Q stages.  `recipe` selects the reference
+ * r <- r - c[code] across Q stages in codebook space (Qwen3 / VieNeu,
+ * VectorQuantizer, k-means tokenisers).  The OmniVoice and Higgs acoustic
+ * quantizers project the residual in and out of each stage's codebook space
+ * and keep it in hidden space: aq_euclid_upload_projected below uploads them
+ * as one cascade; aq_euclid_upload without projections reproduces one of
+ * their stages on already projected queries.  `recipe` selects the reference
  * arithmetic the results are identical to:
  *   AQ_EUCLID_OMNIVOICE  logit = mul_mat(2c, r) + (float)(-(double)|c|^2),
  *                        argmax, last index among equal maxima
@@ -222,6 +236,42 @@ aq_status aq_euclid_release(aq_codebooks *cb);
 aq_status aq_euclid_encode(aq_ctx *ctx, const aq_codebooks *cb, const float *x, int64_t M, int32_t *idx,
                            float *residual, float *dist, int topk, int32_t *topk_idx, float *topk_dist,
                            const int32_t *force_idx);
+
+/* aq_euclid_encode on a strided input, e.g. the channel-major [B, C, T]
+ * latent of a ggml encoder graph (qwen3_tts/tokenizer_speech_encoder.cpp:
+ * 330-335 reads it that way; outetts/dac.cpp:565-571 and
+ * higgs_audio_tts/codec.cpp:965 transpose it first): frame m, channel c at
+ *   x + (m / clip_len) * clip_stride + (m % clip_len) * frame_stride + c * chan_stride.
+ * Channel-major [B, C, T]: clip_len = T, clip_stride = C*T, frame_stride = 1,
+ * chan_stride = T.  Frame-major [M, C]: clip_len = M, frame_stride = C,
+ * chan_stride = 1 (= aq_euclid_encode).  The outputs stay frame-major. */
+aq_status aq_euclid_encode_strided(aq_ctx *ctx, const aq_codebooks *cb, const float *x, int64_t M, int64_t clip_len,
+                                   int64_t clip_stride, int64_t frame_stride, int64_t chan_stride, int32_t *idx,
+                                   float *residual, float *dist, int topk, int32_t *topk_idx, float *topk_dist,
+                                   const int32_t *force_idx);
+
+/* Projected Euclidean RVQ: the OmniVoice and Higgs acoustic quantizers
+ * (omnivoice/audio_tokenizer.cpp:1886-1927; higgs_audio_tts/codec.cpp:958-1016).
+ * Per stage s, on the residual r of hidden size H (x at stage 0):
+ *   p    = W_in[s] r + b_in[s]              (LinearModule H -> K)
+ *   code = argmax of the recipe's logits of p against codebook s
+ *   r   -= W_out[s] c[s][code] + b_out[s]   (LinearModule K -> H)
+ * in ggml's arithmetic (tinyBLAS or ggml_vec_dot_f32 for F32 weights as ggml
+ * picks them, the quantised block dot for Q8_0 weights).  Replaces the
+ * quantizer loops of those two graphs and their weight loads
+ * (audio_tokenizer.cpp:1223-1271; higgs codec.cpp:544-568).
+ *   codebook  [Q, N, K] as cb_type (Q8_0 with AQ_EUCLID_HIGGS only)
+ *   w_in      [Q, K, H] and w_out [Q, H, K] as proj_type (AQ_CB_F32, or
+ *             AQ_CB_Q8_0 block rows), b_in [Q, K] and b_out [Q, H] float or NULL
+ * recipe AQ_EUCLID_OMNIVOICE or AQ_EUCLID_HIGGS; K as aq_euclid_upload; H a
+ * multiple of 64 (up to 2496 for F32 weights, 1984 for Q8_0).  The handle
+ * works with aq_euclid_encode / aq_euclid_encode_strided (x and residual
+ * [M, H]), aq_euclid_decode (out [M, H] = sum over stages of
+ * W_out c + b_out, the decoders' sum, audio_tokenizer.cpp:1745-1771 and
+ * higgs codec.cpp:1040-1065) and aq_codebook_gather (codebook rows, [M, K]). */
+aq_status aq_euclid_upload_projected(aq_ctx *ctx, int64_t Q, int64_t N, int64_t K, int64_t H, int cb_type,
+                                     const void *codebook, int proj_type, const void *w_in, const float *b_in,
+                                     const void *w_out, const float *b_out, int recipe, aq_codebooks **out);
 
 /* Frames per stage (first min(Q, 64) stages) of the last encode on ctx that
  * the bf16 error certificate could not settle; the split-bf16 refine pass

@@ -242,6 +242,17 @@ class Oracle:
         assert self.lib.aqo_ema_codebook(es, cu, Q, N, K, eps, out) == 0
         return out
 
+    def qwen3_quantize(self, cfg: dict):
+        """The Qwen3 cascade from the oracle's parts: EMA codebooks, then the
+        DIRECT recipe on the semantic latent (stage 0) and on the acoustic
+        latent (stages 1..15), both read channel-major.  Codes [frames, 16]."""
+        cb = self.ema_codebook(cfg["embedding_sum"], cfg["cluster_usage"], 1.0e-5)
+        F, K, N = cfg["frames"], cfg["K"], cfg["N"]
+        sem = self.direct_rvq(dict(x=np.ascontiguousarray(cfg["semantic"].T), M=F, K=K, Q=1, N=N, codebook=cb[:1]))
+        ac = self.direct_rvq(dict(x=np.ascontiguousarray(cfg["acoustic"].T), M=F, K=K, Q=cfg["S"] - 1, N=N,
+                                  codebook=cb[1:]))
+        return np.concatenate([sem["idx"], ac["idx"]], axis=1)
+
     def top_k(self, v, k: int):
         """aqo_top_k_f32 over the rows of v."""
         v = np.ascontiguousarray(v, np.float32)
@@ -367,6 +378,8 @@ class Ref:
         L.aqref_projected_decode.restype = C.c_double
         L.aqref_projected_decode.argtypes = [_i32p, _i64, _i64, _i64, _i64, _i64, C.c_void_p, C.c_int, C.c_void_p,
                                              C.c_void_p, C.c_int, _f32p, C.c_int]
+        L.aqref_qwen3_quantize.restype = C.c_double
+        L.aqref_qwen3_quantize.argtypes = [_f32p, _f32p, _i64, _f32p, _f32p, _i32p]
         L.aqref_quantize_row_q8_0.argtypes = [_f32p, C.c_void_p, _i64]
         L.aqref_vector_quantizer.restype = C.c_int
         L.aqref_vector_quantizer.argtypes = [_f32p, _i64, _i64, _i64, _i64, _f32p, _i64, _i64, _f32p]
@@ -529,6 +542,19 @@ class Ref:
                                         cbt, wo.ctypes.data_as(C.c_void_p), _opt(cfg.get("b_out"), np.float32), pt, out,
                                         threads)
         return out
+
+    def qwen3_quantize(self, cfg: dict):
+        """quantize_projected of the Qwen3 speech tokenizer (the reference's own
+        function): codes [frames, 16]."""
+        F = cfg["frames"]
+        codes = np.zeros((F, cfg["S"]), np.int32)
+        ms = self.lib.aqref_qwen3_quantize(np.ascontiguousarray(cfg["semantic"], np.float32),
+                                           np.ascontiguousarray(cfg["acoustic"], np.float32), F,
+                                           np.ascontiguousarray(cfg["embedding_sum"], np.float32),
+                                           np.ascontiguousarray(cfg["cluster_usage"], np.float32), codes)
+        if ms < 0:
+            raise RuntimeError("the reference quantizer threw")
+        return codes
 
     def vector_quantizer(self, x, codebook, batch: int = 1):
         """engine::runtime::VectorQuantizer::compute: nearest codewords."""

@@ -7,7 +7,7 @@ Inputs come from audio.cpp_amd/aqmi/synth.py (deterministic, seeded), so a
 fixture stores only outputs: codes, and SHA-256 digests of the fp32 residual
 and reconstruction bytes (bit-exact checks), plus small value samples.
 
-    python tests/golden/make_golden.py [dac] [mimi] [kmeans] [q8] [outetts] [moss]
+    python tests/golden/make_golden.py [dac] [mimi] [kmeans] [q8] [outetts] [moss] [qwen3] [projected]
 """
 
 from __future__ import annotations
@@ -119,8 +119,33 @@ def host_loop_bench(ref: Ref):
     save("moss_bench.npz", idx=ref.moss_encode(synth.moss_config(6000)).astype(np.int16))
 
 
+def qwen3(ref: Ref, name: str, frames: int = 600):
+    """Qwen3-TTS speech-tokenizer cascade (quantize_projected, the reference's
+    own function): 1 semantic + 15 acoustic EMA codebooks of 2048 x 256 on
+    channel-major latents, codes [frames, 16]."""
+    save(name, idx=ref.qwen3_quantize(synth.qwen3_config(frames)).astype(np.int16))
+
+
+def projected(ref: Ref):
+    """OmniVoice / Higgs cascades with projections (hidden 1024, dim 64, 1024
+    codes, 8 stages) from the reference's op graphs on ggml."""
+    cases = [("higgs_f32", dict(recipe=1), 0), ("higgs_q8", dict(recipe=1, cb_q8=True, proj_q8=True), 4),
+             ("omnivoice_f32", dict(recipe=0), 0), ("omnivoice_q8proj", dict(recipe=0, proj_q8=True), 0)]
+    for tag, kw, topk in cases:
+        cfg = synth.projected_config(400, **kw)
+        out = ref.projected_rvq(cfg, topk=topk)
+        arrays = dict(idx=out["idx"].astype(np.int16), residual_sha=np.array(sha(out["residual"])),
+                      dist_sha=np.array(sha(out["dist"])), residual_head=out["residual"][:4, :16].copy())
+        if topk:
+            ti, tl = sorted_topk(out["topk_idx"], out["topk_logit"])
+            arrays.update(topk_idx_sha=np.array(sha(ti.astype(np.int32))), topk_logit_sha=np.array(sha(tl)))
+        dec = ref.projected_decode(cfg, out["idx"])
+        arrays.update(decode_sha=np.array(sha(dec)))
+        save(f"projected_{tag}.npz", **arrays)
+
+
 def main():
-    which = set(sys.argv[1:]) or {"dac", "mimi", "kmeans", "q8", "outetts", "moss"}
+    which = set(sys.argv[1:]) or {"dac", "mimi", "kmeans", "q8", "outetts", "moss", "qwen3", "projected"}
     ref = Ref("native")
     if "dac" in which:
         dac(ref, 0, "dac_cfg0.npz")
@@ -137,6 +162,10 @@ def main():
     if "moss" in which:
         moss(ref, "moss_v2.npz")
         host_loop_bench(ref)
+    if "qwen3" in which:
+        qwen3(ref, "qwen3_cascade.npz")
+    if "projected" in which:
+        projected(ref)
 
 
 if __name__ == "__main__":

@@ -358,3 +358,55 @@ def test_ema_codebook_and_upload(torch, ctx, oracle):
     ref = oracle.direct_rvq(dict(x=x, M=M, K=K, Q=Q, N=N, codebook=want))
     assert np.array_equal(idx.cpu().numpy(), ref["idx"])
     assert np.array_equal(bits(res.cpu().numpy()), bits(ref["residual"]))
+
+
+@pytest.mark.parametrize("recipe,cb_type,K,N,M,Q,topk", [
+    (0, 0, 512, 1024, 333, 2, 0), (1, 0, 512, 1024, 250, 2, 0), (1, 1, 512, 1024, 250, 2, 4),
+    (2, 0, 512, 512, 300, 3, 0), (1, 1, 64, 1024, 400, 3, 4), (1, 1, 768, 256, 200, 2, 2),
+    (1, 1, 64, 256, 1, 2, 0)])
+def test_other_widths_and_q8_widths(torch, ctx, oracle, recipe, cb_type, K, N, M, Q, topk):
+    """K = 512 (its own translation unit) for every recipe, and Q8_0
+    codebooks at K = 64 and 768, against the oracle."""
+    from aqmi import synth
+
+    print(f"[gpu] width K={K} recipe={recipe} cb_type={cb_type} topk={topk}", flush=True)
+    x = synth.normal(61, 1, (M, K), 1.0)
+    if cb_type == 1:
+        cb = np.stack([synth.q8_0_random_codebook(61, 10 + s, N, K) for s in range(Q)])
+        # queries near the dequantised codes keep the distances in the codebook's range
+        x = (synth.q8_0_dequantize(cb[0])[np.arange(M) % N] + synth.normal(61, 2, (M, K), 0.05)).astype(np.float32)
+        cfg = dict(x=x, M=M, K=K, Q=Q, N=N, codebook_q8=cb)
+    else:
+        cb = synth.normal(61, 3, (Q, N, K), 1.0 / 16)
+        cfg = dict(x=x, M=M, K=K, Q=Q, N=N, codebook=cb)
+    out = run(torch, ctx, cb, recipe, x, cb_type=cb_type, topk=topk)
+    ref = {0: oracle.euclid_rvq, 1: oracle.higgs_rvq, 2: oracle.direct_rvq}[recipe]
+    ref = ref(cfg, topk=topk) if recipe == 1 else ref(cfg)
+    assert np.array_equal(out["idx"], ref["idx"])
+    assert np.array_equal(bits(out["residual"]), bits(ref["residual"]))
+    if recipe == 0:
+        assert np.array_equal(bits(out["dist"]), bits(-ref["logit"]))
+    else:
+        assert np.array_equal(bits(out["dist"]), bits(ref["dist"]))
+    if topk:
+        check_topk(out, ref)
+
+
+def test_refine_capacity_overflow_goes_to_exact_scan(torch, ctx, oracle, monkeypatch):
+    """With the refine pass's key buffer capped at two frames (test hook
+    AQ_EUCLID_REFINE_KEY_FLOATS), every further frame the first certificate
+    leaves open must reach the exact scan without reading keys past the
+    buffer, and the results stay the reference's."""
+    import aqmi
+
+    print("[gpu] refine capacity overflow", flush=True)
+    cfg = mimi(4000, Q=2)
+    monkeypatch.setenv("AQ_EUCLID_REFINE_KEY_FLOATS", "2048")
+    out = run(torch, ctx, cfg["codebook"], aqmi.OMNIVOICE, cfg["x"])
+    scans = out["cbs"].exact_scans()
+    ref = oracle.euclid_rvq(cfg)
+    assert np.array_equal(out["idx"], ref["idx"])
+    assert np.array_equal(bits(out["residual"]), bits(ref["residual"]))
+    assert np.array_equal(bits(out["dist"]), bits(-ref["logit"]))
+    print(f"[gpu] open frames {out['fails'].tolist()}, exact scans {scans.tolist()}", flush=True)
+    assert (out["fails"] > 2).all() and (scans >= out["fails"] - 2).all()

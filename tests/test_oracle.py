@@ -580,3 +580,35 @@ def test_synth_q8_weight_rounding_matches_ggml(ref):
     want = np.zeros((16, 8), dtype=synth.Q8_DTYPE)
     ref.lib.aqref_quantize_chunk_q8_0(np.ascontiguousarray(w, np.float32), want.ctypes.data_as(__import__("ctypes").c_void_p), 16, 256)
     assert np.array_equal(got.view(np.uint8), want.view(np.uint8))
+
+
+@pytest.mark.parametrize("tag,kw,topk", [
+    ("higgs_f32", dict(recipe=1), 0), ("higgs_q8", dict(recipe=1, cb_q8=True, proj_q8=True), 4),
+    ("omnivoice_f32", dict(recipe=0), 0), ("omnivoice_q8proj", dict(recipe=0, proj_q8=True), 0)])
+def test_oracle_projected_matches_golden(o, tag, kw, topk):
+    """The projected cascades at the reference's shapes (1024 -> 64, 8 x 1024
+    codes, 400 frames) against fixtures the reference's graphs wrote."""
+    g = np.load(GOLDEN / f"projected_{tag}.npz")
+    cfg = synth.projected_config(400, **kw)
+    out = o.projected_rvq(cfg, topk=topk)
+    assert np.array_equal(out["idx"], g["idx"].astype(np.int32))
+    assert _sha(out["residual"]) == str(g["residual_sha"])
+    assert _sha(out["dist"]) == str(g["dist_sha"])
+    if topk:
+        ti, tl = _sorted_topk(out["topk_idx"], out["topk_logit"])
+        assert _sha(ti.astype(np.int32)) == str(g["topk_idx_sha"])
+        assert _sha(tl) == str(g["topk_logit_sha"])
+    assert _sha(o.projected_decode(cfg, out["idx"])) == str(g["decode_sha"])
+
+
+def test_oracle_qwen3_cascade_matches_golden(o):
+    """Qwen3's 1 + 15 stage DIRECT cascade over EMA codebooks, read
+    channel-major, against the reference's own quantize_projected."""
+    g = np.load(GOLDEN / "qwen3_cascade.npz")
+    cfg = synth.qwen3_config(g["idx"].shape[0])
+    assert np.array_equal(o.qwen3_quantize(cfg), g["idx"].astype(np.int32))
+
+
+def test_oracle_qwen3_vs_reference_function(o, ref):
+    cfg = synth.qwen3_config(25, seed=21)
+    assert np.array_equal(o.qwen3_quantize(cfg), ref.qwen3_quantize(cfg))
