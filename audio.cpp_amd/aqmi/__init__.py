@@ -31,7 +31,7 @@ EXPORTED = [
     "aq_codebook_gather", "aq_ema_codebook", "aq_euclid_upload_ema",
     "aq_euclid_decode", "aq_ctx_set_timing", "aq_ctx_read_timing",
     "aq_moss_upload", "aq_moss_release", "aq_moss_encode", "aq_moss_decode",
-    "aq_euclid_encode_strided", "aq_euclid_upload_projected",
+    "aq_euclid_encode_strided", "aq_euclid_upload_projected", "aq_euclid_encode_noalloc",
 ]
 
 # aq_euclid_recipe / aq_codebook_type
@@ -76,6 +76,7 @@ def load_library(path: str | pathlib.Path | None = None) -> C.CDLL:
     lib.aq_ema_codebook.argtypes = [vp, vp, vp, i64, i64, i64, C.c_float, vp]
     lib.aq_euclid_upload_ema.argtypes = [vp, i64, i64, i64, vp, vp, C.c_float, C.c_int, C.POINTER(vp)]
     lib.aq_euclid_decode.argtypes = [vp, vp, vp, i64, vp]
+    lib.aq_euclid_encode_noalloc.argtypes = [vp, vp, vp, i64, vp, vp, vp, C.c_int, vp, vp, vp]
     lib.aq_euclid_encode_strided.argtypes = [vp, vp, vp, i64, i64, i64, i64, i64, vp, vp, vp, C.c_int, vp, vp, vp]
     lib.aq_euclid_upload_projected.argtypes = [vp, i64, i64, i64, i64, C.c_int, vp, C.c_int, vp, vp, vp, vp,
                                                C.c_int, C.POINTER(vp)]
@@ -325,6 +326,14 @@ class Codebooks:
         self.ctx.check(self.ctx.lib.aq_euclid_encode(self.ctx.h, self.h, _dptr(x), x.shape[0], _dptr(idx),
                                                      _dptr(residual), _dptr(dist), topk, _dptr(topk_idx),
                                                      _dptr(topk_dist), _dptr(force_idx)))
+
+    def encode_noalloc(self, x, idx, residual=None, dist=None, topk: int = 0, topk_idx=None, topk_dist=None,
+                       force_idx=None):
+        """aq_euclid_encode_noalloc: the same encode without device allocation."""
+        self.ctx.use_current_stream()
+        self.ctx.check(self.ctx.lib.aq_euclid_encode_noalloc(self.ctx.h, self.h, _dptr(x), x.shape[0], _dptr(idx),
+                                                             _dptr(residual), _dptr(dist), topk, _dptr(topk_idx),
+                                                             _dptr(topk_dist), _dptr(force_idx)))
 
     def encode_strided(self, x, M: int, clip_len: int, clip_stride: int, frame_stride: int, chan_stride: int, idx,
                        residual=None, dist=None, topk: int = 0, topk_idx=None, topk_dist=None, force_idx=None):

@@ -9,6 +9,7 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <vector>
 
@@ -352,6 +353,60 @@ aq_status aq_euclid_release(aq_codebooks *cb) {
 
 namespace {
 
+// Work buffers of one encode: the context's growable buffers (base null), or
+// consecutive 256-byte aligned pieces of a fixed device region (the
+// no-allocation entry point).
+struct Arena {
+    aq_ctx *ctx;
+    unsigned char *base;
+    size_t cap, used;
+    aq_status get(int slot, size_t bytes, void **out) {
+        if (!base) return aq_ctx_scratch(ctx, slot, bytes, out);
+        const size_t off = (used + 255) & ~size_t{255};
+        if (off > cap || bytes > cap - off)
+            return aq_fail(ctx, AQ_E_SHAPE,
+                           "aq_euclid_encode_noalloc: the encode needs more than the %zu bytes of scratch "
+                           "(pass a residual buffer or encode fewer frames per call)", cap);
+        *out = base + off;
+        used = off + bytes;
+        return AQ_OK;
+    }
+    // bytes still free (for the growable buffers: unbounded)
+    size_t left() const {
+        if (!base) return ~size_t{0};
+        const size_t off = (used + 255) & ~size_t{255};
+        return off < cap ? cap - off : 0;
+    }
+};
+
+// Scratch of aq_euclid_encode_noalloc: every call on a device uses this one
+// region (the device holds it until the process ends), so calls that overlap
+// on one device race.  Host code never uses the name `scratch` as an
+// address: each device's address comes from hipGetSymbolAddress.
+constexpr size_t kNoAllocBytes = size_t{32} << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocBytes];
+constexpr int kNoAllocDevices = 64;
+std::mutex g_noalloc_mu;
+void *g_noalloc_ptr[kNoAllocDevices];
+
+// The device address of `scratch` on ctx's device (current when called),
+// looked up on the first call on that device.
+aq_status noalloc_region(aq_ctx *ctx, unsigned char **out) {
+    if (ctx->device < 0 || ctx->device >= kNoAllocDevices)
+        return aq_fail(ctx, AQ_E_UNSUPPORTED, "aq_euclid_encode_noalloc: device %d out of range", ctx->device);
+    std::lock_guard<std::mutex> lock(g_noalloc_mu);
+    if (!g_noalloc_ptr[ctx->device]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return aq_fail(ctx, AQ_E_DEVICE, "aq_euclid_encode_noalloc: hipGetSymbolAddress failed: %s",
+                           hipGetErrorString(e));
+        g_noalloc_ptr[ctx->device] = p;
+    }
+    *out = static_cast<unsigned char *>(g_noalloc_ptr[ctx->device]);
+    return AQ_OK;
+}
+
 // Encode M frames (strided input `in`) through every stage of cb.  Plain
 // codebooks: the residual cascade in codebook space, r -= c[code].
 // Projected codebooks: per stage p = project_in(r), the stage pipeline on p,
@@ -359,7 +414,7 @@ namespace {
 // projection.
 aq_status euclid_encode_impl(aq_ctx *ctx, const aq_codebooks *cb, const aq_frames_desc &in, int64_t M, int32_t *idx,
                              float *residual, float *dist, int topk, int32_t *topk_idx, float *topk_dist,
-                             const int32_t *force_idx) {
+                             const int32_t *force_idx, Arena arena) {
     if (!ctx || !cb || !idx || (!in.x && M > 0)) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_euclid_encode: null argument");
     if (cb->ctx->device != ctx->device)
         return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_euclid_encode: codebooks belong to another device");
@@ -406,19 +461,19 @@ aq_status euclid_encode_impl(aq_ctx *ctx, const aq_codebooks *cb, const aq_frame
     // and frame norms, and the per-stage failure lists.
     float *work = residual;
     if (!work) {
-        aq_status st = aq_ctx_scratch(ctx, 0, static_cast<size_t>(M) * H * sizeof(float), reinterpret_cast<void **>(&work));
+        aq_status st = arena.get(0, static_cast<size_t>(M) * H * sizeof(float), reinterpret_cast<void **>(&work));
         if (st != AQ_OK) return st;
     }
     float *pbuf = nullptr;
     if (pw) {
-        aq_status st = aq_ctx_scratch(ctx, 2, static_cast<size_t>(M) * K * sizeof(float), reinterpret_cast<void **>(&pbuf));
+        aq_status st = arena.get(2, static_cast<size_t>(M) * K * sizeof(float), reinterpret_cast<void **>(&pbuf));
         if (st != AQ_OK) return st;
     }
     float *keys = nullptr;
     {
         const size_t key_bytes = static_cast<size_t>(nsplit) * ngroups * topl * kWave * sizeof(float);
         void *w = nullptr;
-        aq_status st = aq_ctx_scratch(ctx, 4, key_bytes + 3 * static_cast<size_t>(M) * sizeof(float), &w);
+        aq_status st = arena.get(4, key_bytes + 3 * static_cast<size_t>(M) * sizeof(float), &w);
         if (st != AQ_OK) return st;
         keys = static_cast<float *>(w);
     }
@@ -427,10 +482,11 @@ aq_status euclid_encode_impl(aq_ctx *ctx, const aq_codebooks *cb, const aq_frame
     // frame lists.
     int32_t *fails = nullptr;
     {
-        aq_status st = aq_ctx_scratch(ctx, 1, (2 * static_cast<size_t>(M) + 128) * sizeof(int32_t),
-                                      reinterpret_cast<void **>(&fails));
+        aq_status st = arena.get(1, (2 * static_cast<size_t>(M) + 128) * sizeof(int32_t),
+                                 reinterpret_cast<void **>(&fails));
         if (st != AQ_OK) return st;
     }
+    ctx->euclid_counts = fails;   // read by aq_euclid_failures / aq_euclid_exact_scans
     int32_t *counts = fails;
     int32_t *counts2 = fails + 64;
     int32_t *list = fails + 128;
@@ -451,9 +507,11 @@ aq_status euclid_encode_impl(aq_ctx *ctx, const aq_codebooks *cb, const aq_frame
             const long long v = std::atoll(cap);
             if (v > 0) floats = std::min<int64_t>(floats, v);
         }
+        // in a fixed region, whatever is left after the other buffers
+        floats = std::min<int64_t>(floats, static_cast<int64_t>(std::min<size_t>(arena.left() / 4, size_t{1} << 40)));
         floats = std::max(floats, per_small);
         void *w = nullptr;
-        aq_status st = aq_ctx_scratch(ctx, 3, static_cast<size_t>(floats) * 4, &w);
+        aq_status st = arena.get(3, static_cast<size_t>(floats) * 4, &w);
         if (st != AQ_OK) return st;
         rf.keys = static_cast<float *>(w);
         rf.key_floats = floats;
@@ -502,7 +560,7 @@ aq_status euclid_encode_impl(aq_ctx *ctx, const aq_codebooks *cb, const aq_frame
         a.norms = keys + static_cast<size_t>(nsplit) * ngroups * topl * kWave;
         a.nsplit = nsplit;
         if (s >= 64 && s % 64 == 0) AQ_HIP(ctx, hipMemsetAsync(counts, 0, sizeof(int32_t) * 128, ctx->stream));
-        const int tslot = aq_timing_start(ctx);
+        const int tslot = arena.base ? -1 : aq_timing_start(ctx);   // events are not created without allocation
         hipLaunchKernelGGL(sweep, dim3(static_cast<unsigned>((tiles + 7) / 8 * 8 * nsplit)), dim3(kThreads), lds,
                            ctx->stream, a);
         aq_timing_stop(ctx, tslot);
@@ -582,7 +640,20 @@ aq_status aq_euclid_encode(aq_ctx *ctx, const aq_codebooks *cb, const float *x, 
     if (!cb) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_euclid_encode: null argument");
     const int64_t H = cb->proj ? cb->proj->H : cb->K;
     return euclid_encode_impl(ctx, cb, aq_frames_row_major(x, M, H), M, idx, residual, dist, topk, topk_idx, topk_dist,
-                              force_idx);
+                              force_idx, Arena{ctx, nullptr, 0, 0});
+}
+
+aq_status aq_euclid_encode_noalloc(aq_ctx *ctx, const aq_codebooks *cb, const float *x, int64_t M, int32_t *idx,
+                                   float *residual, float *dist, int topk, int32_t *topk_idx, float *topk_dist,
+                                   const int32_t *force_idx) {
+    if (!ctx || !cb) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_euclid_encode_noalloc: null argument");
+    aq_device_guard g(ctx->device);
+    unsigned char *base = nullptr;
+    const aq_status st = noalloc_region(ctx, &base);
+    if (st != AQ_OK) return st;
+    const int64_t H = cb->proj ? cb->proj->H : cb->K;
+    return euclid_encode_impl(ctx, cb, aq_frames_row_major(x, M, H), M, idx, residual, dist, topk, topk_idx, topk_dist,
+                              force_idx, Arena{ctx, base, kNoAllocBytes, 0});
 }
 
 aq_status aq_euclid_encode_strided(aq_ctx *ctx, const aq_codebooks *cb, const float *x, int64_t M, int64_t clip_len,
@@ -590,14 +661,13 @@ aq_status aq_euclid_encode_strided(aq_ctx *ctx, const aq_codebooks *cb, const fl
                                    float *residual, float *dist, int topk, int32_t *topk_idx, float *topk_dist,
                                    const int32_t *force_idx) {
     return euclid_encode_impl(ctx, cb, aq_frames_desc{x, clip_len, clip_stride, frame_stride, chan_stride}, M, idx,
-                              residual, dist, topk, topk_idx, topk_dist, force_idx);
+                              residual, dist, topk, topk_idx, topk_dist, force_idx, Arena{ctx, nullptr, 0, 0});
 }
 
 aq_status aq_euclid_failures(aq_ctx *ctx, const aq_codebooks *cb, int32_t *host_counts) {
     if (!ctx || !cb || !host_counts) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_euclid_failures: null argument");
-    int32_t *fails = nullptr;
-    aq_status st = aq_ctx_scratch(ctx, 1, 0, reinterpret_cast<void **>(&fails));
-    if (st != AQ_OK || !fails) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_euclid_failures: no encode has run");
+    int32_t *fails = ctx->euclid_counts;
+    if (!fails) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_euclid_failures: no encode has run");
     aq_device_guard g(ctx->device);
     const int64_t n = std::min<int64_t>(cb->Q, 64);
     AQ_HIP(ctx, hipMemcpyAsync(host_counts, fails, sizeof(int32_t) * n, hipMemcpyDeviceToHost, ctx->stream));
@@ -607,9 +677,8 @@ aq_status aq_euclid_failures(aq_ctx *ctx, const aq_codebooks *cb, int32_t *host_
 
 aq_status aq_euclid_exact_scans(aq_ctx *ctx, const aq_codebooks *cb, int32_t *host_counts) {
     if (!ctx || !cb || !host_counts) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_euclid_exact_scans: null argument");
-    int32_t *fails = nullptr;
-    aq_status st = aq_ctx_scratch(ctx, 1, 0, reinterpret_cast<void **>(&fails));
-    if (st != AQ_OK || !fails) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_euclid_exact_scans: no encode has run");
+    int32_t *fails = ctx->euclid_counts;
+    if (!fails) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_euclid_exact_scans: no encode has run");
     aq_device_guard g(ctx->device);
     const int64_t n = std::min<int64_t>(cb->Q, 64);
     AQ_HIP(ctx, hipMemcpyAsync(host_counts, fails + 64, sizeof(int32_t) * n, hipMemcpyDeviceToHost, ctx->stream));

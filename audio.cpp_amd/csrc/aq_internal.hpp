@@ -18,9 +18,12 @@ struct aq_ctx {
     int32_t *d_flags = nullptr;   // device status words written by kernels (vector stores only)
     int num_cus = 0;
     // Work buffers owned by the context, grown on demand (slot 0: residual
-    // cascade, 1: per-stage failure counters and lists, 3: refine-pass keys,
-    // 4: sweep keys and frame norms; 2 and 5 unused).
+    // cascade, 1: per-stage failure counters and lists, 2: projected queries,
+    // 3: refine-pass keys, 4: sweep keys and frame norms; 5 unused).
     static constexpr int kScratchSlots = 6;
+    // Per-stage counters of the last Euclidean encode on this context (in
+    // slot 1, or in the no-allocation scratch).
+    int32_t *euclid_counts = nullptr;
     void *scratch[kScratchSlots] = {};
     size_t scratch_bytes[kScratchSlots] = {};
     // Kernel timing (aq_ctx_set_timing): event pairs around each main kernel.

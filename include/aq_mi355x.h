@@ -237,6 +237,23 @@ aq_status aq_euclid_encode(aq_ctx *ctx, const aq_codebooks *cb, const float *x, 
                            float *residual, float *dist, int topk, int32_t *topk_idx, float *topk_dist,
                            const int32_t *force_idx);
 
+/* aq_euclid_encode without any device allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  The work
+ * buffers (the residual when `residual` is NULL, sweep keys, frame lists,
+ * refine keys, projected queries) live in one 32 MiB device region that the
+ * library holds on each device it runs on until the process ends; refine
+ * keys get what the other buffers leave (frames past that go to the exact
+ * scan, same results).  A call that needs more of the region fails with
+ * AQ_E_SHAPE (e.g. a 48 000 x 256 Mimi batch needs a caller residual buffer).
+ * Every call on a device shares the region: calls that overlap on one device
+ * race.  The counters of aq_euclid_failures / aq_euclid_exact_scans refer to
+ * the region until the next encode on the context.  Results equal
+ * aq_euclid_encode's. */
+aq_status aq_euclid_encode_noalloc(aq_ctx *ctx, const aq_codebooks *cb, const float *x, int64_t M, int32_t *idx,
+                                   float *residual, float *dist, int topk, int32_t *topk_idx, float *topk_dist,
+                                   const int32_t *force_idx);
+
 /* aq_euclid_encode on a strided input, e.g. the channel-major [B, C, T]
  * latent of a ggml encoder graph (qwen3_tts/tokenizer_speech_encoder.cpp:
  * 330-335 reads it that way; outetts/dac.cpp:565-571 and
