@@ -32,6 +32,7 @@ EXPORTED = [
     "aq_euclid_decode", "aq_ctx_set_timing", "aq_ctx_read_timing",
     "aq_moss_upload", "aq_moss_release", "aq_moss_encode", "aq_moss_decode",
     "aq_euclid_encode_strided", "aq_euclid_upload_projected", "aq_euclid_encode_noalloc",
+    "aq_dac_encode_ex", "aq_dac_decode_ex",
 ]
 
 # aq_euclid_recipe / aq_codebook_type
@@ -65,6 +66,8 @@ def load_library(path: str | pathlib.Path | None = None) -> C.CDLL:
     lib.aq_dac_release.argtypes = [vp]
     lib.aq_dac_encode.argtypes = [vp, vp, vp, i64, i64, vp, vp, vp, vp]
     lib.aq_dac_decode.argtypes = [vp, vp, vp, i64, vp]
+    lib.aq_dac_encode_ex.argtypes = [vp, vp, vp, i64, i64, i64, i64, i64, vp, i64, vp, vp, C.c_int, vp]
+    lib.aq_dac_decode_ex.argtypes = [vp, vp, vp, i64, i64, vp, C.c_int]
     lib.aq_ctx_set_timing.argtypes = [vp, C.c_int]
     lib.aq_ctx_read_timing.argtypes = [vp, vp, C.c_int, C.POINTER(C.c_int)]
     lib.aq_euclid_upload.argtypes = [vp, i64, i64, i64, C.c_int, vp, C.c_int, C.POINTER(vp)]
@@ -186,6 +189,21 @@ class DacStages:
     def decode(self, idx, out):
         self.ctx.use_current_stream()
         self.ctx.check(self.ctx.lib.aq_dac_decode(self.ctx.h, self.h, _dptr(idx), idx.shape[0], _dptr(out)))
+
+    def encode_ex(self, x, M: int, clip_len: int, strides, idx_ptr: int, idx_ld: int, residual=None, recon=None,
+                  recon_accumulate: bool = False, force_ptr: int | None = None):
+        """aq_dac_encode_ex: strides = (clip_stride, frame_stride, chan_stride)
+        in floats; idx_ptr / force_ptr are device addresses of the first code
+        of this stage set (row stride idx_ld)."""
+        self.ctx.use_current_stream()
+        self.ctx.check(self.ctx.lib.aq_dac_encode_ex(self.ctx.h, self.h, x.data_ptr(), M, clip_len, *strides, idx_ptr,
+                                                     idx_ld, _dptr(residual), _dptr(recon),
+                                                     1 if recon_accumulate else 0, force_ptr))
+
+    def decode_ex(self, idx_ptr: int, idx_ld: int, M: int, out, accumulate: bool = False):
+        self.ctx.use_current_stream()
+        self.ctx.check(self.ctx.lib.aq_dac_decode_ex(self.ctx.h, self.h, idx_ptr, idx_ld, M, _dptr(out),
+                                                     1 if accumulate else 0))
 
     def close(self):
         if getattr(self, "h", None):

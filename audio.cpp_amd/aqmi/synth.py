@@ -270,6 +270,20 @@ def projected_config(M: int, recipe: int = 1, seed: int = 13, H: int = 1024, K: 
     return cfg
 
 
+def fish_config(B: int, T: int, seed: int = 15, D: int = 1024, N0: int = 4096, N: int = 1024, Qr: int = 8,
+                bias: bool = True) -> dict:
+    """The Fish Audio quantizer cascade (fish_audio/codec.cpp:570-611): a
+    semantic stage of N0 = 4096 codes, then Qr residual stages of N = 1024
+    codes, all dim 8, latent dim D; DAC-style weights (dac_weights) with the
+    semantic codebook [N0, 8] ~N(0,1) drawn separately."""
+    Q = 1 + Qr
+    w = dac_weights(seed, Q, D, N, bias=bias)
+    cb0 = normal(seed, 7, (N0, DAC_DIM), 1.0)
+    return dict(kind="fish", seed=seed, B=B, T=T, D=D, Q=Q, N0=N0, N=N, x=normal(seed, 1, (B * T, D)),
+                w_in=w["w_in"], b_in=w["b_in"], codebook0=cb0, codebook=np.ascontiguousarray(w["codebook"][1:]),
+                w_out=w["w_out"], b_out=w["b_out"])
+
+
 def qwen3_config(frames: int, seed: int = 14, S: int = 16, N: int = 2048, K: int = 256) -> dict:
     """Qwen3-TTS speech-tokenizer quantizer inputs (tokenizer_speech_encoder.cpp
     shapes: 1 semantic + 15 acoustic EMA codebooks of 2048 x 256): the

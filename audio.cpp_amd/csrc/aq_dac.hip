@@ -46,6 +46,7 @@
 //    a coalesced 4*D-byte row read from L2/MALL instead of 2*8*D flops.
 #include "aq_device_math.hpp"
 #include "aq_internal.hpp"
+#include "aq_projected.hpp"
 
 #include <algorithm>
 #include <cmath>
@@ -231,7 +232,9 @@ __global__ __launch_bounds__(kMaxBlock, 1) void dac_encode_kernel(
     const float *__restrict__ x, int64_t M, int Q, int N, const float4 *__restrict__ images, int64_t stride_f4,
     int64_t img_f4, const float *__restrict__ tables, int32_t *__restrict__ idx, float *__restrict__ residual,
     float *__restrict__ recon, const int32_t *__restrict__ force_idx, int32_t *__restrict__ flags, int has_bin,
-    int key_bits, float margin, int exact_only, float qeps, int64_t dbuf_f4) {
+    int key_bits, float margin, int exact_only, float qeps, int64_t dbuf_f4, int ld, int recon_acc) {
+    // ld: row stride of idx and force_idx; recon_acc: recon holds the sum of
+    // earlier stages' z (another stage set's), which this cascade adds to.
     // stride_f4: float4 per stage image; img_f4: the prefix staged in LDS
     // (the whole image, or W_in + b_in when CBG reads c_hat from memory).
     extern __shared__ float4 lds[];
@@ -253,6 +256,7 @@ __global__ __launch_bounds__(kMaxBlock, 1) void dac_encode_kernel(
         for (int i = 0; i < DI; ++i) {
             r[f][i] = x[mrow[f] * D + i * kWave + lane];
             rc[f][i] = -0.0f;   // -0 + z == z exactly, for every z
+            if (RECON && recon_acc) rc[f][i] = recon[mrow[f] * D + i * kWave + lane];
         }
     }
 
@@ -509,10 +513,10 @@ __global__ __launch_bounds__(kMaxBlock, 1) void dac_encode_kernel(
         int use[FW];
 #pragma unroll
         for (int f = 0; f < FW; ++f) {
-            if (lane == 0 && active[f]) idx[mrow[f] * Q + s] = code[f];
+            if (lane == 0 && active[f]) idx[mrow[f] * ld + s] = code[f];
             use[f] = code[f];
             if (force_idx) {
-                use[f] = force_idx[mrow[f] * Q + s];
+                use[f] = force_idx[mrow[f] * ld + s];
                 if (use[f] < 0 || use[f] >= N) {
                     if (lane == 0) flags[AQ_FLAG_BAD_INDEX] = 1;
                     use[f] = 0;
@@ -568,28 +572,30 @@ __global__ void dac_table_kernel(const float *__restrict__ cb, const float *__re
 }
 
 // recon[m][d] = sum over stages of z[s][idx[m][s]][d] (decode recipe).
-__global__ void dac_decode_kernel(const int32_t *__restrict__ idx, int64_t M, int Q, int64_t N, int64_t D,
+// (accumulate: out already holds the sum of earlier stages, which the z of
+// these stages are added to in order.)
+__global__ void dac_decode_kernel(const int32_t *__restrict__ idx, int64_t ld, int64_t M, int Q, int64_t N, int64_t D,
                                   const float *__restrict__ tables, float *__restrict__ out,
-                                  int32_t *__restrict__ flags) {
+                                  int32_t *__restrict__ flags, int accumulate) {
     const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (t >= M * D) return;
     const int64_t m = t / D;
     const int64_t d = t % D;
-    float acc = 0.0f;
+    float acc = accumulate ? out[t] : 0.0f;
     for (int s = 0; s < Q; ++s) {
-        int32_t code = idx[m * Q + s];
+        int32_t code = idx[m * ld + s];
         if (code < 0 || code >= N) {
             flags[AQ_FLAG_BAD_INDEX] = 1;
             code = 0;
         }
         const float z = tables[(static_cast<int64_t>(s) * N + code) * D + d];
-        acc = (s == 0) ? z : __fadd_rn(acc, z);
+        acc = (s == 0 && !accumulate) ? z : __fadd_rn(acc, z);
     }
     out[t] = acc;
 }
 
 using EncodeFn = void (*)(const float *, int64_t, int, int, const float4 *, int64_t, int64_t, const float *, int32_t *,
-                          float *, float *, const int32_t *, int32_t *, int, int, float, int, float, int64_t);
+                          float *, float *, const int32_t *, int32_t *, int, int, float, int, float, int64_t, int, int);
 
 constexpr int kPrefetch = 12;   // float4 per thread in the prefetching variant
 
@@ -961,16 +967,43 @@ aq_status aq_dac_release(aq_dac_stages *st) {
 
 aq_status aq_dac_encode(aq_ctx *ctx, const aq_dac_stages *st, const float *x, int64_t M, int64_t clip_len,
                         int32_t *idx, float *residual, float *recon, const int32_t *force_idx) {
+    const int64_t D = st ? st->D : 0;
+    return aq_dac_encode_ex(ctx, st, x, M, clip_len, clip_len * D, D, 1, idx, st ? st->Q : 0, residual, recon, 0,
+                            force_idx);
+}
+
+aq_status aq_dac_encode_ex(aq_ctx *ctx, const aq_dac_stages *st, const float *x, int64_t M, int64_t clip_len,
+                           int64_t clip_stride, int64_t frame_stride, int64_t chan_stride, int32_t *idx,
+                           int64_t idx_ld, float *residual, float *recon, int recon_accumulate,
+                           const int32_t *force_idx) {
     if (!ctx || !st || !idx || (!x && M > 0)) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_dac_encode: null argument");
     if (st->ctx->device != ctx->device) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_dac_encode: stages belong to another device");
     if (M < 0 || clip_len <= 0 || M % clip_len != 0)
         return aq_fail(ctx, AQ_E_SHAPE, "aq_dac_encode: M=%lld must be a non-negative multiple of clip_len=%lld",
                        (long long)M, (long long)clip_len);
+    if (idx_ld < st->Q || idx_ld > (int64_t{1} << 20))
+        return aq_fail(ctx, AQ_E_SHAPE, "aq_dac_encode: idx_ld=%lld must be at least Q=%lld", (long long)idx_ld,
+                       (long long)st->Q);
+    if (recon_accumulate && !recon)
+        return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_dac_encode: recon_accumulate needs a recon buffer");
     if (M == 0) return AQ_OK;
+    // A strided input (e.g. the encoder's channel-major [B, D, T] latent) is
+    // gathered into frame-major rows first.
+    if (!(frame_stride == st->D && chan_stride == 1 && clip_stride == clip_len * st->D)) {
+        aq_device_guard g(ctx->device);
+        float *rows = nullptr;
+        aq_status gs = aq_ctx_scratch(ctx, 5, static_cast<size_t>(M) * st->D * sizeof(float), reinterpret_cast<void **>(&rows));
+        if (gs != AQ_OK) return gs;
+        gs = aq_gather_frames(ctx, aq_frames_desc{x, clip_len, clip_stride, frame_stride, chan_stride}, M, st->D, rows);
+        if (gs != AQ_OK) return gs;
+        x = rows;
+    }
     if (st->recipe == AQ_DAC_OUTETTS) {
         if (recon)
             return aq_fail(ctx, AQ_E_INVALID_ARG,
                            "aq_dac_encode: the OuteTTS recipe gives no recon (aq_dac_decode of the codes does)");
+        if (idx_ld != st->Q)
+            return aq_fail(ctx, AQ_E_UNSUPPORTED, "aq_dac_encode: the OuteTTS recipe writes codes [M, Q] (idx_ld = Q)");
         aq_device_guard g(ctx->device);
         if (force_idx) AQ_HIP(ctx, hipMemsetAsync(ctx->d_flags, 0, sizeof(int32_t) * AQ_FLAG_COUNT, ctx->stream));
         aq_outetts_args a = st->ot;
@@ -1027,7 +1060,7 @@ aq_status aq_dac_encode(aq_ctx *ctx, const aq_dac_stages *st, const float *x, in
                        static_cast<int>(st->N), order == 1 ? st->d_images_tb : st->d_images, st->img_f4, st->lds_f4,
                        st->d_tables, idx, residual, recon,
                        force_idx, ctx->d_flags, st->has_bin ? 1 : 0, st->key_bits, st->margin, st->exact_only ? 1 : 0,
-                       st->qeps, dbuf_f4);
+                       st->qeps, dbuf_f4, static_cast<int>(idx_ld), recon_accumulate ? 1 : 0);
     aq_timing_stop(ctx, tslot);
     AQ_HIP(ctx, hipGetLastError());
     if (force_idx) {
@@ -1040,15 +1073,22 @@ aq_status aq_dac_encode(aq_ctx *ctx, const aq_dac_stages *st, const float *x, in
 }
 
 aq_status aq_dac_decode(aq_ctx *ctx, const aq_dac_stages *st, const int32_t *idx, int64_t M, float *out) {
+    return aq_dac_decode_ex(ctx, st, idx, st ? st->Q : 0, M, out, 0);
+}
+
+aq_status aq_dac_decode_ex(aq_ctx *ctx, const aq_dac_stages *st, const int32_t *idx, int64_t idx_ld, int64_t M,
+                           float *out, int accumulate) {
     if (!ctx || !st || (M > 0 && (!idx || !out))) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_dac_decode: null argument");
     if (M < 0) return aq_fail(ctx, AQ_E_SHAPE, "aq_dac_decode: negative M");
+    if (idx_ld < st->Q) return aq_fail(ctx, AQ_E_SHAPE, "aq_dac_decode: idx_ld must be at least Q");
     if (M == 0) return AQ_OK;
     if (!st->d_tables) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_dac_decode: no out-projection was uploaded");
     aq_device_guard g(ctx->device);
     AQ_HIP(ctx, hipMemsetAsync(ctx->d_flags, 0, sizeof(int32_t) * AQ_FLAG_COUNT, ctx->stream));
     const int64_t total = M * st->D;
     hipLaunchKernelGGL(dac_decode_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, ctx->stream, idx,
-                       M, static_cast<int>(st->Q), st->N, st->D, st->d_tables, out, ctx->d_flags);
+                       idx_ld, M, static_cast<int>(st->Q), st->N, st->D, st->d_tables, out, ctx->d_flags,
+                       accumulate ? 1 : 0);
     AQ_HIP(ctx, hipGetLastError());
     int32_t flag = 0;
     AQ_HIP(ctx, hipMemcpyAsync(&flag, ctx->d_flags + AQ_FLAG_BAD_INDEX, sizeof(int32_t), hipMemcpyDeviceToHost, ctx->stream));

@@ -170,12 +170,36 @@ aq_status aq_dac_encode(aq_ctx *ctx, const aq_dac_stages *stages, const float *x
                         int64_t clip_len, int32_t *idx, float *residual, float *recon,
                         const int32_t *force_idx);
 
+/* aq_dac_encode with a strided input, a row stride for the codes and a
+ * recon that continues an earlier cascade.  For a cascade whose stages do
+ * not share one codebook size, such as Fish's semantic quantizer of 4096
+ * codes followed by residual quantizers of 1024 (fish_audio/codec.cpp:
+ * 606-608), upload each group as its own stages object and chain them:
+ *   encode_ex(semantic, x, ..., idx, idx_ld = Q_total, residual = r, recon, 0)
+ *   encode_ex(rest, r, ..., idx + 1, idx_ld = Q_total, residual, recon, 1)
+ * gives the codes, residual and recon (the decoder's sum z_0 + z_1 + ...,
+ * codec.cpp:552-568) of the single cascade, bit for bit.
+ *   x            frame m, channel d at x + (m / clip_len) * clip_stride +
+ *                (m % clip_len) * frame_stride + d * chan_stride (channel-major
+ *                [B, D, T]: clip_stride = D*T, frame_stride = 1, chan_stride = T)
+ *   idx_ld       row stride of idx and force_idx (>= Q); codes at idx[m*idx_ld + s]
+ *   recon_accumulate  nonzero: recon holds the sum of earlier stages on entry
+ * The OuteTTS recipe takes idx_ld = Q and no recon. */
+aq_status aq_dac_encode_ex(aq_ctx *ctx, const aq_dac_stages *stages, const float *x, int64_t M, int64_t clip_len,
+                           int64_t clip_stride, int64_t frame_stride, int64_t chan_stride, int32_t *idx,
+                           int64_t idx_ld, float *residual, float *recon, int recon_accumulate,
+                           const int32_t *force_idx);
+
 /* Decode: recon[m] = sum_s (W_out[s] c[s][idx[m, s]] + b_out[s])
  * (build_decode_quantizer, codec.cpp:552-568).  idx device [M, Q], out device
  * [M, D].  Out-of-range codes -> AQ_E_INDEX_RANGE (checked on device; the call
  * synchronises the stream to report it). */
 aq_status aq_dac_decode(aq_ctx *ctx, const aq_dac_stages *stages, const int32_t *idx, int64_t M,
                         float *out);
+/* aq_dac_decode with codes at idx[m*idx_ld + s]; accumulate nonzero adds the
+ * stages' z to what out holds (the decode of a chained cascade, as above). */
+aq_status aq_dac_decode_ex(aq_ctx *ctx, const aq_dac_stages *stages, const int32_t *idx, int64_t idx_ld, int64_t M,
+                           float *out, int accumulate);
 
 /* ---- Euclidean VQ / RVQ (Mimi-style codecs, k-means tokenisers) ------------
  *

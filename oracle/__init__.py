@@ -106,6 +106,8 @@ class Oracle:
         L.aqo_moss_normalize_rows.argtypes = [_f32p, _i64, _i64, _f32p]
         L.aqo_moss_rvq.argtypes = [_f32p, _i64, _i64, _i64, _i64, _i64, _f32p, _f32p, _f32p, _f32p, _f32p,
                                    _f32p, _f32p, C.c_void_p, _i32p, C.c_void_p]
+        L.aqo_dac_rvq_mixed.argtypes = [_f32p, _i64, _i64, _i64, _i64, _i64, _i64, _f32p, C.c_void_p, _f32p, _f32p,
+                                        _f32p, C.c_void_p, C.c_void_p, _i32p, _f32p, _f32p]
         L.aqo_projected_rvq.argtypes = [_f32p, _i64, _i64, _i64, _i64, _i64, C.c_int, C.c_void_p, C.c_int,
                                         C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int,
                                         C.c_void_p, _i32p, _f32p, C.c_void_p, C.c_void_p, C.c_void_p]
@@ -133,6 +135,24 @@ class Oracle:
                                      None if rec is None else rec.ctypes.data_as(C.c_void_p), recipe)
         if rc == -2:
             raise ValueError("the recipe rejects a zero codebook row")
+        assert rc == 0
+        return dict(idx=idx, residual=res, recon=rec)
+
+    def dac_rvq_mixed(self, cfg: dict, force_idx=None):
+        """The Fish cascade with a semantic stage of N0 codes (fish_config)."""
+        x = np.ascontiguousarray(cfg["x"], np.float32)
+        M, D = x.shape
+        Q = cfg["Q"]
+        idx = np.zeros((M, Q), np.int32)
+        res = np.zeros((M, D), np.float32)
+        rec = np.zeros((M, D), np.float32)
+        fi = np.ascontiguousarray(force_idx, np.int32) if force_idx is not None else None
+        rc = self.lib.aqo_dac_rvq_mixed(x, M // cfg["T"], cfg["T"], D, Q, cfg["N0"], cfg["N"],
+                                        np.ascontiguousarray(cfg["w_in"], np.float32), _opt(cfg.get("b_in"), np.float32),
+                                        np.ascontiguousarray(cfg["codebook0"], np.float32),
+                                        np.ascontiguousarray(cfg["codebook"], np.float32),
+                                        np.ascontiguousarray(cfg["w_out"], np.float32), _opt(cfg.get("b_out"), np.float32),
+                                        None if fi is None else fi.ctypes.data_as(C.c_void_p), idx, res, rec)
         assert rc == 0
         return dict(idx=idx, residual=res, recon=rec)
 
@@ -371,6 +391,9 @@ class Ref:
         L.aqref_higgs_rvq.restype = C.c_double
         L.aqref_higgs_rvq.argtypes = [_f32p, _i64, _i64, _i64, _i64, C.c_void_p, C.c_int, C.c_int,
                                       _i32p, _f32p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int]
+        L.aqref_dac_rvq_mixed.restype = C.c_double
+        L.aqref_dac_rvq_mixed.argtypes = [_f32p, _i64, _i64, _i64, _i64, _i64, _i64, _f32p, C.c_void_p, _f32p, _f32p,
+                                          _f32p, C.c_void_p, _i32p, _f32p, _f32p, C.c_int]
         L.aqref_projected_rvq.restype = C.c_double
         L.aqref_projected_rvq.argtypes = [_f32p, _i64, _i64, _i64, _i64, _i64, C.c_int, C.c_void_p, C.c_int,
                                           C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int,
@@ -471,6 +494,22 @@ class Ref:
                                        1 if materialize else 0, recipe)
         if ms < 0:
             raise ValueError("the recipe rejects a zero codebook row")
+        return dict(idx=idx, residual=res, recon=rec, ms=ms)
+
+    def dac_rvq_mixed(self, cfg: dict, threads: int = 8):
+        x = np.ascontiguousarray(cfg["x"], np.float32)
+        M, D = x.shape
+        Q = cfg["Q"]
+        idx = np.zeros((M, Q), np.int32)
+        res = np.zeros((M, D), np.float32)
+        rec = np.zeros((M, D), np.float32)
+        ms = self.lib.aqref_dac_rvq_mixed(x, M // cfg["T"], cfg["T"], D, Q, cfg["N0"], cfg["N"],
+                                          np.ascontiguousarray(cfg["w_in"], np.float32),
+                                          _opt(cfg.get("b_in"), np.float32),
+                                          np.ascontiguousarray(cfg["codebook0"], np.float32),
+                                          np.ascontiguousarray(cfg["codebook"], np.float32),
+                                          np.ascontiguousarray(cfg["w_out"], np.float32),
+                                          _opt(cfg.get("b_out"), np.float32), idx, res, rec, threads)
         return dict(idx=idx, residual=res, recon=rec, ms=ms)
 
     def euclid_rvq(self, cfg: dict, threads: int = 8):

@@ -261,64 +261,92 @@ static float dot_f32(int64_t m_rows, int64_t n_rows, int k, const float *src0_ro
  * 110-115: no bias), 2 Vevo2 (l2_normalized_rows components.cpp:566-590:
  * zero rows rejected; build_l2_normalized_rows 848-863: +1e-20).  Returns -2
  * when the recipe rejects the codebook. */
+/* One stage of the cascade on the residual r [M, D] (codes into
+ * idx[m * ld + s]; recon[m] = z when first, else recon[m] + z). */
+static int dac_stage(float *r, int64_t M, int64_t T, int64_t D, int64_t N, const float *Wi, const float *bi,
+                     const float *C, const float *Wo, const float *bo, const int32_t *force_idx, int32_t *idx,
+                     int64_t ld, int64_t s, float *recon, int first, int recipe) {
+    float *cbn = (float *)malloc((size_t)(N * 8) * sizeof(float));
+    float *scores = (float *)malloc((size_t)N * sizeof(float));
+    if (!cbn || !scores) { free(cbn); free(scores); return -1; }
+    const int inproj_tiny = aqo_mul_mat_f32_uses_tinyblas(T, 8, D);
+    for (int64_t n = 0; n < N; ++n) {
+        double sum = 0.0;
+        for (int k = 0; k < 8; ++k) sum += (double)C[n * 8 + k] * (double)C[n * 8 + k];
+        float inv;
+        if (recipe == 1) {
+            inv = 1.0f / (float)sqrt(sum);
+        } else if (recipe == 2) {
+            const double norm = sqrt(sum);
+            if (norm == 0.0) { free(cbn); free(scores); return -2; }
+            inv = (float)(1.0 / norm);
+        } else {
+            inv = sum > 0.0 ? (float)(1.0 / sqrt(sum)) : 0.0f;
+        }
+        for (int k = 0; k < 8; ++k) cbn[n * 8 + k] = C[n * 8 + k] * inv;
+    }
+    for (int64_t m = 0; m < M; ++m) {
+        float *rm = r + m * D;
+        float p[8], pn[8], sq[8];
+        for (int j = 0; j < 8; ++j) {
+            p[j] = inproj_tiny ? aqo_tinyblas_dot_f32((int)D, rm, Wi + j * D) : aqo_vec_dot_f32((int)D, rm, Wi + j * D);
+            if (bi) p[j] = p[j] + bi[j];
+        }
+        for (int j = 0; j < 8; ++j) sq[j] = p[j] * p[j];
+        float ss = aqo_sum_f32(8, sq);
+        if (recipe != 1) ss = fmaf(ss, 1.0f, recipe == 2 ? 1.0e-20f : 1.0e-12f);   /* ggml_scale_bias, vec.h:708-710 */
+        const float den = sqrtf(ss);
+        for (int j = 0; j < 8; ++j) pn[j] = p[j] / den;
+        for (int64_t n = 0; n < N; ++n) scores[n] = aqo_vec_dot_f32(8, cbn + n * 8, pn);
+        const int code = aqo_argmax_f32((int)N, scores);
+        idx[m * ld + s] = code;
+        const int use = force_idx ? force_idx[m * ld + s] : code;
+        const float *q = C + (int64_t)use * 8;
+        if (!Wo) continue;   /* codes only (no out-projection given) */
+        for (int64_t d = 0; d < D; ++d) {
+            float z = aqo_vec_dot_f32(8, q, Wo + d * 8);
+            if (bo) z = z + bo[d];
+            rm[d] = rm[d] - z;
+            if (recon) recon[m * D + d] = first ? z : recon[m * D + d] + z;
+        }
+    }
+    free(cbn);
+    free(scores);
+    return 0;
+}
+
 int aqo_dac_rvq_ex(const float *x, int64_t B, int64_t T, int64_t D, int64_t Q, int64_t N,
                    const float *w_in, const float *b_in, const float *cb,
                    const float *w_out, const float *b_out, const int32_t *force_idx,
                    int32_t *idx, float *residual, float *recon, int recipe) {
     const int64_t M = B * T;
-    float *r = residual;
-    memcpy(r, x, (size_t)(M * D) * sizeof(float));
-    float *cbn = (float *)malloc((size_t)(N * 8) * sizeof(float));
-    float *scores = (float *)malloc((size_t)N * sizeof(float));
-    if (!cbn || !scores) { free(cbn); free(scores); return -1; }
-    const int inproj_tiny = aqo_mul_mat_f32_uses_tinyblas(T, 8, D);
+    memcpy(residual, x, (size_t)(M * D) * sizeof(float));
     for (int64_t s = 0; s < Q; ++s) {
-        const float *Wi = w_in + s * 8 * D;
-        const float *C = cb + s * N * 8;
-        const float *Wo = w_out ? w_out + s * D * 8 : NULL;
-        for (int64_t n = 0; n < N; ++n) {
-            double sum = 0.0;
-            for (int k = 0; k < 8; ++k) sum += (double)C[n * 8 + k] * (double)C[n * 8 + k];
-            float inv;
-            if (recipe == 1) {
-                inv = 1.0f / (float)sqrt(sum);
-            } else if (recipe == 2) {
-                const double norm = sqrt(sum);
-                if (norm == 0.0) { free(cbn); free(scores); return -2; }
-                inv = (float)(1.0 / norm);
-            } else {
-                inv = sum > 0.0 ? (float)(1.0 / sqrt(sum)) : 0.0f;
-            }
-            for (int k = 0; k < 8; ++k) cbn[n * 8 + k] = C[n * 8 + k] * inv;
-        }
-        for (int64_t m = 0; m < M; ++m) {
-            float *rm = r + m * D;
-            float p[8], pn[8], sq[8];
-            for (int j = 0; j < 8; ++j) {
-                p[j] = inproj_tiny ? aqo_tinyblas_dot_f32((int)D, rm, Wi + j * D) : aqo_vec_dot_f32((int)D, rm, Wi + j * D);
-                if (b_in) p[j] = p[j] + b_in[s * 8 + j];
-            }
-            for (int j = 0; j < 8; ++j) sq[j] = p[j] * p[j];
-            float ss = aqo_sum_f32(8, sq);
-            if (recipe != 1) ss = fmaf(ss, 1.0f, recipe == 2 ? 1.0e-20f : 1.0e-12f);   /* ggml_scale_bias, vec.h:708-710 */
-            const float den = sqrtf(ss);
-            for (int j = 0; j < 8; ++j) pn[j] = p[j] / den;
-            for (int64_t n = 0; n < N; ++n) scores[n] = aqo_vec_dot_f32(8, cbn + n * 8, pn);
-            const int code = aqo_argmax_f32((int)N, scores);
-            idx[m * Q + s] = code;
-            const int use = force_idx ? force_idx[m * Q + s] : code;
-            const float *q = C + (int64_t)use * 8;
-            if (!w_out) continue;   /* codes only (no out-projection given) */
-            for (int64_t d = 0; d < D; ++d) {
-                float z = aqo_vec_dot_f32(8, q, Wo + d * 8);
-                if (b_out) z = z + b_out[s * D + d];
-                rm[d] = rm[d] - z;
-                if (recon) recon[m * D + d] = s == 0 ? z : recon[m * D + d] + z;
-            }
-        }
+        const int rc = dac_stage(residual, M, T, D, N, w_in + s * 8 * D, b_in ? b_in + s * 8 : NULL, cb + s * N * 8,
+                                 w_out ? w_out + s * D * 8 : NULL, b_out ? b_out + s * D : NULL, force_idx, idx, Q, s,
+                                 recon, s == 0, recipe);
+        if (rc != 0) return rc;
     }
-    free(cbn);
-    free(scores);
+    return 0;
+}
+
+/* The Fish cascade as build_encode_quantizer runs it (fish_audio/codec.cpp:
+ * 606-608): the semantic quantizer of N0 codes (cb0 [N0, 8]), then Q - 1
+ * residual quantizers of N codes (cb [Q-1, N, 8]); the recon is the
+ * decoder's sum z_0 + z_1 + ... (codec.cpp:552-568).  Weights as
+ * aqo_dac_rvq with Q stages. */
+int aqo_dac_rvq_mixed(const float *x, int64_t B, int64_t T, int64_t D, int64_t Q, int64_t N0, int64_t N,
+                      const float *w_in, const float *b_in, const float *cb0, const float *cb,
+                      const float *w_out, const float *b_out, const int32_t *force_idx,
+                      int32_t *idx, float *residual, float *recon) {
+    const int64_t M = B * T;
+    memcpy(residual, x, (size_t)(M * D) * sizeof(float));
+    for (int64_t s = 0; s < Q; ++s) {
+        const int rc = dac_stage(residual, M, T, D, s == 0 ? N0 : N, w_in + s * 8 * D, b_in ? b_in + s * 8 : NULL,
+                                 s == 0 ? cb0 : cb + (s - 1) * N * 8, w_out + s * D * 8, b_out ? b_out + s * D : NULL,
+                                 force_idx, idx, Q, s, recon, s == 0, 0);
+        if (rc != 0) return rc;
+    }
     return 0;
 }
 

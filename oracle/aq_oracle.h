@@ -56,6 +56,12 @@ int aqo_dac_rvq_ex(const float *x, int64_t B, int64_t T, int64_t D, int64_t Q, i
                    const float *w_out, const float *b_out, const int32_t *force_idx,
                    int32_t *idx, float *residual, float *recon, int recipe);
 
+/* The Fish cascade with a semantic stage of N0 codes (cb0 [N0,8]) before
+ * Q-1 residual stages of N codes (cb [Q-1,N,8]); weights [Q,...] as above. */
+int aqo_dac_rvq_mixed(const float *x, int64_t B, int64_t T, int64_t D, int64_t Q, int64_t N0, int64_t N,
+                      const float *w_in, const float *b_in, const float *cb0, const float *cb,
+                      const float *w_out, const float *b_out, const int32_t *force_idx,
+                      int32_t *idx, float *residual, float *recon);
 /* OmniVoice-style Euclidean RVQ: logit = dot(2c, r) + (-|c|^2). x [M,K],
  * cb [Q,N,K].  logit_best [M,Q] nullable. */
 int aqo_euclid_rvq(const float *x, int64_t M, int64_t K, int64_t Q, int64_t N,

@@ -175,11 +175,14 @@ int aqref_version(void) { return 1; }
 // after each stage.  Returns compute milliseconds.
 // recipe: 0 Fish, 1 IndexTTS2, 2 Vevo2 (query and codebook normalisation).
 // Returns compute milliseconds, or -1 when the recipe rejects the codebook.
-double aqref_dac_rvq_ex(const float * x, int64_t B, int64_t T, int64_t D, int64_t Q, int64_t N,
-                        const float * w_in, const float * b_in, const float * cb,
-                        const float * w_out, const float * b_out,
-                        int32_t * idx, float * residual, float * recon, float * stage_res,
-                        int n_threads, int materialize, int recipe) {
+// N0 / cb0: the first stage's codebook size and codebook (the Fish semantic
+// quantizer, codec.cpp:606); the other stages take N and cb[s - 1].
+static double dac_rvq_core(const float * x, int64_t B, int64_t T, int64_t D, int64_t Q, int64_t N0, const float * cb0,
+                           int64_t N1, const float * cb1,
+                           const float * w_in, const float * b_in,
+                           const float * w_out, const float * b_out,
+                           int32_t * idx, float * residual, float * recon, float * stage_res,
+                           int n_threads, int materialize, int recipe) {
     ggml_cpu_init();
     const int64_t M = B * T;
     double ms = 0.0;
@@ -188,6 +191,8 @@ double aqref_dac_rvq_ex(const float * x, int64_t B, int64_t T, int64_t D, int64_
     to_channel_major(x, B, T, D, res_cm.data());
     std::vector<float> tmp(static_cast<size_t>(M * D));
     for (int64_t s = 0; s < Q; ++s) {
+        const int64_t N = s == 0 ? N0 : N1;
+        const float * cb = s == 0 ? cb0 : cb1 + (s - 1) * N1 * 8;
         const size_t bytes = static_cast<size_t>(M) * static_cast<size_t>(D + N + 64) * 4 * 12 + (64u << 20);
         Ctx c(bytes);
         ggml_context * ctx = c.ctx;
@@ -201,13 +206,13 @@ double aqref_dac_rvq_ex(const float * x, int64_t B, int64_t T, int64_t D, int64_
             std::memcpy(Bin->data, b_in + s * 8, 8 * 4);
         }
         ggml_tensor * CB = ggml_new_tensor_2d(ctx, GGML_TYPE_F32, 8, N);
-        std::memcpy(CB->data, cb + s * N * 8, static_cast<size_t>(N * 8) * 4);
+        std::memcpy(CB->data, cb, static_cast<size_t>(N * 8) * 4);
         ggml_tensor * CBn = ggml_new_tensor_2d(ctx, GGML_TYPE_F32, 8, N);
         {
             std::vector<float> nr;
-            if (recipe == 1) nr = indextts2_normalized_rows(cb + s * N * 8, N, 8);
-            else if (recipe == 2) { if (!vevo2_normalized_rows(cb + s * N * 8, N, 8, nr)) return -1.0; }
-            else nr = fish_normalized_rows(cb + s * N * 8, N, 8);
+            if (recipe == 1) nr = indextts2_normalized_rows(cb, N, 8);
+            else if (recipe == 2) { if (!vevo2_normalized_rows(cb, N, 8, nr)) return -1.0; }
+            else nr = fish_normalized_rows(cb, N, 8);
             std::memcpy(CBn->data, nr.data(), nr.size() * 4);
         }
         ggml_tensor * Wout = ggml_new_tensor_3d(ctx, GGML_TYPE_F32, 1, 8, D);
@@ -248,6 +253,26 @@ double aqref_dac_rvq_ex(const float * x, int64_t B, int64_t T, int64_t D, int64_
     if (residual) from_channel_major(res_cm.data(), B, T, D, residual);
     if (recon) from_channel_major(rec_cm.data(), B, T, D, recon);
     return ms;
+}
+
+double aqref_dac_rvq_ex(const float * x, int64_t B, int64_t T, int64_t D, int64_t Q, int64_t N,
+                        const float * w_in, const float * b_in, const float * cb,
+                        const float * w_out, const float * b_out,
+                        int32_t * idx, float * residual, float * recon, float * stage_res,
+                        int n_threads, int materialize, int recipe) {
+    return dac_rvq_core(x, B, T, D, Q, N, cb, N, cb + N * 8, w_in, b_in, w_out, b_out, idx, residual, recon,
+                        stage_res, n_threads, materialize, recipe);
+}
+
+// The Fish cascade of build_encode_quantizer (codec.cpp:606-608): a semantic
+// quantizer of N0 codes (cb0 [N0, 8]) and Q - 1 residual quantizers of N codes
+// (cb [Q - 1, N, 8]); recon is the decoder's sum.
+double aqref_dac_rvq_mixed(const float * x, int64_t B, int64_t T, int64_t D, int64_t Q, int64_t N0, int64_t N,
+                           const float * w_in, const float * b_in, const float * cb0, const float * cb,
+                           const float * w_out, const float * b_out,
+                           int32_t * idx, float * residual, float * recon, int n_threads) {
+    return dac_rvq_core(x, B, T, D, Q, N0, cb0, N, cb, w_in, b_in, w_out, b_out, idx, residual, recon, nullptr,
+                        n_threads, 1, 0);
 }
 
 double aqref_dac_rvq(const float * x, int64_t B, int64_t T, int64_t D, int64_t Q, int64_t N,

@@ -7,7 +7,7 @@ Inputs come from audio.cpp_amd/aqmi/synth.py (deterministic, seeded), so a
 fixture stores only outputs: codes, and SHA-256 digests of the fp32 residual
 and reconstruction bytes (bit-exact checks), plus small value samples.
 
-    python tests/golden/make_golden.py [dac] [mimi] [kmeans] [q8] [outetts] [moss] [qwen3] [projected]
+    python tests/golden/make_golden.py [dac] [mimi] [kmeans] [q8] [outetts] [moss] [qwen3] [projected] [fish]
 """
 
 from __future__ import annotations
@@ -144,8 +144,17 @@ def projected(ref: Ref):
         save(f"projected_{tag}.npz", **arrays)
 
 
+def fish_mixed(ref: Ref, name: str):
+    """The Fish cascade: a 4096-code semantic stage then 8 residual stages of
+    1024 codes, 4 clips x 250 frames, latent 1024 (the reference's graph
+    recipe on ggml): codes, and digests of the residual and the recon."""
+    out = ref.dac_rvq_mixed(synth.fish_config(4, 250))
+    save(name, idx=out["idx"].astype(np.int16), residual_sha=np.array(sha(out["residual"])),
+         recon_sha=np.array(sha(out["recon"])))
+
+
 def main():
-    which = set(sys.argv[1:]) or {"dac", "mimi", "kmeans", "q8", "outetts", "moss", "qwen3", "projected"}
+    which = set(sys.argv[1:]) or {"dac", "mimi", "kmeans", "q8", "outetts", "moss", "qwen3", "projected", "fish"}
     ref = Ref("native")
     if "dac" in which:
         dac(ref, 0, "dac_cfg0.npz")
@@ -166,6 +175,8 @@ def main():
         qwen3(ref, "qwen3_cascade.npz")
     if "projected" in which:
         projected(ref)
+    if "fish" in which:
+        fish_mixed(ref, "fish_mixed.npz")
 
 
 if __name__ == "__main__":

@@ -328,3 +328,62 @@ def test_dac_tinyblas_inprojection(torch, ctx, oracle, T, B, D):
     assert np.array_equal(out["idx"], ref["idx"])
     assert np.array_equal(_bits(out["residual"]), _bits(ref["residual"]))
     assert np.array_equal(_bits(out["recon"]), _bits(ref["recon"]))
+
+
+def test_fish_mixed_cascade_chained_matches_golden(torch, ctx):
+    """Fish's semantic quantizer (4096 codes) and its 8 residual quantizers
+    (1024 codes) as two uploaded stage sets chained through aq_dac_encode_ex
+    (codes written into one [M, 9] array, the residual handed on, the recon
+    continued): codes, residual and recon equal the single cascade of the
+    reference's graph recipe, and the chained decode equals the recon."""
+    import aqmi
+    from aqmi import synth
+
+    print("[gpu] fish mixed-N cascade", flush=True)
+    g = np.load(GOLDEN / "fish_mixed.npz")
+    cfg = synth.fish_config(4, 250)
+    M, D, T, Q = 1000, cfg["D"], cfg["T"], cfg["Q"]
+    sem = aqmi.DacStages(ctx, cfg["w_in"][:1], cfg["b_in"][:1], cfg["codebook0"][None], cfg["w_out"][:1],
+                         cfg["b_out"][:1])
+    rest = aqmi.DacStages(ctx, cfg["w_in"][1:], cfg["b_in"][1:], cfg["codebook"], cfg["w_out"][1:], cfg["b_out"][1:])
+    x = torch.from_numpy(cfg["x"]).cuda()
+    idx = torch.full((M, Q), -1, dtype=torch.int32, device="cuda")
+    r1 = torch.empty((M, D), dtype=torch.float32, device="cuda")
+    res = torch.empty((M, D), dtype=torch.float32, device="cuda")
+    rec = torch.empty((M, D), dtype=torch.float32, device="cuda")
+    rows = (T * D, D, 1)
+    sem.encode_ex(x, M, T, rows, idx.data_ptr(), Q, r1, rec, False)
+    rest.encode_ex(r1, M, T, rows, idx.data_ptr() + 4, Q, res, rec, True)
+    torch.cuda.synchronize()
+    assert np.array_equal(idx.cpu().numpy(), g["idx"].astype(np.int32))
+    assert _sha(res.cpu().numpy()) == str(g["residual_sha"])
+    assert _sha(rec.cpu().numpy()) == str(g["recon_sha"])
+    dec = torch.empty((M, D), dtype=torch.float32, device="cuda")
+    sem.decode_ex(idx.data_ptr(), Q, M, dec, False)
+    rest.decode_ex(idx.data_ptr() + 4, Q, M, dec, True)
+    torch.cuda.synchronize()
+    assert _sha(dec.cpu().numpy()) == str(g["recon_sha"])
+
+
+@pytest.mark.parametrize("T", [75, 76])
+def test_dac_channel_major_input(torch, ctx, oracle, T):
+    """The encoder's [B, D, T] latent read in place: the same codes, residual
+    and recon as the frame-major call (T = 76 takes tinyBLAS order)."""
+    import aqmi
+    from aqmi import synth
+
+    print(f"[gpu] dac channel-major T={T}", flush=True)
+    B, D, Q, N = 3, 1024, 3, 1024
+    cfg = dict(B=B, T=T, D=D, Q=Q, N=N, x=synth.normal(71, 1, (B * T, D)), **synth.dac_weights(71, Q, D, N, bias=True))
+    st = aqmi.DacStages(ctx, cfg["w_in"], cfg["b_in"], cfg["codebook"], cfg["w_out"], cfg["b_out"])
+    bdt = np.ascontiguousarray(cfg["x"].reshape(B, T, D).transpose(0, 2, 1))
+    M = B * T
+    idx = torch.full((M, Q), -1, dtype=torch.int32, device="cuda")
+    res = torch.empty((M, D), dtype=torch.float32, device="cuda")
+    rec = torch.empty((M, D), dtype=torch.float32, device="cuda")
+    st.encode_ex(torch.from_numpy(bdt).cuda(), M, T, (D * T, 1, T), idx.data_ptr(), Q, res, rec)
+    torch.cuda.synchronize()
+    ref = oracle.dac_rvq(cfg)
+    assert np.array_equal(idx.cpu().numpy(), ref["idx"])
+    assert np.array_equal(res.cpu().numpy().view(np.uint32), ref["residual"].view(np.uint32))
+    assert np.array_equal(rec.cpu().numpy().view(np.uint32), ref["recon"].view(np.uint32))

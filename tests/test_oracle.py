@@ -612,3 +612,19 @@ def test_oracle_qwen3_cascade_matches_golden(o):
 def test_oracle_qwen3_vs_reference_function(o, ref):
     cfg = synth.qwen3_config(25, seed=21)
     assert np.array_equal(o.qwen3_quantize(cfg), ref.qwen3_quantize(cfg))
+
+
+def test_oracle_fish_mixed_cascade_vs_ggml_and_golden(o, ref):
+    """Fish's semantic 4096-code stage before 1024-code residual stages."""
+    cfg = synth.fish_config(2, 100, Qr=3)
+    a, b = o.dac_rvq_mixed(cfg), ref.dac_rvq_mixed(cfg)
+    assert np.array_equal(a["idx"], b["idx"])
+    assert _beq(a["residual"], b["residual"]) and _beq(a["recon"], b["recon"])
+
+
+def test_oracle_fish_mixed_matches_golden(o):
+    g = np.load(GOLDEN / "fish_mixed.npz")
+    out = o.dac_rvq_mixed(synth.fish_config(4, 250))
+    assert np.array_equal(out["idx"], g["idx"].astype(np.int32))
+    assert _sha(out["residual"]) == str(g["residual_sha"])
+    assert _sha(out["recon"]) == str(g["recon_sha"])
