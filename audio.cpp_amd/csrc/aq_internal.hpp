@@ -19,7 +19,8 @@ struct aq_ctx {
     int num_cus = 0;
     // Work buffers owned by the context, grown on demand (slot 0: residual
     // cascade, 1: per-stage failure counters and lists, 2: projected queries,
-    // 3: refine-pass keys, 4: sweep keys and frame norms; 5 unused).
+    // 3: refine-pass keys, 4: sweep keys and frame norms, 5: gathered
+    // strided input rows of a DAC encode).
     static constexpr int kScratchSlots = 6;
     // Per-stage counters of the last Euclidean encode on this context (in
     // slot 1, or in the no-allocation scratch).
