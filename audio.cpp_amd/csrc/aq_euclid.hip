@@ -112,6 +112,18 @@ float from_fp16(uint16_t h) {
     std::memcpy(&out, &bits, 4);
     return out;
 }
+// fp16 round to nearest even (the Q8_0 codebooks' matrix-core operands).
+uint16_t to_f16(float f) {
+    const _Float16 h = static_cast<_Float16>(f);
+    uint16_t u;
+    std::memcpy(&u, &h, 2);
+    return u;
+}
+float from_f16(uint16_t h) {
+    _Float16 f;
+    std::memcpy(&f, &h, 2);
+    return static_cast<float>(f);
+}
 float round_up(double v) {
     float f = static_cast<float>(v);
     if (static_cast<double>(f) < v) f = std::nextafter(f, INFINITY);
@@ -126,8 +138,8 @@ struct aq_codebooks {
     int recipe = 0;
     bool q8 = false;
     bool exact_only = false;
-    uint16_t *d_cbh = nullptr;   // [Q][N][K] bf16
-    uint16_t *d_cbl = nullptr;   // [Q][N][K] bf16(c - bf16(c)) (refine pass)
+    uint16_t *d_cbh = nullptr;   // [Q][N][K] bf16 (fp16 for Q8_0)
+    uint16_t *d_cbl = nullptr;   // [Q][N][K] bf16(c - bf16(c)) (refine pass; fp16 for Q8_0)
     float *d_hh = nullptr;       // [Q][N] -|c|^2 / 2 (fp32 of the double sum)
     float *d_cbf = nullptr;      // [Q][N][K]
     float *d_bias = nullptr;     // [Q][N] (OMNI)
@@ -201,6 +213,9 @@ aq_status aq_euclid_upload(aq_ctx *ctx, int64_t Q, int64_t N, int64_t K, int cb_
     cb->clmax.assign(Q, 0.0f);
     cb->crmax.assign(Q, 0.0f);
     bool nonfinite = false;
+    // bf16 images for F32 codebooks, fp16 for Q8_0 (the kernels' Mx<Q8>)
+    uint16_t (*to_half)(float) = q8 ? to_f16 : to_bf16;
+    float (*from_half)(uint16_t) = q8 ? from_f16 : from_bf16;
     for (int64_t s = 0; s < Q; ++s) {
         double cm = 0.0, dm = 0.0, hm = 0.0, lm = 0.0, rm = 0.0;
         for (int64_t n = 0; n < N; ++n) {
@@ -209,14 +224,14 @@ aq_status aq_euclid_upload(aq_ctx *ctx, int64_t Q, int64_t N, int64_t K, int cb_
             for (int64_t k = 0; k < K; ++k) {
                 const float c = cbf[row + k];
                 if (!std::isfinite(c)) nonfinite = true;
-                const uint16_t h = to_bf16(c);
+                const uint16_t h = to_half(c);
                 cbh[row + k] = h;
                 // c - c_h and c - c_h - c_l are exact in fp32 (finite c)
-                const float dl = c - from_bf16(h);
-                const uint16_t l = std::isfinite(dl) ? to_bf16(dl) : 0;
+                const float dl = c - from_half(h);
+                const uint16_t l = std::isfinite(dl) ? to_half(dl) : 0;
                 cbl[row + k] = l;
-                const double ld = from_bf16(l), rd = static_cast<double>(dl) - ld;
-                const double cd = c, hd = from_bf16(h);
+                const double ld = from_half(l), rd = static_cast<double>(dl) - ld;
+                const double cd = c, hd = from_half(h);
                 sq += cd * cd;                                    // OmniVoice: double products
                 e2d += static_cast<double>(c * c);               // sum_rows(c*c): fp32 squares
                 dq += (hd - cd) * (hd - cd);

@@ -64,6 +64,33 @@ constexpr int kThreads = kWave * kWaves;
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+// Matrix-core operand type of the sweep and the refine pass: bf16 for F32
+// codebooks; fp16 for Q8_0 codebooks, whose dequantised codes q * d carry up
+// to 18 significant bits: fp16's 11-bit mantissa makes the certificate's
+// bound 8x tighter there, which settles most of the frames a bf16 bound
+// leaves open (top-4 needs the 4th/5th gap).  The fp16 matrix ops run
+// slower than bf16 on long sweeps, so F32 codebooks keep bf16.
+template <bool Q8>
+struct Mx {
+    using E = __bf16;
+    using V8 = bf16x8;
+    typedef __bf16 V2 __attribute__((ext_vector_type(2)));
+    __device__ static f32x4 mfma(V8 a, V8 b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0); }
+    // the two values of a packed pair as fp32
+    __device__ static float lo(unsigned w) { return __uint_as_float(w << 16); }
+    __device__ static float hi(unsigned w) { return __uint_as_float(w & 0xFFFF0000u); }
+};
+template <>
+struct Mx<true> {
+    using E = _Float16;
+    using V8 = f16x8;
+    typedef _Float16 V2 __attribute__((ext_vector_type(2)));
+    __device__ static f32x4 mfma(V8 a, V8 b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
+    __device__ static float lo(unsigned w) { return static_cast<float>(__builtin_bit_cast(V2, w)[0]); }
+    __device__ static float hi(unsigned w) { return static_cast<float>(__builtin_bit_cast(V2, w)[1]); }
+};
 
 enum Recipe : int { OMNI = 0, HIGGS = 1, DIRECT = 2 };
 
@@ -521,6 +548,7 @@ __global__ __launch_bounds__(kThreads, sweep_blocks_per_cu(KS)) void euclid_swee
     const int cps = (N / T::CC) / a.nsplit;   // chunks per split
     const int c0 = split * cps, c1 = c0 + cps;
 
+    using MX = Mx<Q8>;
     // ---- phase 0: frames -> bf16 fragments in registers, rounding norms ----
     // x~ fragments stay packed (2 bf16 per register) for the whole sweep.
     u32x4 xb[FG][KS];
@@ -543,11 +571,11 @@ __global__ __launch_bounds__(kThreads, sweep_blocks_per_cu(KS)) void euclid_swee
             u32x4 packed;
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-                typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-                const bf16x2 pr = {static_cast<__bf16>(v[2 * t]), static_cast<__bf16>(v[2 * t + 1])};
+                const typename MX::V2 pr = {static_cast<typename MX::E>(v[2 * t]),
+                                            static_cast<typename MX::E>(v[2 * t + 1])};
                 const unsigned w = __builtin_bit_cast(unsigned, pr);
                 packed[t] = w;
-                const float r0 = __uint_as_float(w << 16), r1 = __uint_as_float(w & 0xFFFF0000u);
+                const float r0 = MX::lo(w), r1 = MX::hi(w);
                 sx = __fmaf_rn(r0, r0, sx);
                 sx = __fmaf_rn(r1, r1, sx);
                 const float d0 = v[2 * t] - r0, d1 = v[2 * t + 1] - r1;
@@ -599,10 +627,10 @@ __global__ __launch_bounds__(kThreads, sweep_blocks_per_cu(KS)) void euclid_swee
     constexpr int L = R - 1;
     constexpr int PPB = (T::STAGE16 + BPC - 1) / BPC;   // staged pieces per block
 
-    auto lds_a = [&](int buf, int blk, int ks) -> bf16x8 {
+    auto lds_a = [&](int buf, int blk, int ks) -> typename MX::V8 {
         const int r = blk * 16 + col;
         const int j = ks * 4 + kq;
-        return *reinterpret_cast<const bf16x8 *>(lds + buf * T::BUFB + r * T::ROWB + ((j ^ (r & T::SWZ)) * 16));
+        return *reinterpret_cast<const typename MX::V8 *>(lds + buf * T::BUFB + r * T::ROWB + ((j ^ (r & T::SWZ)) * 16));
     };
     auto lds_h = [&](int buf, int blk) -> f32x4 {
         return *reinterpret_cast<const f32x4 *>(lds + buf * T::BUFB + T::CHUNKB + (blk * 16 + kq * 4) * 4);
@@ -630,7 +658,7 @@ __global__ __launch_bounds__(kThreads, sweep_blocks_per_cu(KS)) void euclid_swee
     }
     __syncthreads();
 
-    bf16x8 ring[R];
+    typename MX::V8 ring[R];
 #pragma unroll
     for (int l = 0; l < L; ++l) ring[l] = lds_a(0, 0, l);
     f32x4 hcur = lds_h(0, 0);
@@ -694,8 +722,7 @@ __global__ __launch_bounds__(kThreads, sweep_blocks_per_cu(KS)) void euclid_swee
                 else if (b + 1 < BPC) ring[pk % R] = lds_a(buf, b + 1, pk - KS);
 #pragma unroll
                 for (int g = 0; g < FG; ++g)
-                    acc[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ring[ks % R], __builtin_bit_cast(bf16x8, xb[g][ks]),
-                                                                     acc[g], 0, 0, 0);
+                    acc[g] = MX::mfma(ring[ks % R], __builtin_bit_cast(typename MX::V8, xb[g][ks]), acc[g]);
             }
             epilogue(accp, lprev);
             if (b + 1 < BPC) hcur = lds_h(buf, b + 1);
@@ -1456,9 +1483,10 @@ __global__ __launch_bounds__(kWave * kRWaves, KS <= 8 ? 2 : 1) void euclid_refin
         const int r = q / T::CH16, j = q % T::CH16;
         return buf * T::BUFB + arr * (16 * T::ROWB) + r * T::ROWB + ((j ^ (r & T::SWZ)) * 16);
     };
-    auto lds_a = [&](int buf, int arr, int ks) -> bf16x8 {
+    using MX = Mx<Q8>;
+    auto lds_a = [&](int buf, int arr, int ks) -> typename MX::V8 {
         const int j = ks * 4 + kq;
-        return *reinterpret_cast<const bf16x8 *>(lds + buf * T::BUFB + arr * (16 * T::ROWB) + col * T::ROWB +
+        return *reinterpret_cast<const typename MX::V8 *>(lds + buf * T::BUFB + arr * (16 * T::ROWB) + col * T::ROWB +
                                                  ((j ^ (col & T::SWZ)) * 16));
     };
     // global source of piece p of block n16 (16 codes from n16)
@@ -1482,12 +1510,12 @@ __global__ __launch_bounds__(kWave * kRWaves, KS <= 8 ? 2 : 1) void euclid_refin
             if (Q8) q8_image_block(v);
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-                typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-                const bf16x2 ph = {static_cast<__bf16>(v[2 * t]), static_cast<__bf16>(v[2 * t + 1])};
+                using E = typename MX::E;
+                const typename MX::V2 ph = {static_cast<E>(v[2 * t]), static_cast<E>(v[2 * t + 1])};
                 const unsigned wh = __builtin_bit_cast(unsigned, ph);
-                const float d0 = v[2 * t] - __uint_as_float(wh << 16);
-                const float d1 = v[2 * t + 1] - __uint_as_float(wh & 0xFFFF0000u);
-                const bf16x2 pl = {static_cast<__bf16>(d0), static_cast<__bf16>(d1)};
+                const float d0 = v[2 * t] - MX::lo(wh);
+                const float d1 = v[2 * t + 1] - MX::hi(wh);
+                const typename MX::V2 pl = {static_cast<E>(d0), static_cast<E>(d1)};
                 xh[ks][t] = wh;
                 xl[ks][t] = __builtin_bit_cast(unsigned, pl);
             }
@@ -1525,12 +1553,12 @@ __global__ __launch_bounds__(kWave * kRWaves, KS <= 8 ? 2 : 1) void euclid_refin
             f32x4 acx = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
-                const bf16x8 ah = lds_a(buf, 0, ks);
-                const bf16x8 al = lds_a(buf, 1, ks);
-                const bf16x8 bh = __builtin_bit_cast(bf16x8, xh[ks]);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc, 0, 0, 0);
-                acx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acx, 0, 0, 0);
-                acx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, __builtin_bit_cast(bf16x8, xl[ks]), acx, 0, 0, 0);
+                const typename MX::V8 ah = lds_a(buf, 0, ks);
+                const typename MX::V8 al = lds_a(buf, 1, ks);
+                const typename MX::V8 bh = __builtin_bit_cast(typename MX::V8, xh[ks]);
+                acc = MX::mfma(ah, bh, acc);
+                acx = MX::mfma(al, bh, acx);
+                acx = MX::mfma(ah, __builtin_bit_cast(typename MX::V8, xl[ks]), acx);
             }
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -1667,9 +1695,9 @@ __global__ __launch_bounds__(kWave) void euclid_refine_select_kernel(StageArgs a
                 const float id = am != 0.0f ? __fdiv_rn(127.0f, am) : 0.0f;
                 v = __fmul_rn(__builtin_rintf(__fmul_rn(v, id)), dq);
             }
-            const float h = static_cast<float>(static_cast<__bf16>(v));
+            const float h = static_cast<float>(static_cast<typename Mx<Q8>::E>(v));
             const float d = v - h;
-            const float l = static_cast<float>(static_cast<__bf16>(d));
+            const float l = static_cast<float>(static_cast<typename Mx<Q8>::E>(d));
             const float r = d - l;
             sh = __fmaf_rn(h, h, sh);
             sl = __fmaf_rn(l, l, sl);
