@@ -454,6 +454,7 @@ aq_status euclid_encode_impl(aq_ctx *ctx, const aq_codebooks *cb, const aq_frame
     StageFn sweep = kk->sweep[cb->q8 ? 1 : 0][topl - 3];
     StageFn select = kk->select[var][topl - 3];
     StageFn scan = kk->exact_scan[var];
+    StageFn scan_values = kk->scan_values[var];
     const int lds = kk->lds;
     AQ_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void *>(sweep), hipFuncAttributeMaxDynamicSharedMemorySize, lds));
     const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
@@ -531,6 +532,20 @@ aq_status euclid_encode_impl(aq_ctx *ctx, const aq_codebooks *cb, const aq_frame
         rf.keys = static_cast<float *>(w);
         rf.key_floats = floats;
     }
+    // Exact values of the scanned frames' codes ([kScanSplitFrames, N]); a
+    // fixed region too small for them leaves every scan on one CU per frame.
+    float *svals = nullptr;
+    int scap = 0;
+    {
+        const size_t bytes = static_cast<size_t>(kScanSplitFrames) * cb->N * sizeof(float);
+        if (!arena.base || arena.left() >= bytes + (size_t{8} << 20)) {
+            void *w = nullptr;
+            aq_status st = arena.get(6, bytes, &w);
+            if (st != AQ_OK) return st;
+            svals = static_cast<float *>(w);
+            scap = kScanSplitFrames;
+        }
+    }
     rf.list2 = list2;
     RefineFn rvals = kk->refine_values[var];
     RefineFn rsel = kk->refine_select[var];
@@ -574,6 +589,8 @@ aq_status euclid_encode_impl(aq_ctx *ctx, const aq_codebooks *cb, const aq_frame
         a.keys = keys;
         a.norms = keys + static_cast<size_t>(nsplit) * ngroups * topl * kWave;
         a.nsplit = nsplit;
+        a.svals = svals;
+        a.scap = scap;
         if (s >= 64 && s % 64 == 0) AQ_HIP(ctx, hipMemsetAsync(counts, 0, sizeof(int32_t) * 128, ctx->stream));
         const int tslot = arena.base ? -1 : aq_timing_start(ctx);   // events are not created without allocation
         hipLaunchKernelGGL(sweep, dim3(static_cast<unsigned>((tiles + 7) / 8 * 8 * nsplit)), dim3(kThreads), lds,
@@ -597,6 +614,8 @@ aq_status euclid_encode_impl(aq_ctx *ctx, const aq_codebooks *cb, const aq_frame
         StageArgs a2 = a;
         a2.fail_count = r.count2;
         a2.fail_list = list2;
+        hipLaunchKernelGGL(scan_values, dim3(static_cast<unsigned>(cus)), dim3(kScanThreads), 0, ctx->stream, a2);
+        AQ_HIP(ctx, hipGetLastError());
         hipLaunchKernelGGL(scan, dim3(static_cast<unsigned>(cus)), dim3(kScanThreads), scan_lds, ctx->stream, a2);
         AQ_HIP(ctx, hipGetLastError());
         return AQ_OK;

@@ -141,6 +141,8 @@ struct StageArgs {
     float *keys;             // sweep -> select: [nsplit][M/16][TOPL][64] score keys
     float *norms;            // sweep -> select: [3][M] |x~|^2, |x - x~|^2, |x|^2
     int nsplit;              // code splits of the sweep
+    float *svals;            // [scap, N] exact values of the scanned frames, by list slot
+    int scap;                // frames whose values euclid_scan_values_kernel computes
 };
 
 struct RefArgs {
@@ -192,6 +194,7 @@ struct KsKernels {
     StageFn select[4][2];     // [variant][topl]
     RefineFn refine_values[4];
     RefineFn refine_select[4];
+    StageFn scan_values[4];
     StageFn exact_scan[4];
     int lds;                  // sweep dynamic LDS bytes
     int cc;                   // codes per LDS chunk
@@ -327,6 +330,42 @@ __device__ float dot_q8(const int8_t *__restrict__ qc, const float *__restrict__
     return reduce8(acc);
 }
 
+// dot_q8 for a compile-time width: the code row's quants are loaded four
+// blocks (128 bytes) at a time before any of them is used, so a code costs
+// K / 128 memory round trips instead of K / 32.
+template <int K>
+__device__ float dot_q8_k(const int8_t *__restrict__ qc, const float *__restrict__ dc, const int8_t *__restrict__ qx,
+                          const float *__restrict__ dx) {
+    constexpr int NB = K / 32;
+    constexpr int G = NB < 4 ? NB : 4;
+    static_assert(NB % G == 0, "blocks per group");
+    float acc[8];
+#pragma unroll
+    for (int l = 0; l < 8; ++l) acc[l] = 0.0f;
+    const u32x4 *pc = reinterpret_cast<const u32x4 *>(qc);
+#pragma unroll
+    for (int b0 = 0; b0 < NB; b0 += G) {
+        u32x4 c[2 * G];
+        float d[G];
+#pragma unroll
+        for (int j = 0; j < 2 * G; ++j) c[j] = pc[2 * b0 + j];
+#pragma unroll
+        for (int j = 0; j < G; ++j) d[j] = dc[b0 + j];
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+            const int ib = b0 + j;
+            const float dd = __fmul_rn(d[j], dx[ib]);
+            const int *px = reinterpret_cast<const int *>(qx + 32 * ib);
+#pragma unroll
+            for (int l = 0; l < 8; ++l) {
+                const int cw = static_cast<int>(c[2 * j + l / 4][l % 4]);
+                acc[l] = __fmaf_rn(dd, static_cast<float>(__builtin_amdgcn_sdot4(cw, px[l], 0, false)), acc[l]);
+            }
+        }
+    }
+    return reduce8(acc);
+}
+
 // Compile-time-K forms for the stage kernel: the loops unroll, so the loads
 // of later steps are issued ahead of the FMA chains that consume them.
 template <int K>
@@ -447,7 +486,7 @@ template <int RECIPE, bool Q8, int K>
 __device__ float exact_value_kq(const StageArgs &a, const float *__restrict__ x, int n, float x2,
                                 const int8_t *__restrict__ xq, const float *__restrict__ xd) {
     if (!Q8) return exact_value_k<RECIPE, Q8, K>(a, x, n, x2);
-    const float dot = dot_q8(a.q8 + static_cast<int64_t>(n) * K, a.q8d + static_cast<int64_t>(n) * (K / 32), xq, xd, K / 32);
+    const float dot = dot_q8_k<K>(a.q8 + static_cast<int64_t>(n) * K, a.q8d + static_cast<int64_t>(n) * (K / 32), xq, xd);
     return __fsub_rn(__fsub_rn(__fmul_rn(dot, 2.0f), x2), a.e2[n]);
 }
 
@@ -1193,10 +1232,15 @@ __global__ __launch_bounds__(kThreads) void euclid_select_kernel(StageArgs a) {
 
 // ------------------------------------------------------------- exact scan
 
-// Frames that neither certificate settles get an exact scan: one block per
-// frame evaluates the recipe value of every code (kScanChunk codes at a time
-// into LDS, one code per thread), and wave 0 walks each chunk in code order
-// with the reference's selection rules, so the result is the reference's by
+// Frames that neither certificate settles get an exact scan.  The recipe
+// value of every code (one code per thread) comes from
+// euclid_scan_values_kernel, spread over the grid, when a stage has at most
+// kScanSplitFrames such frames, else from the frame's own block.  One block
+// per frame then selects: in parallel (winner and best topk + 1 codes per
+// thread, merged over the block), which is the reference's result unless a
+// value is NaN or the k-th and (k+1)-th values tie; in those cases wave 0
+// walks the values (kScanChunk at a time in LDS) in code order with the
+// reference's selection rules, so the result is the reference's by
 // construction, ties and NaN included:
 //  * ggml recipes: ggml_vec_argmax_f32 (running MAX(max, v), index of the
 //    last element equal to the running max, a NaN restarts it) and
@@ -1241,10 +1285,216 @@ __device__ void heap_adjust(int *hn, float *hv, int hole, int len, int vn, float
 
 constexpr int kScanThreads = 256;
 constexpr int kScanChunk = 2048;
+// Frames per stage whose exact values euclid_scan_values_kernel spreads over
+// the grid; more go through the scan kernel alone.
+constexpr int kScanSplitFrames = 64;
+// Order-preserving key of a non-NaN value: a > b (as floats) exactly when
+// ukey(a) > ukey(b); -0 and +0, which compare equal, share a key.  Every key
+// is at least ukey(-inf) = 0x007FFFFF.
+__device__ inline uint32_t ukey(float v) {
+    const unsigned b = __float_as_uint(__fadd_rn(v, 0.0f));
+    return b ^ ((b >> 31) ? 0xFFFFFFFFu : 0x80000000u);
+}
+
+// Total-order key of a recipe value for the parallel selection of the exact
+// scan: a larger key ranks first (ggml recipes: larger value, then smaller
+// index; DIRECT: smaller value, then smaller index, the order of its top-k).
+// NaN has none: 0, which no value reaches, stands for "no code".
+template <int RECIPE>
+__device__ inline uint64_t rank_key(float v, int n) {
+    if (v != v) return 0;
+    const uint32_t o = RECIPE == DIRECT ? ~ukey(v) : ukey(v);
+    return (static_cast<uint64_t>(o) << 32) | static_cast<uint32_t>(~n);
+}
+
+__device__ inline int key_index(uint64_t k) { return static_cast<int>(~static_cast<uint32_t>(k)); }
+
+// k or its DPP-permuted copy (CTRL: a permutation inside rows of 16 lanes),
+// whichever is larger.
+template <int CTRL>
+__device__ inline uint64_t dpp_max_u64(uint64_t k) {
+    const int lo = __builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<uint32_t>(k)), CTRL, 0xF, 0xF, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<uint32_t>(k >> 32)), CTRL, 0xF, 0xF, false);
+    const uint64_t o = (static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) | static_cast<uint32_t>(lo);
+    return o > k ? o : k;
+}
+
+// Largest key over a wave (every lane active), the same in every lane: lane
+// xor 1 and xor 2 (quad_perm), half-row and row mirrors leave each row's
+// maximum in all its lanes; lanes 0, 16, 32, 48 are compared in scalar
+// registers.
+__device__ inline uint64_t wave_max_u64(uint64_t k) {
+    k = dpp_max_u64<0xB1>(k);
+    k = dpp_max_u64<0x4E>(k);
+    k = dpp_max_u64<0x141>(k);
+    k = dpp_max_u64<0x140>(k);
+    uint64_t m = 0;
+#pragma unroll
+    for (int row = 0; row < kWave / 16; ++row) {
+        const uint32_t lo = __builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(k)), 16 * row);
+        const uint32_t hi = __builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(k >> 32)), 16 * row);
+        const uint64_t q = (static_cast<uint64_t>(hi) << 32) | lo;
+        m = q > m ? q : m;
+    }
+    return m;
+}
+
+// heap_adjust(hn, hv, 0, LEN, nv, v) for a heap of LEN <= 4 entries, with
+// the values as ukey keys (kv = ukey(v)): the root replaced by (kv, nv) and
+// sifted down, then the new entry pushed up, std::__adjust_heap's cases
+// written out so that a wave-uniform heap stays in scalar registers.
+template <int LEN>
+__device__ inline void heap_replace_root(uint32_t (&k)[4], int (&n)[4], uint32_t kv, int nv) {
+    if (LEN == 1) {
+        k[0] = kv;
+        n[0] = nv;
+    } else if (LEN == 2) {
+        if (k[1] > kv) {
+            k[0] = kv;
+            n[0] = nv;
+        } else {
+            k[0] = k[1];
+            n[0] = n[1];
+            k[1] = kv;
+            n[1] = nv;
+        }
+    } else if (LEN == 3) {
+        // the hole moves to the child with the smaller value (child 2 on equality)
+        const bool one = k[2] > k[1];
+        const uint32_t ks = one ? k[1] : k[2];
+        const int ns = one ? n[1] : n[2];
+        if (ks > kv) {
+            k[0] = kv;
+            n[0] = nv;
+        } else {
+            k[0] = ks;
+            n[0] = ns;
+            if (one) {
+                k[1] = kv;
+                n[1] = nv;
+            } else {
+                k[2] = kv;
+                n[2] = nv;
+            }
+        }
+    } else if (k[2] > k[1]) {
+        // hole to child 1, then to its only child 3; push up from 3
+        if (!(k[3] > kv)) {
+            k[0] = k[1];
+            n[0] = n[1];
+            k[1] = k[3];
+            n[1] = n[3];
+            k[3] = kv;
+            n[3] = nv;
+        } else if (!(k[1] > kv)) {
+            k[0] = k[1];
+            n[0] = n[1];
+            k[1] = kv;
+            n[1] = nv;
+        } else {
+            k[0] = kv;
+            n[0] = nv;
+        }
+    } else if (!(k[2] > kv)) {
+        // hole to child 2 (a leaf); push up from 2
+        k[0] = k[2];
+        n[0] = n[2];
+        k[2] = kv;
+        n[2] = nv;
+    } else {
+        k[0] = kv;
+        n[0] = nv;
+    }
+}
+
+// ggml_top_k's std::partial_sort heap over src[0, N) (no NaN), by one wave
+// with the heap in scalar registers: std::make_heap of the first LEN codes,
+// then each later code strictly above the root replaces it
+// (std::__heap_select).  The next 64 values load while a chunk is walked.
+// Lane 0 leaves the heap in hn / hv.
+template <int LEN>
+__device__ void heap_walk(const float *src, int N, int *hn, float *hv) {
+    const int lane = threadIdx.x & (kWave - 1);
+    uint32_t k[4] = {0, 0, 0, 0};
+    int n[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int q = 0; q < LEN; ++q) {
+        k[q] = __builtin_amdgcn_readfirstlane(ukey(src[q]));
+        n[q] = q;
+    }
+    // std::make_heap: __adjust_heap at 1 (LEN 4: its only child 3), then at 0
+    if (LEN == 4 && !(k[3] > k[1])) {
+        const uint32_t t = k[1];
+        k[1] = k[3];
+        k[3] = t;
+        n[1] = 3;
+        n[3] = 1;
+    }
+    if (LEN >= 2) heap_replace_root<LEN>(k, n, k[0], n[0]);
+    uint32_t root = k[0];
+    float v = LEN + lane < N ? src[LEN + lane] : -INFINITY;
+    for (int c0 = LEN; c0 < N; c0 += kWave) {
+        const int nx = c0 + kWave + lane;
+        const float vn = nx < N ? src[nx] : -INFINITY;
+        const uint32_t uk = ukey(v);
+        unsigned long long take = __ballot(uk > root);
+        while (take != 0) {
+            const int f = __ffsll(static_cast<long long>(take)) - 1;
+            heap_replace_root<LEN>(k, n, __builtin_amdgcn_readlane(uk, f), c0 + f);
+            root = k[0];
+            take = __ballot(lane > f && uk > root);
+        }
+        v = vn;
+    }
+    if (lane == 0)
+#pragma unroll
+        for (int q = 0; q < LEN; ++q) {
+            hn[q] = n[q];
+            hv[q] = src[n[q]];
+        }
+}
+
+// Exact values of every code for the frames the refine pass left open, when
+// there are at most a.scap of them (the usual case: a few per stage), spread
+// over the whole grid: a block takes (list slot, kScanThreads-code chunk)
+// items, one code per thread, and writes a.svals[slot][n].  The per-frame
+// scan then only selects, instead of evaluating N codes on one CU.  The
+// values are exact_value_kq's, so the split changes no result.
+template <int RECIPE, bool Q8, int KS>
+__global__ __launch_bounds__(kScanThreads) void euclid_scan_values_kernel(StageArgs a) {
+    constexpr int K = KS * 32;
+    __shared__ __align__(16) float xs[K];
+    __shared__ __align__(16) int8_t xq[K];
+    __shared__ float xd[K / 32];
+    __shared__ float o_x2;
+    const int count = *a.fail_count;
+    if (count > a.scap) return;
+    const int tid = threadIdx.x;
+    const int nch = (a.N + kScanThreads - 1) / kScanThreads;
+    const int items = count * nch;
+    int cur = -1;
+    for (int item = blockIdx.x; item < items; item += gridDim.x) {
+        const int slot = item / nch;   // block-uniform
+        if (slot != cur) {
+            const int64_t m = a.fail_list[slot];
+            __syncthreads();
+            for (int k = tid; k < K; k += kScanThreads) xs[k] = a.xin[m * K + k];
+            __syncthreads();
+            if (tid == 0) o_x2 = RECIPE == HIGGS ? sum_squares_k<K>(xs) : 0.0f;
+            if (Q8 && tid < K / 32) quantize_block_q8(xs + 32 * tid, xq + 32 * tid, xd + tid);
+            __syncthreads();
+            cur = slot;
+        }
+        const int n = (item % nch) * kScanThreads + tid;
+        if (n < a.N) a.svals[static_cast<int64_t>(slot) * a.N + n] = exact_value_kq<RECIPE, Q8, K>(a, xs, n, o_x2, xq, xd);
+    }
+}
 
 template <int RECIPE, bool Q8, int KS>
 __global__ __launch_bounds__(kScanThreads) void euclid_exact_scan_kernel(StageArgs a) {
     constexpr int K = KS * 32;
+    constexpr int ST = kScanThreads;
+    constexpr int PT = kScanChunk / ST;   // values per thread of a one-chunk frame
     extern __shared__ __align__(16) unsigned char lds[];
     float *xs = reinterpret_cast<float *>(lds);                         // [K]
     int8_t *xq = reinterpret_cast<int8_t *>(xs + K);                    // [K]
@@ -1254,29 +1504,170 @@ __global__ __launch_bounds__(kScanThreads) void euclid_exact_scan_kernel(StageAr
     __shared__ float heap_v[4];
     __shared__ int o_code, o_sel_n[4];
     __shared__ float o_code_v, o_sel_v[4], o_x2;
+    __shared__ uint64_t w_top[ST / kWave][5], w_win[ST / kWave], o_key[5], o_win;
+    __shared__ int w_nan[ST / kWave];
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const int count = *a.fail_count;
     const int ktop = a.topk;
+    // pre: euclid_scan_values_kernel has computed every code's exact value
+    const bool pre = count <= a.scap;
     for (int slot = blockIdx.x; slot < count; slot += gridDim.x) {
         const int64_t m = a.fail_list[slot];
         __syncthreads();
-        for (int k = tid; k < K; k += kScanThreads) xs[k] = a.xin[m * K + k];
+        if (!pre) {
+            for (int k = tid; k < K; k += ST) xs[k] = a.xin[m * K + k];
+            __syncthreads();
+            if (tid == 0) o_x2 = RECIPE == HIGGS ? sum_squares_k<K>(xs) : 0.0f;   // unrolled: LDS reads in flight
+            if (Q8 && tid < K / 32) quantize_block_q8(xs + 32 * tid, xq + 32 * tid, xd + tid);
+            __syncthreads();
+        }
+        const float x2 = pre ? 0.0f : o_x2;
+        const float *sv = pre ? a.svals + static_cast<int64_t>(slot) * a.N : nullptr;
+        auto value = [&](int n) -> float { return pre ? sv[n] : exact_value_kq<RECIPE, Q8, K>(a, xs, n, x2, xq, xd); };
+
+        // The frame's values.  Codes that fit one chunk (N <= kScanChunk):
+        // PT per thread in registers (code tid + j * ST), and all in rv in
+        // code order; more codes: read from the grid's values (pre), or
+        // computed chunk by chunk by the walk below.
+        const bool have_all = pre || a.N <= kScanChunk;
+        const bool in_regs = a.N <= kScanChunk;
+        float vr[PT];
+        if (in_regs && pre) {
+#pragma unroll
+            for (int j = 0; j < PT; ++j) {
+                const int i = tid + j * ST;
+                vr[j] = i < a.N ? sv[i] : 0.0f;
+            }
+#pragma unroll
+            for (int j = 0; j < PT; ++j)
+                if (tid + j * ST < a.N) rv[tid + j * ST] = vr[j];
+        } else if (in_regs) {
+#pragma unroll 4
+            for (int i = tid; i < a.N; i += ST) rv[i] = exact_value_kq<RECIPE, Q8, K>(a, xs, i, x2, xq, xd);
+        }
         __syncthreads();
-        if (tid == 0) o_x2 = RECIPE == HIGGS ? sum_squares_k<K>(xs) : 0.0f;   // unrolled: LDS reads in flight
-        if (Q8 && tid < K / 32) quantize_block_q8(xs + 32 * tid, xq + 32 * tid, xd + tid);
-        __syncthreads();
-        const float x2 = o_x2;
+        if (in_regs && !pre) {
+#pragma unroll
+            for (int j = 0; j < PT; ++j) {
+                const int i = tid + j * ST;
+                vr[j] = i < a.N ? rv[i] : 0.0f;
+            }
+        }
+        // Parallel selection, unless a ggml recipe meets a NaN (its argmax
+        // restarts there) or the values are not all at hand: the winner and
+        // the best L codes in rank_key order.  Each wave takes L rounds of a
+        // wave-wide max over its keys below the previous round's, then wave
+        // 0 does the same over the waves' lists.
+        bool slow = !have_all;
+        bool tie = false;
+        if (have_all) {
+            const int L = RECIPE == DIRECT ? (ktop > 1 ? ktop : 1) : ktop + 1;
+            const int wv = tid / kWave;
+            bool nan = false;
+            uint64_t kr[PT];
+#pragma unroll
+            for (int j = 0; j < PT; ++j) {
+                const bool ok = in_regs && tid + j * ST < a.N;
+                nan |= ok && vr[j] != vr[j];
+                kr[j] = ok ? rank_key<RECIPE>(vr[j], tid + j * ST) : 0;
+            }
+            uint64_t prev = ~0ull;
+            for (int r = 0; r < L; ++r) {
+                const bool want_w = RECIPE != DIRECT && r == 0;   // ggml argmax: the largest value, its last index
+                uint64_t best = 0, wb = 0;
+                auto consider = [&](uint64_t k, int i) {
+                    best = k < prev && k > best ? k : best;
+                    const uint64_t w = (k & 0xFFFFFFFF00000000ull) | static_cast<uint32_t>(i);
+                    if (want_w && k != 0 && w > wb) wb = w;
+                };
+                if (in_regs) {
+#pragma unroll
+                    for (int j = 0; j < PT; ++j) consider(kr[j], tid + j * ST);
+                } else {
+                    for (int i = tid; i < a.N; i += ST) {
+                        const float v = sv[i];
+                        nan |= v != v;
+                        consider(rank_key<RECIPE>(v, i), i);
+                    }
+                }
+                best = wave_max_u64(best);
+                if (lane == 0) w_top[wv][r] = best;
+                if (want_w) {
+                    wb = wave_max_u64(wb);
+                    if (lane == 0) w_win[wv] = wb;
+                }
+                prev = best;
+            }
+            if (RECIPE != DIRECT) {
+                const bool wnan = __any(nan);
+                if (lane == 0) w_nan[wv] = wnan ? 1 : 0;
+            }
+            __syncthreads();
+            if (RECIPE != DIRECT)
+                for (int w = 0; w < ST / kWave; ++w) slow |= w_nan[w] != 0;
+            if (!slow) {
+                if (wv == 0) {
+                    const uint64_t c = lane < (ST / kWave) * L ? w_top[lane / L][lane % L] : 0;
+                    uint64_t pv = ~0ull;
+                    for (int r = 0; r < L; ++r) {
+                        const uint64_t b = wave_max_u64(c < pv ? c : 0);
+                        if (lane == 0) o_key[r] = b;
+                        pv = b;
+                    }
+                    if (RECIPE != DIRECT && lane == 0) {
+                        uint64_t w = w_win[0];
+                        for (int q = 1; q < ST / kWave; ++q) w = w_win[q] > w ? w_win[q] : w;
+                        o_win = w;
+                    }
+                }
+                __syncthreads();
+                // ggml_top_k keeps, of codes tied at the k-th place, what its
+                // heap leaves: replayed below
+                tie = RECIPE != DIRECT && ktop > 0 && o_key[ktop] != 0 && (o_key[ktop - 1] >> 32) == (o_key[ktop] >> 32);
+                if (tid == 0) {
+                    // an index below 0 stands for no code (key 0: DIRECT with
+                    // every value NaN, or fewer codes than places).  Tested on
+                    // the index, not as key == 0: ROCm 7.2's compiler lowered
+                    // (key == 0 ? 0 : key_index(key)) here to a scalar select
+                    // on the flag of the preceding s_not_b32, i.e. always 0.
+                    const int n = RECIPE == DIRECT ? key_index(o_key[0]) : static_cast<int>(static_cast<uint32_t>(o_win));
+                    o_code = n < 0 ? 0 : n;
+                    o_code_v = n < 0 ? INFINITY : (in_regs ? rv[n] : sv[n]);
+                    if (!tie)
+                        for (int r = 0; r < ktop; ++r) {
+                            const int q = key_index(o_key[r]);
+                            o_sel_n[r] = q < 0 ? 0 : q;
+                            o_sel_v[r] = q < 0 ? INFINITY : (in_regs ? rv[q] : sv[q]);
+                        }
+                }
+                if (tie && wv == 0) {
+                    // rv (LDS) and sv (global) in separate instances, so that
+                    // each reads through its own address space
+                    switch (ktop) {
+                        case 1: in_regs ? heap_walk<1>(rv, a.N, heap_n, heap_v) : heap_walk<1>(sv, a.N, heap_n, heap_v); break;
+                        case 2: in_regs ? heap_walk<2>(rv, a.N, heap_n, heap_v) : heap_walk<2>(sv, a.N, heap_n, heap_v); break;
+                        case 3: in_regs ? heap_walk<3>(rv, a.N, heap_n, heap_v) : heap_walk<3>(sv, a.N, heap_n, heap_v); break;
+                        default: in_regs ? heap_walk<4>(rv, a.N, heap_n, heap_v) : heap_walk<4>(sv, a.N, heap_n, heap_v); break;
+                    }
+                }
+            }
+        }
+        // The walk (a ggml recipe with a NaN, or values computed chunk by
+        // chunk): wave 0 replays the reference's sequential selection.
         // wave 0's running selection state (uniform across its lanes)
         float mx = RECIPE == DIRECT ? INFINITY : -INFINITY;
         int id = 0;
         float root = 0.0f;   // heap root (ggml recipes) / k-th kept distance (DIRECT)
         int kept = 0;        // DIRECT: entries in the kept list
-        for (int base = 0; base < a.N; base += kScanChunk) {
+        for (int base = 0; base < (slow ? a.N : 0); base += kScanChunk) {
             const int len = min(kScanChunk, a.N - base);
-            // unrolled so that the row loads of several codes are in flight at once
+            // unrolled so that the row loads of several codes are in flight at
+            // once; a single chunk is in rv since pass 1
+            if (a.N > kScanChunk) {
 #pragma unroll 4
-            for (int i = tid; i < len; i += kScanThreads) rv[i] = exact_value_kq<RECIPE, Q8, K>(a, xs, base + i, x2, xq, xd);
+                for (int i = tid; i < len; i += ST) rv[i] = value(base + i);
+            }
             __syncthreads();
             if (tid < kWave) {
                 for (int c0 = 0; c0 < len; c0 += kWave) {
@@ -1385,9 +1776,11 @@ __global__ __launch_bounds__(kScanThreads) void euclid_exact_scan_kernel(StageAr
             }
             __syncthreads();
         }
-        if (tid == 0) {
-            o_code = id;
-            o_code_v = mx;
+        if (tid == 0 && (slow || tie)) {
+            if (slow) {
+                o_code = id;
+                o_code_v = mx;
+            }
             // the kept set, best first, ties by index
             int used[4] = {-1, -1, -1, -1};
             const int nk = RECIPE == DIRECT ? kept : ktop;
@@ -1422,7 +1815,7 @@ __global__ __launch_bounds__(kScanThreads) void euclid_exact_scan_kernel(StageAr
             }
         }
         if (a.xout)
-            for (int k = tid; k < K; k += kScanThreads)
+            for (int k = tid; k < K; k += ST)
                 a.xout[m * K + k] = __fsub_rn(a.xin[m * K + k], a.cbf[static_cast<int64_t>(use) * K + k]);
     }
 }
@@ -1925,6 +2318,8 @@ __global__ __launch_bounds__(kWave) void euclid_refine_select_kernel(StageArgs a
              euclid_refine_values_kernel<DIRECT, false, KS>, euclid_refine_values_kernel<HIGGS, true, KS>},     \
             {euclid_refine_select_kernel<OMNI, false, KS>, euclid_refine_select_kernel<HIGGS, false, KS>,       \
              euclid_refine_select_kernel<DIRECT, false, KS>, euclid_refine_select_kernel<HIGGS, true, KS>},     \
+            {euclid_scan_values_kernel<OMNI, false, KS>, euclid_scan_values_kernel<HIGGS, false, KS>,           \
+             euclid_scan_values_kernel<DIRECT, false, KS>, euclid_scan_values_kernel<HIGGS, true, KS>},         \
             {euclid_exact_scan_kernel<OMNI, false, KS>, euclid_exact_scan_kernel<HIGGS, false, KS>,             \
              euclid_exact_scan_kernel<DIRECT, false, KS>, euclid_exact_scan_kernel<HIGGS, true, KS>},           \
             Tile<KS>::LDS,                                                                                      \

@@ -20,8 +20,9 @@ struct aq_ctx {
     // Work buffers owned by the context, grown on demand (slot 0: residual
     // cascade, 1: per-stage failure counters and lists, 2: projected queries,
     // 3: refine-pass keys, 4: sweep keys and frame norms, 5: gathered
-    // strided input rows of a DAC encode).
-    static constexpr int kScratchSlots = 6;
+    // strided input rows of a DAC encode, 6: exact values of the frames an
+    // exact scan takes).
+    static constexpr int kScratchSlots = 7;
     // Per-stage counters of the last Euclidean encode on this context (in
     // slot 1, or in the no-allocation scratch).
     int32_t *euclid_counts = nullptr;

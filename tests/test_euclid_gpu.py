@@ -322,6 +322,54 @@ def test_topk_tie_at_kth_place_follows_ggml_heap(torch, ctx, oracle, cb_type):
     assert out["fails"][0] == M
 
 
+@pytest.mark.parametrize("recipe,cb_type,topk,dup,inf", [
+    (1, 0, 4, 3, False), (1, 1, 4, 3, False), (1, 0, 3, 2, False), (1, 0, 2, 3, False), (1, 0, 1, 3, False),
+    (1, 0, 3, 3, True), (2, 0, 0, 3, True), (0, 0, 0, 3, True)])
+@pytest.mark.parametrize("N,M", [(2048, 40), (2048, 150), (4096, 40), (4096, 150)])
+def test_exact_scan_with_repeated_codes(torch, ctx, oracle, recipe, cb_type, topk, dup, inf, N, M):
+    """Every codeword appears dup times, so each frame's best value ties
+    exactly with dup - 1 others.  When the k-th and (k+1)-th places tie too
+    (k not a multiple of dup), no certificate settles the frame: every frame
+    of both stages goes to the exact scan, and ggml_top_k's heap (of k = 1
+    to 4 entries) decides which copy stays.  Otherwise (inf) a -inf codebook
+    entry (no NaN: the queries' first element is positive) makes the
+    codebook non-finite, which sends every frame to the scan too.  Up to 64
+    frames per stage take values computed over the whole grid, more are
+    evaluated by their own block; 2048 codes fit the scan's LDS chunk, 4096
+    do not.  The ggml argmax takes the last tied index, DIRECT the first."""
+    from aqmi import synth
+
+    print(f"[gpu] repeated codes recipe={recipe} cb_type={cb_type} topk={topk} dup={dup} inf={inf} N={N} M={M}",
+          flush=True)
+    Q, K = 2, 256
+    rep = np.arange(N) // dup * dup
+    if cb_type == 1:
+        cb = np.stack([synth.q8_0_random_codebook(71, 10 + s, N, K) for s in range(Q)])[:, rep]
+        x = (synth.q8_0_dequantize(cb[0])[(7 * np.arange(M)) % N] + synth.normal(71, 2, (M, K), 0.05)).astype(np.float32)
+        cfg = dict(x=x, M=M, K=K, Q=Q, N=N, codebook_q8=cb)
+    else:
+        cb = np.ascontiguousarray(synth.normal(71, 3, (Q, N, K), 1.0 / 16)[:, rep])
+        x = synth.normal(71, 1, (M, K), 1.0)
+        if inf:
+            cb[0, 5, 0] = -np.inf
+            x[:, 0] = np.abs(x[:, 0]) + 0.25
+        cfg = dict(x=x, M=M, K=K, Q=Q, N=N, codebook=cb)
+    out = run(torch, ctx, cb, recipe, x, cb_type=cb_type, topk=topk)
+    ref = {0: oracle.euclid_rvq, 1: oracle.higgs_rvq, 2: oracle.direct_rvq}[recipe]
+    ref = ref(cfg, topk=topk) if recipe == 1 else ref(cfg)
+    scans = out["cbs"].exact_scans()
+    print(f"[gpu] exact scans per stage {scans.tolist()}", flush=True)
+    assert (scans >= 0.9 * M).all()
+    assert np.array_equal(out["idx"], ref["idx"])
+    assert np.array_equal(bits(out["residual"]), bits(ref["residual"]))
+    if recipe == 0:
+        assert np.array_equal(bits(out["dist"]), bits(-ref["logit"]))
+    else:
+        assert np.array_equal(bits(out["dist"]), bits(ref["dist"]))
+    if topk:
+        check_topk(out, ref)
+
+
 def test_ema_codebook_and_upload(torch, ctx, oracle):
     """aq_ema_codebook bit for bit against the oracle (usage below eps, zero,
     NaN), and aq_euclid_upload_ema encoding exactly like an upload of the
