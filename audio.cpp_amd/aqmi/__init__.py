@@ -32,7 +32,7 @@ EXPORTED = [
     "aq_euclid_decode", "aq_ctx_set_timing", "aq_ctx_read_timing",
     "aq_moss_upload", "aq_moss_release", "aq_moss_encode", "aq_moss_decode",
     "aq_euclid_encode_strided", "aq_euclid_upload_projected", "aq_euclid_encode_noalloc",
-    "aq_dac_encode_ex", "aq_dac_decode_ex",
+    "aq_dac_encode_ex", "aq_dac_decode_ex", "aq_euclid_upload_device", "aq_weight_norm_fold",
 ]
 
 # aq_euclid_recipe / aq_codebook_type
@@ -78,6 +78,8 @@ def load_library(path: str | pathlib.Path | None = None) -> C.CDLL:
     lib.aq_codebook_gather.argtypes = [vp, vp, i64, vp, i64, vp]
     lib.aq_ema_codebook.argtypes = [vp, vp, vp, i64, i64, i64, C.c_float, vp]
     lib.aq_euclid_upload_ema.argtypes = [vp, i64, i64, i64, vp, vp, C.c_float, C.c_int, C.POINTER(vp)]
+    lib.aq_euclid_upload_device.argtypes = [vp, i64, i64, i64, C.c_int, vp, C.c_int, C.POINTER(vp)]
+    lib.aq_weight_norm_fold.argtypes = [vp, vp, vp, i64, i64, C.c_int, vp]
     lib.aq_euclid_decode.argtypes = [vp, vp, vp, i64, vp]
     lib.aq_euclid_encode_noalloc.argtypes = [vp, vp, vp, i64, vp, vp, vp, C.c_int, vp, vp, vp]
     lib.aq_euclid_encode_strided.argtypes = [vp, vp, vp, i64, i64, i64, i64, i64, vp, vp, vp, C.c_int, vp, vp, vp]
@@ -320,6 +322,26 @@ class Codebooks:
         return self
 
     @classmethod
+    def from_device(cls, ctx: Context, codebook, recipe: int, cb_type: int = CB_F32, shape=None):
+        """aq_euclid_upload_device: codebook a device tensor, float32 [Q, N, K]
+        (CB_F32) or the raw block_q8_0 bytes (uint8, CB_Q8_0; shape = (Q, N, K))."""
+        self = cls.__new__(cls)
+        self.ctx = ctx
+        if cb_type == CB_F32:
+            self.Q, self.N, self.K = codebook.shape
+        else:
+            self.Q, self.N, self.K = shape
+            assert codebook.numel() == self.Q * self.N * self.K // 32 * 34
+        self.recipe = recipe
+        self.H = self.K
+        h = C.c_void_p()
+        ctx.use_current_stream()
+        ctx.check(ctx.lib.aq_euclid_upload_device(ctx.h, self.Q, self.N, self.K, cb_type, _dptr(codebook), recipe,
+                                                  C.byref(h)))
+        self.h = h
+        return self
+
+    @classmethod
     def from_ema(cls, ctx: Context, embedding_sum, cluster_usage, recipe: int, eps: float = 1.0e-5):
         """aq_euclid_upload_ema: codebooks materialised from EMA statistics
         (embedding_sum [Q, N, K], cluster_usage [Q, N], host float32)."""
@@ -395,6 +417,18 @@ class Codebooks:
             self.close()
         except Exception:
             pass
+
+
+# aq_wn_rule
+WN_OUTETTS, WN_MOSS = 0, 1
+
+
+def weight_norm_fold(ctx: Context, v, g, rule: int, out):
+    """aq_weight_norm_fold on device tensors: v [rows, ...] (the trailing axes
+    are one row), g [rows]; out like v (may be v)."""
+    rows = v.shape[0]
+    ctx.use_current_stream()
+    ctx.check(ctx.lib.aq_weight_norm_fold(ctx.h, _dptr(v), _dptr(g), rows, v.numel() // rows, rule, _dptr(out)))
 
 
 def ema_codebook(ctx: Context, embedding_sum, cluster_usage, eps: float, out):

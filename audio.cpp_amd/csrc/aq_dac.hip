@@ -555,6 +555,71 @@ __global__ __launch_bounds__(kMaxBlock, 1) void dac_encode_kernel(
     }
 }
 
+// Stage images of the cosine quantizer, built on the device at upload.
+// W_in [Q][8][D] goes to both images: the vec_dot order's layout (element
+// (r, d) at ((d/64 * 2 + r/4) * 64 + d%64) * 4 + r%4) and the tinyBLAS
+// order's (row r, d = 16 * (4 * u4 + c) + t at ((r * 16 + t) * DI + sw) * 4
+// + c, DI = D / 64, sw = u4 ^ (t & (DI - 1)) for a power-of-two DI).
+__global__ void dac_image_win_kernel(const float *__restrict__ w_in, int64_t Q, int64_t D, int64_t img_f,
+                                     float *__restrict__ images, float *__restrict__ images_tb) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= Q * 8 * D) return;
+    const int64_t s = t / (8 * D), e = t % (8 * D);
+    const int r = static_cast<int>(e / D);
+    const int64_t d = e % D;
+    const float w = w_in[t];
+    images[s * img_f + ((d / kWave * 2 + r / 4) * kWave + d % kWave) * 4 + r % 4] = w;
+    const int64_t DI = D / kWave;
+    const int64_t tt = d % 16, u4 = (d / 16) / 4, c = (d / 16) % 4;
+    const int64_t sw = (DI & (DI - 1)) == 0 ? (u4 ^ (tt & (DI - 1))) : u4;
+    images_tb[s * img_f + ((r * 16 + tt) * DI + sw) * 4 + c] = w;
+}
+
+// b_in and the recipe's normalised codebook rows, the same in both images
+// (all recipes: double sum of squares, float products):
+//   Fish      inv = sum > 0 ? (float)(1 / sqrt(sum)) : 0   (fish_audio/codec.cpp:171-189)
+//   IndexTTS2 inv = 1.0F / (float)sqrt(sum)               (index_tts2/semantic_codec.cpp:43-58)
+//   Vevo2     inv = (float)(1 / sqrt(sum)), a zero row is an error (vevo2/components.cpp:566-590)
+// Code n's element 4q + t sits at ((n/64 * 2 + q) * 64 + n%64) * 4 + t after
+// the 2D + 2 float4 of W_in and b_in.  flags[0]: lowest s * N + n of a zero
+// Vevo2 row (atomicMin); flags[1] = 1 on a non-finite normalised entry.
+__global__ void dac_image_cb_kernel(const float *__restrict__ codebook, const float *__restrict__ b_in, int64_t Q,
+                                    int64_t N, int64_t D, int64_t img_f, int recipe, float *__restrict__ images,
+                                    float *__restrict__ images_tb, unsigned long long *__restrict__ flags) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t < Q * 8) {
+        const int64_t s = t / 8;
+        const float b = b_in ? b_in[t] : 0.0f;
+        images[s * img_f + 8 * D + t % 8] = b;
+        images_tb[s * img_f + 8 * D + t % 8] = b;
+    }
+    if (t >= Q * N) return;
+    const int64_t s = t / N, n = t % N;
+    const float *C = codebook + t * 8;
+    double sum = 0.0;
+    for (int k = 0; k < 8; ++k) sum = __dadd_rn(sum, __dmul_rn(static_cast<double>(C[k]), static_cast<double>(C[k])));
+    float inv;
+    if (recipe == AQ_DAC_INDEXTTS2) {
+        inv = __fdiv_rn(1.0f, static_cast<float>(sqrt_rn(sum)));
+    } else if (recipe == AQ_DAC_VEVO2) {
+        const double norm = sqrt_rn(sum);
+        if (norm == 0.0) atomicMin(&flags[0], static_cast<unsigned long long>(t));
+        inv = static_cast<float>(__ddiv_rn(1.0, norm));
+    } else {
+        inv = sum > 0.0 ? static_cast<float>(__ddiv_rn(1.0, sqrt_rn(sum))) : 0.0f;
+    }
+    const int64_t base = s * img_f + 8 * D + 8, c = n / kWave, L = n % kWave;
+    bool nf = false;
+    for (int q = 0; q < 2; ++q)
+        for (int k = 0; k < 4; ++k) {
+            const float v = __fmul_rn(C[4 * q + k], inv);
+            nf |= !__builtin_isfinite(v);
+            images[base + ((c * 2 + q) * kWave + L) * 4 + k] = v;
+            images_tb[base + ((c * 2 + q) * kWave + L) * 4 + k] = v;
+        }
+    if (nf) flags[1] = 1;
+}
+
 // z[s][n][d] = ((0 + c0*w0) + c1*w1 + ... + c7*w7) (+ b_out[d]): the k = 8
 // mul_mat of the out-projection (scalar leftovers of ggml_vec_dot_f32: each
 // product rounded, then added) followed by the bias add.
@@ -828,65 +893,6 @@ aq_status aq_dac_upload_ex(aq_ctx *ctx, int64_t Q, int64_t D, int64_t N, const f
         return aq_fail(ctx, AQ_E_SHAPE, "aq_dac_upload: N=%lld exceeds 2^20", (long long)N);
     aq_device_guard g(ctx->device);
 
-    // Host-side layout of the per-stage images.  c_hat follows the recipe's
-    // codebook normalisation (all: double sum of squares, float products):
-    //   Fish      inv = sum > 0 ? (float)(1 / sqrt(sum)) : 0   (fish_audio/codec.cpp:171-189)
-    //   IndexTTS2 inv = 1.0F / (float)sqrt(sum)               (index_tts2/semantic_codec.cpp:43-58)
-    //   Vevo2     inv = (float)(1 / sqrt(sum)), zero rows rejected (vevo2/components.cpp:566-590)
-    std::vector<float> images(static_cast<size_t>(Q * img * 4), 0.0f);
-    bool any_nonfinite = false;
-    for (int64_t s = 0; s < Q; ++s) {
-        float *im = images.data() + s * img * 4;
-        const float *Wi = w_in + s * 8 * D;
-        for (int64_t i = 0; i < D / kWave; ++i)
-            for (int q = 0; q < 2; ++q)
-                for (int L = 0; L < kWave; ++L)
-                    for (int t = 0; t < 4; ++t)
-                        im[((i * 2 + q) * kWave + L) * 4 + t] = Wi[(4 * q + t) * D + i * kWave + L];
-        float *bi = im + 2 * D * 4;
-        for (int j = 0; j < 8; ++j) bi[j] = b_in ? b_in[s * 8 + j] : 0.0f;
-        float *ch = im + (2 * D + 2) * 4;
-        const float *C = codebook + s * N * 8;
-        for (int64_t n = 0; n < N; ++n) {
-            double sum = 0.0;
-            for (int k = 0; k < 8; ++k) sum += static_cast<double>(C[n * 8 + k]) * static_cast<double>(C[n * 8 + k]);
-            float inv;
-            if (recipe == AQ_DAC_INDEXTTS2) {
-                inv = 1.0f / static_cast<float>(std::sqrt(sum));
-            } else if (recipe == AQ_DAC_VEVO2) {
-                const double norm = std::sqrt(sum);
-                if (norm == 0.0)
-                    return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_dac_upload: codebook row %lld of stage %lld has zero norm",
-                                   (long long)n, (long long)s);
-                inv = static_cast<float>(1.0 / norm);
-            } else {
-                inv = sum > 0.0 ? static_cast<float>(1.0 / std::sqrt(sum)) : 0.0f;
-            }
-            const int64_t c = n / kWave, L = n % kWave;
-            for (int q = 0; q < 2; ++q)
-                for (int t = 0; t < 4; ++t) {
-                    const float v = C[n * 8 + 4 * q + t] * inv;
-                    ch[((c * 2 + q) * kWave + L) * 4 + t] = v;
-                    if (!std::isfinite(v)) any_nonfinite = true;
-                }
-        }
-    }
-
-    // The same images with W_in in the tinyBLAS order's layout (see tb_sw).
-    std::vector<float> images_tb(images);
-    for (int64_t s = 0; s < Q; ++s) {
-        float *im = images_tb.data() + s * img * 4;
-        const float *Wi = w_in + s * 8 * D;
-        const int DI = static_cast<int>(D / kWave);
-        for (int j = 0; j < 8; ++j)
-            for (int t = 0; t < 16; ++t)
-                for (int u4 = 0; u4 < DI; ++u4) {
-                    const int sw = (DI & (DI - 1)) == 0 ? (u4 ^ (t & (DI - 1))) : u4;
-                    for (int c = 0; c < 4; ++c)
-                        im[((j * 16 + t) * DI + sw) * 4 + c] = Wi[j * D + 16 * (4 * u4 + c) + t];
-                }
-    }
-
     aq_dac_stages *st = new (std::nothrow) aq_dac_stages();
     if (!st) return aq_fail(ctx, AQ_E_NOMEM, "aq_dac_upload: host allocation failed");
     st->ctx = ctx;
@@ -894,7 +900,6 @@ aq_status aq_dac_upload_ex(aq_ctx *ctx, int64_t Q, int64_t D, int64_t N, const f
     st->D = D;
     st->N = N;
     st->has_bin = b_in != nullptr;
-    st->exact_only = any_nonfinite;
     st->recipe = recipe;
     st->qeps = recipe == AQ_DAC_INDEXTTS2 ? 0.0f : (recipe == AQ_DAC_VEVO2 ? 1.0e-20f : 1.0e-12f);
     st->cbg = cbg;
@@ -911,28 +916,44 @@ aq_status aq_dac_upload_ex(aq_ctx *ctx, int64_t Q, int64_t D, int64_t N, const f
         st->margin = 5.0e-6f + std::ldexp(1.001f, bits - 22);
     }
     st->img_f4 = img;
-    float *d_cb = nullptr, *d_wout = nullptr, *d_bout = nullptr;
+    // The host arrays go to the device as given; the stage images and the
+    // out-projection tables are built there.
+    const size_t img_bytes = sizeof(float) * static_cast<size_t>(Q * img * 4);
+    float *d_cb = nullptr, *d_win = nullptr, *d_bin = nullptr, *d_wout = nullptr, *d_bout = nullptr;
+    unsigned long long *d_flags = nullptr;
     auto cleanup = [&]() {
-        if (d_cb) (void)hipFree(d_cb);
-        if (d_wout) (void)hipFree(d_wout);
-        if (d_bout) (void)hipFree(d_bout);
+        for (void *p : {static_cast<void *>(d_cb), static_cast<void *>(d_win), static_cast<void *>(d_bin),
+                        static_cast<void *>(d_wout), static_cast<void *>(d_bout), static_cast<void *>(d_flags)})
+            if (p) (void)hipFree(p);
     };
-    if (hipMalloc(&st->d_images, images.size() * sizeof(float)) != hipSuccess ||
-        hipMalloc(&st->d_images_tb, images_tb.size() * sizeof(float)) != hipSuccess ||
+    if (hipMalloc(&st->d_images, img_bytes) != hipSuccess || hipMalloc(&st->d_images_tb, img_bytes) != hipSuccess ||
+        hipMalloc(&d_cb, sizeof(float) * static_cast<size_t>(Q * N * 8)) != hipSuccess ||
+        hipMalloc(&d_win, sizeof(float) * static_cast<size_t>(Q * 8 * D)) != hipSuccess ||
+        hipMalloc(&d_flags, 2 * sizeof(unsigned long long)) != hipSuccess ||
+        (b_in && hipMalloc(&d_bin, sizeof(float) * static_cast<size_t>(Q * 8)) != hipSuccess) ||
         (w_out && (hipMalloc(&st->d_tables, sizeof(float) * static_cast<size_t>(Q * N * D)) != hipSuccess ||
-                   hipMalloc(&d_cb, sizeof(float) * static_cast<size_t>(Q * N * 8)) != hipSuccess ||
                    hipMalloc(&d_wout, sizeof(float) * static_cast<size_t>(Q * D * 8)) != hipSuccess ||
                    (b_out && hipMalloc(&d_bout, sizeof(float) * static_cast<size_t>(Q * D)) != hipSuccess)))) {
         cleanup();
         aq_dac_release(st);
         return aq_fail(ctx, AQ_E_NOMEM, "aq_dac_upload: device allocation failed");
     }
-    bool ok = hipMemcpyAsync(st->d_images, images.data(), images.size() * sizeof(float), hipMemcpyHostToDevice, ctx->stream) == hipSuccess &&
-              hipMemcpyAsync(st->d_images_tb, images_tb.data(), images_tb.size() * sizeof(float), hipMemcpyHostToDevice,
-                             ctx->stream) == hipSuccess;
+    const unsigned long long flags_init[2] = {~0ull, 0ull};
+    bool ok = hipMemcpyAsync(d_cb, codebook, sizeof(float) * static_cast<size_t>(Q * N * 8), hipMemcpyHostToDevice, ctx->stream) == hipSuccess &&
+              hipMemcpyAsync(d_win, w_in, sizeof(float) * static_cast<size_t>(Q * 8 * D), hipMemcpyHostToDevice, ctx->stream) == hipSuccess &&
+              (!b_in || hipMemcpyAsync(d_bin, b_in, sizeof(float) * static_cast<size_t>(Q * 8), hipMemcpyHostToDevice, ctx->stream) == hipSuccess) &&
+              hipMemcpyAsync(d_flags, flags_init, sizeof(flags_init), hipMemcpyHostToDevice, ctx->stream) == hipSuccess &&
+              hipMemsetAsync(st->d_images, 0, img_bytes, ctx->stream) == hipSuccess &&
+              hipMemsetAsync(st->d_images_tb, 0, img_bytes, ctx->stream) == hipSuccess;
+    if (ok) {
+        hipLaunchKernelGGL(dac_image_win_kernel, dim3(static_cast<unsigned>((Q * 8 * D + 255) / 256)), dim3(256), 0,
+                           ctx->stream, d_win, Q, D, img * 4, reinterpret_cast<float *>(st->d_images), reinterpret_cast<float *>(st->d_images_tb));
+        hipLaunchKernelGGL(dac_image_cb_kernel, dim3(static_cast<unsigned>((Q * N + 255) / 256)), dim3(256), 0,
+                           ctx->stream, d_cb, d_bin, Q, N, D, img * 4, recipe, reinterpret_cast<float *>(st->d_images), reinterpret_cast<float *>(st->d_images_tb), d_flags);
+        ok = hipGetLastError() == hipSuccess;
+    }
     if (w_out)
         ok = ok &&
-             hipMemcpyAsync(d_cb, codebook, sizeof(float) * static_cast<size_t>(Q * N * 8), hipMemcpyHostToDevice, ctx->stream) == hipSuccess &&
              hipMemcpyAsync(d_wout, w_out, sizeof(float) * static_cast<size_t>(Q * D * 8), hipMemcpyHostToDevice, ctx->stream) == hipSuccess &&
              (!b_out || hipMemcpyAsync(d_bout, b_out, sizeof(float) * static_cast<size_t>(Q * D), hipMemcpyHostToDevice, ctx->stream) == hipSuccess);
     for (int64_t s = 0; ok && w_out && s < Q; ++s) {
@@ -942,12 +963,21 @@ aq_status aq_dac_upload_ex(aq_ctx *ctx, int64_t Q, int64_t D, int64_t N, const f
                            d_bout ? d_bout + s * D : nullptr, N, D, st->d_tables + s * N * D);
         ok = hipGetLastError() == hipSuccess;
     }
-    ok = ok && hipStreamSynchronize(ctx->stream) == hipSuccess;
+    unsigned long long flags[2] = {~0ull, 0ull};
+    ok = ok && hipMemcpyAsync(flags, d_flags, sizeof(flags), hipMemcpyDeviceToHost, ctx->stream) == hipSuccess &&
+         hipStreamSynchronize(ctx->stream) == hipSuccess;
     cleanup();
     if (!ok) {
         aq_dac_release(st);
-        return aq_fail(ctx, AQ_E_DEVICE, "aq_dac_upload: device copy or table preparation failed");
+        return aq_fail(ctx, AQ_E_DEVICE, "aq_dac_upload: device copy or image preparation failed");
     }
+    if (flags[0] != ~0ull) {
+        const long long n = static_cast<long long>(flags[0] % static_cast<unsigned long long>(N)),
+                        s = static_cast<long long>(flags[0] / static_cast<unsigned long long>(N));
+        aq_dac_release(st);
+        return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_dac_upload: codebook row %lld of stage %lld has zero norm", n, s);
+    }
+    st->exact_only = flags[1] != 0;
     *out = st;
     return AQ_OK;
 }

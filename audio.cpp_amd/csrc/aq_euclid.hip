@@ -63,6 +63,88 @@ __global__ void ema_codebook_kernel(const float *__restrict__ esum, const float 
     out[t] = __fdiv_rn(esum[t], denom);
 }
 
+// ------------------------------------------------------ codebook preparation
+
+// block_q8_0 rows {fp16 d; int8 qs[32]} (ggml-common.h:241-246) -> quants,
+// scales and the dequantised codebook q * d (ggml-quants.c:491-505; the
+// product is exact in fp32).  One thread per element.
+__global__ void q8_unpack_kernel(const unsigned char *__restrict__ raw, int64_t nblocks, int8_t *__restrict__ qs,
+                                 float *__restrict__ qd, float *__restrict__ cbf) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= nblocks * 32) return;
+    const int64_t b = t / 32;
+    const int j = static_cast<int>(t % 32);
+    const unsigned char *p = raw + b * 34;
+    const uint16_t h = static_cast<uint16_t>(p[0] | (p[1] << 8));
+    const float d = static_cast<float>(__builtin_bit_cast(_Float16, h));
+    const int8_t q = static_cast<int8_t>(p[2 + j]);
+    qs[t] = q;
+    cbf[t] = __fmul_rn(static_cast<float>(q), d);
+    if (j == 0) qd[b] = d;
+}
+
+// bf16 / fp16 images, round to nearest even (bf16: NaN kept quiet, as a
+// truncation with the quiet bit set).
+__device__ inline uint16_t img_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7F800000u) == 0x7F800000u) return static_cast<uint16_t>((u >> 16) | ((u & 0xFFFFu) ? 0x40u : 0u));
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return static_cast<uint16_t>(u >> 16);
+}
+__device__ inline uint16_t img_f16(float f) { return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f)); }
+template <bool Q8>
+__device__ inline uint16_t img_half(float f) { return Q8 ? img_f16(f) : img_bf16(f); }
+template <bool Q8>
+__device__ inline float img_float(uint16_t h) {
+    return Q8 ? static_cast<float>(__builtin_bit_cast(_Float16, h)) : __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+// Per code row (one thread each): the matrix-core images c_h = half(c) and
+// c_l = half(c - c_h) (bf16 for F32 codebooks, fp16 for Q8_0), the per-code
+// constants -|c|^2 / 2 (sweep), -|c|^2 (OmniVoice bias, double sum of double
+// products) and sum_rows(c * c) (Higgs: fp32 squares summed in double), and
+// per stage the largest |c|, |c_h - c|, |c_h|, |c_l| and |c - c_h - c_l|
+// (as double bit patterns, atomicMax over non-negative values; NaN skipped)
+// for the certificate's bounds.  nonfinite[0] = 1 on any non-finite entry.
+template <bool Q8>
+__global__ void euclid_prep_kernel(const float *__restrict__ cbf, int64_t QN, int64_t N, int K,
+                                   uint16_t *__restrict__ cbh, uint16_t *__restrict__ cbl, float *__restrict__ hh,
+                                   float *__restrict__ bias, float *__restrict__ e2,
+                                   unsigned long long *__restrict__ smax, int32_t *__restrict__ nonfinite) {
+    const int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (r >= QN) return;
+    const int64_t row = r * K;
+    double sq = 0.0, dq = 0.0, hq = 0.0, e2d = 0.0, lq = 0.0, rq = 0.0;
+    bool nf = false;
+    for (int k = 0; k < K; ++k) {
+        const float c = cbf[row + k];
+        nf |= !__builtin_isfinite(c);
+        const uint16_t h = img_half<Q8>(c);
+        cbh[row + k] = h;
+        const float hf = img_float<Q8>(h);
+        // c - c_h and c - c_h - c_l are exact in fp32 (finite c)
+        const float dl = __fsub_rn(c, hf);
+        const uint16_t l = __builtin_isfinite(dl) ? img_half<Q8>(dl) : 0;
+        cbl[row + k] = l;
+        const double ld = img_float<Q8>(l), rd = __dsub_rn(static_cast<double>(dl), ld);
+        const double cd = c, hd = hf, dd = __dsub_rn(hd, cd);
+        sq = __dadd_rn(sq, __dmul_rn(cd, cd));
+        e2d = __dadd_rn(e2d, static_cast<double>(__fmul_rn(c, c)));
+        dq = __dadd_rn(dq, __dmul_rn(dd, dd));
+        hq = __dadd_rn(hq, __dmul_rn(hd, hd));
+        lq = __dadd_rn(lq, __dmul_rn(ld, ld));
+        rq = __dadd_rn(rq, __dmul_rn(rd, rd));
+    }
+    hh[r] = static_cast<float>(__dmul_rn(-0.5, sq));
+    bias[r] = static_cast<float>(-sq);
+    e2[r] = static_cast<float>(e2d);
+    const int64_t s = r / N;
+    const double norms[5] = {sqrt(sq), sqrt(dq), sqrt(hq), sqrt(lq), sqrt(rq)};
+    for (int i = 0; i < 5; ++i)
+        if (norms[i] == norms[i]) atomicMax(&smax[s * 5 + i], static_cast<unsigned long long>(__double_as_longlong(norms[i])));
+    if (nf) nonfinite[0] = 1;
+}
+
 // --------------------------------------------------------------- dispatch
 
 const KsKernels *kernels_for(int ks) {
@@ -78,52 +160,6 @@ const KsKernels *kernels_for(int ks) {
 // Recipe variant index of KsKernels.
 int variant_of(int recipe, bool q8) { return q8 ? 3 : recipe; }
 
-uint16_t to_bf16(float f) {   // round to nearest even (finite inputs)
-    uint32_t u;
-    std::memcpy(&u, &f, 4);
-    if ((u & 0x7F800000u) == 0x7F800000u) return static_cast<uint16_t>((u >> 16) | ((u & 0xFFFFu) ? 0x40u : 0u));
-    u += 0x7FFFu + ((u >> 16) & 1u);
-    return static_cast<uint16_t>(u >> 16);
-}
-float from_bf16(uint16_t h) {
-    const uint32_t u = static_cast<uint32_t>(h) << 16;
-    float f;
-    std::memcpy(&f, &u, 4);
-    return f;
-}
-float from_fp16(uint16_t h) {
-    const uint32_t sign = (static_cast<uint32_t>(h) & 0x8000u) << 16;
-    const uint32_t e = (h >> 10) & 0x1Fu, mant = h & 0x3FFu;
-    uint32_t bits;
-    if (e == 0) {
-        if (mant == 0) {
-            bits = sign;
-        } else {
-            float v = std::ldexp(static_cast<float>(mant), -24);
-            std::memcpy(&bits, &v, 4);
-            bits |= sign;
-        }
-    } else if (e == 31) {
-        bits = sign | 0x7F800000u | (mant << 13);
-    } else {
-        bits = sign | ((e + 112u) << 23) | (mant << 13);
-    }
-    float out;
-    std::memcpy(&out, &bits, 4);
-    return out;
-}
-// fp16 round to nearest even (the Q8_0 codebooks' matrix-core operands).
-uint16_t to_f16(float f) {
-    const _Float16 h = static_cast<_Float16>(f);
-    uint16_t u;
-    std::memcpy(&u, &h, 2);
-    return u;
-}
-float from_f16(uint16_t h) {
-    _Float16 f;
-    std::memcpy(&f, &h, 2);
-    return static_cast<float>(f);
-}
 float round_up(double v) {
     float f = static_cast<float>(v);
     if (static_cast<double>(f) < v) f = std::nextafter(f, INFINITY);
@@ -151,54 +187,27 @@ struct aq_codebooks {
     aq_proj_weights *proj = nullptr;   // project_in / project_out (projected cascades)
 };
 
-extern "C" {
+namespace {
 
-aq_status aq_euclid_upload(aq_ctx *ctx, int64_t Q, int64_t N, int64_t K, int cb_type, const void *data, int recipe,
-                           aq_codebooks **out) {
-    if (!ctx || !out || !data) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_euclid_upload: null argument");
-    *out = nullptr;
+// Shape and type checks shared by the uploads.
+aq_status check_upload(aq_ctx *ctx, const char *fn, int64_t Q, int64_t N, int64_t K, int cb_type, int recipe) {
     if (recipe < AQ_EUCLID_OMNIVOICE || recipe > AQ_EUCLID_DIRECT)
-        return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_euclid_upload: unknown recipe %d", recipe);
+        return aq_fail(ctx, AQ_E_INVALID_ARG, "%s: unknown recipe %d", fn, recipe);
     if (cb_type != AQ_CB_F32 && cb_type != AQ_CB_Q8_0)
-        return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_euclid_upload: unknown codebook type %d", cb_type);
-    const bool q8 = cb_type == AQ_CB_Q8_0;
-    if (q8 && recipe != AQ_EUCLID_HIGGS)
-        return aq_fail(ctx, AQ_E_UNSUPPORTED, "aq_euclid_upload: Q8_0 codebooks follow the Higgs recipe only");
-    const int ks = static_cast<int>(K / 32);
-    const KsKernels *kk = K % 32 == 0 ? kernels_for(ks) : nullptr;
-    if (Q <= 0 || N <= 0 || K <= 0 || !kk)
-        return aq_fail(ctx, AQ_E_SHAPE, "aq_euclid_upload: unsupported shape Q=%lld N=%lld K=%lld (K in {64,256,512,768})",
+        return aq_fail(ctx, AQ_E_INVALID_ARG, "%s: unknown codebook type %d", fn, cb_type);
+    if (cb_type == AQ_CB_Q8_0 && recipe != AQ_EUCLID_HIGGS)
+        return aq_fail(ctx, AQ_E_UNSUPPORTED, "%s: Q8_0 codebooks follow the Higgs recipe only", fn);
+    const KsKernels *kk = K > 0 && K % 32 == 0 ? kernels_for(static_cast<int>(K / 32)) : nullptr;
+    if (Q <= 0 || N <= 0 || !kk)
+        return aq_fail(ctx, AQ_E_SHAPE, "%s: unsupported shape Q=%lld N=%lld K=%lld (K in {64,256,512,768})", fn,
                        (long long)Q, (long long)N, (long long)K);
     if (N % kk->cc != 0 || N > (1 << 20))
-        return aq_fail(ctx, AQ_E_SHAPE, "aq_euclid_upload: N=%lld must be a multiple of %d", (long long)N, kk->cc);
-    aq_device_guard g(ctx->device);
+        return aq_fail(ctx, AQ_E_SHAPE, "%s: N=%lld must be a multiple of %d", fn, (long long)N, kk->cc);
+    return AQ_OK;
+}
 
-    const size_t QNK = static_cast<size_t>(Q * N * K), QN = static_cast<size_t>(Q * N);
-    std::vector<float> cbf(QNK);
-    std::vector<int8_t> qs;
-    std::vector<float> qd;
-    if (q8) {
-        // block_q8_0 {fp16 d; int8 qs[32]} (ggml-common.h:241-246); dequantised
-        // as q * d (ggml-quants.c:491-505).
-        qs.resize(QNK);
-        qd.resize(QNK / 32);
-        const unsigned char *p = static_cast<const unsigned char *>(data);
-        for (size_t b = 0; b < QNK / 32; ++b) {
-            uint16_t h;
-            std::memcpy(&h, p + b * 34, 2);
-            const float d = from_fp16(h);
-            qd[b] = d;
-            for (int j = 0; j < 32; ++j) {
-                const int8_t q = static_cast<int8_t>(p[b * 34 + 2 + j]);
-                qs[b * 32 + j] = q;
-                cbf[b * 32 + j] = static_cast<float>(q) * d;
-            }
-        }
-    } else {
-        std::memcpy(cbf.data(), data, QNK * sizeof(float));
-    }
-    std::vector<uint16_t> cbh(QNK), cbl(QNK);
-    std::vector<float> hh(QN), bias(QN), e2(QN);
+// A codebook set with its device buffers allocated, not yet filled.
+aq_status euclid_alloc(aq_ctx *ctx, int64_t Q, int64_t N, int64_t K, bool q8, int recipe, aq_codebooks **out) {
     aq_codebooks *cb = new (std::nothrow) aq_codebooks();
     if (!cb) return aq_fail(ctx, AQ_E_NOMEM, "aq_euclid_upload: host allocation failed");
     cb->ctx = ctx;
@@ -207,78 +216,128 @@ aq_status aq_euclid_upload(aq_ctx *ctx, int64_t Q, int64_t N, int64_t K, int cb_
     cb->K = K;
     cb->recipe = recipe;
     cb->q8 = q8;
-    cb->cmax.assign(Q, 0.0f);
-    cb->dcmax.assign(Q, 0.0f);
-    cb->chmax.assign(Q, 0.0f);
-    cb->clmax.assign(Q, 0.0f);
-    cb->crmax.assign(Q, 0.0f);
-    bool nonfinite = false;
-    // bf16 images for F32 codebooks, fp16 for Q8_0 (the kernels' Mx<Q8>)
-    uint16_t (*to_half)(float) = q8 ? to_f16 : to_bf16;
-    float (*from_half)(uint16_t) = q8 ? from_f16 : from_bf16;
-    for (int64_t s = 0; s < Q; ++s) {
-        double cm = 0.0, dm = 0.0, hm = 0.0, lm = 0.0, rm = 0.0;
-        for (int64_t n = 0; n < N; ++n) {
-            const size_t row = static_cast<size_t>((s * N + n) * K);
-            double sq = 0.0, dq = 0.0, hq = 0.0, e2d = 0.0, lq = 0.0, rq = 0.0;
-            for (int64_t k = 0; k < K; ++k) {
-                const float c = cbf[row + k];
-                if (!std::isfinite(c)) nonfinite = true;
-                const uint16_t h = to_half(c);
-                cbh[row + k] = h;
-                // c - c_h and c - c_h - c_l are exact in fp32 (finite c)
-                const float dl = c - from_half(h);
-                const uint16_t l = std::isfinite(dl) ? to_half(dl) : 0;
-                cbl[row + k] = l;
-                const double ld = from_half(l), rd = static_cast<double>(dl) - ld;
-                const double cd = c, hd = from_half(h);
-                sq += cd * cd;                                    // OmniVoice: double products
-                e2d += static_cast<double>(c * c);               // sum_rows(c*c): fp32 squares
-                dq += (hd - cd) * (hd - cd);
-                hq += hd * hd;
-                lq += ld * ld;
-                rq += rd * rd;
-            }
-            lm = std::max(lm, std::sqrt(lq));
-            rm = std::max(rm, std::sqrt(rq));
-            hh[s * N + n] = static_cast<float>(-0.5 * sq);
-            bias[s * N + n] = static_cast<float>(-sq);
-            e2[s * N + n] = static_cast<float>(e2d);
-            cm = std::max(cm, std::sqrt(sq));
-            dm = std::max(dm, std::sqrt(dq));
-            hm = std::max(hm, std::sqrt(hq));
-        }
-        cb->cmax[s] = round_up(cm * (1.0 + 1e-6));
-        cb->dcmax[s] = round_up(dm * (1.0 + 1e-6));
-        cb->chmax[s] = round_up(hm * (1.0 + 1e-6));
-        cb->clmax[s] = round_up(lm * (1.0 + 1e-6));
-        cb->crmax[s] = round_up(rm * (1.0 + 1e-6));
-    }
-    cb->exact_only = nonfinite;
+    const size_t QNK = static_cast<size_t>(Q * N * K), QN = static_cast<size_t>(Q * N);
     bool ok = hipMalloc(&cb->d_cbh, QNK * 2) == hipSuccess && hipMalloc(&cb->d_cbl, QNK * 2) == hipSuccess &&
-              hipMalloc(&cb->d_hh, QN * 4) == hipSuccess &&
-              hipMalloc(&cb->d_cbf, QNK * 4) == hipSuccess && hipMalloc(&cb->d_bias, QN * 4) == hipSuccess &&
-              hipMalloc(&cb->d_e2, QN * 4) == hipSuccess;
+              hipMalloc(&cb->d_hh, QN * 4) == hipSuccess && hipMalloc(&cb->d_cbf, QNK * 4) == hipSuccess &&
+              hipMalloc(&cb->d_bias, QN * 4) == hipSuccess && hipMalloc(&cb->d_e2, QN * 4) == hipSuccess;
     if (ok && q8) ok = hipMalloc(&cb->d_q8, QNK) == hipSuccess && hipMalloc(&cb->d_q8d, QNK / 32 * 4) == hipSuccess;
     if (!ok) {
         aq_euclid_release(cb);
         return aq_fail(ctx, AQ_E_NOMEM, "aq_euclid_upload: device allocation failed");
     }
-    ok = hipMemcpy(cb->d_cbh, cbh.data(), QNK * 2, hipMemcpyHostToDevice) == hipSuccess &&
-         hipMemcpy(cb->d_cbl, cbl.data(), QNK * 2, hipMemcpyHostToDevice) == hipSuccess &&
-         hipMemcpy(cb->d_hh, hh.data(), QN * 4, hipMemcpyHostToDevice) == hipSuccess &&
-         hipMemcpy(cb->d_cbf, cbf.data(), QNK * 4, hipMemcpyHostToDevice) == hipSuccess &&
-         hipMemcpy(cb->d_bias, bias.data(), QN * 4, hipMemcpyHostToDevice) == hipSuccess &&
-         hipMemcpy(cb->d_e2, e2.data(), QN * 4, hipMemcpyHostToDevice) == hipSuccess;
-    if (ok && q8)
-        ok = hipMemcpy(cb->d_q8, qs.data(), QNK, hipMemcpyHostToDevice) == hipSuccess &&
-             hipMemcpy(cb->d_q8d, qd.data(), QNK / 32 * 4, hipMemcpyHostToDevice) == hipSuccess;
-    if (!ok) {
-        aq_euclid_release(cb);
-        return aq_fail(ctx, AQ_E_DEVICE, "aq_euclid_upload: host to device copy failed");
+    *out = cb;
+    return AQ_OK;
+}
+
+// Fills the codebook (d_cbf; for Q8_0 also the quants and scales) from
+// `data` in host or device memory (F32 [Q][N][K], or block_q8_0 rows).
+aq_status euclid_fill(aq_ctx *ctx, aq_codebooks *cb, const void *data, hipMemcpyKind kind) {
+    const size_t QNK = static_cast<size_t>(cb->Q * cb->N * cb->K);
+    if (!cb->q8) {
+        AQ_HIP(ctx, hipMemcpyAsync(cb->d_cbf, data, QNK * 4, kind, ctx->stream));
+        return AQ_OK;
+    }
+    const size_t nblocks = QNK / 32;
+    unsigned char *raw = nullptr;
+    if (hipMalloc(&raw, nblocks * 34) != hipSuccess)
+        return aq_fail(ctx, AQ_E_NOMEM, "aq_euclid_upload: device allocation failed");
+    aq_status st = AQ_OK;
+    if (hipMemcpyAsync(raw, data, nblocks * 34, kind, ctx->stream) != hipSuccess) {
+        st = aq_fail(ctx, AQ_E_DEVICE, "aq_euclid_upload: copy of the Q8_0 blocks failed");
+    } else {
+        hipLaunchKernelGGL(q8_unpack_kernel, dim3(static_cast<unsigned>((QNK + 255) / 256)), dim3(256), 0, ctx->stream,
+                           raw, static_cast<int64_t>(nblocks), cb->d_q8, cb->d_q8d, cb->d_cbf);
+        if (hipGetLastError() != hipSuccess || hipStreamSynchronize(ctx->stream) != hipSuccess)
+            st = aq_fail(ctx, AQ_E_DEVICE, "aq_euclid_upload: Q8_0 unpack failed");
+    }
+    (void)hipFree(raw);
+    return st;
+}
+
+// Builds the matrix-core images, the per-code constants and the
+// certificate's per-stage bounds from d_cbf on the device; only the 5 * Q
+// stage maxima and the non-finite flag come back to the host.
+aq_status euclid_prepare(aq_ctx *ctx, aq_codebooks *cb) {
+    const int64_t QN = cb->Q * cb->N;
+    unsigned long long *smax = nullptr;
+    if (hipMalloc(&smax, sizeof(unsigned long long) * (5 * cb->Q + 1)) != hipSuccess)
+        return aq_fail(ctx, AQ_E_NOMEM, "aq_euclid_upload: device allocation failed");
+    int32_t *nonfinite = reinterpret_cast<int32_t *>(smax + 5 * cb->Q);
+    std::vector<unsigned long long> host(5 * cb->Q + 1, 0);
+    aq_status st = AQ_OK;
+    bool ok = hipMemsetAsync(smax, 0, sizeof(unsigned long long) * (5 * cb->Q + 1), ctx->stream) == hipSuccess;
+    if (ok) {
+        const dim3 grid(static_cast<unsigned>((QN + 127) / 128)), block(128);
+        if (cb->q8)
+            hipLaunchKernelGGL(euclid_prep_kernel<true>, grid, block, 0, ctx->stream, cb->d_cbf, QN, cb->N,
+                               static_cast<int>(cb->K), cb->d_cbh, cb->d_cbl, cb->d_hh, cb->d_bias, cb->d_e2, smax,
+                               nonfinite);
+        else
+            hipLaunchKernelGGL(euclid_prep_kernel<false>, grid, block, 0, ctx->stream, cb->d_cbf, QN, cb->N,
+                               static_cast<int>(cb->K), cb->d_cbh, cb->d_cbl, cb->d_hh, cb->d_bias, cb->d_e2, smax,
+                               nonfinite);
+        ok = hipGetLastError() == hipSuccess &&
+             hipMemcpyAsync(host.data(), smax, sizeof(unsigned long long) * host.size(), hipMemcpyDeviceToHost,
+                            ctx->stream) == hipSuccess &&
+             hipStreamSynchronize(ctx->stream) == hipSuccess;
+    }
+    (void)hipFree(smax);
+    if (!ok) return aq_fail(ctx, AQ_E_DEVICE, "aq_euclid_upload: codebook preparation failed");
+    auto bound = [&](int64_t s, int i) {
+        double v;
+        std::memcpy(&v, &host[s * 5 + i], 8);
+        return round_up(v * (1.0 + 1e-6));
+    };
+    cb->cmax.resize(cb->Q);
+    cb->dcmax.resize(cb->Q);
+    cb->chmax.resize(cb->Q);
+    cb->clmax.resize(cb->Q);
+    cb->crmax.resize(cb->Q);
+    for (int64_t s = 0; s < cb->Q; ++s) {
+        cb->cmax[s] = bound(s, 0);
+        cb->dcmax[s] = bound(s, 1);
+        cb->chmax[s] = bound(s, 2);
+        cb->clmax[s] = bound(s, 3);
+        cb->crmax[s] = bound(s, 4);
+    }
+    int32_t nf;
+    std::memcpy(&nf, &host[5 * cb->Q], 4);
+    cb->exact_only = nf != 0;
+    return st;
+}
+
+aq_status euclid_upload_from(aq_ctx *ctx, const char *fn, int64_t Q, int64_t N, int64_t K, int cb_type,
+                             const void *data, hipMemcpyKind kind, int recipe, aq_codebooks **out) {
+    if (!ctx || !out || !data) return aq_fail(ctx, AQ_E_INVALID_ARG, "%s: null argument", fn);
+    *out = nullptr;
+    aq_status st = check_upload(ctx, fn, Q, N, K, cb_type, recipe);
+    if (st != AQ_OK) return st;
+    aq_device_guard g(ctx->device);
+    aq_codebooks *cb = nullptr;
+    st = euclid_alloc(ctx, Q, N, K, cb_type == AQ_CB_Q8_0, recipe, &cb);
+    if (st == AQ_OK) st = euclid_fill(ctx, cb, data, kind);
+    if (st == AQ_OK) st = euclid_prepare(ctx, cb);
+    if (st != AQ_OK) {
+        if (cb) aq_euclid_release(cb);
+        return st;
     }
     *out = cb;
     return AQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+aq_status aq_euclid_upload(aq_ctx *ctx, int64_t Q, int64_t N, int64_t K, int cb_type, const void *data, int recipe,
+                           aq_codebooks **out) {
+    return euclid_upload_from(ctx, "aq_euclid_upload", Q, N, K, cb_type, data, hipMemcpyHostToDevice, recipe, out);
+}
+
+aq_status aq_euclid_upload_device(aq_ctx *ctx, int64_t Q, int64_t N, int64_t K, int cb_type, const void *data,
+                                  int recipe, aq_codebooks **out) {
+    return euclid_upload_from(ctx, "aq_euclid_upload_device", Q, N, K, cb_type, data, hipMemcpyDeviceToDevice, recipe,
+                              out);
 }
 
 aq_status aq_ema_codebook(aq_ctx *ctx, const float *embedding_sum, const float *cluster_usage, int64_t Q, int64_t N,
@@ -298,26 +357,33 @@ aq_status aq_euclid_upload_ema(aq_ctx *ctx, int64_t Q, int64_t N, int64_t K, con
                                const float *cluster_usage, float eps, int recipe, aq_codebooks **out) {
     if (!ctx || !out || !embedding_sum || !cluster_usage)
         return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_euclid_upload_ema: null argument");
-    if (Q <= 0 || N <= 0 || K <= 0) return aq_fail(ctx, AQ_E_SHAPE, "aq_euclid_upload_ema: empty shape");
+    *out = nullptr;
+    aq_status st = check_upload(ctx, "aq_euclid_upload_ema", Q, N, K, AQ_CB_F32, recipe);
+    if (st != AQ_OK) return st;
     aq_device_guard g(ctx->device);
     const size_t QNK = static_cast<size_t>(Q * N * K), QN = static_cast<size_t>(Q * N);
-    float *d = nullptr;
-    if (hipMalloc(&d, (2 * QNK + QN) * sizeof(float)) != hipSuccess)
-        return aq_fail(ctx, AQ_E_NOMEM, "aq_euclid_upload_ema: device allocation failed");
-    std::vector<float> cb(QNK);
-    aq_status st = AQ_OK;
-    if (hipMemcpy(d, embedding_sum, QNK * 4, hipMemcpyHostToDevice) != hipSuccess ||
-        hipMemcpy(d + QNK, cluster_usage, QN * 4, hipMemcpyHostToDevice) != hipSuccess) {
-        st = aq_fail(ctx, AQ_E_DEVICE, "aq_euclid_upload_ema: host to device copy failed");
-    } else {
-        st = aq_ema_codebook(ctx, d, d + QNK, Q, N, K, eps, d + QNK + QN);
-        if (st == AQ_OK && (hipStreamSynchronize(ctx->stream) != hipSuccess ||
-                            hipMemcpy(cb.data(), d + QNK + QN, QNK * 4, hipMemcpyDeviceToHost) != hipSuccess))
-            st = aq_fail(ctx, AQ_E_DEVICE, "aq_euclid_upload_ema: device to host copy failed");
-    }
-    (void)hipFree(d);
+    aq_codebooks *cb = nullptr;
+    st = euclid_alloc(ctx, Q, N, K, false, recipe, &cb);
     if (st != AQ_OK) return st;
-    return aq_euclid_upload(ctx, Q, N, K, AQ_CB_F32, cb.data(), recipe, out);
+    // the inputs go to the device once; the codebook is materialised straight
+    // into the set's fp32 buffer and prepared there
+    float *d = nullptr;
+    if (hipMalloc(&d, (QNK + QN) * sizeof(float)) != hipSuccess) {
+        aq_euclid_release(cb);
+        return aq_fail(ctx, AQ_E_NOMEM, "aq_euclid_upload_ema: device allocation failed");
+    }
+    if (hipMemcpyAsync(d, embedding_sum, QNK * 4, hipMemcpyHostToDevice, ctx->stream) != hipSuccess ||
+        hipMemcpyAsync(d + QNK, cluster_usage, QN * 4, hipMemcpyHostToDevice, ctx->stream) != hipSuccess)
+        st = aq_fail(ctx, AQ_E_DEVICE, "aq_euclid_upload_ema: host to device copy failed");
+    if (st == AQ_OK) st = aq_ema_codebook(ctx, d, d + QNK, Q, N, K, eps, cb->d_cbf);
+    if (st == AQ_OK) st = euclid_prepare(ctx, cb);
+    (void)hipFree(d);
+    if (st != AQ_OK) {
+        aq_euclid_release(cb);
+        return st;
+    }
+    *out = cb;
+    return AQ_OK;
 }
 
 aq_status aq_euclid_upload_projected(aq_ctx *ctx, int64_t Q, int64_t N, int64_t K, int64_t H, int cb_type,

@@ -376,6 +376,45 @@ __global__ __launch_bounds__(kWave *kHW) void moss_cascade_kernel(aq_moss_args a
 // Constructor tables (:77-115): per stage, comb[o][0..7] = sum_j w_op[o][j]
 // w_out[j][k] and comb[o][8] = sum_j w_op[o][j] b_out[j] (fp32, from 0, in
 // order), then table[n][o] = comb[o][8] + sum_k comb[o][k] c[n][k].
+// Weight-norm folding w = g v / |v| per output row (one thread per row, the
+// reference's sequential double sum of double squares):
+//   AQ_WN_OUTETTS  scale = g / (float)sqrt(norm2), fp32 division
+//                  (fold_weight_norm, community_models/outetts/dac.cpp:91-110)
+//   AQ_WN_MOSS     scale = (float)(g / sqrt(norm)), double division
+//                  (reconstruct_weight_norm, audio_tokenizer_quantizer.cpp:17-39)
+// then w = v * scale in fp32.
+__global__ void weight_norm_fold_kernel(const float *v, const float *__restrict__ g, int64_t rows,
+                                        int64_t cols, int rule, float *w) {
+    const int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (r >= rows) return;
+    const float *vr = v + r * cols;
+    double norm = 0.0;
+    for (int64_t k = 0; k < cols; ++k) {
+        const double x = vr[k];
+        norm = __dadd_rn(norm, __dmul_rn(x, x));
+    }
+    const double root = aq_math::sqrt_rn(norm);
+    const float scale = rule == AQ_WN_OUTETTS ? __fdiv_rn(g[r], static_cast<float>(root))
+                                              : static_cast<float>(__ddiv_rn(static_cast<double>(g[r]), root));
+    for (int64_t k = 0; k < cols; ++k) w[r * cols + k] = __fmul_rn(vr[k], scale);
+}
+
+// Codebook rows normalised once, in double (audio_tokenizer_quantizer.cpp
+// :116-130): scale = 1 / std::max(sqrt(sum c*c), 1e-12), tn = (float)(c *
+// scale).  One thread per row.
+__global__ void moss_normalize_kernel(const float *__restrict__ cb, int64_t rows, float *__restrict__ tn) {
+    const int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (r >= rows) return;
+    double norm = 0.0;
+    for (int k = 0; k < 8; ++k) {
+        const double c = cb[r * 8 + k];
+        norm = __dadd_rn(norm, __dmul_rn(c, c));
+    }
+    const double n = aq_math::sqrt_rn(norm);
+    const double scale = __ddiv_rn(1.0, n < 1.0e-12 ? 1.0e-12 : n);   // std::max: NaN stays
+    for (int k = 0; k < 8; ++k) tn[r * 8 + k] = static_cast<float>(__dmul_rn(static_cast<double>(cb[r * 8 + k]), scale));
+}
+
 __global__ void moss_combine_kernel(const float *__restrict__ w_op, const float *__restrict__ w_out,
                                     const float *__restrict__ b_out, int Q, int C, int R, float *__restrict__ comb) {
     const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -478,6 +517,20 @@ constexpr int64_t kMossMaxR = 1024;
 
 extern "C" {
 
+aq_status aq_weight_norm_fold(aq_ctx *ctx, const float *v, const float *g, int64_t rows, int64_t cols, int rule,
+                              float *w) {
+    if (!ctx || !v || !g || !w) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_weight_norm_fold: null argument");
+    if (rule != AQ_WN_OUTETTS && rule != AQ_WN_MOSS)
+        return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_weight_norm_fold: unknown rule %d", rule);
+    if (rows <= 0 || cols <= 0 || rows > (int64_t{1} << 31) - 1)
+        return aq_fail(ctx, AQ_E_SHAPE, "aq_weight_norm_fold: rows=%lld cols=%lld", (long long)rows, (long long)cols);
+    aq_device_guard gd(ctx->device);
+    hipLaunchKernelGGL(weight_norm_fold_kernel, dim3(static_cast<unsigned>((rows + 63) / 64)), dim3(64), 0, ctx->stream,
+                       v, g, rows, cols, rule, w);
+    AQ_HIP(ctx, hipGetLastError());
+    return AQ_OK;
+}
+
 aq_status aq_moss_upload(aq_ctx *ctx, int64_t Q, int64_t N, int64_t code_dim, int64_t rvq_dim, const float *input_w,
                          const float *input_b, const float *in_w, const float *in_b, const float *codebook,
                          const float *out_w, const float *out_b, const float *output_w, const float *output_b,
@@ -497,14 +550,6 @@ aq_status aq_moss_upload(aq_ctx *ctx, int64_t Q, int64_t N, int64_t code_dim, in
                        (long long)N, (long long)code_dim, (long long)rvq_dim);
     aq_device_guard g(ctx->device);
     const int64_t C = code_dim, R = rvq_dim;
-    // codebook rows normalised once, in double (:116-130)
-    std::vector<float> tn(static_cast<size_t>(Q * N * 8));
-    for (int64_t n = 0; n < Q * N; ++n) {
-        double norm = 0.0;
-        for (int k = 0; k < 8; ++k) norm = norm + static_cast<double>(codebook[n * 8 + k]) * codebook[n * 8 + k];
-        const double scale = 1.0 / std::max(std::sqrt(norm), 1.0e-12);
-        for (int k = 0; k < 8; ++k) tn[n * 8 + k] = static_cast<float>(codebook[n * 8 + k] * scale);
-    }
     const int64_t sizes[] = {R * C, R, Q * 8 * R, Q * 8, Q * N * 8, Q * N * 8, Q * R * 8, Q * R, C};
     int64_t total = 0;
     for (int64_t s : sizes) total += (s + 63) / 64 * 64;
@@ -520,7 +565,8 @@ aq_status aq_moss_upload(aq_ctx *ctx, int64_t Q, int64_t N, int64_t code_dim, in
                        (long long)(total * 4));
     }
     float **slots[] = {&q->d_wip, &q->d_bip, &q->d_win, &q->d_bin, &q->d_cb, &q->d_tn, &q->d_wout, &q->d_bout, &q->d_bop};
-    const float *srcs[] = {input_w, input_b, in_w, in_b, codebook, tn.data(), out_w, out_b, output_b};
+    // the normalised codebook (slot 5) is built on the device below
+    const float *srcs[] = {input_w, input_b, in_w, in_b, codebook, nullptr, out_w, out_b, output_b};
     int64_t off = 0;
     bool ok = true;
     for (int i = 0; i < 9; ++i) {
@@ -529,6 +575,11 @@ aq_status aq_moss_upload(aq_ctx *ctx, int64_t Q, int64_t N, int64_t code_dim, in
             ok = ok && hipMemcpyAsync(*slots[i], srcs[i], static_cast<size_t>(sizes[i]) * sizeof(float),
                                       hipMemcpyHostToDevice, ctx->stream) == hipSuccess;
         off += (sizes[i] + 63) / 64 * 64;
+    }
+    if (ok) {
+        hipLaunchKernelGGL(moss_normalize_kernel, dim3(static_cast<unsigned>((Q * N + 255) / 256)), dim3(256), 0,
+                           ctx->stream, q->d_cb, Q * N, q->d_tn);
+        ok = hipGetLastError() == hipSuccess;
     }
     float *d_wop = nullptr;
     float *d_comb = nullptr;

@@ -240,11 +240,18 @@ typedef enum aq_codebook_type {
 
 /* Upload Q codebooks of N codes of dimension K from host memory (upload
  * once; replaces BackendWeightStore loads, backend_weight_store.h:272-392,
- * and the per-call codebook set-up of the host loops).
+ * and the per-call codebook set-up of the host loops).  The data goes to
+ * the device as given; Q8_0 blocks are unpacked and every derived image and
+ * constant is built there (only 5 bounds per stage come back).
  * Supported: K in {64, 256, 512, 768}; N a multiple of 256, 64, 32, 16
  * respectively; Q8_0 with AQ_EUCLID_HIGGS only. */
 aq_status aq_euclid_upload(aq_ctx *ctx, int64_t Q, int64_t N, int64_t K, int cb_type, const void *data,
                            int recipe, aq_codebooks **out);
+/* aq_euclid_upload from device memory (a codebook already resident, e.g.
+ * read by aq_gguf_* into a device buffer or produced by a graph): data is a
+ * device pointer of the same layout, copied on the context's stream. */
+aq_status aq_euclid_upload_device(aq_ctx *ctx, int64_t Q, int64_t N, int64_t K, int cb_type, const void *data,
+                                  int recipe, aq_codebooks **out);
 aq_status aq_euclid_release(aq_codebooks *cb);
 
 /* Encode M frames through all stages.
@@ -338,9 +345,27 @@ aq_status aq_ema_codebook(aq_ctx *ctx, const float *embedding_sum, const float *
 
 /* aq_euclid_upload of an EMA codebook: host embedding_sum [Q,N,K] and
  * cluster_usage [Q,N] are materialised on the device with aq_ema_codebook's
- * arithmetic, then prepared as an F32 codebook for `recipe`. */
+ * arithmetic, straight into the set's buffer, and prepared there as an F32
+ * codebook for `recipe` (no copy back to the host). */
 aq_status aq_euclid_upload_ema(aq_ctx *ctx, int64_t Q, int64_t N, int64_t K, const float *embedding_sum,
                                const float *cluster_usage, float eps, int recipe, aq_codebooks **out);
+
+/* ---- Weight-norm folding on the device -----------------------------------
+ *
+ * w[r, :] = v[r, :] * scale_r for a weight-normalised conv (rows = output
+ * channels, cols = in_channels * kernel), scale_r from g[r] and the double
+ * sum of squares of v's row, as the model loaders fold them:
+ *   AQ_WN_OUTETTS  scale = g / (float)sqrt(norm2), fp32 division
+ *                  (fold_weight_norm, community_models/outetts/dac.cpp:91-110)
+ *   AQ_WN_MOSS     scale = (float)(g / sqrt(norm)), double division
+ *                  (reconstruct_weight_norm,
+ *                  models/moss/shared/audio_tokenizer_quantizer.cpp:17-39)
+ * Device pointers v [rows, cols], g [rows], w [rows, cols] (w may be v).
+ * Replaces those host loops; the folded weights then go to aq_dac_upload_ex
+ * (AQ_DAC_OUTETTS) or aq_moss_upload. */
+typedef enum aq_wn_rule { AQ_WN_OUTETTS = 0, AQ_WN_MOSS = 1 } aq_wn_rule;
+aq_status aq_weight_norm_fold(aq_ctx *ctx, const float *v, const float *g, int64_t rows, int64_t cols, int rule,
+                              float *w);
 
 /* ---- MOSS RLFQ quantizer (fp64 host loop) ---------------------------------
  *

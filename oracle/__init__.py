@@ -100,6 +100,8 @@ class Oracle:
         L.aqo_ema_codebook.argtypes = [_f32p, _f32p, _i64, _i64, _i64, C.c_float, _f32p]
         L.aqo_outetts_rvq.argtypes = [_f32p, _i64, _i64, _i64, _i64, _f32p, C.c_void_p, _f32p, _f32p,
                                       C.c_void_p, C.c_void_p, _i32p, _f32p]
+        L.aqo_outetts_weight_norm.restype = None
+        L.aqo_outetts_weight_norm.argtypes = [_f32p, _f32p, _i64, _i64, _f32p]
         L.aqo_moss_weight_norm.restype = None
         L.aqo_moss_weight_norm.argtypes = [_f32p, _f32p, _i64, _i64, _f32p]
         L.aqo_moss_normalize_rows.restype = None
@@ -199,6 +201,14 @@ class Oracle:
                                       None if fi is None else fi.ctypes.data_as(C.c_void_p), idx, res)
         assert rc == 0
         return dict(idx=idx, residual=res)
+
+    def outetts_weight_norm(self, v, g):
+        """fold_weight_norm: v [rows, ...] (trailing axes one row), g [rows]."""
+        v = np.ascontiguousarray(v, np.float32)
+        g = np.ascontiguousarray(g, np.float32).reshape(-1)
+        w = np.zeros_like(v)
+        self.lib.aqo_outetts_weight_norm(v, g, v.shape[0], v.size // v.shape[0], w)
+        return w
 
     def moss_weight_norm(self, g, v):
         """reconstruct_weight_norm over the last two axes of v ([..., out, in])."""
@@ -409,6 +419,8 @@ class Ref:
         L.aqref_quantize_chunk_q8_0.argtypes = [_f32p, C.c_void_p, _i64, _i64]
         L.aqref_top_k.restype = None
         L.aqref_top_k.argtypes = [_f32p, _i64, _i64, C.c_int, _i32p, C.c_int]
+        L.aqref_outetts_fold.restype = None
+        L.aqref_outetts_fold.argtypes = [_f32p, _f32p, _i64, _i64, _i64, _f32p]
         L.aqref_outetts_rvq.restype = C.c_double
         L.aqref_outetts_rvq.argtypes = [_f32p, _i64, _f32p, _f32p, _f32p, _f32p, _f32p, _i32p, C.c_int]
         L.aqref_moss_encode_timed.restype = C.c_double
@@ -417,6 +429,14 @@ class Ref:
         L.aqref_moss_encode.argtypes = [C.POINTER(_MossWeights), _f32p, _i64, _i32p]
         L.aqref_moss_decode.restype = C.c_int
         L.aqref_moss_decode.argtypes = [C.POINTER(_MossWeights), _i32p, _i64, _f32p]
+
+    def outetts_fold(self, v, g):
+        """The reference's fold_weight_norm: v [dim0, dim1, kernel], g [dim0]."""
+        v = np.ascontiguousarray(v, np.float32)
+        g = np.ascontiguousarray(g, np.float32).reshape(-1)
+        w = np.zeros_like(v)
+        self.lib.aqref_outetts_fold(v, g, v.shape[0], v.shape[1], v.shape[2], w)
+        return w
 
     def outetts_rvq(self, cfg: dict, threads: int = 0, timed: bool = False):
         """The reference's quantize_reference (2 stages, D = N = 1024): codes

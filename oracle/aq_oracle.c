@@ -758,6 +758,21 @@ int aqo_outetts_rvq(const float *x, int64_t M, int64_t D, int64_t Q, int64_t N,
     return 0;
 }
 
+/* fold_weight_norm, src/community_models/outetts/dac.cpp:91-110: per output
+   row (dim1 * kernel weights) the double sum of double squares, then
+   scale = g / (float)sqrt(norm2) in fp32 and w = v * scale. */
+void aqo_outetts_weight_norm(const float *v, const float *g, int64_t rows, int64_t cols, float *w) {
+    for (int64_t i = 0; i < rows; ++i) {
+        double norm2 = 0.0;
+        for (int64_t j = 0; j < cols; ++j) {
+            const double x = v[i * cols + j];
+            norm2 += x * x;
+        }
+        const float scale = g[i] / (float)sqrt(norm2);
+        for (int64_t j = 0; j < cols; ++j) w[i * cols + j] = v[i * cols + j] * scale;
+    }
+}
+
 /* reconstruct_weight_norm, src/models/moss/shared/audio_tokenizer_quantizer.cpp:17-39. */
 void aqo_moss_weight_norm(const float *g, const float *v, int64_t out_ch, int64_t in_ch, float *w) {
     for (int64_t o = 0; o < out_ch; ++o) {

@@ -47,3 +47,13 @@ extern "C" __attribute__((visibility("default"))) double aqref_outetts_rvq(
     }
     return ms;
 }
+
+// fold_weight_norm (dac.cpp:91-110) as the loader calls it: v [dim0, dim1,
+// kernel], g [dim0] -> out [dim0, dim1, kernel].
+extern "C" __attribute__((visibility("default"))) void aqref_outetts_fold(const float *v, const float *g, int64_t dim0,
+                                                                         int64_t dim1, int64_t kernel, float *out) {
+    namespace ot = engine::models::outetts;
+    const std::vector<float> vv(v, v + dim0 * dim1 * kernel), gg(g, g + dim0);
+    const std::vector<float> w = ot::fold_weight_norm(vv, gg, dim0, dim1, kernel);
+    std::memcpy(out, w.data(), w.size() * sizeof(float));
+}

@@ -485,6 +485,29 @@ def test_oracle_moss_weight_norm_closed_form(o):
     assert (np.sign(w) == np.sign(v)).all()
 
 
+@pytest.mark.parametrize("shape", [(8, 1024, 1), (1024, 8, 1), (64, 32, 7), (3, 5, 3)])
+def test_oracle_outetts_weight_norm_matches_reference(o, ref, shape):
+    """fold_weight_norm (outetts/dac.cpp:91-110) from the reference's own
+    source, bit for bit, on conv shapes [out, in, kernel] (the quantizer's
+    1x1 in / out projections and wider kernels), including a zero-magnitude
+    row and a row whose v is tiny."""
+    v = synth.normal(17, shape[0], shape, 1.0)
+    v[min(1, shape[0] - 1)] *= 1e-30
+    g = synth.uniform(17, 99, (shape[0],), 0.1, 3.0)
+    g[0] = 0.0
+    assert np.array_equal(o.outetts_weight_norm(v, g).view(np.uint32), ref.outetts_fold(v, g).view(np.uint32))
+
+
+def test_oracle_outetts_weight_norm_closed_form(o):
+    """w = g v / |v| row-wise: rows of w have norm g (to fp32 rounding), and
+    the result does not depend on v's scale (up to rounding)."""
+    g = synth.uniform(18, 1, (16,), 0.5, 2.0)
+    v = synth.normal(18, 2, (16, 40))
+    w = o.outetts_weight_norm(v, g)
+    np.testing.assert_allclose(np.linalg.norm(w.astype(np.float64), axis=1), g, rtol=1e-6)
+    np.testing.assert_allclose(o.outetts_weight_norm(v * 8.0, g), w, rtol=1e-6)
+
+
 def test_oracle_moss_decode_range(o, ref):
     cfg = synth.moss_config(2, Q=2, N=64)
     bad = np.array([[0, 64], [1, 2]], np.int32)

@@ -1,0 +1,111 @@
+"""GPU parity of the codebook ingest and preparation done on the device:
+weight-norm folding (aq_weight_norm_fold) against the oracle's restatement
+of both loaders' folds (the OuteTTS one pinned to the reference's own
+fold_weight_norm in test_oracle.py), and codebooks uploaded from device
+memory (aq_euclid_upload_device) encoding exactly like host uploads.  The
+device-side preparation inside aq_euclid_upload / aq_dac_upload /
+aq_moss_upload is covered by every parity test of those paths.
+"""
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch as t
+
+    if not t.cuda.is_available():
+        pytest.skip("no GPU")
+    return t
+
+
+@pytest.fixture(scope="module")
+def ctx(torch):
+    import aqmi
+
+    return aqmi.Context(0)
+
+
+@pytest.fixture(scope="module")
+def oracle():
+    from oracle import Oracle
+
+    return Oracle()
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+@pytest.mark.parametrize("shape", [(8, 1024, 1), (1024, 8, 1), (64, 32, 7), (512, 1024, 1)])
+@pytest.mark.parametrize("rule", [0, 1])
+def test_weight_norm_fold_matches_oracle(torch, ctx, oracle, rule, shape):
+    """Both folds bit for bit (a zero magnitude, a tiny row), out of place
+    and in place."""
+    import aqmi
+    from aqmi import synth
+
+    print(f"[gpu] weight norm fold rule={rule} shape={shape}", flush=True)
+    v = synth.normal(23, shape[0], shape, 1.0)
+    v[min(1, shape[0] - 1)] *= 1e-30
+    g = synth.uniform(23, 77, (shape[0],), 0.1, 3.0)
+    g[0] = 0.0
+    if rule == aqmi.WN_OUTETTS:
+        want = oracle.outetts_weight_norm(v, g)
+    else:
+        want = oracle.moss_weight_norm(g, v.reshape(shape[0], -1)).reshape(shape)
+    dv = torch.from_numpy(v).cuda()
+    dg = torch.from_numpy(g).cuda()
+    out = torch.empty_like(dv)
+    aqmi.weight_norm_fold(ctx, dv, dg, rule, out)
+    aqmi.weight_norm_fold(ctx, dv, dg, rule, dv)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(out.cpu().numpy()), bits(want))
+    assert np.array_equal(bits(dv.cpu().numpy()), bits(want))
+
+
+def test_weight_norm_fold_errors(torch, ctx):
+    import aqmi
+
+    dv = torch.zeros((4, 8), device="cuda")
+    dg = torch.ones(4, device="cuda")
+    with pytest.raises(aqmi.AqError):
+        aqmi.weight_norm_fold(ctx, dv, dg, 7, dv)
+
+
+@pytest.mark.parametrize("cb_type,recipe", [(0, 0), (0, 2), (1, 1)])
+def test_upload_from_device_memory(torch, ctx, cb_type, recipe):
+    """A codebook handed over in device memory encodes exactly like the same
+    codebook uploaded from the host (codes, residual, distances, top-k)."""
+    import aqmi
+    from aqmi import synth
+
+    print(f"[gpu] device upload cb_type={cb_type} recipe={recipe}", flush=True)
+    Q, N, K, M = 2, 1024, 256, 300
+    topk = 4 if recipe == 1 else 0
+    if cb_type == 1:
+        cb = np.stack([synth.q8_0_random_codebook(29, 10 + s, N, K) for s in range(Q)])
+        x = (synth.q8_0_dequantize(cb[0])[np.arange(M) % N] + synth.normal(29, 2, (M, K), 0.05)).astype(np.float32)
+        dcb = torch.from_numpy(np.frombuffer(cb.tobytes(), np.uint8).copy()).cuda()
+    else:
+        cb = synth.normal(29, 3, (Q, N, K), 1.0 / 16)
+        x = synth.normal(29, 1, (M, K), 1.0)
+        dcb = torch.from_numpy(cb).cuda()
+    outs = []
+    for cbs in (aqmi.Codebooks(ctx, cb, recipe, cb_type),
+                aqmi.Codebooks.from_device(ctx, dcb, recipe, cb_type, shape=(Q, N, K))):
+        xd = torch.from_numpy(x).cuda()
+        idx = torch.full((M, Q), -1, dtype=torch.int32, device="cuda")
+        res = torch.empty((M, K), dtype=torch.float32, device="cuda")
+        dist = torch.empty((M, Q), dtype=torch.float32, device="cuda")
+        tki = torch.zeros((M, Q, 4), dtype=torch.int32, device="cuda")
+        tkd = torch.zeros((M, Q, 4), dtype=torch.float32, device="cuda")
+        cbs.encode(xd, idx, res, dist, topk, tki if topk else None, tkd if topk else None, None)
+        torch.cuda.synchronize()
+        outs.append([t.cpu().numpy() for t in (idx, res, dist, tki, tkd)])
+    for a, b in zip(*outs):
+        assert np.array_equal(a.view(np.uint32) if a.dtype == np.float32 else a,
+                              b.view(np.uint32) if b.dtype == np.float32 else b)
