@@ -39,7 +39,7 @@ EXPORTED = [
 OMNIVOICE, HIGGS, DIRECT = 0, 1, 2
 # aq_dac_recipe
 DAC_FISH, DAC_INDEXTTS2, DAC_VEVO2, DAC_OUTETTS = 0, 1, 2, 3
-CB_F32, CB_Q8_0 = 0, 1
+CB_F32, CB_Q8_0, CB_F32_AS_Q8_0 = 0, 1, 2
 
 
 class AqError(RuntimeError):
@@ -264,13 +264,14 @@ class MossQuantizer:
 class Codebooks:
     """Uploaded Euclidean codebooks (aq_euclid_upload).
 
-    codebook: float32 [Q, N, K] (CB_F32) or a structured block_q8_0 array
-    [Q, N, K/32] (CB_Q8_0, dtype aqmi.synth.Q8_DTYPE).  recipe: OMNIVOICE,
-    HIGGS or DIRECT."""
+    codebook: float32 [Q, N, K] (CB_F32, or CB_F32_AS_Q8_0: quantised to
+    Q8_0 on the device as the reference's weight store does at load) or a
+    structured block_q8_0 array [Q, N, K/32] (CB_Q8_0, dtype
+    aqmi.synth.Q8_DTYPE).  recipe: OMNIVOICE, HIGGS or DIRECT."""
 
     def __init__(self, ctx: Context, codebook, recipe: int, cb_type: int = CB_F32):
         self.ctx = ctx
-        if cb_type == CB_F32:
+        if cb_type in (CB_F32, CB_F32_AS_Q8_0):
             cb = np.ascontiguousarray(codebook, np.float32)
             self.Q, self.N, self.K = cb.shape
         else:
@@ -327,7 +328,7 @@ class Codebooks:
         (CB_F32) or the raw block_q8_0 bytes (uint8, CB_Q8_0; shape = (Q, N, K))."""
         self = cls.__new__(cls)
         self.ctx = ctx
-        if cb_type == CB_F32:
+        if cb_type in (CB_F32, CB_F32_AS_Q8_0):
             self.Q, self.N, self.K = codebook.shape
         else:
             self.Q, self.N, self.K = shape

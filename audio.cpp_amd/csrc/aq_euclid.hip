@@ -83,6 +83,34 @@ __global__ void q8_unpack_kernel(const unsigned char *__restrict__ raw, int64_t 
     if (j == 0) qd[b] = d;
 }
 
+// F32 rows quantised to Q8_0 the way the reference's weight store does at
+// load (ggml_quantize_chunk -> quantize_row_q8_0_ref, ggml-quants.c:236-256;
+// backend_weight_store.h:343-392, tensor_source.cpp:173-200): per 32-block
+// amax = MAX(amax, |x|) (C's MAX: a NaN is passed over by the next value),
+// d = amax / 127, id = d ? 1 / d : 0 in fp32, q = roundf(x * id), the scale
+// stored as fp16(d).  Writes the quants, the scales and q * d.  One thread
+// per block.
+__global__ void q8_quantize_kernel(const float *__restrict__ x, int64_t nblocks, int8_t *__restrict__ qs,
+                                   float *__restrict__ qd, float *__restrict__ cbf) {
+    const int64_t b = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (b >= nblocks) return;
+    const float *xb = x + b * 32;
+    float amax = 0.0f;
+    for (int j = 0; j < 32; ++j) {
+        const float a = fabsf(xb[j]);
+        amax = amax > a ? amax : a;
+    }
+    const float d = __fdiv_rn(amax, 127.0f);
+    const float id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
+    const float ds = static_cast<float>(static_cast<_Float16>(d));
+    qd[b] = ds;
+    for (int j = 0; j < 32; ++j) {
+        const int8_t q = static_cast<int8_t>(static_cast<int>(roundf(__fmul_rn(xb[j], id))));
+        qs[b * 32 + j] = q;
+        cbf[b * 32 + j] = __fmul_rn(static_cast<float>(q), ds);
+    }
+}
+
 // bf16 / fp16 images, round to nearest even (bf16: NaN kept quiet, as a
 // truncation with the quiet bit set).
 __device__ inline uint16_t img_bf16(float f) {
@@ -193,9 +221,9 @@ namespace {
 aq_status check_upload(aq_ctx *ctx, const char *fn, int64_t Q, int64_t N, int64_t K, int cb_type, int recipe) {
     if (recipe < AQ_EUCLID_OMNIVOICE || recipe > AQ_EUCLID_DIRECT)
         return aq_fail(ctx, AQ_E_INVALID_ARG, "%s: unknown recipe %d", fn, recipe);
-    if (cb_type != AQ_CB_F32 && cb_type != AQ_CB_Q8_0)
+    if (cb_type != AQ_CB_F32 && cb_type != AQ_CB_Q8_0 && cb_type != AQ_CB_F32_AS_Q8_0)
         return aq_fail(ctx, AQ_E_INVALID_ARG, "%s: unknown codebook type %d", fn, cb_type);
-    if (cb_type == AQ_CB_Q8_0 && recipe != AQ_EUCLID_HIGGS)
+    if (cb_type != AQ_CB_F32 && recipe != AQ_EUCLID_HIGGS)
         return aq_fail(ctx, AQ_E_UNSUPPORTED, "%s: Q8_0 codebooks follow the Higgs recipe only", fn);
     const KsKernels *kk = K > 0 && K % 32 == 0 ? kernels_for(static_cast<int>(K / 32)) : nullptr;
     if (Q <= 0 || N <= 0 || !kk)
@@ -230,12 +258,28 @@ aq_status euclid_alloc(aq_ctx *ctx, int64_t Q, int64_t N, int64_t K, bool q8, in
 }
 
 // Fills the codebook (d_cbf; for Q8_0 also the quants and scales) from
-// `data` in host or device memory (F32 [Q][N][K], or block_q8_0 rows).
-aq_status euclid_fill(aq_ctx *ctx, aq_codebooks *cb, const void *data, hipMemcpyKind kind) {
+// `data` in host or device memory (F32 [Q][N][K], or block_q8_0 rows; F32
+// rows for AQ_CB_F32_AS_Q8_0, quantised here).
+aq_status euclid_fill(aq_ctx *ctx, aq_codebooks *cb, int cb_type, const void *data, hipMemcpyKind kind) {
     const size_t QNK = static_cast<size_t>(cb->Q * cb->N * cb->K);
     if (!cb->q8) {
         AQ_HIP(ctx, hipMemcpyAsync(cb->d_cbf, data, QNK * 4, kind, ctx->stream));
         return AQ_OK;
+    }
+    if (cb_type == AQ_CB_F32_AS_Q8_0) {
+        float *f = nullptr;
+        if (hipMalloc(&f, QNK * 4) != hipSuccess) return aq_fail(ctx, AQ_E_NOMEM, "aq_euclid_upload: device allocation failed");
+        aq_status st = AQ_OK;
+        if (hipMemcpyAsync(f, data, QNK * 4, kind, ctx->stream) != hipSuccess) {
+            st = aq_fail(ctx, AQ_E_DEVICE, "aq_euclid_upload: copy of the codebook failed");
+        } else {
+            hipLaunchKernelGGL(q8_quantize_kernel, dim3(static_cast<unsigned>((QNK / 32 + 127) / 128)), dim3(128), 0,
+                               ctx->stream, f, static_cast<int64_t>(QNK / 32), cb->d_q8, cb->d_q8d, cb->d_cbf);
+            if (hipGetLastError() != hipSuccess || hipStreamSynchronize(ctx->stream) != hipSuccess)
+                st = aq_fail(ctx, AQ_E_DEVICE, "aq_euclid_upload: Q8_0 quantisation failed");
+        }
+        (void)hipFree(f);
+        return st;
     }
     const size_t nblocks = QNK / 32;
     unsigned char *raw = nullptr;
@@ -314,8 +358,8 @@ aq_status euclid_upload_from(aq_ctx *ctx, const char *fn, int64_t Q, int64_t N, 
     if (st != AQ_OK) return st;
     aq_device_guard g(ctx->device);
     aq_codebooks *cb = nullptr;
-    st = euclid_alloc(ctx, Q, N, K, cb_type == AQ_CB_Q8_0, recipe, &cb);
-    if (st == AQ_OK) st = euclid_fill(ctx, cb, data, kind);
+    st = euclid_alloc(ctx, Q, N, K, cb_type != AQ_CB_F32, recipe, &cb);
+    if (st == AQ_OK) st = euclid_fill(ctx, cb, cb_type, data, kind);
     if (st == AQ_OK) st = euclid_prepare(ctx, cb);
     if (st != AQ_OK) {
         if (cb) aq_euclid_release(cb);

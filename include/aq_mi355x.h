@@ -234,8 +234,14 @@ typedef enum aq_euclid_recipe {
 
 typedef enum aq_codebook_type {
     AQ_CB_F32 = 0,    /* float [Q][N][K]                                       */
-    AQ_CB_Q8_0 = 1    /* GGUF block_q8_0 {fp16 d; int8 qs[32]} [Q][N][K/32],
+    AQ_CB_Q8_0 = 1,   /* GGUF block_q8_0 {fp16 d; int8 qs[32]} [Q][N][K/32],
                          34 bytes per block (ggml-common.h:241-246)             */
+    AQ_CB_F32_AS_Q8_0 = 2  /* float [Q][N][K] stored as Q8_0, quantised on the
+                         device at upload as the reference's weight store does
+                         for a Q8_0 storage type (ggml_quantize_chunk ->
+                         quantize_row_q8_0_ref: d = amax/127, q = roundf(x/d);
+                         backend_weight_store.h:272-287,343-392,
+                         tensor_source.cpp:173-200)                             */
 } aq_codebook_type;
 
 /* Upload Q codebooks of N codes of dimension K from host memory (upload

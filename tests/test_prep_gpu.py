@@ -109,3 +109,47 @@ def test_upload_from_device_memory(torch, ctx, cb_type, recipe):
     for a, b in zip(*outs):
         assert np.array_equal(a.view(np.uint32) if a.dtype == np.float32 else a,
                               b.view(np.uint32) if b.dtype == np.float32 else b)
+
+
+def test_upload_quantises_f32_like_the_weight_store(torch, ctx, oracle):
+    """CB_F32_AS_Q8_0: F32 codebooks quantised to Q8_0 on the device give the
+    blocks of the reference weight store's ggml_quantize_chunk
+    (synth.q8_0_quantize_ref, pinned to the reference in test_oracle.py):
+    the gathered rows equal the dequantised reference blocks bit for bit, and
+    encodes (codes, residual, distances, top-4) equal an upload of those
+    blocks and the oracle.  Rows include zeros, ties at amax and halves."""
+    import aqmi
+    from aqmi import synth
+
+    print("[gpu] f32 -> q8_0 upload", flush=True)
+    Q, N, K, M = 2, 1024, 256, 200
+    f = synth.normal(31, 5, (Q, N, K), 0.3)
+    f[0, 3] = 0.0
+    f[0, 4, :32] = 1.0
+    f[1, 9, :32] = np.linspace(-63.5, 63.5, 32, dtype=np.float32) / 127.0
+    blocks = synth.q8_0_quantize_ref(f)
+    x = (synth.q8_0_dequantize(blocks[0])[np.arange(M) % N] + synth.normal(31, 6, (M, K), 0.02)).astype(np.float32)
+    got = aqmi.Codebooks(ctx, f, aqmi.HIGGS, aqmi.CB_F32_AS_Q8_0)
+    ref = aqmi.Codebooks(ctx, blocks, aqmi.HIGGS, aqmi.CB_Q8_0)
+    for s in range(Q):
+        idx = torch.arange(N, dtype=torch.int32, device="cuda")
+        rows = torch.empty((N, K), dtype=torch.float32, device="cuda")
+        got.gather(s, idx, rows)
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(rows.cpu().numpy()), bits(synth.q8_0_dequantize(blocks[s])))
+    outs = []
+    for cbs in (got, ref):
+        xd = torch.from_numpy(x).cuda()
+        idx = torch.full((M, Q), -1, dtype=torch.int32, device="cuda")
+        res = torch.empty((M, K), dtype=torch.float32, device="cuda")
+        dist = torch.empty((M, Q), dtype=torch.float32, device="cuda")
+        tki = torch.zeros((M, Q, 4), dtype=torch.int32, device="cuda")
+        tkd = torch.zeros((M, Q, 4), dtype=torch.float32, device="cuda")
+        cbs.encode(xd, idx, res, dist, 4, tki, tkd, None)
+        torch.cuda.synchronize()
+        outs.append([t.cpu().numpy() for t in (idx, res, dist)])
+    want = oracle.higgs_rvq(dict(x=x, M=M, K=K, Q=Q, N=N, codebook_q8=blocks), topk=4)
+    assert np.array_equal(outs[0][0], want["idx"])
+    assert np.array_equal(bits(outs[0][1]), bits(want["residual"]))
+    for a, b in zip(*outs):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
