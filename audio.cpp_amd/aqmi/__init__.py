@@ -33,6 +33,7 @@ EXPORTED = [
     "aq_moss_upload", "aq_moss_release", "aq_moss_encode", "aq_moss_decode",
     "aq_euclid_encode_strided", "aq_euclid_upload_projected", "aq_euclid_encode_noalloc",
     "aq_dac_encode_ex", "aq_dac_decode_ex", "aq_euclid_upload_device", "aq_weight_norm_fold",
+    "aq_linear_upload", "aq_linear_forward", "aq_linear_release",
 ]
 
 # aq_euclid_recipe / aq_codebook_type
@@ -80,6 +81,9 @@ def load_library(path: str | pathlib.Path | None = None) -> C.CDLL:
     lib.aq_euclid_upload_ema.argtypes = [vp, i64, i64, i64, vp, vp, C.c_float, C.c_int, C.POINTER(vp)]
     lib.aq_euclid_upload_device.argtypes = [vp, i64, i64, i64, C.c_int, vp, C.c_int, C.POINTER(vp)]
     lib.aq_weight_norm_fold.argtypes = [vp, vp, vp, i64, i64, C.c_int, vp]
+    lib.aq_linear_upload.argtypes = [vp, i64, i64, C.c_int, vp, vp, C.POINTER(vp)]
+    lib.aq_linear_forward.argtypes = [vp, vp, vp, i64, i64, i64, i64, i64, vp]
+    lib.aq_linear_release.argtypes = [vp]
     lib.aq_euclid_decode.argtypes = [vp, vp, vp, i64, vp]
     lib.aq_euclid_encode_noalloc.argtypes = [vp, vp, vp, i64, vp, vp, vp, C.c_int, vp, vp, vp]
     lib.aq_euclid_encode_strided.argtypes = [vp, vp, vp, i64, i64, i64, i64, i64, vp, vp, vp, C.c_int, vp, vp, vp]
@@ -411,6 +415,46 @@ class Codebooks:
     def close(self):
         if getattr(self, "h", None):
             self.ctx.lib.aq_euclid_release(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Linear:
+    """aq_linear: an encoder output Linear with ggml's CPU arithmetic.
+
+    w: float32 [out, in] or block_q8_0 [out, in/32] (host); bias [out] or
+    None."""
+
+    def __init__(self, ctx: Context, w, bias=None):
+        self.ctx = ctx
+        wt = CB_F32 if w.dtype == np.float32 else CB_Q8_0
+        w = np.ascontiguousarray(w)
+        self.out_features = w.shape[0]
+        self.in_features = w.shape[1] * (1 if wt == CB_F32 else 32)
+        b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+        h = C.c_void_p()
+        ctx.check(ctx.lib.aq_linear_upload(ctx.h, self.out_features, self.in_features, wt,
+                                           w.ctypes.data_as(C.c_void_p), _host_ptr(b), C.byref(h)))
+        self.h = h
+
+    def forward(self, x, out, M=None, clip_len=None, strides=None):
+        """x device: frame-major [M, in] or any layout given by
+        strides = (clip_stride, frame_stride, chan_stride) with clip_len
+        frames per clip; out device [M, out]."""
+        if strides is None:
+            M = x.shape[0]
+            clip_len, strides = M, (M * self.in_features, self.in_features, 1)
+        self.ctx.use_current_stream()
+        self.ctx.check(self.ctx.lib.aq_linear_forward(self.ctx.h, self.h, _dptr(x), M, clip_len, *strides, _dptr(out)))
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.ctx.lib.aq_linear_release(self.h)
             self.h = None
 
     def __del__(self):

@@ -470,6 +470,34 @@ aq_status aq_proj_create(aq_ctx *ctx, int64_t Q, int64_t N, int64_t K, int64_t H
     return AQ_OK;
 }
 
+aq_status aq_proj_create_linear(aq_ctx *ctx, int64_t O, int64_t I, int w_type, const void *w, const float *b,
+                                aq_proj_weights **out) {
+    aq_proj_weights *pw = new (std::nothrow) aq_proj_weights();
+    if (!pw) return aq_fail(ctx, AQ_E_NOMEM, "aq_linear_upload: host allocation failed");
+    pw->Q = 1;
+    pw->N = 0;
+    pw->K = O;
+    pw->H = I;
+    pw->q8 = w_type == AQ_CB_Q8_0;
+    const size_t OI = static_cast<size_t>(O * I);
+    bool ok;
+    if (pw->q8) {
+        std::vector<int8_t> wq;
+        std::vector<float> wd;
+        split_q8(w, OI / 32, wq, wd);
+        ok = upload(&pw->w_in_q, wq.data(), OI) && upload(&pw->w_in_d, wd.data(), OI / 32);
+    } else {
+        ok = upload(&pw->w_in, static_cast<const float *>(w), OI);
+    }
+    if (ok && b) ok = upload(&pw->b_in, b, static_cast<size_t>(O));
+    if (!ok) {
+        aq_proj_release(pw);
+        return aq_fail(ctx, AQ_E_NOMEM, "aq_linear_upload: device allocation or copy failed");
+    }
+    *out = pw;
+    return AQ_OK;
+}
+
 void aq_proj_release(aq_proj_weights *pw) {
     if (!pw) return;
     for (void *p : {static_cast<void *>(pw->w_in), static_cast<void *>(pw->w_in_q), static_cast<void *>(pw->w_in_d),
@@ -550,3 +578,63 @@ aq_status aq_gather_frames(aq_ctx *ctx, const aq_frames_desc &in, int64_t M, int
     AQ_HIP(ctx, hipGetLastError());
     return AQ_OK;
 }
+
+// ---------------------------------------------------------------- C ABI
+
+struct aq_linear {
+    aq_ctx *ctx = nullptr;
+    aq_proj_weights *pw = nullptr;
+};
+
+extern "C" {
+
+aq_status aq_linear_upload(aq_ctx *ctx, int64_t out_features, int64_t in_features, int w_type, const void *w,
+                           const float *bias, aq_linear **out) {
+    if (!ctx || !w || !out) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_linear_upload: null argument");
+    *out = nullptr;
+    if (w_type != AQ_CB_F32 && w_type != AQ_CB_Q8_0)
+        return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_linear_upload: unknown weight type %d", w_type);
+    const int64_t lds = 16 * (in_features + 1) * 4 +
+                        (w_type == AQ_CB_Q8_0 ? 16 * in_features + 16 * (in_features / 32) * 4 : 0);
+    if (out_features <= 0 || out_features % 64 != 0 || out_features > (int64_t{1} << 16) || in_features <= 0 ||
+        in_features % 64 != 0 || lds > 160 * 1024)
+        return aq_fail(ctx, AQ_E_SHAPE,
+                       "aq_linear_upload: out_features=%lld in_features=%lld (multiples of 64; in_features up to %d)",
+                       (long long)out_features, (long long)in_features, w_type == AQ_CB_Q8_0 ? 1984 : 2496);
+    aq_device_guard g(ctx->device);
+    aq_linear *lin = new (std::nothrow) aq_linear();
+    if (!lin) return aq_fail(ctx, AQ_E_NOMEM, "aq_linear_upload: host allocation failed");
+    lin->ctx = ctx;
+    aq_status st = aq_proj_create_linear(ctx, out_features, in_features, w_type, w, bias, &lin->pw);
+    if (st != AQ_OK) {
+        delete lin;
+        return st;
+    }
+    *out = lin;
+    return AQ_OK;
+}
+
+aq_status aq_linear_forward(aq_ctx *ctx, const aq_linear *lin, const float *x, int64_t M, int64_t clip_len,
+                            int64_t clip_stride, int64_t frame_stride, int64_t chan_stride, float *out) {
+    if (!ctx || !lin || (M > 0 && (!x || !out))) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_linear_forward: null argument");
+    if (lin->ctx->device != ctx->device)
+        return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_linear_forward: weights belong to another device");
+    if (M < 0 || M > (int64_t{1} << 31) - 1 || clip_len <= 0)
+        return aq_fail(ctx, AQ_E_SHAPE, "aq_linear_forward: M=%lld clip_len=%lld", (long long)M, (long long)clip_len);
+    if (M == 0) return AQ_OK;
+    aq_device_guard g(ctx->device);
+    const aq_frames_desc in{x, clip_len, clip_stride, frame_stride, chan_stride};
+    return aq_proj_step(ctx, lin->pw, 0, -1, in, nullptr, nullptr, 0, out, M);
+}
+
+aq_status aq_linear_release(aq_linear *lin) {
+    if (!lin) return AQ_E_INVALID_ARG;
+    {
+        aq_device_guard g(lin->ctx->device);
+        aq_proj_release(lin->pw);
+    }
+    delete lin;
+    return AQ_OK;
+}
+
+}  // extern "C"

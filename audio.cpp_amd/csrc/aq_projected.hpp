@@ -42,6 +42,12 @@ aq_status aq_proj_create(aq_ctx *ctx, int64_t Q, int64_t N, int64_t K, int64_t H
                          const float *b_out, aq_proj_weights **out);
 void aq_proj_release(aq_proj_weights *pw);
 
+// A single F32 / Q8_0 linear layer (Q = 1, no codebook, no out-projection):
+// w [O][I] (F32) or block_q8_0 rows, b [O] or null; run with aq_proj_step
+// (s = 0, prev = -1).
+aq_status aq_proj_create_linear(aq_ctx *ctx, int64_t O, int64_t I, int w_type, const void *w, const float *b,
+                                aq_proj_weights **out);
+
 // One projection step over M frames:
 //   r = in (frame m's hidden vector);
 //   if prev >= 0: r -= table[prev][code(m)], code(m) = codes[m * ld + prev]

@@ -424,6 +424,33 @@ aq_status aq_codebook_gather(aq_ctx *ctx, const aq_codebooks *cb, int64_t stage,
  * idx device [M, Q], out device [M, K]. */
 aq_status aq_euclid_decode(aq_ctx *ctx, const aq_codebooks *cb, const int32_t *idx, int64_t M, float *out);
 
+/* ---- Encoder output projection in the CPU's arithmetic --------------------
+ *
+ * The layer in front of the quantizer (an encoder's output Linear / 1x1
+ * conv, LinearModule::forward, src/framework/modules/linear_module.cpp:73-108)
+ * with ggml's CPU arithmetic, deterministic on the device:
+ *   out[m, o] = mul_mat(W, x_m)[o] (+ bias[o], ggml_add)
+ * F32 weights: tinyBLAS order for a batch of M >= 2 frames (16 FMA lanes
+ * over k = 16u + t, then _mm512_reduce_add_ps's pairing; sgemm.cpp), the
+ * ggml_vec_dot_f32 order for one frame (ggml-cpu.c:1245-1443); Q8_0 weights:
+ * x quantised by x86 quantize_row_q8_0, then int8 block dots scaled by
+ * d_w * d_x and FMA-accumulated over 8 lanes (tinyBLAS_Q0 /
+ * ggml_vec_dot_q8_0_q8_0).  The reference pins voice-prompt encoding to the
+ * CPU because its CUDA path runs TF32 (qwen3_tts/session.cpp:101-107); this
+ * gives the CPU's bits on the GPU.  The input is read through the frame
+ * descriptor of aq_euclid_encode_strided (channel-major [B, C, T] taken
+ * as is); the output is frame-major [M, out_features].
+ *   w     host [out_features, in_features] F32, or block_q8_0 rows (w_type
+ *         AQ_CB_Q8_0); bias host [out_features] or NULL.
+ * Supported: out_features a multiple of 64; in_features a multiple of 64 up
+ * to 2496 (F32) / 1984 (Q8_0). */
+typedef struct aq_linear aq_linear;
+aq_status aq_linear_upload(aq_ctx *ctx, int64_t out_features, int64_t in_features, int w_type, const void *w,
+                           const float *bias, aq_linear **out);
+aq_status aq_linear_forward(aq_ctx *ctx, const aq_linear *lin, const float *x, int64_t M, int64_t clip_len,
+                            int64_t clip_stride, int64_t frame_stride, int64_t chan_stride, float *out);
+aq_status aq_linear_release(aq_linear *lin);
+
 #ifdef __cplusplus
 }
 #endif

@@ -100,6 +100,8 @@ class Oracle:
         L.aqo_ema_codebook.argtypes = [_f32p, _f32p, _i64, _i64, _i64, C.c_float, _f32p]
         L.aqo_outetts_rvq.argtypes = [_f32p, _i64, _i64, _i64, _i64, _f32p, C.c_void_p, _f32p, _f32p,
                                       C.c_void_p, C.c_void_p, _i32p, _f32p]
+        L.aqo_linear.restype = C.c_int
+        L.aqo_linear.argtypes = [C.c_void_p, C.c_int, C.c_void_p, _i64, _i64, _i64, _f32p, _f32p]
         L.aqo_outetts_weight_norm.restype = None
         L.aqo_outetts_weight_norm.argtypes = [_f32p, _f32p, _i64, _i64, _f32p]
         L.aqo_moss_weight_norm.restype = None
@@ -344,6 +346,18 @@ class Oracle:
             out["topk_logit"] = tkl
         return out
 
+    def linear(self, w, bias, x):
+        """LinearModule over the rows of x [M, k]: w F32 [n_out, k] or
+        block_q8_0 [n_out, k/32]; bias [n_out] or None (aqo_linear)."""
+        x = np.ascontiguousarray(x, np.float32)
+        M, k = x.shape
+        wt = 0 if w.dtype == np.float32 else 1
+        w = np.ascontiguousarray(w)
+        n_out = w.shape[0]
+        out = np.zeros((M, n_out), np.float32)
+        assert self.lib.aqo_linear(w.ctypes.data_as(C.c_void_p), wt, _opt(bias, np.float32), n_out, k, M, x, out) == 0
+        return out
+
     def projected_decode(self, cfg: dict, idx):
         """Sum over stages of project_out(c[idx]) (aqo_projected_decode)."""
         idx = np.ascontiguousarray(idx, np.int32)
@@ -419,6 +433,8 @@ class Ref:
         L.aqref_quantize_chunk_q8_0.argtypes = [_f32p, C.c_void_p, _i64, _i64]
         L.aqref_top_k.restype = None
         L.aqref_top_k.argtypes = [_f32p, _i64, _i64, C.c_int, _i32p, C.c_int]
+        L.aqref_linear.restype = C.c_double
+        L.aqref_linear.argtypes = [C.c_void_p, C.c_int, C.c_void_p, _i64, _i64, _i64, _f32p, _f32p, C.c_int]
         L.aqref_outetts_fold.restype = None
         L.aqref_outetts_fold.argtypes = [_f32p, _f32p, _i64, _i64, _i64, _f32p]
         L.aqref_outetts_rvq.restype = C.c_double
@@ -429,6 +445,17 @@ class Ref:
         L.aqref_moss_encode.argtypes = [C.POINTER(_MossWeights), _f32p, _i64, _i32p]
         L.aqref_moss_decode.restype = C.c_int
         L.aqref_moss_decode.argtypes = [C.POINTER(_MossWeights), _i32p, _i64, _f32p]
+
+    def linear(self, w, bias, x, threads: int = 8):
+        """The reference's LinearModule graph (mul_mat + add) on x [M, k]."""
+        x = np.ascontiguousarray(x, np.float32)
+        M, k = x.shape
+        wt = 0 if w.dtype == np.float32 else 1
+        w = np.ascontiguousarray(w)
+        n_out = w.shape[0]
+        out = np.zeros((M, n_out), np.float32)
+        self.lib.aqref_linear(w.ctypes.data_as(C.c_void_p), wt, _opt(bias, np.float32), n_out, k, M, x, out, threads)
+        return out
 
     def outetts_fold(self, v, g):
         """The reference's fold_weight_norm: v [dim0, dim1, kernel], g [dim0]."""

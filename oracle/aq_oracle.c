@@ -550,6 +550,18 @@ static void linear_row(const void *w, int w_type, const float *bias, int64_t n_o
     }
 }
 
+/* LinearModule over a batch: out [M, n_out] = linear_row of each of the M
+ * input rows x [M, k] (the batch size M is the mul_mat's, which picks the
+ * F32 summation order). */
+int aqo_linear(const void *w, int w_type, const float *bias, int64_t n_out, int64_t k, int64_t M, const float *x,
+               float *out) {
+    aqo_block_q8_0 *xq = (aqo_block_q8_0 *)malloc((size_t)(k / 32 + 1) * sizeof(aqo_block_q8_0));
+    if (!xq) return -1;
+    for (int64_t m = 0; m < M; ++m) linear_row(w, w_type, bias, n_out, k, M, x + m * k, xq, out + m * n_out);
+    free(xq);
+    return 0;
+}
+
 /* OmniVoice and Higgs acoustic RVQ with the projections of the reference
  * (omnivoice/audio_tokenizer.cpp:1886-1927; higgs_audio_tts/codec.cpp:958-1016):
  * per stage, on the residual r of hidden size H (frame-major after the

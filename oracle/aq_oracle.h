@@ -127,6 +127,8 @@ int aqo_outetts_rvq(const float *x, int64_t M, int64_t D, int64_t Q, int64_t N,
  * w[o,k] = v[o,k] * (float)(g[o] / sqrt(sum_k (double)v[o,k]^2)). */
 void aqo_moss_weight_norm(const float *g, const float *v, int64_t out_ch, int64_t in_ch, float *w);
 void aqo_outetts_weight_norm(const float *v, const float *g, int64_t rows, int64_t cols, float *w);
+int aqo_linear(const void *w, int w_type, const float *bias, int64_t n_out, int64_t k, int64_t M, const float *x,
+               float *out);
 
 /* MOSS codebook row normalisation (constructor, :116-130):
  * row * (1 / max(sqrt(sum (double)c^2), 1e-12)) in double, stored as float. */

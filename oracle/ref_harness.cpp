@@ -490,6 +490,32 @@ double aqref_projected_rvq(const float * x, int64_t M, int64_t H, int64_t K, int
     return ms;
 }
 
+// LinearModule::forward (linear_module.cpp:73-108) on M frame-major rows:
+// out = mul_mat(W, x) (+ ggml_add bias).  W [n_out, k] F32 (w_type 0) or
+// Q8_0 rows (1); x [M, k]; out [M, n_out].
+double aqref_linear(const void * w, int w_type, const float * bias, int64_t n_out, int64_t k, int64_t M,
+                    const float * x, float * out, int n_threads) {
+    ggml_cpu_init();
+    const ggml_type tp = w_type == 1 ? GGML_TYPE_Q8_0 : GGML_TYPE_F32;
+    const size_t w_bytes = ggml_row_size(tp, k) * static_cast<size_t>(n_out);
+    Ctx c(w_bytes + static_cast<size_t>(M) * static_cast<size_t>(k + 3 * n_out) * 4 + (64u << 20));
+    ggml_context * ctx = c.ctx;
+    ggml_tensor * W = ggml_new_tensor_2d(ctx, tp, k, n_out);
+    std::memcpy(W->data, w, w_bytes);
+    ggml_tensor * X = ggml_new_tensor_2d(ctx, GGML_TYPE_F32, k, M);
+    std::memcpy(X->data, x, static_cast<size_t>(M * k) * 4);
+    ggml_tensor * y = ggml_mul_mat(ctx, W, X);
+    ggml_mul_mat_set_prec(y, GGML_PREC_F32);
+    if (bias) {
+        ggml_tensor * B = ggml_new_tensor_1d(ctx, GGML_TYPE_F32, n_out);
+        std::memcpy(B->data, bias, static_cast<size_t>(n_out) * 4);
+        y = ggml_add(ctx, y, B);
+    }
+    const double ms = run_graph(ctx, y, n_threads);
+    std::memcpy(out, y->data, static_cast<size_t>(M * n_out) * 4);
+    return ms;
+}
+
 // Their decode (omnivoice/audio_tokenizer.cpp:1745-1771; higgs codec.cpp:
 // 1040-1065): latent = z_0, then latent = latent + z_s, z_s =
 // Linear(project_out)(get_rows(c_s, idx[:, s])).  idx [M, Q]; out [M, H].

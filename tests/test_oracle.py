@@ -508,6 +508,23 @@ def test_oracle_outetts_weight_norm_closed_form(o):
     np.testing.assert_allclose(o.outetts_weight_norm(v * 8.0, g), w, rtol=1e-6)
 
 
+@pytest.mark.parametrize("n_out,k,M,q8,bias", [(64, 1024, 1, False, True), (64, 1024, 2, False, True),
+                                                (128, 512, 37, False, False), (1024, 64, 5, False, True),
+                                                (64, 1024, 1, True, True), (256, 512, 33, True, False)])
+def test_oracle_linear_matches_reference(o, ref, n_out, k, M, q8, bias):
+    """LinearModule (mul_mat + add) against the reference's ggml graph, bit
+    for bit: F32 weights with one frame (ggml_vec_dot_f32) and batches
+    (tinyBLAS), and Q8_0 weights (x quantised, int8 block dots)."""
+    from aqmi import synth as sy
+
+    w = sy.normal(19, n_out + k, (n_out, k), 0.05)
+    if q8:
+        w = sy.q8_0_quantize_ref(w)
+    x = sy.normal(19, M, (M, k), 1.0)
+    b = sy.normal(19, 3, (n_out,), 0.1) if bias else None
+    assert np.array_equal(o.linear(w, b, x).view(np.uint32), ref.linear(w, b, x).view(np.uint32))
+
+
 def test_oracle_moss_decode_range(o, ref):
     cfg = synth.moss_config(2, Q=2, N=64)
     bad = np.array([[0, 64], [1, 2]], np.int32)

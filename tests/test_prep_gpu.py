@@ -153,3 +153,57 @@ def test_upload_quantises_f32_like_the_weight_store(torch, ctx, oracle):
     assert np.array_equal(bits(outs[0][1]), bits(want["residual"]))
     for a, b in zip(*outs):
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@pytest.mark.parametrize("n_out,k,M,q8,bias", [(64, 1024, 1, False, True), (64, 1024, 2, False, True),
+                                                (128, 512, 301, False, False), (1024, 64, 77, False, True),
+                                                (64, 1024, 1, True, True), (256, 512, 333, True, False),
+                                                (512, 2496, 40, False, True), (128, 1984, 40, True, True)])
+def test_linear_matches_oracle(torch, ctx, oracle, n_out, k, M, q8, bias):
+    """aq_linear (encoder output projection) bit for bit against the
+    oracle's LinearModule (pinned to the reference's ggml graph in
+    test_oracle.py): one frame and batches, F32 and Q8_0 weights, the
+    largest supported widths."""
+    import aqmi
+    from aqmi import synth
+
+    print(f"[gpu] linear {n_out}x{k} M={M} q8={q8}", flush=True)
+    w = synth.normal(37, n_out + k, (n_out, k), 0.05)
+    if q8:
+        w = synth.q8_0_quantize_ref(w)
+    x = synth.normal(37, M, (M, k), 1.0)
+    b = synth.normal(37, 3, (n_out,), 0.1) if bias else None
+    lin = aqmi.Linear(ctx, w, b)
+    out = torch.empty((M, n_out), dtype=torch.float32, device="cuda")
+    lin.forward(torch.from_numpy(x).cuda(), out)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(out.cpu().numpy()), bits(oracle.linear(w, b, x)))
+
+
+@pytest.mark.parametrize("q8", [False, True])
+def test_linear_channel_major_input(torch, ctx, oracle, q8):
+    """The encoder's [B, C, T] output read in place (frames of two clips):
+    the same bits as the frame-major rows."""
+    import aqmi
+    from aqmi import synth
+
+    B, Cc, T, n_out = 2, 512, 150, 128
+    w = synth.normal(38, 1, (n_out, Cc), 0.05)
+    if q8:
+        w = synth.q8_0_quantize_ref(w)
+    lat = synth.normal(38, 2, (B, Cc, T), 1.0)
+    x = np.ascontiguousarray(lat.transpose(0, 2, 1).reshape(B * T, Cc))
+    lin = aqmi.Linear(ctx, w, synth.normal(38, 3, (n_out,), 0.1))
+    out = torch.empty((B * T, n_out), dtype=torch.float32, device="cuda")
+    lin.forward(torch.from_numpy(lat).cuda(), out, M=B * T, clip_len=T, strides=(Cc * T, 1, T))
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(out.cpu().numpy()), bits(oracle.linear(w, synth.normal(38, 3, (n_out,), 0.1), x)))
+
+
+def test_linear_errors(torch, ctx):
+    import aqmi
+
+    with pytest.raises(aqmi.AqError):
+        aqmi.Linear(ctx, np.zeros((60, 64), np.float32))
+    with pytest.raises(aqmi.AqError):
+        aqmi.Linear(ctx, np.zeros((64, 2560), np.float32))
