@@ -564,7 +564,6 @@ aq_status euclid_encode_impl(aq_ctx *ctx, const aq_codebooks *cb, const aq_frame
     StageFn sweep = kk->sweep[cb->q8 ? 1 : 0][topl - 3];
     StageFn select = kk->select[var][topl - 3];
     StageFn scan = kk->exact_scan[var];
-    StageFn scan_values = kk->scan_values[var];
     const int lds = kk->lds;
     AQ_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void *>(sweep), hipFuncAttributeMaxDynamicSharedMemorySize, lds));
     const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
@@ -604,18 +603,21 @@ aq_status euclid_encode_impl(aq_ctx *ctx, const aq_codebooks *cb, const aq_frame
         keys = static_cast<float *>(w);
     }
     // Counters (per stage, modulo 64): [0, 64) frames the bf16 certificate
-    // left open, [64, 128) frames sent on to the exact scan; then the two
+    // left open, [64, 128) frames sent on to the exact scan, [128, 128 +
+    // kScanSplitFrames) the exact scan's chunks done per frame; then the two
     // frame lists.
+    constexpr int kCounters = 128 + kScanSplitFrames;
     int32_t *fails = nullptr;
     {
-        aq_status st = arena.get(1, (2 * static_cast<size_t>(M) + 128) * sizeof(int32_t),
+        aq_status st = arena.get(1, (2 * static_cast<size_t>(M) + kCounters) * sizeof(int32_t),
                                  reinterpret_cast<void **>(&fails));
         if (st != AQ_OK) return st;
     }
     ctx->euclid_counts = fails;   // read by aq_euclid_failures / aq_euclid_exact_scans
     int32_t *counts = fails;
     int32_t *counts2 = fails + 64;
-    int32_t *list = fails + 128;
+    int32_t *slot_done = fails + 128;
+    int32_t *list = fails + kCounters;
     int32_t *list2 = list + M;
     RefArgs rf{};
     // Refine-pass keys: the larger of the two slicings' needs (short slices
@@ -659,7 +661,7 @@ aq_status euclid_encode_impl(aq_ctx *ctx, const aq_codebooks *cb, const aq_frame
     rf.list2 = list2;
     RefineFn rvals = kk->refine_values[var];
     RefineFn rsel = kk->refine_select[var];
-    AQ_HIP(ctx, hipMemsetAsync(counts, 0, sizeof(int32_t) * 128, ctx->stream));
+    AQ_HIP(ctx, hipMemsetAsync(counts, 0, sizeof(int32_t) * kCounters, ctx->stream));
     AQ_HIP(ctx, hipMemsetAsync(ctx->d_flags, 0, sizeof(int32_t) * AQ_FLAG_COUNT, ctx->stream));
 
     // Stage s of the pipeline: queries xin [M, K], residual out xout (null:
@@ -701,6 +703,7 @@ aq_status euclid_encode_impl(aq_ctx *ctx, const aq_codebooks *cb, const aq_frame
         a.nsplit = nsplit;
         a.svals = svals;
         a.scap = scap;
+        a.slot_done = slot_done;
         if (s >= 64 && s % 64 == 0) AQ_HIP(ctx, hipMemsetAsync(counts, 0, sizeof(int32_t) * 128, ctx->stream));
         const int tslot = arena.base ? -1 : aq_timing_start(ctx);   // events are not created without allocation
         hipLaunchKernelGGL(sweep, dim3(static_cast<unsigned>((tiles + 7) / 8 * 8 * nsplit)), dim3(kThreads), lds,
@@ -724,8 +727,6 @@ aq_status euclid_encode_impl(aq_ctx *ctx, const aq_codebooks *cb, const aq_frame
         StageArgs a2 = a;
         a2.fail_count = r.count2;
         a2.fail_list = list2;
-        hipLaunchKernelGGL(scan_values, dim3(static_cast<unsigned>(cus)), dim3(kScanThreads), 0, ctx->stream, a2);
-        AQ_HIP(ctx, hipGetLastError());
         hipLaunchKernelGGL(scan, dim3(static_cast<unsigned>(cus)), dim3(kScanThreads), scan_lds, ctx->stream, a2);
         AQ_HIP(ctx, hipGetLastError());
         return AQ_OK;

@@ -142,7 +142,8 @@ struct StageArgs {
     float *norms;            // sweep -> select: [3][M] |x~|^2, |x - x~|^2, |x|^2
     int nsplit;              // code splits of the sweep
     float *svals;            // [scap, N] exact values of the scanned frames, by list slot
-    int scap;                // frames whose values euclid_scan_values_kernel computes
+    int scap;                // frames whose values the exact scan spreads over its grid
+    int32_t *slot_done;      // [scap] chunks done per slot (zero between stages)
 };
 
 struct RefArgs {
@@ -194,7 +195,6 @@ struct KsKernels {
     StageFn select[4][2];     // [variant][topl]
     RefineFn refine_values[4];
     RefineFn refine_select[4];
-    StageFn scan_values[4];
     StageFn exact_scan[4];
     int lds;                  // sweep dynamic LDS bytes
     int cc;                   // codes per LDS chunk
@@ -1233,10 +1233,10 @@ __global__ __launch_bounds__(kThreads) void euclid_select_kernel(StageArgs a) {
 // ------------------------------------------------------------- exact scan
 
 // Frames that neither certificate settles get an exact scan.  The recipe
-// value of every code (one code per thread) comes from
-// euclid_scan_values_kernel, spread over the grid, when a stage has at most
-// kScanSplitFrames such frames, else from the frame's own block.  One block
-// per frame then selects: in parallel (winner and best topk + 1 codes per
+// value of every code (one code per thread) is computed over the whole grid
+// when a stage has at most kScanSplitFrames such frames (the block that
+// completes a frame's values then selects for it), else by the frame's own
+// block.  The selection, per frame: in parallel (winner and best topk + 1 codes per
 // thread, merged over the block), which is the reference's result unless a
 // value is NaN or the k-th and (k+1)-th values tie; in those cases wave 0
 // walks the values (kScanChunk at a time in LDS) in code order with the
@@ -1285,8 +1285,8 @@ __device__ void heap_adjust(int *hn, float *hv, int hole, int len, int vn, float
 
 constexpr int kScanThreads = 256;
 constexpr int kScanChunk = 2048;
-// Frames per stage whose exact values euclid_scan_values_kernel spreads over
-// the grid; more go through the scan kernel alone.
+// Frames per stage whose exact values the scan spreads over its grid; with
+// more, each frame's block computes its own.
 constexpr int kScanSplitFrames = 64;
 // Order-preserving key of a non-NaN value: a > b (as floats) exactly when
 // ukey(a) > ukey(b); -0 and +0, which compare equal, share a key.  Every key
@@ -1454,42 +1454,6 @@ __device__ void heap_walk(const float *src, int N, int *hn, float *hv) {
         }
 }
 
-// Exact values of every code for the frames the refine pass left open, when
-// there are at most a.scap of them (the usual case: a few per stage), spread
-// over the whole grid: a block takes (list slot, kScanThreads-code chunk)
-// items, one code per thread, and writes a.svals[slot][n].  The per-frame
-// scan then only selects, instead of evaluating N codes on one CU.  The
-// values are exact_value_kq's, so the split changes no result.
-template <int RECIPE, bool Q8, int KS>
-__global__ __launch_bounds__(kScanThreads) void euclid_scan_values_kernel(StageArgs a) {
-    constexpr int K = KS * 32;
-    __shared__ __align__(16) float xs[K];
-    __shared__ __align__(16) int8_t xq[K];
-    __shared__ float xd[K / 32];
-    __shared__ float o_x2;
-    const int count = *a.fail_count;
-    if (count > a.scap) return;
-    const int tid = threadIdx.x;
-    const int nch = (a.N + kScanThreads - 1) / kScanThreads;
-    const int items = count * nch;
-    int cur = -1;
-    for (int item = blockIdx.x; item < items; item += gridDim.x) {
-        const int slot = item / nch;   // block-uniform
-        if (slot != cur) {
-            const int64_t m = a.fail_list[slot];
-            __syncthreads();
-            for (int k = tid; k < K; k += kScanThreads) xs[k] = a.xin[m * K + k];
-            __syncthreads();
-            if (tid == 0) o_x2 = RECIPE == HIGGS ? sum_squares_k<K>(xs) : 0.0f;
-            if (Q8 && tid < K / 32) quantize_block_q8(xs + 32 * tid, xq + 32 * tid, xd + tid);
-            __syncthreads();
-            cur = slot;
-        }
-        const int n = (item % nch) * kScanThreads + tid;
-        if (n < a.N) a.svals[static_cast<int64_t>(slot) * a.N + n] = exact_value_kq<RECIPE, Q8, K>(a, xs, n, o_x2, xq, xd);
-    }
-}
-
 template <int RECIPE, bool Q8, int KS>
 __global__ __launch_bounds__(kScanThreads) void euclid_exact_scan_kernel(StageArgs a) {
     constexpr int K = KS * 32;
@@ -1510,9 +1474,12 @@ __global__ __launch_bounds__(kScanThreads) void euclid_exact_scan_kernel(StageAr
     const int lane = tid & (kWave - 1);
     const int count = *a.fail_count;
     const int ktop = a.topk;
-    // pre: euclid_scan_values_kernel has computed every code's exact value
+    // pre: up to a.scap frames, whose code values the grid computes first
+    // (one (frame, kScanThreads-code chunk) item per block and pass); the
+    // block that completes a frame's last chunk selects for it
     const bool pre = count <= a.scap;
-    for (int slot = blockIdx.x; slot < count; slot += gridDim.x) {
+    __shared__ int o_last;
+    auto scan_slot = [&](int slot) {
         const int64_t m = a.fail_list[slot];
         __syncthreads();
         if (!pre) {
@@ -1817,6 +1784,40 @@ __global__ __launch_bounds__(kScanThreads) void euclid_exact_scan_kernel(StageAr
         if (a.xout)
             for (int k = tid; k < K; k += ST)
                 a.xout[m * K + k] = __fsub_rn(a.xin[m * K + k], a.cbf[static_cast<int64_t>(use) * K + k]);
+    };
+    if (!pre) {
+        for (int slot = blockIdx.x; slot < count; slot += gridDim.x) scan_slot(slot);
+        return;
+    }
+    const int nch = (a.N + ST - 1) / ST;
+    int cur = -1;
+    for (int item = blockIdx.x; item < count * nch; item += gridDim.x) {
+        const int slot = item / nch;   // block-uniform
+        if (slot != cur) {
+            const int64_t m = a.fail_list[slot];
+            __syncthreads();
+            for (int k = tid; k < K; k += ST) xs[k] = a.xin[m * K + k];
+            __syncthreads();
+            if (tid == 0) o_x2 = RECIPE == HIGGS ? sum_squares_k<K>(xs) : 0.0f;
+            if (Q8 && tid < K / 32) quantize_block_q8(xs + 32 * tid, xq + 32 * tid, xd + tid);
+            __syncthreads();
+            cur = slot;
+        }
+        const int n = (item % nch) * ST + tid;
+        if (n < a.N)
+            a.svals[static_cast<int64_t>(slot) * a.N + n] = exact_value_kq<RECIPE, Q8, K>(a, xs, n, o_x2, xq, xd);
+        // release: this block's values before the frame's counter; the block
+        // that brings it to nch sees every chunk's values after its acquire
+        __threadfence();
+        __syncthreads();
+        if (tid == 0) o_last = atomicAdd(&a.slot_done[slot], 1) == nch - 1;
+        __syncthreads();
+        if (o_last) {
+            __threadfence();
+            scan_slot(slot);
+            if (tid == 0) a.slot_done[slot] = 0;   // ready for the next stage
+            cur = -1;                              // scan_slot used xs
+        }
     }
 }
 
@@ -2318,8 +2319,6 @@ __global__ __launch_bounds__(kWave) void euclid_refine_select_kernel(StageArgs a
              euclid_refine_values_kernel<DIRECT, false, KS>, euclid_refine_values_kernel<HIGGS, true, KS>},     \
             {euclid_refine_select_kernel<OMNI, false, KS>, euclid_refine_select_kernel<HIGGS, false, KS>,       \
              euclid_refine_select_kernel<DIRECT, false, KS>, euclid_refine_select_kernel<HIGGS, true, KS>},     \
-            {euclid_scan_values_kernel<OMNI, false, KS>, euclid_scan_values_kernel<HIGGS, false, KS>,           \
-             euclid_scan_values_kernel<DIRECT, false, KS>, euclid_scan_values_kernel<HIGGS, true, KS>},         \
             {euclid_exact_scan_kernel<OMNI, false, KS>, euclid_exact_scan_kernel<HIGGS, false, KS>,             \
              euclid_exact_scan_kernel<DIRECT, false, KS>, euclid_exact_scan_kernel<HIGGS, true, KS>},           \
             Tile<KS>::LDS,                                                                                      \
