@@ -254,7 +254,7 @@ typedef enum aq_codebook_type {
 aq_status aq_euclid_upload(aq_ctx *ctx, int64_t Q, int64_t N, int64_t K, int cb_type, const void *data,
                            int recipe, aq_codebooks **out);
 /* aq_euclid_upload from device memory (a codebook already resident, e.g.
- * read by aq_gguf_* into a device buffer or produced by a graph): data is a
+ * loaded by the caller's weight store or produced by a graph): data is a
  * device pointer of the same layout, copied on the context's stream. */
 aq_status aq_euclid_upload_device(aq_ctx *ctx, int64_t Q, int64_t N, int64_t K, int cb_type, const void *data,
                                   int recipe, aq_codebooks **out);
