@@ -207,6 +207,8 @@ public:
         ctx_->check(aq_dac_decode(ctx_->get(), st_, codes, M, recon));
     }
 
+    const aq_dac_stages *handle() const { return st_; }
+
 private:
     Context *ctx_;
     int64_t Q_, D_, N_;
