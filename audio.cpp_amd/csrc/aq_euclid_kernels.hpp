@@ -658,13 +658,18 @@ __global__ __launch_bounds__(kThreads, sweep_blocks_per_cu(KS)) void euclid_swee
     //    the VALU work only overlaps the matrix pipe when it sits between
     //    the MFMAs;
     //  * the next chunk is staged into the other LDS buffer a few 16-byte
-    //    pieces per block (global load in one block, LDS store in the next),
-    //    with one barrier per chunk.  The last chunk re-stages itself into
-    //    the idle buffer, which keeps the loop free of branches.
+    //    pieces per block, with one barrier per chunk.  Where a chunk holds
+    //    several blocks the pieces go straight from global memory to LDS
+    //    (global_load_lds: no registers, and nothing waits for them before
+    //    the chunk's end); a one-block chunk (K = 768) stages them through
+    //    registers (global load in the block, LDS store after it), which
+    //    measured faster there.  The last chunk re-stages itself into the
+    //    idle buffer, which keeps the loop free of branches.
     constexpr int BPC = T::CC / 16;
     constexpr int R = KS % 4 == 0 ? 4 : 2;
     constexpr int L = R - 1;
     constexpr int PPB = (T::STAGE16 + BPC - 1) / BPC;   // staged pieces per block
+    constexpr bool kDirect = BPC > 1;
 
     auto lds_a = [&](int buf, int blk, int ks) -> typename MX::V8 {
         const int r = blk * 16 + col;
@@ -685,9 +690,36 @@ __global__ __launch_bounds__(kThreads, sweep_blocks_per_cu(KS)) void euclid_swee
     };
     const u32x4 *cb16 = reinterpret_cast<const u32x4 *>(a.cbh);
     const int hsrc = threadIdx.x < T::CC ? threadIdx.x : 0;
+    // Direct staging: the 16 bytes of lane l of wave w land at LDS piece
+    // q = k * kThreads + 64 w + l (a wave's 64 pieces are contiguous, as the
+    // instruction requires), so piece q fetches code row q / CH16, k-piece
+    // (q % CH16) ^ (row & SWZ): the XOR swizzle that lds_a reads.  The
+    // |c|^2/2 slots follow the same per-thread layout as h_dst.
+    const unsigned char *cbb = reinterpret_cast<const unsigned char *>(a.cbh);
+    auto stage_piece = [&](int buf, int chunk, int k) {
+        const int q = threadIdx.x + k * kThreads;
+        const int r = q / T::CH16, j = (q % T::CH16) ^ (r & T::SWZ);
+        const unsigned char *g = cbb + static_cast<int64_t>(chunk) * T::CHUNKB + r * T::ROWB + j * 16;
+        unsigned char *d = lds + buf * T::BUFB + (k * kThreads + wave * kWave) * 16;
+        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)g,
+                                         (__attribute__((address_space(3))) void *)d, 16, 0, 0);
+    };
+    auto stage_h = [&](int buf, int chunk) {
+        const float *g = a.nhh + static_cast<int64_t>(chunk) * T::CC + hsrc;
+        unsigned char *d = lds + buf * T::BUFB + T::CHUNKB + wave * kWave * 4;
+        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)g,
+                                         (__attribute__((address_space(3))) void *)d, 4, 0, 0);
+    };
+    // s_waitcnt vmcnt(0) lgkmcnt(0): this wave's direct loads have landed
+    constexpr int kWaitLoads = 0x0070;
 
     // prologue: chunk 0 in full
-    {
+    if constexpr (kDirect) {
+#pragma unroll
+        for (int k = 0; k < T::STAGE16; ++k) stage_piece(0, c0, k);
+        stage_h(0, c0);
+        __builtin_amdgcn_s_waitcnt(kWaitLoads);
+    } else {
 #pragma unroll
         for (int k = 0; k < T::STAGE16; ++k) {
             const int p = threadIdx.x + k * kThreads;
@@ -734,21 +766,31 @@ __global__ __launch_bounds__(kThreads, sweep_blocks_per_cu(KS)) void euclid_swee
         const u32x4 *src = cb16 + static_cast<int64_t>(cs) * (T::CHUNKB / 16);
 #pragma unroll
         for (int b = 0; b < BPC; ++b) {
-            // store the pieces fetched in the previous block, fetch this block's
-            if (b > 0) {
+            if constexpr (kDirect) {
+                // this block's share of the next chunk, straight into LDS
 #pragma unroll
                 for (int i = 0; i < PPB; ++i) {
-                    const int k = (b - 1) + i * BPC;
-                    if (k < T::STAGE16) *piece_dst(buf ^ 1, threadIdx.x + k * kThreads) = stg[i];
+                    const int k = b + i * BPC;
+                    if (k < T::STAGE16) stage_piece(buf ^ 1, cs, k);
                 }
-                if (b == 1) *h_dst(buf ^ 1) = hstg;
-            }
+                if (b == 0) stage_h(buf ^ 1, cs);
+            } else {
+                // store the pieces fetched in the previous block, fetch this block's
+                if (b > 0) {
 #pragma unroll
-            for (int i = 0; i < PPB; ++i) {
-                const int k = b + i * BPC;
-                if (k < T::STAGE16) stg[i] = src[threadIdx.x + k * kThreads];
+                    for (int i = 0; i < PPB; ++i) {
+                        const int k = (b - 1) + i * BPC;
+                        if (k < T::STAGE16) *piece_dst(buf ^ 1, threadIdx.x + k * kThreads) = stg[i];
+                    }
+                    if (b == 1) *h_dst(buf ^ 1) = hstg;
+                }
+#pragma unroll
+                for (int i = 0; i < PPB; ++i) {
+                    const int k = b + i * BPC;
+                    if (k < T::STAGE16) stg[i] = src[threadIdx.x + k * kThreads];
+                }
+                if (b == 0) hstg = a.nhh[static_cast<int64_t>(cs) * T::CC + hsrc];
             }
-            if (b == 0) hstg = a.nhh[static_cast<int64_t>(cs) * T::CC + hsrc];
 
             // the accumulators start from -|c|^2/2 of the block's codes
             f32x4 acc[FG];
@@ -776,13 +818,17 @@ __global__ __launch_bounds__(kThreads, sweep_blocks_per_cu(KS)) void euclid_swee
             for (int g = 0; g < FG; ++g) accp[g] = acc[g];
             lprev = static_cast<unsigned>((c * BPC + b) * 4);
         }
-        // the pieces fetched in the chunk's last block
+        if constexpr (kDirect) {
+            __builtin_amdgcn_s_waitcnt(kWaitLoads);
+        } else {
+            // the pieces fetched in the chunk's last block
 #pragma unroll
-        for (int i = 0; i < PPB; ++i) {
-            const int k = (BPC - 1) + i * BPC;
-            if (k < T::STAGE16) *piece_dst(buf ^ 1, threadIdx.x + k * kThreads) = stg[i];
+            for (int i = 0; i < PPB; ++i) {
+                const int k = (BPC - 1) + i * BPC;
+                if (k < T::STAGE16) *piece_dst(buf ^ 1, threadIdx.x + k * kThreads) = stg[i];
+            }
+            if (BPC == 1) *h_dst(buf ^ 1) = hstg;
         }
-        if (BPC == 1) *h_dst(buf ^ 1) = hstg;
         __syncthreads();
 #pragma unroll
         for (int l = 0; l < L; ++l) ring[l] = lds_a(buf ^ 1, 0, l);
