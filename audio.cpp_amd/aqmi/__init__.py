@@ -392,7 +392,7 @@ class Codebooks:
             _dptr(residual), _dptr(dist), topk, _dptr(topk_idx), _dptr(topk_dist), _dptr(force_idx)))
 
     def failures(self) -> np.ndarray:
-        """Frames per stage the bf16 certificate left to the refine pass."""
+        """Frames per stage the fp16 certificate left open (refine pass or exact scan)."""
         out = np.zeros(64, np.int32)
         self.ctx.check(self.ctx.lib.aq_euclid_failures(self.ctx.h, self.h, out.ctypes.data_as(C.c_void_p)))
         return out[: min(self.Q, 64)]

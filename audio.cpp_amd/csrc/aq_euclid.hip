@@ -111,30 +111,18 @@ __global__ void q8_quantize_kernel(const float *__restrict__ x, int64_t nblocks,
     }
 }
 
-// bf16 / fp16 images, round to nearest even (bf16: NaN kept quiet, as a
-// truncation with the quiet bit set).
-__device__ inline uint16_t img_bf16(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7F800000u) == 0x7F800000u) return static_cast<uint16_t>((u >> 16) | ((u & 0xFFFFu) ? 0x40u : 0u));
-    u += 0x7FFFu + ((u >> 16) & 1u);
-    return static_cast<uint16_t>(u >> 16);
-}
-__device__ inline uint16_t img_f16(float f) { return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f)); }
-template <bool Q8>
-__device__ inline uint16_t img_half(float f) { return Q8 ? img_f16(f) : img_bf16(f); }
-template <bool Q8>
-__device__ inline float img_float(uint16_t h) {
-    return Q8 ? static_cast<float>(__builtin_bit_cast(_Float16, h)) : __uint_as_float(static_cast<uint32_t>(h) << 16);
-}
+// fp16 images, round to nearest even.
+__device__ inline uint16_t img_half(float f) { return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f)); }
+__device__ inline float img_float(uint16_t h) { return static_cast<float>(__builtin_bit_cast(_Float16, h)); }
 
-// Per code row (one thread each): the matrix-core images c_h = half(c) and
-// c_l = half(c - c_h) (bf16 for F32 codebooks, fp16 for Q8_0), the per-code
+// Per code row (one thread each): the matrix-core images c_h = fp16(c) and
+// c_l = fp16(c - c_h), the per-code
 // constants -|c|^2 / 2 (sweep), -|c|^2 (OmniVoice bias, double sum of double
 // products) and sum_rows(c * c) (Higgs: fp32 squares summed in double), and
 // per stage the largest |c|, |c_h - c|, |c_h|, |c_l| and |c - c_h - c_l|
 // (as double bit patterns, atomicMax over non-negative values; NaN skipped)
-// for the certificate's bounds.  nonfinite[0] = 1 on any non-finite entry.
-template <bool Q8>
+// for the certificate's bounds.  nonfinite[0] = 1 on any non-finite entry
+// or one beyond fp16's range (the stage is then scanned exactly).
 __global__ void euclid_prep_kernel(const float *__restrict__ cbf, int64_t QN, int64_t N, int K,
                                    uint16_t *__restrict__ cbh, uint16_t *__restrict__ cbl, float *__restrict__ hh,
                                    float *__restrict__ bias, float *__restrict__ e2,
@@ -146,15 +134,15 @@ __global__ void euclid_prep_kernel(const float *__restrict__ cbf, int64_t QN, in
     bool nf = false;
     for (int k = 0; k < K; ++k) {
         const float c = cbf[row + k];
-        nf |= !__builtin_isfinite(c);
-        const uint16_t h = img_half<Q8>(c);
+        const uint16_t h = img_half(c);
         cbh[row + k] = h;
-        const float hf = img_float<Q8>(h);
+        const float hf = img_float(h);
+        nf |= !__builtin_isfinite(hf);
         // c - c_h and c - c_h - c_l are exact in fp32 (finite c)
         const float dl = __fsub_rn(c, hf);
-        const uint16_t l = __builtin_isfinite(dl) ? img_half<Q8>(dl) : 0;
+        const uint16_t l = __builtin_isfinite(dl) ? img_half(dl) : 0;
         cbl[row + k] = l;
-        const double ld = img_float<Q8>(l), rd = __dsub_rn(static_cast<double>(dl), ld);
+        const double ld = img_float(l), rd = __dsub_rn(static_cast<double>(dl), ld);
         const double cd = c, hd = hf, dd = __dsub_rn(hd, cd);
         sq = __dadd_rn(sq, __dmul_rn(cd, cd));
         e2d = __dadd_rn(e2d, static_cast<double>(__fmul_rn(c, c)));
@@ -202,8 +190,8 @@ struct aq_codebooks {
     int recipe = 0;
     bool q8 = false;
     bool exact_only = false;
-    uint16_t *d_cbh = nullptr;   // [Q][N][K] bf16 (fp16 for Q8_0)
-    uint16_t *d_cbl = nullptr;   // [Q][N][K] bf16(c - bf16(c)) (refine pass; fp16 for Q8_0)
+    uint16_t *d_cbh = nullptr;   // [Q][N][K] fp16(c)
+    uint16_t *d_cbl = nullptr;   // [Q][N][K] fp16(c - fp16(c)) (refine pass)
     float *d_hh = nullptr;       // [Q][N] -|c|^2 / 2 (fp32 of the double sum)
     float *d_cbf = nullptr;      // [Q][N][K]
     float *d_bias = nullptr;     // [Q][N] (OMNI)
@@ -312,14 +300,9 @@ aq_status euclid_prepare(aq_ctx *ctx, aq_codebooks *cb) {
     bool ok = hipMemsetAsync(smax, 0, sizeof(unsigned long long) * (5 * cb->Q + 1), ctx->stream) == hipSuccess;
     if (ok) {
         const dim3 grid(static_cast<unsigned>((QN + 127) / 128)), block(128);
-        if (cb->q8)
-            hipLaunchKernelGGL(euclid_prep_kernel<true>, grid, block, 0, ctx->stream, cb->d_cbf, QN, cb->N,
-                               static_cast<int>(cb->K), cb->d_cbh, cb->d_cbl, cb->d_hh, cb->d_bias, cb->d_e2, smax,
-                               nonfinite);
-        else
-            hipLaunchKernelGGL(euclid_prep_kernel<false>, grid, block, 0, ctx->stream, cb->d_cbf, QN, cb->N,
-                               static_cast<int>(cb->K), cb->d_cbh, cb->d_cbl, cb->d_hh, cb->d_bias, cb->d_e2, smax,
-                               nonfinite);
+        hipLaunchKernelGGL(euclid_prep_kernel, grid, block, 0, ctx->stream, cb->d_cbf, QN, cb->N,
+                           static_cast<int>(cb->K), cb->d_cbh, cb->d_cbl, cb->d_hh, cb->d_bias, cb->d_e2, smax,
+                           nonfinite);
         ok = hipGetLastError() == hipSuccess &&
              hipMemcpyAsync(host.data(), smax, sizeof(unsigned long long) * host.size(), hipMemcpyDeviceToHost,
                             ctx->stream) == hipSuccess &&
@@ -556,7 +539,7 @@ aq_status euclid_encode_impl(aq_ctx *ctx, const aq_codebooks *cb, const aq_frame
     const aq_proj_weights *pw = cb->proj;
     const int64_t H = pw ? pw->H : K;   // width of the input and of the residual
     // Keys per lane: 4 for top-4, and for large codebooks (N * K >= 2^22),
-    // where a frame the first certificate leaves open costs a split-bf16
+    // where a frame the first certificate leaves open costs a split-fp16
     // pass over N * K; 3 otherwise (one med3 less per score in the sweep).
     const int topl = (topk >= 4 || cb->N * cb->K >= (int64_t{1} << 22)) ? 4 : 3;
     const KsKernels *kk = kernels_for(ks);
@@ -602,7 +585,7 @@ aq_status euclid_encode_impl(aq_ctx *ctx, const aq_codebooks *cb, const aq_frame
         if (st != AQ_OK) return st;
         keys = static_cast<float *>(w);
     }
-    // Counters (per stage, modulo 64): [0, 64) frames the bf16 certificate
+    // Counters (per stage, modulo 64): [0, 64) frames the fp16 certificate
     // left open, [64, 128) frames sent on to the exact scan, [128, 128 +
     // kScanSplitFrames) the exact scan's chunks done per frame; then the two
     // frame lists.
@@ -727,6 +710,7 @@ aq_status euclid_encode_impl(aq_ctx *ctx, const aq_codebooks *cb, const aq_frame
         StageArgs a2 = a;
         a2.fail_count = r.count2;
         a2.fail_list = list2;
+        a2.open_count = a.fail_count;
         hipLaunchKernelGGL(scan, dim3(static_cast<unsigned>(cus)), dim3(kScanThreads), scan_lds, ctx->stream, a2);
         AQ_HIP(ctx, hipGetLastError());
         return AQ_OK;

@@ -1,7 +1,7 @@
 // Euclidean VQ / RVQ kernels for gfx950, shared by the per-width translation
 // units (aq_euclid_ks*.hip) and the host code (aq_euclid.hip).
 //
-// Euclidean VQ / RVQ encode on gfx950: nearest codeword by bf16 MFMA
+// Euclidean VQ / RVQ encode on gfx950: nearest codeword by fp16 MFMA
 // distance contraction, a per-lane top-L epilogue, a rigorous error
 // certificate, and exact re-ranking in the reference recipe's own fp32
 // arithmetic.  Also the codebook gather and the multi-stage decode sum.
@@ -26,8 +26,8 @@
 // accumulation), ggml_vec_argmax_f32 (vec.h:1576-1584, last index of the max).
 //
 // Design
-//  * Scores: v(n) = x~ . c~_n - |c_n|^2/2 with x~, c~ rounded to bf16, from
-//    v_mfma_f32_16x16x32_bf16 with codes as A and frames as B.  Each wave
+//  * Scores: v(n) = x~ . c~_n - |c_n|^2/2 with x~, c~ rounded to fp16, from
+//    v_mfma_f32_16x16x32_f16 with codes as A and frames as B.  Each wave
 //    keeps FG groups of 16 frames of x~ in registers for the whole sweep over
 //    the codebook, which streams through double-buffered, XOR-swizzled LDS
 //    (conflict-free 16-byte reads).  Output lane l owns frame l%16 and codes
@@ -41,10 +41,11 @@
 //    Cauchy-Schwarz), the fp32 accumulation bounds and the key truncation.
 //    Kept candidates that could still be in the top T are re-ranked exactly;
 //    the result is certified when the T-th exact value beats every unkept
-//    code's bound.  Otherwise the frame is scored again with split bf16
-//    operands (a bound about 2^-8 of the first) and, if that certificate
-//    fails too, by an exact full scan, so results never depend on bf16
-//    rounding.
+//    code's bound.  Otherwise the frame is scored again with split fp16
+//    operands (a bound about 2^-11 of the first) and, if that certificate
+//    fails too, by an exact full scan, so results never depend on fp16
+//    rounding.  A few open frames (up to the exact scan's spread capacity)
+//    skip the split pass and go to the exact scan at once.
 //  * Residual cascade: per stage the sweep, the select (re-rank, update
 //    r -= c), the refine pair and the exact scan; the last three exit at
 //    once when no frame is left for them.
@@ -61,33 +62,25 @@ constexpr int kWave = 64;
 constexpr int kWaves = 4;
 constexpr int kThreads = kWave * kWaves;
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
-// Matrix-core operand type of the sweep and the refine pass: bf16 for F32
-// codebooks; fp16 for Q8_0 codebooks, whose dequantised codes q * d carry up
-// to 18 significant bits: fp16's 11-bit mantissa makes the certificate's
-// bound 8x tighter there, which settles most of the frames a bf16 bound
-// leaves open (top-4 needs the 4th/5th gap).  The fp16 matrix ops run
-// slower than bf16 on long sweeps, so F32 codebooks keep bf16.
-template <bool Q8>
+// Matrix-core operand type of the sweep and the refine pass: fp16.  Its
+// 11-bit mantissa makes the certificate's bound 8x tighter than bf16's
+// (about 30x fewer frames left open on Mimi-shaped data; Q8_0's dequantised
+// codes q * d carry up to 18 significant bits, and top-4 needs the 4th/5th
+// gap), at the same matrix-core rate.  The matrix cores keep fp16 subnormal
+// inputs, so the images' rounding errors, which the bounds measure, are the
+// errors the products see.  Values beyond fp16's range become infinite:
+// such a frame fails its certificate and is scanned exactly, and a codebook
+// with such an entry is scanned exactly for every frame.
 struct Mx {
-    using E = __bf16;
-    using V8 = bf16x8;
-    typedef __bf16 V2 __attribute__((ext_vector_type(2)));
-    __device__ static f32x4 mfma(V8 a, V8 b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0); }
-    // the two values of a packed pair as fp32
-    __device__ static float lo(unsigned w) { return __uint_as_float(w << 16); }
-    __device__ static float hi(unsigned w) { return __uint_as_float(w & 0xFFFF0000u); }
-};
-template <>
-struct Mx<true> {
     using E = _Float16;
     using V8 = f16x8;
     typedef _Float16 V2 __attribute__((ext_vector_type(2)));
     __device__ static f32x4 mfma(V8 a, V8 b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
+    // the two values of a packed pair as fp32
     __device__ static float lo(unsigned w) { return static_cast<float>(__builtin_bit_cast(V2, w)[0]); }
     __device__ static float hi(unsigned w) { return static_cast<float>(__builtin_bit_cast(V2, w)[1]); }
 };
@@ -103,7 +96,7 @@ constexpr int kRWaves = 4;     // refine_values waves per block
 template <int KS>
 struct Tile {
     static constexpr int K = KS * 32;
-    static constexpr int ROWB = K * 2;                         // bytes per bf16 code row
+    static constexpr int ROWB = K * 2;                         // bytes per fp16 code row
     static constexpr int CH16 = K / 8;                         // 16-byte chunks per row
     static constexpr int SWZ = CH16 >= 16 ? 15 : CH16 - 1;     // XOR swizzle mask
     static constexpr int CC = (32768 / ROWB) >= 16 ? ((32768 / ROWB) / 16) * 16 : 16;   // codes per LDS chunk
@@ -118,7 +111,7 @@ struct StageArgs {
     float *xout;             // [M, K] residual leaving the stage (may alias xin; null: not needed)
     int64_t M;
     int N;
-    const uint16_t *cbh;     // [N, K] bf16 codebook (scores)
+    const uint16_t *cbh;     // [N, K] fp16 codebook (scores)
     const float *nhh;        // [N] -|c|^2 / 2 (the score accumulators start from it)
     const float *cbf;        // [N, K] fp32 codebook (dequantised for Q8_0)
     const float *bias;       // [N] OmniVoice score bias
@@ -144,10 +137,11 @@ struct StageArgs {
     float *svals;            // [scap, N] exact values of the scanned frames, by list slot
     int scap;                // frames whose values the exact scan spreads over its grid
     int32_t *slot_done;      // [scap] chunks done per slot (zero between stages)
+    const int32_t *open_count;   // exact scan: the frames the select left open (null: not known)
 };
 
 struct RefArgs {
-    const uint16_t *cbl;       // [N, K] bf16(c - bf16(c))
+    const uint16_t *cbl;       // [N, K] fp16(c - fp16(c))
     float *keys;               // [cap][nslices][4][kTopR] (RefShape)
     int64_t key_floats;        // capacity of the key buffer
     int32_t *count2;           // exact-scan counter of this stage
@@ -180,7 +174,7 @@ __device__ inline RefShape ref_shape(const RefArgs &rf, int N, int count) {
 using StageFn = void (*)(StageArgs);
 using RefineFn = void (*)(StageArgs, RefArgs);
 
-// 16-frame groups per sweep wave: the bf16 frames of a wave stay in
+// 16-frame groups per sweep wave: the fp16 frames of a wave stay in
 // registers (4 * KS registers per group), so wider codebooks take fewer.
 constexpr int groups_for(int ks) { return ks <= 2 ? 4 : (ks <= 8 ? 3 : 2); }
 // Sweep blocks resident per CU (the launch bound the register budget follows).
@@ -587,9 +581,9 @@ __global__ __launch_bounds__(kThreads, sweep_blocks_per_cu(KS)) void euclid_swee
     const int cps = (N / T::CC) / a.nsplit;   // chunks per split
     const int c0 = split * cps, c1 = c0 + cps;
 
-    using MX = Mx<Q8>;
-    // ---- phase 0: frames -> bf16 fragments in registers, rounding norms ----
-    // x~ fragments stay packed (2 bf16 per register) for the whole sweep.
+    using MX = Mx;
+    // ---- phase 0: frames -> fp16 fragments in registers, rounding norms ----
+    // x~ fragments stay packed (2 fp16 per register) for the whole sweep.
     u32x4 xb[FG][KS];
     float nx2[FG], nd2[FG], nxx2[FG];
 #pragma unroll
@@ -604,8 +598,8 @@ __global__ __launch_bounds__(kThreads, sweep_blocks_per_cu(KS)) void euclid_swee
             const f32x4 hi = *reinterpret_cast<const f32x4 *>(xr + ks * 32 + kq * 8 + 4);
             float v[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
             // A Q8_0 mul_mat scores the query's Q8_0 image x_q = q * d, so
-            // the matrix cores contract bf16(x_q) and the bound only has to
-            // cover bf16 rounding.
+            // the matrix cores contract fp16(x_q) and the bound only has to
+            // cover fp16 rounding.
             if (Q8) q8_image_block(v);
             u32x4 packed;
 #pragma unroll
@@ -937,14 +931,14 @@ __global__ __launch_bounds__(kThreads) void euclid_select_kernel(StageArgs a) {
         // Bound E (in units of v = x.c - |c|^2/2) on |v(n) - S'(n)| for every n.
         const float nx = sqrtf(nx2[g]) * 1.0001f, nd = sqrtf(nd2[g]) * 1.0001f;
         const float nxe = nx + nd;                           // >= |x|
-        const float e_bf16 = nx * a.dcmax + nd * a.cmax;
+        const float e_half = nx * a.dcmax + nd * a.cmax;
         // fp32 accumulation from -|c|^2/2: partial sums stay below
         // |x~||c~| + |c|^2/2
         const float e_acc = (K + 4) * u * (nx * a.chmax + 0.5f * a.cmax * a.cmax);
         const float e_rec = (K + 16) * u * (nxe * a.cmax + nxe * nxe + a.cmax * a.cmax);
         const float vmax = nx * a.chmax + 0.5f * a.cmax * a.cmax + e_rec;
         const float trunc = ldexpf(vmax, lbits - 23);
-        const float E = 1.02f * (e_bf16 + e_acc + e_rec + 4.0f * u * vmax) + trunc + 1e-30f;
+        const float E = 1.02f * (e_half + e_acc + e_rec + 4.0f * u * vmax) + trunc + 1e-30f;
 
         // Keys of the frame's 4 lanes, gathered in every one of them.
         float all[4 * TOPL];
@@ -1334,6 +1328,7 @@ constexpr int kScanChunk = 2048;
 // Frames per stage whose exact values the scan spreads over its grid; with
 // more, each frame's block computes its own.
 constexpr int kScanSplitFrames = 64;
+constexpr int kScanQuadCodes = kScanThreads / 4;   // codes per spread item, four lanes each
 // Order-preserving key of a non-NaN value: a > b (as floats) exactly when
 // ukey(a) > ukey(b); -0 and +0, which compare equal, share a key.  Every key
 // is at least ukey(-inf) = 0x007FFFFF.
@@ -1498,6 +1493,79 @@ __device__ void heap_walk(const float *src, int N, int *hn, float *hv) {
             hn[q] = n[q];
             hv[q] = src[n[q]];
         }
+}
+
+// ---------------------------------------------------- spread exact values
+// The exact values of every code of up to scap open frames, spread over the
+// grid: item (slot, chunk) writes svals[slot][chunk codes].  F32 codebooks
+// in tinyBLAS order take four lanes per code (lane q of a quad accumulates
+// k = 16 l + 4 q + t, t < 4: tinyBLAS lanes 4q .. 4q+3) and kScanQuadCodes
+// codes per item, every row and frame read issued at once, then reduce16's
+// tree across the quad (lanes q, q ^ 2 hold accumulators j, j + 8; lanes 0,
+// 1 then hold t3[j], t3[j + 4]).  Otherwise a code per thread, kScanThreads
+// codes per item, from the frame staged in xs (its Q8_0 blocks in xq, xd)
+// while the block stays on one slot (cur).  x2s: the frame's
+// sum_rows(x*x) (Higgs).  Called by every thread of a kScanThreads block.
+template <int RECIPE, bool Q8>
+__device__ inline bool spread_quad(const StageArgs &a) { return !Q8 && RECIPE != DIRECT && a.order == 0; }
+template <int RECIPE, bool Q8>
+__device__ inline int spread_chunks(const StageArgs &a) {
+    const int cpi = spread_quad<RECIPE, Q8>(a) ? kScanQuadCodes : kScanThreads;
+    return (a.N + cpi - 1) / cpi;
+}
+template <int RECIPE, bool Q8, int K>
+__device__ void spread_item(const StageArgs &a, int slot, int chunk, int &cur, float *xs, int8_t *xq, float *xd,
+                            float &x2s) {
+    const int tid = threadIdx.x;
+    constexpr bool kQuadOk = !Q8 && RECIPE != DIRECT;
+    if (kQuadOk && spread_quad<RECIPE, Q8>(a)) {
+        const int64_t m = a.fail_list[slot];
+        const float *xr = a.xin + m * K;
+        __syncthreads();   // the previous item's readers of x2s
+        if (RECIPE == HIGGS && tid == 0) x2s = sum_squares_k<K>(xr);
+        const int n = chunk * kScanQuadCodes + tid / 4;
+        const int q = tid & 3;
+        const int nc = n < a.N ? n : a.N - 1;
+        const float *cr = a.cbf + static_cast<int64_t>(nc) * K;
+        const float sa = RECIPE == OMNI ? 2.0f : 1.0f;
+        f32x4 vc[K / 16], vx[K / 16];
+#pragma unroll
+        for (int l = 0; l < K / 16; ++l) {
+            vc[l] = *reinterpret_cast<const f32x4 *>(cr + 16 * l + 4 * q);
+            vx[l] = *reinterpret_cast<const f32x4 *>(xr + 16 * l + 4 * q);
+        }
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int l = 0; l < K / 16; ++l)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) acc[t] = __fmaf_rn(vc[l][t] * sa, vx[l][t], acc[t]);
+        float t3[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) t3[t] = __fadd_rn(__shfl_xor(acc[t], 2), acc[t]);
+        float t6[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) t6[t] = __fadd_rn(__shfl_xor(t3[t], 1), t3[t]);
+        const float dot = __fadd_rn(__fadd_rn(t6[0], t6[2]), __fadd_rn(t6[1], t6[3]));
+        if (RECIPE == HIGGS) __syncthreads();   // x2s
+        if (q == 0 && n < a.N) {
+            const float v = RECIPE == OMNI ? __fadd_rn(dot, a.bias[n])
+                                           : __fsub_rn(__fsub_rn(__fmul_rn(dot, 2.0f), x2s), a.e2[n]);
+            a.svals[static_cast<int64_t>(slot) * a.N + n] = v;
+        }
+        return;
+    }
+    if (slot != cur) {
+        const int64_t m = a.fail_list[slot];
+        __syncthreads();
+        for (int k = tid; k < K; k += kScanThreads) xs[k] = a.xin[m * K + k];
+        __syncthreads();
+        if (tid == 0) x2s = RECIPE == HIGGS ? sum_squares_k<K>(xs) : 0.0f;
+        if (Q8 && tid < K / 32) quantize_block_q8(xs + 32 * tid, xq + 32 * tid, xd + tid);
+        __syncthreads();
+        cur = slot;
+    }
+    const int n = chunk * kScanThreads + tid;
+    if (n < a.N) a.svals[static_cast<int64_t>(slot) * a.N + n] = exact_value_kq<RECIPE, Q8, K>(a, xs, n, x2s, xq, xd);
 }
 
 template <int RECIPE, bool Q8, int KS>
@@ -1831,27 +1899,19 @@ __global__ __launch_bounds__(kScanThreads) void euclid_exact_scan_kernel(StageAr
             for (int k = tid; k < K; k += ST)
                 a.xout[m * K + k] = __fsub_rn(a.xin[m * K + k], a.cbf[static_cast<int64_t>(use) * K + k]);
     };
-    if (!pre) {
+    // Values already spread by the refine_values launch: the select left no
+    // more open frames than the spread holds, and refine_select handed them
+    // all on (the kernel boundary orders their values before these reads).
+    const bool ready = pre && a.open_count != nullptr && *a.open_count <= a.scap;
+    if (!pre || ready) {
         for (int slot = blockIdx.x; slot < count; slot += gridDim.x) scan_slot(slot);
         return;
     }
-    const int nch = (a.N + ST - 1) / ST;
+    const int nch = spread_chunks<RECIPE, Q8>(a);
     int cur = -1;
     for (int item = blockIdx.x; item < count * nch; item += gridDim.x) {
         const int slot = item / nch;   // block-uniform
-        if (slot != cur) {
-            const int64_t m = a.fail_list[slot];
-            __syncthreads();
-            for (int k = tid; k < K; k += ST) xs[k] = a.xin[m * K + k];
-            __syncthreads();
-            if (tid == 0) o_x2 = RECIPE == HIGGS ? sum_squares_k<K>(xs) : 0.0f;
-            if (Q8 && tid < K / 32) quantize_block_q8(xs + 32 * tid, xq + 32 * tid, xd + tid);
-            __syncthreads();
-            cur = slot;
-        }
-        const int n = (item % nch) * ST + tid;
-        if (n < a.N)
-            a.svals[static_cast<int64_t>(slot) * a.N + n] = exact_value_kq<RECIPE, Q8, K>(a, xs, n, o_x2, xq, xd);
+        spread_item<RECIPE, Q8, K>(a, slot, item % nch, cur, xs, xq, xd, o_x2);
         // release: this block's values before the frame's counter; the block
         // that brings it to nch sees every chunk's values after its acquire
         __threadfence();
@@ -1869,17 +1929,21 @@ __global__ __launch_bounds__(kScanThreads) void euclid_exact_scan_kernel(StageAr
 
 // ------------------------------------------------------------- refine pass
 
-// Frames the bf16 certificate leaves open are scored again with split bf16
+// Frames the fp16 certificate leaves open are scored again with split fp16
 // operands before any exact scan.  With x = x_h + x_l + x_r and
-// c = c_h + c_l + c_r (x_h = bf16(x), x_l = bf16(x - x_h), x_r the exact
+// c = c_h + c_l + c_r (x_h = fp16(x), x_l = fp16(x - x_h), x_r the exact
 // remainder; likewise c), the refined score is
 //   s(n) = x_h.c_h + (x_h.c_l + x_l.c_h) - |c_n|^2/2
 // from three MFMAs per K slice.  The dropped terms x_h.c_r + x_l.c_l +
 // x_l.c_r + x_r.c are bounded by Cauchy-Schwarz with the frame's |x_h|,
-// |x_l|, |x_r| and the codebook's largest |c_l|, |c_r|, |c|: about 2^-16 of
-// |x||c|, against 2^-8 for plain bf16.  The same certificate as in the stage
-// kernel then settles nearly every open frame with a bound about 100 times
-// smaller; the rest go to the exact scan.
+// |x_l|, |x_r| and the codebook's largest |c_l|, |c_r|, |c|: about 2^-22 of
+// |x||c|, against 2^-11 for plain fp16 (less where x_l or c_l fall into
+// fp16's subnormal range; the bounds use the measured remainders).  The
+// same certificate as in the stage kernel then settles nearly every open
+// frame; the rest go to the exact scan.  When no more open frames than the
+// exact scan spreads over the grid are left, the pass is skipped:
+// refine_values computes their exact values over the grid instead,
+// refine_select hands the list on, and the exact scan selects.
 //  * refine_values: a wave takes 16 open frames x one slice of rs codes and
 //    keeps, per lane, its kTopR best keys (score with the slice-local code
 //    index in the low 6 mantissa bits) in a key buffer.
@@ -1888,7 +1952,7 @@ __global__ __launch_bounds__(kScanThreads) void euclid_exact_scan_kernel(StageAr
 //    certificate and writes codes, distances, top-k and the residual.
 
 
-// LDS image of one 16-code block for the refine pass: bf16 high and low
+// LDS image of one 16-code block for the refine pass: fp16 high and low
 // rows (XOR-swizzled 16-byte pieces, as in the sweep) and -|c|^2/2.
 template <int KS>
 struct RefTile {
@@ -1906,12 +1970,27 @@ template <int RECIPE, bool Q8, int KS>
 __global__ __launch_bounds__(kWave * kRWaves, KS <= 8 ? 2 : 1) void euclid_refine_values_kernel(StageArgs a, RefArgs rf) {
     using T = RefTile<KS>;
     constexpr int K = KS * 32;
-    static_assert(kWave * kRWaves == kThreads, "refine blocks have the sweep's shape");
+    static_assert(kWave * kRWaves == kThreads && kThreads == kScanThreads,
+                  "refine blocks have the sweep's and the spread items' shape");
     __shared__ __align__(16) unsigned char lds[2 * T::BUFB];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
     const int col = lane & 15, kq = lane >> 4;
-    const RefShape rsh = ref_shape(rf, a.N, *a.fail_count);
+    const int open = *a.fail_count;
+    if (open <= a.scap) {
+        // Few open frames: no split pass.  Their exact values, spread over
+        // the grid, for the exact scan, which then only selects.
+        float *xs = reinterpret_cast<float *>(lds);
+        int8_t *xq = reinterpret_cast<int8_t *>(xs + K);
+        float *xd = reinterpret_cast<float *>(xq + K);
+        float *x2s = xd + K / 32;
+        const int nch = spread_chunks<RECIPE, Q8>(a);
+        int cur = -1;
+        for (int item = blockIdx.x; item < open * nch; item += gridDim.x)
+            spread_item<RECIPE, Q8, K>(a, item / nch, item % nch, cur, xs, xq, xd, *x2s);
+        return;
+    }
+    const RefShape rsh = ref_shape(rf, a.N, open);
     const int count = rsh.cap;
     const int ntiles = (count + 16 * kRWaves - 1) / (16 * kRWaves);
     const int64_t nwork = static_cast<int64_t>(ntiles) * rsh.nslices;
@@ -1923,7 +2002,7 @@ __global__ __launch_bounds__(kWave * kRWaves, KS <= 8 ? 2 : 1) void euclid_refin
         const int r = q / T::CH16, j = q % T::CH16;
         return buf * T::BUFB + arr * (16 * T::ROWB) + r * T::ROWB + ((j ^ (r & T::SWZ)) * 16);
     };
-    using MX = Mx<Q8>;
+    using MX = Mx;
     auto lds_a = [&](int buf, int arr, int ks) -> typename MX::V8 {
         const int j = ks * 4 + kq;
         return *reinterpret_cast<const typename MX::V8 *>(lds + buf * T::BUFB + arr * (16 * T::ROWB) + col * T::ROWB +
@@ -2113,6 +2192,14 @@ __global__ __launch_bounds__(kWave) void euclid_refine_select_kernel(StageArgs a
     const int Tk = a.topk > 0 ? a.topk : 1;
     const int Tsel = a.topk > 0 ? a.topk + 1 : 1;
     const int count = *a.fail_count;
+    if (count <= a.scap) {
+        // few open frames: no split pass, the exact scan takes the list
+        if (blockIdx.x == 0) {
+            for (int i = lane; i < count; i += kWave) rf.list2[i] = a.fail_list[i];
+            if (lane == 0) *rf.count2 = count;
+        }
+        return;
+    }
     const RefShape rsh = ref_shape(rf, a.N, count);
     const int nk = rsh.nslices * 4 * kTopR;
     for (int slot = blockIdx.x; slot < count; slot += gridDim.x) {
@@ -2135,9 +2222,9 @@ __global__ __launch_bounds__(kWave) void euclid_refine_select_kernel(StageArgs a
                 const float id = am != 0.0f ? __fdiv_rn(127.0f, am) : 0.0f;
                 v = __fmul_rn(__builtin_rintf(__fmul_rn(v, id)), dq);
             }
-            const float h = static_cast<float>(static_cast<typename Mx<Q8>::E>(v));
+            const float h = static_cast<float>(static_cast<Mx::E>(v));
             const float d = v - h;
-            const float l = static_cast<float>(static_cast<typename Mx<Q8>::E>(d));
+            const float l = static_cast<float>(static_cast<Mx::E>(d));
             const float r = d - l;
             sh = __fmaf_rn(h, h, sh);
             sl = __fmaf_rn(l, l, sl);

@@ -222,7 +222,7 @@ aq_status aq_dac_decode_ex(aq_ctx *ctx, const aq_dac_stages *stages, const int32
  *                        order), first index of the minimum
  *                        (VectorQuantizer::compute, host_ops.cpp:236-273;
  *                        Qwen3 nearest_code, tokenizer_speech_encoder.cpp:287-303)
- * Scores are contracted in bf16 on the matrix cores; every code that could
+ * Scores are contracted in fp16 on the matrix cores; every code that could
  * win is re-ranked in the recipe's fp32 arithmetic under a rigorous error
  * bound, and frames the bound cannot settle are rescanned exactly, so the
  * outputs equal the reference's. */
@@ -328,15 +328,16 @@ aq_status aq_euclid_upload_projected(aq_ctx *ctx, int64_t Q, int64_t N, int64_t 
                                      const void *w_out, const float *b_out, int recipe, aq_codebooks **out);
 
 /* Frames per stage (first min(Q, 64) stages) of the last encode on ctx that
- * the bf16 error certificate could not settle; the split-bf16 refine pass
- * took them (host int32 array; synchronises the stream).  A measurement aid
- * with no reference counterpart. */
+ * the fp16 error certificate could not settle: the split-fp16 refine pass
+ * took them or, when no more than 64 were open, the exact scan (host int32
+ * array; synchronises the stream).  A measurement aid with no reference
+ * counterpart. */
 aq_status aq_euclid_failures(aq_ctx *ctx, const aq_codebooks *cb, int32_t *host_counts);
 
 /* Frames per stage (first min(Q, 64) stages) of the last encode on ctx that
- * the refine pass could not settle either and the exact scan decided (host
- * int32 array; synchronises the stream).  A measurement aid with no
- * reference counterpart. */
+ * the exact scan decided: those the refine pass left open, or all open
+ * frames when no more than 64 were (host int32 array; synchronises the
+ * stream).  A measurement aid with no reference counterpart. */
 aq_status aq_euclid_exact_scans(aq_ctx *ctx, const aq_codebooks *cb, int32_t *host_counts);
 
 /* EMA codebook materialisation, once at load (Mimi-style codecs store

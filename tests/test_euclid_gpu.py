@@ -2,7 +2,7 @@
 
 Every recipe is compared with the oracle on the same seeded inputs: codes
 equal, the final residual and the reported distances bit-identical, top-k
-sets and values identical.  The bf16 matrix-core scores only choose
+sets and values identical.  The fp16 matrix-core scores only choose
 candidates; the certificate plus the exact re-rank make the outputs the
 reference arithmetic's, which these tests check at shapes the oracle
 finishes in seconds (full BASELINE sizes are checked against golden
@@ -440,6 +440,48 @@ def test_other_widths_and_q8_widths(torch, ctx, oracle, recipe, cb_type, K, N, M
         check_topk(out, ref)
 
 
+def near_duplicate_groups(rows, Q=2):
+    """Mimi-shaped data whose codewords come in groups of 8 that differ by
+    multiples of 2^-13 (relative) and fall in the same sweep lane (codes
+    16 apart): more near-ties than a lane keeps, closer than the fp16
+    certificate can separate and far apart for the split-fp16 refine pass,
+    so every frame is left open and the refine pass settles it."""
+    from aqmi import synth
+
+    cfg = mimi(rows, Q=Q)
+    cb = cfg["codebook"]
+    Qn, N, K = cb.shape
+    g = cb.reshape(Qn, N // 128, 8, 16, K)
+    scale = (1.0 + np.arange(8, dtype=np.float32) * np.float32(2.0 ** -13))[None, None, :, None, None]
+    g[:] = (g[:, :, :1] * scale + synth.normal(72, 1, g.shape, 2.0 ** -20)).astype(np.float32)
+    cfg["codebook"] = np.ascontiguousarray(g.reshape(Qn, N, K))
+    half = rows // 2
+    cfg["x"][:half] = (cfg["codebook"][0, (37 * np.arange(half)) % N]
+                       + synth.normal(72, 2, (half, K), 0.05)).astype(np.float32)
+    return cfg
+
+
+@pytest.mark.parametrize("recipe", [0, 1, 2])
+def test_refine_pass_settles_near_duplicates(torch, ctx, oracle, recipe):
+    """More open frames than the exact scan spreads (64) go through the
+    split-fp16 refine pass, which settles nearly all of them; results are
+    the reference's.  (Up to 512 open frames the pass works in 32-code
+    slices, whose lane lists keep two members of each group.)"""
+    print(f"[gpu] refine near duplicates recipe={recipe}", flush=True)
+    cfg = near_duplicate_groups(400)
+    out = run(torch, ctx, cfg["codebook"], recipe, cfg["x"])
+    ref = {0: oracle.euclid_rvq, 1: oracle.higgs_rvq, 2: oracle.direct_rvq}[recipe](cfg)
+    scans = out["cbs"].exact_scans()
+    print(f"[gpu] open frames {out['fails'].tolist()}, exact scans {scans.tolist()}", flush=True)
+    assert (out["fails"] > 64).all() and (scans < out["fails"] // 4).all()
+    assert np.array_equal(out["idx"], ref["idx"])
+    assert np.array_equal(bits(out["residual"]), bits(ref["residual"]))
+    if recipe == 0:
+        assert np.array_equal(bits(out["dist"]), bits(-ref["logit"]))
+    else:
+        assert np.array_equal(bits(out["dist"]), bits(ref["dist"]))
+
+
 def test_refine_capacity_overflow_goes_to_exact_scan(torch, ctx, oracle, monkeypatch):
     """With the refine pass's key buffer capped at two frames (test hook
     AQ_EUCLID_REFINE_KEY_FLOATS), every further frame the first certificate
@@ -448,7 +490,7 @@ def test_refine_capacity_overflow_goes_to_exact_scan(torch, ctx, oracle, monkeyp
     import aqmi
 
     print("[gpu] refine capacity overflow", flush=True)
-    cfg = mimi(4000, Q=2)
+    cfg = near_duplicate_groups(400)
     monkeypatch.setenv("AQ_EUCLID_REFINE_KEY_FLOATS", "2048")
     out = run(torch, ctx, cfg["codebook"], aqmi.OMNIVOICE, cfg["x"])
     scans = out["cbs"].exact_scans()
@@ -457,4 +499,4 @@ def test_refine_capacity_overflow_goes_to_exact_scan(torch, ctx, oracle, monkeyp
     assert np.array_equal(bits(out["residual"]), bits(ref["residual"]))
     assert np.array_equal(bits(out["dist"]), bits(-ref["logit"]))
     print(f"[gpu] open frames {out['fails'].tolist()}, exact scans {scans.tolist()}", flush=True)
-    assert (out["fails"] > 2).all() and (scans >= out["fails"] - 2).all()
+    assert (out["fails"] > 64).all() and (scans >= out["fails"] - 2).all()
