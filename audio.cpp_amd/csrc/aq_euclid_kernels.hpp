@@ -284,19 +284,26 @@ __device__ float dist_direct(const float *__restrict__ x, const float *__restric
 
 // x86 quantize_row_q8_0 on one 32-element block: d = amax/127 stored as fp16,
 // id = 127/amax, q = round-half-even(x*id) with int8 saturation.
+// One quant of x86 quantize_row_q8_0: round half to even of x * id (the
+// conversion of _mm256_cvtps_epi32, whose out-of-range result packs to -128),
+// saturated to int8 by the packs.
+__device__ inline int q8_quant(float x, float id) {
+    const float v = __builtin_rintf(__fmul_rn(x, id));
+    if (!(v >= -2147483648.0f && v < 2147483648.0f)) return -128;
+    const int qi = static_cast<int>(v);
+    return qi < -128 ? -128 : (qi > 127 ? 127 : qi);
+}
+// The block's scale d = fp16(amax / 127) (as fp32) and 127 / amax.
+__device__ inline void q8_scale(float amax, float &d, float &id) {
+    d = static_cast<float>(static_cast<_Float16>(__fdiv_rn(amax, 127.0f)));
+    id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+}
 __device__ inline void quantize_block_q8(const float *__restrict__ x, int8_t *__restrict__ q, float *__restrict__ d) {
     float amax = 0.0f;
     for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(x[j]));
-    const _Float16 h = static_cast<_Float16>(__fdiv_rn(amax, 127.0f));
-    *d = static_cast<float>(h);
-    const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
-    for (int j = 0; j < 32; ++j) {
-        const float v = __builtin_rintf(__fmul_rn(x[j], id));
-        int qi;
-        if (!(v >= -2147483648.0f && v < 2147483648.0f)) qi = -128;
-        else qi = static_cast<int>(v) < -128 ? -128 : (static_cast<int>(v) > 127 ? 127 : static_cast<int>(v));
-        q[j] = static_cast<int8_t>(qi);
-    }
+    float id;
+    q8_scale(amax, *d, id);
+    for (int j = 0; j < 32; ++j) q[j] = static_cast<int8_t>(q8_quant(x[j], id));
 }
 
 // tinyBLAS_Q0 / ggml_vec_dot_q8_0_q8_0: per block, 8 exact 4-element int
@@ -910,7 +917,11 @@ __global__ __launch_bounds__(kThreads) void euclid_select_kernel(StageArgs a) {
     constexpr int QCAP = FG * 16 * 4 * TOPL;
     __shared__ int32_t q_n_s[kWaves][QCAP], q_f_s[kWaves][QCAP];
     __shared__ float q_v_s[kWaves][QCAP], q_x2_s[kWaves][FG * 16];
-    __shared__ __align__(16) int8_t q_xq_s[kWaves][Q8 ? 16 * K : 4];     // Q8_0 blocks of the frames
+    // Q8_0 blocks of the frames, XQS bytes apart: the 8 lane groups of a
+    // pass read 8 frames' blocks, which a stride of K + 32 bytes puts in
+    // different LDS banks.
+    constexpr int XQS = K + 32;
+    __shared__ __align__(16) int8_t q_xq_s[kWaves][Q8 ? 16 * XQS : 4];
     __shared__ float q_xd_s[kWaves][Q8 ? 16 * (K / 32) : 1];
     int32_t *q_n = q_n_s[wave];
     int32_t *q_f = q_f_s[wave];
@@ -1000,23 +1011,75 @@ __global__ __launch_bounds__(kThreads) void euclid_select_kernel(StageArgs a) {
             qcount += __popcll(bal);
         }
     }
-    // 2b: sum_rows(x*x) of each frame that has candidates (one lane per frame)
-    if (RECIPE == HIGGS) {
-        int needmask = 0;   // bit g: frame (g, lane % 16) has candidates
+    // 2b: sum_rows(x*x) of each frame that has candidates, and (Q8_0) each
+    // frame's query blocks quantised once (x86 quantize_row_q8_0).  For
+    // K % 256 == 0 the frame's 4 lanes load it in one round trip per 256
+    // elements (lane kq the 64 from 64 kq), add their squares in order in
+    // turn (the double running sum handed on from lane to lane) and quantise
+    // their two blocks from registers.
+    if (RECIPE == HIGGS && K % 256 == 0) {
+        if (__any(needg[0])) {
+            static_assert(FG == 1, "one frame group per select wave");
+            const int64_t mq = m_base + col < a.M ? m_base + col : a.M - 1;
+            const float *xr = a.xin + mq * K;
+            double sq = 0.0;
 #pragma unroll
-        for (int g = 0; g < FG; ++g) needmask |= (__shfl(needg[g] ? 1 : 0, lane % 16) & 1) << g;
-        if (lane < FG * 16) {
-            const bool need = ((needmask >> (lane / 16)) & 1) != 0;
-            q_x2[lane] = need ? sum_squares_k<K>(a.xin + (m_base + lane) * K) : 0.0f;
+            for (int c = 0; c < K / 256; ++c) {
+                f32x4 v[16];
+#pragma unroll
+                for (int i = 0; i < 16; ++i) v[i] = *reinterpret_cast<const f32x4 *>(xr + 256 * c + 64 * kq + 4 * i);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    if (kq == q)
+#pragma unroll
+                        for (int i = 0; i < 16; ++i)
+#pragma unroll
+                            for (int t = 0; t < 4; ++t) sq += static_cast<double>(__fmul_rn(v[i][t], v[i][t]));
+                    sq = __shfl(sq, col + 16 * q);
+                }
+                if (Q8) {
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const int blk = 8 * c + 2 * kq + h;
+                        float amax = 0.0f;
+#pragma unroll
+                        for (int i = 0; i < 8; ++i)
+#pragma unroll
+                            for (int t = 0; t < 4; ++t) amax = fmaxf(amax, fabsf(v[8 * h + i][t]));
+                        float d, id;
+                        q8_scale(amax, d, id);
+                        int *qw = reinterpret_cast<int *>(q_xq + col * XQS + 32 * blk);
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) {
+                            unsigned w = 0;
+#pragma unroll
+                            for (int t = 0; t < 4; ++t)
+                                w |= (static_cast<unsigned>(q8_quant(v[8 * h + i][t], id)) & 0xFFu) << (8 * t);
+                            qw[i] = static_cast<int>(w);
+                        }
+                        q_xd[col * (K / 32) + blk] = d;
+                    }
+                }
+            }
+            if (kq == 0) q_x2[col] = static_cast<float>(sq);
         }
-    }
-    // Q8_0: each frame's query blocks are quantised once (x86
-    // quantize_row_q8_0), the 4 lanes of a frame taking every 4th block.
-    if (Q8 && qcount > 0) {
-        const int64_t mq = m_base + col < a.M ? m_base + col : a.M - 1;
+    } else {
+        if (RECIPE == HIGGS) {
+            int needmask = 0;   // bit g: frame (g, lane % 16) has candidates
 #pragma unroll
-        for (int ib = kq; ib < K / 32; ib += 4)
-            quantize_block_q8(a.xin + mq * K + 32 * ib, q_xq + col * K + 32 * ib, q_xd + col * (K / 32) + ib);
+            for (int g = 0; g < FG; ++g) needmask |= (__shfl(needg[g] ? 1 : 0, lane % 16) & 1) << g;
+            if (lane < FG * 16) {
+                const bool need = ((needmask >> (lane / 16)) & 1) != 0;
+                q_x2[lane] = need ? sum_squares_k<K>(a.xin + (m_base + lane) * K) : 0.0f;
+            }
+        }
+        // Q8_0: the 4 lanes of a frame taking every 4th block.
+        if (Q8 && qcount > 0) {
+            const int64_t mq = m_base + col < a.M ? m_base + col : a.M - 1;
+#pragma unroll
+            for (int ib = kq; ib < K / 32; ib += 4)
+                quantize_block_q8(a.xin + mq * K + 32 * ib, q_xq + col * XQS + 32 * ib, q_xd + col * (K / 32) + ib);
+        }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -1026,9 +1089,9 @@ __global__ __launch_bounds__(kThreads) void euclid_select_kernel(StageArgs a) {
         // tinyBLAS: 16 accumulators over k = 16 l + j, one per lane of a
         // 16-lane row (coalesced row reads), then _mm512_reduce_add_ps's
         // pairing tree as DPP row rotations 8, 4, 2, 1; 4 pairs per pass.
-        // Two pairs per row and pass, so that their row reads are in flight
-        // together.
-        constexpr int P = 2;
+        // Several pairs per row and pass (four up to K = 256, else two), so
+        // that their row reads are in flight together.
+        constexpr int P = K <= 256 ? 4 : 2;
         const int j = lane & 15, grp = lane >> 4;
         const float sa = RECIPE == OMNI ? 2.0f : 1.0f;
         for (int e0 = grp; e0 < qcount; e0 += 4 * P) {
@@ -1064,25 +1127,43 @@ __global__ __launch_bounds__(kThreads) void euclid_select_kernel(StageArgs a) {
         // ggml_vec_dot_q8_0_q8_0: 8 accumulators over the 4-element groups
         // of every block, one per lane of an 8-lane group, then hsum_float_8
         // (i + 4, then pairs) as lane exchanges 4, 2, 1; 8 pairs per pass.
+        // Several pairs per group and pass (as registers allow), so that
+        // their code rows are read together.
+        constexpr int P = K <= 256 ? 4 : (K <= 512 ? 2 : 1);
         const int j = lane & 7, grp = lane >> 3;
-        for (int e = grp; e < qcount; e += 8) {
-            const int fs = q_f[e];
-            const int n = q_n[e];
-            const int *cq = reinterpret_cast<const int *>(a.q8 + static_cast<int64_t>(n) * K) + j;
-            const float *cd = a.q8d + static_cast<int64_t>(n) * (K / 32);
-            const int *xq = reinterpret_cast<const int *>(q_xq + fs * K) + j;
-            const float *xd = q_xd + fs * (K / 32);
-            float acc = 0.0f;
+        for (int e0 = grp; e0 < qcount; e0 += 8 * P) {
+            int cq[P][K / 32], fs[P], n[P];
+            float cd[P][K / 32];
 #pragma unroll
-            for (int ib = 0; ib < K / 32; ++ib) {
-                const float dd = __fmul_rn(cd[ib], xd[ib]);
-                acc = __fmaf_rn(dd, static_cast<float>(__builtin_amdgcn_sdot4(cq[8 * ib], xq[8 * ib], 0, false)), acc);
+            for (int p = 0; p < P; ++p) {
+                const int e = e0 + 8 * p < qcount ? e0 + 8 * p : e0;
+                fs[p] = q_f[e];
+                n[p] = q_n[e];
+                const int *cqp = reinterpret_cast<const int *>(a.q8 + static_cast<int64_t>(n[p]) * K) + j;
+                const float *cdp = a.q8d + static_cast<int64_t>(n[p]) * (K / 32);
+#pragma unroll
+                for (int ib = 0; ib < K / 32; ++ib) {
+                    cq[p][ib] = cqp[8 * ib];
+                    cd[p][ib] = cdp[ib];
+                }
             }
-            // lane 0 of the group: ((a0 + a4) + (a2 + a6)) + ((a1 + a5) + (a3 + a7))
-            acc = __fadd_rn(acc, __shfl_xor(acc, 4));
-            acc = __fadd_rn(acc, __shfl_xor(acc, 2));
-            acc = __fadd_rn(acc, __shfl_xor(acc, 1));
-            if (j == 0) q_v[e] = __fsub_rn(__fsub_rn(__fmul_rn(acc, 2.0f), q_x2[fs]), a.e2[n]);
+#pragma unroll
+            for (int p = 0; p < P; ++p) {
+                const int *xq = reinterpret_cast<const int *>(q_xq + fs[p] * XQS) + j;
+                const float *xd = q_xd + fs[p] * (K / 32);
+                float acc = 0.0f;
+#pragma unroll
+                for (int ib = 0; ib < K / 32; ++ib) {
+                    const float dd = __fmul_rn(cd[p][ib], xd[ib]);
+                    acc = __fmaf_rn(dd, static_cast<float>(__builtin_amdgcn_sdot4(cq[p][ib], xq[8 * ib], 0, false)), acc);
+                }
+                // lane 0 of the group: ((a0 + a4) + (a2 + a6)) + ((a1 + a5) + (a3 + a7))
+                acc = __fadd_rn(acc, __shfl_xor(acc, 4));
+                acc = __fadd_rn(acc, __shfl_xor(acc, 2));
+                acc = __fadd_rn(acc, __shfl_xor(acc, 1));
+                const int e = e0 + 8 * p;
+                if (j == 0 && e < qcount) q_v[e] = __fsub_rn(__fsub_rn(__fmul_rn(acc, 2.0f), q_x2[fs[p]]), a.e2[n[p]]);
+            }
         }
     } else {
         for (int e0 = 0; e0 < qcount; e0 += kWave) {
