@@ -603,14 +603,18 @@ aq_status euclid_encode_impl(aq_ctx *ctx, const aq_codebooks *cb, const aq_frame
     int32_t *list = fails + kCounters;
     int32_t *list2 = list + M;
     RefArgs rf{};
-    // Refine-pass keys: the larger of the two slicings' needs (short slices
-    // for up to kRSmallFrames open frames, long slices for all M), at most
-    // 64 MiB; frames beyond the capacity go straight to the exact scan.
+    // Refine-pass keys: the largest of the slicings' needs (short slices for
+    // up to kRSmallFrames open frames, middle ones for up to kRMidFrames,
+    // long slices for all M), at most
+    // 64 MiB; frames beyond the capacity go straight to the exact scan (a
+    // buffer too small for short slices of the open frames takes long ones).
     {
         const int64_t per_small =   // floats per frame
             cb->N <= kRSmallCodes ? ((cb->N + kRSSmall - 1) / kRSSmall) * 4 * kTopR : ((cb->N + kRS - 1) / kRS) * 4 * kTopR;
+        const int64_t per_mid = ((cb->N + kRSMid - 1) / kRSMid) * 4 * kTopR;
         const int64_t per_big = ((cb->N + kRS - 1) / kRS) * 4 * kTopR;
-        int64_t floats = std::max(std::min<int64_t>(M, kRSmallFrames) * per_small, M * per_big);
+        int64_t floats = std::max({std::min<int64_t>(M, kRSmallFrames) * per_small,
+                                   std::min<int64_t>(M, kRMidFrames) * per_mid, M * per_big});
         floats = std::min<int64_t>(floats, (int64_t{64} << 20) / 4);
         // Test hook: AQ_EUCLID_REFINE_KEY_FLOATS caps the buffer, so that the
         // path from the capacity limit to the exact scan runs at small sizes.
