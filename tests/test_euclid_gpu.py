@@ -483,10 +483,11 @@ def test_refine_pass_settles_near_duplicates(torch, ctx, oracle, recipe):
 
 
 def test_refine_capacity_overflow_goes_to_exact_scan(torch, ctx, oracle, monkeypatch):
-    """With the refine pass's key buffer capped at two frames (test hook
-    AQ_EUCLID_REFINE_KEY_FLOATS), every further frame the first certificate
-    leaves open must reach the exact scan without reading keys past the
-    buffer, and the results stay the reference's."""
+    """With the refine pass's key buffer capped at 2048 floats (test hook
+    AQ_EUCLID_REFINE_KEY_FLOATS: too few for short or middle slices of the
+    open frames, and 16 frames of long-slice keys), every further frame the
+    first certificate leaves open must reach the exact scan without reading
+    keys past the buffer, and the results stay the reference's."""
     import aqmi
 
     print("[gpu] refine capacity overflow", flush=True)
@@ -499,4 +500,4 @@ def test_refine_capacity_overflow_goes_to_exact_scan(torch, ctx, oracle, monkeyp
     assert np.array_equal(bits(out["residual"]), bits(ref["residual"]))
     assert np.array_equal(bits(out["dist"]), bits(-ref["logit"]))
     print(f"[gpu] open frames {out['fails'].tolist()}, exact scans {scans.tolist()}", flush=True)
-    assert (out["fails"] > 64).all() and (scans >= out["fails"] - 2).all()
+    assert (out["fails"] > 64).all() and (scans >= out["fails"] - 16).all() and (scans <= out["fails"]).all()
