@@ -1596,6 +1596,14 @@ __device__ void heap_walk(const float *src, int N, int *hn, float *hv) {
 // sum_rows(x*x) (Higgs).  Called by every thread of a kScanThreads block.
 template <int RECIPE, bool Q8>
 __device__ inline bool spread_quad(const StageArgs &a) { return !Q8 && RECIPE != DIRECT && a.order == 0; }
+// Whether the open frames of a stage skip the split pass: at most scap of
+// them, and their exact values read at most kDirectElems codebook elements
+// (count * N * K; 64 MiB of fp32 rows), above which the split pass, which
+// reads the fp16 codebook once per 64 open frames, costs less.
+constexpr int64_t kDirectElems = int64_t{1} << 24;
+__device__ inline bool direct_scan(const StageArgs &a, int count, int K) {
+    return count <= a.scap && static_cast<int64_t>(count) * a.N * K <= kDirectElems;
+}
 template <int RECIPE, bool Q8>
 __device__ inline int spread_chunks(const StageArgs &a) {
     const int cpi = spread_quad<RECIPE, Q8>(a) ? kScanQuadCodes : kScanThreads;
@@ -1616,17 +1624,22 @@ __device__ void spread_item(const StageArgs &a, int slot, int chunk, int &cur, f
         const int nc = n < a.N ? n : a.N - 1;
         const float *cr = a.cbf + static_cast<int64_t>(nc) * K;
         const float sa = RECIPE == OMNI ? 2.0f : 1.0f;
-        f32x4 vc[K / 16], vx[K / 16];
-#pragma unroll
-        for (int l = 0; l < K / 16; ++l) {
-            vc[l] = *reinterpret_cast<const f32x4 *>(cr + 16 * l + 4 * q);
-            vx[l] = *reinterpret_cast<const f32x4 *>(xr + 16 * l + 4 * q);
-        }
+        // up to 256 elements' reads in flight at once (32 float4 registers)
+        constexpr int KC = K < 256 ? K : 256;
         float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int l = 0; l < K / 16; ++l)
+        for (int k0 = 0; k0 < K; k0 += KC) {
+            f32x4 vc[KC / 16], vx[KC / 16];
 #pragma unroll
-            for (int t = 0; t < 4; ++t) acc[t] = __fmaf_rn(vc[l][t] * sa, vx[l][t], acc[t]);
+            for (int l = 0; l < KC / 16; ++l) {
+                vc[l] = *reinterpret_cast<const f32x4 *>(cr + k0 + 16 * l + 4 * q);
+                vx[l] = *reinterpret_cast<const f32x4 *>(xr + k0 + 16 * l + 4 * q);
+            }
+#pragma unroll
+            for (int l = 0; l < KC / 16; ++l)
+#pragma unroll
+                for (int t = 0; t < 4; ++t) acc[t] = __fmaf_rn(vc[l][t] * sa, vx[l][t], acc[t]);
+        }
         float t3[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) t3[t] = __fadd_rn(__shfl_xor(acc[t], 2), acc[t]);
@@ -1987,10 +2000,10 @@ __global__ __launch_bounds__(kScanThreads) void euclid_exact_scan_kernel(StageAr
             for (int k = tid; k < K; k += ST)
                 a.xout[m * K + k] = __fsub_rn(a.xin[m * K + k], a.cbf[static_cast<int64_t>(use) * K + k]);
     };
-    // Values already spread by the refine_values launch: the select left no
-    // more open frames than the spread holds, and refine_select handed them
-    // all on (the kernel boundary orders their values before these reads).
-    const bool ready = pre && a.open_count != nullptr && *a.open_count <= a.scap;
+    // Values already spread by the refine_values launch: the select left
+    // few open frames (direct_scan), and refine_select handed them all on
+    // (the kernel boundary orders their values before these reads).
+    const bool ready = pre && a.open_count != nullptr && direct_scan(a, *a.open_count, K);
     if (!pre || ready) {
         for (int slot = blockIdx.x; slot < count; slot += gridDim.x) scan_slot(slot);
         return;
@@ -2065,7 +2078,7 @@ __global__ __launch_bounds__(kWave * kRWaves, KS <= 8 ? 2 : 1) void euclid_refin
     const int wave = threadIdx.x / kWave;
     const int col = lane & 15, kq = lane >> 4;
     const int open = *a.fail_count;
-    if (open <= a.scap) {
+    if (direct_scan(a, open, K)) {
         // Few open frames: no split pass.  Their exact values, spread over
         // the grid, for the exact scan, which then only selects.
         float *xs = reinterpret_cast<float *>(lds);
@@ -2280,7 +2293,7 @@ __global__ __launch_bounds__(kWave) void euclid_refine_select_kernel(StageArgs a
     const int Tk = a.topk > 0 ? a.topk : 1;
     const int Tsel = a.topk > 0 ? a.topk + 1 : 1;
     const int count = *a.fail_count;
-    if (count <= a.scap) {
+    if (direct_scan(a, count, K)) {
         // few open frames: no split pass, the exact scan takes the list
         if (blockIdx.x == 0) {
             for (int i = lane; i < count; i += kWave) rf.list2[i] = a.fail_list[i];
