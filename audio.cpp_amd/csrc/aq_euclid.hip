@@ -20,6 +20,14 @@ using namespace aq_euclid;
 // --------------------------------------------------------------- gather, sum
 
 // out[m] = cbf[stage][idx[m]] (get_rows; Q8_0 rows dequantised).
+// Zeroes a[0, na) and b[0, nb) (the encode's counters and status words).  A
+// kernel rather than hipMemsetAsync, so that a caller may capture the encode
+// in a HIP graph: memset nodes have given wrong results on graph replays.
+__global__ void zero2_kernel(int32_t *__restrict__ a, int na, int32_t *__restrict__ b, int nb) {
+    for (int i = threadIdx.x; i < na; i += blockDim.x) a[i] = 0;
+    for (int i = threadIdx.x; i < nb; i += blockDim.x) b[i] = 0;
+}
+
 __global__ void gather_kernel(const float *__restrict__ cbf, int64_t N, int64_t K, const int32_t *__restrict__ idx,
                               int64_t M, float *__restrict__ out, int32_t *__restrict__ flags) {
     const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -648,8 +656,9 @@ aq_status euclid_encode_impl(aq_ctx *ctx, const aq_codebooks *cb, const aq_frame
     rf.list2 = list2;
     RefineFn rvals = kk->refine_values[var];
     RefineFn rsel = kk->refine_select[var];
-    AQ_HIP(ctx, hipMemsetAsync(counts, 0, sizeof(int32_t) * kCounters, ctx->stream));
-    AQ_HIP(ctx, hipMemsetAsync(ctx->d_flags, 0, sizeof(int32_t) * AQ_FLAG_COUNT, ctx->stream));
+    hipLaunchKernelGGL(zero2_kernel, dim3(1), dim3(256), 0, ctx->stream, counts, kCounters, ctx->d_flags,
+                       static_cast<int>(AQ_FLAG_COUNT));
+    AQ_HIP(ctx, hipGetLastError());
 
     // Stage s of the pipeline: queries xin [M, K], residual out xout (null:
     // not needed), teacher forcing `force` of the codebook-space update.
@@ -691,7 +700,10 @@ aq_status euclid_encode_impl(aq_ctx *ctx, const aq_codebooks *cb, const aq_frame
         a.svals = svals;
         a.scap = scap;
         a.slot_done = slot_done;
-        if (s >= 64 && s % 64 == 0) AQ_HIP(ctx, hipMemsetAsync(counts, 0, sizeof(int32_t) * 128, ctx->stream));
+        if (s >= 64 && s % 64 == 0) {
+            hipLaunchKernelGGL(zero2_kernel, dim3(1), dim3(256), 0, ctx->stream, counts, 128, counts, 0);
+            AQ_HIP(ctx, hipGetLastError());
+        }
         const int tslot = arena.base ? -1 : aq_timing_start(ctx);   // events are not created without allocation
         hipLaunchKernelGGL(sweep, dim3(static_cast<unsigned>((tiles + 7) / 8 * 8 * nsplit)), dim3(kThreads), lds,
                            ctx->stream, a);
@@ -824,7 +836,9 @@ aq_status aq_codebook_gather(aq_ctx *ctx, const aq_codebooks *cb, int64_t stage,
     if (stage < 0 || stage >= cb->Q || M < 0) return aq_fail(ctx, AQ_E_SHAPE, "aq_codebook_gather: stage or M out of range");
     if (M == 0) return AQ_OK;
     aq_device_guard g(ctx->device);
-    AQ_HIP(ctx, hipMemsetAsync(ctx->d_flags, 0, sizeof(int32_t) * AQ_FLAG_COUNT, ctx->stream));
+    hipLaunchKernelGGL(zero2_kernel, dim3(1), dim3(256), 0, ctx->stream, ctx->d_flags, static_cast<int>(AQ_FLAG_COUNT),
+                       ctx->d_flags, 0);
+    AQ_HIP(ctx, hipGetLastError());
     const int64_t total = M * cb->K;
     hipLaunchKernelGGL(gather_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, ctx->stream,
                        cb->d_cbf + stage * cb->N * cb->K, cb->N, cb->K, idx, M, out, ctx->d_flags);
@@ -841,7 +855,9 @@ aq_status aq_euclid_decode(aq_ctx *ctx, const aq_codebooks *cb, const int32_t *i
     if (M < 0) return aq_fail(ctx, AQ_E_SHAPE, "aq_euclid_decode: negative M");
     if (M == 0) return AQ_OK;
     aq_device_guard g(ctx->device);
-    AQ_HIP(ctx, hipMemsetAsync(ctx->d_flags, 0, sizeof(int32_t) * AQ_FLAG_COUNT, ctx->stream));
+    hipLaunchKernelGGL(zero2_kernel, dim3(1), dim3(256), 0, ctx->stream, ctx->d_flags, static_cast<int>(AQ_FLAG_COUNT),
+                       ctx->d_flags, 0);
+    AQ_HIP(ctx, hipGetLastError());
     const int64_t total = M * cb->K;
     if (cb->proj) {
         aq_status st = aq_proj_decode(ctx, cb->proj, idx, M, out);

@@ -22,7 +22,11 @@
 // code dimension j of frame f -- the reference's sequential sum over the
 // latent channels -- and then scores codes j, j + 8, ... of the frame; the
 // 8 lanes of a frame merge their winners with the reference's tie rule.  The
-// residual update then sweeps each frame's channels across the wave.
+// residual update then sweeps each frame's channels across the wave.  The
+// chains are latency-bound (one wave per SIMD or fewer), so the stage's
+// in-projection weights and normalised codebook are staged in LDS when they
+// fit (an L2 round trip per few elements otherwise), and the residual update
+// reads each channel's out-projection row once for the wave's 8 frames.
 #include "aq_device_math.hpp"
 #include "aq_internal.hpp"
 
@@ -34,7 +38,8 @@ namespace {
 
 constexpr int kWave = 64;
 constexpr int kHF = 8;   // frames per wave
-constexpr int kHW = 2;   // waves per block
+constexpr int kOtW = 3;  // waves per block (OuteTTS: 24 frames share the staged in-projection)
+constexpr int kMsW = 3;  // waves per block (MOSS)
 
 // ------------------------------------------------------------------ OuteTTS
 
@@ -48,14 +53,19 @@ __global__ void outetts_chat_kernel(const float *__restrict__ cb, int64_t rows, 
     for (int d = 0; d < 8; ++d) chat[n * 8 + d] = c[d] / en;   // dac.cpp:426-427
 }
 
-__global__ __launch_bounds__(kWave *kHW) void outetts_encode_kernel(aq_outetts_args a) {
+__global__ __launch_bounds__(kWave *kOtW) void outetts_encode_kernel(aq_outetts_args a) {
     extern __shared__ float lds_ot[];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
     const int D = a.D;
     const int stride = D + 4;
     float *r = lds_ot + wave * kHF * stride;
-    const int64_t m0 = (static_cast<int64_t>(blockIdx.x) * kHW + wave) * kHF;
+    const int nw = blockDim.x / kWave;                      // waves per block (up to kOtW)
+    // [8][D + 4] (a.win_lds; rows padded so that the 8 rows read at one k
+    // fall in different banks)
+    float *win_s = lds_ot + nw * kHF * stride;
+    float *chat_s = win_s + (a.win_lds ? 8 * stride : 0);  // [N][8] (a.chat_lds)
+    const int64_t m0 = (static_cast<int64_t>(blockIdx.x) * nw + wave) * kHF;
     for (int f = 0; f < kHF; ++f) {
         const int64_t m = m0 + f;
         for (int e = lane * 4; e < D; e += kWave * 4) {
@@ -64,14 +74,27 @@ __global__ __launch_bounds__(kWave *kHW) void outetts_encode_kernel(aq_outetts_a
             *reinterpret_cast<float4 *>(r + f * stride + e) = v;
         }
     }
-    __syncthreads();
     const int f = lane >> 3;
     const int j = lane & 7;
     const int64_t mf = m0 + f;
     const bool live = mf < a.M;
     for (int s = 0; s < a.Q; ++s) {
+        // the stage's tables into LDS (the previous stage's readers are past
+        // its closing barrier)
+        if (a.win_lds) {
+            const float4 *src = reinterpret_cast<const float4 *>(a.w_in + static_cast<int64_t>(s) * 8 * D);
+            for (int i = threadIdx.x; i < 2 * D; i += blockDim.x) {
+                const int row = i / (D / 4), c4 = i % (D / 4);
+                reinterpret_cast<float4 *>(win_s + row * stride)[c4] = src[i];
+            }
+        }
+        if (a.chat_lds) {
+            const float4 *src = reinterpret_cast<const float4 *>(a.chat + static_cast<int64_t>(s) * a.N * 8);
+            for (int i = threadIdx.x; i < 2 * a.N; i += blockDim.x) reinterpret_cast<float4 *>(chat_s)[i] = src[i];
+        }
+        __syncthreads();
         // in-projection chain of (frame f, dim j), dac.cpp:402-410
-        const float *W = a.w_in + (static_cast<int64_t>(s) * 8 + j) * D;
+        const float *W = a.win_lds ? win_s + j * stride : a.w_in + (static_cast<int64_t>(s) * 8 + j) * D;
         const float *rf = r + f * stride;
         float v = a.b_in[s * 8 + j];
         // unrolled: the weight loads of 8 steps are in flight ahead of the chain
@@ -99,14 +122,14 @@ __global__ __launch_bounds__(kWave *kHW) void outetts_encode_kernel(aq_outetts_a
         // the first index of the minimum; NaN distances never win
         float bd = INFINITY;
         int bn = -1;
-        const float *Ch = a.chat + static_cast<int64_t>(s) * a.N * 8;
-        // four codes per step, their distance chains interleaved (the
+        const float *Ch = a.chat_lds ? chat_s : a.chat + static_cast<int64_t>(s) * a.N * 8;
+        // eight codes per step, their distance chains interleaved (the
         // compares stay in code order)
-        for (int n0 = j; n0 < a.N; n0 += 32) {
-            float dist[4];
-            float cv[4][8];
+        for (int n0 = j; n0 < a.N; n0 += 64) {
+            float dist[8];
+            float cv[8][8];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
+            for (int q = 0; q < 8; ++q) {
                 const int n = n0 + 8 * q < a.N ? n0 + 8 * q : j;
                 const float4 c0 = *reinterpret_cast<const float4 *>(Ch + static_cast<int64_t>(n) * 8);
                 const float4 c1 = *reinterpret_cast<const float4 *>(Ch + static_cast<int64_t>(n) * 8 + 4);
@@ -117,12 +140,12 @@ __global__ __launch_bounds__(kWave *kHW) void outetts_encode_kernel(aq_outetts_a
 #pragma unroll
             for (int d = 0; d < 8; ++d)
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
+                for (int q = 0; q < 8; ++q) {
                     const float diff = p[d] - cv[q][d];
                     dist[q] = dist[q] + diff * diff;
                 }
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
+            for (int q = 0; q < 8; ++q)
                 if (n0 + 8 * q < a.N && dist[q] < bd) {
                     bd = dist[q];
                     bn = n0 + 8 * q;
@@ -150,28 +173,47 @@ __global__ __launch_bounds__(kWave *kHW) void outetts_encode_kernel(aq_outetts_a
             }
         }
         __syncthreads();
-        // residual -= b_out + W_out c[use], dac.cpp:438-453
+        // residual -= b_out + W_out c[use], dac.cpp:438-453: the 8 frames'
+        // code rows first, then 4 channels at a time, each channel's
+        // out-projection row read once for the 8 frames
+        float4 cr0[kHF], cr1[kHF];
+#pragma unroll
         for (int g = 0; g < kHF; ++g) {
             const int ug = __shfl(use, g << 3);
             const float *c = a.cb + (static_cast<int64_t>(s) * a.N + ug) * 8;
-            const float4 c0 = *reinterpret_cast<const float4 *>(c);
-            const float4 c1 = *reinterpret_cast<const float4 *>(c + 4);
-            float *rg = r + g * stride;
-#pragma unroll 4
-            for (int o = lane; o < D; o += kWave) {
+            cr0[g] = *reinterpret_cast<const float4 *>(c);
+            cr1[g] = *reinterpret_cast<const float4 *>(c + 4);
+        }
+        for (int o0 = lane; o0 < D; o0 += 4 * kWave) {
+            float4 w0[4], w1[4];
+            float bo[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int o = o0 + t * kWave < D ? o0 + t * kWave : o0;
                 const float *wo = a.w_out + (static_cast<int64_t>(s) * D + o) * 8;
-                const float4 w0 = *reinterpret_cast<const float4 *>(wo);
-                const float4 w1 = *reinterpret_cast<const float4 *>(wo + 4);
-                float val = a.b_out[static_cast<int64_t>(s) * D + o];
-                val = val + w0.x * c0.x;
-                val = val + w0.y * c0.y;
-                val = val + w0.z * c0.z;
-                val = val + w0.w * c0.w;
-                val = val + w1.x * c1.x;
-                val = val + w1.y * c1.y;
-                val = val + w1.z * c1.z;
-                val = val + w1.w * c1.w;
-                rg[o] = rg[o] - val;
+                w0[t] = *reinterpret_cast<const float4 *>(wo);
+                w1[t] = *reinterpret_cast<const float4 *>(wo + 4);
+                bo[t] = a.b_out[static_cast<int64_t>(s) * D + o];
+            }
+#pragma unroll
+            for (int g = 0; g < kHF; ++g) {
+                float *rg = r + g * stride;
+                const float4 c0 = cr0[g], c1 = cr1[g];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const int o = o0 + t * kWave;
+                    if (o >= D) continue;
+                    float val = bo[t];
+                    val = val + w0[t].x * c0.x;
+                    val = val + w0[t].y * c0.y;
+                    val = val + w0[t].z * c0.z;
+                    val = val + w0[t].w * c0.w;
+                    val = val + w1[t].x * c1.x;
+                    val = val + w1[t].y * c1.y;
+                    val = val + w1[t].z * c1.z;
+                    val = val + w1[t].w * c1.w;
+                    rg[o] = rg[o] - val;
+                }
             }
         }
         __syncthreads();
@@ -240,14 +282,19 @@ __global__ __launch_bounds__(256) void moss_input_kernel(const float *__restrict
     }
 }
 
-__global__ __launch_bounds__(kWave *kHW) void moss_cascade_kernel(aq_moss_args a) {
+__global__ __launch_bounds__(kWave *kMsW) void moss_cascade_kernel(aq_moss_args a) {
     extern __shared__ double lds_ms[];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
     const int R = a.R;
     const int stride = R + 2;
     double *r = lds_ms + wave * kHF * stride;
-    const int64_t m0 = (static_cast<int64_t>(blockIdx.x) * kHW + wave) * kHF;
+    const int nw = blockDim.x / kWave;   // waves per block (up to kMsW)
+    // the stage's in-projection [8][R + 4] (rows padded so that the 8 rows
+    // read at one k fall in different banks) and normalised codebook [N][8]
+    float *win_s = reinterpret_cast<float *>(lds_ms + nw * kHF * stride);
+    float *tn_s = win_s + (a.win_lds ? 8 * (R + 4) : 0);
+    const int64_t m0 = (static_cast<int64_t>(blockIdx.x) * nw + wave) * kHF;
     for (int f = 0; f < kHF; ++f) {
         const int64_t m = m0 + f;
         for (int e = lane * 2; e < R; e += kWave * 2) {
@@ -256,15 +303,28 @@ __global__ __launch_bounds__(kWave *kHW) void moss_cascade_kernel(aq_moss_args a
             *reinterpret_cast<double2 *>(r + f * stride + e) = v;
         }
     }
-    __syncthreads();
     const int f = lane >> 3;
     const int j = lane & 7;
     const int64_t mf = m0 + f;
     const bool live = mf < a.M;
     for (int s = 0; s < a.Q; ++s) {
+        // the stage's tables into LDS (the previous stage's readers are past
+        // its closing barrier)
+        if (a.win_lds) {
+            const float4 *src = reinterpret_cast<const float4 *>(a.w_in + static_cast<int64_t>(s) * 8 * R);
+            for (int i = threadIdx.x; i < 2 * R; i += blockDim.x) {
+                const int row = i / (R / 4), c4 = i % (R / 4);
+                reinterpret_cast<float4 *>(win_s + row * (R + 4))[c4] = src[i];
+            }
+        }
+        if (a.tn_lds) {
+            const float4 *src = reinterpret_cast<const float4 *>(a.tn + static_cast<int64_t>(s) * a.N * 8);
+            for (int i = threadIdx.x; i < 2 * a.N; i += blockDim.x) reinterpret_cast<float4 *>(tn_s)[i] = src[i];
+        }
+        __syncthreads();
         // in_proj of (frame f, dim j): float weight times fp64 residual,
         // rounded, then added (:207-216)
-        const float *W = a.w_in + (static_cast<int64_t>(s) * 8 + j) * R;
+        const float *W = a.win_lds ? win_s + j * (R + 4) : a.w_in + (static_cast<int64_t>(s) * 8 + j) * R;
         const double *rf = r + f * stride;
         double v = a.b_in[s * 8 + j];
         // unrolled: the weight loads of 8 steps are in flight ahead of the chain
@@ -293,7 +353,7 @@ __global__ __launch_bounds__(kWave *kHW) void moss_cascade_kernel(aq_moss_args a
         // first index of the maximum dot with the normalised codebook (:225-237)
         double bd = -INFINITY;
         int bn = -1;
-        const float *T = a.tn + static_cast<int64_t>(s) * a.N * 8;
+        const float *T = a.tn_lds ? tn_s : a.tn + static_cast<int64_t>(s) * a.N * 8;
         // four codes per step, their dot chains interleaved (the compares stay
         // in code order)
         for (int n0 = j; n0 < a.N; n0 += 32) {
@@ -341,24 +401,42 @@ __global__ __launch_bounds__(kWave *kHW) void moss_cascade_kernel(aq_moss_args a
             }
         }
         __syncthreads();
-        // residual -= b_out + W_out c[use] in fp64 (:240-248)
+        // residual -= b_out + W_out c[use] in fp64 (:240-248): the 8 frames'
+        // code rows first, then 4 channels at a time, each channel's
+        // out-projection row read once for the 8 frames
+        float4 cr0[kHF], cr1[kHF];
+#pragma unroll
         for (int g = 0; g < kHF; ++g) {
             const int ug = __shfl(use, g << 3);
             const float *c = a.cb + (static_cast<int64_t>(s) * a.N + ug) * 8;
-            const float4 c0 = *reinterpret_cast<const float4 *>(c);
-            const float4 c1 = *reinterpret_cast<const float4 *>(c + 4);
-            const double cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-            double *rg = r + g * stride;
-#pragma unroll 4
-            for (int o = lane; o < R; o += kWave) {
-                const float *wo = a.w_out + (static_cast<int64_t>(s) * R + o) * 8;
-                const float4 w0 = *reinterpret_cast<const float4 *>(wo);
-                const float4 w1 = *reinterpret_cast<const float4 *>(wo + 4);
-                const double wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-                double z = a.b_out[static_cast<int64_t>(s) * R + o];
+            cr0[g] = *reinterpret_cast<const float4 *>(c);
+            cr1[g] = *reinterpret_cast<const float4 *>(c + 4);
+        }
+        for (int o0 = lane; o0 < R; o0 += 4 * kWave) {
+            float4 w0[4], w1[4];
+            float bo[4];
 #pragma unroll
-                for (int k = 0; k < 8; ++k) z = __fma_rn(wv[k], cv[k], z);   // exact product
-                rg[o] = rg[o] - z;
+            for (int t = 0; t < 4; ++t) {
+                const int o = o0 + t * kWave < R ? o0 + t * kWave : o0;
+                const float *wo = a.w_out + (static_cast<int64_t>(s) * R + o) * 8;
+                w0[t] = *reinterpret_cast<const float4 *>(wo);
+                w1[t] = *reinterpret_cast<const float4 *>(wo + 4);
+                bo[t] = a.b_out[static_cast<int64_t>(s) * R + o];
+            }
+#pragma unroll
+            for (int g = 0; g < kHF; ++g) {
+                double *rg = r + g * stride;
+                const double cv[8] = {cr0[g].x, cr0[g].y, cr0[g].z, cr0[g].w, cr1[g].x, cr1[g].y, cr1[g].z, cr1[g].w};
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const int o = o0 + t * kWave;
+                    if (o >= R) continue;
+                    const double wv[8] = {w0[t].x, w0[t].y, w0[t].z, w0[t].w, w1[t].x, w1[t].y, w1[t].z, w1[t].w};
+                    double z = bo[t];
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) z = __fma_rn(wv[k], cv[k], z);   // exact product
+                    rg[o] = rg[o] - z;
+                }
             }
         }
         __syncthreads();
@@ -471,7 +549,9 @@ __global__ void moss_decode_kernel(const int32_t *__restrict__ idx, int64_t M, i
 
 // ---------------------------------------------------------------- OuteTTS host
 
-size_t aq_outetts_lds_bytes(int64_t D) { return static_cast<size_t>(kHW) * kHF * (D + 4) * sizeof(float); }
+namespace {
+constexpr size_t kLdsMax = 160 * 1024;
+}
 
 aq_status aq_outetts_prepare(aq_ctx *ctx, const float *d_cb, int64_t rows, float *d_chat) {
     hipLaunchKernelGGL(outetts_chat_kernel, dim3(static_cast<unsigned>((rows + 255) / 256)), dim3(256), 0, ctx->stream,
@@ -480,14 +560,26 @@ aq_status aq_outetts_prepare(aq_ctx *ctx, const float *d_cb, int64_t rows, float
     return AQ_OK;
 }
 
-aq_status aq_outetts_launch(aq_ctx *ctx, const aq_outetts_args &a) {
-    const size_t lds = aq_outetts_lds_bytes(a.D);
+aq_status aq_outetts_launch(aq_ctx *ctx, const aq_outetts_args &args) {
+    // the residuals, then the stage tables while they fit the CU's LDS
+    // (kOtW waves per block while they and the in-projection fit, fewer for
+    // wide latents)
+    aq_outetts_args a = args;
+    const size_t per_wave = static_cast<size_t>(kHF) * (a.D + 4) * sizeof(float);
+    const size_t win = static_cast<size_t>(8) * (a.D + 4) * sizeof(float), chat = static_cast<size_t>(8) * a.N * sizeof(float);
+    int nw = kOtW;
+    while (nw > 1 && nw * per_wave + win > kLdsMax) --nw;
+    size_t lds = nw * per_wave;
+    a.win_lds = lds + win <= kLdsMax ? 1 : 0;
+    if (a.win_lds) lds += win;
+    a.chat_lds = lds + chat <= kLdsMax ? 1 : 0;
+    if (a.chat_lds) lds += chat;
     AQ_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void *>(outetts_encode_kernel),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
-    const int64_t per_block = static_cast<int64_t>(kHW) * kHF;
+    const int64_t per_block = static_cast<int64_t>(nw) * kHF;
     const unsigned blocks = static_cast<unsigned>((a.M + per_block - 1) / per_block);
     const int tslot = aq_timing_start(ctx);
-    hipLaunchKernelGGL(outetts_encode_kernel, dim3(blocks), dim3(kWave * kHW), lds, ctx->stream, a);
+    hipLaunchKernelGGL(outetts_encode_kernel, dim3(blocks), dim3(kWave * nw), lds, ctx->stream, a);
     aq_timing_stop(ctx, tslot);
     AQ_HIP(ctx, hipGetLastError());
     return AQ_OK;
@@ -659,12 +751,22 @@ aq_status aq_moss_encode(aq_ctx *ctx, const aq_moss_quantizer *q, const float *h
     a.idx = idx;
     a.flags = ctx->d_flags;
     a.write_res = residual ? 1 : 0;
-    const size_t lds = static_cast<size_t>(kHW) * kHF * (q->R + 2) * sizeof(double);
+    // the residuals, then the stage tables while they fit the CU's LDS
+    // (kMsW waves per block while they and the in-projection fit)
+    const size_t per_wave = static_cast<size_t>(kHF) * (q->R + 2) * sizeof(double);
+    const size_t win = static_cast<size_t>(8) * (q->R + 4) * sizeof(float), tn = static_cast<size_t>(8) * q->N * sizeof(float);
+    int nw = kMsW;
+    while (nw > 1 && nw * per_wave + win > kLdsMax) --nw;
+    size_t lds = nw * per_wave;
+    a.win_lds = lds + win <= kLdsMax ? 1 : 0;
+    if (a.win_lds) lds += win;
+    a.tn_lds = lds + tn <= kLdsMax ? 1 : 0;
+    if (a.tn_lds) lds += tn;
     AQ_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void *>(moss_cascade_kernel),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
-    const int64_t per_block = static_cast<int64_t>(kHW) * kHF;
+    const int64_t per_block = static_cast<int64_t>(nw) * kHF;
     const int tslot = aq_timing_start(ctx);
-    hipLaunchKernelGGL(moss_cascade_kernel, dim3(static_cast<unsigned>((M + per_block - 1) / per_block)), dim3(kWave * kHW),
+    hipLaunchKernelGGL(moss_cascade_kernel, dim3(static_cast<unsigned>((M + per_block - 1) / per_block)), dim3(kWave * nw),
                        lds, ctx->stream, a);
     aq_timing_stop(ctx, tslot);
     AQ_HIP(ctx, hipGetLastError());

@@ -103,8 +103,8 @@ struct aq_outetts_args {
     int32_t *idx;          // [M, Q]
     float *residual;       // [M, D] or null
     int32_t *flags;
+    int win_lds, chat_lds;   // set by aq_outetts_launch: stage tables staged in LDS
 };
-size_t aq_outetts_lds_bytes(int64_t D);
 // chat[n] = c[n] / (sqrt(|c[n]|^2) + 1e-12) for `rows` codes of dim 8.
 aq_status aq_outetts_prepare(aq_ctx *ctx, const float *d_cb, int64_t rows, float *d_chat);
 aq_status aq_outetts_launch(aq_ctx *ctx, const aq_outetts_args &a);
@@ -123,4 +123,5 @@ struct aq_moss_args {
     int32_t *idx;          // [M, Q]
     int32_t *flags;
     int write_res;
+    int win_lds, tn_lds;     // set at launch: stage tables staged in LDS
 };
