@@ -239,8 +239,9 @@ constexpr int kIpK = 32;   //                         channels per LDS chunk
 __global__ __launch_bounds__(256) void moss_input_kernel(const float *__restrict__ h, int64_t M, int C, int R,
                                                          const float *__restrict__ w, const float *__restrict__ b,
                                                          double *__restrict__ res) {
-    __shared__ float hs[kIpK][kIpF + 4];
-    __shared__ float ws[kIpK][kIpO + 4];
+    // staged as doubles: each element is converted once, not once per use
+    __shared__ double hs[kIpK][kIpF + 2];
+    __shared__ double ws[kIpK][kIpO + 2];
     const int tid = threadIdx.x;
     const int tx = tid & 15;
     const int ty = tid >> 4;
@@ -251,21 +252,40 @@ __global__ __launch_bounds__(256) void moss_input_kernel(const float *__restrict
     for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int q = 0; q < 4; ++q) acc[i][q] = static_cast<double>(b[o0 + tx * 4 + q]);
+    // The next chunk's inputs are loaded into registers while this chunk
+    // computes (kIpF * kIpK / 256 = 8 elements of each per thread).
+    constexpr int kPer = kIpF * kIpK / 256;
+    float hn[kPer], wn[kPer];
+    auto fetch = [&](int k0) {
+        const int kn = min(kIpK, C - k0);
+#pragma unroll
+        for (int t = 0; t < kPer; ++t) {
+            const int e = tid + t * 256;
+            const int rr = e / kIpK, cc = e % kIpK;
+            const int64_t m = m0 + rr;
+            hn[t] = (m < M && cc < kn) ? h[m * C + k0 + cc] : 0.0f;
+            wn[t] = cc < kn ? w[static_cast<int64_t>(o0 + rr) * C + k0 + cc] : 0.0f;
+        }
+    };
+    fetch(0);
     for (int k0 = 0; k0 < C; k0 += kIpK) {
         const int kn = min(kIpK, C - k0);
-        for (int e = tid; e < kIpF * kIpK; e += 256) {
-            const int rr = e / kIpK;
-            const int cc = e % kIpK;
-            const int64_t m = m0 + rr;
-            hs[cc][rr] = (m < M && cc < kn) ? h[m * C + k0 + cc] : 0.0f;
-            ws[cc][rr] = cc < kn ? w[static_cast<int64_t>(o0 + rr) * C + k0 + cc] : 0.0f;
+#pragma unroll
+        for (int t = 0; t < kPer; ++t) {
+            const int e = tid + t * 256;
+            const int rr = e / kIpK, cc = e % kIpK;
+            hs[cc][rr] = static_cast<double>(hn[t]);
+            ws[cc][rr] = static_cast<double>(wn[t]);
         }
         __syncthreads();
+        if (k0 + kIpK < C) fetch(k0 + kIpK);
         for (int kk = 0; kk < kn; ++kk) {
-            const float4 xa = *reinterpret_cast<const float4 *>(&hs[kk][ty * 4]);
-            const float4 wb = *reinterpret_cast<const float4 *>(&ws[kk][tx * 4]);
-            const double xv[4] = {xa.x, xa.y, xa.z, xa.w};
-            const double wv[4] = {wb.x, wb.y, wb.z, wb.w};
+            const double2 xa0 = *reinterpret_cast<const double2 *>(&hs[kk][ty * 4]);
+            const double2 xa1 = *reinterpret_cast<const double2 *>(&hs[kk][ty * 4 + 2]);
+            const double2 wb0 = *reinterpret_cast<const double2 *>(&ws[kk][tx * 4]);
+            const double2 wb1 = *reinterpret_cast<const double2 *>(&ws[kk][tx * 4 + 2]);
+            const double xv[4] = {xa0.x, xa0.y, xa1.x, xa1.y};
+            const double wv[4] = {wb0.x, wb0.y, wb1.x, wb1.y};
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
