@@ -374,13 +374,13 @@ __global__ __launch_bounds__(kWave *kMsW) void moss_cascade_kernel(aq_moss_args 
         double bd = -INFINITY;
         int bn = -1;
         const float *T = a.tn_lds ? tn_s : a.tn + static_cast<int64_t>(s) * a.N * 8;
-        // four codes per step, their dot chains interleaved (the compares stay
-        // in code order)
-        for (int n0 = j; n0 < a.N; n0 += 32) {
-            double dot[4];
-            float tv[4][8];
+        // eight codes per step, their dot chains interleaved (the compares
+        // stay in code order)
+        for (int n0 = j; n0 < a.N; n0 += 64) {
+            double dot[8];
+            float tv[8][8];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
+            for (int q = 0; q < 8; ++q) {
                 const int n = n0 + 8 * q < a.N ? n0 + 8 * q : j;
                 const float4 t0 = *reinterpret_cast<const float4 *>(T + static_cast<int64_t>(n) * 8);
                 const float4 t1 = *reinterpret_cast<const float4 *>(T + static_cast<int64_t>(n) * 8 + 4);
@@ -391,9 +391,9 @@ __global__ __launch_bounds__(kWave *kMsW) void moss_cascade_kernel(aq_moss_args 
 #pragma unroll
             for (int c = 0; c < 8; ++c)
 #pragma unroll
-                for (int q = 0; q < 4; ++q) dot[q] = dot[q] + static_cast<double>(tv[q][c]) * e[c];
+                for (int q = 0; q < 8; ++q) dot[q] = dot[q] + static_cast<double>(tv[q][c]) * e[c];
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
+            for (int q = 0; q < 8; ++q)
                 if (n0 + 8 * q < a.N && dot[q] > bd) {
                     bd = dot[q];
                     bn = n0 + 8 * q;
@@ -422,7 +422,7 @@ __global__ __launch_bounds__(kWave *kMsW) void moss_cascade_kernel(aq_moss_args 
         }
         __syncthreads();
         // residual -= b_out + W_out c[use] in fp64 (:240-248): the 8 frames'
-        // code rows first, then 4 channels at a time, each channel's
+        // code rows first, then 8 channels at a time, each channel's
         // out-projection row read once for the 8 frames
         float4 cr0[kHF], cr1[kHF];
 #pragma unroll
@@ -432,11 +432,11 @@ __global__ __launch_bounds__(kWave *kMsW) void moss_cascade_kernel(aq_moss_args 
             cr0[g] = *reinterpret_cast<const float4 *>(c);
             cr1[g] = *reinterpret_cast<const float4 *>(c + 4);
         }
-        for (int o0 = lane; o0 < R; o0 += 4 * kWave) {
-            float4 w0[4], w1[4];
-            float bo[4];
+        for (int o0 = lane; o0 < R; o0 += 8 * kWave) {
+            float4 w0[8], w1[8];
+            float bo[8];
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
+            for (int t = 0; t < 8; ++t) {
                 const int o = o0 + t * kWave < R ? o0 + t * kWave : o0;
                 const float *wo = a.w_out + (static_cast<int64_t>(s) * R + o) * 8;
                 w0[t] = *reinterpret_cast<const float4 *>(wo);
@@ -448,7 +448,7 @@ __global__ __launch_bounds__(kWave *kMsW) void moss_cascade_kernel(aq_moss_args 
                 double *rg = r + g * stride;
                 const double cv[8] = {cr0[g].x, cr0[g].y, cr0[g].z, cr0[g].w, cr1[g].x, cr1[g].y, cr1[g].z, cr1[g].w};
 #pragma unroll
-                for (int t = 0; t < 4; ++t) {
+                for (int t = 0; t < 8; ++t) {
                     const int o = o0 + t * kWave;
                     if (o >= R) continue;
                     const double wv[8] = {w0[t].x, w0[t].y, w0[t].z, w0[t].w, w1[t].x, w1[t].y, w1[t].z, w1[t].w};
