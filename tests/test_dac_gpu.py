@@ -104,7 +104,10 @@ def test_dac_teacher_forced(torch, ctx, oracle):
     assert np.array_equal(out["residual"].view(np.uint32), ref["residual"].view(np.uint32))
 
 
-def test_dac_decode_matches_encode_recon(torch, ctx):
+def test_dac_decode_matches_encode_recon(torch, ctx, oracle):
+    """Decode of the encode's codes equals its recon, and decode of arbitrary
+    codes (teacher-forced, so independent of the encode) equals the oracle's
+    out-projection sum for them."""
     from aqmi import synth
 
     cfg = synth.make_config(1, rows=1500)
@@ -115,6 +118,14 @@ def test_dac_decode_matches_encode_recon(torch, ctx):
     st.decode(idx, dec)
     torch.cuda.synchronize()
     assert np.array_equal(dec.cpu().numpy().view(np.uint32), out["recon"].view(np.uint32))
+    rng = np.random.default_rng(17)
+    cfg0 = synth.make_config(1, rows=750)
+    force = rng.integers(0, cfg0["N"], size=(750, cfg0["Q"]), dtype=np.int32)
+    want = oracle.dac_rvq(cfg0, force_idx=force)["recon"]
+    dec2 = torch.empty((750, cfg0["D"]), dtype=torch.float32, device="cuda")
+    st.decode(torch.from_numpy(force).cuda(), dec2)
+    torch.cuda.synchronize()
+    assert np.array_equal(dec2.cpu().numpy().view(np.uint32), want.view(np.uint32))
 
 
 def test_dac_errors(torch, ctx):
