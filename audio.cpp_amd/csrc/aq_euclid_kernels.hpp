@@ -1212,13 +1212,21 @@ __global__ __launch_bounds__(kThreads) void euclid_select_kernel(StageArgs a) {
         }
         if (needg[g]) {
             // Branch-free insertion of every evaluated candidate of the
-            // frame's 4 lanes into the ranked list sel[0..Tsel).
+            // frame's 4 lanes into the ranked list sel[0..Tsel) (one place
+            // without top-k); a slot no frame of the wave fills is skipped.
 #pragma unroll
             for (int j = 0; j < TOPL; ++j) {
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     int cn = __shfl(cand_n[g][j], col + 16 * q);
+                    if (!__any(cn >= 0)) continue;
                     float cv = __shfl(cand_val[j], col + 16 * q);
+                    if (Tsel == 1) {
+                        const bool take = cn >= 0 && (sel_n[0] < 0 || ranks_before<RECIPE>(cv, cn, sel_v[0], sel_n[0]));
+                        sel_v[0] = take ? cv : sel_v[0];
+                        sel_n[0] = take ? cn : sel_n[0];
+                        continue;
+                    }
 #pragma unroll
                     for (int r = 0; r < 5; ++r) {
                         const bool before = a.topk == 0 ? ranks_before<RECIPE>(cv, cn, sel_v[r], sel_n[r])
