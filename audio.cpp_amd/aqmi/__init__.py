@@ -448,7 +448,7 @@ class Linear:
         frames per clip; out device [M, out]."""
         if strides is None:
             M = x.shape[0]
-            clip_len, strides = M, (M * self.in_features, self.in_features, 1)
+            clip_len, strides = max(M, 1), (max(M, 1) * self.in_features, self.in_features, 1)
         self.ctx.use_current_stream()
         self.ctx.check(self.ctx.lib.aq_linear_forward(self.ctx.h, self.h, _dptr(x), M, clip_len, *strides, _dptr(out)))
 

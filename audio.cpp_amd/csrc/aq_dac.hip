@@ -1006,7 +1006,7 @@ aq_status aq_dac_encode_ex(aq_ctx *ctx, const aq_dac_stages *st, const float *x,
                            int64_t clip_stride, int64_t frame_stride, int64_t chan_stride, int32_t *idx,
                            int64_t idx_ld, float *residual, float *recon, int recon_accumulate,
                            const int32_t *force_idx) {
-    if (!ctx || !st || !idx || (!x && M > 0)) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_dac_encode: null argument");
+    if (!ctx || !st || (M > 0 && (!idx || !x))) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_dac_encode: null argument");
     if (st->ctx->device != ctx->device) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_dac_encode: stages belong to another device");
     if (M < 0 || clip_len <= 0 || M % clip_len != 0)
         return aq_fail(ctx, AQ_E_SHAPE, "aq_dac_encode: M=%lld must be a non-negative multiple of clip_len=%lld",

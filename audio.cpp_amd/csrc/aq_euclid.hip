@@ -531,14 +531,14 @@ aq_status noalloc_region(aq_ctx *ctx, unsigned char **out) {
 aq_status euclid_encode_impl(aq_ctx *ctx, const aq_codebooks *cb, const aq_frames_desc &in, int64_t M, int32_t *idx,
                              float *residual, float *dist, int topk, int32_t *topk_idx, float *topk_dist,
                              const int32_t *force_idx, Arena arena) {
-    if (!ctx || !cb || !idx || (!in.x && M > 0)) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_euclid_encode: null argument");
+    if (!ctx || !cb || (M > 0 && (!idx || !in.x))) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_euclid_encode: null argument");
     if (cb->ctx->device != ctx->device)
         return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_euclid_encode: codebooks belong to another device");
     if (M < 0 || M > (int64_t{1} << 31) - 1) return aq_fail(ctx, AQ_E_SHAPE, "aq_euclid_encode: M=%lld out of range", (long long)M);
     if (in.clip_len <= 0) return aq_fail(ctx, AQ_E_SHAPE, "aq_euclid_encode: clip_len must be positive");
     if (topk < 0 || topk > 4 || topk > cb->N)
         return aq_fail(ctx, AQ_E_SHAPE, "aq_euclid_encode: topk=%d (supported 0..4, at most N)", topk);
-    if (topk > 0 && (!topk_idx || !topk_dist))
+    if (topk > 0 && M > 0 && (!topk_idx || !topk_dist))
         return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_euclid_encode: topk outputs missing");
     if (M == 0) return AQ_OK;
     aq_device_guard g(ctx->device);

@@ -736,12 +736,13 @@ aq_status aq_moss_release(aq_moss_quantizer *q) {
 
 aq_status aq_moss_encode(aq_ctx *ctx, const aq_moss_quantizer *q, const float *hidden, int64_t M, int32_t *idx,
                          double *residual, const int32_t *force_idx) {
-    if (!ctx || !q || !idx) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_moss_encode: null argument");
+    if (!ctx || !q) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_moss_encode: null argument");
     if (q->ctx->device != ctx->device)
         return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_moss_encode: quantizer belongs to another device");
+    // the shape first, as the reference rejects an empty latent before use
     if (M <= 0 || M > (int64_t{1} << 31) - 1)
         return aq_fail(ctx, AQ_E_SHAPE, "aq_moss_encode: MOSS codec quantizer requires a non-empty encoder latent");
-    if (!hidden) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_moss_encode: null argument");
+    if (!hidden || !idx) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_moss_encode: null argument");
     aq_device_guard g(ctx->device);
     double *res = residual;
     if (!res) {

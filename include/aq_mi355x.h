@@ -28,6 +28,8 @@
  *    thread; a context performs no internal locking (the reference also runs
  *    one session per model under its own lock).
  *  - Matrices are row-major.  Frames are rows: x[m, d] at x + m*D + d.
+ *  - An empty batch (M = 0) enqueues nothing and returns AQ_OK whatever its
+ *    data pointers hold, except for MOSS, whose reference rejects it.
  *
  * Reference interfaces replaced (paths relative to the audio.cpp tree):
  *  - engine::runtime::VectorQuantizer::compute
