@@ -305,6 +305,14 @@ __device__ inline void q8_scale(float amax, float &d, float &id) {
     d = static_cast<float>(static_cast<_Float16>(__fdiv_rn(amax, 127.0f)));
     id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
 }
+// Four quants in [-128, 127] packed into a dword, first in the low byte
+// (two saturating 16-bit packs, then a byte select).
+__device__ inline int q8_pack4(int q0, int q1, int q2, int q3) {
+    const auto lo = __builtin_amdgcn_cvt_pk_i16(q0, q1);
+    const auto hi = __builtin_amdgcn_cvt_pk_i16(q2, q3);
+    return static_cast<int>(__builtin_amdgcn_perm(__builtin_bit_cast(unsigned, hi), __builtin_bit_cast(unsigned, lo),
+                                                  0x06040200u));
+}
 __device__ inline void quantize_block_q8(const float *__restrict__ x, int8_t *__restrict__ q, float *__restrict__ d) {
     float amax = 0.0f;
     for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(x[j]));
@@ -1048,21 +1056,38 @@ __global__ __launch_bounds__(kThreads) void euclid_select_kernel(StageArgs a) {
 #pragma unroll
                     for (int h = 0; h < 2; ++h) {
                         const int blk = 8 * c + 2 * kq + h;
-                        float amax = 0.0f;
+                        float amax = 0.0f, fin = 0.0f;   // fin: 0 unless a value is inf or NaN
 #pragma unroll
                         for (int i = 0; i < 8; ++i)
 #pragma unroll
-                            for (int t = 0; t < 4; ++t) amax = fmaxf(amax, fabsf(v[8 * h + i][t]));
+                            for (int t = 0; t < 4; ++t) {
+                                amax = fmaxf(amax, fabsf(v[8 * h + i][t]));
+                                fin = __fmaf_rn(v[8 * h + i][t], 0.0f, fin);
+                            }
                         float d, id;
                         q8_scale(amax, d, id);
                         int *qw = reinterpret_cast<int *>(q_xq + col * XQS + 32 * blk);
+                        if (fin == 0.0f && id < INFINITY) {
+                            // finite values and |v * id| <= 127 (1 + 2^-23)^2:
+                            // the rounded values are integers in [-127, 127],
+                            // where q8_quant's range test and clamp are idle
 #pragma unroll
-                        for (int i = 0; i < 8; ++i) {
-                            unsigned w = 0;
+                            for (int i = 0; i < 8; ++i) {
+                                const f32x4 x = v[8 * h + i];
+                                qw[i] = q8_pack4(static_cast<int>(__builtin_rintf(__fmul_rn(x[0], id))),
+                                                 static_cast<int>(__builtin_rintf(__fmul_rn(x[1], id))),
+                                                 static_cast<int>(__builtin_rintf(__fmul_rn(x[2], id))),
+                                                 static_cast<int>(__builtin_rintf(__fmul_rn(x[3], id))));
+                            }
+                        } else {
 #pragma unroll
-                            for (int t = 0; t < 4; ++t)
-                                w |= (static_cast<unsigned>(q8_quant(v[8 * h + i][t], id)) & 0xFFu) << (8 * t);
-                            qw[i] = static_cast<int>(w);
+                            for (int i = 0; i < 8; ++i) {
+                                unsigned w = 0;
+#pragma unroll
+                                for (int t = 0; t < 4; ++t)
+                                    w |= (static_cast<unsigned>(q8_quant(v[8 * h + i][t], id)) & 0xFFu) << (8 * t);
+                                qw[i] = static_cast<int>(w);
+                            }
                         }
                         q_xd[col * (K / 32) + blk] = d;
                     }

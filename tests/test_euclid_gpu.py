@@ -120,6 +120,38 @@ def test_higgs_q8_topk_matches_oracle(torch, ctx, oracle):
     check_topk(out, ref)
 
 
+def test_higgs_q8_query_blocks_with_special_values(torch, ctx, oracle):
+    """The query's Q8_0 blocks: an all-zero block (amax 0), a block of values
+    near 1e-38 (127 / amax overflows to inf: every quant -128, scale 0), a
+    block holding +-inf and one holding a NaN, in frames otherwise near the
+    codes, so that the certificate and the exact values meet each kind of
+    block; codes, residuals, distances and top-4 against the oracle."""
+    import aqmi
+    from aqmi import synth
+
+    print("[gpu] higgs q8 special query blocks", flush=True)
+    Q, N, K, M = 2, 2048, 256, 320
+    cb = np.stack([synth.q8_0_random_codebook(91, 10 + s, N, K) for s in range(Q)])
+    x = (synth.q8_0_dequantize(cb[0])[np.arange(M) % N] + synth.normal(91, 2, (M, K), 0.05)).astype(np.float32)
+    x[0::5, 32:64] = 0.0
+    x[1::5, 64:96] = synth.normal(91, 3, (len(range(1, M, 5)), 32), 1.0e-38)
+    x[2::5, 96:128] = x[2::5, 96:128] * np.float32(1.0e-39)   # subnormal block
+    x[3, 130] = np.inf
+    x[4, 200] = -np.inf
+    x[7, 10] = np.nan
+    cfg = dict(x=x, M=M, K=K, Q=Q, N=N, codebook_q8=cb)
+    out = run(torch, ctx, cb, aqmi.HIGGS, x, cb_type=aqmi.CB_Q8_0, topk=4)
+    ref = oracle.higgs_rvq(cfg, topk=4)
+    assert np.array_equal(out["idx"], ref["idx"])
+    for key in ("residual", "dist"):
+        a, b = out[key], ref[key]
+        assert np.array_equal(np.isnan(a), np.isnan(b))
+        assert np.array_equal(bits(a[~np.isnan(a)]), bits(b[~np.isnan(b)]))
+    fin = np.isfinite(x).all(1)   # top-k of the non-finite frames: codes above
+    check_topk({k: out[k][fin] for k in ("topk_idx", "topk_dist")},
+               {k: ref[k][fin] for k in ("topk_idx", "topk_logit")})
+
+
 def test_direct_matches_oracle(torch, ctx, oracle):
     import aqmi
 
