@@ -16,17 +16,20 @@
 // formed in double it is exact, and a fused multiply-add gives the same
 // result as the reference's multiply then add; those places use __fma_rn.
 //
-// Layout of one encode: a wave owns 8 frames and keeps their residuals in
-// LDS (row stride padded by 16 bytes so the 8 frames fall in different
-// banks).  Lane (f, j) = (lane / 8, lane % 8) runs the in-projection chain of
-// code dimension j of frame f -- the reference's sequential sum over the
-// latent channels -- and then scores codes j, j + 8, ... of the frame; the
-// 8 lanes of a frame merge their winners with the reference's tie rule.  The
-// residual update then sweeps each frame's channels across the wave.  The
-// chains are latency-bound (one wave per SIMD or fewer), so the stage's
-// in-projection weights and normalised codebook are staged in LDS when they
-// fit (an L2 round trip per few elements otherwise), and the residual update
-// reads each channel's out-projection row once for the wave's 8 frames.
+// Layout of one encode: a wave owns 4 frames and keeps their residuals in
+// LDS (row stride padded by 16 bytes so the frames fall in different
+// banks).  Lane (f, j) = (lane / 16, lane % 16): lanes j < 8 run the
+// in-projection chain of code dimension j of frame f -- the reference's
+// sequential sum over the latent channels; lanes j >= 8 repeat it -- and
+// all 16 then score codes j, j + 16, ... of the frame and merge their
+// winners with the reference's tie rule.  The residual update then sweeps
+// each frame's channels across the wave.  The chains are latency-bound, so
+// a block holds six such waves (24 frames; the residuals and the stage
+// tables fill the LDS, so one block per CU): two SIMDs of each CU run two
+// waves, whose chains interleave.  The stage's in-projection weights and
+// normalised codebook are staged in LDS when they fit (an L2 round trip per
+// few elements otherwise), and the residual update reads each channel's
+// out-projection row once for the wave's frames.
 #include "aq_device_math.hpp"
 #include "aq_internal.hpp"
 
@@ -37,9 +40,10 @@
 namespace {
 
 constexpr int kWave = 64;
-constexpr int kHF = 8;   // frames per wave
-constexpr int kOtW = 3;  // waves per block (OuteTTS: 24 frames share the staged in-projection)
-constexpr int kMsW = 3;  // waves per block (MOSS)
+constexpr int kHF = 4;               // frames per wave
+constexpr int kLPF = kWave / kHF;    // lanes per frame: 16 (in-projection: dims of lanes j < 8)
+constexpr int kOtW = 6;  // waves per block (OuteTTS: 24 frames share the staged in-projection)
+constexpr int kMsW = 6;  // waves per block (MOSS)
 
 // ------------------------------------------------------------------ OuteTTS
 
@@ -74,8 +78,9 @@ __global__ __launch_bounds__(kWave *kOtW) void outetts_encode_kernel(aq_outetts_
             *reinterpret_cast<float4 *>(r + f * stride + e) = v;
         }
     }
-    const int f = lane >> 3;
-    const int j = lane & 7;
+    const int f = lane / kLPF;
+    const int j = lane % kLPF;
+    const int jd = j & 7;   // in-projection output (lanes j >= 8 repeat it)
     const int64_t mf = m0 + f;
     const bool live = mf < a.M;
     for (int s = 0; s < a.Q; ++s) {
@@ -94,9 +99,9 @@ __global__ __launch_bounds__(kWave *kOtW) void outetts_encode_kernel(aq_outetts_
         }
         __syncthreads();
         // in-projection chain of (frame f, dim j), dac.cpp:402-410
-        const float *W = a.win_lds ? win_s + j * stride : a.w_in + (static_cast<int64_t>(s) * 8 + j) * D;
+        const float *W = a.win_lds ? win_s + jd * stride : a.w_in + (static_cast<int64_t>(s) * 8 + jd) * D;
         const float *rf = r + f * stride;
-        float v = a.b_in[s * 8 + j];
+        float v = a.b_in[s * 8 + jd];
         // unrolled: the weight loads of 8 steps are in flight ahead of the chain
 #pragma unroll 8
         for (int h = 0; h < D; h += 4) {
@@ -112,7 +117,7 @@ __global__ __launch_bounds__(kWave *kOtW) void outetts_encode_kernel(aq_outetts_
         float nsq = 0.0f;
 #pragma unroll
         for (int d = 0; d < 8; ++d) {
-            p[d] = __shfl(v, (f << 3) + d);
+            p[d] = __shfl(v, f * kLPF + d);
             nsq = nsq + p[d] * p[d];
         }
         const float pn = aq_math::sqrt_rn(nsq) + 1.0e-12f;
@@ -125,12 +130,12 @@ __global__ __launch_bounds__(kWave *kOtW) void outetts_encode_kernel(aq_outetts_
         const float *Ch = a.chat_lds ? chat_s : a.chat + static_cast<int64_t>(s) * a.N * 8;
         // eight codes per step, their distance chains interleaved (the
         // compares stay in code order)
-        for (int n0 = j; n0 < a.N; n0 += 64) {
+        for (int n0 = j; n0 < a.N; n0 += 8 * kLPF) {
             float dist[8];
             float cv[8][8];
 #pragma unroll
             for (int q = 0; q < 8; ++q) {
-                const int n = n0 + 8 * q < a.N ? n0 + 8 * q : j;
+                const int n = n0 + kLPF * q < a.N ? n0 + kLPF * q : 0;
                 const float4 c0 = *reinterpret_cast<const float4 *>(Ch + static_cast<int64_t>(n) * 8);
                 const float4 c1 = *reinterpret_cast<const float4 *>(Ch + static_cast<int64_t>(n) * 8 + 4);
                 cv[q][0] = c0.x; cv[q][1] = c0.y; cv[q][2] = c0.z; cv[q][3] = c0.w;
@@ -146,13 +151,13 @@ __global__ __launch_bounds__(kWave *kOtW) void outetts_encode_kernel(aq_outetts_
                 }
 #pragma unroll
             for (int q = 0; q < 8; ++q)
-                if (n0 + 8 * q < a.N && dist[q] < bd) {
+                if (n0 + kLPF * q < a.N && dist[q] < bd) {
                     bd = dist[q];
-                    bn = n0 + 8 * q;
+                    bn = n0 + kLPF * q;
                 }
         }
 #pragma unroll
-        for (int o = 1; o < 8; o <<= 1) {
+        for (int o = 1; o < kLPF; o <<= 1) {
             const float od = __shfl_xor(bd, o);
             const int on = __shfl_xor(bn, o);
             if (on >= 0 && (bn < 0 || od < bd || (od == bd && on < bn))) {
@@ -173,13 +178,13 @@ __global__ __launch_bounds__(kWave *kOtW) void outetts_encode_kernel(aq_outetts_
             }
         }
         __syncthreads();
-        // residual -= b_out + W_out c[use], dac.cpp:438-453: the 8 frames'
+        // residual -= b_out + W_out c[use], dac.cpp:438-453: the frames'
         // code rows first, then 4 channels at a time, each channel's
-        // out-projection row read once for the 8 frames
+        // out-projection row read once for the wave's frames
         float4 cr0[kHF], cr1[kHF];
 #pragma unroll
         for (int g = 0; g < kHF; ++g) {
-            const int ug = __shfl(use, g << 3);
+            const int ug = __shfl(use, g * kLPF);
             const float *c = a.cb + (static_cast<int64_t>(s) * a.N + ug) * 8;
             cr0[g] = *reinterpret_cast<const float4 *>(c);
             cr1[g] = *reinterpret_cast<const float4 *>(c + 4);
@@ -323,8 +328,9 @@ __global__ __launch_bounds__(kWave *kMsW) void moss_cascade_kernel(aq_moss_args 
             *reinterpret_cast<double2 *>(r + f * stride + e) = v;
         }
     }
-    const int f = lane >> 3;
-    const int j = lane & 7;
+    const int f = lane / kLPF;
+    const int j = lane % kLPF;
+    const int jd = j & 7;   // in-projection output (lanes j >= 8 repeat it)
     const int64_t mf = m0 + f;
     const bool live = mf < a.M;
     for (int s = 0; s < a.Q; ++s) {
@@ -344,9 +350,9 @@ __global__ __launch_bounds__(kWave *kMsW) void moss_cascade_kernel(aq_moss_args 
         __syncthreads();
         // in_proj of (frame f, dim j): float weight times fp64 residual,
         // rounded, then added (:207-216)
-        const float *W = a.win_lds ? win_s + j * (R + 4) : a.w_in + (static_cast<int64_t>(s) * 8 + j) * R;
+        const float *W = a.win_lds ? win_s + jd * (R + 4) : a.w_in + (static_cast<int64_t>(s) * 8 + jd) * R;
         const double *rf = r + f * stride;
-        double v = a.b_in[s * 8 + j];
+        double v = a.b_in[s * 8 + jd];
         // unrolled: the weight loads of 8 steps are in flight ahead of the chain
 #pragma unroll 8
         for (int k = 0; k < R; k += 4) {
@@ -363,7 +369,7 @@ __global__ __launch_bounds__(kWave *kMsW) void moss_cascade_kernel(aq_moss_args 
         double nrm = 0.0;
 #pragma unroll
         for (int d = 0; d < 8; ++d) {
-            e[d] = __shfl(v, (f << 3) + d);
+            e[d] = __shfl(v, f * kLPF + d);
             nrm = nrm + e[d] * e[d];
         }
         const double sq = aq_math::sqrt_rn(nrm);
@@ -376,12 +382,12 @@ __global__ __launch_bounds__(kWave *kMsW) void moss_cascade_kernel(aq_moss_args 
         const float *T = a.tn_lds ? tn_s : a.tn + static_cast<int64_t>(s) * a.N * 8;
         // eight codes per step, their dot chains interleaved (the compares
         // stay in code order)
-        for (int n0 = j; n0 < a.N; n0 += 64) {
+        for (int n0 = j; n0 < a.N; n0 += 8 * kLPF) {
             double dot[8];
             float tv[8][8];
 #pragma unroll
             for (int q = 0; q < 8; ++q) {
-                const int n = n0 + 8 * q < a.N ? n0 + 8 * q : j;
+                const int n = n0 + kLPF * q < a.N ? n0 + kLPF * q : 0;
                 const float4 t0 = *reinterpret_cast<const float4 *>(T + static_cast<int64_t>(n) * 8);
                 const float4 t1 = *reinterpret_cast<const float4 *>(T + static_cast<int64_t>(n) * 8 + 4);
                 tv[q][0] = t0.x; tv[q][1] = t0.y; tv[q][2] = t0.z; tv[q][3] = t0.w;
@@ -394,13 +400,13 @@ __global__ __launch_bounds__(kWave *kMsW) void moss_cascade_kernel(aq_moss_args 
                 for (int q = 0; q < 8; ++q) dot[q] = dot[q] + static_cast<double>(tv[q][c]) * e[c];
 #pragma unroll
             for (int q = 0; q < 8; ++q)
-                if (n0 + 8 * q < a.N && dot[q] > bd) {
+                if (n0 + kLPF * q < a.N && dot[q] > bd) {
                     bd = dot[q];
-                    bn = n0 + 8 * q;
+                    bn = n0 + kLPF * q;
                 }
         }
 #pragma unroll
-        for (int o = 1; o < 8; o <<= 1) {
+        for (int o = 1; o < kLPF; o <<= 1) {
             const double od = __shfl_xor(bd, o);
             const int on = __shfl_xor(bn, o);
             if (on >= 0 && (bn < 0 || od > bd || (od == bd && on < bn))) {
@@ -421,22 +427,22 @@ __global__ __launch_bounds__(kWave *kMsW) void moss_cascade_kernel(aq_moss_args 
             }
         }
         __syncthreads();
-        // residual -= b_out + W_out c[use] in fp64 (:240-248): the 8 frames'
-        // code rows first, then 8 channels at a time, each channel's
-        // out-projection row read once for the 8 frames
+        // residual -= b_out + W_out c[use] in fp64 (:240-248): the frames'
+        // code rows first, then 4 channels at a time, each channel's
+        // out-projection row read once for the wave's frames
         float4 cr0[kHF], cr1[kHF];
 #pragma unroll
         for (int g = 0; g < kHF; ++g) {
-            const int ug = __shfl(use, g << 3);
+            const int ug = __shfl(use, g * kLPF);
             const float *c = a.cb + (static_cast<int64_t>(s) * a.N + ug) * 8;
             cr0[g] = *reinterpret_cast<const float4 *>(c);
             cr1[g] = *reinterpret_cast<const float4 *>(c + 4);
         }
-        for (int o0 = lane; o0 < R; o0 += 8 * kWave) {
-            float4 w0[8], w1[8];
-            float bo[8];
+        for (int o0 = lane; o0 < R; o0 += 4 * kWave) {
+            float4 w0[4], w1[4];
+            float bo[4];
 #pragma unroll
-            for (int t = 0; t < 8; ++t) {
+            for (int t = 0; t < 4; ++t) {
                 const int o = o0 + t * kWave < R ? o0 + t * kWave : o0;
                 const float *wo = a.w_out + (static_cast<int64_t>(s) * R + o) * 8;
                 w0[t] = *reinterpret_cast<const float4 *>(wo);
@@ -448,7 +454,7 @@ __global__ __launch_bounds__(kWave *kMsW) void moss_cascade_kernel(aq_moss_args 
                 double *rg = r + g * stride;
                 const double cv[8] = {cr0[g].x, cr0[g].y, cr0[g].z, cr0[g].w, cr1[g].x, cr1[g].y, cr1[g].z, cr1[g].w};
 #pragma unroll
-                for (int t = 0; t < 8; ++t) {
+                for (int t = 0; t < 4; ++t) {
                     const int o = o0 + t * kWave;
                     if (o >= R) continue;
                     const double wv[8] = {w0[t].x, w0[t].y, w0[t].z, w0[t].w, w1[t].x, w1[t].y, w1[t].z, w1[t].w};
