@@ -240,7 +240,8 @@ constexpr int kIpO = 64;   //                         outputs
 constexpr int kIpK = 32;   //                         channels per LDS chunk
 
 // residual[m, o] = b[o] + sum_k w[o, k] h[m, k] in fp64, k in order
-// (audio_tokenizer_quantizer.cpp:193-201).  256 threads, 4 x 4 outputs each.
+// (audio_tokenizer_quantizer.cpp:193-201).  256 threads, 4 frames x 4
+// outputs each.
 __global__ __launch_bounds__(256) void moss_input_kernel(const float *__restrict__ h, int64_t M, int C, int R,
                                                          const float *__restrict__ w, const float *__restrict__ b,
                                                          double *__restrict__ res) {
@@ -252,11 +253,14 @@ __global__ __launch_bounds__(256) void moss_input_kernel(const float *__restrict
     const int ty = tid >> 4;
     const int64_t m0 = static_cast<int64_t>(blockIdx.x) * kIpF;
     const int o0 = blockIdx.y * kIpO;
+    // outputs 2 tx, 2 tx + 1, 32 + 2 tx, 33 + 2 tx: the 16 lanes of a row
+    // read 256 contiguous bytes of ws per 16-byte load (no bank conflicts)
+    auto oq = [&](int q) { return (q < 2 ? 0 : kIpO / 2 - 2) + 2 * tx + q; };
     double acc[4][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) acc[i][q] = static_cast<double>(b[o0 + tx * 4 + q]);
+        for (int q = 0; q < 4; ++q) acc[i][q] = static_cast<double>(b[o0 + oq(q)]);
     // The next chunk's inputs are loaded into registers while this chunk
     // computes (kIpF * kIpK / 256 = 8 elements of each per thread).
     constexpr int kPer = kIpF * kIpK / 256;
@@ -287,8 +291,8 @@ __global__ __launch_bounds__(256) void moss_input_kernel(const float *__restrict
         for (int kk = 0; kk < kn; ++kk) {
             const double2 xa0 = *reinterpret_cast<const double2 *>(&hs[kk][ty * 4]);
             const double2 xa1 = *reinterpret_cast<const double2 *>(&hs[kk][ty * 4 + 2]);
-            const double2 wb0 = *reinterpret_cast<const double2 *>(&ws[kk][tx * 4]);
-            const double2 wb1 = *reinterpret_cast<const double2 *>(&ws[kk][tx * 4 + 2]);
+            const double2 wb0 = *reinterpret_cast<const double2 *>(&ws[kk][2 * tx]);
+            const double2 wb1 = *reinterpret_cast<const double2 *>(&ws[kk][kIpO / 2 + 2 * tx]);
             const double xv[4] = {xa0.x, xa0.y, xa1.x, xa1.y};
             const double wv[4] = {wb0.x, wb0.y, wb1.x, wb1.y};
 #pragma unroll
@@ -303,7 +307,7 @@ __global__ __launch_bounds__(256) void moss_input_kernel(const float *__restrict
         const int64_t m = m0 + ty * 4 + i;
         if (m >= M) break;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) res[m * R + o0 + tx * 4 + q] = acc[i][q];
+        for (int q = 0; q < 4; ++q) res[m * R + o0 + oq(q)] = acc[i][q];
     }
 }
 
