@@ -770,7 +770,9 @@ Shape launch_shape(int64_t M, int64_t D, int64_t img_f4, bool recon, int num_cus
 }  // namespace
 
 struct aq_dac_stages {
-    aq_ctx *ctx = nullptr;
+    // device of the creating context (the handle keeps no pointer to it, so
+    // it may be released after that context is destroyed)
+    int device = -1;
     int64_t Q = 0, D = 0, N = 0;
     int recipe = AQ_DAC_FISH;
     float qeps = 1.0e-12f;        // ggml_scale_bias bias before the query norm's sqrt
@@ -816,7 +818,7 @@ aq_status upload_outetts(aq_ctx *ctx, int64_t Q, int64_t D, int64_t N, const flo
     int64_t total = 0;
     for (int64_t v : sizes) total += (v + 63) / 64 * 64;
     auto *st = new aq_dac_stages();
-    st->ctx = ctx;
+    st->device = ctx->device;
     st->Q = Q;
     st->D = D;
     st->N = N;
@@ -895,7 +897,7 @@ aq_status aq_dac_upload_ex(aq_ctx *ctx, int64_t Q, int64_t D, int64_t N, const f
 
     aq_dac_stages *st = new (std::nothrow) aq_dac_stages();
     if (!st) return aq_fail(ctx, AQ_E_NOMEM, "aq_dac_upload: host allocation failed");
-    st->ctx = ctx;
+    st->device = ctx->device;
     st->Q = Q;
     st->D = D;
     st->N = N;
@@ -985,7 +987,7 @@ aq_status aq_dac_upload_ex(aq_ctx *ctx, int64_t Q, int64_t D, int64_t N, const f
 aq_status aq_dac_release(aq_dac_stages *st) {
     if (!st) return AQ_E_INVALID_ARG;
     {
-        aq_device_guard g(st->ctx->device);
+        aq_device_guard g(st->device);
         if (st->d_images) (void)hipFree(st->d_images);
         if (st->d_images_tb) (void)hipFree(st->d_images_tb);
         if (st->d_tables) (void)hipFree(st->d_tables);
@@ -1007,7 +1009,7 @@ aq_status aq_dac_encode_ex(aq_ctx *ctx, const aq_dac_stages *st, const float *x,
                            int64_t idx_ld, float *residual, float *recon, int recon_accumulate,
                            const int32_t *force_idx) {
     if (!ctx || !st || (M > 0 && (!idx || !x))) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_dac_encode: null argument");
-    if (st->ctx->device != ctx->device) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_dac_encode: stages belong to another device");
+    if (st->device != ctx->device) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_dac_encode: stages belong to another device");
     if (M < 0 || clip_len <= 0 || M % clip_len != 0)
         return aq_fail(ctx, AQ_E_SHAPE, "aq_dac_encode: M=%lld must be a non-negative multiple of clip_len=%lld",
                        (long long)M, (long long)clip_len);

@@ -193,7 +193,9 @@ float round_up(double v) {
 }  // namespace
 
 struct aq_codebooks {
-    aq_ctx *ctx = nullptr;
+    // device of the creating context (the handle keeps no pointer to it, so
+    // it may be released after that context is destroyed)
+    int device = -1;
     int64_t Q = 0, N = 0, K = 0;
     int recipe = 0;
     bool q8 = false;
@@ -234,7 +236,7 @@ aq_status check_upload(aq_ctx *ctx, const char *fn, int64_t Q, int64_t N, int64_
 aq_status euclid_alloc(aq_ctx *ctx, int64_t Q, int64_t N, int64_t K, bool q8, int recipe, aq_codebooks **out) {
     aq_codebooks *cb = new (std::nothrow) aq_codebooks();
     if (!cb) return aq_fail(ctx, AQ_E_NOMEM, "aq_euclid_upload: host allocation failed");
-    cb->ctx = ctx;
+    cb->device = ctx->device;
     cb->Q = Q;
     cb->N = N;
     cb->K = K;
@@ -305,19 +307,29 @@ aq_status euclid_prepare(aq_ctx *ctx, aq_codebooks *cb) {
     int32_t *nonfinite = reinterpret_cast<int32_t *>(smax + 5 * cb->Q);
     std::vector<unsigned long long> host(5 * cb->Q + 1, 0);
     aq_status st = AQ_OK;
-    bool ok = hipMemsetAsync(smax, 0, sizeof(unsigned long long) * (5 * cb->Q + 1), ctx->stream) == hipSuccess;
-    if (ok) {
+    const char *step = "memset";
+    hipError_t e = hipMemsetAsync(smax, 0, sizeof(unsigned long long) * (5 * cb->Q + 1), ctx->stream);
+    if (e == hipSuccess) {
         const dim3 grid(static_cast<unsigned>((QN + 127) / 128)), block(128);
         hipLaunchKernelGGL(euclid_prep_kernel, grid, block, 0, ctx->stream, cb->d_cbf, QN, cb->N,
                            static_cast<int>(cb->K), cb->d_cbh, cb->d_cbl, cb->d_hh, cb->d_bias, cb->d_e2, smax,
                            nonfinite);
-        ok = hipGetLastError() == hipSuccess &&
-             hipMemcpyAsync(host.data(), smax, sizeof(unsigned long long) * host.size(), hipMemcpyDeviceToHost,
-                            ctx->stream) == hipSuccess &&
-             hipStreamSynchronize(ctx->stream) == hipSuccess;
+        step = "launch";
+        e = hipGetLastError();
+        if (e == hipSuccess) {
+            step = "copy";
+            e = hipMemcpyAsync(host.data(), smax, sizeof(unsigned long long) * host.size(), hipMemcpyDeviceToHost,
+                               ctx->stream);
+        }
+        if (e == hipSuccess) {
+            step = "synchronize";
+            e = hipStreamSynchronize(ctx->stream);
+        }
     }
     (void)hipFree(smax);
-    if (!ok) return aq_fail(ctx, AQ_E_DEVICE, "aq_euclid_upload: codebook preparation failed");
+    if (e != hipSuccess)
+        return aq_fail(ctx, AQ_E_DEVICE, "aq_euclid_upload: codebook preparation failed (%s: %s)", step,
+                       hipGetErrorString(e));
     auto bound = [&](int64_t s, int i) {
         double v;
         std::memcpy(&v, &host[s * 5 + i], 8);
@@ -453,7 +465,7 @@ aq_status aq_euclid_upload_projected(aq_ctx *ctx, int64_t Q, int64_t N, int64_t 
 aq_status aq_euclid_release(aq_codebooks *cb) {
     if (!cb) return AQ_E_INVALID_ARG;
     {
-        aq_device_guard g(cb->ctx->device);
+        aq_device_guard g(cb->device);
         aq_proj_release(cb->proj);
         for (void *p : {static_cast<void *>(cb->d_cbh), static_cast<void *>(cb->d_cbl), static_cast<void *>(cb->d_hh),
                         static_cast<void *>(cb->d_cbf),
@@ -532,7 +544,7 @@ aq_status euclid_encode_impl(aq_ctx *ctx, const aq_codebooks *cb, const aq_frame
                              float *residual, float *dist, int topk, int32_t *topk_idx, float *topk_dist,
                              const int32_t *force_idx, Arena arena) {
     if (!ctx || !cb || (M > 0 && (!idx || !in.x))) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_euclid_encode: null argument");
-    if (cb->ctx->device != ctx->device)
+    if (cb->device != ctx->device)
         return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_euclid_encode: codebooks belong to another device");
     if (M < 0 || M > (int64_t{1} << 31) - 1) return aq_fail(ctx, AQ_E_SHAPE, "aq_euclid_encode: M=%lld out of range", (long long)M);
     if (in.clip_len <= 0) return aq_fail(ctx, AQ_E_SHAPE, "aq_euclid_encode: clip_len must be positive");

@@ -618,7 +618,9 @@ aq_status aq_outetts_launch(aq_ctx *ctx, const aq_outetts_args &args) {
 // ------------------------------------------------------------------- MOSS host
 
 struct aq_moss_quantizer {
-    aq_ctx *ctx = nullptr;
+    // device of the creating context (the handle keeps no pointer to it, so
+    // it may be released after that context is destroyed)
+    int device = -1;
     int64_t Q = 0, N = 0, C = 0, R = 0;
     float *d_mem = nullptr;      // one allocation holding the arrays below
     float *d_wip = nullptr;      // [R][C]
@@ -676,7 +678,7 @@ aq_status aq_moss_upload(aq_ctx *ctx, int64_t Q, int64_t N, int64_t code_dim, in
     int64_t total = 0;
     for (int64_t s : sizes) total += (s + 63) / 64 * 64;
     auto *q = new aq_moss_quantizer();
-    q->ctx = ctx;
+    q->device = ctx->device;
     q->Q = Q;
     q->N = N;
     q->C = C;
@@ -736,7 +738,7 @@ aq_status aq_moss_upload(aq_ctx *ctx, int64_t Q, int64_t N, int64_t code_dim, in
 aq_status aq_moss_release(aq_moss_quantizer *q) {
     if (!q) return AQ_E_INVALID_ARG;
     {
-        aq_device_guard g(q->ctx->device);
+        aq_device_guard g(q->device);
         if (q->d_mem) (void)hipFree(q->d_mem);
         if (q->d_tables) (void)hipFree(q->d_tables);
     }
@@ -747,7 +749,7 @@ aq_status aq_moss_release(aq_moss_quantizer *q) {
 aq_status aq_moss_encode(aq_ctx *ctx, const aq_moss_quantizer *q, const float *hidden, int64_t M, int32_t *idx,
                          double *residual, const int32_t *force_idx) {
     if (!ctx || !q) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_moss_encode: null argument");
-    if (q->ctx->device != ctx->device)
+    if (q->device != ctx->device)
         return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_moss_encode: quantizer belongs to another device");
     // the shape first, as the reference rejects an empty latent before use
     if (M <= 0 || M > (int64_t{1} << 31) - 1)
@@ -813,7 +815,7 @@ aq_status aq_moss_encode(aq_ctx *ctx, const aq_moss_quantizer *q, const float *h
 
 aq_status aq_moss_decode(aq_ctx *ctx, const aq_moss_quantizer *q, const int32_t *idx, int64_t M, float *latent) {
     if (!ctx || !q) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_moss_decode: null argument");
-    if (q->ctx->device != ctx->device)
+    if (q->device != ctx->device)
         return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_moss_decode: quantizer belongs to another device");
     if (M <= 0) return aq_fail(ctx, AQ_E_SHAPE, "aq_moss_decode: MOSS codec dequantizer requires a non-empty code sequence");
     if (!idx || !latent) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_moss_decode: null argument");

@@ -582,7 +582,9 @@ aq_status aq_gather_frames(aq_ctx *ctx, const aq_frames_desc &in, int64_t M, int
 // ---------------------------------------------------------------- C ABI
 
 struct aq_linear {
-    aq_ctx *ctx = nullptr;
+    // device of the creating context (the handle keeps no pointer to it, so
+    // it may be released after that context is destroyed)
+    int device = -1;
     aq_proj_weights *pw = nullptr;
 };
 
@@ -604,7 +606,7 @@ aq_status aq_linear_upload(aq_ctx *ctx, int64_t out_features, int64_t in_feature
     aq_device_guard g(ctx->device);
     aq_linear *lin = new (std::nothrow) aq_linear();
     if (!lin) return aq_fail(ctx, AQ_E_NOMEM, "aq_linear_upload: host allocation failed");
-    lin->ctx = ctx;
+    lin->device = ctx->device;
     aq_status st = aq_proj_create_linear(ctx, out_features, in_features, w_type, w, bias, &lin->pw);
     if (st != AQ_OK) {
         delete lin;
@@ -617,7 +619,7 @@ aq_status aq_linear_upload(aq_ctx *ctx, int64_t out_features, int64_t in_feature
 aq_status aq_linear_forward(aq_ctx *ctx, const aq_linear *lin, const float *x, int64_t M, int64_t clip_len,
                             int64_t clip_stride, int64_t frame_stride, int64_t chan_stride, float *out) {
     if (!ctx || !lin || (M > 0 && (!x || !out))) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_linear_forward: null argument");
-    if (lin->ctx->device != ctx->device)
+    if (lin->device != ctx->device)
         return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_linear_forward: weights belong to another device");
     if (M < 0 || M > (int64_t{1} << 31) - 1 || clip_len <= 0)
         return aq_fail(ctx, AQ_E_SHAPE, "aq_linear_forward: M=%lld clip_len=%lld", (long long)M, (long long)clip_len);
@@ -630,7 +632,7 @@ aq_status aq_linear_forward(aq_ctx *ctx, const aq_linear *lin, const float *x, i
 aq_status aq_linear_release(aq_linear *lin) {
     if (!lin) return AQ_E_INVALID_ARG;
     {
-        aq_device_guard g(lin->ctx->device);
+        aq_device_guard g(lin->device);
         aq_proj_release(lin->pw);
     }
     delete lin;

@@ -30,6 +30,9 @@
  *  - Matrices are row-major.  Frames are rows: x[m, d] at x + m*D + d.
  *  - An empty batch (M = 0) enqueues nothing and returns AQ_OK whatever its
  *    data pointers hold, except for MOSS, whose reference rejects it.
+ *  - A handle (stages, codebooks, quantizer, linear) records its device,
+ *    not its creating context: it may be released after that context is
+ *    destroyed, and is used with any context on the same device.
  *
  * Reference interfaces replaced (paths relative to the audio.cpp tree):
  *  - engine::runtime::VectorQuantizer::compute

@@ -132,3 +132,35 @@ def test_moss_rejects_empty_latent(torch, ctx):
     with pytest.raises(aqmi.AqError) as e:
         q.decode(empty(torch, 0, 2, dtype=torch.int32), empty(torch, 0, 32))
     assert "requires a non-empty code sequence" in str(e.value)
+
+
+def test_handles_outlive_their_context(torch):
+    """Handles released after the context that created them (as Python's
+    collector may order it): no handle reads its creator, so the releases
+    leave no HIP error behind, and a new context uploads and encodes."""
+    import aqmi
+    from aqmi import synth
+
+    print("[gpu] handles released after their context", flush=True)
+    c = aqmi.Context(0)
+    cfg = synth.make_config(2, rows=64)
+    cbs = aqmi.Codebooks(c, np.ascontiguousarray(cfg["codebook"][:2]), aqmi.OMNIVOICE)
+    d0 = synth.make_config(0)
+    st = aqmi.DacStages(c, d0["w_in"], d0.get("b_in"), d0["codebook"], d0["w_out"], d0.get("b_out"))
+    mc = synth.moss_config(4, Q=2, N=64, C=32, R=64)
+    f = synth.moss_fold(mc)
+    q = aqmi.MossQuantizer(c, f["w_ip"], mc["ip_b"], f["w_in"], mc["in_b"], mc["codebook"], f["w_out"], mc["out_b"])
+    lin = aqmi.Linear(c, np.ones((64, 64), np.float32))
+    torch.cuda.synchronize()
+    c.close()
+    for h in (cbs, st, q, lin):
+        h.close()
+    c2 = aqmi.Context(0)
+    again = aqmi.Codebooks(c2, np.ascontiguousarray(cfg["codebook"][:2]), aqmi.OMNIVOICE)
+    x = torch.from_numpy(np.ascontiguousarray(cfg["x"])).cuda()
+    idx = torch.full((64, 2), -1, dtype=torch.int32, device="cuda")
+    again.encode(x, idx)
+    torch.cuda.synchronize()
+    assert int(idx.min()) >= 0
+    again.close()
+    c2.close()
