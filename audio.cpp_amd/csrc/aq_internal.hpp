@@ -64,10 +64,14 @@ inline aq_status aq_fail(aq_ctx *ctx, aq_status st, const char *fmt, ...) {
     } while (0)
 
 // Makes ctx->device current for the lifetime of the guard, restoring the
-// caller's device afterwards.
+// caller's device afterwards.  It also clears the thread's last-error slot,
+// so that the hipGetLastError checks after this call's launches report
+// this call's errors, not one the caller's own HIP calls left behind (a
+// fault of earlier work stays visible: the launches and copies fail).
 class aq_device_guard {
 public:
     explicit aq_device_guard(int device) {
+        (void)hipGetLastError();
         if (hipGetDevice(&prev_) != hipSuccess) prev_ = -1;
         if (prev_ != device) (void)hipSetDevice(device);
     }

@@ -164,3 +164,30 @@ def test_handles_outlive_their_context(torch):
     assert int(idx.min()) >= 0
     again.close()
     c2.close()
+
+
+def test_foreign_sticky_error_is_not_ours(torch, ctx):
+    """A HIP error that the caller's own code left in the thread's last-error
+    slot (here hipSetDevice on a device that does not exist) does not make
+    the next upload or encode fail: the library's launch checks see only
+    its own calls."""
+    import ctypes
+    import aqmi
+    from aqmi import synth
+
+    print("[gpu] foreign sticky HIP error", flush=True)
+    hip = ctypes.CDLL("libamdhip64.so")
+    cur = ctypes.c_int(-1)
+    assert hip.hipGetDevice(ctypes.byref(cur)) == 0
+    torch.cuda.synchronize()
+    assert hip.hipSetDevice(ctypes.c_int(4096)) != 0   # invalid device ordinal, left unread
+    cfg = synth.make_config(2, rows=64)
+    cbs = aqmi.Codebooks(ctx, np.ascontiguousarray(cfg["codebook"][:2]), aqmi.OMNIVOICE)
+    x = torch.from_numpy(np.ascontiguousarray(cfg["x"])).cuda()   # (torch's own launch checks read the slot)
+    idx = torch.full((64, 2), -1, dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
+    assert hip.hipSetDevice(ctypes.c_int(4096)) != 0
+    cbs.encode(x, idx)
+    torch.cuda.synchronize()
+    assert int(idx.min()) >= 0
+    assert hip.hipGetDevice(ctypes.byref(cur)) == 0 and cur.value == 0
