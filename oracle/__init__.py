@@ -62,6 +62,8 @@ class Oracle:
         L = self.lib
         L.aqo_vec_dot_f32.restype = C.c_float
         L.aqo_vec_dot_f32.argtypes = [C.c_int, _f32p, _f32p]
+        L.aqo_vec_dot_f32_tail.restype = C.c_float
+        L.aqo_vec_dot_f32_tail.argtypes = [C.c_int, _f32p, _f32p, C.c_int]
         L.aqo_tinyblas_dot_f32.restype = C.c_float
         L.aqo_tinyblas_dot_f32.argtypes = [C.c_int, _f32p, _f32p]
         L.aqo_argmax_f32.restype = C.c_int
@@ -431,6 +433,8 @@ class Ref:
         L.aqref_vector_quantizer.restype = C.c_int
         L.aqref_vector_quantizer.argtypes = [_f32p, _i64, _i64, _i64, _i64, _f32p, _i64, _i64, _f32p]
         L.aqref_quantize_chunk_q8_0.argtypes = [_f32p, C.c_void_p, _i64, _i64]
+        L.aqref_vec_dot_f32.restype = C.c_float
+        L.aqref_vec_dot_f32.argtypes = [C.c_int, _f32p, _f32p]
         L.aqref_top_k.restype = None
         L.aqref_top_k.argtypes = [_f32p, _i64, _i64, C.c_int, _i32p, C.c_int]
         L.aqref_linear.restype = C.c_double

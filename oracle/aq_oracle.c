@@ -49,10 +49,21 @@ static float reduce8(const float a[8]) {
  * GGML_F32_STEP 64, GGML_F32_EPR 16, GGML_F32_ARR 4 at simd-mappings.h:
  * 439-478).  Four 16-lane accumulators take elements i+16j+l with FMA
  * (GGML_F32x16_FMA = _mm512_fmadd_ps), are combined 0+=2, 1+=3, 0+=1, then
- * reduced by reduce16.  The scalar leftovers `sumf += x[i]*y[i]` are a
- * separate multiply and add: the reference build does not fuse them (checked
- * bit for bit against oracle/_ref on the dim-8 score and out-projection). */
+ * reduced by reduce16.  The scalar leftovers `sumf += x[i]*y[i]` (n % 64 of
+ * them, vec.cpp:125-128) are compiled by GCC 11 with -O3 -march=native on
+ * the reference's AVX-512 build host as: the products of the first
+ * rem - rem % 4 leftovers computed 8 (then 4) at a time and added to sumf in
+ * order (a rounded multiply, then an add), the last rem % 4 contracted to
+ * scalar fused multiply-adds.  That is the reference's default build
+ * (GGML_NATIVE); an x86-64-v4 build of the same source fuses the last
+ * rem % 8 instead (tests/test_oracle.py pins both against oracle/_ref). */
 float aqo_vec_dot_f32(int n, const float *x, const float *y) {
+    return aqo_vec_dot_f32_tail(n, x, y, 4);
+}
+
+/* aqo_vec_dot_f32 with the last rem % tail_mod leftovers fused (4: the
+ * native build, 8: x86-64-v4). */
+float aqo_vec_dot_f32_tail(int n, const float *x, const float *y, int tail_mod) {
     const int np = n & ~63;
     float sum[4][16];
     memset(sum, 0, sizeof(sum));
@@ -66,9 +77,14 @@ float aqo_vec_dot_f32(int n, const float *x, const float *y) {
     }
     for (int l = 0; l < 16; ++l) sum[0][l] = sum[0][l] + sum[1][l];
     float sumf = reduce16(sum[0]);
+    const int fused_from = n - (n - np) % tail_mod;
     for (int i = np; i < n; ++i) {
-        const float prod = x[i] * y[i];
-        sumf = sumf + prod;
+        if (i >= fused_from) {
+            sumf = fmaf(x[i], y[i], sumf);
+        } else {
+            const float prod = x[i] * y[i];
+            sumf = sumf + prod;
+        }
     }
     return sumf;
 }

@@ -29,6 +29,7 @@ typedef struct {
 
 /* ---- primitives ---------------------------------------------------------- */
 float aqo_vec_dot_f32(int n, const float *x, const float *y);
+float aqo_vec_dot_f32_tail(int n, const float *x, const float *y, int tail_mod);
 float aqo_tinyblas_dot_f32(int k, const float *a, const float *b);
 int   aqo_mul_mat_f32_uses_tinyblas(int64_t m, int64_t n, int64_t k);
 int   aqo_argmax_f32(int n, const float *x);

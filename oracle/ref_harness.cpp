@@ -591,6 +591,17 @@ void aqref_quantize_row_q8_0(const float * x, void * y, int64_t k) {
     tr->from_float(x, y, k);
 }
 
+// ggml_vec_dot_f32 (ggml-cpu/vec.cpp:11-135) through the CPU type traits:
+// one dot product of n floats in the arithmetic of mul_mat's non-tinyBLAS
+// path, as this build's compiler laid out its scalar leftover loop.
+float aqref_vec_dot_f32(int n, const float * x, const float * y) {
+    ggml_cpu_init();
+    const auto * tr = ggml_get_type_traits_cpu(GGML_TYPE_F32);
+    float s = 0.0f;
+    tr->vec_dot(n, &s, 0, x, 0, y, 0, 1);
+    return s;
+}
+
 // Reference-rounding quantisation (ggml_quantize_chunk -> quantize_row_q8_0_ref,
 // ggml-quants.c:236-256), used by the reference's weight store for Q8_0 weights.
 void aqref_quantize_chunk_q8_0(const float * x, void * y, int64_t rows, int64_t k) {
