@@ -575,6 +575,21 @@ __global__ void dac_image_win_kernel(const float *__restrict__ w_in, int64_t Q, 
     images_tb[s * img_f + ((r * 16 + tt) * DI + sw) * 4 + c] = w;
 }
 
+// The recipe's inverse norm of codebook row C (8 floats; t: the row's index
+// over all stages, reported in flags[0] for a zero Vevo2 row).
+__device__ inline float dac_row_inv(const float *__restrict__ C, int recipe, int64_t t,
+                                    unsigned long long *__restrict__ flags) {
+    double sum = 0.0;
+    for (int k = 0; k < 8; ++k) sum = __dadd_rn(sum, __dmul_rn(static_cast<double>(C[k]), static_cast<double>(C[k])));
+    if (recipe == AQ_DAC_INDEXTTS2) return __fdiv_rn(1.0f, static_cast<float>(sqrt_rn(sum)));
+    if (recipe == AQ_DAC_VEVO2) {
+        const double norm = sqrt_rn(sum);
+        if (norm == 0.0) atomicMin(&flags[0], static_cast<unsigned long long>(t));
+        return static_cast<float>(__ddiv_rn(1.0, norm));
+    }
+    return sum > 0.0 ? static_cast<float>(__ddiv_rn(1.0, sqrt_rn(sum))) : 0.0f;
+}
+
 // b_in and the recipe's normalised codebook rows, the same in both images
 // (all recipes: double sum of squares, float products):
 //   Fish      inv = sum > 0 ? (float)(1 / sqrt(sum)) : 0   (fish_audio/codec.cpp:171-189)
@@ -596,18 +611,7 @@ __global__ void dac_image_cb_kernel(const float *__restrict__ codebook, const fl
     if (t >= Q * N) return;
     const int64_t s = t / N, n = t % N;
     const float *C = codebook + t * 8;
-    double sum = 0.0;
-    for (int k = 0; k < 8; ++k) sum = __dadd_rn(sum, __dmul_rn(static_cast<double>(C[k]), static_cast<double>(C[k])));
-    float inv;
-    if (recipe == AQ_DAC_INDEXTTS2) {
-        inv = __fdiv_rn(1.0f, static_cast<float>(sqrt_rn(sum)));
-    } else if (recipe == AQ_DAC_VEVO2) {
-        const double norm = sqrt_rn(sum);
-        if (norm == 0.0) atomicMin(&flags[0], static_cast<unsigned long long>(t));
-        inv = static_cast<float>(__ddiv_rn(1.0, norm));
-    } else {
-        inv = sum > 0.0 ? static_cast<float>(__ddiv_rn(1.0, sqrt_rn(sum))) : 0.0f;
-    }
+    const float inv = dac_row_inv(C, recipe, t, flags);
     const int64_t base = s * img_f + 8 * D + 8, c = n / kWave, L = n % kWave;
     bool nf = false;
     for (int q = 0; q < 2; ++q)
@@ -657,6 +661,197 @@ __global__ void dac_decode_kernel(const int32_t *__restrict__ idx, int64_t ld, i
         acc = (s == 0 && !accumulate) ? z : __fadd_rn(acc, z);
     }
     out[t] = acc;
+}
+
+// ----------------------------------------------------------- any shape
+// Latent widths D and codebook sizes N outside the fused kernel's (D in
+// {64, ..., 1024} by its register tiles, N a multiple of 64) take a cascade
+// kernel with run-time D and N and the same ggml arithmetic, at the cost of
+// rescoring every code exactly (no certificate) and of a residual in LDS.
+
+// Plain normalised codebook rows [Q][N][8] of the recipe.
+__global__ void dac_any_chat_kernel(const float *__restrict__ codebook, int64_t QN, int recipe, float *__restrict__ chat,
+                                    unsigned long long *__restrict__ flags) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= QN) return;
+    const float *C = codebook + t * 8;
+    const float inv = dac_row_inv(C, recipe, t, flags);
+    bool nf = false;
+    for (int k = 0; k < 8; ++k) {
+        const float v = __fmul_rn(C[k], inv);
+        nf |= !__builtin_isfinite(v);
+        chat[t * 8 + k] = v;
+    }
+    if (nf) flags[1] = 1;
+}
+
+struct DacAnyArgs {
+    const float *x;          // [M, D] frame-major
+    int64_t M;
+    int D, N, Q;
+    const float *w_in;       // [Q][8][D]
+    const float *b_in;       // [Q][8] or null
+    const float *chat;       // [Q][N][8] normalised codes
+    const float *tables;     // [Q][N][D] out-projection (+ bias) per code, or null (codes only)
+    int32_t *idx;            // [M, ld]
+    int ld;
+    float *residual;         // [M, D] or null
+    float *recon;            // [M, D] or null
+    int recon_acc;
+    const int32_t *force_idx;
+    int32_t *flags;
+    float qeps;
+    int order;               // 0 ggml_vec_dot_f32, 1 tinyBLAS
+};
+
+// Orders this wave's LDS stores before its other lanes' loads.
+__device__ inline void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// One wave per frame; its residual row (D floats) in LDS for all stages.
+__global__ __launch_bounds__(256) void dac_any_kernel(DacAnyArgs a) {
+    extern __shared__ float any_lds[];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int64_t m = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave) + wave;
+    if (m >= a.M) return;   // wave-uniform
+    const int D = a.D;
+    float *r = any_lds + static_cast<int64_t>(wave) * D;
+    for (int d = lane; d < D; d += kWave) r[d] = a.x[m * D + d];
+    wave_lds_sync();
+    const int np = D & ~(kWave - 1);
+    const int fused_from = D - (D - np) % 4;
+    for (int s = 0; s < a.Q; ++s) {
+        const float *W = a.w_in + static_cast<int64_t>(s) * 8 * D;
+        float p[8];
+        if (a.order == 1) {
+            // tinyBLAS (sgemm.cpp:527-545): lane 16 g + t runs accumulator t
+            // (k = 16 u + t) of outputs 2g and 2g+1, then _mm512_reduce_add_ps
+            // (pairs 8, 4, 2, 1 apart) inside the 16-lane row
+            const int t = lane & 15, g = lane >> 4;
+            float a0 = 0.0f, a1 = 0.0f;
+            for (int k = t; k < D; k += 16) {
+                const float v = r[k];
+                a0 = __fmaf_rn(v, W[(2 * g) * D + k], a0);
+                a1 = __fmaf_rn(v, W[(2 * g + 1) * D + k], a1);
+            }
+            for (int off = 8; off >= 1; off >>= 1) {
+                a0 = __fadd_rn(a0, __shfl_xor(a0, off));
+                a1 = __fadd_rn(a1, __shfl_xor(a1, off));
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                p[2 * q] = __shfl(a0, 16 * q);
+                p[2 * q + 1] = __shfl(a1, 16 * q);
+            }
+        } else {
+            // ggml_vec_dot_f32 (vec.cpp:11-135): accumulator (j, l) = lane
+            // 16 j + l over 64-element steps, GGML_F32_VEC_REDUCE's pairing
+            // (lanes 32 apart, then 16, then 8, 4, 2, 1), then the leftovers:
+            // rounded products added in order, the last rem % 4 fused (the
+            // reference's native build)
+            float acc[8];
+#pragma unroll
+            for (int o = 0; o < 8; ++o) acc[o] = 0.0f;
+            for (int k = lane; k < np; k += kWave) {
+                const float v = r[k];
+#pragma unroll
+                for (int o = 0; o < 8; ++o) acc[o] = __fmaf_rn(v, W[o * D + k], acc[o]);
+            }
+#pragma unroll
+            for (int o = 0; o < 8; ++o)
+                for (int off = 32; off >= 1; off >>= 1) acc[o] = __fadd_rn(acc[o], __shfl_xor(acc[o], off));
+            float sum = acc[0];
+#pragma unroll
+            for (int o = 1; o < 8; ++o)
+                if ((lane & 7) == o) sum = acc[o];
+            if (lane < 8) {
+                const float *w = W + lane * D;
+                for (int k = np; k < D; ++k)
+                    sum = k >= fused_from ? __fmaf_rn(r[k], w[k], sum) : __fadd_rn(sum, __fmul_rn(r[k], w[k]));
+            }
+#pragma unroll
+            for (int o = 0; o < 8; ++o) p[o] = __shfl(sum, o);
+        }
+        if (a.b_in) {
+#pragma unroll
+            for (int o = 0; o < 8; ++o) p[o] = __fadd_rn(p[o], a.b_in[s * 8 + o]);
+        }
+        // l2 normalisation: fp32 squares summed in double in output order,
+        // + eps (ggml_scale_bias), correctly rounded sqrt, IEEE division
+        double ss = 0.0;
+#pragma unroll
+        for (int o = 0; o < 8; ++o) ss += static_cast<double>(__fmul_rn(p[o], p[o]));
+        const float den = sqrt_rn(__fadd_rn(static_cast<float>(ss), a.qeps));
+        float pn[8];
+#pragma unroll
+        for (int o = 0; o < 8; ++o) pn[o] = __fdiv_rn(p[o], den);
+        // exact scores (k = 8 mul_mat: rounded products added in order) and
+        // ggml_vec_argmax_f32 (last index of the maximum; a NaN restarts it)
+        const float *C = a.chat + static_cast<int64_t>(s) * a.N * 8;
+        float bv = -INFINITY;
+        int bn = -1;
+        bool bad = false;
+        for (int n = lane; n < a.N; n += kWave) {
+            const float4 c0 = *reinterpret_cast<const float4 *>(C + static_cast<int64_t>(n) * 8);
+            const float4 c1 = *reinterpret_cast<const float4 *>(C + static_cast<int64_t>(n) * 8 + 4);
+            const float sc = exact_score(c0, c1, pn);
+            bad |= sc != sc;
+            if (sc >= bv) {
+                bv = sc;
+                bn = n;
+            }
+        }
+#pragma unroll
+        for (int off = 1; off <= 32; off <<= 1) {
+            const float ov = __shfl_xor(bv, off);
+            const int on = __shfl_xor(bn, off);
+            if (ov > bv || (ov == bv && on > bn)) {
+                bv = ov;
+                bn = on;
+            }
+        }
+        int code = uniform_i(bn < 0 ? 0 : bn);
+        if (__any(bad)) {
+            float mx = -INFINITY;
+            int id = 0;
+            for (int n = 0; n < a.N; ++n) {
+                const float4 c0 = *reinterpret_cast<const float4 *>(C + static_cast<int64_t>(n) * 8);
+                const float4 c1 = *reinterpret_cast<const float4 *>(C + static_cast<int64_t>(n) * 8 + 4);
+                const float sc = exact_score(c0, c1, pn);
+                mx = mx > sc ? mx : sc;
+                if (mx == sc) id = n;
+            }
+            code = uniform_i(id);
+        }
+        if (lane == 0) a.idx[m * a.ld + s] = code;
+        int use = code;
+        if (a.force_idx) {
+            use = a.force_idx[m * a.ld + s];
+            if (use < 0 || use >= a.N) {
+                if (lane == 0) a.flags[AQ_FLAG_BAD_INDEX] = 1;
+                use = 0;
+            }
+        }
+        if (a.tables) {
+            // r -= z; recon += z (each lane its own elements)
+            const float *z = a.tables + (static_cast<int64_t>(s) * a.N + use) * D;
+            for (int d = lane; d < D; d += kWave) {
+                const float zd = z[d];
+                r[d] = __fsub_rn(r[d], zd);
+                if (a.recon) {
+                    const float prev = (s == 0 && !a.recon_acc) ? -0.0f : a.recon[m * D + d];
+                    a.recon[m * D + d] = __fadd_rn(prev, zd);
+                }
+            }
+            wave_lds_sync();
+        }
+    }
+    if (a.residual)
+        for (int d = lane; d < D; d += kWave) a.residual[m * D + d] = r[d];
 }
 
 using EncodeFn = void (*)(const float *, int64_t, int, int, const float4 *, int64_t, int64_t, const float *, int32_t *,
@@ -740,14 +935,14 @@ Shape launch_shape(int64_t M, int64_t D, int64_t img_f4, bool recon, int num_cus
             if (cbg && !prefetch) continue;   // the in-memory codebook variant always prefetches
             hipFuncAttributes attr{};
             int64_t simd_waves = 8;
-            if (hipFuncGetAttributes(&attr, reinterpret_cast<const void *>(pick_kernel(D, fw, recon, prefetch, cbg, order))) ==
-                    hipSuccess && attr.numRegs > 0)
+            const void *kfn = reinterpret_cast<const void *>(pick_kernel(D, fw, recon, prefetch, cbg, order));
+            if (hipFuncGetAttributes(&attr, kfn) == hipSuccess && attr.numRegs > 0)
                 simd_waves = std::min<int64_t>(8, 512 / ((attr.numRegs + 7) / 8 * 8));
             // The block must fit on a CU at all (waves per SIMD by registers,
-            // one stage image in LDS).
+            // one stage image in LDS next to the kernel's static LDS).
             // order 1 adds a transposed copy of one frame per wave to LDS
             const size_t lds_total = lds_bytes + (order == 1 ? static_cast<size_t>(wpb) * D * 4 : 0);
-            if (simd_waves < (wpb + 3) / 4 || lds_total > static_cast<size_t>(160 * 1024)) continue;
+            if (simd_waves < (wpb + 3) / 4 || lds_total > aq_lds_budget(kfn)) continue;
             const int64_t waves = (M + fw - 1) / fw;
             const int64_t blocks = (waves + wpb - 1) / wpb;
             const int64_t per_simd = ((blocks + cus - 1) / cus) * ((wpb * fw + 3) / 4);
@@ -786,6 +981,10 @@ struct aq_dac_stages {
     float4 *d_images = nullptr;   // [Q][img_f4]
     float4 *d_images_tb = nullptr;   // the same with W_in in the tinyBLAS layout
     float *d_tables = nullptr;    // [Q][N][D]
+    // Shapes outside the fused kernel's (dac_any_kernel): W_in [Q][8][D],
+    // b_in [Q][8], normalised codes [Q][N][8], one allocation
+    bool any = false;
+    float *d_any = nullptr;
     // OuteTTS host-loop recipe: raw weights, one allocation
     float *d_ot = nullptr;
     aq_outetts_args ot{};         // the weight pointers into d_ot
@@ -866,6 +1065,129 @@ aq_status upload_outetts(aq_ctx *ctx, int64_t Q, int64_t D, int64_t N, const flo
     return AQ_OK;
 }
 
+// Largest latent of the any-shape kernel (one frame's residual in LDS) and
+// largest codebook of either kernel.
+constexpr int64_t kAnyMaxD = 40000;
+constexpr int64_t kMaxN = int64_t{1} << 24;
+
+// Upload for dac_any_kernel: the weights as given, the recipe's normalised
+// codebook rows and the out-projection tables, built on the device.
+aq_status upload_any(aq_ctx *ctx, int64_t Q, int64_t D, int64_t N, const float *w_in, const float *b_in,
+                     const float *codebook, const float *w_out, const float *b_out, int recipe, aq_dac_stages **out) {
+    if (D > kAnyMaxD || N > kMaxN)
+        return aq_fail(ctx, AQ_E_SHAPE, "aq_dac_upload: D=%lld N=%lld exceed the supported %lld x %lld", (long long)D,
+                       (long long)N, (long long)kAnyMaxD, (long long)kMaxN);
+    aq_device_guard g(ctx->device);
+    aq_dac_stages *st = new (std::nothrow) aq_dac_stages();
+    if (!st) return aq_fail(ctx, AQ_E_NOMEM, "aq_dac_upload: host allocation failed");
+    st->device = ctx->device;
+    st->Q = Q;
+    st->D = D;
+    st->N = N;
+    st->recipe = recipe;
+    st->any = true;
+    st->has_bin = b_in != nullptr;
+    st->qeps = recipe == AQ_DAC_INDEXTTS2 ? 0.0f : (recipe == AQ_DAC_VEVO2 ? 1.0e-20f : 1.0e-12f);
+    const size_t nwin = static_cast<size_t>(Q * 8 * D), nbin = static_cast<size_t>(Q * 8),
+                 nchat = static_cast<size_t>(Q * N * 8);
+    float *d_cb = nullptr, *d_wout = nullptr, *d_bout = nullptr;
+    unsigned long long *d_flags = nullptr;
+    auto cleanup = [&]() {
+        for (void *p : {static_cast<void *>(d_cb), static_cast<void *>(d_wout), static_cast<void *>(d_bout),
+                        static_cast<void *>(d_flags)})
+            if (p) (void)hipFree(p);
+    };
+    if (hipMalloc(&st->d_any, sizeof(float) * (nwin + nbin + nchat)) != hipSuccess ||
+        hipMalloc(&d_cb, sizeof(float) * nchat) != hipSuccess ||
+        hipMalloc(&d_flags, 2 * sizeof(unsigned long long)) != hipSuccess ||
+        (w_out && (hipMalloc(&st->d_tables, sizeof(float) * static_cast<size_t>(Q * N * D)) != hipSuccess ||
+                   hipMalloc(&d_wout, sizeof(float) * static_cast<size_t>(Q * D * 8)) != hipSuccess ||
+                   (b_out && hipMalloc(&d_bout, sizeof(float) * static_cast<size_t>(Q * D)) != hipSuccess)))) {
+        cleanup();
+        aq_dac_release(st);
+        return aq_fail(ctx, AQ_E_NOMEM, "aq_dac_upload: device allocation failed");
+    }
+    float *win = st->d_any, *bin = st->d_any + nwin, *chat = st->d_any + nwin + nbin;
+    const unsigned long long flags_init[2] = {~0ull, 0ull};
+    bool ok = hipMemcpyAsync(win, w_in, sizeof(float) * nwin, hipMemcpyHostToDevice, ctx->stream) == hipSuccess &&
+              (!b_in || hipMemcpyAsync(bin, b_in, sizeof(float) * nbin, hipMemcpyHostToDevice, ctx->stream) == hipSuccess) &&
+              hipMemcpyAsync(d_cb, codebook, sizeof(float) * nchat, hipMemcpyHostToDevice, ctx->stream) == hipSuccess &&
+              hipMemcpyAsync(d_flags, flags_init, sizeof(flags_init), hipMemcpyHostToDevice, ctx->stream) == hipSuccess;
+    if (ok) {
+        hipLaunchKernelGGL(dac_any_chat_kernel, dim3(static_cast<unsigned>((Q * N + 255) / 256)), dim3(256), 0,
+                           ctx->stream, d_cb, Q * N, recipe, chat, d_flags);
+        ok = hipGetLastError() == hipSuccess;
+    }
+    if (w_out)
+        ok = ok &&
+             hipMemcpyAsync(d_wout, w_out, sizeof(float) * static_cast<size_t>(Q * D * 8), hipMemcpyHostToDevice, ctx->stream) == hipSuccess &&
+             (!b_out || hipMemcpyAsync(d_bout, b_out, sizeof(float) * static_cast<size_t>(Q * D), hipMemcpyHostToDevice, ctx->stream) == hipSuccess);
+    for (int64_t s = 0; ok && w_out && s < Q; ++s) {
+        hipLaunchKernelGGL(dac_table_kernel, dim3(static_cast<unsigned>((N * D + 255) / 256)), dim3(256), 0, ctx->stream,
+                           d_cb + s * N * 8, d_wout + s * D * 8, d_bout ? d_bout + s * D : nullptr, N, D,
+                           st->d_tables + s * N * D);
+        ok = hipGetLastError() == hipSuccess;
+    }
+    unsigned long long flags[2] = {~0ull, 0ull};
+    ok = ok && hipMemcpyAsync(flags, d_flags, sizeof(flags), hipMemcpyDeviceToHost, ctx->stream) == hipSuccess &&
+         hipStreamSynchronize(ctx->stream) == hipSuccess;
+    cleanup();
+    if (!ok) {
+        aq_dac_release(st);
+        return aq_fail(ctx, AQ_E_DEVICE, "aq_dac_upload: device copy or codebook preparation failed");
+    }
+    if (flags[0] != ~0ull) {
+        const long long n = static_cast<long long>(flags[0] % static_cast<unsigned long long>(N)),
+                        s = static_cast<long long>(flags[0] / static_cast<unsigned long long>(N));
+        aq_dac_release(st);
+        return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_dac_upload: codebook row %lld of stage %lld has zero norm", n, s);
+    }
+    *out = st;
+    return AQ_OK;
+}
+
+// Launch of dac_any_kernel on frame-major rows x [M, D].
+aq_status encode_any(aq_ctx *ctx, const aq_dac_stages *st, const float *x, int64_t M, int64_t clip_len, int32_t *idx,
+                     int64_t idx_ld, float *residual, float *recon, int recon_accumulate, const int32_t *force_idx) {
+    const int64_t D = st->D;
+    int wpb = 4;
+    while (wpb > 1 && static_cast<size_t>(wpb) * D * sizeof(float) > aq_lds_budget(reinterpret_cast<const void *>(dac_any_kernel)))
+        wpb /= 2;
+    const size_t lds = static_cast<size_t>(wpb) * D * sizeof(float);
+    {
+        aq_status ls = aq_launch_lds(ctx, reinterpret_cast<const void *>(dac_any_kernel), lds, "aq_dac_encode");
+        if (ls != AQ_OK) return ls;
+    }
+    DacAnyArgs a{};
+    a.x = x;
+    a.M = M;
+    a.D = static_cast<int>(D);
+    a.N = static_cast<int>(st->N);
+    a.Q = static_cast<int>(st->Q);
+    const float *win = st->d_any;
+    a.w_in = win;
+    a.b_in = st->has_bin ? win + st->Q * 8 * D : nullptr;
+    a.chat = win + st->Q * 8 * D + st->Q * 8;
+    a.tables = st->d_tables;
+    a.idx = idx;
+    a.ld = static_cast<int>(idx_ld);
+    a.residual = residual;
+    a.recon = recon;
+    a.recon_acc = recon_accumulate ? 1 : 0;
+    a.force_idx = force_idx;
+    a.flags = ctx->d_flags;
+    a.qeps = st->qeps;
+    // tinyBLAS takes the in-projection when the clip length is a multiple of
+    // 4 and D of 16 (ggml-cpu.c:1285-1306, sgemm.cpp:3705-3725)
+    a.order = (clip_len % 4 == 0 && D % 16 == 0) ? 1 : 0;
+    const int tslot = aq_timing_start(ctx);
+    hipLaunchKernelGGL(dac_any_kernel, dim3(static_cast<unsigned>((M + wpb - 1) / wpb)), dim3(wpb * kWave), lds,
+                       ctx->stream, a);
+    aq_timing_stop(ctx, tslot);
+    AQ_HIP(ctx, hipGetLastError());
+    return AQ_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -886,13 +1208,19 @@ aq_status aq_dac_upload_ex(aq_ctx *ctx, int64_t Q, int64_t D, int64_t N, const f
     if (!w_out && Q != 1)
         return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_dac_upload: a residual cascade (Q=%lld) needs the out-projection",
                        (long long)Q);
-    if (Q <= 0 || D <= 0 || N <= 0 || D % kWave != 0 || N % kWave != 0 || !pick_kernel(D, 1, false, false, false))
-        return aq_fail(ctx, AQ_E_SHAPE, "aq_dac_upload: unsupported shape Q=%lld D=%lld N=%lld (D in {64,128,256,512,768,1024}, N multiple of 64)",
-                       (long long)Q, (long long)D, (long long)N);
+    if (Q <= 0 || D <= 0 || N <= 0)
+        return aq_fail(ctx, AQ_E_SHAPE, "aq_dac_upload: empty shape Q=%lld D=%lld N=%lld", (long long)Q, (long long)D,
+                       (long long)N);
+    // The fused kernel's shapes: D a multiple of 64 with a register tile
+    // (64 ... 1024), N a multiple of 64 up to 2^20; anything else takes the
+    // any-shape kernel.
+    if (D % kWave != 0 || N % kWave != 0 || N > (int64_t{1} << 20) || !pick_kernel(D, 1, false, false, false))
+        return upload_any(ctx, Q, D, N, w_in, b_in, codebook, w_out, b_out, recipe, out);
     const int64_t img = image_f4(D, N);
-    const bool cbg = img * 16 > 160 * 1024;
-    if (N > (int64_t{1} << 20))
-        return aq_fail(ctx, AQ_E_SHAPE, "aq_dac_upload: N=%lld exceeds 2^20", (long long)N);
+    // c_hat read from memory when the whole stage image does not fit in LDS
+    // next to the kernel's static LDS
+    const bool cbg = static_cast<size_t>(img) * 16 >
+                     aq_lds_budget(reinterpret_cast<const void *>(pick_kernel(D, 1, false, false, false)));
     aq_device_guard g(ctx->device);
 
     aq_dac_stages *st = new (std::nothrow) aq_dac_stages();
@@ -992,6 +1320,7 @@ aq_status aq_dac_release(aq_dac_stages *st) {
         if (st->d_images_tb) (void)hipFree(st->d_images_tb);
         if (st->d_tables) (void)hipFree(st->d_tables);
         if (st->d_ot) (void)hipFree(st->d_ot);
+        if (st->d_any) (void)hipFree(st->d_any);
     }
     delete st;
     return AQ_OK;
@@ -1064,6 +1393,20 @@ aq_status aq_dac_encode_ex(aq_ctx *ctx, const aq_dac_stages *st, const float *x,
     if (!st->d_tables && (residual || recon))
         return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_dac_encode: no out-projection was uploaded (codes only)");
     aq_device_guard g(ctx->device);
+    if (st->any) {
+        if (force_idx) AQ_HIP(ctx, hipMemsetAsync(ctx->d_flags, 0, sizeof(int32_t) * AQ_FLAG_COUNT, ctx->stream));
+        aq_status as = encode_any(ctx, st, x, M, clip_len, idx, idx_ld, residual, recon, recon_accumulate, force_idx);
+        if (as != AQ_OK) return as;
+        if (force_idx) {
+            int32_t flag = 0;
+            AQ_HIP(ctx, hipMemcpyAsync(&flag, ctx->d_flags + AQ_FLAG_BAD_INDEX, sizeof(int32_t), hipMemcpyDeviceToHost,
+                                       ctx->stream));
+            AQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
+            if (flag)
+                return aq_fail(ctx, AQ_E_INDEX_RANGE, "aq_dac_encode: force_idx holds a code outside [0, %lld)", (long long)st->N);
+        }
+        return AQ_OK;
+    }
     const size_t img_bytes = static_cast<size_t>(st->lds_f4) * sizeof(float4);
     const int shape_key = (recon != nullptr ? 1 : 0) | (order << 1);
     if (st->shape_m != M || st->shape_key != shape_key) {
@@ -1076,11 +1419,12 @@ aq_status aq_dac_encode_ex(aq_ctx *ctx, const aq_dac_stages *st, const float *x,
     EncodeFn fn = pick_kernel(st->D, fw, recon != nullptr, shape.prefetch, st->cbg, order);
     const size_t rt_bytes = order == 1 ? static_cast<size_t>(shape.waves_per_block) * static_cast<size_t>(st->D) * 4 : 0;
     // A second stage image in LDS when it fits: one barrier per stage.
-    const int64_t dbuf_f4 = 2 * img_bytes + rt_bytes <= static_cast<size_t>(160 * 1024) ? st->lds_f4 : 0;
+    const size_t budget = aq_lds_budget(reinterpret_cast<const void *>(fn));
+    const int64_t dbuf_f4 = 2 * img_bytes + rt_bytes <= budget ? st->lds_f4 : 0;
     const size_t lds_bytes = img_bytes * (dbuf_f4 > 0 ? 2 : 1) + rt_bytes;
     if (st->lds_fn != reinterpret_cast<const void *>(fn) || st->lds_limit != lds_bytes) {
-        AQ_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void *>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                        static_cast<int>(lds_bytes)));
+        aq_status ls = aq_launch_lds(ctx, reinterpret_cast<const void *>(fn), lds_bytes, "aq_dac_encode");
+        if (ls != AQ_OK) return ls;
         st->lds_fn = reinterpret_cast<const void *>(fn);
         st->lds_limit = lds_bytes;
     }

@@ -28,6 +28,13 @@ __global__ void zero2_kernel(int32_t *__restrict__ a, int na, int32_t *__restric
     for (int i = threadIdx.x; i < nb; i += blockDim.x) b[i] = 0;
 }
 
+// Per-stage counters of an any-width encode: no frame goes through a
+// certificate ([0, 64) stay 0) and the exact scan decides all M ([64, 128)).
+__global__ void any_counts_kernel(int32_t *__restrict__ c, int32_t m) {
+    const int i = threadIdx.x;
+    if (i < 128) c[i] = i < 64 ? 0 : m;
+}
+
 __global__ void gather_kernel(const float *__restrict__ cbf, int64_t N, int64_t K, const int32_t *__restrict__ idx,
                               int64_t M, float *__restrict__ out, int32_t *__restrict__ flags) {
     const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -200,6 +207,9 @@ struct aq_codebooks {
     int recipe = 0;
     bool q8 = false;
     bool exact_only = false;
+    // A width or size outside the fast kernels' (K in {64, 256, 512, 768},
+    // N a multiple of their chunk): every frame is scanned exactly.
+    bool any = false;
     uint16_t *d_cbh = nullptr;   // [Q][N][K] fp16(c)
     uint16_t *d_cbl = nullptr;   // [Q][N][K] fp16(c - fp16(c)) (refine pass)
     float *d_hh = nullptr;       // [Q][N] -|c|^2 / 2 (fp32 of the double sum)
@@ -215,20 +225,34 @@ struct aq_codebooks {
 
 namespace {
 
-// Shape and type checks shared by the uploads.
-aq_status check_upload(aq_ctx *ctx, const char *fn, int64_t Q, int64_t N, int64_t K, int cb_type, int recipe) {
+// Largest codebook width of the any-width path (the exact scan stages the
+// frame, its Q8_0 image and scales in LDS) and largest codebook size of
+// either path (codes are int32; the fast path keys carry 20 index bits).
+constexpr int64_t kAnyMaxK = 16384;
+constexpr int64_t kAnyMaxN = int64_t{1} << 24;
+constexpr int64_t kFastMaxN = int64_t{1} << 20;
+
+// Shape and type checks shared by the uploads.  *any: the shape takes the
+// any-width exact path (every width and size the reference accepts; GGUF
+// Q8_0 rows are whole 32-element blocks).
+aq_status check_upload(aq_ctx *ctx, const char *fn, int64_t Q, int64_t N, int64_t K, int cb_type, int recipe,
+                       bool *any) {
     if (recipe < AQ_EUCLID_OMNIVOICE || recipe > AQ_EUCLID_DIRECT)
         return aq_fail(ctx, AQ_E_INVALID_ARG, "%s: unknown recipe %d", fn, recipe);
     if (cb_type != AQ_CB_F32 && cb_type != AQ_CB_Q8_0 && cb_type != AQ_CB_F32_AS_Q8_0)
         return aq_fail(ctx, AQ_E_INVALID_ARG, "%s: unknown codebook type %d", fn, cb_type);
     if (cb_type != AQ_CB_F32 && recipe != AQ_EUCLID_HIGGS)
         return aq_fail(ctx, AQ_E_UNSUPPORTED, "%s: Q8_0 codebooks follow the Higgs recipe only", fn);
-    const KsKernels *kk = K > 0 && K % 32 == 0 ? kernels_for(static_cast<int>(K / 32)) : nullptr;
-    if (Q <= 0 || N <= 0 || !kk)
-        return aq_fail(ctx, AQ_E_SHAPE, "%s: unsupported shape Q=%lld N=%lld K=%lld (K in {64,256,512,768})", fn,
-                       (long long)Q, (long long)N, (long long)K);
-    if (N % kk->cc != 0 || N > (1 << 20))
-        return aq_fail(ctx, AQ_E_SHAPE, "%s: N=%lld must be a multiple of %d", fn, (long long)N, kk->cc);
+    if (Q <= 0 || N <= 0 || K <= 0)
+        return aq_fail(ctx, AQ_E_SHAPE, "%s: empty shape Q=%lld N=%lld K=%lld", fn, (long long)Q, (long long)N,
+                       (long long)K);
+    if (cb_type != AQ_CB_F32 && K % 32 != 0)
+        return aq_fail(ctx, AQ_E_SHAPE, "%s: Q8_0 rows of K=%lld are not whole 32-element blocks", fn, (long long)K);
+    const KsKernels *kk = K % 32 == 0 ? kernels_for(static_cast<int>(K / 32)) : nullptr;
+    *any = !kk || N % kk->cc != 0 || N > kFastMaxN;
+    if (*any && (K > kAnyMaxK || N > kAnyMaxN))
+        return aq_fail(ctx, AQ_E_SHAPE, "%s: K=%lld N=%lld exceed the supported %lld x %lld", fn, (long long)K,
+                       (long long)N, (long long)kAnyMaxK, (long long)kAnyMaxN);
     return AQ_OK;
 }
 
@@ -357,11 +381,13 @@ aq_status euclid_upload_from(aq_ctx *ctx, const char *fn, int64_t Q, int64_t N, 
                              const void *data, hipMemcpyKind kind, int recipe, aq_codebooks **out) {
     if (!ctx || !out || !data) return aq_fail(ctx, AQ_E_INVALID_ARG, "%s: null argument", fn);
     *out = nullptr;
-    aq_status st = check_upload(ctx, fn, Q, N, K, cb_type, recipe);
+    bool any = false;
+    aq_status st = check_upload(ctx, fn, Q, N, K, cb_type, recipe, &any);
     if (st != AQ_OK) return st;
     aq_device_guard g(ctx->device);
     aq_codebooks *cb = nullptr;
     st = euclid_alloc(ctx, Q, N, K, cb_type != AQ_CB_F32, recipe, &cb);
+    if (st == AQ_OK) cb->any = any;
     if (st == AQ_OK) st = euclid_fill(ctx, cb, cb_type, data, kind);
     if (st == AQ_OK) st = euclid_prepare(ctx, cb);
     if (st != AQ_OK) {
@@ -405,13 +431,15 @@ aq_status aq_euclid_upload_ema(aq_ctx *ctx, int64_t Q, int64_t N, int64_t K, con
     if (!ctx || !out || !embedding_sum || !cluster_usage)
         return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_euclid_upload_ema: null argument");
     *out = nullptr;
-    aq_status st = check_upload(ctx, "aq_euclid_upload_ema", Q, N, K, AQ_CB_F32, recipe);
+    bool any = false;
+    aq_status st = check_upload(ctx, "aq_euclid_upload_ema", Q, N, K, AQ_CB_F32, recipe, &any);
     if (st != AQ_OK) return st;
     aq_device_guard g(ctx->device);
     const size_t QNK = static_cast<size_t>(Q * N * K), QN = static_cast<size_t>(Q * N);
     aq_codebooks *cb = nullptr;
     st = euclid_alloc(ctx, Q, N, K, false, recipe, &cb);
     if (st != AQ_OK) return st;
+    cb->any = any;
     // the inputs go to the device once; the codebook is materialised straight
     // into the set's fp32 buffer and prepared there
     float *d = nullptr;
@@ -443,15 +471,24 @@ aq_status aq_euclid_upload_projected(aq_ctx *ctx, int64_t Q, int64_t N, int64_t 
         return aq_fail(ctx, AQ_E_UNSUPPORTED, "aq_euclid_upload_projected: projections follow the OmniVoice and Higgs recipes");
     if (proj_type != AQ_CB_F32 && proj_type != AQ_CB_Q8_0)
         return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_euclid_upload_projected: unknown weight type %d", proj_type);
-    // The projection block keeps 16 residual rows of H + 1 floats in LDS
-    // (plus their Q8_0 image for Q8_0 weights).
-    const int64_t lds = 16 * (H + 1) * 4 + (proj_type == AQ_CB_Q8_0 ? 16 * H + 16 * (H / 32) * 4 : 0);
-    if (H <= 0 || H % 64 != 0 || lds > 160 * 1024)
+    if (H <= 0 || H % 64 != 0)
         return aq_fail(ctx, AQ_E_SHAPE, "aq_euclid_upload_projected: hidden size H=%lld (a multiple of 64 up to %d)",
                        (long long)H, proj_type == AQ_CB_Q8_0 ? 1984 : 2496);
+    {
+        // the projection block keeps 16 residual rows of H + 1 floats in LDS
+        // (plus their Q8_0 image for Q8_0 weights)
+        aq_status ls = aq_proj_check_lds(ctx, H, proj_type == AQ_CB_Q8_0, "aq_euclid_upload_projected");
+        if (ls != AQ_OK) return ls;
+    }
     aq_codebooks *cb = nullptr;
     aq_status st = aq_euclid_upload(ctx, Q, N, K, cb_type, codebook, recipe, &cb);
     if (st != AQ_OK) return st;
+    if (cb->any) {
+        aq_euclid_release(cb);
+        return aq_fail(ctx, AQ_E_SHAPE,
+                       "aq_euclid_upload_projected: codebook shape N=%lld K=%lld (K in {64,256,512,768}, N a multiple of "
+                       "the chunk)", (long long)N, (long long)K);
+    }
     aq_device_guard g(ctx->device);
     st = aq_proj_create(ctx, Q, N, K, H, cb->d_cbf, proj_type, w_in, b_in, w_out, b_out, &cb->proj);
     if (st != AQ_OK) {
@@ -516,6 +553,12 @@ static __device__ __align__(256) unsigned char scratch[kNoAllocBytes];
 constexpr int kNoAllocDevices = 64;
 std::mutex g_noalloc_mu;
 void *g_noalloc_ptr[kNoAllocDevices];
+// Calls on one device are ordered through one event per device: each call's
+// stream waits for the previous call's work, which records the event after
+// it (the host enqueues one call at a time per device).  Calls captured
+// into a HIP graph are not ordered by it.
+std::mutex g_noalloc_call_mu[kNoAllocDevices];
+hipEvent_t g_noalloc_done[kNoAllocDevices];
 
 // The device address of `scratch` on ctx's device (current when called),
 // looked up on the first call on that device.
@@ -529,9 +572,89 @@ aq_status noalloc_region(aq_ctx *ctx, unsigned char **out) {
         if (e != hipSuccess || !p)
             return aq_fail(ctx, AQ_E_DEVICE, "aq_euclid_encode_noalloc: hipGetSymbolAddress failed: %s",
                            hipGetErrorString(e));
+        hipEvent_t ev = nullptr;
+        const hipError_t e2 = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+        if (e2 != hipSuccess)
+            return aq_fail(ctx, AQ_E_DEVICE, "aq_euclid_encode_noalloc: hipEventCreate failed: %s", hipGetErrorString(e2));
+        g_noalloc_done[ctx->device] = ev;
         g_noalloc_ptr[ctx->device] = p;
     }
     *out = static_cast<unsigned char *>(g_noalloc_ptr[ctx->device]);
+    return AQ_OK;
+}
+
+// Encode on an any-width codebook set: per stage, the exact scan of every
+// frame in the recipe's arithmetic (the run-time-width exact scan, one block
+// per frame), with the residual cascade r -= c[code] in between.
+aq_status euclid_encode_any(aq_ctx *ctx, const aq_codebooks *cb, const aq_frames_desc &in, int64_t M, int32_t *idx,
+                            float *residual, float *dist, int topk, int32_t *topk_idx, float *topk_dist,
+                            const int32_t *force_idx, Arena &arena) {
+    const int64_t K = cb->K;
+    StageFn scan = kernels_any()->exact_scan[variant_of(cb->recipe, cb->q8)];
+    const size_t lds = scan_lds_bytes(K);
+    {
+        aq_status ls = aq_launch_lds(ctx, reinterpret_cast<const void *>(scan), lds, "aq_euclid_encode (exact scan)");
+        if (ls != AQ_OK) return ls;
+    }
+    float *work = residual;
+    if (!work) {
+        aq_status st = arena.get(0, static_cast<size_t>(M) * K * sizeof(float), reinterpret_cast<void **>(&work));
+        if (st != AQ_OK) return st;
+    }
+    int32_t *counts = nullptr;
+    {
+        aq_status st = arena.get(1, 128 * sizeof(int32_t), reinterpret_cast<void **>(&counts));
+        if (st != AQ_OK) return st;
+    }
+    ctx->euclid_counts = counts;
+    hipLaunchKernelGGL(any_counts_kernel, dim3(1), dim3(128), 0, ctx->stream, counts, static_cast<int32_t>(M));
+    AQ_HIP(ctx, hipGetLastError());
+    hipLaunchKernelGGL(zero2_kernel, dim3(1), dim3(64), 0, ctx->stream, ctx->d_flags, static_cast<int>(AQ_FLAG_COUNT),
+                       ctx->d_flags, 0);
+    AQ_HIP(ctx, hipGetLastError());
+    const float *x0 = in.x;
+    const bool row_major = in.frame_stride == K && in.chan_stride == 1 && (in.clip_len >= M || in.clip_stride == in.clip_len * K);
+    if (!row_major) {
+        aq_status st = aq_gather_frames(ctx, in, M, K, work);
+        if (st != AQ_OK) return st;
+        x0 = work;
+    }
+    const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
+    const unsigned grid = static_cast<unsigned>(std::min<int64_t>(M, int64_t{8} * cus));
+    for (int64_t s = 0; s < cb->Q; ++s) {
+        StageArgs a{};
+        a.xin = s == 0 ? x0 : work;
+        a.xout = (s + 1 < cb->Q || residual) ? work : nullptr;
+        a.M = M;
+        a.N = static_cast<int>(cb->N);
+        a.K = static_cast<int>(K);
+        a.cbf = cb->d_cbf + s * cb->N * K;
+        a.bias = cb->d_bias + s * cb->N;
+        a.e2 = cb->d_e2 + s * cb->N;
+        a.q8 = cb->q8 ? cb->d_q8 + s * cb->N * K : nullptr;
+        a.q8d = cb->q8 ? cb->d_q8d + s * cb->N * (K / 32) : nullptr;
+        // ggml's choice between tinyBLAS and ggml_vec_dot_f32 (see run_stage)
+        a.order = (M >= 2 && K % 16 == 0 && cb->N % 4 == 0) ? 0 : 1;
+        a.Q = static_cast<int>(cb->Q);
+        a.s = static_cast<int>(s);
+        a.idx = idx;
+        a.dist = dist;
+        a.topk = topk;
+        a.topk_idx = topk_idx;
+        a.topk_dist = topk_dist;
+        a.force_idx = force_idx;
+        a.flags = ctx->d_flags;
+        const int tslot = arena.base ? -1 : aq_timing_start(ctx);
+        hipLaunchKernelGGL(scan, dim3(grid), dim3(kScanThreads), lds, ctx->stream, a);
+        aq_timing_stop(ctx, tslot);
+        AQ_HIP(ctx, hipGetLastError());
+    }
+    if (force_idx) {
+        int32_t flag = 0;
+        AQ_HIP(ctx, hipMemcpyAsync(&flag, ctx->d_flags + AQ_FLAG_BAD_INDEX, sizeof(int32_t), hipMemcpyDeviceToHost, ctx->stream));
+        AQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        if (flag) return aq_fail(ctx, AQ_E_INDEX_RANGE, "aq_euclid_encode: force_idx holds a code outside [0, %lld)", (long long)cb->N);
+    }
     return AQ_OK;
 }
 
@@ -554,6 +677,7 @@ aq_status euclid_encode_impl(aq_ctx *ctx, const aq_codebooks *cb, const aq_frame
         return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_euclid_encode: topk outputs missing");
     if (M == 0) return AQ_OK;
     aq_device_guard g(ctx->device);
+    if (cb->any) return euclid_encode_any(ctx, cb, in, M, idx, residual, dist, topk, topk_idx, topk_dist, force_idx, arena);
     const int K = static_cast<int>(cb->K);
     const int ks = K / 32;
     const aq_proj_weights *pw = cb->proj;
@@ -568,7 +692,12 @@ aq_status euclid_encode_impl(aq_ctx *ctx, const aq_codebooks *cb, const aq_frame
     StageFn select = kk->select[var][topl - 3];
     StageFn scan = kk->exact_scan[var];
     const int lds = kk->lds;
-    AQ_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void *>(sweep), hipFuncAttributeMaxDynamicSharedMemorySize, lds));
+    const size_t scan_lds = scan_lds_bytes(K);
+    {
+        aq_status ls = aq_launch_lds(ctx, reinterpret_cast<const void *>(sweep), static_cast<size_t>(lds), "aq_euclid_encode (sweep)");
+        if (ls == AQ_OK) ls = aq_launch_lds(ctx, reinterpret_cast<const void *>(scan), scan_lds, "aq_euclid_encode (exact scan)");
+        if (ls != AQ_OK) return ls;
+    }
     const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
 
     // Sweep launch: tiles of kWaves * FG * 16 frames; the codebook is split
@@ -582,7 +711,6 @@ aq_status euclid_encode_impl(aq_ctx *ctx, const aq_codebooks *cb, const aq_frame
     for (int sp = 1; sp <= 4; ++sp)
         if (nch % sp == 0 && tiles * sp <= 2 * cus) nsplit = sp;
     const int64_t ngroups = (M + 15) / 16;
-    const size_t scan_lds = static_cast<size_t>(K) * 5 + (K / 32) * 4 + 64;
 
     // Work buffers: the residual (the caller's buffer when given; [M, H]),
     // the projected queries of a projected cascade ([M, K]), the sweep's keys
@@ -680,6 +808,7 @@ aq_status euclid_encode_impl(aq_ctx *ctx, const aq_codebooks *cb, const aq_frame
         a.xout = xout;
         a.M = M;
         a.N = static_cast<int>(cb->N);
+        a.K = K;
         a.cbh = cb->d_cbh + s * cb->N * K;
         a.nhh = cb->d_hh + s * cb->N;
         a.cbf = cb->d_cbf + s * cb->N * K;
@@ -806,11 +935,24 @@ aq_status aq_euclid_encode_noalloc(aq_ctx *ctx, const aq_codebooks *cb, const fl
     if (!ctx || !cb) return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_euclid_encode_noalloc: null argument");
     aq_device_guard g(ctx->device);
     unsigned char *base = nullptr;
-    const aq_status st = noalloc_region(ctx, &base);
+    aq_status st = noalloc_region(ctx, &base);
     if (st != AQ_OK) return st;
     const int64_t H = cb->proj ? cb->proj->H : cb->K;
-    return euclid_encode_impl(ctx, cb, aq_frames_row_major(x, M, H), M, idx, residual, dist, topk, topk_idx, topk_dist,
-                              force_idx, Arena{ctx, base, kNoAllocBytes, 0});
+    // One call at a time per device on the host; on the device, this call's
+    // stream waits for the previous call's work (any context, any stream).
+    std::lock_guard<std::mutex> order(g_noalloc_call_mu[ctx->device]);
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    AQ_HIP(ctx, hipStreamIsCapturing(ctx->stream, &cap));
+    const bool ordered = cap == hipStreamCaptureStatusNone;
+    if (ordered) AQ_HIP(ctx, hipStreamWaitEvent(ctx->stream, g_noalloc_done[ctx->device], 0));
+    st = euclid_encode_impl(ctx, cb, aq_frames_row_major(x, M, H), M, idx, residual, dist, topk, topk_idx, topk_dist,
+                            force_idx, Arena{ctx, base, kNoAllocBytes, 0});
+    if (ordered) {
+        const hipError_t e = hipEventRecord(g_noalloc_done[ctx->device], ctx->stream);
+        if (e != hipSuccess && st == AQ_OK)
+            return aq_fail(ctx, AQ_E_DEVICE, "aq_euclid_encode_noalloc: hipEventRecord failed: %s", hipGetErrorString(e));
+    }
+    return st;
 }
 
 aq_status aq_euclid_encode_strided(aq_ctx *ctx, const aq_codebooks *cb, const float *x, int64_t M, int64_t clip_len,

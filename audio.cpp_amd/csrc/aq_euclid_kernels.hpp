@@ -138,6 +138,7 @@ struct StageArgs {
     int scap;                // frames whose values the exact scan spreads over its grid
     int32_t *slot_done;      // [scap] chunks done per slot (zero between stages)
     const int32_t *open_count;   // exact scan: the frames the select left open (null: not known)
+    int K;                   // codebook width (read by the any-width exact scan, KS = 0)
 };
 
 struct RefArgs {
@@ -205,6 +206,17 @@ const KsKernels *kernels_ks8();
 const KsKernels *kernels_ks16();
 const KsKernels *kernels_ks24();
 
+// The exact scan at a run-time width (any K; K % 32 == 0 for Q8_0), built in
+// aq_euclid_any.hip: codebooks outside the fast widths and tile sizes scan
+// every frame exactly in the recipe's arithmetic.  Variants as KsKernels.
+struct AnyKernels {
+    StageFn exact_scan[4];
+};
+const AnyKernels *kernels_any();
+// Dynamic LDS of the exact scan: the frame (K floats), its Q8_0 quants (K
+// bytes) and scales (K / 32 floats).
+constexpr size_t scan_lds_bytes(int64_t K) { return static_cast<size_t>(K) * 5 + static_cast<size_t>(K / 32) * 4 + 64; }
+
 }  // namespace aq_euclid
 
 namespace {
@@ -256,8 +268,7 @@ __device__ float dot_tinyblas(const float *__restrict__ a, const float *__restri
 }
 
 // ggml_vec_dot_f32, AVX-512 branch: 4 x 16 accumulators over 64-element
-// steps, combined 0+=2, 1+=3, 0+=1, reduced, then scalar leftovers (rounded
-// products added in order).
+// steps, combined 0+=2, 1+=3, 0+=1, reduced, then the scalar leftovers.
 __device__ float dot_vecdot(const float *__restrict__ a, const float *__restrict__ b, int K, float sa) {
     float s[4][16];
 #pragma unroll
@@ -275,7 +286,13 @@ __device__ float dot_vecdot(const float *__restrict__ a, const float *__restrict
 #pragma unroll
     for (int l = 0; l < 16; ++l) r[l] = __fadd_rn(__fadd_rn(s[0][l], s[2][l]), __fadd_rn(s[1][l], s[3][l]));
     float sum = reduce16(r);
-    for (int i = np; i < K; ++i) sum = __fadd_rn(sum, __fmul_rn(a[i] * sa, b[i]));
+    // The leftover loop `sumf += x[i]*y[i]` as GCC 11 compiles it for the
+    // reference's native AVX-512 build: the products of the first
+    // rem - rem % 4 leftovers rounded and added in order, the last rem % 4
+    // fused (vec.cpp:125-128).
+    const int fused_from = K - (K - np) % 4;
+    for (int i = np; i < K; ++i)
+        sum = i >= fused_from ? __fmaf_rn(a[i] * sa, b[i], sum) : __fadd_rn(sum, __fmul_rn(a[i] * sa, b[i]));
     return sum;
 }
 
@@ -1702,9 +1719,30 @@ __device__ void spread_item(const StageArgs &a, int slot, int chunk, int &cur, f
     if (n < a.N) a.svals[static_cast<int64_t>(slot) * a.N + n] = exact_value_kq<RECIPE, Q8, K>(a, xs, n, x2s, xq, xd);
 }
 
+// The exact scan's per-frame arithmetic at the compile-time width K = 32 KS,
+// or at the run-time width K (KS = 0: any width).
+template <int RECIPE, bool Q8, int KS>
+__device__ inline float scan_value(const StageArgs &a, int K, const float *__restrict__ x, int n, float x2,
+                                   const int8_t *__restrict__ xq, const float *__restrict__ xd) {
+    if constexpr (KS != 0) return exact_value_kq<RECIPE, Q8, KS * 32>(a, x, n, x2, xq, xd);
+    else return exact_value<RECIPE, Q8>(a, K, x, n, x2, xq, xd);
+}
+template <int KS>
+__device__ inline float scan_sum_squares(const float *__restrict__ x, int K) {
+    if constexpr (KS != 0) {
+        return sum_squares_k<KS * 32>(x);
+    } else {
+        double s = 0.0;
+        for (int k = 0; k < K; ++k) s += static_cast<double>(__fmul_rn(x[k], x[k]));
+        return static_cast<float>(s);
+    }
+}
+
 template <int RECIPE, bool Q8, int KS>
 __global__ __launch_bounds__(kScanThreads) void euclid_exact_scan_kernel(StageArgs a) {
-    constexpr int K = KS * 32;
+    // KS = 0: the width is a run-time argument and every frame of the batch
+    // is scanned (no frame list, no spread values)
+    const int K = KS != 0 ? KS * 32 : a.K;
     constexpr int ST = kScanThreads;
     constexpr int PT = kScanChunk / ST;   // values per thread of a one-chunk frame
     extern __shared__ __align__(16) unsigned char lds[];
@@ -1720,26 +1758,26 @@ __global__ __launch_bounds__(kScanThreads) void euclid_exact_scan_kernel(StageAr
     __shared__ int w_nan[ST / kWave];
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
-    const int count = *a.fail_count;
+    const int count = KS != 0 ? *a.fail_count : static_cast<int>(a.M);
     const int ktop = a.topk;
     // pre: up to a.scap frames, whose code values the grid computes first
     // (one (frame, kScanThreads-code chunk) item per block and pass); the
     // block that completes a frame's last chunk selects for it
-    const bool pre = count <= a.scap;
+    const bool pre = KS != 0 && count <= a.scap;
     __shared__ int o_last;
     auto scan_slot = [&](int slot) {
-        const int64_t m = a.fail_list[slot];
+        const int64_t m = KS != 0 ? a.fail_list[slot] : slot;
         __syncthreads();
         if (!pre) {
             for (int k = tid; k < K; k += ST) xs[k] = a.xin[m * K + k];
             __syncthreads();
-            if (tid == 0) o_x2 = RECIPE == HIGGS ? sum_squares_k<K>(xs) : 0.0f;   // unrolled: LDS reads in flight
+            if (tid == 0) o_x2 = RECIPE == HIGGS ? scan_sum_squares<KS>(xs, K) : 0.0f;   // unrolled: LDS reads in flight
             if (Q8 && tid < K / 32) quantize_block_q8(xs + 32 * tid, xq + 32 * tid, xd + tid);
             __syncthreads();
         }
         const float x2 = pre ? 0.0f : o_x2;
         const float *sv = pre ? a.svals + static_cast<int64_t>(slot) * a.N : nullptr;
-        auto value = [&](int n) -> float { return pre ? sv[n] : exact_value_kq<RECIPE, Q8, K>(a, xs, n, x2, xq, xd); };
+        auto value = [&](int n) -> float { return pre ? sv[n] : scan_value<RECIPE, Q8, KS>(a, K, xs, n, x2, xq, xd); };
 
         // The frame's values.  Codes that fit one chunk (N <= kScanChunk):
         // PT per thread in registers (code tid + j * ST), and all in rv in
@@ -1759,7 +1797,7 @@ __global__ __launch_bounds__(kScanThreads) void euclid_exact_scan_kernel(StageAr
                 if (tid + j * ST < a.N) rv[tid + j * ST] = vr[j];
         } else if (in_regs) {
 #pragma unroll 4
-            for (int i = tid; i < a.N; i += ST) rv[i] = exact_value_kq<RECIPE, Q8, K>(a, xs, i, x2, xq, xd);
+            for (int i = tid; i < a.N; i += ST) rv[i] = scan_value<RECIPE, Q8, KS>(a, K, xs, i, x2, xq, xd);
         }
         __syncthreads();
         if (in_regs && !pre) {
@@ -2041,11 +2079,12 @@ __global__ __launch_bounds__(kScanThreads) void euclid_exact_scan_kernel(StageAr
         for (int slot = blockIdx.x; slot < count; slot += gridDim.x) scan_slot(slot);
         return;
     }
+    if constexpr (KS != 0) {
     const int nch = spread_chunks<RECIPE, Q8>(a);
     int cur = -1;
     for (int item = blockIdx.x; item < count * nch; item += gridDim.x) {
         const int slot = item / nch;   // block-uniform
-        spread_item<RECIPE, Q8, K>(a, slot, item % nch, cur, xs, xq, xd, o_x2);
+        spread_item<RECIPE, Q8, KS * 32>(a, slot, item % nch, cur, xs, xq, xd, o_x2);
         // release: this block's values before the frame's counter; the block
         // that brings it to nch sees every chunk's values after its acquire
         __threadfence();
@@ -2058,6 +2097,7 @@ __global__ __launch_bounds__(kScanThreads) void euclid_exact_scan_kernel(StageAr
             if (tid == 0) a.slot_done[slot] = 0;   // ready for the next stage
             cur = -1;                              // scan_slot used xs
         }
+    }
     }
 }
 

@@ -579,9 +579,6 @@ __global__ void moss_decode_kernel(const int32_t *__restrict__ idx, int64_t M, i
 
 // ---------------------------------------------------------------- OuteTTS host
 
-namespace {
-constexpr size_t kLdsMax = 160 * 1024;
-}
 
 aq_status aq_outetts_prepare(aq_ctx *ctx, const float *d_cb, int64_t rows, float *d_chat) {
     hipLaunchKernelGGL(outetts_chat_kernel, dim3(static_cast<unsigned>((rows + 255) / 256)), dim3(256), 0, ctx->stream,
@@ -595,17 +592,21 @@ aq_status aq_outetts_launch(aq_ctx *ctx, const aq_outetts_args &args) {
     // (kOtW waves per block while they and the in-projection fit, fewer for
     // wide latents)
     aq_outetts_args a = args;
+    const void *fn = reinterpret_cast<const void *>(outetts_encode_kernel);
+    const size_t budget = aq_lds_budget(fn);
     const size_t per_wave = static_cast<size_t>(kHF) * (a.D + 4) * sizeof(float);
     const size_t win = static_cast<size_t>(8) * (a.D + 4) * sizeof(float), chat = static_cast<size_t>(8) * a.N * sizeof(float);
     int nw = kOtW;
-    while (nw > 1 && nw * per_wave + win > kLdsMax) --nw;
+    while (nw > 1 && nw * per_wave + win > budget) --nw;
     size_t lds = nw * per_wave;
-    a.win_lds = lds + win <= kLdsMax ? 1 : 0;
+    a.win_lds = lds + win <= budget ? 1 : 0;
     if (a.win_lds) lds += win;
-    a.chat_lds = lds + chat <= kLdsMax ? 1 : 0;
+    a.chat_lds = lds + chat <= budget ? 1 : 0;
     if (a.chat_lds) lds += chat;
-    AQ_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void *>(outetts_encode_kernel),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+    {
+        aq_status ls = aq_launch_lds(ctx, fn, lds, "aq_dac_encode (OuteTTS)");
+        if (ls != AQ_OK) return ls;
+    }
     const int64_t per_block = static_cast<int64_t>(nw) * kHF;
     const unsigned blocks = static_cast<unsigned>((a.M + per_block - 1) / per_block);
     const int tslot = aq_timing_start(ctx);
@@ -786,17 +787,21 @@ aq_status aq_moss_encode(aq_ctx *ctx, const aq_moss_quantizer *q, const float *h
     a.write_res = residual ? 1 : 0;
     // the residuals, then the stage tables while they fit the CU's LDS
     // (kMsW waves per block while they and the in-projection fit)
+    const void *fn = reinterpret_cast<const void *>(moss_cascade_kernel);
+    const size_t budget = aq_lds_budget(fn);
     const size_t per_wave = static_cast<size_t>(kHF) * (q->R + 2) * sizeof(double);
     const size_t win = static_cast<size_t>(8) * (q->R + 4) * sizeof(float), tn = static_cast<size_t>(8) * q->N * sizeof(float);
     int nw = kMsW;
-    while (nw > 1 && nw * per_wave + win > kLdsMax) --nw;
+    while (nw > 1 && nw * per_wave + win > budget) --nw;
     size_t lds = nw * per_wave;
-    a.win_lds = lds + win <= kLdsMax ? 1 : 0;
+    a.win_lds = lds + win <= budget ? 1 : 0;
     if (a.win_lds) lds += win;
-    a.tn_lds = lds + tn <= kLdsMax ? 1 : 0;
+    a.tn_lds = lds + tn <= budget ? 1 : 0;
     if (a.tn_lds) lds += tn;
-    AQ_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void *>(moss_cascade_kernel),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+    {
+        aq_status ls = aq_launch_lds(ctx, fn, lds, "aq_moss_encode");
+        if (ls != AQ_OK) return ls;
+    }
     const int64_t per_block = static_cast<int64_t>(nw) * kHF;
     const int tslot = aq_timing_start(ctx);
     hipLaunchKernelGGL(moss_cascade_kernel, dim3(static_cast<unsigned>((M + per_block - 1) / per_block)), dim3(kWave * nw),

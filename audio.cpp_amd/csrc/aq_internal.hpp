@@ -43,6 +43,30 @@ void aq_timing_stop(aq_ctx *ctx, int slot);
 // first; bytes == 0 returns the current buffer, possibly null).
 aq_status aq_ctx_scratch(aq_ctx *ctx, int slot, size_t bytes, void **out);
 
+// LDS of a gfx950 compute unit: a block's static and dynamic LDS together
+// must fit in it.  HIP does not reject a launch whose total exceeds it (the
+// queue aborts instead), so every launch with dynamic LDS is checked first.
+constexpr size_t kAqLdsBytes = 160 * 1024;
+// Static LDS of kernel `fn` (hipFuncGetAttributes, cached per kernel; an
+// unreadable attribute counts as the whole LDS, so the check fails).
+size_t aq_static_lds(const void *fn);
+// True when `dynamic` bytes of dynamic LDS fit next to fn's static LDS.
+inline bool aq_lds_fits(const void *fn, size_t dynamic) {
+    const size_t st = aq_static_lds(fn);
+    return st <= kAqLdsBytes && dynamic <= kAqLdsBytes - st;
+}
+
+// LDS left for dynamic allocation next to fn's static LDS.
+inline size_t aq_lds_budget(const void *fn) {
+    const size_t st = aq_static_lds(fn);
+    return st < kAqLdsBytes ? kAqLdsBytes - st : 0;
+}
+// Before a launch of fn with `dynamic` bytes of dynamic LDS on ctx's device:
+// AQ_E_SHAPE (naming `what`) when it does not fit next to the kernel's
+// static LDS, else raises the kernel's dynamic-LDS limit if needed (once
+// per device and size, not per call).
+aq_status aq_launch_lds(aq_ctx *ctx, const void *fn, size_t dynamic, const char *what);
+
 // Sets `ctx->err` and returns `st`.
 inline aq_status aq_fail(aq_ctx *ctx, aq_status st, const char *fmt, ...) {
     if (ctx) {

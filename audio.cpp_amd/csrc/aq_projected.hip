@@ -36,6 +36,15 @@ namespace {
 constexpr int kPF = 16;     // frames per projection block
 constexpr int kPT = 256;    // threads per projection block
 
+// Dynamic LDS of the batched projection kernels: kPF residual rows of H + 1
+// floats (channel-major reads spread over the banks), and for Q8_0 weights
+// their quantised image (H bytes and H / 32 scales per row).
+inline size_t proj_rows_lds(int64_t H, bool q8) {
+    size_t b = static_cast<size_t>(kPF) * static_cast<size_t>(H + 1) * sizeof(float);
+    if (q8) b += static_cast<size_t>(kPF) * static_cast<size_t>(H) + static_cast<size_t>(kPF) * static_cast<size_t>(H / 32) * sizeof(float);
+    return b;
+}
+
 struct ProjArgs {
     aq_frames_desc in;
     float *rout;            // [M, H] or null
@@ -537,23 +546,34 @@ aq_status aq_proj_step(aq_ctx *ctx, const aq_proj_weights *pw, int s, int prev, 
             o.b_out_prev = pw->b_out ? pw->b_out + prev * pw->H : nullptr;
             o.cbf_prev = pw->cbf + prev * pw->N * pw->K;
         }
-        hipLaunchKernelGGL(proj_one_kernel, dim3(1), dim3(kPT), (H + K) * sizeof(float), ctx->stream, o);
+        // the frame's H floats, and the previous stage's K-float code row
+        // when a table row is subtracted
+        const size_t lds = (static_cast<size_t>(H) + (prev >= 0 ? static_cast<size_t>(K) : 0)) * sizeof(float);
+        aq_status ls = aq_launch_lds(ctx, reinterpret_cast<const void *>(proj_one_kernel), lds, "projection of one frame");
+        if (ls != AQ_OK) return ls;
+        hipLaunchKernelGGL(proj_one_kernel, dim3(1), dim3(kPT), lds, ctx->stream, o);
         AQ_HIP(ctx, hipGetLastError());
         return AQ_OK;
     }
-    const size_t rows = static_cast<size_t>(kPF) * (H + 1) * sizeof(float);
+    const size_t lds = proj_rows_lds(H, pw->q8);
+    const void *fn = pw->q8 ? reinterpret_cast<const void *>(proj_in_q8_kernel)
+                            : reinterpret_cast<const void *>(proj_in_f32_kernel);
+    aq_status ls = aq_launch_lds(ctx, fn, lds, "projection");
+    if (ls != AQ_OK) return ls;
     const unsigned grid = static_cast<unsigned>((M + kPF - 1) / kPF);
-    if (pw->q8) {
-        const size_t lds = rows + static_cast<size_t>(kPF) * H + static_cast<size_t>(kPF) * (H / 32) * sizeof(float);
-        AQ_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void *>(proj_in_q8_kernel),
-                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
-        hipLaunchKernelGGL(proj_in_q8_kernel, dim3(grid), dim3(kPT), lds, ctx->stream, a);
-    } else {
-        AQ_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void *>(proj_in_f32_kernel),
-                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(rows)));
-        hipLaunchKernelGGL(proj_in_f32_kernel, dim3(grid), dim3(kPT), rows, ctx->stream, a);
-    }
+    if (pw->q8) hipLaunchKernelGGL(proj_in_q8_kernel, dim3(grid), dim3(kPT), lds, ctx->stream, a);
+    else hipLaunchKernelGGL(proj_in_f32_kernel, dim3(grid), dim3(kPT), lds, ctx->stream, a);
     AQ_HIP(ctx, hipGetLastError());
+    return AQ_OK;
+}
+
+aq_status aq_proj_check_lds(aq_ctx *ctx, int64_t H, bool q8, const char *fn) {
+    const void *k = q8 ? reinterpret_cast<const void *>(proj_in_q8_kernel)
+                       : reinterpret_cast<const void *>(proj_in_f32_kernel);
+    if (H <= 0 || !aq_lds_fits(k, proj_rows_lds(H, q8)) ||
+        !aq_lds_fits(reinterpret_cast<const void *>(proj_one_kernel), static_cast<size_t>(H) * sizeof(float)))
+        return aq_fail(ctx, AQ_E_SHAPE, "%s: hidden size H=%lld needs more LDS than a CU has (up to %d)", fn,
+                       (long long)H, q8 ? 1984 : 2496);
     return AQ_OK;
 }
 
@@ -596,13 +616,15 @@ aq_status aq_linear_upload(aq_ctx *ctx, int64_t out_features, int64_t in_feature
     *out = nullptr;
     if (w_type != AQ_CB_F32 && w_type != AQ_CB_Q8_0)
         return aq_fail(ctx, AQ_E_INVALID_ARG, "aq_linear_upload: unknown weight type %d", w_type);
-    const int64_t lds = 16 * (in_features + 1) * 4 +
-                        (w_type == AQ_CB_Q8_0 ? 16 * in_features + 16 * (in_features / 32) * 4 : 0);
     if (out_features <= 0 || out_features % 64 != 0 || out_features > (int64_t{1} << 16) || in_features <= 0 ||
-        in_features % 64 != 0 || lds > 160 * 1024)
+        in_features % 64 != 0)
         return aq_fail(ctx, AQ_E_SHAPE,
                        "aq_linear_upload: out_features=%lld in_features=%lld (multiples of 64; in_features up to %d)",
                        (long long)out_features, (long long)in_features, w_type == AQ_CB_Q8_0 ? 1984 : 2496);
+    {
+        aq_status ls = aq_proj_check_lds(ctx, in_features, w_type == AQ_CB_Q8_0, "aq_linear_upload");
+        if (ls != AQ_OK) return ls;
+    }
     aq_device_guard g(ctx->device);
     aq_linear *lin = new (std::nothrow) aq_linear();
     if (!lin) return aq_fail(ctx, AQ_E_NOMEM, "aq_linear_upload: host allocation failed");

@@ -65,5 +65,11 @@ aq_status aq_proj_step(aq_ctx *ctx, const aq_proj_weights *pw, int s, int prev, 
 // (frame-major [M, H]); AQ_FLAG_BAD_INDEX on an out-of-range code.
 aq_status aq_proj_decode(aq_ctx *ctx, const aq_proj_weights *pw, const int32_t *idx, int64_t M, float *out);
 
+// AQ_OK when the projection kernels' LDS (16 frames of H + 1 floats, plus
+// their Q8_0 image for Q8_0 weights; one H-float row for a single frame)
+// fits a CU next to their static LDS; else AQ_E_SHAPE with `fn` in the
+// message.
+aq_status aq_proj_check_lds(aq_ctx *ctx, int64_t H, bool q8, const char *fn);
+
 // Gather of a strided input into frame-major rows: out[m, c] for c < C.
 aq_status aq_gather_frames(aq_ctx *ctx, const aq_frames_desc &in, int64_t M, int64_t C, float *out);

@@ -1,6 +1,21 @@
 // Context management for the C ABI declared in include/aq_mi355x.h.
 #include "aq_internal.hpp"
 
+#include <mutex>
+#include <unordered_map>
+
+size_t aq_static_lds(const void *fn) {
+    static std::mutex mu;
+    static std::unordered_map<const void *, size_t> cache;
+    std::lock_guard<std::mutex> lock(mu);
+    const auto it = cache.find(fn);
+    if (it != cache.end()) return it->second;
+    hipFuncAttributes attr{};
+    const size_t v = hipFuncGetAttributes(&attr, fn) == hipSuccess ? attr.sharedSizeBytes : kAqLdsBytes + 1;
+    cache.emplace(fn, v);
+    return v;
+}
+
 aq_status aq_ctx_scratch(aq_ctx *ctx, int slot, size_t bytes, void **out) {
     if (!ctx || !out || slot < 0 || slot >= aq_ctx::kScratchSlots) return AQ_E_INVALID_ARG;
     if (bytes > ctx->scratch_bytes[slot]) {
@@ -33,6 +48,24 @@ int aq_timing_start(aq_ctx *ctx) {
 void aq_timing_stop(aq_ctx *ctx, int slot) {
     if (!ctx || slot < 0) return;
     (void)hipEventRecord(ctx->ev_stop[static_cast<size_t>(slot)], ctx->stream);
+}
+
+aq_status aq_launch_lds(aq_ctx *ctx, const void *fn, size_t dynamic, const char *what) {
+    if (!aq_lds_fits(fn, dynamic))
+        return aq_fail(ctx, AQ_E_SHAPE, "%s: %zu bytes of LDS (%zu dynamic) exceed a CU's %zu", what,
+                       dynamic + aq_static_lds(fn), dynamic, kAqLdsBytes);
+    static std::mutex mu;
+    static std::unordered_map<const void *, size_t> raised[64];
+    const int dev = ctx->device >= 0 && ctx->device < 64 ? ctx->device : 0;
+    std::lock_guard<std::mutex> lock(mu);
+    size_t &have = raised[dev][fn];
+    if (dynamic > have) {
+        const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(dynamic));
+        if (e != hipSuccess)
+            return aq_fail(ctx, AQ_E_DEVICE, "%s: hipFuncSetAttribute failed: %s", what, hipGetErrorString(e));
+        have = dynamic;
+    }
+    return AQ_OK;
 }
 
 extern "C" {

@@ -279,18 +279,24 @@ class VectorQuantizer {
 public:
     explicit VectorQuantizer(Context &ctx) : ctx_(&ctx) {}
 
+    // Any dim and codebook_size, as the reference: shapes outside the fast
+    // kernels' tiles take the library's exact any-width scan.  The size check
+    // is the reference's (a plain product of the arguments); frames exist
+    // only for batch > 0 and steps > 0, as its loops run.  An empty codebook
+    // with frames to encode is an error here (the reference reads past the
+    // end of its codebook vector).
     FloatHostTensor compute(const std::vector<float> &input, const std::vector<float> &codebook, int64_t batch,
                             int64_t steps, int64_t dim, int64_t codebook_size) const {
-        if (batch < 0 || steps < 0 || dim < 0 || codebook_size < 0 ||
-            static_cast<int64_t>(input.size()) != batch * steps * dim ||
+        if (static_cast<int64_t>(input.size()) != batch * steps * dim ||
             static_cast<int64_t>(codebook.size()) != codebook_size * dim) {
             throw std::runtime_error("VectorQuantizer input size mismatch");
         }
         FloatHostTensor result;
         result.shape = {batch, steps, dim};
         result.values.resize(input.size());
-        const int64_t M = batch * steps;
-        if (M == 0) return result;
+        const int64_t M = batch > 0 && steps > 0 ? batch * steps : 0;
+        if (M == 0 || dim <= 0) return result;
+        if (codebook_size <= 0) throw std::runtime_error("VectorQuantizer: empty codebook");
         EuclideanRvq rvq(*ctx_, 1, codebook_size, dim, codebook.data(), AQ_EUCLID_DIRECT);
         detail::DeviceBuffer<float> x(input.size()), out(input.size());
         detail::DeviceBuffer<int32_t> idx(static_cast<size_t>(M));

@@ -158,13 +158,24 @@ int main() {
                    "MossQuantizer shape message");
         }
     }
+    {   // VectorQuantizer at a dim and codebook size outside the fast tiles
+        const int64_t B = 2, T = 50, K = 100, N = 1000;
+        const auto x = rng.normal(B * T * K, 1.0);
+        const auto cb = rng.normal(N * K, 0.25);
+        const auto got = vq.compute(x, cb, B, T, K, N);
+        std::vector<int32_t> idx(B * T);
+        std::vector<float> res(B * T * K), dist(B * T), want(B * T * K);
+        aqo_direct_rvq(x.data(), B * T, K, 1, N, cb.data(), nullptr, idx.data(), res.data(), dist.data());
+        aqo_gather_f32(cb.data(), N, K, idx.data(), B * T, want.data());
+        expect(same_bits(got.values.data(), want.data(), want.size()), "VectorQuantizer dim 100 x 1000 == oracle");
+    }
     {   // errors surface as std::runtime_error with the library's message
         try {
-            const auto cb = rng.normal(100 * 256, 1.0);
-            aq::EuclideanRvq bad(*ctx, 1, 100, 256, cb.data(), AQ_EUCLID_OMNIVOICE);
-            expect(false, "unsupported codebook size throws");
+            const auto cb = rng.normal(100 * 40, 1.0);
+            aq::EuclideanRvq bad(*ctx, 1, 100, 40, cb.data(), AQ_EUCLID_HIGGS, AQ_CB_F32_AS_Q8_0);
+            expect(false, "Q8_0 rows of partial blocks throw");
         } catch (const std::runtime_error &e) {
-            expect(std::string(e.what()).find("aq_euclid_upload") != std::string::npos, "unsupported codebook size message");
+            expect(std::string(e.what()).find("aq_euclid_upload") != std::string::npos, "Q8_0 partial block message");
         }
     }
     std::printf("%s (%d failed)\n", failures ? "FAILED" : "OK", failures);

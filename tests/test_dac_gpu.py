@@ -147,8 +147,8 @@ def test_dac_errors(torch, ctx):
     with pytest.raises(aqmi.AqError) as e:
         st.decode(bad, out)
     assert e.value.status == 3
-    with pytest.raises(aqmi.AqError) as e:
-        aqmi.DacStages(ctx, np.zeros((1, 8, 100), np.float32), None, np.zeros((1, 64, 8), np.float32),
+    with pytest.raises(aqmi.AqError) as e:   # an empty codebook
+        aqmi.DacStages(ctx, np.zeros((1, 8, 100), np.float32), None, np.zeros((1, 0, 8), np.float32),
                        np.zeros((1, 100, 8), np.float32), None)
     assert e.value.status == 2
 

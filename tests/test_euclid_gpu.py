@@ -237,8 +237,8 @@ def test_gather_and_decode(torch, ctx):
     with pytest.raises(aqmi.AqError) as e:
         cbs.gather(0, bad, out[:2])
     assert e.value.status == 3
-    with pytest.raises(aqmi.AqError) as e:
-        aqmi.Codebooks(ctx, synth.normal(1, 1, (1, 100, 256)), aqmi.OMNIVOICE)
+    with pytest.raises(aqmi.AqError) as e:   # an empty codebook
+        aqmi.Codebooks(ctx, synth.normal(1, 1, (1, 0, 256)), aqmi.OMNIVOICE)
     assert e.value.status == 2
     q8 = synth.q8_0_random_codebook(1, 1, 64, 256)[None]
     with pytest.raises(aqmi.AqError) as e:

@@ -158,7 +158,8 @@ def test_upload_quantises_f32_like_the_weight_store(torch, ctx, oracle):
 @pytest.mark.parametrize("n_out,k,M,q8,bias", [(64, 1024, 1, False, True), (64, 1024, 2, False, True),
                                                 (128, 512, 301, False, False), (1024, 64, 77, False, True),
                                                 (64, 1024, 1, True, True), (256, 512, 333, True, False),
-                                                (512, 2496, 40, False, True), (128, 1984, 40, True, True)])
+                                                (512, 2496, 40, False, True), (128, 1984, 40, True, True),
+                                                (40960, 256, 1, False, True), (128, 2496, 1, False, False)])
 def test_linear_matches_oracle(torch, ctx, oracle, n_out, k, M, q8, bias):
     """aq_linear (encoder output projection) bit for bit against the
     oracle's LinearModule (pinned to the reference's ggml graph in
@@ -207,3 +208,37 @@ def test_linear_errors(torch, ctx):
         aqmi.Linear(ctx, np.zeros((60, 64), np.float32))
     with pytest.raises(aqmi.AqError):
         aqmi.Linear(ctx, np.zeros((64, 2560), np.float32))
+
+
+@pytest.mark.parametrize("q8,last_ok", [(False, 2496), (True, 1984)])
+def test_lds_limits_include_static_lds(torch, ctx, q8, last_ok):
+    """The projection kernels keep 16 frames' rows in LDS: the largest
+    hidden size that fits next to the kernels' static LDS uploads, the next
+    multiple of 64 returns AQ_E_SHAPE before anything is launched (linear and
+    projected uploads alike)."""
+    import aqmi
+    from aqmi import synth
+
+    print(f"[gpu] LDS limit q8={q8}", flush=True)
+
+    def weights(rows, cols):
+        w = synth.normal(39, rows + cols, (rows, cols), 0.05)
+        return synth.q8_0_quantize_ref(w) if q8 else w
+
+    aqmi.Linear(ctx, weights(64, last_ok)).close()
+    with pytest.raises(aqmi.AqError) as e:
+        aqmi.Linear(ctx, weights(64, last_ok + 64))
+    assert e.value.status == 2
+    Q, N, K = 1, 256, 64
+    cb = synth.normal(39, 5, (Q, N, K), 0.3)
+    for H, ok in ((last_ok, True), (last_ok + 64, False)):
+        w_in = np.stack([weights(K, H)])
+        w_out = np.stack([weights(H, K)])
+        if ok:
+            aqmi.Codebooks.projected(ctx, cb, w_in, None, w_out, None, aqmi.HIGGS,
+                                     proj_type=aqmi.CB_Q8_0 if q8 else aqmi.CB_F32).close()
+        else:
+            with pytest.raises(aqmi.AqError) as e:
+                aqmi.Codebooks.projected(ctx, cb, w_in, None, w_out, None, aqmi.HIGGS,
+                                         proj_type=aqmi.CB_Q8_0 if q8 else aqmi.CB_F32)
+            assert e.value.status == 2
