@@ -113,8 +113,12 @@ aq_status aq_ctx_read_timing(aq_ctx *ctx, float *ms, int capacity, int *count);
  *   w_in  [Q, 8, D]   b_in  [Q, 8]   (NULL = no bias)
  *   codebook [Q, N, 8]
  *   w_out [Q, D, 8]   b_out [Q, D]   (NULL = no bias)
- * Supported: codebook dim 8, D in {64, 128, ..., 1024} (multiple of 64),
- * N a multiple of 64 up to 2^20.
+ * Supported: codebook dim 8, any D >= 1 (up to 40000) and N >= 1 (up to
+ * 2^24), as the reference's graphs accept.  D in {64, 128, 256, 512, 768,
+ * 1024} with N a multiple of 64 up to 2^20 runs the fused kernel (residual
+ * in registers, certified approximate scores); other shapes run a cascade
+ * kernel with run-time D and N (residual in LDS, every score exact), with
+ * the same results.
  * Replaces load_quantizer_unit (codec.cpp:693-720) / BackendWeightStore. */
 aq_status aq_dac_upload(aq_ctx *ctx, int64_t Q, int64_t D, int64_t N,
                         const float *w_in, const float *b_in, const float *codebook,
@@ -254,8 +258,16 @@ typedef enum aq_codebook_type {
  * and the per-call codebook set-up of the host loops).  The data goes to
  * the device as given; Q8_0 blocks are unpacked and every derived image and
  * constant is built there (only 5 bounds per stage come back).
- * Supported: K in {64, 256, 512, 768}; N a multiple of 256, 64, 32, 16
- * respectively; Q8_0 with AQ_EUCLID_HIGGS only. */
+ * Supported: any K >= 1 (up to 16384) and N >= 1 (up to 2^24), as the
+ * reference's VectorQuantizer and mul_mat graphs accept; Q8_0 rows are whole
+ * 32-element blocks (K % 32 == 0) and follow AQ_EUCLID_HIGGS only.  K in
+ * {64, 256, 512, 768} with N a multiple of 256, 64, 32, 16 respectively (up
+ * to 2^20) runs the matrix-core sweep with its certificate; other shapes
+ * scan every frame exactly in the recipe's arithmetic (same results).  For
+ * a codebook width that is not a multiple of 64 in ggml_vec_dot_f32's order
+ * (one query, or K % 16 != 0, or N % 4 != 0), the results are those of the
+ * reference's default native x86 build (its leftover products: the last
+ * n % 4 fused, the others rounded then added). */
 aq_status aq_euclid_upload(aq_ctx *ctx, int64_t Q, int64_t N, int64_t K, int cb_type, const void *data,
                            int recipe, aq_codebooks **out);
 /* aq_euclid_upload from device memory (a codebook already resident, e.g.
@@ -288,10 +300,15 @@ aq_status aq_euclid_encode(aq_ctx *ctx, const aq_codebooks *cb, const float *x, 
  * keys get what the other buffers leave (frames past that go to the exact
  * scan, same results).  A call that needs more of the region fails with
  * AQ_E_SHAPE (e.g. a 48 000 x 256 Mimi batch needs a caller residual buffer).
- * Every call on a device shares the region: calls that overlap on one device
- * race.  The counters of aq_euclid_failures / aq_euclid_exact_scans refer to
- * the region until the next encode on the context.  Results equal
- * aq_euclid_encode's. */
+ * Every call on a device shares the region.  Calls are ordered on the device
+ * through one HIP event per device (created with the region's address at
+ * the first call): each call's stream waits for the previous call's work,
+ * from any context and stream, and the host enqueues one call at a time per
+ * device.  Calls captured into a HIP graph are not ordered by the event:
+ * graph launches that contain this call must not overlap each other or
+ * other calls on the device.  The counters of aq_euclid_failures /
+ * aq_euclid_exact_scans refer to the region, i.e. to the last no-allocation
+ * call on the device.  Results equal aq_euclid_encode's. */
 aq_status aq_euclid_encode_noalloc(aq_ctx *ctx, const aq_codebooks *cb, const float *x, int64_t M, int32_t *idx,
                                    float *residual, float *dist, int topk, int32_t *topk_idx, float *topk_dist,
                                    const int32_t *force_idx);
