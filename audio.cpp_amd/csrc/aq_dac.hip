@@ -1180,10 +1180,8 @@ aq_status encode_any(aq_ctx *ctx, const aq_dac_stages *st, const float *x, int64
     // tinyBLAS takes the in-projection when the clip length is a multiple of
     // 4 and D of 16 (ggml-cpu.c:1285-1306, sgemm.cpp:3705-3725)
     a.order = (clip_len % 4 == 0 && D % 16 == 0) ? 1 : 0;
-    const int tslot = aq_timing_start(ctx);
-    hipLaunchKernelGGL(dac_any_kernel, dim3(static_cast<unsigned>((M + wpb - 1) / wpb)), dim3(wpb * kWave), lds,
-                       ctx->stream, a);
-    aq_timing_stop(ctx, tslot);
+    aq_launch_timed(ctx, true, dac_any_kernel, dim3(static_cast<unsigned>((M + wpb - 1) / wpb)), dim3(wpb * kWave),
+                    static_cast<uint32_t>(lds), a);
     AQ_HIP(ctx, hipGetLastError());
     return AQ_OK;
 }
@@ -1431,13 +1429,11 @@ aq_status aq_dac_encode_ex(aq_ctx *ctx, const aq_dac_stages *st, const float *x,
     if (force_idx) AQ_HIP(ctx, hipMemsetAsync(ctx->d_flags, 0, sizeof(int32_t) * AQ_FLAG_COUNT, ctx->stream));
     const int64_t frames_per_block = static_cast<int64_t>(shape.waves_per_block) * fw;
     const unsigned blocks = static_cast<unsigned>((M + frames_per_block - 1) / frames_per_block);
-    const int tslot = aq_timing_start(ctx);
-    hipLaunchKernelGGL(fn, dim3(blocks), dim3(shape.waves_per_block * kWave), lds_bytes, ctx->stream, x, M, static_cast<int>(st->Q),
-                       static_cast<int>(st->N), order == 1 ? st->d_images_tb : st->d_images, st->img_f4, st->lds_f4,
-                       st->d_tables, idx, residual, recon,
-                       force_idx, ctx->d_flags, st->has_bin ? 1 : 0, st->key_bits, st->margin, st->exact_only ? 1 : 0,
-                       st->qeps, dbuf_f4, static_cast<int>(idx_ld), recon_accumulate ? 1 : 0);
-    aq_timing_stop(ctx, tslot);
+    aq_launch_timed(ctx, true, fn, dim3(blocks), dim3(shape.waves_per_block * kWave), static_cast<uint32_t>(lds_bytes), x, M,
+                    static_cast<int>(st->Q), static_cast<int>(st->N), order == 1 ? st->d_images_tb : st->d_images,
+                    st->img_f4, st->lds_f4, static_cast<const float *>(st->d_tables), idx, residual, recon, force_idx,
+                    ctx->d_flags, st->has_bin ? 1 : 0, st->key_bits, st->margin, st->exact_only ? 1 : 0, st->qeps,
+                    dbuf_f4, static_cast<int>(idx_ld), recon_accumulate ? 1 : 0);
     AQ_HIP(ctx, hipGetLastError());
     if (force_idx) {
         int32_t flag = 0;

@@ -644,9 +644,7 @@ aq_status euclid_encode_any(aq_ctx *ctx, const aq_codebooks *cb, const aq_frames
         a.topk_dist = topk_dist;
         a.force_idx = force_idx;
         a.flags = ctx->d_flags;
-        const int tslot = arena.base ? -1 : aq_timing_start(ctx);
-        hipLaunchKernelGGL(scan, dim3(grid), dim3(kScanThreads), lds, ctx->stream, a);
-        aq_timing_stop(ctx, tslot);
+        aq_launch_timed(ctx, !arena.base, scan, dim3(grid), dim3(kScanThreads), static_cast<uint32_t>(lds), a);
         AQ_HIP(ctx, hipGetLastError());
     }
     if (force_idx) {
@@ -845,10 +843,9 @@ aq_status euclid_encode_impl(aq_ctx *ctx, const aq_codebooks *cb, const aq_frame
             hipLaunchKernelGGL(zero2_kernel, dim3(1), dim3(256), 0, ctx->stream, counts, 128, counts, 0);
             AQ_HIP(ctx, hipGetLastError());
         }
-        const int tslot = arena.base ? -1 : aq_timing_start(ctx);   // events are not created without allocation
-        hipLaunchKernelGGL(sweep, dim3(static_cast<unsigned>((tiles + 7) / 8 * 8 * nsplit)), dim3(kThreads), lds,
-                           ctx->stream, a);
-        aq_timing_stop(ctx, tslot);
+        // (the no-allocation entry point creates no timing events)
+        aq_launch_timed(ctx, !arena.base, sweep, dim3(static_cast<unsigned>((tiles + 7) / 8 * 8 * nsplit)), dim3(kThreads),
+                        static_cast<uint32_t>(lds), a);
         AQ_HIP(ctx, hipGetLastError());
         hipLaunchKernelGGL(select, dim3(static_cast<unsigned>((ngroups + kWaves - 1) / kWaves)), dim3(kThreads), 0,
                            ctx->stream, a);

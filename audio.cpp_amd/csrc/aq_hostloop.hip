@@ -609,9 +609,7 @@ aq_status aq_outetts_launch(aq_ctx *ctx, const aq_outetts_args &args) {
     }
     const int64_t per_block = static_cast<int64_t>(nw) * kHF;
     const unsigned blocks = static_cast<unsigned>((a.M + per_block - 1) / per_block);
-    const int tslot = aq_timing_start(ctx);
-    hipLaunchKernelGGL(outetts_encode_kernel, dim3(blocks), dim3(kWave * nw), lds, ctx->stream, a);
-    aq_timing_stop(ctx, tslot);
+    aq_launch_timed(ctx, true, outetts_encode_kernel, dim3(blocks), dim3(kWave * nw), static_cast<uint32_t>(lds), a);
     AQ_HIP(ctx, hipGetLastError());
     return AQ_OK;
 }
@@ -763,11 +761,10 @@ aq_status aq_moss_encode(aq_ctx *ctx, const aq_moss_quantizer *q, const float *h
         if (st != AQ_OK) return st;
     }
     if (force_idx) AQ_HIP(ctx, hipMemsetAsync(ctx->d_flags, 0, sizeof(int32_t) * AQ_FLAG_COUNT, ctx->stream));
-    const int islot = aq_timing_start(ctx);
-    hipLaunchKernelGGL(moss_input_kernel, dim3(static_cast<unsigned>((M + kIpF - 1) / kIpF), static_cast<unsigned>(q->R / kIpO)),
-                       dim3(256), 0, ctx->stream, hidden, M, static_cast<int>(q->C), static_cast<int>(q->R), q->d_wip,
-                       q->d_bip, res);
-    aq_timing_stop(ctx, islot);
+    aq_launch_timed(ctx, true, moss_input_kernel,
+                    dim3(static_cast<unsigned>((M + kIpF - 1) / kIpF), static_cast<unsigned>(q->R / kIpO)), dim3(256), 0u,
+                    hidden, M, static_cast<int>(q->C), static_cast<int>(q->R), static_cast<const float *>(q->d_wip),
+                    static_cast<const float *>(q->d_bip), res);
     AQ_HIP(ctx, hipGetLastError());
     aq_moss_args a{};
     a.res = res;
@@ -803,10 +800,8 @@ aq_status aq_moss_encode(aq_ctx *ctx, const aq_moss_quantizer *q, const float *h
         if (ls != AQ_OK) return ls;
     }
     const int64_t per_block = static_cast<int64_t>(nw) * kHF;
-    const int tslot = aq_timing_start(ctx);
-    hipLaunchKernelGGL(moss_cascade_kernel, dim3(static_cast<unsigned>((M + per_block - 1) / per_block)), dim3(kWave * nw),
-                       lds, ctx->stream, a);
-    aq_timing_stop(ctx, tslot);
+    aq_launch_timed(ctx, true, moss_cascade_kernel, dim3(static_cast<unsigned>((M + per_block - 1) / per_block)),
+                    dim3(kWave * nw), static_cast<uint32_t>(lds), a);
     AQ_HIP(ctx, hipGetLastError());
     if (force_idx) {
         int32_t flag = 0;

@@ -1,6 +1,7 @@
 // Internal definitions shared by the C-ABI translation units.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
@@ -34,10 +35,22 @@ struct aq_ctx {
     size_t ev_used = 0;
 };
 
-// Records the start of a timed kernel on ctx's stream; returns the slot, or
-// -1 when timing is off.  aq_timing_stop closes it.
-int aq_timing_start(aq_ctx *ctx);
-void aq_timing_stop(aq_ctx *ctx, int slot);
+// The event pair of the next timed launch (false when timing is off or the
+// events cannot be created).
+bool aq_timing_events(aq_ctx *ctx, hipEvent_t *start, hipEvent_t *stop);
+
+// Launch of one of the timed kernels on ctx's stream.  With timing on (and
+// `may_time`), the dispatch itself records the kernel's start and end
+// (hipExtLaunchKernelGGL), so no event packets sit between the launches and
+// the durations are the kernels' own; otherwise a plain launch.
+template <typename F, typename... Args>
+inline void aq_launch_timed(aq_ctx *ctx, bool may_time, F kernel, dim3 grid, dim3 block, uint32_t lds, Args... args) {
+    hipEvent_t a = nullptr, b = nullptr;
+    if (may_time && aq_timing_events(ctx, &a, &b))
+        hipExtLaunchKernelGGL(kernel, grid, block, lds, ctx->stream, a, b, 0, args...);
+    else
+        hipLaunchKernelGGL(kernel, grid, block, lds, ctx->stream, args...);
+}
 
 // Device buffer `slot` of at least `bytes` (grows it, waiting for the stream
 // first; bytes == 0 returns the current buffer, possibly null).

@@ -32,22 +32,22 @@ aq_status aq_ctx_scratch(aq_ctx *ctx, int slot, size_t bytes, void **out) {
     return AQ_OK;
 }
 
-int aq_timing_start(aq_ctx *ctx) {
-    if (!ctx || !ctx->timing) return -1;
+bool aq_timing_events(aq_ctx *ctx, hipEvent_t *start, hipEvent_t *stop) {
+    if (!ctx || !ctx->timing) return false;
     if (ctx->ev_used == ctx->ev_start.size()) {
         hipEvent_t a = nullptr, b = nullptr;
-        if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess) return -1;
+        if (hipEventCreate(&a) != hipSuccess) return false;
+        if (hipEventCreate(&b) != hipSuccess) {
+            (void)hipEventDestroy(a);
+            return false;
+        }
         ctx->ev_start.push_back(a);
         ctx->ev_stop.push_back(b);
     }
     const size_t slot = ctx->ev_used++;
-    if (hipEventRecord(ctx->ev_start[slot], ctx->stream) != hipSuccess) return -1;
-    return static_cast<int>(slot);
-}
-
-void aq_timing_stop(aq_ctx *ctx, int slot) {
-    if (!ctx || slot < 0) return;
-    (void)hipEventRecord(ctx->ev_stop[static_cast<size_t>(slot)], ctx->stream);
+    *start = ctx->ev_start[slot];
+    *stop = ctx->ev_stop[slot];
+    return true;
 }
 
 aq_status aq_launch_lds(aq_ctx *ctx, const void *fn, size_t dynamic, const char *what) {

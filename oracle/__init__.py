@@ -18,7 +18,9 @@ import subprocess
 import numpy as np
 
 HERE = pathlib.Path(__file__).resolve().parent
-REF_DIR = HERE / "_ref"
+# AQ_REF_DIR selects another directory of builds (the sanitizer build of
+# tests/test_sanitizers.py)
+REF_DIR = pathlib.Path(os.environ.get("AQ_REF_DIR") or HERE / "_ref")
 
 _f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
 _i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
@@ -55,7 +57,9 @@ def host_isa() -> str:
 
 class Oracle:
     def __init__(self, path: str | os.PathLike | None = None):
-        path = pathlib.Path(path) if path else HERE / "liboracle.so"
+        # AQ_ORACLE_LIB selects another build of the same source (the
+        # sanitizer build of tests/test_sanitizers.py)
+        path = pathlib.Path(path or os.environ.get("AQ_ORACLE_LIB") or HERE / "liboracle.so")
         if not path.exists():
             build_oracle()
         self.lib = C.CDLL(str(path))
