@@ -218,6 +218,7 @@ struct aq_codebooks {
     float *d_e2 = nullptr;       // [Q][N] (HIGGS)
     int8_t *d_q8 = nullptr;      // [Q][N][K]
     float *d_q8d = nullptr;      // [Q][N][K/32]
+    float *d_bounds = nullptr;   // [Q][3] max |c|, max |c~ - c|, max |c~| (the cascade kernel's certificate)
     std::vector<float> cmax, dcmax, chmax;
     std::vector<float> clmax, crmax;   // max |c_l|, max |c - c_h - c_l| (refine bound)
     aq_proj_weights *proj = nullptr;   // project_in / project_out (projected cascades)
@@ -374,6 +375,17 @@ aq_status euclid_prepare(aq_ctx *ctx, aq_codebooks *cb) {
     int32_t nf;
     std::memcpy(&nf, &host[5 * cb->Q], 4);
     cb->exact_only = nf != 0;
+    // the per-stage bounds on the device, for the one-launch cascade
+    std::vector<float> b3(static_cast<size_t>(3 * cb->Q));
+    for (int64_t s = 0; s < cb->Q; ++s) {
+        b3[3 * s] = cb->cmax[s];
+        b3[3 * s + 1] = cb->dcmax[s];
+        b3[3 * s + 2] = cb->chmax[s];
+    }
+    if (!cb->d_bounds && hipMalloc(&cb->d_bounds, b3.size() * sizeof(float)) != hipSuccess)
+        return aq_fail(ctx, AQ_E_NOMEM, "aq_euclid_upload: device allocation failed");
+    AQ_HIP(ctx, hipMemcpyAsync(cb->d_bounds, b3.data(), b3.size() * sizeof(float), hipMemcpyHostToDevice, ctx->stream));
+    AQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
     return st;
 }
 
@@ -507,7 +519,7 @@ aq_status aq_euclid_release(aq_codebooks *cb) {
         for (void *p : {static_cast<void *>(cb->d_cbh), static_cast<void *>(cb->d_cbl), static_cast<void *>(cb->d_hh),
                         static_cast<void *>(cb->d_cbf),
                         static_cast<void *>(cb->d_bias), static_cast<void *>(cb->d_e2), static_cast<void *>(cb->d_q8),
-                        static_cast<void *>(cb->d_q8d)})
+                        static_cast<void *>(cb->d_q8d), static_cast<void *>(cb->d_bounds)})
             if (p) (void)hipFree(p);
     }
     delete cb;
@@ -656,6 +668,115 @@ aq_status euclid_encode_any(aq_ctx *ctx, const aq_codebooks *cb, const aq_frames
     return AQ_OK;
 }
 
+// Whether encodes take the one-launch cascade (AQ_EUCLID_PIPELINE=stages
+// selects the per-stage pipeline instead, for comparisons).
+bool cascade_enabled() {
+    const char *e = std::getenv("AQ_EUCLID_PIPELINE");
+    return !(e && std::strcmp(e, "stages") == 0);
+}
+
+// Encode with the one-launch cascade: every stage of every frame in
+// euclid_cascade_kernel (frames the certificate cannot settle continue with
+// their best exact candidate and are listed), the exact verification of the
+// listed (frame, stage) pairs, and the fix-up of frames whose continuation
+// was wrong.  Four launches per encode, whatever the number of stages.
+aq_status euclid_encode_cascade(aq_ctx *ctx, const aq_codebooks *cb, const aq_frames_desc &in, int64_t M, int32_t *idx,
+                                float *residual, float *dist, int topk, int32_t *topk_idx, float *topk_dist,
+                                const int32_t *force_idx, Arena &arena, const KsKernels *kk, int var, int topl) {
+    const int K = static_cast<int>(cb->K);
+    CascadeFn casc = kk->cascade[var][topl - 3], ver = kk->verify[var], fix = kk->fixup[var];
+    const size_t clds = static_cast<size_t>(kk->cascade_lds), slds = scan_lds_bytes(K);
+    {
+        aq_status ls = aq_launch_lds(ctx, reinterpret_cast<const void *>(casc), clds, "aq_euclid_encode (cascade)");
+        if (ls == AQ_OK) ls = aq_launch_lds(ctx, reinterpret_cast<const void *>(ver), slds, "aq_euclid_encode (verify)");
+        if (ls == AQ_OK) ls = aq_launch_lds(ctx, reinterpret_cast<const void *>(fix), slds, "aq_euclid_encode (fix-up)");
+        if (ls != AQ_OK) return ls;
+    }
+    float *work = residual;
+    if (!work) {
+        aq_status st = arena.get(0, static_cast<size_t>(M) * K * sizeof(float), reinterpret_cast<void **>(&work));
+        if (st != AQ_OK) return st;
+    }
+    // the stage-0 input stays intact for the verification: a strided input
+    // is gathered into a buffer of its own
+    const float *x0 = in.x;
+    const bool row_major = in.frame_stride == K && in.chan_stride == 1 && (in.clip_len >= M || in.clip_stride == in.clip_len * K);
+    if (!row_major) {
+        float *g = nullptr;
+        aq_status st = arena.get(2, static_cast<size_t>(M) * K * sizeof(float), reinterpret_cast<void **>(&g));
+        if (st == AQ_OK) st = aq_gather_frames(ctx, in, M, K, g);
+        if (st != AQ_OK) return st;
+        x0 = g;
+    }
+    // counters: [0, 128) per stage, 128 listed pairs, 129 frames to fix;
+    // then the pair list [2 M Q], bad_stage [M] and the frames to fix [M]
+    constexpr int kHead = 256;
+    int32_t *ints = nullptr;
+    {
+        const size_t n = kHead + 2 * static_cast<size_t>(M) * cb->Q + 2 * static_cast<size_t>(M);
+        aq_status st = arena.get(1, n * sizeof(int32_t), reinterpret_cast<void **>(&ints));
+        if (st != AQ_OK) return st;
+    }
+    ctx->euclid_counts = ints;
+    hipLaunchKernelGGL(zero2_kernel, dim3(1), dim3(256), 0, ctx->stream, ints, 130, ctx->d_flags,
+                       static_cast<int>(AQ_FLAG_COUNT));
+    AQ_HIP(ctx, hipGetLastError());
+    CascadeArgs c{};
+    StageArgs &a = c.a;
+    a.M = M;
+    a.N = static_cast<int>(cb->N);
+    a.K = K;
+    a.cbh = cb->d_cbh;
+    a.nhh = cb->d_hh;
+    a.cbf = cb->d_cbf;
+    a.bias = cb->d_bias;
+    a.e2 = cb->d_e2;
+    a.q8 = cb->q8 ? cb->d_q8 : nullptr;
+    a.q8d = cb->q8 ? cb->d_q8d : nullptr;
+    // ggml's choice between tinyBLAS and ggml_vec_dot_f32 (see run_stage)
+    a.order = (M >= 2 && K % 16 == 0 && cb->N % 4 == 0) ? 0 : 1;
+    a.Q = static_cast<int>(cb->Q);
+    a.idx = idx;
+    a.dist = dist;
+    a.topk = topk;
+    a.topk_idx = topk_idx;
+    a.topk_dist = topk_dist;
+    a.force_idx = force_idx;
+    a.flags = ctx->d_flags;
+    a.spec_count = ints + 128;
+    a.spec_list = ints + kHead;
+    {
+        // test hook: every frame speculates on a wrong code (the verification
+        // and fix-up then decide all of them)
+        const char *e = std::getenv("AQ_EUCLID_TEST_MISSPECULATE");
+        a.misspeculate = e && e[0] == '1';
+    }
+    c.x0 = x0;
+    c.work = work;
+    c.bounds = cb->d_bounds;
+    c.counts = ints;
+    c.bad_count = ints + 129;
+    c.bad_stage = ints + kHead + 2 * M * cb->Q;
+    c.bad_list = c.bad_stage + M;
+    c.write_last = residual ? 1 : 0;
+    const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
+    const int64_t blocks = (M + kk->cascade_frames - 1) / kk->cascade_frames;
+    aq_launch_timed(ctx, !arena.base, casc, dim3(static_cast<unsigned>(blocks)), dim3(kCThreads),
+                    static_cast<uint32_t>(clds), c);
+    AQ_HIP(ctx, hipGetLastError());
+    hipLaunchKernelGGL(ver, dim3(static_cast<unsigned>(2 * cus)), dim3(kScanThreads), slds, ctx->stream, c);
+    AQ_HIP(ctx, hipGetLastError());
+    hipLaunchKernelGGL(fix, dim3(static_cast<unsigned>(cus)), dim3(kScanThreads), slds, ctx->stream, c);
+    AQ_HIP(ctx, hipGetLastError());
+    if (force_idx) {
+        int32_t flag = 0;
+        AQ_HIP(ctx, hipMemcpyAsync(&flag, ctx->d_flags + AQ_FLAG_BAD_INDEX, sizeof(int32_t), hipMemcpyDeviceToHost, ctx->stream));
+        AQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        if (flag) return aq_fail(ctx, AQ_E_INDEX_RANGE, "aq_euclid_encode: force_idx holds a code outside [0, %lld)", (long long)cb->N);
+    }
+    return AQ_OK;
+}
+
 // Encode M frames (strided input `in`) through every stage of cb.  Plain
 // codebooks: the residual cascade in codebook space, r -= c[code].
 // Projected codebooks: per stage p = project_in(r), the stage pipeline on p,
@@ -686,6 +807,9 @@ aq_status euclid_encode_impl(aq_ctx *ctx, const aq_codebooks *cb, const aq_frame
     const int topl = (topk >= 4 || cb->N * cb->K >= (int64_t{1} << 22)) ? 4 : 3;
     const KsKernels *kk = kernels_for(ks);
     const int var = variant_of(cb->recipe, cb->q8);
+    if (!pw && !cb->exact_only && kk->cascade[var][topl - 3] && cascade_enabled())
+        return euclid_encode_cascade(ctx, cb, in, M, idx, residual, dist, topk, topk_idx, topk_dist, force_idx, arena, kk,
+                                     var, topl);
     StageFn sweep = kk->sweep[cb->q8 ? 1 : 0][topl - 3];
     StageFn select = kk->select[var][topl - 3];
     StageFn scan = kk->exact_scan[var];

@@ -129,6 +129,9 @@ struct StageArgs {
     const int32_t *force_idx;   // [M, Q] or null
     int32_t *fail_count;     // this stage's counter
     int32_t *fail_list;      // [M]
+    int32_t *spec_count;     // speculative (frame, stage) pairs listed (cascade)
+    int32_t *spec_list;      // [2 * M * Q] the pairs, for the exact verification
+    int misspeculate;        // test hook: every frame speculates, on a wrong code (cascade)
     int32_t *flags;
     int exact_only;
     float *keys;             // sweep -> select: [nsplit][M/16][TOPL][64] score keys
@@ -179,8 +182,26 @@ __device__ inline RefShape ref_shape(const RefArgs &rf, int N, int count) {
     return r;
 }
 
+// The whole residual cascade in one launch (euclid_cascade_kernel): per
+// stage s the kernel takes `a` with the stage's codebook pointers
+// (cbh / nhh / cbf / bias / e2 / q8 / q8d advanced by s codebooks), bounds
+// (bounds[3 s .. 3 s + 2] = max |c|, max |c~ - c|, max |c~|), xin = x0 at
+// stage 0 and the residual buffer after, xout = the residual buffer.
+struct CascadeArgs {
+    StageArgs a;             // stage 0's pointers; spec_count / spec_list set
+    const float *x0;         // [M, K] stage 0's input (frame-major; kept for the verification)
+    float *work;             // [M, K] the residual
+    const float *bounds;     // [Q][3] certificate bounds per stage
+    int32_t *counts;         // [128]: [0, 64) frames speculated per stage, [64, 128) frames the fix-up recomputed
+    int32_t *bad_stage;      // [M] the earliest stage whose speculation was wrong (Q: none)
+    int32_t *bad_count;      // frames listed in bad_list
+    int32_t *bad_list;       // [M]
+    int write_last;          // the last stage writes the residual
+};
+
 using StageFn = void (*)(StageArgs);
 using RefineFn = void (*)(StageArgs, RefArgs);
+using CascadeFn = void (*)(CascadeArgs);
 
 // 16-frame groups per sweep wave: the fp16 frames of a wave stay in
 // registers (4 * KS registers per group), so wider codebooks take fewer.
@@ -200,6 +221,13 @@ struct KsKernels {
     StageFn exact_scan[4];
     int lds;                  // sweep dynamic LDS bytes
     int cc;                   // codes per LDS chunk
+    // One-launch cascade (widths whose frame tiles keep two waves per SIMD;
+    // null otherwise), its verification and fix-up.
+    CascadeFn cascade[4][2];  // [variant][topl]
+    CascadeFn verify[4];
+    CascadeFn fixup[4];
+    int cascade_lds;          // cascade dynamic LDS bytes (TOPL 4)
+    int cascade_frames;       // frames per cascade block
 };
 const KsKernels *kernels_ks2();
 const KsKernels *kernels_ks8();
@@ -888,54 +916,48 @@ __global__ __launch_bounds__(kThreads, sweep_blocks_per_cu(KS)) void euclid_swee
     }
 }
 
-// Certificate, exact re-ranking and residual update of one stage.  A wave
-// takes 16 frames (4 lanes per frame, the sweep's lane layout), merges each
-// lane's key lists of all code splits and applies the certificate; the
-// frames it cannot settle go to the refine pass.
+// Per-wave LDS of the select: the queue of (frame, code) pairs evaluated
+// exactly, the frames' sum_rows(x*x) and (Q8_0) their query blocks, XQS
+// bytes apart: the 8 lane groups of a pass read 8 frames' blocks, which a
+// stride of K + 32 bytes puts in different LDS banks.
+template <bool Q8, int K, int TOPL>
+struct SelLds {
+    static constexpr int QCAP = 16 * 4 * TOPL;
+    static constexpr int XQS = K + 32;
+    alignas(16) int8_t q_xq[Q8 ? 16 * XQS : 16];
+    float q_xd[Q8 ? 16 * (K / 32) : 1];
+    int32_t q_n[QCAP], q_f[QCAP];
+    float q_v[QCAP], q_x2[16];
+};
+
+// Certificate, exact re-ranking, outputs and residual update of one group of
+// 16 frames (m_base ...) in one wave, 4 lanes per frame (the sweep's lane
+// layout): top / taul are the lane's merged keys and the bound of the keys it
+// dropped, nx2 / nd2 / nxx2 the frame's |x~|^2, |x - x~|^2, |x|^2.  Frames
+// the certificate cannot settle go to a.fail_list for the refine pass, or,
+// with `speculate`, take the best exactly evaluated candidate (outputs and
+// residual update as if certified) and are listed in a.spec_list as
+// (frame, stage) for the exact verification after the cascade.
 template <int RECIPE, bool Q8, int KS, int TOPL>
-__global__ __launch_bounds__(kThreads) void euclid_select_kernel(StageArgs a) {
+__device__ void select_group(const StageArgs &a, int64_t m_base, const float (&top_in)[TOPL], float taul_in,
+                             float nx2_in, float nd2_in, float nxx2_in, SelLds<Q8, KS * 32, TOPL> &sl,
+                             bool speculate) {
     constexpr int K = KS * 32;
     constexpr int FG = 1;
     const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x / kWave;
     const int col = lane & 15;
     const int kq = lane >> 4;
-    const int64_t m_base = (static_cast<int64_t>(blockIdx.x) * kWaves + wave) * 16;
-    // Waves past the last frame group leave at once (no block barrier
-    // follows; the exact-evaluation queues are per wave).
-    if (m_base >= a.M) return;
     const int N = a.N;
     int lbits = 0;
     while ((1 << lbits) < N / 4) ++lbits;
     const unsigned kmask = (1u << lbits) - 1u;
-
-    // Merge the lane's key lists of every split.  tau_l bounds every key the
-    // lane dropped, in the sweep (each split's TOPL-th key) or here.
-    const int64_t ngroups = (a.M + 15) / 16;
-    const int64_t gi = m_base / 16;
-    float top[FG][TOPL], taul[FG];
+    float top[FG][TOPL], taul[FG], nx2[FG], nd2[FG], nxx2[FG];
 #pragma unroll
-    for (int j = 0; j < TOPL; ++j) top[0][j] = -INFINITY;
-    taul[0] = -INFINITY;
-    for (int sp = 0; sp < a.nsplit; ++sp) {
-#pragma unroll
-        for (int j = 0; j < TOPL; ++j) {
-            const float key = a.keys[((static_cast<int64_t>(sp) * ngroups + gi) * TOPL + j) * kWave + lane];
-            if (j == TOPL - 1) taul[0] = fmaxf(taul[0], key);
-#pragma unroll
-            for (int i = TOPL - 1; i > 0; --i) top[0][i] = __builtin_amdgcn_fmed3f(top[0][i - 1], top[0][i], key);
-            top[0][0] = __builtin_amdgcn_fmed3f(top[0][0], key, 3.40282347e38f);
-        }
-    }
-    taul[0] = fmaxf(taul[0], top[0][TOPL - 1]);
-    float nx2[FG], nd2[FG], nxx2[FG];
-    {
-        const int64_t m = m_base + col;
-        const int64_t mc = m < a.M ? m : a.M - 1;
-        nx2[0] = a.norms[mc];
-        nd2[0] = a.norms[a.M + mc];
-        nxx2[0] = a.norms[2 * a.M + mc];
-    }
+    for (int j = 0; j < TOPL; ++j) top[0][j] = top_in[j];
+    taul[0] = taul_in;
+    nx2[0] = nx2_in;
+    nd2[0] = nd2_in;
+    nxx2[0] = nxx2_in;
 
     // ---- phase 2: per-frame certificate and exact re-ranking ----
     // 2a bounds and candidates per frame; 2b the frames' |x|^2 (Higgs);
@@ -946,21 +968,13 @@ __global__ __launch_bounds__(kThreads) void euclid_select_kernel(StageArgs a) {
     const int Tk = a.topk > 0 ? a.topk : 1;
     const int Tsel = a.topk > 0 ? a.topk + 1 : 1;
     const bool want_value = a.dist != nullptr || a.topk > 0;
-    constexpr int QCAP = FG * 16 * 4 * TOPL;
-    __shared__ int32_t q_n_s[kWaves][QCAP], q_f_s[kWaves][QCAP];
-    __shared__ float q_v_s[kWaves][QCAP], q_x2_s[kWaves][FG * 16];
-    // Q8_0 blocks of the frames, XQS bytes apart: the 8 lane groups of a
-    // pass read 8 frames' blocks, which a stride of K + 32 bytes puts in
-    // different LDS banks.
-    constexpr int XQS = K + 32;
-    __shared__ __align__(16) int8_t q_xq_s[kWaves][Q8 ? 16 * XQS : 4];
-    __shared__ float q_xd_s[kWaves][Q8 ? 16 * (K / 32) : 1];
-    int32_t *q_n = q_n_s[wave];
-    int32_t *q_f = q_f_s[wave];
-    float *q_v = q_v_s[wave];
-    float *q_x2 = q_x2_s[wave];
-    int8_t *q_xq = q_xq_s[wave];
-    float *q_xd = q_xd_s[wave];
+    constexpr int XQS = SelLds<Q8, K, TOPL>::XQS;
+    int32_t *q_n = sl.q_n;
+    int32_t *q_f = sl.q_f;
+    float *q_v = sl.q_v;
+    float *q_x2 = sl.q_x2;
+    int8_t *q_xq = sl.q_xq;
+    float *q_xd = sl.q_xd;
 
     float Eg[FG], taug[FG], best0g[FG];
     bool okg[FG], needg[FG];
@@ -1328,20 +1342,37 @@ __global__ __launch_bounds__(kThreads) void euclid_select_kernel(StageArgs a) {
             win_code[g] = n;
             ok = ok && n < N;
         }
-        win_ok[g] = ok;
+        if (speculate) {
+            // an uncertified frame continues with the best evaluated code
+            const int w = win_code[g];
+            win_code[g] = w >= 0 && w < N ? w : 0;
+            if (a.misspeculate) {
+                // test hook: the verification and fix-up see every frame,
+                // each continued with a code that is not its best
+                ok = false;
+                win_code[g] = win_code[g] + 1 < N ? win_code[g] + 1 : 0;
+            }
+        }
+        win_ok[g] = ok || (speculate && live);
 
         if (kq == 0 && live) {
-            if (!ok) {
+            if (!ok && !speculate) {
                 const int slot = atomicAdd(a.fail_count, 1);
                 a.fail_list[slot] = static_cast<int32_t>(m);
             } else {
+                if (!ok) {
+                    atomicAdd(a.fail_count, 1);
+                    const int slot = atomicAdd(a.spec_count, 1);
+                    a.spec_list[2 * slot] = static_cast<int32_t>(m);
+                    a.spec_list[2 * slot + 1] = a.s;
+                }
                 a.idx[m * a.Q + a.s] = win_code[g];
                 if (a.dist) {
                     const float v = sel_v[0];   // the argmax's value (ties share it)
                     a.dist[m * a.Q + a.s] = RECIPE == DIRECT ? v : -v;
                 }
                 for (int r = 0; r < a.topk; ++r) {
-                    a.topk_idx[(m * a.Q + a.s) * a.topk + r] = sel_n[r];
+                    a.topk_idx[(m * a.Q + a.s) * a.topk + r] = sel_n[r] < 0 ? 0 : sel_n[r];
                     a.topk_dist[(m * a.Q + a.s) * a.topk + r] = RECIPE == DIRECT ? sel_v[r] : -sel_v[r];
                 }
             }
@@ -1406,6 +1437,45 @@ __global__ __launch_bounds__(kThreads) void euclid_select_kernel(StageArgs a) {
             }
         }
     }
+}
+
+
+// Certificate, exact re-ranking and residual update of one stage.  A wave
+// takes 16 frames (4 lanes per frame, the sweep's lane layout), merges each
+// lane's key lists of all code splits and applies the certificate; the
+// frames it cannot settle go to the refine pass.
+template <int RECIPE, bool Q8, int KS, int TOPL>
+__global__ __launch_bounds__(kThreads) void euclid_select_kernel(StageArgs a) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int col = lane & 15;
+    const int64_t m_base = (static_cast<int64_t>(blockIdx.x) * kWaves + wave) * 16;
+    // Waves past the last frame group leave at once (no block barrier
+    // follows; the exact-evaluation queues are per wave).
+    if (m_base >= a.M) return;
+    // Merge the lane's key lists of every split.  tau_l bounds every key the
+    // lane dropped, in the sweep (each split's TOPL-th key) or here.
+    const int64_t ngroups = (a.M + 15) / 16;
+    const int64_t gi = m_base / 16;
+    float top[TOPL], taul = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < TOPL; ++j) top[j] = -INFINITY;
+    for (int sp = 0; sp < a.nsplit; ++sp) {
+#pragma unroll
+        for (int j = 0; j < TOPL; ++j) {
+            const float key = a.keys[((static_cast<int64_t>(sp) * ngroups + gi) * TOPL + j) * kWave + lane];
+            if (j == TOPL - 1) taul = fmaxf(taul, key);
+#pragma unroll
+            for (int i = TOPL - 1; i > 0; --i) top[i] = __builtin_amdgcn_fmed3f(top[i - 1], top[i], key);
+            top[0] = __builtin_amdgcn_fmed3f(top[0], key, 3.40282347e38f);
+        }
+    }
+    taul = fmaxf(taul, top[TOPL - 1]);
+    const int64_t m = m_base + col;
+    const int64_t mc = m < a.M ? m : a.M - 1;
+    __shared__ SelLds<Q8, KS * 32, TOPL> sl[kWaves];
+    select_group<RECIPE, Q8, KS, TOPL>(a, m_base, top, taul, a.norms[mc], a.norms[a.M + mc], a.norms[2 * a.M + mc],
+                                       sl[wave], false);
 }
 
 // ------------------------------------------------------------- exact scan
@@ -1738,28 +1808,332 @@ __device__ inline float scan_sum_squares(const float *__restrict__ x, int K) {
     }
 }
 
+// Shared state of the exact scan's selection for one frame.
+struct ScanSh {
+    float rv[kScanChunk];
+    int heap_n[4];
+    float heap_v[4];
+    int o_code, o_sel_n[4];
+    float o_code_v, o_sel_v[4], o_x2;
+    uint64_t w_top[kScanThreads / kWave][5], w_win[kScanThreads / kWave], o_key[5], o_win;
+    int w_nan[kScanThreads / kWave];
+};
+
+// The exact scan's selection for one frame, by a whole kScanThreads block:
+// every code's recipe value (from sv when pre, else computed from the frame
+// xs in LDS, with x2 its sum_rows(x*x) and xq / xd its Q8_0 blocks) and the
+// reference's selection rules; the winner and the top-k land in
+// sh.o_code / o_code_v / o_sel_n / o_sel_v.
+template <int RECIPE, bool Q8, int KS>
+__device__ void scan_select(const StageArgs &a, int K, bool pre, const float *sv, const float *xs, const int8_t *xq,
+                            const float *xd, float x2, ScanSh &sh) {
+    constexpr int ST = kScanThreads;
+    constexpr int PT = kScanChunk / ST;   // values per thread of a one-chunk frame
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int ktop = a.topk;
+    float *rv = sh.rv;
+    int *heap_n = sh.heap_n;
+    float *heap_v = sh.heap_v;
+    int &o_code = sh.o_code;
+    int *o_sel_n = sh.o_sel_n;
+    float &o_code_v = sh.o_code_v;
+    float *o_sel_v = sh.o_sel_v;
+    uint64_t(*w_top)[5] = sh.w_top;
+    uint64_t *w_win = sh.w_win;
+    uint64_t *o_key = sh.o_key;
+    uint64_t &o_win = sh.o_win;
+    int *w_nan = sh.w_nan;
+    auto value = [&](int n) -> float { return pre ? sv[n] : scan_value<RECIPE, Q8, KS>(a, K, xs, n, x2, xq, xd); };
+    // The frame's values.  Codes that fit one chunk (N <= kScanChunk):
+    // PT per thread in registers (code tid + j * ST), and all in rv in
+    // code order; more codes: read from the grid's values (pre), or
+    // computed chunk by chunk by the walk below.
+    const bool have_all = pre || a.N <= kScanChunk;
+    const bool in_regs = a.N <= kScanChunk;
+    float vr[PT];
+    if (in_regs && pre) {
+#pragma unroll
+        for (int j = 0; j < PT; ++j) {
+            const int i = tid + j * ST;
+            vr[j] = i < a.N ? sv[i] : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < PT; ++j)
+            if (tid + j * ST < a.N) rv[tid + j * ST] = vr[j];
+    } else if (in_regs) {
+#pragma unroll 4
+        for (int i = tid; i < a.N; i += ST) rv[i] = scan_value<RECIPE, Q8, KS>(a, K, xs, i, x2, xq, xd);
+    }
+    __syncthreads();
+    if (in_regs && !pre) {
+#pragma unroll
+        for (int j = 0; j < PT; ++j) {
+            const int i = tid + j * ST;
+            vr[j] = i < a.N ? rv[i] : 0.0f;
+        }
+    }
+    // Parallel selection, unless a ggml recipe meets a NaN (its argmax
+    // restarts there) or the values are not all at hand: the winner and
+    // the best L codes in rank_key order.  Each wave takes L rounds of a
+    // wave-wide max over its keys below the previous round's, then wave
+    // 0 does the same over the waves' lists.
+    bool slow = !have_all;
+    bool tie = false;
+    if (have_all) {
+        const int L = RECIPE == DIRECT ? (ktop > 1 ? ktop : 1) : ktop + 1;
+        const int wv = tid / kWave;
+        bool nan = false;
+        uint64_t kr[PT];
+#pragma unroll
+        for (int j = 0; j < PT; ++j) {
+            const bool ok = in_regs && tid + j * ST < a.N;
+            nan |= ok && vr[j] != vr[j];
+            kr[j] = ok ? rank_key<RECIPE>(vr[j], tid + j * ST) : 0;
+        }
+        uint64_t prev = ~0ull;
+        for (int r = 0; r < L; ++r) {
+            const bool want_w = RECIPE != DIRECT && r == 0;   // ggml argmax: the largest value, its last index
+            uint64_t best = 0, wb = 0;
+            auto consider = [&](uint64_t k, int i) {
+                best = k < prev && k > best ? k : best;
+                const uint64_t w = (k & 0xFFFFFFFF00000000ull) | static_cast<uint32_t>(i);
+                if (want_w && k != 0 && w > wb) wb = w;
+            };
+            if (in_regs) {
+#pragma unroll
+                for (int j = 0; j < PT; ++j) consider(kr[j], tid + j * ST);
+            } else {
+                for (int i = tid; i < a.N; i += ST) {
+                    const float v = sv[i];
+                    nan |= v != v;
+                    consider(rank_key<RECIPE>(v, i), i);
+                }
+            }
+            best = wave_max_u64(best);
+            if (lane == 0) w_top[wv][r] = best;
+            if (want_w) {
+                wb = wave_max_u64(wb);
+                if (lane == 0) w_win[wv] = wb;
+            }
+            prev = best;
+        }
+        if (RECIPE != DIRECT) {
+            const bool wnan = __any(nan);
+            if (lane == 0) w_nan[wv] = wnan ? 1 : 0;
+        }
+        __syncthreads();
+        if (RECIPE != DIRECT)
+            for (int w = 0; w < ST / kWave; ++w) slow |= w_nan[w] != 0;
+        if (!slow) {
+            if (wv == 0) {
+                const uint64_t c = lane < (ST / kWave) * L ? w_top[lane / L][lane % L] : 0;
+                uint64_t pv = ~0ull;
+                for (int r = 0; r < L; ++r) {
+                    const uint64_t b = wave_max_u64(c < pv ? c : 0);
+                    if (lane == 0) o_key[r] = b;
+                    pv = b;
+                }
+                if (RECIPE != DIRECT && lane == 0) {
+                    uint64_t w = w_win[0];
+                    for (int q = 1; q < ST / kWave; ++q) w = w_win[q] > w ? w_win[q] : w;
+                    o_win = w;
+                }
+            }
+            __syncthreads();
+            // ggml_top_k keeps, of codes tied at the k-th place, what its
+            // heap leaves: replayed below
+            tie = RECIPE != DIRECT && ktop > 0 && o_key[ktop] != 0 && (o_key[ktop - 1] >> 32) == (o_key[ktop] >> 32);
+            if (tid == 0) {
+                // an index below 0 stands for no code (key 0: DIRECT with
+                // every value NaN, or fewer codes than places).  Tested on
+                // the index, not as key == 0: ROCm 7.2's compiler lowered
+                // (key == 0 ? 0 : key_index(key)) here to a scalar select
+                // on the flag of the preceding s_not_b32, i.e. always 0.
+                const int n = RECIPE == DIRECT ? key_index(o_key[0]) : static_cast<int>(static_cast<uint32_t>(o_win));
+                o_code = n < 0 ? 0 : n;
+                o_code_v = n < 0 ? INFINITY : (in_regs ? rv[n] : sv[n]);
+                if (!tie)
+                    for (int r = 0; r < ktop; ++r) {
+                        const int q = key_index(o_key[r]);
+                        o_sel_n[r] = q < 0 ? 0 : q;
+                        o_sel_v[r] = q < 0 ? INFINITY : (in_regs ? rv[q] : sv[q]);
+                    }
+            }
+            if (tie && wv == 0) {
+                // rv (LDS) and sv (global) in separate instances, so that
+                // each reads through its own address space
+                switch (ktop) {
+                    case 1: in_regs ? heap_walk<1>(rv, a.N, heap_n, heap_v) : heap_walk<1>(sv, a.N, heap_n, heap_v); break;
+                    case 2: in_regs ? heap_walk<2>(rv, a.N, heap_n, heap_v) : heap_walk<2>(sv, a.N, heap_n, heap_v); break;
+                    case 3: in_regs ? heap_walk<3>(rv, a.N, heap_n, heap_v) : heap_walk<3>(sv, a.N, heap_n, heap_v); break;
+                    default: in_regs ? heap_walk<4>(rv, a.N, heap_n, heap_v) : heap_walk<4>(sv, a.N, heap_n, heap_v); break;
+                }
+            }
+        }
+    }
+    // The walk (a ggml recipe with a NaN, or values computed chunk by
+    // chunk): wave 0 replays the reference's sequential selection.
+    // wave 0's running selection state (uniform across its lanes)
+    float mx = RECIPE == DIRECT ? INFINITY : -INFINITY;
+    int id = 0;
+    float root = 0.0f;   // heap root (ggml recipes) / k-th kept distance (DIRECT)
+    int kept = 0;        // DIRECT: entries in the kept list
+    for (int base = 0; base < (slow ? a.N : 0); base += kScanChunk) {
+        const int len = min(kScanChunk, a.N - base);
+        // unrolled so that the row loads of several codes are in flight at
+        // once; a single chunk is in rv since pass 1
+        if (a.N > kScanChunk) {
+#pragma unroll 4
+            for (int i = tid; i < len; i += ST) rv[i] = value(base + i);
+        }
+        __syncthreads();
+        if (tid < kWave) {
+            for (int c0 = 0; c0 < len; c0 += kWave) {
+                const int i = c0 + lane;
+                const bool in = i < len;
+                const float v = in ? rv[i] : 0.0f;
+                if (RECIPE == DIRECT) {
+                    // first index of the minimum: strict <, NaN never wins
+                    // (a chunk with no code below the running minimum is
+                    // skipped after one ballot)
+                    float cm = INFINITY;
+                    if (__any(in && v < mx)) {
+                        cm = in ? v : INFINITY;
+#pragma unroll
+                        for (int off = 1; off < kWave; off <<= 1) cm = fminf(cm, __shfl_xor(cm, off));
+                    }
+                    if (cm < mx) {
+                        const unsigned long long eq = __ballot(in && v == cm);
+                        const int first = __ffsll(static_cast<long long>(eq)) - 1;
+                        mx = cm;
+                        id = base + c0 + first;
+                    }
+                    if (ktop > 0) {
+                        // the k smallest (value, index): insert, in code
+                        // order, every code that ranks before the k-th
+                        int from = 0;
+                        while (true) {
+                            const bool cand = in && lane >= from && v == v &&
+                                              (kept < ktop || v < root);
+                            const unsigned long long take = __ballot(cand);
+                            if (take == 0) break;
+                            const int f = __ffsll(static_cast<long long>(take)) - 1;
+                            const float vf = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), f));
+                            if (lane == 0) {
+                                int p = kept < ktop ? kept : ktop - 1;
+                                while (p > 0 && vf < heap_v[p - 1]) {
+                                    heap_v[p] = heap_v[p - 1];
+                                    heap_n[p] = heap_n[p - 1];
+                                    --p;
+                                }
+                                heap_v[p] = vf;
+                                heap_n[p] = base + c0 + f;
+                            }
+                            __builtin_amdgcn_wave_barrier();
+                            kept = min(kept + 1, ktop);
+                            root = heap_v[ktop - 1];
+                            from = f + 1;
+                        }
+                    }
+                    continue;
+                }
+                // ggml_vec_argmax_f32
+                const bool nan_chunk = __any(in && v != v) || mx != mx;
+                if (nan_chunk) {
+                    const int cl = min(kWave, len - c0);
+                    for (int t = 0; t < cl; ++t) {
+                        const float vt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), t));
+                        mx = mx > vt ? mx : vt;
+                        if (mx == vt) id = base + c0 + t;
+                    }
+                } else if (__any(in && v >= mx)) {
+                    // only a chunk with a code >= the running max can
+                    // move the argmax (MAX keeps a later equal element)
+                    float cm = in ? v : -INFINITY;
+#pragma unroll
+                    for (int off = 1; off < kWave; off <<= 1) cm = fmaxf(cm, __shfl_xor(cm, off));
+                    const unsigned long long eq = __ballot(in && v == cm);
+                    if (eq != 0 && !(mx > cm)) {
+                        const int last = 63 - __clzll(static_cast<long long>(eq));
+                        mx = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), last));
+                        id = base + c0 + last;
+                    }
+                }
+                if (ktop > 0) {
+                    // ggml_top_k: the first ktop codes build the heap,
+                    // a later code replaces the root if strictly better
+                    for (int t = 0; t < kWave && base + c0 + t < ktop; ++t) {
+                        const int n_t = base + c0 + t;
+                        const float vt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), t));
+                        if (lane == 0) {
+                            heap_n[n_t] = n_t;
+                            heap_v[n_t] = vt;
+                            if (n_t == ktop - 1 && ktop >= 2)
+                                for (int par = (ktop - 2) / 2;; --par) {
+                                    heap_adjust(heap_n, heap_v, par, ktop, heap_n[par], heap_v[par]);
+                                    if (par == 0) break;
+                                }
+                        }
+                        __builtin_amdgcn_wave_barrier();
+                        if (n_t == ktop - 1) root = heap_v[0];
+                    }
+                    int from = 0;   // lanes before `from` are done
+                    while (true) {
+                        const unsigned long long take =
+                            __ballot(in && lane >= from && base + i >= ktop && v > root);
+                        if (take == 0) break;
+                        const int f = __ffsll(static_cast<long long>(take)) - 1;
+                        const float vf = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), f));
+                        if (lane == 0) heap_adjust(heap_n, heap_v, 0, ktop, base + c0 + f, vf);
+                        __builtin_amdgcn_wave_barrier();
+                        root = heap_v[0];
+                        from = f + 1;
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
+    if (tid == 0 && (slow || tie)) {
+        if (slow) {
+            o_code = id;
+            o_code_v = mx;
+        }
+        // the kept set, best first, ties by index
+        int used[4] = {-1, -1, -1, -1};
+        const int nk = RECIPE == DIRECT ? kept : ktop;
+        for (int r = 0; r < ktop; ++r) {
+            int b = -1;
+            for (int q = 0; q < nk; ++q) {
+                bool u = false;
+                for (int t = 0; t < r; ++t) u |= used[t] == q;
+                if (!u && (b < 0 || topk_before<RECIPE>(heap_v[q], heap_n[q], heap_v[b], heap_n[b]))) b = q;
+            }
+            used[r] = b;
+            o_sel_n[r] = b < 0 ? 0 : heap_n[b];
+            o_sel_v[r] = b < 0 ? INFINITY : heap_v[b];
+        }
+    }
+    __syncthreads();
+}
+
 template <int RECIPE, bool Q8, int KS>
 __global__ __launch_bounds__(kScanThreads) void euclid_exact_scan_kernel(StageArgs a) {
     // KS = 0: the width is a run-time argument and every frame of the batch
     // is scanned (no frame list, no spread values)
     const int K = KS != 0 ? KS * 32 : a.K;
     constexpr int ST = kScanThreads;
-    constexpr int PT = kScanChunk / ST;   // values per thread of a one-chunk frame
     extern __shared__ __align__(16) unsigned char lds[];
     float *xs = reinterpret_cast<float *>(lds);                         // [K]
     int8_t *xq = reinterpret_cast<int8_t *>(xs + K);                    // [K]
     float *xd = reinterpret_cast<float *>(xq + K);                      // [K/32]
-    __shared__ float rv[kScanChunk];
-    __shared__ int heap_n[4];
-    __shared__ float heap_v[4];
-    __shared__ int o_code, o_sel_n[4];
-    __shared__ float o_code_v, o_sel_v[4], o_x2;
-    __shared__ uint64_t w_top[ST / kWave][5], w_win[ST / kWave], o_key[5], o_win;
-    __shared__ int w_nan[ST / kWave];
+    __shared__ ScanSh sh;
+    int &o_code = sh.o_code;
+    int *o_sel_n = sh.o_sel_n;
+    float &o_code_v = sh.o_code_v, *o_sel_v = sh.o_sel_v, &o_x2 = sh.o_x2;
     const int tid = threadIdx.x;
-    const int lane = tid & (kWave - 1);
     const int count = KS != 0 ? *a.fail_count : static_cast<int>(a.M);
-    const int ktop = a.topk;
     // pre: up to a.scap frames, whose code values the grid computes first
     // (one (frame, kScanThreads-code chunk) item per block and pass); the
     // block that completes a frame's last chunk selects for it
@@ -1777,278 +2151,7 @@ __global__ __launch_bounds__(kScanThreads) void euclid_exact_scan_kernel(StageAr
         }
         const float x2 = pre ? 0.0f : o_x2;
         const float *sv = pre ? a.svals + static_cast<int64_t>(slot) * a.N : nullptr;
-        auto value = [&](int n) -> float { return pre ? sv[n] : scan_value<RECIPE, Q8, KS>(a, K, xs, n, x2, xq, xd); };
-
-        // The frame's values.  Codes that fit one chunk (N <= kScanChunk):
-        // PT per thread in registers (code tid + j * ST), and all in rv in
-        // code order; more codes: read from the grid's values (pre), or
-        // computed chunk by chunk by the walk below.
-        const bool have_all = pre || a.N <= kScanChunk;
-        const bool in_regs = a.N <= kScanChunk;
-        float vr[PT];
-        if (in_regs && pre) {
-#pragma unroll
-            for (int j = 0; j < PT; ++j) {
-                const int i = tid + j * ST;
-                vr[j] = i < a.N ? sv[i] : 0.0f;
-            }
-#pragma unroll
-            for (int j = 0; j < PT; ++j)
-                if (tid + j * ST < a.N) rv[tid + j * ST] = vr[j];
-        } else if (in_regs) {
-#pragma unroll 4
-            for (int i = tid; i < a.N; i += ST) rv[i] = scan_value<RECIPE, Q8, KS>(a, K, xs, i, x2, xq, xd);
-        }
-        __syncthreads();
-        if (in_regs && !pre) {
-#pragma unroll
-            for (int j = 0; j < PT; ++j) {
-                const int i = tid + j * ST;
-                vr[j] = i < a.N ? rv[i] : 0.0f;
-            }
-        }
-        // Parallel selection, unless a ggml recipe meets a NaN (its argmax
-        // restarts there) or the values are not all at hand: the winner and
-        // the best L codes in rank_key order.  Each wave takes L rounds of a
-        // wave-wide max over its keys below the previous round's, then wave
-        // 0 does the same over the waves' lists.
-        bool slow = !have_all;
-        bool tie = false;
-        if (have_all) {
-            const int L = RECIPE == DIRECT ? (ktop > 1 ? ktop : 1) : ktop + 1;
-            const int wv = tid / kWave;
-            bool nan = false;
-            uint64_t kr[PT];
-#pragma unroll
-            for (int j = 0; j < PT; ++j) {
-                const bool ok = in_regs && tid + j * ST < a.N;
-                nan |= ok && vr[j] != vr[j];
-                kr[j] = ok ? rank_key<RECIPE>(vr[j], tid + j * ST) : 0;
-            }
-            uint64_t prev = ~0ull;
-            for (int r = 0; r < L; ++r) {
-                const bool want_w = RECIPE != DIRECT && r == 0;   // ggml argmax: the largest value, its last index
-                uint64_t best = 0, wb = 0;
-                auto consider = [&](uint64_t k, int i) {
-                    best = k < prev && k > best ? k : best;
-                    const uint64_t w = (k & 0xFFFFFFFF00000000ull) | static_cast<uint32_t>(i);
-                    if (want_w && k != 0 && w > wb) wb = w;
-                };
-                if (in_regs) {
-#pragma unroll
-                    for (int j = 0; j < PT; ++j) consider(kr[j], tid + j * ST);
-                } else {
-                    for (int i = tid; i < a.N; i += ST) {
-                        const float v = sv[i];
-                        nan |= v != v;
-                        consider(rank_key<RECIPE>(v, i), i);
-                    }
-                }
-                best = wave_max_u64(best);
-                if (lane == 0) w_top[wv][r] = best;
-                if (want_w) {
-                    wb = wave_max_u64(wb);
-                    if (lane == 0) w_win[wv] = wb;
-                }
-                prev = best;
-            }
-            if (RECIPE != DIRECT) {
-                const bool wnan = __any(nan);
-                if (lane == 0) w_nan[wv] = wnan ? 1 : 0;
-            }
-            __syncthreads();
-            if (RECIPE != DIRECT)
-                for (int w = 0; w < ST / kWave; ++w) slow |= w_nan[w] != 0;
-            if (!slow) {
-                if (wv == 0) {
-                    const uint64_t c = lane < (ST / kWave) * L ? w_top[lane / L][lane % L] : 0;
-                    uint64_t pv = ~0ull;
-                    for (int r = 0; r < L; ++r) {
-                        const uint64_t b = wave_max_u64(c < pv ? c : 0);
-                        if (lane == 0) o_key[r] = b;
-                        pv = b;
-                    }
-                    if (RECIPE != DIRECT && lane == 0) {
-                        uint64_t w = w_win[0];
-                        for (int q = 1; q < ST / kWave; ++q) w = w_win[q] > w ? w_win[q] : w;
-                        o_win = w;
-                    }
-                }
-                __syncthreads();
-                // ggml_top_k keeps, of codes tied at the k-th place, what its
-                // heap leaves: replayed below
-                tie = RECIPE != DIRECT && ktop > 0 && o_key[ktop] != 0 && (o_key[ktop - 1] >> 32) == (o_key[ktop] >> 32);
-                if (tid == 0) {
-                    // an index below 0 stands for no code (key 0: DIRECT with
-                    // every value NaN, or fewer codes than places).  Tested on
-                    // the index, not as key == 0: ROCm 7.2's compiler lowered
-                    // (key == 0 ? 0 : key_index(key)) here to a scalar select
-                    // on the flag of the preceding s_not_b32, i.e. always 0.
-                    const int n = RECIPE == DIRECT ? key_index(o_key[0]) : static_cast<int>(static_cast<uint32_t>(o_win));
-                    o_code = n < 0 ? 0 : n;
-                    o_code_v = n < 0 ? INFINITY : (in_regs ? rv[n] : sv[n]);
-                    if (!tie)
-                        for (int r = 0; r < ktop; ++r) {
-                            const int q = key_index(o_key[r]);
-                            o_sel_n[r] = q < 0 ? 0 : q;
-                            o_sel_v[r] = q < 0 ? INFINITY : (in_regs ? rv[q] : sv[q]);
-                        }
-                }
-                if (tie && wv == 0) {
-                    // rv (LDS) and sv (global) in separate instances, so that
-                    // each reads through its own address space
-                    switch (ktop) {
-                        case 1: in_regs ? heap_walk<1>(rv, a.N, heap_n, heap_v) : heap_walk<1>(sv, a.N, heap_n, heap_v); break;
-                        case 2: in_regs ? heap_walk<2>(rv, a.N, heap_n, heap_v) : heap_walk<2>(sv, a.N, heap_n, heap_v); break;
-                        case 3: in_regs ? heap_walk<3>(rv, a.N, heap_n, heap_v) : heap_walk<3>(sv, a.N, heap_n, heap_v); break;
-                        default: in_regs ? heap_walk<4>(rv, a.N, heap_n, heap_v) : heap_walk<4>(sv, a.N, heap_n, heap_v); break;
-                    }
-                }
-            }
-        }
-        // The walk (a ggml recipe with a NaN, or values computed chunk by
-        // chunk): wave 0 replays the reference's sequential selection.
-        // wave 0's running selection state (uniform across its lanes)
-        float mx = RECIPE == DIRECT ? INFINITY : -INFINITY;
-        int id = 0;
-        float root = 0.0f;   // heap root (ggml recipes) / k-th kept distance (DIRECT)
-        int kept = 0;        // DIRECT: entries in the kept list
-        for (int base = 0; base < (slow ? a.N : 0); base += kScanChunk) {
-            const int len = min(kScanChunk, a.N - base);
-            // unrolled so that the row loads of several codes are in flight at
-            // once; a single chunk is in rv since pass 1
-            if (a.N > kScanChunk) {
-#pragma unroll 4
-                for (int i = tid; i < len; i += ST) rv[i] = value(base + i);
-            }
-            __syncthreads();
-            if (tid < kWave) {
-                for (int c0 = 0; c0 < len; c0 += kWave) {
-                    const int i = c0 + lane;
-                    const bool in = i < len;
-                    const float v = in ? rv[i] : 0.0f;
-                    if (RECIPE == DIRECT) {
-                        // first index of the minimum: strict <, NaN never wins
-                        // (a chunk with no code below the running minimum is
-                        // skipped after one ballot)
-                        float cm = INFINITY;
-                        if (__any(in && v < mx)) {
-                            cm = in ? v : INFINITY;
-#pragma unroll
-                            for (int off = 1; off < kWave; off <<= 1) cm = fminf(cm, __shfl_xor(cm, off));
-                        }
-                        if (cm < mx) {
-                            const unsigned long long eq = __ballot(in && v == cm);
-                            const int first = __ffsll(static_cast<long long>(eq)) - 1;
-                            mx = cm;
-                            id = base + c0 + first;
-                        }
-                        if (ktop > 0) {
-                            // the k smallest (value, index): insert, in code
-                            // order, every code that ranks before the k-th
-                            int from = 0;
-                            while (true) {
-                                const bool cand = in && lane >= from && v == v &&
-                                                  (kept < ktop || v < root);
-                                const unsigned long long take = __ballot(cand);
-                                if (take == 0) break;
-                                const int f = __ffsll(static_cast<long long>(take)) - 1;
-                                const float vf = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), f));
-                                if (lane == 0) {
-                                    int p = kept < ktop ? kept : ktop - 1;
-                                    while (p > 0 && vf < heap_v[p - 1]) {
-                                        heap_v[p] = heap_v[p - 1];
-                                        heap_n[p] = heap_n[p - 1];
-                                        --p;
-                                    }
-                                    heap_v[p] = vf;
-                                    heap_n[p] = base + c0 + f;
-                                }
-                                __builtin_amdgcn_wave_barrier();
-                                kept = min(kept + 1, ktop);
-                                root = heap_v[ktop - 1];
-                                from = f + 1;
-                            }
-                        }
-                        continue;
-                    }
-                    // ggml_vec_argmax_f32
-                    const bool nan_chunk = __any(in && v != v) || mx != mx;
-                    if (nan_chunk) {
-                        const int cl = min(kWave, len - c0);
-                        for (int t = 0; t < cl; ++t) {
-                            const float vt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), t));
-                            mx = mx > vt ? mx : vt;
-                            if (mx == vt) id = base + c0 + t;
-                        }
-                    } else if (__any(in && v >= mx)) {
-                        // only a chunk with a code >= the running max can
-                        // move the argmax (MAX keeps a later equal element)
-                        float cm = in ? v : -INFINITY;
-#pragma unroll
-                        for (int off = 1; off < kWave; off <<= 1) cm = fmaxf(cm, __shfl_xor(cm, off));
-                        const unsigned long long eq = __ballot(in && v == cm);
-                        if (eq != 0 && !(mx > cm)) {
-                            const int last = 63 - __clzll(static_cast<long long>(eq));
-                            mx = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), last));
-                            id = base + c0 + last;
-                        }
-                    }
-                    if (ktop > 0) {
-                        // ggml_top_k: the first ktop codes build the heap,
-                        // a later code replaces the root if strictly better
-                        for (int t = 0; t < kWave && base + c0 + t < ktop; ++t) {
-                            const int n_t = base + c0 + t;
-                            const float vt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), t));
-                            if (lane == 0) {
-                                heap_n[n_t] = n_t;
-                                heap_v[n_t] = vt;
-                                if (n_t == ktop - 1 && ktop >= 2)
-                                    for (int par = (ktop - 2) / 2;; --par) {
-                                        heap_adjust(heap_n, heap_v, par, ktop, heap_n[par], heap_v[par]);
-                                        if (par == 0) break;
-                                    }
-                            }
-                            __builtin_amdgcn_wave_barrier();
-                            if (n_t == ktop - 1) root = heap_v[0];
-                        }
-                        int from = 0;   // lanes before `from` are done
-                        while (true) {
-                            const unsigned long long take =
-                                __ballot(in && lane >= from && base + i >= ktop && v > root);
-                            if (take == 0) break;
-                            const int f = __ffsll(static_cast<long long>(take)) - 1;
-                            const float vf = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), f));
-                            if (lane == 0) heap_adjust(heap_n, heap_v, 0, ktop, base + c0 + f, vf);
-                            __builtin_amdgcn_wave_barrier();
-                            root = heap_v[0];
-                            from = f + 1;
-                        }
-                    }
-                }
-            }
-            __syncthreads();
-        }
-        if (tid == 0 && (slow || tie)) {
-            if (slow) {
-                o_code = id;
-                o_code_v = mx;
-            }
-            // the kept set, best first, ties by index
-            int used[4] = {-1, -1, -1, -1};
-            const int nk = RECIPE == DIRECT ? kept : ktop;
-            for (int r = 0; r < ktop; ++r) {
-                int b = -1;
-                for (int q = 0; q < nk; ++q) {
-                    bool u = false;
-                    for (int t = 0; t < r; ++t) u |= used[t] == q;
-                    if (!u && (b < 0 || topk_before<RECIPE>(heap_v[q], heap_n[q], heap_v[b], heap_n[b]))) b = q;
-                }
-                used[r] = b;
-                o_sel_n[r] = b < 0 ? 0 : heap_n[b];
-                o_sel_v[r] = b < 0 ? INFINITY : heap_v[b];
-            }
-        }
+        scan_select<RECIPE, Q8, KS>(a, K, pre, sv, xs, xq, xd, x2, sh);
         __syncthreads();
         const int code = o_code;
         if (tid == 0) {
@@ -2608,6 +2711,451 @@ __global__ __launch_bounds__(kWave) void euclid_refine_select_kernel(StageArgs a
     }
 }
 
+
+// ------------------------------------------------------------- cascade
+// The residual cascade of every stage in one launch.  A block of kCWaves
+// waves owns kCRows x FG x 16 frames through all stages; per stage it
+//  1. converts its frames' residual to fp16 fragments in registers (wave w
+//     takes row w % kCRows; waves w and w + kCRows hold the same frames);
+//  2. sweeps the stage's codebook through double-buffered LDS chunks, waves
+//     0 .. kCRows-1 taking the even 16-code blocks of each chunk and the
+//     others the odd ones (two waves per SIMD share every staged chunk);
+//  3. merges the two halves' keys and runs the select of the block's
+//     kCRows x FG groups over its waves: certificate, exact re-ranking,
+//     outputs and the residual update, in place.  A frame the certificate
+//     cannot settle continues with its best exactly evaluated code and is
+//     listed for the exact verification that follows the cascade
+//     (euclid_verify_kernel); a frame whose guess was wrong is recomputed
+//     from that stage on by euclid_fixup_kernel.
+// No block depends on another: the launch needs no grid synchronisation,
+// and the stages of a block follow each other with block barriers only.
+constexpr int kCWaves = 8;
+constexpr int kCThreads = kCWaves * kWave;
+constexpr int kCRows = kCWaves / 2;
+
+template <int KS>
+struct CTile {
+    using T = Tile<KS>;
+    static constexpr int BUFB = T::CHUNKB + kCThreads * 4;    // chunk + one |c|^2/2 slot per thread
+    static constexpr int STAGE16 = T::CHUNKB / 16 / kCThreads;
+    static constexpr int SWEEP = 2 * BUFB;
+};
+
+constexpr int cmax3(int a, int b, int c) { return a > b ? (a > c ? a : c) : (b > c ? b : c); }
+
+// Dynamic LDS of the cascade kernel: a phase region (the chunk buffers while
+// sweeping; then the second half's keys; then the waves' select queues) and
+// the merged keys (TOPL keys and the dropped-key bound per lane) and frame
+// norms of every group, which the select phase reads.
+template <int KS, int FG, int TOPL, bool Q8>
+struct CLayout {
+    static constexpr int K = KS * 32;
+    static constexpr int G = kCRows * FG;
+    static constexpr int SEL = kCWaves * static_cast<int>(sizeof(SelLds<Q8, K, TOPL>));
+    static constexpr int MERGE = G * TOPL * kWave * 4;
+    static constexpr int PHASE = (cmax3(CTile<KS>::SWEEP, SEL, MERGE) + 15) / 16 * 16;
+    static constexpr int SELK = G * (TOPL + 1) * kWave * 4;
+    static constexpr int NRM = G * 3 * 16 * 4;
+    static constexpr int BYTES = PHASE + SELK + NRM;
+};
+
+// StageArgs of stage s of a cascade.
+__device__ inline StageArgs cascade_stage(const CascadeArgs &c, int s, int K) {
+    StageArgs a = c.a;
+    const int64_t NK = static_cast<int64_t>(a.N) * K;
+    a.s = s;
+    a.cbh += s * NK;
+    a.nhh += static_cast<int64_t>(s) * a.N;
+    a.cbf += s * NK;
+    a.bias += static_cast<int64_t>(s) * a.N;
+    a.e2 += static_cast<int64_t>(s) * a.N;
+    if (a.q8) {
+        a.q8 += s * NK;
+        a.q8d += s * (NK / 32);
+    }
+    a.cmax = c.bounds[3 * s];
+    a.dcmax = c.bounds[3 * s + 1];
+    a.chmax = c.bounds[3 * s + 2];
+    a.xin = s == 0 ? c.x0 : c.work;
+    a.xout = (s + 1 < a.Q || c.write_last) ? c.work : nullptr;
+    a.fail_count = c.counts + (s % 64);
+    return a;
+}
+
+template <int RECIPE, bool Q8, int KS, int FG, int TOPL>
+__global__ __launch_bounds__(kCThreads, 1) void euclid_cascade_kernel(CascadeArgs c) {
+    using T = Tile<KS>;
+    using CT = CTile<KS>;
+    using LY = CLayout<KS, FG, TOPL, Q8>;
+    using MX = Mx;
+    constexpr int K = T::K;
+    constexpr int BPC = T::CC / 16;
+    constexpr int NB = BPC / 2;   // blocks of a chunk per half
+    static_assert(BPC % 2 == 0, "the halves take alternate 16-code blocks");
+    static_assert(T::CHUNKB % (16 * kCThreads) == 0, "a chunk splits evenly over the block");
+    extern __shared__ __align__(16) unsigned char lds[];
+    float *selk = reinterpret_cast<float *>(lds + LY::PHASE);             // [G][TOPL + 1][64]
+    float *nrm = reinterpret_cast<float *>(lds + LY::PHASE + LY::SELK);   // [G][3][16]
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);   // uniform: addresses stay scalar
+    const int row = wave % kCRows, half = wave / kCRows;
+    const int col = lane & 15, kq = lane >> 4;
+    const int64_t M = c.a.M;
+    const int N = c.a.N;
+    const int64_t m_tile = static_cast<int64_t>(blockIdx.x) * (LY::G * 16);
+    if (m_tile >= M) return;   // block-uniform
+    const int64_t m_row = m_tile + row * (FG * 16);
+    for (int i = threadIdx.x; i < LY::G * 16; i += kCThreads)
+        if (m_tile + i < M) c.bad_stage[m_tile + i] = c.a.Q;
+
+    int lbits = 0;   // bits of the lane-local code index (N/4 codes per lane)
+    while ((1 << lbits) < N / 4) ++lbits;
+    const unsigned kmask = (1u << lbits) - 1u;
+    unsigned vkeep;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(vkeep) : "s"(~kmask));
+    const int nch = N / T::CC;
+    constexpr int R = KS % 4 == 0 ? 4 : 2;
+    constexpr int L = R - 1;
+    constexpr int PPB = (CT::STAGE16 + NB - 1) / NB;   // staged pieces per block
+    constexpr int kWaitLoads = 0x0070;                 // s_waitcnt vmcnt(0) lgkmcnt(0)
+    const int hsrc = threadIdx.x < T::CC ? threadIdx.x : 0;
+
+    for (int s = 0; s < c.a.Q; ++s) {
+        const StageArgs a = cascade_stage(c, s, K);
+        // ---- the frames' residual -> fp16 fragments, rounding norms ----
+        u32x4 xb[FG][KS];
+        float nx2[FG], nd2[FG], nxx2[FG];
+#pragma unroll
+        for (int g = 0; g < FG; ++g) {
+            const int64_t m = m_row + g * 16 + col;
+            const int64_t mc = m < M ? m : M - 1;
+            const float *xr = a.xin + mc * K;
+            float sx = 0.0f, sd = 0.0f, sxx = 0.0f;
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                const f32x4 lo = *reinterpret_cast<const f32x4 *>(xr + ks * 32 + kq * 8);
+                const f32x4 hi = *reinterpret_cast<const f32x4 *>(xr + ks * 32 + kq * 8 + 4);
+                float v[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                if (Q8) q8_image_block(v);
+                u32x4 packed;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const typename MX::V2 pr = {static_cast<typename MX::E>(v[2 * t]),
+                                                static_cast<typename MX::E>(v[2 * t + 1])};
+                    const unsigned w = __builtin_bit_cast(unsigned, pr);
+                    packed[t] = w;
+                    const float r0 = MX::lo(w), r1 = MX::hi(w);
+                    sx = __fmaf_rn(r0, r0, sx);
+                    sx = __fmaf_rn(r1, r1, sx);
+                    const float d0 = v[2 * t] - r0, d1 = v[2 * t + 1] - r1;
+                    sd = __fmaf_rn(d0, d0, sd);
+                    sd = __fmaf_rn(d1, d1, sd);
+                    sxx = __fmaf_rn(v[2 * t], v[2 * t], sxx);
+                    sxx = __fmaf_rn(v[2 * t + 1], v[2 * t + 1], sxx);
+                }
+                xb[g][ks] = packed;
+            }
+            sx += __shfl_xor(sx, 16);
+            sx += __shfl_xor(sx, 32);
+            sd += __shfl_xor(sd, 16);
+            sd += __shfl_xor(sd, 32);
+            sxx += __shfl_xor(sxx, 16);
+            sxx += __shfl_xor(sxx, 32);
+            nx2[g] = sx;
+            nd2[g] = sd;
+            nxx2[g] = sxx;
+        }
+
+        // ---- sweep of the stage's codebook ----
+        float top[FG][TOPL];
+#pragma unroll
+        for (int g = 0; g < FG; ++g)
+#pragma unroll
+            for (int j = 0; j < TOPL; ++j) top[g][j] = -INFINITY;
+        auto lds_a = [&](int buf, int blk, int ks) -> typename MX::V8 {
+            const int r = blk * 16 + col;
+            const int j = ks * 4 + kq;
+            return *reinterpret_cast<const typename MX::V8 *>(lds + buf * CT::BUFB + r * T::ROWB + ((j ^ (r & T::SWZ)) * 16));
+        };
+        auto lds_h = [&](int buf, int blk) -> f32x4 {
+            return *reinterpret_cast<const f32x4 *>(lds + buf * CT::BUFB + T::CHUNKB + (blk * 16 + kq * 4) * 4);
+        };
+        // direct global-to-LDS staging, as in the sweep kernel (lane l of
+        // wave w lands at piece k * kCThreads + 64 w + l)
+        const unsigned char *cbb = reinterpret_cast<const unsigned char *>(a.cbh);
+        auto stage_piece = [&](int buf, int chunk, int k) {
+            const int q = threadIdx.x + k * kCThreads;
+            const int r = q / T::CH16, j = (q % T::CH16) ^ (r & T::SWZ);
+            const unsigned char *gp = cbb + static_cast<int64_t>(chunk) * T::CHUNKB + r * T::ROWB + j * 16;
+            unsigned char *d = lds + buf * CT::BUFB + (k * kCThreads + wave * kWave) * 16;
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)gp,
+                                             (__attribute__((address_space(3))) void *)d, 16, 0, 0);
+        };
+        auto stage_h = [&](int buf, int chunk) {
+            const float *gp = a.nhh + static_cast<int64_t>(chunk) * T::CC + hsrc;
+            unsigned char *d = lds + buf * CT::BUFB + T::CHUNKB + wave * kWave * 4;
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)gp,
+                                             (__attribute__((address_space(3))) void *)d, 4, 0, 0);
+        };
+        __syncthreads();   // the previous stage's select is done with the phase region
+#pragma unroll
+        for (int k = 0; k < CT::STAGE16; ++k) stage_piece(0, 0, k);
+        stage_h(0, 0);
+        __builtin_amdgcn_s_waitcnt(kWaitLoads);
+        __syncthreads();
+
+        typename MX::V8 ring[R];
+#pragma unroll
+        for (int l = 0; l < L; ++l) ring[l] = lds_a(0, half, l);
+        f32x4 hcur = lds_h(0, half);
+        f32x4 accp[FG];
+#pragma unroll
+        for (int g = 0; g < FG; ++g) accp[g] = f32x4{-3.40282347e38f, -3.40282347e38f, -3.40282347e38f, -3.40282347e38f};
+        unsigned lprev = 0;
+        auto epilogue = [&](const f32x4 (&acc)[FG], unsigned local0) {
+#pragma unroll
+            for (int g = 0; g < FG; ++g)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float key = key_of(acc[g][i], local0 + i, vkeep);
+#pragma unroll
+                    for (int j = TOPL - 1; j > 0; --j) top[g][j] = __builtin_amdgcn_fmed3f(top[g][j - 1], top[g][j], key);
+                    top[g][0] = __builtin_amdgcn_fmed3f(top[g][0], key, 3.40282347e38f);
+                }
+        };
+        for (int ch = 0; ch < nch; ++ch) {
+            const int buf = ch & 1;
+            const int cs = ch + 1 < nch ? ch + 1 : ch;   // the last chunk re-stages itself (no branch)
+#pragma unroll
+            for (int i = 0; i < NB; ++i) {
+                const int b = 2 * i + half;
+#pragma unroll
+                for (int j = 0; j < PPB; ++j) {
+                    const int k = i + j * NB;
+                    if (k < CT::STAGE16) stage_piece(buf ^ 1, cs, k);
+                }
+                if (i == 0) stage_h(buf ^ 1, cs);
+                f32x4 acc[FG];
+#pragma unroll
+                for (int g = 0; g < FG; ++g) acc[g] = hcur;
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) {
+                    const int pk = ks + L;
+                    if (pk < KS) ring[pk % R] = lds_a(buf, b, pk);
+                    else if (i + 1 < NB) ring[pk % R] = lds_a(buf, b + 2, pk - KS);
+#pragma unroll
+                    for (int g = 0; g < FG; ++g)
+                        acc[g] = MX::mfma(ring[ks % R], __builtin_bit_cast(typename MX::V8, xb[g][ks]), acc[g]);
+                }
+                epilogue(accp, lprev);
+                if (i + 1 < NB) hcur = lds_h(buf, b + 2);
+#pragma unroll
+                for (int q = 0; q < KS * FG; ++q) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x002, (4 * 4 * FG + 4 * FG) / (KS * FG) + 1, 0);   // VALU
+                }
+#pragma unroll
+                for (int g = 0; g < FG; ++g) accp[g] = acc[g];
+                lprev = static_cast<unsigned>((ch * BPC + b) * 4);
+            }
+            __builtin_amdgcn_s_waitcnt(kWaitLoads);
+            __syncthreads();
+#pragma unroll
+            for (int l = 0; l < L; ++l) ring[l] = lds_a(buf ^ 1, half, l);
+            hcur = lds_h(buf ^ 1, half);
+        }
+        epilogue(accp, lprev);
+
+        // ---- merge the halves' keys; groups' keys and norms to LDS ----
+        __syncthreads();   // every wave is done with the chunk buffers
+        float *mk = reinterpret_cast<float *>(lds);   // [G][TOPL][64], the second half's keys
+        if (half == 1) {
+#pragma unroll
+            for (int g = 0; g < FG; ++g)
+#pragma unroll
+                for (int j = 0; j < TOPL; ++j) mk[((row * FG + g) * TOPL + j) * kWave + lane] = top[g][j];
+        }
+        __syncthreads();
+        if (half == 0) {
+#pragma unroll
+            for (int g = 0; g < FG; ++g) {
+                const int gi = row * FG + g;
+                // tau bounds every key either half dropped
+                float taul = top[g][TOPL - 1];
+#pragma unroll
+                for (int j = 0; j < TOPL; ++j) {
+                    const float key = mk[(gi * TOPL + j) * kWave + lane];
+                    if (j == TOPL - 1) taul = fmaxf(taul, key);
+#pragma unroll
+                    for (int i = TOPL - 1; i > 0; --i) top[g][i] = __builtin_amdgcn_fmed3f(top[g][i - 1], top[g][i], key);
+                    top[g][0] = __builtin_amdgcn_fmed3f(top[g][0], key, 3.40282347e38f);
+                }
+                taul = fmaxf(taul, top[g][TOPL - 1]);
+#pragma unroll
+                for (int j = 0; j < TOPL; ++j) selk[(gi * (TOPL + 1) + j) * kWave + lane] = top[g][j];
+                selk[(gi * (TOPL + 1) + TOPL) * kWave + lane] = taul;
+                if (kq == 0) {
+                    nrm[(gi * 3 + 0) * 16 + col] = nx2[g];
+                    nrm[(gi * 3 + 1) * 16 + col] = nd2[g];
+                    nrm[(gi * 3 + 2) * 16 + col] = nxx2[g];
+                }
+            }
+        }
+        __syncthreads();
+
+        // ---- select of the block's groups over its waves ----
+        SelLds<Q8, K, TOPL> *sl = reinterpret_cast<SelLds<Q8, K, TOPL> *>(lds);
+        for (int gi = wave; gi < LY::G; gi += kCWaves) {
+            const int64_t mb = m_tile + gi * 16;
+            if (mb >= M) break;   // wave-uniform; later groups are further on
+            float tp[TOPL];
+#pragma unroll
+            for (int j = 0; j < TOPL; ++j) tp[j] = selk[(gi * (TOPL + 1) + j) * kWave + lane];
+            const float taul = selk[(gi * (TOPL + 1) + TOPL) * kWave + lane];
+            select_group<RECIPE, Q8, KS, TOPL>(a, mb, tp, taul, nrm[(gi * 3 + 0) * 16 + col], nrm[(gi * 3 + 1) * 16 + col],
+                                               nrm[(gi * 3 + 2) * 16 + col], sl[wave], true);
+        }
+        __syncthreads();   // the stage's residuals are written before the next stage reads them
+    }
+}
+
+// The residual of frame m entering stage s of a cascade, replayed from the
+// input in the cascade's arithmetic (r -= c_t[code_t], t < s, the forced
+// codes where given), into xs (every thread of the block).
+__device__ inline void replay_residual(const CascadeArgs &c, int64_t m, int s, float *xs, int K) {
+    const StageArgs &a = c.a;
+    for (int k = threadIdx.x; k < K; k += blockDim.x) {
+        float v = c.x0[m * K + k];
+        for (int t = 0; t < s; ++t) {
+            int u = a.force_idx ? a.force_idx[m * a.Q + t] : a.idx[m * a.Q + t];
+            if (u < 0 || u >= a.N) u = 0;
+            v = __fsub_rn(v, a.cbf[(static_cast<int64_t>(t) * a.N + u) * K + k]);
+        }
+        xs[k] = v;
+    }
+}
+
+// The recipe's per-frame terms of the frame in xs: sum_rows(x*x) (Higgs)
+// into sh.o_x2, and the Q8_0 query blocks into xq / xd.
+template <int RECIPE, bool Q8, int KS>
+__device__ inline void scan_prepare(const float *xs, int8_t *xq, float *xd, ScanSh &sh) {
+    constexpr int K = KS * 32;
+    __syncthreads();
+    if (threadIdx.x == 0) sh.o_x2 = RECIPE == HIGGS ? sum_squares_k<K>(xs) : 0.0f;
+    if (Q8 && threadIdx.x < K / 32) quantize_block_q8(xs + 32 * threadIdx.x, xq + 32 * threadIdx.x, xd + threadIdx.x);
+    __syncthreads();
+}
+
+__device__ inline bool same_bits(float x, float y) { return __float_as_uint(x) == __float_as_uint(y); }
+
+// Exact verification of the cascade's speculative (frame, stage) pairs, a
+// block per pair: the stage's input residual is replayed, every code's
+// recipe value computed and the reference's selection made (the exact
+// scan's); where the code, distance or top-k differ from the cascade's,
+// the frame's earliest wrong stage is recorded for the fix-up.
+template <int RECIPE, bool Q8, int KS>
+__global__ __launch_bounds__(kScanThreads) void euclid_verify_kernel(CascadeArgs c) {
+    constexpr int K = KS * 32;
+    extern __shared__ __align__(16) unsigned char lds[];
+    float *xs = reinterpret_cast<float *>(lds);
+    int8_t *xq = reinterpret_cast<int8_t *>(xs + K);
+    float *xd = reinterpret_cast<float *>(xq + K);
+    __shared__ ScanSh sh;
+    const int count = *c.a.spec_count;
+    for (int p = blockIdx.x; p < count; p += gridDim.x) {
+        const int64_t m = c.a.spec_list[2 * p];
+        const int s = c.a.spec_list[2 * p + 1];
+        const StageArgs a = cascade_stage(c, s, K);
+        __syncthreads();
+        replay_residual(c, m, s, xs, K);
+        scan_prepare<RECIPE, Q8, KS>(xs, xq, xd, sh);
+        scan_select<RECIPE, Q8, KS>(a, K, false, nullptr, xs, xq, xd, sh.o_x2, sh);
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            const int64_t o = m * a.Q + s;
+            bool bad = a.idx[o] != sh.o_code;
+            if (a.dist) bad |= !same_bits(a.dist[o], RECIPE == DIRECT ? sh.o_code_v : -sh.o_code_v);
+            for (int r = 0; r < a.topk; ++r) {
+                bad |= a.topk_idx[o * a.topk + r] != sh.o_sel_n[r];
+                bad |= !same_bits(a.topk_dist[o * a.topk + r], RECIPE == DIRECT ? sh.o_sel_v[r] : -sh.o_sel_v[r]);
+            }
+            if (bad && atomicMin(&c.bad_stage[m], s) == a.Q) c.bad_list[atomicAdd(c.bad_count, 1)] = static_cast<int32_t>(m);
+        }
+    }
+}
+
+// Recomputes the frames whose speculation was wrong from their earliest
+// wrong stage on, a block per frame, with the exact scan of every stage.
+template <int RECIPE, bool Q8, int KS>
+__global__ __launch_bounds__(kScanThreads) void euclid_fixup_kernel(CascadeArgs c) {
+    constexpr int K = KS * 32;
+    extern __shared__ __align__(16) unsigned char lds[];
+    float *xs = reinterpret_cast<float *>(lds);
+    int8_t *xq = reinterpret_cast<int8_t *>(xs + K);
+    float *xd = reinterpret_cast<float *>(xq + K);
+    __shared__ ScanSh sh;
+    const int nb = *c.bad_count;
+    for (int b = blockIdx.x; b < nb; b += gridDim.x) {
+        const int64_t m = c.bad_list[b];
+        const int t0 = c.bad_stage[m];
+        __syncthreads();
+        replay_residual(c, m, t0, xs, K);
+        for (int s = t0; s < c.a.Q; ++s) {
+            const StageArgs a = cascade_stage(c, s, K);
+            scan_prepare<RECIPE, Q8, KS>(xs, xq, xd, sh);
+            scan_select<RECIPE, Q8, KS>(a, K, false, nullptr, xs, xq, xd, sh.o_x2, sh);
+            __syncthreads();
+            const int64_t o = m * a.Q + s;
+            if (threadIdx.x == 0) {
+                a.idx[o] = sh.o_code;
+                if (a.dist) a.dist[o] = RECIPE == DIRECT ? sh.o_code_v : -sh.o_code_v;
+                for (int r = 0; r < a.topk; ++r) {
+                    a.topk_idx[o * a.topk + r] = sh.o_sel_n[r];
+                    a.topk_dist[o * a.topk + r] = RECIPE == DIRECT ? sh.o_sel_v[r] : -sh.o_sel_v[r];
+                }
+                atomicAdd(&c.counts[64 + (s % 64)], 1);
+            }
+            int use = sh.o_code;
+            if (a.force_idx) {
+                use = a.force_idx[o];
+                if (use < 0 || use >= a.N) {
+                    if (threadIdx.x == 0) a.flags[AQ_FLAG_BAD_INDEX] = 1;
+                    use = 0;
+                }
+            }
+            for (int k = threadIdx.x; k < K; k += blockDim.x)
+                xs[k] = __fsub_rn(xs[k], a.cbf[static_cast<int64_t>(use) * K + k]);
+        }
+        __syncthreads();
+        if (c.write_last)
+            for (int k = threadIdx.x; k < K; k += blockDim.x) c.work[m * K + k] = xs[k];
+    }
+}
+
+// Cascade kernels of a width (null where the frame tiles would not keep
+// two waves per SIMD busy: the widest codebooks take the stage pipeline).
+template <int RECIPE, bool Q8, int KS, int TOPL>
+constexpr CascadeFn cascade_fn() {
+    if constexpr (KS == 2 || KS == 8) return euclid_cascade_kernel<RECIPE, Q8, KS, groups_for(KS), TOPL>;
+    else return nullptr;
+}
+template <int RECIPE, bool Q8, int KS>
+constexpr CascadeFn verify_fn() {
+    if constexpr (KS == 2 || KS == 8) return euclid_verify_kernel<RECIPE, Q8, KS>;
+    else return nullptr;
+}
+template <int RECIPE, bool Q8, int KS>
+constexpr CascadeFn fixup_fn() {
+    if constexpr (KS == 2 || KS == 8) return euclid_fixup_kernel<RECIPE, Q8, KS>;
+    else return nullptr;
+}
+template <int KS>
+constexpr int cascade_lds_bytes() {
+    if constexpr (KS == 2 || KS == 8) return CLayout<KS, groups_for(KS), 4, true>::BYTES;
+    else return 0;
+}
+
 }  // namespace
 
 // Defines aq_euclid::kernels_ks<KS>(): the kernel table of one width.
@@ -2629,7 +3177,17 @@ __global__ __launch_bounds__(kWave) void euclid_refine_select_kernel(StageArgs a
             {euclid_exact_scan_kernel<OMNI, false, KS>, euclid_exact_scan_kernel<HIGGS, false, KS>,             \
              euclid_exact_scan_kernel<DIRECT, false, KS>, euclid_exact_scan_kernel<HIGGS, true, KS>},           \
             Tile<KS>::LDS,                                                                                      \
-            Tile<KS>::CC};                                                                                      \
+            Tile<KS>::CC,                                                                                       \
+            {{cascade_fn<OMNI, false, KS, 3>(), cascade_fn<OMNI, false, KS, 4>()},                              \
+             {cascade_fn<HIGGS, false, KS, 3>(), cascade_fn<HIGGS, false, KS, 4>()},                            \
+             {cascade_fn<DIRECT, false, KS, 3>(), cascade_fn<DIRECT, false, KS, 4>()},                          \
+             {cascade_fn<HIGGS, true, KS, 3>(), cascade_fn<HIGGS, true, KS, 4>()}},                             \
+            {verify_fn<OMNI, false, KS>(), verify_fn<HIGGS, false, KS>(), verify_fn<DIRECT, false, KS>(),       \
+             verify_fn<HIGGS, true, KS>()},                                                                     \
+            {fixup_fn<OMNI, false, KS>(), fixup_fn<HIGGS, false, KS>(), fixup_fn<DIRECT, false, KS>(),          \
+             fixup_fn<HIGGS, true, KS>()},                                                                      \
+            cascade_lds_bytes<KS>(),                                                                            \
+            kCRows * groups_for(KS) * 16};                                                                      \
         return &t;                                                                                              \
     }                                                                                                           \
     }
