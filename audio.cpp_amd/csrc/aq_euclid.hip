@@ -669,10 +669,16 @@ aq_status euclid_encode_any(aq_ctx *ctx, const aq_codebooks *cb, const aq_frames
 }
 
 // Whether encodes take the one-launch cascade (AQ_EUCLID_PIPELINE=stages
-// selects the per-stage pipeline instead, for comparisons).
+// selects the per-stage pipeline instead, =cascade the cascade that keeps the
+// residual in memory where the register-resident one exists, for
+// comparisons).
 bool cascade_enabled() {
     const char *e = std::getenv("AQ_EUCLID_PIPELINE");
     return !(e && std::strcmp(e, "stages") == 0);
+}
+bool resident_enabled() {
+    const char *e = std::getenv("AQ_EUCLID_PIPELINE");
+    return !(e && std::strcmp(e, "cascade") == 0);
 }
 
 // Encode with the one-launch cascade: every stage of every frame in
@@ -685,7 +691,15 @@ aq_status euclid_encode_cascade(aq_ctx *ctx, const aq_codebooks *cb, const aq_fr
                                 const int32_t *force_idx, Arena &arena, const KsKernels *kk, int var, int topl) {
     const int K = static_cast<int>(cb->K);
     CascadeFn casc = kk->cascade[var][topl - 3], ver = kk->verify[var], fix = kk->fixup[var];
-    const size_t clds = static_cast<size_t>(kk->cascade_lds), slds = scan_lds_bytes(K);
+    size_t clds = static_cast<size_t>(kk->cascade_lds);
+    int frames = kk->cascade_frames, threads = kCThreads;
+    if (var < 3 && kk->resident[var][topl - 3] && resident_enabled()) {
+        casc = kk->resident[var][topl - 3];
+        clds = static_cast<size_t>(kk->resident_lds);
+        frames = kk->resident_frames;
+        threads = kRsThreads;
+    }
+    const size_t slds = scan_lds_bytes(K);
     {
         aq_status ls = aq_launch_lds(ctx, reinterpret_cast<const void *>(casc), clds, "aq_euclid_encode (cascade)");
         if (ls == AQ_OK) ls = aq_launch_lds(ctx, reinterpret_cast<const void *>(ver), slds, "aq_euclid_encode (verify)");
@@ -760,8 +774,8 @@ aq_status euclid_encode_cascade(aq_ctx *ctx, const aq_codebooks *cb, const aq_fr
     c.bad_list = c.bad_stage + M;
     c.write_last = residual ? 1 : 0;
     const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
-    const int64_t blocks = (M + kk->cascade_frames - 1) / kk->cascade_frames;
-    aq_launch_timed(ctx, !arena.base, casc, dim3(static_cast<unsigned>(blocks)), dim3(kCThreads),
+    const int64_t blocks = (M + frames - 1) / frames;
+    aq_launch_timed(ctx, !arena.base, casc, dim3(static_cast<unsigned>(blocks)), dim3(threads),
                     static_cast<uint32_t>(clds), c);
     AQ_HIP(ctx, hipGetLastError());
     hipLaunchKernelGGL(ver, dim3(static_cast<unsigned>(2 * cus)), dim3(kScanThreads), slds, ctx->stream, c);

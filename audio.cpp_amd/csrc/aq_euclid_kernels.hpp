@@ -228,6 +228,11 @@ struct KsKernels {
     CascadeFn fixup[4];
     int cascade_lds;          // cascade dynamic LDS bytes (TOPL 4)
     int cascade_frames;       // frames per cascade block
+    // The register-resident cascade (f32 codebooks of the widths whose
+    // residual fits the registers; null otherwise).
+    CascadeFn resident[3][2]; // [recipe][topl]
+    int resident_lds;         // its dynamic LDS bytes (TOPL 4)
+    int resident_frames;      // frames per block
 };
 const KsKernels *kernels_ks2();
 const KsKernels *kernels_ks8();
@@ -933,15 +938,19 @@ struct SelLds {
 // Certificate, exact re-ranking, outputs and residual update of one group of
 // 16 frames (m_base ...) in one wave, 4 lanes per frame (the sweep's lane
 // layout): top / taul are the lane's merged keys and the bound of the keys it
-// dropped, nx2 / nd2 / nxx2 the frame's |x~|^2, |x - x~|^2, |x|^2.  Frames
-// the certificate cannot settle go to a.fail_list for the refine pass, or,
-// with `speculate`, take the best exactly evaluated candidate (outputs and
-// residual update as if certified) and are listed in a.spec_list as
-// (frame, stage) for the exact verification after the cascade.
+// dropped, nx2 / nd2 / nxx2 the frame's |x~|^2, |x - x~|^2, |x|^2; the
+// frames' fp32 rows are read at xrows + f * xstride (f < 16; global memory
+// or LDS).  Frames the certificate cannot settle go to a.fail_list for the
+// refine pass, or, with `speculate`, take the best exactly evaluated
+// candidate (outputs and residual update as if certified) and are listed in
+// a.spec_list as (frame, stage) for the exact verification after the
+// cascade.  With `update` the residual a.xout = a.xin - c[code] is written
+// for the settled frames; the lane's frame's code is returned (-1: frame
+// not settled or past M).
 template <int RECIPE, bool Q8, int KS, int TOPL>
-__device__ void select_group(const StageArgs &a, int64_t m_base, const float (&top_in)[TOPL], float taul_in,
-                             float nx2_in, float nd2_in, float nxx2_in, SelLds<Q8, KS * 32, TOPL> &sl,
-                             bool speculate) {
+__device__ int select_group(const StageArgs &a, int64_t m_base, const float (&top_in)[TOPL], float taul_in,
+                            float nx2_in, float nd2_in, float nxx2_in, SelLds<Q8, KS * 32, TOPL> &sl,
+                            bool speculate, const float *xrows, int xstride, bool update) {
     constexpr int K = KS * 32;
     constexpr int FG = 1;
     const int lane = threadIdx.x & (kWave - 1);
@@ -1066,8 +1075,8 @@ __device__ void select_group(const StageArgs &a, int64_t m_base, const float (&t
     if (RECIPE == HIGGS && K % 256 == 0) {
         if (__any(needg[0])) {
             static_assert(FG == 1, "one frame group per select wave");
-            const int64_t mq = m_base + col < a.M ? m_base + col : a.M - 1;
-            const float *xr = a.xin + mq * K;
+            const int fq = m_base + col < a.M ? col : static_cast<int>(a.M - 1 - m_base);
+            const float *xr = xrows + static_cast<int64_t>(fq) * xstride;
             double sq = 0.0;
 #pragma unroll
             for (int c = 0; c < K / 256; ++c) {
@@ -1133,15 +1142,16 @@ __device__ void select_group(const StageArgs &a, int64_t m_base, const float (&t
             for (int g = 0; g < FG; ++g) needmask |= (__shfl(needg[g] ? 1 : 0, lane % 16) & 1) << g;
             if (lane < FG * 16) {
                 const bool need = ((needmask >> (lane / 16)) & 1) != 0;
-                q_x2[lane] = need ? sum_squares_k<K>(a.xin + (m_base + lane) * K) : 0.0f;
+                q_x2[lane] = need ? sum_squares_k<K>(xrows + static_cast<int64_t>(lane) * xstride) : 0.0f;
             }
         }
         // Q8_0: the 4 lanes of a frame taking every 4th block.
         if (Q8 && qcount > 0) {
-            const int64_t mq = m_base + col < a.M ? m_base + col : a.M - 1;
+            const int fq = m_base + col < a.M ? col : static_cast<int>(a.M - 1 - m_base);
 #pragma unroll
             for (int ib = kq; ib < K / 32; ib += 4)
-                quantize_block_q8(a.xin + mq * K + 32 * ib, q_xq + col * XQS + 32 * ib, q_xd + col * (K / 32) + ib);
+                quantize_block_q8(xrows + static_cast<int64_t>(fq) * xstride + 32 * ib, q_xq + col * XQS + 32 * ib,
+                                  q_xd + col * (K / 32) + ib);
         }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -1172,7 +1182,7 @@ __device__ void select_group(const StageArgs &a, int64_t m_base, const float (&t
 #pragma unroll
                 for (int p = 0; p < P; ++p)
                     acc[p] = __fmaf_rn(a.cbf[static_cast<int64_t>(n[p]) * K + 16 * l + j] * sa,
-                                       a.xin[(m_base + fs[p]) * K + 16 * l + j], acc[p]);
+                                       xrows[static_cast<int64_t>(fs[p]) * xstride + 16 * l + j], acc[p]);
 #pragma unroll
             for (int p = 0; p < P; ++p) {
                 float v = row_ror_add<8>(acc[p]);
@@ -1235,7 +1245,7 @@ __device__ void select_group(const StageArgs &a, int64_t m_base, const float (&t
                 const int fs = q_f[e];
                 const int n = q_n[e];
                 const float x2 = RECIPE == HIGGS ? q_x2[fs] : 0.0f;
-                q_v[e] = exact_value_k<RECIPE, Q8, K>(a, a.xin + (m_base + fs) * K, n, x2);
+                q_v[e] = exact_value_k<RECIPE, Q8, K>(a, xrows + static_cast<int64_t>(fs) * xstride, n, x2);
             }
         }
     }
@@ -1379,6 +1389,8 @@ __device__ void select_group(const StageArgs &a, int64_t m_base, const float (&t
         }
     }
 
+    if (!update) return win_ok[0] && m_base + col < a.M ? win_code[0] : -1;
+
     // ---- phase 3: residual update r -= c[code] for certified frames ----
     // Rows across the lanes (coalesced), and the loads of kP3 frames issued
     // before the first wait so one memory round trip covers all of them.
@@ -1437,6 +1449,7 @@ __device__ void select_group(const StageArgs &a, int64_t m_base, const float (&t
             }
         }
     }
+    return win_ok[0] && m_base + col < a.M ? win_code[0] : -1;
 }
 
 
@@ -1475,7 +1488,7 @@ __global__ __launch_bounds__(kThreads) void euclid_select_kernel(StageArgs a) {
     const int64_t mc = m < a.M ? m : a.M - 1;
     __shared__ SelLds<Q8, KS * 32, TOPL> sl[kWaves];
     select_group<RECIPE, Q8, KS, TOPL>(a, m_base, top, taul, a.norms[mc], a.norms[a.M + mc], a.norms[2 * a.M + mc],
-                                       sl[wave], false);
+                                       sl[wave], false, a.xin + m_base * (KS * 32), KS * 32, true);
 }
 
 // ------------------------------------------------------------- exact scan
@@ -3014,9 +3027,298 @@ __global__ __launch_bounds__(kCThreads, 1) void euclid_cascade_kernel(CascadeArg
             for (int j = 0; j < TOPL; ++j) tp[j] = selk[(gi * (TOPL + 1) + j) * kWave + lane];
             const float taul = selk[(gi * (TOPL + 1) + TOPL) * kWave + lane];
             select_group<RECIPE, Q8, KS, TOPL>(a, mb, tp, taul, nrm[(gi * 3 + 0) * 16 + col], nrm[(gi * 3 + 1) * 16 + col],
-                                               nrm[(gi * 3 + 2) * 16 + col], sl[wave], true);
+                                               nrm[(gi * 3 + 2) * 16 + col], sl[wave], true, a.xin + mb * K, K, true);
         }
         __syncthreads();   // the stage's residuals are written before the next stage reads them
+    }
+}
+
+// ------------------------------------------------------------- resident cascade
+// The residual cascade with the residual held in registers.  A block of
+// kRsWaves waves (one per SIMD, up to 512 registers each) owns kRsWaves x FG
+// x 16 frames through all stages.  Wave w keeps the fp32 residual of its FG
+// frame groups in the MFMA fragment layout (lane (col, kq) of group g holds
+// x[16 g + col][32 ks + 8 kq + t], t < 8) and per stage
+//  1. builds the fp16 fragments and rounding norms from it;
+//  2. sweeps the stage's whole codebook through double-buffered LDS chunks
+//     that the block's waves stage together (no code split between waves,
+//     so no merge of key lists);
+//  3. per group: copies the residual rows into its LDS scratch (read by the
+//     exact re-ranking), runs the select (certificate, exact re-ranking and
+//     outputs; a frame the certificate cannot settle continues with its
+//     best evaluated code and is listed for euclid_verify_kernel) and
+//     subtracts the chosen (or forced) code's row in registers.
+// Only the last stage's residual is written to memory.
+constexpr int kRsWaves = 4;
+constexpr int kRsThreads = kRsWaves * kWave;
+
+template <int KS, int FG, int TOPL>
+struct RsLayout {
+    static constexpr int K = KS * 32;
+    static constexpr int BUFB = Tile<KS>::CHUNKB + kRsThreads * 4;   // chunk + one |c|^2/2 slot per thread
+    static constexpr int STAGE16 = Tile<KS>::CHUNKB / 16 / kRsThreads;
+    static constexpr int SWEEP = 2 * BUFB;
+    static constexpr int XSTR = K + 4;   // row stride of the scratch rows (floats; padded against bank conflicts)
+    static constexpr int SELB = (static_cast<int>(sizeof(SelLds<false, K, TOPL>)) + 15) / 16 * 16;
+    static constexpr int WSCR = SELB + 16 * XSTR * 4;                 // per wave: select queues + 16 rows
+    static constexpr int BYTES = SWEEP > kRsWaves * WSCR ? SWEEP : kRsWaves * WSCR;
+    static constexpr int FRAMES = kRsWaves * FG * 16;
+};
+
+template <int RECIPE, int KS, int FG, int TOPL>
+__global__ __launch_bounds__(kRsThreads, 1) void euclid_resident_kernel(CascadeArgs c) {
+    using T = Tile<KS>;
+    using LY = RsLayout<KS, FG, TOPL>;
+    using MX = Mx;
+    constexpr int K = T::K;
+    constexpr int BPC = T::CC / 16;                       // 16-code blocks per chunk
+    static_assert(T::CHUNKB % (16 * kRsThreads) == 0, "a chunk splits evenly over the block");
+    constexpr int PPB = (LY::STAGE16 + BPC - 1) / BPC;    // staged pieces per block
+    extern __shared__ __align__(16) unsigned char lds[];
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);   // uniform: addresses stay scalar
+    const int col = lane & 15, kq = lane >> 4;
+    const int64_t M = c.a.M;
+    const int N = c.a.N;
+    const int64_t m_tile = static_cast<int64_t>(blockIdx.x) * LY::FRAMES;
+    if (m_tile >= M) return;   // block-uniform
+    const int64_t m_wave = m_tile + wave * (FG * 16);
+    for (int i = threadIdx.x; i < LY::FRAMES; i += kRsThreads)
+        if (m_tile + i < M) c.bad_stage[m_tile + i] = c.a.Q;
+
+    int lbits = 0;   // bits of the lane-local code index (N/4 codes per lane)
+    while ((1 << lbits) < N / 4) ++lbits;
+    const unsigned kmask = (1u << lbits) - 1u;
+    unsigned vkeep;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(vkeep) : "s"(~kmask));
+    const int nch = N / T::CC;
+    constexpr int R = KS % 4 == 0 ? 4 : 2;
+    constexpr int L = R - 1;
+    constexpr int kWaitLoads = 0x0070;   // s_waitcnt vmcnt(0) lgkmcnt(0)
+    const int hsrc = threadIdx.x < T::CC ? threadIdx.x : 0;
+
+    // the stage-0 input, in the fragment layout (rows past M read row M - 1)
+    float xr[FG][KS][8];
+#pragma unroll
+    for (int g = 0; g < FG; ++g) {
+        const int64_t m = m_wave + g * 16 + col;
+        const float *row = c.x0 + (m < M ? m : M - 1) * K;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const f32x4 lo = *reinterpret_cast<const f32x4 *>(row + ks * 32 + kq * 8);
+            const f32x4 hi = *reinterpret_cast<const f32x4 *>(row + ks * 32 + kq * 8 + 4);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                xr[g][ks][t] = lo[t];
+                xr[g][ks][4 + t] = hi[t];
+            }
+        }
+    }
+
+    for (int s = 0; s < c.a.Q; ++s) {
+        const StageArgs a = cascade_stage(c, s, K);
+        // ---- fp16 fragments and rounding norms of the residual ----
+        u32x4 xb[FG][KS];
+        float nx2[FG], nd2[FG], nxx2[FG];
+#pragma unroll
+        for (int g = 0; g < FG; ++g) {
+            float sx = 0.0f, sd = 0.0f, sxx = 0.0f;
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                u32x4 packed;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const float v0 = xr[g][ks][2 * t], v1 = xr[g][ks][2 * t + 1];
+                    const typename MX::V2 pr = {static_cast<typename MX::E>(v0), static_cast<typename MX::E>(v1)};
+                    const unsigned w = __builtin_bit_cast(unsigned, pr);
+                    packed[t] = w;
+                    const float r0 = MX::lo(w), r1 = MX::hi(w);
+                    sx = __fmaf_rn(r0, r0, sx);
+                    sx = __fmaf_rn(r1, r1, sx);
+                    const float d0 = v0 - r0, d1 = v1 - r1;
+                    sd = __fmaf_rn(d0, d0, sd);
+                    sd = __fmaf_rn(d1, d1, sd);
+                    sxx = __fmaf_rn(v0, v0, sxx);
+                    sxx = __fmaf_rn(v1, v1, sxx);
+                }
+                xb[g][ks] = packed;
+            }
+            sx += __shfl_xor(sx, 16);
+            sx += __shfl_xor(sx, 32);
+            sd += __shfl_xor(sd, 16);
+            sd += __shfl_xor(sd, 32);
+            sxx += __shfl_xor(sxx, 16);
+            sxx += __shfl_xor(sxx, 32);
+            nx2[g] = sx;
+            nd2[g] = sd;
+            nxx2[g] = sxx;
+        }
+
+        // ---- sweep of the stage's codebook ----
+        float top[FG][TOPL];
+#pragma unroll
+        for (int g = 0; g < FG; ++g)
+#pragma unroll
+            for (int j = 0; j < TOPL; ++j) top[g][j] = -INFINITY;
+        auto lds_a = [&](int buf, int blk, int ks) -> typename MX::V8 {
+            const int r = blk * 16 + col;
+            const int j = ks * 4 + kq;
+            return *reinterpret_cast<const typename MX::V8 *>(lds + buf * LY::BUFB + r * T::ROWB + ((j ^ (r & T::SWZ)) * 16));
+        };
+        auto lds_h = [&](int buf, int blk) -> f32x4 {
+            return *reinterpret_cast<const f32x4 *>(lds + buf * LY::BUFB + T::CHUNKB + (blk * 16 + kq * 4) * 4);
+        };
+        // direct global-to-LDS staging, as in the sweep kernel (lane l of
+        // wave w lands at piece k * kRsThreads + 64 w + l)
+        const unsigned char *cbb = reinterpret_cast<const unsigned char *>(a.cbh);
+        auto stage_piece = [&](int buf, int chunk, int k) {
+            const int q = threadIdx.x + k * kRsThreads;
+            const int r = q / T::CH16, j = (q % T::CH16) ^ (r & T::SWZ);
+            const unsigned char *gp = cbb + static_cast<int64_t>(chunk) * T::CHUNKB + r * T::ROWB + j * 16;
+            unsigned char *d = lds + buf * LY::BUFB + (k * kRsThreads + wave * kWave) * 16;
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)gp,
+                                             (__attribute__((address_space(3))) void *)d, 16, 0, 0);
+        };
+        auto stage_h = [&](int buf, int chunk) {
+            const float *gp = a.nhh + static_cast<int64_t>(chunk) * T::CC + hsrc;
+            unsigned char *d = lds + buf * LY::BUFB + T::CHUNKB + wave * kWave * 4;
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)gp,
+                                             (__attribute__((address_space(3))) void *)d, 4, 0, 0);
+        };
+        __syncthreads();   // the previous stage's select is done with the scratch
+#pragma unroll
+        for (int k = 0; k < LY::STAGE16; ++k) stage_piece(0, 0, k);
+        stage_h(0, 0);
+        __builtin_amdgcn_s_waitcnt(kWaitLoads);
+        __syncthreads();
+
+        typename MX::V8 ring[R];
+#pragma unroll
+        for (int l = 0; l < L; ++l) ring[l] = lds_a(0, 0, l);
+        f32x4 hcur = lds_h(0, 0);
+        f32x4 accp[FG];
+#pragma unroll
+        for (int g = 0; g < FG; ++g) accp[g] = f32x4{-3.40282347e38f, -3.40282347e38f, -3.40282347e38f, -3.40282347e38f};
+        unsigned lprev = 0;
+        auto epilogue = [&](const f32x4 (&acc)[FG], unsigned local0) {
+#pragma unroll
+            for (int g = 0; g < FG; ++g)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float key = key_of(acc[g][i], local0 + i, vkeep);
+#pragma unroll
+                    for (int j = TOPL - 1; j > 0; --j) top[g][j] = __builtin_amdgcn_fmed3f(top[g][j - 1], top[g][j], key);
+                    top[g][0] = __builtin_amdgcn_fmed3f(top[g][0], key, 3.40282347e38f);
+                }
+        };
+        for (int ch = 0; ch < nch; ++ch) {
+            const int buf = ch & 1;
+            const int cs = ch + 1 < nch ? ch + 1 : ch;   // the last chunk re-stages itself (no branch)
+#pragma unroll
+            for (int b = 0; b < BPC; ++b) {
+#pragma unroll
+                for (int j = 0; j < PPB; ++j) {
+                    const int k = b + j * BPC;
+                    if (k < LY::STAGE16) stage_piece(buf ^ 1, cs, k);
+                }
+                if (b == 0) stage_h(buf ^ 1, cs);
+                f32x4 acc[FG];
+#pragma unroll
+                for (int g = 0; g < FG; ++g) acc[g] = hcur;
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) {
+                    const int pk = ks + L;
+                    if (pk < KS) ring[pk % R] = lds_a(buf, b, pk);
+                    else if (b + 1 < BPC) ring[pk % R] = lds_a(buf, b + 1, pk - KS);
+#pragma unroll
+                    for (int g = 0; g < FG; ++g)
+                        acc[g] = MX::mfma(ring[ks % R], __builtin_bit_cast(typename MX::V8, xb[g][ks]), acc[g]);
+                }
+                epilogue(accp, lprev);
+                if (b + 1 < BPC) hcur = lds_h(buf, b + 1);
+#pragma unroll
+                for (int q = 0; q < KS * FG; ++q) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x002, (4 * 4 * FG + 4 * FG) / (KS * FG) + 1, 0);   // VALU
+                }
+#pragma unroll
+                for (int g = 0; g < FG; ++g) accp[g] = acc[g];
+                lprev = static_cast<unsigned>((ch * BPC + b) * 4);
+            }
+            __builtin_amdgcn_s_waitcnt(kWaitLoads);
+            __syncthreads();
+#pragma unroll
+            for (int l = 0; l < L; ++l) ring[l] = lds_a(buf ^ 1, 0, l);
+            hcur = lds_h(buf ^ 1, 0);
+        }
+        epilogue(accp, lprev);
+        __syncthreads();   // every wave is done with the chunk buffers
+
+        // ---- select and residual update of the wave's groups ----
+        unsigned char *ws = lds + wave * LY::WSCR;
+        SelLds<false, K, TOPL> &sl = *reinterpret_cast<SelLds<false, K, TOPL> *>(ws);
+        float *xs = reinterpret_cast<float *>(ws + LY::SELB);
+#pragma unroll
+        for (int g = 0; g < FG; ++g) {
+            const int64_t mb = m_wave + g * 16;
+            if (mb >= M) break;   // wave-uniform; later groups are further on
+            // the group's rows, for the exact re-ranking
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                float *d = xs + col * LY::XSTR + ks * 32 + kq * 8;
+                *reinterpret_cast<f32x4 *>(d) = f32x4{xr[g][ks][0], xr[g][ks][1], xr[g][ks][2], xr[g][ks][3]};
+                *reinterpret_cast<f32x4 *>(d + 4) = f32x4{xr[g][ks][4], xr[g][ks][5], xr[g][ks][6], xr[g][ks][7]};
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            const int code = select_group<RECIPE, false, KS, TOPL>(a, mb, top[g], top[g][TOPL - 1], nx2[g], nd2[g],
+                                                                   nxx2[g], sl, true, xs, LY::XSTR, false);
+            // r -= c[code] (the forced code where given) in registers
+            const int64_t m = mb + col;
+            int use = code >= 0 ? code : 0;
+            if (a.force_idx && m < M) {
+                use = a.force_idx[m * a.Q + s];
+                if (use < 0 || use >= N) {
+                    a.flags[AQ_FLAG_BAD_INDEX] = 1;
+                    use = 0;
+                }
+            }
+            if (s + 1 < a.Q || c.write_last) {
+                const float *crow = a.cbf + static_cast<int64_t>(use) * K;
+                f32x4 cv[KS][2];
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) {
+                    cv[ks][0] = *reinterpret_cast<const f32x4 *>(crow + ks * 32 + kq * 8);
+                    cv[ks][1] = *reinterpret_cast<const f32x4 *>(crow + ks * 32 + kq * 8 + 4);
+                }
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) xr[g][ks][t] = __fsub_rn(xr[g][ks][t], cv[ks][t / 4][t % 4]);
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
+    }
+
+    // the residual after the last stage
+    if (c.write_last) {
+#pragma unroll
+        for (int g = 0; g < FG; ++g) {
+            const int64_t m = m_wave + g * 16 + col;
+            if (m >= M) continue;
+            float *row = c.work + m * K;
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                *reinterpret_cast<f32x4 *>(row + ks * 32 + kq * 8) =
+                    f32x4{xr[g][ks][0], xr[g][ks][1], xr[g][ks][2], xr[g][ks][3]};
+                *reinterpret_cast<f32x4 *>(row + ks * 32 + kq * 8 + 4) =
+                    f32x4{xr[g][ks][4], xr[g][ks][5], xr[g][ks][6], xr[g][ks][7]};
+            }
+        }
     }
 }
 
@@ -3155,6 +3457,19 @@ constexpr int cascade_lds_bytes() {
     if constexpr (KS == 2 || KS == 8) return CLayout<KS, groups_for(KS), 4, true>::BYTES;
     else return 0;
 }
+// Register-resident cascade: K = 256 (3 groups of fp32 residual and fp16
+// fragments per wave fit its 512 registers).
+constexpr int kRsGroups = 3;
+template <int RECIPE, int KS, int TOPL>
+constexpr CascadeFn resident_fn() {
+    if constexpr (KS == 8) return euclid_resident_kernel<RECIPE, KS, kRsGroups, TOPL>;
+    else return nullptr;
+}
+template <int KS>
+constexpr int resident_lds_bytes() {
+    if constexpr (KS == 8) return RsLayout<KS, kRsGroups, 4>::BYTES;
+    else return 0;
+}
 
 }  // namespace
 
@@ -3187,7 +3502,12 @@ constexpr int cascade_lds_bytes() {
             {fixup_fn<OMNI, false, KS>(), fixup_fn<HIGGS, false, KS>(), fixup_fn<DIRECT, false, KS>(),          \
              fixup_fn<HIGGS, true, KS>()},                                                                      \
             cascade_lds_bytes<KS>(),                                                                            \
-            kCRows * groups_for(KS) * 16};                                                                      \
+            kCRows * groups_for(KS) * 16,                                                                       \
+            {{resident_fn<OMNI, KS, 3>(), resident_fn<OMNI, KS, 4>()},                                          \
+             {resident_fn<HIGGS, KS, 3>(), resident_fn<HIGGS, KS, 4>()},                                        \
+             {resident_fn<DIRECT, KS, 3>(), resident_fn<DIRECT, KS, 4>()}},                                     \
+            resident_lds_bytes<KS>(),                                                                           \
+            kRsWaves * kRsGroups * 16};                                                                         \
         return &t;                                                                                              \
     }                                                                                                           \
     }

