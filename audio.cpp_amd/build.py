@@ -39,9 +39,15 @@ def sources() -> list[pathlib.Path]:
     return sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.cpp")))
 
 
+# Per-source flags.  aq_euclid_ks8.hip holds the register-resident cascade
+# (one wave per SIMD, residual in AGPRs): MFMA results in VGPRs keep its key
+# epilogue free of AGPR-to-VGPR copies.
+SOURCE_FLAGS = {"aq_euclid_ks8.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def compile_one(src: pathlib.Path) -> pathlib.Path:
     obj = BUILD / (src.name + ".o")
-    cmd = [HIPCC, *FLAGS, "-x", "hip", "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *FLAGS, *SOURCE_FLAGS.get(src.name, []), "-x", "hip", "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         sys.stderr.write(r.stdout + r.stderr)

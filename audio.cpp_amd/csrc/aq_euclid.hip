@@ -724,6 +724,7 @@ aq_status euclid_encode_cascade(aq_ctx *ctx, const aq_codebooks *cb, const aq_fr
     }
     // counters: [0, 128) per stage, 128 listed pairs, 129 frames to fix;
     // then the pair list [2 M Q], bad_stage [M] and the frames to fix [M]
+    constexpr int kZeroInts = 130;
     constexpr int kHead = 256;
     int32_t *ints = nullptr;
     {
@@ -732,7 +733,7 @@ aq_status euclid_encode_cascade(aq_ctx *ctx, const aq_codebooks *cb, const aq_fr
         if (st != AQ_OK) return st;
     }
     ctx->euclid_counts = ints;
-    hipLaunchKernelGGL(zero2_kernel, dim3(1), dim3(256), 0, ctx->stream, ints, 130, ctx->d_flags,
+    hipLaunchKernelGGL(zero2_kernel, dim3(1), dim3(256), 0, ctx->stream, ints, kZeroInts, ctx->d_flags,
                        static_cast<int>(AQ_FLAG_COUNT));
     AQ_HIP(ctx, hipGetLastError());
     CascadeArgs c{};

@@ -1742,16 +1742,12 @@ __device__ inline int spread_chunks(const StageArgs &a) {
     const int cpi = spread_quad<RECIPE, Q8>(a) ? kScanQuadCodes : kScanThreads;
     return (a.N + cpi - 1) / cpi;
 }
-template <int RECIPE, bool Q8, int K>
-__device__ void spread_item(const StageArgs &a, int slot, int chunk, int &cur, float *xs, int8_t *xq, float *xd,
-                            float &x2s) {
+// The quad path's values of one chunk of codes for the frame xr (global
+// memory or LDS) into out[n]; x2s (Higgs) is read after a block barrier.
+template <int RECIPE, int K>
+__device__ void quad_values(const StageArgs &a, float *out, int chunk, const float *xr, float &x2s) {
     const int tid = threadIdx.x;
-    constexpr bool kQuadOk = !Q8 && RECIPE != DIRECT;
-    if (kQuadOk && spread_quad<RECIPE, Q8>(a)) {
-        const int64_t m = a.fail_list[slot];
-        const float *xr = a.xin + m * K;
-        __syncthreads();   // the previous item's readers of x2s
-        if (RECIPE == HIGGS && tid == 0) x2s = sum_squares_k<K>(xr);
+    {
         const int n = chunk * kScanQuadCodes + tid / 4;
         const int q = tid & 3;
         const int nc = n < a.N ? n : a.N - 1;
@@ -1784,8 +1780,63 @@ __device__ void spread_item(const StageArgs &a, int slot, int chunk, int &cur, f
         if (q == 0 && n < a.N) {
             const float v = RECIPE == OMNI ? __fadd_rn(dot, a.bias[n])
                                            : __fsub_rn(__fsub_rn(__fmul_rn(dot, 2.0f), x2s), a.e2[n]);
-            a.svals[static_cast<int64_t>(slot) * a.N + n] = v;
+            out[n] = v;
         }
+    }
+}
+// Every code's value (a.N <= kScanChunk) of the frame xs (LDS) into rv by one
+// kScanThreads block in the quad layout of quad_values, two kScanQuadCodes
+// chunks per pass with all their row reads issued together.  x2: the
+// frame's sum_rows(x*x) (Higgs).
+template <int RECIPE, int K>
+__device__ void block_values_quad(const StageArgs &a, const float *xs, float x2, float *rv) {
+    const int tid = threadIdx.x;
+    const int q = tid & 3, cl = tid >> 2;
+    const float sa = RECIPE == OMNI ? 2.0f : 1.0f;
+    constexpr int U = 2;
+    f32x4 vx[K / 16];
+#pragma unroll
+    for (int l = 0; l < K / 16; ++l) vx[l] = *reinterpret_cast<const f32x4 *>(xs + 16 * l + 4 * q);
+    for (int c0 = 0; c0 < a.N; c0 += U * kScanQuadCodes) {
+        f32x4 vc[U][K / 16];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int n = c0 + u * kScanQuadCodes + cl;
+            const float *cr = a.cbf + static_cast<int64_t>(n < a.N ? n : a.N - 1) * K;
+#pragma unroll
+            for (int l = 0; l < K / 16; ++l) vc[u][l] = *reinterpret_cast<const f32x4 *>(cr + 16 * l + 4 * q);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int l = 0; l < K / 16; ++l)
+#pragma unroll
+                for (int t = 0; t < 4; ++t) acc[t] = __fmaf_rn(vc[u][l][t] * sa, vx[l][t], acc[t]);
+            float t3[4], t6[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) t3[t] = __fadd_rn(__shfl_xor(acc[t], 2), acc[t]);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) t6[t] = __fadd_rn(__shfl_xor(t3[t], 1), t3[t]);
+            const float dot = __fadd_rn(__fadd_rn(t6[0], t6[2]), __fadd_rn(t6[1], t6[3]));
+            const int n = c0 + u * kScanQuadCodes + cl;
+            if (q == 0 && n < a.N)
+                rv[n] = RECIPE == OMNI ? __fadd_rn(dot, a.bias[n])
+                                       : __fsub_rn(__fsub_rn(__fmul_rn(dot, 2.0f), x2), a.e2[n]);
+        }
+    }
+}
+template <int RECIPE, bool Q8, int K>
+__device__ void spread_item(const StageArgs &a, int slot, int chunk, int &cur, float *xs, int8_t *xq, float *xd,
+                            float &x2s) {
+    const int tid = threadIdx.x;
+    constexpr bool kQuadOk = !Q8 && RECIPE != DIRECT;
+    if (kQuadOk && spread_quad<RECIPE, Q8>(a)) {
+        const int64_t m = a.fail_list[slot];
+        const float *xr = a.xin + m * K;
+        __syncthreads();   // the previous item's readers of x2s
+        if (RECIPE == HIGGS && tid == 0) x2s = sum_squares_k<K>(xr);
+        if constexpr (kQuadOk) quad_values<RECIPE, K>(a, a.svals + static_cast<int64_t>(slot) * a.N, chunk, xr, x2s);
         return;
     }
     if (slot != cur) {
@@ -3052,6 +3103,20 @@ __global__ __launch_bounds__(kCThreads, 1) void euclid_cascade_kernel(CascadeArg
 constexpr int kRsWaves = 4;
 constexpr int kRsThreads = kRsWaves * kWave;
 
+// The resident residual lives in accumulation registers (AGPRs): the sweep
+// keeps the architectural registers for its fragments, accumulators and
+// key lists, and the residual is read and written only between sweeps.
+__device__ inline float agpr_put(float x) {
+    float a;
+    asm("v_accvgpr_write_b32 %0, %1" : "=a"(a) : "v"(x));
+    return a;
+}
+__device__ inline float agpr_get(float a) {
+    float x;
+    asm("v_accvgpr_read_b32 %0, %1" : "=v"(x) : "a"(a));
+    return x;
+}
+
 template <int KS, int FG, int TOPL>
 struct RsLayout {
     static constexpr int K = KS * 32;
@@ -3098,7 +3163,8 @@ __global__ __launch_bounds__(kRsThreads, 1) void euclid_resident_kernel(CascadeA
     constexpr int kWaitLoads = 0x0070;   // s_waitcnt vmcnt(0) lgkmcnt(0)
     const int hsrc = threadIdx.x < T::CC ? threadIdx.x : 0;
 
-    // the stage-0 input, in the fragment layout (rows past M read row M - 1)
+    // the stage-0 input, in the fragment layout (rows past M read row M - 1),
+    // held in AGPRs
     float xr[FG][KS][8];
 #pragma unroll
     for (int g = 0; g < FG; ++g) {
@@ -3110,8 +3176,8 @@ __global__ __launch_bounds__(kRsThreads, 1) void euclid_resident_kernel(CascadeA
             const f32x4 hi = *reinterpret_cast<const f32x4 *>(row + ks * 32 + kq * 8 + 4);
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-                xr[g][ks][t] = lo[t];
-                xr[g][ks][4 + t] = hi[t];
+                xr[g][ks][t] = agpr_put(lo[t]);
+                xr[g][ks][4 + t] = agpr_put(hi[t]);
             }
         }
     }
@@ -3129,7 +3195,7 @@ __global__ __launch_bounds__(kRsThreads, 1) void euclid_resident_kernel(CascadeA
                 u32x4 packed;
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
-                    const float v0 = xr[g][ks][2 * t], v1 = xr[g][ks][2 * t + 1];
+                    const float v0 = agpr_get(xr[g][ks][2 * t]), v1 = agpr_get(xr[g][ks][2 * t + 1]);
                     const typename MX::V2 pr = {static_cast<typename MX::E>(v0), static_cast<typename MX::E>(v1)};
                     const unsigned w = __builtin_bit_cast(unsigned, pr);
                     packed[t] = w;
@@ -3201,17 +3267,15 @@ __global__ __launch_bounds__(kRsThreads, 1) void euclid_resident_kernel(CascadeA
 #pragma unroll
         for (int g = 0; g < FG; ++g) accp[g] = f32x4{-3.40282347e38f, -3.40282347e38f, -3.40282347e38f, -3.40282347e38f};
         unsigned lprev = 0;
-        auto epilogue = [&](const f32x4 (&acc)[FG], unsigned local0) {
+        // key e (< 4 FG) of the previous block's sums into its group's list
+        auto insert_key = [&](const f32x4 (&acc)[FG], unsigned local0, int e) {
+            const int g = e / 4, i = e % 4;
+            const float key = key_of(acc[g][i], local0 + i, vkeep);
 #pragma unroll
-            for (int g = 0; g < FG; ++g)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float key = key_of(acc[g][i], local0 + i, vkeep);
-#pragma unroll
-                    for (int j = TOPL - 1; j > 0; --j) top[g][j] = __builtin_amdgcn_fmed3f(top[g][j - 1], top[g][j], key);
-                    top[g][0] = __builtin_amdgcn_fmed3f(top[g][0], key, 3.40282347e38f);
-                }
+            for (int j = TOPL - 1; j > 0; --j) top[g][j] = __builtin_amdgcn_fmed3f(top[g][j - 1], top[g][j], key);
+            top[g][0] = __builtin_amdgcn_fmed3f(top[g][0], key, 3.40282347e38f);
         };
+        constexpr int E = 4 * FG;   // keys per block and lane
         for (int ch = 0; ch < nch; ++ch) {
             const int buf = ch & 1;
             const int cs = ch + 1 < nch ? ch + 1 : ch;   // the last chunk re-stages itself (no branch)
@@ -3223,27 +3287,31 @@ __global__ __launch_bounds__(kRsThreads, 1) void euclid_resident_kernel(CascadeA
                     if (k < LY::STAGE16) stage_piece(buf ^ 1, cs, k);
                 }
                 if (b == 0) stage_h(buf ^ 1, cs);
+                const f32x4 hnext = b + 1 < BPC ? lds_h(buf, b + 1) : hcur;
                 f32x4 acc[FG];
 #pragma unroll
                 for (int g = 0; g < FG; ++g) acc[g] = hcur;
+                // One wave per SIMD hides no latency behind another wave:
+                // scheduling barriers keep each step's fragment load L steps
+                // ahead of its MFMAs (the compiler would sink it next to
+                // them), and each step takes its share of the previous
+                // block's keys.
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks) {
                     const int pk = ks + L;
                     if (pk < KS) ring[pk % R] = lds_a(buf, b, pk);
                     else if (b + 1 < BPC) ring[pk % R] = lds_a(buf, b + 1, pk - KS);
+                    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                     for (int g = 0; g < FG; ++g)
                         acc[g] = MX::mfma(ring[ks % R], __builtin_bit_cast(typename MX::V8, xb[g][ks]), acc[g]);
-                }
-                epilogue(accp, lprev);
-                if (b + 1 < BPC) hcur = lds_h(buf, b + 1);
 #pragma unroll
-                for (int q = 0; q < KS * FG; ++q) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
-                    __builtin_amdgcn_sched_group_barrier(0x002, (4 * 4 * FG + 4 * FG) / (KS * FG) + 1, 0);   // VALU
+                    for (int e = ks * E / KS; e < (ks + 1) * E / KS; ++e) insert_key(accp, lprev, e);
+                    __builtin_amdgcn_sched_barrier(0);
                 }
 #pragma unroll
                 for (int g = 0; g < FG; ++g) accp[g] = acc[g];
+                hcur = hnext;
                 lprev = static_cast<unsigned>((ch * BPC + b) * 4);
             }
             __builtin_amdgcn_s_waitcnt(kWaitLoads);
@@ -3252,7 +3320,8 @@ __global__ __launch_bounds__(kRsThreads, 1) void euclid_resident_kernel(CascadeA
             for (int l = 0; l < L; ++l) ring[l] = lds_a(buf ^ 1, 0, l);
             hcur = lds_h(buf ^ 1, 0);
         }
-        epilogue(accp, lprev);
+#pragma unroll
+        for (int e = 0; e < E; ++e) insert_key(accp, lprev, e);
         __syncthreads();   // every wave is done with the chunk buffers
 
         // ---- select and residual update of the wave's groups ----
@@ -3267,8 +3336,10 @@ __global__ __launch_bounds__(kRsThreads, 1) void euclid_resident_kernel(CascadeA
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
                 float *d = xs + col * LY::XSTR + ks * 32 + kq * 8;
-                *reinterpret_cast<f32x4 *>(d) = f32x4{xr[g][ks][0], xr[g][ks][1], xr[g][ks][2], xr[g][ks][3]};
-                *reinterpret_cast<f32x4 *>(d + 4) = f32x4{xr[g][ks][4], xr[g][ks][5], xr[g][ks][6], xr[g][ks][7]};
+                *reinterpret_cast<f32x4 *>(d) = f32x4{agpr_get(xr[g][ks][0]), agpr_get(xr[g][ks][1]),
+                                                      agpr_get(xr[g][ks][2]), agpr_get(xr[g][ks][3])};
+                *reinterpret_cast<f32x4 *>(d + 4) = f32x4{agpr_get(xr[g][ks][4]), agpr_get(xr[g][ks][5]),
+                                                          agpr_get(xr[g][ks][6]), agpr_get(xr[g][ks][7])};
             }
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
@@ -3296,7 +3367,8 @@ __global__ __launch_bounds__(kRsThreads, 1) void euclid_resident_kernel(CascadeA
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-                    for (int t = 0; t < 8; ++t) xr[g][ks][t] = __fsub_rn(xr[g][ks][t], cv[ks][t / 4][t % 4]);
+                    for (int t = 0; t < 8; ++t)
+                        xr[g][ks][t] = agpr_put(__fsub_rn(agpr_get(xr[g][ks][t]), cv[ks][t / 4][t % 4]));
             }
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
@@ -3314,9 +3386,9 @@ __global__ __launch_bounds__(kRsThreads, 1) void euclid_resident_kernel(CascadeA
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
                 *reinterpret_cast<f32x4 *>(row + ks * 32 + kq * 8) =
-                    f32x4{xr[g][ks][0], xr[g][ks][1], xr[g][ks][2], xr[g][ks][3]};
+                    f32x4{agpr_get(xr[g][ks][0]), agpr_get(xr[g][ks][1]), agpr_get(xr[g][ks][2]), agpr_get(xr[g][ks][3])};
                 *reinterpret_cast<f32x4 *>(row + ks * 32 + kq * 8 + 4) =
-                    f32x4{xr[g][ks][4], xr[g][ks][5], xr[g][ks][6], xr[g][ks][7]};
+                    f32x4{agpr_get(xr[g][ks][4]), agpr_get(xr[g][ks][5]), agpr_get(xr[g][ks][6]), agpr_get(xr[g][ks][7])};
             }
         }
     }
@@ -3327,12 +3399,24 @@ __global__ __launch_bounds__(kRsThreads, 1) void euclid_resident_kernel(CascadeA
 // codes where given), into xs (every thread of the block).
 __device__ inline void replay_residual(const CascadeArgs &c, int64_t m, int s, float *xs, int K) {
     const StageArgs &a = c.a;
+    const int32_t *codes = (a.force_idx ? a.force_idx : a.idx) + m * a.Q;
+    constexpr int B = 8;   // stages whose codes and rows are read together
     for (int k = threadIdx.x; k < K; k += blockDim.x) {
         float v = c.x0[m * K + k];
-        for (int t = 0; t < s; ++t) {
-            int u = a.force_idx ? a.force_idx[m * a.Q + t] : a.idx[m * a.Q + t];
-            if (u < 0 || u >= a.N) u = 0;
-            v = __fsub_rn(v, a.cbf[(static_cast<int64_t>(t) * a.N + u) * K + k]);
+        for (int t0 = 0; t0 < s; t0 += B) {
+            int u[B];
+#pragma unroll
+            for (int j = 0; j < B; ++j) {
+                u[j] = t0 + j < s ? codes[t0 + j] : 0;
+                if (u[j] < 0 || u[j] >= a.N) u[j] = 0;
+            }
+            float cv[B];
+#pragma unroll
+            for (int j = 0; j < B; ++j)
+                cv[j] = t0 + j < s ? a.cbf[(static_cast<int64_t>(t0 + j) * a.N + u[j]) * K + k] : 0.0f;
+#pragma unroll
+            for (int j = 0; j < B; ++j)
+                if (t0 + j < s) v = __fsub_rn(v, cv[j]);
         }
         xs[k] = v;
     }
@@ -3355,7 +3439,24 @@ __device__ inline bool same_bits(float x, float y) { return __float_as_uint(x) =
 // block per pair: the stage's input residual is replayed, every code's
 // recipe value computed and the reference's selection made (the exact
 // scan's); where the code, distance or top-k differ from the cascade's,
-// the frame's earliest wrong stage is recorded for the fix-up.
+// the frame's earliest wrong stage is recorded for the fix-up.  F32
+// codebooks of up to kScanChunk codes in tinyBLAS order take the values in
+// the quad layout (coalesced row reads, many in flight).
+template <int RECIPE, bool Q8, int KS>
+__device__ inline void scan_frame(const StageArgs &a, const float *xs, const int8_t *xq, const float *xd, ScanSh &sh) {
+    constexpr int K = KS * 32;
+    constexpr bool kQuadOk = !Q8 && RECIPE != DIRECT;
+    if constexpr (kQuadOk) {
+        if (spread_quad<RECIPE, Q8>(a) && a.N <= kScanChunk) {
+            block_values_quad<RECIPE, K>(a, xs, sh.o_x2, sh.rv);
+            __syncthreads();
+            scan_select<RECIPE, Q8, KS>(a, K, true, sh.rv, xs, xq, xd, sh.o_x2, sh);
+            return;
+        }
+    }
+    scan_select<RECIPE, Q8, KS>(a, K, false, nullptr, xs, xq, xd, sh.o_x2, sh);
+}
+
 template <int RECIPE, bool Q8, int KS>
 __global__ __launch_bounds__(kScanThreads) void euclid_verify_kernel(CascadeArgs c) {
     constexpr int K = KS * 32;
@@ -3372,7 +3473,7 @@ __global__ __launch_bounds__(kScanThreads) void euclid_verify_kernel(CascadeArgs
         __syncthreads();
         replay_residual(c, m, s, xs, K);
         scan_prepare<RECIPE, Q8, KS>(xs, xq, xd, sh);
-        scan_select<RECIPE, Q8, KS>(a, K, false, nullptr, xs, xq, xd, sh.o_x2, sh);
+        scan_frame<RECIPE, Q8, KS>(a, xs, xq, xd, sh);
         __syncthreads();
         if (threadIdx.x == 0) {
             const int64_t o = m * a.Q + s;
@@ -3406,7 +3507,7 @@ __global__ __launch_bounds__(kScanThreads) void euclid_fixup_kernel(CascadeArgs 
         for (int s = t0; s < c.a.Q; ++s) {
             const StageArgs a = cascade_stage(c, s, K);
             scan_prepare<RECIPE, Q8, KS>(xs, xq, xd, sh);
-            scan_select<RECIPE, Q8, KS>(a, K, false, nullptr, xs, xq, xd, sh.o_x2, sh);
+            scan_frame<RECIPE, Q8, KS>(a, xs, xq, xd, sh);
             __syncthreads();
             const int64_t o = m * a.Q + s;
             if (threadIdx.x == 0) {
