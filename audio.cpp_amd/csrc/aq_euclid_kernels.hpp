@@ -600,6 +600,51 @@ __device__ inline float row_ror_add(float v) {
     return __fadd_rn(v, __int_as_float(o));
 }
 
+// The values of x at the lane's column in each of the wave's four 16-lane
+// rows (out[q] = x of lane col + 16 q), by three gfx950 lane-swap
+// instructions instead of LDS permutes: permlane16_swap(x, x) gives rows
+// (r & 2) and (r & 2) + 1 at a lane of row r, permlane32_swap of each then
+// rows 0, 2 and 1, 3.
+__device__ inline void rows4_u(unsigned x, unsigned (&out)[4]) {
+    const auto ab = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    const auto a = __builtin_amdgcn_permlane32_swap(ab[0], ab[0], false, false);
+    const auto b = __builtin_amdgcn_permlane32_swap(ab[1], ab[1], false, false);
+    out[0] = a[0];
+    out[1] = b[0];
+    out[2] = a[1];
+    out[3] = b[1];
+}
+__device__ inline void rows4(float x, float (&out)[4]) {
+    unsigned u[4];
+    rows4_u(__float_as_uint(x), u);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) out[q] = __uint_as_float(u[q]);
+}
+__device__ inline void rows4(int x, int (&out)[4]) {
+    unsigned u[4];
+    rows4_u(static_cast<unsigned>(x), u);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) out[q] = static_cast<int>(u[q]);
+}
+__device__ inline double row_bcast(double x, int q) {
+    unsigned lo[4], hi[4];
+    const uint64_t b = __double_as_longlong(x);
+    rows4_u(static_cast<unsigned>(b), lo);
+    rows4_u(static_cast<unsigned>(b >> 32), hi);
+    return __longlong_as_double(static_cast<long long>((static_cast<uint64_t>(hi[q]) << 32) | lo[q]));
+}
+// max and sum over the four rows (every lane of a column gets the same value)
+__device__ inline float rows_max(float x) {
+    float r[4];
+    rows4(x, r);
+    return fmaxf(fmaxf(r[0], r[1]), fmaxf(r[2], r[3]));
+}
+__device__ inline float rows_sum(float x) {
+    float r[4];
+    rows4(x, r);
+    return (r[0] + r[1]) + (r[2] + r[3]);
+}
+
 // The query's Q8_0 image x_q = q * d of one 32-wide block (x86
 // quantize_row_q8_0: d = fp16(amax/127), q = round-half-even(x * 127/amax)),
 // held by 4 lanes 16 apart with 8 elements each.  x_q is exact in fp32
@@ -608,8 +653,7 @@ __device__ inline void q8_image_block(float (&v)[8]) {
     float am = 0.0f;
 #pragma unroll
     for (int t = 0; t < 8; ++t) am = fmaxf(am, fabsf(v[t]));
-    am = fmaxf(am, __shfl_xor(am, 16));
-    am = fmaxf(am, __shfl_xor(am, 32));
+    am = rows_max(am);
     const float dq = static_cast<float>(static_cast<_Float16>(__fdiv_rn(am, 127.0f)));
     const float id = am != 0.0f ? __fdiv_rn(127.0f, am) : 0.0f;
 #pragma unroll
@@ -691,12 +735,9 @@ __global__ __launch_bounds__(kThreads, sweep_blocks_per_cu(KS)) void euclid_swee
             }
             xb[g][ks] = packed;
         }
-        sx += __shfl_xor(sx, 16);
-        sx += __shfl_xor(sx, 32);
-        sd += __shfl_xor(sd, 16);
-        sd += __shfl_xor(sd, 32);
-        sxx += __shfl_xor(sxx, 16);
-        sxx += __shfl_xor(sxx, 32);
+        sx = rows_sum(sx);
+        sd = rows_sum(sd);
+        sxx = rows_sum(sxx);
         nx2[g] = sx;
         nd2[g] = sd;
         nxx2[g] = sxx;
@@ -1010,19 +1051,14 @@ __device__ int select_group(const StageArgs &a, int64_t m_base, const float (&to
         float all[4 * TOPL];
 #pragma unroll
         for (int j = 0; j < TOPL; ++j) {
-            const float k0 = top[g][j];
-            const float k1 = __shfl_xor(k0, 16);
-            const float k2 = __shfl_xor(k0, 32);
-            const float k3 = __shfl_xor(k1, 32);
-            all[4 * j + 0] = k0;
-            all[4 * j + 1] = k1;
-            all[4 * j + 2] = k2;
-            all[4 * j + 3] = k3;
+            float kr[4];
+            rows4(top[g][j], kr);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) all[4 * j + q] = kr[q];
         }
         // tau bounds every key a lane dropped; vT is the T-th largest kept key.
         float tau = taul[g];
-        tau = fmaxf(tau, __shfl_xor(tau, 16));
-        tau = fmaxf(tau, __shfl_xor(tau, 32));
+        tau = rows_max(tau);
         float best[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
 #pragma unroll
         for (int t = 0; t < 4 * TOPL; ++t) {
@@ -1090,7 +1126,7 @@ __device__ int select_group(const StageArgs &a, int64_t m_base, const float (&to
                         for (int i = 0; i < 16; ++i)
 #pragma unroll
                             for (int t = 0; t < 4; ++t) sq += static_cast<double>(__fmul_rn(v[i][t], v[i][t]));
-                    sq = __shfl(sq, col + 16 * q);
+                    sq = row_bcast(sq, q);
                 }
                 if (Q8) {
 #pragma unroll
@@ -1282,11 +1318,15 @@ __device__ int select_group(const StageArgs &a, int64_t m_base, const float (&to
             // without top-k); a slot no frame of the wave fills is skipped.
 #pragma unroll
             for (int j = 0; j < TOPL; ++j) {
+                int cnq[4];
+                float cvq[4];
+                rows4(cand_n[g][j], cnq);
+                rows4(cand_val[j], cvq);
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
-                    int cn = __shfl(cand_n[g][j], col + 16 * q);
+                    int cn = cnq[q];
                     if (!__any(cn >= 0)) continue;
-                    float cv = __shfl(cand_val[j], col + 16 * q);
+                    float cv = cvq[q];
                     if (Tsel == 1) {
                         const bool take = cn >= 0 && (sel_n[0] < 0 || ranks_before<RECIPE>(cv, cn, sel_v[0], sel_n[0]));
                         sel_v[0] = take ? cv : sel_v[0];
@@ -1347,8 +1387,11 @@ __device__ int select_group(const StageArgs &a, int64_t m_base, const float (&to
             const bool mine = top[g][0] == kb;
             const unsigned local = __float_as_uint(kb) & kmask;
             int n = mine ? static_cast<int>((local >> 2) * 16 + kq * 4 + (local & 3)) : 0x7fffffff;
-            n = min(n, __shfl_xor(n, 16));
-            n = min(n, __shfl_xor(n, 32));
+            {
+                int nq[4];
+                rows4(n, nq);
+                n = min(min(nq[0], nq[1]), min(nq[2], nq[3]));
+            }
             win_code[g] = n;
             ok = ok && n < N;
         }
@@ -2920,12 +2963,9 @@ __global__ __launch_bounds__(kCThreads, 1) void euclid_cascade_kernel(CascadeArg
                 }
                 xb[g][ks] = packed;
             }
-            sx += __shfl_xor(sx, 16);
-            sx += __shfl_xor(sx, 32);
-            sd += __shfl_xor(sd, 16);
-            sd += __shfl_xor(sd, 32);
-            sxx += __shfl_xor(sxx, 16);
-            sxx += __shfl_xor(sxx, 32);
+            sx = rows_sum(sx);
+            sd = rows_sum(sd);
+            sxx = rows_sum(sxx);
             nx2[g] = sx;
             nd2[g] = sd;
             nxx2[g] = sxx;
@@ -3210,12 +3250,9 @@ __global__ __launch_bounds__(kRsThreads, 1) void euclid_resident_kernel(CascadeA
                 }
                 xb[g][ks] = packed;
             }
-            sx += __shfl_xor(sx, 16);
-            sx += __shfl_xor(sx, 32);
-            sd += __shfl_xor(sd, 16);
-            sd += __shfl_xor(sd, 32);
-            sxx += __shfl_xor(sxx, 16);
-            sxx += __shfl_xor(sxx, 32);
+            sx = rows_sum(sx);
+            sd = rows_sum(sd);
+            sxx = rows_sum(sxx);
             nx2[g] = sx;
             nd2[g] = sd;
             nxx2[g] = sxx;
