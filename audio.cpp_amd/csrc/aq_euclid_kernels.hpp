@@ -208,6 +208,13 @@ using CascadeFn = void (*)(CascadeArgs);
 constexpr int groups_for(int ks) { return ks <= 2 ? 4 : (ks <= 8 ? 3 : 2); }
 // Sweep blocks resident per CU (the launch bound the register budget follows).
 constexpr int sweep_blocks_per_cu(int ks) { return ks <= 8 ? 2 : 1; }
+// LDS chunk buffers of the sweep: two where two blocks share a CU; four for
+// one block per CU, so that a chunk's codebook loads are issued two chunks
+// before it is read (a chunk of the widest codebooks is a single 16-code
+// block, too short to hide a global load behind).
+constexpr int sweep_buffers(int ks) { return sweep_blocks_per_cu(ks) == 1 ? 4 : 2; }
+template <int KS>
+constexpr int sweep_lds_bytes() { return sweep_buffers(KS) * Tile<KS>::BUFB; }
 
 // Kernels of one codebook width (K = 32 * KS), built in their own
 // translation unit (aq_euclid_ks<KS>.hip).  Recipe variants: 0 OmniVoice,
@@ -759,24 +766,24 @@ __global__ __launch_bounds__(kThreads, sweep_blocks_per_cu(KS)) void euclid_swee
     // Software pipeline over 16-code blocks (chunk c holds blocks b = 0 ..
     // BPC-1; the block loop is unrolled so that a chunk is one basic block):
     //  * A fragments live in a ring of R registers, loaded L = R-1 K-slices
-    //    ahead (across the block boundary inside a chunk);
-    //  * the epilogue of the previous block is interleaved with this block's
-    //    MFMAs (sched_group_barrier): one wave per SIMD issues in order, so
-    //    the VALU work only overlaps the matrix pipe when it sits between
-    //    the MFMAs;
-    //  * the next chunk is staged into the other LDS buffer a few 16-byte
-    //    pieces per block, with one barrier per chunk.  Where a chunk holds
-    //    several blocks the pieces go straight from global memory to LDS
-    //    (global_load_lds: no registers, and nothing waits for them before
-    //    the chunk's end); a one-block chunk (K = 768) stages them through
-    //    registers (global load in the block, LDS store after it), which
-    //    measured faster there.  The last chunk re-stages itself into the
-    //    idle buffer, which keeps the loop free of branches.
+    //    ahead (across the block boundary inside a chunk); scheduling
+    //    barriers between the slices keep the loads there;
+    //  * each K-slice's MFMAs carry a share of the previous block's
+    //    epilogue (the VALU work costs issue cycles of the SIMD either way;
+    //    spread out, it waits on no MFMA result);
+    //  * chunk c + NB - 1 is staged into the buffer chunk c - 1 left, a few
+    //    16-byte pieces per block, straight from global memory to LDS
+    //    (global_load_lds: no registers); at the chunk's end only chunk
+    //    c + 1's loads are waited for, then one barrier.  Chunks past the
+    //    last re-stage the last into the idle buffer, which keeps the loop
+    //    free of branches.
+    constexpr int NB = sweep_buffers(KS);
     constexpr int BPC = T::CC / 16;
-    constexpr int R = KS % 4 == 0 ? 4 : 2;
+    // ring depth: fewer frame groups per wave give fewer MFMAs per slice,
+    // so the loads run more slices ahead
+    constexpr int R = KS % 4 != 0 ? 2 : (FG <= 2 ? 8 : 4);
     constexpr int L = R - 1;
     constexpr int PPB = (T::STAGE16 + BPC - 1) / BPC;   // staged pieces per block
-    constexpr bool kDirect = BPC > 1;
 
     auto lds_a = [&](int buf, int blk, int ks) -> typename MX::V8 {
         const int r = blk * 16 + col;
@@ -786,16 +793,8 @@ __global__ __launch_bounds__(kThreads, sweep_blocks_per_cu(KS)) void euclid_swee
     auto lds_h = [&](int buf, int blk) -> f32x4 {
         return *reinterpret_cast<const f32x4 *>(lds + buf * T::BUFB + T::CHUNKB + (blk * 16 + kq * 4) * 4);
     };
-    auto piece_dst = [&](int buf, int p) -> u32x4 * {
-        const int r = p / T::CH16, j = p % T::CH16;
-        return reinterpret_cast<u32x4 *>(lds + buf * T::BUFB + r * T::ROWB + ((j ^ (r & T::SWZ)) * 16));
-    };
     // Every thread stages one |c|^2/2 slot (threads >= CC write a slot past
     // the chunk's, which nothing reads): no divergent branch.
-    auto h_dst = [&](int buf) -> float * {
-        return reinterpret_cast<float *>(lds + buf * T::BUFB + T::CHUNKB) + threadIdx.x;
-    };
-    const u32x4 *cb16 = reinterpret_cast<const u32x4 *>(a.cbh);
     const int hsrc = threadIdx.x < T::CC ? threadIdx.x : 0;
     // Direct staging: the 16 bytes of lane l of wave w land at LDS piece
     // q = k * kThreads + 64 w + l (a wave's 64 pieces are contiguous, as the
@@ -817,23 +816,21 @@ __global__ __launch_bounds__(kThreads, sweep_blocks_per_cu(KS)) void euclid_swee
         __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)g,
                                          (__attribute__((address_space(3))) void *)d, 4, 0, 0);
     };
-    // s_waitcnt vmcnt(0) lgkmcnt(0): this wave's direct loads have landed
-    constexpr int kWaitLoads = 0x0070;
+    // s_waitcnt vmcnt(n) (no other counter): at most n of this wave's
+    // global loads still in flight; a chunk is STAGE16 + 1 of them
+    constexpr int kPerChunk = T::STAGE16 + 1;
+    constexpr int kWaitNext = ((kPerChunk * (NB - 2)) & 15) | (((kPerChunk * (NB - 2)) >> 4) << 14) | 0x0070 | 0x0F00;
+    static_assert(kPerChunk * (NB - 2) < 64, "vmcnt holds 6 bits");
 
-    // prologue: chunk 0 in full
-    if constexpr (kDirect) {
+    // prologue: chunks c0 .. c0 + NB - 2, and wait for the first
 #pragma unroll
-        for (int k = 0; k < T::STAGE16; ++k) stage_piece(0, c0, k);
-        stage_h(0, c0);
-        __builtin_amdgcn_s_waitcnt(kWaitLoads);
-    } else {
+    for (int q = 0; q < NB - 1; ++q) {
+        const int cq = c0 + q < c1 ? c0 + q : c1 - 1;
 #pragma unroll
-        for (int k = 0; k < T::STAGE16; ++k) {
-            const int p = threadIdx.x + k * kThreads;
-            *piece_dst(0, p) = cb16[static_cast<int64_t>(c0) * (T::CHUNKB / 16) + p];
-        }
-        *h_dst(0) = a.nhh[static_cast<int64_t>(c0) * T::CC + hsrc];
+        for (int k = 0; k < T::STAGE16; ++k) stage_piece(q, cq, k);
+        stage_h(q, cq);
     }
+    __builtin_amdgcn_s_waitcnt(kWaitNext);
     __syncthreads();
 
     typename MX::V8 ring[R];
@@ -848,98 +845,70 @@ __global__ __launch_bounds__(kThreads, sweep_blocks_per_cu(KS)) void euclid_swee
 #pragma unroll
     for (int g = 0; g < FG; ++g) accp[g] = f32x4{-3.40282347e38f, -3.40282347e38f, -3.40282347e38f, -3.40282347e38f};
     unsigned lprev = 0;
-    u32x4 stg[PPB];
-    float hstg = 0.0f;
 
     // Per score: key (1 op), TOPL-1 med3 and one max-by-med3.  The upper
     // clamp is FLT_MAX rather than +inf so the compiler keeps a plain med3
     // (an fmax would need NaN canonicalisation of both operands); frames with
     // a key of +inf or NaN fail the certificate in any case.
+    // key e (< 4 FG) of a block's sums into its group's list
+    auto insert_key = [&](const f32x4 (&acc)[FG], unsigned local0, int e) {
+        const int g = e / 4, i = e % 4;
+        const float key = key_of(acc[g][i], local0 + i, vkeep);
+#pragma unroll
+        for (int j = TOPL - 1; j > 0; --j) top[g][j] = __builtin_amdgcn_fmed3f(top[g][j - 1], top[g][j], key);
+        top[g][0] = __builtin_amdgcn_fmed3f(top[g][0], key, 3.40282347e38f);
+    };
     auto epilogue = [&](const f32x4 (&acc)[FG], unsigned local0) {
 #pragma unroll
-        for (int g = 0; g < FG; ++g)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float key = key_of(acc[g][i], local0 + i, vkeep);
-#pragma unroll
-                for (int j = TOPL - 1; j > 0; --j) top[g][j] = __builtin_amdgcn_fmed3f(top[g][j - 1], top[g][j], key);
-                top[g][0] = __builtin_amdgcn_fmed3f(top[g][0], key, 3.40282347e38f);
-            }
+        for (int e = 0; e < 4 * FG; ++e) insert_key(acc, local0, e);
     };
 
     for (int c = c0; c < c1; ++c) {
-        const int buf = (c - c0) & 1;
-        const int cs = c + 1 < c1 ? c + 1 : c;
-        const u32x4 *src = cb16 + static_cast<int64_t>(cs) * (T::CHUNKB / 16);
+        const int buf = (c - c0) % NB;
+        const int sbuf = (buf + NB - 1) % NB;   // left by chunk c - 1
+        const int cs = c + NB - 1 < c1 ? c + NB - 1 : c1 - 1;
 #pragma unroll
         for (int b = 0; b < BPC; ++b) {
-            if constexpr (kDirect) {
-                // this block's share of the next chunk, straight into LDS
+            // this block's share of chunk cs, straight into LDS
 #pragma unroll
-                for (int i = 0; i < PPB; ++i) {
-                    const int k = b + i * BPC;
-                    if (k < T::STAGE16) stage_piece(buf ^ 1, cs, k);
-                }
-                if (b == 0) stage_h(buf ^ 1, cs);
-            } else {
-                // store the pieces fetched in the previous block, fetch this block's
-                if (b > 0) {
-#pragma unroll
-                    for (int i = 0; i < PPB; ++i) {
-                        const int k = (b - 1) + i * BPC;
-                        if (k < T::STAGE16) *piece_dst(buf ^ 1, threadIdx.x + k * kThreads) = stg[i];
-                    }
-                    if (b == 1) *h_dst(buf ^ 1) = hstg;
-                }
-#pragma unroll
-                for (int i = 0; i < PPB; ++i) {
-                    const int k = b + i * BPC;
-                    if (k < T::STAGE16) stg[i] = src[threadIdx.x + k * kThreads];
-                }
-                if (b == 0) hstg = a.nhh[static_cast<int64_t>(cs) * T::CC + hsrc];
+            for (int i = 0; i < PPB; ++i) {
+                const int k = b + i * BPC;
+                if (k < T::STAGE16) stage_piece(sbuf, cs, k);
             }
+            if (b == 0) stage_h(sbuf, cs);
 
             // the accumulators start from -|c|^2/2 of the block's codes
+            const f32x4 hnext = b + 1 < BPC ? lds_h(buf, b + 1) : hcur;
             f32x4 acc[FG];
 #pragma unroll
             for (int g = 0; g < FG; ++g) acc[g] = hcur;
+            // Scheduling barriers keep each K-slice's fragment load L slices
+            // ahead of its MFMAs (the compiler would sink it next to them);
+            // each slice takes its share of the previous block's epilogue.
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
                 const int pk = ks + L;
                 if (pk < KS) ring[pk % R] = lds_a(buf, b, pk);
                 else if (b + 1 < BPC) ring[pk % R] = lds_a(buf, b + 1, pk - KS);
+                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int g = 0; g < FG; ++g)
                     acc[g] = MX::mfma(ring[ks % R], __builtin_bit_cast(typename MX::V8, xb[g][ks]), acc[g]);
-            }
-            epilogue(accp, lprev);
-            if (b + 1 < BPC) hcur = lds_h(buf, b + 1);
-            // Issue order for the block: MFMAs with the previous block's
-            // epilogue (4 VALU per score) spread between them.
 #pragma unroll
-            for (int i = 0; i < KS * FG; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
-                __builtin_amdgcn_sched_group_barrier(0x002, (4 * 4 * FG + 4 * FG) / (KS * FG) + 1, 0);   // VALU
+                for (int e = ks * 4 * FG / KS; e < (ks + 1) * 4 * FG / KS; ++e) insert_key(accp, lprev, e);
+                __builtin_amdgcn_sched_barrier(0);
             }
+            hcur = hnext;
 #pragma unroll
             for (int g = 0; g < FG; ++g) accp[g] = acc[g];
             lprev = static_cast<unsigned>((c * BPC + b) * 4);
         }
-        if constexpr (kDirect) {
-            __builtin_amdgcn_s_waitcnt(kWaitLoads);
-        } else {
-            // the pieces fetched in the chunk's last block
-#pragma unroll
-            for (int i = 0; i < PPB; ++i) {
-                const int k = (BPC - 1) + i * BPC;
-                if (k < T::STAGE16) *piece_dst(buf ^ 1, threadIdx.x + k * kThreads) = stg[i];
-            }
-            if (BPC == 1) *h_dst(buf ^ 1) = hstg;
-        }
+        __builtin_amdgcn_s_waitcnt(kWaitNext);   // chunk c + 1 has landed (this wave's part)
         __syncthreads();
+        const int nbuf = (buf + 1) % NB;
 #pragma unroll
-        for (int l = 0; l < L; ++l) ring[l] = lds_a(buf ^ 1, 0, l);
-        hcur = lds_h(buf ^ 1, 0);
+        for (int l = 0; l < L; ++l) ring[l] = lds_a(nbuf, 0, l);
+        hcur = lds_h(nbuf, 0);
     }
     epilogue(accp, lprev);
 
@@ -3629,7 +3598,7 @@ constexpr int resident_lds_bytes() {
              euclid_refine_select_kernel<DIRECT, false, KS>, euclid_refine_select_kernel<HIGGS, true, KS>},     \
             {euclid_exact_scan_kernel<OMNI, false, KS>, euclid_exact_scan_kernel<HIGGS, false, KS>,             \
              euclid_exact_scan_kernel<DIRECT, false, KS>, euclid_exact_scan_kernel<HIGGS, true, KS>},           \
-            Tile<KS>::LDS,                                                                                      \
+            sweep_lds_bytes<KS>(),                                                                              \
             Tile<KS>::CC,                                                                                       \
             {{cascade_fn<OMNI, false, KS, 3>(), cascade_fn<OMNI, false, KS, 4>()},                              \
              {cascade_fn<HIGGS, false, KS, 3>(), cascade_fn<HIGGS, false, KS, 4>()},                            \
