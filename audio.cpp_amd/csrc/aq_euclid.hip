@@ -847,6 +847,22 @@ aq_status euclid_encode_impl(aq_ctx *ctx, const aq_codebooks *cb, const aq_frame
     int nsplit = 1;
     for (int sp = 1; sp <= 4; ++sp)
         if (nch % sp == 0 && tiles * sp <= 2 * cus) nsplit = sp;
+    // Grids of several rounds: the split count whose last round of blocks is
+    // fullest, at a small price per split (each split loads its frames again
+    // and the select merges one more key list).
+    if (tiles > 2 * cus) {
+        const int64_t slots = static_cast<int64_t>(cus) * sweep_blocks_per_cu(ks);
+        double best = 1e30;
+        for (int sp : {1, 2, 4}) {
+            if (nch % sp != 0) continue;
+            const int64_t blocks = (tiles + 7) / 8 * 8 * sp;
+            const double rounds = static_cast<double>((blocks + slots - 1) / slots) / sp * (1.0 + 0.03 * (sp - 1));
+            if (rounds < best) {
+                best = rounds;
+                nsplit = sp;
+            }
+        }
+    }
     const int64_t ngroups = (M + 15) / 16;
 
     // Work buffers: the residual (the caller's buffer when given; [M, H]),

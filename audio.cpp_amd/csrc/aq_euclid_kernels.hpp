@@ -204,8 +204,10 @@ using RefineFn = void (*)(StageArgs, RefArgs);
 using CascadeFn = void (*)(CascadeArgs);
 
 // 16-frame groups per sweep wave: the fp16 frames of a wave stay in
-// registers (4 * KS registers per group), so wider codebooks take fewer.
-constexpr int groups_for(int ks) { return ks <= 2 ? 4 : (ks <= 8 ? 3 : 2); }
+// registers (4 * KS registers per group), so wider codebooks take fewer;
+// K = 768 takes three again, its fragments partly in AGPRs (one wave per
+// SIMD), for one A-fragment read per three MFMAs.
+constexpr int groups_for(int ks) { return ks <= 2 ? 4 : (ks <= 8 ? 3 : (ks <= 16 ? 2 : 3)); }
 // Sweep blocks resident per CU (the launch bound the register budget follows).
 constexpr int sweep_blocks_per_cu(int ks) { return ks <= 8 ? 2 : 1; }
 // LDS chunk buffers of the sweep: two where two blocks share a CU; four for
