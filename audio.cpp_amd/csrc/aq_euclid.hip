@@ -668,32 +668,37 @@ aq_status euclid_encode_any(aq_ctx *ctx, const aq_codebooks *cb, const aq_frames
     return AQ_OK;
 }
 
-// Whether encodes take the one-launch cascade (AQ_EUCLID_PIPELINE=stages
-// selects the per-stage pipeline instead, =cascade the cascade that keeps the
-// residual in memory where the register-resident one exists, for
-// comparisons).
-bool cascade_enabled() {
+// The encode pipeline of a plain codebook: the register-resident one-launch
+// cascade where it exists (f32 codebooks at K = 256), else the per-stage
+// pipeline.  The one-launch cascade that keeps the residual in memory
+// measured no faster than the per-stage pipeline at K = 256 and slower for
+// Q8_0 codebooks (its verification then scans 2-3 % of the frames); it runs
+// when AQ_EUCLID_PIPELINE=cascade asks for it (comparisons and tests), as
+// AQ_EUCLID_PIPELINE=stages asks for the per-stage pipeline.
+enum class Pipeline { kStages, kCascade, kResident };
+Pipeline pipeline_for(const aq_codebooks *cb, const KsKernels *kk, int var, int topl) {
+    if (cb->proj || cb->exact_only || !kk->cascade[var][topl - 3]) return Pipeline::kStages;
     const char *e = std::getenv("AQ_EUCLID_PIPELINE");
-    return !(e && std::strcmp(e, "stages") == 0);
-}
-bool resident_enabled() {
-    const char *e = std::getenv("AQ_EUCLID_PIPELINE");
-    return !(e && std::strcmp(e, "cascade") == 0);
+    if (e && std::strcmp(e, "stages") == 0) return Pipeline::kStages;
+    if (e && std::strcmp(e, "cascade") == 0) return Pipeline::kCascade;
+    return var < 3 && kk->resident[var][topl - 3] ? Pipeline::kResident : Pipeline::kStages;
 }
 
-// Encode with the one-launch cascade: every stage of every frame in
-// euclid_cascade_kernel (frames the certificate cannot settle continue with
-// their best exact candidate and are listed), the exact verification of the
-// listed (frame, stage) pairs, and the fix-up of frames whose continuation
-// was wrong.  Four launches per encode, whatever the number of stages.
+// Encode with a one-launch cascade: every stage of every frame in
+// euclid_resident_kernel (resident) or euclid_cascade_kernel (frames the
+// certificate cannot settle continue with their best exact candidate and
+// are listed), the exact verification of the listed (frame, stage) pairs,
+// and the fix-up of frames whose continuation was wrong.  Four launches per
+// encode, whatever the number of stages.
 aq_status euclid_encode_cascade(aq_ctx *ctx, const aq_codebooks *cb, const aq_frames_desc &in, int64_t M, int32_t *idx,
                                 float *residual, float *dist, int topk, int32_t *topk_idx, float *topk_dist,
-                                const int32_t *force_idx, Arena &arena, const KsKernels *kk, int var, int topl) {
+                                const int32_t *force_idx, Arena &arena, const KsKernels *kk, int var, int topl,
+                                bool resident) {
     const int K = static_cast<int>(cb->K);
     CascadeFn casc = kk->cascade[var][topl - 3], ver = kk->verify[var], fix = kk->fixup[var];
     size_t clds = static_cast<size_t>(kk->cascade_lds);
     int frames = kk->cascade_frames, threads = kCThreads;
-    if (var < 3 && kk->resident[var][topl - 3] && resident_enabled()) {
+    if (resident) {
         casc = kk->resident[var][topl - 3];
         clds = static_cast<size_t>(kk->resident_lds);
         frames = kk->resident_frames;
@@ -822,9 +827,10 @@ aq_status euclid_encode_impl(aq_ctx *ctx, const aq_codebooks *cb, const aq_frame
     const int topl = (topk >= 4 || cb->N * cb->K >= (int64_t{1} << 22)) ? 4 : 3;
     const KsKernels *kk = kernels_for(ks);
     const int var = variant_of(cb->recipe, cb->q8);
-    if (!pw && !cb->exact_only && kk->cascade[var][topl - 3] && cascade_enabled())
+    const Pipeline pipe = pipeline_for(cb, kk, var, topl);
+    if (pipe != Pipeline::kStages)
         return euclid_encode_cascade(ctx, cb, in, M, idx, residual, dist, topk, topk_idx, topk_dist, force_idx, arena, kk,
-                                     var, topl);
+                                     var, topl, pipe == Pipeline::kResident);
     StageFn sweep = kk->sweep[cb->q8 ? 1 : 0][topl - 3];
     StageFn select = kk->select[var][topl - 3];
     StageFn scan = kk->exact_scan[var];
