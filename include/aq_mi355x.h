@@ -351,14 +351,18 @@ aq_status aq_euclid_upload_projected(aq_ctx *ctx, int64_t Q, int64_t N, int64_t 
 
 /* Frames per stage (first min(Q, 64) stages) of the last encode on ctx that
  * the fp16 error certificate could not settle: the split-fp16 refine pass
- * took them or, when no more than 64 were open, the exact scan (host int32
- * array; synchronises the stream).  A measurement aid with no reference
- * counterpart. */
+ * took them or, when no more than 64 were open, the exact scan; in the
+ * one-launch cascade (F32 codebooks at K = 256) the frames that continued
+ * with their best exactly evaluated candidate and were verified by the
+ * exact scan afterwards (host int32 array; synchronises the stream).  A
+ * measurement aid with no reference counterpart. */
 aq_status aq_euclid_failures(aq_ctx *ctx, const aq_codebooks *cb, int32_t *host_counts);
 
 /* Frames per stage (first min(Q, 64) stages) of the last encode on ctx that
  * the exact scan decided: those the refine pass left open, or all open
- * frames when no more than 64 were (host int32 array; synchronises the
+ * frames when no more than 64 were; in the one-launch cascade the frames
+ * whose verified continuation was wrong, recomputed from that stage on and
+ * counted at each recomputed stage (host int32 array; synchronises the
  * stream).  A measurement aid with no reference counterpart. */
 aq_status aq_euclid_exact_scans(aq_ctx *ctx, const aq_codebooks *cb, int32_t *host_counts);
 
