@@ -687,15 +687,17 @@ Pipeline pipeline_for(const aq_codebooks *cb, const KsKernels *kk, int var, int 
 // Encode with a one-launch cascade: every stage of every frame in
 // euclid_resident_kernel (resident) or euclid_cascade_kernel (frames the
 // certificate cannot settle continue with their best exact candidate and
-// are listed), the exact verification of the listed (frame, stage) pairs,
-// and the fix-up of frames whose continuation was wrong.  Four launches per
-// encode, whatever the number of stages.
+// are listed), the exact verification of the listed (frame, stage) pairs
+// (their values spread over the grid, then the selections), and the fix-up
+// of frames whose continuation was wrong.  Five launches per encode,
+// whatever the number of stages.
 aq_status euclid_encode_cascade(aq_ctx *ctx, const aq_codebooks *cb, const aq_frames_desc &in, int64_t M, int32_t *idx,
                                 float *residual, float *dist, int topk, int32_t *topk_idx, float *topk_dist,
                                 const int32_t *force_idx, Arena &arena, const KsKernels *kk, int var, int topl,
                                 bool resident) {
     const int K = static_cast<int>(cb->K);
     CascadeFn casc = kk->cascade[var][topl - 3], ver = kk->verify[var], fix = kk->fixup[var];
+    CascadeFn vvals = kk->verify_values[var];
     size_t clds = static_cast<size_t>(kk->cascade_lds);
     int frames = kk->cascade_frames, threads = kCThreads;
     if (resident) {
@@ -708,6 +710,8 @@ aq_status euclid_encode_cascade(aq_ctx *ctx, const aq_codebooks *cb, const aq_fr
     {
         aq_status ls = aq_launch_lds(ctx, reinterpret_cast<const void *>(casc), clds, "aq_euclid_encode (cascade)");
         if (ls == AQ_OK) ls = aq_launch_lds(ctx, reinterpret_cast<const void *>(ver), slds, "aq_euclid_encode (verify)");
+        if (ls == AQ_OK)
+            ls = aq_launch_lds(ctx, reinterpret_cast<const void *>(vvals), slds, "aq_euclid_encode (verify values)");
         if (ls == AQ_OK) ls = aq_launch_lds(ctx, reinterpret_cast<const void *>(fix), slds, "aq_euclid_encode (fix-up)");
         if (ls != AQ_OK) return ls;
     }
@@ -741,6 +745,24 @@ aq_status euclid_encode_cascade(aq_ctx *ctx, const aq_codebooks *cb, const aq_fr
     hipLaunchKernelGGL(zero2_kernel, dim3(1), dim3(256), 0, ctx->stream, ints, kZeroInts, ctx->d_flags,
                        static_cast<int>(AQ_FLAG_COUNT));
     AQ_HIP(ctx, hipGetLastError());
+    // Exact values of up to kVerifySpread verified pairs ([pairs, N], at most
+    // 64 MiB), spread over the grid by euclid_verify_values_kernel; a fixed
+    // region too small for them leaves a block per pair computing its own.
+    constexpr int kVerifySpread = 256;
+    float *svals = nullptr;
+    int scap = 0;
+    {
+        const int64_t fit = (int64_t{64} << 20) / (cb->N * static_cast<int64_t>(sizeof(float)));
+        const int want = static_cast<int>(std::min<int64_t>(kVerifySpread, fit));
+        const size_t bytes = static_cast<size_t>(want) * cb->N * sizeof(float);
+        if (want > 0 && (!arena.base || arena.left() >= bytes + (size_t{4} << 20))) {
+            void *w = nullptr;
+            aq_status st = arena.get(6, bytes, &w);
+            if (st != AQ_OK) return st;
+            svals = static_cast<float *>(w);
+            scap = want;
+        }
+    }
     CascadeArgs c{};
     StageArgs &a = c.a;
     a.M = M;
@@ -765,6 +787,8 @@ aq_status euclid_encode_cascade(aq_ctx *ctx, const aq_codebooks *cb, const aq_fr
     a.flags = ctx->d_flags;
     a.spec_count = ints + 128;
     a.spec_list = ints + kHead;
+    a.svals = svals;
+    a.scap = scap;
     {
         // test hook: every frame speculates on a wrong code (the verification
         // and fix-up then decide all of them)
@@ -783,6 +807,8 @@ aq_status euclid_encode_cascade(aq_ctx *ctx, const aq_codebooks *cb, const aq_fr
     const int64_t blocks = (M + frames - 1) / frames;
     aq_launch_timed(ctx, !arena.base, casc, dim3(static_cast<unsigned>(blocks)), dim3(threads),
                     static_cast<uint32_t>(clds), c);
+    AQ_HIP(ctx, hipGetLastError());
+    hipLaunchKernelGGL(vvals, dim3(static_cast<unsigned>(2 * cus)), dim3(kScanThreads), slds, ctx->stream, c);
     AQ_HIP(ctx, hipGetLastError());
     hipLaunchKernelGGL(ver, dim3(static_cast<unsigned>(2 * cus)), dim3(kScanThreads), slds, ctx->stream, c);
     AQ_HIP(ctx, hipGetLastError());

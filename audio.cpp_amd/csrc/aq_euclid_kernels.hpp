@@ -234,6 +234,7 @@ struct KsKernels {
     // null otherwise), its verification and fix-up.
     CascadeFn cascade[4][2];  // [variant][topl]
     CascadeFn verify[4];
+    CascadeFn verify_values[4];
     CascadeFn fixup[4];
     int cascade_lds;          // cascade dynamic LDS bytes (TOPL 4)
     int cascade_frames;       // frames per cascade block
@@ -1798,12 +1799,12 @@ __device__ void quad_values(const StageArgs &a, float *out, int chunk, const flo
         }
     }
 }
-// Every code's value (a.N <= kScanChunk) of the frame xs (LDS) into rv by one
+// The values of codes [n0, n1) of the frame xs (LDS) into rv[n] by one
 // kScanThreads block in the quad layout of quad_values, two kScanQuadCodes
 // chunks per pass with all their row reads issued together.  x2: the
 // frame's sum_rows(x*x) (Higgs).
 template <int RECIPE, int K>
-__device__ void block_values_quad(const StageArgs &a, const float *xs, float x2, float *rv) {
+__device__ void block_values_quad(const StageArgs &a, const float *xs, float x2, float *rv, int n0, int n1) {
     const int tid = threadIdx.x;
     const int q = tid & 3, cl = tid >> 2;
     const float sa = RECIPE == OMNI ? 2.0f : 1.0f;
@@ -1811,12 +1812,12 @@ __device__ void block_values_quad(const StageArgs &a, const float *xs, float x2,
     f32x4 vx[K / 16];
 #pragma unroll
     for (int l = 0; l < K / 16; ++l) vx[l] = *reinterpret_cast<const f32x4 *>(xs + 16 * l + 4 * q);
-    for (int c0 = 0; c0 < a.N; c0 += U * kScanQuadCodes) {
+    for (int c0 = n0; c0 < n1; c0 += U * kScanQuadCodes) {
         f32x4 vc[U][K / 16];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int n = c0 + u * kScanQuadCodes + cl;
-            const float *cr = a.cbf + static_cast<int64_t>(n < a.N ? n : a.N - 1) * K;
+            const float *cr = a.cbf + static_cast<int64_t>(n < n1 ? n : n1 - 1) * K;
 #pragma unroll
             for (int l = 0; l < K / 16; ++l) vc[u][l] = *reinterpret_cast<const f32x4 *>(cr + 16 * l + 4 * q);
         }
@@ -1834,7 +1835,7 @@ __device__ void block_values_quad(const StageArgs &a, const float *xs, float x2,
             for (int t = 0; t < 4; ++t) t6[t] = __fadd_rn(__shfl_xor(t3[t], 1), t3[t]);
             const float dot = __fadd_rn(__fadd_rn(t6[0], t6[2]), __fadd_rn(t6[1], t6[3]));
             const int n = c0 + u * kScanQuadCodes + cl;
-            if (q == 0 && n < a.N)
+            if (q == 0 && n < n1)
                 rv[n] = RECIPE == OMNI ? __fadd_rn(dot, a.bias[n])
                                        : __fsub_rn(__fsub_rn(__fmul_rn(dot, 2.0f), x2), a.e2[n]);
         }
@@ -3448,21 +3449,61 @@ __device__ inline bool same_bits(float x, float y) { return __float_as_uint(x) =
 // recipe value computed and the reference's selection made (the exact
 // scan's); where the code, distance or top-k differ from the cascade's,
 // the frame's earliest wrong stage is recorded for the fix-up.  F32
-// codebooks of up to kScanChunk codes in tinyBLAS order take the values in
-// the quad layout (coalesced row reads, many in flight).
+// codebooks in tinyBLAS order take the values that
+// euclid_verify_values_kernel spread over the grid (up to a.scap pairs), or
+// compute them in the block in the quad layout (coalesced row reads, many in
+// flight).
 template <int RECIPE, bool Q8, int KS>
 __device__ inline void scan_frame(const StageArgs &a, const float *xs, const int8_t *xq, const float *xd, ScanSh &sh) {
     constexpr int K = KS * 32;
     constexpr bool kQuadOk = !Q8 && RECIPE != DIRECT;
     if constexpr (kQuadOk) {
         if (spread_quad<RECIPE, Q8>(a) && a.N <= kScanChunk) {
-            block_values_quad<RECIPE, K>(a, xs, sh.o_x2, sh.rv);
+            block_values_quad<RECIPE, K>(a, xs, sh.o_x2, sh.rv, 0, a.N);
             __syncthreads();
             scan_select<RECIPE, Q8, KS>(a, K, true, sh.rv, xs, xq, xd, sh.o_x2, sh);
             return;
         }
     }
     scan_select<RECIPE, Q8, KS>(a, K, false, nullptr, xs, xq, xd, sh.o_x2, sh);
+}
+
+// Whether the verification takes its pairs' values from
+// euclid_verify_values_kernel (into a.svals, up to a.scap pairs).
+template <int RECIPE, bool Q8>
+__device__ inline bool verify_spread(const StageArgs &a, int count) {
+    return !Q8 && RECIPE != DIRECT && spread_quad<RECIPE, Q8>(a) && count <= a.scap;
+}
+constexpr int kVerifyPart = 512;   // codes per item of euclid_verify_values_kernel
+
+// The exact values of the speculative pairs' codes, spread over the grid in
+// (pair, kVerifyPart codes) items, for euclid_verify_kernel (the kernel
+// boundary orders them before their reader): a.svals[p][n].
+template <int RECIPE, bool Q8, int KS>
+__global__ __launch_bounds__(kScanThreads) void euclid_verify_values_kernel(CascadeArgs c) {
+    constexpr int K = KS * 32;
+    constexpr bool kQuadOk = !Q8 && RECIPE != DIRECT;
+    if constexpr (kQuadOk) {
+        extern __shared__ __align__(16) unsigned char lds[];
+        float *xs = reinterpret_cast<float *>(lds);
+        int8_t *xq = reinterpret_cast<int8_t *>(xs + K);
+        float *xd = reinterpret_cast<float *>(xq + K);
+        __shared__ ScanSh sh;
+        const int count = *c.a.spec_count;
+        if (!verify_spread<RECIPE, Q8>(c.a, count)) return;   // grid-uniform
+        const int parts = (c.a.N + kVerifyPart - 1) / kVerifyPart;
+        for (int item = blockIdx.x; item < count * parts; item += gridDim.x) {
+            const int p = item / parts, part = item - p * parts;
+            const int64_t m = c.a.spec_list[2 * p];
+            const int s = c.a.spec_list[2 * p + 1];
+            const StageArgs a = cascade_stage(c, s, K);
+            __syncthreads();   // the previous item's readers of xs
+            replay_residual(c, m, s, xs, K);
+            scan_prepare<RECIPE, Q8, KS>(xs, xq, xd, sh);
+            const int n0 = part * kVerifyPart, n1 = min(a.N, n0 + kVerifyPart);
+            block_values_quad<RECIPE, K>(a, xs, sh.o_x2, a.svals + static_cast<int64_t>(p) * a.N, n0, n1);
+        }
+    }
 }
 
 template <int RECIPE, bool Q8, int KS>
@@ -3474,14 +3515,21 @@ __global__ __launch_bounds__(kScanThreads) void euclid_verify_kernel(CascadeArgs
     float *xd = reinterpret_cast<float *>(xq + K);
     __shared__ ScanSh sh;
     const int count = *c.a.spec_count;
+    const bool spread = verify_spread<RECIPE, Q8>(c.a, count);
     for (int p = blockIdx.x; p < count; p += gridDim.x) {
         const int64_t m = c.a.spec_list[2 * p];
         const int s = c.a.spec_list[2 * p + 1];
         const StageArgs a = cascade_stage(c, s, K);
         __syncthreads();
-        replay_residual(c, m, s, xs, K);
-        scan_prepare<RECIPE, Q8, KS>(xs, xq, xd, sh);
-        scan_frame<RECIPE, Q8, KS>(a, xs, xq, xd, sh);
+        if (spread) {
+            // values from euclid_verify_values_kernel; the selection reads
+            // neither the frame nor its norms
+            scan_select<RECIPE, Q8, KS>(a, K, true, a.svals + static_cast<int64_t>(p) * a.N, xs, xq, xd, 0.0f, sh);
+        } else {
+            replay_residual(c, m, s, xs, K);
+            scan_prepare<RECIPE, Q8, KS>(xs, xq, xd, sh);
+            scan_frame<RECIPE, Q8, KS>(a, xs, xq, xd, sh);
+        }
         __syncthreads();
         if (threadIdx.x == 0) {
             const int64_t o = m * a.Q + s;
@@ -3557,6 +3605,11 @@ constexpr CascadeFn verify_fn() {
     else return nullptr;
 }
 template <int RECIPE, bool Q8, int KS>
+constexpr CascadeFn verify_values_fn() {
+    if constexpr (KS == 2 || KS == 8) return euclid_verify_values_kernel<RECIPE, Q8, KS>;
+    else return nullptr;
+}
+template <int RECIPE, bool Q8, int KS>
 constexpr CascadeFn fixup_fn() {
     if constexpr (KS == 2 || KS == 8) return euclid_fixup_kernel<RECIPE, Q8, KS>;
     else return nullptr;
@@ -3608,6 +3661,8 @@ constexpr int resident_lds_bytes() {
              {cascade_fn<HIGGS, true, KS, 3>(), cascade_fn<HIGGS, true, KS, 4>()}},                             \
             {verify_fn<OMNI, false, KS>(), verify_fn<HIGGS, false, KS>(), verify_fn<DIRECT, false, KS>(),       \
              verify_fn<HIGGS, true, KS>()},                                                                     \
+            {verify_values_fn<OMNI, false, KS>(), verify_values_fn<HIGGS, false, KS>(),                         \
+             verify_values_fn<DIRECT, false, KS>(), verify_values_fn<HIGGS, true, KS>()},                       \
             {fixup_fn<OMNI, false, KS>(), fixup_fn<HIGGS, false, KS>(), fixup_fn<DIRECT, false, KS>(),          \
              fixup_fn<HIGGS, true, KS>()},                                                                      \
             cascade_lds_bytes<KS>(),                                                                            \
