@@ -41,8 +41,11 @@ def sources() -> list[pathlib.Path]:
 
 # Per-source flags.  aq_euclid_ks8.hip holds the register-resident cascade
 # (one wave per SIMD, residual in AGPRs): MFMA results in VGPRs keep its key
-# epilogue free of AGPR-to-VGPR copies.
-SOURCE_FLAGS = {"aq_euclid_ks8.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+# epilogue free of AGPR-to-VGPR copies, and a higher full-unroll limit lets
+# its per-group select loop (the Q8_0 variant's body is the largest) unroll,
+# so that the residual array is indexed by constants and stays in registers
+# (unrolled short, it would live in scratch memory).
+SOURCE_FLAGS = {"aq_euclid_ks8.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-pragma-unroll-threshold=200000"]}
 
 
 def compile_one(src: pathlib.Path) -> pathlib.Path:

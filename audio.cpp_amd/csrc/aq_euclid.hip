@@ -669,11 +669,11 @@ aq_status euclid_encode_any(aq_ctx *ctx, const aq_codebooks *cb, const aq_frames
 }
 
 // The encode pipeline of a plain codebook: the register-resident one-launch
-// cascade where it exists (f32 codebooks at K = 256), else the per-stage
-// pipeline.  The one-launch cascade that keeps the residual in memory
-// measured no faster than the per-stage pipeline at K = 256 and slower for
-// Q8_0 codebooks (its verification then scans 2-3 % of the frames); it runs
-// when AQ_EUCLID_PIPELINE=cascade asks for it (comparisons and tests), as
+// cascade where it exists (K = 256), else the per-stage pipeline.  The
+// one-launch cascade that keeps the residual in memory measured no faster
+// than the per-stage pipeline at K = 256 and slower for Q8_0 codebooks (its
+// verification then scans 2-3 % of the frames); it runs when
+// AQ_EUCLID_PIPELINE=cascade asks for it (comparisons and tests), as
 // AQ_EUCLID_PIPELINE=stages asks for the per-stage pipeline.
 enum class Pipeline { kStages, kCascade, kResident };
 Pipeline pipeline_for(const aq_codebooks *cb, const KsKernels *kk, int var, int topl) {
@@ -681,7 +681,7 @@ Pipeline pipeline_for(const aq_codebooks *cb, const KsKernels *kk, int var, int 
     const char *e = std::getenv("AQ_EUCLID_PIPELINE");
     if (e && std::strcmp(e, "stages") == 0) return Pipeline::kStages;
     if (e && std::strcmp(e, "cascade") == 0) return Pipeline::kCascade;
-    return var < 3 && kk->resident[var][topl - 3] ? Pipeline::kResident : Pipeline::kStages;
+    return kk->resident[var][topl - 3] ? Pipeline::kResident : Pipeline::kStages;
 }
 
 // Encode with a one-launch cascade: every stage of every frame in

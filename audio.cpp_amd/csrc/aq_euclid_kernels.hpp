@@ -238,9 +238,9 @@ struct KsKernels {
     CascadeFn fixup[4];
     int cascade_lds;          // cascade dynamic LDS bytes (TOPL 4)
     int cascade_frames;       // frames per cascade block
-    // The register-resident cascade (f32 codebooks of the widths whose
-    // residual fits the registers; null otherwise).
-    CascadeFn resident[3][2]; // [recipe][topl]
+    // The register-resident cascade (the widths whose residual fits the
+    // registers; null otherwise).
+    CascadeFn resident[4][2]; // [variant][topl]
     int resident_lds;         // its dynamic LDS bytes (TOPL 4)
     int resident_frames;      // frames per block
 };
@@ -1841,6 +1841,56 @@ __device__ void block_values_quad(const StageArgs &a, const float *xs, float x2,
         }
     }
 }
+// The Higgs values of codes [n0, n1) against a Q8_0 codebook into rv[n] by
+// one kScanThreads block: ggml_vec_dot_q8_0_q8_0's eight accumulators (one
+// per 4-byte group of a block) on the 8 lanes of a code, hsum_float_8 as
+// lane exchanges 4, 2, 1 (dot_q8_k's arithmetic), so that a code row's
+// quants are read by 8 neighbouring lanes, two codes per group and pass.
+// xq / xd: the frame's quantised blocks (LDS), x2 its sum_rows(x*x).
+template <int K>
+__device__ void block_values_q8(const StageArgs &a, const int8_t *xq, const float *xd, float x2, float *rv, int n0,
+                                int n1) {
+    constexpr int NB = K / 32;
+    constexpr int G = kScanThreads / 8;   // codes per pass and code slot
+    constexpr int P = 2;
+    const int j = threadIdx.x & 7, grp = threadIdx.x >> 3;
+    int xw[NB];
+    float xs[NB];
+#pragma unroll
+    for (int ib = 0; ib < NB; ++ib) {
+        xw[ib] = reinterpret_cast<const int *>(xq)[8 * ib + j];
+        xs[ib] = xd[ib];
+    }
+    for (int c0 = n0; c0 < n1; c0 += P * G) {
+        int cq[P][NB];
+        float cd[P][NB];
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            const int n = c0 + p * G + grp;
+            const int nn = n < n1 ? n : n1 - 1;
+            const int *cqp = reinterpret_cast<const int *>(a.q8 + static_cast<int64_t>(nn) * K) + j;
+            const float *cdp = a.q8d + static_cast<int64_t>(nn) * NB;
+#pragma unroll
+            for (int ib = 0; ib < NB; ++ib) {
+                cq[p][ib] = cqp[8 * ib];
+                cd[p][ib] = cdp[ib];
+            }
+        }
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int ib = 0; ib < NB; ++ib)
+                acc = __fmaf_rn(__fmul_rn(cd[p][ib], xs[ib]),
+                                static_cast<float>(__builtin_amdgcn_sdot4(cq[p][ib], xw[ib], 0, false)), acc);
+            acc = __fadd_rn(acc, __shfl_xor(acc, 4));
+            acc = __fadd_rn(acc, __shfl_xor(acc, 2));
+            acc = __fadd_rn(acc, __shfl_xor(acc, 1));
+            const int n = c0 + p * G + grp;
+            if (j == 0 && n < n1) rv[n] = __fsub_rn(__fsub_rn(__fmul_rn(acc, 2.0f), x2), a.e2[n]);
+        }
+    }
+}
 template <int RECIPE, bool Q8, int K>
 __device__ void spread_item(const StageArgs &a, int slot, int chunk, int &cur, float *xs, int8_t *xq, float *xd,
                             float &x2s) {
@@ -3129,23 +3179,23 @@ __device__ inline float agpr_get(float a) {
     return x;
 }
 
-template <int KS, int FG, int TOPL>
+template <int KS, int FG, int TOPL, bool Q8>
 struct RsLayout {
     static constexpr int K = KS * 32;
     static constexpr int BUFB = Tile<KS>::CHUNKB + kRsThreads * 4;   // chunk + one |c|^2/2 slot per thread
     static constexpr int STAGE16 = Tile<KS>::CHUNKB / 16 / kRsThreads;
     static constexpr int SWEEP = 2 * BUFB;
     static constexpr int XSTR = K + 4;   // row stride of the scratch rows (floats; padded against bank conflicts)
-    static constexpr int SELB = (static_cast<int>(sizeof(SelLds<false, K, TOPL>)) + 15) / 16 * 16;
+    static constexpr int SELB = (static_cast<int>(sizeof(SelLds<Q8, K, TOPL>)) + 15) / 16 * 16;
     static constexpr int WSCR = SELB + 16 * XSTR * 4;                 // per wave: select queues + 16 rows
     static constexpr int BYTES = SWEEP > kRsWaves * WSCR ? SWEEP : kRsWaves * WSCR;
     static constexpr int FRAMES = kRsWaves * FG * 16;
 };
 
-template <int RECIPE, int KS, int FG, int TOPL>
+template <int RECIPE, bool Q8, int KS, int FG, int TOPL>
 __global__ __launch_bounds__(kRsThreads, 1) void euclid_resident_kernel(CascadeArgs c) {
     using T = Tile<KS>;
-    using LY = RsLayout<KS, FG, TOPL>;
+    using LY = RsLayout<KS, FG, TOPL, Q8>;
     using MX = Mx;
     constexpr int K = T::K;
     constexpr int BPC = T::CC / 16;                       // 16-code blocks per chunk
@@ -3204,10 +3254,15 @@ __global__ __launch_bounds__(kRsThreads, 1) void euclid_resident_kernel(CascadeA
             float sx = 0.0f, sd = 0.0f, sxx = 0.0f;
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
+                float v[8];
+#pragma unroll
+                for (int t = 0; t < 8; ++t) v[t] = agpr_get(xr[g][ks][t]);
+                // a Q8_0 codebook scores the query's Q8_0 image (as the sweep)
+                if (Q8) q8_image_block(v);
                 u32x4 packed;
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
-                    const float v0 = agpr_get(xr[g][ks][2 * t]), v1 = agpr_get(xr[g][ks][2 * t + 1]);
+                    const float v0 = v[2 * t], v1 = v[2 * t + 1];
                     const typename MX::V2 pr = {static_cast<typename MX::E>(v0), static_cast<typename MX::E>(v1)};
                     const unsigned w = __builtin_bit_cast(unsigned, pr);
                     packed[t] = w;
@@ -3335,7 +3390,7 @@ __global__ __launch_bounds__(kRsThreads, 1) void euclid_resident_kernel(CascadeA
 
         // ---- select and residual update of the wave's groups ----
         unsigned char *ws = lds + wave * LY::WSCR;
-        SelLds<false, K, TOPL> &sl = *reinterpret_cast<SelLds<false, K, TOPL> *>(ws);
+        SelLds<Q8, K, TOPL> &sl = *reinterpret_cast<SelLds<Q8, K, TOPL> *>(ws);
         float *xs = reinterpret_cast<float *>(ws + LY::SELB);
 #pragma unroll
         for (int g = 0; g < FG; ++g) {
@@ -3353,7 +3408,7 @@ __global__ __launch_bounds__(kRsThreads, 1) void euclid_resident_kernel(CascadeA
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            const int code = select_group<RECIPE, false, KS, TOPL>(a, mb, top[g], top[g][TOPL - 1], nx2[g], nd2[g],
+            const int code = select_group<RECIPE, Q8, KS, TOPL>(a, mb, top[g], top[g][TOPL - 1], nx2[g], nd2[g],
                                                                    nxx2[g], sl, true, xs, LY::XSTR, false);
             // r -= c[code] (the forced code where given) in registers
             const int64_t m = mb + col;
@@ -3447,12 +3502,12 @@ __device__ inline bool same_bits(float x, float y) { return __float_as_uint(x) =
 // Exact verification of the cascade's speculative (frame, stage) pairs, a
 // block per pair: the stage's input residual is replayed, every code's
 // recipe value computed and the reference's selection made (the exact
-// scan's); where the code, distance or top-k differ from the cascade's,
-// the frame's earliest wrong stage is recorded for the fix-up.  F32
-// codebooks in tinyBLAS order take the values that
-// euclid_verify_values_kernel spread over the grid (up to a.scap pairs), or
-// compute them in the block in the quad layout (coalesced row reads, many in
-// flight).
+// scan's); where the code differs from the cascade's, the frame's earliest
+// wrong stage is recorded for the fix-up, and where only the distance or
+// top-k list differ they are corrected in place.  F32 codebooks in tinyBLAS
+// order and Q8_0 codebooks take the values that euclid_verify_values_kernel
+// spread over the grid (up to a.scap pairs), or compute them in the block
+// (coalesced code-row reads: the quad layout, or 8 lanes per Q8_0 code).
 template <int RECIPE, bool Q8, int KS>
 __device__ inline void scan_frame(const StageArgs &a, const float *xs, const int8_t *xq, const float *xd, ScanSh &sh) {
     constexpr int K = KS * 32;
@@ -3465,6 +3520,14 @@ __device__ inline void scan_frame(const StageArgs &a, const float *xs, const int
             return;
         }
     }
+    if constexpr (Q8 && RECIPE == HIGGS) {
+        if (a.N <= kScanChunk) {
+            block_values_q8<K>(a, xq, xd, sh.o_x2, sh.rv, 0, a.N);
+            __syncthreads();
+            scan_select<RECIPE, Q8, KS>(a, K, true, sh.rv, xs, xq, xd, sh.o_x2, sh);
+            return;
+        }
+    }
     scan_select<RECIPE, Q8, KS>(a, K, false, nullptr, xs, xq, xd, sh.o_x2, sh);
 }
 
@@ -3472,7 +3535,8 @@ __device__ inline void scan_frame(const StageArgs &a, const float *xs, const int
 // euclid_verify_values_kernel (into a.svals, up to a.scap pairs).
 template <int RECIPE, bool Q8>
 __device__ inline bool verify_spread(const StageArgs &a, int count) {
-    return !Q8 && RECIPE != DIRECT && spread_quad<RECIPE, Q8>(a) && count <= a.scap;
+    const bool form = Q8 ? RECIPE == HIGGS : RECIPE != DIRECT && spread_quad<RECIPE, Q8>(a);
+    return form && count <= a.scap;
 }
 constexpr int kVerifyPart = 512;   // codes per item of euclid_verify_values_kernel
 
@@ -3483,7 +3547,7 @@ template <int RECIPE, bool Q8, int KS>
 __global__ __launch_bounds__(kScanThreads) void euclid_verify_values_kernel(CascadeArgs c) {
     constexpr int K = KS * 32;
     constexpr bool kQuadOk = !Q8 && RECIPE != DIRECT;
-    if constexpr (kQuadOk) {
+    if constexpr (kQuadOk || (Q8 && RECIPE == HIGGS)) {
         extern __shared__ __align__(16) unsigned char lds[];
         float *xs = reinterpret_cast<float *>(lds);
         int8_t *xq = reinterpret_cast<int8_t *>(xs + K);
@@ -3501,7 +3565,9 @@ __global__ __launch_bounds__(kScanThreads) void euclid_verify_values_kernel(Casc
             replay_residual(c, m, s, xs, K);
             scan_prepare<RECIPE, Q8, KS>(xs, xq, xd, sh);
             const int n0 = part * kVerifyPart, n1 = min(a.N, n0 + kVerifyPart);
-            block_values_quad<RECIPE, K>(a, xs, sh.o_x2, a.svals + static_cast<int64_t>(p) * a.N, n0, n1);
+            float *rv = a.svals + static_cast<int64_t>(p) * a.N;
+            if constexpr (Q8) block_values_q8<K>(a, xq, xd, sh.o_x2, rv, n0, n1);
+            else block_values_quad<RECIPE, K>(a, xs, sh.o_x2, rv, n0, n1);
         }
     }
 }
@@ -3532,14 +3598,20 @@ __global__ __launch_bounds__(kScanThreads) void euclid_verify_kernel(CascadeArgs
         }
         __syncthreads();
         if (threadIdx.x == 0) {
+            // A wrong code sends the frame to the fix-up from this stage on;
+            // with the right code (the later stages' input is then right)
+            // a wrong distance or top-k list is corrected here.
             const int64_t o = m * a.Q + s;
-            bool bad = a.idx[o] != sh.o_code;
-            if (a.dist) bad |= !same_bits(a.dist[o], RECIPE == DIRECT ? sh.o_code_v : -sh.o_code_v);
-            for (int r = 0; r < a.topk; ++r) {
-                bad |= a.topk_idx[o * a.topk + r] != sh.o_sel_n[r];
-                bad |= !same_bits(a.topk_dist[o * a.topk + r], RECIPE == DIRECT ? sh.o_sel_v[r] : -sh.o_sel_v[r]);
+            const bool bad = a.idx[o] != sh.o_code;
+            if (bad) {
+                if (atomicMin(&c.bad_stage[m], s) == a.Q) c.bad_list[atomicAdd(c.bad_count, 1)] = static_cast<int32_t>(m);
+            } else {
+                if (a.dist) a.dist[o] = RECIPE == DIRECT ? sh.o_code_v : -sh.o_code_v;
+                for (int r = 0; r < a.topk; ++r) {
+                    a.topk_idx[o * a.topk + r] = sh.o_sel_n[r];
+                    a.topk_dist[o * a.topk + r] = RECIPE == DIRECT ? sh.o_sel_v[r] : -sh.o_sel_v[r];
+                }
             }
-            if (bad && atomicMin(&c.bad_stage[m], s) == a.Q) c.bad_list[atomicAdd(c.bad_count, 1)] = static_cast<int32_t>(m);
         }
     }
 }
@@ -3620,16 +3692,21 @@ constexpr int cascade_lds_bytes() {
     else return 0;
 }
 // Register-resident cascade: K = 256 (3 groups of fp32 residual and fp16
-// fragments per wave fit its 512 registers).
+// fragments per wave fit its 512 registers).  The Q8_0 variant for top-k
+// keeps six keys per lane in place of four: its fp16 images of q * d leave
+// about 2.7 % of the frames of each stage uncertified with four (their
+// verification then costs more than the cascade saves), a few with six.
 constexpr int kRsGroups = 3;
-template <int RECIPE, int KS, int TOPL>
+template <bool Q8, int TOPL>
+constexpr int resident_keys() { return Q8 && TOPL == 4 ? 6 : TOPL; }
+template <int RECIPE, bool Q8, int KS, int TOPL>
 constexpr CascadeFn resident_fn() {
-    if constexpr (KS == 8) return euclid_resident_kernel<RECIPE, KS, kRsGroups, TOPL>;
+    if constexpr (KS == 8) return euclid_resident_kernel<RECIPE, Q8, KS, kRsGroups, resident_keys<Q8, TOPL>()>;
     else return nullptr;
 }
 template <int KS>
-constexpr int resident_lds_bytes() {
-    if constexpr (KS == 8) return RsLayout<KS, kRsGroups, 4>::BYTES;
+constexpr int resident_lds_bytes() {   // the largest variant's (Q8_0, six keys)
+    if constexpr (KS == 8) return RsLayout<KS, kRsGroups, resident_keys<true, 4>(), true>::BYTES;
     else return 0;
 }
 
@@ -3667,9 +3744,10 @@ constexpr int resident_lds_bytes() {
              fixup_fn<HIGGS, true, KS>()},                                                                      \
             cascade_lds_bytes<KS>(),                                                                            \
             kCRows * groups_for(KS) * 16,                                                                       \
-            {{resident_fn<OMNI, KS, 3>(), resident_fn<OMNI, KS, 4>()},                                          \
-             {resident_fn<HIGGS, KS, 3>(), resident_fn<HIGGS, KS, 4>()},                                        \
-             {resident_fn<DIRECT, KS, 3>(), resident_fn<DIRECT, KS, 4>()}},                                     \
+            {{resident_fn<OMNI, false, KS, 3>(), resident_fn<OMNI, false, KS, 4>()},                            \
+             {resident_fn<HIGGS, false, KS, 3>(), resident_fn<HIGGS, false, KS, 4>()},                          \
+             {resident_fn<DIRECT, false, KS, 3>(), resident_fn<DIRECT, false, KS, 4>()},                        \
+             {resident_fn<HIGGS, true, KS, 3>(), resident_fn<HIGGS, true, KS, 4>()}},                           \
             resident_lds_bytes<KS>(),                                                                           \
             kRsWaves * kRsGroups * 16};                                                                         \
         return &t;                                                                                              \

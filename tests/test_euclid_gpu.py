@@ -40,7 +40,7 @@ def pipeline(request, monkeypatch):
 
 def effective(pipeline, K, cb_type=0):
     """The pipeline an encode takes under the `pipeline` fixture's setting."""
-    return "stages" if pipeline == "resident" and (K != 256 or cb_type) else pipeline
+    return "stages" if pipeline == "resident" and K != 256 else pipeline
 
 
 @pytest.fixture(scope="module")
