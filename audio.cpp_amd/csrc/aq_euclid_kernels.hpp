@@ -610,6 +610,19 @@ __device__ inline float row_ror_add(float v) {
     return __fadd_rn(v, __int_as_float(o));
 }
 
+// ggml's hsum_float_8 ((a0+a4) + (a2+a6)) + ((a1+a5) + (a3+a7)) of eight
+// accumulators held by 8 neighbouring lanes, lane j holding a_{q8_lane_word(j)}
+// (words 0, 1, 2, 3, 7, 6, 5, 4): the half-row mirror pairs a_i with a_{i+4},
+// the quad permutations [2,3,0,1] and [1,0,3,2] then add as the reference
+// does (IEEE addition is commutative), all as DPP moves.  Lane 0 of the 8
+// holds the sum.
+__device__ inline int q8_lane_word(int j) { return j < 4 ? j : 11 - j; }
+__device__ inline float hsum8_dpp(float a) {
+    float v = __fadd_rn(a, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x141, 0xF, 0xF, false)));
+    v = __fadd_rn(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false)));
+    return __fadd_rn(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false)));
+}
+
 // The values of x at the lane's column in each of the wave's four 16-lane
 // rows (out[q] = x of lane col + 16 q), by three gfx950 lane-swap
 // instructions instead of LDS permutes: permlane16_swap(x, x) gives rows
@@ -1207,43 +1220,57 @@ __device__ int select_group(const StageArgs &a, int64_t m_base, const float (&to
     } else if (Q8) {
         // ggml_vec_dot_q8_0_q8_0: 8 accumulators over the 4-element groups
         // of every block, one per lane of an 8-lane group, then hsum_float_8
-        // (i + 4, then pairs) as lane exchanges 4, 2, 1; 8 pairs per pass.
-        // Several pairs per group and pass (as registers allow), so that
-        // their code rows are read together.
+        // by DPP (hsum8_dpp); 8 pairs per pass.  Several pairs per group and
+        // pass (as registers allow): the queue entries are read first, then
+        // every memory operand of the pass (code rows, scales, |c|^2, the
+        // frames' query blocks) is issued before the first is used, so a
+        // pass costs one memory round trip.
         constexpr int P = K <= 256 ? 4 : (K <= 512 ? 2 : 1);
         const int j = lane & 7, grp = lane >> 3;
+        const int jw = q8_lane_word(j);
         for (int e0 = grp; e0 < qcount; e0 += 8 * P) {
-            int cq[P][K / 32], fs[P], n[P];
-            float cd[P][K / 32];
+            int cq[P][K / 32], xw[P][K / 32], fs[P], n[P];
+            float cd[P][K / 32], xd[P][K / 32], e2v[P], x2v[P];
 #pragma unroll
             for (int p = 0; p < P; ++p) {
                 const int e = e0 + 8 * p < qcount ? e0 + 8 * p : e0;
                 fs[p] = q_f[e];
                 n[p] = q_n[e];
-                const int *cqp = reinterpret_cast<const int *>(a.q8 + static_cast<int64_t>(n[p]) * K) + j;
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int p = 0; p < P; ++p) {
+                const int *cqp = reinterpret_cast<const int *>(a.q8 + static_cast<int64_t>(n[p]) * K) + jw;
                 const float *cdp = a.q8d + static_cast<int64_t>(n[p]) * (K / 32);
 #pragma unroll
                 for (int ib = 0; ib < K / 32; ++ib) {
                     cq[p][ib] = cqp[8 * ib];
                     cd[p][ib] = cdp[ib];
                 }
+                e2v[p] = a.e2[n[p]];
             }
 #pragma unroll
             for (int p = 0; p < P; ++p) {
-                const int *xq = reinterpret_cast<const int *>(q_xq + fs[p] * XQS) + j;
-                const float *xd = q_xd + fs[p] * (K / 32);
+                const int *xq = reinterpret_cast<const int *>(q_xq + fs[p] * XQS) + jw;
+#pragma unroll
+                for (int ib = 0; ib < K / 32; ++ib) {
+                    xw[p][ib] = xq[8 * ib];
+                    xd[p][ib] = q_xd[fs[p] * (K / 32) + ib];
+                }
+                x2v[p] = q_x2[fs[p]];
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int p = 0; p < P; ++p) {
                 float acc = 0.0f;
 #pragma unroll
                 for (int ib = 0; ib < K / 32; ++ib) {
-                    const float dd = __fmul_rn(cd[p][ib], xd[ib]);
-                    acc = __fmaf_rn(dd, static_cast<float>(__builtin_amdgcn_sdot4(cq[p][ib], xq[8 * ib], 0, false)), acc);
+                    const float dd = __fmul_rn(cd[p][ib], xd[p][ib]);
+                    acc = __fmaf_rn(dd, static_cast<float>(__builtin_amdgcn_sdot4(cq[p][ib], xw[p][ib], 0, false)), acc);
                 }
-                // lane 0 of the group: ((a0 + a4) + (a2 + a6)) + ((a1 + a5) + (a3 + a7))
-                acc = __fadd_rn(acc, __shfl_xor(acc, 4));
-                acc = __fadd_rn(acc, __shfl_xor(acc, 2));
-                acc = __fadd_rn(acc, __shfl_xor(acc, 1));
+                acc = hsum8_dpp(acc);
                 const int e = e0 + 8 * p;
-                if (j == 0 && e < qcount) q_v[e] = __fsub_rn(__fsub_rn(__fmul_rn(acc, 2.0f), q_x2[fs[p]]), a.e2[n[p]]);
+                if (j == 0 && e < qcount) q_v[e] = __fsub_rn(__fsub_rn(__fmul_rn(acc, 2.0f), x2v[p]), e2v[p]);
             }
         }
     } else {
@@ -1843,8 +1870,8 @@ __device__ void block_values_quad(const StageArgs &a, const float *xs, float x2,
 }
 // The Higgs values of codes [n0, n1) against a Q8_0 codebook into rv[n] by
 // one kScanThreads block: ggml_vec_dot_q8_0_q8_0's eight accumulators (one
-// per 4-byte group of a block) on the 8 lanes of a code, hsum_float_8 as
-// lane exchanges 4, 2, 1 (dot_q8_k's arithmetic), so that a code row's
+// per 4-byte group of a block) on the 8 lanes of a code, hsum_float_8 by DPP
+// (hsum8_dpp; dot_q8_k's arithmetic), so that a code row's
 // quants are read by 8 neighbouring lanes, two codes per group and pass.
 // xq / xd: the frame's quantised blocks (LDS), x2 its sum_rows(x*x).
 template <int K>
@@ -1854,11 +1881,12 @@ __device__ void block_values_q8(const StageArgs &a, const int8_t *xq, const floa
     constexpr int G = kScanThreads / 8;   // codes per pass and code slot
     constexpr int P = 2;
     const int j = threadIdx.x & 7, grp = threadIdx.x >> 3;
+    const int jw = q8_lane_word(j);
     int xw[NB];
     float xs[NB];
 #pragma unroll
     for (int ib = 0; ib < NB; ++ib) {
-        xw[ib] = reinterpret_cast<const int *>(xq)[8 * ib + j];
+        xw[ib] = reinterpret_cast<const int *>(xq)[8 * ib + jw];
         xs[ib] = xd[ib];
     }
     for (int c0 = n0; c0 < n1; c0 += P * G) {
@@ -1868,7 +1896,7 @@ __device__ void block_values_q8(const StageArgs &a, const int8_t *xq, const floa
         for (int p = 0; p < P; ++p) {
             const int n = c0 + p * G + grp;
             const int nn = n < n1 ? n : n1 - 1;
-            const int *cqp = reinterpret_cast<const int *>(a.q8 + static_cast<int64_t>(nn) * K) + j;
+            const int *cqp = reinterpret_cast<const int *>(a.q8 + static_cast<int64_t>(nn) * K) + jw;
             const float *cdp = a.q8d + static_cast<int64_t>(nn) * NB;
 #pragma unroll
             for (int ib = 0; ib < NB; ++ib) {
@@ -1883,9 +1911,7 @@ __device__ void block_values_q8(const StageArgs &a, const int8_t *xq, const floa
             for (int ib = 0; ib < NB; ++ib)
                 acc = __fmaf_rn(__fmul_rn(cd[p][ib], xs[ib]),
                                 static_cast<float>(__builtin_amdgcn_sdot4(cq[p][ib], xw[ib], 0, false)), acc);
-            acc = __fadd_rn(acc, __shfl_xor(acc, 4));
-            acc = __fadd_rn(acc, __shfl_xor(acc, 2));
-            acc = __fadd_rn(acc, __shfl_xor(acc, 1));
+            acc = hsum8_dpp(acc);
             const int n = c0 + p * G + grp;
             if (j == 0 && n < n1) rv[n] = __fsub_rn(__fsub_rn(__fmul_rn(acc, 2.0f), x2), a.e2[n]);
         }
