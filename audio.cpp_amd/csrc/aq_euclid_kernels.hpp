@@ -600,6 +600,64 @@ __device__ inline bool topk_before(float va, int na, float vb, int nb) {
     return va > vb || (va == vb && na < nb);
 }
 
+// (va, na) before (vb, nb) in top-k order, an empty place (n < 0) last.
+template <int RECIPE>
+__device__ inline bool topk_first(float va, int na, float vb, int nb) {
+    return na >= 0 && (nb < 0 || topk_before<RECIPE>(va, na, vb, nb));
+}
+// Compare-exchange of places i < k of a ranked list.
+template <int RECIPE>
+__device__ inline void topk_cx(float (&v)[5], int (&n)[5], int i, int k) {
+    const bool s = topk_first<RECIPE>(v[k], n[k], v[i], n[i]);
+    const float vi = v[i], vk = v[k];
+    const int ni = n[i], nk = n[k];
+    v[i] = s ? vk : vi;
+    n[i] = s ? nk : ni;
+    v[k] = s ? vi : vk;
+    n[k] = s ? ni : nk;
+}
+// x of the lane in the partner row (row r ^ X, X = 1 or 2) of the lane's
+// column, by one gfx950 lane swap (kq: the lane's row).
+template <int X>
+__device__ inline unsigned row_partner(unsigned x, int kq) {
+    if constexpr (X == 1) {
+        const auto ab = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+        return (kq & 1) ? ab[0] : ab[1];
+    } else {
+        const auto ab = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+        return (kq & 2) ? ab[0] : ab[1];
+    }
+}
+// The top 5 of the union of the lane's ranked list of 5 and its partner
+// row's (disjoint codes): the better of L_i and R_{4-i} gives the union's
+// top 5 (the first half of a bitonic merge), which a 5-input sorting
+// network (9 compare-exchanges) ranks.  Both partners end with the same list.
+template <int RECIPE, int X>
+__device__ inline void merge_rows5(float (&v)[5], int (&n)[5], int kq) {
+    float pv[5];
+    int pn[5];
+#pragma unroll
+    for (int i = 0; i < 5; ++i) {
+        pv[i] = __uint_as_float(row_partner<X>(__float_as_uint(v[i]), kq));
+        pn[i] = static_cast<int>(row_partner<X>(static_cast<unsigned>(n[i]), kq));
+    }
+#pragma unroll
+    for (int i = 0; i < 5; ++i) {
+        const bool s = topk_first<RECIPE>(pv[4 - i], pn[4 - i], v[i], n[i]);
+        v[i] = s ? pv[4 - i] : v[i];
+        n[i] = s ? pn[4 - i] : n[i];
+    }
+    topk_cx<RECIPE>(v, n, 0, 1);
+    topk_cx<RECIPE>(v, n, 3, 4);
+    topk_cx<RECIPE>(v, n, 2, 4);
+    topk_cx<RECIPE>(v, n, 2, 3);
+    topk_cx<RECIPE>(v, n, 0, 3);
+    topk_cx<RECIPE>(v, n, 0, 2);
+    topk_cx<RECIPE>(v, n, 1, 4);
+    topk_cx<RECIPE>(v, n, 1, 3);
+    topk_cx<RECIPE>(v, n, 1, 2);
+}
+
 // --------------------------------------------------------------- score kernel
 
 // v + v[lane rotated by N inside its 16-lane row] (DPP row_ror).  IEEE
@@ -1312,31 +1370,43 @@ __device__ int select_group(const StageArgs &a, int64_t m_base, const float (&to
             sel_n[r] = -1;
         }
         if (needg[g]) {
-            // Branch-free insertion of every evaluated candidate of the
-            // frame's 4 lanes into the ranked list sel[0..Tsel) (one place
-            // without top-k); a slot no frame of the wave fills is skipped.
+            if (Tsel == 1) {
+                // The best evaluated candidate of the frame's 4 lanes; a slot
+                // no frame of the wave fills is skipped.
 #pragma unroll
-            for (int j = 0; j < TOPL; ++j) {
-                int cnq[4];
-                float cvq[4];
-                rows4(cand_n[g][j], cnq);
-                rows4(cand_val[j], cvq);
+                for (int j = 0; j < TOPL; ++j) {
+                    int cnq[4];
+                    float cvq[4];
+                    rows4(cand_n[g][j], cnq);
+                    rows4(cand_val[j], cvq);
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    int cn = cnq[q];
-                    if (!__any(cn >= 0)) continue;
-                    float cv = cvq[q];
-                    if (Tsel == 1) {
+                    for (int q = 0; q < 4; ++q) {
+                        const int cn = cnq[q];
+                        if (!__any(cn >= 0)) continue;
+                        const float cv = cvq[q];
                         const bool take = cn >= 0 && (sel_n[0] < 0 || ranks_before<RECIPE>(cv, cn, sel_v[0], sel_n[0]));
                         sel_v[0] = take ? cv : sel_v[0];
                         sel_n[0] = take ? cn : sel_n[0];
-                        continue;
                     }
+                }
+            } else {
+                // Top-k: each lane ranks its own candidates (a prefix of its
+                // sorted keys) into a list of 5 (k <= 4 places and the next
+                // one), then the lists of the frame's 4 lanes are merged
+                // across rows (partner row r^1, then r^2; merge_rows5).  The
+                // order is total for finite values and the lanes' codes are
+                // disjoint, so the list is the frame's exact top 5; a frame
+                // with a non-finite candidate is left to the exact scan.
+                bool nonfin = false;
+#pragma unroll
+                for (int j = 0; j < TOPL; ++j) {
+                    int cn = cand_n[g][j];
+                    if (!__any(cn >= 0)) break;
+                    float cv = cand_val[j];
+                    nonfin = nonfin || (cn >= 0 && !(cv - cv == 0.0f));
 #pragma unroll
                     for (int r = 0; r < 5; ++r) {
-                        const bool before = a.topk == 0 ? ranks_before<RECIPE>(cv, cn, sel_v[r], sel_n[r])
-                                                        : topk_before<RECIPE>(cv, cn, sel_v[r], sel_n[r]);
-                        const bool take = cn >= 0 && r < Tsel && (sel_n[r] < 0 || before);
+                        const bool take = cn >= 0 && (sel_n[r] < 0 || topk_before<RECIPE>(cv, cn, sel_v[r], sel_n[r]));
                         const float tv = sel_v[r];
                         const int tn = sel_n[r];
                         sel_v[r] = take ? cv : tv;
@@ -1345,6 +1415,9 @@ __device__ int select_group(const StageArgs &a, int64_t m_base, const float (&to
                         cn = take ? tn : cn;
                     }
                 }
+                merge_rows5<RECIPE, 1>(sel_v, sel_n, kq);
+                merge_rows5<RECIPE, 2>(sel_v, sel_n, kq);
+                if (rows_max(nonfin ? 1.0f : 0.0f) != 0.0f) ok = false;
             }
             // S' of the T-th exact value in v units, against the bound of unkept codes.
             if (sel_n[Tk - 1] < 0) {
