@@ -628,6 +628,16 @@ __device__ inline unsigned row_partner(unsigned x, int kq) {
         return (kq & 2) ? ab[0] : ab[1];
     }
 }
+// The better (ranks_before; an empty place, n < 0, last) of the lane's
+// candidate and its partner row's.
+template <int RECIPE, int X>
+__device__ inline void best_rows(float &v, int &n, int kq) {
+    const float pv = __uint_as_float(row_partner<X>(__float_as_uint(v), kq));
+    const int pn = static_cast<int>(row_partner<X>(static_cast<unsigned>(n), kq));
+    const bool s = pn >= 0 && (n < 0 || ranks_before<RECIPE>(pv, pn, v, n));
+    v = s ? pv : v;
+    n = s ? pn : n;
+}
 // The top 5 of the union of the lane's ranked list of 5 and its partner
 // row's (disjoint codes): the better of L_i and R_{4-i} gives the union's
 // top 5 (the first half of a bitonic merge), which a 5-input sorting
@@ -1248,7 +1258,7 @@ __device__ int select_group(const StageArgs &a, int64_t m_base, const float (&to
         const float sa = RECIPE == OMNI ? 2.0f : 1.0f;
         for (int e0 = grp; e0 < qcount; e0 += 4 * P) {
             int fs[P], n[P];
-            float acc[P];
+            float acc[P], off[P];
 #pragma unroll
             for (int p = 0; p < P; ++p) {
                 const int e = e0 + 4 * p;
@@ -1256,6 +1266,10 @@ __device__ int select_group(const StageArgs &a, int64_t m_base, const float (&to
                 n[p] = e < qcount ? q_n[e] : 0;
                 acc[p] = 0.0f;
             }
+            // the code's bias (OmniVoice) or |c|^2 (Higgs) is loaded with
+            // its row, not after the sum
+#pragma unroll
+            for (int p = 0; p < P; ++p) off[p] = RECIPE == OMNI ? a.bias[n[p]] : a.e2[n[p]];
 #pragma unroll
             for (int l = 0; l < K / 16; ++l)
 #pragma unroll
@@ -1270,8 +1284,8 @@ __device__ int select_group(const StageArgs &a, int64_t m_base, const float (&to
                 v = row_ror_add<1>(v);
                 const int e = e0 + 4 * p;
                 if (j == 0 && e < qcount) {
-                    if (RECIPE == OMNI) q_v[e] = __fadd_rn(v, a.bias[n[p]]);
-                    else q_v[e] = __fsub_rn(__fsub_rn(__fmul_rn(v, 2.0f), q_x2[fs[p]]), a.e2[n[p]]);
+                    if (RECIPE == OMNI) q_v[e] = __fadd_rn(v, off[p]);
+                    else q_v[e] = __fsub_rn(__fsub_rn(__fmul_rn(v, 2.0f), q_x2[fs[p]]), off[p]);
                 }
             }
         }
@@ -1371,37 +1385,38 @@ __device__ int select_group(const StageArgs &a, int64_t m_base, const float (&to
         }
         if (needg[g]) {
             if (Tsel == 1) {
-                // The best evaluated candidate of the frame's 4 lanes; a slot
-                // no frame of the wave fills is skipped.
+                // The best evaluated candidate: each lane's own, then the
+                // better of the partner rows'
+                // (r^1, then r^2).  ranks_before is a total order on finite
+                // values over the lanes' disjoint codes; a frame with a
+                // non-finite candidate is left to the exact scan.
+                bool nonfin = false;
 #pragma unroll
                 for (int j = 0; j < TOPL; ++j) {
-                    int cnq[4];
-                    float cvq[4];
-                    rows4(cand_n[g][j], cnq);
-                    rows4(cand_val[j], cvq);
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const int cn = cnq[q];
-                        if (!__any(cn >= 0)) continue;
-                        const float cv = cvq[q];
-                        const bool take = cn >= 0 && (sel_n[0] < 0 || ranks_before<RECIPE>(cv, cn, sel_v[0], sel_n[0]));
-                        sel_v[0] = take ? cv : sel_v[0];
-                        sel_n[0] = take ? cn : sel_n[0];
-                    }
+                    const int cn = cand_n[g][j];
+                    if (!__any(cn >= 0)) continue;
+                    const float cv = cand_val[j];
+                    nonfin = nonfin || (cn >= 0 && !(cv - cv == 0.0f));
+                    const bool take = cn >= 0 && (sel_n[0] < 0 || ranks_before<RECIPE>(cv, cn, sel_v[0], sel_n[0]));
+                    sel_v[0] = take ? cv : sel_v[0];
+                    sel_n[0] = take ? cn : sel_n[0];
                 }
+                best_rows<RECIPE, 1>(sel_v[0], sel_n[0], kq);
+                best_rows<RECIPE, 2>(sel_v[0], sel_n[0], kq);
+                if (rows_max(nonfin ? 1.0f : 0.0f) != 0.0f) ok = false;
             } else {
-                // Top-k: each lane ranks its own candidates (a prefix of its
-                // sorted keys) into a list of 5 (k <= 4 places and the next
-                // one), then the lists of the frame's 4 lanes are merged
-                // across rows (partner row r^1, then r^2; merge_rows5).  The
-                // order is total for finite values and the lanes' codes are
-                // disjoint, so the list is the frame's exact top 5; a frame
-                // with a non-finite candidate is left to the exact scan.
+                // Top-k: each lane ranks its own candidates into a list of 5
+                // (k <= 4 places and the next one), then the lists of the
+                // frame's 4 lanes are merged across rows (partner row r^1,
+                // then r^2; merge_rows5).  The order is total for finite
+                // values and the lanes' codes are disjoint, so the list is
+                // the frame's exact top 5; a frame with a non-finite
+                // candidate is left to the exact scan.
                 bool nonfin = false;
 #pragma unroll
                 for (int j = 0; j < TOPL; ++j) {
                     int cn = cand_n[g][j];
-                    if (!__any(cn >= 0)) break;
+                    if (!__any(cn >= 0)) continue;
                     float cv = cand_val[j];
                     nonfin = nonfin || (cn >= 0 && !(cv - cv == 0.0f));
 #pragma unroll
