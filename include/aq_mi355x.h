@@ -352,7 +352,7 @@ aq_status aq_euclid_upload_projected(aq_ctx *ctx, int64_t Q, int64_t N, int64_t 
 /* Frames per stage (first min(Q, 64) stages) of the last encode on ctx that
  * the fp16 error certificate could not settle: the split-fp16 refine pass
  * took them or, when no more than 64 were open, the exact scan; in the
- * one-launch cascade (F32 codebooks at K = 256) the frames that continued
+ * one-launch cascade (codebooks at K = 256) the frames that continued
  * with their best exactly evaluated candidate and were verified by the
  * exact scan afterwards (host int32 array; synchronises the stream).  A
  * measurement aid with no reference counterpart. */
