@@ -3652,7 +3652,7 @@ __device__ inline bool verify_spread(const StageArgs &a, int count) {
     const bool form = Q8 ? RECIPE == HIGGS : RECIPE != DIRECT && spread_quad<RECIPE, Q8>(a);
     return form && count <= a.scap;
 }
-constexpr int kVerifyPart = 512;   // codes per item of euclid_verify_values_kernel
+constexpr int kVerifyPart = 128;   // codes per item of euclid_verify_values_kernel
 
 // The exact values of the speculative pairs' codes, spread over the grid in
 // (pair, kVerifyPart codes) items, for euclid_verify_kernel (the kernel
