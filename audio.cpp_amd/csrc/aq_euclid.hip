@@ -790,10 +790,11 @@ aq_status euclid_encode_cascade(aq_ctx *ctx, const aq_codebooks *cb, const aq_fr
     a.svals = svals;
     a.scap = scap;
     {
-        // test hook: every frame speculates on a wrong code (the verification
-        // and fix-up then decide all of them)
+        // test hooks: every frame speculates, on a wrong code (1: the
+        // verification and fix-up then decide all of them), or with its best
+        // code and distances one bit off (2: the verification corrects them)
         const char *e = std::getenv("AQ_EUCLID_TEST_MISSPECULATE");
-        a.misspeculate = e && e[0] == '1';
+        a.misspeculate = e && (e[0] == '1' || e[0] == '2') ? e[0] - '0' : 0;
     }
     c.x0 = x0;
     c.work = work;

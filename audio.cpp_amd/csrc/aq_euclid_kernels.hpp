@@ -131,7 +131,8 @@ struct StageArgs {
     int32_t *fail_list;      // [M]
     int32_t *spec_count;     // speculative (frame, stage) pairs listed (cascade)
     int32_t *spec_list;      // [2 * M * Q] the pairs, for the exact verification
-    int misspeculate;        // test hook: every frame speculates, on a wrong code (cascade)
+    int misspeculate;        // test hook (cascade): every frame speculates, on a wrong code (1) or with
+                             // its best code and perturbed distances (2)
     int32_t *flags;
     int exact_only;
     float *keys;             // sweep -> select: [nsplit][M/16][TOPL][64] score keys
@@ -1487,10 +1488,12 @@ __device__ int select_group(const StageArgs &a, int64_t m_base, const float (&to
             const int w = win_code[g];
             win_code[g] = w >= 0 && w < N ? w : 0;
             if (a.misspeculate) {
-                // test hook: the verification and fix-up see every frame,
-                // each continued with a code that is not its best
+                // test hooks: the verification sees every frame, continued
+                // with a code that is not its best (1: the fix-up recomputes
+                // it) or with its best code and distances one bit off (2:
+                // the verification corrects them in place)
                 ok = false;
-                win_code[g] = win_code[g] + 1 < N ? win_code[g] + 1 : 0;
+                if (a.misspeculate == 1) win_code[g] = win_code[g] + 1 < N ? win_code[g] + 1 : 0;
             }
         }
         win_ok[g] = ok || (speculate && live);
@@ -1507,13 +1510,15 @@ __device__ int select_group(const StageArgs &a, int64_t m_base, const float (&to
                     a.spec_list[2 * slot + 1] = a.s;
                 }
                 a.idx[m * a.Q + a.s] = win_code[g];
+                const unsigned flip = speculate && a.misspeculate == 2 ? 1u : 0u;   // test hook 2
                 if (a.dist) {
                     const float v = sel_v[0];   // the argmax's value (ties share it)
-                    a.dist[m * a.Q + a.s] = RECIPE == DIRECT ? v : -v;
+                    a.dist[m * a.Q + a.s] = __uint_as_float(__float_as_uint(RECIPE == DIRECT ? v : -v) ^ flip);
                 }
                 for (int r = 0; r < a.topk; ++r) {
                     a.topk_idx[(m * a.Q + a.s) * a.topk + r] = sel_n[r] < 0 ? 0 : sel_n[r];
-                    a.topk_dist[(m * a.Q + a.s) * a.topk + r] = RECIPE == DIRECT ? sel_v[r] : -sel_v[r];
+                    a.topk_dist[(m * a.Q + a.s) * a.topk + r] =
+                        __uint_as_float(__float_as_uint(RECIPE == DIRECT ? sel_v[r] : -sel_v[r]) ^ flip);
                 }
             }
         }

@@ -602,3 +602,44 @@ def test_cascade_fixup_recomputes_wrong_continuations(torch, ctx, oracle, monkey
         assert np.array_equal(bits(out["dist"]), bits(ref["dist"]))
     if topk:
         check_topk(out, ref)
+
+
+@pytest.mark.parametrize("recipe,cb_type,topk,K", [(0, 0, 0, 256), (1, 0, 4, 256), (1, 1, 4, 256), (2, 0, 0, 64)])
+def test_cascade_verification_corrects_outputs_in_place(torch, ctx, oracle, monkeypatch, pipeline, recipe, cb_type,
+                                                        topk, K):
+    """Test hook AQ_EUCLID_TEST_MISSPECULATE=2: every frame of every stage
+    continues with its best code but writes its distances (and top-k
+    distances) one bit off, uncertified.  The verification must find the
+    codes right and correct the outputs in place, without sending the
+    frames to the fix-up: every output ends as the reference's."""
+    from aqmi import synth
+
+    if effective(pipeline, K, cb_type) == "stages":
+        pytest.skip("speculation belongs to the one-launch cascades")
+    M, Q, N = 300, 4, 1024
+    print(f"[gpu] cascade in-place correction recipe={recipe} cb_type={cb_type} topk={topk} K={K}", flush=True)
+    x = synth.normal(83, 1, (M, K), 1.0)
+    if cb_type == 1:
+        cb = np.stack([synth.q8_0_random_codebook(83, 10 + s, N, K) for s in range(Q)])
+        cfg = dict(x=x, M=M, K=K, Q=Q, N=N, codebook_q8=cb)
+    else:
+        cb = synth.normal(83, 2, (Q, N, K), 1.0 / 16)
+        cfg = dict(x=x, M=M, K=K, Q=Q, N=N, codebook=cb)
+    monkeypatch.setenv("AQ_EUCLID_TEST_MISSPECULATE", "2")
+    out = run(torch, ctx, cb, recipe, x, cb_type=cb_type, topk=topk)
+    ref = {0: oracle.euclid_rvq, 1: oracle.higgs_rvq, 2: oracle.direct_rvq}[recipe]
+    ref = ref(cfg, topk=topk) if recipe == 1 else ref(cfg)
+    scans = out["cbs"].exact_scans()
+    print(f"[gpu] verified {out['fails'].tolist()}, recomputed {scans.tolist()}", flush=True)
+    assert out["fails"].tolist() == [M] * Q
+    # only a frame whose best evaluated code was not the reference's (a
+    # genuine misspeculation, rare) goes to the fix-up
+    assert (scans < M // 10).all()
+    assert np.array_equal(out["idx"], ref["idx"])
+    assert np.array_equal(bits(out["residual"]), bits(ref["residual"]))
+    if recipe == 0:
+        assert np.array_equal(bits(out["dist"]), bits(-ref["logit"]))
+    else:
+        assert np.array_equal(bits(out["dist"]), bits(ref["dist"]))
+    if topk:
+        check_topk(out, ref)
