@@ -106,6 +106,41 @@ struct Tile {
     static constexpr int LDS = 2 * BUFB;
 };
 
+// The byte offsets, within a codebook chunk, of a thread's 16-byte staging
+// pieces: piece k of thread t is row r = (t + THREADS k) / CH16, 16-byte
+// column ((t + THREADS k) % CH16) ^ (r & SWZ).  Where THREADS is a multiple
+// of CH16 and the rows per piece index (RPK) and the swizzle period divide
+// one another, piece k's offset is k RPK ROWB (uniform) plus one of NVO
+// per-thread values, which is all a thread keeps (the general form holds an
+// address per piece across the sweep).
+template <typename T, int THREADS>
+struct StageOffsets {
+    static constexpr int RPK0 = THREADS / T::CH16;
+    static constexpr bool kAffine = THREADS % T::CH16 == 0 &&
+                                    ((T::SWZ + 1) % RPK0 == 0 || RPK0 % (T::SWZ + 1) == 0);
+    static constexpr int RPK = kAffine ? RPK0 : 1;
+    static constexpr int NVO = kAffine && T::SWZ + 1 > RPK ? (T::SWZ + 1) / RPK : 1;
+    unsigned v[NVO];
+    __device__ StageOffsets() {
+        if constexpr (kAffine) {
+            const int br = threadIdx.x / T::CH16, c16 = threadIdx.x % T::CH16;
+#pragma unroll
+            for (int i = 0; i < NVO; ++i) v[i] = br * T::ROWB + 16 * (c16 ^ ((br + RPK * i) & T::SWZ));
+        }
+    }
+    // piece k's offset = uni(k) (the same for every thread) + lane(k)
+    __device__ int uni(int k) const { return kAffine ? k * RPK * T::ROWB : 0; }
+    __device__ unsigned lane(int k) const {
+        if constexpr (kAffine) {
+            return v[k % NVO];
+        } else {
+            const int q = threadIdx.x + k * THREADS;
+            const int r = q / T::CH16, j = (q % T::CH16) ^ (r & T::SWZ);
+            return static_cast<unsigned>(r * T::ROWB + j * 16);
+        }
+    }
+};
+
 struct StageArgs {
     const float *xin;        // [M, K] residual entering the stage
     float *xout;             // [M, K] residual leaving the stage (may alias xin; null: not needed)
@@ -887,10 +922,9 @@ __global__ __launch_bounds__(kThreads, sweep_blocks_per_cu(KS)) void euclid_swee
     // (q % CH16) ^ (row & SWZ): the XOR swizzle that lds_a reads.  The
     // |c|^2/2 slots follow the same per-thread layout as h_dst.
     const unsigned char *cbb = reinterpret_cast<const unsigned char *>(a.cbh);
+    const StageOffsets<T, kThreads> so;
     auto stage_piece = [&](int buf, int chunk, int k) {
-        const int q = threadIdx.x + k * kThreads;
-        const int r = q / T::CH16, j = (q % T::CH16) ^ (r & T::SWZ);
-        const unsigned char *g = cbb + static_cast<int64_t>(chunk) * T::CHUNKB + r * T::ROWB + j * 16;
+        const unsigned char *g = cbb + (static_cast<int64_t>(chunk) * T::CHUNKB + so.uni(k)) + so.lane(k);
         unsigned char *d = lds + buf * T::BUFB + (k * kThreads + wave * kWave) * 16;
         __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)g,
                                          (__attribute__((address_space(3))) void *)d, 16, 0, 0);
@@ -3068,6 +3102,7 @@ __global__ __launch_bounds__(kCThreads, 1) void euclid_cascade_kernel(CascadeArg
     constexpr int PPB = (CT::STAGE16 + NB - 1) / NB;   // staged pieces per block
     constexpr int kWaitLoads = 0x0070;                 // s_waitcnt vmcnt(0) lgkmcnt(0)
     const int hsrc = threadIdx.x < T::CC ? threadIdx.x : 0;
+    const StageOffsets<T, kCThreads> so;
 
     for (int s = 0; s < c.a.Q; ++s) {
         const StageArgs a = cascade_stage(c, s, K);
@@ -3130,9 +3165,7 @@ __global__ __launch_bounds__(kCThreads, 1) void euclid_cascade_kernel(CascadeArg
         // wave w lands at piece k * kCThreads + 64 w + l)
         const unsigned char *cbb = reinterpret_cast<const unsigned char *>(a.cbh);
         auto stage_piece = [&](int buf, int chunk, int k) {
-            const int q = threadIdx.x + k * kCThreads;
-            const int r = q / T::CH16, j = (q % T::CH16) ^ (r & T::SWZ);
-            const unsigned char *gp = cbb + static_cast<int64_t>(chunk) * T::CHUNKB + r * T::ROWB + j * 16;
+            const unsigned char *gp = cbb + (static_cast<int64_t>(chunk) * T::CHUNKB + so.uni(k)) + so.lane(k);
             unsigned char *d = lds + buf * CT::BUFB + (k * kCThreads + wave * kWave) * 16;
             __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)gp,
                                              (__attribute__((address_space(3))) void *)d, 16, 0, 0);
@@ -3343,6 +3376,7 @@ __global__ __launch_bounds__(kRsThreads, 1) void euclid_resident_kernel(CascadeA
     constexpr int L = R - 1;
     constexpr int kWaitLoads = 0x0070;   // s_waitcnt vmcnt(0) lgkmcnt(0)
     const int hsrc = threadIdx.x < T::CC ? threadIdx.x : 0;
+    const StageOffsets<T, kRsThreads> so;
 
     // the stage-0 input, in the fragment layout (rows past M read row M - 1),
     // held in AGPRs
@@ -3422,9 +3456,7 @@ __global__ __launch_bounds__(kRsThreads, 1) void euclid_resident_kernel(CascadeA
         // wave w lands at piece k * kRsThreads + 64 w + l)
         const unsigned char *cbb = reinterpret_cast<const unsigned char *>(a.cbh);
         auto stage_piece = [&](int buf, int chunk, int k) {
-            const int q = threadIdx.x + k * kRsThreads;
-            const int r = q / T::CH16, j = (q % T::CH16) ^ (r & T::SWZ);
-            const unsigned char *gp = cbb + static_cast<int64_t>(chunk) * T::CHUNKB + r * T::ROWB + j * 16;
+            const unsigned char *gp = cbb + (static_cast<int64_t>(chunk) * T::CHUNKB + so.uni(k)) + so.lane(k);
             unsigned char *d = lds + buf * LY::BUFB + (k * kRsThreads + wave * kWave) * 16;
             __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)gp,
                                              (__attribute__((address_space(3))) void *)d, 16, 0, 0);
