@@ -878,26 +878,58 @@ aq_status euclid_encode_impl(aq_ctx *ctx, const aq_codebooks *cb, const aq_frame
     const int64_t frames_per_block = static_cast<int64_t>(kWaves) * FG * 16;
     const int64_t tiles = (M + frames_per_block - 1) / frames_per_block;
     const int nch = static_cast<int>(cb->N / kk->cc);
+    const int64_t tiles8 = (tiles + 7) / 8 * 8;
     int nsplit = 1;
     for (int sp = 1; sp <= 4; ++sp)
         if (nch % sp == 0 && tiles * sp <= 2 * cus) nsplit = sp;
-    // Grids of several rounds: the split count whose last round of blocks is
-    // fullest, at a small price per split (each split loads its frames again
-    // and the select merges one more key list).
+    int nsplit2 = nsplit;
+    int64_t tile2 = tiles8;   // no second part
+    // Grids of several rounds of blocks: the tiles that fill whole rounds
+    // take nsplit splits, the rest (the last, partial round) nsplit2 >=
+    // nsplit, so that the last round's blocks are short; both chosen to
+    // minimise the estimated time in whole-codebook block times, at a small
+    // price per split (each split loads its frames again and the select
+    // merges one more key list: about 6 %; k-means took the same time with
+    // 2 and 4 splits throughout).
     if (tiles > 2 * cus) {
         const int64_t slots = static_cast<int64_t>(cus) * sweep_blocks_per_cu(ks);
+        auto cost = [&](int64_t blocks, int sp) {
+            return static_cast<double>((blocks + slots - 1) / slots) / sp * (1.0 + 0.06 * (sp - 1));
+        };
         double best = 1e30;
         for (int sp : {1, 2, 4}) {
             if (nch % sp != 0) continue;
-            const int64_t blocks = (tiles + 7) / 8 * 8 * sp;
-            // (per split about 6 %: k-means took the same time with 2 and 4)
-            const double rounds = static_cast<double>((blocks + slots - 1) / slots) / sp * (1.0 + 0.06 * (sp - 1));
-            if (rounds < best) {
-                best = rounds;
-                nsplit = sp;
+            const double one = cost(tiles8 * sp, sp);
+            if (one < best) {
+                best = one;
+                nsplit = nsplit2 = sp;
+                tile2 = tiles8;
+            }
+            const int64_t t1 = (tiles8 * sp / slots) * slots / sp / 8 * 8;   // tiles of the whole rounds
+            if (t1 <= 0 || t1 >= tiles) continue;
+            for (int sp2 : {2, 4, 8, 16}) {
+                if (sp2 <= sp || nch % sp2 != 0) continue;
+                const double two = cost(t1 * sp, sp) + cost((tiles - t1 + 7) / 8 * 8 * sp2, sp2);
+                if (two < best) {
+                    best = two;
+                    nsplit = sp;
+                    nsplit2 = sp2;
+                    tile2 = t1;
+                }
             }
         }
     }
+    {
+        // test hook: one split count for every tile (the results are the
+        // same bits either way)
+        const char *e = std::getenv("AQ_EUCLID_TEST_SPLIT");
+        if (e && std::strcmp(e, "uniform") == 0) {
+            nsplit2 = nsplit;
+            tile2 = tiles8;
+        }
+    }
+    const int maxsplit = nsplit2 > nsplit ? nsplit2 : nsplit;
+    const int64_t sweep_blocks = tile2 * nsplit + (tiles8 - tile2) * nsplit2;
     const int64_t ngroups = (M + 15) / 16;
 
     // Work buffers: the residual (the caller's buffer when given; [M, H]),
@@ -915,7 +947,7 @@ aq_status euclid_encode_impl(aq_ctx *ctx, const aq_codebooks *cb, const aq_frame
     }
     float *keys = nullptr;
     {
-        const size_t key_bytes = static_cast<size_t>(nsplit) * ngroups * topl * kWave * sizeof(float);
+        const size_t key_bytes = static_cast<size_t>(maxsplit) * ngroups * topl * kWave * sizeof(float);
         void *w = nullptr;
         aq_status st = arena.get(4, key_bytes + 3 * static_cast<size_t>(M) * sizeof(float), &w);
         if (st != AQ_OK) return st;
@@ -1024,8 +1056,10 @@ aq_status euclid_encode_impl(aq_ctx *ctx, const aq_codebooks *cb, const aq_frame
         a.flags = ctx->d_flags;
         a.exact_only = cb->exact_only ? 1 : 0;
         a.keys = keys;
-        a.norms = keys + static_cast<size_t>(nsplit) * ngroups * topl * kWave;
+        a.norms = keys + static_cast<size_t>(maxsplit) * ngroups * topl * kWave;
         a.nsplit = nsplit;
+        a.nsplit2 = nsplit2;
+        a.tile2 = tile2;
         a.svals = svals;
         a.scap = scap;
         a.slot_done = slot_done;
@@ -1034,7 +1068,7 @@ aq_status euclid_encode_impl(aq_ctx *ctx, const aq_codebooks *cb, const aq_frame
             AQ_HIP(ctx, hipGetLastError());
         }
         // (the no-allocation entry point creates no timing events)
-        aq_launch_timed(ctx, !arena.base, sweep, dim3(static_cast<unsigned>((tiles + 7) / 8 * 8 * nsplit)), dim3(kThreads),
+        aq_launch_timed(ctx, !arena.base, sweep, dim3(static_cast<unsigned>(sweep_blocks)), dim3(kThreads),
                         static_cast<uint32_t>(lds), a);
         AQ_HIP(ctx, hipGetLastError());
         hipLaunchKernelGGL(select, dim3(static_cast<unsigned>((ngroups + kWaves - 1) / kWaves)), dim3(kThreads), 0,

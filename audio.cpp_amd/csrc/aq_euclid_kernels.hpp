@@ -172,7 +172,9 @@ struct StageArgs {
     int exact_only;
     float *keys;             // sweep -> select: [nsplit][M/16][TOPL][64] score keys
     float *norms;            // sweep -> select: [3][M] |x~|^2, |x - x~|^2, |x|^2
-    int nsplit;              // code splits of the sweep
+    int nsplit;              // code splits of the sweep (tiles before tile2)
+    int nsplit2;             // code splits of the tiles from tile2 on (a finer last round)
+    int64_t tile2;           // first tile of the second part (a multiple of 8)
     float *svals;            // [scap, N] exact values of the scanned frames, by list slot
     int scap;                // frames whose values the exact scan spreads over its grid
     int32_t *slot_done;      // [scap] chunks done per slot (zero between stages)
@@ -813,15 +815,25 @@ __global__ __launch_bounds__(kThreads, sweep_blocks_per_cu(KS)) void euclid_swee
     const int kq = lane >> 4;       // which 8-element quarter of each 32-wide K slice
     // Block order: the nsplit blocks of a frame tile have ids 8 apart, so
     // the round-robin dispatch over the 8 XCDs puts them on one XCD and the
-    // second read of the tile's frames is served by that XCD's L2.  Ids
-    // past the last tile (the grid is a whole number of 8-tile groups) exit.
-    const int per = 8 * a.nsplit;
-    const int split = static_cast<int>(blockIdx.x % per) / 8;
-    const int64_t tile = static_cast<int64_t>(blockIdx.x / per) * 8 + (blockIdx.x % per) % 8;
+    // second read of the tile's frames is served by that XCD's L2.  Tiles
+    // from tile2 on (the grid's last, partial round) take nsplit2 splits
+    // with the same order after the first part's blocks.  Ids past the last
+    // tile (each part is a whole number of 8-tile groups) exit.
+    int64_t bi = blockIdx.x;
+    int nsp = a.nsplit;
+    int64_t tbase = 0;
+    if (bi >= a.tile2 * a.nsplit) {
+        bi -= a.tile2 * a.nsplit;
+        nsp = a.nsplit2;
+        tbase = a.tile2;
+    }
+    const int per = 8 * nsp;
+    const int split = static_cast<int>(bi % per) / 8;
+    const int64_t tile = tbase + (bi / per) * 8 + (bi % per) % 8;
     if (tile * (kWaves * FG * 16) >= a.M) return;
     const int64_t m_base = (tile * kWaves + wave) * (FG * 16);
     const int N = a.N;
-    const int cps = (N / T::CC) / a.nsplit;   // chunks per split
+    const int cps = (N / T::CC) / nsp;   // chunks per split
     const int c0 = split * cps, c1 = c0 + cps;
 
     using MX = Mx;
@@ -1644,7 +1656,9 @@ __global__ __launch_bounds__(kThreads) void euclid_select_kernel(StageArgs a) {
     float top[TOPL], taul = -INFINITY;
 #pragma unroll
     for (int j = 0; j < TOPL; ++j) top[j] = -INFINITY;
-    for (int sp = 0; sp < a.nsplit; ++sp) {
+    // the sweep's split count for this group's tile
+    const int nsp = m_base >= a.tile2 * (kWaves * groups_for(KS) * 16) ? a.nsplit2 : a.nsplit;
+    for (int sp = 0; sp < nsp; ++sp) {
 #pragma unroll
         for (int j = 0; j < TOPL; ++j) {
             const float key = a.keys[((static_cast<int64_t>(sp) * ngroups + gi) * TOPL + j) * kWave + lane];

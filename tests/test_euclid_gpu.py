@@ -643,3 +643,30 @@ def test_cascade_verification_corrects_outputs_in_place(torch, ctx, oracle, monk
         assert np.array_equal(bits(out["dist"]), bits(ref["dist"]))
     if topk:
         check_topk(out, ref)
+
+
+def test_sweep_split_parts_agree(torch, ctx, oracle, monkeypatch):
+    """A grid of several rounds of sweep blocks takes one code-split count
+    for the tiles of its whole rounds and a finer one for the last, partial
+    round.  The results are the bits of one split count for every tile
+    (test hook AQ_EUCLID_TEST_SPLIT=uniform) and, on frames of both parts,
+    the reference's."""
+    import aqmi
+    from aqmi import synth
+
+    M, K, N, Q = 70000, 512, 1024, 2   # 547 tiles of 128 frames: 512 in whole rounds, then 35
+    print(f"[gpu] sweep split parts M={M} K={K} N={N} Q={Q}", flush=True)
+    x = synth.normal(91, 1, (M, K), 1.0)
+    cb = synth.normal(91, 2, (Q, N, K), 1.0 / 16)
+    monkeypatch.setenv("AQ_EUCLID_PIPELINE", "stages")
+    two = run(torch, ctx, cb, aqmi.HIGGS, x)
+    monkeypatch.setenv("AQ_EUCLID_TEST_SPLIT", "uniform")
+    one = run(torch, ctx, cb, aqmi.HIGGS, x)
+    assert np.array_equal(two["idx"], one["idx"])
+    assert np.array_equal(bits(two["dist"]), bits(one["dist"]))
+    assert np.array_equal(bits(two["residual"]), bits(one["residual"]))
+    for lo in (0, 68000):   # a tile of the whole rounds, one of the last round
+        sub = dict(x=x[lo:lo + 1000], M=1000, K=K, Q=Q, N=N, codebook=cb)
+        ref = oracle.higgs_rvq(sub)
+        assert np.array_equal(two["idx"][lo:lo + 1000], ref["idx"])
+        assert np.array_equal(bits(two["dist"][lo:lo + 1000]), bits(ref["dist"]))
