@@ -227,131 +227,61 @@ __device__ __host__ inline int tb_sw(int u4, int t) {
     return (DI & (DI - 1)) == 0 ? (u4 ^ (t & (DI - 1))) : u4;
 }
 
-template <int DI, int FW, bool RECON, int PF, bool CBG, int ORDER>
-__global__ __launch_bounds__(kMaxBlock, 1) void dac_encode_kernel(
-    const float *__restrict__ x, int64_t M, int Q, int N, const float4 *__restrict__ images, int64_t stride_f4,
-    int64_t img_f4, const float *__restrict__ tables, int32_t *__restrict__ idx, float *__restrict__ residual,
-    float *__restrict__ recon, const int32_t *__restrict__ force_idx, int32_t *__restrict__ flags, int has_bin,
-    int key_bits, float margin, int exact_only, float qeps, int64_t dbuf_f4, int ld, int recon_acc) {
-    // ld: row stride of idx and force_idx; recon_acc: recon holds the sum of
-    // earlier stages' z (another stage set's), which this cascade adds to.
-    // stride_f4: float4 per stage image; img_f4: the prefix staged in LDS
-    // (the whole image, or W_in + b_in when CBG reads c_hat from memory).
-    extern __shared__ float4 lds[];
+// In-projection of a wave's FW frames in one of ggml's summation orders:
+// afterwards lane 16 g holds outputs 2 g and 2 g + 1 of each frame in wred.
+// win: the stage's W_in in LDS (the order's layout); rt: the wave's D-float
+// LDS area for the transposed frame (tinyBLAS order only).
+template <int DI, int FW, int ORDER>
+__device__ __forceinline__ void project_frames(const float (&r)[FW][DI], const float4 *win, float *rt, int lane,
+                                               float (&wred)[FW][2]) {
     constexpr int D = DI * kWave;
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x / kWave;
-    const int waves_per_block = blockDim.x / kWave;
-    const int64_t m_first = (static_cast<int64_t>(blockIdx.x) * waves_per_block + wave) * FW;
-
-    int64_t mrow[FW];
-    bool active[FW];
-    float r[FW][DI];
-    float rc[FW][DI];
+    if (ORDER == 1) {
+        // ---- in-projection, tinyBLAS order (sgemm.cpp:527-545: 16 FMA
+        // accumulators over k = 16 u + t, then _mm512_reduce_add_ps) ----
+        // Lane L = 16 g + t runs accumulator t of outputs 2g and 2g+1 over
+        // the frame's elements k = 16 u + t, read from a transposed copy
+        // of the residual in LDS (the cascade keeps k = L + 64 i per lane).
+        const int t = lane & 15, g = lane >> 4;
+        const float4 *w0 = win + (2 * g * 16 + t) * DI;
+        const float4 *w1 = win + ((2 * g + 1) * 16 + t) * DI;
 #pragma unroll
-    for (int f = 0; f < FW; ++f) {
-        active[f] = (m_first + f) < M;
-        mrow[f] = active[f] ? (m_first + f) : (M - 1);
+        for (int f = 0; f < FW; ++f) {
 #pragma unroll
-        for (int i = 0; i < DI; ++i) {
-            r[f][i] = x[mrow[f] * D + i * kWave + lane];
-            rc[f][i] = -0.0f;   // -0 + z == z exactly, for every z
-            if (RECON && recon_acc) rc[f][i] = recon[mrow[f] * D + i * kWave + lane];
+            for (int i = 0; i < DI; ++i) rt[t * (D / 16) + tb_sw<DI>(i, t) * 4 + g] = r[f][i];
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+            for (int u4 = 0; u4 < DI; ++u4) {
+                const int sw = tb_sw<DI>(u4, t);
+                const float4 rv = *reinterpret_cast<const float4 *>(rt + t * (D / 16) + sw * 4);
+                const float4 x0 = w0[sw], x1 = w1[sw];
+                a0 = __fmaf_rn(x0.x, rv.x, a0);
+                a0 = __fmaf_rn(x0.y, rv.y, a0);
+                a0 = __fmaf_rn(x0.z, rv.z, a0);
+                a0 = __fmaf_rn(x0.w, rv.w, a0);
+                a1 = __fmaf_rn(x1.x, rv.x, a1);
+                a1 = __fmaf_rn(x1.y, rv.y, a1);
+                a1 = __fmaf_rn(x1.z, rv.z, a1);
+                a1 = __fmaf_rn(x1.w, rv.w, a1);
+            }
+            a0 = row_ror_add<8>(a0);
+            a0 = row_ror_add<4>(a0);
+            a0 = row_ror_add<2>(a0);
+            a0 = row_ror_add<1>(a0);
+            a1 = row_ror_add<8>(a1);
+            a1 = row_ror_add<4>(a1);
+            a1 = row_ror_add<2>(a1);
+            a1 = row_ror_add<1>(a1);
+            wred[f][0] = a0;
+            wred[f][1] = a1;
+            // the next frame overwrites rt
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         }
-    }
-
-    const int NC = N / kWave;
-    const int key_mask = (1 << key_bits) - 1;
-
-    f32x4 pre[PF > 0 ? PF : 1];
-    if (PF > 0) fetch_image<PF>(pre, images, img_f4);
-
-    for (int s = 0; s < Q; ++s) {
-        // dbuf_f4 > 0: two LDS images, stage s in the one at (s & 1) * dbuf_f4.
-        // The image written here was last read two stages ago, and every wave
-        // has finished that stage once it passed the previous stage's barrier,
-        // so one barrier per stage suffices.
-        float4 *img_lds = lds + ((s & 1) ? dbuf_f4 : 0);
-        if (dbuf_f4 == 0) __syncthreads();
-        if (PF > 0) {
-            f32x4 *lds4 = reinterpret_cast<f32x4 *>(img_lds);
-#pragma unroll
-            for (int k = 0; k < PF; ++k) {
-                const int64_t t = threadIdx.x + static_cast<int64_t>(k) * blockDim.x;
-                if (t < img_f4) lds4[t] = pre[k];
-            }
-        } else {
-            const float4 *img = images + static_cast<int64_t>(s) * stride_f4;
-            for (int64_t t0 = 0; t0 < img_f4; t0 += static_cast<int64_t>(kCopyBatch) * blockDim.x) {
-                float4 buf[kCopyBatch];
-#pragma unroll
-                for (int k = 0; k < kCopyBatch; ++k) {
-                    const int64_t t = t0 + threadIdx.x + static_cast<int64_t>(k) * blockDim.x;
-                    buf[k] = img[t < img_f4 ? t : img_f4 - 1];
-                }
-#pragma unroll
-                for (int k = 0; k < kCopyBatch; ++k) {
-                    const int64_t t = t0 + threadIdx.x + static_cast<int64_t>(k) * blockDim.x;
-                    if (t < img_f4) img_lds[t] = buf[k];
-                }
-            }
-        }
-        __syncthreads();
-        if (PF > 0 && s + 1 < Q) fetch_image<PF>(pre, images + static_cast<int64_t>(s + 1) * stride_f4, img_f4);
-        const float4 *win = img_lds;
-        const float *bin = reinterpret_cast<const float *>(img_lds + 2 * DI * kWave);
-        const float4 *chat = CBG ? images + static_cast<int64_t>(s) * stride_f4 + 2 * DI * kWave + 2
-                                 : img_lds + 2 * DI * kWave + 2;
-
-        float wred[FW][2];   // lane 16 g holds outputs 2 g and 2 g + 1 of each frame
-        if (ORDER == 1) {
-            // ---- in-projection, tinyBLAS order (sgemm.cpp:527-545: 16 FMA
-            // accumulators over k = 16 u + t, then _mm512_reduce_add_ps) ----
-            // Lane L = 16 g + t runs accumulator t of outputs 2g and 2g+1 over
-            // the frame's elements k = 16 u + t, read from a transposed copy
-            // of the residual in LDS (the cascade keeps k = L + 64 i per lane).
-            float *rt = reinterpret_cast<float *>(lds + img_f4 + dbuf_f4) + wave * D;
-            const int t = lane & 15, g = lane >> 4;
-            const float4 *w0 = win + (2 * g * 16 + t) * DI;
-            const float4 *w1 = win + ((2 * g + 1) * 16 + t) * DI;
-#pragma unroll
-            for (int f = 0; f < FW; ++f) {
-#pragma unroll
-                for (int i = 0; i < DI; ++i) rt[t * (D / 16) + tb_sw<DI>(i, t) * 4 + g] = r[f][i];
-                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-                __builtin_amdgcn_wave_barrier();
-                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-                float a0 = 0.0f, a1 = 0.0f;
-#pragma unroll
-                for (int u4 = 0; u4 < DI; ++u4) {
-                    const int sw = tb_sw<DI>(u4, t);
-                    const float4 rv = *reinterpret_cast<const float4 *>(rt + t * (D / 16) + sw * 4);
-                    const float4 x0 = w0[sw], x1 = w1[sw];
-                    a0 = __fmaf_rn(x0.x, rv.x, a0);
-                    a0 = __fmaf_rn(x0.y, rv.y, a0);
-                    a0 = __fmaf_rn(x0.z, rv.z, a0);
-                    a0 = __fmaf_rn(x0.w, rv.w, a0);
-                    a1 = __fmaf_rn(x1.x, rv.x, a1);
-                    a1 = __fmaf_rn(x1.y, rv.y, a1);
-                    a1 = __fmaf_rn(x1.z, rv.z, a1);
-                    a1 = __fmaf_rn(x1.w, rv.w, a1);
-                }
-                a0 = row_ror_add<8>(a0);
-                a0 = row_ror_add<4>(a0);
-                a0 = row_ror_add<2>(a0);
-                a0 = row_ror_add<1>(a0);
-                a1 = row_ror_add<8>(a1);
-                a1 = row_ror_add<4>(a1);
-                a1 = row_ror_add<2>(a1);
-                a1 = row_ror_add<1>(a1);
-                wred[f][0] = a0;
-                wred[f][1] = a1;
-                // the next frame overwrites rt
-                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-                __builtin_amdgcn_wave_barrier();
-                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            }
-        } else {
+    } else {
         // ---- in-projection: one FMA chain per lane and output, ggml order ----
         float acc[FW][8];
 #pragma unroll
@@ -423,48 +353,212 @@ __global__ __launch_bounds__(kMaxBlock, 1) void dac_encode_kernel(
             wred[f][0] = w[0];
             wred[f][1] = w[1];
         }
+    }
+}
+
+// The stage's queries, normalised as l2_normalize_last does, for all FW
+// frames of a wave at once: lane 8 f + o returns output o of frame f (lanes
+// 8 FW .. 63 carry don't-care values).  bias: b_in[lane & 7] when has_bin.
+template <int FW>
+__device__ __forceinline__ float normalise_queries(const float (&wred)[FW][2], int lane, bool has_bin, float bias,
+                                                   float qeps) {
+    // Output o of frame f moves to lane 8 f + o: in row g, lane 16 g + j
+    // (j < 2 FW) offers wred[j / 2][j % 2], i.e. output 2 g + j % 2 of
+    // frame j / 2.  Lanes 8 FW .. 63 carry don't-care values.
+    const int jrow = lane & 15;
+    float offer = wred[0][0];
+#pragma unroll
+    for (int f = 0; f < FW; ++f) {
+        if (jrow == 2 * f) offer = wred[f][0];
+        if (jrow == 2 * f + 1) offer = wred[f][1];
+    }
+    const int ol = lane & 7;
+    float p = __shfl(offer, 16 * (ol >> 1) + 2 * (lane >> 3) + (ol & 1));
+    if (has_bin) p = __fadd_rn(p, bias);
+    // l2_normalize_last: fp32 squares, double row sum in output order,
+    // + eps, sqrt, divide.  Lane 8 f sums ((sq_0 + sq_1) + sq_2) + ... of
+    // frame f, reading sq_k from lane 8 f + k (the leading 0.0 + sq_0 of
+    // the reference is sq_0 exactly: a square is +0 or more, or NaN).
+    const float sq = __fmul_rn(p, p);
+    double ss = static_cast<double>(sq);
+    ss += static_cast<double>(row_shl<1>(sq));
+    ss += static_cast<double>(row_shl<2>(sq));
+    ss += static_cast<double>(row_shl<3>(sq));
+    ss += static_cast<double>(row_shl<4>(sq));
+    ss += static_cast<double>(row_shl<5>(sq));
+    ss += static_cast<double>(row_shl<6>(sq));
+    ss += static_cast<double>(row_shl<7>(sq));
+    // ggml_scale_bias(sum, 1, eps): 1e-12 (Fish), 1e-20 (Vevo2), none
+    // (IndexTTS2: qeps = 0, and sum + 0 == sum for a sum >= +0)
+    const float den8 = sqrt_rn(__fadd_rn(static_cast<float>(ss), qeps));
+    return __fdiv_rn(p, __shfl(den8, lane & ~7));
+}
+
+// Frame f's normalised query in scalar registers (pn[f][o] from lane 8 f + o)
+// and whether all of its outputs are finite.
+template <int FW>
+__device__ __forceinline__ void query_scalars(float qv, float (&pn)[FW][8], bool (&finite)[FW]) {
+    const uint64_t good = __ballot((qv - qv) == 0.0f);
+#pragma unroll
+    for (int f = 0; f < FW; ++f) {
+        finite[f] = ((good >> (8 * f)) & 0xffull) == 0xffull;
+#pragma unroll
+        for (int o = 0; o < 8; ++o) pn[f][o] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(qv), 8 * f + o));
+    }
+}
+
+// The wave's frames: residual rows into registers (rc: -0, or the recon
+// rows that this cascade adds to), and out again at the end.
+template <int DI, int FW, bool RECON>
+__device__ __forceinline__ void load_frames(const float *__restrict__ x, int64_t M, int64_t m_first, int lane,
+                                            const float *__restrict__ recon, int recon_acc, int64_t (&mrow)[FW],
+                                            bool (&active)[FW], float (&r)[FW][DI], float (&rc)[FW][DI]) {
+    constexpr int D = DI * kWave;
+#pragma unroll
+    for (int f = 0; f < FW; ++f) {
+        active[f] = (m_first + f) < M;
+        mrow[f] = active[f] ? (m_first + f) : (M - 1);
+#pragma unroll
+        for (int i = 0; i < DI; ++i) {
+            r[f][i] = x[mrow[f] * D + i * kWave + lane];
+            rc[f][i] = -0.0f;   // -0 + z == z exactly, for every z
+            if (RECON && recon_acc) rc[f][i] = recon[mrow[f] * D + i * kWave + lane];
         }
-        // ---- query normalisation, every frame of the wave at once ----
-        // Output o of frame f moves to lane 8 f + o: in row g, lane 16 g + j
-        // (j < 2 FW) offers wred[j / 2][j % 2], i.e. output 2 g + j % 2 of
-        // frame j / 2.  Lanes 8 FW .. 63 carry don't-care values.
-        const int jrow = lane & 15;
-        float offer = wred[0][0];
+    }
+}
+
+template <int DI, int FW, bool RECON>
+__device__ __forceinline__ void store_frames(const int64_t (&mrow)[FW], const bool (&active)[FW], int lane,
+                                             const float (&r)[FW][DI], const float (&rc)[FW][DI],
+                                             float *__restrict__ residual, float *__restrict__ recon) {
+    constexpr int D = DI * kWave;
+#pragma unroll
+    for (int f = 0; f < FW; ++f) {
+        if (!active[f]) continue;
+#pragma unroll
+        for (int i = 0; i < DI; ++i) {
+            if (residual) residual[mrow[f] * D + i * kWave + lane] = r[f][i];
+            if (RECON) recon[mrow[f] * D + i * kWave + lane] = rc[f][i];
+        }
+    }
+}
+
+// Codes out, then the out-projection by table gather and the residual update
+// of a wave's FW frames at stage s (force_idx: teacher forcing, checked).
+template <int DI, int FW, bool RECON>
+__device__ __forceinline__ void apply_codes(const int (&code)[FW], int s, int N, const int64_t (&mrow)[FW],
+                                            const bool (&active)[FW], int lane, int ld, int32_t *__restrict__ idx,
+                                            const int32_t *__restrict__ force_idx, int32_t *__restrict__ flags,
+                                            const float *__restrict__ tables, float (&r)[FW][DI], float (&rc)[FW][DI]) {
+    constexpr int D = DI * kWave;
+    int use[FW];
+#pragma unroll
+    for (int f = 0; f < FW; ++f) {
+        if (lane == 0 && active[f]) idx[mrow[f] * ld + s] = code[f];
+        use[f] = code[f];
+        if (force_idx) {
+            use[f] = force_idx[mrow[f] * ld + s];
+            if (use[f] < 0 || use[f] >= N) {
+                if (lane == 0) flags[AQ_FLAG_BAD_INDEX] = 1;
+                use[f] = 0;
+            }
+        }
+    }
+    if (tables) {   // (codes only: no out-projection was uploaded)
+        // Every row load of the wave's frames is issued before the first
+        // use, so the gathers overlap instead of waiting one by one.
+        float z[FW][DI];
 #pragma unroll
         for (int f = 0; f < FW; ++f) {
-            if (jrow == 2 * f) offer = wred[f][0];
-            if (jrow == 2 * f + 1) offer = wred[f][1];
+            const float *zrow = tables + (static_cast<int64_t>(s) * N + use[f]) * D;
+#pragma unroll
+            for (int i = 0; i < DI; ++i) z[f][i] = zrow[i * kWave + lane];
         }
-        const int ol = lane & 7;
-        float p = __shfl(offer, 16 * (ol >> 1) + 2 * (lane >> 3) + (ol & 1));
-        if (has_bin) p = __fadd_rn(p, bin[ol]);
-        // l2_normalize_last: fp32 squares, double row sum in output order,
-        // + eps, sqrt, divide.  Lane 8 f sums ((sq_0 + sq_1) + sq_2) + ... of
-        // frame f, reading sq_k from lane 8 f + k (the leading 0.0 + sq_0 of
-        // the reference is sq_0 exactly: a square is +0 or more, or NaN).
-        const float sq = __fmul_rn(p, p);
-        double ss = static_cast<double>(sq);
-        ss += static_cast<double>(row_shl<1>(sq));
-        ss += static_cast<double>(row_shl<2>(sq));
-        ss += static_cast<double>(row_shl<3>(sq));
-        ss += static_cast<double>(row_shl<4>(sq));
-        ss += static_cast<double>(row_shl<5>(sq));
-        ss += static_cast<double>(row_shl<6>(sq));
-        ss += static_cast<double>(row_shl<7>(sq));
-        // ggml_scale_bias(sum, 1, eps): 1e-12 (Fish), 1e-20 (Vevo2), none
-        // (IndexTTS2: qeps = 0, and sum + 0 == sum for a sum >= +0)
-        const float den8 = sqrt_rn(__fadd_rn(static_cast<float>(ss), qeps));
-        const float qv = __fdiv_rn(p, __shfl(den8, lane & ~7));
-        const uint64_t good = __ballot((qv - qv) == 0.0f);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int f = 0; f < FW; ++f)
+#pragma unroll
+            for (int i = 0; i < DI; ++i) {
+                r[f][i] = __fsub_rn(r[f][i], z[f][i]);
+                if (RECON) rc[f][i] = __fadd_rn(rc[f][i], z[f][i]);
+            }
+    }
+}
+
+template <int DI, int FW, bool RECON, int PF, bool CBG, int ORDER>
+__global__ __launch_bounds__(kMaxBlock, 1) void dac_encode_kernel(
+    const float *__restrict__ x, int64_t M, int Q, int N, const float4 *__restrict__ images, int64_t stride_f4,
+    int64_t img_f4, const float *__restrict__ tables, int32_t *__restrict__ idx, float *__restrict__ residual,
+    float *__restrict__ recon, const int32_t *__restrict__ force_idx, int32_t *__restrict__ flags, int has_bin,
+    int key_bits, float margin, int exact_only, float qeps, int64_t dbuf_f4, int ld, int recon_acc) {
+    // ld: row stride of idx and force_idx; recon_acc: recon holds the sum of
+    // earlier stages' z (another stage set's), which this cascade adds to.
+    // stride_f4: float4 per stage image; img_f4: the prefix staged in LDS
+    // (the whole image, or W_in + b_in when CBG reads c_hat from memory).
+    extern __shared__ float4 lds[];
+    constexpr int D = DI * kWave;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int waves_per_block = blockDim.x / kWave;
+    const int64_t m_first = (static_cast<int64_t>(blockIdx.x) * waves_per_block + wave) * FW;
+
+    int64_t mrow[FW];
+    bool active[FW];
+    float r[FW][DI];
+    float rc[FW][DI];
+    load_frames<DI, FW, RECON>(x, M, m_first, lane, recon, recon_acc, mrow, active, r, rc);
+
+    const int NC = N / kWave;
+    const int key_mask = (1 << key_bits) - 1;
+
+    f32x4 pre[PF > 0 ? PF : 1];
+    if (PF > 0) fetch_image<PF>(pre, images, img_f4);
+
+    for (int s = 0; s < Q; ++s) {
+        // dbuf_f4 > 0: two LDS images, stage s in the one at (s & 1) * dbuf_f4.
+        // The image written here was last read two stages ago, and every wave
+        // has finished that stage once it passed the previous stage's barrier,
+        // so one barrier per stage suffices.
+        float4 *img_lds = lds + ((s & 1) ? dbuf_f4 : 0);
+        if (dbuf_f4 == 0) __syncthreads();
+        if (PF > 0) {
+            f32x4 *lds4 = reinterpret_cast<f32x4 *>(img_lds);
+#pragma unroll
+            for (int k = 0; k < PF; ++k) {
+                const int64_t t = threadIdx.x + static_cast<int64_t>(k) * blockDim.x;
+                if (t < img_f4) lds4[t] = pre[k];
+            }
+        } else {
+            const float4 *img = images + static_cast<int64_t>(s) * stride_f4;
+            for (int64_t t0 = 0; t0 < img_f4; t0 += static_cast<int64_t>(kCopyBatch) * blockDim.x) {
+                float4 buf[kCopyBatch];
+#pragma unroll
+                for (int k = 0; k < kCopyBatch; ++k) {
+                    const int64_t t = t0 + threadIdx.x + static_cast<int64_t>(k) * blockDim.x;
+                    buf[k] = img[t < img_f4 ? t : img_f4 - 1];
+                }
+#pragma unroll
+                for (int k = 0; k < kCopyBatch; ++k) {
+                    const int64_t t = t0 + threadIdx.x + static_cast<int64_t>(k) * blockDim.x;
+                    if (t < img_f4) img_lds[t] = buf[k];
+                }
+            }
+        }
+        __syncthreads();
+        if (PF > 0 && s + 1 < Q) fetch_image<PF>(pre, images + static_cast<int64_t>(s + 1) * stride_f4, img_f4);
+        const float4 *win = img_lds;
+        const float *bin = reinterpret_cast<const float *>(img_lds + 2 * DI * kWave);
+        const float4 *chat = CBG ? images + static_cast<int64_t>(s) * stride_f4 + 2 * DI * kWave + 2
+                                 : img_lds + 2 * DI * kWave + 2;
+
+        float wred[FW][2];   // lane 16 g holds outputs 2 g and 2 g + 1 of each frame
+        project_frames<DI, FW, ORDER>(r, win, ORDER == 1 ? reinterpret_cast<float *>(lds + img_f4 + dbuf_f4) + wave * D : nullptr,
+                                      lane, wred);
+        // ---- query normalisation, every frame of the wave at once ----
+        const float qv = normalise_queries<FW>(wred, lane, has_bin != 0, has_bin ? bin[lane & 7] : 0.0f, qeps);
         float pn[FW][8];
         bool finite[FW];
-#pragma unroll
-        for (int f = 0; f < FW; ++f) {
-            finite[f] = ((good >> (8 * f)) & 0xffull) == 0xffull;
-#pragma unroll
-            for (int o = 0; o < 8; ++o) pn[f][o] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(qv), 8 * f + o));
-        }
-
+        query_scalars<FW>(qv, pn, finite);
         // ---- approximate scores, two best keys per lane ----
         const float pinf = opaque_inf();
         const int vmask = in_vgpr(key_mask);
@@ -509,50 +603,232 @@ __global__ __launch_bounds__(kMaxBlock, 1) void dac_encode_kernel(
             }
         }
 
-        // ---- out-projection by table gather, residual update ----
-        int use[FW];
-#pragma unroll
-        for (int f = 0; f < FW; ++f) {
-            if (lane == 0 && active[f]) idx[mrow[f] * ld + s] = code[f];
-            use[f] = code[f];
-            if (force_idx) {
-                use[f] = force_idx[mrow[f] * ld + s];
-                if (use[f] < 0 || use[f] >= N) {
-                    if (lane == 0) flags[AQ_FLAG_BAD_INDEX] = 1;
-                    use[f] = 0;
-                }
-            }
-        }
-        if (tables) {   // (codes only: no out-projection was uploaded)
-            // Every row load of the wave's frames is issued before the first
-            // use, so the gathers overlap instead of waiting one by one.
-            float z[FW][DI];
-#pragma unroll
-            for (int f = 0; f < FW; ++f) {
-                const float *zrow = tables + (static_cast<int64_t>(s) * N + use[f]) * D;
-#pragma unroll
-                for (int i = 0; i < DI; ++i) z[f][i] = zrow[i * kWave + lane];
-            }
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int f = 0; f < FW; ++f)
-#pragma unroll
-                for (int i = 0; i < DI; ++i) {
-                    r[f][i] = __fsub_rn(r[f][i], z[f][i]);
-                    if (RECON) rc[f][i] = __fadd_rn(rc[f][i], z[f][i]);
-                }
-        }
+        apply_codes<DI, FW, RECON>(code, s, N, mrow, active, lane, ld, idx, force_idx, flags, tables, r, rc);
     }
 
+    store_frames<DI, FW, RECON>(mrow, active, lane, r, rc, residual, recon);
+}
+
+// ------------------------------------------------ scores on matrix cores
+// A variant of dac_encode_kernel for blocks of 8 waves x 3 frames, N a
+// multiple of 128 up to 1024 and D up to 1024.  The in-projection, the query
+// normalisation, the exact rescoring and the out-projection are the same;
+// the approximate scores run on fp16 matrix cores over the block's 24 frames:
+//  * Codes and queries are scaled by 2^12 and split into fp16 pairs
+//    (hi = fp16(v), lo = fp16(v - hi)), so one v_mfma_f32_16x16x32_f16 with
+//    k-slices (c_hi, c_lo, c_hi, c_lo) x (q_hi, q_hi, q_lo, q_lo) gives
+//    2^24 c.q for 16 codes x 16 frames.  The scaling keeps every operand that
+//    matters out of fp16's subnormal range.
+//  * Wave w scores codes [w N/8, (w+1) N/8) for all 24 frames (two 16-frame
+//    column tiles; frames 24-31 are zero) and keeps two keys per lane and
+//    frame; keys carry the code's index inside the wave's range.  The four
+//    lanes of a frame merge theirs by lane swaps, the block's eight waves
+//    through LDS.
+//  * The certificate bound covers the split (2^-22 relative per operand), the
+//    matrix core's fp32 accumulation of 32 products (taken as 2u per add),
+//    the fp16 flush of operands below 2^-14 (2^-26 after scaling back),
+//    ggml's own rounding and the key truncation.
+// Stage images hold W_in, b_in, c_hat and the split codebook (c16); each
+// part has one LDS copy, rewritten at a point where every wave has finished
+// reading it and made visible by the next barrier:
+//   W_in(s+1)  after barrier B_s (in-projections done), read after C_s
+//   c_hat(s)   after B_s (stage s - 1's selects done), read after C_s
+//   c16(s+1)   after C_s (scores done), read after B_{s+1}
+// with B_s after the queries are written and C_s after the keys are.
+constexpr int kMsWaves = 8;
+constexpr int kMsFw = 3;
+constexpr int kMsFrames = kMsWaves * kMsFw;   // frames per block (<= 32)
+constexpr int kMsPart = 4;                    // float4 per thread of each image part
+constexpr float kMsScale = 4096.0f;           // 2^12 before the fp16 split
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+// c16 region of a stage image: code n, part h (0 hi, 1 lo) at float4
+// (n / 16) * 32 + h * 16 + n % 16 (16 codes' parts contiguous: the MFMA
+// operand reads of a row of lanes are conflict-free).
+__host__ __device__ inline int64_t c16_at(int64_t n, int h) { return (n >> 4) * 32 + h * 16 + (n & 15); }
+
+template <int CTRL>
+__device__ inline float dpp_max(float v, float pinf) {
+    const int o = __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false);
+    return __builtin_amdgcn_fmed3f(v, __int_as_float(o), pinf);
+}
+// Maximum over each group of 8 lanes (xor 1, xor 2, half-row mirror).
+__device__ inline float max8(float v, float pinf) {
+    v = dpp_max<0xB1>(v, pinf);
+    v = dpp_max<0x4E>(v, pinf);
+    return dpp_max<0x141>(v, pinf);
+}
+// Two best keys of a lane pair given as {own, partner} (swap16 / swap32
+// results): best = max, second = the larger of the other best and the
+// better second.
+__device__ inline void merge_top2(float lo1, float hi1, float lo2, float hi2, float pinf, float &k1, float &k2) {
+    k1 = __builtin_amdgcn_fmed3f(lo1, hi1, pinf);
+    k2 = __builtin_amdgcn_fmed3f(lo1, hi1, __builtin_amdgcn_fmed3f(lo2, hi2, pinf));
+}
+
+template <int DI, bool RECON, int ORDER>
+__global__ __launch_bounds__(kMsWaves * kWave, 1) void dac_encode_ms_kernel(
+    const float *__restrict__ x, int64_t M, int Q, int N, const float4 *__restrict__ images, int64_t stride_f4,
+    const float *__restrict__ tables, int32_t *__restrict__ idx, float *__restrict__ residual,
+    float *__restrict__ recon, const int32_t *__restrict__ force_idx, int32_t *__restrict__ flags, int has_bin,
+    int key_bits, float margin, int exact_only, float qeps, int ld, int recon_acc) {
+    // margin: in units of the scaled scores (2^24 c.q); key_bits: bits of a
+    // code's index inside a wave's range of N / 8 codes.
+    extern __shared__ float4 lds[];
+    constexpr int FW = kMsFw;
+    constexpr int D = DI * kWave;
+    constexpr int kThreads = kMsWaves * kWave;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int64_t m_first = (static_cast<int64_t>(blockIdx.x) * kMsWaves + wave) * FW;
+    const int n2 = 2 * N;                    // float4 of c_hat, and of c16
+    const int64_t ch_off = 2 * D + 2;        // c_hat in the stage image (after W_in, b_in)
+    const int64_t c16_off = ch_off + n2;
+    float4 *w_lds = lds;                     // [2D]
+    float4 *ch_lds = lds + 2 * D;            // [2N]
+    float4 *c16_lds = ch_lds + n2;           // [2N]
+    float4 *qb = c16_lds + n2;               // [32 frames][hi, lo] of fp16 x 8
+    float2 *kb = reinterpret_cast<float2 *>(qb + 64);   // [8 waves][32 frames] two keys
+    float *rt = reinterpret_cast<float *>(qb + 64 + kMsWaves * 16) + wave * D;   // tinyBLAS order only
+
+    int64_t mrow[FW];
+    bool active[FW];
+    float r[FW][DI];
+    float rc[FW][DI];
+    load_frames<DI, FW, RECON>(x, M, m_first, lane, recon, recon_acc, mrow, active, r, rc);
+    if (threadIdx.x < (32 - kMsFrames) * 2) qb[kMsFrames * 2 + threadIdx.x] = float4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    f32x4 pw[kMsPart], pch[kMsPart], pc16[kMsPart];
+    auto fetch = [&](f32x4 (&dst)[kMsPart], const float4 *src, int cnt) {
+        const f32x4 *v = reinterpret_cast<const f32x4 *>(src);
 #pragma unroll
-    for (int f = 0; f < FW; ++f) {
-        if (!active[f]) continue;
-#pragma unroll
-        for (int i = 0; i < DI; ++i) {
-            if (residual) residual[mrow[f] * D + i * kWave + lane] = r[f][i];
-            if (RECON) recon[mrow[f] * D + i * kWave + lane] = rc[f][i];
+        for (int k = 0; k < kMsPart; ++k) {
+            const int t = static_cast<int>(threadIdx.x) + k * kThreads;
+            dst[k] = v[t < cnt ? t : cnt - 1];
         }
+    };
+    auto put = [&](float4 *dst, const f32x4 (&src)[kMsPart], int cnt) {
+        f32x4 *v = reinterpret_cast<f32x4 *>(dst);
+#pragma unroll
+        for (int k = 0; k < kMsPart; ++k) {
+            const int t = static_cast<int>(threadIdx.x) + k * kThreads;
+            if (t < cnt) v[t] = src[k];
+        }
+    };
+    auto image = [&](int s) { return images + static_cast<int64_t>(s) * stride_f4; };
+    fetch(pw, image(0), 2 * D);
+    fetch(pch, image(0) + ch_off, n2);
+    fetch(pc16, image(0) + c16_off, n2);
+    put(w_lds, pw, 2 * D);
+    put(c16_lds, pc16, n2);
+    if (Q > 1) {
+        fetch(pw, image(1), 2 * D);
+        fetch(pc16, image(1) + c16_off, n2);
     }
+    __syncthreads();
+
+    const int cpw = N / kMsWaves;            // codes per wave, a multiple of 16
+    const int key_mask = (1 << key_bits) - 1;
+    const int g = lane >> 4, j = lane & 15;
+    for (int s = 0; s < Q; ++s) {
+        const float bias = has_bin ? reinterpret_cast<const float *>(image(s) + 2 * D)[lane & 7] : 0.0f;
+        float wred[FW][2];
+        project_frames<DI, FW, ORDER>(r, w_lds, rt, lane, wred);
+        const float qv = normalise_queries<FW>(wred, lane, has_bin != 0, bias, qeps);
+        // The wave's queries into the block's B operands.
+        if (lane < 8 * FW) {
+            const float qs = qv * kMsScale;
+            const _Float16 hi = static_cast<_Float16>(qs);
+            const _Float16 lo = static_cast<_Float16>(qs - static_cast<float>(hi));
+            _Float16 *qh = reinterpret_cast<_Float16 *>(qb) + (wave * FW + (lane >> 3)) * 16 + (lane & 7);
+            qh[0] = hi;
+            qh[8] = lo;
+        }
+        __syncthreads();   // B_s
+        if (s + 1 < Q) {
+            put(w_lds, pw, 2 * D);
+            if (s + 2 < Q) fetch(pw, image(s + 2), 2 * D);
+        }
+        put(ch_lds, pch, n2);
+        if (s + 1 < Q) fetch(pch, image(s + 1) + ch_off, n2);
+
+        // ---- scores of this wave's codes for the block's frames ----
+        const float pinf = opaque_inf();
+        const int vmask = in_vgpr(key_mask);
+        float k1[2] = {-INFINITY, -INFINITY}, k2[2] = {-INFINITY, -INFINITY};
+        {
+            const f16x8 bq0 = *reinterpret_cast<const f16x8 *>(qb + j * 2 + (g >> 1));
+            const f16x8 bq1 = *reinterpret_cast<const f16x8 *>(qb + (16 + j) * 2 + (g >> 1));
+            const f16x8 *ca = reinterpret_cast<const f16x8 *>(c16_lds) + c16_at(static_cast<int64_t>(wave) * cpw + j, g & 1);
+            const int lane_id = in_vgpr(0) + 4 * g;   // rows 4 g + i of each 16-code tile
+            const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 2
+            for (int t = 0; t < cpw / 16; ++t) {
+                const f16x8 a = ca[t * 32];
+                const f32x4 s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq0, zero, 0, 0, 0);
+                const f32x4 s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq1, zero, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int id = lane_id + (t * 16 + i);
+                    const float key0 = __int_as_float((__float_as_int(s0[i]) & ~vmask) | id);
+                    k2[0] = __builtin_amdgcn_fmed3f(k1[0], k2[0], key0);
+                    k1[0] = __builtin_amdgcn_fmed3f(k1[0], key0, pinf);
+                    const float key1 = __int_as_float((__float_as_int(s1[i]) & ~vmask) | id);
+                    k2[1] = __builtin_amdgcn_fmed3f(k1[1], k2[1], key1);
+                    k1[1] = __builtin_amdgcn_fmed3f(k1[1], key1, pinf);
+                }
+            }
+        }
+        // the four lanes of a frame (16 apart), then the block's waves
+#pragma unroll
+        for (int ft = 0; ft < 2; ++ft) {
+            float lo1, hi1, lo2, hi2;
+            swap16(k1[ft], k1[ft], lo1, hi1);
+            swap16(k2[ft], k2[ft], lo2, hi2);
+            merge_top2(lo1, hi1, lo2, hi2, pinf, k1[ft], k2[ft]);
+            swap32(k1[ft], k1[ft], lo1, hi1);
+            swap32(k2[ft], k2[ft], lo2, hi2);
+            merge_top2(lo1, hi1, lo2, hi2, pinf, k1[ft], k2[ft]);
+        }
+        if (g == 0) kb[wave * 32 + j] = float2{k1[0], k2[0]};
+        if (g == 1 && 16 + j < kMsFrames) kb[wave * 32 + 16 + j] = float2{k1[1], k2[1]};
+        __syncthreads();   // C_s
+        if (s + 1 < Q) {
+            put(c16_lds, pc16, n2);
+            if (s + 2 < Q) fetch(pc16, image(s + 2) + c16_off, n2);
+        }
+
+        // ---- this wave's frames: lane 8 f + w reads wave w's keys ----
+        const int fl = lane >> 3;
+        float a1 = -INFINITY, a2 = -INFINITY;
+        if (fl < FW) {
+            const float2 kv = kb[(lane & 7) * 32 + wave * FW + fl];
+            a1 = kv.x;
+            a2 = kv.y;
+        }
+        const float best8 = max8(a1, pinf);
+        const bool mine = a1 == best8;
+        const uint64_t owners = __ballot(mine);
+        const float second8 = max8(mine ? a2 : a1, pinf);
+        float pn[FW][8];
+        bool finite[FW];
+        query_scalars<FW>(qv, pn, finite);
+        int code[FW];
+#pragma unroll
+        for (int f = 0; f < FW; ++f) {
+            const unsigned grp = static_cast<unsigned>(owners >> (8 * f)) & 0xffu;
+            const float best = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(best8), 8 * f));
+            const float second = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(second8), 8 * f));
+            const bool pass = finite[f] && !exact_only && __popc(grp) == 1 && (best - second) > margin;
+            if (pass)
+                code[f] = (__ffs(grp) - 1) * cpw + (__float_as_int(best) & key_mask);
+            else
+                code[f] = exact_argmax(ch_lds, N, pn[f], lane);
+        }
+        apply_codes<DI, FW, RECON>(code, s, N, mrow, active, lane, ld, idx, force_idx, flags, tables, r, rc);
+    }
+    store_frames<DI, FW, RECON>(mrow, active, lane, r, rc, residual, recon);
 }
 
 // Stage images of the cosine quantizer, built on the device at upload.
@@ -622,6 +898,29 @@ __global__ void dac_image_cb_kernel(const float *__restrict__ codebook, const fl
             images_tb[base + ((c * 2 + q) * kWave + L) * 4 + k] = v;
         }
     if (nf) flags[1] = 1;
+}
+
+// The split codebook of each stage image (after c_hat, read from it): code
+// n's normalised row scaled by 2^12, as fp16 hi = fp16(v) and lo =
+// fp16(v - hi), at c16_at(n, 0) and c16_at(n, 1); the same in both images.
+__global__ void dac_image_c16_kernel(int64_t Q, int64_t N, int64_t D, int64_t img_f, float *__restrict__ images,
+                                     float *__restrict__ images_tb) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= Q * N) return;
+    const int64_t s = t / N, n = t % N, c = n / kWave, L = n % kWave;
+    const int64_t chat = s * img_f + 8 * D + 8;
+    const int64_t c16 = (chat + 8 * N) * 2;   // in halves
+    for (int q = 0; q < 2; ++q)
+        for (int k = 0; k < 4; ++k) {
+            const float v = images[chat + ((c * 2 + q) * kWave + L) * 4 + k] * kMsScale;
+            const _Float16 hi = static_cast<_Float16>(v);
+            const _Float16 lo = static_cast<_Float16>(v - static_cast<float>(hi));
+            for (float *img : {images, images_tb}) {
+                _Float16 *h = reinterpret_cast<_Float16 *>(img) + c16;
+                h[c16_at(n, 0) * 8 + 4 * q + k] = hi;
+                h[c16_at(n, 1) * 8 + 4 * q + k] = lo;
+            }
+        }
 }
 
 // z[s][n][d] = ((0 + c0*w0) + c1*w1 + ... + c7*w7) (+ b_out[d]): the k = 8
@@ -900,6 +1199,31 @@ EncodeFn pick_kernel(int64_t D, int fw, bool recon, bool prefetch, bool cbg, int
     return order == 1 ? pick_kernel_o<1>(D, fw, recon, prefetch, cbg) : pick_kernel_o<0>(D, fw, recon, prefetch, cbg);
 }
 
+using MsFn = void (*)(const float *, int64_t, int, int, const float4 *, int64_t, const float *, int32_t *, float *,
+                      float *, const int32_t *, int32_t *, int, int, float, int, float, int, int);
+
+template <int DI, int ORDER>
+MsFn pick_ms_recon(bool recon) {
+    return recon ? dac_encode_ms_kernel<DI, true, ORDER> : dac_encode_ms_kernel<DI, false, ORDER>;
+}
+
+template <int ORDER>
+MsFn pick_ms_o(int64_t D, bool recon) {
+    switch (D / kWave) {
+        case 1: return pick_ms_recon<1, ORDER>(recon);
+        case 2: return pick_ms_recon<2, ORDER>(recon);
+        case 4: return pick_ms_recon<4, ORDER>(recon);
+        case 8: return pick_ms_recon<8, ORDER>(recon);
+        case 12: return pick_ms_recon<12, ORDER>(recon);
+        case 16: return pick_ms_recon<16, ORDER>(recon);
+        default: return nullptr;
+    }
+}
+
+MsFn pick_ms(int64_t D, bool recon, int order) {
+    return order == 1 ? pick_ms_o<1>(D, recon) : pick_ms_o<0>(D, recon);
+}
+
 // Launch shape.  A wave keeps its frames' residuals in registers for the
 // whole cascade, so work cannot be rebalanced after launch.  The shape is
 // ranked by
@@ -977,7 +1301,12 @@ struct aq_dac_stages {
     bool exact_only = false;      // a normalised codebook entry is not finite
     int key_bits = 0;             // chunk-index bits in the score keys
     float margin = 0.0f;          // score-certificate margin
-    int64_t img_f4 = 0;
+    // Matrix-core scores (dac_encode_ms_kernel) where the shape allows them:
+    // their key bits and margin (in units of 2^24 c.q)
+    bool ms = false;
+    int ms_key_bits = 0;
+    float ms_margin = 0.0f;
+    int64_t img_f4 = 0;           // float4 per stage image (W_in, b_in, c_hat, c16)
     float4 *d_images = nullptr;   // [Q][img_f4]
     float4 *d_images_tb = nullptr;   // the same with W_in in the tinyBLAS layout
     float *d_tables = nullptr;    // [Q][N][D]
@@ -1186,6 +1515,17 @@ aq_status encode_any(aq_ctx *ctx, const aq_dac_stages *st, const float *x, int64
     return AQ_OK;
 }
 
+// After a teacher-forced encode: AQ_E_INDEX_RANGE when force_idx held a code
+// outside [0, N) (the kernels flag it and use code 0 instead).
+aq_status dac_check_forced(aq_ctx *ctx, const aq_dac_stages *st, const int32_t *force_idx) {
+    if (!force_idx) return AQ_OK;
+    int32_t flag = 0;
+    AQ_HIP(ctx, hipMemcpyAsync(&flag, ctx->d_flags + AQ_FLAG_BAD_INDEX, sizeof(int32_t), hipMemcpyDeviceToHost, ctx->stream));
+    AQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (flag) return aq_fail(ctx, AQ_E_INDEX_RANGE, "aq_dac_encode: force_idx holds a code outside [0, %lld)", (long long)st->N);
+    return AQ_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1214,7 +1554,7 @@ aq_status aq_dac_upload_ex(aq_ctx *ctx, int64_t Q, int64_t D, int64_t N, const f
     // any-shape kernel.
     if (D % kWave != 0 || N % kWave != 0 || N > (int64_t{1} << 20) || !pick_kernel(D, 1, false, false, false))
         return upload_any(ctx, Q, D, N, w_in, b_in, codebook, w_out, b_out, recipe, out);
-    const int64_t img = image_f4(D, N);
+    int64_t img = image_f4(D, N);
     // c_hat read from memory when the whole stage image does not fit in LDS
     // next to the kernel's static LDS
     const bool cbg = static_cast<size_t>(img) * 16 >
@@ -1243,6 +1583,19 @@ aq_status aq_dac_upload_ex(aq_ctx *ctx, int64_t Q, int64_t D, int64_t N, const f
         st->key_bits = bits;
         st->margin = 5.0e-6f + std::ldexp(1.001f, bits - 22);
     }
+    // Matrix-core scores: each score is within 4.3e-6 of the exact dot
+    // (split 2^-21 + accumulation 62u + flushed operands 1e-7) and ggml's
+    // within 15u: 1.2e-5 for the pair, plus the keys' truncation; scaled by
+    // 2^24 like the scores.
+    st->ms = !cbg && N % (16 * kMsWaves) == 0 && N <= kMsPart * kMsWaves * kWave / 2 &&
+             D <= kMsPart * kMsWaves * kWave / 2;
+    {
+        int bits = 0;
+        while ((int64_t{1} << bits) < N / kMsWaves) ++bits;
+        st->ms_key_bits = bits;
+        st->ms_margin = std::ldexp(1.2e-5f + std::ldexp(1.001f, bits - 22), 24);
+    }
+    img += 2 * N;   // the split codebook (c16) after c_hat
     st->img_f4 = img;
     // The host arrays go to the device as given; the stage images and the
     // out-projection tables are built there.
@@ -1278,6 +1631,8 @@ aq_status aq_dac_upload_ex(aq_ctx *ctx, int64_t Q, int64_t D, int64_t N, const f
                            ctx->stream, d_win, Q, D, img * 4, reinterpret_cast<float *>(st->d_images), reinterpret_cast<float *>(st->d_images_tb));
         hipLaunchKernelGGL(dac_image_cb_kernel, dim3(static_cast<unsigned>((Q * N + 255) / 256)), dim3(256), 0,
                            ctx->stream, d_cb, d_bin, Q, N, D, img * 4, recipe, reinterpret_cast<float *>(st->d_images), reinterpret_cast<float *>(st->d_images_tb), d_flags);
+        hipLaunchKernelGGL(dac_image_c16_kernel, dim3(static_cast<unsigned>((Q * N + 255) / 256)), dim3(256), 0,
+                           ctx->stream, Q, N, D, img * 4, reinterpret_cast<float *>(st->d_images), reinterpret_cast<float *>(st->d_images_tb));
         ok = hipGetLastError() == hipSuccess;
     }
     if (w_out)
@@ -1414,6 +1769,37 @@ aq_status aq_dac_encode_ex(aq_ctx *ctx, const aq_dac_stages *st, const float *x,
     }
     const Shape shape = st->shape;
     const int fw = shape.fw;
+    // Matrix-core scores where the shape allows them and the launch shape is
+    // the one they use (8 waves x 3 frames); AQ_DAC_MS=0 / 1 turns them off /
+    // takes them whenever the codebook allows (tests of both paths).
+    {
+        const char *e = std::getenv("AQ_DAC_MS");
+        const bool want = st->ms && !st->exact_only &&
+                          (e && e[0] == '1' ? true
+                           : e && e[0] == '0' ? false
+                                               : fw == kMsFw && shape.waves_per_block == kMsWaves);
+        MsFn mfn = want ? pick_ms(st->D, recon != nullptr, order) : nullptr;
+        const size_t ms_lds = static_cast<size_t>(2 * st->D + 4 * st->N + 64 + kMsWaves * 16) * sizeof(float4) +
+                              (order == 1 ? static_cast<size_t>(kMsWaves) * st->D * sizeof(float) : 0);
+        if (mfn && ms_lds <= aq_lds_budget(reinterpret_cast<const void *>(mfn))) {
+            if (st->lds_fn != reinterpret_cast<const void *>(mfn) || st->lds_limit != ms_lds) {
+                aq_status ls = aq_launch_lds(ctx, reinterpret_cast<const void *>(mfn), ms_lds, "aq_dac_encode");
+                if (ls != AQ_OK) return ls;
+                st->lds_fn = reinterpret_cast<const void *>(mfn);
+                st->lds_limit = ms_lds;
+            }
+            if (force_idx) AQ_HIP(ctx, hipMemsetAsync(ctx->d_flags, 0, sizeof(int32_t) * AQ_FLAG_COUNT, ctx->stream));
+            const unsigned blocks = static_cast<unsigned>((M + kMsFrames - 1) / kMsFrames);
+            if (std::getenv("AQ_DEBUG")) std::fprintf(stderr, "aq_dac matrix scores blocks=%u\n", blocks);
+            aq_launch_timed(ctx, true, mfn, dim3(blocks), dim3(kMsWaves * kWave), static_cast<uint32_t>(ms_lds), x, M,
+                            static_cast<int>(st->Q), static_cast<int>(st->N), order == 1 ? st->d_images_tb : st->d_images,
+                            st->img_f4, static_cast<const float *>(st->d_tables), idx, residual, recon, force_idx,
+                            ctx->d_flags, st->has_bin ? 1 : 0, st->ms_key_bits, st->ms_margin, 0, st->qeps,
+                            static_cast<int>(idx_ld), recon_accumulate ? 1 : 0);
+            AQ_HIP(ctx, hipGetLastError());
+            return dac_check_forced(ctx, st, force_idx);
+        }
+    }
     EncodeFn fn = pick_kernel(st->D, fw, recon != nullptr, shape.prefetch, st->cbg, order);
     const size_t rt_bytes = order == 1 ? static_cast<size_t>(shape.waves_per_block) * static_cast<size_t>(st->D) * 4 : 0;
     // A second stage image in LDS when it fits: one barrier per stage.
@@ -1435,13 +1821,7 @@ aq_status aq_dac_encode_ex(aq_ctx *ctx, const aq_dac_stages *st, const float *x,
                     ctx->d_flags, st->has_bin ? 1 : 0, st->key_bits, st->margin, st->exact_only ? 1 : 0, st->qeps,
                     dbuf_f4, static_cast<int>(idx_ld), recon_accumulate ? 1 : 0);
     AQ_HIP(ctx, hipGetLastError());
-    if (force_idx) {
-        int32_t flag = 0;
-        AQ_HIP(ctx, hipMemcpyAsync(&flag, ctx->d_flags + AQ_FLAG_BAD_INDEX, sizeof(int32_t), hipMemcpyDeviceToHost, ctx->stream));
-        AQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
-        if (flag) return aq_fail(ctx, AQ_E_INDEX_RANGE, "aq_dac_encode: force_idx holds a code outside [0, %lld)", (long long)st->N);
-    }
-    return AQ_OK;
+    return dac_check_forced(ctx, st, force_idx);
 }
 
 aq_status aq_dac_decode(aq_ctx *ctx, const aq_dac_stages *st, const int32_t *idx, int64_t M, float *out) {

@@ -398,3 +398,81 @@ def test_dac_channel_major_input(torch, ctx, oracle, T):
     assert np.array_equal(idx.cpu().numpy(), ref["idx"])
     assert np.array_equal(res.cpu().numpy().view(np.uint32), ref["residual"].view(np.uint32))
     assert np.array_equal(rec.cpu().numpy().view(np.uint32), ref["recon"].view(np.uint32))
+
+
+def _ms_case(case, D, N, Q, B, T, bias):
+    from aqmi import synth
+
+    w = synth.dac_weights(61, Q, D, N, bias=bias)
+    x = synth.normal(61, 1, (B * T, D))
+    if case == "near_dup":                 # scores of a pair a few ulps apart: exact rescoring decides
+        cb = synth.normal(62, 90, (Q, N, 8))
+        cb[:, 1::2] = cb[:, 0::2] * np.float32(1.0 + 1e-7)
+        cb[:, 2:8:2] = cb[:, 3:9:2]
+        w["codebook"] = cb.astype(np.float32)
+    elif case == "special":                # zero frames (all scores 0), one-hot codes, NaN / Inf frames
+        cb = w["codebook"]
+        for n in range(16):
+            cb[:, n, :] = 0.0
+            cb[:, n, n % 8] = 1.0 if n < 8 else -1.0
+        x[:T] = 0.0
+        x[T + 1, 5] = np.nan
+        x[T + 4, :] = np.inf
+    return dict(kind="dac", B=B, T=T, D=D, Q=Q, N=N, x=x, **w)
+
+
+@pytest.mark.parametrize("case,D,N,Q,B,T,bias", [
+    ("random", 1024, 1024, 3, 3, 75, True),       # vec_dot order, a partial last block
+    ("random", 1024, 1024, 2, 2, 76, True),       # tinyBLAS order (T % 4 == 0)
+    ("random", 512, 512, 3, 4, 33, False),
+    ("random", 64, 128, 2, 2, 12, True),
+    ("random", 768, 256, 2, 3, 50, True),
+    ("near_dup", 256, 512, 3, 6, 7, False),
+    ("special", 128, 128, 2, 3, 9, True),
+])
+def test_dac_matrix_scores_match_oracle(torch, ctx, oracle, monkeypatch, capfd, case, D, N, Q, B, T, bias):
+    """The matrix-core score kernel (split fp16 scores over a block's 24
+    frames; AQ_DAC_MS=1 takes it whatever the launch shape) bit for bit
+    against the oracle and against the per-wave score kernel (AQ_DAC_MS=0):
+    codes, residual and reconstruction, in both in-projection orders,
+    including near-tied codes, zero, NaN and Inf frames."""
+    print(f"[gpu] dac matrix scores {case} D={D} N={N} Q={Q} B={B} T={T}", flush=True)
+    cfg = _ms_case(case, D, N, Q, B, T, bias)
+    monkeypatch.setenv("AQ_DEBUG", "1")
+    monkeypatch.setenv("AQ_DAC_MS", "1")
+    ms = run_gpu(torch, ctx, cfg)
+    assert "aq_dac matrix scores" in capfd.readouterr().err
+    monkeypatch.setenv("AQ_DAC_MS", "0")
+    vw = run_gpu(torch, ctx, cfg)
+    assert "aq_dac matrix scores" not in capfd.readouterr().err
+    ref = oracle.dac_rvq(cfg)
+    for out in (ms, vw):
+        assert np.array_equal(out["idx"], ref["idx"])
+        for k in ("residual", "recon"):
+            a, b = out[k], ref[k]
+            assert np.array_equal(np.isnan(a), np.isnan(b))
+            ok = ~np.isnan(a)
+            assert np.array_equal(_bits(a[ok]), _bits(b[ok])), k
+
+
+def test_dac_matrix_scores_teacher_forced(torch, ctx, oracle, monkeypatch):
+    """Teacher forcing on the matrix-core score kernel: forced codes drive the
+    residual, the chosen codes are still reported, and a forced code out of
+    range is an error."""
+    import aqmi
+    from aqmi import synth
+
+    D, N, Q, B, T = 1024, 1024, 3, 2, 75
+    cfg = dict(kind="dac", B=B, T=T, D=D, Q=Q, N=N, x=synth.normal(63, 1, (B * T, D)),
+               **synth.dac_weights(63, Q, D, N, bias=True))
+    forced = np.random.default_rng(63).integers(0, N, (B * T, Q)).astype(np.int32)
+    monkeypatch.setenv("AQ_DAC_MS", "1")
+    out = run_gpu(torch, ctx, cfg, force_idx=forced)
+    ref = oracle.dac_rvq(cfg, force_idx=forced)
+    assert np.array_equal(out["idx"], ref["idx"])
+    assert np.array_equal(_bits(out["residual"]), _bits(ref["residual"]))
+    assert np.array_equal(_bits(out["recon"]), _bits(ref["recon"]))
+    bad = forced.copy()
+    bad[5, 1] = N
+    with pytest.raises(aqmi.AqError):
+        run_gpu(torch, ctx, cfg, force_idx=bad)
