@@ -746,12 +746,6 @@ __global__ __launch_bounds__(kMsWaves * kWave, 1) void dac_encode_ms_kernel(
             qh[8] = lo;
         }
         __syncthreads();   // B_s
-        if (s + 1 < Q) {
-            put(w_lds, pw, 2 * D);
-            if (s + 2 < Q) fetch(pw, image(s + 2), 2 * D);
-        }
-        put(ch_lds, pch, n2);
-        if (s + 1 < Q) fetch(pch, image(s + 1) + ch_off, n2);
 
         // ---- scores of this wave's codes for the block's frames ----
         const float pinf = opaque_inf();
@@ -791,6 +785,14 @@ __global__ __launch_bounds__(kMsWaves * kWave, 1) void dac_encode_ms_kernel(
             swap32(k2[ft], k2[ft], lo2, hi2);
             merge_top2(lo1, hi1, lo2, hi2, pinf, k1[ft], k2[ft]);
         }
+        // W_in(s+1) and c_hat(s), stored after the scores so that their
+        // operand reads do not queue behind these stores
+        if (s + 1 < Q) {
+            put(w_lds, pw, 2 * D);
+            if (s + 2 < Q) fetch(pw, image(s + 2), 2 * D);
+        }
+        put(ch_lds, pch, n2);
+        if (s + 1 < Q) fetch(pch, image(s + 1) + ch_off, n2);
         if (g == 0) kb[wave * 32 + j] = float2{k1[0], k2[0]};
         if (g == 1 && 16 + j < kMsFrames) kb[wave * 32 + 16 + j] = float2{k1[1], k2[1]};
         __syncthreads();   // C_s
@@ -811,20 +813,24 @@ __global__ __launch_bounds__(kMsWaves * kWave, 1) void dac_encode_ms_kernel(
         const bool mine = a1 == best8;
         const uint64_t owners = __ballot(mine);
         const float second8 = max8(mine ? a2 : a1, pinf);
-        float pn[FW][8];
-        bool finite[FW];
-        query_scalars<FW>(qv, pn, finite);
+        const uint64_t good = __ballot((qv - qv) == 0.0f);
         int code[FW];
 #pragma unroll
         for (int f = 0; f < FW; ++f) {
             const unsigned grp = static_cast<unsigned>(owners >> (8 * f)) & 0xffu;
             const float best = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(best8), 8 * f));
             const float second = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(second8), 8 * f));
-            const bool pass = finite[f] && !exact_only && __popc(grp) == 1 && (best - second) > margin;
-            if (pass)
+            const bool finite = ((good >> (8 * f)) & 0xffull) == 0xffull;
+            const bool pass = finite && !exact_only && __popc(grp) == 1 && (best - second) > margin;
+            if (pass) {
                 code[f] = (__ffs(grp) - 1) * cpw + (__float_as_int(best) & key_mask);
-            else
-                code[f] = exact_argmax(ch_lds, N, pn[f], lane);
+            } else {
+                // the query in scalar registers, for the exact rescoring only
+                float pn[8];
+#pragma unroll
+                for (int o = 0; o < 8; ++o) pn[o] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(qv), 8 * f + o));
+                code[f] = exact_argmax(ch_lds, N, pn, lane);
+            }
         }
         apply_codes<DI, FW, RECON>(code, s, N, mrow, active, lane, ld, idx, force_idx, flags, tables, r, rc);
     }
