@@ -476,3 +476,41 @@ def test_dac_matrix_scores_teacher_forced(torch, ctx, oracle, monkeypatch):
     bad[5, 1] = N
     with pytest.raises(aqmi.AqError):
         run_gpu(torch, ctx, cfg, force_idx=bad)
+
+
+@pytest.mark.parametrize("recipe", [1, 2])
+def test_dac_matrix_scores_recipes(torch, ctx, oracle, monkeypatch, recipe):
+    """IndexTTS2 and Vevo2 normalisation on the matrix-core score kernel,
+    through the cascade and as one codes-only stage (no out-projection, a
+    zero frame: IndexTTS2's NaN query takes the exact rescoring)."""
+    import aqmi
+    from aqmi import synth
+
+    print(f"[gpu] dac matrix scores recipe {recipe}", flush=True)
+    monkeypatch.setenv("AQ_DAC_MS", "1")
+    T, B, D, N, Q = 75, 2, 1024, 1024, 3
+    cfg = dict(kind="dac", B=B, T=T, D=D, Q=Q, N=N, x=synth.normal(64, 1, (B * T, D)),
+               **synth.dac_weights(64, Q, D, N, bias=True))
+    st = aqmi.DacStages(ctx, cfg["w_in"], cfg["b_in"], cfg["codebook"], cfg["w_out"], cfg["b_out"], recipe)
+    x = torch.from_numpy(cfg["x"]).cuda()
+    idx = torch.full((B * T, Q), -1, dtype=torch.int32, device="cuda")
+    res = torch.empty((B * T, D), dtype=torch.float32, device="cuda")
+    rec = torch.empty((B * T, D), dtype=torch.float32, device="cuda")
+    st.encode(x, T, idx, res, rec)
+    torch.cuda.synchronize()
+    ref = oracle.dac_rvq(cfg, recipe=recipe)
+    assert np.array_equal(idx.cpu().numpy(), ref["idx"])
+    assert np.array_equal(_bits(res.cpu().numpy()), _bits(ref["residual"]))
+    assert np.array_equal(_bits(rec.cpu().numpy()), _bits(ref["recon"]))
+
+    xz = cfg["x"].copy()
+    xz[3] = 0.0
+    b0 = np.zeros_like(cfg["b_in"][:1])
+    one = dict(kind="dac", B=B, T=T, D=D, Q=1, N=N, x=xz, w_in=cfg["w_in"][:1], b_in=b0,
+               codebook=cfg["codebook"][:1], w_out=None, b_out=None)
+    st1 = aqmi.DacStages(ctx, one["w_in"], b0, one["codebook"], None, None, recipe)
+    idx1 = torch.full((B * T, 1), -1, dtype=torch.int32, device="cuda")
+    st1.encode(torch.from_numpy(xz).cuda(), T, idx1)
+    torch.cuda.synchronize()
+    ref1 = oracle.dac_rvq(one, recon=False, recipe=recipe)
+    assert np.array_equal(idx1.cpu().numpy(), ref1["idx"])
