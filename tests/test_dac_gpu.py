@@ -427,6 +427,7 @@ def _ms_case(case, D, N, Q, B, T, bias):
     ("random", 512, 512, 3, 4, 33, False),
     ("random", 64, 128, 2, 2, 12, True),
     ("random", 768, 256, 2, 3, 50, True),
+    ("random", 768, 384, 2, 3, 52, True),        # tinyBLAS order without the bank swizzle (D / 64 = 12)
     ("near_dup", 256, 512, 3, 6, 7, False),
     ("special", 128, 128, 2, 3, 9, True),
 ])
